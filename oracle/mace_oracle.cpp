@@ -1,0 +1,1416 @@
+// CPU ORACLE — test infrastructure only.
+//
+// A C++/OpenMP restatement of the reference's MACE energy + forces + stress
+// path, used by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline as
+// the checker of the HIP path.  It is never part of the product: the product
+// library (symmetrix-xl_amd/csrc) neither links nor loads it.
+//
+// What it restates (file:line in the reference snapshot):
+//   * periodic neighbour list, bit-exact (IEEE double, no FMA contraction):
+//     libsymmetrix/source/neighbor_graph_kokkos.cpp:38-405
+//   * prepared edge geometry with the cutoff clamp:
+//     libsymmetrix/source/mace_kokkos_factorized_lifecycle.cpp:2915-3079
+//   * compact radial tabulation: compact_radial.cpp:110-387 (features :227-267,
+//     MLP :269-289 via multilayer_perceptron.cpp:30-80, spline derivatives
+//     :326-366); Hermite coefficients and evaluation cubic_spline_set.cpp:8-96
+//   * stage math of the streamed serial evaluator mace.cpp:232-319 and
+//     :1356-2657 (A0 :1356-1403, reverse A0 :1486-1560, M0 :1639-1689,
+//     H1 :1691-1757, v4 affine capture :1759-1814, Phi1 :2023-2084,
+//     reverse Phi1 :2199-2303, A1 :2305-2379, M1 :2461-2514, H2 :2516-2620,
+//     readouts :2622-2657), with the Kokkos evaluator's precision policy
+//     (FP64 H2, readouts, node energies, directed forces, and the FP64
+//     accumulation of the FP32 source adjoint: mace_kokkos.hpp:501,907-909,
+//     1805-1828)
+//   * polynomial semantics: multivariate_polynomial.cpp:11-103 (a repeated
+//     monomial keeps its first coefficient)
+//   * force and stress reductions: mace_kokkos_evaluate.cpp:49-128, 189-291
+//
+// Y: the reference evaluates sphericart's real harmonics at the shuffled
+// direction (z, x, y) and scales by sqrt(4 pi) rounding once from double
+// (spherical_harmonic_device.hpp:15-199).  sphericart is not vendored, so the
+// polynomials are written here from the real-harmonic closed forms; edges with
+// r >= r_cut carry Y = 0 as in the direct plan (:201-223).
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <limits>
+#include <map>
+#include <memory>
+#include <numeric>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include <omp.h>
+
+#include "../symmetrix-xl_amd/csrc/json_lite.hpp"
+
+namespace oracle {
+
+using json_lite::Value;
+
+thread_local std::string last_error;
+
+// ---------------------------------------------------------------------------
+// Compact radial model (compact_radial.cpp)
+// ---------------------------------------------------------------------------
+
+struct Network {
+    std::vector<int> shape;
+    std::vector<std::vector<double>> weights;  // [layer][out*in]
+    double scale = 1.0;
+};
+
+static Network parse_network(const Value& v) {
+    Network n;
+    n.shape = v.at("shape").as_ints();
+    const Value& w = v.at("weights");
+    for (std::size_t i = 0; i < w.size(); ++i) n.weights.push_back(w.at(i).as_doubles());
+    n.scale = v.at("activation_scale").as_number();
+    if (v.at("activation").as_string() != "silu")
+        throw std::invalid_argument("radial network must use SiLU");
+    if (n.shape.size() < 2 || n.weights.size() != n.shape.size() - 1)
+        throw std::invalid_argument("radial network has an invalid shape");
+    for (std::size_t l = 0; l < n.weights.size(); ++l)
+        if (n.weights[l].size() != static_cast<std::size_t>(n.shape[l]) * n.shape[l + 1])
+            throw std::invalid_argument("radial network has invalid weights");
+    return n;
+}
+
+// multilayer_perceptron.cpp:30-80: hidden layers scale*x*sigmoid(x), linear output.
+static void mlp_forward(const Network& n, const double* in, double* out) {
+    std::vector<double> cur(in, in + n.shape[0]);
+    for (std::size_t l = 0; l < n.weights.size(); ++l) {
+        const int ni = n.shape[l], no = n.shape[l + 1];
+        std::vector<double> nxt(no, 0.0);
+        for (int o = 0; o < no; ++o) {
+            double s = 0.0;
+            for (int i = 0; i < ni; ++i) s += n.weights[l][static_cast<std::size_t>(o) * ni + i] * cur[i];
+            nxt[o] = s;
+        }
+        if (l + 1 < n.weights.size())
+            for (int o = 0; o < no; ++o) nxt[o] = n.scale * nxt[o] / (1.0 + std::exp(-nxt[o]));
+        cur.swap(nxt);
+    }
+    std::copy(cur.begin(), cur.end(), out);
+}
+
+struct RadialModel {
+    double grid_min = 0, h = 0, r_max = 0, prefactor = 0;
+    int points = 0, p = 0;
+    std::vector<double> bessel;
+    Network R0, R1;
+    bool has_R1 = false;
+
+    void load(const Value& def, double r_cut) {
+        grid_min = def.at("spline_grid_min").as_number();
+        points = def.at("num_spline_points").as_int();
+        if (!(grid_min > 0.0) || points < 4)
+            throw std::invalid_argument("compact radial grid is invalid");
+        h = (r_cut - grid_min) / (points - 1);
+        const Value& basis = def.at("basis");
+        if (basis.at("type").as_string() != "bessel")
+            throw std::invalid_argument("only a Bessel basis is supported");
+        bessel = basis.at("weights").as_doubles();
+        prefactor = basis.at("prefactor").as_number();
+        const Value& cut = def.at("cutoff");
+        if (cut.at("type").as_string() != "polynomial")
+            throw std::invalid_argument("only a polynomial cutoff is supported");
+        r_max = cut.at("r_max").as_number();
+        p = cut.at("p").as_int();
+        if (std::abs(r_max - r_cut) > 1e-12)
+            throw std::invalid_argument("compact radial cutoff does not match r_cut");
+        if (def.at("distance_transform").at("type").as_string() != "none")
+            throw std::invalid_argument("only distance_transform 'none' is supported");
+        const Value& nets = def.at("networks");
+        R0 = parse_network(nets.at("R0"));
+        if (nets.contains("R1")) { R1 = parse_network(nets.at("R1")); has_R1 = true; }
+        if (nets.contains("A0") || nets.contains("A1"))
+            throw std::invalid_argument("density-scaled (A0/A1) networks are not supported");
+    }
+
+    // compact_radial.cpp:227-267 (no distance transform)
+    std::vector<double> features() const {
+        const std::size_t nb = bessel.size();
+        std::vector<double> f(static_cast<std::size_t>(points) * nb);
+        for (int node = 0; node < points; ++node) {
+            const double r = grid_min + node * h;
+            double cutoff_value = 0.0;
+            if (r < r_max) {
+                const double s = r / r_max;
+                cutoff_value = 1.0 - ((p + 1.0) * (p + 2.0) / 2.0) * std::pow(s, p)
+                    + p * (p + 2.0) * std::pow(s, p + 1)
+                    - (p * (p + 1.0) / 2.0) * std::pow(s, p + 2);
+            }
+            for (std::size_t b = 0; b < nb; ++b)
+                f[node * nb + b] = prefactor * std::sin(bessel[b] * r) / r * cutoff_value;
+        }
+        return f;
+    }
+
+    // compact_radial.cpp:326-366: not-a-knot left, clamped (zero) right.
+    std::vector<double> spline_derivatives(const std::vector<double>& v) const {
+        const int n = points, unknowns = n - 2;
+        std::vector<double> lower(unknowns, 0.0), diag(unknowns, 4.0), upper(unknowns, 0.0), rhs(unknowns, 0.0);
+        const double left = 2.0 * (-v[0] + 2.0 * v[1] - v[2]) / h;
+        upper[0] = 2.0;
+        rhs[0] = 3.0 * (v[2] - v[0]) / h - left;
+        for (int node = 2; node < n - 1; ++node) {
+            const int row = node - 1;
+            lower[row] = 1.0;
+            if (node + 1 <= n - 2) upper[row] = 1.0;
+            rhs[row] = 3.0 * (v[node + 1] - v[node - 1]) / h;
+        }
+        for (int row = 1; row < unknowns; ++row) {
+            const double factor = lower[row] / diag[row - 1];
+            diag[row] -= factor * upper[row - 1];
+            rhs[row] -= factor * rhs[row - 1];
+        }
+        std::vector<double> sol(unknowns, 0.0);
+        sol.back() = rhs.back() / diag.back();
+        for (int row = unknowns - 2; row >= 0; --row)
+            sol[row] = (rhs[row] - upper[row] * sol[row + 1]) / diag[row];
+        std::vector<double> d(n, 0.0);
+        for (int node = 1; node < n - 1; ++node) d[node] = sol[node - 1];
+        d[0] = d[2] + left;
+        d.back() = 0.0;
+        return d;
+    }
+
+    // Nodal values and derivatives [function][node] of a network on the grid.
+    void tabulate(const Network& net, std::vector<std::vector<double>>& values,
+                  std::vector<std::vector<double>>& derivs) const {
+        const auto f = features();
+        const int nout = net.shape.back();
+        values.assign(nout, std::vector<double>(points));
+        std::vector<double> out(nout);
+        for (int node = 0; node < points; ++node) {
+            mlp_forward(net, f.data() + static_cast<std::size_t>(node) * bessel.size(), out.data());
+            for (int o = 0; o < nout; ++o) values[o][node] = out[o];
+        }
+        derivs.resize(nout);
+        for (int o = 0; o < nout; ++o) derivs[o] = spline_derivatives(values[o]);
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Cubic Hermite spline set (cubic_spline_set.cpp:8-96), arithmetic in P.
+// ---------------------------------------------------------------------------
+
+template <class P>
+struct SplineSet {
+    P h{}, x0{};
+    int num_nodes = 0, num_splines = 0;
+    std::vector<P> c;  // [interval][4][function]
+
+    SplineSet(P h_, const std::vector<std::vector<P>>& v, const std::vector<std::vector<P>>& d, P x0_)
+        : h(h_), x0(x0_) {
+        num_nodes = static_cast<int>(v[0].size());
+        num_splines = static_cast<int>(v.size());
+        c.assign(static_cast<std::size_t>(4) * num_splines * (num_nodes - 1), P(0));
+        for (int i = 0; i < num_nodes - 1; ++i)
+            for (int j = 0; j < num_splines; ++j) {
+                c[(4 * i) * num_splines + j] = v[j][i];
+                c[(4 * i + 1) * num_splines + j] = d[j][i];
+                c[(4 * i + 2) * num_splines + j] =
+                    (-3 * v[j][i] - 2 * h * d[j][i] + 3 * v[j][i + 1] - h * d[j][i + 1]) / (h * h);
+                c[(4 * i + 3) * num_splines + j] =
+                    (2 * v[j][i] + h * d[j][i] - 2 * v[j][i + 1] + h * d[j][i + 1]) / (h * h * h);
+            }
+    }
+    struct Point { int interval; P x, xx, xxx; };
+    Point point(P r) const {
+        int interval = static_cast<int>(std::floor((r - x0) / h));
+        P x = r - x0 - h * interval;
+        if (interval < 0) { interval = 0; x = 0; }
+        else if (interval >= num_nodes - 1) { interval = num_nodes - 2; x = h; }
+        const P xx = x * x;
+        return {interval, x, xx, xx * x};
+    }
+    const P* coefficients(const Point& pt) const {
+        return c.data() + static_cast<std::size_t>(4) * pt.interval * num_splines;
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Real spherical harmonics l <= 3 (component normalisation), P precision.
+// Values at unit vector (x,y,z) already shuffled; returns raw orthonormal values
+// and the Cartesian gradients on the sphere before normalisation.
+// ---------------------------------------------------------------------------
+
+template <class P>
+static void sph_raw(int l_max, P x, P y, P z, P* v, P* dx, P* dy, P* dz) {
+    // constants of the orthonormal real harmonics
+    const double pi = 3.14159265358979323846;
+    const P c0 = P(0.5 / std::sqrt(pi));
+    v[0] = c0; dx[0] = dy[0] = dz[0] = 0;
+    if (l_max < 1) return;
+    const P c1 = P(std::sqrt(3.0 / (4.0 * pi)));
+    v[1] = c1 * y; dx[1] = 0; dy[1] = c1; dz[1] = 0;
+    v[2] = c1 * z; dx[2] = 0; dy[2] = 0; dz[2] = c1;
+    v[3] = c1 * x; dx[3] = c1; dy[3] = 0; dz[3] = 0;
+    if (l_max < 2) return;
+    const P c2 = P(0.5 * std::sqrt(15.0 / pi));
+    const P c20 = P(0.25 * std::sqrt(5.0 / pi));
+    const P c22 = P(0.25 * std::sqrt(15.0 / pi));
+    v[4] = c2 * x * y; dx[4] = c2 * y; dy[4] = c2 * x; dz[4] = 0;
+    v[5] = c2 * y * z; dx[5] = 0; dy[5] = c2 * z; dz[5] = c2 * y;
+    v[6] = c20 * (2 * z * z - x * x - y * y); dx[6] = -2 * c20 * x; dy[6] = -2 * c20 * y; dz[6] = 4 * c20 * z;
+    v[7] = c2 * x * z; dx[7] = c2 * z; dy[7] = 0; dz[7] = c2 * x;
+    v[8] = c22 * (x * x - y * y); dx[8] = 2 * c22 * x; dy[8] = -2 * c22 * y; dz[8] = 0;
+    if (l_max < 3) return;
+    const P c33 = P(0.25 * std::sqrt(35.0 / (2.0 * pi)));
+    const P c32 = P(0.5 * std::sqrt(105.0 / pi));
+    const P c31 = P(0.25 * std::sqrt(21.0 / (2.0 * pi)));
+    const P c30 = P(0.25 * std::sqrt(7.0 / pi));
+    const P c32b = P(0.25 * std::sqrt(105.0 / pi));
+    const P r2 = x * x + y * y;
+    v[9] = c33 * y * (3 * x * x - y * y);
+    dx[9] = c33 * 6 * x * y; dy[9] = c33 * (3 * x * x - 3 * y * y); dz[9] = 0;
+    v[10] = c32 * x * y * z;
+    dx[10] = c32 * y * z; dy[10] = c32 * x * z; dz[10] = c32 * x * y;
+    v[11] = c31 * y * (4 * z * z - r2);
+    dx[11] = c31 * (-2 * x * y); dy[11] = c31 * (4 * z * z - x * x - 3 * y * y); dz[11] = c31 * 8 * y * z;
+    v[12] = c30 * z * (2 * z * z - 3 * r2);
+    dx[12] = c30 * (-6 * x * z); dy[12] = c30 * (-6 * y * z); dz[12] = c30 * (6 * z * z - 3 * r2);
+    v[13] = c31 * x * (4 * z * z - r2);
+    dx[13] = c31 * (4 * z * z - 3 * x * x - y * y); dy[13] = c31 * (-2 * x * y); dz[13] = c31 * 8 * x * z;
+    v[14] = c32b * z * (x * x - y * y);
+    dx[14] = c32b * 2 * x * z; dy[14] = -c32b * 2 * y * z; dz[14] = c32b * (x * x - y * y);
+    v[15] = c33 * x * (x * x - 3 * y * y);
+    dx[15] = c33 * (3 * x * x - 3 * y * y); dy[15] = -c33 * 6 * x * y; dz[15] = 0;
+}
+
+static constexpr double kSqrt4Pi = 3.5449077018110318;
+
+// Y and dY/dxyz of one edge from its unit direction (unshuffled) and radius,
+// following spherical_harmonic_device.hpp:150-199 (value normalisation
+// float(double(v)*sqrt(4 pi)); gradients (d - u (u.d))/r scaled by sqrt(4 pi)).
+template <class P>
+static void edge_harmonics(int l_max, const P dir[3], P radius, P* Y, P* G) {
+    const int n = (l_max + 1) * (l_max + 1);
+    P x = dir[2], y = dir[0], z = dir[1];
+    const P rr = x * x + y * y + z * z;
+    const P inv = P(1) / std::sqrt(rr);
+    x *= inv; y *= inv; z *= inv;
+    P v[16], dx[16], dy[16], dz[16];
+    sph_raw<P>(l_max, x, y, z, v, dx, dy, dz);
+    for (int i = 0; i < n; ++i) Y[i] = static_cast<P>(static_cast<double>(v[i]) * kSqrt4Pi);
+    if (!G) return;
+    const P scale = static_cast<P>(kSqrt4Pi) / radius;
+    for (int i = 0; i < n; ++i) {
+        const P radial = dx[i] * x + dy[i] * y + dz[i] * z;
+        const P gx = (dx[i] - x * radial);
+        const P gy = (dy[i] - y * radial);
+        const P gz = (dz[i] - z * radial);
+        // unshuffle: d/dX = d/dy', d/dY = d/dz', d/dZ = d/dx'
+        G[i] = scale * gy;
+        G[n + i] = scale * gz;
+        G[2 * n + i] = scale * gx;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Multivariate polynomial (multivariate_polynomial.cpp:11-103): keep the first
+// coefficient of a repeated monomial; f = sum c_t prod x; gradient by product
+// rule.  Arithmetic in P.
+// ---------------------------------------------------------------------------
+
+struct MonomialSet {
+    std::vector<std::vector<int>> monos;  // deduplicated, first occurrence
+    std::vector<int> source_index;        // index into the file's coefficient list
+};
+
+static MonomialSet dedupe_monomials(const std::vector<std::vector<int>>& monos) {
+    MonomialSet s;
+    std::map<std::vector<int>, int> seen;
+    for (std::size_t i = 0; i < monos.size(); ++i) {
+        if (seen.count(monos[i])) continue;
+        seen[monos[i]] = static_cast<int>(i);
+        s.monos.push_back(monos[i]);
+        s.source_index.push_back(static_cast<int>(i));
+    }
+    return s;
+}
+
+template <class P>
+static P poly_eval_grad(const MonomialSet& ms, const P* coef, const P* x, P* g, int nvar) {
+    P f = 0;
+    if (g) for (int v = 0; v < nvar; ++v) g[v] = 0;
+    for (std::size_t t = 0; t < ms.monos.size(); ++t) {
+        const auto& m = ms.monos[t];
+        P prod = 1;
+        for (int v : m) prod *= x[v];
+        f += coef[t] * prod;
+        if (g) {
+            for (std::size_t q = 0; q < m.size(); ++q) {
+                P d = coef[t];
+                for (std::size_t q2 = 0; q2 < m.size(); ++q2)
+                    if (q2 != q) d *= x[m[q2]];
+                g[m[q]] += d;
+            }
+        }
+    }
+    return f;
+}
+
+// ---------------------------------------------------------------------------
+// Model and evaluator
+// ---------------------------------------------------------------------------
+
+template <class P>
+struct Mace {
+    int num_elements = 0, C = 0, l_max = 0, L_max = 0, num_lm = 0, num_LM = 0;
+    double r_cut = 0;
+    std::vector<int> atomic_numbers;
+    std::vector<double> atomic_energies;
+    RadialModel radial;
+    std::vector<P> H0;                      // [type][C]
+    std::vector<std::vector<std::vector<P>>> A0_w;  // [type][l][C*C]
+    std::vector<MonomialSet> M0_monos;      // [LM]
+    std::vector<std::vector<P>> M0_coef;    // [type*num_LM + LM][k*T + t]
+    std::vector<P> H1_w;                    // [l][C][C]
+    std::vector<int> Phi1_l, Phi1_l1, Phi1_l2, Phi1_lme, Phi1_row;
+    std::vector<P> Phi1_cg;
+    int num_rows = 0, num_lme = 0;
+    std::vector<int> num_e;                 // paths per output l
+    std::vector<int> lme_base;              // first lme of output l
+    std::vector<std::vector<P>> A1_w;       // [l][e*C*C]
+    MonomialSet M1_monos;
+    std::vector<std::vector<P>> M1_coef;    // [type][k*T + t]
+    std::vector<std::vector<double>> H2_T;  // [type][C*C] (float-rounded, used in FP64)
+    std::vector<double> H2_M1;              // [C*C]
+    std::vector<double> q;                  // readout_1 (FP64)
+    int hidden = 16;
+    std::vector<double> W1, W2;             // readout_2 (FP64)
+    double readout_scale = 1.0;
+
+    // active radial tables
+    std::vector<int> active_types, type_to_active;
+    std::vector<std::shared_ptr<SplineSet<P>>> spl0, spl1;
+
+    // state of the last evaluation (exposed for stage-level debugging)
+    std::vector<P> Y, Ygrad, A0, M0, M0_grad, H1, xaff, Phi1, A1, M1, M1_grad, A1_adj, dPhi1,
+        H1_adj, M0_adj, A0_adj;
+    std::vector<double> H2, H2_adj, direct;
+    std::vector<double> node_energies, node_forces;
+
+    static P cast(double v) {
+        if (!std::isfinite(v) || std::abs(v) > static_cast<double>(std::numeric_limits<P>::max()))
+            throw std::invalid_argument("model value outside the requested precision range");
+        return static_cast<P>(v);
+    }
+    static std::vector<P> castv(const std::vector<double>& v) {
+        std::vector<P> o(v.size());
+        for (std::size_t i = 0; i < v.size(); ++i) o[i] = cast(v[i]);
+        return o;
+    }
+
+    void load(const std::string& path) {
+        const Value j = json_lite::parse_file(path);
+        if (j.get_int("symmetrix_format_version", 1) != 4)
+            throw std::invalid_argument("only Symmetrix MACE format version 4 is supported");
+        if (j.get_string("h1_affine_mode", "") != "m0_composite")
+            throw std::invalid_argument("only h1_affine_mode 'm0_composite' is supported");
+        if (j.get_string("radial_representation", "") != "compact")
+            throw std::invalid_argument("only the compact radial representation is supported");
+        if (j.get_bool("has_zbl", false) || j.get_bool("A0_scaled", false) ||
+            j.get_bool("A1_scaled", false) || j.get_bool("has_field_coupling", false) ||
+            j.get_bool("first_interaction_residual", false) || j.get_bool("single_layer_readout", false))
+            throw std::invalid_argument("model features outside the supported MACE path");
+        num_elements = j.at("num_elements").as_int();
+        C = j.at("num_channels").as_int();
+        r_cut = j.at("r_cut").as_number();
+        l_max = j.at("l_max").as_int();
+        L_max = j.at("L_max").as_int();
+        num_lm = (l_max + 1) * (l_max + 1);
+        num_LM = (L_max + 1) * (L_max + 1);
+        if (l_max > 3 || L_max > l_max) throw std::invalid_argument("l_max must be <= 3");
+        atomic_numbers = j.at("atomic_numbers").as_ints();
+        atomic_energies = j.at("atomic_energies").as_doubles();
+        radial.load(j.at("compact_radial"), r_cut);
+        H0 = castv(j.at("H0_weights").as_doubles());
+        const Value& a0 = j.at("A0_weights");
+        A0_w.resize(num_elements);
+        for (int t = 0; t < num_elements; ++t)
+            for (int l = 0; l <= l_max; ++l) A0_w[t].push_back(castv(a0.at(t).at(l).as_doubles()));
+        // M0
+        const Value& m0m = j.at("M0_monomials");
+        const Value& m0w = j.at("M0_weights");
+        M0_monos.resize(num_LM);
+        M0_coef.assign(static_cast<std::size_t>(num_elements) * num_LM, {});
+        for (int LM = 0; LM < num_LM; ++LM) {
+            const Value& ml = m0m.at(std::to_string(LM));
+            std::vector<std::vector<int>> monos;
+            for (std::size_t i = 0; i < ml.size(); ++i) monos.push_back(ml.at(i).as_ints());
+            M0_monos[LM] = dedupe_monomials(monos);
+            const int T = static_cast<int>(M0_monos[LM].monos.size());
+            for (int t = 0; t < num_elements; ++t) {
+                auto& dst = M0_coef[t * num_LM + LM];
+                dst.resize(static_cast<std::size_t>(C) * T);
+                const Value& wl = m0w.at(std::to_string(t)).at(std::to_string(LM));
+                for (int k = 0; k < C; ++k) {
+                    const auto cf = wl.at(std::to_string(k)).as_doubles();
+                    if (cf.size() != monos.size()) throw std::invalid_argument("M0 coefficient count mismatch");
+                    for (int s = 0; s < T; ++s) dst[k * T + s] = cast(cf[M0_monos[LM].source_index[s]]);
+                }
+            }
+        }
+        H1_w = castv(j.at("H1_weights").as_doubles());
+        Phi1_l = j.at("Phi1_l").as_ints();
+        Phi1_l1 = j.at("Phi1_l1").as_ints();
+        Phi1_l2 = j.at("Phi1_l2").as_ints();
+        Phi1_lme = j.at("Phi1_lme").as_ints();
+        Phi1_row = j.at("Phi1_lelm1lm2").as_ints();
+        Phi1_cg = castv(j.at("Phi1_clebsch_gordan").as_doubles());
+        num_lme = 0;
+        for (int l : Phi1_l) num_lme += 2 * l + 1;
+        num_rows = 0;
+        for (std::size_t p = 0; p < Phi1_l.size(); ++p) num_rows += (2 * Phi1_l1[p] + 1) * (2 * Phi1_l2[p] + 1);
+        num_e.assign(l_max + 1, 0);
+        for (int l : Phi1_l) num_e[l] += 1;
+        lme_base.assign(l_max + 2, 0);
+        for (int l = 0; l <= l_max; ++l) lme_base[l + 1] = lme_base[l] + (2 * l + 1) * num_e[l];
+        const Value& a1 = j.at("A1_weights");
+        for (int l = 0; l <= l_max; ++l) A1_w.push_back(castv(a1.at(l).as_doubles()));
+        // M1
+        const Value& m1m = j.at("M1_monomials");
+        std::vector<std::vector<int>> monos1;
+        for (std::size_t i = 0; i < m1m.size(); ++i) monos1.push_back(m1m.at(i).as_ints());
+        M1_monos = dedupe_monomials(monos1);
+        const int T1 = static_cast<int>(M1_monos.monos.size());
+        const Value& m1w = j.at("M1_weights");
+        M1_coef.resize(num_elements);
+        for (int t = 0; t < num_elements; ++t) {
+            M1_coef[t].resize(static_cast<std::size_t>(C) * T1);
+            for (int k = 0; k < C; ++k) {
+                const auto cf = m1w.at(std::to_string(t)).at(std::to_string(k)).as_doubles();
+                for (int s = 0; s < T1; ++s) M1_coef[t][k * T1 + s] = cast(cf[M1_monos.source_index[s]]);
+            }
+        }
+        // H2 and readouts: the OpenMP backend keeps H2 weights in Precision and
+        // accumulates H2 in FP64 (mace_kokkos.hpp:1805-1816).
+        const Value& t2 = j.at("H2_weights_for_M0");
+        for (int t = 0; t < num_elements; ++t) {
+            const auto w = t2.at(t).as_doubles();
+            std::vector<double> r(w.size());
+            for (std::size_t i = 0; i < w.size(); ++i) r[i] = static_cast<double>(cast(w[i]));
+            H2_T.push_back(r);
+        }
+        {
+            const auto w = j.at("H2_weights_for_M1").as_doubles();
+            H2_M1.resize(w.size());
+            for (std::size_t i = 0; i < w.size(); ++i) H2_M1[i] = static_cast<double>(cast(w[i]));
+        }
+        q = j.at("readout_1_weights_for_M0").as_doubles();
+        hidden = j.get_int("readout_2_hidden_size", 16);
+        W1 = j.at("readout_2_weights_1").as_doubles();
+        W2 = j.at("readout_2_weights_2").as_doubles();
+        readout_scale = j.at("readout_2_scale_factor").as_number();
+        if (W1.size() != static_cast<std::size_t>(hidden) * C || W2.size() != static_cast<std::size_t>(hidden))
+            throw std::invalid_argument("readout weights do not match the hidden size");
+        type_to_active.assign(num_elements, -1);
+    }
+
+    // mace.cpp:119-214
+    void prepare_active_types(const int* node_types, int n) {
+        std::vector<int> req(node_types, node_types + n);
+        std::sort(req.begin(), req.end());
+        req.erase(std::unique(req.begin(), req.end()), req.end());
+        if (req.empty()) throw std::invalid_argument("no active types");
+        for (int t : req)
+            if (t < 0 || t >= num_elements) throw std::out_of_range("type index out of range");
+        if (req == active_types) return;
+        std::vector<std::vector<double>> v0, d0, v1, d1;
+        radial.tabulate(radial.R0, v0, d0);
+        radial.tabulate(radial.R1, v1, d1);
+        auto tof = [](const std::vector<std::vector<double>>& a) {
+            std::vector<std::vector<P>> o(a.size());
+            for (std::size_t i = 0; i < a.size(); ++i) o[i] = castv(a[i]);
+            return o;
+        };
+        const P hp = cast(radial.h), x0 = cast(radial.grid_min);
+        spl0.clear();
+        spl1.clear();
+        const int na = static_cast<int>(req.size());
+        // features do not depend on the pair without a distance transform,
+        // so each pair's tables are the same tabulation
+        const auto fv0 = tof(v0), fd0 = tof(d0), fv1 = tof(v1), fd1 = tof(d1);
+        const auto s0 = std::make_shared<SplineSet<P>>(hp, fv0, fd0, x0);
+        const auto s1 = std::make_shared<SplineSet<P>>(hp, fv1, fd1, x0);
+        for (int a = 0; a < na; ++a)
+            for (int b = a; b < na; ++b) {
+                spl0.push_back(s0);
+                spl1.push_back(s1);
+            }
+        type_to_active.assign(num_elements, -1);
+        for (int a = 0; a < na; ++a) type_to_active[req[a]] = a;
+        active_types = req;
+    }
+
+    int pair_index(int ti, int tj) const {
+        const int a = type_to_active[ti], b = type_to_active[tj];
+        if (a < 0 || b < 0) throw std::runtime_error("radial cache not prepared for a type");
+        const int n = static_cast<int>(active_types.size());
+        return a <= b ? a * (2 * n - a - 1) / 2 + b : b * (2 * n - b - 1) / 2 + a;
+    }
+
+    int row_base_of_path(int p) const {
+        int acc = 0;
+        for (int i = 0; i < p; ++i) acc += (2 * Phi1_l1[i] + 1) * (2 * Phi1_l2[i] + 1);
+        return acc;
+    }
+
+    void evaluate(int n, const int* types, const int* num_neigh, const int* neigh, const int* neigh_types,
+                  const double* xyz, const double* r) {
+        prepare_active_types(types, n);
+        std::vector<long long> off(n + 1, 0);
+        for (int i = 0; i < n; ++i) off[i + 1] = off[i] + num_neigh[i];
+        const long long E = off[n];
+        for (long long e = 0; e < E; ++e)
+            if (neigh[e] < 0 || neigh[e] >= n) throw std::invalid_argument("neighbour index out of range");
+        const int nY = num_lm;
+        const std::size_t Cs = static_cast<std::size_t>(C);
+        Y.assign(static_cast<std::size_t>(E) * nY, P(0));
+        Ygrad.assign(static_cast<std::size_t>(E) * 3 * nY, P(0));
+        std::vector<P> dirs(static_cast<std::size_t>(E) * 3, P(0));
+        std::vector<char> active(E, 0);
+#pragma omp parallel for schedule(static)
+        for (long long e = 0; e < E; ++e) {
+            if (!(r[e] < r_cut)) continue;  // direct plan: Y = 0, no force
+            active[e] = 1;
+            P d[3];
+            for (int c = 0; c < 3; ++c) d[c] = static_cast<P>(xyz[3 * e + c] / r[e]);
+            for (int c = 0; c < 3; ++c) dirs[3 * e + c] = d[c];
+            edge_harmonics<P>(l_max, d, static_cast<P>(r[e]), &Y[e * nY], &Ygrad[e * 3 * nY]);
+        }
+
+        // ---- A0 (mace.cpp:1356-1403)
+        A0.assign(static_cast<std::size_t>(n) * nY * Cs, P(0));
+#pragma omp parallel for schedule(dynamic, 16)
+        for (int i = 0; i < n; ++i) {
+            std::vector<P> phi(nY * Cs, P(0)), rad(Cs);
+            for (long long e = off[i]; e < off[i + 1]; ++e) {
+                if (!active[e]) continue;
+                const auto& sp = *spl0[pair_index(types[i], neigh_types[e])];
+                const auto pt = sp.point(static_cast<P>(r[e]));
+                const P* cf = sp.coefficients(pt);
+                const int ns = sp.num_splines;
+                const P* h0 = &H0[static_cast<std::size_t>(neigh_types[e]) * Cs];
+                for (int l = 0; l <= l_max; ++l) {
+                    for (int k = 0; k < C; ++k) {
+                        const int f = l * C + k;
+                        rad[k] = cf[f] + cf[ns + f] * pt.x + cf[2 * ns + f] * pt.xx + cf[3 * ns + f] * pt.xxx;
+                    }
+                    for (int m = -l; m <= l; ++m) {
+                        const int lm = l * l + l + m;
+                        const P y = Y[e * nY + lm];
+                        P* dst = &phi[lm * Cs];
+                        for (int k = 0; k < C; ++k) dst[k] += rad[k] * y * h0[k];
+                    }
+                }
+            }
+            for (int l = 0; l <= l_max; ++l) {
+                const P* W = A0_w[types[i]][l].data();
+                for (int m = 0; m < 2 * l + 1; ++m) {
+                    const P* src = &phi[(l * l + m) * Cs];
+                    P* dst = &A0[(static_cast<std::size_t>(i) * nY + l * l + m) * Cs];
+                    for (int kp = 0; kp < C; ++kp) {
+                        const P a = src[kp];
+                        const P* wr = W + kp * Cs;
+                        for (int k = 0; k < C; ++k) dst[k] += a * wr[k];
+                    }
+                }
+            }
+        }
+
+        // ---- M0 (mace.cpp:1639-1663)
+        M0.assign(static_cast<std::size_t>(n) * num_LM * Cs, P(0));
+        M0_grad.assign(static_cast<std::size_t>(n) * num_LM * nY * Cs, P(0));
+#pragma omp parallel for schedule(static)
+        for (int i = 0; i < n; ++i) {
+            P x[16], g[16];
+            for (int LM = 0; LM < num_LM; ++LM) {
+                const int T = static_cast<int>(M0_monos[LM].monos.size());
+                const P* coef = M0_coef[types[i] * num_LM + LM].data();
+                for (int k = 0; k < C; ++k) {
+                    for (int v = 0; v < nY; ++v) x[v] = A0[(static_cast<std::size_t>(i) * nY + v) * Cs + k];
+                    M0[(static_cast<std::size_t>(i) * num_LM + LM) * Cs + k] =
+                        poly_eval_grad<P>(M0_monos[LM], coef + static_cast<std::size_t>(k) * T, x, g, nY);
+                    for (int v = 0; v < nY; ++v)
+                        M0_grad[((static_cast<std::size_t>(i) * num_LM + LM) * nY + v) * Cs + k] = g[v];
+                }
+            }
+        }
+
+        // ---- H1 and the v4 scalar capture (mace.cpp:1691-1783)
+        H1.assign(static_cast<std::size_t>(n) * num_LM * Cs, P(0));
+        xaff.assign(static_cast<std::size_t>(n) * Cs, P(0));
+#pragma omp parallel for schedule(static)
+        for (int i = 0; i < n; ++i) {
+            for (int k = 0; k < C; ++k) xaff[i * Cs + k] = M0[static_cast<std::size_t>(i) * num_LM * Cs + k];
+            for (int l = 0; l <= L_max; ++l)
+                for (int m = 0; m < 2 * l + 1; ++m) {
+                    const P* src = &M0[(static_cast<std::size_t>(i) * num_LM + l * l + m) * Cs];
+                    P* dst = &H1[(static_cast<std::size_t>(i) * num_LM + l * l + m) * Cs];
+                    const P* W = &H1_w[static_cast<std::size_t>(l) * Cs * Cs];
+                    for (int kp = 0; kp < C; ++kp) {
+                        const P a = src[kp];
+                        for (int k = 0; k < C; ++k) dst[k] += a * W[kp * Cs + k];
+                    }
+                }
+        }
+
+        // ---- Phi1 streamed (mace.cpp:2023-2084)
+        const int np = static_cast<int>(Phi1_l.size());
+        std::vector<int> row_base(np);
+        for (int p = 0; p < np; ++p) row_base[p] = row_base_of_path(p);
+        Phi1.assign(static_cast<std::size_t>(n) * num_lme * Cs, P(0));
+#pragma omp parallel for schedule(dynamic, 16)
+        for (int i = 0; i < n; ++i) {
+            std::vector<P> rows(static_cast<std::size_t>(num_rows) * Cs, P(0)), rad(Cs);
+            for (long long e = off[i]; e < off[i + 1]; ++e) {
+                if (!active[e]) continue;
+                const auto& sp = *spl1[pair_index(types[i], neigh_types[e])];
+                const auto pt = sp.point(static_cast<P>(r[e]));
+                const P* cf = sp.coefficients(pt);
+                const int ns = sp.num_splines;
+                const P* Hj = &H1[static_cast<std::size_t>(neigh[e]) * num_LM * Cs];
+                for (int p = 0; p < np; ++p) {
+                    for (int k = 0; k < C; ++k) {
+                        const int f = p * C + k;
+                        rad[k] = cf[f] + cf[ns + f] * pt.x + cf[2 * ns + f] * pt.xx + cf[3 * ns + f] * pt.xxx;
+                    }
+                    const int l1 = Phi1_l1[p], l2 = Phi1_l2[p];
+                    int row = row_base[p];
+                    for (int lm1 = l1 * l1; lm1 <= l1 * (l1 + 2); ++lm1) {
+                        const P y = Y[e * nY + lm1];
+                        for (int lm2 = l2 * l2; lm2 <= l2 * (l2 + 2); ++lm2) {
+                            const P* h = Hj + lm2 * Cs;
+                            P* dst = &rows[row * Cs];
+                            for (int k = 0; k < C; ++k) dst[k] += rad[k] * y * h[k];
+                            ++row;
+                        }
+                    }
+                }
+            }
+            P* out = &Phi1[static_cast<std::size_t>(i) * num_lme * Cs];
+            for (std::size_t t = 0; t < Phi1_cg.size(); ++t) {
+                const P c = Phi1_cg[t];
+                const P* src = &rows[Phi1_row[t] * Cs];
+                P* dst = out + Phi1_lme[t] * Cs;
+                for (int k = 0; k < C; ++k) dst[k] += c * src[k];
+            }
+        }
+
+        // ---- A1 (mace.cpp:2305-2341)
+        A1.assign(static_cast<std::size_t>(n) * nY * Cs, P(0));
+#pragma omp parallel for schedule(static)
+        for (int i = 0; i < n; ++i) {
+            for (int l = 0; l <= l_max; ++l) {
+                const int ne = num_e[l];
+                const P* W = A1_w[l].data();
+                for (int m = 0; m < 2 * l + 1; ++m) {
+                    P* dst = &A1[(static_cast<std::size_t>(i) * nY + l * l + m) * Cs];
+                    for (int e = 0; e < ne; ++e) {
+                        const P* src = &Phi1[(static_cast<std::size_t>(i) * num_lme + lme_base[l] + m * ne + e) * Cs];
+                        for (int kp = 0; kp < C; ++kp) {
+                            const P a = src[kp];
+                            const P* wr = W + (static_cast<std::size_t>(e) * Cs + kp) * Cs;
+                            for (int k = 0; k < C; ++k) dst[k] += a * wr[k];
+                        }
+                    }
+                }
+            }
+        }
+
+        // ---- M1, H2, readouts, reverse H2 / M1 (mace.cpp:2461-2657)
+        const int T1 = static_cast<int>(M1_monos.monos.size());
+        M1.assign(static_cast<std::size_t>(n) * Cs, P(0));
+        M1_grad.assign(static_cast<std::size_t>(n) * nY * Cs, P(0));
+        H2.assign(static_cast<std::size_t>(n) * Cs, 0.0);
+        H2_adj.assign(static_cast<std::size_t>(n) * Cs, 0.0);
+        direct.assign(static_cast<std::size_t>(n) * Cs, 0.0);
+        node_energies.assign(n, 0.0);
+        A1_adj.assign(static_cast<std::size_t>(n) * nY * Cs, P(0));
+#pragma omp parallel for schedule(static)
+        for (int i = 0; i < n; ++i) {
+            P x[16], g[16];
+            const int t = types[i];
+            for (int k = 0; k < C; ++k) {
+                for (int v = 0; v < nY; ++v) x[v] = A1[(static_cast<std::size_t>(i) * nY + v) * Cs + k];
+                M1[i * Cs + k] = poly_eval_grad<P>(M1_monos, M1_coef[t].data() + static_cast<std::size_t>(k) * T1, x, g, nY);
+                for (int v = 0; v < nY; ++v) M1_grad[(static_cast<std::size_t>(i) * nY + v) * Cs + k] = g[v];
+            }
+            double* h2 = &H2[i * Cs];
+            for (int o = 0; o < C; ++o) {
+                double s = 0.0;
+                for (int in = 0; in < C; ++in) s += H2_T[t][in * Cs + o] * static_cast<double>(xaff[i * Cs + in]);
+                for (int in = 0; in < C; ++in) s += H2_M1[in * Cs + o] * static_cast<double>(M1[i * Cs + in]);
+                h2[o] = s;
+            }
+            double e = atomic_energies[t];
+            for (int k = 0; k < C; ++k) e += q[k] * static_cast<double>(xaff[i * Cs + k]);
+            // readout_2 MLP [C, hidden, 1] and its gradient
+            std::vector<double> z(hidden), act(hidden), dact(hidden);
+            for (int hdn = 0; hdn < hidden; ++hdn) {
+                double s = 0.0;
+                for (int k = 0; k < C; ++k) s += W1[hdn * Cs + k] * h2[k];
+                const double sg = 1.0 / (1.0 + std::exp(-s));
+                z[hdn] = s;
+                act[hdn] = readout_scale * s * sg;
+                dact[hdn] = readout_scale * sg + readout_scale * s * sg * (1.0 - sg);
+            }
+            double out = 0.0;
+            for (int hdn = 0; hdn < hidden; ++hdn) out += W2[hdn] * act[hdn];
+            node_energies[i] = e + out;
+            double* h2a = &H2_adj[i * Cs];
+            for (int k = 0; k < C; ++k) {
+                double s = 0.0;
+                for (int hdn = 0; hdn < hidden; ++hdn) s += W2[hdn] * dact[hdn] * W1[hdn * Cs + k];
+                h2a[k] = s;
+            }
+            // reverse_H2 (m0_composite): direct = q + T_z H2_adj; M1_adj = W H2_adj
+            for (int in = 0; in < C; ++in) {
+                double s = q[in], s1 = 0.0;
+                for (int o = 0; o < C; ++o) {
+                    s += H2_T[t][in * Cs + o] * h2a[o];
+                    s1 += H2_M1[in * Cs + o] * h2a[o];
+                }
+                direct[i * Cs + in] = s;
+                const P m1adj = static_cast<P>(s1);
+                for (int v = 0; v < nY; ++v)
+                    A1_adj[(static_cast<std::size_t>(i) * nY + v) * Cs + in] =
+                        M1_grad[(static_cast<std::size_t>(i) * nY + v) * Cs + in] * m1adj;
+            }
+        }
+
+        // ---- reverse A1 (mace.cpp:2343-2379)
+        dPhi1.assign(static_cast<std::size_t>(n) * num_lme * Cs, P(0));
+#pragma omp parallel for schedule(static)
+        for (int i = 0; i < n; ++i) {
+            for (int l = 0; l <= l_max; ++l) {
+                const int ne = num_e[l];
+                const P* W = A1_w[l].data();
+                for (int m = 0; m < 2 * l + 1; ++m) {
+                    const P* src = &A1_adj[(static_cast<std::size_t>(i) * nY + l * l + m) * Cs];
+                    for (int e = 0; e < ne; ++e) {
+                        P* dst = &dPhi1[(static_cast<std::size_t>(i) * num_lme + lme_base[l] + m * ne + e) * Cs];
+                        for (int k = 0; k < C; ++k) {
+                            const P* wr = W + (static_cast<std::size_t>(e) * Cs + k) * Cs;
+                            P s = 0;
+                            for (int kp = 0; kp < C; ++kp) s += src[kp] * wr[kp];
+                            dst[k] = s;
+                        }
+                    }
+                }
+            }
+        }
+
+        // ---- reverse Phi1 (mace.cpp:2199-2303): receiver-owned edge forces,
+        // source adjoint via the source transpose (FP64 accumulation).
+        node_forces.assign(static_cast<std::size_t>(E) * 3, 0.0);
+        std::vector<P> dPhi1r(static_cast<std::size_t>(n) * num_rows * Cs, P(0));
+#pragma omp parallel for schedule(static)
+        for (int i = 0; i < n; ++i) {
+            P* rows = &dPhi1r[static_cast<std::size_t>(i) * num_rows * Cs];
+            const P* src = &dPhi1[static_cast<std::size_t>(i) * num_lme * Cs];
+            for (std::size_t t = 0; t < Phi1_cg.size(); ++t) {
+                const P c = Phi1_cg[t];
+                const P* a = src + Phi1_lme[t] * Cs;
+                P* d = rows + Phi1_row[t] * Cs;
+                for (int k = 0; k < C; ++k) d[k] += c * a[k];
+            }
+        }
+        std::vector<int> recv(E);
+        for (int i = 0; i < n; ++i)
+            for (long long e = off[i]; e < off[i + 1]; ++e) recv[e] = i;
+        auto edge_r1 = [&](long long e, P* rad, P* drad) {
+            const auto& sp = *spl1[pair_index(types[recv[e]], neigh_types[e])];
+            const auto pt = sp.point(static_cast<P>(r[e]));
+            const P* cf = sp.coefficients(pt);
+            const int ns = sp.num_splines;
+            for (int f = 0; f < ns; ++f) {
+                rad[f] = cf[f] + cf[ns + f] * pt.x + cf[2 * ns + f] * pt.xx + cf[3 * ns + f] * pt.xxx;
+                if (drad) drad[f] = cf[ns + f] + P(2.0) * cf[2 * ns + f] * pt.x + P(3.0) * cf[3 * ns + f] * pt.xx;
+            }
+        };
+#pragma omp parallel
+        {
+        std::vector<P> rad(np * Cs), drad(np * Cs);
+#pragma omp for schedule(dynamic, 64)
+        for (long long e = 0; e < E; ++e) {
+            if (!active[e]) continue;
+            const int i = recv[e];
+            edge_r1(e, rad.data(), drad.data());
+            const P* rows = &dPhi1r[static_cast<std::size_t>(i) * num_rows * Cs];
+            const P* Hj = &H1[static_cast<std::size_t>(neigh[e]) * num_LM * Cs];
+            const P* y = &Y[e * nY];
+            const P* g = &Ygrad[e * 3 * nY];
+            double f[3] = {0, 0, 0};
+            for (int p = 0; p < np; ++p) {
+                const int l1 = Phi1_l1[p], l2 = Phi1_l2[p];
+                int row = row_base[p];
+                for (int lm1 = l1 * l1; lm1 <= l1 * (l1 + 2); ++lm1)
+                    for (int lm2 = l2 * l2; lm2 <= l2 * (l2 + 2); ++lm2) {
+                        const P* adj = rows + row * Cs;
+                        const P* h = Hj + lm2 * Cs;
+                        P radial_sum = 0, angular_sum = 0;
+                        for (int k = 0; k < C; ++k) {
+                            radial_sum += adj[k] * drad[p * Cs + k] * h[k];
+                            angular_sum += adj[k] * rad[p * Cs + k] * h[k];
+                        }
+                        for (int c = 0; c < 3; ++c)
+                            f[c] -= static_cast<double>(dirs[3 * e + c] * radial_sum * y[lm1] + angular_sum * g[c * nY + lm1]);
+                        ++row;
+                    }
+            }
+            for (int c = 0; c < 3; ++c) node_forces[3 * e + c] += f[c];
+        }
+        }
+        // source adjoint over the source transpose (deterministic, no atomics)
+        std::vector<long long> soff(n + 1, 0);
+        for (long long e = 0; e < E; ++e) soff[neigh[e] + 1] += 1;
+        for (int s = 0; s < n; ++s) soff[s + 1] += soff[s];
+        std::vector<long long> sedges(E), cursor(soff.begin(), soff.end() - 1);
+        for (long long e = 0; e < E; ++e) sedges[cursor[neigh[e]]++] = e;
+        H1_adj.assign(static_cast<std::size_t>(n) * num_LM * Cs, P(0));
+#pragma omp parallel for schedule(dynamic, 16)
+        for (int s = 0; s < n; ++s) {
+            std::vector<double> acc(num_LM * Cs, 0.0);
+            std::vector<P> rad(np * Cs);
+            for (long long q2 = soff[s]; q2 < soff[s + 1]; ++q2) {
+                const long long e = sedges[q2];
+                if (!active[e]) continue;
+                edge_r1(e, rad.data(), nullptr);
+                const P* rows = &dPhi1r[static_cast<std::size_t>(recv[e]) * num_rows * Cs];
+                const P* y = &Y[e * nY];
+                for (int p = 0; p < np; ++p) {
+                    const int l1 = Phi1_l1[p], l2 = Phi1_l2[p];
+                    int row = row_base[p];
+                    for (int lm1 = l1 * l1; lm1 <= l1 * (l1 + 2); ++lm1)
+                        for (int lm2 = l2 * l2; lm2 <= l2 * (l2 + 2); ++lm2) {
+                            const P* adj = rows + row * Cs;
+                            double* dst = &acc[lm2 * Cs];
+                            for (int k = 0; k < C; ++k)
+                                dst[k] += static_cast<double>(rad[p * Cs + k] * y[lm1] * adj[k]);
+                            ++row;
+                        }
+                }
+            }
+            for (int v = 0; v < num_LM * C; ++v)
+                H1_adj[static_cast<std::size_t>(s) * num_LM * Cs + v] = static_cast<P>(acc[v]);
+        }
+
+        // ---- reverse H1 + direct adjoint (mace.cpp:1727-1757, 1785-1814)
+        M0_adj.assign(static_cast<std::size_t>(n) * num_LM * Cs, P(0));
+#pragma omp parallel for schedule(static)
+        for (int i = 0; i < n; ++i) {
+            for (int l = 0; l <= L_max; ++l)
+                for (int m = 0; m < 2 * l + 1; ++m) {
+                    const P* src = &H1_adj[(static_cast<std::size_t>(i) * num_LM + l * l + m) * Cs];
+                    P* dst = &M0_adj[(static_cast<std::size_t>(i) * num_LM + l * l + m) * Cs];
+                    const P* W = &H1_w[static_cast<std::size_t>(l) * Cs * Cs];
+                    for (int k = 0; k < C; ++k) {
+                        P s = 0;
+                        for (int kp = 0; kp < C; ++kp) s += src[kp] * W[k * Cs + kp];
+                        dst[k] = s;
+                    }
+                }
+            for (int k = 0; k < C; ++k)
+                M0_adj[static_cast<std::size_t>(i) * num_LM * Cs + k] += static_cast<P>(direct[i * Cs + k]);
+        }
+
+        // ---- reverse M0 (mace.cpp:1665-1689)
+        A0_adj.assign(static_cast<std::size_t>(n) * nY * Cs, P(0));
+#pragma omp parallel for schedule(static)
+        for (int i = 0; i < n; ++i)
+            for (int v = 0; v < nY; ++v) {
+                P* dst = &A0_adj[(static_cast<std::size_t>(i) * nY + v) * Cs];
+                for (int LM = 0; LM < num_LM; ++LM) {
+                    const P* g = &M0_grad[((static_cast<std::size_t>(i) * num_LM + LM) * nY + v) * Cs];
+                    const P* a = &M0_adj[(static_cast<std::size_t>(i) * num_LM + LM) * Cs];
+                    for (int k = 0; k < C; ++k) dst[k] += g[k] * a[k];
+                }
+            }
+
+        // ---- reverse A0 (mace.cpp:1486-1560)
+#pragma omp parallel for schedule(dynamic, 16)
+        for (int i = 0; i < n; ++i) {
+            std::vector<P> padj(nY * Cs, P(0)), rad(Cs), drad(Cs);
+            for (int l = 0; l <= l_max; ++l) {
+                const P* W = A0_w[types[i]][l].data();
+                for (int m = 0; m < 2 * l + 1; ++m) {
+                    const P* src = &A0_adj[(static_cast<std::size_t>(i) * nY + l * l + m) * Cs];
+                    P* dst = &padj[(l * l + m) * Cs];
+                    for (int k = 0; k < C; ++k) {
+                        P s = 0;
+                        for (int kp = 0; kp < C; ++kp) s += src[kp] * W[k * Cs + kp];
+                        dst[k] = s;
+                    }
+                }
+            }
+            for (long long e = off[i]; e < off[i + 1]; ++e) {
+                if (!active[e]) continue;
+                const auto& sp = *spl0[pair_index(types[i], neigh_types[e])];
+                const auto pt = sp.point(static_cast<P>(r[e]));
+                const P* cf = sp.coefficients(pt);
+                const int ns = sp.num_splines;
+                const P* h0 = &H0[static_cast<std::size_t>(neigh_types[e]) * Cs];
+                const P* y = &Y[e * nY];
+                const P* g = &Ygrad[e * 3 * nY];
+                double f[3] = {0, 0, 0};
+                for (int l = 0; l <= l_max; ++l) {
+                    for (int k = 0; k < C; ++k) {
+                        const int fi = l * C + k;
+                        rad[k] = cf[fi] + cf[ns + fi] * pt.x + cf[2 * ns + fi] * pt.xx + cf[3 * ns + fi] * pt.xxx;
+                        drad[k] = cf[ns + fi] + P(2.0) * cf[2 * ns + fi] * pt.x + P(3.0) * cf[3 * ns + fi] * pt.xx;
+                    }
+                    for (int m = -l; m <= l; ++m) {
+                        const int lm = l * l + l + m;
+                        const P* adj = &padj[lm * Cs];
+                        P radial_sum = 0, angular_sum = 0;
+                        for (int k = 0; k < C; ++k) {
+                            radial_sum += adj[k] * drad[k] * h0[k];
+                            angular_sum += adj[k] * rad[k] * h0[k];
+                        }
+                        for (int c = 0; c < 3; ++c)
+                            f[c] -= static_cast<double>(dirs[3 * e + c] * radial_sum * y[lm] + angular_sum * g[c * nY + lm]);
+                    }
+                }
+                for (int c = 0; c < 3; ++c) node_forces[3 * e + c] += f[c];
+            }
+        }
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Neighbour list (neighbor_graph_kokkos.cpp:38-405), IEEE double, no FMA.
+// ---------------------------------------------------------------------------
+
+static int floor_div(int a, int b) {
+    const int q = a / b, r = a % b;
+    return q - ((r != 0 && r < 0) ? 1 : 0);
+}
+
+struct Graph {
+    std::vector<int> num_neigh, offsets, sources, shifts;
+    std::vector<double> fractional_xyz;
+};
+
+static void build_graph(const double* pos, int n, const double* cell, const double* inv, double cutoff, Graph& g,
+                        bool fill) {
+    if (!std::isfinite(cutoff) || !(cutoff > 0.0)) throw std::invalid_argument("cutoff must be positive");
+    for (int row = 0; row < 3; ++row)
+        for (int col = 0; col < 3; ++col) {
+            double prod = 0.0;
+            for (int k = 0; k < 3; ++k) prod += cell[3 * row + k] * inv[3 * k + col];
+            if (std::abs(prod - (row == col ? 1.0 : 0.0)) > 1e-9)
+                throw std::invalid_argument("cell and inverse cell are inconsistent");
+        }
+    std::vector<double> frac(3 * n), wfrac(3 * n), wpos(3 * n);
+    std::vector<int> wrap(3 * n);
+    for (int a = 0; a < n; ++a) {
+        double f[3];
+        for (int ax = 0; ax < 3; ++ax) {
+            double v = 0.0;
+            for (int c = 0; c < 3; ++c) v += pos[3 * a + c] * inv[3 * c + ax];
+            frac[3 * a + ax] = v;
+            const int w = static_cast<int>(std::floor(v));
+            v -= w;
+            f[ax] = v;
+            wfrac[3 * a + ax] = v;
+            wrap[3 * a + ax] = w;
+        }
+        for (int c = 0; c < 3; ++c) {
+            double v = 0.0;
+            for (int ax = 0; ax < 3; ++ax) v += f[ax] * cell[3 * ax + c];
+            wpos[3 * a + c] = v;
+        }
+    }
+    int bins[3], reach[3];
+    for (int ax = 0; ax < 3; ++ax) {
+        double ins = 0.0;
+        for (int c = 0; c < 3; ++c) ins += inv[3 * c + ax] * inv[3 * c + ax];
+        if (!(ins > 0.0)) throw std::invalid_argument("cell must be invertible");
+        const double face = 1.0 / std::sqrt(ins);
+        bins[ax] = std::max(1, static_cast<int>(std::floor(face / cutoff)));
+        const double rch = std::ceil(cutoff * std::sqrt(ins) * bins[ax]) + 1.0;
+        reach[ax] = std::max(1, static_cast<int>(rch));
+    }
+    const int nb = bins[0] * bins[1] * bins[2];
+    std::vector<int> abin(n), bsize(nb, 0);
+    for (int a = 0; a < n; ++a) {
+        const int x = std::min(bins[0] - 1, static_cast<int>(wfrac[3 * a] * bins[0]));
+        const int y = std::min(bins[1] - 1, static_cast<int>(wfrac[3 * a + 1] * bins[1]));
+        const int z = std::min(bins[2] - 1, static_cast<int>(wfrac[3 * a + 2] * bins[2]));
+        abin[a] = (z * bins[1] + y) * bins[0] + x;
+        bsize[abin[a]] += 1;
+    }
+    std::vector<int> boff(nb + 1, 0);
+    for (int b = 0; b < nb; ++b) boff[b + 1] = boff[b] + bsize[b];
+    std::vector<int> batoms(n), cur(boff.begin(), boff.end() - 1);
+    for (int a = 0; a < n; ++a) batoms[cur[abin[a]]++] = a;  // ascending atom order within a bin
+    const double cut2 = cutoff * cutoff;
+    g.num_neigh.assign(n, 0);
+    std::vector<long long> counts(n, 0);
+    auto visit = [&](int rcv, bool do_fill, long long base) {
+        const int rb = abin[rcv];
+        const int rx = rb % bins[0], ry = (rb / bins[0]) % bins[1], rz = rb / (bins[0] * bins[1]);
+        long long local = 0;
+        for (int dz = -reach[2]; dz <= reach[2]; ++dz) {
+            const int raw_z = rz + dz, sz = floor_div(raw_z, bins[2]), bz = raw_z - sz * bins[2];
+            for (int dy = -reach[1]; dy <= reach[1]; ++dy) {
+                const int raw_y = ry + dy, sy = floor_div(raw_y, bins[1]), by = raw_y - sy * bins[1];
+                for (int dx = -reach[0]; dx <= reach[0]; ++dx) {
+                    const int raw_x = rx + dx, sx = floor_div(raw_x, bins[0]), bx = raw_x - sx * bins[0];
+                    const int sb = (bz * bins[1] + by) * bins[0] + bx;
+                    const int image[3] = {sx, sy, sz};
+                    for (int idx = boff[sb]; idx < boff[sb + 1]; ++idx) {
+                        const int src = batoms[idx];
+                        if (src == rcv && sx == 0 && sy == 0 && sz == 0) continue;
+                        double d2 = 0.0;
+                        for (int c = 0; c < 3; ++c) {
+                            double d = wpos[3 * src + c] - wpos[3 * rcv + c];
+                            for (int ax = 0; ax < 3; ++ax) d += image[ax] * cell[3 * ax + c];
+                            d2 += d * d;
+                        }
+                        if (d2 > cut2) continue;
+                        if (do_fill) {
+                            const long long e = base + local;
+                            g.sources[e] = src;
+                            for (int ax = 0; ax < 3; ++ax) {
+                                g.shifts[3 * e + ax] = image[ax] - wrap[3 * src + ax] + wrap[3 * rcv + ax];
+                                g.fractional_xyz[3 * e + ax] = wfrac[3 * src + ax] - wfrac[3 * rcv + ax] + image[ax];
+                            }
+                        }
+                        ++local;
+                    }
+                }
+            }
+        }
+        return local;
+    };
+#pragma omp parallel for schedule(dynamic, 64)
+    for (int a = 0; a < n; ++a) counts[a] = visit(a, false, 0);
+    long long total = 0;
+    g.offsets.assign(n + 1, 0);
+    for (int a = 0; a < n; ++a) {
+        g.offsets[a] = static_cast<int>(total);
+        g.num_neigh[a] = static_cast<int>(counts[a]);
+        total += counts[a];
+        if (total > std::numeric_limits<int>::max()) throw std::length_error("edge count exceeds 32 bits");
+    }
+    g.offsets[n] = static_cast<int>(total);
+    if (!fill) return;
+    g.sources.assign(total, 0);
+    g.shifts.assign(3 * total, 0);
+    g.fractional_xyz.assign(3 * total, 0.0);
+#pragma omp parallel for schedule(dynamic, 64)
+    for (int a = 0; a < n; ++a) visit(a, true, g.offsets[a]);
+}
+
+}  // namespace oracle
+
+// ---------------------------------------------------------------------------
+// C interface (ctypes)
+// ---------------------------------------------------------------------------
+
+using namespace oracle;
+
+struct OracleHandle {
+    int fp64 = 0;
+    std::unique_ptr<Mace<float>> f;
+    std::unique_ptr<Mace<double>> d;
+};
+
+template <class F>
+static int guarded(F&& f) {
+    try {
+        return f();
+    } catch (const std::exception& ex) {
+        oracle::last_error = ex.what();
+        return -1;
+    }
+}
+
+extern "C" {
+
+const char* oracle_last_error() { return oracle::last_error.c_str(); }
+
+void* oracle_load(const char* path, int fp64) {
+    try {
+        auto* h = new OracleHandle();
+        h->fp64 = fp64;
+        if (fp64) { h->d = std::make_unique<Mace<double>>(); h->d->load(path); }
+        else { h->f = std::make_unique<Mace<float>>(); h->f->load(path); }
+        return h;
+    } catch (const std::exception& ex) {
+        oracle::last_error = ex.what();
+        return nullptr;
+    }
+}
+
+void oracle_free(void* h) { delete static_cast<OracleHandle*>(h); }
+
+// info: [num_elements, C, l_max, L_max, num_lm, num_LM, num_paths, num_rows, num_lme, T_M1]
+int oracle_info(void* hv, int* info, double* r_cut) {
+    auto* h = static_cast<OracleHandle*>(hv);
+    auto fill = [&](auto& m) {
+        info[0] = m.num_elements; info[1] = m.C; info[2] = m.l_max; info[3] = m.L_max;
+        info[4] = m.num_lm; info[5] = m.num_LM; info[6] = static_cast<int>(m.Phi1_l.size());
+        info[7] = m.num_rows; info[8] = m.num_lme; info[9] = static_cast<int>(m.M1_monos.monos.size());
+        *r_cut = m.r_cut;
+    };
+    if (h->fp64) fill(*h->d); else fill(*h->f);
+    return 0;
+}
+
+int oracle_atomic_numbers(void* hv, int* out) {
+    auto* h = static_cast<OracleHandle*>(hv);
+    const auto& z = h->fp64 ? h->d->atomic_numbers : h->f->atomic_numbers;
+    std::copy(z.begin(), z.end(), out);
+    return 0;
+}
+
+int oracle_evaluate(void* hv, int n, const int* types, const int* num_neigh, const int* neigh,
+                    const int* neigh_types, const double* xyz, const double* r, double* energies,
+                    double* forces) {
+    return guarded([&]() -> int {
+        auto* h = static_cast<OracleHandle*>(hv);
+        long long E = 0;
+        for (int i = 0; i < n; ++i) E += num_neigh[i];
+        auto run = [&](auto& m) {
+            m.evaluate(n, types, num_neigh, neigh, neigh_types, xyz, r);
+            std::copy(m.node_energies.begin(), m.node_energies.end(), energies);
+            std::copy(m.node_forces.begin(), m.node_forces.end(), forces);
+        };
+        if (h->fp64) run(*h->d); else run(*h->f);
+        (void)E;
+        return 0;
+    });
+}
+
+// Stage buffers of the last evaluation, as float64: name in {Y, Ygrad, A0, M0,
+// M0_grad, H1, Phi1, A1, M1, H2, H2_adj, A1_adj, dPhi1, H1_adj, M0_adj, A0_adj}.
+long long oracle_stage(void* hv, const char* name, double* out, long long capacity) {
+    auto* h = static_cast<OracleHandle*>(hv);
+    auto get = [&](auto& m) -> long long {
+        const std::string s(name);
+        auto emit = [&](const auto& v) -> long long {
+            if (out && static_cast<long long>(v.size()) <= capacity)
+                for (std::size_t i = 0; i < v.size(); ++i) out[i] = static_cast<double>(v[i]);
+            return static_cast<long long>(v.size());
+        };
+        if (s == "Y") return emit(m.Y);
+        if (s == "Ygrad") return emit(m.Ygrad);
+        if (s == "A0") return emit(m.A0);
+        if (s == "M0") return emit(m.M0);
+        if (s == "M0_grad") return emit(m.M0_grad);
+        if (s == "H1") return emit(m.H1);
+        if (s == "Phi1") return emit(m.Phi1);
+        if (s == "A1") return emit(m.A1);
+        if (s == "M1") return emit(m.M1);
+        if (s == "H2") return emit(m.H2);
+        if (s == "H2_adj") return emit(m.H2_adj);
+        if (s == "A1_adj") return emit(m.A1_adj);
+        if (s == "dPhi1") return emit(m.dPhi1);
+        if (s == "H1_adj") return emit(m.H1_adj);
+        if (s == "M0_adj") return emit(m.M0_adj);
+        if (s == "A0_adj") return emit(m.A0_adj);
+        return -1;
+    };
+    return h->fp64 ? get(*h->d) : get(*h->f);
+}
+
+// Radial nodal tables of the model on its spline grid (FP64):
+// which 0 = R0, 1 = R1; values/derivs [function][point].
+int oracle_radial_tables(void* hv, int which, double* values, double* derivs, int* shape) {
+    return guarded([&]() -> int {
+        auto* h = static_cast<OracleHandle*>(hv);
+        const RadialModel& rm = h->fp64 ? h->d->radial : h->f->radial;
+        std::vector<std::vector<double>> v, d;
+        rm.tabulate(which == 0 ? rm.R0 : rm.R1, v, d);
+        shape[0] = static_cast<int>(v.size());
+        shape[1] = rm.points;
+        if (values)
+            for (std::size_t f = 0; f < v.size(); ++f)
+                for (int p = 0; p < rm.points; ++p) {
+                    values[f * rm.points + p] = v[f][p];
+                    derivs[f * rm.points + p] = d[f][p];
+                }
+        return 0;
+    });
+}
+
+int oracle_radial_features(void* hv, double* out, int* shape) {
+    auto* h = static_cast<OracleHandle*>(hv);
+    const RadialModel& rm = h->fp64 ? h->d->radial : h->f->radial;
+    const auto f = rm.features();
+    shape[0] = rm.points;
+    shape[1] = static_cast<int>(rm.bessel.size());
+    if (out) std::copy(f.begin(), f.end(), out);
+    return 0;
+}
+
+// Spline derivative solve of arbitrary nodal values on a uniform grid of step h.
+int oracle_spline_derivatives(const double* values, int points, double h, double* derivs) {
+    return guarded([&]() -> int {
+        RadialModel rm;
+        rm.points = points;
+        rm.h = h;
+        const auto d = rm.spline_derivatives(std::vector<double>(values, values + points));
+        std::copy(d.begin(), d.end(), derivs);
+        return 0;
+    });
+}
+
+// FP32 Hermite spline set evaluation (cubic_spline_set.cpp): values/derivs
+// [functions][nodes] (float), evaluated at r[count] -> out_v/out_d [count][functions].
+int oracle_spline_eval_f32(float h, float x0, int functions, int nodes, const float* values, const float* derivs,
+                           const double* r, int count, float* out_v, float* out_d) {
+    return guarded([&]() -> int {
+        std::vector<std::vector<float>> v(functions), d(functions);
+        for (int f = 0; f < functions; ++f) {
+            v[f].assign(values + static_cast<std::size_t>(f) * nodes, values + static_cast<std::size_t>(f + 1) * nodes);
+            d[f].assign(derivs + static_cast<std::size_t>(f) * nodes, derivs + static_cast<std::size_t>(f + 1) * nodes);
+        }
+        SplineSet<float> s(h, v, d, x0);
+        for (int i = 0; i < count; ++i) {
+            const auto pt = s.point(static_cast<float>(r[i]));
+            const float* c = s.coefficients(pt);
+            for (int f = 0; f < functions; ++f) {
+                out_v[static_cast<std::size_t>(i) * functions + f] =
+                    c[f] + c[functions + f] * pt.x + c[2 * functions + f] * pt.xx + c[3 * functions + f] * pt.xxx;
+                out_d[static_cast<std::size_t>(i) * functions + f] =
+                    c[functions + f] + 2.0f * c[2 * functions + f] * pt.x + 3.0f * c[3 * functions + f] * pt.xx;
+            }
+        }
+        return 0;
+    });
+}
+
+// Y / dY of edges (FP32, as the evaluator) from xyz[count][3].
+int oracle_harmonics(const double* xyz, int count, int l_max, float* Y, float* G) {
+    const int nY = (l_max + 1) * (l_max + 1);
+    for (int e = 0; e < count; ++e) {
+        const double rr = std::sqrt(xyz[3 * e] * xyz[3 * e] + xyz[3 * e + 1] * xyz[3 * e + 1] + xyz[3 * e + 2] * xyz[3 * e + 2]);
+        float d[3];
+        for (int c = 0; c < 3; ++c) d[c] = static_cast<float>(xyz[3 * e + c] / rr);
+        edge_harmonics<float>(l_max, d, static_cast<float>(rr), Y + static_cast<std::size_t>(e) * nY,
+                              G ? G + static_cast<std::size_t>(e) * 3 * nY : nullptr);
+    }
+    return 0;
+}
+
+// Polynomial with the reference's semantics (FP64): monomials flattened as
+// offsets[nterms+1] into vars.  Returns f; grad[nvar].
+double oracle_polynomial(int nvar, int nterms, const double* coef, const int* offsets, const int* vars,
+                         const double* x, double* grad) {
+    std::vector<std::vector<int>> monos(nterms);
+    for (int t = 0; t < nterms; ++t) monos[t].assign(vars + offsets[t], vars + offsets[t + 1]);
+    const MonomialSet ms = dedupe_monomials(monos);
+    std::vector<double> c(ms.monos.size());
+    for (std::size_t t = 0; t < ms.monos.size(); ++t) c[t] = coef[ms.source_index[t]];
+    return poly_eval_grad<double>(ms, c.data(), x, grad, nvar);
+}
+
+// Neighbour list: count pass then fill pass.
+long long oracle_neighbor_count(const double* pos, int n, const double* cell, const double* inv, double cutoff) {
+    try {
+        Graph g;
+        build_graph(pos, n, cell, inv, cutoff, g, false);
+        return g.offsets[n];
+    } catch (const std::exception& ex) {
+        oracle::last_error = ex.what();
+        return -1;
+    }
+}
+
+int oracle_neighbor_fill(const double* pos, int n, const double* cell, const double* inv, double cutoff,
+                         int* num_neigh, int* offsets, int* sources, int* shifts, double* fractional_xyz) {
+    return guarded([&]() -> int {
+        Graph g;
+        build_graph(pos, n, cell, inv, cutoff, g, true);
+        std::copy(g.num_neigh.begin(), g.num_neigh.end(), num_neigh);
+        std::copy(g.offsets.begin(), g.offsets.end(), offsets);
+        std::copy(g.sources.begin(), g.sources.end(), sources);
+        std::copy(g.shifts.begin(), g.shifts.end(), shifts);
+        std::copy(g.fractional_xyz.begin(), g.fractional_xyz.end(), fractional_xyz);
+        return 0;
+    });
+}
+
+// Prepared edge geometry (lifecycle.cpp:2915-3079, fractional reference):
+// xyz_e = frac_e . cell + disp[src] - disp[rcv]; r = |xyz|, clamped to cutoff
+// with xyz scaled to it.  Returns the number of invalid edges.
+int oracle_prepared_geometry(int n, long long E, const int* receivers, const int* sources,
+                             const double* fractional_xyz, const double* cell, const double* inv,
+                             const double* reference_positions, const double* positions, double cutoff,
+                             double* xyz, double* r) {
+    std::vector<double> disp(3 * static_cast<std::size_t>(n));
+    for (int a = 0; a < n; ++a) {
+        double delta[3], f[3];
+        for (int c = 0; c < 3; ++c) delta[c] = positions[3 * a + c] - reference_positions[3 * a + c];
+        for (int lat = 0; lat < 3; ++lat) {
+            f[lat] = 0.0;
+            for (int c = 0; c < 3; ++c) f[lat] += delta[c] * inv[3 * c + lat];
+            f[lat] -= std::floor(f[lat] + 0.5);
+        }
+        for (int c = 0; c < 3; ++c) {
+            double v = 0.0;
+            for (int lat = 0; lat < 3; ++lat) v += f[lat] * cell[3 * lat + c];
+            disp[3 * a + c] = v;
+        }
+    }
+    int invalid = 0;
+    for (long long e = 0; e < E; ++e) {
+        const int rc = receivers[e], sc = sources[e];
+        double vec[3], d2 = 0.0;
+        for (int c = 0; c < 3; ++c) {
+            double ref = 0.0;
+            for (int lat = 0; lat < 3; ++lat) ref += fractional_xyz[3 * e + lat] * cell[3 * lat + c];
+            vec[c] = ref + disp[3 * sc + c] - disp[3 * rc + c];
+            d2 += vec[c] * vec[c];
+        }
+        if (!std::isfinite(d2) || !(d2 > 0.0)) {
+            ++invalid;
+            xyz[3 * e] = cutoff; xyz[3 * e + 1] = 0.0; xyz[3 * e + 2] = 0.0;
+            r[e] = cutoff;
+            continue;
+        }
+        const double dist = std::sqrt(d2);
+        const double scale = dist >= cutoff ? cutoff / dist : 1.0;
+        for (int c = 0; c < 3; ++c) xyz[3 * e + c] = scale * vec[c];
+        r[e] = dist >= cutoff ? cutoff : dist;
+    }
+    return invalid;
+}
+
+// mace_kokkos_evaluate.cpp:49-105 (F[src] += f, F[rcv] -= f), serial order.
+int oracle_reduce_forces(int n, long long E, const int* receivers, const int* sources, const double* f,
+                         double* atom_forces) {
+    std::fill(atom_forces, atom_forces + 3 * static_cast<std::size_t>(n), 0.0);
+    for (long long e = 0; e < E; ++e)
+        for (int c = 0; c < 3; ++c) {
+            atom_forces[3 * sources[e] + c] += f[3 * e + c];
+            atom_forces[3 * receivers[e] + c] -= f[3 * e + c];
+        }
+    return 0;
+}
+
+// evaluate.cpp:291 / calculator.py:3884: sigma_ab = -(1/V) sum_e f_a xyz_b.
+int oracle_reduce_stress(long long E, const double* f, const double* xyz, double volume, double* stress) {
+    for (int a = 0; a < 3; ++a)
+        for (int b = 0; b < 3; ++b) {
+            double s = 0.0;
+            for (long long e = 0; e < E; ++e) s += f[3 * e + a] * xyz[3 * e + b];
+            stress[3 * a + b] = -s / volume;
+        }
+    return 0;
+}
+
+int oracle_num_threads() { return omp_get_max_threads(); }
+
+}  // extern "C"

@@ -1,0 +1,270 @@
+"""Seeded random-init MACE models in the reference's JSON format version 4.
+
+The file layout is the one the reference's loaders read
+(libsymmetrix/source/mace.cpp:2660-2959, mace_kokkos_model.cpp:146,
+compact_radial.cpp:110-214, h1_affine_schema.hpp:196-259): compact radial
+representation, h1_affine_mode "m0_composite", no ZBL, no density scaling.
+
+Weights are drawn from ``numpy.random.default_rng(seed)`` with the fan-in
+scalings the reference's extractor folds into its exported weights
+(extract_mace_data.py:660-666 radial MLP, :922-933 H0, :982-1001 A0 with
+1/avg_num_neighbors, :1166-1184 H1, :1439-1444 A1, :1590-1611 H2,
+:1615-1680 readouts).  Values are rounded to float32 before they are written so
+that the FP32 and FP64 readers of the file see the same numbers.
+
+Named shapes (``MODEL_CONFIGS``) are the benchmark configurations: ``tiny``,
+``medium`` and ``wide``.
+"""
+
+from __future__ import annotations
+
+import json
+import math
+import os
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from . import e3
+
+# e3nn normalize2mom(silu) constant: 1/sqrt(E[silu(z)^2]), z ~ N(0,1)
+SILU_SCALE = 1.6791767923989418
+
+
+@dataclass
+class ModelConfig:
+    name: str
+    num_channels: int
+    l_max: int
+    L_max: int
+    correlation: int
+    atomic_numbers: list
+    num_bessel: int = 8
+    cutoff_p: int = 5
+    radial_mlp: list = field(default_factory=lambda: [64, 64, 64])
+    r_cut: float = 6.0
+    avg_num_neighbors: float = 60.0
+    num_spline_points: int = 256
+    readout_hidden: int = 16
+    # plays the role of MACE's scale_shift.scale folded into the readouts
+    # (extract_mace_data.py:1623-1625,1676-1680)
+    energy_scale: float = 10.0
+    seed: int = 0
+
+
+MODEL_CONFIGS = {
+    # 32x0e+32x1o, lmax 2, corr 2, Sr/Ti/O, MLP [32,32], 5.0 A
+    "tiny": ModelConfig("tiny", 32, 2, 1, 2, [8, 22, 38], radial_mlp=[32, 32],
+                        r_cut=5.0, avg_num_neighbors=40.0),
+    # 128x0e+128x1o, lmax 3, corr 3, 89 elements,
+    # MLP [64,64,64], 6.0 A
+    "medium": ModelConfig("medium", 128, 3, 1, 3, list(range(1, 90)),
+                          radial_mlp=[64, 64, 64], r_cut=6.0,
+                          avg_num_neighbors=70.0),
+    # 256 channels, 0e+1o+2e hidden, lmax 3, corr 3, 5.0 A
+    "wide": ModelConfig("wide", 256, 3, 2, 3, [1, 8], radial_mlp=[64, 64, 64],
+                        r_cut=5.0, avg_num_neighbors=40.0),
+}
+
+
+def _f32(a):
+    return np.asarray(a, dtype=np.float32).astype(np.float64)
+
+
+def _fmt(a):
+    """Compact JSON list text of a flat float array (9 significant digits,
+    exact for float32 values)."""
+    a = np.asarray(a, dtype=np.float32).ravel()
+    return "[" + ",".join("%.9g" % v for v in a.tolist()) + "]"
+
+
+def _product_weights(rng, l_in_max, L_out, correlation, num_types, C, scale):
+    """Per-(type, m_out, channel) polynomial coefficients over a shared monomial
+    list (the reference's U x W contraction, extract_mace_data.py:1070-1112)."""
+    d_out = 2 * L_out + 1
+    monos_all = [[] for _ in range(d_out)]
+    coef_all = [None] * d_out
+    blocks = []
+    for nu in range(1, correlation + 1):
+        monos, U = e3.symmetric_basis(l_in_max, L_out, nu)
+        if U.shape[0] == 0:
+            continue
+        W = rng.normal(size=(num_types, U.shape[0], C)) * (
+            scale[nu - 1] / math.sqrt(U.shape[0]))
+        blocks.append((monos, U, W))
+    for M in range(d_out):
+        keys = []
+        cols = []
+        for monos, U, W in blocks:
+            nz = np.nonzero(np.abs(U[:, M, :]).max(axis=0) > 1e-9)[0]
+            keys.extend(monos[j] for j in nz)
+            # coefficient [type, channel, term]
+            cols.append(np.einsum("tec,ej->tcj", W, U[:, M, nz]))
+        order = sorted(range(len(keys)), key=lambda i: (len(keys[i]), keys[i]))
+        coef = np.concatenate(cols, axis=2)[:, :, order]
+        monos_all[M] = [list(keys[i]) for i in order]
+        coef_all[M] = coef
+    return monos_all, coef_all
+
+
+def generate_model(config, seed=None):
+    """Return the model as a dict of JSON *text fragments* keyed by JSON key
+    (large arrays pre-formatted), plus a small dict of plain metadata."""
+    cfg = config if isinstance(config, ModelConfig) else MODEL_CONFIGS[config]
+    if seed is None:
+        seed = cfg.seed
+    rng = np.random.default_rng(seed)
+    C, l_max, L_max = cfg.num_channels, cfg.l_max, cfg.L_max
+    n_el = len(cfg.atomic_numbers)
+    num_lm, num_LM = (l_max + 1) ** 2, (L_max + 1) ** 2
+    frag = {}
+
+    def put(key, value):
+        frag[key] = json.dumps(value)
+
+    put("symmetrix_format_version", 4)
+    put("model_type", "MACE")
+    put("h1_affine_mode", "m0_composite")
+    put("h1_affine_version", 1)
+    put("generator", {"name": "symmetrix-mi355x random_model", "config": cfg.name,
+                      "seed": seed})
+    put("num_elements", n_el)
+    put("num_channels", C)
+    put("num_interactions", 2)
+    put("r_cut", cfg.r_cut)
+    put("l_max", l_max)
+    put("L_max", L_max)
+    put("atomic_numbers", list(cfg.atomic_numbers))
+    put("atomic_energies",
+        [float(v) for v in _f32(-1.0 - 0.05 * np.asarray(cfg.atomic_numbers)
+                                 + 0.1 * rng.normal(size=n_el))])
+    put("has_zbl", False)
+    put("radial_representation", "compact")
+
+    # ---- compact radial (Bessel x polynomial cutoff -> SiLU MLPs)
+    r_cut = cfg.r_cut
+    bessel_w = _f32(np.arange(1, cfg.num_bessel + 1) * math.pi / r_cut)
+    num_paths_r1 = len(e3.r1_paths(l_max, L_max))
+
+    def mlp(out_width):
+        shape = [cfg.num_bessel] + list(cfg.radial_mlp) + [out_width]
+        weights = []
+        for a, b in zip(shape[:-1], shape[1:]):
+            # effective weight W / sqrt(h_in), layout [out][in]
+            weights.append(_f32(rng.normal(size=(b, a)) / math.sqrt(a)))
+        return {"shape": shape,
+                "weights": [w.ravel().tolist() for w in weights],
+                "activation": "silu",
+                "activation_scale": SILU_SCALE}
+
+    compact = {
+        "spline_grid_min": 1e-12,
+        "num_spline_points": cfg.num_spline_points,
+        "basis": {"type": "bessel", "weights": bessel_w.tolist(),
+                  "prefactor": float(_f32(math.sqrt(2.0 / r_cut)))},
+        "cutoff": {"type": "polynomial", "r_max": r_cut, "p": cfg.cutoff_p},
+        "distance_transform": {"type": "none"},
+        "networks": {"R0": mlp((l_max + 1) * C), "R1": mlp(num_paths_r1 * C)},
+    }
+    put("compact_radial", compact)
+
+    # ---- H0: species embedding through linear_up
+    frag["H0_weights"] = _fmt(rng.normal(size=(n_el, C)))
+    put("A0_scaled", False)
+
+    # ---- A0: per species, per l, C x C [input][output]
+    a0 = rng.normal(size=(n_el, l_max + 1, C, C)) / (
+        math.sqrt(C) * cfg.avg_num_neighbors)
+    frag["A0_weights"] = "[" + ",".join(
+        "[" + ",".join(_fmt(a0[t, l]) for l in range(l_max + 1)) + "]"
+        for t in range(n_el)) + "]"
+
+    # ---- M0 symmetric contraction, outputs LM < (L_max+1)^2
+    m0_weights = {str(t): {} for t in range(n_el)}
+    m0_monos = {}
+    parts = [[] for _ in range(n_el)]
+    for L in range(L_max + 1):
+        monos, coef = _product_weights(
+            rng, l_max, L, cfg.correlation, n_el, C,
+            scale=[1.0, 0.5, 0.25][:cfg.correlation] + [0.1] * 4)
+        for M in range(2 * L + 1):
+            lm = L * L + M
+            m0_monos[str(lm)] = monos[M]
+            for t in range(n_el):
+                parts[t].append(
+                    '"%d":{' % lm + ",".join(
+                        '"%d":%s' % (k, _fmt(coef[M][t, k])) for k in range(C))
+                    + "}")
+    frag["M0_weights"] = "{" + ",".join(
+        '"%d":{' % t + ",".join(parts[t]) + "}" for t in range(n_el)) + "}"
+    put("M0_monomials", m0_monos)
+    del m0_weights
+
+    # ---- H1 = product linear x interaction[1].linear_up, per l
+    frag["H1_weights"] = _fmt(rng.normal(size=(L_max + 1, C, C)) / math.sqrt(C))
+
+    # ---- R1 coupling
+    cpl = e3.r1_coupling(l_max, L_max)
+    for key in ("Phi1_l", "Phi1_l1", "Phi1_l2", "Phi1_lme", "Phi1_lelm1lm2"):
+        put(key, cpl[key])
+    put("Phi1_clebsch_gordan", cpl["Phi1_clebsch_gordan"])
+    put("A1_scaled", False)
+
+    # ---- A1: per l, [num_e(l)][C][C]
+    num_e = [sum(1 for l in cpl["Phi1_l"] if l == ll) for ll in range(l_max + 1)]
+    frag["A1_weights"] = "[" + ",".join(
+        _fmt(rng.normal(size=(num_e[l], C, C))
+             / (math.sqrt(num_e[l] * C) * cfg.avg_num_neighbors))
+        for l in range(l_max + 1)) + "]"
+
+    # ---- M1: invariant contraction of A1 (16 harmonic components)
+    monos1, coef1 = _product_weights(
+        rng, l_max, 0, 3, n_el, C, scale=[1.0, 0.5, 0.25])
+    put("M1_monomials", monos1[0])
+    frag["M1_weights"] = "{" + ",".join(
+        '"%d":{' % t + ",".join(
+            '"%d":%s' % (k, _fmt(coef1[0][t, k])) for k in range(C)) + "}"
+        for t in range(n_el)) + "}"
+
+    # ---- H2 skip (T_z, [input][output]) and M1 linear
+    frag["H2_weights_for_M0"] = "[" + ",".join(
+        _fmt(rng.normal(size=(C, C)) / math.sqrt(C)) for _ in range(n_el)) + "]"
+    frag["H2_weights_for_M1"] = _fmt(rng.normal(size=(C, C)) / math.sqrt(C))
+
+    # ---- readouts
+    hid = cfg.readout_hidden
+    frag["readout_1_weights_for_M0"] = _fmt(
+        rng.normal(size=C) / math.sqrt(C) * cfg.energy_scale)
+    put("readout_2_hidden_size", hid)
+    frag["readout_2_weights_1"] = _fmt(rng.normal(size=(hid, C)) / math.sqrt(C))
+    frag["readout_2_weights_2"] = _fmt(
+        rng.normal(size=hid) / math.sqrt(hid) * cfg.energy_scale)
+    put("readout_2_scale_factor", SILU_SCALE)
+    return frag
+
+
+def write_model(config, path, seed=None):
+    """Write the model JSON to ``path`` (atomically) and return the path."""
+    frag = generate_model(config, seed)
+    tmp = path + ".tmp%d" % os.getpid()
+    with open(tmp, "w") as f:
+        f.write("{\n")
+        f.write(",\n".join('"%s":%s' % (k, v) for k, v in frag.items()))
+        f.write("\n}\n")
+    os.replace(tmp, path)
+    return path
+
+
+def cached_model(config, seed=None, directory=None):
+    """Path of the model for a named config, generated on first use under
+    ``directory`` (default: $SYMMETRIX_MODEL_CACHE or /tmp/symmetrix_models)."""
+    cfg = config if isinstance(config, ModelConfig) else MODEL_CONFIGS[config]
+    if seed is None:
+        seed = cfg.seed
+    directory = directory or os.environ.get(
+        "SYMMETRIX_MODEL_CACHE", "/tmp/symmetrix_models")
+    os.makedirs(directory, exist_ok=True)
+    path = os.path.join(directory, "mace_%s_seed%d_v1.json" % (cfg.name, seed))
+    if not os.path.exists(path):
+        write_model(cfg, path, seed)
+    return path
