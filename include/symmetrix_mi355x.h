@@ -1,0 +1,184 @@
+/*
+ * symmetrix_mi355x.h -- C ABI of the MI355X MACE evaluator
+ * (libsymmetrix_mi355x.so).
+ *
+ * Each entry point replaces one member of the reference's C++ evaluator
+ * `MACEKokkos<float>` (libsymmetrix/source/mace_kokkos.hpp:85-1838) as the
+ * reference's pybind module exposes it (symmetrix/source/cpp/mace_kokkos.cpp),
+ * so a ctypes/cgo/JNI binding can stand in for the `MACEKokkosFloat` class.
+ * Conventions:
+ *   - plain pointers and sizes; host pointers unless the name ends in _device;
+ *   - every function returns 0 on success or a negative SMX_ERR_* code, and
+ *     never throws; smx_last_error() holds the message of the calling thread's
+ *     last failure (the reference raises std::invalid_argument /
+ *     std::runtime_error / std::logic_error, which pybind maps to ValueError /
+ *     RuntimeError);
+ *   - one evaluator is driven from one host thread; all device work is
+ *     ordered on the evaluator's own HIP stream (smx_evaluator_stream), and
+ *     calls that return host data synchronise that stream first.
+ * Units: positions and cell in Angstrom, energies in eV, forces eV/Angstrom,
+ * stress eV/Angstrom^3 (3x3, row-major).
+ */
+#ifndef SYMMETRIX_MI355X_H
+#define SYMMETRIX_MI355X_H
+
+#include <stdint.h>
+
+#if defined(__GNUC__)
+#define SMX_API __attribute__((visibility("default")))
+#else
+#define SMX_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SMX_ABI_VERSION 1
+
+enum {
+    SMX_OK = 0,
+    SMX_ERR_INVALID_ARGUMENT = -1, /* bad input, stale graph generation (ValueError) */
+    SMX_ERR_RUNTIME = -2,          /* HIP failure, invalid geometry (RuntimeError) */
+    SMX_ERR_LOGIC = -3,            /* call out of order, e.g. no graph prepared */
+    SMX_ERR_OUT_OF_MEMORY = -4,    /* device or host allocation failed */
+    SMX_ERR_UNSUPPORTED = -5       /* model shape/features without a kernel set */
+};
+
+typedef struct SmxEvaluator SmxEvaluator;
+
+/* Model facts: the fields the reference exposes as read-only attributes
+ * (mace_kokkos.hpp:485-497; pybind mace_kokkos.cpp:2080-2083). */
+typedef struct SmxModelInfo {
+    uint32_t struct_size;
+    int32_t num_elements;
+    int32_t num_channels;
+    int32_t l_max;
+    int32_t L_max;
+    int32_t num_interactions;
+    int32_t num_paths;
+    int32_t num_lme;
+    double r_cut;
+} SmxModelInfo;
+
+/* Device addresses of the evaluator's result buffers (valid until the next
+ * prepare call; FP64). */
+typedef struct SmxDeviceOutputs {
+    uint32_t struct_size;
+    int32_t num_nodes;
+    int64_t num_edges;
+    const double* node_energies; /* [N] */
+    const double* node_forces;   /* [E][3]: -dE/dxyz_e */
+    const double* atom_forces;   /* [N][3] after smx_reduce_prepared_node_forces */
+    const double* stress;        /* [3][3] after smx_reduce_prepared_stress */
+    const double* total_energy;  /* [1] after smx_total_energy_device */
+    const double* xyz;           /* [E][3] edge vectors of the last call */
+    const double* r;             /* [E] edge lengths of the last call */
+} SmxDeviceOutputs;
+
+SMX_API int32_t smx_abi_version(void);
+SMX_API const char* smx_last_error(void);
+
+/* MACEKokkos(std::string filename, std::string head) -- mace_kokkos.hpp:91;
+ * pybind MACEKokkosFloat(filename, head) (mace_kokkos.cpp:2762). */
+SMX_API int32_t smx_evaluator_create(const char* model_path, const char* head, SmxEvaluator** out);
+SMX_API void smx_evaluator_destroy(SmxEvaluator* ev);
+SMX_API int32_t smx_evaluator_info(const SmxEvaluator* ev, SmxModelInfo* info);
+/* atomic_numbers property (pybind mace_kokkos.cpp:1896) */
+SMX_API int32_t smx_evaluator_atomic_numbers(const SmxEvaluator* ev, int32_t* out, int32_t capacity);
+/* set_streamed_edges (mace_kokkos.hpp:93); only "direct" is implemented. */
+SMX_API int32_t smx_set_streamed_edges(SmxEvaluator* ev, const char* mode);
+/* hipStream_t the evaluator enqueues on */
+SMX_API void* smx_evaluator_stream(SmxEvaluator* ev);
+
+/* prepare_factorized_graph (mace_kokkos.hpp:365-370; pybind
+ * _prepare_factorized_graph, mace_kokkos.cpp:1561): receiver-major CSR on
+ * the host.  Returns the graph generation token. */
+SMX_API int32_t smx_prepare_factorized_graph(SmxEvaluator* ev, int32_t num_nodes, const int32_t* node_types,
+                                             const int32_t* num_neigh, int64_t num_edges,
+                                             const int32_t* neigh_indices, const int32_t* neigh_types,
+                                             uint64_t* generation);
+/* prepare_factorized_graph_device (mace_kokkos.hpp:387-392): same CSR,
+ * device pointers (the LAMMPS pair style's entry, pair_symmetrix_mace_kokkos.cpp:1160). */
+SMX_API int32_t smx_prepare_factorized_graph_device(SmxEvaluator* ev, int32_t num_nodes,
+                                                    const int32_t* node_types_device,
+                                                    const int32_t* num_neigh_device, int64_t num_edges,
+                                                    const int32_t* neigh_indices_device,
+                                                    const int32_t* neigh_types_device, uint64_t* generation);
+/* prepare_periodic_factorized_graph (mace_kokkos.hpp:393-398; pybind
+ * _prepare_periodic_factorized_graph, mace_kokkos.cpp:1580): device
+ * neighbour list at neighbor_cutoff, positions kept as the geometry
+ * reference.  cell rows are lattice vectors; inverse_cell = inv(cell). */
+SMX_API int32_t smx_prepare_periodic_factorized_graph(SmxEvaluator* ev, int32_t num_nodes, const int32_t* node_types,
+                                                      const double* positions, const double* cell,
+                                                      const double* inverse_cell, double neighbor_cutoff,
+                                                      uint64_t* generation, int64_t* num_edges);
+/* update_factorized_cell (mace_kokkos.hpp:436; pybind _update_factorized_cell) */
+SMX_API int32_t smx_update_factorized_cell(SmxEvaluator* ev, uint64_t generation, const double* cell,
+                                           const double* inverse_cell);
+
+/* compute_prepared_factorized(token, xyz, r) (mace_kokkos.hpp:440-443):
+ * energies and directed forces from host edge vectors xyz[E][3], r[E]. */
+SMX_API int32_t smx_compute_prepared_factorized(SmxEvaluator* ev, uint64_t generation, const double* xyz,
+                                                const double* r);
+/* compute_prepared_factorized_positions(token, positions) (mace_kokkos.hpp:444-446;
+ * pybind _compute_prepared_factorized_positions, mace_kokkos.cpp:1828) */
+SMX_API int32_t smx_compute_prepared_factorized_positions(SmxEvaluator* ev, uint64_t generation,
+                                                          const double* positions);
+/* same with positions[N][3] already in device memory */
+SMX_API int32_t smx_compute_prepared_factorized_positions_device(SmxEvaluator* ev, uint64_t generation,
+                                                                 const double* positions_device);
+/* compute_node_energies_forces with execution_graph_generation == 0
+ * (mace_kokkos.hpp:654-662; pybind mace_kokkos.cpp:2169): prepares the
+ * graph from the host CSR, then evaluates. */
+SMX_API int32_t smx_compute_node_energies_forces(SmxEvaluator* ev, int32_t num_nodes, const int32_t* node_types,
+                                                 const int32_t* num_neigh, int64_t num_edges,
+                                                 const int32_t* neigh_indices, const int32_t* neigh_types,
+                                                 const double* xyz, const double* r);
+
+/* reduce_prepared_node_forces (mace_kokkos.hpp:702; pybind _reduce_atom_forces,
+ * mace_kokkos.cpp:2103): F[src] += f_e, F[rcv] -= f_e in FP64.  atom_forces
+ * (host, [N][3]) may be NULL to keep the result on the device. */
+SMX_API int32_t smx_reduce_prepared_node_forces(SmxEvaluator* ev, uint64_t generation, double* atom_forces);
+/* reduce_prepared_stress (mace_kokkos.hpp:705; pybind _reduce_stress,
+ * mace_kokkos.cpp:2134): sigma = -(1/V) sum_e f_e xyz_e^T.  stress (host [9])
+ * may be NULL. */
+SMX_API int32_t smx_reduce_prepared_stress(SmxEvaluator* ev, uint64_t generation, double volume, double* stress);
+/* node_energies / node_forces properties (mace_kokkos.hpp:501) */
+SMX_API int32_t smx_node_energies(SmxEvaluator* ev, double* out, int64_t capacity);
+SMX_API int32_t smx_node_forces(SmxEvaluator* ev, double* out, int64_t capacity);
+/* FP64 sum of the node energies on the device (the calculator's sum,
+ * calculator.py:3831-3836); total may be NULL to keep it on the device. */
+SMX_API int32_t smx_total_energy_device(SmxEvaluator* ev, double* total);
+SMX_API int32_t smx_device_outputs(SmxEvaluator* ev, SmxDeviceOutputs* out);
+SMX_API int32_t smx_synchronize(SmxEvaluator* ev);
+
+/* Stage buffers of the last evaluation (FP32, row-major node-major) for
+ * stage-level parity checks: "A0", "M0", "H1", "Phi1", "A1", "A1_adj",
+ * "dPhi1", "H1_adj", "M0_adj", "A0_adj", "edge_records".  Returns the
+ * element count through *count; copies when out != NULL and capacity is
+ * large enough. */
+SMX_API int32_t smx_debug_stage(SmxEvaluator* ev, const char* name, float* out, int64_t capacity, int64_t* count);
+
+/* Launch timing with HIP events on the evaluator stream (off by default). */
+SMX_API int32_t smx_set_kernel_timing(SmxEvaluator* ev, int32_t enabled);
+SMX_API int32_t smx_kernel_timing_reset(SmxEvaluator* ev);
+/* index-th timed kernel name (NULL past the end), total ms and launch count */
+SMX_API int32_t smx_kernel_timing(SmxEvaluator* ev, int32_t index, const char** name, double* total_ms,
+                                  int64_t* launches);
+
+/* Standalone periodic neighbour list (neighbor_graph_kokkos.cpp:38-405),
+ * bit-exact with the reference's device builder.  Two calls: with
+ * sources == NULL it returns the edge count in *num_edges; then with
+ * buffers num_neigh[N], offsets[N+1], sources[E], shifts[E][3],
+ * fractional_xyz[E][3] (host) it fills them. */
+SMX_API int32_t smx_neighbor_list(int32_t num_nodes, const double* positions, const double* cell,
+                                  const double* inverse_cell, double cutoff, int64_t* num_edges,
+                                  int32_t* num_neigh, int32_t* offsets, int32_t* sources, int32_t* shifts,
+                                  double* fractional_xyz);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SYMMETRIX_MI355X_H */

@@ -1,0 +1,602 @@
+// Graph and geometry kernels: periodic neighbour list, edge schedules,
+// prepared edge geometry and per-edge spherical harmonics.
+//
+// This translation unit is compiled with -ffp-contract=off: the neighbour
+// list must be bit-exact with the reference's device builder
+// (libsymmetrix/source/neighbor_graph_kokkos.cpp:38-405), which evaluates
+// every FP64 expression without fused multiply-adds, and the edge geometry
+// (mace_kokkos_factorized_lifecycle.cpp:2915-3079) and harmonics
+// (spherical_harmonic_device.hpp:150-199) follow the same rounding.
+#include <algorithm>
+#include <climits>
+#include <cmath>
+#include <stdexcept>
+#include <vector>
+
+#include "device_common.hpp"
+#include "kernels.hpp"
+#include "shapes.hpp"
+
+namespace smx {
+namespace {
+
+struct Mat3 {
+    double v[9];
+};
+
+// ---------------------------------------------------------------------------
+// Exclusive scan of int32 counts into int64 offsets (three passes).
+// ---------------------------------------------------------------------------
+constexpr int kScanThreads = 256;
+constexpr int kScanItems = 8;
+constexpr int kScanTile = kScanThreads * kScanItems;
+
+__global__ __launch_bounds__(kScanThreads) void k_scan_tiles(const int* __restrict__ in, long long* __restrict__ out,
+                                                             int n, long long* __restrict__ tile_sums) {
+    __shared__ long long warp_tot[kScanThreads / kWave];
+    const int base = blockIdx.x * kScanTile + threadIdx.x * kScanItems;
+    long long v[kScanItems];
+    long long run = 0;
+#pragma unroll
+    for (int j = 0; j < kScanItems; ++j) {
+        const int idx = base + j;
+        const long long x = idx < n ? static_cast<long long>(in[idx]) : 0;
+        v[j] = run;
+        run += x;
+    }
+    // exclusive scan of the per-thread totals across the workgroup
+    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    long long incl = run;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+        const long long y = __shfl_up(incl, off, kWave);
+        if (lane >= off) incl += y;
+    }
+    if (lane == kWave - 1) warp_tot[wave] = incl;
+    __syncthreads();
+    long long wave_base = 0;
+    for (int w = 0; w < wave; ++w) wave_base += warp_tot[w];
+    const long long excl = wave_base + incl - run;
+#pragma unroll
+    for (int j = 0; j < kScanItems; ++j) {
+        const int idx = base + j;
+        if (idx < n) out[idx] = excl + v[j];
+    }
+    if (threadIdx.x == kScanThreads - 1) tile_sums[blockIdx.x] = excl + run;
+}
+
+__global__ __launch_bounds__(1024) void k_scan_tile_sums(long long* __restrict__ sums, int tiles) {
+    // single workgroup, sequential over chunks of 1024 with a running carry
+    __shared__ long long warp_tot[1024 / kWave];
+    __shared__ long long carry;
+    if (threadIdx.x == 0) carry = 0;
+    __syncthreads();
+    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    for (int c0 = 0; c0 < tiles; c0 += 1024) {
+        const int idx = c0 + threadIdx.x;
+        const long long x = idx < tiles ? sums[idx] : 0;
+        long long incl = x;
+        for (int off = 1; off < kWave; off <<= 1) {
+            const long long y = __shfl_up(incl, off, kWave);
+            if (lane >= off) incl += y;
+        }
+        if (lane == kWave - 1) warp_tot[wave] = incl;
+        __syncthreads();
+        long long wb = 0;
+        for (int w = 0; w < wave; ++w) wb += warp_tot[w];
+        const long long base = carry;
+        __syncthreads();
+        if (idx < tiles) sums[idx] = base + wb + incl - x;
+        if (threadIdx.x == 1023) carry = base + wb + incl;
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) sums[tiles] = carry;
+}
+
+__global__ __launch_bounds__(kScanThreads) void k_scan_add(long long* __restrict__ out, int n,
+                                                           const long long* __restrict__ tile_sums, int tiles) {
+    const int idx = blockIdx.x * kScanThreads + threadIdx.x;
+    if (idx < n) out[idx] += tile_sums[idx / kScanTile];
+    if (idx == 0) out[n] = tile_sums[tiles];
+}
+
+__global__ void k_i64_to_i32(const long long* __restrict__ in, int* __restrict__ out, int n) {
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx < n) out[idx] = static_cast<int>(in[idx]);
+}
+
+// ---------------------------------------------------------------------------
+// Neighbour list (neighbor_graph_kokkos.cpp:117-402)
+// ---------------------------------------------------------------------------
+struct BinGrid {
+    int bins[3];
+    int reach[3];
+};
+
+__device__ __forceinline__ int floor_div(int a, int b) {
+    const int q = a / b, r = a % b;
+    return q - ((r != 0 && r < 0) ? 1 : 0);
+}
+
+__global__ void k_wrap(int N, const double* __restrict__ pos, Mat3 cell, Mat3 inv, BinGrid g,
+                       double* __restrict__ wfrac, double* __restrict__ wpos, int* __restrict__ wrap,
+                       int* __restrict__ abin, int* __restrict__ bsize) {
+    const int a = blockIdx.x * blockDim.x + threadIdx.x;
+    if (a >= N) return;
+    double f[3];
+    for (int ax = 0; ax < 3; ++ax) {
+        double v = 0.0;
+        for (int c = 0; c < 3; ++c) v += pos[3 * a + c] * inv.v[3 * c + ax];
+        const int w = static_cast<int>(floor(v));
+        v -= w;
+        f[ax] = v;
+        wfrac[3 * a + ax] = v;
+        wrap[3 * a + ax] = w;
+    }
+    for (int c = 0; c < 3; ++c) {
+        double v = 0.0;
+        for (int ax = 0; ax < 3; ++ax) v += f[ax] * cell.v[3 * ax + c];
+        wpos[3 * a + c] = v;
+    }
+    const int x = min(g.bins[0] - 1, static_cast<int>(f[0] * g.bins[0]));
+    const int y = min(g.bins[1] - 1, static_cast<int>(f[1] * g.bins[1]));
+    const int z = min(g.bins[2] - 1, static_cast<int>(f[2] * g.bins[2]));
+    const int b = (z * g.bins[1] + y) * g.bins[0] + x;
+    abin[a] = b;
+    atomicAdd(&bsize[b], 1);
+}
+
+__global__ void k_bin_fill(int N, const int* __restrict__ abin, int* __restrict__ cursor, int* __restrict__ batoms) {
+    const int a = blockIdx.x * blockDim.x + threadIdx.x;
+    if (a >= N) return;
+    const int slot = atomicAdd(&cursor[abin[a]], 1);
+    batoms[slot] = a;
+}
+
+// ascending atom index within each bin (insertion sort, neighbor_graph_kokkos.cpp:233-249)
+__global__ void k_sort_segments(int nseg, const long long* __restrict__ off, int* __restrict__ items) {
+    const int b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nseg) return;
+    const long long lo = off[b], hi = off[b + 1];
+    for (long long p = lo + 1; p < hi; ++p) {
+        const int v = items[p];
+        long long q = p - 1;
+        while (q >= lo && items[q] > v) {
+            items[q + 1] = items[q];
+            --q;
+        }
+        items[q + 1] = v;
+    }
+}
+
+template <bool FILL>
+__global__ void k_neighbor_visit(int N, Mat3 cell, BinGrid g, double cut2, const double* __restrict__ wfrac,
+                                 const double* __restrict__ wpos, const int* __restrict__ wrap,
+                                 const int* __restrict__ abin, const long long* __restrict__ boff,
+                                 const int* __restrict__ batoms, int* __restrict__ counts,
+                                 const long long* __restrict__ eoff, int* __restrict__ sources,
+                                 int* __restrict__ shifts, double* __restrict__ fxyz) {
+    const int rcv = blockIdx.x * blockDim.x + threadIdx.x;
+    if (rcv >= N) return;
+    const int rb = abin[rcv];
+    const int rx = rb % g.bins[0], ry = (rb / g.bins[0]) % g.bins[1], rz = rb / (g.bins[0] * g.bins[1]);
+    long long e = FILL ? eoff[rcv] : 0;
+    int local = 0;
+    for (int dz = -g.reach[2]; dz <= g.reach[2]; ++dz) {
+        const int raw_z = rz + dz, sz = floor_div(raw_z, g.bins[2]), bz = raw_z - sz * g.bins[2];
+        for (int dy = -g.reach[1]; dy <= g.reach[1]; ++dy) {
+            const int raw_y = ry + dy, sy = floor_div(raw_y, g.bins[1]), by = raw_y - sy * g.bins[1];
+            for (int dx = -g.reach[0]; dx <= g.reach[0]; ++dx) {
+                const int raw_x = rx + dx, sx = floor_div(raw_x, g.bins[0]), bx = raw_x - sx * g.bins[0];
+                const int sb = (bz * g.bins[1] + by) * g.bins[0] + bx;
+                const int image[3] = {sx, sy, sz};
+                for (long long idx = boff[sb]; idx < boff[sb + 1]; ++idx) {
+                    const int src = batoms[idx];
+                    if (src == rcv && sx == 0 && sy == 0 && sz == 0) continue;
+                    double d2 = 0.0;
+                    for (int c = 0; c < 3; ++c) {
+                        double d = wpos[3 * src + c] - wpos[3 * rcv + c];
+                        for (int ax = 0; ax < 3; ++ax) d += image[ax] * cell.v[3 * ax + c];
+                        d2 += d * d;
+                    }
+                    if (d2 > cut2) continue;
+                    if (FILL) {
+                        sources[e] = src;
+                        for (int ax = 0; ax < 3; ++ax) {
+                            shifts[3 * e + ax] = image[ax] - wrap[3 * src + ax] + wrap[3 * rcv + ax];
+                            fxyz[3 * e + ax] = wfrac[3 * src + ax] - wfrac[3 * rcv + ax] + image[ax];
+                        }
+                        ++e;
+                    }
+                    ++local;
+                }
+            }
+        }
+    }
+    if (!FILL) counts[rcv] = local;
+}
+
+// ---------------------------------------------------------------------------
+// Edge schedules: receiver of each edge, source transpose (edges ordered by
+// source, ascending edge id) -- lifecycle.cpp:3605-3823.
+// ---------------------------------------------------------------------------
+__global__ void k_receivers(int N, const int* __restrict__ off, int* __restrict__ receivers) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= N) return;
+    for (int e = off[i]; e < off[i + 1]; ++e) receivers[e] = i;
+}
+
+__global__ void k_count_sources(long long E, const int* __restrict__ sources, int* __restrict__ counts) {
+    const long long e = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (e >= E) return;
+    atomicAdd(&counts[sources[e]], 1);
+}
+
+__global__ void k_fill_sources(long long E, const int* __restrict__ sources, int* __restrict__ cursor,
+                               int* __restrict__ sedges) {
+    const long long e = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (e >= E) return;
+    const int slot = atomicAdd(&cursor[sources[e]], 1);
+    sedges[slot] = static_cast<int>(e);
+}
+
+__global__ void k_gather_int(long long n, const int* __restrict__ idx, const int* __restrict__ table,
+                             int* __restrict__ out) {
+    const long long e = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (e < n) out[e] = table[idx[e]];
+}
+
+__global__ void k_copy_i64_i32_plus(const long long* __restrict__ in, int* __restrict__ out, int n) {
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx <= n) out[idx] = static_cast<int>(in[idx]);
+}
+
+// ---------------------------------------------------------------------------
+// Prepared geometry (lifecycle.cpp:2915-3079)
+// ---------------------------------------------------------------------------
+__global__ void k_displacements(int N, Mat3 cell, Mat3 inv, const double* __restrict__ ref,
+                                const double* __restrict__ pos, double* __restrict__ disp) {
+    const int a = blockIdx.x * blockDim.x + threadIdx.x;
+    if (a >= N) return;
+    double delta[3], f[3];
+    for (int c = 0; c < 3; ++c) delta[c] = pos[3 * a + c] - ref[3 * a + c];
+    for (int lat = 0; lat < 3; ++lat) {
+        f[lat] = 0.0;
+        for (int c = 0; c < 3; ++c) f[lat] += delta[c] * inv.v[3 * c + lat];
+        f[lat] -= floor(f[lat] + 0.5);
+    }
+    for (int c = 0; c < 3; ++c) {
+        double v = 0.0;
+        for (int lat = 0; lat < 3; ++lat) v += f[lat] * cell.v[3 * lat + c];
+        disp[3 * a + c] = v;
+    }
+}
+
+__global__ void k_edge_xyz(long long E, Mat3 cell, const int* __restrict__ receivers, const int* __restrict__ sources,
+                           const double* __restrict__ fxyz, const double* __restrict__ disp, double cutoff,
+                           double* __restrict__ xyz, double* __restrict__ r, int* __restrict__ invalid) {
+    const long long e = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (e >= E) return;
+    const int rc = receivers[e], sc = sources[e];
+    double vec[3], d2 = 0.0;
+    for (int c = 0; c < 3; ++c) {
+        double ref = 0.0;
+        for (int lat = 0; lat < 3; ++lat) ref += fxyz[3 * e + lat] * cell.v[3 * lat + c];
+        vec[c] = ref + disp[3 * sc + c] - disp[3 * rc + c];
+        d2 += vec[c] * vec[c];
+    }
+    if (!isfinite(d2) || !(d2 > 0.0)) {
+        atomicAdd(invalid, 1);
+        xyz[3 * e] = cutoff;
+        xyz[3 * e + 1] = 0.0;
+        xyz[3 * e + 2] = 0.0;
+        r[e] = cutoff;
+        return;
+    }
+    const double dist = sqrt(d2);
+    const double scale = dist >= cutoff ? cutoff / dist : 1.0;
+    for (int c = 0; c < 3; ++c) xyz[3 * e + c] = scale * vec[c];
+    r[e] = dist >= cutoff ? cutoff : dist;
+}
+
+// ---------------------------------------------------------------------------
+// Per-edge records: spline point, Y, dY/dxyz, unit direction
+// ---------------------------------------------------------------------------
+constexpr double kSqrt4Pi = 3.5449077018110318;
+
+// Orthonormal real harmonics l <= LMAX of a unit vector (x,y,z) (already in the
+// shuffled frame (z, x, y) of the edge) and their Cartesian partials.
+template <int LMAX>
+__device__ __forceinline__ void real_harmonics(float x, float y, float z, float* v, float* dx, float* dy, float* dz) {
+    const double pi = 3.14159265358979323846;
+    v[0] = static_cast<float>(0.5 / sqrt(pi));
+    dx[0] = dy[0] = dz[0] = 0.0f;
+    if constexpr (LMAX >= 1) {
+        const float c1 = static_cast<float>(sqrt(3.0 / (4.0 * pi)));
+        v[1] = c1 * y; dx[1] = 0.0f; dy[1] = c1; dz[1] = 0.0f;
+        v[2] = c1 * z; dx[2] = 0.0f; dy[2] = 0.0f; dz[2] = c1;
+        v[3] = c1 * x; dx[3] = c1; dy[3] = 0.0f; dz[3] = 0.0f;
+    }
+    if constexpr (LMAX >= 2) {
+        const float c2 = static_cast<float>(0.5 * sqrt(15.0 / pi));
+        const float c20 = static_cast<float>(0.25 * sqrt(5.0 / pi));
+        const float c22 = static_cast<float>(0.25 * sqrt(15.0 / pi));
+        v[4] = c2 * x * y; dx[4] = c2 * y; dy[4] = c2 * x; dz[4] = 0.0f;
+        v[5] = c2 * y * z; dx[5] = 0.0f; dy[5] = c2 * z; dz[5] = c2 * y;
+        v[6] = c20 * (2 * z * z - x * x - y * y); dx[6] = -2 * c20 * x; dy[6] = -2 * c20 * y; dz[6] = 4 * c20 * z;
+        v[7] = c2 * x * z; dx[7] = c2 * z; dy[7] = 0.0f; dz[7] = c2 * x;
+        v[8] = c22 * (x * x - y * y); dx[8] = 2 * c22 * x; dy[8] = -2 * c22 * y; dz[8] = 0.0f;
+    }
+    if constexpr (LMAX >= 3) {
+        const float c33 = static_cast<float>(0.25 * sqrt(35.0 / (2.0 * pi)));
+        const float c32 = static_cast<float>(0.5 * sqrt(105.0 / pi));
+        const float c31 = static_cast<float>(0.25 * sqrt(21.0 / (2.0 * pi)));
+        const float c30 = static_cast<float>(0.25 * sqrt(7.0 / pi));
+        const float c32b = static_cast<float>(0.25 * sqrt(105.0 / pi));
+        const float r2 = x * x + y * y;
+        v[9] = c33 * y * (3 * x * x - y * y);
+        dx[9] = c33 * 6 * x * y; dy[9] = c33 * (3 * x * x - 3 * y * y); dz[9] = 0.0f;
+        v[10] = c32 * x * y * z;
+        dx[10] = c32 * y * z; dy[10] = c32 * x * z; dz[10] = c32 * x * y;
+        v[11] = c31 * y * (4 * z * z - r2);
+        dx[11] = c31 * (-2 * x * y); dy[11] = c31 * (4 * z * z - x * x - 3 * y * y); dz[11] = c31 * 8 * y * z;
+        v[12] = c30 * z * (2 * z * z - 3 * r2);
+        dx[12] = c30 * (-6 * x * z); dy[12] = c30 * (-6 * y * z); dz[12] = c30 * (6 * z * z - 3 * r2);
+        v[13] = c31 * x * (4 * z * z - r2);
+        dx[13] = c31 * (4 * z * z - 3 * x * x - y * y); dy[13] = c31 * (-2 * x * y); dz[13] = c31 * 8 * x * z;
+        v[14] = c32b * z * (x * x - y * y);
+        dx[14] = c32b * 2 * x * z; dy[14] = -c32b * 2 * y * z; dz[14] = c32b * (x * x - y * y);
+        v[15] = c33 * x * (x * x - 3 * y * y);
+        dx[15] = c33 * (3 * x * x - 3 * y * y); dy[15] = -c33 * 6 * x * y; dz[15] = 0.0f;
+    }
+}
+
+template <int LMAX>
+__global__ __launch_bounds__(256) void k_edge_records(long long E, const double* __restrict__ xyz,
+                                                      const double* __restrict__ r, double r_cut, float x0, float h,
+                                                      int intervals, float* __restrict__ erec) {
+    using S = Shape<LMAX, 0>;
+    constexpr int NY = S::NY;
+    const long long e = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (e >= E) return;
+    float* rec = erec + e * S::REC;
+    const double re = r[e];
+    if (!(re < r_cut)) {
+        for (int q = 0; q < S::REC; ++q) rec[q] = 0.0f;
+        return;
+    }
+    float d[3];
+    for (int c = 0; c < 3; ++c) d[c] = static_cast<float>(xyz[3 * e + c] / re);
+    const float rf = static_cast<float>(re);
+    // spline evaluation point (cubic_spline_set.cpp:33-46)
+    int interval = static_cast<int>(floorf((rf - x0) / h));
+    float xloc = rf - x0 - h * static_cast<float>(interval);
+    if (interval < 0) {
+        interval = 0;
+        xloc = 0.0f;
+    } else if (interval >= intervals) {
+        interval = intervals - 1;
+        xloc = h;
+    }
+    rec[0] = xloc;
+    rec[1] = __int_as_float(interval);
+    rec[2] = __int_as_float(1);
+    rec[3] = 0.0f;
+    // (x, y, z) -> (z, x, y), renormalised in FP32
+    float x = d[2], y = d[0], z = d[1];
+    const float rr = x * x + y * y + z * z;
+    const float inv = 1.0f / sqrtf(rr);
+    x *= inv;
+    y *= inv;
+    z *= inv;
+    float v[NY], dx[NY], dy[NY], dz[NY];
+    real_harmonics<LMAX>(x, y, z, v, dx, dy, dz);
+    const float scale = static_cast<float>(kSqrt4Pi) / rf;
+    for (int q = 0; q < NY; ++q) {
+        rec[S::REC_Y + q] = static_cast<float>(static_cast<double>(v[q]) * kSqrt4Pi);
+        const float radial = dx[q] * x + dy[q] * y + dz[q] * z;
+        const float gx = dx[q] - x * radial;
+        const float gy = dy[q] - y * radial;
+        const float gz = dz[q] - z * radial;
+        // unshuffle: d/dX = d/dy', d/dY = d/dz', d/dZ = d/dx'
+        rec[S::REC_DY + q] = scale * gy;
+        rec[S::REC_DY + NY + q] = scale * gz;
+        rec[S::REC_DY + 2 * NY + q] = scale * gx;
+    }
+    rec[S::REC_U] = d[0];
+    rec[S::REC_U + 1] = d[1];
+    rec[S::REC_U + 2] = d[2];
+    for (int q = S::REC_U + 3; q < S::REC; ++q) rec[q] = 0.0f;
+}
+
+Mat3 mat3(const double* p) {
+    Mat3 m;
+    for (int i = 0; i < 9; ++i) m.v[i] = p[i];
+    return m;
+}
+
+template <class T>
+T* dev_alloc(std::size_t n) {
+    void* p = nullptr;
+    SMX_HIP(hipMalloc(&p, std::max<std::size_t>(1, n) * sizeof(T)));
+    return static_cast<T*>(p);
+}
+
+}  // namespace
+
+std::int64_t device_exclusive_scan(const int* in, long long* out, int n, hipStream_t s) {
+    const int tiles = std::max(1, (n + kScanTile - 1) / kScanTile);
+    long long* sums = dev_alloc<long long>(tiles + 1);
+    k_scan_tiles<<<tiles, kScanThreads, 0, s>>>(in, out, n, sums);
+    SMX_LAUNCH_CHECK("scan_tiles");
+    k_scan_tile_sums<<<1, 1024, 0, s>>>(sums, tiles);
+    SMX_LAUNCH_CHECK("scan_tile_sums");
+    k_scan_add<<<blocks_for(std::max(n, 1), kScanThreads), kScanThreads, 0, s>>>(out, n, sums, tiles);
+    SMX_LAUNCH_CHECK("scan_add");
+    long long total = 0;
+    SMX_HIP(hipMemcpyAsync(&total, out + n, sizeof(long long), hipMemcpyDeviceToHost, s));
+    SMX_HIP(hipStreamSynchronize(s));
+    SMX_HIP(hipFree(sums));
+    return total;
+}
+
+void build_neighbor_list(int N, const double* positions_host, const double* cell_host, const double* inv_host,
+                         double cutoff, NeighborResult& out, hipStream_t s) {
+    if (!std::isfinite(cutoff) || !(cutoff > 0.0)) throw std::invalid_argument("neighbor cutoff must be positive");
+    if (N < 0) throw std::invalid_argument("negative atom count");
+    for (int i = 0; i < 3 * N; ++i)
+        if (!std::isfinite(positions_host[i])) throw std::invalid_argument("positions must be finite");
+    for (int row = 0; row < 3; ++row)
+        for (int col = 0; col < 3; ++col) {
+            double prod = 0.0;
+            for (int k = 0; k < 3; ++k) prod += cell_host[3 * row + k] * inv_host[3 * k + col];
+            if (std::abs(prod - (row == col ? 1.0 : 0.0)) > 1e-9)
+                throw std::invalid_argument("cell and inverse cell are inconsistent");
+        }
+    BinGrid g;
+    for (int ax = 0; ax < 3; ++ax) {
+        double ins = 0.0;
+        for (int c = 0; c < 3; ++c) ins += inv_host[3 * c + ax] * inv_host[3 * c + ax];
+        if (!(ins > 0.0)) throw std::invalid_argument("cell must be invertible");
+        const double face = 1.0 / std::sqrt(ins);
+        g.bins[ax] = std::max(1, static_cast<int>(std::floor(face / cutoff)));
+        const double rch = std::ceil(cutoff * std::sqrt(ins) * g.bins[ax]) + 1.0;
+        g.reach[ax] = std::max(1, static_cast<int>(rch));
+    }
+    const long long nb_ll = static_cast<long long>(g.bins[0]) * g.bins[1] * g.bins[2];
+    if (nb_ll > INT_MAX / 2) throw std::invalid_argument("neighbor bin grid is too large");
+    const int nb = static_cast<int>(nb_ll);
+    const Mat3 cell = mat3(cell_host), inv = mat3(inv_host);
+    const double cut2 = cutoff * cutoff;
+
+    double* d_pos = dev_alloc<double>(3 * static_cast<std::size_t>(N));
+    double* wfrac = dev_alloc<double>(3 * static_cast<std::size_t>(N));
+    double* wpos = dev_alloc<double>(3 * static_cast<std::size_t>(N));
+    int* wrap = dev_alloc<int>(3 * static_cast<std::size_t>(N));
+    int* abin = dev_alloc<int>(N);
+    int* bsize = dev_alloc<int>(nb);
+    long long* boff = dev_alloc<long long>(nb + 1);
+    int* cursor = dev_alloc<int>(nb);
+    int* batoms = dev_alloc<int>(N);
+    int* counts = dev_alloc<int>(N);
+    long long* eoff = dev_alloc<long long>(N + 1);
+    auto release = [&]() {
+        for (void* p : {static_cast<void*>(d_pos), static_cast<void*>(wfrac), static_cast<void*>(wpos),
+                        static_cast<void*>(wrap), static_cast<void*>(abin), static_cast<void*>(bsize),
+                        static_cast<void*>(boff), static_cast<void*>(cursor), static_cast<void*>(batoms),
+                        static_cast<void*>(counts), static_cast<void*>(eoff)})
+            (void)hipFree(p);
+    };
+    try {
+        SMX_HIP(hipMemcpyAsync(d_pos, positions_host, 3 * sizeof(double) * N, hipMemcpyHostToDevice, s));
+        SMX_HIP(hipMemsetAsync(bsize, 0, sizeof(int) * nb, s));
+        const unsigned ab = blocks_for(std::max(N, 1), 256);
+        if (N > 0) {
+            k_wrap<<<ab, 256, 0, s>>>(N, d_pos, cell, inv, g, wfrac, wpos, wrap, abin, bsize);
+            SMX_LAUNCH_CHECK("neighbor_wrap");
+        }
+        device_exclusive_scan(bsize, boff, nb, s);
+        k_i64_to_i32<<<blocks_for(nb, 256), 256, 0, s>>>(boff, cursor, nb);
+        SMX_LAUNCH_CHECK("neighbor_cursor");
+        if (N > 0) {
+            k_bin_fill<<<ab, 256, 0, s>>>(N, abin, cursor, batoms);
+            SMX_LAUNCH_CHECK("neighbor_bin_fill");
+        }
+        k_sort_segments<<<blocks_for(nb, 256), 256, 0, s>>>(nb, boff, batoms);
+        SMX_LAUNCH_CHECK("neighbor_sort_bins");
+        if (N > 0) {
+            k_neighbor_visit<false><<<blocks_for(N, 128), 128, 0, s>>>(N, cell, g, cut2, wfrac, wpos, wrap, abin, boff, batoms, counts,
+                                                       nullptr, nullptr, nullptr, nullptr);
+            SMX_LAUNCH_CHECK("neighbor_count");
+        }
+        const long long E = device_exclusive_scan(counts, eoff, N, s);
+        if (E > INT_MAX) throw std::length_error("neighbor edge count exceeds the 32-bit graph limit");
+        out.num_edges = E;
+        out.num_neigh = dev_alloc<int>(N);
+        out.offsets = dev_alloc<int>(N + 1);
+        out.sources = dev_alloc<int>(E);
+        out.shifts = dev_alloc<int>(3 * static_cast<std::size_t>(E));
+        out.fractional_xyz = dev_alloc<double>(3 * static_cast<std::size_t>(E));
+        SMX_HIP(hipMemcpyAsync(out.num_neigh, counts, sizeof(int) * N, hipMemcpyDeviceToDevice, s));
+        k_copy_i64_i32_plus<<<blocks_for(N + 1, 256), 256, 0, s>>>(eoff, out.offsets, N);
+        SMX_LAUNCH_CHECK("neighbor_offsets");
+        if (N > 0 && E > 0) {
+            k_neighbor_visit<true><<<blocks_for(N, 128), 128, 0, s>>>(N, cell, g, cut2, wfrac, wpos, wrap, abin, boff, batoms, nullptr,
+                                                      eoff, out.sources, out.shifts, out.fractional_xyz);
+            SMX_LAUNCH_CHECK("neighbor_fill");
+        }
+        SMX_HIP(hipStreamSynchronize(s));
+    } catch (...) {
+        release();
+        throw;
+    }
+    release();
+}
+
+void launch_graph_schedule(int N, std::int64_t E, const int* offsets, const int* sources, int* receivers, int* soff,
+                           int* sedges, int* scratch_counts, hipStream_t s) {
+    if (N == 0) return;
+    k_receivers<<<blocks_for(N, 256), 256, 0, s>>>(N, offsets, receivers);
+    SMX_LAUNCH_CHECK("graph_receivers");
+    SMX_HIP(hipMemsetAsync(scratch_counts, 0, sizeof(int) * N, s));
+    if (E > 0) {
+        k_count_sources<<<blocks_for(E, 256), 256, 0, s>>>(E, sources, scratch_counts);
+        SMX_LAUNCH_CHECK("graph_count_sources");
+    }
+    long long* off64 = dev_alloc<long long>(N + 1);
+    try {
+        device_exclusive_scan(scratch_counts, off64, N, s);
+        k_copy_i64_i32_plus<<<blocks_for(N + 1, 256), 256, 0, s>>>(off64, soff, N);
+        SMX_LAUNCH_CHECK("graph_source_offsets");
+        k_i64_to_i32<<<blocks_for(N, 256), 256, 0, s>>>(off64, scratch_counts, N);
+        SMX_LAUNCH_CHECK("graph_source_cursor");
+        if (E > 0) {
+            k_fill_sources<<<blocks_for(E, 256), 256, 0, s>>>(E, sources, scratch_counts, sedges);
+            SMX_LAUNCH_CHECK("graph_fill_sources");
+        }
+        k_sort_segments<<<blocks_for(N, 256), 256, 0, s>>>(N, off64, sedges);
+        SMX_LAUNCH_CHECK("graph_sort_sources");
+        SMX_HIP(hipStreamSynchronize(s));
+    } catch (...) {
+        (void)hipFree(off64);
+        throw;
+    }
+    SMX_HIP(hipFree(off64));
+}
+
+void launch_gather_types(std::int64_t E, const int* sources, const int* node_types, int* neigh_types,
+                         hipStream_t s) {
+    if (E == 0) return;
+    k_gather_int<<<blocks_for(E, 256), 256, 0, s>>>(E, sources, node_types, neigh_types);
+    SMX_LAUNCH_CHECK("gather_types");
+}
+
+void launch_prepared_geometry(int N, std::int64_t E, const int* receivers, const int* sources,
+                              const double* fractional_xyz, const double* cell, const double* inv_cell,
+                              const double* reference_positions, const double* positions, double cutoff, double* disp,
+                              double* xyz, double* r, int* invalid, hipStream_t s) {
+    const Mat3 c = mat3(cell), iv = mat3(inv_cell);
+    if (N > 0) {
+        k_displacements<<<blocks_for(N, 256), 256, 0, s>>>(N, c, iv, reference_positions, positions, disp);
+        SMX_LAUNCH_CHECK("geometry_displacements");
+    }
+    if (E > 0) {
+        k_edge_xyz<<<blocks_for(E, 256), 256, 0, s>>>(E, c, receivers, sources, fractional_xyz, disp, cutoff, xyz, r,
+                                                      invalid);
+        SMX_LAUNCH_CHECK("geometry_edges");
+    }
+}
+
+void geometry_records(int l_max, std::int64_t E, const double* xyz, const double* r, double r_cut, float x0, float h,
+                      int intervals, float* erec, hipStream_t s) {
+    if (E == 0) return;
+    if (l_max == 3)
+        k_edge_records<3><<<blocks_for(E, 256), 256, 0, s>>>(E, xyz, r, r_cut, x0, h, intervals, erec);
+    else if (l_max == 2)
+        k_edge_records<2><<<blocks_for(E, 256), 256, 0, s>>>(E, xyz, r, r_cut, x0, h, intervals, erec);
+    else
+        throw std::invalid_argument("edge records are compiled for l_max 2 and 3");
+    SMX_LAUNCH_CHECK("edge_records");
+}
+
+}  // namespace smx

@@ -1,0 +1,805 @@
+// MACE interaction kernels for MI355X (gfx950, wave64), FP32 with the
+// reference's FP64 islands (readout, node energies, directed forces, source
+// adjoint accumulation).
+//
+// Mapping: one workgroup owns one receiver (edge kernels) or one node (node
+// kernels); lanes are channels, so every per-channel table (spline
+// coefficients, H0/H1 features, polynomial coefficients) is read coalesced
+// while the per-edge quantities (Y, dY, spline interval, direction) are
+// wave-uniform and come through the scalar cache.  Receivers are owned, never
+// shared: every node quantity is a deterministic segment sum without atomics.
+//
+// Reference math (libsymmetrix/source):
+//   R0 forward  mace.cpp:1356-1403 (first_interaction.cpp:620-883)
+//   R0 reverse  mace.cpp:1486-1560 (first_interaction.cpp:992-1335)
+//   M0          mace.cpp:1639-1689, multivariate_polynomial.cpp:11-131
+//   R1 forward  mace.cpp:2023-2084 (h1_phi1.cpp:1385-1845)
+//   R1 reverse  mace.cpp:2199-2303 (factorized_execution.cpp:471-1460)
+//   M1/H2/readouts and their adjoints mace.cpp:2461-2657 with the FP64
+//   policy of mace_kokkos.hpp:1805-1828
+#include <algorithm>
+#include <stdexcept>
+#include <string>
+
+#include "device_common.hpp"
+#include "kernels.hpp"
+#include "shapes.hpp"
+
+namespace smx {
+namespace {
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float spline_value(float4 c, float x, float xx, float xxx) {
+    return c.x + c.y * x + c.z * xx + c.w * xxx;
+}
+__device__ __forceinline__ float spline_slope(float4 c, float x, float xx) {
+    return c.y + 2.0f * c.z * x + 3.0f * c.w * xx;
+}
+__device__ __forceinline__ bool edge_active(const float* rec) { return __float_as_int(rec[2]) != 0; }
+
+template <int C>
+struct Lanes {
+    static constexpr int NW = (C + kWave - 1) / kWave;
+    static constexpr int WIDTH = C < kWave ? C : kWave;
+};
+
+// Sum over the workgroup (C lanes, one value each); every lane gets the total.
+template <int C>
+__device__ __forceinline__ double block_sum(double v, double* sbuf) {
+    v = wave_sum<Lanes<C>::WIDTH>(v);
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    if (lane == 0) sbuf[wave] = v;
+    __syncthreads();
+    double t = 0.0;
+#pragma unroll
+    for (int w = 0; w < Lanes<C>::NW; ++w) t += sbuf[w];
+    __syncthreads();
+    return t;
+}
+
+// ---------------------------------------------------------------------------
+// Layer 1: Phi0[i,lm,k] = sum_j R0_{l,k}(r_ij) Y_lm(ij) H0[type_j,k]
+// ---------------------------------------------------------------------------
+template <int C, int LMAX>
+__global__ __launch_bounds__(C) void k_r0_forward(const int* __restrict__ offsets, const int* __restrict__ neigh_types,
+                                                  const float* __restrict__ erec, const float4* __restrict__ R0c,
+                                                  const float* __restrict__ H0, float* __restrict__ Phi0) {
+    using S = Shape<LMAX, 0>;
+    constexpr int NY = S::NY, NF = (LMAX + 1) * C;
+    const int i = xcd_remap(blockIdx.x, gridDim.x);
+    const int k = threadIdx.x;
+    float acc[NY];
+#pragma unroll
+    for (int v = 0; v < NY; ++v) acc[v] = 0.0f;
+    const int e0 = offsets[i], e1 = offsets[i + 1];
+    for (int e = e0; e < e1; ++e) {
+        const float* rec = erec + static_cast<std::size_t>(e) * S::REC;
+        if (!edge_active(rec)) continue;
+        const float x = rec[0];
+        const int iv = __float_as_int(rec[1]);
+        const float xx = x * x, xxx = xx * x;
+        const float h0 = H0[neigh_types[e] * C + k];
+        const float4* cf = R0c + static_cast<std::size_t>(iv) * NF + k;
+        static_for<0, LMAX + 1>([&](auto lc) {
+            constexpr int l = lc;
+            const float rad = spline_value(cf[l * C], x, xx, xxx);
+            static_for<0, 2 * l + 1>([&](auto mc) {
+                constexpr int lm = l * l + mc;
+                acc[lm] += rad * rec[S::REC_Y + lm] * h0;
+            });
+        });
+    }
+#pragma unroll
+    for (int v = 0; v < NY; ++v) Phi0[(static_cast<std::size_t>(i) * NY + v) * C + k] = acc[v];
+}
+
+// Per-edge directed forces: per-lane partials (fx,fy,fz) are summed over the
+// channels of the workgroup; chunks of edges are finalised together.
+template <int C, int CHUNK>
+struct EdgeForceSink {
+    float (*part)[CHUNK][3];
+    __device__ __forceinline__ void put(int slot, float fx, float fy, float fz) {
+        fx = wave_sum<Lanes<C>::WIDTH>(fx);
+        fy = wave_sum<Lanes<C>::WIDTH>(fy);
+        fz = wave_sum<Lanes<C>::WIDTH>(fz);
+        if (threadIdx.x % kWave == 0) {
+            const int w = threadIdx.x / kWave;
+            part[w][slot][0] = fx;
+            part[w][slot][1] = fy;
+            part[w][slot][2] = fz;
+        }
+    }
+    __device__ __forceinline__ void zero(int slot) {
+        if (threadIdx.x % kWave == 0) {
+            const int w = threadIdx.x / kWave;
+            part[w][slot][0] = part[w][slot][1] = part[w][slot][2] = 0.0f;
+        }
+    }
+    // node_forces[e] = -f (assign) or node_forces[e] -= f (accumulate)
+    template <bool ACCUMULATE>
+    __device__ __forceinline__ void flush(int c0, int count, double* __restrict__ node_forces) {
+        __syncthreads();
+        for (int t = threadIdx.x; t < count * 3; t += C) {
+            const int el = t / 3, comp = t % 3;
+            float s = 0.0f;
+#pragma unroll
+            for (int w = 0; w < Lanes<C>::NW; ++w) s += part[w][el][comp];
+            double* dst = node_forces + static_cast<std::size_t>(c0 + el) * 3 + comp;
+            if (ACCUMULATE)
+                *dst = *dst - static_cast<double>(s);
+            else
+                *dst = 0.0 - static_cast<double>(s);
+        }
+        __syncthreads();
+    }
+};
+
+constexpr int kForceChunk = 64;
+
+// Layer-1 reverse: node_forces[e] -= sum_k sum_lm Phi0_adj[i,lm,k] H0 (u dR Y + R dY)
+template <int C, int LMAX>
+__global__ __launch_bounds__(C) void k_r0_reverse(const int* __restrict__ offsets, const int* __restrict__ neigh_types,
+                                                  const float* __restrict__ erec, const float4* __restrict__ R0c,
+                                                  const float* __restrict__ H0, const float* __restrict__ Phi0_adj,
+                                                  double* __restrict__ node_forces) {
+    using S = Shape<LMAX, 0>;
+    constexpr int NY = S::NY, NF = (LMAX + 1) * C;
+    __shared__ float part[Lanes<C>::NW][kForceChunk][3];
+    EdgeForceSink<C, kForceChunk> sink{part};
+    const int i = xcd_remap(blockIdx.x, gridDim.x);
+    const int k = threadIdx.x;
+    float padj[NY];
+#pragma unroll
+    for (int v = 0; v < NY; ++v) padj[v] = Phi0_adj[(static_cast<std::size_t>(i) * NY + v) * C + k];
+    const int e0 = offsets[i], e1 = offsets[i + 1];
+    for (int c0 = e0; c0 < e1; c0 += kForceChunk) {
+        const int c1 = min(c0 + kForceChunk, e1);
+        for (int e = c0; e < c1; ++e) {
+            const float* rec = erec + static_cast<std::size_t>(e) * S::REC;
+            if (!edge_active(rec)) {
+                sink.zero(e - c0);
+                continue;
+            }
+            const float x = rec[0];
+            const int iv = __float_as_int(rec[1]);
+            const float xx = x * x, xxx = xx * x;
+            const float h0 = H0[neigh_types[e] * C + k];
+            const float4* cf = R0c + static_cast<std::size_t>(iv) * NF + k;
+            float a = 0.0f, b0 = 0.0f, b1 = 0.0f, b2 = 0.0f;
+            static_for<0, LMAX + 1>([&](auto lc) {
+                constexpr int l = lc;
+                const float4 c4 = cf[l * C];
+                const float R = spline_value(c4, x, xx, xxx);
+                const float dR = spline_slope(c4, x, xx);
+                static_for<0, 2 * l + 1>([&](auto mc) {
+                    constexpr int lm = l * l + mc;
+                    const float t = padj[lm] * h0;
+                    a += dR * rec[S::REC_Y + lm] * t;
+                    const float rt = R * t;
+                    b0 += rt * rec[S::REC_DY + lm];
+                    b1 += rt * rec[S::REC_DY + NY + lm];
+                    b2 += rt * rec[S::REC_DY + 2 * NY + lm];
+                });
+            });
+            const float u0 = rec[S::REC_U], u1 = rec[S::REC_U + 1], u2 = rec[S::REC_U + 2];
+            sink.put(e - c0, u0 * a + b0, u1 * a + b1, u2 * a + b2);
+        }
+        sink.template flush<true>(c0, c1 - c0, node_forces);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Layer 2 (R1): rows[i,(p,m1,m2),k] = sum_j R1_{p,k}(r) Y_{lm1} H1[j,lm2,k];
+// Phi1[i,lme,k] = sum CG rows (dense per-path coupling blocks).
+// ---------------------------------------------------------------------------
+template <int C, int LMAX, int LMAXH>
+__global__ __launch_bounds__(C) void k_r1_forward(const int* __restrict__ offsets, const int* __restrict__ neigh,
+                                                  const float* __restrict__ erec, const float4* __restrict__ R1c,
+                                                  const float* __restrict__ H1, const float* __restrict__ cg,
+                                                  float* __restrict__ Phi1) {
+    using S = Shape<LMAX, LMAXH>;
+    constexpr int NH = S::NH, NF = S::P * C;
+    const int i = xcd_remap(blockIdx.x, gridDim.x);
+    const int k = threadIdx.x;
+    float rows[S::NROWS];
+#pragma unroll
+    for (int r = 0; r < S::NROWS; ++r) rows[r] = 0.0f;
+    const int e0 = offsets[i], e1 = offsets[i + 1];
+    for (int e = e0; e < e1; ++e) {
+        const float* rec = erec + static_cast<std::size_t>(e) * S::REC;
+        if (!edge_active(rec)) continue;
+        const float x = rec[0];
+        const int iv = __float_as_int(rec[1]);
+        const float xx = x * x, xxx = xx * x;
+        const float* hj = H1 + static_cast<std::size_t>(neigh[e]) * NH * C + k;
+        float h[NH];
+#pragma unroll
+        for (int q = 0; q < NH; ++q) h[q] = hj[q * C];
+        const float4* cf = R1c + static_cast<std::size_t>(iv) * NF + k;
+        static_for<0, S::P>([&](auto pc) {
+            constexpr int p = pc;
+            constexpr int le = S::paths[p].le, ls = S::paths[p].ls, rb = S::row_base[p];
+            const float rad = spline_value(cf[p * C], x, xx, xxx);
+            static_for<0, 2 * le + 1>([&](auto m1c) {
+                constexpr int m1 = m1c;
+                const float ry = rad * rec[S::REC_Y + le * le + m1];
+                static_for<0, 2 * ls + 1>([&](auto m2c) {
+                    constexpr int m2 = m2c;
+                    rows[rb + m1 * (2 * ls + 1) + m2] += ry * h[ls * ls + m2];
+                });
+            });
+        });
+    }
+    float out[S::NLME];
+#pragma unroll
+    for (int q = 0; q < S::NLME; ++q) out[q] = 0.0f;
+    static_for<0, S::P>([&](auto pc) {
+        constexpr int p = pc;
+        constexpr int le = S::paths[p].le, ls = S::paths[p].ls, lo = S::paths[p].lo;
+        constexpr int rb = S::row_base[p], co = S::cg_offset[p];
+        static_for<0, (2 * le + 1) * (2 * ls + 1)>([&](auto rc) {
+            constexpr int r = rc;
+            static_for<0, 2 * lo + 1>([&](auto mc) {
+                constexpr int mo = mc;
+                constexpr int q = S::lme(p, mo);
+                out[q] += cg[co + r * (2 * lo + 1) + mo] * rows[rb + r];
+            });
+        });
+    });
+#pragma unroll
+    for (int q = 0; q < S::NLME; ++q) Phi1[(static_cast<std::size_t>(i) * S::NLME + q) * C + k] = out[q];
+}
+
+// Fused R1 reverse, receiver-owned: per edge the directed force
+//   f_e = -sum_k sum_rows G[row] H1[j,lm2] (u dR Y_lm1 + R dY_lm1)
+// and the per-edge source-adjoint contribution
+//   W_e[lm2,k] = sum_{p,m1} R Y_lm1 G[row]
+// that k_source_gather sums over each source's edges.
+template <int C, int LMAX, int LMAXH>
+__global__ __launch_bounds__(C) void k_r1_reverse(const int* __restrict__ offsets, const int* __restrict__ neigh,
+                                                  const float* __restrict__ erec, const float4* __restrict__ R1c,
+                                                  const float* __restrict__ H1, const float* __restrict__ cg,
+                                                  const float* __restrict__ dPhi1, float* __restrict__ Wsrc,
+                                                  double* __restrict__ node_forces) {
+    using S = Shape<LMAX, LMAXH>;
+    constexpr int NY = S::NY, NH = S::NH, NF = S::P * C;
+    __shared__ float part[Lanes<C>::NW][kForceChunk][3];
+    EdgeForceSink<C, kForceChunk> sink{part};
+    const int i = xcd_remap(blockIdx.x, gridDim.x);
+    const int k = threadIdx.x;
+    float G[S::NROWS];
+    {
+        float d[S::NLME];
+#pragma unroll
+        for (int q = 0; q < S::NLME; ++q) d[q] = dPhi1[(static_cast<std::size_t>(i) * S::NLME + q) * C + k];
+        static_for<0, S::P>([&](auto pc) {
+            constexpr int p = pc;
+            constexpr int le = S::paths[p].le, ls = S::paths[p].ls, lo = S::paths[p].lo;
+            constexpr int rb = S::row_base[p], co = S::cg_offset[p];
+            static_for<0, (2 * le + 1) * (2 * ls + 1)>([&](auto rc) {
+                constexpr int r = rc;
+                float g = 0.0f;
+                static_for<0, 2 * lo + 1>([&](auto mc) {
+                    constexpr int mo = mc;
+                    constexpr int q = S::lme(p, mo);
+                    g += cg[co + r * (2 * lo + 1) + mo] * d[q];
+                });
+                G[rb + r] = g;
+            });
+        });
+    }
+    const int e0 = offsets[i], e1 = offsets[i + 1];
+    for (int c0 = e0; c0 < e1; c0 += kForceChunk) {
+        const int c1 = min(c0 + kForceChunk, e1);
+        for (int e = c0; e < c1; ++e) {
+            const float* rec = erec + static_cast<std::size_t>(e) * S::REC;
+            if (!edge_active(rec)) {
+                sink.zero(e - c0);
+                continue;
+            }
+            const float x = rec[0];
+            const int iv = __float_as_int(rec[1]);
+            const float xx = x * x, xxx = xx * x;
+            const float* hj = H1 + static_cast<std::size_t>(neigh[e]) * NH * C + k;
+            float h[NH], W[NH];
+#pragma unroll
+            for (int q = 0; q < NH; ++q) {
+                h[q] = hj[q * C];
+                W[q] = 0.0f;
+            }
+            const float4* cf = R1c + static_cast<std::size_t>(iv) * NF + k;
+            float a = 0.0f, b0 = 0.0f, b1 = 0.0f, b2 = 0.0f;
+            static_for<0, S::P>([&](auto pc) {
+                constexpr int p = pc;
+                constexpr int le = S::paths[p].le, ls = S::paths[p].ls, rb = S::row_base[p];
+                const float4 c4 = cf[p * C];
+                const float R = spline_value(c4, x, xx, xxx);
+                const float dR = spline_slope(c4, x, xx);
+                static_for<0, 2 * le + 1>([&](auto m1c) {
+                    constexpr int m1 = m1c;
+                    constexpr int lm1 = le * le + m1;
+                    const float y = rec[S::REC_Y + lm1];
+                    const float ry = R * y;
+                    float sr = 0.0f;
+                    static_for<0, 2 * ls + 1>([&](auto m2c) {
+                        constexpr int m2 = m2c;
+                        const float g = G[rb + m1 * (2 * ls + 1) + m2];
+                        sr += g * h[ls * ls + m2];
+                        W[ls * ls + m2] += ry * g;
+                    });
+                    a += dR * y * sr;
+                    const float t = R * sr;
+                    b0 += t * rec[S::REC_DY + lm1];
+                    b1 += t * rec[S::REC_DY + NY + lm1];
+                    b2 += t * rec[S::REC_DY + 2 * NY + lm1];
+                });
+            });
+            float* wdst = Wsrc + static_cast<std::size_t>(e) * NH * C + k;
+#pragma unroll
+            for (int q = 0; q < NH; ++q) wdst[q * C] = W[q];
+            const float u0 = rec[S::REC_U], u1 = rec[S::REC_U + 1], u2 = rec[S::REC_U + 2];
+            sink.put(e - c0, u0 * a + b0, u1 * a + b1, u2 * a + b2);
+        }
+        sink.template flush<false>(c0, c1 - c0, node_forces);
+    }
+}
+
+// H1_adj[s] = sum over the edges leaving s (source transpose order) of W_e,
+// accumulated in FP64 like the reference's source-adjoint accumulator.
+template <int C, int NH>
+__global__ __launch_bounds__(C) void k_source_gather(const int* __restrict__ soff, const int* __restrict__ sedges,
+                                                     const float* __restrict__ erec, int rec_floats,
+                                                     const float* __restrict__ Wsrc, float* __restrict__ H1_adj) {
+    const int s = xcd_remap(blockIdx.x, gridDim.x);
+    const int k = threadIdx.x;
+    double acc[NH];
+#pragma unroll
+    for (int q = 0; q < NH; ++q) acc[q] = 0.0;
+    const int q0 = soff[s], q1 = soff[s + 1];
+    for (int t = q0; t < q1; ++t) {
+        const int e = sedges[t];
+        if (!edge_active(erec + static_cast<std::size_t>(e) * rec_floats)) continue;
+        const float* w = Wsrc + static_cast<std::size_t>(e) * NH * C + k;
+#pragma unroll
+        for (int q = 0; q < NH; ++q) acc[q] += static_cast<double>(w[q * C]);
+    }
+#pragma unroll
+    for (int q = 0; q < NH; ++q) H1_adj[(static_cast<std::size_t>(s) * NH + q) * C + k] = static_cast<float>(acc[q]);
+}
+
+// ---------------------------------------------------------------------------
+// Product basis (symmetric contraction) polynomials.  Variables live in LDS
+// (column k per lane) so the wave-uniform monomial table can index them.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float monomial(const float* xs, int C, int k, int pk) {
+    const int deg = pk >> 24;
+    float prod = xs[(pk & 0xff) * C + k];
+    if (deg > 1) prod *= xs[((pk >> 8) & 0xff) * C + k];
+    if (deg > 2) prod *= xs[((pk >> 16) & 0xff) * C + k];
+    return prod;
+}
+
+// gs[v] += d f / d x_v for one term with coefficient c (product rule in the
+// reference's order: the coefficient times the other factors in turn).
+__device__ __forceinline__ void monomial_grad(const float* xs, float* gs, int C, int k, int pk, float c) {
+    const int deg = pk >> 24;
+    const int v0 = pk & 0xff, v1 = (pk >> 8) & 0xff, v2 = (pk >> 16) & 0xff;
+    if (deg == 1) {
+        gs[v0 * C + k] += c;
+    } else if (deg == 2) {
+        const float x0 = xs[v0 * C + k], x1 = xs[v1 * C + k];
+        gs[v0 * C + k] += c * x1;
+        gs[v1 * C + k] += c * x0;
+    } else {
+        const float x0 = xs[v0 * C + k], x1 = xs[v1 * C + k], x2 = xs[v2 * C + k];
+        gs[v0 * C + k] += c * x1 * x2;
+        gs[v1 * C + k] += c * x0 * x2;
+        gs[v2 * C + k] += c * x0 * x1;
+    }
+}
+
+template <int C, int NY, int NH>
+__global__ __launch_bounds__(C) void k_m0_forward(const int* __restrict__ types, const float* __restrict__ A0,
+                                                  const std::int32_t* __restrict__ terms, const int* __restrict__ toff,
+                                                  int T0, const float* __restrict__ coef, float* __restrict__ M0) {
+    __shared__ float xs[NY * C];
+    const int i = blockIdx.x;
+    const int k = threadIdx.x;
+#pragma unroll
+    for (int v = 0; v < NY; ++v) xs[v * C + k] = A0[(static_cast<std::size_t>(i) * NY + v) * C + k];
+    const float* cf = coef + static_cast<std::size_t>(types[i]) * T0 * C + k;
+#pragma unroll
+    for (int LM = 0; LM < NH; ++LM) {
+        const int begin = toff[LM], end = toff[LM + 1];
+        float f = 0.0f;
+        for (int t = begin; t < end; ++t) f += cf[static_cast<std::size_t>(t) * C] * monomial(xs, C, k, terms[t]);
+        M0[(static_cast<std::size_t>(i) * NH + LM) * C + k] = f;
+    }
+}
+
+template <int C, int NY, int NH>
+__global__ __launch_bounds__(C) void k_m0_reverse(const int* __restrict__ types, const float* __restrict__ A0,
+                                                  const float* __restrict__ M0_adj, const float* __restrict__ direct,
+                                                  const std::int32_t* __restrict__ terms, const int* __restrict__ toff,
+                                                  int T0, const float* __restrict__ coef,
+                                                  float* __restrict__ A0_adj) {
+    __shared__ float xs[NY * C];
+    __shared__ float gs[NY * C];
+    const int i = blockIdx.x;
+    const int k = threadIdx.x;
+#pragma unroll
+    for (int v = 0; v < NY; ++v) xs[v * C + k] = A0[(static_cast<std::size_t>(i) * NY + v) * C + k];
+    float acc[NY];
+#pragma unroll
+    for (int v = 0; v < NY; ++v) acc[v] = 0.0f;
+    const float* cf = coef + static_cast<std::size_t>(types[i]) * T0 * C + k;
+#pragma unroll
+    for (int LM = 0; LM < NH; ++LM) {
+        const int begin = toff[LM], end = toff[LM + 1];
+        float adj = M0_adj[(static_cast<std::size_t>(i) * NH + LM) * C + k];
+        if (LM == 0) adj += direct[static_cast<std::size_t>(i) * C + k];
+#pragma unroll
+        for (int v = 0; v < NY; ++v) gs[v * C + k] = 0.0f;
+        for (int t = begin; t < end; ++t) monomial_grad(xs, gs, C, k, terms[t], cf[static_cast<std::size_t>(t) * C]);
+#pragma unroll
+        for (int v = 0; v < NY; ++v) acc[v] += gs[v * C + k] * adj;
+    }
+#pragma unroll
+    for (int v = 0; v < NY; ++v) A0_adj[(static_cast<std::size_t>(i) * NY + v) * C + k] = acc[v];
+}
+
+// M1, H2 (FP64), readouts (FP64) and their adjoints for one node:
+//   E_i = E0[z] + q.x + MLP(H2), H2 = T_z^T x + W^T M1 (x = M0[i,0,:])
+//   direct = q + T_z H2_adj, A1_adj[v] = dM1/dA1_v * (W H2_adj)
+template <int C, int NY, int NH>
+__global__ __launch_bounds__(C) void k_readout(
+    const int* __restrict__ types, const float* __restrict__ A1, const float* __restrict__ M0,
+    const std::int32_t* __restrict__ m1_terms, int T1, const float* __restrict__ m1_coef,
+    const float* __restrict__ H2_T, const float* __restrict__ H2_Tt, const float* __restrict__ H2_M1,
+    const float* __restrict__ H2_M1t, const double* __restrict__ q, const double* __restrict__ W1r,
+    const double* __restrict__ W2r, int hidden, double scale, const double* __restrict__ E0,
+    double* __restrict__ node_energies, float* __restrict__ direct, float* __restrict__ A1_adj) {
+    __shared__ float xs[NY * C];
+    __shared__ float gs[NY * C];
+    __shared__ double sx[C], sm1[C], sh2a[C];
+    __shared__ double sbuf[Lanes<C>::NW];
+    const int i = blockIdx.x;
+    const int k = threadIdx.x;
+    const int t = types[i];
+#pragma unroll
+    for (int v = 0; v < NY; ++v) {
+        xs[v * C + k] = A1[(static_cast<std::size_t>(i) * NY + v) * C + k];
+        gs[v * C + k] = 0.0f;
+    }
+    const float* cf = m1_coef + static_cast<std::size_t>(t) * T1 * C + k;
+    float m1 = 0.0f;
+    for (int s = 0; s < T1; ++s) {
+        const float c = cf[static_cast<std::size_t>(s) * C];
+        const int pk = m1_terms[s];
+        m1 += c * monomial(xs, C, k, pk);
+        monomial_grad(xs, gs, C, k, pk, c);
+    }
+    const float xa = M0[static_cast<std::size_t>(i) * NH * C + k];
+    sx[k] = static_cast<double>(xa);
+    sm1[k] = static_cast<double>(m1);
+    __syncthreads();
+    const float* T = H2_T + static_cast<std::size_t>(t) * C * C;
+    double h2 = 0.0;
+    for (int in = 0; in < C; ++in) h2 += static_cast<double>(T[in * C + k]) * sx[in];
+    for (int in = 0; in < C; ++in) h2 += static_cast<double>(H2_M1[in * C + k]) * sm1[in];
+    double e = E0[t] + block_sum<C>(q[k] * sx[k], sbuf);
+    double out = 0.0, h2a = 0.0;
+    for (int hd = 0; hd < hidden; ++hd) {
+        const double w1 = W1r[static_cast<std::size_t>(hd) * C + k];
+        const double z = block_sum<C>(w1 * h2, sbuf);
+        const double sg = 1.0 / (1.0 + exp(-z));
+        const double act = scale * z * sg;
+        const double dact = scale * sg + scale * z * sg * (1.0 - sg);
+        out += W2r[hd] * act;
+        h2a += W2r[hd] * dact * w1;
+    }
+    if (k == 0) node_energies[i] = e + out;
+    sh2a[k] = h2a;
+    __syncthreads();
+    const float* Tt = H2_Tt + static_cast<std::size_t>(t) * C * C;
+    double dsum = q[k], s1 = 0.0;
+    for (int o = 0; o < C; ++o) {
+        dsum += static_cast<double>(Tt[o * C + k]) * sh2a[o];
+        s1 += static_cast<double>(H2_M1t[o * C + k]) * sh2a[o];
+    }
+    direct[static_cast<std::size_t>(i) * C + k] = static_cast<float>(dsum);
+    const float m1adj = static_cast<float>(s1);
+#pragma unroll
+    for (int v = 0; v < NY; ++v) A1_adj[(static_cast<std::size_t>(i) * NY + v) * C + k] = gs[v * C + k] * m1adj;
+}
+
+// ---------------------------------------------------------------------------
+// Node linears on MFMA: out[row, n] = sum_k in[row, k] W[k, n] for 16 rows of
+// one weight group, 64 columns per wave (four 16x16 tiles), FP32 in and out
+// (v_mfma_f32_16x16x4_f32).  Lane l supplies A[l%16][l/16], B[l/16][l%16] and
+// holds D[4*(l/16)+v][l%16]; the K order inside one 16-wide step is permuted
+// so that each lane reads four consecutive inputs with one 16-byte load.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(64) void k_node_gemm(const GemmTile* __restrict__ tiles,
+                                                  const GemmGroup* __restrict__ groups,
+                                                  const int* __restrict__ node_list, const float* __restrict__ W,
+                                                  const float* __restrict__ in, float* __restrict__ out) {
+    const GemmTile tile = tiles[blockIdx.x];
+    const GemmGroup g = groups[tile.group];
+    const int n0 = blockIdx.y * 64;
+    if (n0 >= g.N) return;
+    const int lane = threadIdx.x;
+    const int r = lane & 15, kg = lane >> 4;
+    const int nsub = min(4, (g.N - n0) / 16);
+    const bool row_ok = r < tile.count;
+    const int node = row_ok ? node_list[tile.list_start + r] : 0;
+    const float* arow = in + static_cast<std::size_t>(node) * g.in_stride + g.in_base + tile.m * g.in_mstride;
+    const float* Wg = W + g.w_off + n0 + r;
+    v4f acc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int k0 = 0; k0 < g.K; k0 += 16) {
+        float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (row_ok) a = *reinterpret_cast<const float4*>(arow + k0 + 4 * kg);
+        const float av[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const float* brow = Wg + static_cast<std::size_t>(k0 + 4 * kg + s) * g.N;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (j < nsub) acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[s], brow[16 * j], acc[j], 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        const int row = 4 * kg + v;
+        if (row >= tile.count) continue;
+        const int nd = node_list[tile.list_start + row];
+        float* orow = out + static_cast<std::size_t>(nd) * g.out_stride + g.out_base + tile.m * g.out_mstride + n0 + r;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (j < nsub) orow[16 * j] = acc[j][v];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Reductions
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_atom_forces(int N, const int* __restrict__ offsets,
+                                                     const int* __restrict__ soff, const int* __restrict__ sedges,
+                                                     const double* __restrict__ nf, double* __restrict__ F) {
+    const int a = blockIdx.x * blockDim.x + threadIdx.x;
+    if (a >= N) return;
+    double f0 = 0.0, f1 = 0.0, f2 = 0.0;
+    for (int t = soff[a]; t < soff[a + 1]; ++t) {
+        const int e = sedges[t];
+        f0 += nf[3 * static_cast<std::size_t>(e)];
+        f1 += nf[3 * static_cast<std::size_t>(e) + 1];
+        f2 += nf[3 * static_cast<std::size_t>(e) + 2];
+    }
+    for (int e = offsets[a]; e < offsets[a + 1]; ++e) {
+        f0 -= nf[3 * static_cast<std::size_t>(e)];
+        f1 -= nf[3 * static_cast<std::size_t>(e) + 1];
+        f2 -= nf[3 * static_cast<std::size_t>(e) + 2];
+    }
+    F[3 * static_cast<std::size_t>(a)] = f0;
+    F[3 * static_cast<std::size_t>(a) + 1] = f1;
+    F[3 * static_cast<std::size_t>(a) + 2] = f2;
+}
+
+constexpr int kReduceThreads = 256;
+
+__global__ __launch_bounds__(kReduceThreads) void k_stress_partial(std::int64_t E, const double* __restrict__ nf,
+                                                                   const double* __restrict__ xyz,
+                                                                   double* __restrict__ partial) {
+    double s[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
+    const std::int64_t stride = static_cast<std::int64_t>(gridDim.x) * blockDim.x;
+    for (std::int64_t e = static_cast<std::int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < E; e += stride)
+        for (int a = 0; a < 3; ++a)
+            for (int b = 0; b < 3; ++b) s[3 * a + b] += nf[3 * e + a] * xyz[3 * e + b];
+    __shared__ double red[9][kReduceThreads / kWave];
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    for (int c = 0; c < 9; ++c) {
+        const double v = wave_sum<kWave>(s[c]);
+        if (lane == 0) red[c][wave] = v;
+    }
+    __syncthreads();
+    if (threadIdx.x < 9) {
+        double t = 0.0;
+        for (int w = 0; w < kReduceThreads / kWave; ++w) t += red[threadIdx.x][w];
+        partial[static_cast<std::size_t>(blockIdx.x) * 9 + threadIdx.x] = t;
+    }
+}
+
+__global__ void k_stress_final(int blocks, const double* __restrict__ partial, double volume,
+                               double* __restrict__ stress) {
+    const int c = threadIdx.x;
+    if (c >= 9) return;
+    double t = 0.0;
+    for (int b = 0; b < blocks; ++b) t += partial[static_cast<std::size_t>(b) * 9 + c];
+    stress[c] = -t / volume;
+}
+
+__global__ __launch_bounds__(1024) void k_energy_sum(int N, const double* __restrict__ e, double* __restrict__ total) {
+    double s = 0.0;
+    for (int i = threadIdx.x; i < N; i += blockDim.x) s += e[i];
+    __shared__ double red[1024 / kWave];
+    s = wave_sum<kWave>(s);
+    if (threadIdx.x % kWave == 0) red[threadIdx.x / kWave] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double t = 0.0;
+        for (int w = 0; w < 1024 / kWave; ++w) t += red[w];
+        total[0] = t;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Kernel set of one shape
+// ---------------------------------------------------------------------------
+struct TimerScope {
+    LaunchTimer* t;
+    const char* name;
+    hipStream_t s;
+    TimerScope(LaunchTimer* t_, const char* n, hipStream_t s_) : t(t_), name(n), s(s_) {
+        if (t) t->begin(name, s);
+    }
+    ~TimerScope() {
+        if (t) t->end(name, s);
+    }
+};
+
+template <int C, int LMAX, int LMAXH>
+struct KernelSetImpl final : KernelSet {
+    using S = Shape<LMAX, LMAXH>;
+    int record_floats() const override { return S::REC; }
+
+    void edge_geometry(const DeviceModel& m, std::int64_t E, const double* xyz, const double* r, float* erec,
+                       hipStream_t s) const override {
+        geometry_records(LMAX, E, xyz, r, m.r_cut, m.x0, m.h, m.intervals, erec, s);
+    }
+
+    void forward(const DeviceModel& m, const DeviceGraph& g, const Workspace& w, const GemmPlan& a0,
+                 const GemmPlan& h1, const GemmPlan& a1, hipStream_t s, LaunchTimer* tm) const override {
+        const int N = g.N;
+        if (N == 0) return;
+        {
+            TimerScope ts(tm, "r0_forward", s);
+            k_r0_forward<C, LMAX><<<N, C, 0, s>>>(g.offsets, g.neigh_types, g.erec, m.R0c, m.H0, w.Phi0);
+            SMX_LAUNCH_CHECK("r0_forward");
+        }
+        {
+            TimerScope ts(tm, "a0_linear", s);
+            launch_node_gemm(a0, m.A0_w, w.Phi0, w.A0, s);
+        }
+        {
+            TimerScope ts(tm, "m0_forward", s);
+            k_m0_forward<C, S::NY, S::NH><<<N, C, 0, s>>>(g.node_types, w.A0, m.m0_terms, m.m0_toff, m.T0, m.m0_coef, w.M0);
+            SMX_LAUNCH_CHECK("m0_forward");
+        }
+        {
+            TimerScope ts(tm, "h1_linear", s);
+            launch_node_gemm(h1, m.H1_w, w.M0, w.H1, s);
+        }
+        {
+            TimerScope ts(tm, "r1_forward", s);
+            k_r1_forward<C, LMAX, LMAXH><<<N, C, 0, s>>>(g.offsets, g.neigh, g.erec, m.R1c, w.H1, m.cg, w.Phi1);
+            SMX_LAUNCH_CHECK("r1_forward");
+        }
+        {
+            TimerScope ts(tm, "a1_linear", s);
+            launch_node_gemm(a1, m.A1_w, w.Phi1, w.A1, s);
+        }
+        {
+            TimerScope ts(tm, "readout", s);
+            k_readout<C, S::NY, S::NH><<<N, C, 0, s>>>(g.node_types, w.A1, w.M0, m.m1_terms, m.T1, m.m1_coef, m.H2_T,
+                                                      m.H2_Tt, m.H2_M1, m.H2_M1t, m.q, m.W1r, m.W2r, m.hidden,
+                                                      m.readout_scale, m.E0, w.node_energies, w.direct, w.A1_adj);
+            SMX_LAUNCH_CHECK("readout");
+        }
+    }
+
+    void reverse(const DeviceModel& m, const DeviceGraph& g, const Workspace& w, const GemmPlan& a0r,
+                 const GemmPlan& h1r, const GemmPlan& a1r, hipStream_t s, LaunchTimer* tm) const override {
+        const int N = g.N;
+        if (N == 0) return;
+        {
+            TimerScope ts(tm, "a1_linear_reverse", s);
+            launch_node_gemm(a1r, m.A1_wt, w.A1_adj, w.dPhi1, s);
+        }
+        {
+            TimerScope ts(tm, "r1_reverse", s);
+            k_r1_reverse<C, LMAX, LMAXH><<<N, C, 0, s>>>(g.offsets, g.neigh, g.erec, m.R1c, w.H1, m.cg, w.dPhi1,
+                                                        w.Wsrc, w.node_forces);
+            SMX_LAUNCH_CHECK("r1_reverse");
+        }
+        {
+            TimerScope ts(tm, "source_gather", s);
+            k_source_gather<C, S::NH><<<N, C, 0, s>>>(g.soff, g.sedges, g.erec, S::REC, w.Wsrc, w.H1_adj);
+            SMX_LAUNCH_CHECK("source_gather");
+        }
+        {
+            TimerScope ts(tm, "h1_linear_reverse", s);
+            launch_node_gemm(h1r, m.H1_wt, w.H1_adj, w.M0_adj, s);
+        }
+        {
+            TimerScope ts(tm, "m0_reverse", s);
+            k_m0_reverse<C, S::NY, S::NH><<<N, C, 0, s>>>(g.node_types, w.A0, w.M0_adj, w.direct, m.m0_terms, m.m0_toff,
+                                                         m.T0, m.m0_coef, w.A0_adj);
+            SMX_LAUNCH_CHECK("m0_reverse");
+        }
+        {
+            TimerScope ts(tm, "a0_linear_reverse", s);
+            launch_node_gemm(a0r, m.A0_wt, w.A0_adj, w.Phi0_adj, s);
+        }
+        {
+            TimerScope ts(tm, "r0_reverse", s);
+            k_r0_reverse<C, LMAX><<<N, C, 0, s>>>(g.offsets, g.neigh_types, g.erec, m.R0c, m.H0, w.Phi0_adj,
+                                                  w.node_forces);
+            SMX_LAUNCH_CHECK("r0_reverse");
+        }
+    }
+};
+
+template <int LMAX, int LMAXH>
+void paths_of(std::vector<int>& le, std::vector<int>& ls, std::vector<int>& lo) {
+    using S = Shape<LMAX, LMAXH>;
+    le.clear();
+    ls.clear();
+    lo.clear();
+    for (int p = 0; p < S::P; ++p) {
+        le.push_back(S::paths[p].le);
+        ls.push_back(S::paths[p].ls);
+        lo.push_back(S::paths[p].lo);
+    }
+}
+
+}  // namespace
+
+std::unique_ptr<KernelSet> make_kernel_set(int C, int l_max, int L_max) {
+    if (C == 32 && l_max == 2 && L_max == 1) return std::make_unique<KernelSetImpl<32, 2, 1>>();
+    if (C == 128 && l_max == 3 && L_max == 1) return std::make_unique<KernelSetImpl<128, 3, 1>>();
+    return nullptr;
+}
+
+bool kernel_paths(int l_max, int L_max, std::vector<int>& le, std::vector<int>& ls, std::vector<int>& lo) {
+    if (l_max == 2 && L_max == 1) {
+        paths_of<2, 1>(le, ls, lo);
+        return true;
+    }
+    if (l_max == 3 && L_max == 1) {
+        paths_of<3, 1>(le, ls, lo);
+        return true;
+    }
+    return false;
+}
+
+void launch_node_gemm(const GemmPlan& plan, const float* W, const float* in, float* out, hipStream_t s) {
+    if (plan.num_tiles == 0) return;
+    dim3 grid(plan.num_tiles, (plan.max_n + 63) / 64);
+    k_node_gemm<<<grid, 64, 0, s>>>(plan.tiles, plan.groups, plan.node_list, W, in, out);
+    SMX_LAUNCH_CHECK("node_gemm");
+}
+
+void launch_atom_forces(int N, const int* offsets, const int* soff, const int* sedges, const double* node_forces,
+                        double* atom_forces, hipStream_t s) {
+    if (N == 0) return;
+    k_atom_forces<<<blocks_for(N, 256), 256, 0, s>>>(N, offsets, soff, sedges, node_forces, atom_forces);
+    SMX_LAUNCH_CHECK("atom_forces");
+}
+
+void launch_stress(std::int64_t E, const double* node_forces, const double* xyz, double volume, double* partial,
+                   int partial_blocks, double* stress, hipStream_t s) {
+    k_stress_partial<<<partial_blocks, kReduceThreads, 0, s>>>(E, node_forces, xyz, partial);
+    SMX_LAUNCH_CHECK("stress_partial");
+    k_stress_final<<<1, 64, 0, s>>>(partial_blocks, partial, volume, stress);
+    SMX_LAUNCH_CHECK("stress_final");
+}
+
+void launch_energy_sum(int N, const double* node_energies, double* total, hipStream_t s) {
+    k_energy_sum<<<1, 1024, 0, s>>>(N, node_energies, total);
+    SMX_LAUNCH_CHECK("energy_sum");
+}
+
+}  // namespace smx

@@ -1,0 +1,452 @@
+// Model loader for the MI355X evaluator (host C++; built with
+// -ffp-contract=off so the FP64 radial tabulation rounds like the reference's
+// host code).
+//
+// Reference statements followed:
+//   * key set and validation: libsymmetrix/source/mace.cpp:2660-2959,
+//     mace_kokkos_model.cpp:146; v4 readout basis h1_affine_schema.hpp:196-259
+//   * radial features compact_radial.cpp:227-267, network evaluation
+//     multilayer_perceptron.cpp:30-80 (SiLU*scale hidden, linear output),
+//     spline node derivatives compact_radial.cpp:326-366 (not-a-knot left,
+//     zero-slope right)
+//   * Hermite coefficients cubic_spline_set.cpp:8-30, rounded to Precision
+//     before the coefficient formulas are applied in Precision
+//   * polynomial semantics multivariate_polynomial.cpp:11-103: a repeated
+//     monomial keeps the coefficient of its first occurrence and terms are
+//     ordered by (degree, lexicographic)
+#include "model.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <limits>
+#include <map>
+#include <stdexcept>
+
+#include "json_lite.hpp"
+
+namespace smx {
+namespace {
+
+using json_lite::Value;
+
+float to_f32(double v) {
+    if (!std::isfinite(v) || std::abs(v) > static_cast<double>(std::numeric_limits<float>::max()))
+        throw std::invalid_argument("model value is outside the FP32 range");
+    return static_cast<float>(v);
+}
+
+std::vector<float> to_f32(const std::vector<double>& v) {
+    std::vector<float> o(v.size());
+    for (std::size_t i = 0; i < v.size(); ++i) o[i] = to_f32(v[i]);
+    return o;
+}
+
+struct Mlp {
+    std::vector<int> shape;
+    std::vector<std::vector<double>> w;  // [layer][out*in]
+    double scale = 1.0;
+};
+
+Mlp read_mlp(const Value& v) {
+    Mlp m;
+    m.shape = v.at("shape").as_ints();
+    const Value& w = v.at("weights");
+    for (std::size_t i = 0; i < w.size(); ++i) m.w.push_back(w.at(i).as_doubles());
+    m.scale = v.at("activation_scale").as_number();
+    if (v.at("activation").as_string() != "silu")
+        throw std::invalid_argument("compact radial networks must use SiLU activations");
+    if (m.shape.size() < 2 || m.w.size() + 1 != m.shape.size())
+        throw std::invalid_argument("compact radial network has an invalid shape");
+    for (std::size_t l = 0; l < m.w.size(); ++l)
+        if (m.w[l].size() != static_cast<std::size_t>(m.shape[l]) * m.shape[l + 1])
+            throw std::invalid_argument("compact radial network weights do not match its shape");
+    return m;
+}
+
+// multilayer_perceptron.cpp:30-80 for one input row.
+void mlp_row(const Mlp& m, const double* in, std::vector<double>& out) {
+    std::vector<double> cur(in, in + m.shape[0]), nxt;
+    for (std::size_t l = 0; l < m.w.size(); ++l) {
+        const int ni = m.shape[l], no = m.shape[l + 1];
+        nxt.assign(no, 0.0);
+        const double* W = m.w[l].data();
+        for (int o = 0; o < no; ++o) {
+            double s = 0.0;
+            for (int i = 0; i < ni; ++i) s += W[static_cast<std::size_t>(o) * ni + i] * cur[i];
+            nxt[o] = s;
+        }
+        if (l + 1 < m.w.size())
+            for (int o = 0; o < no; ++o) nxt[o] = m.scale * nxt[o] / (1.0 + std::exp(-nxt[o]));
+        cur.swap(nxt);
+    }
+    out = cur;
+}
+
+// compact_radial.cpp:326-366
+std::vector<double> node_derivatives(const std::vector<double>& v, double h) {
+    const int n = static_cast<int>(v.size());
+    const int u = n - 2;
+    std::vector<double> lo(u, 0.0), di(u, 4.0), up(u, 0.0), rhs(u, 0.0);
+    const double left = 2.0 * (-v[0] + 2.0 * v[1] - v[2]) / h;
+    up[0] = 2.0;
+    rhs[0] = 3.0 * (v[2] - v[0]) / h - left;
+    for (int node = 2; node < n - 1; ++node) {
+        const int row = node - 1;
+        lo[row] = 1.0;
+        if (node + 1 <= n - 2) up[row] = 1.0;
+        rhs[row] = 3.0 * (v[node + 1] - v[node - 1]) / h;
+    }
+    for (int row = 1; row < u; ++row) {
+        const double f = lo[row] / di[row - 1];
+        di[row] -= f * up[row - 1];
+        rhs[row] -= f * rhs[row - 1];
+    }
+    std::vector<double> x(u, 0.0);
+    x[u - 1] = rhs[u - 1] / di[u - 1];
+    for (int row = u - 2; row >= 0; --row) x[row] = (rhs[row] - up[row] * x[row + 1]) / di[row];
+    std::vector<double> d(n, 0.0);
+    for (int node = 1; node < n - 1; ++node) d[node] = x[node - 1];
+    d[0] = d[2] + left;
+    d[n - 1] = 0.0;
+    return d;
+}
+
+// Tabulate one network on the grid and build packed FP32 Hermite coefficients
+// [interval][function][4] (cubic_spline_set.cpp:8-30 in FP32).
+void tabulate(const Mlp& net, const std::vector<double>& features, int nb, int points, double h,
+              std::vector<double>& values, std::vector<double>& derivs, std::vector<float>& coef) {
+    const int nf = net.shape.back();
+    values.assign(static_cast<std::size_t>(nf) * points, 0.0);
+    derivs.assign(values.size(), 0.0);
+    std::vector<double> out;
+    for (int node = 0; node < points; ++node) {
+        mlp_row(net, features.data() + static_cast<std::size_t>(node) * nb, out);
+        for (int f = 0; f < nf; ++f) values[static_cast<std::size_t>(f) * points + node] = out[f];
+    }
+    std::vector<double> col(points);
+    for (int f = 0; f < nf; ++f) {
+        std::copy(values.begin() + static_cast<std::size_t>(f) * points,
+                  values.begin() + static_cast<std::size_t>(f + 1) * points, col.begin());
+        const auto d = node_derivatives(col, h);
+        std::copy(d.begin(), d.end(), derivs.begin() + static_cast<std::size_t>(f) * points);
+    }
+    const float hf = to_f32(h);
+    const int intervals = points - 1;
+    coef.assign(static_cast<std::size_t>(intervals) * nf * 4, 0.0f);
+    for (int i = 0; i < intervals; ++i)
+        for (int f = 0; f < nf; ++f) {
+            const float v0 = to_f32(values[static_cast<std::size_t>(f) * points + i]);
+            const float v1 = to_f32(values[static_cast<std::size_t>(f) * points + i + 1]);
+            const float d0 = to_f32(derivs[static_cast<std::size_t>(f) * points + i]);
+            const float d1 = to_f32(derivs[static_cast<std::size_t>(f) * points + i + 1]);
+            float* c = &coef[(static_cast<std::size_t>(i) * nf + f) * 4];
+            c[0] = v0;
+            c[1] = d0;
+            c[2] = (-3 * v0 - 2 * hf * d0 + 3 * v1 - hf * d1) / (hf * hf);
+            c[3] = (2 * v0 + hf * d0 - 2 * v1 + hf * d1) / (hf * hf * hf);
+        }
+}
+
+// Deduplicate monomials (first occurrence wins) and sort by (degree, lex).
+struct Poly {
+    std::vector<std::vector<int>> monos;
+    std::vector<int> source;  // index of the coefficient in the file's list
+};
+
+Poly canonical_poly(const std::vector<std::vector<int>>& monos, int nvar) {
+    auto less = [](const std::vector<int>& a, const std::vector<int>& b) {
+        if (a.size() != b.size()) return a.size() < b.size();
+        return a < b;
+    };
+    std::map<std::vector<int>, int, decltype(less)> first(less);
+    for (std::size_t i = 0; i < monos.size(); ++i) {
+        const auto& m = monos[i];
+        if (m.empty() || m.size() > 3)
+            throw std::invalid_argument("product-basis monomials must have degree 1 to 3");
+        for (int v : m)
+            if (v < 0 || v >= nvar) throw std::invalid_argument("product-basis monomial variable out of range");
+        first.insert({m, static_cast<int>(i)});
+    }
+    Poly p;
+    for (const auto& [m, i] : first) {
+        p.monos.push_back(m);
+        p.source.push_back(i);
+    }
+    return p;
+}
+
+std::vector<std::vector<int>> read_monomials(const Value& v) {
+    std::vector<std::vector<int>> out;
+    for (std::size_t i = 0; i < v.size(); ++i) {
+        const Value& m = v.at(i);
+        out.push_back(m.size() == 0 ? std::vector<int>{} : m.as_ints());
+    }
+    return out;
+}
+
+void transpose_blocks(const std::vector<float>& src, std::vector<float>& dst, std::size_t blocks, int rows,
+                      int cols) {
+    dst.assign(src.size(), 0.0f);
+    for (std::size_t b = 0; b < blocks; ++b) {
+        const float* s = src.data() + b * rows * cols;
+        float* d = dst.data() + b * rows * cols;
+        for (int r = 0; r < rows; ++r)
+            for (int c = 0; c < cols; ++c) d[static_cast<std::size_t>(c) * rows + r] = s[static_cast<std::size_t>(r) * cols + c];
+    }
+}
+
+}  // namespace
+
+void HostModel::load(const std::string& path, const std::string& head) {
+    const Value j = json_lite::parse_file(path);
+    if (j.get_int("symmetrix_format_version", 1) != 4)
+        throw std::invalid_argument("only Symmetrix MACE model format version 4 is supported");
+    if (!head.empty()) {
+        const Value* heads = j.find("heads");
+        bool found = false;
+        if (heads)
+            for (std::size_t i = 0; i < heads->size(); ++i)
+                if (heads->at(i).as_string() == head) found = true;
+        if (!found) throw std::invalid_argument("requested head '" + head + "' is not available in the model");
+    }
+    if (j.get_string("h1_affine_mode", "") != "m0_composite")
+        throw std::invalid_argument("only h1_affine_mode 'm0_composite' is supported");
+    if (j.get_string("radial_representation", "") != "compact")
+        throw std::invalid_argument("only the compact radial representation is supported");
+    if (j.get_bool("has_zbl", false) || j.get_bool("A0_scaled", false) || j.get_bool("A1_scaled", false) ||
+        j.get_bool("has_field_coupling", false) || j.get_bool("first_interaction_residual", false) ||
+        j.get_bool("single_layer_readout", false))
+        throw std::invalid_argument("the model uses features outside the supported MACE path "
+                                    "(ZBL, density scaling, field coupling or single-layer readout)");
+    num_interactions = j.get_int("num_interactions", 2);
+    if (num_interactions != 2) throw std::invalid_argument("only two-interaction MACE models are supported");
+    num_elements = j.at("num_elements").as_int();
+    C = j.at("num_channels").as_int();
+    r_cut = j.at("r_cut").as_number();
+    l_max = j.at("l_max").as_int();
+    L_max = j.at("L_max").as_int();
+    if (num_elements < 1 || C < 1 || !(r_cut > 0.0) || l_max < 0 || l_max > 3 || L_max < 0 || L_max > l_max)
+        throw std::invalid_argument("model shape is invalid (l_max must be <= 3 and L_max <= l_max)");
+    num_lm = (l_max + 1) * (l_max + 1);
+    num_LM = (L_max + 1) * (L_max + 1);
+    atomic_numbers = j.at("atomic_numbers").as_ints();
+    atomic_energies = j.at("atomic_energies").as_doubles();
+    if (static_cast<int>(atomic_numbers.size()) != num_elements ||
+        static_cast<int>(atomic_energies.size()) != num_elements)
+        throw std::invalid_argument("atomic numbers/energies do not match num_elements");
+    const std::size_t Cs = static_cast<std::size_t>(C);
+
+    // ---- compact radial
+    const Value& cr = j.at("compact_radial");
+    grid_min = cr.at("spline_grid_min").as_number();
+    spline_points = cr.at("num_spline_points").as_int();
+    if (!(grid_min > 0.0) || spline_points < 4)
+        throw std::invalid_argument("compact radial spline grid is invalid");
+    h = (r_cut - grid_min) / (spline_points - 1);
+    grid_min_f = to_f32(grid_min);
+    h_f = to_f32(h);
+    const Value& basis = cr.at("basis");
+    if (basis.at("type").as_string() != "bessel")
+        throw std::invalid_argument("only the Bessel radial basis is supported");
+    const auto bessel = basis.at("weights").as_doubles();
+    const double prefactor = basis.at("prefactor").as_number();
+    const Value& cut = cr.at("cutoff");
+    if (cut.at("type").as_string() != "polynomial")
+        throw std::invalid_argument("only the polynomial radial cutoff is supported");
+    const double r_max = cut.at("r_max").as_number();
+    const int p = cut.at("p").as_int();
+    if (std::abs(r_max - r_cut) > 1e-12) throw std::invalid_argument("compact radial cutoff does not match r_cut");
+    // Without a distance transform the features, hence every pair's tables,
+    // are independent of the pair (compact_radial.cpp:233-235): one table
+    // serves all pairs exactly.
+    if (cr.at("distance_transform").at("type").as_string() != "none")
+        throw std::invalid_argument("only distance_transform 'none' is supported");
+    const Value& nets = cr.at("networks");
+    if (nets.contains("A0") || nets.contains("A1"))
+        throw std::invalid_argument("density-scaled radial networks are not supported");
+    const Mlp R0net = read_mlp(nets.at("R0"));
+    const Mlp R1net = read_mlp(nets.at("R1"));
+    const int nb = static_cast<int>(bessel.size());
+    if (R0net.shape[0] != nb || R1net.shape[0] != nb)
+        throw std::invalid_argument("radial networks do not take the Bessel features");
+    std::vector<double> feat(static_cast<std::size_t>(spline_points) * nb);
+    for (int node = 0; node < spline_points; ++node) {
+        const double r = grid_min + node * h;
+        double cv = 0.0;
+        if (r < r_max) {
+            const double s = r / r_max;
+            cv = 1.0 - ((p + 1.0) * (p + 2.0) / 2.0) * std::pow(s, p) + p * (p + 2.0) * std::pow(s, p + 1) -
+                 (p * (p + 1.0) / 2.0) * std::pow(s, p + 2);
+        }
+        for (int b = 0; b < nb; ++b) feat[static_cast<std::size_t>(node) * nb + b] = prefactor * std::sin(bessel[b] * r) / r * cv;
+    }
+    R0_functions = R0net.shape.back();
+    R1_functions = R1net.shape.back();
+    if (R0_functions != (l_max + 1) * C) throw std::invalid_argument("R0 network width must be (l_max+1)*C");
+    tabulate(R0net, feat, nb, spline_points, h, R0_values, R0_derivs, R0_coef);
+    tabulate(R1net, feat, nb, spline_points, h, R1_values, R1_derivs, R1_coef);
+
+    // ---- H0, A0
+    H0 = to_f32(j.at("H0_weights").as_doubles());
+    if (H0.size() != num_elements * Cs) throw std::invalid_argument("H0 weights have the wrong size");
+    const Value& a0 = j.at("A0_weights");
+    A0_w.assign(num_elements * (l_max + 1) * Cs * Cs, 0.0f);
+    for (int t = 0; t < num_elements; ++t)
+        for (int l = 0; l <= l_max; ++l) {
+            const auto w = a0.at(t).at(l).as_doubles();
+            if (w.size() != Cs * Cs) throw std::invalid_argument("A0 weights have the wrong size");
+            for (std::size_t i = 0; i < w.size(); ++i)
+                A0_w[(static_cast<std::size_t>(t) * (l_max + 1) + l) * Cs * Cs + i] = to_f32(w[i]);
+        }
+    transpose_blocks(A0_w, A0_wt, static_cast<std::size_t>(num_elements) * (l_max + 1), C, C);
+
+    // ---- M0
+    const Value& m0m = j.at("M0_monomials");
+    const Value& m0w = j.at("M0_weights");
+    m0_term_offset.assign(num_LM + 1, 0);
+    std::vector<Poly> polys;
+    for (int LM = 0; LM < num_LM; ++LM) {
+        const auto monos = read_monomials(m0m.at(std::to_string(LM)));
+        polys.push_back(canonical_poly(monos, num_lm));
+        for (const auto& m : polys.back().monos) m0_terms.push_back(pack_monomial(m));
+        m0_term_offset[LM + 1] = static_cast<int>(m0_terms.size());
+    }
+    const std::size_t T0 = m0_terms.size();
+    m0_coef.assign(num_elements * T0 * Cs, 0.0f);
+    for (int t = 0; t < num_elements; ++t) {
+        const Value& wt = m0w.at(std::to_string(t));
+        for (int LM = 0; LM < num_LM; ++LM) {
+            const Value& wl = wt.at(std::to_string(LM));
+            const Poly& P = polys[LM];
+            for (int k = 0; k < C; ++k) {
+                const auto cf = wl.at(std::to_string(k)).as_doubles();
+                if (cf.size() != m0m.at(std::to_string(LM)).size())
+                    throw std::invalid_argument("M0 coefficient count does not match its monomials");
+                for (std::size_t s = 0; s < P.monos.size(); ++s)
+                    m0_coef[(static_cast<std::size_t>(t) * T0 + m0_term_offset[LM] + s) * Cs + k] = to_f32(cf[P.source[s]]);
+            }
+        }
+    }
+
+    // ---- H1
+    H1_w = to_f32(j.at("H1_weights").as_doubles());
+    if (H1_w.size() != static_cast<std::size_t>(L_max + 1) * Cs * Cs)
+        throw std::invalid_argument("H1 weights have the wrong size");
+    transpose_blocks(H1_w, H1_wt, L_max + 1, C, C);
+
+    // ---- R1 coupling (extract_mace_data.py:1326-1400 semantics)
+    path_lo = j.at("Phi1_l").as_ints();
+    path_le = j.at("Phi1_l1").as_ints();
+    path_ls = j.at("Phi1_l2").as_ints();
+    num_paths = static_cast<int>(path_lo.size());
+    if (num_paths == 0 || path_le.size() != path_lo.size() || path_ls.size() != path_lo.size())
+        throw std::invalid_argument("R1 path lists are inconsistent");
+    if (R1_functions != num_paths * C) throw std::invalid_argument("R1 network width must be num_paths*C");
+    num_e.assign(l_max + 1, 0);
+    for (int p2 = 0; p2 < num_paths; ++p2) {
+        if (path_lo[p2] < 0 || path_lo[p2] > l_max || path_le[p2] < 0 || path_le[p2] > l_max || path_ls[p2] < 0 ||
+            path_ls[p2] > L_max)
+            throw std::invalid_argument("R1 path irreps are out of range");
+        num_e[path_lo[p2]] += 1;
+    }
+    lme_base.assign(l_max + 2, 0);
+    for (int l = 0; l <= l_max; ++l) lme_base[l + 1] = lme_base[l] + (2 * l + 1) * num_e[l];
+    num_lme = lme_base[l_max + 1];
+    row_base.assign(num_paths + 1, 0);
+    cg_offset.assign(num_paths + 1, 0);
+    for (int q = 0; q < num_paths; ++q) {
+        row_base[q + 1] = row_base[q] + (2 * path_le[q] + 1) * (2 * path_ls[q] + 1);
+        cg_offset[q + 1] = cg_offset[q] + (2 * path_le[q] + 1) * (2 * path_ls[q] + 1) * (2 * path_lo[q] + 1);
+    }
+    num_rows = row_base[num_paths];
+    cg_dense.assign(cg_offset[num_paths], 0.0f);
+    {
+        const auto lme = j.at("Phi1_lme").as_ints();
+        const auto row = j.at("Phi1_lelm1lm2").as_ints();
+        const auto cg = j.at("Phi1_clebsch_gordan").as_doubles();
+        if (lme.size() != row.size() || cg.size() != row.size())
+            throw std::invalid_argument("R1 coupling term lists are inconsistent");
+        // position of path q's e index among paths with the same output l
+        std::vector<int> e_of(num_paths, 0);
+        std::vector<int> seen(l_max + 1, 0);
+        for (int q = 0; q < num_paths; ++q) e_of[q] = seen[path_lo[q]]++;
+        for (std::size_t t = 0; t < row.size(); ++t) {
+            if (row[t] < 0 || row[t] >= num_rows) throw std::invalid_argument("R1 coupling row out of range");
+            int q = 0;
+            while (row_base[q + 1] <= row[t]) ++q;
+            const int local = row[t] - row_base[q];
+            const int ls = path_ls[q], lo = path_lo[q];
+            const int m1 = local / (2 * ls + 1), m2 = local % (2 * ls + 1);
+            // lme = lme_base[lo] + mo*num_e[lo] + e
+            const int rel = lme[t] - lme_base[lo];
+            if (rel < 0 || rel >= (2 * lo + 1) * num_e[lo] || rel % num_e[lo] != e_of[q])
+                throw std::invalid_argument("R1 coupling output index does not match its path");
+            const int mo = rel / num_e[lo];
+            float& dst = cg_dense[cg_offset[q] + ((m1 * (2 * ls + 1) + m2) * (2 * lo + 1) + mo)];
+            // repeated (row, lme) terms accumulate like the reference's term loop
+            dst = to_f32(static_cast<double>(dst) + cg[t]);
+        }
+    }
+
+    // ---- A1
+    const Value& a1 = j.at("A1_weights");
+    A1_offset.assign(l_max + 2, 0);
+    for (int l = 0; l <= l_max; ++l) A1_offset[l + 1] = A1_offset[l] + static_cast<std::int64_t>(num_e[l]) * Cs * Cs;
+    A1_w.assign(A1_offset[l_max + 1], 0.0f);
+    A1_wt.assign(A1_offset[l_max + 1], 0.0f);
+    for (int l = 0; l <= l_max; ++l) {
+        const auto w = a1.at(l).as_doubles();
+        if (w.size() != static_cast<std::size_t>(num_e[l]) * Cs * Cs)
+            throw std::invalid_argument("A1 weights have the wrong size");
+        const int K = num_e[l] * C;
+        for (int r = 0; r < K; ++r)
+            for (int c = 0; c < C; ++c) {
+                const float v = to_f32(w[static_cast<std::size_t>(r) * Cs + c]);
+                A1_w[A1_offset[l] + static_cast<std::size_t>(r) * Cs + c] = v;
+                A1_wt[A1_offset[l] + static_cast<std::size_t>(c) * K + r] = v;
+            }
+    }
+
+    // ---- M1
+    {
+        const auto monos = read_monomials(j.at("M1_monomials"));
+        const Poly P = canonical_poly(monos, num_lm);
+        for (const auto& m : P.monos) m1_terms.push_back(pack_monomial(m));
+        const std::size_t T1 = m1_terms.size();
+        m1_coef.assign(num_elements * T1 * Cs, 0.0f);
+        const Value& m1w = j.at("M1_weights");
+        for (int t = 0; t < num_elements; ++t)
+            for (int k = 0; k < C; ++k) {
+                const auto cf = m1w.at(std::to_string(t)).at(std::to_string(k)).as_doubles();
+                if (cf.size() != monos.size()) throw std::invalid_argument("M1 coefficient count does not match");
+                for (std::size_t s = 0; s < T1; ++s)
+                    m1_coef[(static_cast<std::size_t>(t) * T1 + s) * Cs + k] = to_f32(cf[P.source[s]]);
+            }
+    }
+
+    // ---- H2 and readouts (mace.cpp:2516-2657, v4 m0_composite basis)
+    {
+        const Value& t2 = j.at("H2_weights_for_M0");
+        H2_T.assign(num_elements * Cs * Cs, 0.0f);
+        for (int t = 0; t < num_elements; ++t) {
+            const auto w = t2.at(t).as_doubles();
+            if (w.size() != Cs * Cs) throw std::invalid_argument("H2 weights have the wrong size");
+            for (std::size_t i = 0; i < w.size(); ++i) H2_T[t * Cs * Cs + i] = to_f32(w[i]);
+        }
+        transpose_blocks(H2_T, H2_Tt, num_elements, C, C);
+        H2_M1 = to_f32(j.at("H2_weights_for_M1").as_doubles());
+        if (H2_M1.size() != Cs * Cs) throw std::invalid_argument("H2 M1 weights have the wrong size");
+        transpose_blocks(H2_M1, H2_M1t, 1, C, C);
+        readout_q = j.at("readout_1_weights_for_M0").as_doubles();
+        readout_hidden = j.get_int("readout_2_hidden_size", 16);
+        readout_W1 = j.at("readout_2_weights_1").as_doubles();
+        readout_W2 = j.at("readout_2_weights_2").as_doubles();
+        readout_scale = j.at("readout_2_scale_factor").as_number();
+        if (readout_q.size() != Cs || readout_hidden < 1 ||
+            readout_W1.size() != static_cast<std::size_t>(readout_hidden) * Cs ||
+            readout_W2.size() != static_cast<std::size_t>(readout_hidden))
+            throw std::invalid_argument("readout weights do not match the model shape");
+    }
+}
+
+}  // namespace smx

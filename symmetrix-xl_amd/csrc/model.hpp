@@ -1,0 +1,88 @@
+// Host-side MACE model (Symmetrix JSON format version 4) laid out for the
+// MI355X kernels.
+//
+// The loader reads the keys of libsymmetrix/source/mace.cpp:2660-2959 and
+// mace_kokkos_model.cpp:146 for the compact-radial, "m0_composite" MACE path,
+// tabulates the radial networks on the spline grid exactly as
+// compact_radial.cpp:227-366 does (FP64, no contraction), and rounds the
+// Hermite coefficients to FP32 with cubic_spline_set.cpp:8-30's formulas.
+// Every table is stored in the layout its kernel reads coalesced: channel
+// index innermost, Hermite coefficients packed four to a lane.
+#pragma once
+
+#include <cstdint>
+#include <string>
+#include <vector>
+
+namespace smx {
+
+// One packed monomial: variables v0,v1,v2 (byte each) and degree (top byte).
+inline std::int32_t pack_monomial(const std::vector<int>& vars) {
+    std::int32_t p = static_cast<std::int32_t>(vars.size()) << 24;
+    for (std::size_t i = 0; i < vars.size(); ++i) p |= (vars[i] & 0xff) << (8 * i);
+    return p;
+}
+
+struct HostModel {
+    // shape
+    int num_elements = 0;
+    int C = 0;
+    int l_max = 0, L_max = 0;
+    int num_lm = 0, num_LM = 0;
+    int num_interactions = 2;
+    double r_cut = 0.0;
+    std::vector<int> atomic_numbers;
+    std::vector<double> atomic_energies;
+
+    // radial spline grid shared by R0 and R1 (compact_radial.cpp:110-214)
+    int spline_points = 0;
+    double grid_min = 0.0, h = 0.0;
+    float grid_min_f = 0.0f, h_f = 0.0f;
+    int R0_functions = 0, R1_functions = 0;
+    // [interval][function][4] with function = l*C+k (R0) or p*C+k (R1)
+    std::vector<float> R0_coef, R1_coef;
+    // nodal FP64 tables [function][node] (kept for diagnostics/tests)
+    std::vector<double> R0_values, R0_derivs, R1_values, R1_derivs;
+
+    // layer 1
+    std::vector<float> H0;                  // [type][C]
+    std::vector<float> A0_w, A0_wt;         // [type][l][C_in][C_out] and transposed
+
+    // M0 product basis: packed monomials concatenated over LM
+    std::vector<std::int32_t> m0_terms;
+    std::vector<std::int32_t> m0_term_offset;  // [num_LM + 1]
+    std::vector<float> m0_coef;                // [type][term][C]
+
+    std::vector<float> H1_w, H1_wt;         // [l][C][C], l <= L_max
+
+    // R1 coupling
+    std::vector<int> path_lo, path_le, path_ls;  // Phi1_l, Phi1_l1, Phi1_l2
+    int num_paths = 0, num_rows = 0, num_lme = 0;
+    std::vector<int> num_e, lme_base;      // per output l
+    std::vector<int> row_base;             // per path
+    // Dense per-path coupling blocks cg[p][m1][m2][mo], concatenated over p.
+    std::vector<float> cg_dense;
+    std::vector<int> cg_offset;            // [num_paths + 1]
+
+    // A1: per l, W[(e,k_in)][k_out] and its transpose, concatenated over l
+    std::vector<float> A1_w, A1_wt;
+    std::vector<std::int64_t> A1_offset;   // [l_max + 2]
+
+    // M1 invariant product basis
+    std::vector<std::int32_t> m1_terms;
+    std::vector<float> m1_coef;            // [type][term][C]
+
+    // H2 skip / M1 linear (values FP32-representable, arithmetic FP64)
+    std::vector<float> H2_T, H2_Tt;        // [type][in][out] and [type][out][in]
+    std::vector<float> H2_M1, H2_M1t;      // [in][out] and [out][in]
+    // readouts (FP64)
+    std::vector<double> readout_q;         // [C]
+    int readout_hidden = 0;
+    std::vector<double> readout_W1;        // [hidden][C]
+    std::vector<double> readout_W2;        // [hidden]
+    double readout_scale = 1.0;
+
+    void load(const std::string& path, const std::string& head);
+};
+
+}  // namespace smx

@@ -1,0 +1,138 @@
+"""ctypes binding of libsymmetrix_mi355x.so (the C ABI declared in
+include/symmetrix_mi355x.h).
+
+The library is built in-tree (``make -C symmetrix-xl_amd/csrc``); there is no
+fallback: importing this module raises ImportError when the library is
+missing, and every entry point's error code becomes a Python exception.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libsymmetrix_mi355x.so")
+
+SMX_OK = 0
+SMX_ERR_INVALID_ARGUMENT = -1
+SMX_ERR_RUNTIME = -2
+SMX_ERR_LOGIC = -3
+SMX_ERR_OUT_OF_MEMORY = -4
+SMX_ERR_UNSUPPORTED = -5
+
+
+class SymmetrixUnsupportedError(ValueError):
+    """The model's shape or features have no compiled MI355X kernel set."""
+
+
+class SmxModelInfo(ctypes.Structure):
+    _fields_ = [("struct_size", ctypes.c_uint32), ("num_elements", ctypes.c_int32),
+                ("num_channels", ctypes.c_int32), ("l_max", ctypes.c_int32),
+                ("L_max", ctypes.c_int32), ("num_interactions", ctypes.c_int32),
+                ("num_paths", ctypes.c_int32), ("num_lme", ctypes.c_int32),
+                ("r_cut", ctypes.c_double)]
+
+
+class SmxDeviceOutputs(ctypes.Structure):
+    _fields_ = [("struct_size", ctypes.c_uint32), ("num_nodes", ctypes.c_int32),
+                ("num_edges", ctypes.c_int64), ("node_energies", ctypes.c_void_p),
+                ("node_forces", ctypes.c_void_p), ("atom_forces", ctypes.c_void_p),
+                ("stress", ctypes.c_void_p), ("total_energy", ctypes.c_void_p),
+                ("xyz", ctypes.c_void_p), ("r", ctypes.c_void_p)]
+
+
+# (name, restype, argtypes) of every exported entry point
+_i32 = ctypes.c_int32
+_i64 = ctypes.c_int64
+_u64 = ctypes.c_uint64
+_dbl = ctypes.c_double
+_vp = ctypes.c_void_p
+_cp = ctypes.c_char_p
+_p_i32 = ctypes.POINTER(ctypes.c_int32)
+_p_i64 = ctypes.POINTER(ctypes.c_int64)
+_p_u64 = ctypes.POINTER(ctypes.c_uint64)
+_p_dbl = ctypes.POINTER(ctypes.c_double)
+
+SIGNATURES = [
+    ("smx_abi_version", _i32, []),
+    ("smx_last_error", _cp, []),
+    ("smx_evaluator_create", _i32, [_cp, _cp, ctypes.POINTER(_vp)]),
+    ("smx_evaluator_destroy", None, [_vp]),
+    ("smx_evaluator_info", _i32, [_vp, ctypes.POINTER(SmxModelInfo)]),
+    ("smx_evaluator_atomic_numbers", _i32, [_vp, _vp, _i32]),
+    ("smx_set_streamed_edges", _i32, [_vp, _cp]),
+    ("smx_evaluator_stream", _vp, [_vp]),
+    ("smx_prepare_factorized_graph", _i32, [_vp, _i32, _vp, _vp, _i64, _vp, _vp, _p_u64]),
+    ("smx_prepare_factorized_graph_device", _i32, [_vp, _i32, _vp, _vp, _i64, _vp, _vp, _p_u64]),
+    ("smx_prepare_periodic_factorized_graph", _i32,
+     [_vp, _i32, _vp, _vp, _vp, _vp, _dbl, _p_u64, _p_i64]),
+    ("smx_update_factorized_cell", _i32, [_vp, _u64, _vp, _vp]),
+    ("smx_compute_prepared_factorized", _i32, [_vp, _u64, _vp, _vp]),
+    ("smx_compute_prepared_factorized_positions", _i32, [_vp, _u64, _vp]),
+    ("smx_compute_prepared_factorized_positions_device", _i32, [_vp, _u64, _vp]),
+    ("smx_compute_node_energies_forces", _i32, [_vp, _i32, _vp, _vp, _i64, _vp, _vp, _vp, _vp]),
+    ("smx_reduce_prepared_node_forces", _i32, [_vp, _u64, _vp]),
+    ("smx_reduce_prepared_stress", _i32, [_vp, _u64, _dbl, _vp]),
+    ("smx_node_energies", _i32, [_vp, _vp, _i64]),
+    ("smx_node_forces", _i32, [_vp, _vp, _i64]),
+    ("smx_total_energy_device", _i32, [_vp, _vp]),
+    ("smx_device_outputs", _i32, [_vp, ctypes.POINTER(SmxDeviceOutputs)]),
+    ("smx_synchronize", _i32, [_vp]),
+    ("smx_debug_stage", _i32, [_vp, _cp, _vp, _i64, _p_i64]),
+    ("smx_set_kernel_timing", _i32, [_vp, _i32]),
+    ("smx_kernel_timing_reset", _i32, [_vp]),
+    ("smx_kernel_timing", _i32, [_vp, _i32, ctypes.POINTER(_cp), _p_dbl, _p_i64]),
+    ("smx_neighbor_list", _i32, [_i32, _vp, _vp, _vp, _dbl, _p_i64, _vp, _vp, _vp, _vp, _vp]),
+]
+
+
+def _load():
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            "libsymmetrix_mi355x.so is not built (expected at %s); run "
+            "`make -C symmetrix-xl_amd/csrc` or __graft_entry__.build()" % LIB_PATH)
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, res, args in SIGNATURES:
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if lib.smx_abi_version() != 1:
+        raise ImportError("libsymmetrix_mi355x.so has an unexpected ABI version")
+    return lib
+
+
+lib = _load()
+
+
+def check(rc):
+    """Raise the Python exception of an SMX_ERR_* code."""
+    if rc == SMX_OK:
+        return
+    msg = lib.smx_last_error().decode(errors="replace")
+    if rc == SMX_ERR_INVALID_ARGUMENT:
+        raise ValueError(msg)
+    if rc == SMX_ERR_UNSUPPORTED:
+        raise SymmetrixUnsupportedError(msg)
+    if rc == SMX_ERR_OUT_OF_MEMORY:
+        raise MemoryError(msg)
+    raise RuntimeError(msg)
+
+
+def ptr(a):
+    """Address of a C-contiguous numpy array (None for an empty array)."""
+    if a is None:
+        return None
+    if not a.flags["C_CONTIGUOUS"]:
+        raise ValueError("array must be C-contiguous")
+    return a.ctypes.data if a.size else None
+
+
+def i32(a):
+    return np.ascontiguousarray(a, dtype=np.int32).reshape(-1)
+
+
+def f64(a):
+    return np.ascontiguousarray(a, dtype=np.float64).reshape(-1)

@@ -1,0 +1,254 @@
+"""``MACEKokkosFloat``: the reference's FP32 evaluator class, backed by the
+MI355X library.
+
+Method names, argument meanings and error behaviour follow the reference's
+pybind class (symmetrix/source/cpp/mace_kokkos.cpp): ``_prepare_factorized_graph``
+(:1561), ``_prepare_periodic_factorized_graph`` (:1580, returns
+``{"generation", "num_edges"}``), ``_update_factorized_cell``,
+``_compute_prepared_factorized`` (:1817), ``_compute_prepared_factorized_positions``
+(:1828), ``compute_node_energies_forces`` (:2169), ``_reduce_atom_forces``
+(:2103), ``_reduce_stress`` (:2134) and the ``node_energies``/``node_forces``/
+``r_cut``/``atomic_numbers`` attributes.  Bad inputs and stale generations
+raise ValueError, device failures RuntimeError.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from . import _native
+from ._native import check, f64, i32, lib, ptr
+
+
+class MACEKokkosFloat:
+    """FP32 MACE evaluator on one MI355X (``streamed_edges="direct"``)."""
+
+    precision = "float32"
+
+    def __init__(self, filename, head=""):
+        h = ctypes.c_void_p()
+        check(lib.smx_evaluator_create(str(filename).encode(), (head or "").encode(), ctypes.byref(h)))
+        self._h = h
+        info = _native.SmxModelInfo()
+        info.struct_size = ctypes.sizeof(info)
+        check(lib.smx_evaluator_info(self._h, ctypes.byref(info)))
+        self.num_elements = info.num_elements
+        self.num_channels = info.num_channels
+        self.l_max = info.l_max
+        self.L_max = info.L_max
+        self.num_interactions = info.num_interactions
+        self.r_cut = info.r_cut
+        z = np.zeros(self.num_elements, dtype=np.int32)
+        check(lib.smx_evaluator_atomic_numbers(self._h, ptr(z), len(z)))
+        self._atomic_numbers = z
+        self.selected_head = head or ""
+        self._num_nodes = 0
+        self._num_edges = 0
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib.smx_evaluator_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+    # ------------------------------------------------------------ attributes
+    @property
+    def atomic_numbers(self):
+        return [int(v) for v in self._atomic_numbers]
+
+    @property
+    def streamed_edges_mode(self):
+        return "direct"
+
+    def set_streamed_edges(self, mode):
+        check(lib.smx_set_streamed_edges(self._h, str(mode).encode()))
+
+    @property
+    def stream(self):
+        return lib.smx_evaluator_stream(self._h)
+
+    @property
+    def node_energies(self):
+        out = np.zeros(self._num_nodes)
+        check(lib.smx_node_energies(self._h, ptr(out), out.size))
+        return out
+
+    @property
+    def node_forces(self):
+        out = np.zeros(3 * self._num_edges)
+        check(lib.smx_node_forces(self._h, ptr(out), out.size))
+        return out
+
+    # ----------------------------------------------------------------- graph
+    def _prepare_factorized_graph(self, num_nodes, node_types, num_neigh, neigh_indices, neigh_types):
+        node_types, num_neigh = i32(node_types), i32(num_neigh)
+        neigh_indices, neigh_types = i32(neigh_indices), i32(neigh_types)
+        if len(node_types) != num_nodes or len(num_neigh) != num_nodes:
+            raise ValueError("node arrays do not match num_nodes")
+        if len(neigh_types) != len(neigh_indices):
+            raise ValueError("neighbour arrays have different lengths")
+        gen = ctypes.c_uint64()
+        check(lib.smx_prepare_factorized_graph(self._h, int(num_nodes), ptr(node_types), ptr(num_neigh),
+                                               len(neigh_indices), ptr(neigh_indices), ptr(neigh_types),
+                                               ctypes.byref(gen)))
+        self._num_nodes = int(num_nodes)
+        self._num_edges = len(neigh_indices)
+        return int(gen.value)
+
+    def _prepare_periodic_factorized_graph(self, node_types, positions, cell, inverse_cell, neighbor_cutoff):
+        node_types = i32(node_types)
+        positions = f64(positions)
+        if positions.size != 3 * node_types.size:
+            raise ValueError("positions must hold three coordinates per node")
+        cell, inverse_cell = f64(cell), f64(inverse_cell)
+        if cell.size != 9 or inverse_cell.size != 9:
+            raise ValueError("cell and inverse_cell must have nine entries")
+        gen = ctypes.c_uint64()
+        ne = ctypes.c_int64()
+        check(lib.smx_prepare_periodic_factorized_graph(self._h, node_types.size, ptr(node_types), ptr(positions),
+                                                        ptr(cell), ptr(inverse_cell), float(neighbor_cutoff),
+                                                        ctypes.byref(gen), ctypes.byref(ne)))
+        self._num_nodes = node_types.size
+        self._num_edges = int(ne.value)
+        return {"generation": int(gen.value), "num_edges": int(ne.value)}
+
+    def _update_factorized_cell(self, execution_graph_generation, cell, inverse_cell):
+        cell, inverse_cell = f64(cell), f64(inverse_cell)
+        check(lib.smx_update_factorized_cell(self._h, int(execution_graph_generation), ptr(cell),
+                                             ptr(inverse_cell)))
+
+    # ------------------------------------------------------------- evaluate
+    def _compute_prepared_factorized(self, execution_graph_generation, xyz, r):
+        xyz, r = f64(xyz), f64(r)
+        if xyz.size != 3 * self._num_edges or r.size != self._num_edges:
+            raise ValueError("xyz and r do not match the prepared graph")
+        check(lib.smx_compute_prepared_factorized(self._h, int(execution_graph_generation), ptr(xyz), ptr(r)))
+
+    def _compute_prepared_factorized_positions(self, execution_graph_generation, positions):
+        positions = f64(positions)
+        if positions.size != 3 * self._num_nodes:
+            raise ValueError("positions do not match the prepared graph")
+        check(lib.smx_compute_prepared_factorized_positions(self._h, int(execution_graph_generation),
+                                                            ptr(positions)))
+
+    def _compute_prepared_factorized_positions_device(self, execution_graph_generation, positions_device_ptr):
+        check(lib.smx_compute_prepared_factorized_positions_device(self._h, int(execution_graph_generation),
+                                                                   ctypes.c_void_p(positions_device_ptr)))
+
+    def compute_node_energies_forces(self, num_nodes, node_types, num_neigh, neigh_indices, neigh_types, xyz, r,
+                                     execution_graph_generation=0):
+        if execution_graph_generation:
+            self._compute_prepared_factorized(execution_graph_generation, xyz, r)
+            return
+        node_types, num_neigh = i32(node_types), i32(num_neigh)
+        neigh_indices, neigh_types = i32(neigh_indices), i32(neigh_types)
+        xyz, r = f64(xyz), f64(r)
+        if xyz.size != 3 * neigh_indices.size or r.size != neigh_indices.size:
+            raise ValueError("xyz and r do not match the neighbour list")
+        check(lib.smx_compute_node_energies_forces(self._h, int(num_nodes), ptr(node_types), ptr(num_neigh),
+                                                   neigh_indices.size, ptr(neigh_indices), ptr(neigh_types),
+                                                   ptr(xyz), ptr(r)))
+        self._num_nodes = int(num_nodes)
+        self._num_edges = neigh_indices.size
+
+    # ------------------------------------------------------------ reductions
+    def _reduce_atom_forces(self, num_nodes, edge_receivers, edge_sources, execution_graph_generation=0):
+        if execution_graph_generation == 0:
+            # unprepared path: reduce the directed forces on the host
+            # (the calculator's bincount fallback, calculator.py:3860-3874)
+            rcv, src = i32(edge_receivers), i32(edge_sources)
+            if rcv.size != src.size:
+                raise ValueError("Atom-force reduction edge extents are inconsistent.")
+            f = self.node_forces.reshape(-1, 3)[: rcv.size]
+            out = np.zeros((num_nodes, 3))
+            for c in range(3):
+                out[:, c] = (np.bincount(src, weights=f[:, c], minlength=num_nodes)
+                             - np.bincount(rcv, weights=f[:, c], minlength=num_nodes))
+            return out
+        out = np.zeros((self._num_nodes, 3))
+        check(lib.smx_reduce_prepared_node_forces(self._h, int(execution_graph_generation), ptr(out)))
+        return out
+
+    def _reduce_stress(self, volume, xyz, execution_graph_generation=0):
+        if execution_graph_generation == 0:
+            f = self.node_forces.reshape(-1, 3)
+            x = f64(xyz).reshape(-1, 3)
+            return (-f[: len(x)].T @ x) / volume
+        out = np.zeros((3, 3))
+        check(lib.smx_reduce_prepared_stress(self._h, int(execution_graph_generation), float(volume), ptr(out)))
+        return out
+
+    def _total_energy(self):
+        out = ctypes.c_double()
+        check(lib.smx_total_energy_device(self._h, ctypes.byref(out)))
+        return float(out.value)
+
+    def _device_outputs(self):
+        o = _native.SmxDeviceOutputs()
+        o.struct_size = ctypes.sizeof(o)
+        check(lib.smx_device_outputs(self._h, ctypes.byref(o)))
+        return o
+
+    def synchronize(self):
+        check(lib.smx_synchronize(self._h))
+
+    # ----------------------------------------------------------- diagnostics
+    def _stage(self, name):
+        n = ctypes.c_int64()
+        check(lib.smx_debug_stage(self._h, name.encode(), None, 0, ctypes.byref(n)))
+        out = np.zeros(n.value, dtype=np.float32)
+        check(lib.smx_debug_stage(self._h, name.encode(), ptr(out), out.size, ctypes.byref(n)))
+        return out
+
+    def set_kernel_timing(self, enabled=True):
+        check(lib.smx_set_kernel_timing(self._h, 1 if enabled else 0))
+
+    def reset_kernel_timing(self):
+        check(lib.smx_kernel_timing_reset(self._h))
+
+    def kernel_timing(self):
+        """{kernel name: (total ms, launches)} of the timed launches."""
+        out = {}
+        i = 0
+        while True:
+            name = ctypes.c_char_p()
+            ms = ctypes.c_double()
+            n = ctypes.c_int64()
+            check(lib.smx_kernel_timing(self._h, i, ctypes.byref(name), ctypes.byref(ms), ctypes.byref(n)))
+            if not name.value:
+                break
+            out[name.value.decode()] = (ms.value, int(n.value))
+            i += 1
+        return out
+
+
+def neighbor_list(positions, cell, cutoff, inverse_cell=None):
+    """Device periodic neighbour list (bit-exact with the reference's
+    builder): dict of num_neigh, offsets, sources, shifts [E,3],
+    fractional_xyz [E,3], receivers."""
+    positions = f64(positions)
+    n = positions.size // 3
+    cell = f64(cell)
+    inv = f64(np.linalg.inv(cell.reshape(3, 3)) if inverse_cell is None else inverse_cell)
+    ne = ctypes.c_int64(0)
+    check(lib.smx_neighbor_list(n, ptr(positions), ptr(cell), ptr(inv), float(cutoff), ctypes.byref(ne),
+                                None, None, None, None, None))
+    E = int(ne.value)
+    out = {"num_neigh": np.zeros(n, np.int32), "offsets": np.zeros(n + 1, np.int32),
+           "sources": np.zeros(max(E, 1), np.int32), "shifts": np.zeros(3 * max(E, 1), np.int32),
+           "fractional_xyz": np.zeros(3 * max(E, 1))}
+    ne2 = ctypes.c_int64(max(E, 1))
+    check(lib.smx_neighbor_list(n, ptr(positions), ptr(cell), ptr(inv), float(cutoff), ctypes.byref(ne2),
+                                ptr(out["num_neigh"]), ptr(out["offsets"]), ptr(out["sources"]),
+                                ptr(out["shifts"]), ptr(out["fractional_xyz"])))
+    if int(ne2.value) != E:
+        raise RuntimeError("neighbour list changed size between its two passes")
+    out["sources"] = out["sources"][:E]
+    out["shifts"] = out["shifts"][: 3 * E].reshape(E, 3)
+    out["fractional_xyz"] = out["fractional_xyz"][: 3 * E].reshape(E, 3)
+    out["receivers"] = np.repeat(np.arange(n, dtype=np.int32), out["num_neigh"])
+    return out

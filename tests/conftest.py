@@ -1,0 +1,35 @@
+"""Test configuration: the ``gpu`` marker, import paths and shared models.
+
+``-m "not gpu"`` runs the CPU suite (oracle against golden vectors and closed
+forms, host logic, the C ABI's exports); ``-m gpu`` runs the parity tests of
+the HIP path against the CPU oracle on one MI355X.
+"""
+
+import os
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+for p in (ROOT, os.path.join(ROOT, "symmetrix-xl_amd")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (HIP device) to run")
+
+
+MODEL_DIR = os.environ.get("SYMMETRIX_MODEL_CACHE", "/tmp/symmetrix_models")
+
+
+@pytest.fixture(scope="session")
+def tiny_model_path():
+    from symmetrix import random_model
+    return random_model.cached_model("tiny", directory=MODEL_DIR)
+
+
+@pytest.fixture(scope="session")
+def medium_model_path():
+    from symmetrix import random_model
+    return random_model.cached_model("medium", directory=MODEL_DIR)

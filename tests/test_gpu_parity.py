@@ -1,0 +1,139 @@
+"""Parity of the HIP path (through the C ABI) with the CPU oracle.
+
+Bars (north star): neighbour lists bit-exact; FP32 energy within 1e-5
+eV/atom, forces within 1e-4 eV/Angstrom, stress within 1e-6 eV/Angstrom^3 of
+the oracle's FP32 restatement of the reference CPU path on the same inputs.
+"""
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+E_TOL = 1e-5   # eV/atom
+F_TOL = 1e-4   # eV/A
+S_TOL = 1e-6   # eV/A^3
+
+
+def _oracle():
+    from oracle import oracle
+    return oracle
+
+
+def _system(name):
+    from symmetrix import systems
+    if name == "tiny":
+        return systems.srtio3_supercell(3, sigma=0.05, seed=0)
+    if name == "medium":
+        return systems.srtio3_supercell(10, sigma=0.05, seed=0)
+    raise KeyError(name)
+
+
+def _check_graph(pos, cell, cutoff):
+    from symmetrix.mace_kokkos import neighbor_list
+    ora = _oracle().neighbor_graph(pos, cell, cutoff)
+    dev = neighbor_list(pos, cell, cutoff)
+    for key in ("num_neigh", "offsets", "sources", "shifts"):
+        np.testing.assert_array_equal(dev[key], ora[key], err_msg=key)
+    # fractional edge vectors bit for bit
+    assert dev["fractional_xyz"].tobytes() == ora["fractional_xyz"].tobytes()
+    return dev
+
+
+@pytest.mark.parametrize("name,cutoff", [("tiny", 5.5), ("tiny", 5.0), ("medium", 6.5)])
+def test_neighbor_list_bit_exact(name, cutoff):
+    s = _system(name)
+    g = _check_graph(s["positions"], s["cell"], cutoff)
+    assert len(g["sources"]) > 0
+
+
+def test_neighbor_list_triclinic_and_wrapped():
+    rng = np.random.default_rng(3)
+    cell = np.array([[9.0, 0.0, 0.0], [2.5, 8.0, 0.0], [-1.5, 1.0, 10.0]])
+    frac = rng.uniform(-0.5, 1.5, size=(60, 3))  # outside the cell on purpose
+    pos = frac @ cell
+    _check_graph(pos, cell, 4.0)
+
+
+def test_neighbor_list_small_cell_many_images():
+    cell = np.eye(3) * 3.0
+    pos = np.array([[0.1, 0.2, 0.3], [1.6, 1.4, 1.5]])
+    g = _check_graph(pos, cell, 5.0)
+    assert len(g["sources"]) > 100
+
+
+def _evaluate_both(model_path, system, skin=0.5):
+    from symmetrix.mace_kokkos import MACEKokkosFloat
+    ora = _oracle()
+    om = ora.OracleModel(model_path)
+    ref = ora.evaluate_system(om, system, skin=skin)
+    ev = MACEKokkosFloat(model_path)
+    types = om.types_of(system["numbers"])
+    cell = np.asarray(system["cell"], float)
+    g = ev._prepare_periodic_factorized_graph(types, system["positions"], cell, np.linalg.inv(cell),
+                                              ev.r_cut + skin)
+    assert g["num_edges"] == len(ref["graph"]["sources"])
+    ev._compute_prepared_factorized_positions(g["generation"], system["positions"])
+    e = ev.node_energies
+    f = ev._reduce_atom_forces(len(types), None, None, g["generation"])
+    s = ev._reduce_stress(abs(np.linalg.det(cell)), None, g["generation"])
+    return om, ref, ev, g, e, f, s
+
+
+def _assert_efs(ref, e, f, s, n):
+    de = abs(np.sum(e) - ref["energy"]) / n
+    df = np.max(np.abs(f - ref["forces"]))
+    ds = np.max(np.abs(s - ref["stress"]))
+    print("energy/atom err %.3e  force err %.3e  stress err %.3e" % (de, df, ds))
+    assert de < E_TOL
+    assert df < F_TOL
+    assert ds < S_TOL
+
+
+def test_energy_forces_stress_tiny(tiny_model_path):
+    s = _system("tiny")
+    om, ref, ev, g, e, f, st = _evaluate_both(tiny_model_path, s)
+    np.testing.assert_allclose(e, ref["energies"], rtol=0, atol=1e-4)
+    _assert_efs(ref, e, f, st, len(e))
+
+
+def _stage_err(a, b):
+    scale = max(np.max(np.abs(b)), 1e-30)
+    return float(np.max(np.abs(a - b)) / scale)
+
+
+def test_stages_tiny(tiny_model_path):
+    s = _system("tiny")
+    om, ref, ev, g, e, f, st = _evaluate_both(tiny_model_path, s)
+    for name in ("A0", "M0", "H1", "Phi1", "A1", "A1_adj", "dPhi1", "H1_adj", "A0_adj"):
+        mine = ev._stage(name).astype(np.float64)
+        theirs = om.stage(name)
+        err = _stage_err(mine, theirs)
+        print(name, "relative max err %.3e" % err)
+        assert err < 1e-4, name
+    m0adj = ev._stage("M0_adj").astype(np.float64).reshape(len(e), -1, om.num_channels)
+    m0adj[:, 0, :] += ev._stage("direct").reshape(len(e), om.num_channels)
+    assert _stage_err(m0adj.ravel(), om.stage("M0_adj")) < 1e-4
+    # directed forces per edge
+    nf = ev.node_forces.reshape(-1, 3)
+    assert np.max(np.abs(nf - ref["node_forces"])) < 1e-5
+
+
+def test_energy_forces_stress_medium(medium_model_path):
+    s = _system("medium")
+    om, ref, ev, g, e, f, st = _evaluate_both(medium_model_path, s)
+    _assert_efs(ref, e, f, st, len(e))
+
+
+def test_repeat_calls_bitwise_deterministic(tiny_model_path):
+    from symmetrix.mace_kokkos import MACEKokkosFloat
+    s = _system("tiny")
+    ev = MACEKokkosFloat(tiny_model_path)
+    types = np.array([{8: 0, 22: 1, 38: 2}[int(z)] for z in s["numbers"]], np.int32)
+    cell = s["cell"]
+    g = ev._prepare_periodic_factorized_graph(types, s["positions"], cell, np.linalg.inv(cell), ev.r_cut + 0.5)
+    outs = []
+    for _ in range(3):
+        ev._compute_prepared_factorized_positions(g["generation"], s["positions"])
+        outs.append((ev.node_energies.tobytes(), ev.node_forces.tobytes()))
+    assert outs[0] == outs[1] == outs[2]
