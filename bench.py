@@ -1,0 +1,238 @@
+#!/usr/bin/env python3
+"""Headline benchmark: FP32 MACE energy + forces + stress per call on one
+MI355X, medium configuration.
+
+Workload: random-init MACE of the medium shape (2 layers, 128x0e+128x1o,
+l_max 3, correlation 3, 89-element embedding, 8 Bessel functions, radial MLP
+[64,64,64], r_cut 6.0 A) on a perturbed cubic SrTiO3 10x10x10 supercell
+(5,000 atoms, sigma 0.05 A, seed 0), neighbour graph at r_cut + 0.5 A skin
+built once on the device and retained (the reference protocol,
+benchmarks/mace_torch_comparison_protocol.md:65-90).
+
+One step = one complete E+F+S call with the positions already resident in
+HBM: edge geometry, both interaction layers forward and reverse, FP64 atom
+forces, stress and the total energy on the device.  W untimed warm-up steps,
+then exactly K timed steps between device synchronisations.
+
+Also reported: per-kernel HIP-event timing of the dominant kernel on the
+evaluator stream (roofline), the PCIe-inclusive host-positions call, the cold
+call (graph rebuild) and the CPU oracle on a bounded sample (cpu_baseline).
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import statistics
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "symmetrix-xl_amd"))
+sys.path.insert(0, ROOT)
+
+PEAK_FP32_TFLOPS = 157.3  # MI355X dense FP32 (matrix and packed vector)
+PEAK_HBM_GBS = 8000.0
+DOMINANT = "r1_reverse"
+
+
+def r1_reverse_flops_per_edge_channel(num_paths, num_terms, num_rows):
+    """Algorithmic FLOPs of the layer-2 reverse per active edge and channel:
+    edge-force part E_a*C*(12P + 2T + 14 rows) plus source-adjoint part
+    E_a*C*(6P + 2 rows + 2T) (FMA = 2 flops)."""
+    return (12 * num_paths + 2 * num_terms + 14 * num_rows) + (6 * num_paths + 2 * num_rows + 2 * num_terms)
+
+
+def model_counts(path):
+    """Paths, CG terms and rows of the model file (for the roofline)."""
+    with open(path) as f:
+        j = json.load(f)
+    P = len(j["Phi1_l"])
+    T = len(j["Phi1_clebsch_gordan"])
+    rows = sum((2 * a + 1) * (2 * b + 1) for a, b in zip(j["Phi1_l1"], j["Phi1_l2"]))
+    return P, T, rows, j["num_channels"]
+
+
+def hip_lib():
+    return ctypes.CDLL("libamdhip64.so")
+
+
+def device_copy_of(hip, a):
+    p = ctypes.c_void_p()
+    if hip.hipMalloc(ctypes.byref(p), ctypes.c_size_t(a.nbytes)) != 0:
+        raise RuntimeError("hipMalloc failed")
+    if hip.hipMemcpy(p, a.ctypes.data_as(ctypes.c_void_p), ctypes.c_size_t(a.nbytes), 1) != 0:
+        raise RuntimeError("hipMemcpy failed")
+    return p
+
+
+def load_traffic():
+    """HBM bytes per launch of the dominant kernel from the committed
+    rocprofv3 PMC summary (FETCH_SIZE + WRITE_SIZE), if present."""
+    path = os.path.join(ROOT, "profiles", "r1_reverse_medium_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get("bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_baseline(model_path, system, cutoff, skin, max_seconds=25.0):
+    """The CPU oracle (FP32 C++/OpenMP restatement of the reference CPU path)
+    on the same workload: warm calls with the graph retained."""
+    from oracle import oracle as ora
+    om = ora.OracleModel(model_path)
+    graph = ora.neighbor_graph(system["positions"], system["cell"], cutoff + skin)
+    cell = np.asarray(system["cell"], float)
+    vol = abs(np.linalg.det(cell))
+    types = om.types_of(system["numbers"])
+    nt = types[graph["sources"]]
+
+    def call():
+        xyz, r = ora.prepared_geometry(graph, cell, system["positions"], system["positions"], om.r_cut)
+        e, f = om.evaluate(types, graph["num_neigh"], graph["sources"], nt, xyz, r)
+        ora.reduce_forces(len(types), graph["receivers"], graph["sources"], f)
+        ora.reduce_stress(f, xyz, vol)
+        return float(np.sum(e))
+
+    call()  # warm-up (radial tabulation for the active types)
+    times = []
+    t_start = time.perf_counter()
+    while True:
+        t0 = time.perf_counter()
+        call()
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start > max_seconds or len(times) >= 5:
+            break
+    n = len(types)
+    return {"value": round(statistics.median(times) * 1e6 / n, 3), "unit": "us/atom",
+            "cores": int(ora.lib().oracle_num_threads()), "kind": "port",
+            "sample": "medium workload (5000 atoms, 496k edges), %d warm call(s) after 1 warm-up, median" % len(times)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures the single-GPU path only: this build runs on one MI355X and "
+              "has no multi-GPU (halo-exchange) path; run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    from symmetrix import random_model, systems
+    from symmetrix.mace_kokkos import MACEKokkosFloat
+
+    model_path = random_model.cached_model("medium")
+    system = systems.srtio3_supercell(10, sigma=0.05, seed=0)
+    skin = 0.5
+    ev = MACEKokkosFloat(model_path)
+    lut = {z: i for i, z in enumerate(ev.atomic_numbers)}
+    types = np.array([lut[int(z)] for z in system["numbers"]], np.int32)
+    cell = np.asarray(system["cell"], float)
+    inv = np.linalg.inv(cell)
+    vol = abs(float(np.linalg.det(cell)))
+    n_atoms = len(types)
+
+    t0 = time.perf_counter()
+    g = ev._prepare_periodic_factorized_graph(types, system["positions"], cell, inv, ev.r_cut + skin)
+    ev._compute_prepared_factorized_positions(g["generation"], system["positions"])
+    cold_ms = (time.perf_counter() - t0) * 1e3
+    gen = g["generation"]
+
+    hip = hip_lib()
+    d_pos = device_copy_of(hip, np.ascontiguousarray(system["positions"], dtype=np.float64))
+
+    from symmetrix._native import check, lib
+
+    def step():
+        ev._compute_prepared_factorized_positions_device(gen, d_pos.value)
+        check(lib.smx_reduce_prepared_node_forces(ev._h, gen, None))
+        check(lib.smx_reduce_prepared_stress(ev._h, gen, vol, None))
+        check(lib.smx_total_energy_device(ev._h, None))
+        ev.synchronize()
+
+    for _ in range(args.warmup):
+        step()
+    # HIP events around the dominant kernel on the evaluator's own stream
+    ev.set_kernel_timing(True)
+    ev.set_kernel_timing_filter(DOMINANT)
+    ev.reset_kernel_timing()
+    per_call = []
+    ev.synchronize()
+    t_all = time.perf_counter()
+    for _ in range(args.steps):
+        t0 = time.perf_counter()
+        step()
+        per_call.append(time.perf_counter() - t0)
+    ev.synchronize()
+    elapsed = time.perf_counter() - t_all
+    timing = ev.kernel_timing()
+    ev.set_kernel_timing(False)
+
+    ms_per_step = elapsed * 1e3 / args.steps
+    us_per_atom = elapsed * 1e6 / (args.steps * n_atoms)
+    median_us_per_atom = statistics.median(per_call) * 1e6 / n_atoms
+
+    # PCIe-inclusive call: positions from host memory, results copied back
+    t0 = time.perf_counter()
+    host_calls = 3
+    for _ in range(host_calls):
+        ev._compute_prepared_factorized_positions(gen, system["positions"])
+        e = ev.node_energies
+        ev._reduce_atom_forces(n_atoms, None, None, gen)
+        ev._reduce_stress(vol, None, gen)
+    host_us_per_atom = (time.perf_counter() - t0) * 1e6 / (host_calls * n_atoms)
+    energy = float(np.sum(e))
+
+    # roofline of the dominant kernel
+    P, T, rows, C = model_counts(model_path)
+    rec = ev._stage("edge_records")
+    E_active = int(np.count_nonzero(rec.reshape(g["num_edges"], -1)[:, 2].view(np.int32)))
+    ms_r1, launches = timing.get(DOMINANT, (float("nan"), 0))
+    avg_ms = ms_r1 / max(launches, 1)
+    flops = E_active * C * r1_reverse_flops_per_edge_channel(P, T, rows)
+    achieved = flops / (avg_ms * 1e-3) / 1e12
+    traffic = load_traffic()
+
+    out = {
+        "metric": "us/atom per E+F+stress call (FP32, 1 MI355X) at 5k atoms",
+        "value": round(us_per_atom, 4),
+        "unit": "us/atom",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic (random-init medium MACE, perturbed SrTiO3 supercell, seed 0)",
+        "config": {"workload": "medium: SrTiO3 10x10x10 (5000 atoms), MACE 128x0e+128x1o l_max 3 corr 3, "
+                               "r_cut 6.0 A + 0.5 A skin, graph retained",
+                   "atoms": n_atoms, "edges": int(g["num_edges"]), "active_edges": E_active,
+                   "positions": "device-resident"},
+        "roofline": {"bound": "mfma", "kernel": DOMINANT, "achieved": round(achieved, 3),
+                     "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_TFLOPS, 4),
+                     "traffic": traffic, "avg_launch_ms": round(avg_ms, 4),
+                     "flops_per_launch": flops},
+        "median_us_per_atom": round(median_us_per_atom, 4),
+        "host_positions_us_per_atom": round(host_us_per_atom, 4),
+        "cold_call_ms": round(cold_ms, 2),
+        "energy_eV": energy,
+        "baseline_reference": {"value": 1.922, "hardware": "RTX 5090", "note": "published, trained OMAT-0 medium"},
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(model_path, system, ev.r_cut, skin)
+    hip.hipFree(d_pos)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -162,6 +162,8 @@ SMX_API int32_t smx_debug_stage(SmxEvaluator* ev, const char* name, float* out, 
 
 /* Launch timing with HIP events on the evaluator stream (off by default). */
 SMX_API int32_t smx_set_kernel_timing(SmxEvaluator* ev, int32_t enabled);
+/* restrict timing to the comma-separated stage names (NULL or "" = all) */
+SMX_API int32_t smx_set_kernel_timing_filter(SmxEvaluator* ev, const char* names);
 SMX_API int32_t smx_kernel_timing_reset(SmxEvaluator* ev);
 /* index-th timed kernel name (NULL past the end), total ms and launch count */
 SMX_API int32_t smx_kernel_timing(SmxEvaluator* ev, int32_t index, const char** name, double* total_ms,

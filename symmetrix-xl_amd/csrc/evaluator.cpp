@@ -90,16 +90,33 @@ public:
         double total_ms = 0.0;
         std::int64_t launches = 0;
     };
-    ~EventTimer() override { clear_pending(); }
+    ~EventTimer() override {
+        clear_pending();
+        for (hipEvent_t e : pool_) (void)hipEventDestroy(e);
+    }
+    // Only launches whose name is in `filter` (comma-separated; empty = all)
+    // are bracketed with events.
+    void set_filter(const std::string& filter) {
+        names_.clear();
+        std::size_t p = 0;
+        while (p <= filter.size()) {
+            const std::size_t q = std::min(filter.find(',', p), filter.size());
+            if (q > p) names_.push_back(filter.substr(p, q - p));
+            p = q + 1;
+        }
+    }
+    bool wanted(const char* name) const {
+        return names_.empty() || std::find(names_.begin(), names_.end(), name) != names_.end();
+    }
     void begin(const char* name, hipStream_t s) override {
-        hipEvent_t a;
-        SMX_HIP(hipEventCreate(&a));
+        if (!wanted(name)) return;
+        hipEvent_t a = take();
         SMX_HIP(hipEventRecord(a, s));
         open_[name] = a;
     }
     void end(const char* name, hipStream_t s) override {
-        hipEvent_t b;
-        SMX_HIP(hipEventCreate(&b));
+        if (!wanted(name)) return;
+        hipEvent_t b = take();
         SMX_HIP(hipEventRecord(b, s));
         pending_.push_back({name, open_[name], b});
         open_.erase(name);
@@ -135,15 +152,27 @@ private:
         std::string name;
         hipEvent_t a, b;
     };
+    hipEvent_t take() {
+        if (pool_.empty()) {
+            hipEvent_t e;
+            SMX_HIP(hipEventCreate(&e));
+            return e;
+        }
+        hipEvent_t e = pool_.back();
+        pool_.pop_back();
+        return e;
+    }
     void clear_pending() {
         for (auto& p : pending_) {
-            (void)hipEventDestroy(p.a);
-            (void)hipEventDestroy(p.b);
+            pool_.push_back(p.a);
+            pool_.push_back(p.b);
         }
         pending_.clear();
-        for (auto& o : open_) (void)hipEventDestroy(o.second);
+        for (auto& o : open_) pool_.push_back(o.second);
         open_.clear();
     }
+    std::vector<hipEvent_t> pool_;
+    std::vector<std::string> names_;
     std::map<std::string, hipEvent_t> open_;
     std::vector<Pending> pending_;
     std::map<std::string, Entry> entries_;
@@ -879,6 +908,14 @@ int32_t smx_set_kernel_timing(SmxEvaluator* ev, int32_t enabled) {
         SMX_HIP(hipStreamSynchronize(e.stream));
         if (enabled && !e.timer) e.timer = std::make_unique<smx::EventTimer>();
         if (!enabled) e.timer.reset();
+    });
+}
+
+int32_t smx_set_kernel_timing_filter(SmxEvaluator* ev, const char* names) {
+    return guarded([&] {
+        auto& e = E(ev);
+        if (!e.timer) throw std::logic_error("kernel timing is not enabled");
+        e.timer->set_filter(names ? names : "");
     });
 }
 

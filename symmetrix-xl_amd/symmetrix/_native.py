@@ -83,6 +83,7 @@ SIGNATURES = [
     ("smx_synchronize", _i32, [_vp]),
     ("smx_debug_stage", _i32, [_vp, _cp, _vp, _i64, _p_i64]),
     ("smx_set_kernel_timing", _i32, [_vp, _i32]),
+    ("smx_set_kernel_timing_filter", _i32, [_vp, _cp]),
     ("smx_kernel_timing_reset", _i32, [_vp]),
     ("smx_kernel_timing", _i32, [_vp, _i32, ctypes.POINTER(_cp), _p_dbl, _p_i64]),
     ("smx_neighbor_list", _i32, [_i32, _vp, _vp, _vp, _dbl, _p_i64, _vp, _vp, _vp, _vp, _vp]),

@@ -207,6 +207,12 @@ class MACEKokkosFloat:
     def set_kernel_timing(self, enabled=True):
         check(lib.smx_set_kernel_timing(self._h, 1 if enabled else 0))
 
+    def set_kernel_timing_filter(self, names=""):
+        """Time only the named stages (iterable or comma-separated string)."""
+        if not isinstance(names, str):
+            names = ",".join(names)
+        check(lib.smx_set_kernel_timing_filter(self._h, names.encode()))
+
     def reset_kernel_timing(self):
         check(lib.smx_kernel_timing_reset(self._h))
 
