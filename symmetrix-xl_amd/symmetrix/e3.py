@@ -324,3 +324,46 @@ def product_basis_support(l_in_max, L_out, correlation):
         for M in range(d_out):
             support[M].extend(monos[j] for j in np.nonzero(nz[M])[0])
     return support
+
+
+def coupling_chain_tensors(l_in_max, L_out, nu):
+    """The unsymmetrised coupling-path tensors of MACE's symmetric contraction
+    (e3nn's iterated Wigner 3j products over (l_1..l_nu) and every
+    intermediate irrep, keeping the chains that end in L_out with parity
+    (-1)^L_out), each embedded as [2L_out+1, n_in, ..., n_in]."""
+    n_in = (l_in_max + 1) ** 2
+    out = []
+    for ls in itertools.product(range(l_in_max + 1), repeat=nu):
+        states = [(ls[0], (-1) ** ls[0], np.eye(2 * ls[0] + 1))]
+        for l in ls[1:]:
+            nxt = []
+            for (L, p, T) in states:
+                for L2 in range(abs(L - l), L + l + 1):
+                    W = wigner_3j(L, l, L2)
+                    nxt.append((L2, p * (-1) ** l, np.einsum("M...,MmN->N...m", T, W)))
+            states = nxt
+        for (L, p, T) in states:
+            if L == L_out and p == (-1) ** L_out:
+                full = np.zeros((2 * L_out + 1,) + (n_in,) * nu)
+                idx = tuple(slice(l * l, (l + 1) ** 2) for l in ls)
+                full[(slice(None),) + idx] = T
+                out.append(full)
+    return out
+
+
+@lru_cache(maxsize=None)
+def structural_support(l_in_max, L_out, correlation):
+    """Monomials per output m as the reference's extractor keys them
+    (extract_mace_data.py:1013-1060): a sorted index tuple is a term when
+    any *ordered* entry of any coupling-path tensor exceeds 1e-12, even if
+    the symmetrised coefficient vanishes.  Ordered by (degree, lex) like
+    multivariate_polynomial.cpp:22-40."""
+    d_out = 2 * L_out + 1
+    keys = [set() for _ in range(d_out)]
+    for nu in range(1, correlation + 1):
+        for T in coupling_chain_tensors(l_in_max, L_out, nu):
+            for M in range(d_out):
+                for t in np.argwhere(np.abs(T[M]) > 1e-12):
+                    keys[M].add(tuple(sorted(int(v) for v in t)))
+    return [sorted(k, key=lambda m: (len(m), m)) for k in keys]
+

@@ -79,11 +79,13 @@ def _fmt(a):
 
 
 def _product_weights(rng, l_in_max, L_out, correlation, num_types, C, scale):
-    """Per-(type, m_out, channel) polynomial coefficients over a shared monomial
-    list (the reference's U x W contraction, extract_mace_data.py:1070-1112)."""
+    """Per-(type, m_out, channel) polynomial coefficients over the monomial
+    list of the reference's extractor (the U x W contraction,
+    extract_mace_data.py:1013-1112).  The list is the structural support of
+    the coupling-path tensors; the monomials whose symmetrised coefficient
+    vanishes carry an exact zero, as the reference's file carries ~0."""
     d_out = 2 * L_out + 1
-    monos_all = [[] for _ in range(d_out)]
-    coef_all = [None] * d_out
+    keys_all = e3.structural_support(l_in_max, L_out, correlation)
     blocks = []
     for nu in range(1, correlation + 1):
         monos, U = e3.symmetric_basis(l_in_max, L_out, nu)
@@ -92,17 +94,17 @@ def _product_weights(rng, l_in_max, L_out, correlation, num_types, C, scale):
         W = rng.normal(size=(num_types, U.shape[0], C)) * (
             scale[nu - 1] / math.sqrt(U.shape[0]))
         blocks.append((monos, U, W))
+    monos_all = [[] for _ in range(d_out)]
+    coef_all = [None] * d_out
     for M in range(d_out):
-        keys = []
-        cols = []
+        index = {k: i for i, k in enumerate(keys_all[M])}
+        coef = np.zeros((num_types, C, len(index)))
         for monos, U, W in blocks:
             nz = np.nonzero(np.abs(U[:, M, :]).max(axis=0) > 1e-9)[0]
-            keys.extend(monos[j] for j in nz)
-            # coefficient [type, channel, term]
-            cols.append(np.einsum("tec,ej->tcj", W, U[:, M, nz]))
-        order = sorted(range(len(keys)), key=lambda i: (len(keys[i]), keys[i]))
-        coef = np.concatenate(cols, axis=2)[:, :, order]
-        monos_all[M] = [list(keys[i]) for i in order]
+            cols = np.einsum("tec,ej->tcj", W, U[:, M, nz])
+            for jj, j in enumerate(nz):
+                coef[:, :, index[tuple(monos[j])]] += cols[:, :, jj]
+        monos_all[M] = [list(k) for k in keys_all[M]]
         coef_all[M] = coef
     return monos_all, coef_all
 
@@ -264,7 +266,7 @@ def cached_model(config, seed=None, directory=None):
     directory = directory or os.environ.get(
         "SYMMETRIX_MODEL_CACHE", "/tmp/symmetrix_models")
     os.makedirs(directory, exist_ok=True)
-    path = os.path.join(directory, "mace_%s_seed%d_v1.json" % (cfg.name, seed))
+    path = os.path.join(directory, "mace_%s_seed%d_v2.json" % (cfg.name, seed))
     if not os.path.exists(path):
         write_model(cfg, path, seed)
     return path
