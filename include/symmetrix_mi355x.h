@@ -68,7 +68,7 @@ typedef struct SmxDeviceOutputs {
     int32_t num_nodes;
     int64_t num_edges;
     const double* node_energies; /* [N] */
-    const double* node_forces;   /* [E][3]: -dE/dxyz_e */
+    const double* node_forces;   /* [E][3]: -dE/dxyz_e (NULL under the tiled plan) */
     const double* atom_forces;   /* [N][3] after smx_reduce_prepared_node_forces */
     const double* stress;        /* [3][3] after smx_reduce_prepared_stress */
     const double* total_energy;  /* [1] after smx_total_energy_device */
@@ -113,6 +113,17 @@ SMX_API int32_t smx_prepare_periodic_factorized_graph(SmxEvaluator* ev, int32_t 
                                                       const double* positions, const double* cell,
                                                       const double* inverse_cell, double neighbor_cutoff,
                                                       uint64_t* generation, int64_t* num_edges);
+/* Execution plan request (set_execution_plan_request, mace_kokkos.hpp:95-96;
+ * calculator execution_profile / allow_fixed_workspace): "speed" keeps every
+ * edge's workspace (one receiver tile), "capacity" runs the three-sweep
+ * tiled plan with at most tile_receivers receivers per tile (the reference's
+ * dual-layer tiled plan, mace_kokkos_evaluate.cpp:755-1148), "auto" picks
+ * the tiled plan when the untiled workspace would exceed 70% of the free
+ * device memory.  tile_receivers 0 keeps the current limit (default 32768,
+ * mace_kokkos.hpp:542).  Applies to graphs prepared afterwards. */
+SMX_API int32_t smx_set_execution_plan(SmxEvaluator* ev, const char* profile, int32_t tile_receivers);
+/* execution_plan report of the prepared graph (execution_plan.hpp:38-50) */
+SMX_API int32_t smx_execution_plan(SmxEvaluator* ev, char* out, int64_t capacity);
 /* update_factorized_cell (mace_kokkos.hpp:436; pybind _update_factorized_cell) */
 SMX_API int32_t smx_update_factorized_cell(SmxEvaluator* ev, uint64_t generation, const double* cell,
                                            const double* inverse_cell);

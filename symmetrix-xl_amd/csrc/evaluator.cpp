@@ -61,6 +61,12 @@ public:
         return static_cast<T*>(ptr_);
     }
     std::size_t capacity() const { return cap_; }
+    // take ownership of a hipMalloc'd block
+    void adopt(void* p, std::size_t bytes) {
+        release();
+        ptr_ = p;
+        cap_ = p ? bytes : 0;
+    }
     void release() {
         if (ptr_) (void)hipFree(ptr_);
         ptr_ = nullptr;
@@ -179,12 +185,11 @@ private:
     std::vector<std::string> order_;
 };
 
-struct HostGemmPlan {
+// Concatenated node-linear tiles of every receiver tile of the graph.
+struct PlanSet {
     std::vector<GemmTile> tiles;
-    std::vector<GemmGroup> groups;
-    int max_n = 0;
-    DevBuf d_tiles, d_groups;
-    GemmPlan view;
+    std::vector<std::size_t> tile_begin;  // per receiver tile: first GemmTile
+    DevBuf d_tiles;
 };
 
 }  // namespace
@@ -196,27 +201,47 @@ struct Evaluator {
     hipStream_t stream = nullptr;
     std::string streamed_edges = "direct";
 
-    // model tables
+    // model tables and node-linear groups (defined for every type and l)
     std::vector<std::unique_ptr<DevBuf>> model_bufs;
+    std::vector<GemmGroup> groups_a0, groups_h1, groups_a1f, groups_a1r;
+    DevBuf d_groups_a0, d_groups_h1, d_groups_a1f, d_groups_a1r;
+    int max_n_a0 = 0, max_n_h1 = 0, max_n_a1f = 0, max_n_a1r = 0;
+
+    // execution plan request
+    std::string profile = "auto";   // auto | speed | capacity
+    int tile_limit = 32768;         // receivers per tile in the tiled plan
+    bool tiled = false;
 
     // graph
     std::uint64_t generation = 0, next_generation = 1;
     int N = 0;
     std::int64_t E = 0;
     std::vector<int> h_node_types;
-    DevBuf d_node_types, d_offsets, d_neigh, d_neigh_types, d_receivers, d_soff, d_sedges, d_counts, d_node_list;
-    // periodic geometry reference
+    std::vector<int> h_offsets;
+    DevBuf d_node_types, d_offsets, d_neigh, d_neigh_types, d_receivers, d_soff, d_sedges, d_counts;
+    // receiver tiles
+    std::vector<TileView> tiles;
+    PlanSet ps_a0, ps_h1, ps_a1f, ps_a1r;
+    std::vector<int> h_node_list;
+    std::vector<std::size_t> node_list_begin;
+    DevBuf d_node_list, d_touched;
+    std::vector<std::size_t> touched_begin;
+    int max_tile_nr = 0;
+    std::int64_t max_tile_ne = 0;
+    // periodic geometry reference (wrapped fractional positions + edge images)
     bool has_fractional = false;
     double cell[9] = {0}, inv_cell[9] = {0};
-    DevBuf d_fxyz, d_ref_positions, d_disp, d_positions;
+    DevBuf d_wfrac, d_images, d_ref_positions, d_disp, d_positions;
     // per call
-    DevBuf d_xyz, d_r, d_erec, d_invalid;
-    DevBuf w_Phi0, w_A0, w_M0, w_H1, w_Phi1, w_A1, w_A1_adj, w_direct, w_dPhi1, w_Wsrc, w_H1_adj, w_M0_adj, w_A0_adj,
-        w_Phi0_adj, d_node_energies, d_node_forces, d_atom_forces, d_stress, d_stress_partial, d_total;
+    DevBuf d_xyz, d_r, d_invalid;
+    DevBuf w_erec, w_Phi0, w_A0, w_M0, w_Phi1, w_A1, w_A1_adj, w_dPhi1, w_Wsrc, w_M0_adj, w_A0_adj, w_Phi0_adj,
+        w_node_forces;
+    DevBuf g_H1, g_H1_adj, g_xaff, g_direct, d_node_energies, d_atom_forces, d_virial, d_stress, d_stress_partial,
+        d_total;
     Workspace ws;
-    HostGemmPlan plan_a0, plan_h1, plan_a1f, plan_a1r;
     bool evaluated = false;
-    int stress_blocks = 1024;
+    bool xyz_host = false;  // this call's edge vectors came from the caller
+    int stress_blocks = 256;
 
     std::unique_ptr<EventTimer> timer;
 
@@ -233,6 +258,7 @@ struct Evaluator {
                                     std::to_string(hm.l_max) + ", L_max " + std::to_string(hm.L_max));
         SMX_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
         upload_model();
+        define_groups();
         SMX_HIP(hipStreamSynchronize(stream));
     }
 
@@ -297,99 +323,204 @@ struct Evaluator {
         dm.E0 = put(hm.atomic_energies);
     }
 
-    // ---------------------------------------------------------------- graph
-    void build_plans() {
+    // Weight groups of the node linears: A0 per (type, l), H1 per l, A1 per
+    // l (forward K = num_e(l)*C -> C; reverse C -> num_e(l)*C).
+    void define_groups() {
         const int C = hm.C, NY = hm.num_lm, NH = hm.num_LM, NLME = hm.num_lme;
-        // node list sorted by type (stable) -> contiguous per-type ranges
-        std::vector<int> order(N);
-        std::iota(order.begin(), order.end(), 0);
-        std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return h_node_types[a] < h_node_types[b]; });
-        upload(d_node_list, order, stream);
-        std::vector<std::pair<int, std::pair<int, int>>> ranges;  // type -> [begin, end)
-        for (int p = 0; p < N;) {
-            int q = p;
-            while (q < N && h_node_types[order[q]] == h_node_types[order[p]]) ++q;
-            ranges.push_back({h_node_types[order[p]], {p, q}});
-            p = q;
-        }
-        auto add_tiles = [](HostGemmPlan& P, int group, int m, int begin, int end) {
-            for (int s = begin; s < end; s += 16) P.tiles.push_back(GemmTile{s, std::min(16, end - s), group, m});
-        };
-        auto finish = [&](HostGemmPlan& P) {
-            for (const auto& g : P.groups) P.max_n = std::max(P.max_n, g.N);
-            P.view.tiles = upload(P.d_tiles, P.tiles, stream);
-            P.view.groups = upload(P.d_groups, P.groups, stream);
-            P.view.node_list = d_node_list.as<int>();
-            P.view.num_tiles = static_cast<int>(P.tiles.size());
-            P.view.max_n = P.max_n;
-        };
-        for (HostGemmPlan* P : {&plan_a0, &plan_h1, &plan_a1f, &plan_a1r}) {
-            P->tiles.clear();
-            P->groups.clear();
-            P->max_n = 0;
-        }
-        // A0: per (type, l), C x C
-        for (const auto& tr : ranges) {
-            const int t = tr.first;
-            for (int l = 0; l <= hm.l_max; ++l) {
-                const int g = static_cast<int>(plan_a0.groups.size());
-                plan_a0.groups.push_back(GemmGroup{(static_cast<std::int64_t>(t) * (hm.l_max + 1) + l) * C * C, C, C,
-                                                   NY * C, l * l * C, C, NY * C, l * l * C, C});
-                for (int m = 0; m < 2 * l + 1; ++m) add_tiles(plan_a0, g, m, tr.second.first, tr.second.second);
-            }
-        }
-        // H1: per l <= L_max
-        for (int l = 0; l <= hm.L_max; ++l) {
-            const int g = static_cast<int>(plan_h1.groups.size());
-            plan_h1.groups.push_back(GemmGroup{static_cast<std::int64_t>(l) * C * C, C, C, NH * C, l * l * C, C,
-                                               NH * C, l * l * C, C});
-            for (int m = 0; m < 2 * l + 1; ++m) add_tiles(plan_h1, g, m, 0, N);
-        }
-        // A1 forward / reverse: per l with paths
+        for (int t = 0; t < hm.num_elements; ++t)
+            for (int l = 0; l <= hm.l_max; ++l)
+                groups_a0.push_back(GemmGroup{(static_cast<std::int64_t>(t) * (hm.l_max + 1) + l) * C * C, C, C,
+                                              NY * C, l * l * C, C, NY * C, l * l * C, C});
+        for (int l = 0; l <= hm.L_max; ++l)
+            groups_h1.push_back(GemmGroup{static_cast<std::int64_t>(l) * C * C, C, C, NH * C, l * l * C, C, NH * C,
+                                          l * l * C, C});
         for (int l = 0; l <= hm.l_max; ++l) {
             const int ne = hm.num_e[l];
-            if (ne == 0) continue;
-            const int gf = static_cast<int>(plan_a1f.groups.size());
-            plan_a1f.groups.push_back(GemmGroup{hm.A1_offset[l], ne * C, C, NLME * C, hm.lme_base[l] * C, ne * C,
-                                                NY * C, l * l * C, C});
-            const int gr = static_cast<int>(plan_a1r.groups.size());
-            plan_a1r.groups.push_back(GemmGroup{hm.A1_offset[l], C, ne * C, NY * C, l * l * C, C, NLME * C,
-                                                hm.lme_base[l] * C, ne * C});
-            for (int m = 0; m < 2 * l + 1; ++m) {
-                add_tiles(plan_a1f, gf, m, 0, N);
-                add_tiles(plan_a1r, gr, m, 0, N);
+            groups_a1f.push_back(GemmGroup{hm.A1_offset[l], std::max(ne, 1) * C, C, NLME * C, hm.lme_base[l] * C,
+                                           ne * C, NY * C, l * l * C, C});
+            groups_a1r.push_back(GemmGroup{hm.A1_offset[l], C, std::max(ne, 1) * C, NY * C, l * l * C, C, NLME * C,
+                                           hm.lme_base[l] * C, ne * C});
+        }
+        auto mx = [](const std::vector<GemmGroup>& g) {
+            int m = 0;
+            for (const auto& x : g) m = std::max(m, x.N);
+            return m;
+        };
+        max_n_a0 = mx(groups_a0);
+        max_n_h1 = mx(groups_h1);
+        max_n_a1f = mx(groups_a1f);
+        max_n_a1r = mx(groups_a1r);
+        upload(d_groups_a0, groups_a0, stream);
+        upload(d_groups_h1, groups_h1, stream);
+        upload(d_groups_a1f, groups_a1f, stream);
+        upload(d_groups_a1r, groups_a1r, stream);
+    }
+
+    // ------------------------------------------------------------- planning
+    // Bytes of the untiled plan for a graph (workspace high-water).
+    std::size_t untiled_bytes(std::int64_t n, std::int64_t e) const {
+        const std::size_t C = hm.C, NY = hm.num_lm, NH = hm.num_LM, NLME = hm.num_lme;
+        const std::size_t node = (6 * NY + 4 * NH + 2 * NLME + 2) * C * 4 + 200;
+        const std::size_t edge = (ks->record_floats() + NH * C) * 4 + 24 + 32 + 24;
+        return node * n + edge * e;
+    }
+
+    void choose_plan() {
+        if (profile == "capacity") {
+            tiled = true;
+        } else if (profile == "speed") {
+            tiled = false;
+        } else {
+            std::size_t free_b = 0, total_b = 0;
+            SMX_HIP(hipMemGetInfo(&free_b, &total_b));
+            const std::size_t have = free_b + workspace_bytes();
+            tiled = untiled_bytes(N, E) > have / 10 * 7;
+        }
+        if (N <= tile_limit && profile != "capacity") tiled = false;
+    }
+
+    std::size_t workspace_bytes() const {
+        std::size_t b = 0;
+        for (const DevBuf* x : {&w_erec, &w_Phi0, &w_A0, &w_M0, &w_Phi1, &w_A1, &w_A1_adj, &w_dPhi1, &w_Wsrc,
+                                &w_M0_adj, &w_A0_adj, &w_Phi0_adj, &w_node_forces, &d_xyz, &d_r})
+            b += x->capacity();
+        return b;
+    }
+
+    void build_tiles() {
+        tiles.clear();
+        const int limit = tiled ? std::max(1, tile_limit) : std::max(N, 1);
+        for (int r0 = 0; r0 < N || (N == 0 && r0 == 0); r0 += limit) {
+            TileView t;
+            t.r0 = r0;
+            t.nr = std::min(limit, N - r0);
+            t.e0 = h_offsets[r0];
+            t.ne = static_cast<std::int64_t>(h_offsets[r0 + t.nr]) - t.e0;
+            tiles.push_back(t);
+            if (N == 0) break;
+        }
+        max_tile_nr = 0;
+        max_tile_ne = 0;
+        for (const auto& t : tiles) {
+            max_tile_nr = std::max(max_tile_nr, t.nr);
+            max_tile_ne = std::max(max_tile_ne, t.ne);
+        }
+        // node lists (local rows sorted by type) and node-linear tiles
+        h_node_list.clear();
+        node_list_begin.clear();
+        for (PlanSet* p : {&ps_a0, &ps_h1, &ps_a1f, &ps_a1r}) {
+            p->tiles.clear();
+            p->tile_begin.clear();
+        }
+        for (const auto& t : tiles) {
+            const std::size_t base = h_node_list.size();
+            node_list_begin.push_back(base);
+            std::vector<int> order(t.nr);
+            std::iota(order.begin(), order.end(), 0);
+            std::stable_sort(order.begin(), order.end(), [&](int a, int b) {
+                return h_node_types[t.r0 + a] < h_node_types[t.r0 + b];
+            });
+            h_node_list.insert(h_node_list.end(), order.begin(), order.end());
+            for (PlanSet* p : {&ps_a0, &ps_h1, &ps_a1f, &ps_a1r}) p->tile_begin.push_back(p->tiles.size());
+            auto add = [](PlanSet& P, int group, int m, int begin, int end) {
+                for (int s = begin; s < end; s += 16) P.tiles.push_back(GemmTile{s, std::min(16, end - s), group, m});
+            };
+            for (int p = 0; p < t.nr;) {
+                int q = p;
+                const int type = h_node_types[t.r0 + order[p]];
+                while (q < t.nr && h_node_types[t.r0 + order[q]] == type) ++q;
+                for (int l = 0; l <= hm.l_max; ++l)
+                    for (int m = 0; m < 2 * l + 1; ++m) add(ps_a0, type * (hm.l_max + 1) + l, m, p, q);
+                p = q;
+            }
+            for (int l = 0; l <= hm.L_max; ++l)
+                for (int m = 0; m < 2 * l + 1; ++m) add(ps_h1, l, m, 0, t.nr);
+            for (int l = 0; l <= hm.l_max; ++l) {
+                if (hm.num_e[l] == 0) continue;
+                for (int m = 0; m < 2 * l + 1; ++m) {
+                    add(ps_a1f, l, m, 0, t.nr);
+                    add(ps_a1r, l, m, 0, t.nr);
+                }
             }
         }
-        for (HostGemmPlan* P : {&plan_a0, &plan_h1, &plan_a1f, &plan_a1r}) finish(*P);
+        for (PlanSet* p : {&ps_a0, &ps_h1, &ps_a1f, &ps_a1r}) {
+            p->tile_begin.push_back(p->tiles.size());
+            upload(p->d_tiles, p->tiles, stream);
+        }
+        upload(d_node_list, h_node_list, stream);
+        auto view = [&](const PlanSet& P, std::size_t ti, const DevBuf& groups, int max_n) {
+            GemmPlan g;
+            g.tiles = P.d_tiles.as<GemmTile>() + P.tile_begin[ti];
+            g.num_tiles = static_cast<int>(P.tile_begin[ti + 1] - P.tile_begin[ti]);
+            g.groups = groups.as<GemmGroup>();
+            g.node_list = d_node_list.as<int>() + node_list_begin[ti];
+            g.max_n = max_n;
+            return g;
+        };
+        for (std::size_t ti = 0; ti < tiles.size(); ++ti) {
+            tiles[ti].a0 = view(ps_a0, ti, d_groups_a0, max_n_a0);
+            tiles[ti].h1 = view(ps_h1, ti, d_groups_h1, max_n_h1);
+            tiles[ti].a1f = view(ps_a1f, ti, d_groups_a1f, max_n_a1f);
+            tiles[ti].a1r = view(ps_a1r, ti, d_groups_a1r, max_n_a1r);
+        }
+        // touched sources of every tile (tiled plan only)
+        touched_begin.assign(1, 0);
+        if (tiled && N > 0) {
+            DevBuf bitmap, counts, one;
+            const int words = N / 32 + 1;
+            bitmap.ensure(sizeof(std::uint32_t) * words);
+            counts.ensure(sizeof(int) * words);
+            one.ensure(sizeof(int) * N);
+            std::vector<int> all;
+            std::vector<int> host(N);
+            for (auto& t : tiles) {
+                const int cnt = build_touched_sources(N, t.e0, t.ne, d_neigh.as<int>(), bitmap.as<std::uint32_t>(),
+                                                      counts.as<int>(), one.as<int>(), stream);
+                if (cnt > 0)
+                    SMX_HIP(hipMemcpy(host.data(), one.as<int>(), sizeof(int) * cnt, hipMemcpyDeviceToHost));
+                all.insert(all.end(), host.begin(), host.begin() + cnt);
+                touched_begin.push_back(all.size());
+            }
+            upload(d_touched, all, stream);
+            for (std::size_t ti = 0; ti < tiles.size(); ++ti) {
+                tiles[ti].touched = d_touched.as<int>() + touched_begin[ti];
+                tiles[ti].touched_count = static_cast<int>(touched_begin[ti + 1] - touched_begin[ti]);
+            }
+        }
     }
 
     void ensure_workspace() {
         const std::size_t C = hm.C, NY = hm.num_lm, NH = hm.num_LM, NLME = hm.num_lme;
-        const std::size_t n = std::max(N, 1), e = std::max<std::int64_t>(E, 1);
+        const std::size_t n = std::max(N, 1), tn = std::max(max_tile_nr, 1);
+        const std::size_t te = std::max<std::int64_t>(max_tile_ne, 1), e = std::max<std::int64_t>(E, 1);
         auto f = [&](DevBuf& b, std::size_t count) { return static_cast<float*>(b.ensure(count * sizeof(float))); };
-        ws.Phi0 = f(w_Phi0, n * NY * C);
-        ws.A0 = f(w_A0, n * NY * C);
-        ws.M0 = f(w_M0, n * NH * C);
-        ws.H1 = f(w_H1, n * NH * C);
-        ws.Phi1 = f(w_Phi1, n * NLME * C);
-        ws.A1 = f(w_A1, n * NY * C);
-        ws.A1_adj = f(w_A1_adj, n * NY * C);
-        ws.direct = f(w_direct, n * C);
-        ws.dPhi1 = f(w_dPhi1, n * NLME * C);
-        ws.Wsrc = f(w_Wsrc, e * NH * C);
-        ws.H1_adj = f(w_H1_adj, n * NH * C);
-        ws.M0_adj = f(w_M0_adj, n * NH * C);
-        ws.A0_adj = f(w_A0_adj, n * NY * C);
-        ws.Phi0_adj = f(w_Phi0_adj, n * NY * C);
+        ws.erec = f(w_erec, te * ks->record_floats());
+        ws.Phi0 = f(w_Phi0, tn * NY * C);
+        ws.A0 = f(w_A0, tn * NY * C);
+        ws.M0 = f(w_M0, tn * NH * C);
+        ws.Phi1 = f(w_Phi1, tn * NLME * C);
+        ws.A1 = f(w_A1, tn * NY * C);
+        ws.A1_adj = f(w_A1_adj, tn * NY * C);
+        ws.dPhi1 = f(w_dPhi1, tn * NLME * C);
+        ws.Wsrc = f(w_Wsrc, te * NH * C);
+        ws.M0_adj = f(w_M0_adj, tn * NH * C);
+        ws.A0_adj = f(w_A0_adj, tn * NY * C);
+        ws.Phi0_adj = f(w_Phi0_adj, tn * NY * C);
+        ws.node_forces = static_cast<double*>(w_node_forces.ensure(te * 3 * sizeof(double)));
+        ws.H1 = f(g_H1, n * NH * C);
+        ws.H1_adj = f(g_H1_adj, n * NH * C);
+        ws.xaff = f(g_xaff, n * C);
+        ws.direct = f(g_direct, n * C);
         ws.node_energies = static_cast<double*>(d_node_energies.ensure(n * sizeof(double)));
-        ws.node_forces = static_cast<double*>(d_node_forces.ensure(e * 3 * sizeof(double)));
         d_atom_forces.ensure(n * 3 * sizeof(double));
+        d_virial.ensure(9 * sizeof(double));
         d_stress.ensure(9 * sizeof(double));
         d_stress_partial.ensure(static_cast<std::size_t>(stress_blocks) * 9 * sizeof(double));
         d_total.ensure(sizeof(double));
-        d_xyz.ensure(e * 3 * sizeof(double));
-        d_r.ensure(e * sizeof(double));
-        d_erec.ensure(e * ks->record_floats() * sizeof(float));
+        // xyz/r: the whole graph when host edge vectors are given, else one tile
+        const std::size_t xe = has_fractional ? te : e;
+        d_xyz.ensure(xe * 3 * sizeof(double));
+        d_r.ensure(xe * sizeof(double));
         d_invalid.ensure(sizeof(int));
         d_positions.ensure(n * 3 * sizeof(double));
         d_disp.ensure(n * 3 * sizeof(double));
@@ -401,7 +532,7 @@ struct Evaluator {
                 throw std::invalid_argument("node type index is out of range");
     }
 
-    // receiver CSR on the device -> schedule, plans, workspace, token
+    // receiver CSR on the device -> schedule, tiles, plans, workspace, token
     std::uint64_t finish_graph() {
         d_receivers.ensure(std::max<std::int64_t>(E, 1) * sizeof(int));
         d_soff.ensure((N + 1) * sizeof(int));
@@ -409,7 +540,12 @@ struct Evaluator {
         d_counts.ensure(std::max(N, 1) * sizeof(int));
         launch_graph_schedule(N, E, d_offsets.as<int>(), d_neigh.as<int>(), d_receivers.as<int>(), d_soff.as<int>(),
                               d_sedges.as<int>(), d_counts.as<int>(), stream);
-        build_plans();
+        if (static_cast<int>(h_offsets.size()) != N + 1) {
+            h_offsets.resize(N + 1);
+            SMX_HIP(hipMemcpy(h_offsets.data(), d_offsets.as<int>(), sizeof(int) * (N + 1), hipMemcpyDeviceToHost));
+        }
+        choose_plan();
+        build_tiles();
         ensure_workspace();
         SMX_HIP(hipStreamSynchronize(stream));
         evaluated = false;
@@ -440,6 +576,7 @@ struct Evaluator {
         N = n;
         E = num_edges;
         h_node_types.assign(node_types, node_types + n);
+        h_offsets = off;
         upload(d_node_types, h_node_types, stream);
         upload(d_offsets, off, stream);
         upload(d_neigh, std::vector<int>(neigh, neigh + E), stream);
@@ -450,8 +587,7 @@ struct Evaluator {
 
     std::uint64_t prepare_graph_device(int n, const int* node_types, const int* num_neigh, std::int64_t num_edges,
                                        const int* neigh, const int* neigh_types) {
-        // The CSR is validated on the host copy: the reference's device path
-        // trusts its LAMMPS caller, this one checks like the host path.
+        // The CSR is validated on a host copy, like the host path.
         std::vector<int> t(n), nn(n), nb(num_edges), nt(num_edges);
         if (n > 0) {
             SMX_HIP(hipMemcpy(t.data(), node_types, sizeof(int) * n, hipMemcpyDeviceToHost));
@@ -469,35 +605,41 @@ struct Evaluator {
                                                             double cutoff) {
         if (n < 0) throw std::invalid_argument("num_nodes must be non-negative");
         validate_types(n, node_types);
+        // release the previous graph's edge arrays first (capacity runs)
+        for (DevBuf* b : {&d_neigh, &d_neigh_types, &d_receivers, &d_sedges, &d_images}) b->release();
         NeighborResult nr;
-        build_neighbor_list(n, positions, cell_, inv_, cutoff, nr, stream);
         struct Guard {
             NeighborResult& r;
             ~Guard() {
                 for (void* p : {static_cast<void*>(r.num_neigh), static_cast<void*>(r.offsets),
-                                static_cast<void*>(r.sources), static_cast<void*>(r.shifts),
+                                static_cast<void*>(r.sources), static_cast<void*>(r.images),
+                                static_cast<void*>(r.wfrac), static_cast<void*>(r.shifts),
                                 static_cast<void*>(r.fractional_xyz)})
                     if (p) (void)hipFree(p);
             }
         } guard{nr};
+        build_neighbor_list(n, positions, cell_, inv_, cutoff, false, nr, stream);
         N = n;
         E = nr.num_edges;
         h_node_types.assign(node_types, node_types + n);
         upload(d_node_types, h_node_types, stream);
-        int* off = static_cast<int*>(d_offsets.ensure((N + 1) * sizeof(int)));
-        SMX_HIP(hipMemcpyAsync(off, nr.offsets, (N + 1) * sizeof(int), hipMemcpyDeviceToDevice, stream));
-        int* nb = static_cast<int*>(d_neigh.ensure(std::max<std::int64_t>(E, 1) * sizeof(int)));
-        if (E > 0) SMX_HIP(hipMemcpyAsync(nb, nr.sources, E * sizeof(int), hipMemcpyDeviceToDevice, stream));
+        d_offsets.adopt(nr.offsets, (N + 1) * sizeof(int));
+        nr.offsets = nullptr;
+        d_neigh.adopt(nr.sources, std::max<std::int64_t>(E, 1) * sizeof(int));
+        nr.sources = nullptr;
+        d_images.adopt(nr.images, std::max<std::int64_t>(E, 1) * sizeof(std::uint32_t));
+        nr.images = nullptr;
+        d_wfrac.adopt(nr.wfrac, std::max(N, 1) * 3 * sizeof(double));
+        nr.wfrac = nullptr;
         int* nt = static_cast<int*>(d_neigh_types.ensure(std::max<std::int64_t>(E, 1) * sizeof(int)));
-        launch_gather_types(E, nb, d_node_types.as<int>(), nt, stream);
-        double* fx = static_cast<double*>(d_fxyz.ensure(std::max<std::int64_t>(E, 1) * 3 * sizeof(double)));
-        if (E > 0)
-            SMX_HIP(hipMemcpyAsync(fx, nr.fractional_xyz, E * 3 * sizeof(double), hipMemcpyDeviceToDevice, stream));
+        launch_gather_types(E, d_neigh.as<int>(), d_node_types.as<int>(), nt, stream);
         double* rp = static_cast<double*>(d_ref_positions.ensure(std::max(N, 1) * 3 * sizeof(double)));
         if (N > 0) SMX_HIP(hipMemcpyAsync(rp, positions, N * 3 * sizeof(double), hipMemcpyHostToDevice, stream));
+        SMX_HIP(hipStreamSynchronize(stream));
         std::memcpy(cell, cell_, sizeof(cell));
         std::memcpy(inv_cell, inv_, sizeof(inv_cell));
         has_fractional = true;
+        h_offsets.clear();
         const std::uint64_t token = finish_graph();
         return {token, E};
     }
@@ -508,15 +650,77 @@ struct Evaluator {
     }
 
     // ----------------------------------------------------------------- calls
-    void evaluate_edges() {
+    const double* tile_xyz(const TileView& t) const {
+        return xyz_host ? d_xyz.as<double>() + 3 * t.e0 : d_xyz.as<double>();
+    }
+    const double* tile_r(const TileView& t) const { return xyz_host ? d_r.as<double>() + t.e0 : d_r.as<double>(); }
+
+    // xyz, r and per-edge records of one tile
+    void tile_geometry(const TileView& t, const double* positions) {
+        LaunchTimer* tm = timer.get();
+        if (!xyz_host) {
+            if (tm) tm->begin("edge_geometry", stream);
+            launch_edge_xyz(t.e0, t.ne, cell, d_receivers.as<int>(), d_neigh.as<int>(), d_wfrac.as<double>(),
+                            d_images.as<std::uint32_t>(), d_disp.as<double>(), hm.r_cut, d_xyz.as<double>(),
+                            d_r.as<double>(), d_invalid.as<int>(), stream);
+            if (tm) tm->end("edge_geometry", stream);
+        }
+        if (tm) tm->begin("edge_records", stream);
+        ks->edge_geometry(dm, t.ne, tile_xyz(t), tile_r(t), ws.erec, stream);
+        if (tm) tm->end("edge_records", stream);
+        (void)positions;
+    }
+
+    void zero_a1_if_needed() {
+        if (std::find(hm.num_e.begin(), hm.num_e.end(), 0) != hm.num_e.end())
+            launch_fill_zero(ws.A1, static_cast<std::size_t>(std::max(max_tile_nr, 1)) * hm.num_lm * hm.C, stream);
+    }
+
+    void evaluate(const double* positions) {
         const DeviceGraph g = view();
-        ks->edge_geometry(dm, E, d_xyz.as<double>(), d_r.as<double>(), d_erec.as<float>(), stream);
-        if (hm.num_e.end() != std::find(hm.num_e.begin(), hm.num_e.end(), 0))
-            SMX_HIP(hipMemsetAsync(ws.A1, 0, sizeof(float) * std::max(N, 1) * hm.num_lm * hm.C, stream));
-        LaunchTimer* t = timer.get();
-        ks->forward(dm, g, ws, plan_a0.view, plan_h1.view, plan_a1f.view, stream, t);
-        ks->reverse(dm, g, ws, plan_a0.view, plan_h1.view, plan_a1r.view, stream, t);
+        LaunchTimer* tm = timer.get();
+        zero_a1_if_needed();
+        if (!tiled) {
+            const TileView& t = tiles[0];
+            tile_geometry(t, positions);
+            ks->layer1_forward(dm, g, t, ws, true, stream, tm);
+            ks->layer2(dm, g, t, ws, stream, tm);
+            ks->source_adjoint_all(g, ws, stream, tm);
+            ks->layer1_reverse(dm, g, t, ws, true, stream, tm);
+            evaluated = true;
+            return;
+        }
+        // three sweeps over receiver tiles (graph-wide H1, H1 adjoint between them)
+        launch_fill_zero(ws.H1_adj, static_cast<std::size_t>(N) * hm.num_LM * hm.C, stream);
+        launch_fill_zero(d_atom_forces.as<double>(), static_cast<std::size_t>(N) * 3, stream);
+        launch_fill_zero(d_virial.as<double>(), 9, stream);
+        for (const auto& t : tiles) {
+            tile_geometry(t, positions);
+            ks->layer1_forward(dm, g, t, ws, true, stream, tm);
+        }
+        for (const auto& t : tiles) {
+            tile_geometry(t, positions);
+            ks->layer2(dm, g, t, ws, stream, tm);
+            ks->source_adjoint_tile(g, t, ws, stream, tm);
+            accumulate_tile_outputs(t);
+        }
+        for (const auto& t : tiles) {
+            tile_geometry(t, positions);
+            ks->layer1_forward(dm, g, t, ws, false, stream, tm);
+            ks->layer1_reverse(dm, g, t, ws, false, stream, tm);
+            accumulate_tile_outputs(t);
+        }
         evaluated = true;
+    }
+
+    void accumulate_tile_outputs(const TileView& t) {
+        LaunchTimer* tm = timer.get();
+        if (tm) tm->begin("tile_reductions", stream);
+        launch_tile_forces(t, d_offsets.as<int>(), d_soff.as<int>(), d_sedges.as<int>(), ws.node_forces,
+                           d_atom_forces.as<double>(), stream);
+        launch_virial_accumulate(t.ne, ws.node_forces, tile_xyz(t), d_stress_partial.as<double>(), stress_blocks,
+                                 d_virial.as<double>(), stream);
+        if (tm) tm->end("tile_reductions", stream);
     }
 
     void finish_call(bool check_invalid) {
@@ -539,19 +743,16 @@ struct Evaluator {
         if (!on_device) {
             for (int i = 0; i < 3 * N; ++i)
                 if (!std::isfinite(positions[i])) throw std::invalid_argument("positions must be finite");
-            double* dp = static_cast<double*>(d_positions.ensure(std::max(N, 1) * 3 * sizeof(double)));
+            double* dp = d_positions.as<double>();
             if (N > 0) SMX_HIP(hipMemcpyAsync(dp, positions, N * 3 * sizeof(double), hipMemcpyHostToDevice, stream));
             pos = dp;
         }
-        SMX_HIP(hipMemsetAsync(d_invalid.as<int>(), 0, sizeof(int), stream));
-        {
-            if (timer) timer->begin("edge_geometry", stream);
-            launch_prepared_geometry(N, E, d_receivers.as<int>(), d_neigh.as<int>(), d_fxyz.as<double>(), cell,
-                                     inv_cell, d_ref_positions.as<double>(), pos, hm.r_cut, d_disp.as<double>(),
-                                     d_xyz.as<double>(), d_r.as<double>(), d_invalid.as<int>(), stream);
-            if (timer) timer->end("edge_geometry", stream);
-        }
-        evaluate_edges();
+        xyz_host = false;
+        launch_fill_zero(reinterpret_cast<float*>(d_invalid.as<int>()), 1, stream);
+        if (timer) timer->begin("displacements", stream);
+        launch_displacements(N, cell, inv_cell, d_ref_positions.as<double>(), pos, d_disp.as<double>(), stream);
+        if (timer) timer->end("displacements", stream);
+        evaluate(pos);
         finish_call(true);
     }
 
@@ -562,11 +763,15 @@ struct Evaluator {
                 !std::isfinite(xyz[3 * e + 2]))
                 throw std::invalid_argument("MACE graph has an invalid distance or displacement vector");
         }
+        // explicit edge vectors of the whole graph
+        d_xyz.ensure(std::max<std::int64_t>(E, 1) * 3 * sizeof(double));
+        d_r.ensure(std::max<std::int64_t>(E, 1) * sizeof(double));
+        xyz_host = true;
         if (E > 0) {
             SMX_HIP(hipMemcpyAsync(d_xyz.as<double>(), xyz, E * 3 * sizeof(double), hipMemcpyHostToDevice, stream));
             SMX_HIP(hipMemcpyAsync(d_r.as<double>(), r, E * sizeof(double), hipMemcpyHostToDevice, stream));
         }
-        evaluate_edges();
+        evaluate(nullptr);
         finish_call(false);
     }
 
@@ -588,7 +793,6 @@ struct Evaluator {
         g.receivers = d_receivers.as<int>();
         g.soff = d_soff.as<int>();
         g.sedges = d_sedges.as<int>();
-        g.erec = d_erec.as<float>();
         return g;
     }
 
@@ -599,8 +803,9 @@ struct Evaluator {
 
     void reduce_forces(std::uint64_t token, double* out) {
         require_evaluated(token);
-        launch_atom_forces(N, d_offsets.as<int>(), d_soff.as<int>(), d_sedges.as<int>(), ws.node_forces,
-                           d_atom_forces.as<double>(), stream);
+        if (!tiled)
+            launch_atom_forces(N, d_offsets.as<int>(), d_soff.as<int>(), d_sedges.as<int>(), ws.node_forces,
+                               d_atom_forces.as<double>(), stream);
         if (out) {
             if (N > 0)
                 SMX_HIP(hipMemcpyAsync(out, d_atom_forces.as<double>(), N * 3 * sizeof(double), hipMemcpyDeviceToHost,
@@ -612,8 +817,11 @@ struct Evaluator {
     void reduce_stress(std::uint64_t token, double volume, double* out) {
         require_evaluated(token);
         if (!(volume > 0.0) || !std::isfinite(volume)) throw std::invalid_argument("volume must be positive");
-        launch_stress(E, ws.node_forces, d_xyz.as<double>(), volume, d_stress_partial.as<double>(), stress_blocks,
-                      d_stress.as<double>(), stream);
+        if (!tiled)
+            launch_stress(E, ws.node_forces, d_xyz.as<double>(), volume, d_stress_partial.as<double>(), stress_blocks,
+                          d_stress.as<double>(), stream);
+        else
+            launch_scale9(d_virial.as<double>(), -1.0 / volume, d_stress.as<double>(), stream);
         if (out) {
             SMX_HIP(hipMemcpyAsync(out, d_stress.as<double>(), 9 * sizeof(double), hipMemcpyDeviceToHost, stream));
             SMX_HIP(hipStreamSynchronize(stream));
@@ -629,23 +837,36 @@ struct Evaluator {
         }
     }
 
+    const double* node_forces_device() const {
+        if (tiled) throw std::logic_error("directed edge forces are not retained by the tiled execution plan");
+        return ws.node_forces;
+    }
+
+    std::string plan_description() const {
+        std::string s = tiled ? "direct-tiled" : "direct";
+        s += " tiles=" + std::to_string(tiles.size()) + " max_tile_receivers=" + std::to_string(max_tile_nr) +
+             " max_tile_edges=" + std::to_string(max_tile_ne);
+        return s;
+    }
+
     std::int64_t stage(const std::string& name, float* out, std::int64_t capacity) {
-        const std::int64_t n = N, C = hm.C, NY = hm.num_lm, NH = hm.num_LM, NLME = hm.num_lme;
+        const std::int64_t n = tiled ? max_tile_nr : N, C = hm.C, NY = hm.num_lm, NH = hm.num_LM,
+                           NLME = hm.num_lme;
         const float* src = nullptr;
         std::int64_t count = 0;
         if (name == "A0") src = ws.A0, count = n * NY * C;
         else if (name == "Phi0") src = ws.Phi0, count = n * NY * C;
         else if (name == "M0") src = ws.M0, count = n * NH * C;
-        else if (name == "H1") src = ws.H1, count = n * NH * C;
+        else if (name == "H1") src = ws.H1, count = static_cast<std::int64_t>(N) * NH * C;
         else if (name == "Phi1") src = ws.Phi1, count = n * NLME * C;
         else if (name == "A1") src = ws.A1, count = n * NY * C;
         else if (name == "A1_adj") src = ws.A1_adj, count = n * NY * C;
         else if (name == "dPhi1") src = ws.dPhi1, count = n * NLME * C;
-        else if (name == "H1_adj") src = ws.H1_adj, count = n * NH * C;
+        else if (name == "H1_adj") src = ws.H1_adj, count = static_cast<std::int64_t>(N) * NH * C;
         else if (name == "M0_adj") src = ws.M0_adj, count = n * NH * C;
         else if (name == "A0_adj") src = ws.A0_adj, count = n * NY * C;
-        else if (name == "direct") src = ws.direct, count = n * C;
-        else if (name == "edge_records") src = d_erec.as<float>(), count = E * ks->record_floats();
+        else if (name == "direct") src = ws.direct, count = static_cast<std::int64_t>(N) * C;
+        else if (name == "edge_records") src = ws.erec, count = (tiled ? max_tile_ne : E) * ks->record_floats();
         else throw std::invalid_argument("unknown stage '" + name + "'");
         if (out && capacity >= count && count > 0) {
             SMX_HIP(hipMemcpyAsync(out, src, count * sizeof(float), hipMemcpyDeviceToHost, stream));
@@ -797,6 +1018,26 @@ int32_t smx_prepare_periodic_factorized_graph(SmxEvaluator* ev, int32_t num_node
     });
 }
 
+int32_t smx_set_execution_plan(SmxEvaluator* ev, const char* profile, int32_t tile_receivers) {
+    return guarded([&] {
+        auto& e = E(ev);
+        const std::string p = profile ? profile : "auto";
+        if (p != "auto" && p != "speed" && p != "capacity")
+            throw std::invalid_argument("execution profile must be 'auto', 'speed' or 'capacity'");
+        if (tile_receivers < 0) throw std::invalid_argument("tile_receivers must be non-negative");
+        e.profile = p;
+        if (tile_receivers > 0) e.tile_limit = tile_receivers;
+    });
+}
+
+int32_t smx_execution_plan(SmxEvaluator* ev, char* out, int64_t capacity) {
+    return guarded([&] {
+        const std::string d = E(ev).plan_description();
+        if (!out || capacity < static_cast<int64_t>(d.size()) + 1) throw std::invalid_argument("buffer too small");
+        std::memcpy(out, d.c_str(), d.size() + 1);
+    });
+}
+
 int32_t smx_update_factorized_cell(SmxEvaluator* ev, uint64_t generation, const double* cell,
                                    const double* inverse_cell) {
     return guarded([&] {
@@ -864,8 +1105,8 @@ int32_t smx_node_forces(SmxEvaluator* ev, double* out, int64_t capacity) {
         auto& e = E(ev);
         if (!out || capacity < 3 * e.E) throw std::invalid_argument("buffer too small");
         if (!e.evaluated) throw std::logic_error("no evaluation has run");
-        if (e.E > 0)
-            SMX_HIP(hipMemcpyAsync(out, e.ws.node_forces, 3 * e.E * sizeof(double), hipMemcpyDeviceToHost, e.stream));
+        const double* nf = e.node_forces_device();
+        if (e.E > 0) SMX_HIP(hipMemcpyAsync(out, nf, 3 * e.E * sizeof(double), hipMemcpyDeviceToHost, e.stream));
         SMX_HIP(hipStreamSynchronize(e.stream));
     });
 }
@@ -882,7 +1123,7 @@ int32_t smx_device_outputs(SmxEvaluator* ev, SmxDeviceOutputs* out) {
         out->num_nodes = e.N;
         out->num_edges = e.E;
         out->node_energies = e.ws.node_energies;
-        out->node_forces = e.ws.node_forces;
+        out->node_forces = e.tiled ? nullptr : e.ws.node_forces;
         out->atom_forces = e.d_atom_forces.as<double>();
         out->stress = e.d_stress.as<double>();
         out->total_energy = e.d_total.as<double>();
@@ -951,13 +1192,14 @@ int32_t smx_neighbor_list(int32_t num_nodes, const double* positions, const doub
         smx::NeighborResult nr;
         auto cleanup = [&]() {
             for (void* p : {static_cast<void*>(nr.num_neigh), static_cast<void*>(nr.offsets),
-                            static_cast<void*>(nr.sources), static_cast<void*>(nr.shifts),
+                            static_cast<void*>(nr.sources), static_cast<void*>(nr.images),
+                            static_cast<void*>(nr.wfrac), static_cast<void*>(nr.shifts),
                             static_cast<void*>(nr.fractional_xyz)})
                 if (p) (void)hipFree(p);
             (void)hipStreamDestroy(s);
         };
         try {
-            smx::build_neighbor_list(num_nodes, positions, cell, inverse_cell, cutoff, nr, s);
+            smx::build_neighbor_list(num_nodes, positions, cell, inverse_cell, cutoff, true, nr, s);
             const std::int64_t Ec = nr.num_edges;
             if (sources) {
                 if (Ec > *num_edges) throw std::invalid_argument("edge buffers are smaller than the edge count");

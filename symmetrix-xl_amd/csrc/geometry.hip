@@ -175,7 +175,8 @@ __global__ void k_neighbor_visit(int N, Mat3 cell, BinGrid g, double cut2, const
                                  const int* __restrict__ abin, const long long* __restrict__ boff,
                                  const int* __restrict__ batoms, int* __restrict__ counts,
                                  const long long* __restrict__ eoff, int* __restrict__ sources,
-                                 int* __restrict__ shifts, double* __restrict__ fxyz) {
+                                 std::uint32_t* __restrict__ images, int* __restrict__ shifts,
+                                 double* __restrict__ fxyz) {
     const int rcv = blockIdx.x * blockDim.x + threadIdx.x;
     if (rcv >= N) return;
     const int rb = abin[rcv];
@@ -202,9 +203,14 @@ __global__ void k_neighbor_visit(int N, Mat3 cell, BinGrid g, double cut2, const
                     if (d2 > cut2) continue;
                     if (FILL) {
                         sources[e] = src;
-                        for (int ax = 0; ax < 3; ++ax) {
-                            shifts[3 * e + ax] = image[ax] - wrap[3 * src + ax] + wrap[3 * rcv + ax];
-                            fxyz[3 * e + ax] = wfrac[3 * src + ax] - wfrac[3 * rcv + ax] + image[ax];
+                        images[e] = (static_cast<std::uint32_t>(image[0]) & 0xffu) |
+                                    ((static_cast<std::uint32_t>(image[1]) & 0xffu) << 8) |
+                                    ((static_cast<std::uint32_t>(image[2]) & 0xffu) << 16);
+                        if (shifts) {
+                            for (int ax = 0; ax < 3; ++ax) {
+                                shifts[3 * e + ax] = image[ax] - wrap[3 * src + ax] + wrap[3 * rcv + ax];
+                                fxyz[3 * e + ax] = wfrac[3 * src + ax] - wfrac[3 * rcv + ax] + image[ax];
+                            }
                         }
                         ++e;
                     }
@@ -272,31 +278,71 @@ __global__ void k_displacements(int N, Mat3 cell, Mat3 inv, const double* __rest
     }
 }
 
-__global__ void k_edge_xyz(long long E, Mat3 cell, const int* __restrict__ receivers, const int* __restrict__ sources,
-                           const double* __restrict__ fxyz, const double* __restrict__ disp, double cutoff,
-                           double* __restrict__ xyz, double* __restrict__ r, int* __restrict__ invalid) {
-    const long long e = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (e >= E) return;
+__device__ __forceinline__ int image_component(std::uint32_t packed, int ax) {
+    return static_cast<int>(static_cast<std::int8_t>((packed >> (8 * ax)) & 0xffu));
+}
+
+// Edges [e0, e0+ne): the reference fractional edge vector is rebuilt exactly
+// as the neighbour list formed it (wfrac[src] - wfrac[rcv] + image), then
+// xyz = frac . cell + disp[src] - disp[rcv]; r clamped to the cutoff.
+__global__ void k_edge_xyz(long long e0, long long ne, Mat3 cell, const int* __restrict__ receivers,
+                           const int* __restrict__ sources, const double* __restrict__ wfrac,
+                           const std::uint32_t* __restrict__ images, const double* __restrict__ disp,
+                           double cutoff, double* __restrict__ xyz, double* __restrict__ r,
+                           int* __restrict__ invalid) {
+    const long long le = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (le >= ne) return;
+    const long long e = e0 + le;
     const int rc = receivers[e], sc = sources[e];
+    const std::uint32_t img = images[e];
+    double fr[3];
+    for (int ax = 0; ax < 3; ++ax) fr[ax] = wfrac[3 * sc + ax] - wfrac[3 * rc + ax] + image_component(img, ax);
     double vec[3], d2 = 0.0;
     for (int c = 0; c < 3; ++c) {
         double ref = 0.0;
-        for (int lat = 0; lat < 3; ++lat) ref += fxyz[3 * e + lat] * cell.v[3 * lat + c];
+        for (int lat = 0; lat < 3; ++lat) ref += fr[lat] * cell.v[3 * lat + c];
         vec[c] = ref + disp[3 * sc + c] - disp[3 * rc + c];
         d2 += vec[c] * vec[c];
     }
     if (!isfinite(d2) || !(d2 > 0.0)) {
         atomicAdd(invalid, 1);
-        xyz[3 * e] = cutoff;
-        xyz[3 * e + 1] = 0.0;
-        xyz[3 * e + 2] = 0.0;
-        r[e] = cutoff;
+        xyz[3 * le] = cutoff;
+        xyz[3 * le + 1] = 0.0;
+        xyz[3 * le + 2] = 0.0;
+        r[le] = cutoff;
         return;
     }
     const double dist = sqrt(d2);
     const double scale = dist >= cutoff ? cutoff / dist : 1.0;
-    for (int c = 0; c < 3; ++c) xyz[3 * e + c] = scale * vec[c];
-    r[e] = dist >= cutoff ? cutoff : dist;
+    for (int c = 0; c < 3; ++c) xyz[3 * le + c] = scale * vec[c];
+    r[le] = dist >= cutoff ? cutoff : dist;
+}
+
+// Touched-source sets of a tile: mark, count per 32-bit word, compact.
+__global__ void k_mark_sources(long long e0, long long ne, const int* __restrict__ sources,
+                               std::uint32_t* __restrict__ bitmap) {
+    const long long le = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (le >= ne) return;
+    const int src = sources[e0 + le];
+    atomicOr(&bitmap[src >> 5], 1u << (src & 31));
+}
+
+__global__ void k_word_counts(int words, const std::uint32_t* __restrict__ bitmap, int* __restrict__ counts) {
+    const int w = blockIdx.x * blockDim.x + threadIdx.x;
+    if (w < words) counts[w] = __popc(bitmap[w]);
+}
+
+__global__ void k_compact_bits(int words, const std::uint32_t* __restrict__ bitmap,
+                               const long long* __restrict__ word_off, int* __restrict__ out) {
+    const int w = blockIdx.x * blockDim.x + threadIdx.x;
+    if (w >= words) return;
+    std::uint32_t b = bitmap[w];
+    long long o = word_off[w];
+    while (b) {
+        const int bit = __ffs(b) - 1;
+        out[o++] = (w << 5) + bit;
+        b &= b - 1u;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -441,7 +487,7 @@ std::int64_t device_exclusive_scan(const int* in, long long* out, int n, hipStre
 }
 
 void build_neighbor_list(int N, const double* positions_host, const double* cell_host, const double* inv_host,
-                         double cutoff, NeighborResult& out, hipStream_t s) {
+                         double cutoff, bool with_shifts, NeighborResult& out, hipStream_t s) {
     if (!std::isfinite(cutoff) || !(cutoff > 0.0)) throw std::invalid_argument("neighbor cutoff must be positive");
     if (N < 0) throw std::invalid_argument("negative atom count");
     for (int i = 0; i < 3 * N; ++i)
@@ -465,12 +511,16 @@ void build_neighbor_list(int N, const double* positions_host, const double* cell
     }
     const long long nb_ll = static_cast<long long>(g.bins[0]) * g.bins[1] * g.bins[2];
     if (nb_ll > INT_MAX / 2) throw std::invalid_argument("neighbor bin grid is too large");
+    // images are stored as signed bytes: |image| <= reach + 1
+    for (int ax = 0; ax < 3; ++ax)
+        if (g.reach[ax] + 1 > 127) throw std::invalid_argument("cell is too small for the cutoff (image range)");
     const int nb = static_cast<int>(nb_ll);
     const Mat3 cell = mat3(cell_host), inv = mat3(inv_host);
     const double cut2 = cutoff * cutoff;
 
     double* d_pos = dev_alloc<double>(3 * static_cast<std::size_t>(N));
     double* wfrac = dev_alloc<double>(3 * static_cast<std::size_t>(N));
+    out.wfrac = wfrac;  // kept: the geometry reference of the graph
     double* wpos = dev_alloc<double>(3 * static_cast<std::size_t>(N));
     int* wrap = dev_alloc<int>(3 * static_cast<std::size_t>(N));
     int* abin = dev_alloc<int>(N);
@@ -481,7 +531,7 @@ void build_neighbor_list(int N, const double* positions_host, const double* cell
     int* counts = dev_alloc<int>(N);
     long long* eoff = dev_alloc<long long>(N + 1);
     auto release = [&]() {
-        for (void* p : {static_cast<void*>(d_pos), static_cast<void*>(wfrac), static_cast<void*>(wpos),
+        for (void* p : {static_cast<void*>(d_pos), static_cast<void*>(wpos),
                         static_cast<void*>(wrap), static_cast<void*>(abin), static_cast<void*>(bsize),
                         static_cast<void*>(boff), static_cast<void*>(cursor), static_cast<void*>(batoms),
                         static_cast<void*>(counts), static_cast<void*>(eoff)})
@@ -506,7 +556,7 @@ void build_neighbor_list(int N, const double* positions_host, const double* cell
         SMX_LAUNCH_CHECK("neighbor_sort_bins");
         if (N > 0) {
             k_neighbor_visit<false><<<blocks_for(N, 128), 128, 0, s>>>(N, cell, g, cut2, wfrac, wpos, wrap, abin, boff, batoms, counts,
-                                                       nullptr, nullptr, nullptr, nullptr);
+                                                       nullptr, nullptr, nullptr, nullptr, nullptr);
             SMX_LAUNCH_CHECK("neighbor_count");
         }
         const long long E = device_exclusive_scan(counts, eoff, N, s);
@@ -515,14 +565,18 @@ void build_neighbor_list(int N, const double* positions_host, const double* cell
         out.num_neigh = dev_alloc<int>(N);
         out.offsets = dev_alloc<int>(N + 1);
         out.sources = dev_alloc<int>(E);
-        out.shifts = dev_alloc<int>(3 * static_cast<std::size_t>(E));
-        out.fractional_xyz = dev_alloc<double>(3 * static_cast<std::size_t>(E));
+        out.images = dev_alloc<std::uint32_t>(E);
+        if (with_shifts) {
+            out.shifts = dev_alloc<int>(3 * static_cast<std::size_t>(E));
+            out.fractional_xyz = dev_alloc<double>(3 * static_cast<std::size_t>(E));
+        }
         SMX_HIP(hipMemcpyAsync(out.num_neigh, counts, sizeof(int) * N, hipMemcpyDeviceToDevice, s));
         k_copy_i64_i32_plus<<<blocks_for(N + 1, 256), 256, 0, s>>>(eoff, out.offsets, N);
         SMX_LAUNCH_CHECK("neighbor_offsets");
         if (N > 0 && E > 0) {
             k_neighbor_visit<true><<<blocks_for(N, 128), 128, 0, s>>>(N, cell, g, cut2, wfrac, wpos, wrap, abin, boff, batoms, nullptr,
-                                                      eoff, out.sources, out.shifts, out.fractional_xyz);
+                                                      eoff, out.sources, out.images, out.shifts,
+                                                      out.fractional_xyz);
             SMX_LAUNCH_CHECK("neighbor_fill");
         }
         SMX_HIP(hipStreamSynchronize(s));
@@ -571,20 +625,46 @@ void launch_gather_types(std::int64_t E, const int* sources, const int* node_typ
     SMX_LAUNCH_CHECK("gather_types");
 }
 
-void launch_prepared_geometry(int N, std::int64_t E, const int* receivers, const int* sources,
-                              const double* fractional_xyz, const double* cell, const double* inv_cell,
-                              const double* reference_positions, const double* positions, double cutoff, double* disp,
-                              double* xyz, double* r, int* invalid, hipStream_t s) {
-    const Mat3 c = mat3(cell), iv = mat3(inv_cell);
-    if (N > 0) {
-        k_displacements<<<blocks_for(N, 256), 256, 0, s>>>(N, c, iv, reference_positions, positions, disp);
-        SMX_LAUNCH_CHECK("geometry_displacements");
+void launch_displacements(int N, const double* cell, const double* inv_cell, const double* reference_positions,
+                          const double* positions, double* disp, hipStream_t s) {
+    if (N == 0) return;
+    k_displacements<<<blocks_for(N, 256), 256, 0, s>>>(N, mat3(cell), mat3(inv_cell), reference_positions, positions,
+                                                       disp);
+    SMX_LAUNCH_CHECK("geometry_displacements");
+}
+
+void launch_edge_xyz(std::int64_t e0, std::int64_t ne, const double* cell, const int* receivers, const int* sources,
+                     const double* wfrac, const std::uint32_t* images, const double* disp, double cutoff,
+                     double* xyz, double* r, int* invalid, hipStream_t s) {
+    if (ne == 0) return;
+    k_edge_xyz<<<blocks_for(ne, 256), 256, 0, s>>>(e0, ne, mat3(cell), receivers, sources, wfrac, images, disp,
+                                                   cutoff, xyz, r, invalid);
+    SMX_LAUNCH_CHECK("geometry_edges");
+}
+
+int build_touched_sources(int N, std::int64_t e0, std::int64_t ne, const int* sources, std::uint32_t* bitmap,
+                          int* word_counts, int* out, hipStream_t s) {
+    const int words = N / 32 + 1;
+    SMX_HIP(hipMemsetAsync(bitmap, 0, sizeof(std::uint32_t) * words, s));
+    if (ne > 0) {
+        k_mark_sources<<<blocks_for(ne, 256), 256, 0, s>>>(e0, ne, sources, bitmap);
+        SMX_LAUNCH_CHECK("touched_mark");
     }
-    if (E > 0) {
-        k_edge_xyz<<<blocks_for(E, 256), 256, 0, s>>>(E, c, receivers, sources, fractional_xyz, disp, cutoff, xyz, r,
-                                                      invalid);
-        SMX_LAUNCH_CHECK("geometry_edges");
+    k_word_counts<<<blocks_for(words, 256), 256, 0, s>>>(words, bitmap, word_counts);
+    SMX_LAUNCH_CHECK("touched_count");
+    long long* off = dev_alloc<long long>(words + 1);
+    long long total = 0;
+    try {
+        total = device_exclusive_scan(word_counts, off, words, s);
+        k_compact_bits<<<blocks_for(words, 256), 256, 0, s>>>(words, bitmap, off, out);
+        SMX_LAUNCH_CHECK("touched_compact");
+        SMX_HIP(hipStreamSynchronize(s));
+    } catch (...) {
+        (void)hipFree(off);
+        throw;
     }
+    SMX_HIP(hipFree(off));
+    return static_cast<int>(total);
 }
 
 void geometry_records(int l_max, std::int64_t E, const double* xyz, const double* r, double r_cut, float x0, float h,

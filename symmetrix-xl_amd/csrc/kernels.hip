@@ -62,19 +62,21 @@ __device__ __forceinline__ double block_sum(double v, double* sbuf) {
 // Layer 1: Phi0[i,lm,k] = sum_j R0_{l,k}(r_ij) Y_lm(ij) H0[type_j,k]
 // ---------------------------------------------------------------------------
 template <int C, int LMAX>
-__global__ __launch_bounds__(C) void k_r0_forward(const int* __restrict__ offsets, const int* __restrict__ neigh_types,
-                                                  const float* __restrict__ erec, const float4* __restrict__ R0c,
-                                                  const float* __restrict__ H0, float* __restrict__ Phi0) {
+__global__ __launch_bounds__(C) void k_r0_forward(int r0, long long e0, const int* __restrict__ offsets,
+                                                  const int* __restrict__ neigh_types, const float* __restrict__ erec,
+                                                  const float4* __restrict__ R0c, const float* __restrict__ H0,
+                                                  float* __restrict__ Phi0) {
     using S = Shape<LMAX, 0>;
     constexpr int NY = S::NY, NF = (LMAX + 1) * C;
-    const int i = xcd_remap(blockIdx.x, gridDim.x);
+    const int li = xcd_remap(blockIdx.x, gridDim.x);
+    const int i = r0 + li;
     const int k = threadIdx.x;
     float acc[NY];
 #pragma unroll
     for (int v = 0; v < NY; ++v) acc[v] = 0.0f;
-    const int e0 = offsets[i], e1 = offsets[i + 1];
-    for (int e = e0; e < e1; ++e) {
-        const float* rec = erec + static_cast<std::size_t>(e) * S::REC;
+    const int ea = offsets[i], eb = offsets[i + 1];
+    for (int e = ea; e < eb; ++e) {
+        const float* rec = erec + static_cast<std::size_t>(e - e0) * S::REC;
         if (!edge_active(rec)) continue;
         const float x = rec[0];
         const int iv = __float_as_int(rec[1]);
@@ -91,7 +93,7 @@ __global__ __launch_bounds__(C) void k_r0_forward(const int* __restrict__ offset
         });
     }
 #pragma unroll
-    for (int v = 0; v < NY; ++v) Phi0[(static_cast<std::size_t>(i) * NY + v) * C + k] = acc[v];
+    for (int v = 0; v < NY; ++v) Phi0[(static_cast<std::size_t>(li) * NY + v) * C + k] = acc[v];
 }
 
 // Per-edge directed forces: per-lane partials (fx,fy,fz) are summed over the
@@ -138,25 +140,26 @@ struct EdgeForceSink {
 constexpr int kForceChunk = 64;
 
 // Layer-1 reverse: node_forces[e] -= sum_k sum_lm Phi0_adj[i,lm,k] H0 (u dR Y + R dY)
-template <int C, int LMAX>
-__global__ __launch_bounds__(C) void k_r0_reverse(const int* __restrict__ offsets, const int* __restrict__ neigh_types,
-                                                  const float* __restrict__ erec, const float4* __restrict__ R0c,
-                                                  const float* __restrict__ H0, const float* __restrict__ Phi0_adj,
-                                                  double* __restrict__ node_forces) {
+template <int C, int LMAX, bool ACCUMULATE>
+__global__ __launch_bounds__(C) void k_r0_reverse(int r0, long long e0, const int* __restrict__ offsets,
+                                                  const int* __restrict__ neigh_types, const float* __restrict__ erec,
+                                                  const float4* __restrict__ R0c, const float* __restrict__ H0,
+                                                  const float* __restrict__ Phi0_adj, double* __restrict__ node_forces) {
     using S = Shape<LMAX, 0>;
     constexpr int NY = S::NY, NF = (LMAX + 1) * C;
     __shared__ float part[Lanes<C>::NW][kForceChunk][3];
     EdgeForceSink<C, kForceChunk> sink{part};
-    const int i = xcd_remap(blockIdx.x, gridDim.x);
+    const int li = xcd_remap(blockIdx.x, gridDim.x);
+    const int i = r0 + li;
     const int k = threadIdx.x;
     float padj[NY];
 #pragma unroll
-    for (int v = 0; v < NY; ++v) padj[v] = Phi0_adj[(static_cast<std::size_t>(i) * NY + v) * C + k];
-    const int e0 = offsets[i], e1 = offsets[i + 1];
-    for (int c0 = e0; c0 < e1; c0 += kForceChunk) {
-        const int c1 = min(c0 + kForceChunk, e1);
+    for (int v = 0; v < NY; ++v) padj[v] = Phi0_adj[(static_cast<std::size_t>(li) * NY + v) * C + k];
+    const int ea = offsets[i], eb = offsets[i + 1];
+    for (int c0 = ea; c0 < eb; c0 += kForceChunk) {
+        const int c1 = min(c0 + kForceChunk, eb);
         for (int e = c0; e < c1; ++e) {
-            const float* rec = erec + static_cast<std::size_t>(e) * S::REC;
+            const float* rec = erec + static_cast<std::size_t>(e - e0) * S::REC;
             if (!edge_active(rec)) {
                 sink.zero(e - c0);
                 continue;
@@ -185,7 +188,7 @@ __global__ __launch_bounds__(C) void k_r0_reverse(const int* __restrict__ offset
             const float u0 = rec[S::REC_U], u1 = rec[S::REC_U + 1], u2 = rec[S::REC_U + 2];
             sink.put(e - c0, u0 * a + b0, u1 * a + b1, u2 * a + b2);
         }
-        sink.template flush<true>(c0, c1 - c0, node_forces);
+        sink.template flush<ACCUMULATE>(static_cast<int>(c0 - e0), c1 - c0, node_forces);
     }
 }
 
@@ -194,20 +197,21 @@ __global__ __launch_bounds__(C) void k_r0_reverse(const int* __restrict__ offset
 // Phi1[i,lme,k] = sum CG rows (dense per-path coupling blocks).
 // ---------------------------------------------------------------------------
 template <int C, int LMAX, int LMAXH>
-__global__ __launch_bounds__(C) void k_r1_forward(const int* __restrict__ offsets, const int* __restrict__ neigh,
-                                                  const float* __restrict__ erec, const float4* __restrict__ R1c,
-                                                  const float* __restrict__ H1, const float* __restrict__ cg,
-                                                  float* __restrict__ Phi1) {
+__global__ __launch_bounds__(C) void k_r1_forward(int r0, long long e0, const int* __restrict__ offsets,
+                                                  const int* __restrict__ neigh, const float* __restrict__ erec,
+                                                  const float4* __restrict__ R1c, const float* __restrict__ H1,
+                                                  const float* __restrict__ cg, float* __restrict__ Phi1) {
     using S = Shape<LMAX, LMAXH>;
     constexpr int NH = S::NH, NF = S::P * C;
-    const int i = xcd_remap(blockIdx.x, gridDim.x);
+    const int li = xcd_remap(blockIdx.x, gridDim.x);
+    const int i = r0 + li;
     const int k = threadIdx.x;
     float rows[S::NROWS];
 #pragma unroll
     for (int r = 0; r < S::NROWS; ++r) rows[r] = 0.0f;
-    const int e0 = offsets[i], e1 = offsets[i + 1];
-    for (int e = e0; e < e1; ++e) {
-        const float* rec = erec + static_cast<std::size_t>(e) * S::REC;
+    const int ea = offsets[i], eb = offsets[i + 1];
+    for (int e = ea; e < eb; ++e) {
+        const float* rec = erec + static_cast<std::size_t>(e - e0) * S::REC;
         if (!edge_active(rec)) continue;
         const float x = rec[0];
         const int iv = __float_as_int(rec[1]);
@@ -248,7 +252,7 @@ __global__ __launch_bounds__(C) void k_r1_forward(const int* __restrict__ offset
         });
     });
 #pragma unroll
-    for (int q = 0; q < S::NLME; ++q) Phi1[(static_cast<std::size_t>(i) * S::NLME + q) * C + k] = out[q];
+    for (int q = 0; q < S::NLME; ++q) Phi1[(static_cast<std::size_t>(li) * S::NLME + q) * C + k] = out[q];
 }
 
 // Fused R1 reverse, receiver-owned: per edge the directed force
@@ -257,22 +261,23 @@ __global__ __launch_bounds__(C) void k_r1_forward(const int* __restrict__ offset
 //   W_e[lm2,k] = sum_{p,m1} R Y_lm1 G[row]
 // that k_source_gather sums over each source's edges.
 template <int C, int LMAX, int LMAXH>
-__global__ __launch_bounds__(C) void k_r1_reverse(const int* __restrict__ offsets, const int* __restrict__ neigh,
-                                                  const float* __restrict__ erec, const float4* __restrict__ R1c,
-                                                  const float* __restrict__ H1, const float* __restrict__ cg,
-                                                  const float* __restrict__ dPhi1, float* __restrict__ Wsrc,
-                                                  double* __restrict__ node_forces) {
+__global__ __launch_bounds__(C) void k_r1_reverse(int r0, long long e0, const int* __restrict__ offsets,
+                                                  const int* __restrict__ neigh, const float* __restrict__ erec,
+                                                  const float4* __restrict__ R1c, const float* __restrict__ H1,
+                                                  const float* __restrict__ cg, const float* __restrict__ dPhi1,
+                                                  float* __restrict__ Wsrc, double* __restrict__ node_forces) {
     using S = Shape<LMAX, LMAXH>;
     constexpr int NY = S::NY, NH = S::NH, NF = S::P * C;
     __shared__ float part[Lanes<C>::NW][kForceChunk][3];
     EdgeForceSink<C, kForceChunk> sink{part};
-    const int i = xcd_remap(blockIdx.x, gridDim.x);
+    const int li = xcd_remap(blockIdx.x, gridDim.x);
+    const int i = r0 + li;
     const int k = threadIdx.x;
     float G[S::NROWS];
     {
         float d[S::NLME];
 #pragma unroll
-        for (int q = 0; q < S::NLME; ++q) d[q] = dPhi1[(static_cast<std::size_t>(i) * S::NLME + q) * C + k];
+        for (int q = 0; q < S::NLME; ++q) d[q] = dPhi1[(static_cast<std::size_t>(li) * S::NLME + q) * C + k];
         static_for<0, S::P>([&](auto pc) {
             constexpr int p = pc;
             constexpr int le = S::paths[p].le, ls = S::paths[p].ls, lo = S::paths[p].lo;
@@ -289,11 +294,11 @@ __global__ __launch_bounds__(C) void k_r1_reverse(const int* __restrict__ offset
             });
         });
     }
-    const int e0 = offsets[i], e1 = offsets[i + 1];
-    for (int c0 = e0; c0 < e1; c0 += kForceChunk) {
-        const int c1 = min(c0 + kForceChunk, e1);
+    const int ea = offsets[i], eb = offsets[i + 1];
+    for (int c0 = ea; c0 < eb; c0 += kForceChunk) {
+        const int c1 = min(c0 + kForceChunk, eb);
         for (int e = c0; e < c1; ++e) {
-            const float* rec = erec + static_cast<std::size_t>(e) * S::REC;
+            const float* rec = erec + static_cast<std::size_t>(e - e0) * S::REC;
             if (!edge_active(rec)) {
                 sink.zero(e - c0);
                 continue;
@@ -335,13 +340,13 @@ __global__ __launch_bounds__(C) void k_r1_reverse(const int* __restrict__ offset
                     b2 += t * rec[S::REC_DY + 2 * NY + lm1];
                 });
             });
-            float* wdst = Wsrc + static_cast<std::size_t>(e) * NH * C + k;
+            float* wdst = Wsrc + static_cast<std::size_t>(e - e0) * NH * C + k;
 #pragma unroll
             for (int q = 0; q < NH; ++q) wdst[q * C] = W[q];
             const float u0 = rec[S::REC_U], u1 = rec[S::REC_U + 1], u2 = rec[S::REC_U + 2];
             sink.put(e - c0, u0 * a + b0, u1 * a + b1, u2 * a + b2);
         }
-        sink.template flush<false>(c0, c1 - c0, node_forces);
+        sink.template flush<false>(static_cast<int>(c0 - e0), c1 - c0, node_forces);
     }
 }
 
@@ -399,37 +404,44 @@ __device__ __forceinline__ void monomial_grad(const float* xs, float* gs, int C,
     }
 }
 
+// Rows li of the tile workspace belong to receiver i = r0 + li; graph-wide
+// arrays (types, scalar capture x, direct adjoint, energies) use i.
 template <int C, int NY, int NH>
-__global__ __launch_bounds__(C) void k_m0_forward(const int* __restrict__ types, const float* __restrict__ A0,
+__global__ __launch_bounds__(C) void k_m0_forward(int r0, const int* __restrict__ types, const float* __restrict__ A0,
                                                   const std::int32_t* __restrict__ terms, const int* __restrict__ toff,
-                                                  int T0, const float* __restrict__ coef, float* __restrict__ M0) {
+                                                  int T0, const float* __restrict__ coef, float* __restrict__ M0,
+                                                  float* __restrict__ xaff) {
     __shared__ float xs[NY * C];
-    const int i = blockIdx.x;
+    const int li = blockIdx.x;
+    const int i = r0 + li;
     const int k = threadIdx.x;
 #pragma unroll
-    for (int v = 0; v < NY; ++v) xs[v * C + k] = A0[(static_cast<std::size_t>(i) * NY + v) * C + k];
+    for (int v = 0; v < NY; ++v) xs[v * C + k] = A0[(static_cast<std::size_t>(li) * NY + v) * C + k];
     const float* cf = coef + static_cast<std::size_t>(types[i]) * T0 * C + k;
 #pragma unroll
     for (int LM = 0; LM < NH; ++LM) {
         const int begin = toff[LM], end = toff[LM + 1];
         float f = 0.0f;
         for (int t = begin; t < end; ++t) f += cf[static_cast<std::size_t>(t) * C] * monomial(xs, C, k, terms[t]);
-        M0[(static_cast<std::size_t>(i) * NH + LM) * C + k] = f;
+        M0[(static_cast<std::size_t>(li) * NH + LM) * C + k] = f;
+        // v4 "m0_composite" readout basis: x = M0[i, 0, :] (h1_affine_schema.hpp)
+        if (LM == 0) xaff[static_cast<std::size_t>(i) * C + k] = f;
     }
 }
 
 template <int C, int NY, int NH>
-__global__ __launch_bounds__(C) void k_m0_reverse(const int* __restrict__ types, const float* __restrict__ A0,
+__global__ __launch_bounds__(C) void k_m0_reverse(int r0, const int* __restrict__ types, const float* __restrict__ A0,
                                                   const float* __restrict__ M0_adj, const float* __restrict__ direct,
                                                   const std::int32_t* __restrict__ terms, const int* __restrict__ toff,
                                                   int T0, const float* __restrict__ coef,
                                                   float* __restrict__ A0_adj) {
     __shared__ float xs[NY * C];
     __shared__ float gs[NY * C];
-    const int i = blockIdx.x;
+    const int li = blockIdx.x;
+    const int i = r0 + li;
     const int k = threadIdx.x;
 #pragma unroll
-    for (int v = 0; v < NY; ++v) xs[v * C + k] = A0[(static_cast<std::size_t>(i) * NY + v) * C + k];
+    for (int v = 0; v < NY; ++v) xs[v * C + k] = A0[(static_cast<std::size_t>(li) * NY + v) * C + k];
     float acc[NY];
 #pragma unroll
     for (int v = 0; v < NY; ++v) acc[v] = 0.0f;
@@ -437,7 +449,7 @@ __global__ __launch_bounds__(C) void k_m0_reverse(const int* __restrict__ types,
 #pragma unroll
     for (int LM = 0; LM < NH; ++LM) {
         const int begin = toff[LM], end = toff[LM + 1];
-        float adj = M0_adj[(static_cast<std::size_t>(i) * NH + LM) * C + k];
+        float adj = M0_adj[(static_cast<std::size_t>(li) * NH + LM) * C + k];
         if (LM == 0) adj += direct[static_cast<std::size_t>(i) * C + k];
 #pragma unroll
         for (int v = 0; v < NY; ++v) gs[v * C + k] = 0.0f;
@@ -446,15 +458,15 @@ __global__ __launch_bounds__(C) void k_m0_reverse(const int* __restrict__ types,
         for (int v = 0; v < NY; ++v) acc[v] += gs[v * C + k] * adj;
     }
 #pragma unroll
-    for (int v = 0; v < NY; ++v) A0_adj[(static_cast<std::size_t>(i) * NY + v) * C + k] = acc[v];
+    for (int v = 0; v < NY; ++v) A0_adj[(static_cast<std::size_t>(li) * NY + v) * C + k] = acc[v];
 }
 
 // M1, H2 (FP64), readouts (FP64) and their adjoints for one node:
 //   E_i = E0[z] + q.x + MLP(H2), H2 = T_z^T x + W^T M1 (x = M0[i,0,:])
 //   direct = q + T_z H2_adj, A1_adj[v] = dM1/dA1_v * (W H2_adj)
-template <int C, int NY, int NH>
+template <int C, int NY>
 __global__ __launch_bounds__(C) void k_readout(
-    const int* __restrict__ types, const float* __restrict__ A1, const float* __restrict__ M0,
+    int r0, const int* __restrict__ types, const float* __restrict__ A1, const float* __restrict__ xaff,
     const std::int32_t* __restrict__ m1_terms, int T1, const float* __restrict__ m1_coef,
     const float* __restrict__ H2_T, const float* __restrict__ H2_Tt, const float* __restrict__ H2_M1,
     const float* __restrict__ H2_M1t, const double* __restrict__ q, const double* __restrict__ W1r,
@@ -464,12 +476,13 @@ __global__ __launch_bounds__(C) void k_readout(
     __shared__ float gs[NY * C];
     __shared__ double sx[C], sm1[C], sh2a[C];
     __shared__ double sbuf[Lanes<C>::NW];
-    const int i = blockIdx.x;
+    const int li = blockIdx.x;
+    const int i = r0 + li;
     const int k = threadIdx.x;
     const int t = types[i];
 #pragma unroll
     for (int v = 0; v < NY; ++v) {
-        xs[v * C + k] = A1[(static_cast<std::size_t>(i) * NY + v) * C + k];
+        xs[v * C + k] = A1[(static_cast<std::size_t>(li) * NY + v) * C + k];
         gs[v * C + k] = 0.0f;
     }
     const float* cf = m1_coef + static_cast<std::size_t>(t) * T1 * C + k;
@@ -480,7 +493,7 @@ __global__ __launch_bounds__(C) void k_readout(
         m1 += c * monomial(xs, C, k, pk);
         monomial_grad(xs, gs, C, k, pk, c);
     }
-    const float xa = M0[static_cast<std::size_t>(i) * NH * C + k];
+    const float xa = xaff[static_cast<std::size_t>(i) * C + k];
     sx[k] = static_cast<double>(xa);
     sm1[k] = static_cast<double>(m1);
     __syncthreads();
@@ -511,7 +524,119 @@ __global__ __launch_bounds__(C) void k_readout(
     direct[static_cast<std::size_t>(i) * C + k] = static_cast<float>(dsum);
     const float m1adj = static_cast<float>(s1);
 #pragma unroll
-    for (int v = 0; v < NY; ++v) A1_adj[(static_cast<std::size_t>(i) * NY + v) * C + k] = gs[v * C + k] * m1adj;
+    for (int v = 0; v < NY; ++v) A1_adj[(static_cast<std::size_t>(li) * NY + v) * C + k] = gs[v * C + k] * m1adj;
+}
+
+// ---------------------------------------------------------------------------
+// Tiled execution: per-tile contributions of edges to their sources.  The
+// edges of source s inside the tile's edge range [e0, e1) are a contiguous
+// run of s's source-transpose segment (edge ids ascend within a segment and
+// edges are receiver-major), found by a binary search.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int lower_edge(const int* __restrict__ sedges, int lo, int hi, long long key) {
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (sedges[mid] < key)
+            lo = mid + 1;
+        else
+            hi = mid;
+    }
+    return lo;
+}
+
+// H1_adj[s] += sum over the tile's edges leaving s of W_e (FP64 sum, one
+// read-modify-write per source and tile; tiles run in order).
+template <int C, int NH>
+__global__ __launch_bounds__(C) void k_tile_source_adjoint(const int* __restrict__ touched, long long e0, long long e1,
+                                                           const int* __restrict__ soff,
+                                                           const int* __restrict__ sedges,
+                                                           const float* __restrict__ erec, int rec_floats,
+                                                           const float* __restrict__ Wsrc,
+                                                           float* __restrict__ H1_adj) {
+    const int s = touched[blockIdx.x];
+    const int k = threadIdx.x;
+    double acc[NH];
+#pragma unroll
+    for (int q = 0; q < NH; ++q) acc[q] = 0.0;
+    const int hi = soff[s + 1];
+    for (int t = lower_edge(sedges, soff[s], hi, e0); t < hi; ++t) {
+        const long long e = sedges[t];
+        if (e >= e1) break;
+        if (!edge_active(erec + static_cast<std::size_t>(e - e0) * rec_floats)) continue;
+        const float* w = Wsrc + static_cast<std::size_t>(e - e0) * NH * C + k;
+#pragma unroll
+        for (int q = 0; q < NH; ++q) acc[q] += static_cast<double>(w[q * C]);
+    }
+    float* dst = H1_adj + static_cast<std::size_t>(s) * NH * C + k;
+#pragma unroll
+    for (int q = 0; q < NH; ++q) dst[q * C] = dst[q * C] + static_cast<float>(acc[q]);
+}
+
+// F[s] += sum of the tile's directed forces on edges leaving s (one wave per source)
+__global__ __launch_bounds__(256) void k_tile_forces_sources(const int* __restrict__ touched, int count, long long e0,
+                                                             long long e1, const int* __restrict__ soff,
+                                                             const int* __restrict__ sedges,
+                                                             const double* __restrict__ nf, double* __restrict__ F) {
+    const int b = blockIdx.x * (256 / kWave) + threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave;
+    if (b >= count) return;
+    const int s = touched[b];
+    const int hi = soff[s + 1];
+    const int lo = lower_edge(sedges, soff[s], hi, e0);
+    double f0 = 0.0, f1 = 0.0, f2 = 0.0;
+    for (int t = lo + lane; t < hi; t += kWave) {
+        const long long e = sedges[t];
+        if (e >= e1) break;
+        const std::size_t le = static_cast<std::size_t>(e - e0);
+        f0 += nf[3 * le];
+        f1 += nf[3 * le + 1];
+        f2 += nf[3 * le + 2];
+    }
+    f0 = wave_sum<kWave>(f0);
+    f1 = wave_sum<kWave>(f1);
+    f2 = wave_sum<kWave>(f2);
+    if (lane == 0) {
+        F[3 * static_cast<std::size_t>(s)] += f0;
+        F[3 * static_cast<std::size_t>(s) + 1] += f1;
+        F[3 * static_cast<std::size_t>(s) + 2] += f2;
+    }
+}
+
+// F[i] -= sum of the directed forces on the edges arriving at receiver i of the tile
+__global__ __launch_bounds__(256) void k_tile_forces_receivers(int r0, int nr, long long e0,
+                                                               const int* __restrict__ offsets,
+                                                               const double* __restrict__ nf, double* __restrict__ F) {
+    const int li = blockIdx.x * (256 / kWave) + threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave;
+    if (li >= nr) return;
+    const int i = r0 + li;
+    double f0 = 0.0, f1 = 0.0, f2 = 0.0;
+    for (int e = offsets[i] + lane; e < offsets[i + 1]; e += kWave) {
+        const std::size_t le = static_cast<std::size_t>(e - e0);
+        f0 += nf[3 * le];
+        f1 += nf[3 * le + 1];
+        f2 += nf[3 * le + 2];
+    }
+    f0 = wave_sum<kWave>(f0);
+    f1 = wave_sum<kWave>(f1);
+    f2 = wave_sum<kWave>(f2);
+    if (lane == 0) {
+        F[3 * static_cast<std::size_t>(i)] -= f0;
+        F[3 * static_cast<std::size_t>(i) + 1] -= f1;
+        F[3 * static_cast<std::size_t>(i) + 2] -= f2;
+    }
+}
+
+__global__ void k_fill_f32(std::size_t n, float* __restrict__ p) {
+    for (std::size_t j = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x; j < n;
+         j += static_cast<std::size_t>(gridDim.x) * blockDim.x)
+        p[j] = 0.0f;
+}
+
+__global__ void k_fill_f64(std::size_t n, double* __restrict__ p) {
+    for (std::size_t j = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x; j < n;
+         j += static_cast<std::size_t>(gridDim.x) * blockDim.x)
+        p[j] = 0.0;
 }
 
 // ---------------------------------------------------------------------------
@@ -566,26 +691,34 @@ __global__ __launch_bounds__(64) void k_node_gemm(const GemmTile* __restrict__ t
 // ---------------------------------------------------------------------------
 // Reductions
 // ---------------------------------------------------------------------------
+// One wave per atom: F[a] = sum over edges leaving a of f_e - sum over edges
+// arriving at a of f_e (FP64; fixed lane partition, deterministic).
 __global__ __launch_bounds__(256) void k_atom_forces(int N, const int* __restrict__ offsets,
                                                      const int* __restrict__ soff, const int* __restrict__ sedges,
                                                      const double* __restrict__ nf, double* __restrict__ F) {
-    const int a = blockIdx.x * blockDim.x + threadIdx.x;
+    const int a = blockIdx.x * (256 / kWave) + threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave;
     if (a >= N) return;
     double f0 = 0.0, f1 = 0.0, f2 = 0.0;
-    for (int t = soff[a]; t < soff[a + 1]; ++t) {
-        const int e = sedges[t];
-        f0 += nf[3 * static_cast<std::size_t>(e)];
-        f1 += nf[3 * static_cast<std::size_t>(e) + 1];
-        f2 += nf[3 * static_cast<std::size_t>(e) + 2];
+    for (int t = soff[a] + lane; t < soff[a + 1]; t += kWave) {
+        const std::size_t e = static_cast<std::size_t>(sedges[t]);
+        f0 += nf[3 * e];
+        f1 += nf[3 * e + 1];
+        f2 += nf[3 * e + 2];
     }
-    for (int e = offsets[a]; e < offsets[a + 1]; ++e) {
+    for (int e = offsets[a] + lane; e < offsets[a + 1]; e += kWave) {
         f0 -= nf[3 * static_cast<std::size_t>(e)];
         f1 -= nf[3 * static_cast<std::size_t>(e) + 1];
         f2 -= nf[3 * static_cast<std::size_t>(e) + 2];
     }
-    F[3 * static_cast<std::size_t>(a)] = f0;
-    F[3 * static_cast<std::size_t>(a) + 1] = f1;
-    F[3 * static_cast<std::size_t>(a) + 2] = f2;
+    f0 = wave_sum<kWave>(f0);
+    f1 = wave_sum<kWave>(f1);
+    f2 = wave_sum<kWave>(f2);
+    if (lane == 0) {
+        F[3 * static_cast<std::size_t>(a)] = f0;
+        F[3 * static_cast<std::size_t>(a) + 1] = f1;
+        F[3 * static_cast<std::size_t>(a) + 2] = f2;
+    }
 }
 
 constexpr int kReduceThreads = 256;
@@ -612,13 +745,28 @@ __global__ __launch_bounds__(kReduceThreads) void k_stress_partial(std::int64_t 
     }
 }
 
-__global__ void k_stress_final(int blocks, const double* __restrict__ partial, double volume,
-                               double* __restrict__ stress) {
-    const int c = threadIdx.x;
-    if (c >= 9) return;
-    double t = 0.0;
-    for (int b = 0; b < blocks; ++b) t += partial[static_cast<std::size_t>(b) * 9 + c];
-    stress[c] = -t / volume;
+// out[c] = scale * sum of the partials (or out[c] += ... when accumulating)
+__global__ __launch_bounds__(kReduceThreads) void k_stress_final(int blocks, const double* __restrict__ partial,
+                                                                 double scale, int accumulate,
+                                                                 double* __restrict__ out) {
+    __shared__ double red[9][kReduceThreads / kWave];
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    for (int c = 0; c < 9; ++c) {
+        double t = 0.0;
+        for (int b = threadIdx.x; b < blocks; b += kReduceThreads) t += partial[static_cast<std::size_t>(b) * 9 + c];
+        t = wave_sum<kWave>(t);
+        if (lane == 0) red[c][wave] = t;
+    }
+    __syncthreads();
+    if (threadIdx.x < 9) {
+        double t = 0.0;
+        for (int w = 0; w < kReduceThreads / kWave; ++w) t += red[threadIdx.x][w];
+        out[threadIdx.x] = accumulate ? out[threadIdx.x] + scale * t : scale * t;
+    }
+}
+
+__global__ void k_scale9(const double* __restrict__ in, double scale, double* __restrict__ out) {
+    if (threadIdx.x < 9) out[threadIdx.x] = scale * in[threadIdx.x];
 }
 
 __global__ __launch_bounds__(1024) void k_energy_sum(int N, const double* __restrict__ e, double* __restrict__ total) {
@@ -660,83 +808,105 @@ struct KernelSetImpl final : KernelSet {
         geometry_records(LMAX, E, xyz, r, m.r_cut, m.x0, m.h, m.intervals, erec, s);
     }
 
-    void forward(const DeviceModel& m, const DeviceGraph& g, const Workspace& w, const GemmPlan& a0,
-                 const GemmPlan& h1, const GemmPlan& a1, hipStream_t s, LaunchTimer* tm) const override {
-        const int N = g.N;
-        if (N == 0) return;
+    void layer1_forward(const DeviceModel& m, const DeviceGraph& g, const TileView& t, const Workspace& w,
+                        bool through_h1, hipStream_t s, LaunchTimer* tm) const override {
+        if (t.nr == 0) return;
         {
             TimerScope ts(tm, "r0_forward", s);
-            k_r0_forward<C, LMAX><<<N, C, 0, s>>>(g.offsets, g.neigh_types, g.erec, m.R0c, m.H0, w.Phi0);
+            k_r0_forward<C, LMAX><<<t.nr, C, 0, s>>>(t.r0, t.e0, g.offsets, g.neigh_types, w.erec, m.R0c, m.H0,
+                                                     w.Phi0);
             SMX_LAUNCH_CHECK("r0_forward");
         }
         {
             TimerScope ts(tm, "a0_linear", s);
-            launch_node_gemm(a0, m.A0_w, w.Phi0, w.A0, s);
+            launch_node_gemm(t.a0, m.A0_w, w.Phi0, w.A0, s);
         }
+        if (!through_h1) return;
         {
             TimerScope ts(tm, "m0_forward", s);
-            k_m0_forward<C, S::NY, S::NH><<<N, C, 0, s>>>(g.node_types, w.A0, m.m0_terms, m.m0_toff, m.T0, m.m0_coef, w.M0);
+            k_m0_forward<C, S::NY, S::NH><<<t.nr, C, 0, s>>>(t.r0, g.node_types, w.A0, m.m0_terms, m.m0_toff, m.T0,
+                                                            m.m0_coef, w.M0, w.xaff);
             SMX_LAUNCH_CHECK("m0_forward");
         }
         {
             TimerScope ts(tm, "h1_linear", s);
-            launch_node_gemm(h1, m.H1_w, w.M0, w.H1, s);
+            launch_node_gemm(t.h1, m.H1_w, w.M0, w.H1 + static_cast<std::size_t>(t.r0) * S::NH * C, s);
         }
+    }
+
+    void layer2(const DeviceModel& m, const DeviceGraph& g, const TileView& t, const Workspace& w, hipStream_t s,
+                LaunchTimer* tm) const override {
+        if (t.nr == 0) return;
         {
             TimerScope ts(tm, "r1_forward", s);
-            k_r1_forward<C, LMAX, LMAXH><<<N, C, 0, s>>>(g.offsets, g.neigh, g.erec, m.R1c, w.H1, m.cg, w.Phi1);
+            k_r1_forward<C, LMAX, LMAXH><<<t.nr, C, 0, s>>>(t.r0, t.e0, g.offsets, g.neigh, w.erec, m.R1c, w.H1, m.cg,
+                                                           w.Phi1);
             SMX_LAUNCH_CHECK("r1_forward");
         }
         {
             TimerScope ts(tm, "a1_linear", s);
-            launch_node_gemm(a1, m.A1_w, w.Phi1, w.A1, s);
+            launch_node_gemm(t.a1f, m.A1_w, w.Phi1, w.A1, s);
         }
         {
             TimerScope ts(tm, "readout", s);
-            k_readout<C, S::NY, S::NH><<<N, C, 0, s>>>(g.node_types, w.A1, w.M0, m.m1_terms, m.T1, m.m1_coef, m.H2_T,
-                                                      m.H2_Tt, m.H2_M1, m.H2_M1t, m.q, m.W1r, m.W2r, m.hidden,
-                                                      m.readout_scale, m.E0, w.node_energies, w.direct, w.A1_adj);
+            k_readout<C, S::NY><<<t.nr, C, 0, s>>>(t.r0, g.node_types, w.A1, w.xaff, m.m1_terms, m.T1, m.m1_coef,
+                                                  m.H2_T, m.H2_Tt, m.H2_M1, m.H2_M1t, m.q, m.W1r, m.W2r, m.hidden,
+                                                  m.readout_scale, m.E0, w.node_energies, w.direct, w.A1_adj);
             SMX_LAUNCH_CHECK("readout");
         }
-    }
-
-    void reverse(const DeviceModel& m, const DeviceGraph& g, const Workspace& w, const GemmPlan& a0r,
-                 const GemmPlan& h1r, const GemmPlan& a1r, hipStream_t s, LaunchTimer* tm) const override {
-        const int N = g.N;
-        if (N == 0) return;
         {
             TimerScope ts(tm, "a1_linear_reverse", s);
-            launch_node_gemm(a1r, m.A1_wt, w.A1_adj, w.dPhi1, s);
+            launch_node_gemm(t.a1r, m.A1_wt, w.A1_adj, w.dPhi1, s);
         }
         {
             TimerScope ts(tm, "r1_reverse", s);
-            k_r1_reverse<C, LMAX, LMAXH><<<N, C, 0, s>>>(g.offsets, g.neigh, g.erec, m.R1c, w.H1, m.cg, w.dPhi1,
-                                                        w.Wsrc, w.node_forces);
+            k_r1_reverse<C, LMAX, LMAXH><<<t.nr, C, 0, s>>>(t.r0, t.e0, g.offsets, g.neigh, w.erec, m.R1c, w.H1, m.cg,
+                                                           w.dPhi1, w.Wsrc, w.node_forces);
             SMX_LAUNCH_CHECK("r1_reverse");
         }
-        {
-            TimerScope ts(tm, "source_gather", s);
-            k_source_gather<C, S::NH><<<N, C, 0, s>>>(g.soff, g.sedges, g.erec, S::REC, w.Wsrc, w.H1_adj);
-            SMX_LAUNCH_CHECK("source_gather");
-        }
+    }
+
+    void source_adjoint_all(const DeviceGraph& g, const Workspace& w, hipStream_t s, LaunchTimer* tm) const override {
+        if (g.N == 0) return;
+        TimerScope ts(tm, "source_gather", s);
+        k_source_gather<C, S::NH><<<g.N, C, 0, s>>>(g.soff, g.sedges, w.erec, S::REC, w.Wsrc, w.H1_adj);
+        SMX_LAUNCH_CHECK("source_gather");
+    }
+
+    void source_adjoint_tile(const DeviceGraph& g, const TileView& t, const Workspace& w, hipStream_t s,
+                             LaunchTimer* tm) const override {
+        if (t.touched_count == 0) return;
+        TimerScope ts(tm, "source_gather", s);
+        k_tile_source_adjoint<C, S::NH><<<t.touched_count, C, 0, s>>>(t.touched, t.e0, t.e0 + t.ne, g.soff, g.sedges,
+                                                                     w.erec, S::REC, w.Wsrc, w.H1_adj);
+        SMX_LAUNCH_CHECK("tile_source_adjoint");
+    }
+
+    void layer1_reverse(const DeviceModel& m, const DeviceGraph& g, const TileView& t, const Workspace& w,
+                        bool accumulate_forces, hipStream_t s, LaunchTimer* tm) const override {
+        if (t.nr == 0) return;
         {
             TimerScope ts(tm, "h1_linear_reverse", s);
-            launch_node_gemm(h1r, m.H1_wt, w.H1_adj, w.M0_adj, s);
+            launch_node_gemm(t.h1, m.H1_wt, w.H1_adj + static_cast<std::size_t>(t.r0) * S::NH * C, w.M0_adj, s);
         }
         {
             TimerScope ts(tm, "m0_reverse", s);
-            k_m0_reverse<C, S::NY, S::NH><<<N, C, 0, s>>>(g.node_types, w.A0, w.M0_adj, w.direct, m.m0_terms, m.m0_toff,
-                                                         m.T0, m.m0_coef, w.A0_adj);
+            k_m0_reverse<C, S::NY, S::NH><<<t.nr, C, 0, s>>>(t.r0, g.node_types, w.A0, w.M0_adj, w.direct, m.m0_terms,
+                                                            m.m0_toff, m.T0, m.m0_coef, w.A0_adj);
             SMX_LAUNCH_CHECK("m0_reverse");
         }
         {
             TimerScope ts(tm, "a0_linear_reverse", s);
-            launch_node_gemm(a0r, m.A0_wt, w.A0_adj, w.Phi0_adj, s);
+            launch_node_gemm(t.a0, m.A0_wt, w.A0_adj, w.Phi0_adj, s);
         }
         {
             TimerScope ts(tm, "r0_reverse", s);
-            k_r0_reverse<C, LMAX><<<N, C, 0, s>>>(g.offsets, g.neigh_types, g.erec, m.R0c, m.H0, w.Phi0_adj,
-                                                  w.node_forces);
+            if (accumulate_forces)
+                k_r0_reverse<C, LMAX, true><<<t.nr, C, 0, s>>>(t.r0, t.e0, g.offsets, g.neigh_types, w.erec, m.R0c,
+                                                               m.H0, w.Phi0_adj, w.node_forces);
+            else
+                k_r0_reverse<C, LMAX, false><<<t.nr, C, 0, s>>>(t.r0, t.e0, g.offsets, g.neigh_types, w.erec, m.R0c,
+                                                                m.H0, w.Phi0_adj, w.node_forces);
             SMX_LAUNCH_CHECK("r0_reverse");
         }
     }
@@ -785,7 +955,7 @@ void launch_node_gemm(const GemmPlan& plan, const float* W, const float* in, flo
 void launch_atom_forces(int N, const int* offsets, const int* soff, const int* sedges, const double* node_forces,
                         double* atom_forces, hipStream_t s) {
     if (N == 0) return;
-    k_atom_forces<<<blocks_for(N, 256), 256, 0, s>>>(N, offsets, soff, sedges, node_forces, atom_forces);
+    k_atom_forces<<<blocks_for(N, 256 / kWave), 256, 0, s>>>(N, offsets, soff, sedges, node_forces, atom_forces);
     SMX_LAUNCH_CHECK("atom_forces");
 }
 
@@ -793,8 +963,48 @@ void launch_stress(std::int64_t E, const double* node_forces, const double* xyz,
                    int partial_blocks, double* stress, hipStream_t s) {
     k_stress_partial<<<partial_blocks, kReduceThreads, 0, s>>>(E, node_forces, xyz, partial);
     SMX_LAUNCH_CHECK("stress_partial");
-    k_stress_final<<<1, 64, 0, s>>>(partial_blocks, partial, volume, stress);
+    k_stress_final<<<1, kReduceThreads, 0, s>>>(partial_blocks, partial, -1.0 / volume, 0, stress);
     SMX_LAUNCH_CHECK("stress_final");
+}
+
+void launch_virial_accumulate(std::int64_t E, const double* node_forces, const double* xyz, double* partial,
+                              int partial_blocks, double* virial, hipStream_t s) {
+    if (E == 0) return;
+    k_stress_partial<<<partial_blocks, kReduceThreads, 0, s>>>(E, node_forces, xyz, partial);
+    SMX_LAUNCH_CHECK("virial_partial");
+    k_stress_final<<<1, kReduceThreads, 0, s>>>(partial_blocks, partial, 1.0, 1, virial);
+    SMX_LAUNCH_CHECK("virial_accumulate");
+}
+
+void launch_scale9(const double* in, double scale, double* out, hipStream_t s) {
+    k_scale9<<<1, 64, 0, s>>>(in, scale, out);
+    SMX_LAUNCH_CHECK("scale9");
+}
+
+void launch_tile_forces(const TileView& t, const int* offsets, const int* soff, const int* sedges,
+                        const double* node_forces, double* F, hipStream_t s) {
+    if (t.touched_count > 0) {
+        k_tile_forces_sources<<<blocks_for(t.touched_count, 256 / kWave), 256, 0, s>>>(
+            t.touched, t.touched_count, t.e0, t.e0 + t.ne, soff, sedges, node_forces, F);
+        SMX_LAUNCH_CHECK("tile_forces_sources");
+    }
+    if (t.nr > 0) {
+        k_tile_forces_receivers<<<blocks_for(t.nr, 256 / kWave), 256, 0, s>>>(t.r0, t.nr, t.e0, offsets, node_forces,
+                                                                              F);
+        SMX_LAUNCH_CHECK("tile_forces_receivers");
+    }
+}
+
+void launch_fill_zero(float* p, std::size_t n, hipStream_t s) {
+    if (n == 0) return;
+    k_fill_f32<<<static_cast<unsigned>(std::min<std::size_t>((n + 255) / 256, 4096)), 256, 0, s>>>(n, p);
+    SMX_LAUNCH_CHECK("fill_f32");
+}
+
+void launch_fill_zero(double* p, std::size_t n, hipStream_t s) {
+    if (n == 0) return;
+    k_fill_f64<<<static_cast<unsigned>(std::min<std::size_t>((n + 255) / 256, 4096)), 256, 0, s>>>(n, p);
+    SMX_LAUNCH_CHECK("fill_f64");
 }
 
 void launch_energy_sum(int N, const double* node_energies, double* total, hipStream_t s) {

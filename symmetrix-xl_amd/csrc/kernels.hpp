@@ -60,7 +60,6 @@ struct DeviceGraph {
     const int* receivers = nullptr;   // [E]
     const int* soff = nullptr;        // [N+1]
     const int* sedges = nullptr;      // [E] edges ordered by source, ascending edge id
-    const float* erec = nullptr;      // [E][REC] per-edge record
 };
 
 // Node-linear tiles: TM=16 rows of one (weight group, m) over a node list.
@@ -76,29 +75,44 @@ struct GemmTile {
 struct GemmPlan {
     const GemmTile* tiles = nullptr;
     const GemmGroup* groups = nullptr;
-    const int* node_list = nullptr;
+    const int* node_list = nullptr;   // tile-local row indices
     int num_tiles = 0;
     int max_n = 0;
 };
 
-// Per-call workspace (node-sized and edge-sized arrays).
+// A receiver tile: receivers [r0, r0+nr), their edges [e0, e0+ne) (edges
+// are receiver-major, so a receiver range owns one contiguous edge range).
+struct TileView {
+    int r0 = 0, nr = 0;
+    std::int64_t e0 = 0, ne = 0;
+    GemmPlan a0, h1, a1f, a1r;
+    const int* touched = nullptr;  // sources with an edge in the tile (ascending)
+    int touched_count = 0;
+};
+
+// Workspace.  Tile-local arrays are indexed by receiver - r0 (or edge - e0);
+// graph-wide arrays by the global index.
 struct Workspace {
-    float* Phi0 = nullptr;      // [N][NY][C]
-    float* A0 = nullptr;        // [N][NY][C]
-    float* M0 = nullptr;        // [N][NH][C]
+    // tile-local
+    float* erec = nullptr;      // [ne][REC] per-edge records
+    float* Phi0 = nullptr;      // [nr][NY][C]
+    float* A0 = nullptr;        // [nr][NY][C]
+    float* M0 = nullptr;        // [nr][NH][C]
+    float* Phi1 = nullptr;      // [nr][NLME][C]
+    float* A1 = nullptr;        // [nr][NY][C]
+    float* A1_adj = nullptr;    // [nr][NY][C]
+    float* dPhi1 = nullptr;     // [nr][NLME][C]
+    float* Wsrc = nullptr;      // [ne][NH][C] per-edge source-adjoint contributions
+    float* M0_adj = nullptr;    // [nr][NH][C]
+    float* A0_adj = nullptr;    // [nr][NY][C]
+    float* Phi0_adj = nullptr;  // [nr][NY][C]
+    double* node_forces = nullptr;  // [ne][3]
+    // graph-wide
     float* H1 = nullptr;        // [N][NH][C]
-    float* Phi1 = nullptr;      // [N][NLME][C]
-    float* A1 = nullptr;        // [N][NY][C]
-    float* A1_adj = nullptr;    // [N][NY][C]
-    float* direct = nullptr;    // [N][C]
-    float* dPhi1 = nullptr;     // [N][NLME][C]
-    float* Wsrc = nullptr;      // [E][NH][C] per-edge source-adjoint contributions
     float* H1_adj = nullptr;    // [N][NH][C]
-    float* M0_adj = nullptr;    // [N][NH][C]
-    float* A0_adj = nullptr;    // [N][NY][C]
-    float* Phi0_adj = nullptr;  // [N][NY][C]
+    float* xaff = nullptr;      // [N][C] scalar capture M0[i,0,:]
+    float* direct = nullptr;    // [N][C] direct adjoint of the scalar capture
     double* node_energies = nullptr;  // [N]
-    double* node_forces = nullptr;    // [E][3]
 };
 
 // Timing hook: the evaluator brackets launches with events when enabled.
@@ -108,20 +122,37 @@ struct LaunchTimer {
     virtual void end(const char* name, hipStream_t s) = 0;
 };
 
-// Kernels specialised for one (C, l_max, L_max) shape.
+// Kernels specialised for one (C, l_max, L_max) shape.  The stages are the
+// reference's direct plan split at the two places where graph-wide state is
+// exchanged (H1 after layer 1, H1 adjoint after the layer-2 reverse).
 struct KernelSet {
     virtual ~KernelSet() = default;
     virtual int record_floats() const = 0;
-    virtual void edge_geometry(const DeviceModel& m, std::int64_t E, const double* xyz, const double* r,
+    // per-edge records of a tile from its FP64 xyz and r
+    virtual void edge_geometry(const DeviceModel& m, std::int64_t ne, const double* xyz, const double* r,
                                float* erec, hipStream_t s) const = 0;
-    virtual void forward(const DeviceModel& m, const DeviceGraph& g, const Workspace& w, const GemmPlan& a0,
-                         const GemmPlan& h1, const GemmPlan& a1, hipStream_t s, LaunchTimer* t) const = 0;
-    virtual void reverse(const DeviceModel& m, const DeviceGraph& g, const Workspace& w, const GemmPlan& a0r,
-                         const GemmPlan& h1r, const GemmPlan& a1r, hipStream_t s, LaunchTimer* t) const = 0;
+    // R0 forward + A0 linear; with through_h1 also M0, the scalar capture and
+    // H1 rows r0.. of the graph-wide H1
+    virtual void layer1_forward(const DeviceModel& m, const DeviceGraph& g, const TileView& t, const Workspace& w,
+                                bool through_h1, hipStream_t s, LaunchTimer* tm) const = 0;
+    // R1 forward, A1, readouts and their reverse, R1 reverse: energies,
+    // direct adjoint, per-edge source terms, directed forces (assigned)
+    virtual void layer2(const DeviceModel& m, const DeviceGraph& g, const TileView& t, const Workspace& w,
+                        hipStream_t s, LaunchTimer* tm) const = 0;
+    // H1_adj = source sums of W over the whole graph (one tile)
+    virtual void source_adjoint_all(const DeviceGraph& g, const Workspace& w, hipStream_t s,
+                                    LaunchTimer* tm) const = 0;
+    // H1_adj[s] += source sums of W over one tile's edges
+    virtual void source_adjoint_tile(const DeviceGraph& g, const TileView& t, const Workspace& w, hipStream_t s,
+                                     LaunchTimer* tm) const = 0;
+    // H1 reverse, M0 reverse, A0 reverse, R0 reverse (directed forces added
+    // to, or assigned to, the tile's buffer)
+    virtual void layer1_reverse(const DeviceModel& m, const DeviceGraph& g, const TileView& t, const Workspace& w,
+                                bool accumulate_forces, hipStream_t s, LaunchTimer* tm) const = 0;
 };
 
 std::unique_ptr<KernelSet> make_kernel_set(int C, int l_max, int L_max);
-// true if (C, l_max, L_max) has a compiled kernel set, and the paths match
+// paths of the compiled kernel set for (l_max, L_max), false if none
 bool kernel_paths(int l_max, int L_max, std::vector<int>& le, std::vector<int>& ls, std::vector<int>& lo);
 
 // Per-edge records (spline point, Y, dY, direction) from FP64 xyz and r.
@@ -135,29 +166,42 @@ void launch_atom_forces(int N, const int* offsets, const int* soff, const int* s
                         double* atom_forces, hipStream_t s);
 void launch_stress(std::int64_t E, const double* node_forces, const double* xyz, double volume, double* partial,
                    int partial_blocks, double* stress, hipStream_t s);
+// virial[9] += sum_e f_e xyz_e^T over E edges
+void launch_virial_accumulate(std::int64_t E, const double* node_forces, const double* xyz, double* partial,
+                              int partial_blocks, double* virial, hipStream_t s);
+void launch_scale9(const double* in, double scale, double* out, hipStream_t s);
+// F[src] += f_e, F[rcv] -= f_e for one tile's edges (tile-local forces)
+void launch_tile_forces(const TileView& t, const int* offsets, const int* soff, const int* sedges,
+                        const double* node_forces, double* F, hipStream_t s);
+void launch_fill_zero(float* p, std::size_t n, hipStream_t s);
+void launch_fill_zero(double* p, std::size_t n, hipStream_t s);
 void launch_energy_sum(int N, const double* node_energies, double* total, hipStream_t s);
 
 // Geometry (FP64, no contraction): per-atom minimum-image displacement from
-// the reference positions, then per-edge xyz/r from fractional edge vectors.
-void launch_prepared_geometry(int N, std::int64_t E, const int* receivers, const int* sources,
-                              const double* fractional_xyz, const double* cell, const double* inv_cell,
-                              const double* reference_positions, const double* positions, double cutoff,
-                              double* disp, double* xyz, double* r, int* invalid, hipStream_t s);
+// the reference positions, then xyz/r of the edges [e0, e0+ne) from the
+// reference fractional edge vector wfrac[src] - wfrac[rcv] + image.
+void launch_displacements(int N, const double* cell, const double* inv_cell, const double* reference_positions,
+                          const double* positions, double* disp, hipStream_t s);
+void launch_edge_xyz(std::int64_t e0, std::int64_t ne, const double* cell, const int* receivers, const int* sources,
+                     const double* wfrac, const std::uint32_t* images, const double* disp, double cutoff,
+                     double* xyz, double* r, int* invalid, hipStream_t s);
 
 // Neighbour list (bit-exact with the reference's device builder).
-struct NeighborBuffers;  // defined in geometry.hip
 struct NeighborResult {
     std::int64_t num_edges = 0;
-    int* num_neigh = nullptr;       // [N]
-    int* offsets = nullptr;         // [N+1]
-    int* sources = nullptr;         // [E]
-    int* shifts = nullptr;          // [E][3]
-    double* fractional_xyz = nullptr;  // [E][3]
+    int* num_neigh = nullptr;        // [N]
+    int* offsets = nullptr;          // [N+1]
+    int* sources = nullptr;          // [E]
+    std::uint32_t* images = nullptr; // [E] packed int8 x3 bin images
+    double* wfrac = nullptr;         // [N][3] wrapped fractional positions
+    int* shifts = nullptr;           // [E][3] (only when requested)
+    double* fractional_xyz = nullptr;  // [E][3] (only when requested)
 };
 // Builds into buffers allocated with hipMalloc (freed by the caller with
-// hipFree); positions/cell/inverse on the host.
+// hipFree); positions/cell/inverse on the host.  with_shifts also fills
+// shifts and fractional_xyz.
 void build_neighbor_list(int N, const double* positions_host, const double* cell_host, const double* inv_host,
-                         double cutoff, NeighborResult& out, hipStream_t s);
+                         double cutoff, bool with_shifts, NeighborResult& out, hipStream_t s);
 
 // Edge receivers and source transpose from a receiver CSR (all on device).
 void launch_graph_schedule(int N, std::int64_t E, const int* offsets, const int* sources, int* receivers,
@@ -165,6 +209,11 @@ void launch_graph_schedule(int N, std::int64_t E, const int* offsets, const int*
 // neigh_types[e] = node_types[sources[e]]
 void launch_gather_types(std::int64_t E, const int* sources, const int* node_types, int* neigh_types,
                          hipStream_t s);
+// Sources with at least one edge in [e0, e0+ne), ascending, into out
+// (capacity >= N); returns the count.  bitmap: N/32+1 words of scratch,
+// word_counts: N/32+1 ints of scratch.
+int build_touched_sources(int N, std::int64_t e0, std::int64_t ne, const int* sources, std::uint32_t* bitmap,
+                          int* word_counts, int* out, hipStream_t s);
 // exclusive scan of int32 counts into int64 (device), returns total on host
 std::int64_t device_exclusive_scan(const int* in, long long* out, int n, hipStream_t s);
 

@@ -69,6 +69,8 @@ SIGNATURES = [
     ("smx_prepare_factorized_graph_device", _i32, [_vp, _i32, _vp, _vp, _i64, _vp, _vp, _p_u64]),
     ("smx_prepare_periodic_factorized_graph", _i32,
      [_vp, _i32, _vp, _vp, _vp, _vp, _dbl, _p_u64, _p_i64]),
+    ("smx_set_execution_plan", _i32, [_vp, _cp, _i32]),
+    ("smx_execution_plan", _i32, [_vp, _vp, _i64]),
     ("smx_update_factorized_cell", _i32, [_vp, _u64, _vp, _vp]),
     ("smx_compute_prepared_factorized", _i32, [_vp, _u64, _vp, _vp]),
     ("smx_compute_prepared_factorized_positions", _i32, [_vp, _u64, _vp]),

@@ -67,6 +67,18 @@ class MACEKokkosFloat:
     def set_streamed_edges(self, mode):
         check(lib.smx_set_streamed_edges(self._h, str(mode).encode()))
 
+    def set_execution_plan_request(self, profile="auto", tile_receivers=0):
+        """``"speed"`` (untiled), ``"capacity"`` (three-sweep tiled plan with at
+        most ``tile_receivers`` receivers per tile) or ``"auto"``; applies to
+        graphs prepared afterwards."""
+        check(lib.smx_set_execution_plan(self._h, str(profile).encode(), int(tile_receivers)))
+
+    @property
+    def execution_plan(self):
+        buf = ctypes.create_string_buffer(256)
+        check(lib.smx_execution_plan(self._h, ctypes.addressof(buf), 256))
+        return buf.value.decode()
+
     @property
     def stream(self):
         return lib.smx_evaluator_stream(self._h)

@@ -138,3 +138,70 @@ def test_repeat_calls_bitwise_deterministic(tiny_model_path):
         ev._compute_prepared_factorized_positions(g["generation"], s["positions"])
         outs.append((ev.node_energies.tobytes(), ev.node_forces.tobytes()))
     assert outs[0] == outs[1] == outs[2]
+
+
+def _run(ev, s, types, skin=0.5):
+    cell = np.asarray(s["cell"], float)
+    g = ev._prepare_periodic_factorized_graph(types, s["positions"], cell, np.linalg.inv(cell), ev.r_cut + skin)
+    ev._compute_prepared_factorized_positions(g["generation"], s["positions"])
+    e = ev.node_energies
+    f = ev._reduce_atom_forces(len(types), None, None, g["generation"])
+    st = ev._reduce_stress(abs(np.linalg.det(cell)), None, g["generation"])
+    return e, f, st
+
+
+@pytest.mark.parametrize("tile", [37, 64, 135])
+def test_tiled_plan_matches_untiled_tiny(tiny_model_path, tile):
+    """Three-sweep tiled plan (mace_kokkos_evaluate.cpp:755-1148) against the
+    untiled direct plan on the same graph (test_dual_layer_fixed_workspace.py:
+    106-128 compares the two at rtol 2e-4 / atol 2e-5 in FP32)."""
+    from symmetrix.mace_kokkos import MACEKokkosFloat
+    s = _system("tiny")
+    a = MACEKokkosFloat(tiny_model_path)
+    a.set_execution_plan_request("speed")
+    types = np.array([{8: 0, 22: 1, 38: 2}[int(z)] for z in s["numbers"]], np.int32)
+    e0, f0, s0 = _run(a, s, types)
+    assert a.execution_plan.startswith("direct ")
+    b = MACEKokkosFloat(tiny_model_path)
+    b.set_execution_plan_request("capacity", tile)
+    e1, f1, s1 = _run(b, s, types)
+    assert b.execution_plan.startswith("direct-tiled")
+    np.testing.assert_array_equal(e1, e0)
+    np.testing.assert_allclose(f1, f0, rtol=0, atol=1e-7)
+    np.testing.assert_allclose(s1, s0, rtol=0, atol=1e-9)
+    with pytest.raises(RuntimeError):
+        b.node_forces  # directed forces are not retained by the tiled plan
+
+
+def test_tiled_plan_medium_against_oracle(medium_model_path):
+    from symmetrix.mace_kokkos import MACEKokkosFloat
+    ora = _oracle()
+    s = _system("medium")
+    om = ora.OracleModel(medium_model_path)
+    ref = ora.evaluate_system(om, s, skin=0.5)
+    ev = MACEKokkosFloat(medium_model_path)
+    ev.set_execution_plan_request("capacity", 1024)
+    e, f, st = _run(ev, s, om.types_of(s["numbers"]))
+    assert "tiles=5" in ev.execution_plan
+    _assert_efs(ref, e, f, st, len(e))
+
+
+def test_host_edge_vectors_path(tiny_model_path):
+    """compute_node_energies_forces with host xyz/r (token 0) equals the
+    prepared-positions path on the same graph."""
+    from symmetrix.mace_kokkos import MACEKokkosFloat
+    ora = _oracle()
+    s = _system("tiny")
+    om = ora.OracleModel(tiny_model_path)
+    ref = ora.evaluate_system(om, s, skin=0.5)
+    g = ref["graph"]
+    types = om.types_of(s["numbers"])
+    ev = MACEKokkosFloat(tiny_model_path)
+    ev.compute_node_energies_forces(len(types), types, g["num_neigh"], g["sources"], types[g["sources"]],
+                                    ref["xyz"], ref["r"])
+    e = ev.node_energies
+    nf = ev.node_forces.reshape(-1, 3)
+    f = ev._reduce_atom_forces(len(types), g["receivers"], g["sources"], 0)
+    assert abs(e.sum() - ref["energy"]) / len(e) < E_TOL
+    assert np.max(np.abs(f - ref["forces"])) < F_TOL
+    assert np.max(np.abs(nf - ref["node_forces"])) < 1e-5
