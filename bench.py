@@ -58,7 +58,12 @@ def model_counts(path):
 
 
 def hip_lib():
-    return ctypes.CDLL("libamdhip64.so")
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    hip.hipFree.argtypes = [ctypes.c_void_p]
+    hip.hipMemGetInfo.argtypes = [ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)]
+    return hip
 
 
 def device_copy_of(hip, a):
@@ -114,17 +119,63 @@ def cpu_baseline(model_path, system, cutoff, skin, max_seconds=25.0):
             "sample": "medium workload (5000 atoms, 496k edges), %d warm call(s) after 1 warm-up, median" % len(times)}
 
 
+def capacity(n, md_steps, tile_receivers):
+    """the medium model in the tiled plan on an n^3
+    SrTiO3 supercell; a velocity-Verlet NVE run of md_steps at 1 fs."""
+    from symmetrix import md, random_model, systems
+    from symmetrix.mace_kokkos import MACEKokkosFloat
+
+    hip = hip_lib()
+    free0, total = ctypes.c_size_t(), ctypes.c_size_t()
+    hip.hipMemGetInfo(ctypes.byref(free0), ctypes.byref(total))
+    def note(msg):
+        print("[capacity] %s" % msg, file=sys.stderr, flush=True)
+
+    model_path = random_model.cached_model("medium")
+    system = systems.srtio3_supercell(n, sigma=0.05, seed=0)
+    note("system n=%d: %d atoms" % (n, len(system["numbers"])))
+    ev = MACEKokkosFloat(model_path)
+    ev.set_execution_plan_request("capacity", tile_receivers)
+    t0 = time.perf_counter()
+    run = md.NVE(ev, system, skin=0.5, temperature=300.0, seed=0)
+    first_s = time.perf_counter() - t0
+    note("graph + first call %.1f s, %d edges, %s" % (first_s, run.num_edges, ev.execution_plan))
+    free1 = ctypes.c_size_t()
+    hip.hipMemGetInfo(ctypes.byref(free1), ctypes.byref(total))
+    per_step, trace = run.run(md_steps, dt_fs=1.0,
+                              progress=lambda k, e: note("step %d total energy %.6f eV" % (k, e)))
+    n_atoms = len(system["numbers"])
+    out = {
+        "metric": "tiled capacity: atoms evaluated (FP32 E+F, 1 MI355X) and us/atom/step of 1 fs NVE",
+        "atoms": n_atoms, "supercell": n, "edges": int(run.num_edges), "plan": ev.execution_plan,
+        "md_steps": md_steps, "us_per_atom_step": round(per_step * 1e6 / n_atoms, 4),
+        "first_call_s": round(first_s, 2), "graph_rebuilds": run.rebuilds,
+        "device_memory_used_GiB": round((free0.value - free1.value) / 2**30, 2),
+        "device_memory_total_GiB": round(total.value / 2**30, 2),
+        "energy_drift_eV_per_atom": (trace[-1] - trace[0]) / n_atoms,
+        "reference": {"atoms": 11240455, "hardware": "A100 80 GB", "mode": "tiled streaming"},
+    }
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--capacity", type=int, default=0, metavar="N",
+                    help="run the tiled capacity config on an N^3 SrTiO3 supercell instead")
+    ap.add_argument("--md-steps", type=int, default=20)
+    ap.add_argument("--tile-receivers", type=int, default=32768)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures the single-GPU path only: this build runs on one MI355X and "
               "has no multi-GPU (halo-exchange) path; run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
+    if args.capacity:
+        capacity(args.capacity, args.md_steps, args.tile_receivers)
+        return
 
     from symmetrix import random_model, systems
     from symmetrix.mace_kokkos import MACEKokkosFloat

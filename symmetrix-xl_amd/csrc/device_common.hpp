@@ -10,6 +10,10 @@
 namespace smx {
 
 constexpr int kWave = 64;
+// Edge ids are int32 (the reference's cardinality guard,
+// mace_kokkos_runtime.cpp:199); the margin keeps strided int loops over edge
+// ranges (stride <= 4096) from overflowing.
+constexpr long long kMaxEdges = 2147483647LL - 4096;
 constexpr int kXcds = 8;
 
 inline void hip_check(hipError_t e, const char* what) {

@@ -556,7 +556,7 @@ struct Evaluator {
     std::uint64_t prepare_graph_host(int n, const int* node_types, const int* num_neigh, std::int64_t num_edges,
                                      const int* neigh, const int* neigh_types) {
         if (n < 0) throw std::invalid_argument("num_nodes must be non-negative");
-        if (num_edges < 0 || num_edges > INT_MAX)
+        if (num_edges < 0 || num_edges > kMaxEdges)
             throw std::invalid_argument("edge count exceeds the 32-bit graph limit");
         validate_types(n, node_types);
         std::vector<int> off(n + 1, 0);
@@ -564,7 +564,7 @@ struct Evaluator {
         for (int i = 0; i < n; ++i) {
             if (num_neigh[i] < 0) throw std::invalid_argument("num_neigh must be non-negative");
             total += num_neigh[i];
-            if (total > INT_MAX) throw std::invalid_argument("edge count exceeds the 32-bit graph limit");
+            if (total > kMaxEdges) throw std::invalid_argument("edge count exceeds the 32-bit graph limit");
             off[i + 1] = static_cast<int>(total);
         }
         if (total != num_edges) throw std::invalid_argument("num_neigh does not sum to the number of edges");

@@ -560,7 +560,7 @@ void build_neighbor_list(int N, const double* positions_host, const double* cell
             SMX_LAUNCH_CHECK("neighbor_count");
         }
         const long long E = device_exclusive_scan(counts, eoff, N, s);
-        if (E > INT_MAX) throw std::length_error("neighbor edge count exceeds the 32-bit graph limit");
+        if (E > kMaxEdges) throw std::length_error("neighbor edge count exceeds the 32-bit graph limit");
         out.num_edges = E;
         out.num_neigh = dev_alloc<int>(N);
         out.offsets = dev_alloc<int>(N + 1);

@@ -535,7 +535,8 @@ __global__ __launch_bounds__(C) void k_readout(
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ int lower_edge(const int* __restrict__ sedges, int lo, int hi, long long key) {
     while (lo < hi) {
-        const int mid = (lo + hi) >> 1;
+        // lo + hi can exceed 2^31 when the graph has more than 2^30 edges
+        const int mid = lo + ((hi - lo) >> 1);
         if (sedges[mid] < key)
             lo = mid + 1;
         else

@@ -18,20 +18,17 @@ _SRTIO3_BASIS = [(38, (0.0, 0.0, 0.0)), (22, (0.5, 0.5, 0.5)),
 
 
 def srtio3_supercell(n, sigma=0.05, seed=0, a=SRTIO3_A):
-    """Cubic SrTiO3 n x n x n supercell (5 n^3 atoms) with Gaussian
-    displacements of standard deviation ``sigma`` (Å)."""
-    numbers = []
-    frac = []
-    for ix in range(n):
-        for iy in range(n):
-            for iz in range(n):
-                for z, (fx, fy, fz) in _SRTIO3_BASIS:
-                    numbers.append(z)
-                    frac.append((ix + fx, iy + fy, iz + fz))
-    positions = np.asarray(frac, dtype=np.float64) * a
+    """Cubic SrTiO3 n x n x n supercell (5 n^3 atoms, cell order ix, iy, iz,
+    then the basis) with Gaussian displacements of standard deviation
+    ``sigma`` (Å) drawn from ``numpy.random.default_rng(seed)``."""
+    numbers = np.array([z for z, _ in _SRTIO3_BASIS], dtype=np.int64)
+    basis = np.array([f for _, f in _SRTIO3_BASIS], dtype=np.float64)
+    r = np.arange(n, dtype=np.float64)
+    cells = np.stack(np.meshgrid(r, r, r, indexing="ij"), axis=-1).reshape(-1, 3)
+    positions = (cells[:, None, :] + basis[None, :, :]).reshape(-1, 3) * a
     rng = np.random.default_rng(seed)
     positions = positions + sigma * rng.normal(size=positions.shape)
-    return {"numbers": np.asarray(numbers, dtype=np.int64),
+    return {"numbers": np.tile(numbers, n ** 3),
             "positions": positions,
             "cell": np.eye(3) * (a * n),
             "pbc": np.array([True, True, True])}
