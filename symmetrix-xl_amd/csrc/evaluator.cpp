@@ -189,7 +189,8 @@ private:
 struct PlanSet {
     std::vector<GemmTile> tiles;
     std::vector<std::size_t> tile_begin;  // per receiver tile: first GemmTile
-    DevBuf d_tiles;
+    std::vector<int> rows;                // packed (local node << 4 | m)
+    DevBuf d_tiles, d_rows;
 };
 
 }  // namespace
@@ -224,7 +225,9 @@ struct Evaluator {
     PlanSet ps_a0, ps_h1, ps_a1f, ps_a1r;
     std::vector<int> h_node_list;
     std::vector<std::size_t> node_list_begin;
-    DevBuf d_node_list, d_touched;
+    std::vector<NodeBatch> h_batches;
+    std::vector<std::size_t> batch_begin;
+    DevBuf d_node_list, d_batches, d_touched;
     std::vector<std::size_t> touched_begin;
     int max_tile_nr = 0;
     std::int64_t max_tile_ne = 0;
@@ -234,7 +237,7 @@ struct Evaluator {
     DevBuf d_wfrac, d_images, d_ref_positions, d_disp, d_positions;
     // per call
     DevBuf d_xyz, d_r, d_invalid;
-    DevBuf w_erec, w_Phi0, w_A0, w_M0, w_Phi1, w_A1, w_A1_adj, w_dPhi1, w_Wsrc, w_M0_adj, w_A0_adj, w_Phi0_adj,
+    DevBuf w_erec, w_Phi0, w_A0, w_M0, w_Phi1, w_A1, w_A1_adj, w_M1, w_dPhi1, w_Wsrc, w_M0_adj, w_A0_adj, w_Phi0_adj,
         w_node_forces;
     DevBuf g_H1, g_H1_adj, g_xaff, g_direct, d_node_energies, d_atom_forces, d_virial, d_stress, d_stress_partial,
         d_total;
@@ -252,7 +255,11 @@ struct Evaluator {
             lo != hm.path_lo)
             throw std::domain_error("the model's R1 paths have no compiled kernel set (l_max " +
                                     std::to_string(hm.l_max) + ", L_max " + std::to_string(hm.L_max) + ")");
-        ks = make_kernel_set(hm.C, hm.l_max, hm.L_max);
+        if (hm.readout_hidden > kMaxReadoutHidden)
+            throw std::domain_error("readout MLP wider than " + std::to_string(kMaxReadoutHidden) +
+                                    " hidden units has no compiled kernel");
+        if (hm.C % 16 != 0) throw std::domain_error("channel counts must be multiples of 16");
+        ks = make_kernel_set(hm.C, hm.l_max, hm.L_max, hm.m0_terms, hm.m0_term_offset, hm.m1_terms);
         if (!ks)
             throw std::domain_error("no kernel set is compiled for " + std::to_string(hm.C) + " channels, l_max " +
                                     std::to_string(hm.l_max) + ", L_max " + std::to_string(hm.L_max));
@@ -293,18 +300,28 @@ struct Evaluator {
         dm.R0c = reinterpret_cast<const float4*>(put(hm.R0_coef));
         dm.R1c = reinterpret_cast<const float4*>(put(hm.R1_coef));
         dm.H0 = put(hm.H0);
-        dm.A0_w = put(hm.A0_w);
-        dm.A0_wt = put(hm.A0_wt);
+        const std::size_t a0_blocks = static_cast<std::size_t>(hm.num_elements) * (hm.l_max + 1);
+        dm.A0_w = put(swizzled(hm.A0_w, a0_blocks, hm.C, hm.C));
+        dm.A0_wt = put(swizzled(hm.A0_wt, a0_blocks, hm.C, hm.C));
         dm.m0_terms = put(hm.m0_terms);
         dm.m0_toff = put(hm.m0_term_offset);
         dm.m0_term_offset = hm.m0_term_offset;
         dm.T0 = static_cast<int>(hm.m0_terms.size());
         dm.m0_coef = put(hm.m0_coef);
-        dm.H1_w = put(hm.H1_w);
-        dm.H1_wt = put(hm.H1_wt);
+        dm.H1_w = put(swizzled(hm.H1_w, hm.L_max + 1, hm.C, hm.C));
+        dm.H1_wt = put(swizzled(hm.H1_wt, hm.L_max + 1, hm.C, hm.C));
         dm.cg = put(hm.cg_dense);
-        dm.A1_w = put(hm.A1_w);
-        dm.A1_wt = put(hm.A1_wt);
+        {
+            std::vector<float> w(hm.A1_w.size()), wt(hm.A1_wt.size());
+            for (int l = 0; l <= hm.l_max; ++l) {
+                const int K = hm.num_e[l] * hm.C;
+                if (K == 0) continue;
+                swizzle_gemm_weights(hm.A1_w.data() + hm.A1_offset[l], K, hm.C, w.data() + hm.A1_offset[l]);
+                swizzle_gemm_weights(hm.A1_wt.data() + hm.A1_offset[l], hm.C, K, wt.data() + hm.A1_offset[l]);
+            }
+            dm.A1_w = put(w);
+            dm.A1_wt = put(wt);
+        }
         dm.A1_offset = hm.A1_offset;
         dm.num_e = hm.num_e;
         dm.lme_base = hm.lme_base;
@@ -321,6 +338,14 @@ struct Evaluator {
         dm.hidden = hm.readout_hidden;
         dm.readout_scale = hm.readout_scale;
         dm.E0 = put(hm.atomic_energies);
+    }
+
+    // blocks [count][K][N] of a weight array in the MFMA operand order
+    static std::vector<float> swizzled(const std::vector<float>& w, std::size_t count, int K, int N) {
+        std::vector<float> out(w.size());
+        const std::size_t blk = static_cast<std::size_t>(K) * N;
+        for (std::size_t b = 0; b < count; ++b) swizzle_gemm_weights(w.data() + b * blk, K, N, out.data() + b * blk);
+        return out;
     }
 
     // Weight groups of the node linears: A0 per (type, l), H1 per l, A1 per
@@ -360,7 +385,7 @@ struct Evaluator {
     // Bytes of the untiled plan for a graph (workspace high-water).
     std::size_t untiled_bytes(std::int64_t n, std::int64_t e) const {
         const std::size_t C = hm.C, NY = hm.num_lm, NH = hm.num_LM, NLME = hm.num_lme;
-        const std::size_t node = (6 * NY + 4 * NH + 2 * NLME + 2) * C * 4 + 200;
+        const std::size_t node = (6 * NY + 4 * NH + 2 * NLME + 3) * C * 4 + 200;
         const std::size_t edge = (ks->record_floats() + NH * C) * 4 + 24 + 32 + 24;
         return node * n + edge * e;
     }
@@ -381,7 +406,7 @@ struct Evaluator {
 
     std::size_t workspace_bytes() const {
         std::size_t b = 0;
-        for (const DevBuf* x : {&w_erec, &w_Phi0, &w_A0, &w_M0, &w_Phi1, &w_A1, &w_A1_adj, &w_dPhi1, &w_Wsrc,
+        for (const DevBuf* x : {&w_erec, &w_Phi0, &w_A0, &w_M0, &w_Phi1, &w_A1, &w_A1_adj, &w_M1, &w_dPhi1, &w_Wsrc,
                                 &w_M0_adj, &w_A0_adj, &w_Phi0_adj, &w_node_forces, &d_xyz, &d_r})
             b += x->capacity();
         return b;
@@ -405,16 +430,20 @@ struct Evaluator {
             max_tile_nr = std::max(max_tile_nr, t.nr);
             max_tile_ne = std::max(max_tile_ne, t.ne);
         }
-        // node lists (local rows sorted by type) and node-linear tiles
+        // node lists (local rows sorted by type), readout batches and node-linear tiles
         h_node_list.clear();
         node_list_begin.clear();
+        h_batches.clear();
+        batch_begin.clear();
         for (PlanSet* p : {&ps_a0, &ps_h1, &ps_a1f, &ps_a1r}) {
             p->tiles.clear();
             p->tile_begin.clear();
+            p->rows.clear();
         }
         for (const auto& t : tiles) {
             const std::size_t base = h_node_list.size();
             node_list_begin.push_back(base);
+            batch_begin.push_back(h_batches.size());
             std::vector<int> order(t.nr);
             std::iota(order.begin(), order.end(), 0);
             std::stable_sort(order.begin(), order.end(), [&](int a, int b) {
@@ -422,38 +451,45 @@ struct Evaluator {
             });
             h_node_list.insert(h_node_list.end(), order.begin(), order.end());
             for (PlanSet* p : {&ps_a0, &ps_h1, &ps_a1f, &ps_a1r}) p->tile_begin.push_back(p->tiles.size());
-            auto add = [](PlanSet& P, int group, int m, int begin, int end) {
-                for (int s = begin; s < end; s += 16) P.tiles.push_back(GemmTile{s, std::min(16, end - s), group, m});
+            // rows (node order[a..b), m in [0, 2l+1)) of one group, cut into wave tiles
+            auto add = [&](PlanSet& P, int group, int l, int a, int b) {
+                const int start = static_cast<int>(P.rows.size());
+                for (int m = 0; m < 2 * l + 1; ++m)
+                    for (int q = a; q < b; ++q) P.rows.push_back(order[q] << 4 | m);
+                const int end = static_cast<int>(P.rows.size());
+                for (int s0 = start; s0 < end; s0 += kGemmRows)
+                    P.tiles.push_back(GemmTile{s0, std::min(kGemmRows, end - s0), group});
             };
             for (int p = 0; p < t.nr;) {
                 int q = p;
                 const int type = h_node_types[t.r0 + order[p]];
                 while (q < t.nr && h_node_types[t.r0 + order[q]] == type) ++q;
-                for (int l = 0; l <= hm.l_max; ++l)
-                    for (int m = 0; m < 2 * l + 1; ++m) add(ps_a0, type * (hm.l_max + 1) + l, m, p, q);
+                for (int l = 0; l <= hm.l_max; ++l) add(ps_a0, type * (hm.l_max + 1) + l, l, p, q);
+                for (int s0 = p; s0 < q; s0 += kReadoutBatch)
+                    h_batches.push_back(NodeBatch{static_cast<int>(s0), std::min(kReadoutBatch, q - s0)});
                 p = q;
             }
-            for (int l = 0; l <= hm.L_max; ++l)
-                for (int m = 0; m < 2 * l + 1; ++m) add(ps_h1, l, m, 0, t.nr);
+            for (int l = 0; l <= hm.L_max; ++l) add(ps_h1, l, l, 0, t.nr);
             for (int l = 0; l <= hm.l_max; ++l) {
                 if (hm.num_e[l] == 0) continue;
-                for (int m = 0; m < 2 * l + 1; ++m) {
-                    add(ps_a1f, l, m, 0, t.nr);
-                    add(ps_a1r, l, m, 0, t.nr);
-                }
+                add(ps_a1f, l, l, 0, t.nr);
+                add(ps_a1r, l, l, 0, t.nr);
             }
         }
+        batch_begin.push_back(h_batches.size());
         for (PlanSet* p : {&ps_a0, &ps_h1, &ps_a1f, &ps_a1r}) {
             p->tile_begin.push_back(p->tiles.size());
             upload(p->d_tiles, p->tiles, stream);
+            upload(p->d_rows, p->rows, stream);
         }
         upload(d_node_list, h_node_list, stream);
+        upload(d_batches, h_batches, stream);
         auto view = [&](const PlanSet& P, std::size_t ti, const DevBuf& groups, int max_n) {
             GemmPlan g;
             g.tiles = P.d_tiles.as<GemmTile>() + P.tile_begin[ti];
             g.num_tiles = static_cast<int>(P.tile_begin[ti + 1] - P.tile_begin[ti]);
             g.groups = groups.as<GemmGroup>();
-            g.node_list = d_node_list.as<int>() + node_list_begin[ti];
+            g.rows = P.d_rows.as<int>();
             g.max_n = max_n;
             return g;
         };
@@ -462,6 +498,9 @@ struct Evaluator {
             tiles[ti].h1 = view(ps_h1, ti, d_groups_h1, max_n_h1);
             tiles[ti].a1f = view(ps_a1f, ti, d_groups_a1f, max_n_a1f);
             tiles[ti].a1r = view(ps_a1r, ti, d_groups_a1r, max_n_a1r);
+            tiles[ti].node_list = d_node_list.as<int>() + node_list_begin[ti];
+            tiles[ti].batches = d_batches.as<NodeBatch>() + batch_begin[ti];
+            tiles[ti].num_batches = static_cast<int>(batch_begin[ti + 1] - batch_begin[ti]);
         }
         // touched sources of every tile (tiled plan only)
         touched_begin.assign(1, 0);
@@ -501,6 +540,7 @@ struct Evaluator {
         ws.Phi1 = f(w_Phi1, tn * NLME * C);
         ws.A1 = f(w_A1, tn * NY * C);
         ws.A1_adj = f(w_A1_adj, tn * NY * C);
+        ws.M1 = f(w_M1, tn * C);
         ws.dPhi1 = f(w_dPhi1, tn * NLME * C);
         ws.Wsrc = f(w_Wsrc, te * NH * C);
         ws.M0_adj = f(w_M0_adj, tn * NH * C);
@@ -844,6 +884,7 @@ struct Evaluator {
 
     std::string plan_description() const {
         std::string s = tiled ? "direct-tiled" : "direct";
+        s += std::string(" polynomials=") + ks->polynomial_mode();
         s += " tiles=" + std::to_string(tiles.size()) + " max_tile_receivers=" + std::to_string(max_tile_nr) +
              " max_tile_edges=" + std::to_string(max_tile_ne);
         return s;

@@ -20,9 +20,11 @@
 #include <algorithm>
 #include <stdexcept>
 #include <string>
+#include <type_traits>
 
 #include "device_common.hpp"
 #include "kernels.hpp"
+#include "product_tables.hpp"
 #include "shapes.hpp"
 
 namespace smx {
@@ -299,7 +301,11 @@ __global__ __launch_bounds__(C) void k_r1_reverse(int r0, long long e0, const in
         const int c1 = min(c0 + kForceChunk, eb);
         for (int e = c0; e < c1; ++e) {
             const float* rec = erec + static_cast<std::size_t>(e - e0) * S::REC;
+            float* wdst = Wsrc + static_cast<std::size_t>(e - e0) * NH * C + k;
             if (!edge_active(rec)) {
+                // inactive edges contribute zero to their source's adjoint
+#pragma unroll
+                for (int q = 0; q < NH; ++q) wdst[q * C] = 0.0f;
                 sink.zero(e - c0);
                 continue;
             }
@@ -340,7 +346,6 @@ __global__ __launch_bounds__(C) void k_r1_reverse(int r0, long long e0, const in
                     b2 += t * rec[S::REC_DY + 2 * NY + lm1];
                 });
             });
-            float* wdst = Wsrc + static_cast<std::size_t>(e - e0) * NH * C + k;
 #pragma unroll
             for (int q = 0; q < NH; ++q) wdst[q * C] = W[q];
             const float u0 = rec[S::REC_U], u1 = rec[S::REC_U + 1], u2 = rec[S::REC_U + 2];
@@ -351,31 +356,56 @@ __global__ __launch_bounds__(C) void k_r1_reverse(int r0, long long e0, const in
 }
 
 // H1_adj[s] = sum over the edges leaving s (source transpose order) of W_e,
-// accumulated in FP64 like the reference's source-adjoint accumulator.
+// accumulated in FP64 like the reference's source-adjoint accumulator
+// (inactive edges carry W_e = 0).  Four edges are loaded per step so that
+// their independent 2 KB rows are in flight together; the sum keeps the
+// source-transpose order.
+template <int C, int NH>
+__device__ __forceinline__ void gather_source_rows(const int* __restrict__ sedges, int t0, int t1, long long e_base,
+                                                   const float* __restrict__ Wsrc, int k, double* acc) {
+    int t = t0;
+    for (; t + 4 <= t1; t += 4) {
+        float w[4][NH];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const float* row = Wsrc + static_cast<std::size_t>(sedges[t + u] - e_base) * NH * C + k;
+#pragma unroll
+            for (int q = 0; q < NH; ++q) w[u][q] = row[q * C];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int q = 0; q < NH; ++q) acc[q] += static_cast<double>(w[u][q]);
+    }
+    for (; t < t1; ++t) {
+        const float* row = Wsrc + static_cast<std::size_t>(sedges[t] - e_base) * NH * C + k;
+#pragma unroll
+        for (int q = 0; q < NH; ++q) acc[q] += static_cast<double>(row[q * C]);
+    }
+}
+
 template <int C, int NH>
 __global__ __launch_bounds__(C) void k_source_gather(const int* __restrict__ soff, const int* __restrict__ sedges,
-                                                     const float* __restrict__ erec, int rec_floats,
                                                      const float* __restrict__ Wsrc, float* __restrict__ H1_adj) {
     const int s = xcd_remap(blockIdx.x, gridDim.x);
     const int k = threadIdx.x;
     double acc[NH];
 #pragma unroll
     for (int q = 0; q < NH; ++q) acc[q] = 0.0;
-    const int q0 = soff[s], q1 = soff[s + 1];
-    for (int t = q0; t < q1; ++t) {
-        const int e = sedges[t];
-        if (!edge_active(erec + static_cast<std::size_t>(e) * rec_floats)) continue;
-        const float* w = Wsrc + static_cast<std::size_t>(e) * NH * C + k;
-#pragma unroll
-        for (int q = 0; q < NH; ++q) acc[q] += static_cast<double>(w[q * C]);
-    }
+    gather_source_rows<C, NH>(sedges, soff[s], soff[s + 1], 0, Wsrc, k, acc);
 #pragma unroll
     for (int q = 0; q < NH; ++q) H1_adj[(static_cast<std::size_t>(s) * NH + q) * C + k] = static_cast<float>(acc[q]);
 }
 
 // ---------------------------------------------------------------------------
-// Product basis (symmetric contraction) polynomials.  Variables live in LDS
-// (column k per lane) so the wave-uniform monomial table can index them.
+// Product basis (symmetric contraction) polynomials.  Two forms:
+//  * unrolled: the monomial list is a compiled table (ProductTable), every
+//    term is straight-line code on the variables held in registers;
+//  * table-driven: variables live in LDS (column k per lane) so the
+//    wave-uniform monomial list in HBM can index them.
+// Both sum the terms of an output in list order; the gradient follows the
+// product rule in the reference's order (the coefficient times the other
+// factors in turn, multivariate_polynomial.cpp:60-131).
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float monomial(const float* xs, int C, int k, int pk) {
     const int deg = pk >> 24;
@@ -385,8 +415,7 @@ __device__ __forceinline__ float monomial(const float* xs, int C, int k, int pk)
     return prod;
 }
 
-// gs[v] += d f / d x_v for one term with coefficient c (product rule in the
-// reference's order: the coefficient times the other factors in turn).
+// gs[v] += d f / d x_v for one term with coefficient c
 __device__ __forceinline__ void monomial_grad(const float* xs, float* gs, int C, int k, int pk, float c) {
     const int deg = pk >> 24;
     const int v0 = pk & 0xff, v1 = (pk >> 8) & 0xff, v2 = (pk >> 16) & 0xff;
@@ -404,8 +433,104 @@ __device__ __forceinline__ void monomial_grad(const float* xs, float* gs, int C,
     }
 }
 
+template <std::int32_t PK>
+__device__ __forceinline__ float monomial_ct(const float* x) {
+    constexpr int deg = PK >> 24, v0 = PK & 0xff, v1 = (PK >> 8) & 0xff, v2 = (PK >> 16) & 0xff;
+    if constexpr (deg == 1)
+        return x[v0];
+    else if constexpr (deg == 2)
+        return x[v0] * x[v1];
+    else
+        return x[v0] * x[v1] * x[v2];
+}
+
+template <std::int32_t PK>
+__device__ __forceinline__ void monomial_grad_ct(const float* x, float* g, float c) {
+    constexpr int deg = PK >> 24, v0 = PK & 0xff, v1 = (PK >> 8) & 0xff, v2 = (PK >> 16) & 0xff;
+    if constexpr (deg == 1) {
+        g[v0] += c;
+    } else if constexpr (deg == 2) {
+        g[v0] += c * x[v1];
+        g[v1] += c * x[v0];
+    } else {
+        g[v0] += c * x[v1] * x[v2];
+        g[v1] += c * x[v0] * x[v2];
+        g[v2] += c * x[v0] * x[v1];
+    }
+}
+
+// f = sum_t c_t mono_t(x) over the compiled terms [B, E); cf points at the
+// lane's coefficient of term 0 (stride C between terms).
+template <class TAB, int B, int E, int C>
+__device__ __forceinline__ float poly_ct(const float* x, const float* __restrict__ cf) {
+    float f = 0.0f;
+    static_range<B, E>([&](auto tc) {
+        constexpr int t = tc;
+        f += cf[t * C] * monomial_ct<TAB::terms[t]>(x);
+    });
+    return f;
+}
+
+template <class TAB, int B, int E, int C>
+__device__ __forceinline__ void poly_grad_ct(const float* x, const float* __restrict__ cf, float* g) {
+    static_range<B, E>([&](auto tc) {
+        constexpr int t = tc;
+        monomial_grad_ct<TAB::terms[t]>(x, g, cf[t * C]);
+    });
+}
+
 // Rows li of the tile workspace belong to receiver i = r0 + li; graph-wide
 // arrays (types, scalar capture x, direct adjoint, energies) use i.
+template <int C, int NY, int NH, class TAB>
+__global__ __launch_bounds__(C) void k_m0_forward_ct(int r0, const int* __restrict__ types,
+                                                     const float* __restrict__ A0, const float* __restrict__ coef,
+                                                     float* __restrict__ M0, float* __restrict__ xaff) {
+    const int li = blockIdx.x;
+    const int i = r0 + li;
+    const int k = threadIdx.x;
+    float x[NY];
+#pragma unroll
+    for (int v = 0; v < NY; ++v) x[v] = A0[(static_cast<std::size_t>(li) * NY + v) * C + k];
+    const float* cf = coef + static_cast<std::size_t>(types[i]) * TAB::NT * C + k;
+    static_range<0, NH>([&](auto LMc) {
+        constexpr int LM = LMc;
+        const float f = poly_ct<TAB, TAB::offset[LM], TAB::offset[LM + 1], C>(x, cf);
+        M0[(static_cast<std::size_t>(li) * NH + LM) * C + k] = f;
+        // v4 "m0_composite" readout basis: x = M0[i, 0, :] (h1_affine_schema.hpp)
+        if constexpr (LM == 0) xaff[static_cast<std::size_t>(i) * C + k] = f;
+    });
+}
+
+template <int C, int NY, int NH, class TAB>
+__global__ __launch_bounds__(C) void k_m0_reverse_ct(int r0, const int* __restrict__ types,
+                                                     const float* __restrict__ A0, const float* __restrict__ M0_adj,
+                                                     const float* __restrict__ direct, const float* __restrict__ coef,
+                                                     float* __restrict__ A0_adj) {
+    const int li = blockIdx.x;
+    const int i = r0 + li;
+    const int k = threadIdx.x;
+    float x[NY], acc[NY];
+#pragma unroll
+    for (int v = 0; v < NY; ++v) {
+        x[v] = A0[(static_cast<std::size_t>(li) * NY + v) * C + k];
+        acc[v] = 0.0f;
+    }
+    const float* cf = coef + static_cast<std::size_t>(types[i]) * TAB::NT * C + k;
+    static_range<0, NH>([&](auto LMc) {
+        constexpr int LM = LMc;
+        float adj = M0_adj[(static_cast<std::size_t>(li) * NH + LM) * C + k];
+        if constexpr (LM == 0) adj += direct[static_cast<std::size_t>(i) * C + k];
+        float g[NY];
+#pragma unroll
+        for (int v = 0; v < NY; ++v) g[v] = 0.0f;
+        poly_grad_ct<TAB, TAB::offset[LM], TAB::offset[LM + 1], C>(x, cf, g);
+#pragma unroll
+        for (int v = 0; v < NY; ++v) acc[v] += g[v] * adj;
+    });
+#pragma unroll
+    for (int v = 0; v < NY; ++v) A0_adj[(static_cast<std::size_t>(li) * NY + v) * C + k] = acc[v];
+}
+
 template <int C, int NY, int NH>
 __global__ __launch_bounds__(C) void k_m0_forward(int r0, const int* __restrict__ types, const float* __restrict__ A0,
                                                   const std::int32_t* __restrict__ terms, const int* __restrict__ toff,
@@ -424,7 +549,6 @@ __global__ __launch_bounds__(C) void k_m0_forward(int r0, const int* __restrict_
         float f = 0.0f;
         for (int t = begin; t < end; ++t) f += cf[static_cast<std::size_t>(t) * C] * monomial(xs, C, k, terms[t]);
         M0[(static_cast<std::size_t>(li) * NH + LM) * C + k] = f;
-        // v4 "m0_composite" readout basis: x = M0[i, 0, :] (h1_affine_schema.hpp)
         if (LM == 0) xaff[static_cast<std::size_t>(i) * C + k] = f;
     }
 }
@@ -461,70 +585,202 @@ __global__ __launch_bounds__(C) void k_m0_reverse(int r0, const int* __restrict_
     for (int v = 0; v < NY; ++v) A0_adj[(static_cast<std::size_t>(li) * NY + v) * C + k] = acc[v];
 }
 
-// M1, H2 (FP64), readouts (FP64) and their adjoints for one node:
+// M1 of one node and channel, and (with G) its gradient dM1/dA1 (unscaled).
+// TAB is a compiled ProductTable or void for the table-driven form (then
+// xs/gs are the node's variables and gradient in LDS, column k).
+template <class TAB, int C, int NY>
+struct M1Poly {
+    __device__ __forceinline__ static float value(const float* __restrict__ A1row, const float* __restrict__ cf,
+                                                  const std::int32_t* __restrict__, int, float*, int k) {
+        float x[NY];
+#pragma unroll
+        for (int v = 0; v < NY; ++v) x[v] = A1row[v * C + k];
+        return poly_ct<TAB, 0, TAB::NT, C>(x, cf);
+    }
+    __device__ __forceinline__ static void grad(const float* __restrict__ A1row, const float* __restrict__ cf,
+                                                const std::int32_t* __restrict__, int, float*, float*, int k,
+                                                float* g) {
+        float x[NY];
+#pragma unroll
+        for (int v = 0; v < NY; ++v) {
+            x[v] = A1row[v * C + k];
+            g[v] = 0.0f;
+        }
+        poly_grad_ct<TAB, 0, TAB::NT, C>(x, cf, g);
+    }
+};
+
+template <int C, int NY>
+struct M1Poly<void, C, NY> {
+    __device__ __forceinline__ static float value(const float* __restrict__ A1row, const float* __restrict__ cf,
+                                                  const std::int32_t* __restrict__ terms, int T1, float* xs, int k) {
+#pragma unroll
+        for (int v = 0; v < NY; ++v) xs[v * C + k] = A1row[v * C + k];
+        float m = 0.0f;
+        for (int s = 0; s < T1; ++s) m += cf[static_cast<std::size_t>(s) * C] * monomial(xs, C, k, terms[s]);
+        return m;
+    }
+    __device__ __forceinline__ static void grad(const float* __restrict__ A1row, const float* __restrict__ cf,
+                                                const std::int32_t* __restrict__ terms, int T1, float* xs, float* gs,
+                                                int k, float* g) {
+#pragma unroll
+        for (int v = 0; v < NY; ++v) {
+            xs[v * C + k] = A1row[v * C + k];
+            gs[v * C + k] = 0.0f;
+        }
+        for (int s = 0; s < T1; ++s) monomial_grad(xs, gs, C, k, terms[s], cf[static_cast<std::size_t>(s) * C]);
+#pragma unroll
+        for (int v = 0; v < NY; ++v) g[v] = gs[v * C + k];
+    }
+};
+
+// M1 of every receiver and its gradient dM1/dA1 (unscaled), one receiver
+// per workgroup: M1[li,k] and grad[li,v,k] (the gradient is scaled by the M1
+// adjoint in k_readout once the readout reverse has produced it).
+template <int C, int NY, class M1TAB>
+__global__ __launch_bounds__(C) void k_m1(int r0, const int* __restrict__ types, const float* __restrict__ A1,
+                                          const std::int32_t* __restrict__ m1_terms, int T1,
+                                          const float* __restrict__ m1_coef, float* __restrict__ M1,
+                                          float* __restrict__ grad) {
+    using Poly = M1Poly<M1TAB, C, NY>;
+    constexpr bool kLds = std::is_same_v<M1TAB, void>;
+    __shared__ float xs[kLds ? NY * C : 1], gs[kLds ? NY * C : 1];
+    const int li = blockIdx.x;
+    const int k = threadIdx.x;
+    const float* cf = m1_coef + static_cast<std::size_t>(types[r0 + li]) * T1 * C + k;
+    const float* row = A1 + static_cast<std::size_t>(li) * NY * C;
+    M1[static_cast<std::size_t>(li) * C + k] = Poly::value(row, cf, m1_terms, T1, xs, k);
+    float g[NY];
+    Poly::grad(row, cf, m1_terms, T1, xs, gs, k, g);
+#pragma unroll
+    for (int v = 0; v < NY; ++v) grad[(static_cast<std::size_t>(li) * NY + v) * C + k] = g[v];
+}
+
+// H2 (FP64), readouts (FP64) and their adjoints for a batch of up to RB
+// receivers of one type (the weights are read once per batch):
 //   E_i = E0[z] + q.x + MLP(H2), H2 = T_z^T x + W^T M1 (x = M0[i,0,:])
 //   direct = q + T_z H2_adj, A1_adj[v] = dM1/dA1_v * (W H2_adj)
-template <int C, int NY>
+// Readout MLP: hidden = SiLU*scale(W1 H2), E += W2 . hidden (mace.cpp:2600-2657).
+// On entry A1_adj holds the unscaled M1 gradient from k_m1.
+template <int C, int NY, int RB>
 __global__ __launch_bounds__(C) void k_readout(
-    int r0, const int* __restrict__ types, const float* __restrict__ A1, const float* __restrict__ xaff,
-    const std::int32_t* __restrict__ m1_terms, int T1, const float* __restrict__ m1_coef,
-    const float* __restrict__ H2_T, const float* __restrict__ H2_Tt, const float* __restrict__ H2_M1,
-    const float* __restrict__ H2_M1t, const double* __restrict__ q, const double* __restrict__ W1r,
-    const double* __restrict__ W2r, int hidden, double scale, const double* __restrict__ E0,
-    double* __restrict__ node_energies, float* __restrict__ direct, float* __restrict__ A1_adj) {
-    __shared__ float xs[NY * C];
-    __shared__ float gs[NY * C];
-    __shared__ double sx[C], sm1[C], sh2a[C];
-    __shared__ double sbuf[Lanes<C>::NW];
-    const int li = blockIdx.x;
-    const int i = r0 + li;
+    int r0, const NodeBatch* __restrict__ batches, const int* __restrict__ node_list, const int* __restrict__ types,
+    const float* __restrict__ M1, const float* __restrict__ xaff, const float* __restrict__ H2_T,
+    const float* __restrict__ H2_Tt, const float* __restrict__ H2_M1, const float* __restrict__ H2_M1t,
+    const double* __restrict__ q, const double* __restrict__ W1r, const double* __restrict__ W2r, int hidden,
+    double scale, const double* __restrict__ E0, double* __restrict__ node_energies, float* __restrict__ direct,
+    float* __restrict__ A1_adj) {
+    __shared__ double sx[RB][C], sm1[RB][C], sh[RB][C];
+    __shared__ double sz[RB][kMaxReadoutHidden + 1], sd[RB][kMaxReadoutHidden];
+    const NodeBatch b = batches[blockIdx.x];
     const int k = threadIdx.x;
-    const int t = types[i];
+    const int t = types[r0 + node_list[b.start]];
+    int li[RB];
 #pragma unroll
-    for (int v = 0; v < NY; ++v) {
-        xs[v * C + k] = A1[(static_cast<std::size_t>(li) * NY + v) * C + k];
-        gs[v * C + k] = 0.0f;
+    for (int n = 0; n < RB; ++n) {
+        li[n] = node_list[b.start + min(n, b.count - 1)];
+        const bool ok = n < b.count;
+        sm1[n][k] = ok ? static_cast<double>(M1[static_cast<std::size_t>(li[n]) * C + k]) : 0.0;
+        sx[n][k] = ok ? static_cast<double>(xaff[static_cast<std::size_t>(r0 + li[n]) * C + k]) : 0.0;
     }
-    const float* cf = m1_coef + static_cast<std::size_t>(t) * T1 * C + k;
-    float m1 = 0.0f;
-    for (int s = 0; s < T1; ++s) {
-        const float c = cf[static_cast<std::size_t>(s) * C];
-        const int pk = m1_terms[s];
-        m1 += c * monomial(xs, C, k, pk);
-        monomial_grad(xs, gs, C, k, pk, c);
-    }
-    const float xa = xaff[static_cast<std::size_t>(i) * C + k];
-    sx[k] = static_cast<double>(xa);
-    sm1[k] = static_cast<double>(m1);
     __syncthreads();
-    const float* T = H2_T + static_cast<std::size_t>(t) * C * C;
-    double h2 = 0.0;
-    for (int in = 0; in < C; ++in) h2 += static_cast<double>(T[in * C + k]) * sx[in];
-    for (int in = 0; in < C; ++in) h2 += static_cast<double>(H2_M1[in * C + k]) * sm1[in];
-    double e = E0[t] + block_sum<C>(q[k] * sx[k], sbuf);
-    double out = 0.0, h2a = 0.0;
-    for (int hd = 0; hd < hidden; ++hd) {
-        const double w1 = W1r[static_cast<std::size_t>(hd) * C + k];
-        const double z = block_sum<C>(w1 * h2, sbuf);
-        const double sg = 1.0 / (1.0 + exp(-z));
-        const double act = scale * z * sg;
-        const double dact = scale * sg + scale * z * sg * (1.0 - sg);
-        out += W2r[hd] * act;
-        h2a += W2r[hd] * dact * w1;
-    }
-    if (k == 0) node_energies[i] = e + out;
-    sh2a[k] = h2a;
-    __syncthreads();
-    const float* Tt = H2_Tt + static_cast<std::size_t>(t) * C * C;
-    double dsum = q[k], s1 = 0.0;
-    for (int o = 0; o < C; ++o) {
-        dsum += static_cast<double>(Tt[o * C + k]) * sh2a[o];
-        s1 += static_cast<double>(H2_M1t[o * C + k]) * sh2a[o];
-    }
-    direct[static_cast<std::size_t>(i) * C + k] = static_cast<float>(dsum);
-    const float m1adj = static_cast<float>(s1);
+    // H2[n][k] = sum_in T[in][k] x[n][in] + sum_in W[in][k] M1[n][in]
+    {
+        const float* T = H2_T + static_cast<std::size_t>(t) * C * C;
+        double h2[RB];
 #pragma unroll
-    for (int v = 0; v < NY; ++v) A1_adj[(static_cast<std::size_t>(li) * NY + v) * C + k] = gs[v * C + k] * m1adj;
+        for (int n = 0; n < RB; ++n) h2[n] = 0.0;
+#pragma unroll 4
+        for (int in = 0; in < C; ++in) {
+            const double w = static_cast<double>(T[in * C + k]);
+#pragma unroll
+            for (int n = 0; n < RB; ++n) h2[n] += w * sx[n][in];
+        }
+#pragma unroll 4
+        for (int in = 0; in < C; ++in) {
+            const double w = static_cast<double>(H2_M1[in * C + k]);
+#pragma unroll
+            for (int n = 0; n < RB; ++n) h2[n] += w * sm1[n][in];
+        }
+#pragma unroll
+        for (int n = 0; n < RB; ++n) sh[n][k] = h2[n];
+    }
+    __syncthreads();
+    // pre-activations z[n][hd] = W1[hd] . H2[n] with the activation slope
+    // act'(z) in sd; z[n][hidden] = q . x[n]
+    const int H1p = hidden + 1;
+    for (int p = k; p < RB * H1p; p += C) {
+        const int n = p / H1p, hd = p % H1p;
+        double z = 0.0;
+        if (hd < hidden) {
+            const double* w = W1r + static_cast<std::size_t>(hd) * C;
+#pragma unroll 4
+            for (int kk = 0; kk < C; ++kk) z += w[kk] * sh[n][kk];
+            const double sg = 1.0 / (1.0 + exp(-z));
+            sd[n][hd] = scale * sg + scale * z * sg * (1.0 - sg);
+        } else {
+#pragma unroll 4
+            for (int kk = 0; kk < C; ++kk) z += q[kk] * sx[n][kk];
+        }
+        sz[n][hd] = z;
+    }
+    __syncthreads();
+    if (k < b.count) {
+        const int n = k;
+        double out = 0.0;
+        for (int hd = 0; hd < hidden; ++hd) {
+            const double z = sz[n][hd];
+            const double sg = 1.0 / (1.0 + exp(-z));
+            out += W2r[hd] * (scale * z * sg);
+        }
+        node_energies[r0 + li[n]] = E0[t] + sz[n][hidden] + out;
+    }
+    // H2 adjoint: h2a[n][k] = sum_hd W2[hd] act'(z[n][hd]) W1[hd][k]
+    {
+        double h2a[RB];
+#pragma unroll
+        for (int n = 0; n < RB; ++n) h2a[n] = 0.0;
+        for (int hd = 0; hd < hidden; ++hd) {
+            const double w1 = W1r[static_cast<std::size_t>(hd) * C + k];
+            const double w2 = W2r[hd];
+#pragma unroll
+            for (int n = 0; n < RB; ++n) h2a[n] += w2 * sd[n][hd] * w1;
+        }
+        __syncthreads();  // every lane has finished reading sh (H2)
+#pragma unroll
+        for (int n = 0; n < RB; ++n) sh[n][k] = h2a[n];
+    }
+    __syncthreads();
+    // direct = q + T H2_adj; M1 adjoint = W H2_adj
+    double dsum[RB], s1[RB];
+#pragma unroll
+    for (int n = 0; n < RB; ++n) {
+        dsum[n] = q[k];
+        s1[n] = 0.0;
+    }
+    {
+        const float* Tt = H2_Tt + static_cast<std::size_t>(t) * C * C;
+#pragma unroll 4
+        for (int o = 0; o < C; ++o) {
+            const double wt = static_cast<double>(Tt[o * C + k]);
+            const double wm = static_cast<double>(H2_M1t[o * C + k]);
+#pragma unroll
+            for (int n = 0; n < RB; ++n) {
+                dsum[n] += wt * sh[n][o];
+                s1[n] += wm * sh[n][o];
+            }
+        }
+    }
+#pragma unroll
+    for (int n = 0; n < RB; ++n) {
+        if (n < b.count) {
+            direct[static_cast<std::size_t>(r0 + li[n]) * C + k] = static_cast<float>(dsum[n]);
+            const float m1adj = static_cast<float>(s1[n]);
+            float* g = A1_adj + static_cast<std::size_t>(li[n]) * NY * C + k;
+#pragma unroll
+            for (int v = 0; v < NY; ++v) g[v * C] = g[v * C] * m1adj;
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -551,7 +807,6 @@ template <int C, int NH>
 __global__ __launch_bounds__(C) void k_tile_source_adjoint(const int* __restrict__ touched, long long e0, long long e1,
                                                            const int* __restrict__ soff,
                                                            const int* __restrict__ sedges,
-                                                           const float* __restrict__ erec, int rec_floats,
                                                            const float* __restrict__ Wsrc,
                                                            float* __restrict__ H1_adj) {
     const int s = touched[blockIdx.x];
@@ -560,14 +815,9 @@ __global__ __launch_bounds__(C) void k_tile_source_adjoint(const int* __restrict
 #pragma unroll
     for (int q = 0; q < NH; ++q) acc[q] = 0.0;
     const int hi = soff[s + 1];
-    for (int t = lower_edge(sedges, soff[s], hi, e0); t < hi; ++t) {
-        const long long e = sedges[t];
-        if (e >= e1) break;
-        if (!edge_active(erec + static_cast<std::size_t>(e - e0) * rec_floats)) continue;
-        const float* w = Wsrc + static_cast<std::size_t>(e - e0) * NH * C + k;
-#pragma unroll
-        for (int q = 0; q < NH; ++q) acc[q] += static_cast<double>(w[q * C]);
-    }
+    const int lo = lower_edge(sedges, soff[s], hi, e0);
+    const int end = lower_edge(sedges, lo, hi, e1);
+    gather_source_rows<C, NH>(sedges, lo, end, e0, Wsrc, k, acc);
     float* dst = H1_adj + static_cast<std::size_t>(s) * NH * C + k;
 #pragma unroll
     for (int q = 0; q < NH; ++q) dst[q * C] = dst[q * C] + static_cast<float>(acc[q]);
@@ -641,16 +891,20 @@ __global__ void k_fill_f64(std::size_t n, double* __restrict__ p) {
 }
 
 // ---------------------------------------------------------------------------
-// Node linears on MFMA: out[row, n] = sum_k in[row, k] W[k, n] for 16 rows of
-// one weight group, 64 columns per wave (four 16x16 tiles), FP32 in and out
-// (v_mfma_f32_16x16x4_f32).  Lane l supplies A[l%16][l/16], B[l/16][l%16] and
-// holds D[4*(l/16)+v][l%16]; the K order inside one 16-wide step is permuted
-// so that each lane reads four consecutive inputs with one 16-byte load.
+// Node linears on MFMA (v_mfma_f32_16x16x4_f32, FP32 in and out).  One wave
+// computes a 64-row x 64-column block as 4x4 tiles of 16x16.  In a tile, lane
+// l supplies A[l%16][kk] and B[kk][l%16] with kk = l/16 and holds
+// D[4*(l/16)+v][l%16].  The K order inside one 16-wide chunk is permuted so
+// that step s uses k = k0 + 4*(l/16) + s: each lane then reads four
+// consecutive inputs of its row with one 16-byte load, and the weights are
+// pre-swizzled (swizzle_gemm_weights) so that the B operands of one chunk and
+// column block are one contiguous 1 KB float4 load per wave.  Per chunk a
+// wave issues 8 loads and 64 MFMAs.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(64) void k_node_gemm(const GemmTile* __restrict__ tiles,
-                                                  const GemmGroup* __restrict__ groups,
-                                                  const int* __restrict__ node_list, const float* __restrict__ W,
-                                                  const float* __restrict__ in, float* __restrict__ out) {
+                                                  const GemmGroup* __restrict__ groups, const int* __restrict__ rows,
+                                                  const float* __restrict__ W, const float* __restrict__ in,
+                                                  float* __restrict__ out) {
     const GemmTile tile = tiles[blockIdx.x];
     const GemmGroup g = groups[tile.group];
     const int n0 = blockIdx.y * 64;
@@ -658,34 +912,57 @@ __global__ __launch_bounds__(64) void k_node_gemm(const GemmTile* __restrict__ t
     const int lane = threadIdx.x;
     const int r = lane & 15, kg = lane >> 4;
     const int nsub = min(4, (g.N - n0) / 16);
-    const bool row_ok = r < tile.count;
-    const int node = row_ok ? node_list[tile.list_start + r] : 0;
-    const float* arow = in + static_cast<std::size_t>(node) * g.in_stride + g.in_base + tile.m * g.in_mstride;
-    const float* Wg = W + g.w_off + n0 + r;
-    v4f acc[4];
+    const float* arow[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-    for (int k0 = 0; k0 < g.K; k0 += 16) {
-        float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (row_ok) a = *reinterpret_cast<const float4*>(arow + k0 + 4 * kg);
-        const float av[4] = {a.x, a.y, a.z, a.w};
+    for (int i = 0; i < 4; ++i) {
+        // rows past the tile's count repeat its last row (their results are not stored)
+        const int q = min(16 * i + r, tile.count - 1);
+        const int pk = rows[tile.row_start + q];
+        arow[i] = in + static_cast<std::size_t>(pk >> 4) * g.in_stride + g.in_base + (pk & 15) * g.in_mstride + 4 * kg;
+    }
+    const int nblk = g.N / 16;
+    const float4* B = reinterpret_cast<const float4*>(W + g.w_off) + (n0 / 16) * 64 + lane;
+    v4f acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    const int chunks = g.K / 16;
+    for (int kc = 0; kc < chunks; ++kc) {
+        float4 a[4], b[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const float4*>(arow[i] + 16 * kc);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            b[j] = j < nsub ? B[(static_cast<std::size_t>(kc) * nblk + j) * 64] : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-            const float* brow = Wg + static_cast<std::size_t>(k0 + 4 * kg + s) * g.N;
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                if (j < nsub) acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[s], brow[16 * j], acc[j], 0, 0, 0);
+            for (int i = 0; i < 4; ++i) {
+                const float av = s == 0 ? a[i].x : s == 1 ? a[i].y : s == 2 ? a[i].z : a[i].w;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    if (j < nsub) {
+                        const float bv = s == 0 ? b[j].x : s == 1 ? b[j].y : s == 2 ? b[j].z : b[j].w;
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[i][j], 0, 0, 0);
+                    }
+                }
+            }
         }
     }
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-        const int row = 4 * kg + v;
-        if (row >= tile.count) continue;
-        const int nd = node_list[tile.list_start + row];
-        float* orow = out + static_cast<std::size_t>(nd) * g.out_stride + g.out_base + tile.m * g.out_mstride + n0 + r;
+    for (int i = 0; i < 4; ++i) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            if (j < nsub) orow[16 * j] = acc[j][v];
+        for (int v = 0; v < 4; ++v) {
+            const int q = 16 * i + 4 * kg + v;
+            if (q >= tile.count) continue;
+            const int pk = rows[tile.row_start + q];
+            float* orow = out + static_cast<std::size_t>(pk >> 4) * g.out_stride + g.out_base + (pk & 15) * g.out_mstride +
+                          n0 + r;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (j < nsub) orow[16 * j] = acc[i][j][v];
+        }
     }
 }
 
@@ -799,10 +1076,14 @@ struct TimerScope {
     }
 };
 
-template <int C, int LMAX, int LMAXH>
+// M0TAB / M1TAB: compiled ProductTable of the model's M0 / M1 monomial lists,
+// or void for the table-driven polynomial kernels.
+template <int C, int LMAX, int LMAXH, class M0TAB, class M1TAB>
 struct KernelSetImpl final : KernelSet {
     using S = Shape<LMAX, LMAXH>;
+    static constexpr bool kM0Unrolled = !std::is_same_v<M0TAB, void>;
     int record_floats() const override { return S::REC; }
+    const char* polynomial_mode() const override { return kM0Unrolled ? "unrolled" : "table"; }
 
     void edge_geometry(const DeviceModel& m, std::int64_t E, const double* xyz, const double* r, float* erec,
                        hipStream_t s) const override {
@@ -825,8 +1106,12 @@ struct KernelSetImpl final : KernelSet {
         if (!through_h1) return;
         {
             TimerScope ts(tm, "m0_forward", s);
-            k_m0_forward<C, S::NY, S::NH><<<t.nr, C, 0, s>>>(t.r0, g.node_types, w.A0, m.m0_terms, m.m0_toff, m.T0,
-                                                            m.m0_coef, w.M0, w.xaff);
+            if constexpr (kM0Unrolled)
+                k_m0_forward_ct<C, S::NY, S::NH, M0TAB><<<t.nr, C, 0, s>>>(t.r0, g.node_types, w.A0, m.m0_coef, w.M0,
+                                                                          w.xaff);
+            else
+                k_m0_forward<C, S::NY, S::NH><<<t.nr, C, 0, s>>>(t.r0, g.node_types, w.A0, m.m0_terms, m.m0_toff,
+                                                                m.T0, m.m0_coef, w.M0, w.xaff);
             SMX_LAUNCH_CHECK("m0_forward");
         }
         {
@@ -850,9 +1135,12 @@ struct KernelSetImpl final : KernelSet {
         }
         {
             TimerScope ts(tm, "readout", s);
-            k_readout<C, S::NY><<<t.nr, C, 0, s>>>(t.r0, g.node_types, w.A1, w.xaff, m.m1_terms, m.T1, m.m1_coef,
-                                                  m.H2_T, m.H2_Tt, m.H2_M1, m.H2_M1t, m.q, m.W1r, m.W2r, m.hidden,
-                                                  m.readout_scale, m.E0, w.node_energies, w.direct, w.A1_adj);
+            k_m1<C, S::NY, M1TAB><<<t.nr, C, 0, s>>>(t.r0, g.node_types, w.A1, m.m1_terms, m.T1, m.m1_coef, w.M1,
+                                                    w.A1_adj);
+            SMX_LAUNCH_CHECK("m1");
+            k_readout<C, S::NY, kReadoutBatch><<<t.num_batches, C, 0, s>>>(
+                t.r0, t.batches, t.node_list, g.node_types, w.M1, w.xaff, m.H2_T, m.H2_Tt, m.H2_M1, m.H2_M1t, m.q,
+                m.W1r, m.W2r, m.hidden, m.readout_scale, m.E0, w.node_energies, w.direct, w.A1_adj);
             SMX_LAUNCH_CHECK("readout");
         }
         {
@@ -870,7 +1158,7 @@ struct KernelSetImpl final : KernelSet {
     void source_adjoint_all(const DeviceGraph& g, const Workspace& w, hipStream_t s, LaunchTimer* tm) const override {
         if (g.N == 0) return;
         TimerScope ts(tm, "source_gather", s);
-        k_source_gather<C, S::NH><<<g.N, C, 0, s>>>(g.soff, g.sedges, w.erec, S::REC, w.Wsrc, w.H1_adj);
+        k_source_gather<C, S::NH><<<g.N, C, 0, s>>>(g.soff, g.sedges, w.Wsrc, w.H1_adj);
         SMX_LAUNCH_CHECK("source_gather");
     }
 
@@ -879,7 +1167,7 @@ struct KernelSetImpl final : KernelSet {
         if (t.touched_count == 0) return;
         TimerScope ts(tm, "source_gather", s);
         k_tile_source_adjoint<C, S::NH><<<t.touched_count, C, 0, s>>>(t.touched, t.e0, t.e0 + t.ne, g.soff, g.sedges,
-                                                                     w.erec, S::REC, w.Wsrc, w.H1_adj);
+                                                                     w.Wsrc, w.H1_adj);
         SMX_LAUNCH_CHECK("tile_source_adjoint");
     }
 
@@ -892,8 +1180,12 @@ struct KernelSetImpl final : KernelSet {
         }
         {
             TimerScope ts(tm, "m0_reverse", s);
-            k_m0_reverse<C, S::NY, S::NH><<<t.nr, C, 0, s>>>(t.r0, g.node_types, w.A0, w.M0_adj, w.direct, m.m0_terms,
-                                                            m.m0_toff, m.T0, m.m0_coef, w.A0_adj);
+            if constexpr (kM0Unrolled)
+                k_m0_reverse_ct<C, S::NY, S::NH, M0TAB><<<t.nr, C, 0, s>>>(t.r0, g.node_types, w.A0, w.M0_adj,
+                                                                          w.direct, m.m0_coef, w.A0_adj);
+            else
+                k_m0_reverse<C, S::NY, S::NH><<<t.nr, C, 0, s>>>(t.r0, g.node_types, w.A0, w.M0_adj, w.direct,
+                                                                m.m0_terms, m.m0_toff, m.T0, m.m0_coef, w.A0_adj);
             SMX_LAUNCH_CHECK("m0_reverse");
         }
         {
@@ -926,11 +1218,53 @@ void paths_of(std::vector<int>& le, std::vector<int>& ls, std::vector<int>& lo) 
     }
 }
 
+// true when the canonical lists equal the compiled table TAB
+template <class TAB>
+bool table_matches(const std::vector<std::int32_t>& terms, const std::vector<std::int32_t>& offsets) {
+    if constexpr (!TAB::available) {
+        return false;
+    } else {
+        if (terms.size() != static_cast<std::size_t>(TAB::NT) || offsets.size() != TAB::offset.size()) return false;
+        for (int t = 0; t < TAB::NT; ++t)
+            if (terms[t] != TAB::terms[t]) return false;
+        for (std::size_t o = 0; o < offsets.size(); ++o)
+            if (offsets[o] != TAB::offset[o]) return false;
+        return true;
+    }
+}
+
+template <int C, int LMAX, int LMAXH, int CORR>
+std::unique_ptr<KernelSet> pick_polynomials(const std::vector<std::int32_t>& m0_terms,
+                                            const std::vector<std::int32_t>& m0_offsets,
+                                            const std::vector<std::int32_t>& m1_terms) {
+    using T0 = ProductTable<LMAX, LMAXH, CORR>;
+    using T1 = ProductTable<LMAX, 0, CORR>;
+    const std::vector<std::int32_t> m1_offsets{0, static_cast<std::int32_t>(m1_terms.size())};
+    if constexpr (T0::available && T1::available) {
+        if (table_matches<T0>(m0_terms, m0_offsets) && table_matches<T1>(m1_terms, m1_offsets))
+            return std::make_unique<KernelSetImpl<C, LMAX, LMAXH, T0, T1>>();
+    }
+    return std::make_unique<KernelSetImpl<C, LMAX, LMAXH, void, void>>();
+}
+
+int max_degree(const std::vector<std::int32_t>& terms) {
+    int d = 0;
+    for (const std::int32_t t : terms) d = std::max(d, t >> 24);
+    return d;
+}
+
 }  // namespace
 
-std::unique_ptr<KernelSet> make_kernel_set(int C, int l_max, int L_max) {
-    if (C == 32 && l_max == 2 && L_max == 1) return std::make_unique<KernelSetImpl<32, 2, 1>>();
-    if (C == 128 && l_max == 3 && L_max == 1) return std::make_unique<KernelSetImpl<128, 3, 1>>();
+std::unique_ptr<KernelSet> make_kernel_set(int C, int l_max, int L_max, const std::vector<std::int32_t>& m0_terms,
+                                           const std::vector<std::int32_t>& m0_offsets,
+                                           const std::vector<std::int32_t>& m1_terms) {
+    const int corr = std::max(max_degree(m0_terms), max_degree(m1_terms));
+    if (C == 32 && l_max == 2 && L_max == 1)
+        return corr == 2 ? pick_polynomials<32, 2, 1, 2>(m0_terms, m0_offsets, m1_terms)
+                         : std::make_unique<KernelSetImpl<32, 2, 1, void, void>>();
+    if (C == 128 && l_max == 3 && L_max == 1)
+        return corr == 3 ? pick_polynomials<128, 3, 1, 3>(m0_terms, m0_offsets, m1_terms)
+                         : std::make_unique<KernelSetImpl<128, 3, 1, void, void>>();
     return nullptr;
 }
 
@@ -949,8 +1283,20 @@ bool kernel_paths(int l_max, int L_max, std::vector<int>& le, std::vector<int>& 
 void launch_node_gemm(const GemmPlan& plan, const float* W, const float* in, float* out, hipStream_t s) {
     if (plan.num_tiles == 0) return;
     dim3 grid(plan.num_tiles, (plan.max_n + 63) / 64);
-    k_node_gemm<<<grid, 64, 0, s>>>(plan.tiles, plan.groups, plan.node_list, W, in, out);
+    k_node_gemm<<<grid, 64, 0, s>>>(plan.tiles, plan.groups, plan.rows, W, in, out);
     SMX_LAUNCH_CHECK("node_gemm");
+}
+
+void swizzle_gemm_weights(const float* w, int K, int N, float* out) {
+    if (K % 16 != 0 || N % 16 != 0) throw std::invalid_argument("node-linear dimensions must be multiples of 16");
+    const int nblk = N / 16;
+    for (int kc = 0; kc < K / 16; ++kc)
+        for (int nb = 0; nb < nblk; ++nb)
+            for (int kg = 0; kg < 4; ++kg)
+                for (int c = 0; c < 16; ++c)
+                    for (int s = 0; s < 4; ++s)
+                        out[((((static_cast<std::size_t>(kc) * nblk + nb) * 4 + kg) * 16 + c) * 4) + s] =
+                            w[static_cast<std::size_t>(16 * kc + 4 * kg + s) * N + 16 * nb + c];
 }
 
 void launch_atom_forces(int N, const int* offsets, const int* soff, const int* sedges, const double* node_forces,

@@ -62,22 +62,34 @@ struct DeviceGraph {
     const int* sedges = nullptr;      // [E] edges ordered by source, ascending edge id
 };
 
-// Node-linear tiles: TM=16 rows of one (weight group, m) over a node list.
+// Node linears: out[row, n] = sum_k in[row, k] W[k, n] over the rows of one
+// weight group.  A row is (tile-local node, m) packed as node << 4 | m; its
+// input starts at node*in_stride + in_base + m*in_mstride (likewise the
+// output).  W is stored in the MFMA operand order of swizzle_gemm_weights.
 struct GemmGroup {
-    std::int64_t w_off;  // element offset of the [K][N] row-major weight block
+    std::int64_t w_off;  // element offset of the group's swizzled [K][N] block
     int K, N;
     int in_stride, in_base, in_mstride;
     int out_stride, out_base, out_mstride;
 };
+constexpr int kGemmRows = 64;  // rows per wave tile
 struct GemmTile {
-    int list_start, count, group, m;
+    int row_start, count, group;  // rows [row_start, row_start+count), count <= kGemmRows
 };
 struct GemmPlan {
     const GemmTile* tiles = nullptr;
     const GemmGroup* groups = nullptr;
-    const int* node_list = nullptr;   // tile-local row indices
+    const int* rows = nullptr;        // packed (node << 4 | m)
     int num_tiles = 0;
     int max_n = 0;
+};
+
+// Readout batches: up to kReadoutBatch receivers of one type, as a range of
+// the tile's type-sorted node list.
+constexpr int kReadoutBatch = 8;
+constexpr int kMaxReadoutHidden = 64;  // readout MLP width the readout kernel holds in LDS
+struct NodeBatch {
+    int start, count;
 };
 
 // A receiver tile: receivers [r0, r0+nr), their edges [e0, e0+ne) (edges
@@ -86,6 +98,9 @@ struct TileView {
     int r0 = 0, nr = 0;
     std::int64_t e0 = 0, ne = 0;
     GemmPlan a0, h1, a1f, a1r;
+    const int* node_list = nullptr;    // tile-local receivers sorted by type
+    const NodeBatch* batches = nullptr;
+    int num_batches = 0;
     const int* touched = nullptr;  // sources with an edge in the tile (ascending)
     int touched_count = 0;
 };
@@ -101,6 +116,7 @@ struct Workspace {
     float* Phi1 = nullptr;      // [nr][NLME][C]
     float* A1 = nullptr;        // [nr][NY][C]
     float* A1_adj = nullptr;    // [nr][NY][C]
+    float* M1 = nullptr;        // [nr][C]
     float* dPhi1 = nullptr;     // [nr][NLME][C]
     float* Wsrc = nullptr;      // [ne][NH][C] per-edge source-adjoint contributions
     float* M0_adj = nullptr;    // [nr][NH][C]
@@ -128,6 +144,8 @@ struct LaunchTimer {
 struct KernelSet {
     virtual ~KernelSet() = default;
     virtual int record_floats() const = 0;
+    // "unrolled" when the product-basis kernels use compiled term tables
+    virtual const char* polynomial_mode() const = 0;
     // per-edge records of a tile from its FP64 xyz and r
     virtual void edge_geometry(const DeviceModel& m, std::int64_t ne, const double* xyz, const double* r,
                                float* erec, hipStream_t s) const = 0;
@@ -151,7 +169,15 @@ struct KernelSet {
                                 bool accumulate_forces, hipStream_t s, LaunchTimer* tm) const = 0;
 };
 
-std::unique_ptr<KernelSet> make_kernel_set(int C, int l_max, int L_max);
+// Kernels for (C, l_max, L_max).  The polynomial kernels run with every
+// product-basis term unrolled when the model's canonical M0 and M1 monomial
+// lists equal a compiled table (ProductTable), else from the lists in HBM.
+std::unique_ptr<KernelSet> make_kernel_set(int C, int l_max, int L_max, const std::vector<std::int32_t>& m0_terms,
+                                           const std::vector<std::int32_t>& m0_offsets,
+                                           const std::vector<std::int32_t>& m1_terms);
+// [K][N] row-major block -> MFMA B-operand order [K/16][N/16][4][16][4]
+// (k chunk, column block, lane/16, lane%16, k within the lane's four)
+void swizzle_gemm_weights(const float* w, int K, int N, float* out);
 // paths of the compiled kernel set for (l_max, L_max), false if none
 bool kernel_paths(int l_max, int L_max, std::vector<int>& le, std::vector<int>& ls, std::vector<int>& lo);
 

@@ -24,6 +24,17 @@ __host__ __device__ __forceinline__ void static_for(F&& f) {
     }
 }
 
+// f(integral_constant<B>), ..., f(integral_constant<E-1>) without recursion
+// (long unrolled ranges such as product-basis term lists)
+template <int B, class F, int... I>
+__host__ __device__ __forceinline__ void static_range_impl(F& f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, B + I>{}), ...);
+}
+template <int B, int E, class F>
+__host__ __device__ __forceinline__ void static_range(F&& f) {
+    if constexpr (B < E) static_range_impl<B>(f, std::make_integer_sequence<int, E - B>{});
+}
+
 struct R1Path {
     int le, ls, lo;
 };

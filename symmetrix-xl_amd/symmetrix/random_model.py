@@ -219,9 +219,10 @@ def generate_model(config, seed=None):
              / (math.sqrt(num_e[l] * C) * cfg.avg_num_neighbors))
         for l in range(l_max + 1)) + "]"
 
-    # ---- M1: invariant contraction of A1 (16 harmonic components)
+    # ---- M1: invariant contraction of A1 ((l_max+1)^2 harmonic components),
+    # with the same correlation order as the first product basis
     monos1, coef1 = _product_weights(
-        rng, l_max, 0, 3, n_el, C, scale=[1.0, 0.5, 0.25])
+        rng, l_max, 0, cfg.correlation, n_el, C, scale=[1.0, 0.5, 0.25][:cfg.correlation])
     put("M1_monomials", monos1[0])
     frag["M1_weights"] = "{" + ",".join(
         '"%d":{' % t + ",".join(
@@ -266,7 +267,7 @@ def cached_model(config, seed=None, directory=None):
     directory = directory or os.environ.get(
         "SYMMETRIX_MODEL_CACHE", "/tmp/symmetrix_models")
     os.makedirs(directory, exist_ok=True)
-    path = os.path.join(directory, "mace_%s_seed%d_v2.json" % (cfg.name, seed))
+    path = os.path.join(directory, "mace_%s_seed%d_v3.json" % (cfg.name, seed))
     if not os.path.exists(path):
         write_model(cfg, path, seed)
     return path

@@ -205,3 +205,42 @@ def test_host_edge_vectors_path(tiny_model_path):
     assert abs(e.sum() - ref["energy"]) / len(e) < E_TOL
     assert np.max(np.abs(f - ref["forces"])) < F_TOL
     assert np.max(np.abs(nf - ref["node_forces"])) < 1e-5
+
+
+def _run_tiny(model_path, system):
+    from symmetrix.mace_kokkos import MACEKokkosFloat
+    ev = MACEKokkosFloat(model_path)
+    lut = {z: i for i, z in enumerate(ev.atomic_numbers)}
+    types = np.array([lut[int(z)] for z in system["numbers"]], np.int32)
+    cell = np.asarray(system["cell"], float)
+    g = ev._prepare_periodic_factorized_graph(types, system["positions"], cell, np.linalg.inv(cell),
+                                              ev.r_cut + 0.5)
+    ev._compute_prepared_factorized_positions(g["generation"], system["positions"])
+    f = ev._reduce_atom_forces(len(types), None, None, g["generation"])
+    return ev, ev.node_energies, f
+
+
+def test_table_driven_polynomials_match_unrolled(tiny_model_path, tmp_path):
+    """A model whose M0 list carries one extra zero-coefficient monomial is
+    the same function, but its canonical list no longer equals the compiled
+    table, so it runs through the table-driven polynomial kernels."""
+    import json
+    s = _system("tiny")
+    ev_a, e_a, f_a = _run_tiny(tiny_model_path, s)
+    assert "polynomials=unrolled" in ev_a.execution_plan
+    with open(tiny_model_path) as fh:
+        j = json.load(fh)
+    monos = j["M0_monomials"]["1"]
+    extra = [5]
+    assert extra not in monos
+    monos.append(extra)
+    for t in j["M0_weights"]:
+        for k in j["M0_weights"][t]["1"]:
+            j["M0_weights"][t]["1"][k].append(0.0)
+    path = str(tmp_path / "tiny_extra_monomial.json")
+    with open(path, "w") as fh:
+        json.dump(j, fh)
+    ev_b, e_b, f_b = _run_tiny(path, s)
+    assert "polynomials=table" in ev_b.execution_plan
+    np.testing.assert_allclose(e_b, e_a, rtol=1e-6, atol=1e-9)
+    np.testing.assert_allclose(f_b, f_a, rtol=1e-5, atol=1e-7)
