@@ -158,6 +158,22 @@ def capacity(n, md_steps, tile_receivers):
     print(json.dumps(out), flush=True)
 
 
+def copy_calibration(nbytes, repeats=5):
+    """A plain device-to-device copy of nbytes (hipMemcpy, one copy kernel
+    per call): the reference point that scales the rocprofv3 FETCH_SIZE /
+    WRITE_SIZE counters to bytes."""
+    hip = hip_lib()
+    src, dst = ctypes.c_void_p(), ctypes.c_void_p()
+    if hip.hipMalloc(ctypes.byref(src), ctypes.c_size_t(nbytes)) or hip.hipMalloc(ctypes.byref(dst), ctypes.c_size_t(nbytes)):
+        raise RuntimeError("hipMalloc failed")
+    for _ in range(repeats):
+        if hip.hipMemcpy(dst, src, ctypes.c_size_t(nbytes), 3) != 0:
+            raise RuntimeError("hipMemcpy failed")
+    hip.hipFree(src)
+    hip.hipFree(dst)
+    print(json.dumps({"copy_calibration_bytes": nbytes, "copies": repeats}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -168,11 +184,16 @@ def main():
                     help="run the tiled capacity config on an N^3 SrTiO3 supercell instead")
     ap.add_argument("--md-steps", type=int, default=20)
     ap.add_argument("--tile-receivers", type=int, default=32768)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
+                    help="only run device-to-device copies of BYTES (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures the single-GPU path only: this build runs on one MI355X and "
               "has no multi-GPU (halo-exchange) path; run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
     if args.capacity:
         capacity(args.capacity, args.md_steps, args.tile_receivers)
         return
@@ -272,7 +293,10 @@ def main():
         "roofline": {"bound": "mfma", "kernel": DOMINANT, "achieved": round(achieved, 3),
                      "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_TFLOPS, 4),
                      "traffic": traffic, "avg_launch_ms": round(avg_ms, 4),
-                     "flops_per_launch": flops},
+                     "flops_per_launch": flops,
+                     "compute": "FP32 VALU (edge-wise channel products; packed FP32 disabled, so 78.6 "
+                                "TFLOP/s is the attainable issue rate)",
+                     "traffic_source": "profiles/hbm_traffic_medium_5k.md (FETCH_SIZE+WRITE_SIZE, copy-scaled)"},
         "median_us_per_atom": round(median_us_per_atom, 4),
         "host_positions_us_per_atom": round(host_us_per_atom, 4),
         "cold_call_ms": round(cold_ms, 2),

@@ -41,6 +41,33 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// v + v[lane permuted by the DPP control CTRL] on the rows in ROW_MASK
+// (other rows add 0)
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_add(float v) {
+    const int moved = __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false);
+    return v + __int_as_float(moved);
+}
+
+// Sum over the first WIDTH (32 or 64) lanes of a wave with DPP row
+// operations (quad permutes, half-row and row mirrors, then the row
+// broadcasts 15 and 31), returned wave-uniform from the last lane.
+template <int WIDTH>
+__device__ __forceinline__ float wave_total(float v) {
+    static_assert(WIDTH == 32 || WIDTH == 64, "DPP reduction over 32 or 64 lanes");
+    v = dpp_add<0xb1, 0xf>(v);   // quad_perm [1,0,3,2]
+    v = dpp_add<0x4e, 0xf>(v);   // quad_perm [2,3,0,1]
+    v = dpp_add<0x141, 0xf>(v);  // row_half_mirror: sums of 8
+    v = dpp_add<0x140, 0xf>(v);  // row_mirror: every lane of a row holds the row sum
+    v = dpp_add<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
+    if constexpr (WIDTH == 64) {
+        v = dpp_add<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
+        return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+    } else {
+        return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 31));
+    }
+}
+
 template <int WIDTH>
 __device__ __forceinline__ double wave_sum(double v) {
 #pragma unroll

@@ -87,10 +87,10 @@ __global__ __launch_bounds__(C) void k_r0_forward(int r0, long long e0, const in
         const float4* cf = R0c + static_cast<std::size_t>(iv) * NF + k;
         static_for<0, LMAX + 1>([&](auto lc) {
             constexpr int l = lc;
-            const float rad = spline_value(cf[l * C], x, xx, xxx);
+            const float rh = spline_value(cf[l * C], x, xx, xxx) * h0;
             static_for<0, 2 * l + 1>([&](auto mc) {
                 constexpr int lm = l * l + mc;
-                acc[lm] += rad * rec[S::REC_Y + lm] * h0;
+                acc[lm] += rh * rec[S::REC_Y + lm];
             });
         });
     }
@@ -104,9 +104,9 @@ template <int C, int CHUNK>
 struct EdgeForceSink {
     float (*part)[CHUNK][3];
     __device__ __forceinline__ void put(int slot, float fx, float fy, float fz) {
-        fx = wave_sum<Lanes<C>::WIDTH>(fx);
-        fy = wave_sum<Lanes<C>::WIDTH>(fy);
-        fz = wave_sum<Lanes<C>::WIDTH>(fz);
+        fx = wave_total<Lanes<C>::WIDTH>(fx);
+        fy = wave_total<Lanes<C>::WIDTH>(fy);
+        fz = wave_total<Lanes<C>::WIDTH>(fz);
         if (threadIdx.x % kWave == 0) {
             const int w = threadIdx.x / kWave;
             part[w][slot][0] = fx;
@@ -171,24 +171,29 @@ __global__ __launch_bounds__(C) void k_r0_reverse(int r0, long long e0, const in
             const float xx = x * x, xxx = xx * x;
             const float h0 = H0[neigh_types[e] * C + k];
             const float4* cf = R0c + static_cast<std::size_t>(iv) * NF + k;
+            // per l: dR_l sum_m adj Y_lm (radial slope) and R_l sum_m adj dY_lm,
+            // the common factor H0[type_j] applied once
             float a = 0.0f, b0 = 0.0f, b1 = 0.0f, b2 = 0.0f;
             static_for<0, LMAX + 1>([&](auto lc) {
                 constexpr int l = lc;
                 const float4 c4 = cf[l * C];
                 const float R = spline_value(c4, x, xx, xxx);
                 const float dR = spline_slope(c4, x, xx);
+                float sa = 0.0f, s0 = 0.0f, s1 = 0.0f, s2 = 0.0f;
                 static_for<0, 2 * l + 1>([&](auto mc) {
                     constexpr int lm = l * l + mc;
-                    const float t = padj[lm] * h0;
-                    a += dR * rec[S::REC_Y + lm] * t;
-                    const float rt = R * t;
-                    b0 += rt * rec[S::REC_DY + lm];
-                    b1 += rt * rec[S::REC_DY + NY + lm];
-                    b2 += rt * rec[S::REC_DY + 2 * NY + lm];
+                    sa += padj[lm] * rec[S::REC_Y + lm];
+                    s0 += padj[lm] * rec[S::REC_DY + lm];
+                    s1 += padj[lm] * rec[S::REC_DY + NY + lm];
+                    s2 += padj[lm] * rec[S::REC_DY + 2 * NY + lm];
                 });
+                a += dR * sa;
+                b0 += R * s0;
+                b1 += R * s1;
+                b2 += R * s2;
             });
             const float u0 = rec[S::REC_U], u1 = rec[S::REC_U + 1], u2 = rec[S::REC_U + 2];
-            sink.put(e - c0, u0 * a + b0, u1 * a + b1, u2 * a + b2);
+            sink.put(e - c0, h0 * (u0 * a + b0), h0 * (u1 * a + b1), h0 * (u2 * a + b2));
         }
         sink.template flush<ACCUMULATE>(static_cast<int>(c0 - e0), c1 - c0, node_forces);
     }
@@ -320,36 +325,52 @@ __global__ __launch_bounds__(C) void k_r1_reverse(int r0, long long e0, const in
                 W[q] = 0.0f;
             }
             const float4* cf = R1c + static_cast<std::size_t>(iv) * NF + k;
-            float a = 0.0f, b0 = 0.0f, b1 = 0.0f, b2 = 0.0f;
+            // Per path p, with T[m2] = sum_m1 Y_m1 G[p,m1,m2] and
+            // s[m1] = sum_m2 G[p,m1,m2] h_m2:
+            //   W[m2] += R T[m2],  A += dR sum_m2 h_m2 T[m2],  SB[lm1] += R s[m1];
+            // then f = u A + sum_lm1 dY_lm1 SB[lm1].
+            float A = 0.0f, SB[NY];
+#pragma unroll
+            for (int v = 0; v < NY; ++v) SB[v] = 0.0f;
             static_for<0, S::P>([&](auto pc) {
                 constexpr int p = pc;
                 constexpr int le = S::paths[p].le, ls = S::paths[p].ls, rb = S::row_base[p];
                 const float4 c4 = cf[p * C];
                 const float R = spline_value(c4, x, xx, xxx);
                 const float dR = spline_slope(c4, x, xx);
+                float T[2 * ls + 1];
+                static_for<0, 2 * ls + 1>([&](auto m2c) { T[m2c] = 0.0f; });
                 static_for<0, 2 * le + 1>([&](auto m1c) {
                     constexpr int m1 = m1c;
-                    constexpr int lm1 = le * le + m1;
-                    const float y = rec[S::REC_Y + lm1];
-                    const float ry = R * y;
+                    const float y = rec[S::REC_Y + le * le + m1];
                     float sr = 0.0f;
                     static_for<0, 2 * ls + 1>([&](auto m2c) {
                         constexpr int m2 = m2c;
                         const float g = G[rb + m1 * (2 * ls + 1) + m2];
+                        T[m2] += y * g;
                         sr += g * h[ls * ls + m2];
-                        W[ls * ls + m2] += ry * g;
                     });
-                    a += dR * y * sr;
-                    const float t = R * sr;
-                    b0 += t * rec[S::REC_DY + lm1];
-                    b1 += t * rec[S::REC_DY + NY + lm1];
-                    b2 += t * rec[S::REC_DY + 2 * NY + lm1];
+                    SB[le * le + m1] += R * sr;
                 });
+                float hT = 0.0f;
+                static_for<0, 2 * ls + 1>([&](auto m2c) {
+                    constexpr int m2 = m2c;
+                    W[ls * ls + m2] += R * T[m2];
+                    hT += h[ls * ls + m2] * T[m2];
+                });
+                A += dR * hT;
             });
+            float b0 = 0.0f, b1 = 0.0f, b2 = 0.0f;
+#pragma unroll
+            for (int v = 0; v < NY; ++v) {
+                b0 += SB[v] * rec[S::REC_DY + v];
+                b1 += SB[v] * rec[S::REC_DY + NY + v];
+                b2 += SB[v] * rec[S::REC_DY + 2 * NY + v];
+            }
 #pragma unroll
             for (int q = 0; q < NH; ++q) wdst[q * C] = W[q];
             const float u0 = rec[S::REC_U], u1 = rec[S::REC_U + 1], u2 = rec[S::REC_U + 2];
-            sink.put(e - c0, u0 * a + b0, u1 * a + b1, u2 * a + b2);
+            sink.put(e - c0, u0 * A + b0, u1 * A + b1, u2 * A + b2);
         }
         sink.template flush<false>(static_cast<int>(c0 - e0), c1 - c0, node_forces);
     }

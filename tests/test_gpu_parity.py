@@ -126,6 +126,19 @@ def test_energy_forces_stress_medium(medium_model_path):
     _assert_efs(ref, e, f, st, len(e))
 
 
+def test_energy_forces_stress_irregular(medium_model_path):
+    """20,000 atoms uniform at 0.08 /A^3 with a 1.8 A
+    minimum separation, 10 species (55 pair types) -- a wide spread of
+    neighbour counts per receiver."""
+    from symmetrix import systems
+    s = systems.irregular_box(20000, density=0.08, min_distance=1.8, seed=0)
+    om, ref, ev, g, e, f, st = _evaluate_both(medium_model_path, s)
+    counts = np.diff(ref["graph"]["offsets"])
+    print("neighbours per receiver: min %d max %d mean %.1f" % (counts.min(), counts.max(), counts.mean()))
+    assert counts.max() - counts.min() > 20
+    _assert_efs(ref, e, f, st, len(e))
+
+
 def test_repeat_calls_bitwise_deterministic(tiny_model_path):
     from symmetrix.mace_kokkos import MACEKokkosFloat
     s = _system("tiny")
