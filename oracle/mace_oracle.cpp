@@ -395,6 +395,7 @@ struct Mace {
         H1_adj, M0_adj, A0_adj;
     std::vector<double> H2, H2_adj, direct;
     std::vector<double> node_energies, node_forces;
+    std::vector<double> node_forces_r1;  // directed forces of the R1 reverse alone
 
     static P cast(double v) {
         if (!std::isfinite(v) || std::abs(v) > static_cast<double>(std::numeric_limits<P>::max()))
@@ -869,6 +870,7 @@ struct Mace {
             for (int c = 0; c < 3; ++c) node_forces[3 * e + c] += f[c];
         }
         }
+        node_forces_r1 = node_forces;
         // source adjoint over the source transpose (deterministic, no atomics)
         std::vector<long long> soff(n + 1, 0);
         for (long long e = 0; e < E; ++e) soff[neigh[e] + 1] += 1;
@@ -1219,6 +1221,7 @@ long long oracle_stage(void* hv, const char* name, double* out, long long capaci
         if (s == "H1_adj") return emit(m.H1_adj);
         if (s == "M0_adj") return emit(m.M0_adj);
         if (s == "A0_adj") return emit(m.A0_adj);
+        if (s == "node_forces_r1") return emit(m.node_forces_r1);
         return -1;
     };
     return h->fp64 ? get(*h->d) : get(*h->f);

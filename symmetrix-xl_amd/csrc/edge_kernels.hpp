@@ -1,0 +1,448 @@
+// Streamed-edge R1 kernels (gfx950, wave64), shared by the evaluator and the
+// reference-compatible R1 plugin entry points.
+//
+// Mapping: one workgroup owns one receiver; lanes are channels, so per-channel
+// data (spline coefficients, H1 rows, coupling adjoints) is read coalesced and
+// the per-edge quantities (evaluation point, Y, dY, direction) are
+// wave-uniform.  Receivers are owned, never shared: every receiver quantity is
+// a deterministic segment sum without atomics.
+//
+// The kernels read their per-edge inputs through a policy:
+//  * RecordEdges: this build's packed per-edge records and float4 spline table
+//    (the evaluator's own layout);
+//  * PluginEdges: the separate arrays of the reference's plugin argument
+//    packets (radius, harmonics, harmonic gradients, coordinates, spline
+//    coefficients [edge type][interval][4][function], type maps;
+//    jit_hip_plugin_abi.h:37-222), with the reference's evaluation point and
+//    radial formulas (jit_codegen.py:2380-2496).
+//
+// Reference math: R1 forward mace.cpp:2023-2084 (h1_phi1.cpp:1385-1845),
+// R1 reverse mace.cpp:2199-2303 (factorized_execution.cpp:471-1460).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "device_common.hpp"
+#include "shapes.hpp"
+
+namespace smx {
+namespace edge {
+namespace {
+
+__device__ __forceinline__ float spline_value(float4 c, float x, float xx, float xxx) {
+    return c.x + c.y * x + c.z * xx + c.w * xxx;
+}
+__device__ __forceinline__ float spline_slope(float4 c, float x, float xx) {
+    return c.y + 2.0f * c.z * x + 3.0f * c.w * xx;
+}
+__device__ __forceinline__ bool edge_active(const float* rec) { return __float_as_int(rec[2]) != 0; }
+
+template <int C>
+struct Lanes {
+    static constexpr int NW = (C + kWave - 1) / kWave;
+    static constexpr int WIDTH = C < kWave ? C : kWave;
+};
+
+// ---------------------------------------------------------------------------
+// Edge-input policies
+// ---------------------------------------------------------------------------
+// Packed record [x, interval, active, 0, Y[NY], dY/dX[NY], dY/dY[NY],
+// dY/dZ[NY], u[3], pad] per edge (tile-local index e - e0) and the Hermite
+// table [interval][function] as float4 (c0..c3).
+template <int NY, int REC>
+struct RecordEdges {
+    const float* __restrict__ erec;
+    long long e0;
+    const float4* __restrict__ coef;
+    int functions;
+
+    struct Point {
+        const float* rec;
+        const float4* cf;
+        float x, xx, xxx;
+    };
+    __device__ __forceinline__ bool open(int e, int /*receiver*/, Point& p) const {
+        p.rec = erec + static_cast<std::size_t>(e - e0) * REC;
+        if (!edge_active(p.rec)) return false;
+        p.x = p.rec[0];
+        p.xx = p.x * p.x;
+        p.xxx = p.xx * p.x;
+        p.cf = coef + static_cast<std::size_t>(__float_as_int(p.rec[1])) * functions;
+        return true;
+    }
+    __device__ __forceinline__ float Y(const Point& p, int lm) const { return p.rec[4 + lm]; }
+    __device__ __forceinline__ float dY(const Point& p, int c, int lm) const { return p.rec[4 + NY + c * NY + lm]; }
+    __device__ __forceinline__ float u(const Point& p, int c) const { return p.rec[4 + 4 * NY + c]; }
+    __device__ __forceinline__ float value(const Point& p, int f) const {
+        return spline_value(p.cf[f], p.x, p.xx, p.xxx);
+    }
+    __device__ __forceinline__ void value_slope(const Point& p, int f, float& R, float& dR) const {
+        const float4 c = p.cf[f];
+        R = spline_value(c, p.x, p.xx, p.xxx);
+        dR = spline_slope(c, p.x, p.xx);
+    }
+};
+
+// Symmetric pair index over active types (jit_codegen.py:2490-2496).
+__device__ __forceinline__ int pair_type(int a, int b, int n) {
+    return a <= b ? a * (2 * n - a - 1) / 2 + b : b * (2 * n - b - 1) / 2 + a;
+}
+
+// The reference plugin's per-edge arrays.  Activity is radius < cutoff; the
+// evaluation point is formed in FP32 from the rounded radius (fp64_point 0,
+// the precision-matched form) or in FP64 and rounded (fp64_point 1); the
+// slope uses the factors (2x) and (3xx) formed before the multiply
+// (jit_codegen.py:2387-2485).
+template <int NY>
+struct PluginEdges {
+    const double* __restrict__ radius;
+    const float* __restrict__ harm;    // [E][NY]
+    const float* __restrict__ grad;    // [E][3][NY]
+    const double* __restrict__ xyz64;  // [E][3] (coordinates_are_unit == 0)
+    const float* __restrict__ unit32;  // [E][3] (coordinates_are_unit != 0)
+    const float* __restrict__ coef;    // [edge type][interval][4][function]
+    const int* __restrict__ node_types;
+    const int* __restrict__ neigh_types;
+    const int* __restrict__ type_to_active;
+    double x0, h, cutoff;
+    int intervals, functions, active_types, fp64_point;
+
+    struct Point {
+        int e;
+        const float* c0;  // coefficient c0 of function 0 of this edge's interval
+        float x, xx, xxx, x2, xx3;
+    };
+    __device__ __forceinline__ bool open(int e, int receiver, Point& p) const {
+        const double r = radius[e];
+        if (!(r < cutoff)) return false;
+        int iv;
+        if (fp64_point) {
+            iv = static_cast<int>(floor((r - x0) / h));
+            double x = r - x0 - h * iv;
+            if (iv < 0) {
+                iv = 0;
+                x = 0.0;
+            } else if (iv >= intervals) {
+                iv = intervals - 1;
+                x = h;
+            }
+            const double xx = x * x;
+            p.x = static_cast<float>(x);
+            p.xx = static_cast<float>(xx);
+            p.xxx = static_cast<float>(xx * x);
+            p.x2 = static_cast<float>(2.0 * x);
+            p.xx3 = static_cast<float>(3.0 * xx);
+        } else {
+            const float rf = static_cast<float>(r), x0f = static_cast<float>(x0), hf = static_cast<float>(h);
+            iv = static_cast<int>(floorf((rf - x0f) / hf));
+            float x = rf - x0f - hf * static_cast<float>(iv);
+            if (iv < 0) {
+                iv = 0;
+                x = 0.0f;
+            } else if (iv >= intervals) {
+                iv = intervals - 1;
+                x = hf;
+            }
+            p.x = x;
+            p.xx = x * x;
+            p.xxx = p.xx * x;
+            p.x2 = static_cast<float>(2.0 * static_cast<double>(x));
+            p.xx3 = static_cast<float>(3.0 * static_cast<double>(p.xx));
+        }
+        const int t = pair_type(type_to_active[node_types[receiver]], type_to_active[neigh_types[e]], active_types);
+        p.c0 = coef + (static_cast<std::size_t>(t) * intervals + iv) * 4 * functions;
+        p.e = e;
+        return true;
+    }
+    __device__ __forceinline__ float Y(const Point& p, int lm) const {
+        return harm[static_cast<std::size_t>(p.e) * NY + lm];
+    }
+    __device__ __forceinline__ float dY(const Point& p, int c, int lm) const {
+        return grad[(static_cast<std::size_t>(p.e) * 3 + c) * NY + lm];
+    }
+    __device__ __forceinline__ float u(const Point& p, int c) const {
+        return unit32 ? unit32[3 * static_cast<std::size_t>(p.e) + c]
+                      : static_cast<float>(xyz64[3 * static_cast<std::size_t>(p.e) + c] / radius[p.e]);
+    }
+    __device__ __forceinline__ float value(const Point& p, int f) const {
+        const float c0 = p.c0[f], c1 = p.c0[functions + f], c2 = p.c0[2 * functions + f],
+                    c3 = p.c0[3 * functions + f];
+        return c0 + c1 * p.x + c2 * p.xx + c3 * p.xxx;
+    }
+    __device__ __forceinline__ void value_slope(const Point& p, int f, float& R, float& dR) const {
+        const float c0 = p.c0[f], c1 = p.c0[functions + f], c2 = p.c0[2 * functions + f],
+                    c3 = p.c0[3 * functions + f];
+        R = c0 + c1 * p.x + c2 * p.xx + c3 * p.xxx;
+        dR = c1 + c2 * p.x2 + c3 * p.xx3;
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Per-edge directed forces: per-lane partials (fx,fy,fz) are summed over the
+// channels of the workgroup; chunks of edges are finalised together.
+// ---------------------------------------------------------------------------
+template <int C, int CHUNK>
+struct EdgeForceSink {
+    float (*part)[CHUNK][3];
+    __device__ __forceinline__ void put(int slot, float fx, float fy, float fz) {
+        fx = wave_total<Lanes<C>::WIDTH>(fx);
+        fy = wave_total<Lanes<C>::WIDTH>(fy);
+        fz = wave_total<Lanes<C>::WIDTH>(fz);
+        if (threadIdx.x % kWave == 0) {
+            const int w = threadIdx.x / kWave;
+            part[w][slot][0] = fx;
+            part[w][slot][1] = fy;
+            part[w][slot][2] = fz;
+        }
+    }
+    __device__ __forceinline__ void zero(int slot) {
+        if (threadIdx.x % kWave == 0) {
+            const int w = threadIdx.x / kWave;
+            part[w][slot][0] = part[w][slot][1] = part[w][slot][2] = 0.0f;
+        }
+    }
+    // node_forces[e] = -f (assign) or node_forces[e] -= f (accumulate)
+    template <bool ACCUMULATE>
+    __device__ __forceinline__ void flush(long long c0, int count, double* __restrict__ node_forces) {
+        __syncthreads();
+        for (int t = threadIdx.x; t < count * 3; t += C) {
+            const int el = t / 3, comp = t % 3;
+            float s = 0.0f;
+#pragma unroll
+            for (int w = 0; w < Lanes<C>::NW; ++w) s += part[w][el][comp];
+            double* dst = node_forces + static_cast<std::size_t>(c0 + el) * 3 + comp;
+            if (ACCUMULATE)
+                *dst = *dst - static_cast<double>(s);
+            else
+                *dst = 0.0 - static_cast<double>(s);
+        }
+        __syncthreads();
+    }
+};
+
+constexpr int kForceChunk = 64;
+
+// ---------------------------------------------------------------------------
+// R1 forward: rows[i,(p,m1,m2),k] = sum_j R1_{p,k}(r) Y_{lm1} H1[j,lm2,k];
+// Phi1[i,lme,k] = sum CG rows (dense per-path coupling blocks), assigned.
+// Receiver i = r0 + li owns edges [first[i], first[i]+count[i]) (or
+// [first[i], first[i+1]) when count is null); Phi1 rows are indexed by li.
+// ---------------------------------------------------------------------------
+template <int C, int LMAX, int LMAXH, class EDGES>
+__global__ __launch_bounds__(C) void k_r1_forward(int r0, const int* __restrict__ first,
+                                                  const int* __restrict__ count, const int* __restrict__ neigh,
+                                                  EDGES edges, const float* __restrict__ H1,
+                                                  const float* __restrict__ cg, float* __restrict__ Phi1) {
+    using S = Shape<LMAX, LMAXH>;
+    constexpr int NH = S::NH;
+    const int li = xcd_remap(blockIdx.x, gridDim.x);
+    const int i = r0 + li;
+    const int k = threadIdx.x;
+    float rows[S::NROWS];
+#pragma unroll
+    for (int r = 0; r < S::NROWS; ++r) rows[r] = 0.0f;
+    const int ea = first[i], eb = count ? ea + count[i] : first[i + 1];
+    for (int e = ea; e < eb; ++e) {
+        typename EDGES::Point pt;
+        if (!edges.open(e, i, pt)) continue;
+        const float* hj = H1 + static_cast<std::size_t>(neigh[e]) * NH * C + k;
+        float h[NH];
+#pragma unroll
+        for (int q = 0; q < NH; ++q) h[q] = hj[q * C];
+        static_for<0, S::P>([&](auto pc) {
+            constexpr int p = pc;
+            constexpr int le = S::paths[p].le, ls = S::paths[p].ls, rb = S::row_base[p];
+            const float rad = edges.value(pt, p * C + k);
+            static_for<0, 2 * le + 1>([&](auto m1c) {
+                constexpr int m1 = m1c;
+                const float ry = rad * edges.Y(pt, le * le + m1);
+                static_for<0, 2 * ls + 1>([&](auto m2c) {
+                    constexpr int m2 = m2c;
+                    rows[rb + m1 * (2 * ls + 1) + m2] += ry * h[ls * ls + m2];
+                });
+            });
+        });
+    }
+    float out[S::NLME];
+#pragma unroll
+    for (int q = 0; q < S::NLME; ++q) out[q] = 0.0f;
+    static_for<0, S::P>([&](auto pc) {
+        constexpr int p = pc;
+        constexpr int le = S::paths[p].le, ls = S::paths[p].ls, lo = S::paths[p].lo;
+        constexpr int rb = S::row_base[p], co = S::cg_offset[p];
+        static_for<0, (2 * le + 1) * (2 * ls + 1)>([&](auto rc) {
+            constexpr int r = rc;
+            static_for<0, 2 * lo + 1>([&](auto mc) {
+                constexpr int mo = mc;
+                constexpr int q = S::lme(p, mo);
+                out[q] += cg[co + r * (2 * lo + 1) + mo] * rows[rb + r];
+            });
+        });
+    });
+#pragma unroll
+    for (int q = 0; q < S::NLME; ++q) Phi1[(static_cast<std::size_t>(li) * S::NLME + q) * C + k] = out[q];
+}
+
+// ---------------------------------------------------------------------------
+// Fused R1 reverse, receiver-owned: per edge the directed force
+//   f_e = -sum_k sum_rows G[row] H1[j,lm2] (u dR Y_lm1 + R dY_lm1)
+// and the per-edge source-adjoint contribution
+//   W_e[lm2,k] = sum_{p,m1} R Y_lm1 G[row]   (zero for inactive edges)
+// that k_source_gather sums over each source's edges.  G = CG^T dPhi1[li].
+// W and node_forces are indexed by e - e0; forces are assigned (-f) or, with
+// ACCUMULATE, subtracted from what the buffer holds.
+// ---------------------------------------------------------------------------
+template <int C, int LMAX, int LMAXH, bool ACCUMULATE, class EDGES>
+__global__ __launch_bounds__(C) void k_r1_reverse(int r0, long long e0, const int* __restrict__ offsets,
+                                                  const int* __restrict__ neigh, EDGES edges,
+                                                  const float* __restrict__ H1, const float* __restrict__ cg,
+                                                  const float* __restrict__ dPhi1, float* __restrict__ Wsrc,
+                                                  double* __restrict__ node_forces) {
+    using S = Shape<LMAX, LMAXH>;
+    constexpr int NY = S::NY, NH = S::NH;
+    __shared__ float part[Lanes<C>::NW][kForceChunk][3];
+    EdgeForceSink<C, kForceChunk> sink{part};
+    const int li = xcd_remap(blockIdx.x, gridDim.x);
+    const int i = r0 + li;
+    const int k = threadIdx.x;
+    float G[S::NROWS];
+    {
+        float d[S::NLME];
+#pragma unroll
+        for (int q = 0; q < S::NLME; ++q) d[q] = dPhi1[(static_cast<std::size_t>(li) * S::NLME + q) * C + k];
+        static_for<0, S::P>([&](auto pc) {
+            constexpr int p = pc;
+            constexpr int le = S::paths[p].le, ls = S::paths[p].ls, lo = S::paths[p].lo;
+            constexpr int rb = S::row_base[p], co = S::cg_offset[p];
+            static_for<0, (2 * le + 1) * (2 * ls + 1)>([&](auto rc) {
+                constexpr int r = rc;
+                float g = 0.0f;
+                static_for<0, 2 * lo + 1>([&](auto mc) {
+                    constexpr int mo = mc;
+                    constexpr int q = S::lme(p, mo);
+                    g += cg[co + r * (2 * lo + 1) + mo] * d[q];
+                });
+                G[rb + r] = g;
+            });
+        });
+    }
+    const int ea = offsets[i], eb = offsets[i + 1];
+    for (int c0 = ea; c0 < eb; c0 += kForceChunk) {
+        const int c1 = min(c0 + kForceChunk, eb);
+        for (int e = c0; e < c1; ++e) {
+            float* wdst = Wsrc + static_cast<std::size_t>(e - e0) * NH * C + k;
+            typename EDGES::Point pt;
+            if (!edges.open(e, i, pt)) {
+                // inactive edges contribute zero to their source's adjoint
+#pragma unroll
+                for (int q = 0; q < NH; ++q) wdst[q * C] = 0.0f;
+                sink.zero(e - c0);
+                continue;
+            }
+            const float* hj = H1 + static_cast<std::size_t>(neigh[e]) * NH * C + k;
+            float h[NH], W[NH];
+#pragma unroll
+            for (int q = 0; q < NH; ++q) {
+                h[q] = hj[q * C];
+                W[q] = 0.0f;
+            }
+            // Per path p, with T[m2] = sum_m1 Y_m1 G[p,m1,m2] and
+            // s[m1] = sum_m2 G[p,m1,m2] h_m2:
+            //   W[m2] += R T[m2],  A += dR sum_m2 h_m2 T[m2],  SB[lm1] += R s[m1];
+            // then f = u A + sum_lm1 dY_lm1 SB[lm1].
+            float A = 0.0f, SB[NY];
+#pragma unroll
+            for (int v = 0; v < NY; ++v) SB[v] = 0.0f;
+            static_for<0, S::P>([&](auto pc) {
+                constexpr int p = pc;
+                constexpr int le = S::paths[p].le, ls = S::paths[p].ls, rb = S::row_base[p];
+                float R, dR;
+                edges.value_slope(pt, p * C + k, R, dR);
+                float T[2 * ls + 1];
+                static_for<0, 2 * ls + 1>([&](auto m2c) { T[m2c] = 0.0f; });
+                static_for<0, 2 * le + 1>([&](auto m1c) {
+                    constexpr int m1 = m1c;
+                    const float y = edges.Y(pt, le * le + m1);
+                    float sr = 0.0f;
+                    static_for<0, 2 * ls + 1>([&](auto m2c) {
+                        constexpr int m2 = m2c;
+                        const float g = G[rb + m1 * (2 * ls + 1) + m2];
+                        T[m2] += y * g;
+                        sr += g * h[ls * ls + m2];
+                    });
+                    SB[le * le + m1] += R * sr;
+                });
+                float hT = 0.0f;
+                static_for<0, 2 * ls + 1>([&](auto m2c) {
+                    constexpr int m2 = m2c;
+                    W[ls * ls + m2] += R * T[m2];
+                    hT += h[ls * ls + m2] * T[m2];
+                });
+                A += dR * hT;
+            });
+            float b0 = 0.0f, b1 = 0.0f, b2 = 0.0f;
+#pragma unroll
+            for (int v = 0; v < NY; ++v) {
+                b0 += SB[v] * edges.dY(pt, 0, v);
+                b1 += SB[v] * edges.dY(pt, 1, v);
+                b2 += SB[v] * edges.dY(pt, 2, v);
+            }
+#pragma unroll
+            for (int q = 0; q < NH; ++q) wdst[q * C] = W[q];
+            sink.put(e - c0, edges.u(pt, 0) * A + b0, edges.u(pt, 1) * A + b1, edges.u(pt, 2) * A + b2);
+        }
+        sink.template flush<ACCUMULATE>(static_cast<long long>(c0) - e0, c1 - c0, node_forces);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Source adjoint: sum over the edges leaving s (source-transpose order) of
+// W_e, accumulated in FP64 like the reference's source-adjoint accumulator.
+// Four edges are loaded per step so that their independent rows are in
+// flight together; the sum keeps the source-transpose order.
+// ---------------------------------------------------------------------------
+template <int C, int NH>
+__device__ __forceinline__ void gather_source_rows(const int* __restrict__ sedges, int t0, int t1, long long e_base,
+                                                   const float* __restrict__ Wsrc, int k, double* acc) {
+    int t = t0;
+    for (; t + 4 <= t1; t += 4) {
+        float w[4][NH];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const float* row = Wsrc + static_cast<std::size_t>(sedges[t + u] - e_base) * NH * C + k;
+#pragma unroll
+            for (int q = 0; q < NH; ++q) w[u][q] = row[q * C];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int q = 0; q < NH; ++q) acc[q] += static_cast<double>(w[u][q]);
+    }
+    for (; t < t1; ++t) {
+        const float* row = Wsrc + static_cast<std::size_t>(sedges[t] - e_base) * NH * C + k;
+#pragma unroll
+        for (int q = 0; q < NH; ++q) acc[q] += static_cast<double>(row[q * C]);
+    }
+}
+
+// H1_adj[s] = (or, with ACCUMULATE, +=) the FP64 sum of W over s's edges
+template <int C, int NH, bool ACCUMULATE>
+__global__ __launch_bounds__(C) void k_source_gather(const int* __restrict__ soff, const int* __restrict__ sedges,
+                                                     const float* __restrict__ Wsrc, float* __restrict__ H1_adj) {
+    const int s = xcd_remap(blockIdx.x, gridDim.x);
+    const int k = threadIdx.x;
+    double acc[NH];
+#pragma unroll
+    for (int q = 0; q < NH; ++q) acc[q] = 0.0;
+    gather_source_rows<C, NH>(sedges, soff[s], soff[s + 1], 0, Wsrc, k, acc);
+    float* dst = H1_adj + static_cast<std::size_t>(s) * NH * C + k;
+#pragma unroll
+    for (int q = 0; q < NH; ++q) dst[q * C] = ACCUMULATE ? dst[q * C] + static_cast<float>(acc[q])
+                                                        : static_cast<float>(acc[q]);
+}
+
+}  // namespace
+}  // namespace edge
+}  // namespace smx

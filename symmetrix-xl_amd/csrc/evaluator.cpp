@@ -195,6 +195,8 @@ struct PlanSet {
 
 }  // namespace
 
+void set_last_error(const std::string& message) { g_last_error = message; }
+
 struct Evaluator {
     HostModel hm;
     DeviceModel dm;

@@ -23,6 +23,7 @@
 #include <type_traits>
 
 #include "device_common.hpp"
+#include "edge_kernels.hpp"
 #include "kernels.hpp"
 #include "product_tables.hpp"
 #include "shapes.hpp"
@@ -30,21 +31,9 @@
 namespace smx {
 namespace {
 
+using namespace edge;
+
 typedef float v4f __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ float spline_value(float4 c, float x, float xx, float xxx) {
-    return c.x + c.y * x + c.z * xx + c.w * xxx;
-}
-__device__ __forceinline__ float spline_slope(float4 c, float x, float xx) {
-    return c.y + 2.0f * c.z * x + 3.0f * c.w * xx;
-}
-__device__ __forceinline__ bool edge_active(const float* rec) { return __float_as_int(rec[2]) != 0; }
-
-template <int C>
-struct Lanes {
-    static constexpr int NW = (C + kWave - 1) / kWave;
-    static constexpr int WIDTH = C < kWave ? C : kWave;
-};
 
 // Sum over the workgroup (C lanes, one value each); every lane gets the total.
 template <int C>
@@ -97,49 +86,6 @@ __global__ __launch_bounds__(C) void k_r0_forward(int r0, long long e0, const in
 #pragma unroll
     for (int v = 0; v < NY; ++v) Phi0[(static_cast<std::size_t>(li) * NY + v) * C + k] = acc[v];
 }
-
-// Per-edge directed forces: per-lane partials (fx,fy,fz) are summed over the
-// channels of the workgroup; chunks of edges are finalised together.
-template <int C, int CHUNK>
-struct EdgeForceSink {
-    float (*part)[CHUNK][3];
-    __device__ __forceinline__ void put(int slot, float fx, float fy, float fz) {
-        fx = wave_total<Lanes<C>::WIDTH>(fx);
-        fy = wave_total<Lanes<C>::WIDTH>(fy);
-        fz = wave_total<Lanes<C>::WIDTH>(fz);
-        if (threadIdx.x % kWave == 0) {
-            const int w = threadIdx.x / kWave;
-            part[w][slot][0] = fx;
-            part[w][slot][1] = fy;
-            part[w][slot][2] = fz;
-        }
-    }
-    __device__ __forceinline__ void zero(int slot) {
-        if (threadIdx.x % kWave == 0) {
-            const int w = threadIdx.x / kWave;
-            part[w][slot][0] = part[w][slot][1] = part[w][slot][2] = 0.0f;
-        }
-    }
-    // node_forces[e] = -f (assign) or node_forces[e] -= f (accumulate)
-    template <bool ACCUMULATE>
-    __device__ __forceinline__ void flush(int c0, int count, double* __restrict__ node_forces) {
-        __syncthreads();
-        for (int t = threadIdx.x; t < count * 3; t += C) {
-            const int el = t / 3, comp = t % 3;
-            float s = 0.0f;
-#pragma unroll
-            for (int w = 0; w < Lanes<C>::NW; ++w) s += part[w][el][comp];
-            double* dst = node_forces + static_cast<std::size_t>(c0 + el) * 3 + comp;
-            if (ACCUMULATE)
-                *dst = *dst - static_cast<double>(s);
-            else
-                *dst = 0.0 - static_cast<double>(s);
-        }
-        __syncthreads();
-    }
-};
-
-constexpr int kForceChunk = 64;
 
 // Layer-1 reverse: node_forces[e] -= sum_k sum_lm Phi0_adj[i,lm,k] H0 (u dR Y + R dY)
 template <int C, int LMAX, bool ACCUMULATE>
@@ -197,225 +143,6 @@ __global__ __launch_bounds__(C) void k_r0_reverse(int r0, long long e0, const in
         }
         sink.template flush<ACCUMULATE>(static_cast<int>(c0 - e0), c1 - c0, node_forces);
     }
-}
-
-// ---------------------------------------------------------------------------
-// Layer 2 (R1): rows[i,(p,m1,m2),k] = sum_j R1_{p,k}(r) Y_{lm1} H1[j,lm2,k];
-// Phi1[i,lme,k] = sum CG rows (dense per-path coupling blocks).
-// ---------------------------------------------------------------------------
-template <int C, int LMAX, int LMAXH>
-__global__ __launch_bounds__(C) void k_r1_forward(int r0, long long e0, const int* __restrict__ offsets,
-                                                  const int* __restrict__ neigh, const float* __restrict__ erec,
-                                                  const float4* __restrict__ R1c, const float* __restrict__ H1,
-                                                  const float* __restrict__ cg, float* __restrict__ Phi1) {
-    using S = Shape<LMAX, LMAXH>;
-    constexpr int NH = S::NH, NF = S::P * C;
-    const int li = xcd_remap(blockIdx.x, gridDim.x);
-    const int i = r0 + li;
-    const int k = threadIdx.x;
-    float rows[S::NROWS];
-#pragma unroll
-    for (int r = 0; r < S::NROWS; ++r) rows[r] = 0.0f;
-    const int ea = offsets[i], eb = offsets[i + 1];
-    for (int e = ea; e < eb; ++e) {
-        const float* rec = erec + static_cast<std::size_t>(e - e0) * S::REC;
-        if (!edge_active(rec)) continue;
-        const float x = rec[0];
-        const int iv = __float_as_int(rec[1]);
-        const float xx = x * x, xxx = xx * x;
-        const float* hj = H1 + static_cast<std::size_t>(neigh[e]) * NH * C + k;
-        float h[NH];
-#pragma unroll
-        for (int q = 0; q < NH; ++q) h[q] = hj[q * C];
-        const float4* cf = R1c + static_cast<std::size_t>(iv) * NF + k;
-        static_for<0, S::P>([&](auto pc) {
-            constexpr int p = pc;
-            constexpr int le = S::paths[p].le, ls = S::paths[p].ls, rb = S::row_base[p];
-            const float rad = spline_value(cf[p * C], x, xx, xxx);
-            static_for<0, 2 * le + 1>([&](auto m1c) {
-                constexpr int m1 = m1c;
-                const float ry = rad * rec[S::REC_Y + le * le + m1];
-                static_for<0, 2 * ls + 1>([&](auto m2c) {
-                    constexpr int m2 = m2c;
-                    rows[rb + m1 * (2 * ls + 1) + m2] += ry * h[ls * ls + m2];
-                });
-            });
-        });
-    }
-    float out[S::NLME];
-#pragma unroll
-    for (int q = 0; q < S::NLME; ++q) out[q] = 0.0f;
-    static_for<0, S::P>([&](auto pc) {
-        constexpr int p = pc;
-        constexpr int le = S::paths[p].le, ls = S::paths[p].ls, lo = S::paths[p].lo;
-        constexpr int rb = S::row_base[p], co = S::cg_offset[p];
-        static_for<0, (2 * le + 1) * (2 * ls + 1)>([&](auto rc) {
-            constexpr int r = rc;
-            static_for<0, 2 * lo + 1>([&](auto mc) {
-                constexpr int mo = mc;
-                constexpr int q = S::lme(p, mo);
-                out[q] += cg[co + r * (2 * lo + 1) + mo] * rows[rb + r];
-            });
-        });
-    });
-#pragma unroll
-    for (int q = 0; q < S::NLME; ++q) Phi1[(static_cast<std::size_t>(li) * S::NLME + q) * C + k] = out[q];
-}
-
-// Fused R1 reverse, receiver-owned: per edge the directed force
-//   f_e = -sum_k sum_rows G[row] H1[j,lm2] (u dR Y_lm1 + R dY_lm1)
-// and the per-edge source-adjoint contribution
-//   W_e[lm2,k] = sum_{p,m1} R Y_lm1 G[row]
-// that k_source_gather sums over each source's edges.
-template <int C, int LMAX, int LMAXH>
-__global__ __launch_bounds__(C) void k_r1_reverse(int r0, long long e0, const int* __restrict__ offsets,
-                                                  const int* __restrict__ neigh, const float* __restrict__ erec,
-                                                  const float4* __restrict__ R1c, const float* __restrict__ H1,
-                                                  const float* __restrict__ cg, const float* __restrict__ dPhi1,
-                                                  float* __restrict__ Wsrc, double* __restrict__ node_forces) {
-    using S = Shape<LMAX, LMAXH>;
-    constexpr int NY = S::NY, NH = S::NH, NF = S::P * C;
-    __shared__ float part[Lanes<C>::NW][kForceChunk][3];
-    EdgeForceSink<C, kForceChunk> sink{part};
-    const int li = xcd_remap(blockIdx.x, gridDim.x);
-    const int i = r0 + li;
-    const int k = threadIdx.x;
-    float G[S::NROWS];
-    {
-        float d[S::NLME];
-#pragma unroll
-        for (int q = 0; q < S::NLME; ++q) d[q] = dPhi1[(static_cast<std::size_t>(li) * S::NLME + q) * C + k];
-        static_for<0, S::P>([&](auto pc) {
-            constexpr int p = pc;
-            constexpr int le = S::paths[p].le, ls = S::paths[p].ls, lo = S::paths[p].lo;
-            constexpr int rb = S::row_base[p], co = S::cg_offset[p];
-            static_for<0, (2 * le + 1) * (2 * ls + 1)>([&](auto rc) {
-                constexpr int r = rc;
-                float g = 0.0f;
-                static_for<0, 2 * lo + 1>([&](auto mc) {
-                    constexpr int mo = mc;
-                    constexpr int q = S::lme(p, mo);
-                    g += cg[co + r * (2 * lo + 1) + mo] * d[q];
-                });
-                G[rb + r] = g;
-            });
-        });
-    }
-    const int ea = offsets[i], eb = offsets[i + 1];
-    for (int c0 = ea; c0 < eb; c0 += kForceChunk) {
-        const int c1 = min(c0 + kForceChunk, eb);
-        for (int e = c0; e < c1; ++e) {
-            const float* rec = erec + static_cast<std::size_t>(e - e0) * S::REC;
-            float* wdst = Wsrc + static_cast<std::size_t>(e - e0) * NH * C + k;
-            if (!edge_active(rec)) {
-                // inactive edges contribute zero to their source's adjoint
-#pragma unroll
-                for (int q = 0; q < NH; ++q) wdst[q * C] = 0.0f;
-                sink.zero(e - c0);
-                continue;
-            }
-            const float x = rec[0];
-            const int iv = __float_as_int(rec[1]);
-            const float xx = x * x, xxx = xx * x;
-            const float* hj = H1 + static_cast<std::size_t>(neigh[e]) * NH * C + k;
-            float h[NH], W[NH];
-#pragma unroll
-            for (int q = 0; q < NH; ++q) {
-                h[q] = hj[q * C];
-                W[q] = 0.0f;
-            }
-            const float4* cf = R1c + static_cast<std::size_t>(iv) * NF + k;
-            // Per path p, with T[m2] = sum_m1 Y_m1 G[p,m1,m2] and
-            // s[m1] = sum_m2 G[p,m1,m2] h_m2:
-            //   W[m2] += R T[m2],  A += dR sum_m2 h_m2 T[m2],  SB[lm1] += R s[m1];
-            // then f = u A + sum_lm1 dY_lm1 SB[lm1].
-            float A = 0.0f, SB[NY];
-#pragma unroll
-            for (int v = 0; v < NY; ++v) SB[v] = 0.0f;
-            static_for<0, S::P>([&](auto pc) {
-                constexpr int p = pc;
-                constexpr int le = S::paths[p].le, ls = S::paths[p].ls, rb = S::row_base[p];
-                const float4 c4 = cf[p * C];
-                const float R = spline_value(c4, x, xx, xxx);
-                const float dR = spline_slope(c4, x, xx);
-                float T[2 * ls + 1];
-                static_for<0, 2 * ls + 1>([&](auto m2c) { T[m2c] = 0.0f; });
-                static_for<0, 2 * le + 1>([&](auto m1c) {
-                    constexpr int m1 = m1c;
-                    const float y = rec[S::REC_Y + le * le + m1];
-                    float sr = 0.0f;
-                    static_for<0, 2 * ls + 1>([&](auto m2c) {
-                        constexpr int m2 = m2c;
-                        const float g = G[rb + m1 * (2 * ls + 1) + m2];
-                        T[m2] += y * g;
-                        sr += g * h[ls * ls + m2];
-                    });
-                    SB[le * le + m1] += R * sr;
-                });
-                float hT = 0.0f;
-                static_for<0, 2 * ls + 1>([&](auto m2c) {
-                    constexpr int m2 = m2c;
-                    W[ls * ls + m2] += R * T[m2];
-                    hT += h[ls * ls + m2] * T[m2];
-                });
-                A += dR * hT;
-            });
-            float b0 = 0.0f, b1 = 0.0f, b2 = 0.0f;
-#pragma unroll
-            for (int v = 0; v < NY; ++v) {
-                b0 += SB[v] * rec[S::REC_DY + v];
-                b1 += SB[v] * rec[S::REC_DY + NY + v];
-                b2 += SB[v] * rec[S::REC_DY + 2 * NY + v];
-            }
-#pragma unroll
-            for (int q = 0; q < NH; ++q) wdst[q * C] = W[q];
-            const float u0 = rec[S::REC_U], u1 = rec[S::REC_U + 1], u2 = rec[S::REC_U + 2];
-            sink.put(e - c0, u0 * A + b0, u1 * A + b1, u2 * A + b2);
-        }
-        sink.template flush<false>(static_cast<int>(c0 - e0), c1 - c0, node_forces);
-    }
-}
-
-// H1_adj[s] = sum over the edges leaving s (source transpose order) of W_e,
-// accumulated in FP64 like the reference's source-adjoint accumulator
-// (inactive edges carry W_e = 0).  Four edges are loaded per step so that
-// their independent 2 KB rows are in flight together; the sum keeps the
-// source-transpose order.
-template <int C, int NH>
-__device__ __forceinline__ void gather_source_rows(const int* __restrict__ sedges, int t0, int t1, long long e_base,
-                                                   const float* __restrict__ Wsrc, int k, double* acc) {
-    int t = t0;
-    for (; t + 4 <= t1; t += 4) {
-        float w[4][NH];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const float* row = Wsrc + static_cast<std::size_t>(sedges[t + u] - e_base) * NH * C + k;
-#pragma unroll
-            for (int q = 0; q < NH; ++q) w[u][q] = row[q * C];
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-#pragma unroll
-            for (int q = 0; q < NH; ++q) acc[q] += static_cast<double>(w[u][q]);
-    }
-    for (; t < t1; ++t) {
-        const float* row = Wsrc + static_cast<std::size_t>(sedges[t] - e_base) * NH * C + k;
-#pragma unroll
-        for (int q = 0; q < NH; ++q) acc[q] += static_cast<double>(row[q * C]);
-    }
-}
-
-template <int C, int NH>
-__global__ __launch_bounds__(C) void k_source_gather(const int* __restrict__ soff, const int* __restrict__ sedges,
-                                                     const float* __restrict__ Wsrc, float* __restrict__ H1_adj) {
-    const int s = xcd_remap(blockIdx.x, gridDim.x);
-    const int k = threadIdx.x;
-    double acc[NH];
-#pragma unroll
-    for (int q = 0; q < NH; ++q) acc[q] = 0.0;
-    gather_source_rows<C, NH>(sedges, soff[s], soff[s + 1], 0, Wsrc, k, acc);
-#pragma unroll
-    for (int q = 0; q < NH; ++q) H1_adj[(static_cast<std::size_t>(s) * NH + q) * C + k] = static_cast<float>(acc[q]);
 }
 
 // ---------------------------------------------------------------------------
@@ -1103,7 +830,11 @@ template <int C, int LMAX, int LMAXH, class M0TAB, class M1TAB>
 struct KernelSetImpl final : KernelSet {
     using S = Shape<LMAX, LMAXH>;
     static constexpr bool kM0Unrolled = !std::is_same_v<M0TAB, void>;
+    using Records = RecordEdges<S::NY, S::REC>;
     int record_floats() const override { return S::REC; }
+    static Records records(const DeviceModel& m, const TileView& t, const Workspace& w) {
+        return Records{w.erec, t.e0, m.R1c, S::P * C};
+    }
     const char* polynomial_mode() const override { return kM0Unrolled ? "unrolled" : "table"; }
 
     void edge_geometry(const DeviceModel& m, std::int64_t E, const double* xyz, const double* r, float* erec,
@@ -1146,8 +877,8 @@ struct KernelSetImpl final : KernelSet {
         if (t.nr == 0) return;
         {
             TimerScope ts(tm, "r1_forward", s);
-            k_r1_forward<C, LMAX, LMAXH><<<t.nr, C, 0, s>>>(t.r0, t.e0, g.offsets, g.neigh, w.erec, m.R1c, w.H1, m.cg,
-                                                           w.Phi1);
+            k_r1_forward<C, LMAX, LMAXH, Records><<<t.nr, C, 0, s>>>(t.r0, g.offsets, nullptr, g.neigh,
+                                                                    records(m, t, w), w.H1, m.cg, w.Phi1);
             SMX_LAUNCH_CHECK("r1_forward");
         }
         {
@@ -1170,8 +901,8 @@ struct KernelSetImpl final : KernelSet {
         }
         {
             TimerScope ts(tm, "r1_reverse", s);
-            k_r1_reverse<C, LMAX, LMAXH><<<t.nr, C, 0, s>>>(t.r0, t.e0, g.offsets, g.neigh, w.erec, m.R1c, w.H1, m.cg,
-                                                           w.dPhi1, w.Wsrc, w.node_forces);
+            k_r1_reverse<C, LMAX, LMAXH, false, Records><<<t.nr, C, 0, s>>>(
+                t.r0, t.e0, g.offsets, g.neigh, records(m, t, w), w.H1, m.cg, w.dPhi1, w.Wsrc, w.node_forces);
             SMX_LAUNCH_CHECK("r1_reverse");
         }
     }
@@ -1179,7 +910,7 @@ struct KernelSetImpl final : KernelSet {
     void source_adjoint_all(const DeviceGraph& g, const Workspace& w, hipStream_t s, LaunchTimer* tm) const override {
         if (g.N == 0) return;
         TimerScope ts(tm, "source_gather", s);
-        k_source_gather<C, S::NH><<<g.N, C, 0, s>>>(g.soff, g.sedges, w.Wsrc, w.H1_adj);
+        k_source_gather<C, S::NH, false><<<g.N, C, 0, s>>>(g.soff, g.sedges, w.Wsrc, w.H1_adj);
         SMX_LAUNCH_CHECK("source_gather");
     }
 

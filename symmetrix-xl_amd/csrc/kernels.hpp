@@ -6,6 +6,7 @@
 
 #include <cstdint>
 #include <memory>
+#include <string>
 #include <vector>
 
 namespace smx {
@@ -168,6 +169,9 @@ struct KernelSet {
     virtual void layer1_reverse(const DeviceModel& m, const DeviceGraph& g, const TileView& t, const Workspace& w,
                                 bool accumulate_forces, hipStream_t s, LaunchTimer* tm) const = 0;
 };
+
+// Message returned by smx_last_error() on the calling thread.
+void set_last_error(const std::string& message);
 
 // Kernels for (C, l_max, L_max).  The polynomial kernels run with every
 // product-basis term unrolled when the model's canonical M0 and M1 monomial

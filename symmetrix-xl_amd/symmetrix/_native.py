@@ -44,6 +44,14 @@ class SmxDeviceOutputs(ctypes.Structure):
                 ("xyz", ctypes.c_void_p), ("r", ctypes.c_void_p)]
 
 
+class SmxR1PluginIdentity(ctypes.Structure):
+    _fields_ = [("struct_size", ctypes.c_uint32), ("artifact_id", ctypes.c_char_p),
+                ("contract_fingerprint", ctypes.c_char_p), ("semantic_fingerprint", ctypes.c_char_p),
+                ("structure_fingerprint", ctypes.c_char_p), ("target_features", ctypes.c_char_p),
+                ("embedding", ctypes.c_int32), ("fp64_evaluation_point", ctypes.c_int32),
+                ("persistent_blocks_per_compute_unit", ctypes.c_int32)]
+
+
 # (name, restype, argtypes) of every exported entry point
 _i32 = ctypes.c_int32
 _i64 = ctypes.c_int64
@@ -89,6 +97,8 @@ SIGNATURES = [
     ("smx_kernel_timing_reset", _i32, [_vp]),
     ("smx_kernel_timing", _i32, [_vp, _i32, ctypes.POINTER(_cp), _p_dbl, _p_i64]),
     ("smx_neighbor_list", _i32, [_i32, _vp, _vp, _vp, _dbl, _p_i64, _vp, _vp, _vp, _vp, _vp]),
+    ("smx_r1_plugin_configure", _i32, [_cp, ctypes.POINTER(SmxR1PluginIdentity)]),
+    ("smx_r1_plugin_spline_table", _i32, [_vp, _i64, _p_i32, _p_i32, _p_dbl, _p_dbl]),
 ]
 
 
