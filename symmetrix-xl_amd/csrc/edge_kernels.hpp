@@ -337,7 +337,7 @@ __global__ __launch_bounds__(C) void k_r1_reverse(int r0, long long e0, const in
             if (!edges.open(e, i, pt)) {
                 // inactive edges contribute zero to their source's adjoint
 #pragma unroll
-                for (int q = 0; q < NH; ++q) wdst[q * C] = 0.0f;
+                for (int q = 0; q < NH; ++q) __builtin_nontemporal_store(0.0f, wdst + q * C);
                 sink.zero(e - c0);
                 continue;
             }
@@ -389,8 +389,10 @@ __global__ __launch_bounds__(C) void k_r1_reverse(int r0, long long e0, const in
                 b1 += SB[v] * edges.dY(pt, 1, v);
                 b2 += SB[v] * edges.dY(pt, 2, v);
             }
+            // W is streamed (read once, by the source gather): keep it out of
+            // the cache lines that H1 and the spline table reuse
 #pragma unroll
-            for (int q = 0; q < NH; ++q) wdst[q * C] = W[q];
+            for (int q = 0; q < NH; ++q) __builtin_nontemporal_store(W[q], wdst + q * C);
             sink.put(e - c0, edges.u(pt, 0) * A + b0, edges.u(pt, 1) * A + b1, edges.u(pt, 2) * A + b2);
         }
         sink.template flush<ACCUMULATE>(static_cast<long long>(c0) - e0, c1 - c0, node_forces);
@@ -413,7 +415,7 @@ __device__ __forceinline__ void gather_source_rows(const int* __restrict__ sedge
         for (int u = 0; u < 4; ++u) {
             const float* row = Wsrc + static_cast<std::size_t>(sedges[t + u] - e_base) * NH * C + k;
 #pragma unroll
-            for (int q = 0; q < NH; ++q) w[u][q] = row[q * C];
+            for (int q = 0; q < NH; ++q) w[u][q] = __builtin_nontemporal_load(row + q * C);
         }
 #pragma unroll
         for (int u = 0; u < 4; ++u)

@@ -676,13 +676,19 @@ __global__ __launch_bounds__(64) void k_node_gemm(const GemmTile* __restrict__ t
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
     const int chunks = g.K / 16;
-    for (int kc = 0; kc < chunks; ++kc) {
-        float4 a[4], b[4];
+    // operands of chunk kc+1 are loaded while chunk kc runs on the MFMA unit
+    float4 a[4], b[4], an[4], bn[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const float4*>(arow[i] + 16 * kc);
+    for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const float4*>(arow[i]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) b[j] = j < nsub ? B[j * 64] : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int kc = 0; kc < chunks; ++kc) {
+        const int kn = kc + 1 < chunks ? kc + 1 : kc;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) an[i] = *reinterpret_cast<const float4*>(arow[i] + 16 * kn);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-            b[j] = j < nsub ? B[(static_cast<std::size_t>(kc) * nblk + j) * 64] : make_float4(0.f, 0.f, 0.f, 0.f);
+            bn[j] = j < nsub ? B[(static_cast<std::size_t>(kn) * nblk + j) * 64] : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
 #pragma unroll
@@ -697,6 +703,10 @@ __global__ __launch_bounds__(64) void k_node_gemm(const GemmTile* __restrict__ t
                 }
             }
         }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a[i] = an[i];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) b[j] = bn[j];
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
