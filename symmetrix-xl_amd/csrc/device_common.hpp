@@ -49,6 +49,15 @@ __device__ __forceinline__ float dpp_add(float v) {
     return v + __int_as_float(moved);
 }
 
+// Sum over each row of 16 lanes with DPP (quad permutes, half-row and row
+// mirrors); every lane of a row holds its row's sum.
+__device__ __forceinline__ float row_total(float v) {
+    v = dpp_add<0xb1, 0xf>(v);   // quad_perm [1,0,3,2]
+    v = dpp_add<0x4e, 0xf>(v);   // quad_perm [2,3,0,1]
+    v = dpp_add<0x141, 0xf>(v);  // row_half_mirror
+    return dpp_add<0x140, 0xf>(v);  // row_mirror
+}
+
 // Sum over the first WIDTH (32 or 64) lanes of a wave with DPP row
 // operations (quad permutes, half-row and row mirrors, then the row
 // broadcasts 15 and 31), returned wave-uniform from the last lane.

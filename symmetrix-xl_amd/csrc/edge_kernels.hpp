@@ -34,9 +34,9 @@ namespace {
 __device__ __forceinline__ float spline_value(float4 c, float x, float xx, float xxx) {
     return c.x + c.y * x + c.z * xx + c.w * xxx;
 }
-__device__ __forceinline__ float spline_slope(float4 c, float x, float xx) {
-    return c.y + 2.0f * c.z * x + 3.0f * c.w * xx;
-}
+// slope c1 + 2 c2 x + 3 c3 x^2 with the edge's factors x2 = 2x (exact) and
+// xx3 = 3x^2 formed once per edge
+__device__ __forceinline__ float spline_slope(float4 c, float x2, float xx3) { return c.y + c.z * x2 + c.w * xx3; }
 __device__ __forceinline__ bool edge_active(const float* rec) { return __float_as_int(rec[2]) != 0; }
 
 template <int C>
@@ -61,7 +61,7 @@ struct RecordEdges {
     struct Point {
         const float* rec;
         const float4* cf;
-        float x, xx, xxx;
+        float x, xx, xxx, x2, xx3;
     };
     __device__ __forceinline__ bool open(int e, int /*receiver*/, Point& p) const {
         p.rec = erec + static_cast<std::size_t>(e - e0) * REC;
@@ -69,6 +69,8 @@ struct RecordEdges {
         p.x = p.rec[0];
         p.xx = p.x * p.x;
         p.xxx = p.xx * p.x;
+        p.x2 = 2.0f * p.x;
+        p.xx3 = 3.0f * p.xx;
         p.cf = coef + static_cast<std::size_t>(__float_as_int(p.rec[1])) * functions;
         return true;
     }
@@ -81,7 +83,7 @@ struct RecordEdges {
     __device__ __forceinline__ void value_slope(const Point& p, int f, float& R, float& dR) const {
         const float4 c = p.cf[f];
         R = spline_value(c, p.x, p.xx, p.xxx);
-        dR = spline_slope(c, p.x, p.xx);
+        dR = spline_slope(c, p.x2, p.xx3);
     }
 };
 
@@ -181,26 +183,29 @@ struct PluginEdges {
 
 // ---------------------------------------------------------------------------
 // Per-edge directed forces: per-lane partials (fx,fy,fz) are summed over the
-// channels of the workgroup; chunks of edges are finalised together.
+// channels of the workgroup.  Each row of 16 lanes is reduced with DPP and
+// its sum parked in LDS; chunks of edges are finalised together, summing the
+// row partials of every wave.
 // ---------------------------------------------------------------------------
 template <int C, int CHUNK>
 struct EdgeForceSink {
-    float (*part)[CHUNK][3];
+    static constexpr int ROWS = (C + 15) / 16;  // 16-lane rows of the workgroup
+    float (*part)[CHUNK][3];                    // [ROWS][CHUNK][3]
     __device__ __forceinline__ void put(int slot, float fx, float fy, float fz) {
-        fx = wave_total<Lanes<C>::WIDTH>(fx);
-        fy = wave_total<Lanes<C>::WIDTH>(fy);
-        fz = wave_total<Lanes<C>::WIDTH>(fz);
-        if (threadIdx.x % kWave == 0) {
-            const int w = threadIdx.x / kWave;
-            part[w][slot][0] = fx;
-            part[w][slot][1] = fy;
-            part[w][slot][2] = fz;
+        fx = row_total(fx);
+        fy = row_total(fy);
+        fz = row_total(fz);
+        if (threadIdx.x % 16 == 0) {
+            const int r = threadIdx.x / 16;
+            part[r][slot][0] = fx;
+            part[r][slot][1] = fy;
+            part[r][slot][2] = fz;
         }
     }
     __device__ __forceinline__ void zero(int slot) {
-        if (threadIdx.x % kWave == 0) {
-            const int w = threadIdx.x / kWave;
-            part[w][slot][0] = part[w][slot][1] = part[w][slot][2] = 0.0f;
+        if (threadIdx.x % 16 == 0) {
+            const int r = threadIdx.x / 16;
+            part[r][slot][0] = part[r][slot][1] = part[r][slot][2] = 0.0f;
         }
     }
     // node_forces[e] = -f (assign) or node_forces[e] -= f (accumulate)
@@ -211,7 +216,7 @@ struct EdgeForceSink {
             const int el = t / 3, comp = t % 3;
             float s = 0.0f;
 #pragma unroll
-            for (int w = 0; w < Lanes<C>::NW; ++w) s += part[w][el][comp];
+            for (int r = 0; r < ROWS; ++r) s += part[r][el][comp];
             double* dst = node_forces + static_cast<std::size_t>(c0 + el) * 3 + comp;
             if (ACCUMULATE)
                 *dst = *dst - static_cast<double>(s);
@@ -255,14 +260,20 @@ __global__ __launch_bounds__(C) void k_r1_forward(int r0, const int* __restrict_
             constexpr int p = pc;
             constexpr int le = S::paths[p].le, ls = S::paths[p].ls, rb = S::row_base[p];
             const float rad = edges.value(pt, p * C + k);
-            static_for<0, 2 * le + 1>([&](auto m1c) {
-                constexpr int m1 = m1c;
-                const float ry = rad * edges.Y(pt, le * le + m1);
-                static_for<0, 2 * ls + 1>([&](auto m2c) {
-                    constexpr int m2 = m2c;
-                    rows[rb + m1 * (2 * ls + 1) + m2] += ry * h[ls * ls + m2];
+            if constexpr (ls == 0) {
+                // one source component: scale R by it once
+                const float rh = rad * h[0];
+                static_for<0, 2 * le + 1>([&](auto m1c) { rows[rb + m1c] += rh * edges.Y(pt, le * le + m1c); });
+            } else {
+                static_for<0, 2 * le + 1>([&](auto m1c) {
+                    constexpr int m1 = m1c;
+                    const float ry = rad * edges.Y(pt, le * le + m1);
+                    static_for<0, 2 * ls + 1>([&](auto m2c) {
+                        constexpr int m2 = m2c;
+                        rows[rb + m1 * (2 * ls + 1) + m2] += ry * h[ls * ls + m2];
+                    });
                 });
-            });
+            }
         });
     }
     float out[S::NLME];
@@ -302,7 +313,7 @@ __global__ __launch_bounds__(C) void k_r1_reverse(int r0, long long e0, const in
                                                   double* __restrict__ node_forces) {
     using S = Shape<LMAX, LMAXH>;
     constexpr int NY = S::NY, NH = S::NH;
-    __shared__ float part[Lanes<C>::NW][kForceChunk][3];
+    __shared__ float part[EdgeForceSink<C, kForceChunk>::ROWS][kForceChunk][3];
     EdgeForceSink<C, kForceChunk> sink{part};
     const int li = xcd_remap(blockIdx.x, gridDim.x);
     const int i = r0 + li;

@@ -95,7 +95,7 @@ __global__ __launch_bounds__(C) void k_r0_reverse(int r0, long long e0, const in
                                                   const float* __restrict__ Phi0_adj, double* __restrict__ node_forces) {
     using S = Shape<LMAX, 0>;
     constexpr int NY = S::NY, NF = (LMAX + 1) * C;
-    __shared__ float part[Lanes<C>::NW][kForceChunk][3];
+    __shared__ float part[EdgeForceSink<C, kForceChunk>::ROWS][kForceChunk][3];
     EdgeForceSink<C, kForceChunk> sink{part};
     const int li = xcd_remap(blockIdx.x, gridDim.x);
     const int i = r0 + li;
@@ -114,7 +114,7 @@ __global__ __launch_bounds__(C) void k_r0_reverse(int r0, long long e0, const in
             }
             const float x = rec[0];
             const int iv = __float_as_int(rec[1]);
-            const float xx = x * x, xxx = xx * x;
+            const float xx = x * x, xxx = xx * x, x2 = 2.0f * x, xx3 = 3.0f * xx;
             const float h0 = H0[neigh_types[e] * C + k];
             const float4* cf = R0c + static_cast<std::size_t>(iv) * NF + k;
             // per l: dR_l sum_m adj Y_lm (radial slope) and R_l sum_m adj dY_lm,
@@ -124,7 +124,7 @@ __global__ __launch_bounds__(C) void k_r0_reverse(int r0, long long e0, const in
                 constexpr int l = lc;
                 const float4 c4 = cf[l * C];
                 const float R = spline_value(c4, x, xx, xxx);
-                const float dR = spline_slope(c4, x, xx);
+                const float dR = spline_slope(c4, x2, xx3);
                 float sa = 0.0f, s0 = 0.0f, s1 = 0.0f, s2 = 0.0f;
                 static_for<0, 2 * l + 1>([&](auto mc) {
                     constexpr int lm = l * l + mc;
