@@ -22,6 +22,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <array>
 #include <cstdint>
 
 #include "device_common.hpp"
@@ -230,24 +231,78 @@ struct EdgeForceSink {
 constexpr int kForceChunk = 64;
 
 // ---------------------------------------------------------------------------
-// R1 forward: rows[i,(p,m1,m2),k] = sum_j R1_{p,k}(r) Y_{lm1} H1[j,lm2,k];
-// Phi1[i,lme,k] = sum CG rows (dense per-path coupling blocks), assigned.
-// Receiver i = r0 + li owns edges [first[i], first[i]+count[i]) (or
-// [first[i], first[i+1]) when count is null); Phi1 rows are indexed by li.
+// Row groups.  A coupling row (p, m1, m2) reads source component
+// lm2 = ls_p^2 + m2.  A group is a set of source components (bit mask); the
+// R1 kernels process the rows of one group, so a shape whose rows do not fit
+// the registers of one pass runs one pass per group.  Groups of one shape
+// are disjoint, so each source-adjoint component W[lm2] comes from exactly one
+// pass; Phi1 and the forces are sums over the passes.
 // ---------------------------------------------------------------------------
-template <int C, int LMAX, int LMAXH, class EDGES>
+template <int LMAX, int LMAXH, unsigned MASK>
+struct RowGroup {
+    using S = Shape<LMAX, LMAXH>;
+    static constexpr bool in(int p, int m2) {
+        return ((MASK >> (S::paths[p].ls * S::paths[p].ls + m2)) & 1u) != 0;
+    }
+    static constexpr int m2_count(int p) {
+        int n = 0;
+        for (int m2 = 0; m2 < 2 * S::paths[p].ls + 1; ++m2) n += in(p, m2) ? 1 : 0;
+        return n;
+    }
+    static constexpr int m2_rank(int p, int m2) {
+        int n = 0;
+        for (int q = 0; q < m2; ++q) n += in(p, q) ? 1 : 0;
+        return n;
+    }
+    static constexpr bool used(int p) { return m2_count(p) > 0; }
+    static constexpr std::array<int, S::P + 1> make_base() {
+        std::array<int, S::P + 1> b{};
+        for (int p = 0; p < S::P; ++p) b[p + 1] = b[p] + (2 * S::paths[p].le + 1) * m2_count(p);
+        return b;
+    }
+    static constexpr std::array<int, S::P + 1> base = make_base();
+    static constexpr int NR = base[S::P] > 0 ? base[S::P] : 1;
+    static constexpr int row(int p, int m1, int m2) { return base[p] + m1 * m2_count(p) + m2_rank(p, m2); }
+    static constexpr bool component(int lm2) { return ((MASK >> lm2) & 1u) != 0; }
+};
+
+// Row groups of a shape, as source-component masks: one pass for L_max 1
+// (88 rows at l_max 3); for L_max 2 (243 rows) the 0e+1o components (88
+// rows), then 2e components m2 0-2 (93 rows) and 3-4 (62 rows).
+template <int LMAX, int LMAXH>
+struct SourceGroups;
+template <int LMAX>
+struct SourceGroups<LMAX, 1> {
+    static constexpr std::array<unsigned, 1> masks{0xfu};
+};
+template <int LMAX>
+struct SourceGroups<LMAX, 2> {
+    static constexpr std::array<unsigned, 3> masks{0x00fu, 0x070u, 0x180u};
+};
+
+// ---------------------------------------------------------------------------
+// R1 forward: rows[i,(p,m1,m2),k] = sum_j R1_{p,k}(r) Y_{lm1} H1[j,lm2,k];
+// Phi1[i,lme,k] = sum CG rows (dense per-path coupling blocks).  Each output
+// lme comes from one path (lme = lme_base[lo] + mo*num_e[lo] + e_p), so it is
+// written once per pass: assigned (zero for paths outside the group) or,
+// with ACCUMULATE, added.  Receiver i = r0 + li owns edges [first[i],
+// first[i]+count[i]) (or [first[i], first[i+1]) when count is null); Phi1
+// rows are indexed by li.
+// ---------------------------------------------------------------------------
+template <int C, int LMAX, int LMAXH, unsigned MASK, bool ACCUMULATE, class EDGES>
 __global__ __launch_bounds__(C) void k_r1_forward(int r0, const int* __restrict__ first,
                                                   const int* __restrict__ count, const int* __restrict__ neigh,
                                                   EDGES edges, const float* __restrict__ H1,
                                                   const float* __restrict__ cg, float* __restrict__ Phi1) {
     using S = Shape<LMAX, LMAXH>;
+    using RG = RowGroup<LMAX, LMAXH, MASK>;
     constexpr int NH = S::NH;
     const int li = xcd_remap(blockIdx.x, gridDim.x);
     const int i = r0 + li;
     const int k = threadIdx.x;
-    float rows[S::NROWS];
+    float rows[RG::NR];
 #pragma unroll
-    for (int r = 0; r < S::NROWS; ++r) rows[r] = 0.0f;
+    for (int r = 0; r < RG::NR; ++r) rows[r] = 0.0f;
     const int ea = first[i], eb = count ? ea + count[i] : first[i + 1];
     for (int e = ea; e < eb; ++e) {
         typename EDGES::Point pt;
@@ -255,88 +310,111 @@ __global__ __launch_bounds__(C) void k_r1_forward(int r0, const int* __restrict_
         const float* hj = H1 + static_cast<std::size_t>(neigh[e]) * NH * C + k;
         float h[NH];
 #pragma unroll
-        for (int q = 0; q < NH; ++q) h[q] = hj[q * C];
+        for (int q = 0; q < NH; ++q) h[q] = RG::component(q) ? hj[q * C] : 0.0f;
         static_for<0, S::P>([&](auto pc) {
             constexpr int p = pc;
-            constexpr int le = S::paths[p].le, ls = S::paths[p].ls, rb = S::row_base[p];
-            const float rad = edges.value(pt, p * C + k);
-            if constexpr (ls == 0) {
-                // one source component: scale R by it once
-                const float rh = rad * h[0];
-                static_for<0, 2 * le + 1>([&](auto m1c) { rows[rb + m1c] += rh * edges.Y(pt, le * le + m1c); });
-            } else {
-                static_for<0, 2 * le + 1>([&](auto m1c) {
-                    constexpr int m1 = m1c;
-                    const float ry = rad * edges.Y(pt, le * le + m1);
-                    static_for<0, 2 * ls + 1>([&](auto m2c) {
-                        constexpr int m2 = m2c;
-                        rows[rb + m1 * (2 * ls + 1) + m2] += ry * h[ls * ls + m2];
+            if constexpr (RG::used(p)) {
+                constexpr int le = S::paths[p].le, ls = S::paths[p].ls;
+                const float rad = edges.value(pt, p * C + k);
+                if constexpr (ls == 0) {
+                    // one source component: scale R by it once
+                    const float rh = rad * h[0];
+                    static_for<0, 2 * le + 1>([&](auto m1c) {
+                        constexpr int m1 = m1c;
+                        constexpr int r = RG::row(p, m1, 0);
+                        rows[r] += rh * edges.Y(pt, le * le + m1);
                     });
-                });
+                } else {
+                    static_for<0, 2 * le + 1>([&](auto m1c) {
+                        constexpr int m1 = m1c;
+                        const float ry = rad * edges.Y(pt, le * le + m1);
+                        static_for<0, 2 * ls + 1>([&](auto m2c) {
+                            constexpr int m2 = m2c;
+                            if constexpr (RG::in(p, m2)) {
+                                constexpr int r = RG::row(p, m1, m2);
+                                rows[r] += ry * h[ls * ls + m2];
+                            }
+                        });
+                    });
+                }
             }
         });
     }
-    float out[S::NLME];
-#pragma unroll
-    for (int q = 0; q < S::NLME; ++q) out[q] = 0.0f;
+    float* out = Phi1 + static_cast<std::size_t>(li) * S::NLME * C + k;
     static_for<0, S::P>([&](auto pc) {
         constexpr int p = pc;
-        constexpr int le = S::paths[p].le, ls = S::paths[p].ls, lo = S::paths[p].lo;
-        constexpr int rb = S::row_base[p], co = S::cg_offset[p];
-        static_for<0, (2 * le + 1) * (2 * ls + 1)>([&](auto rc) {
-            constexpr int r = rc;
-            static_for<0, 2 * lo + 1>([&](auto mc) {
-                constexpr int mo = mc;
-                constexpr int q = S::lme(p, mo);
-                out[q] += cg[co + r * (2 * lo + 1) + mo] * rows[rb + r];
-            });
+        constexpr int le = S::paths[p].le, ls = S::paths[p].ls, lo = S::paths[p].lo, co = S::cg_offset[p];
+        static_for<0, 2 * lo + 1>([&](auto mc) {
+            constexpr int mo = mc;
+            constexpr int q = S::lme(p, mo);
+            if constexpr (RG::used(p)) {
+                float o = 0.0f;
+                static_for<0, 2 * le + 1>([&](auto m1c) {
+                    constexpr int m1 = m1c;
+                    static_for<0, 2 * ls + 1>([&](auto m2c) {
+                        constexpr int m2 = m2c;
+                        if constexpr (RG::in(p, m2)) {
+                            constexpr int r = RG::row(p, m1, m2);
+                            o += cg[co + (m1 * (2 * ls + 1) + m2) * (2 * lo + 1) + mo] * rows[r];
+                        }
+                    });
+                });
+                out[q * C] = ACCUMULATE ? out[q * C] + o : o;
+            } else if constexpr (!ACCUMULATE) {
+                out[q * C] = 0.0f;
+            }
         });
     });
-#pragma unroll
-    for (int q = 0; q < S::NLME; ++q) Phi1[(static_cast<std::size_t>(li) * S::NLME + q) * C + k] = out[q];
 }
 
 // ---------------------------------------------------------------------------
-// Fused R1 reverse, receiver-owned: per edge the directed force
+// Fused R1 reverse, receiver-owned, over the rows of one group: per edge the
+// directed force
 //   f_e = -sum_k sum_rows G[row] H1[j,lm2] (u dR Y_lm1 + R dY_lm1)
-// and the per-edge source-adjoint contribution
+// and the per-edge source-adjoint components in the group
 //   W_e[lm2,k] = sum_{p,m1} R Y_lm1 G[row]   (zero for inactive edges)
 // that k_source_gather sums over each source's edges.  G = CG^T dPhi1[li].
 // W and node_forces are indexed by e - e0; forces are assigned (-f) or, with
-// ACCUMULATE, subtracted from what the buffer holds.
+// FORCE_ACCUMULATE, subtracted from what the buffer holds.
 // ---------------------------------------------------------------------------
-template <int C, int LMAX, int LMAXH, bool ACCUMULATE, class EDGES>
+template <int C, int LMAX, int LMAXH, unsigned MASK, bool FORCE_ACCUMULATE, class EDGES>
 __global__ __launch_bounds__(C) void k_r1_reverse(int r0, long long e0, const int* __restrict__ offsets,
                                                   const int* __restrict__ neigh, EDGES edges,
                                                   const float* __restrict__ H1, const float* __restrict__ cg,
                                                   const float* __restrict__ dPhi1, float* __restrict__ Wsrc,
                                                   double* __restrict__ node_forces) {
     using S = Shape<LMAX, LMAXH>;
+    using RG = RowGroup<LMAX, LMAXH, MASK>;
     constexpr int NY = S::NY, NH = S::NH;
     __shared__ float part[EdgeForceSink<C, kForceChunk>::ROWS][kForceChunk][3];
     EdgeForceSink<C, kForceChunk> sink{part};
     const int li = xcd_remap(blockIdx.x, gridDim.x);
     const int i = r0 + li;
     const int k = threadIdx.x;
-    float G[S::NROWS];
-    {
-        float d[S::NLME];
+    float G[RG::NR];
 #pragma unroll
-        for (int q = 0; q < S::NLME; ++q) d[q] = dPhi1[(static_cast<std::size_t>(li) * S::NLME + q) * C + k];
+    for (int r = 0; r < RG::NR; ++r) G[r] = 0.0f;
+    {
+        const float* d = dPhi1 + static_cast<std::size_t>(li) * S::NLME * C + k;
         static_for<0, S::P>([&](auto pc) {
             constexpr int p = pc;
-            constexpr int le = S::paths[p].le, ls = S::paths[p].ls, lo = S::paths[p].lo;
-            constexpr int rb = S::row_base[p], co = S::cg_offset[p];
-            static_for<0, (2 * le + 1) * (2 * ls + 1)>([&](auto rc) {
-                constexpr int r = rc;
-                float g = 0.0f;
+            if constexpr (RG::used(p)) {
+                constexpr int le = S::paths[p].le, ls = S::paths[p].ls, lo = S::paths[p].lo, co = S::cg_offset[p];
                 static_for<0, 2 * lo + 1>([&](auto mc) {
                     constexpr int mo = mc;
-                    constexpr int q = S::lme(p, mo);
-                    g += cg[co + r * (2 * lo + 1) + mo] * d[q];
+                    const float dq = d[S::lme(p, mo) * C];
+                    static_for<0, 2 * le + 1>([&](auto m1c) {
+                        constexpr int m1 = m1c;
+                        static_for<0, 2 * ls + 1>([&](auto m2c) {
+                            constexpr int m2 = m2c;
+                            if constexpr (RG::in(p, m2)) {
+                                constexpr int r = RG::row(p, m1, m2);
+                                G[r] += cg[co + (m1 * (2 * ls + 1) + m2) * (2 * lo + 1) + mo] * dq;
+                            }
+                        });
+                    });
                 });
-                G[rb + r] = g;
-            });
+            }
         });
     }
     const int ea = offsets[i], eb = offsets[i + 1];
@@ -348,7 +426,8 @@ __global__ __launch_bounds__(C) void k_r1_reverse(int r0, long long e0, const in
             if (!edges.open(e, i, pt)) {
                 // inactive edges contribute zero to their source's adjoint
 #pragma unroll
-                for (int q = 0; q < NH; ++q) __builtin_nontemporal_store(0.0f, wdst + q * C);
+                for (int q = 0; q < NH; ++q)
+                    if (RG::component(q)) __builtin_nontemporal_store(0.0f, wdst + q * C);
                 sink.zero(e - c0);
                 continue;
             }
@@ -356,7 +435,7 @@ __global__ __launch_bounds__(C) void k_r1_reverse(int r0, long long e0, const in
             float h[NH], W[NH];
 #pragma unroll
             for (int q = 0; q < NH; ++q) {
-                h[q] = hj[q * C];
+                h[q] = RG::component(q) ? hj[q * C] : 0.0f;
                 W[q] = 0.0f;
             }
             // Per path p, with T[m2] = sum_m1 Y_m1 G[p,m1,m2] and
@@ -368,30 +447,37 @@ __global__ __launch_bounds__(C) void k_r1_reverse(int r0, long long e0, const in
             for (int v = 0; v < NY; ++v) SB[v] = 0.0f;
             static_for<0, S::P>([&](auto pc) {
                 constexpr int p = pc;
-                constexpr int le = S::paths[p].le, ls = S::paths[p].ls, rb = S::row_base[p];
-                float R, dR;
-                edges.value_slope(pt, p * C + k, R, dR);
-                float T[2 * ls + 1];
-                static_for<0, 2 * ls + 1>([&](auto m2c) { T[m2c] = 0.0f; });
-                static_for<0, 2 * le + 1>([&](auto m1c) {
-                    constexpr int m1 = m1c;
-                    const float y = edges.Y(pt, le * le + m1);
-                    float sr = 0.0f;
+                if constexpr (RG::used(p)) {
+                    constexpr int le = S::paths[p].le, ls = S::paths[p].ls;
+                    float R, dR;
+                    edges.value_slope(pt, p * C + k, R, dR);
+                    float T[2 * ls + 1];
+                    static_for<0, 2 * ls + 1>([&](auto m2c) { T[m2c] = 0.0f; });
+                    static_for<0, 2 * le + 1>([&](auto m1c) {
+                        constexpr int m1 = m1c;
+                        const float y = edges.Y(pt, le * le + m1);
+                        float sr = 0.0f;
+                        static_for<0, 2 * ls + 1>([&](auto m2c) {
+                            constexpr int m2 = m2c;
+                            if constexpr (RG::in(p, m2)) {
+                                constexpr int r = RG::row(p, m1, m2);
+                                const float g = G[r];
+                                T[m2] += y * g;
+                                sr += g * h[ls * ls + m2];
+                            }
+                        });
+                        SB[le * le + m1] += R * sr;
+                    });
+                    float hT = 0.0f;
                     static_for<0, 2 * ls + 1>([&](auto m2c) {
                         constexpr int m2 = m2c;
-                        const float g = G[rb + m1 * (2 * ls + 1) + m2];
-                        T[m2] += y * g;
-                        sr += g * h[ls * ls + m2];
+                        if constexpr (RG::in(p, m2)) {
+                            W[ls * ls + m2] += R * T[m2];
+                            hT += h[ls * ls + m2] * T[m2];
+                        }
                     });
-                    SB[le * le + m1] += R * sr;
-                });
-                float hT = 0.0f;
-                static_for<0, 2 * ls + 1>([&](auto m2c) {
-                    constexpr int m2 = m2c;
-                    W[ls * ls + m2] += R * T[m2];
-                    hT += h[ls * ls + m2] * T[m2];
-                });
-                A += dR * hT;
+                    A += dR * hT;
+                }
             });
             float b0 = 0.0f, b1 = 0.0f, b2 = 0.0f;
 #pragma unroll
@@ -403,10 +489,11 @@ __global__ __launch_bounds__(C) void k_r1_reverse(int r0, long long e0, const in
             // W is streamed (read once, by the source gather): keep it out of
             // the cache lines that H1 and the spline table reuse
 #pragma unroll
-            for (int q = 0; q < NH; ++q) __builtin_nontemporal_store(W[q], wdst + q * C);
+            for (int q = 0; q < NH; ++q)
+                if (RG::component(q)) __builtin_nontemporal_store(W[q], wdst + q * C);
             sink.put(e - c0, edges.u(pt, 0) * A + b0, edges.u(pt, 1) * A + b1, edges.u(pt, 2) * A + b2);
         }
-        sink.template flush<ACCUMULATE>(static_cast<long long>(c0) - e0, c1 - c0, node_forces);
+        sink.template flush<FORCE_ACCUMULATE>(static_cast<long long>(c0) - e0, c1 - c0, node_forces);
     }
 }
 

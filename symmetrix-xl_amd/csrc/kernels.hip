@@ -841,6 +841,8 @@ struct KernelSetImpl final : KernelSet {
     using S = Shape<LMAX, LMAXH>;
     static constexpr bool kM0Unrolled = !std::is_same_v<M0TAB, void>;
     using Records = RecordEdges<S::NY, S::REC>;
+    using Groups = SourceGroups<LMAX, LMAXH>;
+    static constexpr int kGroups = static_cast<int>(Groups::masks.size());
     int record_floats() const override { return S::REC; }
     static Records records(const DeviceModel& m, const TileView& t, const Workspace& w) {
         return Records{w.erec, t.e0, m.R1c, S::P * C};
@@ -887,9 +889,12 @@ struct KernelSetImpl final : KernelSet {
         if (t.nr == 0) return;
         {
             TimerScope ts(tm, "r1_forward", s);
-            k_r1_forward<C, LMAX, LMAXH, Records><<<t.nr, C, 0, s>>>(t.r0, g.offsets, nullptr, g.neigh,
-                                                                    records(m, t, w), w.H1, m.cg, w.Phi1);
-            SMX_LAUNCH_CHECK("r1_forward");
+            static_for<0, kGroups>([&](auto gc) {
+                constexpr int gi = gc;
+                k_r1_forward<C, LMAX, LMAXH, Groups::masks[gi], (gi > 0), Records><<<t.nr, C, 0, s>>>(
+                    t.r0, g.offsets, nullptr, g.neigh, records(m, t, w), w.H1, m.cg, w.Phi1);
+                SMX_LAUNCH_CHECK("r1_forward");
+            });
         }
         {
             TimerScope ts(tm, "a1_linear", s);
@@ -911,9 +916,12 @@ struct KernelSetImpl final : KernelSet {
         }
         {
             TimerScope ts(tm, "r1_reverse", s);
-            k_r1_reverse<C, LMAX, LMAXH, false, Records><<<t.nr, C, 0, s>>>(
-                t.r0, t.e0, g.offsets, g.neigh, records(m, t, w), w.H1, m.cg, w.dPhi1, w.Wsrc, w.node_forces);
-            SMX_LAUNCH_CHECK("r1_reverse");
+            static_for<0, kGroups>([&](auto gc) {
+                constexpr int gi = gc;
+                k_r1_reverse<C, LMAX, LMAXH, Groups::masks[gi], (gi > 0), Records><<<t.nr, C, 0, s>>>(
+                    t.r0, t.e0, g.offsets, g.neigh, records(m, t, w), w.H1, m.cg, w.dPhi1, w.Wsrc, w.node_forces);
+                SMX_LAUNCH_CHECK("r1_reverse");
+            });
         }
     }
 
@@ -1021,6 +1029,9 @@ std::unique_ptr<KernelSet> make_kernel_set(int C, int l_max, int L_max, const st
                                            const std::vector<std::int32_t>& m0_offsets,
                                            const std::vector<std::int32_t>& m1_terms) {
     const int corr = std::max(max_degree(m0_terms), max_degree(m1_terms));
+    if (C == 256 && l_max == 3 && L_max == 2)
+        return corr == 3 ? pick_polynomials<256, 3, 2, 3>(m0_terms, m0_offsets, m1_terms)
+                         : std::make_unique<KernelSetImpl<256, 3, 2, void, void>>();
     if (C == 32 && l_max == 2 && L_max == 1)
         return corr == 2 ? pick_polynomials<32, 2, 1, 2>(m0_terms, m0_offsets, m1_terms)
                          : std::make_unique<KernelSetImpl<32, 2, 1, void, void>>();
@@ -1037,6 +1048,10 @@ bool kernel_paths(int l_max, int L_max, std::vector<int>& le, std::vector<int>& 
     }
     if (l_max == 3 && L_max == 1) {
         paths_of<3, 1>(le, ls, lo);
+        return true;
+    }
+    if (l_max == 3 && L_max == 2) {
+        paths_of<3, 2>(le, ls, lo);
         return true;
     }
     return false;

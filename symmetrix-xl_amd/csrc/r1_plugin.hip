@@ -119,7 +119,9 @@ int32_t forward_launch(const SymmetrixJitHipR1ForwardArgsV1* a, void* stream, in
     const auto edges = plugin_edges<S::NY>(*st, a->radial, a->radius, a->harmonics_values, nullptr, nullptr, false,
                                            a->node_types, a->neigh_types, a->type_to_active, a->active_type_count,
                                            a->cutoff);
-    k_r1_forward<C, LMAX, LMAXH, PluginEdges<S::NY>><<<static_cast<unsigned>(a->num_nodes), C, 0,
+    static_assert(SourceGroups<LMAX, LMAXH>::masks.size() == 1, "the plugin runs single-pass shapes");
+    constexpr unsigned kAll = SourceGroups<LMAX, LMAXH>::masks[0];
+    k_r1_forward<C, LMAX, LMAXH, kAll, false, PluginEdges<S::NY>><<<static_cast<unsigned>(a->num_nodes), C, 0,
                                                       static_cast<hipStream_t>(stream)>>>(
         0, a->first_neigh, a->num_neigh, a->neigh_indices, edges, static_cast<const float*>(a->neighbor_features),
         st->cg, static_cast<float*>(a->output));
@@ -161,7 +163,8 @@ int32_t reverse_launch(const SymmetrixJitHipR1SourceArgsV1* s, const SymmetrixJi
     const auto edges = plugin_edges<S::NY>(*st, e->radial, e->radius, e->harmonics_values, e->harmonics_gradients,
                                            e->xyz, unit, e->node_types, e->neigh_types, e->type_to_active,
                                            e->active_type_count, e->cutoff);
-    k_r1_reverse<C, LMAX, LMAXH, true, PluginEdges<S::NY>><<<static_cast<unsigned>(N), C, 0, hs>>>(
+    constexpr unsigned kAll = SourceGroups<LMAX, LMAXH>::masks[0];
+    k_r1_reverse<C, LMAX, LMAXH, kAll, true, PluginEdges<S::NY>><<<static_cast<unsigned>(N), C, 0, hs>>>(
         0, 0, offsets, e->neigh_indices, edges, static_cast<const float*>(e->neighbor_features), st->cg,
         static_cast<const float*>(e->output_adjoint), W, e->directed_forces);
     k_source_gather<C, S::NH, true><<<static_cast<unsigned>(N), C, 0, hs>>>(s->source_offsets, s->source_edges, W,

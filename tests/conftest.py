@@ -33,3 +33,9 @@ def tiny_model_path():
 def medium_model_path():
     from symmetrix import random_model
     return random_model.cached_model("medium", directory=MODEL_DIR)
+
+
+@pytest.fixture(scope="session")
+def wide_model_path():
+    from symmetrix import random_model
+    return random_model.cached_model("wide", directory=MODEL_DIR)

@@ -139,6 +139,22 @@ def test_energy_forces_stress_irregular(medium_model_path):
     _assert_efs(ref, e, f, st, len(e))
 
 
+def test_energy_forces_stress_wide(wide_model_path):
+    """BASELINE configs[4] shape: 256 channels, 0e+1o+2e hidden (L_max 2, 243
+    coupling rows run as three source-component passes), l_max 3,
+    correlation 3, r_cut 5 A, on a rigid-water box (1,000 molecules, 3,000
+    atoms; the config's 30,000-atom box has the same per-atom work)."""
+    from symmetrix import systems
+    s = systems.water_box(1000, seed=0)
+    om, ref, ev, g, e, f, st = _evaluate_both(wide_model_path, s)
+    assert "polynomials=unrolled" in ev.execution_plan
+    for name in ("Phi1", "A1", "dPhi1", "H1_adj"):
+        err = _stage_err(ev._stage(name).astype(np.float64), om.stage(name))
+        print(name, "relative max err %.3e" % err)
+        assert err < 1e-4, name
+    _assert_efs(ref, e, f, st, len(e))
+
+
 def test_repeat_calls_bitwise_deterministic(tiny_model_path):
     from symmetrix.mace_kokkos import MACEKokkosFloat
     s = _system("tiny")
