@@ -47,25 +47,112 @@ struct Lanes {
 };
 
 // ---------------------------------------------------------------------------
+// Receiver records staged through LDS.  A receiver's edge records are
+// contiguous; they are copied in chunks of kRecordChunk edges with coalesced
+// float4 loads into one of two LDS buffers, the next chunk's loads in flight
+// while the current chunk is processed, so the wave-uniform record fields
+// come from LDS (broadcast reads) rather than from scalar loads that miss.
+//   for (c = 0; c < chunks(); ++c) { const float* r = begin(c); ... end(c); }
+// begin/end synchronise the workgroup; every thread must run the loop.
+// ---------------------------------------------------------------------------
+constexpr int kRecordChunk = 16;
+
+// native 4-float vector: copies are plain vector loads and stores (float4,
+// a struct, copies through memcpy and keeps the staging array in scratch)
+typedef float stage4 __attribute__((ext_vector_type(4)));
+
+constexpr int stage_per(int C, int REC) { return (kRecordChunk * (REC / 4) + C - 1) / C; }
+
+template <int C, int REC>
+struct RecordStage {
+    static constexpr int R4 = REC / 4;               // float4 per record
+    static constexpr int SLOTS = kRecordChunk * R4;  // float4 per buffer
+    static constexpr int PER = (SLOTS + C - 1) / C;  // float4 per thread
+};
+
+// Loads of chunk c into held (unconditional: past the chunk they repeat its
+// last float4, so there is no branch and they stay in flight while the
+// current chunk runs).
+template <int C, int REC>
+__device__ __forceinline__ void stage_fetch(stage4 (&held)[stage_per(C, REC)], const stage4* __restrict__ src,
+                                            int c, int edges) {
+    using RS = RecordStage<C, REC>;
+    const int limit = min(kRecordChunk, edges - c * kRecordChunk) * RS::R4;
+#pragma unroll
+    for (int p = 0; p < RS::PER; ++p) {
+        const int idx = min(static_cast<int>(threadIdx.x) + p * C, limit - 1);
+        held[p] = src[static_cast<std::size_t>(c) * RS::SLOTS + idx];
+    }
+}
+
+template <int C, int REC>
+__device__ __forceinline__ void stage_commit(const stage4 (&held)[stage_per(C, REC)], stage4* buf, int c,
+                                             int edges) {
+    using RS = RecordStage<C, REC>;
+    const int limit = min(kRecordChunk, edges - c * kRecordChunk) * RS::R4;
+#pragma unroll
+    for (int p = 0; p < RS::PER; ++p) {
+        const int idx = static_cast<int>(threadIdx.x) + p * C;
+        if (idx < limit) buf[(c & 1) * RS::SLOTS + idx] = held[p];
+    }
+}
+
+// Runs body(chunk_records, first_edge_offset, count) over the chunks of
+// `edges` records at src (records contiguous), staged through two LDS
+// buffers of SLOTS float4 each at buf.
+template <int C, int REC, class BODY>
+__device__ __forceinline__ void staged_records(stage4* buf, const stage4* __restrict__ src, int edges, BODY&& body) {
+    using RS = RecordStage<C, REC>;
+    const int chunks = (edges + kRecordChunk - 1) / kRecordChunk;
+    stage4 held[RS::PER];
+    if (chunks > 0) {
+        stage_fetch<C, REC>(held, src, 0, edges);
+        stage_commit<C, REC>(held, buf, 0, edges);
+    }
+    __syncthreads();
+    for (int c = 0; c < chunks; ++c) {
+        if (c + 1 < chunks) stage_fetch<C, REC>(held, src, c + 1, edges);
+        body(reinterpret_cast<const float*>(buf + (c & 1) * RS::SLOTS), c * kRecordChunk,
+             min(kRecordChunk, edges - c * kRecordChunk));
+        if (c + 1 < chunks) stage_commit<C, REC>(held, buf, c + 1, edges);
+        __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Edge-input policies
 // ---------------------------------------------------------------------------
 // Packed record [x, interval, active, 0, Y[NY], dY/dX[NY], dY/dY[NY],
 // dY/dZ[NY], u[3], pad] per edge (tile-local index e - e0) and the Hermite
-// table [interval][function] as float4 (c0..c3).
-template <int NY, int REC>
+// table [interval][function] as float4 (c0..c3).  With STAGED a receiver's
+// records are staged through LDS in chunks (staged_records; the fields then
+// sit in VGPRs), else the wave reads them with scalar loads (SGPRs).
+template <int C, int NY, int REC, bool STAGED>
 struct RecordEdges {
     const float* __restrict__ erec;
     long long e0;
     const float4* __restrict__ coef;
     int functions;
 
+    static constexpr int kStageSlots = STAGED ? RecordStage<C, REC>::SLOTS : 1;
     struct Point {
         const float* rec;
         const float4* cf;
         float x, xx, xxx, x2, xx3;
     };
-    __device__ __forceinline__ bool open(int e, int /*receiver*/, Point& p) const {
-        p.rec = erec + static_cast<std::size_t>(e - e0) * REC;
+    // body(first edge, count, staged records of the chunk) over [ea, eb)
+    template <class BODY>
+    __device__ __forceinline__ void chunks(int ea, int eb, stage4* lds, BODY&& body) const {
+        if constexpr (STAGED) {
+            const stage4* src = reinterpret_cast<const stage4*>(erec) + static_cast<std::size_t>(ea - e0) * (REC / 4);
+            staged_records<C, REC>(lds, src, eb - ea, [&](const float* chunk, int first, int n)
+                                                          __attribute__((always_inline)) { body(ea + first, n, chunk); });
+        } else {
+            for (int c0 = ea; c0 < eb; c0 += kRecordChunk) body(c0, min(kRecordChunk, eb - c0), nullptr);
+        }
+    }
+    __device__ __forceinline__ bool open_at(int e, int /*receiver*/, const float* chunk, int j, Point& p) const {
+        p.rec = STAGED ? chunk + j * REC : erec + static_cast<std::size_t>(e - e0) * REC;
         if (!edge_active(p.rec)) return false;
         p.x = p.rec[0];
         p.xx = p.x * p.x;
@@ -112,11 +199,19 @@ struct PluginEdges {
     double x0, h, cutoff;
     int intervals, functions, active_types, fp64_point;
 
+    static constexpr int kStageSlots = 1;
     struct Point {
         int e;
         const float* c0;  // coefficient c0 of function 0 of this edge's interval
         float x, xx, xxx, x2, xx3;
     };
+    template <class BODY>
+    __device__ __forceinline__ void chunks(int ea, int eb, stage4*, BODY&& body) const {
+        for (int c0 = ea; c0 < eb; c0 += kRecordChunk) body(c0, min(kRecordChunk, eb - c0), nullptr);
+    }
+    __device__ __forceinline__ bool open_at(int e, int receiver, const float*, int, Point& p) const {
+        return open(e, receiver, p);
+    }
     __device__ __forceinline__ bool open(int e, int receiver, Point& p) const {
         const double r = radius[e];
         if (!(r < cutoff)) return false;
@@ -228,8 +323,6 @@ struct EdgeForceSink {
     }
 };
 
-constexpr int kForceChunk = 64;
-
 // ---------------------------------------------------------------------------
 // Row groups.  A coupling row (p, m1, m2) reads source component
 // lm2 = ls_p^2 + m2.  A group is a set of source components (bit mask); the
@@ -304,9 +397,12 @@ __global__ __launch_bounds__(C) void k_r1_forward(int r0, const int* __restrict_
 #pragma unroll
     for (int r = 0; r < RG::NR; ++r) rows[r] = 0.0f;
     const int ea = first[i], eb = count ? ea + count[i] : first[i + 1];
-    for (int e = ea; e < eb; ++e) {
+    __shared__ stage4 stage_buf[2 * EDGES::kStageSlots];
+    edges.chunks(ea, eb, stage_buf, [&](int e_first, int n, const float* chunk) __attribute__((always_inline)) {
+    for (int j = 0; j < n; ++j) {
+        const int e = e_first + j;
         typename EDGES::Point pt;
-        if (!edges.open(e, i, pt)) continue;
+        if (!edges.open_at(e, i, chunk, j, pt)) continue;
         const float* hj = H1 + static_cast<std::size_t>(neigh[e]) * NH * C + k;
         float h[NH];
 #pragma unroll
@@ -340,6 +436,7 @@ __global__ __launch_bounds__(C) void k_r1_forward(int r0, const int* __restrict_
             }
         });
     }
+    });
     float* out = Phi1 + static_cast<std::size_t>(li) * S::NLME * C + k;
     static_for<0, S::P>([&](auto pc) {
         constexpr int p = pc;
@@ -386,8 +483,9 @@ __global__ __launch_bounds__(C) void k_r1_reverse(int r0, long long e0, const in
     using S = Shape<LMAX, LMAXH>;
     using RG = RowGroup<LMAX, LMAXH, MASK>;
     constexpr int NY = S::NY, NH = S::NH;
-    __shared__ float part[EdgeForceSink<C, kForceChunk>::ROWS][kForceChunk][3];
-    EdgeForceSink<C, kForceChunk> sink{part};
+    __shared__ float part[EdgeForceSink<C, kRecordChunk>::ROWS][kRecordChunk][3];
+    EdgeForceSink<C, kRecordChunk> sink{part};
+    __shared__ stage4 stage_buf[2 * EDGES::kStageSlots];
     const int li = xcd_remap(blockIdx.x, gridDim.x);
     const int i = r0 + li;
     const int k = threadIdx.x;
@@ -418,17 +516,17 @@ __global__ __launch_bounds__(C) void k_r1_reverse(int r0, long long e0, const in
         });
     }
     const int ea = offsets[i], eb = offsets[i + 1];
-    for (int c0 = ea; c0 < eb; c0 += kForceChunk) {
-        const int c1 = min(c0 + kForceChunk, eb);
-        for (int e = c0; e < c1; ++e) {
+    edges.chunks(ea, eb, stage_buf, [&](int c0, int n, const float* chunk) __attribute__((always_inline)) {
+        for (int j = 0; j < n; ++j) {
+            const int e = c0 + j;
             float* wdst = Wsrc + static_cast<std::size_t>(e - e0) * NH * C + k;
             typename EDGES::Point pt;
-            if (!edges.open(e, i, pt)) {
+            if (!edges.open_at(e, i, chunk, j, pt)) {
                 // inactive edges contribute zero to their source's adjoint
 #pragma unroll
                 for (int q = 0; q < NH; ++q)
                     if (RG::component(q)) __builtin_nontemporal_store(0.0f, wdst + q * C);
-                sink.zero(e - c0);
+                sink.zero(j);
                 continue;
             }
             const float* hj = H1 + static_cast<std::size_t>(neigh[e]) * NH * C + k;
@@ -491,10 +589,10 @@ __global__ __launch_bounds__(C) void k_r1_reverse(int r0, long long e0, const in
 #pragma unroll
             for (int q = 0; q < NH; ++q)
                 if (RG::component(q)) __builtin_nontemporal_store(W[q], wdst + q * C);
-            sink.put(e - c0, edges.u(pt, 0) * A + b0, edges.u(pt, 1) * A + b1, edges.u(pt, 2) * A + b2);
+            sink.put(j, edges.u(pt, 0) * A + b0, edges.u(pt, 1) * A + b1, edges.u(pt, 2) * A + b2);
         }
-        sink.template flush<FORCE_ACCUMULATE>(static_cast<long long>(c0) - e0, c1 - c0, node_forces);
-    }
+        sink.template flush<FORCE_ACCUMULATE>(static_cast<long long>(c0) - e0, n, node_forces);
+    });
 }
 
 // ---------------------------------------------------------------------------

@@ -66,23 +66,29 @@ __global__ __launch_bounds__(C) void k_r0_forward(int r0, long long e0, const in
 #pragma unroll
     for (int v = 0; v < NY; ++v) acc[v] = 0.0f;
     const int ea = offsets[i], eb = offsets[i + 1];
-    for (int e = ea; e < eb; ++e) {
-        const float* rec = erec + static_cast<std::size_t>(e - e0) * S::REC;
-        if (!edge_active(rec)) continue;
-        const float x = rec[0];
-        const int iv = __float_as_int(rec[1]);
-        const float xx = x * x, xxx = xx * x;
-        const float h0 = H0[neigh_types[e] * C + k];
-        const float4* cf = R0c + static_cast<std::size_t>(iv) * NF + k;
-        static_for<0, LMAX + 1>([&](auto lc) {
-            constexpr int l = lc;
-            const float rh = spline_value(cf[l * C], x, xx, xxx) * h0;
-            static_for<0, 2 * l + 1>([&](auto mc) {
-                constexpr int lm = l * l + mc;
-                acc[lm] += rh * rec[S::REC_Y + lm];
+    __shared__ stage4 stage_buf[2 * RecordStage<C, S::REC>::SLOTS];
+    const stage4* src = reinterpret_cast<const stage4*>(erec) + static_cast<std::size_t>(ea - e0) * (S::REC / 4);
+    staged_records<C, S::REC>(stage_buf, src, eb - ea, [&](const float* chunk, int first, int n)
+                                                           __attribute__((always_inline)) {
+        for (int j = 0; j < n; ++j) {
+            const float* rec = chunk + j * S::REC;
+            if (!edge_active(rec)) continue;
+            const int e = ea + first + j;
+            const float x = rec[0];
+            const int iv = __float_as_int(rec[1]);
+            const float xx = x * x, xxx = xx * x;
+            const float h0 = H0[neigh_types[e] * C + k];
+            const float4* cf = R0c + static_cast<std::size_t>(iv) * NF + k;
+            static_for<0, LMAX + 1>([&](auto lc) {
+                constexpr int l = lc;
+                const float rh = spline_value(cf[l * C], x, xx, xxx) * h0;
+                static_for<0, 2 * l + 1>([&](auto mc) {
+                    constexpr int lm = l * l + mc;
+                    acc[lm] += rh * rec[S::REC_Y + lm];
+                });
             });
-        });
-    }
+        }
+    });
 #pragma unroll
     for (int v = 0; v < NY; ++v) Phi0[(static_cast<std::size_t>(li) * NY + v) * C + k] = acc[v];
 }
@@ -95,8 +101,9 @@ __global__ __launch_bounds__(C) void k_r0_reverse(int r0, long long e0, const in
                                                   const float* __restrict__ Phi0_adj, double* __restrict__ node_forces) {
     using S = Shape<LMAX, 0>;
     constexpr int NY = S::NY, NF = (LMAX + 1) * C;
-    __shared__ float part[EdgeForceSink<C, kForceChunk>::ROWS][kForceChunk][3];
-    EdgeForceSink<C, kForceChunk> sink{part};
+    __shared__ float part[EdgeForceSink<C, kRecordChunk>::ROWS][kRecordChunk][3];
+    EdgeForceSink<C, kRecordChunk> sink{part};
+    __shared__ stage4 stage_buf[2 * RecordStage<C, S::REC>::SLOTS];
     const int li = xcd_remap(blockIdx.x, gridDim.x);
     const int i = r0 + li;
     const int k = threadIdx.x;
@@ -104,14 +111,16 @@ __global__ __launch_bounds__(C) void k_r0_reverse(int r0, long long e0, const in
 #pragma unroll
     for (int v = 0; v < NY; ++v) padj[v] = Phi0_adj[(static_cast<std::size_t>(li) * NY + v) * C + k];
     const int ea = offsets[i], eb = offsets[i + 1];
-    for (int c0 = ea; c0 < eb; c0 += kForceChunk) {
-        const int c1 = min(c0 + kForceChunk, eb);
-        for (int e = c0; e < c1; ++e) {
-            const float* rec = erec + static_cast<std::size_t>(e - e0) * S::REC;
+    const stage4* src = reinterpret_cast<const stage4*>(erec) + static_cast<std::size_t>(ea - e0) * (S::REC / 4);
+    staged_records<C, S::REC>(stage_buf, src, eb - ea, [&](const float* chunk, int first, int n)
+                                                           __attribute__((always_inline)) {
+        for (int j = 0; j < n; ++j) {
+            const float* rec = chunk + j * S::REC;
             if (!edge_active(rec)) {
-                sink.zero(e - c0);
+                sink.zero(j);
                 continue;
             }
+            const int e = ea + first + j;
             const float x = rec[0];
             const int iv = __float_as_int(rec[1]);
             const float xx = x * x, xxx = xx * x, x2 = 2.0f * x, xx3 = 3.0f * xx;
@@ -139,10 +148,10 @@ __global__ __launch_bounds__(C) void k_r0_reverse(int r0, long long e0, const in
                 b2 += R * s2;
             });
             const float u0 = rec[S::REC_U], u1 = rec[S::REC_U + 1], u2 = rec[S::REC_U + 2];
-            sink.put(e - c0, h0 * (u0 * a + b0), h0 * (u1 * a + b1), h0 * (u2 * a + b2));
+            sink.put(j, h0 * (u0 * a + b0), h0 * (u1 * a + b1), h0 * (u2 * a + b2));
         }
-        sink.template flush<ACCUMULATE>(static_cast<int>(c0 - e0), c1 - c0, node_forces);
-    }
+        sink.template flush<ACCUMULATE>(static_cast<long long>(ea + first) - e0, n, node_forces);
+    });
 }
 
 // ---------------------------------------------------------------------------
@@ -640,8 +649,8 @@ __global__ void k_fill_f64(std::size_t n, double* __restrict__ p) {
 
 // ---------------------------------------------------------------------------
 // Node linears on MFMA (v_mfma_f32_16x16x4_f32, FP32 in and out).  One wave
-// computes a 64-row x 64-column block as 4x4 tiles of 16x16.  In a tile, lane
-// l supplies A[l%16][kk] and B[kk][l%16] with kk = l/16 and holds
+// computes a kGemmRows x 64-column block as (kGemmRows/16) x 4 tiles of
+// 16x16.  In a tile, lane l supplies A[l%16][kk] and B[kk][l%16] with kk = l/16 and holds
 // D[4*(l/16)+v][l%16].  The K order inside one 16-wide chunk is permuted so
 // that step s uses k = k0 + 4*(l/16) + s: each lane then reads four
 // consecutive inputs of its row with one 16-byte load, and the weights are
@@ -660,9 +669,10 @@ __global__ __launch_bounds__(64) void k_node_gemm(const GemmTile* __restrict__ t
     const int lane = threadIdx.x;
     const int r = lane & 15, kg = lane >> 4;
     const int nsub = min(4, (g.N - n0) / 16);
-    const float* arow[4];
+    constexpr int RI = kGemmRows / 16;  // 16-row MFMA tiles per wave
+    const float* arow[RI];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < RI; ++i) {
         // rows past the tile's count repeat its last row (their results are not stored)
         const int q = min(16 * i + r, tile.count - 1);
         const int pk = rows[tile.row_start + q];
@@ -670,29 +680,29 @@ __global__ __launch_bounds__(64) void k_node_gemm(const GemmTile* __restrict__ t
     }
     const int nblk = g.N / 16;
     const float4* B = reinterpret_cast<const float4*>(W + g.w_off) + (n0 / 16) * 64 + lane;
-    v4f acc[4][4];
+    v4f acc[RI][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < RI; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
     const int chunks = g.K / 16;
     // operands of chunk kc+1 are loaded while chunk kc runs on the MFMA unit
-    float4 a[4], b[4], an[4], bn[4];
+    float4 a[RI], b[4], an[RI], bn[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const float4*>(arow[i]);
+    for (int i = 0; i < RI; ++i) a[i] = *reinterpret_cast<const float4*>(arow[i]);
 #pragma unroll
     for (int j = 0; j < 4; ++j) b[j] = j < nsub ? B[j * 64] : make_float4(0.f, 0.f, 0.f, 0.f);
     for (int kc = 0; kc < chunks; ++kc) {
         const int kn = kc + 1 < chunks ? kc + 1 : kc;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) an[i] = *reinterpret_cast<const float4*>(arow[i] + 16 * kn);
+        for (int i = 0; i < RI; ++i) an[i] = *reinterpret_cast<const float4*>(arow[i] + 16 * kn);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             bn[j] = j < nsub ? B[(static_cast<std::size_t>(kn) * nblk + j) * 64] : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < RI; ++i) {
                 const float av = s == 0 ? a[i].x : s == 1 ? a[i].y : s == 2 ? a[i].z : a[i].w;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
@@ -704,12 +714,12 @@ __global__ __launch_bounds__(64) void k_node_gemm(const GemmTile* __restrict__ t
             }
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) a[i] = an[i];
+        for (int i = 0; i < RI; ++i) a[i] = an[i];
 #pragma unroll
         for (int j = 0; j < 4; ++j) b[j] = bn[j];
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < RI; ++i) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
             const int q = 16 * i + 4 * kg + v;
@@ -840,12 +850,16 @@ template <int C, int LMAX, int LMAXH, class M0TAB, class M1TAB>
 struct KernelSetImpl final : KernelSet {
     using S = Shape<LMAX, LMAXH>;
     static constexpr bool kM0Unrolled = !std::is_same_v<M0TAB, void>;
-    using Records = RecordEdges<S::NY, S::REC>;
+    // R1 forward reads records with scalar loads (its VGPRs hold the 88+
+    // coupling rows); the R1 reverse stages them through LDS
+    using Records = RecordEdges<C, S::NY, S::REC, false>;
+    using StagedRecords = RecordEdges<C, S::NY, S::REC, true>;
     using Groups = SourceGroups<LMAX, LMAXH>;
     static constexpr int kGroups = static_cast<int>(Groups::masks.size());
     int record_floats() const override { return S::REC; }
-    static Records records(const DeviceModel& m, const TileView& t, const Workspace& w) {
-        return Records{w.erec, t.e0, m.R1c, S::P * C};
+    template <class R = Records>
+    static R records(const DeviceModel& m, const TileView& t, const Workspace& w) {
+        return R{w.erec, t.e0, m.R1c, S::P * C};
     }
     const char* polynomial_mode() const override { return kM0Unrolled ? "unrolled" : "table"; }
 
@@ -918,8 +932,9 @@ struct KernelSetImpl final : KernelSet {
             TimerScope ts(tm, "r1_reverse", s);
             static_for<0, kGroups>([&](auto gc) {
                 constexpr int gi = gc;
-                k_r1_reverse<C, LMAX, LMAXH, Groups::masks[gi], (gi > 0), Records><<<t.nr, C, 0, s>>>(
-                    t.r0, t.e0, g.offsets, g.neigh, records(m, t, w), w.H1, m.cg, w.dPhi1, w.Wsrc, w.node_forces);
+                k_r1_reverse<C, LMAX, LMAXH, Groups::masks[gi], (gi > 0), StagedRecords><<<t.nr, C, 0, s>>>(
+                    t.r0, t.e0, g.offsets, g.neigh, records<StagedRecords>(m, t, w), w.H1, m.cg, w.dPhi1, w.Wsrc,
+                    w.node_forces);
                 SMX_LAUNCH_CHECK("r1_reverse");
             });
         }

@@ -73,7 +73,9 @@ struct GemmGroup {
     int in_stride, in_base, in_mstride;
     int out_stride, out_base, out_mstride;
 };
-constexpr int kGemmRows = 64;  // rows per wave tile
+// rows per wave tile (a multiple of 16): 64 rows x 64 columns per wave
+// reuses every loaded operand four times
+constexpr int kGemmRows = 64;
 struct GemmTile {
     int row_start, count, group;  // rows [row_start, row_start+count), count <= kGemmRows
 };
