@@ -551,21 +551,33 @@ __global__ __launch_bounds__(C) void k_r1_reverse(int r0, long long e0, const in
                     edges.value_slope(pt, p * C + k, R, dR);
                     float T[2 * ls + 1];
                     static_for<0, 2 * ls + 1>([&](auto m2c) { T[m2c] = 0.0f; });
-                    static_for<0, 2 * le + 1>([&](auto m1c) {
-                        constexpr int m1 = m1c;
-                        const float y = edges.Y(pt, le * le + m1);
-                        float sr = 0.0f;
-                        static_for<0, 2 * ls + 1>([&](auto m2c) {
-                            constexpr int m2 = m2c;
-                            if constexpr (RG::in(p, m2)) {
-                                constexpr int r = RG::row(p, m1, m2);
-                                const float g = G[r];
-                                T[m2] += y * g;
-                                sr += g * h[ls * ls + m2];
-                            }
+                    if constexpr (ls == 0) {
+                        // one source component: SB += (R h0) G
+                        const float rh = R * h[0];
+                        static_for<0, 2 * le + 1>([&](auto m1c) {
+                            constexpr int m1 = m1c;
+                            constexpr int r = RG::row(p, m1, 0);
+                            const float g = G[r];
+                            T[0] += edges.Y(pt, le * le + m1) * g;
+                            SB[le * le + m1] += rh * g;
                         });
-                        SB[le * le + m1] += R * sr;
-                    });
+                    } else {
+                        static_for<0, 2 * le + 1>([&](auto m1c) {
+                            constexpr int m1 = m1c;
+                            const float y = edges.Y(pt, le * le + m1);
+                            float sr = 0.0f;
+                            static_for<0, 2 * ls + 1>([&](auto m2c) {
+                                constexpr int m2 = m2c;
+                                if constexpr (RG::in(p, m2)) {
+                                    constexpr int r = RG::row(p, m1, m2);
+                                    const float g = G[r];
+                                    T[m2] += y * g;
+                                    sr += g * h[ls * ls + m2];
+                                }
+                            });
+                            SB[le * le + m1] += R * sr;
+                        });
+                    }
                     float hT = 0.0f;
                     static_for<0, 2 * ls + 1>([&](auto m2c) {
                         constexpr int m2 = m2c;
