@@ -209,6 +209,7 @@ struct Evaluator {
     std::vector<GemmGroup> groups_a0, groups_h1, groups_a1f, groups_a1r;
     DevBuf d_groups_a0, d_groups_h1, d_groups_a1f, d_groups_a1r;
     int max_n_a0 = 0, max_n_h1 = 0, max_n_a1f = 0, max_n_a1r = 0;
+    int sub_a0 = 1, sub_h1 = 1, sub_a1f = 1, sub_a1r = 1;
 
     // execution plan request
     std::string profile = "auto";   // auto | speed | capacity
@@ -373,10 +374,20 @@ struct Evaluator {
             for (const auto& x : g) m = std::max(m, x.N);
             return m;
         };
+        auto sub = [](const std::vector<GemmGroup>& g) {
+            int n = 4;
+            for (const auto& x : g)
+                while ((x.N / 16) % n != 0) n /= 2;
+            return n;
+        };
         max_n_a0 = mx(groups_a0);
         max_n_h1 = mx(groups_h1);
         max_n_a1f = mx(groups_a1f);
         max_n_a1r = mx(groups_a1r);
+        sub_a0 = sub(groups_a0);
+        sub_h1 = sub(groups_h1);
+        sub_a1f = sub(groups_a1f);
+        sub_a1r = sub(groups_a1r);
         upload(d_groups_a0, groups_a0, stream);
         upload(d_groups_h1, groups_h1, stream);
         upload(d_groups_a1f, groups_a1f, stream);
@@ -486,8 +497,9 @@ struct Evaluator {
         }
         upload(d_node_list, h_node_list, stream);
         upload(d_batches, h_batches, stream);
-        auto view = [&](const PlanSet& P, std::size_t ti, const DevBuf& groups, int max_n) {
+        auto view = [&](const PlanSet& P, std::size_t ti, const DevBuf& groups, int max_n, int n_sub) {
             GemmPlan g;
+            g.n_sub = n_sub;
             g.tiles = P.d_tiles.as<GemmTile>() + P.tile_begin[ti];
             g.num_tiles = static_cast<int>(P.tile_begin[ti + 1] - P.tile_begin[ti]);
             g.groups = groups.as<GemmGroup>();
@@ -496,10 +508,10 @@ struct Evaluator {
             return g;
         };
         for (std::size_t ti = 0; ti < tiles.size(); ++ti) {
-            tiles[ti].a0 = view(ps_a0, ti, d_groups_a0, max_n_a0);
-            tiles[ti].h1 = view(ps_h1, ti, d_groups_h1, max_n_h1);
-            tiles[ti].a1f = view(ps_a1f, ti, d_groups_a1f, max_n_a1f);
-            tiles[ti].a1r = view(ps_a1r, ti, d_groups_a1r, max_n_a1r);
+            tiles[ti].a0 = view(ps_a0, ti, d_groups_a0, max_n_a0, sub_a0);
+            tiles[ti].h1 = view(ps_h1, ti, d_groups_h1, max_n_h1, sub_h1);
+            tiles[ti].a1f = view(ps_a1f, ti, d_groups_a1f, max_n_a1f, sub_a1f);
+            tiles[ti].a1r = view(ps_a1r, ti, d_groups_a1r, max_n_a1r, sub_a1r);
             tiles[ti].node_list = d_node_list.as<int>() + node_list_begin[ti];
             tiles[ti].batches = d_batches.as<NodeBatch>() + batch_begin[ti];
             tiles[ti].num_batches = static_cast<int>(batch_begin[ti + 1] - batch_begin[ti]);

@@ -649,27 +649,64 @@ __global__ void k_fill_f64(std::size_t n, double* __restrict__ p) {
 
 // ---------------------------------------------------------------------------
 // Node linears on MFMA (v_mfma_f32_16x16x4_f32, FP32 in and out).  One wave
-// computes a kGemmRows x 64-column block as (kGemmRows/16) x 4 tiles of
-// 16x16.  In a tile, lane l supplies A[l%16][kk] and B[kk][l%16] with kk = l/16 and holds
-// D[4*(l/16)+v][l%16].  The K order inside one 16-wide chunk is permuted so
-// that step s uses k = k0 + 4*(l/16) + s: each lane then reads four
-// consecutive inputs of its row with one 16-byte load, and the weights are
-// pre-swizzled (swizzle_gemm_weights) so that the B operands of one chunk and
-// column block are one contiguous 1 KB float4 load per wave.  Per chunk a
-// wave issues 8 loads and 64 MFMAs.
+// computes a kGemmRows x 16*NSUB-column block as (kGemmRows/16) x NSUB tiles
+// of 16x16.  In a tile, lane l supplies A[l%16][kk] and B[kk][l%16] with
+// kk = l/16 and holds D[4*(l/16)+v][l%16].  The K order inside one 16-wide
+// chunk is permuted so that step s uses k = k0 + 4*(l/16) + s: each lane then
+// reads four consecutive inputs of its row with one 16-byte load, and the
+// weights are pre-swizzled (swizzle_gemm_weights) so that the B operands of
+// one chunk and 16-column block are one contiguous 1 KB float4 load per wave.
+// Per chunk a wave issues RI + NSUB loads and 4*RI*NSUB MFMAs.  Two operand
+// sets alternate: the loads of chunk kc+1 are in flight while chunk kc runs on
+// the MFMA unit.  NSUB is a template constant so that the chunk body is
+// straight-line code (no per-tile branches) and the only waits are for the
+// operands of the chunk about to run.
 // ---------------------------------------------------------------------------
+template <int RI, int NSUB>
+struct GemmOperands {
+    float4 a[RI], b[NSUB];
+};
+
+template <int RI, int NSUB>
+__device__ __forceinline__ void gemm_load(GemmOperands<RI, NSUB>& o, const float* const (&arow)[RI],
+                                          const float4* __restrict__ B, int kc, int nblk) {
+#pragma unroll
+    for (int i = 0; i < RI; ++i) o.a[i] = *reinterpret_cast<const float4*>(arow[i] + 16 * kc);
+#pragma unroll
+    for (int j = 0; j < NSUB; ++j) o.b[j] = B[(static_cast<std::size_t>(kc) * nblk + j) * 64];
+}
+
+template <int RI, int NSUB>
+__device__ __forceinline__ void gemm_chunk(v4f (&acc)[RI][NSUB], const GemmOperands<RI, NSUB>& o) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+#pragma unroll
+        for (int i = 0; i < RI; ++i) {
+            const float av = s == 0 ? o.a[i].x : s == 1 ? o.a[i].y : s == 2 ? o.a[i].z : o.a[i].w;
+#pragma unroll
+            for (int j = 0; j < NSUB; ++j) {
+                const float bv = s == 0 ? o.b[j].x : s == 1 ? o.b[j].y : s == 2 ? o.b[j].z : o.b[j].w;
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[i][j], 0, 0, 0);
+            }
+        }
+    }
+}
+
+template <int NSUB>
 __global__ __launch_bounds__(64) void k_node_gemm(const GemmTile* __restrict__ tiles,
                                                   const GemmGroup* __restrict__ groups, const int* __restrict__ rows,
                                                   const float* __restrict__ W, const float* __restrict__ in,
                                                   float* __restrict__ out) {
+    constexpr int RI = kGemmRows / 16;  // 16-row MFMA tiles per wave
+    // blockIdx.x: row tile; blockIdx.y: 16*NSUB-column block.  (Dispatch
+    // order x-fastest: concurrent waves share one column block's weights.
+    // Grouping a tile's column blocks on one XCD measured slower.)
     const GemmTile tile = tiles[blockIdx.x];
     const GemmGroup g = groups[tile.group];
-    const int n0 = blockIdx.y * 64;
+    const int n0 = blockIdx.y * 16 * NSUB;
     if (n0 >= g.N) return;
     const int lane = threadIdx.x;
     const int r = lane & 15, kg = lane >> 4;
-    const int nsub = min(4, (g.N - n0) / 16);
-    constexpr int RI = kGemmRows / 16;  // 16-row MFMA tiles per wave
     const float* arow[RI];
 #pragma unroll
     for (int i = 0; i < RI; ++i) {
@@ -680,44 +717,30 @@ __global__ __launch_bounds__(64) void k_node_gemm(const GemmTile* __restrict__ t
     }
     const int nblk = g.N / 16;
     const float4* B = reinterpret_cast<const float4*>(W + g.w_off) + (n0 / 16) * 64 + lane;
-    v4f acc[RI][4];
+    v4f acc[RI][NSUB];
 #pragma unroll
     for (int i = 0; i < RI; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int j = 0; j < NSUB; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
     const int chunks = g.K / 16;
-    // operands of chunk kc+1 are loaded while chunk kc runs on the MFMA unit
-    float4 a[RI], b[4], an[RI], bn[4];
+    GemmOperands<RI, NSUB> o0, o1;
+    gemm_load(o0, arow, B, 0, nblk);
+    int kc = 0;
+    for (; kc + 2 <= chunks; kc += 2) {
+        gemm_load(o1, arow, B, kc + 1, nblk);
+        gemm_chunk(acc, o0);
+        gemm_load(o0, arow, B, min(kc + 2, chunks - 1), nblk);
+        gemm_chunk(acc, o1);
+        // issue order: each load set, then the chunk that does not need it,
+        // so every load is one full chunk of MFMAs ahead of its use (left
+        // alone, the scheduler sinks the loads towards their use)
 #pragma unroll
-    for (int i = 0; i < RI; ++i) a[i] = *reinterpret_cast<const float4*>(arow[i]);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) b[j] = j < nsub ? B[j * 64] : make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int kc = 0; kc < chunks; ++kc) {
-        const int kn = kc + 1 < chunks ? kc + 1 : kc;
-#pragma unroll
-        for (int i = 0; i < RI; ++i) an[i] = *reinterpret_cast<const float4*>(arow[i] + 16 * kn);
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            bn[j] = j < nsub ? B[(static_cast<std::size_t>(kn) * nblk + j) * 64] : make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-#pragma unroll
-            for (int i = 0; i < RI; ++i) {
-                const float av = s == 0 ? a[i].x : s == 1 ? a[i].y : s == 2 ? a[i].z : a[i].w;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    if (j < nsub) {
-                        const float bv = s == 0 ? b[j].x : s == 1 ? b[j].y : s == 2 ? b[j].z : b[j].w;
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[i][j], 0, 0, 0);
-                    }
-                }
-            }
+        for (int h = 0; h < 2; ++h) {
+            __builtin_amdgcn_sched_group_barrier(0x020, RI + NSUB, 0);     // VMEM reads
+            __builtin_amdgcn_sched_group_barrier(0x008, 4 * RI * NSUB, 0);  // MFMA
         }
-#pragma unroll
-        for (int i = 0; i < RI; ++i) a[i] = an[i];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) b[j] = bn[j];
     }
+    if (kc < chunks) gemm_chunk(acc, o0);
 #pragma unroll
     for (int i = 0; i < RI; ++i) {
 #pragma unroll
@@ -728,8 +751,7 @@ __global__ __launch_bounds__(64) void k_node_gemm(const GemmTile* __restrict__ t
             float* orow = out + static_cast<std::size_t>(pk >> 4) * g.out_stride + g.out_base + (pk & 15) * g.out_mstride +
                           n0 + r;
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                if (j < nsub) orow[16 * j] = acc[i][j][v];
+            for (int j = 0; j < NSUB; ++j) orow[16 * j] = acc[i][j][v];
         }
     }
 }
@@ -1074,8 +1096,20 @@ bool kernel_paths(int l_max, int L_max, std::vector<int>& le, std::vector<int>& 
 
 void launch_node_gemm(const GemmPlan& plan, const float* W, const float* in, float* out, hipStream_t s) {
     if (plan.num_tiles == 0) return;
-    dim3 grid(plan.num_tiles, (plan.max_n + 63) / 64);
-    k_node_gemm<<<grid, 64, 0, s>>>(plan.tiles, plan.groups, plan.rows, W, in, out);
+    const int cols = 16 * plan.n_sub;
+    const dim3 grid(plan.num_tiles, (plan.max_n + cols - 1) / cols);
+    const unsigned block = 64;
+    switch (plan.n_sub) {
+        case 4:
+            k_node_gemm<4><<<grid, block, 0, s>>>(plan.tiles, plan.groups, plan.rows, W, in, out);
+            break;
+        case 2:
+            k_node_gemm<2><<<grid, block, 0, s>>>(plan.tiles, plan.groups, plan.rows, W, in, out);
+            break;
+        default:
+            k_node_gemm<1><<<grid, block, 0, s>>>(plan.tiles, plan.groups, plan.rows, W, in, out);
+            break;
+    }
     SMX_LAUNCH_CHECK("node_gemm");
 }
 

@@ -73,9 +73,11 @@ struct GemmGroup {
     int in_stride, in_base, in_mstride;
     int out_stride, out_base, out_mstride;
 };
-// rows per wave tile (a multiple of 16): 64 rows x 64 columns per wave
-// reuses every loaded operand four times
-constexpr int kGemmRows = 64;
+// rows per wave tile (a multiple of 16): 32 rows x 64 columns per wave; the
+// smaller tile (against 64 rows) spreads the work over about five waves per
+// SIMD at the medium shape, which balances the SIMDs better than the
+// operand reuse of the larger tile gains
+constexpr int kGemmRows = 32;
 struct GemmTile {
     int row_start, count, group;  // rows [row_start, row_start+count), count <= kGemmRows
 };
@@ -85,6 +87,7 @@ struct GemmPlan {
     const int* rows = nullptr;        // packed (node << 4 | m)
     int num_tiles = 0;
     int max_n = 0;
+    int n_sub = 1;  // 16-column tiles per wave (4, 2 or 1): divides every group's N/16
 };
 
 // Readout batches: up to kReadoutBatch receivers of one type, as a range of
