@@ -135,6 +135,22 @@ struct RecordEdges {
     int functions;
 
     static constexpr int kStageSlots = STAGED ? RecordStage<C, REC>::SLOTS : 1;
+    // The unstaged records can be read one edge ahead (hold): the fields a
+    // forward pass needs, wave-uniform, so they sit in SGPRs.
+    static constexpr bool kHold = !STAGED;
+    struct Held {
+        float x;
+        int iv, active;
+        float y[NY];
+    };
+    __device__ __forceinline__ void hold(int e, Held& h) const {
+        const float* r = erec + static_cast<std::size_t>(e - e0) * REC;
+        h.x = r[0];
+        h.iv = __float_as_int(r[1]);
+        h.active = __float_as_int(r[2]);
+#pragma unroll
+        for (int lm = 0; lm < NY; ++lm) h.y[lm] = r[4 + lm];
+    }
     struct Point {
         const float* rec;
         const float4* cf;
@@ -200,6 +216,7 @@ struct PluginEdges {
     int intervals, functions, active_types, fp64_point;
 
     static constexpr int kStageSlots = 1;
+    static constexpr bool kHold = false;
     struct Point {
         int e;
         const float* c0;  // coefficient c0 of function 0 of this edge's interval
@@ -397,13 +414,9 @@ __global__ __launch_bounds__(C) void k_r1_forward(int r0, const int* __restrict_
 #pragma unroll
     for (int r = 0; r < RG::NR; ++r) rows[r] = 0.0f;
     const int ea = first[i], eb = count ? ea + count[i] : first[i + 1];
-    __shared__ stage4 stage_buf[2 * EDGES::kStageSlots];
-    edges.chunks(ea, eb, stage_buf, [&](int e_first, int n, const float* chunk) __attribute__((always_inline)) {
-    for (int j = 0; j < n; ++j) {
-        const int e = e_first + j;
-        typename EDGES::Point pt;
-        if (!edges.open_at(e, i, chunk, j, pt)) continue;
-        const float* hj = H1 + static_cast<std::size_t>(neigh[e]) * NH * C + k;
+    // rows += R_p(r) Y_lm1 h_lm2 for one edge, given its radial values
+    // (radial(p)), harmonics (Y(lm)) and source row hj
+    auto add_edge = [&](auto&& radial, auto&& Y, const float* hj) __attribute__((always_inline)) {
         float h[NH];
 #pragma unroll
         for (int q = 0; q < NH; ++q) h[q] = RG::component(q) ? hj[q * C] : 0.0f;
@@ -411,19 +424,19 @@ __global__ __launch_bounds__(C) void k_r1_forward(int r0, const int* __restrict_
             constexpr int p = pc;
             if constexpr (RG::used(p)) {
                 constexpr int le = S::paths[p].le, ls = S::paths[p].ls;
-                const float rad = edges.value(pt, p * C + k);
+                const float rad = radial(p);
                 if constexpr (ls == 0) {
                     // one source component: scale R by it once
                     const float rh = rad * h[0];
                     static_for<0, 2 * le + 1>([&](auto m1c) {
                         constexpr int m1 = m1c;
                         constexpr int r = RG::row(p, m1, 0);
-                        rows[r] += rh * edges.Y(pt, le * le + m1);
+                        rows[r] += rh * Y(le * le + m1);
                     });
                 } else {
                     static_for<0, 2 * le + 1>([&](auto m1c) {
                         constexpr int m1 = m1c;
-                        const float ry = rad * edges.Y(pt, le * le + m1);
+                        const float ry = rad * Y(le * le + m1);
                         static_for<0, 2 * ls + 1>([&](auto m2c) {
                             constexpr int m2 = m2c;
                             if constexpr (RG::in(p, m2)) {
@@ -435,8 +448,42 @@ __global__ __launch_bounds__(C) void k_r1_forward(int r0, const int* __restrict_
                 }
             }
         });
+    };
+    if constexpr (EDGES::kHold) {
+        // The wave-uniform record fields and source index of edge e+1 are
+        // loaded while edge e runs, so an edge starts with its spline and
+        // H1 loads instead of a chain of dependent scalar loads.
+        typename EDGES::Held cur, nxt;
+        int src = 0;
+        if (ea < eb) {
+            edges.hold(ea, cur);
+            src = neigh[ea];
+        }
+        for (int e = ea; e < eb; ++e) {
+            const int en = min(e + 1, eb - 1);
+            edges.hold(en, nxt);
+            const int src_n = neigh[en];
+            if (cur.active) {
+                const float x = cur.x, xx = x * x, xxx = xx * x;
+                const float4* cf = edges.coef + static_cast<std::size_t>(cur.iv) * edges.functions;
+                add_edge([&](int p) { return spline_value(cf[p * C + k], x, xx, xxx); },
+                         [&](int lm) { return cur.y[lm]; }, H1 + static_cast<std::size_t>(src) * NH * C + k);
+            }
+            cur = nxt;
+            src = src_n;
+        }
+    } else {
+        __shared__ stage4 stage_buf[2 * EDGES::kStageSlots];
+        edges.chunks(ea, eb, stage_buf, [&](int e_first, int n, const float* chunk) __attribute__((always_inline)) {
+            for (int j = 0; j < n; ++j) {
+                const int e = e_first + j;
+                typename EDGES::Point pt;
+                if (!edges.open_at(e, i, chunk, j, pt)) continue;
+                add_edge([&](int p) { return edges.value(pt, p * C + k); },
+                         [&](int lm) { return edges.Y(pt, lm); }, H1 + static_cast<std::size_t>(neigh[e]) * NH * C + k);
+            }
+        });
     }
-    });
     float* out = Phi1 + static_cast<std::size_t>(li) * S::NLME * C + k;
     static_for<0, S::P>([&](auto pc) {
         constexpr int p = pc;
