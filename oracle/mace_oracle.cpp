@@ -396,6 +396,11 @@ struct Mace {
     std::vector<double> H2, H2_adj, direct;
     std::vector<double> node_energies, node_forces;
     std::vector<double> node_forces_r1;  // directed forces of the R1 reverse alone
+    // layer-1 intermediates: Phi0 = sum_e R0 Y H0 before the A0 linear, its
+    // adjoint (A0_adj through the transposed linear) and the directed forces
+    // of the R0 reverse alone
+    std::vector<P> Phi0, Phi0_adj;
+    std::vector<double> node_forces_r0;
 
     static P cast(double v) {
         if (!std::isfinite(v) || std::abs(v) > static_cast<double>(std::numeric_limits<P>::max()))
@@ -589,6 +594,7 @@ struct Mace {
 
         // ---- A0 (mace.cpp:1356-1403)
         A0.assign(static_cast<std::size_t>(n) * nY * Cs, P(0));
+        Phi0.assign(static_cast<std::size_t>(n) * nY * Cs, P(0));
 #pragma omp parallel for schedule(dynamic, 16)
         for (int i = 0; i < n; ++i) {
             std::vector<P> phi(nY * Cs, P(0)), rad(Cs);
@@ -612,6 +618,7 @@ struct Mace {
                     }
                 }
             }
+            std::copy(phi.begin(), phi.end(), Phi0.begin() + static_cast<std::size_t>(i) * nY * Cs);
             for (int l = 0; l <= l_max; ++l) {
                 const P* W = A0_w[types[i]][l].data();
                 for (int m = 0; m < 2 * l + 1; ++m) {
@@ -938,6 +945,8 @@ struct Mace {
             }
 
         // ---- reverse A0 (mace.cpp:1486-1560)
+        Phi0_adj.assign(static_cast<std::size_t>(n) * nY * Cs, P(0));
+        node_forces_r0.assign(static_cast<std::size_t>(E) * 3, 0.0);
 #pragma omp parallel for schedule(dynamic, 16)
         for (int i = 0; i < n; ++i) {
             std::vector<P> padj(nY * Cs, P(0)), rad(Cs), drad(Cs);
@@ -981,8 +990,12 @@ struct Mace {
                             f[c] -= static_cast<double>(dirs[3 * e + c] * radial_sum * y[lm] + angular_sum * g[c * nY + lm]);
                     }
                 }
-                for (int c = 0; c < 3; ++c) node_forces[3 * e + c] += f[c];
+                for (int c = 0; c < 3; ++c) {
+                    node_forces[3 * e + c] += f[c];
+                    node_forces_r0[3 * e + c] = f[c];
+                }
             }
+            std::copy(padj.begin(), padj.end(), Phi0_adj.begin() + static_cast<std::size_t>(i) * nY * Cs);
         }
     }
 };
@@ -1195,7 +1208,8 @@ int oracle_evaluate(void* hv, int n, const int* types, const int* num_neigh, con
 }
 
 // Stage buffers of the last evaluation, as float64: name in {Y, Ygrad, A0, M0,
-// M0_grad, H1, Phi1, A1, M1, H2, H2_adj, A1_adj, dPhi1, H1_adj, M0_adj, A0_adj}.
+// M0_grad, H1, Phi1, A1, M1, H2, H2_adj, A1_adj, dPhi1, H1_adj, M0_adj, A0_adj,
+// node_forces_r1, Phi0, Phi0_adj, node_forces_r0}.
 long long oracle_stage(void* hv, const char* name, double* out, long long capacity) {
     auto* h = static_cast<OracleHandle*>(hv);
     auto get = [&](auto& m) -> long long {
@@ -1222,6 +1236,9 @@ long long oracle_stage(void* hv, const char* name, double* out, long long capaci
         if (s == "M0_adj") return emit(m.M0_adj);
         if (s == "A0_adj") return emit(m.A0_adj);
         if (s == "node_forces_r1") return emit(m.node_forces_r1);
+        if (s == "Phi0") return emit(m.Phi0);
+        if (s == "Phi0_adj") return emit(m.Phi0_adj);
+        if (s == "node_forces_r0") return emit(m.node_forces_r0);
         return -1;
     };
     return h->fp64 ? get(*h->d) : get(*h->f);

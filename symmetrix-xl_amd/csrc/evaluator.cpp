@@ -18,6 +18,7 @@
 #include <cstring>
 #include <map>
 #include <memory>
+#include <mutex>
 #include <new>
 #include <numeric>
 #include <stdexcept>
@@ -25,6 +26,7 @@
 #include <vector>
 
 #include "../../include/symmetrix_mi355x.h"
+#include "../../include/symmetrix_operator_modules.h"
 #include "device_common.hpp"
 #include "kernels.hpp"
 #include "model.hpp"
@@ -979,6 +981,31 @@ smx::Evaluator& E(SmxEvaluator* ev) {
     if (!ev) throw std::invalid_argument("evaluator handle is NULL");
     return ev->impl;
 }
+
+// Host model of the last file the array exports read (a model is parsed once
+// for the several arrays a caller asks for).
+std::mutex g_export_mutex;
+std::string g_export_path;
+std::shared_ptr<smx::HostModel> g_export_model;
+
+std::shared_ptr<smx::HostModel> export_model(const char* path) {
+    if (!path) throw std::invalid_argument("model path is NULL");
+    if (!g_export_model || g_export_path != path) {
+        auto m = std::make_shared<smx::HostModel>();
+        m->load(path, "");
+        g_export_model = std::move(m);
+        g_export_path = path;
+    }
+    return g_export_model;
+}
+
+template <class T>
+void export_array(const std::vector<T>& v, T* out, int64_t capacity, int64_t* count) {
+    if (count) *count = static_cast<int64_t>(v.size());
+    if (!out) return;
+    if (capacity < static_cast<int64_t>(v.size())) throw std::invalid_argument("output capacity is too small");
+    std::copy(v.begin(), v.end(), out);
+}
 const smx::Evaluator& E(const SmxEvaluator* ev) {
     if (!ev) throw std::invalid_argument("evaluator handle is NULL");
     return ev->impl;
@@ -1275,6 +1302,66 @@ int32_t smx_neighbor_list(int32_t num_nodes, const double* positions, const doub
             throw;
         }
         cleanup();
+    });
+}
+
+int32_t smx_model_array_f32(const char* model_path, const char* name, float* out, int64_t capacity, int64_t* count,
+                            int32_t dims[4], double* h, double* x0) {
+    return guarded([&] {
+        if (!name) throw std::invalid_argument("array name is NULL");
+        std::lock_guard<std::mutex> lock(g_export_mutex);
+        const auto m = export_model(model_path);
+        const std::string n(name);
+        int32_t d[4] = {0, 0, 0, 0};
+        if (n == "M0_weights") {
+            d[0] = m->num_elements;
+            d[1] = static_cast<int32_t>(m->m0_terms.size());
+            d[2] = m->C;
+            export_array(m->m0_coef, out, capacity, count);
+        } else if (n == "H0") {
+            d[0] = m->num_elements;
+            d[1] = m->C;
+            export_array(m->H0, out, capacity, count);
+        } else if (n == "R0_spline") {
+            // stored [interval][function][4]; exported [interval][4][function]
+            const int F = m->R0_functions, I = m->spline_points - 1;
+            d[0] = I;
+            d[1] = 4;
+            d[2] = F;
+            std::vector<float> t(static_cast<std::size_t>(I) * 4 * F);
+            for (int i = 0; i < I; ++i)
+                for (int f = 0; f < F; ++f)
+                    for (int c = 0; c < 4; ++c)
+                        t[(static_cast<std::size_t>(i) * 4 + c) * F + f] =
+                            m->R0_coef[(static_cast<std::size_t>(i) * F + f) * 4 + c];
+            export_array(t, out, capacity, count);
+            if (h) *h = m->h;
+            if (x0) *x0 = m->grid_min;
+        } else {
+            throw std::invalid_argument("unknown model array " + n);
+        }
+        if (dims) std::copy(d, d + 4, dims);
+    });
+}
+
+int32_t smx_model_array_i32(const char* model_path, const char* name, int32_t* out, int64_t capacity, int64_t* count,
+                            int32_t dims[4]) {
+    return guarded([&] {
+        if (!name) throw std::invalid_argument("array name is NULL");
+        std::lock_guard<std::mutex> lock(g_export_mutex);
+        const auto m = export_model(model_path);
+        const std::string n(name);
+        int32_t d[4] = {0, 0, 0, 0};
+        if (n == "M0_terms") {
+            d[0] = static_cast<int32_t>(m->m0_terms.size());
+            export_array(m->m0_terms, out, capacity, count);
+        } else if (n == "M0_offsets") {
+            d[0] = static_cast<int32_t>(m->m0_term_offset.size());
+            export_array(m->m0_term_offset, out, capacity, count);
+        } else {
+            throw std::invalid_argument("unknown model array " + n);
+        }
+        if (dims) std::copy(d, d + 4, dims);
     });
 }
 

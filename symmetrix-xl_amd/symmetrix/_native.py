@@ -99,6 +99,8 @@ SIGNATURES = [
     ("smx_neighbor_list", _i32, [_i32, _vp, _vp, _vp, _dbl, _p_i64, _vp, _vp, _vp, _vp, _vp]),
     ("smx_r1_plugin_configure", _i32, [_cp, ctypes.POINTER(SmxR1PluginIdentity)]),
     ("smx_r1_plugin_spline_table", _i32, [_vp, _i64, _p_i32, _p_i32, _p_dbl, _p_dbl]),
+    ("smx_model_array_f32", _i32, [_cp, _cp, _vp, _i64, _p_i64, _p_i32, _p_dbl, _p_dbl]),
+    ("smx_model_array_i32", _i32, [_cp, _cp, _vp, _i64, _p_i64, _p_i32]),
 ]
 
 
@@ -149,3 +151,27 @@ def i32(a):
 
 def f64(a):
     return np.ascontiguousarray(a, dtype=np.float64).reshape(-1)
+
+
+def model_array(model_path, name):
+    """A model array in an operator module's layout (smx_model_array_f32/i32):
+    float32 "M0_weights", "H0", "R0_spline" (returned with the grid h, x0) or
+    int32 "M0_terms", "M0_offsets"."""
+    is_int = name in ("M0_terms", "M0_offsets")
+    count, dims = ctypes.c_int64(), (ctypes.c_int32 * 4)()
+    h, x0 = ctypes.c_double(), ctypes.c_double()
+    path = str(model_path).encode()
+    if is_int:
+        check(lib.smx_model_array_i32(path, name.encode(), None, 0, ctypes.byref(count), dims))
+    else:
+        check(lib.smx_model_array_f32(path, name.encode(), None, 0, ctypes.byref(count), dims, None, None))
+    shape = tuple(d for d in dims if d > 0)
+    out = np.empty(count.value, dtype=np.int32 if is_int else np.float32)
+    if is_int:
+        check(lib.smx_model_array_i32(path, name.encode(), ptr(out), out.size, ctypes.byref(count), dims))
+        return out.reshape(shape)
+    check(lib.smx_model_array_f32(path, name.encode(), ptr(out), out.size, ctypes.byref(count), dims,
+                                  ctypes.byref(h), ctypes.byref(x0)))
+    if name == "R0_spline":
+        return out.reshape(shape), h.value, x0.value
+    return out.reshape(shape)
