@@ -1433,4 +1433,9 @@ int oracle_reduce_stress(long long E, const double* f, const double* xyz, double
 
 int oracle_num_threads() { return omp_get_max_threads(); }
 
+// OpenMP threads of later calls (the CPU baseline's 8-core comparison run)
+void oracle_set_num_threads(int n) {
+    if (n > 0) omp_set_num_threads(n);
+}
+
 }  // extern "C"

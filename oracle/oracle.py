@@ -41,6 +41,7 @@ def lib():
         L.oracle_atomic_numbers.argtypes = [ctypes.c_void_p, _i32p]
         L.oracle_evaluate.argtypes = [ctypes.c_void_p, ctypes.c_int, _i32p, _i32p, _i32p, _i32p,
                                       _f64p, _f64p, _f64p, _f64p]
+        L.oracle_set_num_threads.argtypes = [ctypes.c_int]
         L.oracle_stage.restype = ctypes.c_longlong
         L.oracle_stage.argtypes = [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_void_p, ctypes.c_longlong]
         L.oracle_radial_tables.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p,

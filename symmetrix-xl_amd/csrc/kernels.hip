@@ -368,129 +368,142 @@ __global__ __launch_bounds__(C) void k_m1(int r0, const int* __restrict__ types,
     for (int v = 0; v < NY; ++v) grad[(static_cast<std::size_t>(li) * NY + v) * C + k] = g[v];
 }
 
-// H2 (FP64), readouts (FP64) and their adjoints for a batch of up to RB
-// receivers of one type (the weights are read once per batch):
+// H2 (FP64), readouts (FP64) and their adjoints for a tile of up to 16
+// receivers of one type:
 //   E_i = E0[z] + q.x + MLP(H2), H2 = T_z^T x + W^T M1 (x = M0[i,0,:])
 //   direct = q + T_z H2_adj, A1_adj[v] = dM1/dA1_v * (W H2_adj)
 // Readout MLP: hidden = SiLU*scale(W1 H2), E += W2 . hidden (mace.cpp:2600-2657).
 // On entry A1_adj holds the unscaled M1 gradient from k_m1.
-template <int C, int NY, int RB>
-__global__ __launch_bounds__(C) void k_readout(
+//
+// The four products (H2; the MLP pre-activations W1 H2; the hidden adjoint
+// times W1; T and W times H2_adj) run as FP64 MFMA tiles
+// (v_mfma_f64_16x16x4_f64, exact FP64 products and sums): the tile's 16
+// receivers are the 16 rows, each of the workgroup's kReadoutWaves waves
+// takes every kReadoutWaves-th 16-column block, the row operands come from LDS and the weights (FP32
+// values, widened) straight from L2.  Lane l supplies A[l%16][l/16] and
+// B[l/16][l%16] and holds D[l/16 + 4v][l%16], v = 0..3.
+// ---------------------------------------------------------------------------
+typedef double v4d __attribute__((ext_vector_type(4)));
+static_assert(kReadoutBatch == 16, "readout tiles are the 16 rows of an FP64 MFMA tile");
+
+__device__ __forceinline__ v4d mfma_f64(double a, double b, v4d c) {
+    return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
+}
+
+constexpr int kReadoutWaves = 8;
+
+template <int C, int NY>
+__global__ __launch_bounds__(64 * kReadoutWaves) void k_readout(
     int r0, const NodeBatch* __restrict__ batches, const int* __restrict__ node_list, const int* __restrict__ types,
     const float* __restrict__ M1, const float* __restrict__ xaff, const float* __restrict__ H2_T,
     const float* __restrict__ H2_Tt, const float* __restrict__ H2_M1, const float* __restrict__ H2_M1t,
     const double* __restrict__ q, const double* __restrict__ W1r, const double* __restrict__ W2r, int hidden,
     double scale, const double* __restrict__ E0, double* __restrict__ node_energies, float* __restrict__ direct,
     float* __restrict__ A1_adj) {
-    __shared__ double sx[RB][C], sm1[RB][C], sh[RB][C];
-    __shared__ double sz[RB][kMaxReadoutHidden + 1], sd[RB][kMaxReadoutHidden];
+    static_assert(C % 16 == 0, "16-column MFMA blocks");
+    constexpr int R = kReadoutBatch, NT = C / 16, WAVES = kReadoutWaves, THREADS = 64 * WAVES;
+    constexpr int HMAX = kMaxReadoutHidden;
+    __shared__ float sA[R][2 * C + 1];      // [x | M1] rows (FP32 values)
+    __shared__ double sH[R][C + 1];         // H2, then its adjoint
+    __shared__ double sZ[R][HMAX + 1];      // pre-activations, then W2 act'(z)
+    __shared__ double sP[R][HMAX + 1];      // W2 act(z) terms of the energy
     const NodeBatch b = batches[blockIdx.x];
-    const int k = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int r = lane & 15, kk = lane >> 4;
     const int t = types[r0 + node_list[b.start]];
-    int li[RB];
-#pragma unroll
-    for (int n = 0; n < RB; ++n) {
-        li[n] = node_list[b.start + min(n, b.count - 1)];
+    for (int p = tid; p < R * C; p += THREADS) {
+        const int n = p / C, k = p % C;
         const bool ok = n < b.count;
-        sm1[n][k] = ok ? static_cast<double>(M1[static_cast<std::size_t>(li[n]) * C + k]) : 0.0;
-        sx[n][k] = ok ? static_cast<double>(xaff[static_cast<std::size_t>(r0 + li[n]) * C + k]) : 0.0;
+        const int li = ok ? node_list[b.start + n] : 0;
+        sA[n][k] = ok ? xaff[static_cast<std::size_t>(r0 + li) * C + k] : 0.0f;
+        sA[n][C + k] = ok ? M1[static_cast<std::size_t>(li) * C + k] : 0.0f;
     }
+    for (int p = tid; p < R * (HMAX + 1); p += THREADS) sZ[p / (HMAX + 1)][p % (HMAX + 1)] = 0.0;
     __syncthreads();
-    // H2[n][k] = sum_in T[in][k] x[n][in] + sum_in W[in][k] M1[n][in]
+    // H2[n][c] = sum_in T[in][c] x[n][in] + sum_in W[in][c] M1[n][in]
     {
         const float* T = H2_T + static_cast<std::size_t>(t) * C * C;
-        double h2[RB];
+        for (int j = w; j < NT; j += WAVES) {
+            const int col = 16 * j + r;
+            // the two products accumulate separately (independent MFMA chains)
+            v4d ax = {0.0, 0.0, 0.0, 0.0}, am = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll 8
+            for (int k0 = 0; k0 < C; k0 += 4) {
+                ax = mfma_f64(sA[r][k0 + kk], T[(k0 + kk) * C + col], ax);
+                am = mfma_f64(sA[r][C + k0 + kk], H2_M1[(k0 + kk) * C + col], am);
+            }
 #pragma unroll
-        for (int n = 0; n < RB; ++n) h2[n] = 0.0;
-#pragma unroll 4
-        for (int in = 0; in < C; ++in) {
-            const double w = static_cast<double>(T[in * C + k]);
-#pragma unroll
-            for (int n = 0; n < RB; ++n) h2[n] += w * sx[n][in];
+            for (int v = 0; v < 4; ++v) sH[kk + 4 * v][col] = ax[v] + am[v];
         }
-#pragma unroll 4
-        for (int in = 0; in < C; ++in) {
-            const double w = static_cast<double>(H2_M1[in * C + k]);
-#pragma unroll
-            for (int n = 0; n < RB; ++n) h2[n] += w * sm1[n][in];
-        }
-#pragma unroll
-        for (int n = 0; n < RB; ++n) sh[n][k] = h2[n];
     }
     __syncthreads();
-    // pre-activations z[n][hd] = W1[hd] . H2[n] with the activation slope
-    // act'(z) in sd; z[n][hidden] = q . x[n]
-    const int H1p = hidden + 1;
-    for (int p = k; p < RB * H1p; p += C) {
-        const int n = p / H1p, hd = p % H1p;
-        double z = 0.0;
-        if (hd < hidden) {
-            const double* w = W1r + static_cast<std::size_t>(hd) * C;
-#pragma unroll 4
-            for (int kk = 0; kk < C; ++kk) z += w[kk] * sh[n][kk];
-            const double sg = 1.0 / (1.0 + exp(-z));
-            sd[n][hd] = scale * sg + scale * z * sg * (1.0 - sg);
-        } else {
-#pragma unroll 4
-            for (int kk = 0; kk < C; ++kk) z += q[kk] * sx[n][kk];
-        }
-        sz[n][hd] = z;
+    // z[n][hd] = W1[hd] . H2[n]; columns past hidden stay zero
+    const int HT = (hidden + 15) / 16;
+    for (int j = w; j < HT; j += WAVES) {
+        const int hd = 16 * j + r;
+        const double* w1 = W1r + static_cast<std::size_t>(min(hd, hidden - 1)) * C;
+        const bool ok = hd < hidden;
+        v4d acc = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll 8
+        for (int k0 = 0; k0 < C; k0 += 4) acc = mfma_f64(sH[r][k0 + kk], ok ? w1[k0 + kk] : 0.0, acc);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) sZ[kk + 4 * v][hd] = acc[v];
     }
     __syncthreads();
-    if (k < b.count) {
-        const int n = k;
+    // activation: energy terms and g = W2 act'(z)
+    for (int p = tid; p < R * hidden; p += THREADS) {
+        const int n = p / hidden, hd = p % hidden;
+        const double z = sZ[n][hd];
+        const double sg = 1.0 / (1.0 + exp(-z));
+        sP[n][hd] = W2r[hd] * (scale * z * sg);
+        sZ[n][hd] = W2r[hd] * (scale * sg + scale * z * sg * (1.0 - sg));
+    }
+    __syncthreads();
+    if (tid < b.count) {
+        const int n = tid;
+        double qx = 0.0;
+        for (int k = 0; k < C; ++k) qx += q[k] * static_cast<double>(sA[n][k]);
         double out = 0.0;
-        for (int hd = 0; hd < hidden; ++hd) {
-            const double z = sz[n][hd];
-            const double sg = 1.0 / (1.0 + exp(-z));
-            out += W2r[hd] * (scale * z * sg);
-        }
-        node_energies[r0 + li[n]] = E0[t] + sz[n][hidden] + out;
+        for (int hd = 0; hd < hidden; ++hd) out += sP[n][hd];
+        node_energies[r0 + node_list[b.start + n]] = E0[t] + qx + out;
     }
-    // H2 adjoint: h2a[n][k] = sum_hd W2[hd] act'(z[n][hd]) W1[hd][k]
-    {
-        double h2a[RB];
-#pragma unroll
-        for (int n = 0; n < RB; ++n) h2a[n] = 0.0;
-        for (int hd = 0; hd < hidden; ++hd) {
-            const double w1 = W1r[static_cast<std::size_t>(hd) * C + k];
-            const double w2 = W2r[hd];
-#pragma unroll
-            for (int n = 0; n < RB; ++n) h2a[n] += w2 * sd[n][hd] * w1;
+    // H2 adjoint h2a[n][c] = sum_hd g[n][hd] W1[hd][c] (over sH: H2 is no
+    // longer read)
+    for (int j = w; j < NT; j += WAVES) {
+        const int col = 16 * j + r;
+        v4d acc = {0.0, 0.0, 0.0, 0.0};
+        for (int k0 = 0; k0 < 16 * HT; k0 += 4) {
+            const int hd = k0 + kk;
+            acc = mfma_f64(sZ[r][hd], hd < hidden ? W1r[static_cast<std::size_t>(hd) * C + col] : 0.0, acc);
         }
-        __syncthreads();  // every lane has finished reading sh (H2)
 #pragma unroll
-        for (int n = 0; n < RB; ++n) sh[n][k] = h2a[n];
+        for (int v = 0; v < 4; ++v) sH[kk + 4 * v][col] = acc[v];
     }
     __syncthreads();
     // direct = q + T H2_adj; M1 adjoint = W H2_adj
-    double dsum[RB], s1[RB];
-#pragma unroll
-    for (int n = 0; n < RB; ++n) {
-        dsum[n] = q[k];
-        s1[n] = 0.0;
-    }
     {
         const float* Tt = H2_Tt + static_cast<std::size_t>(t) * C * C;
-#pragma unroll 4
-        for (int o = 0; o < C; ++o) {
-            const double wt = static_cast<double>(Tt[o * C + k]);
-            const double wm = static_cast<double>(H2_M1t[o * C + k]);
-#pragma unroll
-            for (int n = 0; n < RB; ++n) {
-                dsum[n] += wt * sh[n][o];
-                s1[n] += wm * sh[n][o];
+        for (int j = w; j < NT; j += WAVES) {
+            const int col = 16 * j + r;
+            v4d ad = {0.0, 0.0, 0.0, 0.0}, as = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll 8
+            for (int k0 = 0; k0 < C; k0 += 4) {
+                const double a = sH[r][k0 + kk];
+                ad = mfma_f64(a, Tt[(k0 + kk) * C + col], ad);
+                as = mfma_f64(a, H2_M1t[(k0 + kk) * C + col], as);
             }
-        }
-    }
 #pragma unroll
-    for (int n = 0; n < RB; ++n) {
-        if (n < b.count) {
-            direct[static_cast<std::size_t>(r0 + li[n]) * C + k] = static_cast<float>(dsum[n]);
-            const float m1adj = static_cast<float>(s1[n]);
-            float* g = A1_adj + static_cast<std::size_t>(li[n]) * NY * C + k;
+            for (int v = 0; v < 4; ++v) {
+                const int n = kk + 4 * v;
+                if (n < b.count) {
+                    const int li = node_list[b.start + n];
+                    direct[static_cast<std::size_t>(r0 + li) * C + col] = static_cast<float>(q[col] + ad[v]);
+                    const float m1adj = static_cast<float>(as[v]);
+                    float* g = A1_adj + static_cast<std::size_t>(li) * NY * C + col;
 #pragma unroll
-            for (int v = 0; v < NY; ++v) g[v * C] = g[v * C] * m1adj;
+                    for (int u = 0; u < NY; ++u) g[u * C] = g[u * C] * m1adj;
+                }
+            }
         }
     }
 }
@@ -896,7 +909,7 @@ struct KernelSetImpl final : KernelSet {
             k_m1<C, S::NY, M1TAB><<<t.nr, C, 0, s>>>(t.r0, g.node_types, w.A1, m.m1_terms, m.T1, m.m1_coef, w.M1,
                                                     w.A1_adj);
             SMX_LAUNCH_CHECK("m1");
-            k_readout<C, S::NY, kReadoutBatch><<<t.num_batches, C, 0, s>>>(
+            k_readout<C, S::NY><<<t.num_batches, 64 * kReadoutWaves, 0, s>>>(
                 t.r0, t.batches, t.node_list, g.node_types, w.M1, w.xaff, m.H2_T, m.H2_Tt, m.H2_M1, m.H2_M1t, m.q,
                 m.W1r, m.W2r, m.hidden, m.readout_scale, m.E0, w.node_energies, w.direct, w.A1_adj);
             SMX_LAUNCH_CHECK("readout");

@@ -92,7 +92,7 @@ struct GemmPlan {
 
 // Readout batches: up to kReadoutBatch receivers of one type, as a range of
 // the tile's type-sorted node list.
-constexpr int kReadoutBatch = 8;
+constexpr int kReadoutBatch = 16;  // the readout kernel's MFMA tile rows
 constexpr int kMaxReadoutHidden = 64;  // readout MLP width the readout kernel holds in LDS
 struct NodeBatch {
     int start, count;
