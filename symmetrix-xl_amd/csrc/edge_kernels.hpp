@@ -569,10 +569,8 @@ __global__ __launch_bounds__(C) void k_r1_reverse(int r0, long long e0, const in
             float* wdst = Wsrc + static_cast<std::size_t>(e - e0) * NH * C + k;
             typename EDGES::Point pt;
             if (!edges.open_at(e, i, chunk, j, pt)) {
-                // inactive edges contribute zero to their source's adjoint
-#pragma unroll
-                for (int q = 0; q < NH; ++q)
-                    if (RG::component(q)) __builtin_nontemporal_store(0.0f, wdst + q * C);
+                // inactive edges (r >= cutoff) contribute nothing: their W is
+                // not written and the source gathers skip them
                 sink.zero(j);
                 continue;
             }
@@ -657,43 +655,64 @@ __global__ __launch_bounds__(C) void k_r1_reverse(int r0, long long e0, const in
 // ---------------------------------------------------------------------------
 // Source adjoint: sum over the edges leaving s (source-transpose order) of
 // W_e, accumulated in FP64 like the reference's source-adjoint accumulator.
-// Four edges are loaded per step so that their independent rows are in
-// flight together; the sum keeps the source-transpose order.
+// Only active edges (r < r_cut; r indexed like W) have a W row; the others
+// contribute zero and are skipped, which saves reading a quarter of W at a
+// 0.5 A skin.  Each wave reads one edge id and length per lane for the next
+// 64 transpose slots, takes the ballot of the active ones and walks its set
+// bits in order, eight rows in flight at a time; the sum keeps the
+// source-transpose order (a padded slot adds +0.0, which leaves the FP64
+// accumulator unchanged: it starts at +0.0 and so is never -0.0).
 // ---------------------------------------------------------------------------
 template <int C, int NH>
 __device__ __forceinline__ void gather_source_rows(const int* __restrict__ sedges, int t0, int t1, long long e_base,
-                                                   const float* __restrict__ Wsrc, int k, double* acc) {
-    int t = t0;
-    for (; t + 4 <= t1; t += 4) {
-        float w[4][NH];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const float* row = Wsrc + static_cast<std::size_t>(sedges[t + u] - e_base) * NH * C + k;
-#pragma unroll
-            for (int q = 0; q < NH; ++q) w[u][q] = __builtin_nontemporal_load(row + q * C);
+                                                   const float* __restrict__ Wsrc, const double* __restrict__ r,
+                                                   double r_cut, int k, double* acc) {
+    constexpr int L = C < kWave ? C : kWave;
+    constexpr int G = 8;
+    const int lane = threadIdx.x % kWave;
+    for (int base = t0; base < t1; base += L) {
+        int e = 0;
+        bool on = false;
+        if (base + lane < t1) {
+            e = static_cast<int>(sedges[base + lane] - e_base);
+            on = r[e] < r_cut;
         }
+        unsigned long long live = __ballot(on);
+        while (live) {
+            float w[G][NH];
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
+            for (int u = 0; u < G; ++u) {
+                if (live) {
+                    const int l = __builtin_ctzll(live);
+                    live &= live - 1;
+                    const int eu = __builtin_amdgcn_readlane(e, l);
+                    const float* row = Wsrc + static_cast<std::size_t>(eu) * NH * C + k;
 #pragma unroll
-            for (int q = 0; q < NH; ++q) acc[q] += static_cast<double>(w[u][q]);
-    }
-    for (; t < t1; ++t) {
-        const float* row = Wsrc + static_cast<std::size_t>(sedges[t] - e_base) * NH * C + k;
+                    for (int q = 0; q < NH; ++q) w[u][q] = __builtin_nontemporal_load(row + q * C);
+                } else {
 #pragma unroll
-        for (int q = 0; q < NH; ++q) acc[q] += static_cast<double>(row[q * C]);
+                    for (int q = 0; q < NH; ++q) w[u][q] = 0.0f;
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < G; ++u)
+#pragma unroll
+                for (int q = 0; q < NH; ++q) acc[q] += static_cast<double>(w[u][q]);
+        }
     }
 }
 
 // H1_adj[s] = (or, with ACCUMULATE, +=) the FP64 sum of W over s's edges
 template <int C, int NH, bool ACCUMULATE>
 __global__ __launch_bounds__(C) void k_source_gather(const int* __restrict__ soff, const int* __restrict__ sedges,
-                                                     const float* __restrict__ Wsrc, float* __restrict__ H1_adj) {
+                                                     const float* __restrict__ Wsrc, const double* __restrict__ r,
+                                                     double r_cut, float* __restrict__ H1_adj) {
     const int s = xcd_remap(blockIdx.x, gridDim.x);
     const int k = threadIdx.x;
     double acc[NH];
 #pragma unroll
     for (int q = 0; q < NH; ++q) acc[q] = 0.0;
-    gather_source_rows<C, NH>(sedges, soff[s], soff[s + 1], 0, Wsrc, k, acc);
+    gather_source_rows<C, NH>(sedges, soff[s], soff[s + 1], 0, Wsrc, r, r_cut, k, acc);
     float* dst = H1_adj + static_cast<std::size_t>(s) * NH * C + k;
 #pragma unroll
     for (int q = 0; q < NH; ++q) dst[q * C] = ACCUMULATE ? dst[q * C] + static_cast<float>(acc[q])

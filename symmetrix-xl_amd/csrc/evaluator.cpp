@@ -741,7 +741,7 @@ struct Evaluator {
             tile_geometry(t, positions);
             ks->layer1_forward(dm, g, t, ws, true, stream, tm);
             ks->layer2(dm, g, t, ws, stream, tm);
-            ks->source_adjoint_all(g, ws, stream, tm);
+            ks->source_adjoint_all(g, ws, tile_r(t), hm.r_cut, stream, tm);
             ks->layer1_reverse(dm, g, t, ws, true, stream, tm);
             evaluated = true;
             return;
@@ -757,7 +757,7 @@ struct Evaluator {
         for (const auto& t : tiles) {
             tile_geometry(t, positions);
             ks->layer2(dm, g, t, ws, stream, tm);
-            ks->source_adjoint_tile(g, t, ws, stream, tm);
+            ks->source_adjoint_tile(g, t, ws, tile_r(t), hm.r_cut, stream, tm);
             accumulate_tile_outputs(t);
         }
         for (const auto& t : tiles) {

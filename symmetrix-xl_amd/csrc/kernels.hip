@@ -533,6 +533,7 @@ __global__ __launch_bounds__(C) void k_tile_source_adjoint(const int* __restrict
                                                            const int* __restrict__ soff,
                                                            const int* __restrict__ sedges,
                                                            const float* __restrict__ Wsrc,
+                                                           const double* __restrict__ r, double r_cut,
                                                            float* __restrict__ H1_adj) {
     const int s = touched[blockIdx.x];
     const int k = threadIdx.x;
@@ -542,7 +543,7 @@ __global__ __launch_bounds__(C) void k_tile_source_adjoint(const int* __restrict
     const int hi = soff[s + 1];
     const int lo = lower_edge(sedges, soff[s], hi, e0);
     const int end = lower_edge(sedges, lo, hi, e1);
-    gather_source_rows<C, NH>(sedges, lo, end, e0, Wsrc, k, acc);
+    gather_source_rows<C, NH>(sedges, lo, end, e0, Wsrc, r, r_cut, k, acc);
     float* dst = H1_adj + static_cast<std::size_t>(s) * NH * C + k;
 #pragma unroll
     for (int q = 0; q < NH; ++q) dst[q * C] = dst[q * C] + static_cast<float>(acc[q]);
@@ -930,19 +931,20 @@ struct KernelSetImpl final : KernelSet {
         }
     }
 
-    void source_adjoint_all(const DeviceGraph& g, const Workspace& w, hipStream_t s, LaunchTimer* tm) const override {
+    void source_adjoint_all(const DeviceGraph& g, const Workspace& w, const double* r, double r_cut, hipStream_t s,
+                            LaunchTimer* tm) const override {
         if (g.N == 0) return;
         TimerScope ts(tm, "source_gather", s);
-        k_source_gather<C, S::NH, false><<<g.N, C, 0, s>>>(g.soff, g.sedges, w.Wsrc, w.H1_adj);
+        k_source_gather<C, S::NH, false><<<g.N, C, 0, s>>>(g.soff, g.sedges, w.Wsrc, r, r_cut, w.H1_adj);
         SMX_LAUNCH_CHECK("source_gather");
     }
 
-    void source_adjoint_tile(const DeviceGraph& g, const TileView& t, const Workspace& w, hipStream_t s,
-                             LaunchTimer* tm) const override {
+    void source_adjoint_tile(const DeviceGraph& g, const TileView& t, const Workspace& w, const double* r,
+                             double r_cut, hipStream_t s, LaunchTimer* tm) const override {
         if (t.touched_count == 0) return;
         TimerScope ts(tm, "source_gather", s);
         k_tile_source_adjoint<C, S::NH><<<t.touched_count, C, 0, s>>>(t.touched, t.e0, t.e0 + t.ne, g.soff, g.sedges,
-                                                                     w.Wsrc, w.H1_adj);
+                                                                     w.Wsrc, r, r_cut, w.H1_adj);
         SMX_LAUNCH_CHECK("tile_source_adjoint");
     }
 

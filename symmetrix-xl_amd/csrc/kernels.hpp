@@ -163,12 +163,13 @@ struct KernelSet {
     // direct adjoint, per-edge source terms, directed forces (assigned)
     virtual void layer2(const DeviceModel& m, const DeviceGraph& g, const TileView& t, const Workspace& w,
                         hipStream_t s, LaunchTimer* tm) const = 0;
-    // H1_adj = source sums of W over the whole graph (one tile)
-    virtual void source_adjoint_all(const DeviceGraph& g, const Workspace& w, hipStream_t s,
-                                    LaunchTimer* tm) const = 0;
-    // H1_adj[s] += source sums of W over one tile's edges
-    virtual void source_adjoint_tile(const DeviceGraph& g, const TileView& t, const Workspace& w, hipStream_t s,
-                                     LaunchTimer* tm) const = 0;
+    // H1_adj = source sums of W over the whole graph (one tile); r: edge
+    // lengths indexed like W (edges with r >= r_cut have no W row)
+    virtual void source_adjoint_all(const DeviceGraph& g, const Workspace& w, const double* r, double r_cut,
+                                    hipStream_t s, LaunchTimer* tm) const = 0;
+    // H1_adj[s] += source sums of W over one tile's edges (r of the tile)
+    virtual void source_adjoint_tile(const DeviceGraph& g, const TileView& t, const Workspace& w, const double* r,
+                                     double r_cut, hipStream_t s, LaunchTimer* tm) const = 0;
     // H1 reverse, M0 reverse, A0 reverse, R0 reverse (directed forces added
     // to, or assigned to, the tile's buffer)
     virtual void layer1_reverse(const DeviceModel& m, const DeviceGraph& g, const TileView& t, const Workspace& w,

@@ -167,8 +167,8 @@ int32_t reverse_launch(const SymmetrixJitHipR1SourceArgsV1* s, const SymmetrixJi
     k_r1_reverse<C, LMAX, LMAXH, kAll, true, PluginEdges<S::NY>><<<static_cast<unsigned>(N), C, 0, hs>>>(
         0, 0, offsets, e->neigh_indices, edges, static_cast<const float*>(e->neighbor_features), st->cg,
         static_cast<const float*>(e->output_adjoint), W, e->directed_forces);
-    k_source_gather<C, S::NH, true><<<static_cast<unsigned>(N), C, 0, hs>>>(s->source_offsets, s->source_edges, W,
-                                                                           static_cast<float*>(s->source_adjoint));
+    k_source_gather<C, S::NH, true><<<static_cast<unsigned>(N), C, 0, hs>>>(
+        s->source_offsets, s->source_edges, W, e->radius, e->cutoff, static_cast<float*>(s->source_adjoint));
     err = hipPeekAtLastError();
     const hipError_t ferr = hipFreeAsync(ws, hs);
     return static_cast<int32_t>(err != hipSuccess ? err : ferr);
