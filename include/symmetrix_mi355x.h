@@ -136,7 +136,11 @@ SMX_API int32_t smx_compute_prepared_factorized(SmxEvaluator* ev, uint64_t gener
  * pybind _compute_prepared_factorized_positions, mace_kokkos.cpp:1828) */
 SMX_API int32_t smx_compute_prepared_factorized_positions(SmxEvaluator* ev, uint64_t generation,
                                                           const double* positions);
-/* same with positions[N][3] already in device memory */
+/* same with positions[N][3] already in device memory.  Returns once the
+ * edge geometry has been checked (an invalid edge raises, as the reference's
+ * streamed-positions path does, mace_kokkos_factorized_lifecycle.cpp:790-794);
+ * the model kernels stay queued on the evaluator stream, so device outputs
+ * are ready for work ordered on that stream or after smx_synchronize. */
 SMX_API int32_t smx_compute_prepared_factorized_positions_device(SmxEvaluator* ev, uint64_t generation,
                                                                  const double* positions_device);
 /* compute_node_energies_forces with execution_graph_generation == 0

@@ -249,6 +249,12 @@ struct Evaluator {
     Workspace ws;
     bool evaluated = false;
     bool xyz_host = false;  // this call's edge vectors came from the caller
+    // The invalid-edge count of a positions call is copied to pinned host
+    // memory right after the edge geometry, so the call can raise without
+    // waiting for the model kernels queued behind it.
+    int* h_invalid = nullptr;
+    hipEvent_t geometry_done = nullptr;
+    bool geometry_flag_pending = false;
     int stress_blocks = 256;
 
     std::unique_ptr<EventTimer> timer;
@@ -269,6 +275,8 @@ struct Evaluator {
             throw std::domain_error("no kernel set is compiled for " + std::to_string(hm.C) + " channels, l_max " +
                                     std::to_string(hm.l_max) + ", L_max " + std::to_string(hm.L_max));
         SMX_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
+        SMX_HIP(hipHostMalloc(reinterpret_cast<void**>(&h_invalid), sizeof(int), hipHostMallocDefault));
+        SMX_HIP(hipEventCreateWithFlags(&geometry_done, hipEventDisableTiming));
         upload_model();
         define_groups();
         SMX_HIP(hipStreamSynchronize(stream));
@@ -280,6 +288,8 @@ struct Evaluator {
             timer.reset();
             (void)hipStreamDestroy(stream);
         }
+        if (geometry_done) (void)hipEventDestroy(geometry_done);
+        if (h_invalid) (void)hipHostFree(h_invalid);
     }
 
     template <class T>
@@ -727,6 +737,14 @@ struct Evaluator {
         (void)positions;
     }
 
+    // queue the D2H copy of the invalid-edge count (positions calls only)
+    void post_geometry_flag() {
+        if (xyz_host) return;
+        SMX_HIP(hipMemcpyAsync(h_invalid, d_invalid.as<int>(), sizeof(int), hipMemcpyDeviceToHost, stream));
+        SMX_HIP(hipEventRecord(geometry_done, stream));
+        geometry_flag_pending = true;
+    }
+
     void zero_a1_if_needed() {
         if (std::find(hm.num_e.begin(), hm.num_e.end(), 0) != hm.num_e.end())
             launch_fill_zero(ws.A1, static_cast<std::size_t>(std::max(max_tile_nr, 1)) * hm.num_lm * hm.C, stream);
@@ -739,6 +757,7 @@ struct Evaluator {
         if (!tiled) {
             const TileView& t = tiles[0];
             tile_geometry(t, positions);
+            post_geometry_flag();
             ks->layer1_forward(dm, g, t, ws, true, stream, tm);
             ks->layer2(dm, g, t, ws, stream, tm);
             ks->source_adjoint_all(g, ws, tile_r(t), hm.r_cut, stream, tm);
@@ -754,6 +773,7 @@ struct Evaluator {
             tile_geometry(t, positions);
             ks->layer1_forward(dm, g, t, ws, true, stream, tm);
         }
+        post_geometry_flag();
         for (const auto& t : tiles) {
             tile_geometry(t, positions);
             ks->layer2(dm, g, t, ws, stream, tm);
@@ -779,15 +799,28 @@ struct Evaluator {
         if (tm) tm->end("tile_reductions", stream);
     }
 
-    void finish_call(bool check_invalid) {
-        int invalid = 0;
-        if (check_invalid)
-            SMX_HIP(hipMemcpyAsync(&invalid, d_invalid.as<int>(), sizeof(int), hipMemcpyDeviceToHost, stream));
+    // drain the stream; launch timings recorded so far become readable
+    void sync() {
         SMX_HIP(hipStreamSynchronize(stream));
         if (timer) timer->collect();
-        if (invalid > 0)
-            throw std::runtime_error("prepared geometry produced " + std::to_string(invalid) +
-                                     " invalid (zero-length or non-finite) edges");
+    }
+
+    // wait: synchronise the stream before returning (host inputs); else the
+    // call returns once the geometry check is readable and the model kernels
+    // stay queued on the evaluator stream (device outputs are stream-ordered)
+    void finish_call(bool wait) {
+        int invalid = 0;
+        if (geometry_flag_pending) {
+            geometry_flag_pending = false;
+            SMX_HIP(hipEventSynchronize(geometry_done));
+            invalid = *h_invalid;
+        }
+        if (wait) sync();
+        if (invalid > 0) {
+            evaluated = false;
+            throw std::invalid_argument("positions produced an invalid edge geometry (" + std::to_string(invalid) +
+                                        " zero-length or non-finite edges)");
+        }
     }
 
     void compute_positions(std::uint64_t token, const double* positions, bool on_device) {
@@ -809,7 +842,7 @@ struct Evaluator {
         launch_displacements(N, cell, inv_cell, d_ref_positions.as<double>(), pos, d_disp.as<double>(), stream);
         if (timer) timer->end("displacements", stream);
         evaluate(pos);
-        finish_call(true);
+        finish_call(!on_device);
     }
 
     void compute_xyz(std::uint64_t token, const double* xyz, const double* r) {
@@ -828,7 +861,7 @@ struct Evaluator {
             SMX_HIP(hipMemcpyAsync(d_r.as<double>(), r, E * sizeof(double), hipMemcpyHostToDevice, stream));
         }
         evaluate(nullptr);
-        finish_call(false);
+        finish_call(true);
     }
 
     void update_cell(std::uint64_t token, const double* cell_, const double* inv_) {
@@ -1215,7 +1248,7 @@ int32_t smx_device_outputs(SmxEvaluator* ev, SmxDeviceOutputs* out) {
 }
 
 int32_t smx_synchronize(SmxEvaluator* ev) {
-    return guarded([&] { SMX_HIP(hipStreamSynchronize(E(ev).stream)); });
+    return guarded([&] { E(ev).sync(); });
 }
 
 int32_t smx_debug_stage(SmxEvaluator* ev, const char* name, float* out, int64_t capacity, int64_t* count) {
@@ -1245,7 +1278,10 @@ int32_t smx_set_kernel_timing_filter(SmxEvaluator* ev, const char* names) {
 int32_t smx_kernel_timing_reset(SmxEvaluator* ev) {
     return guarded([&] {
         auto& e = E(ev);
-        if (e.timer) e.timer->reset();
+        if (e.timer) {
+            e.sync();
+            e.timer->reset();
+        }
     });
 }
 
@@ -1257,6 +1293,7 @@ int32_t smx_kernel_timing(SmxEvaluator* ev, int32_t index, const char** name, do
         *total_ms = 0.0;
         *launches = 0;
         if (e.timer) {
+            e.sync();
             std::int64_t n = 0;
             if (e.timer->get(index, name, total_ms, &n)) *launches = n;
         }

@@ -273,3 +273,78 @@ def test_table_driven_polynomials_match_unrolled(tiny_model_path, tmp_path):
     assert "polynomials=table" in ev_b.execution_plan
     np.testing.assert_allclose(e_b, e_a, rtol=1e-6, atol=1e-9)
     np.testing.assert_allclose(f_b, f_a, rtol=1e-5, atol=1e-7)
+
+
+def _device_copy(a):
+    """Device copy of a numpy array through the HIP runtime the library
+    uses (hipMalloc + hipMemcpy); returns (pointer, free)."""
+    import ctypes
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    hip.hipFree.argtypes = [ctypes.c_void_p]
+    a = np.ascontiguousarray(a, dtype=np.float64)
+    p = ctypes.c_void_p()
+    assert hip.hipMalloc(ctypes.byref(p), ctypes.c_size_t(a.nbytes)) == 0
+    assert hip.hipMemcpy(p, a.ctypes.data_as(ctypes.c_void_p), ctypes.c_size_t(a.nbytes), 1) == 0
+    return p.value, lambda: hip.hipFree(p)
+
+
+def test_device_positions_call_matches_host_positions(tiny_model_path):
+    """The device-positions call returns once the geometry is checked and
+    leaves the model kernels queued on the evaluator stream; outputs read
+    through the stream-ordered reductions equal the host-positions call's."""
+    from symmetrix._native import check, lib
+    from symmetrix.mace_kokkos import MACEKokkosFloat
+    s = _system("tiny")
+    ev = MACEKokkosFloat(tiny_model_path)
+    types = np.array([{8: 0, 22: 1, 38: 2}[int(z)] for z in s["numbers"]], np.int32)
+    cell = np.asarray(s["cell"], float)
+    vol = abs(np.linalg.det(cell))
+    e0, f0, s0 = _run(ev, s, types)
+    gen = ev._prepare_periodic_factorized_graph(types, s["positions"], cell, np.linalg.inv(cell),
+                                                ev.r_cut + 0.5)["generation"]
+    d_pos, free = _device_copy(s["positions"])
+    try:
+        for _ in range(2):
+            ev._compute_prepared_factorized_positions_device(gen, d_pos)
+            check(lib.smx_reduce_prepared_node_forces(ev._h, gen, None))
+            check(lib.smx_reduce_prepared_stress(ev._h, gen, vol, None))
+        ev.synchronize()
+    finally:
+        free()
+    f1 = ev._reduce_atom_forces(len(types), None, None, gen)
+    s1 = ev._reduce_stress(vol, None, gen)
+    assert ev.node_energies.tobytes() == e0.tobytes()
+    assert f1.tobytes() == f0.tobytes()
+    assert s1.tobytes() == s0.tobytes()
+
+
+def test_invalid_positions_raise_and_next_call_recovers(tiny_model_path):
+    """A non-finite position is refused on the host for host positions
+    (mace_kokkos_factorized_lifecycle.cpp:686-690); on the device it makes
+    every edge of that atom invalid and the call raises after the geometry
+    (mace_kokkos_factorized_lifecycle.cpp:766-794).  A following valid call
+    gives the same results as before."""
+    from symmetrix.mace_kokkos import MACEKokkosFloat
+    s = _system("tiny")
+    ev = MACEKokkosFloat(tiny_model_path)
+    types = np.array([{8: 0, 22: 1, 38: 2}[int(z)] for z in s["numbers"]], np.int32)
+    cell = np.asarray(s["cell"], float)
+    g = ev._prepare_periodic_factorized_graph(types, s["positions"], cell, np.linalg.inv(cell), ev.r_cut + 0.5)
+    gen = g["generation"]
+    ev._compute_prepared_factorized_positions(gen, s["positions"])
+    e0 = ev.node_energies.copy()
+    bad = np.array(s["positions"], dtype=np.float64)
+    bad[1, 0] = np.nan
+    with pytest.raises(ValueError, match="finite"):
+        ev._compute_prepared_factorized_positions(gen, bad)
+    d_bad, free = _device_copy(bad)
+    try:
+        with pytest.raises(ValueError, match="invalid edge geometry"):
+            ev._compute_prepared_factorized_positions_device(gen, d_bad)
+        ev.synchronize()
+    finally:
+        free()
+    ev._compute_prepared_factorized_positions(gen, s["positions"])
+    assert ev.node_energies.tobytes() == e0.tobytes()
