@@ -24,6 +24,13 @@
 //   * polynomial semantics: multivariate_polynomial.cpp:11-103 (a repeated
 //     monomial keeps its first coefficient)
 //   * force and stress reductions: mace_kokkos_evaluate.cpp:49-128, 189-291
+//   * density scaling of A0 and A1 as the Kokkos evaluator computes it (FP64
+//     splines and sums): mace_kokkos_first_interaction.cpp:1335-1419
+//     (A0 /= 1 + sum_j f0(r_ij)), :1421-1531 (reverse: edge forces
+//     (dA0.A0)/s * f0'(r) r^, A0_adj /= s); mace_kokkos_second_interaction.cpp:
+//     1310-1490 (A1 *= float(1/s)), :1493-1720 (reverse, A1_adj *= float(1/s));
+//     tanh-square networks compact_radial.cpp:17-24,181-193,295-303; FP64
+//     splines radial_function_set_kokkos.cpp:14-45, .hpp:48-146
 //
 // Y: the reference evaluates sphericart's real harmonics at the shuffled
 // direction (z, x, y) and scales by sqrt(4 pi) rounding once from double
@@ -60,6 +67,7 @@ struct Network {
     std::vector<int> shape;
     std::vector<std::vector<double>> weights;  // [layer][out*in]
     double scale = 1.0;
+    bool tanh_square = false;  // postprocess "tanh-square": tanh(v^2)
 };
 
 static Network parse_network(const Value& v) {
@@ -68,6 +76,10 @@ static Network parse_network(const Value& v) {
     const Value& w = v.at("weights");
     for (std::size_t i = 0; i < w.size(); ++i) n.weights.push_back(w.at(i).as_doubles());
     n.scale = v.at("activation_scale").as_number();
+    const std::string post = v.get_string("postprocess", "");
+    if (!post.empty() && post != "tanh-square")
+        throw std::invalid_argument("radial network has unsupported postprocessing");
+    n.tanh_square = post == "tanh-square";
     if (v.at("activation").as_string() != "silu")
         throw std::invalid_argument("radial network must use SiLU");
     if (n.shape.size() < 2 || n.weights.size() != n.shape.size() - 1)
@@ -100,8 +112,8 @@ struct RadialModel {
     double grid_min = 0, h = 0, r_max = 0, prefactor = 0;
     int points = 0, p = 0;
     std::vector<double> bessel;
-    Network R0, R1;
-    bool has_R1 = false;
+    Network R0, R1, A0, A1;
+    bool has_R1 = false, has_A0 = false, has_A1 = false;
 
     void load(const Value& def, double r_cut) {
         grid_min = def.at("spline_grid_min").as_number();
@@ -126,8 +138,19 @@ struct RadialModel {
         const Value& nets = def.at("networks");
         R0 = parse_network(nets.at("R0"));
         if (nets.contains("R1")) { R1 = parse_network(nets.at("R1")); has_R1 = true; }
-        if (nets.contains("A0") || nets.contains("A1"))
-            throw std::invalid_argument("density-scaled (A0/A1) networks are not supported");
+        if (R0.tanh_square || (has_R1 && R1.tanh_square))
+            throw std::invalid_argument("R0/R1 networks cannot use postprocessing");
+        // density networks: Bessel features in, one output, tanh-square
+        auto density = [&](const char* name, Network& net, bool& has) {
+            if (!nets.contains(name)) return;
+            net = parse_network(nets.at(name));
+            has = true;
+            if (net.shape.front() != static_cast<int>(bessel.size()) || net.shape.back() != 1 || !net.tanh_square)
+                throw std::invalid_argument(std::string("compact radial ") + name +
+                                            " network has an invalid shape or postprocessing");
+        };
+        density("A0", A0, has_A0);
+        density("A1", A1, has_A1);
     }
 
     // compact_radial.cpp:227-267 (no distance transform)
@@ -187,7 +210,7 @@ struct RadialModel {
         std::vector<double> out(nout);
         for (int node = 0; node < points; ++node) {
             mlp_forward(net, f.data() + static_cast<std::size_t>(node) * bessel.size(), out.data());
-            for (int o = 0; o < nout; ++o) values[o][node] = out[o];
+            for (int o = 0; o < nout; ++o) values[o][node] = net.tanh_square ? std::tanh(out[o] * out[o]) : out[o];
         }
         derivs.resize(nout);
         for (int o = 0; o < nout; ++o) derivs[o] = spline_derivatives(values[o]);
@@ -389,6 +412,10 @@ struct Mace {
     // active radial tables
     std::vector<int> active_types, type_to_active;
     std::vector<std::shared_ptr<SplineSet<P>>> spl0, spl1;
+    // density scaling: FP64 splines of the A0/A1 networks (one function)
+    bool A0_scaled = false, A1_scaled = false;
+    std::shared_ptr<SplineSet<double>> dens0, dens1;
+    std::vector<double> A0_scale, A1_scale;  // per node: 1 + sum_j f(r_ij)
 
     // state of the last evaluation (exposed for stage-level debugging)
     std::vector<P> Y, Ygrad, A0, M0, M0_grad, H1, xaff, Phi1, A1, M1, M1_grad, A1_adj, dPhi1,
@@ -401,6 +428,8 @@ struct Mace {
     // of the R0 reverse alone
     std::vector<P> Phi0, Phi0_adj;
     std::vector<double> node_forces_r0;
+    // directed-force terms of the A0/A1 density scales
+    std::vector<double> density_forces;
 
     static P cast(double v) {
         if (!std::isfinite(v) || std::abs(v) > static_cast<double>(std::numeric_limits<P>::max()))
@@ -421,8 +450,7 @@ struct Mace {
             throw std::invalid_argument("only h1_affine_mode 'm0_composite' is supported");
         if (j.get_string("radial_representation", "") != "compact")
             throw std::invalid_argument("only the compact radial representation is supported");
-        if (j.get_bool("has_zbl", false) || j.get_bool("A0_scaled", false) ||
-            j.get_bool("A1_scaled", false) || j.get_bool("has_field_coupling", false) ||
+        if (j.get_bool("has_zbl", false) || j.get_bool("has_field_coupling", false) ||
             j.get_bool("first_interaction_residual", false) || j.get_bool("single_layer_readout", false))
             throw std::invalid_argument("model features outside the supported MACE path");
         num_elements = j.at("num_elements").as_int();
@@ -436,6 +464,11 @@ struct Mace {
         atomic_numbers = j.at("atomic_numbers").as_ints();
         atomic_energies = j.at("atomic_energies").as_doubles();
         radial.load(j.at("compact_radial"), r_cut);
+        // mace_kokkos_model.cpp:200,215-216,1109,1122-1123
+        A0_scaled = j.at("A0_scaled").as_bool();
+        A1_scaled = j.get_bool("A1_scaled", false);
+        if (A0_scaled != radial.has_A0) throw std::invalid_argument("compact radial A0 network does not match A0_scaled");
+        if (A1_scaled != radial.has_A1) throw std::invalid_argument("compact radial A1 network does not match A1_scaled");
         H0 = castv(j.at("H0_weights").as_doubles());
         const Value& a0 = j.at("A0_weights");
         A0_w.resize(num_elements);
@@ -550,6 +583,20 @@ struct Mace {
                 spl0.push_back(s0);
                 spl1.push_back(s1);
             }
+        // RadialFunctionSetKokkos<double>(h, values, derivs, x0): FP64
+        // coefficients and evaluation (mace_kokkos_factorized_lifecycle.cpp:4084-4091)
+        dens0.reset();
+        dens1.reset();
+        if (A0_scaled) {
+            std::vector<std::vector<double>> v, d;
+            radial.tabulate(radial.A0, v, d);
+            dens0 = std::make_shared<SplineSet<double>>(radial.h, v, d, radial.grid_min);
+        }
+        if (A1_scaled) {
+            std::vector<std::vector<double>> v, d;
+            radial.tabulate(radial.A1, v, d);
+            dens1 = std::make_shared<SplineSet<double>>(radial.h, v, d, radial.grid_min);
+        }
         type_to_active.assign(num_elements, -1);
         for (int a = 0; a < na; ++a) type_to_active[req[a]] = a;
         active_types = req;
@@ -566,6 +613,27 @@ struct Mace {
         int acc = 0;
         for (int i = 0; i < p; ++i) acc += (2 * Phi1_l1[i] + 1) * (2 * Phi1_l2[i] + 1);
         return acc;
+    }
+
+    // f(r) and f'(r) of a one-function FP64 density spline
+    // (radial_function_set_kokkos.hpp:48-62,104-146)
+    static void density_eval(const SplineSet<double>& sp, double r, double& f, double& d) {
+        const auto pt = sp.point(r);
+        const double* c = sp.coefficients(pt);
+        f = c[0] + c[1] * pt.x + c[2] * pt.xx + c[3] * pt.xxx;
+        d = c[1] + c[2] * (2.0 * pt.x) + c[3] * (3.0 * pt.xx);
+    }
+
+    // 1 + sum over every CSR edge of i (skin edges included, r clamped to the
+    // cutoff) of f(r): the Kokkos team reduction then += 1.0
+    static double density_factor(const SplineSet<double>& sp, long long e0, long long e1, const double* r) {
+        double s = 0.0;
+        for (long long e = e0; e < e1; ++e) {
+            double f, d;
+            density_eval(sp, r[e], f, d);
+            s += f;
+        }
+        return s + 1.0;
     }
 
     void evaluate(int n, const int* types, const int* num_neigh, const int* neigh, const int* neigh_types,
@@ -593,6 +661,8 @@ struct Mace {
         }
 
         // ---- A0 (mace.cpp:1356-1403)
+        A0_scale.assign(A0_scaled ? n : 0, 1.0);
+        A1_scale.assign(A1_scaled ? n : 0, 1.0);
         A0.assign(static_cast<std::size_t>(n) * nY * Cs, P(0));
         Phi0.assign(static_cast<std::size_t>(n) * nY * Cs, P(0));
 #pragma omp parallel for schedule(dynamic, 16)
@@ -630,6 +700,14 @@ struct Mace {
                         for (int k = 0; k < C; ++k) dst[k] += a * wr[k];
                     }
                 }
+            }
+            // A0 /= 1 + sum_j f0(r_ij), the division in FP64
+            // (mace_kokkos_first_interaction.cpp:1383-1416)
+            if (A0_scaled) {
+                const double sc = density_factor(*dens0, off[i], off[i + 1], r);
+                A0_scale[i] = sc;
+                P* a = &A0[static_cast<std::size_t>(i) * nY * Cs];
+                for (std::size_t v = 0; v < nY * Cs; ++v) a[v] = static_cast<P>(static_cast<double>(a[v]) / sc);
             }
         }
 
@@ -731,6 +809,15 @@ struct Mace {
                     }
                 }
             }
+            // A1 *= Precision(1 / (1 + sum_j f1(r_ij)))
+            // (mace_kokkos_second_interaction.cpp:1449-1488)
+            if (A1_scaled) {
+                const double sc = density_factor(*dens1, off[i], off[i + 1], r);
+                A1_scale[i] = sc;
+                const P inv = static_cast<P>(1.0 / sc);
+                P* a = &A1[static_cast<std::size_t>(i) * nY * Cs];
+                for (std::size_t v = 0; v < nY * Cs; ++v) a[v] *= inv;
+            }
         }
 
         // ---- M1, H2, readouts, reverse H2 / M1 (mace.cpp:2461-2657)
@@ -791,6 +878,31 @@ struct Mace {
                 for (int v = 0; v < nY; ++v)
                     A1_adj[(static_cast<std::size_t>(i) * nY + v) * Cs + in] =
                         M1_grad[(static_cast<std::size_t>(i) * nY + v) * Cs + in] * m1adj;
+            }
+        }
+
+        // ---- reverse of the A1 density scale (mace_kokkos_second_interaction.cpp:
+        // 1636-1719): dot = sum A1_adj*A1 (FP32 products, FP64 sum); edge
+        // forces += (dot/s) f1'(r) (xyz/r); A1_adj *= Precision(1/s).  The
+        // edge terms are kept apart and added to the directed forces after the
+        // R1 reverse (FP64 sums in another order than the reference's).
+        density_forces.assign(static_cast<std::size_t>(E) * 3, 0.0);
+        if (A1_scaled) {
+#pragma omp parallel for schedule(static)
+            for (int i = 0; i < n; ++i) {
+                const double sc = A1_scale[i];
+                P* adj = &A1_adj[static_cast<std::size_t>(i) * nY * Cs];
+                const P* a = &A1[static_cast<std::size_t>(i) * nY * Cs];
+                double dot = 0.0;
+                for (std::size_t v = 0; v < nY * Cs; ++v) dot += static_cast<double>(adj[v] * a[v]);
+                for (long long e = off[i]; e < off[i + 1]; ++e) {
+                    double f, d;
+                    density_eval(*dens1, r[e], f, d);
+                    const double scale = dot / sc * d;
+                    for (int c = 0; c < 3; ++c) density_forces[3 * e + c] += scale * (xyz[3 * e + c] / r[e]);
+                }
+                const P inv = static_cast<P>(1.0 / sc);
+                for (std::size_t v = 0; v < nY * Cs; ++v) adj[v] *= inv;
             }
         }
 
@@ -944,6 +1056,26 @@ struct Mace {
                 }
             }
 
+        // ---- reverse of the A0 density scale (mace_kokkos_first_interaction.cpp:
+        // 1508-1528): dot = sum A0_adj*A0; edge forces += dot/s*f0'(r)*xyz/r;
+        // A0_adj /= s in FP64
+        if (A0_scaled) {
+#pragma omp parallel for schedule(static)
+            for (int i = 0; i < n; ++i) {
+                const double sc = A0_scale[i];
+                P* adj = &A0_adj[static_cast<std::size_t>(i) * nY * Cs];
+                const P* a = &A0[static_cast<std::size_t>(i) * nY * Cs];
+                double dot = 0.0;
+                for (std::size_t v = 0; v < nY * Cs; ++v) dot += static_cast<double>(adj[v] * a[v]);
+                for (long long e = off[i]; e < off[i + 1]; ++e) {
+                    double f, d;
+                    density_eval(*dens0, r[e], f, d);
+                    for (int c = 0; c < 3; ++c) density_forces[3 * e + c] += dot / sc * d * xyz[3 * e + c] / r[e];
+                }
+                for (std::size_t v = 0; v < nY * Cs; ++v) adj[v] = static_cast<P>(static_cast<double>(adj[v]) / sc);
+            }
+        }
+
         // ---- reverse A0 (mace.cpp:1486-1560)
         Phi0_adj.assign(static_cast<std::size_t>(n) * nY * Cs, P(0));
         node_forces_r0.assign(static_cast<std::size_t>(E) * 3, 0.0);
@@ -997,6 +1129,8 @@ struct Mace {
             }
             std::copy(padj.begin(), padj.end(), Phi0_adj.begin() + static_cast<std::size_t>(i) * nY * Cs);
         }
+        if (A0_scaled || A1_scaled)
+            for (long long v = 0; v < 3 * E; ++v) node_forces[v] += density_forces[v];
     }
 };
 
@@ -1209,7 +1343,8 @@ int oracle_evaluate(void* hv, int n, const int* types, const int* num_neigh, con
 
 // Stage buffers of the last evaluation, as float64: name in {Y, Ygrad, A0, M0,
 // M0_grad, H1, Phi1, A1, M1, H2, H2_adj, A1_adj, dPhi1, H1_adj, M0_adj, A0_adj,
-// node_forces_r1, Phi0, Phi0_adj, node_forces_r0}.
+// node_forces_r1, Phi0, Phi0_adj, node_forces_r0, A0_scale, A1_scale,
+// density_forces}.
 long long oracle_stage(void* hv, const char* name, double* out, long long capacity) {
     auto* h = static_cast<OracleHandle*>(hv);
     auto get = [&](auto& m) -> long long {
@@ -1239,19 +1374,25 @@ long long oracle_stage(void* hv, const char* name, double* out, long long capaci
         if (s == "Phi0") return emit(m.Phi0);
         if (s == "Phi0_adj") return emit(m.Phi0_adj);
         if (s == "node_forces_r0") return emit(m.node_forces_r0);
+        if (s == "A0_scale") return emit(m.A0_scale);
+        if (s == "A1_scale") return emit(m.A1_scale);
+        if (s == "density_forces") return emit(m.density_forces);
         return -1;
     };
     return h->fp64 ? get(*h->d) : get(*h->f);
 }
 
 // Radial nodal tables of the model on its spline grid (FP64):
-// which 0 = R0, 1 = R1; values/derivs [function][point].
+// which 0 = R0, 1 = R1, 2 = A0 density, 3 = A1 density; values/derivs
+// [function][point].
 int oracle_radial_tables(void* hv, int which, double* values, double* derivs, int* shape) {
     return guarded([&]() -> int {
         auto* h = static_cast<OracleHandle*>(hv);
         const RadialModel& rm = h->fp64 ? h->d->radial : h->f->radial;
+        if ((which == 2 && !rm.has_A0) || (which == 3 && !rm.has_A1) || which < 0 || which > 3)
+            throw std::invalid_argument("the model has no such radial network");
         std::vector<std::vector<double>> v, d;
-        rm.tabulate(which == 0 ? rm.R0 : rm.R1, v, d);
+        rm.tabulate(which == 0 ? rm.R0 : which == 1 ? rm.R1 : which == 2 ? rm.A0 : rm.A1, v, d);
         shape[0] = static_cast<int>(v.size());
         shape[1] = rm.points;
         if (values)

@@ -122,7 +122,8 @@ class OracleModel:
 
     def radial_tables(self, which):
         shape = np.zeros(2, dtype=np.int32)
-        lib().oracle_radial_tables(self._h, which, None, None, shape)
+        if lib().oracle_radial_tables(self._h, which, None, None, shape) != 0:
+            raise ValueError(_err())
         v = np.zeros(int(shape[0]) * int(shape[1]))
         d = np.zeros_like(v)
         if lib().oracle_radial_tables(self._h, which, v.ctypes.data, d.ctypes.data, shape) != 0:

@@ -243,7 +243,7 @@ struct Evaluator {
     // per call
     DevBuf d_xyz, d_r, d_invalid;
     DevBuf w_erec, w_Phi0, w_A0, w_M0, w_Phi1, w_A1, w_A1_adj, w_M1, w_dPhi1, w_Wsrc, w_M0_adj, w_A0_adj, w_Phi0_adj,
-        w_node_forces;
+        w_node_forces, w_density;
     DevBuf g_H1, g_H1_adj, g_xaff, g_direct, d_node_energies, d_atom_forces, d_virial, d_stress, d_stress_partial,
         d_total;
     Workspace ws;
@@ -312,6 +312,12 @@ struct Evaluator {
         dm.intervals = hm.spline_points - 1;
         dm.x0 = hm.grid_min_f;
         dm.h = hm.h_f;
+        dm.x0_f64 = hm.grid_min;
+        dm.h_f64 = hm.h;
+        dm.A0_scaled = hm.A0_scaled;
+        dm.A1_scaled = hm.A1_scaled;
+        if (hm.A0_scaled) dm.dens0 = put(hm.A0_density);
+        if (hm.A1_scaled) dm.dens1 = put(hm.A1_density);
         dm.R0c = reinterpret_cast<const float4*>(put(hm.R0_coef));
         dm.R1c = reinterpret_cast<const float4*>(put(hm.R1_coef));
         dm.H0 = put(hm.H0);
@@ -573,6 +579,13 @@ struct Evaluator {
         ws.A0_adj = f(w_A0_adj, tn * NY * C);
         ws.Phi0_adj = f(w_Phi0_adj, tn * NY * C);
         ws.node_forces = static_cast<double*>(w_node_forces.ensure(te * 3 * sizeof(double)));
+        if (hm.A0_scaled || hm.A1_scaled) {
+            double* d = static_cast<double*>(w_density.ensure(4 * tn * sizeof(double)));
+            ws.dens_s0 = d;
+            ws.dens_s1 = d + tn;
+            ws.dens_dot0 = d + 2 * tn;
+            ws.dens_dot1 = d + 3 * tn;
+        }
         ws.H1 = f(g_H1, n * NH * C);
         ws.H1_adj = f(g_H1_adj, n * NH * C);
         ws.xaff = f(g_xaff, n * C);
@@ -752,6 +765,10 @@ struct Evaluator {
 
     void evaluate(const double* positions) {
         const DeviceGraph g = view();
+        for (auto& t : tiles) {
+            t.r = tile_r(t);
+            t.xyz = tile_xyz(t);
+        }
         LaunchTimer* tm = timer.get();
         zero_a1_if_needed();
         if (!tiled) {

@@ -872,6 +872,11 @@ struct KernelSetImpl final : KernelSet {
             TimerScope ts(tm, "a0_linear", s);
             launch_node_gemm(t.a0, m.A0_w, w.Phi0, w.A0, s);
         }
+        if (m.A0_scaled) {
+            TimerScope ts(tm, "a0_density_scale", s);
+            launch_density_factors(m, g, t, w.dens_s0, nullptr, s);
+            launch_density_scale(t.nr, S::NY * C, w.dens_s0, true, w.A0, s);
+        }
         if (!through_h1) return;
         {
             TimerScope ts(tm, "m0_forward", s);
@@ -905,6 +910,11 @@ struct KernelSetImpl final : KernelSet {
             TimerScope ts(tm, "a1_linear", s);
             launch_node_gemm(t.a1f, m.A1_w, w.Phi1, w.A1, s);
         }
+        if (m.A1_scaled) {
+            TimerScope ts(tm, "a1_density_scale", s);
+            launch_density_factors(m, g, t, nullptr, w.dens_s1, s);
+            launch_density_scale(t.nr, S::NY * C, w.dens_s1, false, w.A1, s);
+        }
         {
             TimerScope ts(tm, "readout", s);
             k_m1<C, S::NY, M1TAB><<<t.nr, C, 0, s>>>(t.r0, g.node_types, w.A1, m.m1_terms, m.T1, m.m1_coef, w.M1,
@@ -914,6 +924,10 @@ struct KernelSetImpl final : KernelSet {
                 t.r0, t.batches, t.node_list, g.node_types, w.M1, w.xaff, m.H2_T, m.H2_Tt, m.H2_M1, m.H2_M1t, m.q,
                 m.W1r, m.W2r, m.hidden, m.readout_scale, m.E0, w.node_energies, w.direct, w.A1_adj);
             SMX_LAUNCH_CHECK("readout");
+        }
+        if (m.A1_scaled) {
+            TimerScope ts(tm, "a1_density_reverse", s);
+            launch_density_adjoint(t.nr, S::NY * C, w.A1, w.dens_s1, false, w.A1_adj, w.dens_dot1, s);
         }
         {
             TimerScope ts(tm, "a1_linear_reverse", s);
@@ -928,6 +942,10 @@ struct KernelSetImpl final : KernelSet {
                     w.node_forces);
                 SMX_LAUNCH_CHECK("r1_reverse");
             });
+        }
+        if (m.A1_scaled) {
+            TimerScope ts(tm, "a1_density_forces", s);
+            launch_density_forces(m, g, t, nullptr, nullptr, w.dens_s1, w.dens_dot1, w.node_forces, s);
         }
     }
 
@@ -965,6 +983,10 @@ struct KernelSetImpl final : KernelSet {
                                                                 m.m0_terms, m.m0_toff, m.T0, m.m0_coef, w.A0_adj);
             SMX_LAUNCH_CHECK("m0_reverse");
         }
+        if (m.A0_scaled) {
+            TimerScope ts(tm, "a0_density_reverse", s);
+            launch_density_adjoint(t.nr, S::NY * C, w.A0, w.dens_s0, true, w.A0_adj, w.dens_dot0, s);
+        }
         {
             TimerScope ts(tm, "a0_linear_reverse", s);
             launch_node_gemm(t.a0, m.A0_wt, w.A0_adj, w.Phi0_adj, s);
@@ -978,6 +1000,10 @@ struct KernelSetImpl final : KernelSet {
                 k_r0_reverse<C, LMAX, false><<<t.nr, C, 0, s>>>(t.r0, t.e0, g.offsets, g.neigh_types, w.erec, m.R0c,
                                                                 m.H0, w.Phi0_adj, w.node_forces);
             SMX_LAUNCH_CHECK("r0_reverse");
+        }
+        if (m.A0_scaled) {
+            TimerScope ts(tm, "a0_density_forces", s);
+            launch_density_forces(m, g, t, w.dens_s0, w.dens_dot0, nullptr, nullptr, w.node_forces, s);
         }
     }
 };

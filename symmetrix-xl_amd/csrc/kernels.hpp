@@ -48,6 +48,12 @@ struct DeviceModel {
     int hidden = 0;
     double readout_scale = 1.0;
     const double* E0 = nullptr;
+    // density scaling (A0_scaled / A1_scaled): FP64 Hermite coefficients
+    // [intervals][4] of the one-output density networks on the radial grid
+    bool A0_scaled = false, A1_scaled = false;
+    const double* dens0 = nullptr;
+    const double* dens1 = nullptr;
+    double x0_f64 = 0.0, h_f64 = 0.0;
 };
 
 // One prepared graph on the device (receiver-major CSR + source transpose).
@@ -109,6 +115,10 @@ struct TileView {
     int num_batches = 0;
     const int* touched = nullptr;  // sources with an edge in the tile (ascending)
     int touched_count = 0;
+    // this call's FP64 edge lengths and vectors of the tile (indexed by
+    // edge - e0); set before each evaluation
+    const double* r = nullptr;
+    const double* xyz = nullptr;
 };
 
 // Workspace.  Tile-local arrays are indexed by receiver - r0 (or edge - e0);
@@ -129,6 +139,12 @@ struct Workspace {
     float* A0_adj = nullptr;    // [nr][NY][C]
     float* Phi0_adj = nullptr;  // [nr][NY][C]
     double* node_forces = nullptr;  // [ne][3]
+    // density scaling: factors s = 1 + sum_j f(r_ij) and adjoint dot
+    // products of A0 and A1, [nr] each
+    double* dens_s0 = nullptr;
+    double* dens_s1 = nullptr;
+    double* dens_dot0 = nullptr;
+    double* dens_dot1 = nullptr;
     // graph-wide
     float* H1 = nullptr;        // [N][NH][C]
     float* H1_adj = nullptr;    // [N][NH][C]
@@ -196,6 +212,19 @@ void geometry_records(int l_max, std::int64_t E, const double* xyz, const double
                       int intervals, float* erec, hipStream_t s);
 
 void launch_node_gemm(const GemmPlan& plan, const float* W, const float* in, float* out, hipStream_t s);
+
+// Density scaling (density.hip).  Factors s0/s1 (either may be null) of the
+// tile's receivers from t.r; rows [nr][row_len] scaled (divide: A /= s in
+// FP64, else A *= float(1/s)); the adjoint dot products dot = sum A_adj*A
+// and the scaled adjoint; the directed-force terms added to node_forces.
+void launch_density_factors(const DeviceModel& m, const DeviceGraph& g, const TileView& t, double* s0, double* s1,
+                            hipStream_t s);
+void launch_density_scale(int nr, int row_len, const double* s, bool divide, float* A, hipStream_t st);
+void launch_density_adjoint(int nr, int row_len, const float* A, const double* s, bool divide, float* adj,
+                            double* dot, hipStream_t st);
+void launch_density_forces(const DeviceModel& m, const DeviceGraph& g, const TileView& t, const double* s0,
+                           const double* dot0, const double* s1, const double* dot1, double* node_forces,
+                           hipStream_t s);
 
 // Reductions (FP64, deterministic order)
 void launch_atom_forces(int N, const int* offsets, const int* soff, const int* sedges, const double* node_forces,

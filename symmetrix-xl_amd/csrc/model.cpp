@@ -11,6 +11,9 @@
 //     zero-slope right)
 //   * Hermite coefficients cubic_spline_set.cpp:8-30, rounded to Precision
 //     before the coefficient formulas are applied in Precision
+//   * density networks (A0/A1 scaling): "tanh-square" postprocessing
+//     compact_radial.cpp:17-24,181-193,295-303, FP64 Hermite coefficients
+//     radial_function_set_kokkos.cpp:14-45 (RadialFunctionSetKokkos<double>)
 //   * polynomial semantics multivariate_polynomial.cpp:11-103: a repeated
 //     monomial keeps the coefficient of its first occurrence and terms are
 //     ordered by (degree, lexicographic)
@@ -45,6 +48,7 @@ struct Mlp {
     std::vector<int> shape;
     std::vector<std::vector<double>> w;  // [layer][out*in]
     double scale = 1.0;
+    bool tanh_square = false;            // postprocess "tanh-square": tanh(v^2)
 };
 
 Mlp read_mlp(const Value& v) {
@@ -53,6 +57,10 @@ Mlp read_mlp(const Value& v) {
     const Value& w = v.at("weights");
     for (std::size_t i = 0; i < w.size(); ++i) m.w.push_back(w.at(i).as_doubles());
     m.scale = v.at("activation_scale").as_number();
+    const std::string post = v.get_string("postprocess", "");
+    if (!post.empty() && post != "tanh-square")
+        throw std::invalid_argument("compact radial network has unsupported postprocessing");
+    m.tanh_square = post == "tanh-square";
     if (v.at("activation").as_string() != "silu")
         throw std::invalid_argument("compact radial networks must use SiLU activations");
     if (m.shape.size() < 2 || m.w.size() + 1 != m.shape.size())
@@ -147,6 +155,27 @@ void tabulate(const Mlp& net, const std::vector<double>& features, int nb, int p
         }
 }
 
+// A density network (one output, tanh(v^2)) on the grid, as FP64 Hermite
+// coefficients [interval][4] (radial_function_set_kokkos.cpp:30-41 with
+// Precision = double).
+std::vector<double> density_table(const Mlp& net, const std::vector<double>& features, int nb, int points,
+                                  double h) {
+    std::vector<double> v(points), out;
+    for (int node = 0; node < points; ++node) {
+        mlp_row(net, features.data() + static_cast<std::size_t>(node) * nb, out);
+        v[node] = std::tanh(out[0] * out[0]);
+    }
+    const auto d = node_derivatives(v, h);
+    std::vector<double> c(static_cast<std::size_t>(points - 1) * 4);
+    for (int i = 0; i < points - 1; ++i) {
+        c[4 * i] = v[i];
+        c[4 * i + 1] = d[i];
+        c[4 * i + 2] = (-3 * v[i] - 2 * h * d[i] + 3 * v[i + 1] - h * d[i + 1]) / (h * h);
+        c[4 * i + 3] = (2 * v[i] + h * d[i] - 2 * v[i + 1] + h * d[i + 1]) / (h * h * h);
+    }
+    return c;
+}
+
 // Deduplicate monomials (first occurrence wins) and sort by (degree, lex).
 struct Poly {
     std::vector<std::vector<int>> monos;
@@ -213,11 +242,13 @@ void HostModel::load(const std::string& path, const std::string& head) {
         throw std::invalid_argument("only h1_affine_mode 'm0_composite' is supported");
     if (j.get_string("radial_representation", "") != "compact")
         throw std::invalid_argument("only the compact radial representation is supported");
-    if (j.get_bool("has_zbl", false) || j.get_bool("A0_scaled", false) || j.get_bool("A1_scaled", false) ||
-        j.get_bool("has_field_coupling", false) || j.get_bool("first_interaction_residual", false) ||
-        j.get_bool("single_layer_readout", false))
+    if (j.get_bool("has_zbl", false) || j.get_bool("has_field_coupling", false) ||
+        j.get_bool("first_interaction_residual", false) || j.get_bool("single_layer_readout", false))
         throw std::invalid_argument("the model uses features outside the supported MACE path "
-                                    "(ZBL, density scaling, field coupling or single-layer readout)");
+                                    "(ZBL, field coupling or single-layer readout)");
+    // mace_kokkos_model.cpp:200 (required key), :1109 (optional key)
+    A0_scaled = j.at("A0_scaled").as_bool();
+    A1_scaled = j.get_bool("A1_scaled", false);
     num_interactions = j.get_int("num_interactions", 2);
     if (num_interactions != 2) throw std::invalid_argument("only two-interaction MACE models are supported");
     num_elements = j.at("num_elements").as_int();
@@ -262,13 +293,27 @@ void HostModel::load(const std::string& path, const std::string& head) {
     if (cr.at("distance_transform").at("type").as_string() != "none")
         throw std::invalid_argument("only distance_transform 'none' is supported");
     const Value& nets = cr.at("networks");
-    if (nets.contains("A0") || nets.contains("A1"))
-        throw std::invalid_argument("density-scaled radial networks are not supported");
     const Mlp R0net = read_mlp(nets.at("R0"));
     const Mlp R1net = read_mlp(nets.at("R1"));
     const int nb = static_cast<int>(bessel.size());
     if (R0net.shape[0] != nb || R1net.shape[0] != nb)
         throw std::invalid_argument("radial networks do not take the Bessel features");
+    if (R0net.tanh_square || R1net.tanh_square)
+        throw std::invalid_argument("compact radial R0/R1 networks cannot use postprocessing");
+    // density networks (compact_radial.cpp:181-193; mace_kokkos_model.cpp:215-216,1122-1123)
+    Mlp A0net, A1net;
+    auto density_net = [&](const char* name, bool scaled, Mlp& net) {
+        if (nets.contains(name) != scaled)
+            throw std::invalid_argument(std::string("compact radial ") + name + " network does not match " + name +
+                                        "_scaled");
+        if (!scaled) return;
+        net = read_mlp(nets.at(name));
+        if (net.shape.front() != nb || net.shape.back() != 1 || !net.tanh_square)
+            throw std::invalid_argument(std::string("compact radial ") + name +
+                                        " network has an invalid shape or postprocessing");
+    };
+    density_net("A0", A0_scaled, A0net);
+    density_net("A1", A1_scaled, A1net);
     std::vector<double> feat(static_cast<std::size_t>(spline_points) * nb);
     for (int node = 0; node < spline_points; ++node) {
         const double r = grid_min + node * h;
@@ -285,6 +330,8 @@ void HostModel::load(const std::string& path, const std::string& head) {
     if (R0_functions != (l_max + 1) * C) throw std::invalid_argument("R0 network width must be (l_max+1)*C");
     tabulate(R0net, feat, nb, spline_points, h, R0_values, R0_derivs, R0_coef);
     tabulate(R1net, feat, nb, spline_points, h, R1_values, R1_derivs, R1_coef);
+    if (A0_scaled) A0_density = density_table(A0net, feat, nb, spline_points, h);
+    if (A1_scaled) A1_density = density_table(A1net, feat, nb, spline_points, h);
 
     // ---- H0, A0
     H0 = to_f32(j.at("H0_weights").as_doubles());

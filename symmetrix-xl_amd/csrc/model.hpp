@@ -43,6 +43,10 @@ struct HostModel {
     std::vector<float> R0_coef, R1_coef;
     // nodal FP64 tables [function][node] (kept for diagnostics/tests)
     std::vector<double> R0_values, R0_derivs, R1_values, R1_derivs;
+    // density scaling of A0 / A1 (A /= 1 + sum_j f(r_ij)): FP64 Hermite
+    // coefficients [interval][4] of the one-output density networks
+    bool A0_scaled = false, A1_scaled = false;
+    std::vector<double> A0_density, A1_density;
 
     // layer 1
     std::vector<float> H0;                  // [type][C]

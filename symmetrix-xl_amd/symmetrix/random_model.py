@@ -3,7 +3,12 @@
 The file layout is the one the reference's loaders read
 (libsymmetrix/source/mace.cpp:2660-2959, mace_kokkos_model.cpp:146,
 compact_radial.cpp:110-214, h1_affine_schema.hpp:196-259): compact radial
-representation, h1_affine_mode "m0_composite", no ZBL, no density scaling.
+representation, h1_affine_mode "m0_composite", no ZBL.  A config with
+``density_scaled`` adds the A0 and A1 density networks (one output,
+"tanh-square" postprocessing, compact_radial.cpp:17-24,181-193) and sets
+``A0_scaled``/``A1_scaled``; their weights come from a second generator
+(``default_rng([seed, 1])``) so that every other weight equals the unscaled
+config's.
 
 Weights are drawn from ``numpy.random.default_rng(seed)`` with the fan-in
 scalings the reference's extractor folds into its exported weights
@@ -49,6 +54,7 @@ class ModelConfig:
     # plays the role of MACE's scale_shift.scale folded into the readouts
     # (extract_mace_data.py:1623-1625,1676-1680)
     energy_scale: float = 10.0
+    density_scaled: bool = False
     seed: int = 0
 
 
@@ -56,6 +62,9 @@ MODEL_CONFIGS = {
     # 32x0e+32x1o, lmax 2, corr 2, Sr/Ti/O, MLP [32,32], 5.0 A
     "tiny": ModelConfig("tiny", 32, 2, 1, 2, [8, 22, 38], radial_mlp=[32, 32],
                         r_cut=5.0, avg_num_neighbors=40.0),
+    # tiny with A0/A1 density scaling (mace.cpp:1562-1636, 2381-2459)
+    "tiny_scaled": ModelConfig("tiny_scaled", 32, 2, 1, 2, [8, 22, 38], radial_mlp=[32, 32],
+                               r_cut=5.0, avg_num_neighbors=40.0, density_scaled=True),
     # 128x0e+128x1o, lmax 3, corr 3, 89 elements,
     # MLP [64,64,64], 6.0 A
     "medium": ModelConfig("medium", 128, 3, 1, 3, list(range(1, 90)),
@@ -148,12 +157,12 @@ def generate_model(config, seed=None):
     bessel_w = _f32(np.arange(1, cfg.num_bessel + 1) * math.pi / r_cut)
     num_paths_r1 = len(e3.r1_paths(l_max, L_max))
 
-    def mlp(out_width):
+    def mlp(out_width, gen=rng):
         shape = [cfg.num_bessel] + list(cfg.radial_mlp) + [out_width]
         weights = []
         for a, b in zip(shape[:-1], shape[1:]):
             # effective weight W / sqrt(h_in), layout [out][in]
-            weights.append(_f32(rng.normal(size=(b, a)) / math.sqrt(a)))
+            weights.append(_f32(gen.normal(size=(b, a)) / math.sqrt(a)))
         return {"shape": shape,
                 "weights": [w.ravel().tolist() for w in weights],
                 "activation": "silu",
@@ -168,11 +177,19 @@ def generate_model(config, seed=None):
         "distance_transform": {"type": "none"},
         "networks": {"R0": mlp((l_max + 1) * C), "R1": mlp(num_paths_r1 * C)},
     }
+    if cfg.density_scaled:
+        drng = np.random.default_rng([seed, 1])
+        for name in ("A0", "A1"):
+            net = mlp(1, drng)
+            # a larger last layer so that tanh(v^2) spans (0, 1) over the grid
+            net["weights"][-1] = _f32(4.0 * np.asarray(net["weights"][-1])).tolist()
+            net["postprocess"] = "tanh-square"
+            compact["networks"][name] = net
     put("compact_radial", compact)
 
     # ---- H0: species embedding through linear_up
     frag["H0_weights"] = _fmt(rng.normal(size=(n_el, C)))
-    put("A0_scaled", False)
+    put("A0_scaled", bool(cfg.density_scaled))
 
     # ---- A0: per species, per l, C x C [input][output]
     a0 = rng.normal(size=(n_el, l_max + 1, C, C)) / (
@@ -210,7 +227,7 @@ def generate_model(config, seed=None):
     for key in ("Phi1_l", "Phi1_l1", "Phi1_l2", "Phi1_lme", "Phi1_lelm1lm2"):
         put(key, cpl[key])
     put("Phi1_clebsch_gordan", cpl["Phi1_clebsch_gordan"])
-    put("A1_scaled", False)
+    put("A1_scaled", bool(cfg.density_scaled))
 
     # ---- A1: per l, [num_e(l)][C][C]
     num_e = [sum(1 for l in cpl["Phi1_l"] if l == ll) for ll in range(l_max + 1)]

@@ -39,3 +39,9 @@ def medium_model_path():
 def wide_model_path():
     from symmetrix import random_model
     return random_model.cached_model("wide", directory=MODEL_DIR)
+
+
+@pytest.fixture(scope="session")
+def tiny_scaled_model_path():
+    from symmetrix import random_model
+    return random_model.cached_model("tiny_scaled", directory=MODEL_DIR)

@@ -120,6 +120,40 @@ def test_stages_tiny(tiny_model_path):
     assert np.max(np.abs(nf - ref["node_forces"])) < 1e-5
 
 
+
+def test_density_scaled_stages_and_efs(tiny_scaled_model_path):
+    """A0/A1 density scaling (mace_kokkos_first_interaction.cpp:1335-1531,
+    mace_kokkos_second_interaction.cpp:1310-1720) against the oracle: the
+    scaled A0 and A1, the scaled adjoints, directed forces and E/F/S."""
+    s = _system("tiny")
+    om, ref, ev, g, e, f, st = _evaluate_both(tiny_scaled_model_path, s)
+    for name in ("A0", "A1", "A1_adj", "dPhi1", "A0_adj"):
+        err = _stage_err(ev._stage(name).astype(np.float64), om.stage(name))
+        print(name, "relative max err %.3e" % err)
+        assert err < 1e-4, name
+    nf = ev.node_forces.reshape(-1, 3)
+    assert np.max(np.abs(nf - ref["node_forces"])) < 1e-5
+    _assert_efs(ref, e, f, st, len(e))
+
+
+@pytest.mark.parametrize("tile", [37, 64])
+def test_density_scaled_tiled_plan_matches_untiled(tiny_scaled_model_path, tile):
+    """The three-sweep tiled plan with density scaling: the factors are
+    per receiver, so tiles recompute them (A0 in sweeps 1 and 3, A1 in
+    sweep 2) and add their edge-force terms to each tile's forces."""
+    from symmetrix.mace_kokkos import MACEKokkosFloat
+    s = _system("tiny")
+    a = MACEKokkosFloat(tiny_scaled_model_path)
+    types = np.array([{8: 0, 22: 1, 38: 2}[int(z)] for z in s["numbers"]], np.int32)
+    e0, f0, s0 = _run(a, s, types)
+    b = MACEKokkosFloat(tiny_scaled_model_path)
+    b.set_execution_plan_request("capacity", tile)
+    e1, f1, s1 = _run(b, s, types)
+    assert b.execution_plan.startswith("direct-tiled")
+    np.testing.assert_array_equal(e1, e0)
+    np.testing.assert_allclose(f1, f0, rtol=0, atol=1e-7)
+    np.testing.assert_allclose(s1, s0, rtol=0, atol=1e-9)
+
 def test_energy_forces_stress_medium(medium_model_path):
     s = _system("medium")
     om, ref, ev, g, e, f, st = _evaluate_both(medium_model_path, s)

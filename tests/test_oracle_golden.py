@@ -366,3 +366,126 @@ def test_oracle_fp32_tracks_fp64(tiny_model_path):
     assert abs(r32["energy"] - r64["energy"]) / n < 1e-5
     assert np.max(np.abs(r32["forces"] - r64["forces"])) < 1e-4
     assert np.max(np.abs(r32["stress"] - r64["stress"])) < 1e-6
+
+
+# ---------------------------------------------------------------------------
+# Density scaling (A0_scaled / A1_scaled)
+# ---------------------------------------------------------------------------
+def _silu_mlp(net, x):
+    """multilayer_perceptron.cpp:30-80 in numpy: [out][in] weights, scaled
+    SiLU on hidden layers, linear output."""
+    h = np.asarray(x, dtype=np.float64)
+    layers = [np.asarray(w, dtype=np.float64).reshape(b, a)
+              for w, a, b in zip(net["weights"], net["shape"][:-1], net["shape"][1:])]
+    for k, W in enumerate(layers):
+        h = h @ W.T
+        if k + 1 < len(layers):
+            h = net["activation_scale"] * h / (1.0 + np.exp(-h))
+    return h
+
+
+def _density_splines(path, model):
+    with open(path) as f:
+        j = json.load(f)
+    cr = j["compact_radial"]
+    S = cr["num_spline_points"]
+    grid = cr["spline_grid_min"] + np.arange(S) * (j["r_cut"] - cr["spline_grid_min"]) / (S - 1)
+    feats = model.radial_features()
+    out = {}
+    for which, name in ((2, "A0"), (3, "A1")):
+        net = cr["networks"][name]
+        assert net["postprocess"] == "tanh-square" and net["shape"][-1] == 1
+        v = np.tanh(_silu_mlp(net, feats)[:, 0] ** 2)
+        ov, od = model.radial_tables(which)
+        np.testing.assert_allclose(ov[0], v, rtol=1e-12, atol=1e-14)
+        spl = CubicSpline(grid, v, bc_type=("not-a-knot", "clamped"))
+        np.testing.assert_allclose(od[0], spl.derivative()(grid), rtol=1e-8, atol=1e-9)
+        out[name] = spl
+    return out, j
+
+
+def test_density_networks_and_scale_factors(tiny_scaled_model_path, tiny_model_path):
+    """A0/A1 density networks: tanh(MLP(features)^2) on the grid (compact_radial.cpp:
+    295-303), spline node derivatives not-a-knot/clamped; per-receiver factor
+    s = 1 + sum over every CSR edge (skin edges at r clamped to the cutoff)
+    of f(r) (mace_kokkos_first_interaction.cpp:1389-1406); A0 /= s in FP64
+    after the A0 linear (:1409-1415), checked bit for bit against the
+    unscaled model (identical weights otherwise)."""
+    m = oracle.OracleModel(tiny_scaled_model_path)
+    spl, _ = _density_splines(tiny_scaled_model_path, m)
+    s = systems.srtio3_supercell(3, sigma=0.05, seed=0)
+    ref = oracle.evaluate_system(m, s, skin=0.5)
+    g, r = ref["graph"], ref["r"]
+    assert np.any(r >= m.r_cut)  # the graph holds skin edges
+    for name in ("A0", "A1"):
+        fr = spl[name](np.clip(r, 1e-12, m.r_cut))
+        expect = 1.0 + np.bincount(g["receivers"], weights=fr, minlength=len(s["numbers"]))
+        np.testing.assert_allclose(m.stage(name + "_scale"), expect, rtol=1e-11)
+    m0 = oracle.OracleModel(tiny_model_path)
+    oracle.evaluate_system(m0, s, skin=0.5)
+    n, C, nY = len(s["numbers"]), m.num_channels, m.num_lm
+    a0_plain = m0.stage("A0").reshape(n, nY * C).astype(np.float32)
+    a0_scaled = m.stage("A0").reshape(n, nY * C).astype(np.float32)
+    expect = (a0_plain.astype(np.float64) / m.stage("A0_scale")[:, None]).astype(np.float32)
+    assert a0_scaled.tobytes() == expect.tobytes()
+
+
+def test_density_scaled_A1_is_linear_times_inverse_factor(tiny_scaled_model_path):
+    """A1 = (A1 linear of Phi1) * float(1/s1) (mace_kokkos_second_interaction.cpp:
+    1474-1487), the linear restated here in FP64 numpy."""
+    m = oracle.OracleModel(tiny_scaled_model_path)
+    with open(tiny_scaled_model_path) as f:
+        j = json.load(f)
+    s = systems.srtio3_supercell(3, sigma=0.05, seed=0)
+    oracle.evaluate_system(m, s, skin=0.5)
+    n, C, nY = len(s["numbers"]), m.num_channels, m.num_lm
+    phi1 = m.stage("Phi1").reshape(n, m.num_lme, C)
+    paths_l = j["Phi1_l"]
+    lin = np.zeros((n, nY, C))
+    base = 0
+    for l in range(m.l_max + 1):
+        ne = sum(1 for x in paths_l if x == l)
+        if ne == 0:
+            continue
+        W = np.asarray(j["A1_weights"][l]).reshape(ne, C, C)
+        for mm in range(2 * l + 1):
+            for e in range(ne):
+                lin[:, l * l + mm, :] += phi1[:, base + mm * ne + e, :] @ W[e]
+        base += (2 * l + 1) * ne
+    inv = (1.0 / m.stage("A1_scale")).astype(np.float32).astype(np.float64)
+    a1 = m.stage("A1").reshape(n, nY, C)
+    np.testing.assert_allclose(a1, lin * inv[:, None, None], rtol=0, atol=2e-6 * np.abs(lin).max())
+
+
+def test_density_scaled_forces_and_stress_are_energy_derivatives(tiny_scaled_model_path):
+    """Central differences of the FP64 oracle energy with both density scales:
+    pins the reverse (edge-force terms (dot/s) f'(r) r^ and the scaled
+    adjoints)."""
+    m = oracle.OracleModel(tiny_scaled_model_path, fp64=True)
+    s = _small_system()
+    base = oracle.evaluate_system(m, s, skin=0.5)
+    assert np.max(np.abs(m.stage("density_forces"))) > 1e-3
+    h = 1e-4
+    rng = np.random.default_rng(8)
+    for a in rng.choice(len(s["numbers"]), 4, replace=False):
+        for c in range(3):
+            plus, minus = dict(s), dict(s)
+            pp, pm = s["positions"].copy(), s["positions"].copy()
+            pp[a, c] += h
+            pm[a, c] -= h
+            plus["positions"], minus["positions"] = pp, pm
+            ep = oracle.evaluate_system(m, plus, skin=0.5)["energy"]
+            em = oracle.evaluate_system(m, minus, skin=0.5)["energy"]
+            assert base["forces"][a, c] == pytest.approx(-(ep - em) / (2 * h), abs=2e-6)
+    V = abs(np.linalg.det(s["cell"]))
+    for (i, k) in [(0, 0), (2, 1)]:
+        eps = np.zeros((3, 3))
+        eps[i, k] = h
+
+        def strained(sign):
+            t = dict(s)
+            F = np.eye(3) + sign * eps
+            t["positions"] = s["positions"] @ F.T
+            t["cell"] = s["cell"] @ F.T
+            return oracle.evaluate_system(m, t, skin=0.5)["energy"]
+        assert base["stress"][i, k] == pytest.approx((strained(+1) - strained(-1)) / (2 * h) / V, abs=1e-7)
