@@ -24,6 +24,10 @@
 //   * polynomial semantics: multivariate_polynomial.cpp:11-103 (a repeated
 //     monomial keeps its first coefficient)
 //   * force and stress reductions: mace_kokkos_evaluate.cpp:49-128, 189-291
+//   * ZBL pair repulsion (FP64): zbl_kokkos.cpp:11-160 (pair constants,
+//     value and gradient with the polynomial envelope), applied per edge
+//     before the model as mace_kokkos_evaluate.cpp:418-434 does
+//     (node_energies += sum_j V, directed forces -= (xyz/r) dV/dr)
 //   * density scaling of A0 and A1 as the Kokkos evaluator computes it (FP64
 //     splines and sums): mace_kokkos_first_interaction.cpp:1335-1419
 //     (A0 /= 1 + sum_j f0(r_ij)), :1421-1531 (reverse: edge forces
@@ -214,6 +218,68 @@ struct RadialModel {
         }
         derivs.resize(nout);
         for (int o = 0; o < nout; ++o) derivs[o] = spline_derivatives(values[o]);
+    }
+};
+
+// ---------------------------------------------------------------------------
+// ZBL pair repulsion (zbl_kokkos.cpp:11-160, FP64)
+// ---------------------------------------------------------------------------
+struct Zbl {
+    static constexpr double kExp[4] = {-3.2, -0.9423, -0.4028, -0.2016};
+    static constexpr double kPrefactor = 14.3996;
+    double a_exp = 0, a_prefactor = 0;
+    double c[4] = {0, 0, 0, 0};
+    std::vector<double> radii;
+    int p = 0;
+
+    void init(double a_exp_, double a_prefactor_, const std::vector<double>& c_, const std::vector<double>& radii_,
+              int p_) {
+        if (c_.size() != 4) throw std::invalid_argument("ZBL requires four screening coefficients");
+        if (radii_.empty()) throw std::invalid_argument("ZBL requires at least one covalent radius");
+        if (!(a_prefactor_ > 0.0)) throw std::invalid_argument("ZBL screening prefactor must be positive");
+        if (p_ < 1) throw std::invalid_argument("ZBL envelope power must be positive");
+        a_exp = a_exp_;
+        a_prefactor = a_prefactor_;
+        for (int i = 0; i < 4; ++i) c[i] = c_[i];
+        radii = radii_;
+        p = p_;
+    }
+    // polynomial envelope and its derivative (zbl_kokkos.cpp:125-137)
+    void envelope(double r, double r_max, double& v, double& g) const {
+        if (r >= r_max) {
+            v = g = 0.0;
+            return;
+        }
+        const double c0 = (p + 1.0) * (p + 2.0) / 2.0, c1 = p * (p + 2.0), c2 = p * (p + 1.0) / 2.0;
+        const double x = r / r_max;
+        const double xm1 = std::pow(x, p - 1), xp = xm1 * x, xp1 = xp * x, xp2 = xp1 * x;
+        v = 1.0 - c0 * xp + c1 * xp1 - c2 * xp2;
+        g = (-c0 * p * xm1 + c1 * (p + 1.0) * xp - c2 * (p + 2.0) * xp1) / r_max;
+    }
+    // value and dV/dr of one directed edge (zbl_kokkos.cpp:92-139)
+    void value_gradient(int Zu, int Zv, double r, double& value, double& gradient) const {
+        if (Zu < 0 || Zv < 0 || Zu >= static_cast<int>(radii.size()) || Zv >= static_cast<int>(radii.size()))
+            throw std::out_of_range("ZBL atomic number outside the covalent-radius table");
+        const double inverse_a = (std::pow(static_cast<double>(Zu), a_exp) + std::pow(static_cast<double>(Zv), a_exp)) /
+                                 (a_prefactor * 0.529);
+        const double bare_prefactor = kPrefactor * static_cast<double>(Zu * Zv);
+        const double r_max = radii[Zu] + radii[Zv];
+        if (r >= r_max) {
+            value = gradient = 0.0;
+            return;
+        }
+        const double ra = r * inverse_a;
+        double e[4];
+        for (int i = 0; i < 4; ++i) e[i] = c[i] * std::exp(kExp[i] * ra);
+        const double phi = e[0] + e[1] + e[2] + e[3];
+        const double dphi = inverse_a * (kExp[0] * e[0] + kExp[1] * e[1] + kExp[2] * e[2] + kExp[3] * e[3]);
+        const double inv_r = 1.0 / r;
+        const double bare = bare_prefactor * inv_r * phi;
+        const double bare_g = bare_prefactor * inv_r * inv_r * (r * dphi - phi);
+        double env, env_g;
+        envelope(r, r_max, env, env_g);
+        value = 0.5 * bare * env;
+        gradient = 0.5 * (bare * env_g + bare_g * env);
     }
 };
 
@@ -412,6 +478,10 @@ struct Mace {
     // active radial tables
     std::vector<int> active_types, type_to_active;
     std::vector<std::shared_ptr<SplineSet<P>>> spl0, spl1;
+    // ZBL pair repulsion
+    bool has_zbl = false;
+    Zbl zbl;
+    std::vector<double> zbl_energies, zbl_forces;  // per node, per edge [3]
     // density scaling: FP64 splines of the A0/A1 networks (one function)
     bool A0_scaled = false, A1_scaled = false;
     std::shared_ptr<SplineSet<double>> dens0, dens1;
@@ -450,7 +520,7 @@ struct Mace {
             throw std::invalid_argument("only h1_affine_mode 'm0_composite' is supported");
         if (j.get_string("radial_representation", "") != "compact")
             throw std::invalid_argument("only the compact radial representation is supported");
-        if (j.get_bool("has_zbl", false) || j.get_bool("has_field_coupling", false) ||
+        if (j.get_bool("has_field_coupling", false) ||
             j.get_bool("first_interaction_residual", false) || j.get_bool("single_layer_readout", false))
             throw std::invalid_argument("model features outside the supported MACE path");
         num_elements = j.at("num_elements").as_int();
@@ -464,6 +534,11 @@ struct Mace {
         atomic_numbers = j.at("atomic_numbers").as_ints();
         atomic_energies = j.at("atomic_energies").as_doubles();
         radial.load(j.at("compact_radial"), r_cut);
+        // mace_kokkos_model.cpp:191-198
+        has_zbl = j.at("has_zbl").as_bool();
+        if (has_zbl)
+            zbl.init(j.at("zbl_a_exp").as_number(), j.at("zbl_a_prefactor").as_number(), j.at("zbl_c").as_doubles(),
+                     j.at("zbl_covalent_radii").as_doubles(), j.at("zbl_p").as_int());
         // mace_kokkos_model.cpp:200,215-216,1109,1122-1123
         A0_scaled = j.at("A0_scaled").as_bool();
         A1_scaled = j.get_bool("A1_scaled", false);
@@ -658,6 +733,25 @@ struct Mace {
             for (int c = 0; c < 3; ++c) d[c] = static_cast<P>(xyz[3 * e + c] / r[e]);
             for (int c = 0; c < 3; ++c) dirs[3 * e + c] = d[c];
             edge_harmonics<P>(l_max, d, static_cast<P>(r[e]), &Y[e * nY], &Ygrad[e * 3 * nY]);
+        }
+
+        // ---- ZBL (mace_kokkos_evaluate.cpp:418-434; zbl_kokkos.cpp:163-199):
+        // every CSR edge, node energy += V, directed force -= (xyz/r) dV/dr
+        zbl_energies.assign(has_zbl ? n : 0, 0.0);
+        zbl_forces.assign(has_zbl ? static_cast<std::size_t>(E) * 3 : 0, 0.0);
+        if (has_zbl) {
+#pragma omp parallel for schedule(static)
+            for (int i = 0; i < n; ++i) {
+                const int Zi = atomic_numbers[types[i]];
+                double ei = 0.0;
+                for (long long e = off[i]; e < off[i + 1]; ++e) {
+                    double v, g;
+                    zbl.value_gradient(Zi, atomic_numbers[neigh_types[e]], r[e], v, g);
+                    ei += v;
+                    for (int c = 0; c < 3; ++c) zbl_forces[3 * e + c] -= xyz[3 * e + c] / r[e] * g;
+                }
+                zbl_energies[i] = ei;
+            }
         }
 
         // ---- A0 (mace.cpp:1356-1403)
@@ -1131,6 +1225,10 @@ struct Mace {
         }
         if (A0_scaled || A1_scaled)
             for (long long v = 0; v < 3 * E; ++v) node_forces[v] += density_forces[v];
+        if (has_zbl) {
+            for (long long v = 0; v < 3 * E; ++v) node_forces[v] += zbl_forces[v];
+            for (int i = 0; i < n; ++i) node_energies[i] += zbl_energies[i];
+        }
     }
 };
 
@@ -1344,7 +1442,7 @@ int oracle_evaluate(void* hv, int n, const int* types, const int* num_neigh, con
 // Stage buffers of the last evaluation, as float64: name in {Y, Ygrad, A0, M0,
 // M0_grad, H1, Phi1, A1, M1, H2, H2_adj, A1_adj, dPhi1, H1_adj, M0_adj, A0_adj,
 // node_forces_r1, Phi0, Phi0_adj, node_forces_r0, A0_scale, A1_scale,
-// density_forces}.
+// density_forces, zbl_energies, zbl_forces}.
 long long oracle_stage(void* hv, const char* name, double* out, long long capacity) {
     auto* h = static_cast<OracleHandle*>(hv);
     auto get = [&](auto& m) -> long long {
@@ -1377,6 +1475,8 @@ long long oracle_stage(void* hv, const char* name, double* out, long long capaci
         if (s == "A0_scale") return emit(m.A0_scale);
         if (s == "A1_scale") return emit(m.A1_scale);
         if (s == "density_forces") return emit(m.density_forces);
+        if (s == "zbl_energies") return emit(m.zbl_energies);
+        if (s == "zbl_forces") return emit(m.zbl_forces);
         return -1;
     };
     return h->fp64 ? get(*h->d) : get(*h->f);
@@ -1570,6 +1670,20 @@ int oracle_reduce_stress(long long E, const double* f, const double* xyz, double
             stress[3 * a + b] = -s / volume;
         }
     return 0;
+}
+
+// One ZBL pair (zbl_kokkos.cpp; the reference's symmetrix.ZBL binding):
+// out = {value, dV/dr, envelope, d envelope/dr} at distance r.
+int oracle_zbl(double a_exp, double a_prefactor, const double* c, const double* radii, int num_radii, int p, int Zu,
+               int Zv, double r, double* out) {
+    return guarded([&]() -> int {
+        Zbl z;
+        z.init(a_exp, a_prefactor, std::vector<double>(c, c + 4), std::vector<double>(radii, radii + num_radii), p);
+        z.value_gradient(Zu, Zv, r, out[0], out[1]);
+        if (Zu < 0 || Zv < 0 || Zu >= num_radii || Zv >= num_radii) throw std::out_of_range("Z out of range");
+        z.envelope(r, radii[Zu] + radii[Zv], out[2], out[3]);
+        return 0;
+    });
 }
 
 int oracle_num_threads() { return omp_get_max_threads(); }

@@ -61,8 +61,19 @@ def lib():
                                                _f64p, _f64p, _f64p, _f64p, ctypes.c_double, _f64p, _f64p]
         L.oracle_reduce_forces.argtypes = [ctypes.c_int, ctypes.c_longlong, _i32p, _i32p, _f64p, _f64p]
         L.oracle_reduce_stress.argtypes = [ctypes.c_longlong, _f64p, _f64p, ctypes.c_double, _f64p]
+        L.oracle_zbl.argtypes = [ctypes.c_double, ctypes.c_double, _f64p, _f64p, ctypes.c_int, ctypes.c_int,
+                                 ctypes.c_int, ctypes.c_int, ctypes.c_double, _f64p]
         _lib = L
     return _lib
+
+
+def zbl_pair(a_exp, a_prefactor, c, covalent_radii, p, Zu, Zv, r):
+    """(value, dV/dr, envelope, d envelope/dr) of one ZBL pair at r."""
+    out = np.zeros(4)
+    radii = _c(covalent_radii, np.float64)
+    if lib().oracle_zbl(a_exp, a_prefactor, _c(c, np.float64), radii, len(radii), p, Zu, Zv, r, out) != 0:
+        raise ValueError(_err())
+    return tuple(float(v) for v in out)
 
 
 def _err():

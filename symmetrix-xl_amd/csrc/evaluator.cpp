@@ -318,6 +318,12 @@ struct Evaluator {
         dm.A1_scaled = hm.A1_scaled;
         if (hm.A0_scaled) dm.dens0 = put(hm.A0_density);
         if (hm.A1_scaled) dm.dens1 = put(hm.A1_density);
+        dm.has_zbl = hm.has_zbl;
+        if (hm.has_zbl) {
+            dm.zbl_pair = put(hm.zbl_pair);
+            for (int k = 0; k < 4; ++k) dm.zbl_c[k] = hm.zbl_c[k];
+            dm.zbl_p = hm.zbl_p;
+        }
         dm.R0c = reinterpret_cast<const float4*>(put(hm.R0_coef));
         dm.R1c = reinterpret_cast<const float4*>(put(hm.R1_coef));
         dm.H0 = put(hm.H0);

@@ -947,6 +947,10 @@ struct KernelSetImpl final : KernelSet {
             TimerScope ts(tm, "a1_density_forces", s);
             launch_density_forces(m, g, t, nullptr, nullptr, w.dens_s1, w.dens_dot1, w.node_forces, s);
         }
+        if (m.has_zbl) {
+            TimerScope ts(tm, "zbl", s);
+            launch_zbl(m, g, t, w.node_energies, w.node_forces, s);
+        }
     }
 
     void source_adjoint_all(const DeviceGraph& g, const Workspace& w, const double* r, double r_cut, hipStream_t s,

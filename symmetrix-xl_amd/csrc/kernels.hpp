@@ -54,6 +54,11 @@ struct DeviceModel {
     const double* dens0 = nullptr;
     const double* dens1 = nullptr;
     double x0_f64 = 0.0, h_f64 = 0.0;
+    // ZBL pair repulsion: per (type, type) 1/a, 14.3996 Z_u Z_v, r_max
+    bool has_zbl = false;
+    const double* zbl_pair = nullptr;
+    double zbl_c[4] = {0.0, 0.0, 0.0, 0.0};
+    int zbl_p = 0;
 };
 
 // One prepared graph on the device (receiver-major CSR + source transpose).
@@ -225,6 +230,10 @@ void launch_density_adjoint(int nr, int row_len, const float* A, const double* s
 void launch_density_forces(const DeviceModel& m, const DeviceGraph& g, const TileView& t, const double* s0,
                            const double* dot0, const double* s1, const double* dot1, double* node_forces,
                            hipStream_t s);
+// ZBL (zbl.hip): node_energies (graph-wide) += pair energies of the tile's
+// receivers, node_forces (tile-local) -= their edge gradients
+void launch_zbl(const DeviceModel& m, const DeviceGraph& g, const TileView& t, double* node_energies,
+                double* node_forces, hipStream_t s);
 
 // Reductions (FP64, deterministic order)
 void launch_atom_forces(int N, const int* offsets, const int* soff, const int* sedges, const double* node_forces,

@@ -242,10 +242,10 @@ void HostModel::load(const std::string& path, const std::string& head) {
         throw std::invalid_argument("only h1_affine_mode 'm0_composite' is supported");
     if (j.get_string("radial_representation", "") != "compact")
         throw std::invalid_argument("only the compact radial representation is supported");
-    if (j.get_bool("has_zbl", false) || j.get_bool("has_field_coupling", false) ||
-        j.get_bool("first_interaction_residual", false) || j.get_bool("single_layer_readout", false))
+    if (j.get_bool("has_field_coupling", false) || j.get_bool("first_interaction_residual", false) ||
+        j.get_bool("single_layer_readout", false))
         throw std::invalid_argument("the model uses features outside the supported MACE path "
-                                    "(ZBL, field coupling or single-layer readout)");
+                                    "(field coupling, first-interaction residual or single-layer readout)");
     // mace_kokkos_model.cpp:200 (required key), :1109 (optional key)
     A0_scaled = j.at("A0_scaled").as_bool();
     A1_scaled = j.get_bool("A1_scaled", false);
@@ -265,6 +265,32 @@ void HostModel::load(const std::string& path, const std::string& head) {
     if (static_cast<int>(atomic_numbers.size()) != num_elements ||
         static_cast<int>(atomic_energies.size()) != num_elements)
         throw std::invalid_argument("atomic numbers/energies do not match num_elements");
+    // ZBL (mace_kokkos_model.cpp:191-198; constructor checks and per-pair
+    // constants zbl_kokkos.cpp:11-56, here per pair of the model's types)
+    has_zbl = j.at("has_zbl").as_bool();
+    if (has_zbl) {
+        const double a_exp = j.at("zbl_a_exp").as_number(), a_prefactor = j.at("zbl_a_prefactor").as_number();
+        const auto c = j.at("zbl_c").as_doubles();
+        const auto radii = j.at("zbl_covalent_radii").as_doubles();
+        zbl_p = j.at("zbl_p").as_int();
+        if (c.size() != 4) throw std::invalid_argument("ZBL requires four screening coefficients");
+        if (radii.empty()) throw std::invalid_argument("ZBL requires at least one covalent radius");
+        if (!(a_prefactor > 0.0)) throw std::invalid_argument("ZBL screening prefactor must be positive");
+        if (zbl_p < 1) throw std::invalid_argument("ZBL envelope power must be positive");
+        for (int k = 0; k < 4; ++k) zbl_c[k] = c[k];
+        zbl_pair.assign(static_cast<std::size_t>(num_elements) * num_elements * 3, 0.0);
+        for (int u = 0; u < num_elements; ++u)
+            for (int v = 0; v < num_elements; ++v) {
+                const int Zu = atomic_numbers[u], Zv = atomic_numbers[v];
+                if (Zu < 0 || Zv < 0 || Zu >= static_cast<int>(radii.size()) || Zv >= static_cast<int>(radii.size()))
+                    throw std::invalid_argument("ZBL covalent radii do not cover the model's atomic numbers");
+                double* pc = &zbl_pair[(static_cast<std::size_t>(u) * num_elements + v) * 3];
+                pc[0] = (std::pow(static_cast<double>(Zu), a_exp) + std::pow(static_cast<double>(Zv), a_exp)) /
+                        (a_prefactor * 0.529);
+                pc[1] = 14.3996 * static_cast<double>(Zu * Zv);
+                pc[2] = radii[Zu] + radii[Zv];
+            }
+    }
     const std::size_t Cs = static_cast<std::size_t>(C);
 
     // ---- compact radial

@@ -47,6 +47,11 @@ struct HostModel {
     // coefficients [interval][4] of the one-output density networks
     bool A0_scaled = false, A1_scaled = false;
     std::vector<double> A0_density, A1_density;
+    // ZBL pair repulsion: per (type, type) {1/a, 14.3996 Z_u Z_v, r_max}
+    bool has_zbl = false;
+    std::vector<double> zbl_pair;
+    double zbl_c[4] = {0.0, 0.0, 0.0, 0.0};
+    int zbl_p = 0;
 
     // layer 1
     std::vector<float> H0;                  // [type][C]

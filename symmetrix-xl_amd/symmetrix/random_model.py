@@ -3,7 +3,10 @@
 The file layout is the one the reference's loaders read
 (libsymmetrix/source/mace.cpp:2660-2959, mace_kokkos_model.cpp:146,
 compact_radial.cpp:110-214, h1_affine_schema.hpp:196-259): compact radial
-representation, h1_affine_mode "m0_composite", no ZBL.  A config with
+representation, h1_affine_mode "m0_composite".  A config with ``zbl`` adds
+the ZBL pair repulsion with the parameters of the reference's ZBL test model
+(symmetrix/test/conftest.py:177-184: a_exp 0.3, a_prefactor 0.4543, the
+four screening coefficients, covalent radii 1.0 A, p 6).  A config with
 ``density_scaled`` adds the A0 and A1 density networks (one output,
 "tanh-square" postprocessing, compact_radial.cpp:17-24,181-193) and sets
 ``A0_scaled``/``A1_scaled``; their weights come from a second generator
@@ -55,6 +58,7 @@ class ModelConfig:
     # (extract_mace_data.py:1623-1625,1676-1680)
     energy_scale: float = 10.0
     density_scaled: bool = False
+    zbl: bool = False
     seed: int = 0
 
 
@@ -65,6 +69,9 @@ MODEL_CONFIGS = {
     # tiny with A0/A1 density scaling (mace.cpp:1562-1636, 2381-2459)
     "tiny_scaled": ModelConfig("tiny_scaled", 32, 2, 1, 2, [8, 22, 38], radial_mlp=[32, 32],
                                r_cut=5.0, avg_num_neighbors=40.0, density_scaled=True),
+    # tiny with ZBL pair repulsion (zbl_kokkos.cpp)
+    "tiny_zbl": ModelConfig("tiny_zbl", 32, 2, 1, 2, [8, 22, 38], radial_mlp=[32, 32],
+                            r_cut=5.0, avg_num_neighbors=40.0, zbl=True),
     # 128x0e+128x1o, lmax 3, corr 3, 89 elements,
     # MLP [64,64,64], 6.0 A
     "medium": ModelConfig("medium", 128, 3, 1, 3, list(range(1, 90)),
@@ -149,7 +156,13 @@ def generate_model(config, seed=None):
     put("atomic_energies",
         [float(v) for v in _f32(-1.0 - 0.05 * np.asarray(cfg.atomic_numbers)
                                  + 0.1 * rng.normal(size=n_el))])
-    put("has_zbl", False)
+    put("has_zbl", bool(cfg.zbl))
+    if cfg.zbl:
+        put("zbl_a_exp", 0.3)
+        put("zbl_a_prefactor", 0.4543)
+        put("zbl_c", [0.1818, 0.5099, 0.2802, 0.02817])
+        put("zbl_covalent_radii", [1.0] * 119)
+        put("zbl_p", 6)
     put("radial_representation", "compact")
 
     # ---- compact radial (Bessel x polynomial cutoff -> SiLU MLPs)

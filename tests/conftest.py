@@ -45,3 +45,9 @@ def wide_model_path():
 def tiny_scaled_model_path():
     from symmetrix import random_model
     return random_model.cached_model("tiny_scaled", directory=MODEL_DIR)
+
+
+@pytest.fixture(scope="session")
+def tiny_zbl_model_path():
+    from symmetrix import random_model
+    return random_model.cached_model("tiny_zbl", directory=MODEL_DIR)

@@ -154,6 +154,26 @@ def test_density_scaled_tiled_plan_matches_untiled(tiny_scaled_model_path, tile)
     np.testing.assert_allclose(f1, f0, rtol=0, atol=1e-7)
     np.testing.assert_allclose(s1, s0, rtol=0, atol=1e-9)
 
+
+def test_zbl_efs_and_tiled_plan(tiny_zbl_model_path):
+    """ZBL pair repulsion (zbl_kokkos.cpp:92-199) against the oracle: node
+    energies, directed forces and E/F/S; the tiled plan equals the direct one."""
+    from symmetrix.mace_kokkos import MACEKokkosFloat
+    s = _system("tiny")
+    om, ref, ev, g, e, f, st = _evaluate_both(tiny_zbl_model_path, s)
+    assert np.max(np.abs(om.stage("zbl_forces"))) > 1e-3
+    np.testing.assert_allclose(e, ref["energies"], rtol=0, atol=1e-4)
+    nf = ev.node_forces.reshape(-1, 3)
+    assert np.max(np.abs(nf - ref["node_forces"])) < 1e-5
+    _assert_efs(ref, e, f, st, len(e))
+    b = MACEKokkosFloat(tiny_zbl_model_path)
+    b.set_execution_plan_request("capacity", 64)
+    e1, f1, s1 = _run(b, s, om.types_of(s["numbers"]))
+    assert b.execution_plan.startswith("direct-tiled")
+    np.testing.assert_array_equal(e1, e)
+    np.testing.assert_allclose(f1, f, rtol=0, atol=1e-7)
+    np.testing.assert_allclose(s1, st, rtol=0, atol=1e-9)
+
 def test_energy_forces_stress_medium(medium_model_path):
     s = _system("medium")
     om, ref, ev, g, e, f, st = _evaluate_both(medium_model_path, s)

@@ -489,3 +489,77 @@ def test_density_scaled_forces_and_stress_are_energy_derivatives(tiny_scaled_mod
             t["cell"] = s["cell"] @ F.T
             return oracle.evaluate_system(m, t, skin=0.5)["energy"]
         assert base["stress"][i, k] == pytest.approx((strained(+1) - strained(-1)) / (2 * h) / V, abs=1e-7)
+
+
+# ---------------------------------------------------------------------------
+# ZBL pair repulsion (zbl_kokkos.cpp)
+# ---------------------------------------------------------------------------
+_ZBL_RADII = [0.2, 0.31, 0.28, 1.28, 0.96, 0.84, 0.76, 0.71, 0.66, 0.57, 0.58]
+_ZBL_C = [0.1818, 0.5099, 0.2802, 0.02817]
+
+
+def test_zbl_known_answers():
+    """The reference's test_zbl.py:1-44 values: envelope 0.4374788794430078
+    and V 0.3166652764835175 for Z 5-10 at 1 A; zero at r_max; gradients
+    against central differences."""
+    r_max = _ZBL_RADII[5] + _ZBL_RADII[10]
+    v, g, env, env_g = oracle.zbl_pair(0.3, 0.4543, _ZBL_C, _ZBL_RADII, 6, 5, 10, 1.0)
+    assert env == pytest.approx(0.4374788794430078)
+    assert v == pytest.approx(0.3166652764835175)
+    assert oracle.zbl_pair(0.3, 0.4543, _ZBL_C, _ZBL_RADII, 6, 5, 10, r_max)[:4] == (0.0, 0.0, 0.0, 0.0)
+    dx = 1e-4
+    vp, _, ep, _ = oracle.zbl_pair(0.3, 0.4543, _ZBL_C, _ZBL_RADII, 6, 5, 10, 1.0 + dx)
+    vm, _, em, _ = oracle.zbl_pair(0.3, 0.4543, _ZBL_C, _ZBL_RADII, 6, 5, 10, 1.0 - dx)
+    assert g == pytest.approx((vp - vm) / (2 * dx))
+    assert env_g == pytest.approx((ep - em) / (2 * dx))
+
+
+def test_zbl_model_energy_is_the_pair_sum(tiny_zbl_model_path, tiny_model_path):
+    """A ZBL model's energy is the plain model's plus sum over directed edges
+    of V(Z_i, Z_j, r) (test_mace.py:753-790; mace_kokkos_evaluate.cpp:418-434),
+    skin edges included (they lie beyond r_max)."""
+    with open(tiny_zbl_model_path) as f:
+        j = json.load(f)
+    s = systems.srtio3_supercell(3, sigma=0.05, seed=0)
+    mz = oracle.OracleModel(tiny_zbl_model_path, fp64=True)
+    m0 = oracle.OracleModel(tiny_model_path, fp64=True)
+    rz = oracle.evaluate_system(mz, s, skin=0.5)
+    r0 = oracle.evaluate_system(m0, s, skin=0.5)
+    g = rz["graph"]
+    Z = np.asarray(s["numbers"])
+    pairs = [oracle.zbl_pair(j["zbl_a_exp"], j["zbl_a_prefactor"], j["zbl_c"], j["zbl_covalent_radii"], j["zbl_p"],
+                             int(Z[i]), int(Z[k]), float(r))[0]
+             for i, k, r in zip(g["receivers"], g["sources"], rz["r"])]
+    assert sum(v != 0.0 for v in pairs) > 10
+    per_node = np.bincount(g["receivers"], weights=pairs, minlength=len(Z))
+    np.testing.assert_allclose(rz["energies"] - r0["energies"], per_node, rtol=0, atol=1e-12)
+
+
+def test_zbl_forces_and_stress_are_energy_derivatives(tiny_zbl_model_path):
+    m = oracle.OracleModel(tiny_zbl_model_path, fp64=True)
+    s = systems.srtio3_supercell(2, sigma=0.15, seed=5)
+    base = oracle.evaluate_system(m, s, skin=0.5)
+    assert np.max(np.abs(m.stage("zbl_forces"))) > 1e-3
+    h = 1e-5
+    rng = np.random.default_rng(9)
+    for a in rng.choice(len(s["numbers"]), 5, replace=False):
+        for c in range(3):
+            plus, minus = dict(s), dict(s)
+            pp, pm = s["positions"].copy(), s["positions"].copy()
+            pp[a, c] += h
+            pm[a, c] -= h
+            plus["positions"], minus["positions"] = pp, pm
+            ep = oracle.evaluate_system(m, plus, skin=0.5)["energy"]
+            em = oracle.evaluate_system(m, minus, skin=0.5)["energy"]
+            assert base["forces"][a, c] == pytest.approx(-(ep - em) / (2 * h), abs=2e-6)
+    V = abs(np.linalg.det(s["cell"]))
+    eps = np.zeros((3, 3))
+    eps[0, 1] = h
+
+    def strained(sign):
+        t = dict(s)
+        F = np.eye(3) + sign * eps
+        t["positions"] = s["positions"] @ F.T
+        t["cell"] = s["cell"] @ F.T
+        return oracle.evaluate_system(m, t, skin=0.5)["energy"]
+    assert base["stress"][0, 1] == pytest.approx((strained(+1) - strained(-1)) / (2 * h) / V, abs=1e-7)
