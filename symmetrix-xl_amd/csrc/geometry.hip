@@ -349,41 +349,55 @@ __global__ void k_compact_bits(int words, const std::uint32_t* __restrict__ bitm
 // ---------------------------------------------------------------------------
 // Per-edge records: spline point, Y, dY/dxyz, unit direction
 // ---------------------------------------------------------------------------
+// One thread per edge builds its record in LDS; the workgroup then writes
+// its contiguous block of records with coalesced float4 stores (a record per
+// lane written directly strides 288 B between lanes).
+constexpr int kRecordThreads = 128;
+
 template <int LMAX>
-__global__ __launch_bounds__(256) void k_edge_records(long long E, const double* __restrict__ xyz,
-                                                      const double* __restrict__ r, double r_cut, float x0, float h,
-                                                      int intervals, float* __restrict__ erec) {
+__global__ __launch_bounds__(kRecordThreads) void k_edge_records(long long E, const double* __restrict__ xyz,
+                                                                 const double* __restrict__ r, double r_cut,
+                                                                 float x0, float h, int intervals,
+                                                                 float* __restrict__ erec) {
     using S = Shape<LMAX, 0>;
-    const long long e = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (e >= E) return;
-    float* rec = erec + e * S::REC;
-    const double re = r[e];
-    if (!(re < r_cut)) {
-        for (int q = 0; q < S::REC; ++q) rec[q] = 0.0f;
-        return;
+    static_assert(S::REC % 4 == 0, "records are whole float4s");
+    __shared__ float4 stage[kRecordThreads * S::REC / 4];
+    const long long base = static_cast<long long>(blockIdx.x) * kRecordThreads;
+    const long long e = base + threadIdx.x;
+    float* rec = reinterpret_cast<float*>(stage) + threadIdx.x * S::REC;
+    if (e < E) {
+        const double re = r[e];
+        if (!(re < r_cut)) {
+            for (int q = 0; q < S::REC; ++q) rec[q] = 0.0f;
+        } else {
+            float d[3];
+            for (int c = 0; c < 3; ++c) d[c] = static_cast<float>(xyz[3 * e + c] / re);
+            const float rf = static_cast<float>(re);
+            // spline evaluation point (cubic_spline_set.cpp:33-46)
+            int interval = static_cast<int>(floorf((rf - x0) / h));
+            float xloc = rf - x0 - h * static_cast<float>(interval);
+            if (interval < 0) {
+                interval = 0;
+                xloc = 0.0f;
+            } else if (interval >= intervals) {
+                interval = intervals - 1;
+                xloc = h;
+            }
+            rec[0] = xloc;
+            rec[1] = __int_as_float(interval);
+            rec[2] = __int_as_float(1);
+            rec[3] = 0.0f;
+            edge_harmonics<LMAX>(d, rf, rec + S::REC_Y, rec + S::REC_DY);
+            rec[S::REC_U] = d[0];
+            rec[S::REC_U + 1] = d[1];
+            rec[S::REC_U + 2] = d[2];
+            for (int q = S::REC_U + 3; q < S::REC; ++q) rec[q] = 0.0f;
+        }
     }
-    float d[3];
-    for (int c = 0; c < 3; ++c) d[c] = static_cast<float>(xyz[3 * e + c] / re);
-    const float rf = static_cast<float>(re);
-    // spline evaluation point (cubic_spline_set.cpp:33-46)
-    int interval = static_cast<int>(floorf((rf - x0) / h));
-    float xloc = rf - x0 - h * static_cast<float>(interval);
-    if (interval < 0) {
-        interval = 0;
-        xloc = 0.0f;
-    } else if (interval >= intervals) {
-        interval = intervals - 1;
-        xloc = h;
-    }
-    rec[0] = xloc;
-    rec[1] = __int_as_float(interval);
-    rec[2] = __int_as_float(1);
-    rec[3] = 0.0f;
-    edge_harmonics<LMAX>(d, rf, rec + S::REC_Y, rec + S::REC_DY);
-    rec[S::REC_U] = d[0];
-    rec[S::REC_U + 1] = d[1];
-    rec[S::REC_U + 2] = d[2];
-    for (int q = S::REC_U + 3; q < S::REC; ++q) rec[q] = 0.0f;
+    __syncthreads();
+    const long long count = E - base < kRecordThreads ? E - base : kRecordThreads;
+    float4* dst = reinterpret_cast<float4*>(erec + base * S::REC);
+    for (int q = threadIdx.x; q < count * (S::REC / 4); q += kRecordThreads) dst[q] = stage[q];
 }
 
 Mat3 mat3(const double* p) {
@@ -602,9 +616,9 @@ void geometry_records(int l_max, std::int64_t E, const double* xyz, const double
                       int intervals, float* erec, hipStream_t s) {
     if (E == 0) return;
     if (l_max == 3)
-        k_edge_records<3><<<blocks_for(E, 256), 256, 0, s>>>(E, xyz, r, r_cut, x0, h, intervals, erec);
+        k_edge_records<3><<<blocks_for(E, kRecordThreads), kRecordThreads, 0, s>>>(E, xyz, r, r_cut, x0, h, intervals, erec);
     else if (l_max == 2)
-        k_edge_records<2><<<blocks_for(E, 256), 256, 0, s>>>(E, xyz, r, r_cut, x0, h, intervals, erec);
+        k_edge_records<2><<<blocks_for(E, kRecordThreads), kRecordThreads, 0, s>>>(E, xyz, r, r_cut, x0, h, intervals, erec);
     else
         throw std::invalid_argument("edge records are compiled for l_max 2 and 3");
     SMX_LAUNCH_CHECK("edge_records");
