@@ -168,6 +168,43 @@ SMX_API int32_t smx_total_energy_device(SmxEvaluator* ev, double* total);
 SMX_API int32_t smx_device_outputs(SmxEvaluator* ev, SmxDeviceOutputs* out);
 SMX_API int32_t smx_synchronize(SmxEvaluator* ev);
 
+/* LAMMPS pair-style entry: the single-rank path of pair_style
+ * symmetrix/mace/kk without domain decomposition
+ * (pair_symmetrix_mace_kokkos.cpp:1010-1282), over the device arrays the
+ * Kokkos pair style holds.  Local atoms ilist[ii] are the graph's nodes; every
+ * neighbour j (local or ghost) of a full neighbour list becomes an edge to the
+ * local atom owner[j] (the pair style's atom->map(tag[j])), with
+ * xyz = x[j] - x[i] clamped to the model cutoff (r_cut/r scaling, the
+ * prepared-execution rule).  The topology is rebuilt when `rebuild` is set
+ * (neighbor->ago == 0), when inum or nall change, or after another graph was
+ * prepared on the evaluator; otherwise only the edge vectors are refreshed.
+ * Forces are added to f (ghost rows included; the caller's reverse
+ * communication folds them into their owners), per-atom energies to eatom
+ * (when non-NULL), and the total energy and the six virial components
+ * (xx, yy, zz, xy, xz, yz: sum over edges of xyz (x) f, symmetrised) are
+ * returned on the host.  Direct execution plan only (edge forces retained). */
+typedef struct SmxLammpsArgsV1 {
+    uint32_t struct_size;
+    int32_t inum;                  /* local atoms in ilist */
+    int32_t nall;                  /* local + ghost atoms (rows of x, type, owner, f) */
+    int32_t ntypes;                /* LAMMPS atom types */
+    const int32_t* ilist;          /* [inum] local atom indices */
+    const int32_t* numneigh;       /* [atom] neighbour count of each ilist atom */
+    const int32_t* neighbors;      /* neighbour j of atom i at i*stride_atom + jj*stride_neighbor;
+                                      bits above NEIGHMASK (0x1FFFFFFF) are masked off */
+    int64_t stride_atom;
+    int64_t stride_neighbor;
+    const double* x;               /* [nall][3] positions (Angstrom) */
+    const int32_t* type;           /* [nall] LAMMPS types, 1-based */
+    const int32_t* type_to_model;  /* [ntypes] model type index of LAMMPS type t+1 (-1: not mapped) */
+    const int32_t* owner;          /* [nall] local atom index each atom is an image of */
+    int32_t rebuild;               /* the neighbour list was rebuilt since the last call */
+    int32_t reserved;
+    double* f;                     /* [nall][3] forces, added to */
+    double* eatom;                 /* [nall] per-atom energies, added to; may be NULL */
+} SmxLammpsArgsV1;
+SMX_API int32_t smx_lammps_compute(SmxEvaluator* ev, const SmxLammpsArgsV1* args, double* energy, double* virial);
+
 /* Stage buffers of the last evaluation (FP32, row-major node-major) for
  * stage-level parity checks: "A0", "M0", "H1", "Phi1", "A1", "A1_adj",
  * "dPhi1", "H1_adj", "M0_adj", "A0_adj", "edge_records".  Returns the

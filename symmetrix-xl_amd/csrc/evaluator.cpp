@@ -949,6 +949,116 @@ struct Evaluator {
         }
     }
 
+    // ---------------------------------------------------------- LAMMPS entry
+    // pair_symmetrix_mace_kokkos.cpp:1010-1282: topology on a rebuild,
+    // edge vectors every call, reductions into LAMMPS's per-atom arrays
+    DevBuf l_node_types, l_num_neigh, l_node_of_atom, l_neigh, l_neigh_types, l_lmp_j, l_joff, l_jedges, l_counts,
+        l_flag;
+    int l_inum = -1, l_nall = -1;
+    std::uint64_t l_generation = 0;
+    std::vector<int> l_ilist_host;
+
+    int read_flag(DevBuf& b) {
+        int v = 0;
+        SMX_HIP(hipMemcpyAsync(&v, b.as<int>(), sizeof(int), hipMemcpyDeviceToHost, stream));
+        SMX_HIP(hipStreamSynchronize(stream));
+        return v;
+    }
+
+    void lammps_topology(const SmxLammpsArgsV1& a, const LammpsList& L) {
+        const int inum = a.inum, nall = a.nall;
+        int* nt = static_cast<int*>(l_node_types.ensure(std::max(inum, 1) * sizeof(int)));
+        int* nn = static_cast<int*>(l_num_neigh.ensure(std::max(inum, 1) * sizeof(int)));
+        int* noa = static_cast<int*>(l_node_of_atom.ensure(std::max(nall, 1) * sizeof(int)));
+        int* flag = static_cast<int*>(l_flag.ensure(sizeof(int)));
+        launch_fill_zero(reinterpret_cast<float*>(flag), 1, stream);
+        lammps_nodes(inum, nall, L, nt, nn, noa, flag, stream);
+        if (read_flag(l_flag) != 0)
+            throw std::invalid_argument("LAMMPS ilist holds an atom outside [0, nall), a negative neighbour count "
+                                        "or a type without a model type");
+        std::vector<int> h_nn(inum), off(inum + 1, 0);
+        if (inum > 0) SMX_HIP(hipMemcpy(h_nn.data(), nn, sizeof(int) * inum, hipMemcpyDeviceToHost));
+        std::int64_t total = 0;
+        for (int ii = 0; ii < inum; ++ii) {
+            total += h_nn[ii];
+            if (total > kMaxEdges) throw std::invalid_argument("edge count exceeds the 32-bit graph limit");
+            off[ii + 1] = static_cast<int>(total);
+        }
+        DevBuf d_off;
+        upload(d_off, off, stream);
+        const std::size_t e = static_cast<std::size_t>(std::max<std::int64_t>(total, 1));
+        int* nb = static_cast<int*>(l_neigh.ensure(e * sizeof(int)));
+        int* nbt = static_cast<int*>(l_neigh_types.ensure(e * sizeof(int)));
+        int* lj = static_cast<int*>(l_lmp_j.ensure(e * sizeof(int)));
+        launch_fill_zero(reinterpret_cast<float*>(flag), 1, stream);
+        lammps_edges(inum, nall, L, d_off.as<int>(), noa, nb, nbt, lj, flag, stream);
+        if (read_flag(l_flag) != 0)
+            throw std::invalid_argument("LAMMPS neighbour outside [0, nall), with an owner that is not a local "
+                                        "ilist atom, or with an unmapped type");
+        prepare_graph_device(inum, nt, nn, total, nb, nbt);
+        int* joff = static_cast<int*>(l_joff.ensure((static_cast<std::size_t>(nall) + 1) * sizeof(int)));
+        int* jed = static_cast<int*>(l_jedges.ensure(e * sizeof(int)));
+        int* cnt = static_cast<int*>(l_counts.ensure(std::max(nall, 1) * sizeof(int)));
+        launch_transpose(nall, total, lj, joff, jed, cnt, stream);
+        l_inum = inum;
+        l_nall = nall;
+        l_generation = generation;
+    }
+
+    void lammps_compute(const SmxLammpsArgsV1& a, double* energy, double* virial6) {
+        if (a.struct_size < sizeof(SmxLammpsArgsV1)) throw std::invalid_argument("SmxLammpsArgsV1.struct_size is too small");
+        if (a.inum < 0 || a.nall < a.inum || a.ntypes < 1)
+            throw std::invalid_argument("LAMMPS counts are invalid (0 <= inum <= nall, ntypes >= 1)");
+        if (a.inum > 0 && (!a.ilist || !a.numneigh || !a.neighbors))
+            throw std::invalid_argument("LAMMPS neighbour list arrays are required");
+        if (a.nall > 0 && (!a.x || !a.type || !a.owner || !a.f))
+            throw std::invalid_argument("LAMMPS per-atom arrays (x, type, owner, f) are required");
+        if (!a.type_to_model) throw std::invalid_argument("the LAMMPS type map is required");
+        if (a.stride_atom < 0 || a.stride_neighbor < 0) throw std::invalid_argument("neighbour strides must be >= 0");
+        const LammpsList L{a.ilist, a.numneigh, a.neighbors, a.stride_atom, a.stride_neighbor, a.type,
+                           a.type_to_model, a.ntypes, a.owner};
+        if (a.rebuild || l_generation == 0 || l_generation != generation || a.inum != l_inum || a.nall != l_nall)
+            lammps_topology(a, L);
+        if (tiled)
+            throw std::domain_error("the LAMMPS entry needs the direct execution plan (per-edge forces); "
+                                    "this graph was planned as tiles");
+        // edge vectors of this call
+        launch_fill_zero(reinterpret_cast<float*>(d_invalid.as<int>()), 1, stream);
+        lammps_geometry(E, d_receivers.as<int>(), a.ilist, l_lmp_j.as<int>(), a.x, hm.r_cut, d_xyz.as<double>(),
+                        d_r.as<double>(), d_invalid.as<int>(), stream);
+        xyz_host = true;
+        evaluate(nullptr);
+        // reductions into the LAMMPS arrays
+        lammps_forces(a.nall, l_joff.as<int>(), l_jedges.as<int>(), l_node_of_atom.as<int>(), d_offsets.as<int>(),
+                      ws.node_forces, a.f, stream);
+        if (a.eatom) lammps_eatom(a.inum, a.ilist, ws.node_energies, a.eatom, stream);
+        launch_energy_sum(N, ws.node_energies, d_total.as<double>(), stream);
+        launch_fill_zero(d_virial.as<double>(), 9, stream);
+        launch_virial_accumulate(E, ws.node_forces, d_xyz.as<double>(), d_stress_partial.as<double>(), stress_blocks,
+                                 d_virial.as<double>(), stream);
+        double total = 0.0, w[9];
+        int invalid = 0;
+        SMX_HIP(hipMemcpyAsync(&total, d_total.as<double>(), sizeof(double), hipMemcpyDeviceToHost, stream));
+        SMX_HIP(hipMemcpyAsync(w, d_virial.as<double>(), sizeof(w), hipMemcpyDeviceToHost, stream));
+        SMX_HIP(hipMemcpyAsync(&invalid, d_invalid.as<int>(), sizeof(int), hipMemcpyDeviceToHost, stream));
+        sync();
+        if (invalid > 0) {
+            evaluated = false;
+            throw std::invalid_argument("LAMMPS positions produced an invalid edge geometry (" +
+                                        std::to_string(invalid) + " zero-length or non-finite edges)");
+        }
+        // w[a*3+b] = sum_e f_a xyz_b; LAMMPS order xx, yy, zz, xy, xz, yz
+        if (energy) *energy = total;
+        if (virial6) {
+            virial6[0] = w[0];
+            virial6[1] = w[4];
+            virial6[2] = w[8];
+            virial6[3] = 0.5 * (w[1] + w[3]);
+            virial6[4] = 0.5 * (w[2] + w[6]);
+            virial6[5] = 0.5 * (w[5] + w[7]);
+        }
+    }
+
     const double* node_forces_device() const {
         if (tiled) throw std::logic_error("directed edge forces are not retained by the tiled execution plan");
         return ws.node_forces;
@@ -1267,6 +1377,13 @@ int32_t smx_device_outputs(SmxEvaluator* ev, SmxDeviceOutputs* out) {
         out->total_energy = e.d_total.as<double>();
         out->xyz = e.d_xyz.as<double>();
         out->r = e.d_r.as<double>();
+    });
+}
+
+int32_t smx_lammps_compute(SmxEvaluator* ev, const SmxLammpsArgsV1* args, double* energy, double* virial) {
+    return guarded([&] {
+        if (!args) throw std::invalid_argument("LAMMPS arguments are required");
+        E(ev).lammps_compute(*args, energy, virial);
     });
 }
 

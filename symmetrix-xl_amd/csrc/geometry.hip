@@ -532,35 +532,41 @@ void build_neighbor_list(int N, const double* positions_host, const double* cell
     release();
 }
 
-void launch_graph_schedule(int N, std::int64_t E, const int* offsets, const int* sources, int* receivers, int* soff,
-                           int* sedges, int* scratch_counts, hipStream_t s) {
-    if (N == 0) return;
-    k_receivers<<<blocks_for(N, 256), 256, 0, s>>>(N, offsets, receivers);
-    SMX_LAUNCH_CHECK("graph_receivers");
-    SMX_HIP(hipMemsetAsync(scratch_counts, 0, sizeof(int) * N, s));
+void launch_transpose(int K, std::int64_t E, const int* keys, int* koff, int* kedges, int* scratch_counts,
+                      hipStream_t s) {
+    if (K == 0) return;
+    SMX_HIP(hipMemsetAsync(scratch_counts, 0, sizeof(int) * K, s));
     if (E > 0) {
-        k_count_sources<<<blocks_for(E, 256), 256, 0, s>>>(E, sources, scratch_counts);
-        SMX_LAUNCH_CHECK("graph_count_sources");
+        k_count_sources<<<blocks_for(E, 256), 256, 0, s>>>(E, keys, scratch_counts);
+        SMX_LAUNCH_CHECK("transpose_count");
     }
-    long long* off64 = dev_alloc<long long>(N + 1);
+    long long* off64 = dev_alloc<long long>(K + 1);
     try {
-        device_exclusive_scan(scratch_counts, off64, N, s);
-        k_copy_i64_i32_plus<<<blocks_for(N + 1, 256), 256, 0, s>>>(off64, soff, N);
-        SMX_LAUNCH_CHECK("graph_source_offsets");
-        k_i64_to_i32<<<blocks_for(N, 256), 256, 0, s>>>(off64, scratch_counts, N);
-        SMX_LAUNCH_CHECK("graph_source_cursor");
+        device_exclusive_scan(scratch_counts, off64, K, s);
+        k_copy_i64_i32_plus<<<blocks_for(K + 1, 256), 256, 0, s>>>(off64, koff, K);
+        SMX_LAUNCH_CHECK("transpose_offsets");
+        k_i64_to_i32<<<blocks_for(K, 256), 256, 0, s>>>(off64, scratch_counts, K);
+        SMX_LAUNCH_CHECK("transpose_cursor");
         if (E > 0) {
-            k_fill_sources<<<blocks_for(E, 256), 256, 0, s>>>(E, sources, scratch_counts, sedges);
-            SMX_LAUNCH_CHECK("graph_fill_sources");
+            k_fill_sources<<<blocks_for(E, 256), 256, 0, s>>>(E, keys, scratch_counts, kedges);
+            SMX_LAUNCH_CHECK("transpose_fill");
         }
-        k_sort_segments<<<blocks_for(N, 256), 256, 0, s>>>(N, off64, sedges);
-        SMX_LAUNCH_CHECK("graph_sort_sources");
+        k_sort_segments<<<blocks_for(K, 256), 256, 0, s>>>(K, off64, kedges);
+        SMX_LAUNCH_CHECK("transpose_sort");
         SMX_HIP(hipStreamSynchronize(s));
     } catch (...) {
         (void)hipFree(off64);
         throw;
     }
     SMX_HIP(hipFree(off64));
+}
+
+void launch_graph_schedule(int N, std::int64_t E, const int* offsets, const int* sources, int* receivers, int* soff,
+                           int* sedges, int* scratch_counts, hipStream_t s) {
+    if (N == 0) return;
+    k_receivers<<<blocks_for(N, 256), 256, 0, s>>>(N, offsets, receivers);
+    SMX_LAUNCH_CHECK("graph_receivers");
+    launch_transpose(N, E, sources, soff, sedges, scratch_counts, s);
 }
 
 void launch_gather_types(std::int64_t E, const int* sources, const int* node_types, int* neigh_types,

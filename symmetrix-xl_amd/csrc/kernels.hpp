@@ -280,6 +280,36 @@ void build_neighbor_list(int N, const double* positions_host, const double* cell
 // Edge receivers and source transpose from a receiver CSR (all on device).
 void launch_graph_schedule(int N, std::int64_t E, const int* offsets, const int* sources, int* receivers,
                            int* soff, int* sedges, int* scratch_counts, hipStream_t s);
+// LAMMPS pair-style entry (lammps.hip): a full neighbour list as the Kokkos
+// pair style holds it, on the device.
+struct LammpsList {
+    const int* ilist;
+    const int* numneigh;
+    const int* neighbors;
+    long long stride_atom, stride_neighbor;
+    const int* type;
+    const int* type_to_model;
+    int ntypes;
+    const int* owner;
+};
+// node_types/num_neigh of the ilist atoms and node_of_atom[atom] (-1 when
+// not in ilist); bad counts unmapped types and negative counts
+void lammps_nodes(int inum, int nall, const LammpsList& L, int* node_types, int* num_neigh, int* node_of_atom,
+                  int* bad, hipStream_t s);
+// edges of each node (offsets from num_neigh): node of the owner, its model
+// type and the LAMMPS index of the neighbour
+void lammps_edges(int inum, int nall, const LammpsList& L, const int* offsets, const int* node_of_atom, int* neigh,
+                  int* neigh_types, int* lmp_j, int* bad, hipStream_t s);
+void lammps_geometry(std::int64_t E, const int* receivers, const int* ilist, const int* lmp_j, const double* x,
+                     double r_cut, double* xyz, double* r, int* invalid, hipStream_t s);
+void lammps_forces(int nall, const int* joff, const int* jedges, const int* node_of_atom, const int* offsets,
+                   const double* node_forces, double* f, hipStream_t s);
+void lammps_eatom(int inum, const int* ilist, const double* node_energies, double* eatom, hipStream_t s);
+
+// Transpose of an edge -> key map (keys in [0, K)): koff[K+1] and kedges[E]
+// listing each key's edges in ascending edge order.  scratch_counts: K ints.
+void launch_transpose(int K, std::int64_t E, const int* keys, int* koff, int* kedges, int* scratch_counts,
+                      hipStream_t s);
 // neigh_types[e] = node_types[sources[e]]
 void launch_gather_types(std::int64_t E, const int* sources, const int* node_types, int* neigh_types,
                          hipStream_t s);

@@ -52,6 +52,16 @@ class SmxR1PluginIdentity(ctypes.Structure):
                 ("persistent_blocks_per_compute_unit", ctypes.c_int32)]
 
 
+class SmxLammpsArgsV1(ctypes.Structure):
+    """Arguments of smx_lammps_compute (device pointers as integers)."""
+    _fields_ = [("struct_size", ctypes.c_uint32), ("inum", ctypes.c_int32), ("nall", ctypes.c_int32),
+                ("ntypes", ctypes.c_int32), ("ilist", ctypes.c_void_p), ("numneigh", ctypes.c_void_p),
+                ("neighbors", ctypes.c_void_p), ("stride_atom", ctypes.c_int64),
+                ("stride_neighbor", ctypes.c_int64), ("x", ctypes.c_void_p), ("type", ctypes.c_void_p),
+                ("type_to_model", ctypes.c_void_p), ("owner", ctypes.c_void_p), ("rebuild", ctypes.c_int32),
+                ("reserved", ctypes.c_int32), ("f", ctypes.c_void_p), ("eatom", ctypes.c_void_p)]
+
+
 # (name, restype, argtypes) of every exported entry point
 _i32 = ctypes.c_int32
 _i64 = ctypes.c_int64
@@ -91,6 +101,8 @@ SIGNATURES = [
     ("smx_total_energy_device", _i32, [_vp, _vp]),
     ("smx_device_outputs", _i32, [_vp, ctypes.POINTER(SmxDeviceOutputs)]),
     ("smx_synchronize", _i32, [_vp]),
+    ("smx_lammps_compute", _i32, [_vp, ctypes.POINTER(SmxLammpsArgsV1), ctypes.POINTER(_dbl),
+                                  ctypes.POINTER(_dbl)]),
     ("smx_debug_stage", _i32, [_vp, _cp, _vp, _i64, _p_i64]),
     ("smx_set_kernel_timing", _i32, [_vp, _i32]),
     ("smx_set_kernel_timing_filter", _i32, [_vp, _cp]),

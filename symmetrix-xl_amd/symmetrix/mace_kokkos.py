@@ -216,6 +216,18 @@ class MACEKokkosFloat:
         check(lib.smx_debug_stage(self._h, name.encode(), ptr(out), out.size, ctypes.byref(n)))
         return out
 
+    def _lammps_compute(self, args):
+        """smx_lammps_compute (the pair style's single-rank path) with an
+        SmxLammpsArgsV1 of device pointers; returns (energy, virial[6])."""
+        from ._native import SmxLammpsArgsV1
+        if not isinstance(args, SmxLammpsArgsV1):
+            raise TypeError("args must be an SmxLammpsArgsV1")
+        args.struct_size = ctypes.sizeof(SmxLammpsArgsV1)
+        energy = ctypes.c_double()
+        virial = (ctypes.c_double * 6)()
+        check(lib.smx_lammps_compute(self._h, ctypes.byref(args), ctypes.byref(energy), virial))
+        return energy.value, np.array(virial[:])
+
     def set_kernel_timing(self, enabled=True):
         check(lib.smx_set_kernel_timing(self._h, 1 if enabled else 0))
 

@@ -1,0 +1,164 @@
+"""The LAMMPS pair-style entry (smx_lammps_compute) against the oracle.
+
+The inputs are built the way LAMMPS holds them for pair_style
+symmetrix/mace/kk without domain decomposition
+(pair_symmetrix_mace_kokkos.cpp:1010-1282): local atoms plus ghost images
+of the periodic cell, 1-based atom types with a type map, a full neighbour
+list in a column-major (Kokkos LayoutLeft) array with special-bond bits set
+on some entries, an ilist that is not the identity, and atom->map(tag) as
+`owner`.  Forces land on local and ghost rows; folded onto their owners they
+must equal the oracle's periodic forces, the energy and per-atom energies
+the oracle's, and -virial/V the oracle's stress.  A second call without a
+neighbour-list rebuild uses moved positions on the same list.
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+E_TOL = 1e-5   # eV/atom
+F_TOL = 1e-4   # eV/A
+S_TOL = 1e-6   # eV/A^3
+
+
+class _Hip:
+    def __init__(self):
+        h = ctypes.CDLL("libamdhip64.so")
+        h.hipMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]
+        h.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+        h.hipFree.argtypes = [ctypes.c_void_p]
+        self.h = h
+        self.held = []
+
+    def put(self, a):
+        a = np.ascontiguousarray(a)
+        p = ctypes.c_void_p()
+        assert self.h.hipMalloc(ctypes.byref(p), max(a.nbytes, 8)) == 0
+        if a.nbytes:
+            assert self.h.hipMemcpy(p, a.ctypes.data_as(ctypes.c_void_p), a.nbytes, 1) == 0
+        self.held.append(p)
+        return p.value
+
+    def get(self, ptr, like):
+        out = np.empty_like(like)
+        assert self.h.hipMemcpy(out.ctypes.data_as(ctypes.c_void_p), ctypes.c_void_p(ptr), out.nbytes, 2) == 0
+        return out
+
+    def free(self):
+        for p in self.held:
+            self.h.hipFree(p)
+        self.held = []
+
+
+def _lammps_arrays(positions, cell, numbers, cutoff, lmp_type_of_z):
+    """Local atoms, 26 ghost images, full neighbour list within cutoff."""
+    n = len(positions)
+    shifts = [np.array([a, b, c]) for a in (-1, 0, 1) for b in (-1, 0, 1) for c in (-1, 0, 1)
+              if (a, b, c) != (0, 0, 0)]
+    allpos = np.concatenate([positions] + [positions + s @ cell for s in shifts])
+    owner = np.tile(np.arange(n, dtype=np.int32), 1 + len(shifts))
+    types = np.array([lmp_type_of_z[int(z)] for z in numbers], np.int32)
+    alltypes = np.tile(types, 1 + len(shifts))
+    rows = []
+    for i in range(n):
+        d = np.linalg.norm(allpos - positions[i], axis=1)
+        js = np.nonzero(d < cutoff)[0]
+        rows.append(js[js != i].astype(np.int32))
+    return allpos, owner, alltypes, rows
+
+
+def _run(ev, hip, allpos, owner, alltypes, rows, ilist, type_to_model, rebuild):
+    from symmetrix._native import SmxLammpsArgsV1
+    n, nall = len(rows), len(allpos)
+    maxn = max(len(r) for r in rows)
+    # column-major [maxn][n] with special-bond bits on every 7th entry
+    nb = np.zeros((maxn, n), np.int32)
+    for i, r in enumerate(rows):
+        marked = r.copy()
+        marked[::7] |= (1 << 30)
+        nb[:len(r), i] = marked
+    numneigh = np.array([len(r) for r in rows], np.int32)
+    f = np.zeros((nall, 3))
+    eatom = np.zeros(nall)
+    a = SmxLammpsArgsV1()
+    a.inum, a.nall, a.ntypes = n, nall, len(type_to_model)
+    a.ilist = hip.put(ilist)
+    a.numneigh = hip.put(numneigh)
+    a.neighbors = hip.put(nb)
+    a.stride_atom, a.stride_neighbor = 1, n
+    a.x = hip.put(allpos)
+    a.type = hip.put(alltypes)
+    a.type_to_model = hip.put(np.asarray(type_to_model, np.int32))
+    a.owner = hip.put(owner)
+    a.rebuild = 1 if rebuild else 0
+    a.f = hip.put(f)
+    a.eatom = hip.put(eatom)
+    energy, virial = ev._lammps_compute(a)
+    return energy, virial, hip.get(a.f, f), hip.get(a.eatom, eatom)
+
+
+def test_lammps_entry_matches_oracle(tiny_model_path):
+    from oracle import oracle
+    from symmetrix import systems
+    from symmetrix.mace_kokkos import MACEKokkosFloat
+    s = systems.srtio3_supercell(3, sigma=0.05, seed=0)
+    om = oracle.OracleModel(tiny_model_path)
+    ref = oracle.evaluate_system(om, s, skin=0.5)
+    ev = MACEKokkosFloat(tiny_model_path)
+    # LAMMPS types: O=1, Ti=2, Sr=3 ; model types follow the model's atomic numbers
+    lmp_type_of_z = {8: 1, 22: 2, 38: 3}
+    model_of_z = {int(z): k for k, z in enumerate(ev.atomic_numbers)}
+    type_to_model = [model_of_z[8], model_of_z[22], model_of_z[38]]
+    cell = np.asarray(s["cell"], float)
+    V = abs(np.linalg.det(cell))
+    n = len(s["numbers"])
+    allpos, owner, alltypes, rows = _lammps_arrays(s["positions"], cell, s["numbers"], ev.r_cut + 0.5,
+                                                   lmp_type_of_z)
+    assert sum(len(r) for r in rows) == len(ref["graph"]["sources"])
+    ilist = np.arange(n, dtype=np.int32)[::-1].copy()
+    hip = _Hip()
+    try:
+        for step, pos in enumerate([s["positions"],
+                                    s["positions"] + 0.03 * np.random.default_rng(1).normal(size=(n, 3))]):
+            if step:
+                ref = oracle.evaluate_system(om, s, skin=0.5, positions=pos, graph=ref["graph"])
+                shifts = allpos - s["positions"][owner]
+                allpos_step = pos[owner] + shifts
+            else:
+                allpos_step = allpos
+            energy, virial, f, eatom = _run(ev, hip, allpos_step, owner, alltypes, rows, ilist, type_to_model,
+                                            rebuild=(step == 0))
+            folded = np.zeros((n, 3))
+            np.add.at(folded, owner, f)
+            print("step %d energy/atom err %.3e force err %.3e" % (
+                step, abs(energy - ref["energy"]) / n, np.max(np.abs(folded - ref["forces"]))))
+            assert abs(energy - ref["energy"]) / n < E_TOL
+            np.testing.assert_allclose(eatom[:n], ref["energies"], rtol=0, atol=1e-4)
+            assert np.all(eatom[n:] == 0.0)
+            assert np.max(np.abs(folded - ref["forces"])) < F_TOL
+            st = ref["stress"]
+            mine = -np.array(virial) / V
+            expect = [st[0, 0], st[1, 1], st[2, 2], 0.5 * (st[0, 1] + st[1, 0]), 0.5 * (st[0, 2] + st[2, 0]),
+                      0.5 * (st[1, 2] + st[2, 1])]
+            np.testing.assert_allclose(mine, expect, rtol=0, atol=S_TOL)
+    finally:
+        hip.free()
+
+
+def test_lammps_entry_rejects_unmapped_types(tiny_model_path):
+    from symmetrix import systems
+    from symmetrix.mace_kokkos import MACEKokkosFloat
+    s = systems.srtio3_supercell(3, sigma=0.05, seed=0)
+    ev = MACEKokkosFloat(tiny_model_path)
+    cell = np.asarray(s["cell"], float)
+    allpos, owner, alltypes, rows = _lammps_arrays(s["positions"], cell, s["numbers"], ev.r_cut + 0.5,
+                                                   {8: 1, 22: 2, 38: 3})
+    hip = _Hip()
+    try:
+        with pytest.raises(ValueError, match="type"):
+            _run(ev, hip, allpos, owner, alltypes, rows, np.arange(len(rows), dtype=np.int32), [0, -1, 2], True)
+    finally:
+        hip.free()
