@@ -86,6 +86,10 @@ SMX_API void smx_evaluator_destroy(SmxEvaluator* ev);
 SMX_API int32_t smx_evaluator_info(const SmxEvaluator* ev, SmxModelInfo* info);
 /* atomic_numbers property (pybind mace_kokkos.cpp:1896) */
 SMX_API int32_t smx_evaluator_atomic_numbers(const SmxEvaluator* ev, int32_t* out, int32_t capacity);
+/* selected_head / available_heads (mace_kokkos.cpp:1904-1905): index -1 gives
+ * the head in use ("" when the file names none), index 0.. the heads the
+ * file stores (NULL past the end).  The strings live as long as ev. */
+SMX_API int32_t smx_prediction_head(const SmxEvaluator* ev, int32_t index, const char** name);
 /* set_streamed_edges (mace_kokkos.hpp:93); only "direct" is implemented. */
 SMX_API int32_t smx_set_streamed_edges(SmxEvaluator* ev, const char* mode);
 /* hipStream_t the evaluator enqueues on */

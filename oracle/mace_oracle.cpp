@@ -512,8 +512,26 @@ struct Mace {
         return o;
     }
 
-    void load(const std::string& path) {
+    // prediction_heads.hpp:10-88: the selected head's payload (its atomic
+    // energies, readouts and zbl_c) stands in for the top-level fields
+    std::string selected_head;
+
+    void load(const std::string& path, const std::string& head = "") {
         const Value j = json_lite::parse_file(path);
+        const Value* payload = nullptr;
+        if (const Value* ph = j.find("prediction_heads")) {
+            selected_head = head.empty() ? ph->at("default").as_string() : head;
+            payload = ph->at("parameters").find(selected_head);
+            if (!payload) throw std::invalid_argument("prediction head '" + selected_head + "' is not in the model");
+        } else {
+            selected_head = j.get_string("head", "");
+            if (!head.empty() && head != selected_head)
+                throw std::invalid_argument("prediction head '" + head + "' is not in the model");
+        }
+        auto field = [&](const char* name) -> const Value& {
+            if (payload && payload->contains(name)) return payload->at(name);
+            return j.at(name);
+        };
         if (j.get_int("symmetrix_format_version", 1) != 4)
             throw std::invalid_argument("only Symmetrix MACE format version 4 is supported");
         if (j.get_string("h1_affine_mode", "") != "m0_composite")
@@ -532,12 +550,12 @@ struct Mace {
         num_LM = (L_max + 1) * (L_max + 1);
         if (l_max > 3 || L_max > l_max) throw std::invalid_argument("l_max must be <= 3");
         atomic_numbers = j.at("atomic_numbers").as_ints();
-        atomic_energies = j.at("atomic_energies").as_doubles();
+        atomic_energies = field("atomic_energies").as_doubles();
         radial.load(j.at("compact_radial"), r_cut);
         // mace_kokkos_model.cpp:191-198
         has_zbl = j.at("has_zbl").as_bool();
         if (has_zbl)
-            zbl.init(j.at("zbl_a_exp").as_number(), j.at("zbl_a_prefactor").as_number(), j.at("zbl_c").as_doubles(),
+            zbl.init(j.at("zbl_a_exp").as_number(), j.at("zbl_a_prefactor").as_number(), field("zbl_c").as_doubles(),
                      j.at("zbl_covalent_radii").as_doubles(), j.at("zbl_p").as_int());
         // mace_kokkos_model.cpp:200,215-216,1109,1122-1123
         A0_scaled = j.at("A0_scaled").as_bool();
@@ -617,10 +635,10 @@ struct Mace {
             H2_M1.resize(w.size());
             for (std::size_t i = 0; i < w.size(); ++i) H2_M1[i] = static_cast<double>(cast(w[i]));
         }
-        q = j.at("readout_1_weights_for_M0").as_doubles();
+        q = field("readout_1_weights_for_M0").as_doubles();
         hidden = j.get_int("readout_2_hidden_size", 16);
-        W1 = j.at("readout_2_weights_1").as_doubles();
-        W2 = j.at("readout_2_weights_2").as_doubles();
+        W1 = field("readout_2_weights_1").as_doubles();
+        W2 = field("readout_2_weights_2").as_doubles();
         readout_scale = j.at("readout_2_scale_factor").as_number();
         if (W1.size() != static_cast<std::size_t>(hidden) * C || W2.size() != static_cast<std::size_t>(hidden))
             throw std::invalid_argument("readout weights do not match the hidden size");
@@ -1386,18 +1404,21 @@ extern "C" {
 
 const char* oracle_last_error() { return oracle::last_error.c_str(); }
 
-void* oracle_load(const char* path, int fp64) {
+void* oracle_load_head(const char* path, const char* head, int fp64) {
     try {
-        auto* h = new OracleHandle();
+        auto h = std::make_unique<OracleHandle>();
         h->fp64 = fp64;
-        if (fp64) { h->d = std::make_unique<Mace<double>>(); h->d->load(path); }
-        else { h->f = std::make_unique<Mace<float>>(); h->f->load(path); }
-        return h;
+        const std::string hd = head ? head : "";
+        if (fp64) { h->d = std::make_unique<Mace<double>>(); h->d->load(path, hd); }
+        else { h->f = std::make_unique<Mace<float>>(); h->f->load(path, hd); }
+        return h.release();
     } catch (const std::exception& ex) {
         oracle::last_error = ex.what();
         return nullptr;
     }
 }
+
+void* oracle_load(const char* path, int fp64) { return oracle_load_head(path, "", fp64); }
 
 void oracle_free(void* h) { delete static_cast<OracleHandle*>(h); }
 

@@ -36,6 +36,8 @@ def lib():
         L.oracle_last_error.restype = ctypes.c_char_p
         L.oracle_load.restype = ctypes.c_void_p
         L.oracle_load.argtypes = [ctypes.c_char_p, ctypes.c_int]
+        L.oracle_load_head.restype = ctypes.c_void_p
+        L.oracle_load_head.argtypes = [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_int]
         L.oracle_free.argtypes = [ctypes.c_void_p]
         L.oracle_info.argtypes = [ctypes.c_void_p, _i32p, ctypes.POINTER(ctypes.c_double)]
         L.oracle_atomic_numbers.argtypes = [ctypes.c_void_p, _i32p]
@@ -87,8 +89,8 @@ def _c(a, dt):
 class OracleModel:
     """The oracle evaluator for one model file, FP32 (default) or FP64."""
 
-    def __init__(self, path, fp64=False):
-        self._h = lib().oracle_load(path.encode(), 1 if fp64 else 0)
+    def __init__(self, path, fp64=False, head=""):
+        self._h = lib().oracle_load_head(path.encode(), (head or "").encode(), 1 if fp64 else 0)
         if not self._h:
             raise ValueError(_err())
         info = np.zeros(10, dtype=np.int32)

@@ -1219,6 +1219,18 @@ int32_t smx_evaluator_atomic_numbers(const SmxEvaluator* ev, int32_t* out, int32
     });
 }
 
+int32_t smx_prediction_head(const SmxEvaluator* ev, int32_t index, const char** name) {
+    return guarded([&] {
+        if (!name) throw std::invalid_argument("name output is required");
+        const auto& hm = E(ev).hm;
+        if (index < 0)
+            *name = hm.selected_head.c_str();
+        else
+            *name = index < static_cast<int32_t>(hm.available_heads.size()) ? hm.available_heads[index].c_str()
+                                                                             : nullptr;
+    });
+}
+
 int32_t smx_set_streamed_edges(SmxEvaluator* ev, const char* mode) {
     return guarded([&] {
         auto& e = E(ev);

@@ -224,20 +224,91 @@ void transpose_blocks(const std::vector<float>& src, std::vector<float>& dst, st
     }
 }
 
+void set_member(Value& obj, const std::string& key, const Value& v) {
+    for (auto& m : obj.members)
+        if (m.first == key) {
+            m.second = v;
+            return;
+        }
+    obj.members.emplace_back(key, v);
+}
+
+// Prediction heads (prediction_heads.hpp:10-88).  Without a
+// "prediction_heads" section the file's optional "head" names its only head.
+// With one, the section (schema 1) lists unique non-empty names, a default,
+// and per head exactly the fields that differ between heads (atomic
+// energies, both readouts, and zbl_c for ZBL models); the requested head, or
+// the default, replaces those top-level fields.
+void select_prediction_head(Value& j, const std::string& requested, std::string& selected,
+                            std::vector<std::string>& available) {
+    const Value* section = j.find("prediction_heads");
+    if (!section) {
+        const std::string legacy = j.get_string("head", "");
+        if (!requested.empty() && requested != legacy) {
+            if (legacy.empty())
+                throw std::invalid_argument("the model file names no prediction head, so head '" + requested +
+                                            "' cannot be selected");
+            throw std::invalid_argument("prediction head '" + requested + "' is not in the model (it holds '" +
+                                        legacy + "')");
+        }
+        selected = legacy;
+        available.clear();
+        if (!legacy.empty()) available.push_back(legacy);
+        return;
+    }
+    if (!section->is_object() || section->get_int("schema_version", 0) != 1)
+        throw std::invalid_argument("prediction_heads has an unsupported schema version");
+    const Value* names_v = section->find("names");
+    if (!names_v || !names_v->is_array()) throw std::invalid_argument("prediction_heads.names must be an array");
+    std::vector<std::string> names;
+    for (std::size_t i = 0; i < names_v->size(); ++i) names.push_back(names_v->at(i).as_string());
+    std::vector<std::string> sorted = names;
+    std::sort(sorted.begin(), sorted.end());
+    if (names.empty() || std::adjacent_find(sorted.begin(), sorted.end()) != sorted.end() || sorted.front().empty())
+        throw std::invalid_argument("prediction_heads.names must hold unique non-empty strings");
+    const Value* params = section->find("parameters");
+    if (!params || !params->is_object() || params->size() != names.size())
+        throw std::invalid_argument("prediction_heads.parameters must define every named head");
+    if (j.get_string("model_type", "MACE") == "MACE_Nonlinear")
+        throw std::invalid_argument("MACE_Nonlinear models are not supported");
+    std::vector<std::string> expected = {
+        "atomic_energies",
+        j.get_string("h1_affine_mode", "") == "pre_linear_up" ? "readout_1_weights_for_H1_pre_linear_up"
+                                                               : "readout_1_weights_for_M0",
+        "readout_2_weights_1", "readout_2_weights_2"};
+    if (j.get_bool("has_zbl", false)) expected.push_back("zbl_c");
+    std::sort(expected.begin(), expected.end());
+    for (const auto& name : names) {
+        const Value* p = params->find(name);
+        if (!p || !p->is_object()) throw std::invalid_argument("prediction_heads.parameters must define every named head");
+        std::vector<std::string> fields;
+        for (const auto& m : p->members) fields.push_back(m.first);
+        std::sort(fields.begin(), fields.end());
+        if (fields != expected)
+            throw std::invalid_argument("every prediction-head payload must hold exactly the per-head fields");
+    }
+    const std::string def = section->get_string("default", "");
+    if (std::find(names.begin(), names.end(), def) == names.end())
+        throw std::invalid_argument("prediction_heads.default must name a stored head");
+    selected = requested.empty() ? def : requested;
+    if (std::find(names.begin(), names.end(), selected) == names.end())
+        throw std::invalid_argument("prediction head '" + selected + "' is not in the model");
+    const Value payload = *params->find(selected);
+    for (const auto& m : payload.members) set_member(j, m.first, m.second);
+    Value hv;
+    hv.kind = Value::String;
+    hv.str = selected;
+    set_member(j, "head", hv);
+    available = names;
+}
+
 }  // namespace
 
 void HostModel::load(const std::string& path, const std::string& head) {
-    const Value j = json_lite::parse_file(path);
+    Value j = json_lite::parse_file(path);
     if (j.get_int("symmetrix_format_version", 1) != 4)
         throw std::invalid_argument("only Symmetrix MACE model format version 4 is supported");
-    if (!head.empty()) {
-        const Value* heads = j.find("heads");
-        bool found = false;
-        if (heads)
-            for (std::size_t i = 0; i < heads->size(); ++i)
-                if (heads->at(i).as_string() == head) found = true;
-        if (!found) throw std::invalid_argument("requested head '" + head + "' is not available in the model");
-    }
+    select_prediction_head(j, head, selected_head, available_heads);
     if (j.get_string("h1_affine_mode", "") != "m0_composite")
         throw std::invalid_argument("only h1_affine_mode 'm0_composite' is supported");
     if (j.get_string("radial_representation", "") != "compact")

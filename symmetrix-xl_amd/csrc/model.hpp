@@ -31,6 +31,9 @@ struct HostModel {
     int num_lm = 0, num_LM = 0;
     int num_interactions = 2;
     double r_cut = 0.0;
+    // prediction head in use and the heads the file stores
+    std::string selected_head;
+    std::vector<std::string> available_heads;
     std::vector<int> atomic_numbers;
     std::vector<double> atomic_energies;
 

@@ -81,6 +81,7 @@ SIGNATURES = [
     ("smx_evaluator_destroy", None, [_vp]),
     ("smx_evaluator_info", _i32, [_vp, ctypes.POINTER(SmxModelInfo)]),
     ("smx_evaluator_atomic_numbers", _i32, [_vp, _vp, _i32]),
+    ("smx_prediction_head", _i32, [_vp, _i32, ctypes.POINTER(ctypes.c_char_p)]),
     ("smx_set_streamed_edges", _i32, [_vp, _cp]),
     ("smx_evaluator_stream", _vp, [_vp]),
     ("smx_prepare_factorized_graph", _i32, [_vp, _i32, _vp, _vp, _i64, _vp, _vp, _p_u64]),

@@ -43,9 +43,20 @@ class MACEKokkosFloat:
         z = np.zeros(self.num_elements, dtype=np.int32)
         check(lib.smx_evaluator_atomic_numbers(self._h, ptr(z), len(z)))
         self._atomic_numbers = z
-        self.selected_head = head or ""
+        self.selected_head = self._head(-1)
+        self.available_heads = []
+        while True:
+            name = self._head(len(self.available_heads))
+            if name is None:
+                break
+            self.available_heads.append(name)
         self._num_nodes = 0
         self._num_edges = 0
+
+    def _head(self, index):
+        name = ctypes.c_char_p()
+        check(lib.smx_prediction_head(self._h, index, ctypes.byref(name)))
+        return None if name.value is None else name.value.decode()
 
     def close(self):
         if getattr(self, "_h", None):

@@ -59,6 +59,7 @@ class ModelConfig:
     energy_scale: float = 10.0
     density_scaled: bool = False
     zbl: bool = False
+    prediction_heads: bool = False
     seed: int = 0
 
 
@@ -69,6 +70,9 @@ MODEL_CONFIGS = {
     # tiny with A0/A1 density scaling (mace.cpp:1562-1636, 2381-2459)
     "tiny_scaled": ModelConfig("tiny_scaled", 32, 2, 1, 2, [8, 22, 38], radial_mlp=[32, 32],
                                r_cut=5.0, avg_num_neighbors=40.0, density_scaled=True),
+    # tiny with two prediction heads (prediction_heads.hpp)
+    "tiny_heads": ModelConfig("tiny_heads", 32, 2, 1, 2, [8, 22, 38], radial_mlp=[32, 32],
+                              r_cut=5.0, avg_num_neighbors=40.0, prediction_heads=True),
     # tiny with ZBL pair repulsion (zbl_kokkos.cpp)
     "tiny_zbl": ModelConfig("tiny_zbl", 32, 2, 1, 2, [8, 22, 38], radial_mlp=[32, 32],
                             r_cut=5.0, avg_num_neighbors=40.0, zbl=True),
@@ -273,6 +277,27 @@ def generate_model(config, seed=None):
     frag["readout_2_weights_2"] = _fmt(
         rng.normal(size=hid) / math.sqrt(hid) * cfg.energy_scale)
     put("readout_2_scale_factor", SILU_SCALE)
+    if cfg.prediction_heads:
+        # a "prediction_heads" section (schema 1, prediction_heads.hpp:30-88):
+        # the top-level fields are the default head "default"; a second head
+        # "finetune" has its own energies and readouts (second generator)
+        hrng = np.random.default_rng([seed, 2])
+        per_head = ["atomic_energies", "readout_1_weights_for_M0", "readout_2_weights_1",
+                    "readout_2_weights_2"] + (["zbl_c"] if cfg.zbl else [])
+        tuned = {
+            "atomic_energies": _fmt(np.asarray(json.loads(frag["atomic_energies"])) + 0.3 * hrng.normal(size=n_el)),
+            "readout_1_weights_for_M0": _fmt(hrng.normal(size=C) / math.sqrt(C) * cfg.energy_scale),
+            "readout_2_weights_1": _fmt(hrng.normal(size=(hid, C)) / math.sqrt(C)),
+            "readout_2_weights_2": _fmt(hrng.normal(size=hid) / math.sqrt(hid) * cfg.energy_scale),
+        }
+        if cfg.zbl:
+            tuned["zbl_c"] = json.dumps([0.2, 0.5, 0.27, 0.03])
+
+        def payload(src):
+            return "{" + ",".join('"%s":%s' % (k, src[k]) for k in per_head) + "}"
+        frag["prediction_heads"] = (
+            '{"schema_version":1,"names":["default","finetune"],"default":"default","parameters":{'
+            '"default":' + payload(frag) + ',"finetune":' + payload(tuned) + "}}")
     return frag
 
 

@@ -174,6 +174,37 @@ def test_zbl_efs_and_tiled_plan(tiny_zbl_model_path):
     np.testing.assert_allclose(f1, f, rtol=0, atol=1e-7)
     np.testing.assert_allclose(s1, st, rtol=0, atol=1e-9)
 
+
+def test_prediction_heads(tiny_heads_model_path, tiny_model_path, tmp_path):
+    """MACEKokkos(filename, head) (mace_kokkos.hpp:91; prediction_heads.hpp):
+    the head's energies and readouts are used, selected_head and
+    available_heads are reported, unknown heads and malformed sections are
+    refused; a file without a section names no head."""
+    import json
+    from symmetrix.mace_kokkos import MACEKokkosFloat
+    ora = _oracle()
+    s = _system("tiny")
+    ev = MACEKokkosFloat(tiny_heads_model_path, "finetune")
+    assert ev.selected_head == "finetune" and ev.available_heads == ["default", "finetune"]
+    assert MACEKokkosFloat(tiny_heads_model_path).selected_head == "default"
+    plain = MACEKokkosFloat(tiny_model_path)
+    assert plain.selected_head == "" and plain.available_heads == []
+    om = ora.OracleModel(tiny_heads_model_path, head="finetune")
+    ref = ora.evaluate_system(om, s, skin=0.5)
+    e, f, st = _run(ev, s, om.types_of(s["numbers"]))
+    _assert_efs(ref, e, f, st, len(e))
+    with pytest.raises(ValueError, match="not in the model"):
+        MACEKokkosFloat(tiny_heads_model_path, "absent")
+    with pytest.raises(ValueError, match="names no prediction head"):
+        MACEKokkosFloat(tiny_model_path, "finetune")
+    with open(tiny_heads_model_path) as fh:
+        j = json.load(fh)
+    j["prediction_heads"]["parameters"]["finetune"]["zbl_c"] = [0.1, 0.2, 0.3, 0.4]
+    bad = tmp_path / "bad_heads.json"
+    bad.write_text(json.dumps(j))
+    with pytest.raises(ValueError, match="per-head fields"):
+        MACEKokkosFloat(str(bad))
+
 def test_energy_forces_stress_medium(medium_model_path):
     s = _system("medium")
     om, ref, ev, g, e, f, st = _evaluate_both(medium_model_path, s)

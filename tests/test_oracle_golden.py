@@ -563,3 +563,30 @@ def test_zbl_forces_and_stress_are_energy_derivatives(tiny_zbl_model_path):
         t["cell"] = s["cell"] @ F.T
         return oracle.evaluate_system(m, t, skin=0.5)["energy"]
     assert base["stress"][0, 1] == pytest.approx((strained(+1) - strained(-1)) / (2 * h) / V, abs=1e-7)
+
+
+# ---------------------------------------------------------------------------
+# Prediction heads (prediction_heads.hpp)
+# ---------------------------------------------------------------------------
+def test_prediction_head_payload_replaces_the_top_level_fields(tiny_heads_model_path, tiny_model_path, tmp_path):
+    """Selecting a head equals a single-head file whose top-level fields are
+    that head's payload (prediction_heads.hpp:83-88); the default head is the
+    section's default; an unknown head is refused."""
+    with open(tiny_heads_model_path) as f:
+        j = json.load(f)
+    section = j.pop("prediction_heads")
+    flat = dict(j)
+    flat.update(section["parameters"]["finetune"])
+    flat_path = tmp_path / "finetune_flat.json"
+    flat_path.write_text(json.dumps(flat))
+    s = systems.srtio3_supercell(3, sigma=0.05, seed=0)
+    a = oracle.evaluate_system(oracle.OracleModel(tiny_heads_model_path, head="finetune"), s, skin=0.5)
+    b = oracle.evaluate_system(oracle.OracleModel(str(flat_path)), s, skin=0.5)
+    assert a["energies"].tobytes() == b["energies"].tobytes()
+    assert a["forces"].tobytes() == b["forces"].tobytes()
+    d = oracle.evaluate_system(oracle.OracleModel(tiny_heads_model_path), s, skin=0.5)
+    t = oracle.evaluate_system(oracle.OracleModel(tiny_model_path), s, skin=0.5)
+    assert d["energies"].tobytes() == t["energies"].tobytes()
+    assert abs(a["energy"] - d["energy"]) > 1.0
+    with pytest.raises(ValueError, match="not in the model"):
+        oracle.OracleModel(tiny_heads_model_path, head="absent")
