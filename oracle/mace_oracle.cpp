@@ -118,6 +118,10 @@ struct RadialModel {
     std::vector<double> bessel;
     Network R0, R1, A0, A1;
     bool has_R1 = false, has_A0 = false, has_A1 = false;
+    // Agnesi distance transform (compact_radial.cpp:144-163, 233-247)
+    bool agnesi = false;
+    double agnesi_a = 0, agnesi_q = 0, agnesi_p = 0;
+    std::vector<double> covalent_radii;  // per model type
 
     void load(const Value& def, double r_cut) {
         grid_min = def.at("spline_grid_min").as_number();
@@ -137,8 +141,17 @@ struct RadialModel {
         p = cut.at("p").as_int();
         if (std::abs(r_max - r_cut) > 1e-12)
             throw std::invalid_argument("compact radial cutoff does not match r_cut");
-        if (def.at("distance_transform").at("type").as_string() != "none")
-            throw std::invalid_argument("only distance_transform 'none' is supported");
+        const Value& tr = def.at("distance_transform");
+        const std::string tt = tr.at("type").as_string();
+        agnesi = tt == "agnesi";
+        if (agnesi) {
+            agnesi_a = tr.at("a").as_number();
+            agnesi_q = tr.at("q").as_number();
+            agnesi_p = tr.at("p").as_number();
+            covalent_radii = tr.at("covalent_radii").as_doubles();
+        } else if (tt != "none") {
+            throw std::invalid_argument("unsupported distance transform");
+        }
         const Value& nets = def.at("networks");
         R0 = parse_network(nets.at("R0"));
         if (nets.contains("R1")) { R1 = parse_network(nets.at("R1")); has_R1 = true; }
@@ -157,12 +170,25 @@ struct RadialModel {
         density("A1", A1, has_A1);
     }
 
-    // compact_radial.cpp:227-267 (no distance transform)
-    std::vector<double> features() const {
+    // compact_radial.cpp:227-267: the features of the pair (ti, tj) (model
+    // types); without a transform every pair has the same features
+    std::vector<double> features(int ti = 0, int tj = 0) const {
         const std::size_t nb = bessel.size();
         std::vector<double> f(static_cast<std::size_t>(points) * nb);
+        double r0 = 1.0;
+        if (agnesi) {
+            if (ti < 0 || tj < 0 || ti >= static_cast<int>(covalent_radii.size()) ||
+                tj >= static_cast<int>(covalent_radii.size()))
+                throw std::out_of_range("agnesi covalent radius index out of range");
+            r0 = 0.5 * (covalent_radii[ti] + covalent_radii[tj]);
+        }
         for (int node = 0; node < points; ++node) {
             const double r = grid_min + node * h;
+            double x = r;
+            if (agnesi) {
+                const double s = r / r0;
+                x = 1.0 / (1.0 + agnesi_a * std::pow(s, agnesi_q) / (1.0 + std::pow(s, agnesi_q - agnesi_p)));
+            }
             double cutoff_value = 0.0;
             if (r < r_max) {
                 const double s = r / r_max;
@@ -171,7 +197,7 @@ struct RadialModel {
                     - (p * (p + 1.0) / 2.0) * std::pow(s, p + 2);
             }
             for (std::size_t b = 0; b < nb; ++b)
-                f[node * nb + b] = prefactor * std::sin(bessel[b] * r) / r * cutoff_value;
+                f[node * nb + b] = prefactor * std::sin(bessel[b] * x) / x * cutoff_value;
         }
         return f;
     }
@@ -207,8 +233,8 @@ struct RadialModel {
 
     // Nodal values and derivatives [function][node] of a network on the grid.
     void tabulate(const Network& net, std::vector<std::vector<double>>& values,
-                  std::vector<std::vector<double>>& derivs) const {
-        const auto f = features();
+                  std::vector<std::vector<double>>& derivs, int ti = 0, int tj = 0) const {
+        const auto f = features(ti, tj);
         const int nout = net.shape.back();
         values.assign(nout, std::vector<double>(points));
         std::vector<double> out(nout);
@@ -484,7 +510,7 @@ struct Mace {
     std::vector<double> zbl_energies, zbl_forces;  // per node, per edge [3]
     // density scaling: FP64 splines of the A0/A1 networks (one function)
     bool A0_scaled = false, A1_scaled = false;
-    std::shared_ptr<SplineSet<double>> dens0, dens1;
+    std::vector<std::shared_ptr<SplineSet<double>>> dens0, dens1;  // per active pair
     std::vector<double> A0_scale, A1_scale;  // per node: 1 + sum_j f(r_ij)
 
     // state of the last evaluation (exposed for stage-level debugging)
@@ -654,9 +680,6 @@ struct Mace {
         for (int t : req)
             if (t < 0 || t >= num_elements) throw std::out_of_range("type index out of range");
         if (req == active_types) return;
-        std::vector<std::vector<double>> v0, d0, v1, d1;
-        radial.tabulate(radial.R0, v0, d0);
-        radial.tabulate(radial.R1, v1, d1);
         auto tof = [](const std::vector<std::vector<double>>& a) {
             std::vector<std::vector<P>> o(a.size());
             for (std::size_t i = 0; i < a.size(); ++i) o[i] = castv(a[i]);
@@ -665,31 +688,39 @@ struct Mace {
         const P hp = cast(radial.h), x0 = cast(radial.grid_min);
         spl0.clear();
         spl1.clear();
+        dens0.clear();
+        dens1.clear();
         const int na = static_cast<int>(req.size());
-        // features do not depend on the pair without a distance transform,
-        // so each pair's tables are the same tabulation
-        const auto fv0 = tof(v0), fd0 = tof(d0), fv1 = tof(v1), fd1 = tof(d1);
-        const auto s0 = std::make_shared<SplineSet<P>>(hp, fv0, fd0, x0);
-        const auto s1 = std::make_shared<SplineSet<P>>(hp, fv1, fd1, x0);
+        // one set of tables per active pair (a <= b); without a distance
+        // transform they are all the same tabulation
         for (int a = 0; a < na; ++a)
             for (int b = a; b < na; ++b) {
-                spl0.push_back(s0);
-                spl1.push_back(s1);
+                if (radial.agnesi || spl0.empty()) {
+                    const int ti = req[a], tj = req[b];
+                    std::vector<std::vector<double>> v0, d0, v1, d1;
+                    radial.tabulate(radial.R0, v0, d0, ti, tj);
+                    radial.tabulate(radial.R1, v1, d1, ti, tj);
+                    spl0.push_back(std::make_shared<SplineSet<P>>(hp, tof(v0), tof(d0), x0));
+                    spl1.push_back(std::make_shared<SplineSet<P>>(hp, tof(v1), tof(d1), x0));
+                    // RadialFunctionSetKokkos<double>(h, values, derivs, x0): FP64
+                    // coefficients and evaluation (mace_kokkos_factorized_lifecycle.cpp:4084-4091)
+                    if (A0_scaled) {
+                        std::vector<std::vector<double>> v, d;
+                        radial.tabulate(radial.A0, v, d, ti, tj);
+                        dens0.push_back(std::make_shared<SplineSet<double>>(radial.h, v, d, radial.grid_min));
+                    }
+                    if (A1_scaled) {
+                        std::vector<std::vector<double>> v, d;
+                        radial.tabulate(radial.A1, v, d, ti, tj);
+                        dens1.push_back(std::make_shared<SplineSet<double>>(radial.h, v, d, radial.grid_min));
+                    }
+                } else {
+                    spl0.push_back(spl0.front());
+                    spl1.push_back(spl1.front());
+                    if (A0_scaled) dens0.push_back(dens0.front());
+                    if (A1_scaled) dens1.push_back(dens1.front());
+                }
             }
-        // RadialFunctionSetKokkos<double>(h, values, derivs, x0): FP64
-        // coefficients and evaluation (mace_kokkos_factorized_lifecycle.cpp:4084-4091)
-        dens0.reset();
-        dens1.reset();
-        if (A0_scaled) {
-            std::vector<std::vector<double>> v, d;
-            radial.tabulate(radial.A0, v, d);
-            dens0 = std::make_shared<SplineSet<double>>(radial.h, v, d, radial.grid_min);
-        }
-        if (A1_scaled) {
-            std::vector<std::vector<double>> v, d;
-            radial.tabulate(radial.A1, v, d);
-            dens1 = std::make_shared<SplineSet<double>>(radial.h, v, d, radial.grid_min);
-        }
         type_to_active.assign(num_elements, -1);
         for (int a = 0; a < na; ++a) type_to_active[req[a]] = a;
         active_types = req;
@@ -719,11 +750,12 @@ struct Mace {
 
     // 1 + sum over every CSR edge of i (skin edges included, r clamped to the
     // cutoff) of f(r): the Kokkos team reduction then += 1.0
-    static double density_factor(const SplineSet<double>& sp, long long e0, long long e1, const double* r) {
+    double density_factor(const std::vector<std::shared_ptr<SplineSet<double>>>& sp, int type_i,
+                          const int* neigh_types, long long e0, long long e1, const double* r) const {
         double s = 0.0;
         for (long long e = e0; e < e1; ++e) {
             double f, d;
-            density_eval(sp, r[e], f, d);
+            density_eval(*sp[pair_index(type_i, neigh_types[e])], r[e], f, d);
             s += f;
         }
         return s + 1.0;
@@ -816,7 +848,7 @@ struct Mace {
             // A0 /= 1 + sum_j f0(r_ij), the division in FP64
             // (mace_kokkos_first_interaction.cpp:1383-1416)
             if (A0_scaled) {
-                const double sc = density_factor(*dens0, off[i], off[i + 1], r);
+                const double sc = density_factor(dens0, types[i], neigh_types, off[i], off[i + 1], r);
                 A0_scale[i] = sc;
                 P* a = &A0[static_cast<std::size_t>(i) * nY * Cs];
                 for (std::size_t v = 0; v < nY * Cs; ++v) a[v] = static_cast<P>(static_cast<double>(a[v]) / sc);
@@ -924,7 +956,7 @@ struct Mace {
             // A1 *= Precision(1 / (1 + sum_j f1(r_ij)))
             // (mace_kokkos_second_interaction.cpp:1449-1488)
             if (A1_scaled) {
-                const double sc = density_factor(*dens1, off[i], off[i + 1], r);
+                const double sc = density_factor(dens1, types[i], neigh_types, off[i], off[i + 1], r);
                 A1_scale[i] = sc;
                 const P inv = static_cast<P>(1.0 / sc);
                 P* a = &A1[static_cast<std::size_t>(i) * nY * Cs];
@@ -1009,7 +1041,7 @@ struct Mace {
                 for (std::size_t v = 0; v < nY * Cs; ++v) dot += static_cast<double>(adj[v] * a[v]);
                 for (long long e = off[i]; e < off[i + 1]; ++e) {
                     double f, d;
-                    density_eval(*dens1, r[e], f, d);
+                    density_eval(*dens1[pair_index(types[i], neigh_types[e])], r[e], f, d);
                     const double scale = dot / sc * d;
                     for (int c = 0; c < 3; ++c) density_forces[3 * e + c] += scale * (xyz[3 * e + c] / r[e]);
                 }
@@ -1181,7 +1213,7 @@ struct Mace {
                 for (std::size_t v = 0; v < nY * Cs; ++v) dot += static_cast<double>(adj[v] * a[v]);
                 for (long long e = off[i]; e < off[i + 1]; ++e) {
                     double f, d;
-                    density_eval(*dens0, r[e], f, d);
+                    density_eval(*dens0[pair_index(types[i], neigh_types[e])], r[e], f, d);
                     for (int c = 0; c < 3; ++c) density_forces[3 * e + c] += dot / sc * d * xyz[3 * e + c] / r[e];
                 }
                 for (std::size_t v = 0; v < nY * Cs; ++v) adj[v] = static_cast<P>(static_cast<double>(adj[v]) / sc);
@@ -1506,14 +1538,14 @@ long long oracle_stage(void* hv, const char* name, double* out, long long capaci
 // Radial nodal tables of the model on its spline grid (FP64):
 // which 0 = R0, 1 = R1, 2 = A0 density, 3 = A1 density; values/derivs
 // [function][point].
-int oracle_radial_tables(void* hv, int which, double* values, double* derivs, int* shape) {
+int oracle_radial_tables(void* hv, int which, int ti, int tj, double* values, double* derivs, int* shape) {
     return guarded([&]() -> int {
         auto* h = static_cast<OracleHandle*>(hv);
         const RadialModel& rm = h->fp64 ? h->d->radial : h->f->radial;
         if ((which == 2 && !rm.has_A0) || (which == 3 && !rm.has_A1) || which < 0 || which > 3)
             throw std::invalid_argument("the model has no such radial network");
         std::vector<std::vector<double>> v, d;
-        rm.tabulate(which == 0 ? rm.R0 : which == 1 ? rm.R1 : which == 2 ? rm.A0 : rm.A1, v, d);
+        rm.tabulate(which == 0 ? rm.R0 : which == 1 ? rm.R1 : which == 2 ? rm.A0 : rm.A1, v, d, ti, tj);
         shape[0] = static_cast<int>(v.size());
         shape[1] = rm.points;
         if (values)
@@ -1526,14 +1558,18 @@ int oracle_radial_tables(void* hv, int which, double* values, double* derivs, in
     });
 }
 
-int oracle_radial_features(void* hv, double* out, int* shape) {
-    auto* h = static_cast<OracleHandle*>(hv);
-    const RadialModel& rm = h->fp64 ? h->d->radial : h->f->radial;
-    const auto f = rm.features();
-    shape[0] = rm.points;
-    shape[1] = static_cast<int>(rm.bessel.size());
-    if (out) std::copy(f.begin(), f.end(), out);
-    return 0;
+// Features [point][basis] of the pair of model types (ti, tj) (the same for
+// every pair without a distance transform).
+int oracle_radial_features(void* hv, int ti, int tj, double* out, int* shape) {
+    return guarded([&]() -> int {
+        auto* h = static_cast<OracleHandle*>(hv);
+        const RadialModel& rm = h->fp64 ? h->d->radial : h->f->radial;
+        const auto f = rm.features(ti, tj);
+        shape[0] = rm.points;
+        shape[1] = static_cast<int>(rm.bessel.size());
+        if (out) std::copy(f.begin(), f.end(), out);
+        return 0;
+    });
 }
 
 // Spline derivative solve of arbitrary nodal values on a uniform grid of step h.

@@ -46,9 +46,9 @@ def lib():
         L.oracle_set_num_threads.argtypes = [ctypes.c_int]
         L.oracle_stage.restype = ctypes.c_longlong
         L.oracle_stage.argtypes = [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_void_p, ctypes.c_longlong]
-        L.oracle_radial_tables.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p,
-                                           ctypes.c_void_p, _i32p]
-        L.oracle_radial_features.argtypes = [ctypes.c_void_p, ctypes.c_void_p, _i32p]
+        L.oracle_radial_tables.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                           ctypes.c_void_p, ctypes.c_void_p, _i32p]
+        L.oracle_radial_features.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, _i32p]
         L.oracle_spline_derivatives.argtypes = [_f64p, ctypes.c_int, ctypes.c_double, _f64p]
         L.oracle_spline_eval_f32.argtypes = [ctypes.c_float, ctypes.c_float, ctypes.c_int, ctypes.c_int,
                                              _f32p, _f32p, _f64p, ctypes.c_int, _f32p, _f32p]
@@ -133,21 +133,24 @@ class OracleModel:
         lib().oracle_stage(self._h, name.encode(), out.ctypes.data, size)
         return out
 
-    def radial_tables(self, which):
+    def radial_tables(self, which, ti=0, tj=0):
+        """Nodal values and derivatives [function][point] of network which
+        (0 R0, 1 R1, 2 A0, 3 A1) for the pair of model types (ti, tj)."""
         shape = np.zeros(2, dtype=np.int32)
-        if lib().oracle_radial_tables(self._h, which, None, None, shape) != 0:
+        if lib().oracle_radial_tables(self._h, which, ti, tj, None, None, shape) != 0:
             raise ValueError(_err())
         v = np.zeros(int(shape[0]) * int(shape[1]))
         d = np.zeros_like(v)
-        if lib().oracle_radial_tables(self._h, which, v.ctypes.data, d.ctypes.data, shape) != 0:
+        if lib().oracle_radial_tables(self._h, which, ti, tj, v.ctypes.data, d.ctypes.data, shape) != 0:
             raise ValueError(_err())
         return v.reshape(shape), d.reshape(shape)
 
-    def radial_features(self):
+    def radial_features(self, ti=0, tj=0):
         shape = np.zeros(2, dtype=np.int32)
-        lib().oracle_radial_features(self._h, None, shape)
+        if lib().oracle_radial_features(self._h, ti, tj, None, shape) != 0:
+            raise ValueError(_err())
         out = np.zeros(int(shape[0]) * int(shape[1]))
-        lib().oracle_radial_features(self._h, out.ctypes.data, shape)
+        lib().oracle_radial_features(self._h, ti, tj, out.ctypes.data, shape)
         return out.reshape(shape)
 
 

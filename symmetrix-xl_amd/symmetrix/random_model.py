@@ -60,6 +60,7 @@ class ModelConfig:
     density_scaled: bool = False
     zbl: bool = False
     prediction_heads: bool = False
+    agnesi: bool = False
     seed: int = 0
 
 
@@ -73,6 +74,10 @@ MODEL_CONFIGS = {
     # tiny with two prediction heads (prediction_heads.hpp)
     "tiny_heads": ModelConfig("tiny_heads", 32, 2, 1, 2, [8, 22, 38], radial_mlp=[32, 32],
                               r_cut=5.0, avg_num_neighbors=40.0, prediction_heads=True),
+    # tiny with the Agnesi distance transform (per-pair radial tables,
+    # compact_radial.cpp:144-163,233-247)
+    "tiny_agnesi": ModelConfig("tiny_agnesi", 32, 2, 1, 2, [8, 22, 38], radial_mlp=[32, 32],
+                               r_cut=5.0, avg_num_neighbors=40.0, agnesi=True),
     # tiny with ZBL pair repulsion (zbl_kokkos.cpp)
     "tiny_zbl": ModelConfig("tiny_zbl", 32, 2, 1, 2, [8, 22, 38], radial_mlp=[32, 32],
                             r_cut=5.0, avg_num_neighbors=40.0, zbl=True),
@@ -85,6 +90,12 @@ MODEL_CONFIGS = {
     "wide": ModelConfig("wide", 256, 3, 2, 3, [1, 8], radial_mlp=[64, 64, 64],
                         r_cut=5.0, avg_num_neighbors=40.0),
 }
+
+
+# Cordero et al. (2008) covalent radii (Angstrom) of the elements the named
+# configs use; other elements get 1.5 A (the models are synthetic)
+_COVALENT_RADII = {1: 0.31, 6: 0.76, 7: 0.71, 8: 0.66, 13: 1.21, 14: 1.11, 22: 1.60, 26: 1.32, 29: 1.32,
+                   38: 1.95}
 
 
 def _f32(a):
@@ -191,7 +202,10 @@ def generate_model(config, seed=None):
         "basis": {"type": "bessel", "weights": bessel_w.tolist(),
                   "prefactor": float(_f32(math.sqrt(2.0 / r_cut)))},
         "cutoff": {"type": "polynomial", "r_max": r_cut, "p": cfg.cutoff_p},
-        "distance_transform": {"type": "none"},
+        "distance_transform": (
+            {"type": "agnesi", "a": 1.0805, "q": 0.9183, "p": 4.5791,
+             "covalent_radii": [_COVALENT_RADII.get(z, 1.5) for z in cfg.atomic_numbers]}
+            if cfg.agnesi else {"type": "none"}),
         "networks": {"R0": mlp((l_max + 1) * C), "R1": mlp(num_paths_r1 * C)},
     }
     if cfg.density_scaled:

@@ -57,3 +57,9 @@ def tiny_zbl_model_path():
 def tiny_heads_model_path():
     from symmetrix import random_model
     return random_model.cached_model("tiny_heads", directory=MODEL_DIR)
+
+
+@pytest.fixture(scope="session")
+def tiny_agnesi_model_path():
+    from symmetrix import random_model
+    return random_model.cached_model("tiny_agnesi", directory=MODEL_DIR)

@@ -590,3 +590,74 @@ def test_prediction_head_payload_replaces_the_top_level_fields(tiny_heads_model_
     assert abs(a["energy"] - d["energy"]) > 1.0
     with pytest.raises(ValueError, match="not in the model"):
         oracle.OracleModel(tiny_heads_model_path, head="absent")
+
+
+# ---------------------------------------------------------------------------
+# Agnesi distance transform (compact_radial.cpp:144-163, 227-267)
+# ---------------------------------------------------------------------------
+def test_agnesi_features_closed_form(tiny_agnesi_model_path):
+    """Per-pair features: the Bessel basis at x = 1/(1 + a s^q/(1 + s^(q-p))),
+    s = r/r0, r0 the mean covalent radius of the pair, times the polynomial
+    cutoff of r itself."""
+    m = oracle.OracleModel(tiny_agnesi_model_path)
+    with open(tiny_agnesi_model_path) as f:
+        j = json.load(f)
+    cr = j["compact_radial"]
+    tr = cr["distance_transform"]
+    S = cr["num_spline_points"]
+    r = cr["spline_grid_min"] + np.arange(S) * (j["r_cut"] - cr["spline_grid_min"]) / (S - 1)
+    p = cr["cutoff"]["p"]
+    s = r / j["r_cut"]
+    u = 1 - (p + 1) * (p + 2) / 2 * s**p + p * (p + 2) * s ** (p + 1) - p * (p + 1) / 2 * s ** (p + 2)
+    u[r >= j["r_cut"]] = 0.0
+    w = np.array(cr["basis"]["weights"])
+    for ti, tj in [(0, 0), (0, 1), (1, 2), (2, 0)]:
+        r0 = 0.5 * (tr["covalent_radii"][ti] + tr["covalent_radii"][tj])
+        sr = r / r0
+        x = 1.0 / (1.0 + tr["a"] * sr ** tr["q"] / (1.0 + sr ** (tr["q"] - tr["p"])))
+        ref = cr["basis"]["prefactor"] * np.sin(np.outer(x, w)) / x[:, None] * u[:, None]
+        np.testing.assert_allclose(m.radial_features(ti, tj), ref, rtol=1e-12, atol=1e-12)
+
+
+def test_agnesi_edges_use_their_pair_tables(tiny_agnesi_model_path, tmp_path):
+    """An O-Ti dimer: with every covalent radius set to the O-Ti mean the
+    model's tables are all the O-Ti pair's, so the dimer's energy and forces
+    are unchanged only if its edges use the O-Ti pair's tables."""
+    with open(tiny_agnesi_model_path) as f:
+        j = json.load(f)
+    z = j["atomic_numbers"]
+    radii = j["compact_radial"]["distance_transform"]["covalent_radii"]
+    mean = 0.5 * (radii[z.index(8)] + radii[z.index(22)])
+    j["compact_radial"]["distance_transform"]["covalent_radii"] = [mean] * len(radii)
+    flat = tmp_path / "agnesi_flat.json"
+    flat.write_text(json.dumps(j))
+    dimer = {"positions": np.array([[1.0, 1.0, 1.0], [2.9, 1.3, 1.2]]), "cell": np.eye(3) * 12.0,
+             "numbers": np.array([8, 22])}
+    a = oracle.evaluate_system(oracle.OracleModel(tiny_agnesi_model_path, fp64=True), dimer, skin=0.5)
+    b = oracle.evaluate_system(oracle.OracleModel(str(flat), fp64=True), dimer, skin=0.5)
+    assert len(a["graph"]["sources"]) == 2
+    np.testing.assert_allclose(a["energies"], b["energies"], rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(a["forces"], b["forces"], rtol=1e-10, atol=1e-12)
+    # and the O-O table differs: the same dimer with all radii at the O radius
+    j["compact_radial"]["distance_transform"]["covalent_radii"] = [radii[z.index(8)]] * len(radii)
+    oo = tmp_path / "agnesi_oo.json"
+    oo.write_text(json.dumps(j))
+    c = oracle.evaluate_system(oracle.OracleModel(str(oo), fp64=True), dimer, skin=0.5)
+    assert abs(c["energy"] - a["energy"]) > 1e-6
+
+
+def test_agnesi_forces_are_energy_derivatives(tiny_agnesi_model_path):
+    m = oracle.OracleModel(tiny_agnesi_model_path, fp64=True)
+    s = _small_system()
+    base = oracle.evaluate_system(m, s, skin=0.5)
+    h = 1e-4
+    for a in (0, 5, 17):
+        for c in range(3):
+            plus, minus = dict(s), dict(s)
+            pp, pm = s["positions"].copy(), s["positions"].copy()
+            pp[a, c] += h
+            pm[a, c] -= h
+            plus["positions"], minus["positions"] = pp, pm
+            fd = -(oracle.evaluate_system(m, plus, skin=0.5)["energy"]
+                   - oracle.evaluate_system(m, minus, skin=0.5)["energy"]) / (2 * h)
+            assert base["forces"][a, c] == pytest.approx(fd, abs=2e-6)
