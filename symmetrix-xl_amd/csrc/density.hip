@@ -26,12 +26,13 @@ namespace smx {
 namespace {
 
 struct DensitySpline {
-    const double* c;  // [interval][4]
+    const double* c;  // [pair][interval][4]
     int intervals;
     double x0, h;
 };
 
-__device__ __forceinline__ void density_eval(const DensitySpline& sp, double r, double& f, double& d) {
+// f(r), f'(r) of the density spline of table pair `pair` ([pair][interval][4])
+__device__ __forceinline__ void density_eval(const DensitySpline& sp, int pair, double r, double& f, double& d) {
     int iv = static_cast<int>(floor((r - sp.x0) / sp.h));
     double x = r - sp.x0 - sp.h * iv;
     if (iv < 0) {
@@ -42,7 +43,7 @@ __device__ __forceinline__ void density_eval(const DensitySpline& sp, double r, 
         x = sp.h;
     }
     const double xx = x * x;
-    const double* c = sp.c + 4 * static_cast<std::size_t>(iv);
+    const double* c = sp.c + 4 * (static_cast<std::size_t>(pair) * sp.intervals + iv);
     f = c[0] + c[1] * x + c[2] * xx + c[3] * (xx * x);
     d = c[1] + c[2] * (2.0 * x) + c[3] * (3.0 * xx);
 }
@@ -56,7 +57,8 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
 // s[i] = 1 + sum_e f(r_e) over receiver r0+i's edges; one wave per receiver
 // (four per workgroup).  r is indexed by edge - e0.
 __global__ __launch_bounds__(256) void k_density_factors(int nr, int r0, long long e0, const int* __restrict__ offsets,
-                                                         const double* __restrict__ r, DensitySpline sp0,
+                                                         const double* __restrict__ r,
+                                                         const int* __restrict__ edge_pair, DensitySpline sp0,
                                                          DensitySpline sp1, double* __restrict__ s0,
                                                          double* __restrict__ s1) {
     const int i = blockIdx.x * 4 + threadIdx.x / kWave;
@@ -66,12 +68,13 @@ __global__ __launch_bounds__(256) void k_density_factors(int nr, int r0, long lo
     double a0 = 0.0, a1 = 0.0;
     for (long long e = ea + lane; e < eb; e += kWave) {
         double f, d;
+        const int pair = edge_pair ? edge_pair[e0 + e] : 0;
         if (s0) {
-            density_eval(sp0, r[e], f, d);
+            density_eval(sp0, pair, r[e], f, d);
             a0 += f;
         }
         if (s1) {
-            density_eval(sp1, r[e], f, d);
+            density_eval(sp1, pair, r[e], f, d);
             a1 += f;
         }
     }
@@ -129,21 +132,23 @@ __global__ __launch_bounds__(256) void k_density_forces(long long ne, long long 
                                                         const double* __restrict__ r, DensitySpline sp0,
                                                         const double* __restrict__ s0, const double* __restrict__ dot0,
                                                         DensitySpline sp1, const double* __restrict__ s1,
-                                                        const double* __restrict__ dot1, double* __restrict__ nf) {
+                                                        const double* __restrict__ dot1,
+                                                        const int* __restrict__ edge_pair, double* __restrict__ nf) {
     const long long le = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (le >= ne) return;
     const int i = receivers[e0 + le] - r0;
     const double re = r[le];
+    const int pair = edge_pair ? edge_pair[e0 + le] : 0;
     double f[3] = {nf[3 * le], nf[3 * le + 1], nf[3 * le + 2]};
     if (dot1) {
         double v, d;
-        density_eval(sp1, re, v, d);
+        density_eval(sp1, pair, re, v, d);
         const double scale = dot1[i] / s1[i] * d;
         for (int c = 0; c < 3; ++c) f[c] += scale * (xyz[3 * le + c] / re);
     }
     if (dot0) {
         double v, d;
-        density_eval(sp0, re, v, d);
+        density_eval(sp0, pair, re, v, d);
         for (int c = 0; c < 3; ++c) f[c] += dot0[i] / s0[i] * d * xyz[3 * le + c] / re;
     }
     for (int c = 0; c < 3; ++c) nf[3 * le + c] = f[c];
@@ -157,8 +162,8 @@ void launch_density_factors(const DeviceModel& m, const DeviceGraph& g, const Ti
                             hipStream_t s) {
     if (t.nr == 0 || (!s0 && !s1)) return;
     if (!t.r) throw std::logic_error("density scaling needs the tile's edge lengths");
-    k_density_factors<<<(t.nr + 3) / 4, 256, 0, s>>>(t.nr, t.r0, t.e0, g.offsets, t.r, spline_of(m, m.dens0),
-                                                     spline_of(m, m.dens1), s0, s1);
+    k_density_factors<<<(t.nr + 3) / 4, 256, 0, s>>>(t.nr, t.r0, t.e0, g.offsets, t.r, g.edge_pair,
+                                                     spline_of(m, m.dens0), spline_of(m, m.dens1), s0, s1);
     SMX_LAUNCH_CHECK("density_factors");
 }
 
@@ -182,7 +187,7 @@ void launch_density_forces(const DeviceModel& m, const DeviceGraph& g, const Til
     if (!t.r || !t.xyz) throw std::logic_error("density scaling needs the tile's edge geometry");
     k_density_forces<<<static_cast<unsigned>((t.ne + 255) / 256), 256, 0, s>>>(
         t.ne, t.e0, t.r0, g.receivers, t.xyz, t.r, spline_of(m, m.dens0), s0, dot0, spline_of(m, m.dens1), s1, dot1,
-        node_forces);
+        g.edge_pair, node_forces);
     SMX_LAUNCH_CHECK("density_forces");
 }
 

@@ -252,6 +252,10 @@ struct Evaluator {
     // The invalid-edge count of a positions call is copied to pinned host
     // memory right after the edge geometry, so the call can raise without
     // waiting for the model kernels queued behind it.
+    // per-pair radial tables (Agnesi transform): the active types whose
+    // tables are on the device, and each edge's table pair
+    std::vector<int> pair_active;
+    DevBuf d_pair_R0, d_pair_R1, d_pair_D0, d_pair_D1, d_type_to_active, d_edge_pair;
     int* h_invalid = nullptr;
     hipEvent_t geometry_done = nullptr;
     bool geometry_flag_pending = false;
@@ -629,6 +633,7 @@ struct Evaluator {
             h_offsets.resize(N + 1);
             SMX_HIP(hipMemcpy(h_offsets.data(), d_offsets.as<int>(), sizeof(int) * (N + 1), hipMemcpyDeviceToHost));
         }
+        prepare_pair_tables();
         choose_plan();
         build_tiles();
         ensure_workspace();
@@ -636,6 +641,47 @@ struct Evaluator {
         evaluated = false;
         generation = next_generation++;
         return generation;
+    }
+
+    // mace.cpp:119-214 / compact_radial.cpp:368-387: with the Agnesi
+    // transform every pair of active types (a <= b) has its own tables,
+    // tabulated when the active types change; edges select theirs by pair.
+    void prepare_pair_tables() {
+        if (!hm.agnesi) return;
+        std::vector<int> act(h_node_types.begin(), h_node_types.end());
+        std::sort(act.begin(), act.end());
+        act.erase(std::unique(act.begin(), act.end()), act.end());
+        if (act.empty()) act.push_back(0);
+        const int na = static_cast<int>(act.size());
+        if (act != pair_active) {
+            std::vector<float> R0, R1, t0, t1;
+            std::vector<double> D0, D1, u0, u1;
+            for (int a = 0; a < na; ++a)
+                for (int b = a; b < na; ++b) {
+                    hm.pair_tables(act[a], act[b], t0, t1, u0, u1);
+                    R0.insert(R0.end(), t0.begin(), t0.end());
+                    R1.insert(R1.end(), t1.begin(), t1.end());
+                    D0.insert(D0.end(), u0.begin(), u0.end());
+                    D1.insert(D1.end(), u1.begin(), u1.end());
+                }
+            dm.R0c = reinterpret_cast<const float4*>(upload(d_pair_R0, R0, stream));
+            dm.R1c = reinterpret_cast<const float4*>(upload(d_pair_R1, R1, stream));
+            if (hm.A0_scaled) dm.dens0 = upload(d_pair_D0, D0, stream);
+            if (hm.A1_scaled) dm.dens1 = upload(d_pair_D1, D1, stream);
+            std::vector<int> t2a(hm.num_elements, -1);
+            for (int a = 0; a < na; ++a) t2a[act[a]] = a;
+            upload(d_type_to_active, t2a, stream);
+            pair_active = act;
+        }
+        int* ep = static_cast<int*>(d_edge_pair.ensure(std::max<std::int64_t>(E, 1) * sizeof(int)));
+        int* bad = static_cast<int*>(d_counts.ensure(std::max(N, 1) * sizeof(int)));
+        launch_fill_zero(reinterpret_cast<float*>(bad), 1, stream);
+        launch_edge_pairs(E, d_receivers.as<int>(), d_node_types.as<int>(), d_neigh_types.as<int>(),
+                          d_type_to_active.as<int>(), na, ep, bad, stream);
+        int nbad = 0;
+        SMX_HIP(hipMemcpyAsync(&nbad, bad, sizeof(int), hipMemcpyDeviceToHost, stream));
+        SMX_HIP(hipStreamSynchronize(stream));
+        if (nbad > 0) throw std::invalid_argument("a neighbour type is not among the graph's node types");
     }
 
     std::uint64_t prepare_graph_host(int n, const int* node_types, const int* num_neigh, std::int64_t num_edges,
@@ -751,7 +797,8 @@ struct Evaluator {
             if (tm) tm->end("edge_geometry", stream);
         }
         if (tm) tm->begin("edge_records", stream);
-        ks->edge_geometry(dm, t.ne, tile_xyz(t), tile_r(t), ws.erec, stream);
+        ks->edge_geometry(dm, t.ne, tile_xyz(t), tile_r(t), hm.agnesi ? d_edge_pair.as<int>() + t.e0 : nullptr,
+                          ws.erec, stream);
         if (tm) tm->end("edge_records", stream);
         (void)positions;
     }
@@ -905,6 +952,7 @@ struct Evaluator {
         g.receivers = d_receivers.as<int>();
         g.soff = d_soff.as<int>();
         g.sedges = d_sedges.as<int>();
+        g.edge_pair = hm.agnesi ? d_edge_pair.as<int>() : nullptr;
         return g;
     }
 

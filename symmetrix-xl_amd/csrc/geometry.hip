@@ -358,6 +358,7 @@ template <int LMAX>
 __global__ __launch_bounds__(kRecordThreads) void k_edge_records(long long E, const double* __restrict__ xyz,
                                                                  const double* __restrict__ r, double r_cut,
                                                                  float x0, float h, int intervals,
+                                                                 const int* __restrict__ edge_pair,
                                                                  float* __restrict__ erec) {
     using S = Shape<LMAX, 0>;
     static_assert(S::REC % 4 == 0, "records are whole float4s");
@@ -384,7 +385,8 @@ __global__ __launch_bounds__(kRecordThreads) void k_edge_records(long long E, co
                 xloc = h;
             }
             rec[0] = xloc;
-            rec[1] = __int_as_float(interval);
+            // table row: the pair's block of intervals (one block without per-pair tables)
+            rec[1] = __int_as_float((edge_pair ? edge_pair[e] * intervals : 0) + interval);
             rec[2] = __int_as_float(1);
             rec[3] = 0.0f;
             edge_harmonics<LMAX>(d, rf, rec + S::REC_Y, rec + S::REC_DY);
@@ -398,6 +400,22 @@ __global__ __launch_bounds__(kRecordThreads) void k_edge_records(long long E, co
     const long long count = E - base < kRecordThreads ? E - base : kRecordThreads;
     float4* dst = reinterpret_cast<float4*>(erec + base * S::REC);
     for (int q = threadIdx.x; q < count * (S::REC / 4); q += kRecordThreads) dst[q] = stage[q];
+}
+
+// Symmetric pair index over the active types (a <= b: a(2n-a-1)/2 + b,
+// mace.cpp:216-229); an edge whose types are not active is counted in bad.
+__global__ void k_edge_pairs(long long E, const int* __restrict__ receivers, const int* __restrict__ node_types,
+                             const int* __restrict__ neigh_types, const int* __restrict__ type_to_active, int n,
+                             int* __restrict__ edge_pair, int* __restrict__ bad) {
+    const long long e = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (e >= E) return;
+    const int a = type_to_active[node_types[receivers[e]]], b = type_to_active[neigh_types[e]];
+    if (a < 0 || b < 0) {
+        atomicAdd(bad, 1);
+        edge_pair[e] = 0;
+        return;
+    }
+    edge_pair[e] = a <= b ? a * (2 * n - a - 1) / 2 + b : b * (2 * n - b - 1) / 2 + a;
 }
 
 Mat3 mat3(const double* p) {
@@ -569,6 +587,14 @@ void launch_graph_schedule(int N, std::int64_t E, const int* offsets, const int*
     launch_transpose(N, E, sources, soff, sedges, scratch_counts, s);
 }
 
+void launch_edge_pairs(std::int64_t E, const int* receivers, const int* node_types, const int* neigh_types,
+                       const int* type_to_active, int active_types, int* edge_pair, int* bad, hipStream_t s) {
+    if (E == 0) return;
+    k_edge_pairs<<<blocks_for(E, 256), 256, 0, s>>>(E, receivers, node_types, neigh_types, type_to_active,
+                                                    active_types, edge_pair, bad);
+    SMX_LAUNCH_CHECK("edge_pairs");
+}
+
 void launch_gather_types(std::int64_t E, const int* sources, const int* node_types, int* neigh_types,
                          hipStream_t s) {
     if (E == 0) return;
@@ -619,12 +645,14 @@ int build_touched_sources(int N, std::int64_t e0, std::int64_t ne, const int* so
 }
 
 void geometry_records(int l_max, std::int64_t E, const double* xyz, const double* r, double r_cut, float x0, float h,
-                      int intervals, float* erec, hipStream_t s) {
+                      int intervals, const int* edge_pair, float* erec, hipStream_t s) {
     if (E == 0) return;
     if (l_max == 3)
-        k_edge_records<3><<<blocks_for(E, kRecordThreads), kRecordThreads, 0, s>>>(E, xyz, r, r_cut, x0, h, intervals, erec);
+        k_edge_records<3><<<blocks_for(E, kRecordThreads), kRecordThreads, 0, s>>>(E, xyz, r, r_cut, x0, h, intervals,
+                                                                                edge_pair, erec);
     else if (l_max == 2)
-        k_edge_records<2><<<blocks_for(E, kRecordThreads), kRecordThreads, 0, s>>>(E, xyz, r, r_cut, x0, h, intervals, erec);
+        k_edge_records<2><<<blocks_for(E, kRecordThreads), kRecordThreads, 0, s>>>(E, xyz, r, r_cut, x0, h, intervals,
+                                                                                edge_pair, erec);
     else
         throw std::invalid_argument("edge records are compiled for l_max 2 and 3");
     SMX_LAUNCH_CHECK("edge_records");

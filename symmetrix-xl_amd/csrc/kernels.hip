@@ -854,9 +854,9 @@ struct KernelSetImpl final : KernelSet {
     }
     const char* polynomial_mode() const override { return kM0Unrolled ? "unrolled" : "table"; }
 
-    void edge_geometry(const DeviceModel& m, std::int64_t E, const double* xyz, const double* r, float* erec,
-                       hipStream_t s) const override {
-        geometry_records(LMAX, E, xyz, r, m.r_cut, m.x0, m.h, m.intervals, erec, s);
+    void edge_geometry(const DeviceModel& m, std::int64_t E, const double* xyz, const double* r,
+                       const int* edge_pair, float* erec, hipStream_t s) const override {
+        geometry_records(LMAX, E, xyz, r, m.r_cut, m.x0, m.h, m.intervals, edge_pair, erec, s);
     }
 
     void layer1_forward(const DeviceModel& m, const DeviceGraph& g, const TileView& t, const Workspace& w,

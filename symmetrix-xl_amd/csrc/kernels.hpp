@@ -72,6 +72,9 @@ struct DeviceGraph {
     const int* receivers = nullptr;   // [E]
     const int* soff = nullptr;        // [N+1]
     const int* sedges = nullptr;      // [E] edges ordered by source, ascending edge id
+    // [E] radial-table pair of each edge (symmetric index over the active
+    // types) when tables differ per pair (Agnesi transform), else null
+    const int* edge_pair = nullptr;
 };
 
 // Node linears: out[row, n] = sum_k in[row, k] W[k, n] over the rows of one
@@ -174,8 +177,9 @@ struct KernelSet {
     // "unrolled" when the product-basis kernels use compiled term tables
     virtual const char* polynomial_mode() const = 0;
     // per-edge records of a tile from its FP64 xyz and r
+    // (edge_pair, indexed like xyz, selects each edge's table; null: one table)
     virtual void edge_geometry(const DeviceModel& m, std::int64_t ne, const double* xyz, const double* r,
-                               float* erec, hipStream_t s) const = 0;
+                               const int* edge_pair, float* erec, hipStream_t s) const = 0;
     // R0 forward + A0 linear; with through_h1 also M0, the scalar capture and
     // H1 rows r0.. of the graph-wide H1
     virtual void layer1_forward(const DeviceModel& m, const DeviceGraph& g, const TileView& t, const Workspace& w,
@@ -213,8 +217,12 @@ void swizzle_gemm_weights(const float* w, int K, int N, float* out);
 bool kernel_paths(int l_max, int L_max, std::vector<int>& le, std::vector<int>& ls, std::vector<int>& lo);
 
 // Per-edge records (spline point, Y, dY, direction) from FP64 xyz and r.
+// (record field 1 is the table row: pair * intervals + interval)
 void geometry_records(int l_max, std::int64_t E, const double* xyz, const double* r, double r_cut, float x0, float h,
-                      int intervals, float* erec, hipStream_t s);
+                      int intervals, const int* edge_pair, float* erec, hipStream_t s);
+// edge_pair[e] = symmetric pair of the active types of receiver and source
+void launch_edge_pairs(std::int64_t E, const int* receivers, const int* node_types, const int* neigh_types,
+                       const int* type_to_active, int active_types, int* edge_pair, int* bad, hipStream_t s);
 
 void launch_node_gemm(const GemmPlan& plan, const float* W, const float* in, float* out, hipStream_t s);
 

@@ -44,12 +44,7 @@ std::vector<float> to_f32(const std::vector<double>& v) {
     return o;
 }
 
-struct Mlp {
-    std::vector<int> shape;
-    std::vector<std::vector<double>> w;  // [layer][out*in]
-    double scale = 1.0;
-    bool tanh_square = false;            // postprocess "tanh-square": tanh(v^2)
-};
+using Mlp = RadialNetwork;
 
 Mlp read_mlp(const Value& v) {
     Mlp m;
@@ -304,6 +299,51 @@ void select_prediction_head(Value& j, const std::string& requested, std::string&
 
 }  // namespace
 
+// compact_radial.cpp:227-267: Bessel features of the pair (ti, tj) on the
+// grid, at the (optionally Agnesi-transformed) distance, times the
+// polynomial cutoff of the distance itself.
+std::vector<double> HostModel::features(int ti, int tj) const {
+    const int nb = static_cast<int>(bessel.size());
+    double r0 = 1.0;
+    if (agnesi) {
+        if (ti < 0 || tj < 0 || ti >= num_elements || tj >= num_elements)
+            throw std::out_of_range("radial pair type out of range");
+        r0 = 0.5 * (covalent_radii[ti] + covalent_radii[tj]);
+    }
+    const double p = cutoff_p;
+    std::vector<double> feat(static_cast<std::size_t>(spline_points) * nb);
+    for (int node = 0; node < spline_points; ++node) {
+        const double r = grid_min + node * h;
+        double x = r;
+        if (agnesi) {
+            const double s = r / r0;
+            x = 1.0 / (1.0 + agnesi_a * std::pow(s, agnesi_q) / (1.0 + std::pow(s, agnesi_q - agnesi_p)));
+        }
+        double cv = 0.0;
+        if (r < cutoff_r_max) {
+            const double s = r / cutoff_r_max;
+            cv = 1.0 - ((p + 1.0) * (p + 2.0) / 2.0) * std::pow(s, cutoff_p) +
+                 p * (p + 2.0) * std::pow(s, cutoff_p + 1) - (p * (p + 1.0) / 2.0) * std::pow(s, cutoff_p + 2);
+        }
+        for (int b = 0; b < nb; ++b)
+            feat[static_cast<std::size_t>(node) * nb + b] = bessel_prefactor * std::sin(bessel[b] * x) / x * cv;
+    }
+    return feat;
+}
+
+void HostModel::pair_tables(int ti, int tj, std::vector<float>& R0, std::vector<float>& R1, std::vector<double>& D0,
+                            std::vector<double>& D1) const {
+    const auto feat = features(ti, tj);
+    const int nb = static_cast<int>(bessel.size());
+    std::vector<double> v, d;
+    tabulate(R0_net, feat, nb, spline_points, h, v, d, R0);
+    tabulate(R1_net, feat, nb, spline_points, h, v, d, R1);
+    D0.clear();
+    D1.clear();
+    if (A0_scaled) D0 = density_table(A0_net, feat, nb, spline_points, h);
+    if (A1_scaled) D1 = density_table(A1_net, feat, nb, spline_points, h);
+}
+
 void HostModel::load(const std::string& path, const std::string& head) {
     Value j = json_lite::parse_file(path);
     if (j.get_int("symmetrix_format_version", 1) != 4)
@@ -386,9 +426,25 @@ void HostModel::load(const std::string& path, const std::string& head) {
     if (std::abs(r_max - r_cut) > 1e-12) throw std::invalid_argument("compact radial cutoff does not match r_cut");
     // Without a distance transform the features, hence every pair's tables,
     // are independent of the pair (compact_radial.cpp:233-235): one table
-    // serves all pairs exactly.
-    if (cr.at("distance_transform").at("type").as_string() != "none")
-        throw std::invalid_argument("only distance_transform 'none' is supported");
+    // serves all pairs exactly.  The Agnesi transform (compact_radial.cpp:
+    // 144-163) makes them depend on the pair's mean covalent radius.
+    const Value& tr = cr.at("distance_transform");
+    const std::string transform = tr.at("type").as_string();
+    agnesi = transform == "agnesi";
+    if (agnesi) {
+        agnesi_a = tr.at("a").as_number();
+        agnesi_q = tr.at("q").as_number();
+        agnesi_p = tr.at("p").as_number();
+        covalent_radii = tr.at("covalent_radii").as_doubles();
+        if (static_cast<int>(covalent_radii.size()) != num_elements)
+            throw std::invalid_argument("agnesi covalent radii do not match the model's elements");
+        for (double v : covalent_radii)
+            if (!std::isfinite(v) || !(v > 0.0)) throw std::invalid_argument("agnesi covalent radii must be positive");
+        if (!std::isfinite(agnesi_a) || !std::isfinite(agnesi_q) || !std::isfinite(agnesi_p))
+            throw std::invalid_argument("agnesi transform parameters must be finite");
+    } else if (transform != "none") {
+        throw std::invalid_argument("only the 'none' and 'agnesi' distance transforms are supported");
+    }
     const Value& nets = cr.at("networks");
     const Mlp R0net = read_mlp(nets.at("R0"));
     const Mlp R1net = read_mlp(nets.at("R1"));
@@ -411,20 +467,18 @@ void HostModel::load(const std::string& path, const std::string& head) {
     };
     density_net("A0", A0_scaled, A0net);
     density_net("A1", A1_scaled, A1net);
-    std::vector<double> feat(static_cast<std::size_t>(spline_points) * nb);
-    for (int node = 0; node < spline_points; ++node) {
-        const double r = grid_min + node * h;
-        double cv = 0.0;
-        if (r < r_max) {
-            const double s = r / r_max;
-            cv = 1.0 - ((p + 1.0) * (p + 2.0) / 2.0) * std::pow(s, p) + p * (p + 2.0) * std::pow(s, p + 1) -
-                 (p * (p + 1.0) / 2.0) * std::pow(s, p + 2);
-        }
-        for (int b = 0; b < nb; ++b) feat[static_cast<std::size_t>(node) * nb + b] = prefactor * std::sin(bessel[b] * r) / r * cv;
-    }
+    this->bessel = bessel;
+    bessel_prefactor = prefactor;
+    cutoff_r_max = r_max;
+    cutoff_p = p;
+    R0_net = R0net;
+    R1_net = R1net;
+    A0_net = A0net;
+    A1_net = A1net;
     R0_functions = R0net.shape.back();
     R1_functions = R1net.shape.back();
     if (R0_functions != (l_max + 1) * C) throw std::invalid_argument("R0 network width must be (l_max+1)*C");
+    const auto feat = features(0, 0);
     tabulate(R0net, feat, nb, spline_points, h, R0_values, R0_derivs, R0_coef);
     tabulate(R1net, feat, nb, spline_points, h, R1_values, R1_derivs, R1_coef);
     if (A0_scaled) A0_density = density_table(A0net, feat, nb, spline_points, h);

@@ -23,6 +23,15 @@ inline std::int32_t pack_monomial(const std::vector<int>& vars) {
     return p;
 }
 
+// One compact-radial network (multilayer_perceptron.cpp: scaled SiLU hidden
+// layers, linear output; "tanh-square" postprocessing for density networks).
+struct RadialNetwork {
+    std::vector<int> shape;
+    std::vector<std::vector<double>> w;  // [layer][out*in]
+    double scale = 1.0;
+    bool tanh_square = false;
+};
+
 struct HostModel {
     // shape
     int num_elements = 0;
@@ -50,6 +59,21 @@ struct HostModel {
     // coefficients [interval][4] of the one-output density networks
     bool A0_scaled = false, A1_scaled = false;
     std::vector<double> A0_density, A1_density;
+    // radial definition: Bessel basis, polynomial cutoff, optional Agnesi
+    // distance transform (per-pair features), networks
+    std::vector<double> bessel;
+    double bessel_prefactor = 0.0, cutoff_r_max = 0.0;
+    int cutoff_p = 0;
+    bool agnesi = false;
+    double agnesi_a = 0.0, agnesi_q = 0.0, agnesi_p = 0.0;
+    std::vector<double> covalent_radii;  // per model type
+    RadialNetwork R0_net, R1_net, A0_net, A1_net;
+    // tables of the model-type pair (ti, tj): packed FP32 R0/R1 Hermite
+    // coefficients [interval][function][4] and FP64 density coefficients
+    // [interval][4] (the tables above are the pair (0, 0))
+    void pair_tables(int ti, int tj, std::vector<float>& R0, std::vector<float>& R1, std::vector<double>& D0,
+                     std::vector<double>& D1) const;
+    std::vector<double> features(int ti, int tj) const;
     // ZBL pair repulsion: per (type, type) {1/a, 14.3996 Z_u Z_v, r_max}
     bool has_zbl = false;
     std::vector<double> zbl_pair;

@@ -75,9 +75,10 @@ MODEL_CONFIGS = {
     "tiny_heads": ModelConfig("tiny_heads", 32, 2, 1, 2, [8, 22, 38], radial_mlp=[32, 32],
                               r_cut=5.0, avg_num_neighbors=40.0, prediction_heads=True),
     # tiny with the Agnesi distance transform (per-pair radial tables,
-    # compact_radial.cpp:144-163,233-247)
+    # compact_radial.cpp:144-163,233-247) and density scaling (per-pair
+    # density tables)
     "tiny_agnesi": ModelConfig("tiny_agnesi", 32, 2, 1, 2, [8, 22, 38], radial_mlp=[32, 32],
-                               r_cut=5.0, avg_num_neighbors=40.0, agnesi=True),
+                               r_cut=5.0, avg_num_neighbors=40.0, agnesi=True, density_scaled=True),
     # tiny with ZBL pair repulsion (zbl_kokkos.cpp)
     "tiny_zbl": ModelConfig("tiny_zbl", 32, 2, 1, 2, [8, 22, 38], radial_mlp=[32, 32],
                             r_cut=5.0, avg_num_neighbors=40.0, zbl=True),

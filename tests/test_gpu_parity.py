@@ -205,6 +205,26 @@ def test_prediction_heads(tiny_heads_model_path, tiny_model_path, tmp_path):
     with pytest.raises(ValueError, match="per-head fields"):
         MACEKokkosFloat(str(bad))
 
+
+@pytest.mark.parametrize("tile", [0, 64])
+def test_agnesi_per_pair_tables(tiny_agnesi_model_path, tile):
+    """Agnesi distance transform (compact_radial.cpp:144-163): every pair of
+    active types has its own R0/R1 and density tables, selected per edge;
+    direct and tiled plans against the oracle."""
+    from symmetrix.mace_kokkos import MACEKokkosFloat
+    ora = _oracle()
+    s = _system("tiny")
+    om = ora.OracleModel(tiny_agnesi_model_path)
+    ref = ora.evaluate_system(om, s, skin=0.5)
+    ev = MACEKokkosFloat(tiny_agnesi_model_path)
+    if tile:
+        ev.set_execution_plan_request("capacity", tile)
+    e, f, st = _run(ev, s, om.types_of(s["numbers"]))
+    if not tile:
+        nf = ev.node_forces.reshape(-1, 3)
+        assert np.max(np.abs(nf - ref["node_forces"])) < 1e-5
+    _assert_efs(ref, e, f, st, len(e))
+
 def test_energy_forces_stress_medium(medium_model_path):
     s = _system("medium")
     om, ref, ev, g, e, f, st = _evaluate_both(medium_model_path, s)
