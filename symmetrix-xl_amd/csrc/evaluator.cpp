@@ -403,7 +403,7 @@ struct Evaluator {
             return m;
         };
         auto sub = [](const std::vector<GemmGroup>& g) {
-            int n = 4;
+            int n = 8;
             for (const auto& x : g)
                 while ((x.N / 16) % n != 0) n /= 2;
             return n;
@@ -414,7 +414,7 @@ struct Evaluator {
         max_n_a1r = mx(groups_a1r);
         sub_a0 = sub(groups_a0);
         sub_h1 = sub(groups_h1);
-        sub_a1f = sub(groups_a1f);
+        sub_a1f = std::min(sub(groups_a1f), 4);  // the A1 forward (K up to 3C) measured faster at 64 columns
         sub_a1r = sub(groups_a1r);
         upload(d_groups_a0, groups_a0, stream);
         upload(d_groups_h1, groups_h1, stream);

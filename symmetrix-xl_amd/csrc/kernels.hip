@@ -1100,6 +1100,9 @@ void launch_node_gemm(const GemmPlan& plan, const float* W, const float* in, flo
     const dim3 grid(plan.num_tiles, (plan.max_n + cols - 1) / cols);
     const unsigned block = 64;
     switch (plan.n_sub) {
+        case 8:
+            k_node_gemm<8><<<grid, block, 0, s>>>(plan.tiles, plan.groups, plan.rows, W, in, out);
+            break;
         case 4:
             k_node_gemm<4><<<grid, block, 0, s>>>(plan.tiles, plan.groups, plan.rows, W, in, out);
             break;

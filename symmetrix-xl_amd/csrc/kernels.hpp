@@ -87,11 +87,11 @@ struct GemmGroup {
     int in_stride, in_base, in_mstride;
     int out_stride, out_base, out_mstride;
 };
-// rows per wave tile (a multiple of 16): 32 rows x 64 columns per wave; the
-// smaller tile (against 64 rows) spreads the work over about five waves per
-// SIMD at the medium shape, which balances the SIMDs better than the
-// operand reuse of the larger tile gains
-constexpr int kGemmRows = 32;
+// rows per wave tile (a multiple of 16): 16 rows x up to 128 columns per
+// wave.  At the medium shape this reads each input row once per 128 output
+// columns and still gives about five waves per SIMD; it measured faster than
+// 32 x 64 and 64 x 64 tiles.
+constexpr int kGemmRows = 16;
 struct GemmTile {
     int row_start, count, group;  // rows [row_start, row_start+count), count <= kGemmRows
 };
@@ -101,7 +101,7 @@ struct GemmPlan {
     const int* rows = nullptr;        // packed (node << 4 | m)
     int num_tiles = 0;
     int max_n = 0;
-    int n_sub = 1;  // 16-column tiles per wave (4, 2 or 1): divides every group's N/16
+    int n_sub = 1;  // 16-column tiles per wave (8, 4, 2 or 1): divides every group's N/16
 };
 
 // Readout batches: up to kReadoutBatch receivers of one type, as a range of
