@@ -69,12 +69,12 @@ def _edited_tiny(tmp_path, **changes):
 
 
 def test_unsupported_features_are_rejected(tmp_path):
-    rc, _ = _create(_edited_tiny(tmp_path, has_zbl=True))
-    assert rc == _native.SMX_ERR_INVALID_ARGUMENT
-    rc, _ = _create(_edited_tiny(tmp_path, symmetrix_format_version=3))
-    assert rc == _native.SMX_ERR_INVALID_ARGUMENT
-    rc, _ = _create(_edited_tiny(tmp_path, h1_affine_mode="legacy"))
-    assert rc == _native.SMX_ERR_INVALID_ARGUMENT
+    # ZBL without its parameters, other formats and bases, other model families
+    for change in ({"has_zbl": True}, {"symmetrix_format_version": 3}, {"h1_affine_mode": "legacy"},
+                   {"has_field_coupling": True}, {"first_interaction_residual": True},
+                   {"single_layer_readout": True}, {"A0_scaled": True}):
+        rc, _ = _create(_edited_tiny(tmp_path, **change))
+        assert rc == _native.SMX_ERR_INVALID_ARGUMENT, change
 
 
 def test_shape_without_kernel_set_is_unsupported(tmp_path):
