@@ -7,6 +7,7 @@
 #pragma once
 
 #include <cerrno>
+#include <charconv>
 #include <cstdlib>
 #include <cstring>
 #include <fstream>
@@ -140,18 +141,15 @@ private:
         return p_ < end_ && (*p_ == '-' || (*p_ >= '0' && *p_ <= '9'));
     }
     double parse_number() {
-        // strtod needs a terminated buffer; numbers are short, copy them.
-        const char* s = p_;
-        while (p_ < end_ && (std::strchr("+-0123456789.eE", *p_) != nullptr)) ++p_;
-        const std::size_t n = static_cast<std::size_t>(p_ - s);
-        if (n == 0 || n > 63) fail("invalid number");
-        char buf[64];
-        std::memcpy(buf, s, n);
-        buf[n] = '\0';
-        char* endp = nullptr;
-        errno = 0;
-        const double v = std::strtod(buf, &endp);
-        if (endp != buf + n || errno == ERANGE) fail("invalid number");
+        // from_chars is correctly rounded (the same double as strtod) and
+        // needs no terminated copy; a number must end in a digit or '.', so
+        // "inf"/"nan" spellings are refused as JSON requires.
+        double v = 0.0;
+        const auto r = std::from_chars(p_, end_, v, std::chars_format::general);
+        if (r.ec != std::errc() || r.ptr == p_) fail("invalid number");
+        const char last = r.ptr[-1];
+        if (!((last >= '0' && last <= '9') || last == '.')) fail("invalid number");
+        p_ = r.ptr;
         return v;
     }
     std::string parse_string() {

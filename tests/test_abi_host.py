@@ -77,6 +77,22 @@ def test_unsupported_features_are_rejected(tmp_path):
         assert rc == _native.SMX_ERR_INVALID_ARGUMENT, change
 
 
+def test_malformed_numbers_are_rejected(tmp_path):
+    # strict JSON numbers: no non-finite spellings, no leading '+', no overflow
+    text = open(random_model.cached_model("tiny")).read()
+    key = '"r_max": '
+    at = text.index(key) + len(key)
+    end = at
+    while text[end] not in ",}":
+        end += 1
+    for bad in ("NaN", "-Infinity", "+6.0", "1e999", "6.0.0"):
+        p = tmp_path / "bad_number.json"
+        p.write_text(text[:at] + bad + text[end:])
+        rc, _ = _create(str(p))
+        assert rc == _native.SMX_ERR_INVALID_ARGUMENT, bad
+        assert b"model" in _native.lib.smx_last_error().lower() or b"number" in _native.lib.smx_last_error(), bad
+
+
 def test_shape_without_kernel_set_is_unsupported(tmp_path):
     cfg = random_model.ModelConfig("small", 16, 1, 0, 2, [1, 8], radial_mlp=[8], r_cut=4.0,
                                    num_spline_points=32)
