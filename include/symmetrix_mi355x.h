@@ -186,7 +186,9 @@ SMX_API int32_t smx_synchronize(SmxEvaluator* ev);
  * communication folds them into their owners), per-atom energies to eatom
  * (when non-NULL), and the total energy and the six virial components
  * (xx, yy, zz, xy, xz, yz: sum over edges of xyz (x) f, symmetrised) are
- * returned on the host.  Direct execution plan only (edge forces retained). */
+ * returned on the host.  Both execution plans: the direct plan reduces its
+ * retained edge forces after the call, the tiled plan adds each tile's edge
+ * forces to f as the tile finishes (the same rows, another summation order). */
 typedef struct SmxLammpsArgsV1 {
     uint32_t struct_size;
     int32_t inum;                  /* local atoms in ilist */

@@ -606,10 +606,10 @@ struct Evaluator {
         d_stress.ensure(9 * sizeof(double));
         d_stress_partial.ensure(static_cast<std::size_t>(stress_blocks) * 9 * sizeof(double));
         d_total.ensure(sizeof(double));
-        // xyz/r: the whole graph when host edge vectors are given, else one tile
-        const std::size_t xe = has_fractional ? te : e;
-        d_xyz.ensure(xe * 3 * sizeof(double));
-        d_r.ensure(xe * sizeof(double));
+        // xyz/r of one tile (host edge vectors of the whole graph grow them
+        // when they are given)
+        d_xyz.ensure(te * 3 * sizeof(double));
+        d_r.ensure(te * sizeof(double));
         d_invalid.ensure(sizeof(int));
         d_positions.ensure(n * 3 * sizeof(double));
         d_disp.ensure(n * 3 * sizeof(double));
@@ -789,7 +789,12 @@ struct Evaluator {
     // xyz, r and per-edge records of one tile
     void tile_geometry(const TileView& t, const double* positions) {
         LaunchTimer* tm = timer.get();
-        if (!xyz_host) {
+        if (lmp) {
+            if (tm) tm->begin("edge_geometry", stream);
+            lammps_geometry(t.e0, t.ne, d_receivers.as<int>(), lmp->ilist, l_lmp_j.as<int>(), lmp->x, hm.r_cut,
+                            d_xyz.as<double>(), d_r.as<double>(), d_invalid.as<int>(), stream);
+            if (tm) tm->end("edge_geometry", stream);
+        } else if (!xyz_host) {
             if (tm) tm->begin("edge_geometry", stream);
             launch_edge_xyz(t.e0, t.ne, cell, d_receivers.as<int>(), d_neigh.as<int>(), d_wfrac.as<double>(),
                             d_images.as<std::uint32_t>(), d_disp.as<double>(), hm.r_cut, d_xyz.as<double>(),
@@ -805,7 +810,7 @@ struct Evaluator {
 
     // queue the D2H copy of the invalid-edge count (positions calls only)
     void post_geometry_flag() {
-        if (xyz_host) return;
+        if (xyz_host || lmp) return;
         SMX_HIP(hipMemcpyAsync(h_invalid, d_invalid.as<int>(), sizeof(int), hipMemcpyDeviceToHost, stream));
         SMX_HIP(hipEventRecord(geometry_done, stream));
         geometry_flag_pending = true;
@@ -862,8 +867,16 @@ struct Evaluator {
     void accumulate_tile_outputs(const TileView& t) {
         LaunchTimer* tm = timer.get();
         if (tm) tm->begin("tile_reductions", stream);
-        launch_tile_forces(t, d_offsets.as<int>(), d_soff.as<int>(), d_sedges.as<int>(), ws.node_forces,
-                           d_atom_forces.as<double>(), stream);
+        if (lmp) {
+            // LAMMPS rows: sources by LAMMPS index (ghosts included), receivers through ilist
+            const std::size_t ti = static_cast<std::size_t>(&t - tiles.data());
+            launch_tile_forces(t, l_touched.as<int>() + l_touched_begin[ti],
+                               static_cast<int>(l_touched_begin[ti + 1] - l_touched_begin[ti]), d_offsets.as<int>(),
+                               l_joff.as<int>(), l_jedges.as<int>(), lmp->ilist, ws.node_forces, lmp->f, stream);
+        } else {
+            launch_tile_forces(t, t.touched, t.touched_count, d_offsets.as<int>(), d_soff.as<int>(),
+                               d_sedges.as<int>(), nullptr, ws.node_forces, d_atom_forces.as<double>(), stream);
+        }
         launch_virial_accumulate(t.ne, ws.node_forces, tile_xyz(t), d_stress_partial.as<double>(), stress_blocks,
                                  d_virial.as<double>(), stream);
         if (tm) tm->end("tile_reductions", stream);
@@ -1001,7 +1014,9 @@ struct Evaluator {
     // pair_symmetrix_mace_kokkos.cpp:1010-1282: topology on a rebuild,
     // edge vectors every call, reductions into LAMMPS's per-atom arrays
     DevBuf l_node_types, l_num_neigh, l_node_of_atom, l_neigh, l_neigh_types, l_lmp_j, l_joff, l_jedges, l_counts,
-        l_flag;
+        l_flag, l_touched;
+    std::vector<std::size_t> l_touched_begin;  // tiled plan: LAMMPS atoms each tile's edges leave
+    const SmxLammpsArgsV1* lmp = nullptr;      // set while a LAMMPS call evaluates
     int l_inum = -1, l_nall = -1;
     std::uint64_t l_generation = 0;
     std::vector<int> l_ilist_host;
@@ -1048,6 +1063,23 @@ struct Evaluator {
         int* jed = static_cast<int*>(l_jedges.ensure(e * sizeof(int)));
         int* cnt = static_cast<int*>(l_counts.ensure(std::max(nall, 1) * sizeof(int)));
         launch_transpose(nall, total, lj, joff, jed, cnt, stream);
+        l_touched_begin.assign(1, 0);
+        if (tiled && nall > 0) {
+            DevBuf bitmap, counts, one;
+            const int words = nall / 32 + 1;
+            bitmap.ensure(sizeof(std::uint32_t) * words);
+            counts.ensure(sizeof(int) * words);
+            one.ensure(sizeof(int) * nall);
+            std::vector<int> all, host(nall);
+            for (const auto& t : tiles) {
+                const int c = build_touched_sources(nall, t.e0, t.ne, lj, bitmap.as<std::uint32_t>(), counts.as<int>(),
+                                                    one.as<int>(), stream);
+                if (c > 0) SMX_HIP(hipMemcpy(host.data(), one.as<int>(), sizeof(int) * c, hipMemcpyDeviceToHost));
+                all.insert(all.end(), host.begin(), host.begin() + c);
+                l_touched_begin.push_back(all.size());
+            }
+            upload(l_touched, all, stream);
+        }
         l_inum = inum;
         l_nall = nall;
         l_generation = generation;
@@ -1067,23 +1099,27 @@ struct Evaluator {
                            a.type_to_model, a.ntypes, a.owner};
         if (a.rebuild || l_generation == 0 || l_generation != generation || a.inum != l_inum || a.nall != l_nall)
             lammps_topology(a, L);
-        if (tiled)
-            throw std::domain_error("the LAMMPS entry needs the direct execution plan (per-edge forces); "
-                                    "this graph was planned as tiles");
-        // edge vectors of this call
+        // edge vectors are made per tile from a.x (tile_geometry); forces of
+        // the tiled plan go into a.f tile by tile, the direct plan's after
+        // the call from its retained per-edge forces
         launch_fill_zero(reinterpret_cast<float*>(d_invalid.as<int>()), 1, stream);
-        lammps_geometry(E, d_receivers.as<int>(), a.ilist, l_lmp_j.as<int>(), a.x, hm.r_cut, d_xyz.as<double>(),
-                        d_r.as<double>(), d_invalid.as<int>(), stream);
-        xyz_host = true;
+        xyz_host = false;
+        struct Reset {
+            const SmxLammpsArgsV1*& p;
+            ~Reset() { p = nullptr; }
+        } reset{lmp};
+        lmp = &a;
         evaluate(nullptr);
-        // reductions into the LAMMPS arrays
-        lammps_forces(a.nall, l_joff.as<int>(), l_jedges.as<int>(), l_node_of_atom.as<int>(), d_offsets.as<int>(),
-                      ws.node_forces, a.f, stream);
+        lmp = nullptr;
+        if (!tiled) {
+            lammps_forces(a.nall, l_joff.as<int>(), l_jedges.as<int>(), l_node_of_atom.as<int>(), d_offsets.as<int>(),
+                          ws.node_forces, a.f, stream);
+            launch_fill_zero(d_virial.as<double>(), 9, stream);
+            launch_virial_accumulate(E, ws.node_forces, d_xyz.as<double>(), d_stress_partial.as<double>(),
+                                     stress_blocks, d_virial.as<double>(), stream);
+        }
         if (a.eatom) lammps_eatom(a.inum, a.ilist, ws.node_energies, a.eatom, stream);
         launch_energy_sum(N, ws.node_energies, d_total.as<double>(), stream);
-        launch_fill_zero(d_virial.as<double>(), 9, stream);
-        launch_virial_accumulate(E, ws.node_forces, d_xyz.as<double>(), d_stress_partial.as<double>(), stress_blocks,
-                                 d_virial.as<double>(), stream);
         double total = 0.0, w[9];
         int invalid = 0;
         SMX_HIP(hipMemcpyAsync(&total, d_total.as<double>(), sizeof(double), hipMemcpyDeviceToHost, stream));

@@ -582,6 +582,7 @@ __global__ __launch_bounds__(256) void k_tile_forces_sources(const int* __restri
 // F[i] -= sum of the directed forces on the edges arriving at receiver i of the tile
 __global__ __launch_bounds__(256) void k_tile_forces_receivers(int r0, int nr, long long e0,
                                                                const int* __restrict__ offsets,
+                                                               const int* __restrict__ receiver_row,
                                                                const double* __restrict__ nf, double* __restrict__ F) {
     const int li = blockIdx.x * (256 / kWave) + threadIdx.x / kWave;
     const int lane = threadIdx.x % kWave;
@@ -598,9 +599,10 @@ __global__ __launch_bounds__(256) void k_tile_forces_receivers(int r0, int nr, l
     f1 = wave_sum<kWave>(f1);
     f2 = wave_sum<kWave>(f2);
     if (lane == 0) {
-        F[3 * static_cast<std::size_t>(i)] -= f0;
-        F[3 * static_cast<std::size_t>(i) + 1] -= f1;
-        F[3 * static_cast<std::size_t>(i) + 2] -= f2;
+        const std::size_t row = receiver_row ? static_cast<std::size_t>(receiver_row[i]) : static_cast<std::size_t>(i);
+        F[3 * row] -= f0;
+        F[3 * row + 1] -= f1;
+        F[3 * row + 2] -= f2;
     }
 }
 
@@ -1157,16 +1159,17 @@ void launch_scale9(const double* in, double scale, double* out, hipStream_t s) {
     SMX_LAUNCH_CHECK("scale9");
 }
 
-void launch_tile_forces(const TileView& t, const int* offsets, const int* soff, const int* sedges,
-                        const double* node_forces, double* F, hipStream_t s) {
-    if (t.touched_count > 0) {
-        k_tile_forces_sources<<<blocks_for(t.touched_count, 256 / kWave), 256, 0, s>>>(
-            t.touched, t.touched_count, t.e0, t.e0 + t.ne, soff, sedges, node_forces, F);
+void launch_tile_forces(const TileView& t, const int* touched, int touched_count, const int* offsets,
+                        const int* soff, const int* sedges, const int* receiver_row, const double* node_forces,
+                        double* F, hipStream_t s) {
+    if (touched_count > 0) {
+        k_tile_forces_sources<<<blocks_for(touched_count, 256 / kWave), 256, 0, s>>>(
+            touched, touched_count, t.e0, t.e0 + t.ne, soff, sedges, node_forces, F);
         SMX_LAUNCH_CHECK("tile_forces_sources");
     }
     if (t.nr > 0) {
-        k_tile_forces_receivers<<<blocks_for(t.nr, 256 / kWave), 256, 0, s>>>(t.r0, t.nr, t.e0, offsets, node_forces,
-                                                                              F);
+        k_tile_forces_receivers<<<blocks_for(t.nr, 256 / kWave), 256, 0, s>>>(t.r0, t.nr, t.e0, offsets,
+                                                                              receiver_row, node_forces, F);
         SMX_LAUNCH_CHECK("tile_forces_receivers");
     }
 }

@@ -252,9 +252,13 @@ void launch_stress(std::int64_t E, const double* node_forces, const double* xyz,
 void launch_virial_accumulate(std::int64_t E, const double* node_forces, const double* xyz, double* partial,
                               int partial_blocks, double* virial, hipStream_t s);
 void launch_scale9(const double* in, double scale, double* out, hipStream_t s);
-// F[src] += f_e, F[rcv] -= f_e for one tile's edges (tile-local forces)
-void launch_tile_forces(const TileView& t, const int* offsets, const int* soff, const int* sedges,
-                        const double* node_forces, double* F, hipStream_t s);
+// F[src] += f_e, F[rcv] -= f_e for one tile's edges (tile-local forces).
+// touched/touched_count: the sources the tile's edges leave, listed in the
+// index space of soff/sedges; receiver_row maps a graph node to its F row
+// (nullptr: the node index itself).
+void launch_tile_forces(const TileView& t, const int* touched, int touched_count, const int* offsets,
+                        const int* soff, const int* sedges, const int* receiver_row, const double* node_forces,
+                        double* F, hipStream_t s);
 void launch_fill_zero(float* p, std::size_t n, hipStream_t s);
 void launch_fill_zero(double* p, std::size_t n, hipStream_t s);
 void launch_energy_sum(int N, const double* node_energies, double* total, hipStream_t s);
@@ -308,8 +312,9 @@ void lammps_nodes(int inum, int nall, const LammpsList& L, int* node_types, int*
 // type and the LAMMPS index of the neighbour
 void lammps_edges(int inum, int nall, const LammpsList& L, const int* offsets, const int* node_of_atom, int* neigh,
                   int* neigh_types, int* lmp_j, int* bad, hipStream_t s);
-void lammps_geometry(std::int64_t E, const int* receivers, const int* ilist, const int* lmp_j, const double* x,
-                     double r_cut, double* xyz, double* r, int* invalid, hipStream_t s);
+// edge vectors of edges [e0, e0+ne), written tile-local (row e - e0)
+void lammps_geometry(std::int64_t e0, std::int64_t ne, const int* receivers, const int* ilist, const int* lmp_j,
+                     const double* x, double r_cut, double* xyz, double* r, int* invalid, hipStream_t s);
 void lammps_forces(int nall, const int* joff, const int* jedges, const int* node_of_atom, const int* offsets,
                    const double* node_forces, double* f, hipStream_t s);
 void lammps_eatom(int inum, const int* ilist, const double* node_energies, double* eatom, hipStream_t s);

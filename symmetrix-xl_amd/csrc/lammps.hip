@@ -75,11 +75,13 @@ __global__ void k_lmp_edges(int inum, int nall, LammpsList L, const int* __restr
 
 // xyz = x[j] - x[i], scaled to the cutoff when longer; a non-finite or zero
 // length is counted and parked at the cutoff (no force)
-__global__ void k_lmp_geometry(long long E, const int* __restrict__ receivers, const int* __restrict__ ilist,
-                               const int* __restrict__ lmp_j, const double* __restrict__ x, double r_cut,
-                               double* __restrict__ xyz, double* __restrict__ r, int* __restrict__ invalid) {
-    const long long e = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (e >= E) return;
+__global__ void k_lmp_geometry(long long e0, long long ne, const int* __restrict__ receivers,
+                               const int* __restrict__ ilist, const int* __restrict__ lmp_j,
+                               const double* __restrict__ x, double r_cut, double* __restrict__ xyz,
+                               double* __restrict__ r, int* __restrict__ invalid) {
+    const long long le = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (le >= ne) return;
+    const long long e = e0 + le;
     const int i = ilist[receivers[e]], j = lmp_j[e];
     const double dx = x[3 * static_cast<long long>(j)] - x[3 * static_cast<long long>(i)];
     const double dy = x[3 * static_cast<long long>(j) + 1] - x[3 * static_cast<long long>(i) + 1];
@@ -87,18 +89,18 @@ __global__ void k_lmp_geometry(long long E, const int* __restrict__ receivers, c
     const double r2 = dx * dx + dy * dy + dz * dz;
     if (!isfinite(r2) || !(r2 > 0.0)) {
         atomicAdd(invalid, 1);
-        xyz[3 * e] = r_cut;
-        xyz[3 * e + 1] = 0.0;
-        xyz[3 * e + 2] = 0.0;
-        r[e] = r_cut;
+        xyz[3 * le] = r_cut;
+        xyz[3 * le + 1] = 0.0;
+        xyz[3 * le + 2] = 0.0;
+        r[le] = r_cut;
         return;
     }
     const double d = sqrt(r2);
     const double scale = d >= r_cut ? r_cut / d : 1.0;
-    xyz[3 * e] = scale * dx;
-    xyz[3 * e + 1] = scale * dy;
-    xyz[3 * e + 2] = scale * dz;
-    r[e] = scale * d;
+    xyz[3 * le] = scale * dx;
+    xyz[3 * le + 1] = scale * dy;
+    xyz[3 * le + 2] = scale * dz;
+    r[le] = scale * d;
 }
 
 // f[a] += sum of the edges pointing at atom a - (a local) sum of a's edges
@@ -158,10 +160,10 @@ void lammps_edges(int inum, int nall, const LammpsList& L, const int* offsets, c
     SMX_LAUNCH_CHECK("lammps_edges");
 }
 
-void lammps_geometry(std::int64_t E, const int* receivers, const int* ilist, const int* lmp_j, const double* x,
-                     double r_cut, double* xyz, double* r, int* invalid, hipStream_t s) {
-    if (E == 0) return;
-    k_lmp_geometry<<<blocks_for(E, 256), 256, 0, s>>>(E, receivers, ilist, lmp_j, x, r_cut, xyz, r, invalid);
+void lammps_geometry(std::int64_t e0, std::int64_t ne, const int* receivers, const int* ilist, const int* lmp_j,
+                     const double* x, double r_cut, double* xyz, double* r, int* invalid, hipStream_t s) {
+    if (ne == 0) return;
+    k_lmp_geometry<<<blocks_for(ne, 256), 256, 0, s>>>(e0, ne, receivers, ilist, lmp_j, x, r_cut, xyz, r, invalid);
     SMX_LAUNCH_CHECK("lammps_geometry");
 }
 

@@ -9,7 +9,9 @@ on some entries, an ilist that is not the identity, and atom->map(tag) as
 `owner`.  Forces land on local and ghost rows; folded onto their owners they
 must equal the oracle's periodic forces, the energy and per-atom energies
 the oracle's, and -virial/V the oracle's stress.  A second call without a
-neighbour-list rebuild uses moved positions on the same list.
+neighbour-list rebuild uses moved positions on the same list.  The same
+calls run under the direct plan and the tiled (capacity) plan, whose forces
+reach the LAMMPS rows tile by tile; both must give the same rows.
 """
 
 import ctypes
@@ -100,7 +102,11 @@ def _run(ev, hip, allpos, owner, alltypes, rows, ilist, type_to_model, rebuild):
     return energy, virial, hip.get(a.f, f), hip.get(a.eatom, eatom)
 
 
-def test_lammps_entry_matches_oracle(tiny_model_path):
+_ROWS = {}  # plan -> per-step LAMMPS force rows, for the cross-plan check
+
+
+@pytest.mark.parametrize("tile", [None, 32], ids=["direct", "tiled32"])
+def test_lammps_entry_matches_oracle(tiny_model_path, tile):
     from oracle import oracle
     from symmetrix import systems
     from symmetrix.mace_kokkos import MACEKokkosFloat
@@ -108,6 +114,8 @@ def test_lammps_entry_matches_oracle(tiny_model_path):
     om = oracle.OracleModel(tiny_model_path)
     ref = oracle.evaluate_system(om, s, skin=0.5)
     ev = MACEKokkosFloat(tiny_model_path)
+    if tile is not None:
+        ev.set_execution_plan_request("capacity", tile)
     # LAMMPS types: O=1, Ti=2, Sr=3 ; model types follow the model's atomic numbers
     lmp_type_of_z = {8: 1, 22: 2, 38: 3}
     model_of_z = {int(z): k for k, z in enumerate(ev.atomic_numbers)}
@@ -144,6 +152,13 @@ def test_lammps_entry_matches_oracle(tiny_model_path):
             expect = [st[0, 0], st[1, 1], st[2, 2], 0.5 * (st[0, 1] + st[1, 0]), 0.5 * (st[0, 2] + st[2, 0]),
                       0.5 * (st[1, 2] + st[2, 1])]
             np.testing.assert_allclose(mine, expect, rtol=0, atol=S_TOL)
+            _ROWS[(tile, step)] = f
+            if tile is not None:
+                assert ev.execution_plan.startswith("direct-tiled")
+                if (None, step) in _ROWS:
+                    # ghost rows included; the plans differ only in FP32
+                    # summation order (3e-8 measured), a misplaced row by ~0.1
+                    np.testing.assert_allclose(f, _ROWS[(None, step)], rtol=0, atol=1e-6)
     finally:
         hip.free()
 
