@@ -573,7 +573,7 @@ struct Evaluator {
     void ensure_workspace() {
         const std::size_t C = hm.C, NY = hm.num_lm, NH = hm.num_LM, NLME = hm.num_lme;
         const std::size_t n = std::max(N, 1), tn = std::max(max_tile_nr, 1);
-        const std::size_t te = std::max<std::int64_t>(max_tile_ne, 1), e = std::max<std::int64_t>(E, 1);
+        const std::size_t te = std::max<std::int64_t>(max_tile_ne, 1);
         auto f = [&](DevBuf& b, std::size_t count) { return static_cast<float*>(b.ensure(count * sizeof(float))); };
         ws.erec = f(w_erec, te * ks->record_floats());
         ws.Phi0 = f(w_Phi0, tn * NY * C);
