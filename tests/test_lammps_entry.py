@@ -102,11 +102,14 @@ def _run(ev, hip, allpos, owner, alltypes, rows, ilist, type_to_model, rebuild):
     return energy, virial, hip.get(a.f, f), hip.get(a.eatom, eatom)
 
 
-_ROWS = {}  # plan -> per-step LAMMPS force rows, for the cross-plan check
+_ROWS = {}  # (model, plan, step) -> LAMMPS force rows, for the cross-plan check
 
 
+@pytest.mark.parametrize("model", ["tiny", "tiny_scaled", "tiny_zbl", "tiny_agnesi"])
 @pytest.mark.parametrize("tile", [None, 32], ids=["direct", "tiled32"])
-def test_lammps_entry_matches_oracle(tiny_model_path, tile):
+def test_lammps_entry_matches_oracle(request, model, tile):
+    # plain, density-scaled, ZBL and Agnesi (per-pair tables) models
+    tiny_model_path = request.getfixturevalue(model + "_model_path")
     from oracle import oracle
     from symmetrix import systems
     from symmetrix.mace_kokkos import MACEKokkosFloat
@@ -152,13 +155,13 @@ def test_lammps_entry_matches_oracle(tiny_model_path, tile):
             expect = [st[0, 0], st[1, 1], st[2, 2], 0.5 * (st[0, 1] + st[1, 0]), 0.5 * (st[0, 2] + st[2, 0]),
                       0.5 * (st[1, 2] + st[2, 1])]
             np.testing.assert_allclose(mine, expect, rtol=0, atol=S_TOL)
-            _ROWS[(tile, step)] = f
+            _ROWS[(model, tile, step)] = f
             if tile is not None:
                 assert ev.execution_plan.startswith("direct-tiled")
-                if (None, step) in _ROWS:
+                if (model, None, step) in _ROWS:
                     # ghost rows included; the plans differ only in FP32
                     # summation order (3e-8 measured), a misplaced row by ~0.1
-                    np.testing.assert_allclose(f, _ROWS[(None, step)], rtol=0, atol=1e-6)
+                    np.testing.assert_allclose(f, _ROWS[(model, None, step)], rtol=0, atol=1e-6)
     finally:
         hip.free()
 
