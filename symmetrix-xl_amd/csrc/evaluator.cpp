@@ -808,9 +808,9 @@ struct Evaluator {
         (void)positions;
     }
 
-    // queue the D2H copy of the invalid-edge count (positions calls only)
+    // queue the D2H copy of the invalid-edge count (positions and LAMMPS calls)
     void post_geometry_flag() {
-        if (xyz_host || lmp) return;
+        if (xyz_host) return;
         SMX_HIP(hipMemcpyAsync(h_invalid, d_invalid.as<int>(), sizeof(int), hipMemcpyDeviceToHost, stream));
         SMX_HIP(hipEventRecord(geometry_done, stream));
         geometry_flag_pending = true;
@@ -1121,11 +1121,16 @@ struct Evaluator {
         if (a.eatom) lammps_eatom(a.inum, a.ilist, ws.node_energies, a.eatom, stream);
         launch_energy_sum(N, ws.node_energies, d_total.as<double>(), stream);
         double total = 0.0, w[9];
-        int invalid = 0;
         SMX_HIP(hipMemcpyAsync(&total, d_total.as<double>(), sizeof(double), hipMemcpyDeviceToHost, stream));
         SMX_HIP(hipMemcpyAsync(w, d_virial.as<double>(), sizeof(w), hipMemcpyDeviceToHost, stream));
-        SMX_HIP(hipMemcpyAsync(&invalid, d_invalid.as<int>(), sizeof(int), hipMemcpyDeviceToHost, stream));
         sync();
+        // the count copied after the first geometry pass (the tiled plan
+        // makes each tile's edge vectors again in its later sweeps)
+        int invalid = 0;
+        if (geometry_flag_pending) {
+            geometry_flag_pending = false;
+            invalid = *h_invalid;
+        }
         if (invalid > 0) {
             evaluated = false;
             throw std::invalid_argument("LAMMPS positions produced an invalid edge geometry (" +

@@ -180,3 +180,37 @@ def test_lammps_entry_rejects_unmapped_types(tiny_model_path):
             _run(ev, hip, allpos, owner, alltypes, rows, np.arange(len(rows), dtype=np.int32), [0, -1, 2], True)
     finally:
         hip.free()
+
+
+@pytest.mark.parametrize("tile", [None, 32], ids=["direct", "tiled32"])
+def test_lammps_entry_zero_length_edge_raises_and_next_call_recovers(tiny_model_path, tile):
+    # a ghost placed on the local atom that lists it: exactly one zero-length
+    # edge, counted once in either plan; the next call on good positions
+    # (same list, no rebuild) gives the first call's results again
+    from symmetrix import systems
+    from symmetrix.mace_kokkos import MACEKokkosFloat
+    s = systems.srtio3_supercell(3, sigma=0.05, seed=0)
+    ev = MACEKokkosFloat(tiny_model_path)
+    if tile is not None:
+        ev.set_execution_plan_request("capacity", tile)
+    model_of_z = {int(z): k for k, z in enumerate(ev.atomic_numbers)}
+    type_to_model = [model_of_z[8], model_of_z[22], model_of_z[38]]
+    cell = np.asarray(s["cell"], float)
+    allpos, owner, alltypes, rows = _lammps_arrays(s["positions"], cell, s["numbers"], ev.r_cut + 0.5,
+                                                   {8: 1, 22: 2, 38: 3})
+    n = len(rows)
+    ghost = int(next(j for j in rows[0] if j >= n))
+    bad = allpos.copy()
+    bad[ghost] = allpos[0]
+    ilist = np.arange(n, dtype=np.int32)
+    hip = _Hip()
+    try:
+        e0, v0, f0, _ = _run(ev, hip, allpos, owner, alltypes, rows, ilist, type_to_model, True)
+        with pytest.raises(ValueError, match=r"invalid edge geometry \(1 zero-length"):
+            _run(ev, hip, bad, owner, alltypes, rows, ilist, type_to_model, False)
+        e1, v1, f1, _ = _run(ev, hip, allpos, owner, alltypes, rows, ilist, type_to_model, False)
+        assert e1 == e0
+        np.testing.assert_array_equal(f1, f0)
+        np.testing.assert_array_equal(v1, v0)
+    finally:
+        hip.free()
