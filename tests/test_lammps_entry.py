@@ -214,3 +214,33 @@ def test_lammps_entry_zero_length_edge_raises_and_next_call_recovers(tiny_model_
         np.testing.assert_array_equal(v1, v0)
     finally:
         hip.free()
+
+
+def test_lammps_entry_rejects_bad_arguments(tiny_model_path):
+    # host-side checks, before any device work: struct size, counts, arrays
+    import ctypes
+    from symmetrix import _native
+    from symmetrix._native import SmxLammpsArgsV1
+    from symmetrix.mace_kokkos import MACEKokkosFloat
+    ev = MACEKokkosFloat(tiny_model_path)
+    energy, virial = ctypes.c_double(), (ctypes.c_double * 6)()
+
+    def call(**fields):
+        a = SmxLammpsArgsV1()
+        a.struct_size = ctypes.sizeof(SmxLammpsArgsV1)
+        a.inum, a.nall, a.ntypes = 0, 0, 1
+        a.type_to_model = 8          # any non-null: never read for these cases
+        for k, v in fields.items():
+            setattr(a, k, v)
+        rc = _native.lib.smx_lammps_compute(ev._h, ctypes.byref(a), ctypes.byref(energy), virial)
+        return rc, _native.lib.smx_last_error()
+
+    for fields, text in [({"struct_size": 8}, b"struct_size"),
+                         ({"inum": 2, "nall": 1}, b"counts"),
+                         ({"ntypes": 0}, b"counts"),
+                         ({"inum": 1, "nall": 1}, b"neighbour list arrays"),
+                         ({"nall": 3}, b"per-atom arrays"),
+                         ({"type_to_model": None}, b"type map")]:
+        rc, msg = call(**fields)
+        assert rc == _native.SMX_ERR_INVALID_ARGUMENT, (fields, msg)
+        assert text in msg, (fields, msg)
