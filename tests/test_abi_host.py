@@ -101,6 +101,24 @@ def test_shape_without_kernel_set_is_unsupported(tmp_path):
     assert rc == _native.SMX_ERR_UNSUPPORTED
 
 
+def test_reference_written_fixture_loads_or_is_unsupported():
+    """The product's loader reads the models the reference's own writer makes
+    (symmetrix/test/compact_r1_model.py): the medium-shape ones load their
+    radial tables; the four-channel l_max 0 fixture has no kernel set."""
+    from _compact import compact_model
+    for name in ("compact_medium_m0", "compact_medium_linear"):
+        path, _ = compact_model(name)
+        cnt = ctypes.c_int64()
+        dims = (ctypes.c_int32 * 4)()
+        rc = _native.lib.smx_model_array_f32(path.encode(), b"R0_spline", None, 0, ctypes.byref(cnt), dims,
+                                             None, None)
+        assert rc == 0, _native.lib.smx_last_error()
+        assert list(dims)[:3] == [15, 4, 4 * 128]
+    path, _ = compact_model("compact_c4")
+    rc, _ = _create(path)
+    assert rc == _native.SMX_ERR_UNSUPPORTED
+
+
 def test_inconsistent_model_arrays_are_invalid(tmp_path):
     src = random_model.cached_model("tiny")
     with open(src) as f:
