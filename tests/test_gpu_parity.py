@@ -260,6 +260,19 @@ def test_energy_forces_stress_wide(wide_model_path):
     _assert_efs(ref, e, f, st, len(e))
 
 
+@pytest.mark.timeout(900)
+def test_energy_forces_stress_wide_full_size(wide_model_path):
+    """BASELINE configs[4] at its stated size: 10,000 rigid waters (30,000
+    atoms, L = 66.9 A) with the wide model, against the oracle."""
+    from symmetrix import systems
+    s = systems.water_box(10000, seed=0)
+    print("wide 30,000-atom box: oracle and HIP path", flush=True)
+    om, ref, ev, g, e, f, st = _evaluate_both(wide_model_path, s)
+    assert len(e) == 30000
+    print("edges %d, plan %s" % (g["num_edges"], ev.execution_plan), flush=True)
+    _assert_efs(ref, e, f, st, len(e))
+
+
 def test_repeat_calls_bitwise_deterministic(tiny_model_path):
     from symmetrix.mace_kokkos import MACEKokkosFloat
     s = _system("tiny")
