@@ -128,7 +128,9 @@ SMX_API int32_t smx_prepare_periodic_factorized_graph(SmxEvaluator* ev, int32_t 
 SMX_API int32_t smx_set_execution_plan(SmxEvaluator* ev, const char* profile, int32_t tile_receivers);
 /* execution_plan report of the prepared graph (execution_plan.hpp:38-50) */
 SMX_API int32_t smx_execution_plan(SmxEvaluator* ev, char* out, int64_t capacity);
-/* update_factorized_cell (mace_kokkos.hpp:436; pybind _update_factorized_cell) */
+/* update_factorized_cell (mace_kokkos.hpp:436; pybind _update_factorized_cell):
+ * finite entries and a non-zero determinant are required, as in
+ * mace_kokkos_factorized_lifecycle.cpp:2735-2766. */
 SMX_API int32_t smx_update_factorized_cell(SmxEvaluator* ev, uint64_t generation, const double* cell,
                                            const double* inverse_cell);
 
@@ -188,7 +190,14 @@ SMX_API int32_t smx_synchronize(SmxEvaluator* ev);
  * (xx, yy, zz, xy, xz, yz: sum over edges of xyz (x) f, symmetrised) are
  * returned on the host.  Both execution plans: the direct plan reduces its
  * retained edge forces after the call, the tiled plan adds each tile's edge
- * forces to f as the tile finishes (the same rows, another summation order). */
+ * forces to f as the tile finishes (the same rows, another summation order).
+ * Ordering: the evaluator runs on its own stream.  With SmxLammpsArgsV2 the
+ * call first makes that stream wait for the work the caller queued on
+ * args->stream (positions update, force clearing); with SmxLammpsArgsV1 it
+ * synchronises the device on entry.  The call returns after its writes to
+ * f and eatom are complete.  Positions that give an invalid edge (zero
+ * length or non-finite) raise SMX_ERR_INVALID_ARGUMENT with f and eatom left
+ * unchanged. */
 typedef struct SmxLammpsArgsV1 {
     uint32_t struct_size;
     int32_t inum;                  /* local atoms in ilist */
@@ -209,6 +218,28 @@ typedef struct SmxLammpsArgsV1 {
     double* f;                     /* [nall][3] forces, added to */
     double* eatom;                 /* [nall] per-atom energies, added to; may be NULL */
 } SmxLammpsArgsV1;
+/* V1 followed by the caller's stream (struct_size = sizeof(SmxLammpsArgsV2));
+ * pass it through the SmxLammpsArgsV1 pointer. */
+typedef struct SmxLammpsArgsV2 {
+    uint32_t struct_size;
+    int32_t inum;
+    int32_t nall;
+    int32_t ntypes;
+    const int32_t* ilist;
+    const int32_t* numneigh;
+    const int32_t* neighbors;
+    int64_t stride_atom;
+    int64_t stride_neighbor;
+    const double* x;
+    const int32_t* type;
+    const int32_t* type_to_model;
+    const int32_t* owner;
+    int32_t rebuild;
+    int32_t reserved;
+    double* f;
+    double* eatom;
+    void* stream;                  /* hipStream_t of the caller's device work (NULL: the null stream) */
+} SmxLammpsArgsV2;
 SMX_API int32_t smx_lammps_compute(SmxEvaluator* ev, const SmxLammpsArgsV1* args, double* energy, double* virial);
 
 /* Stage buffers of the last evaluation (FP32, row-major node-major) for

@@ -29,8 +29,16 @@
  *   never throw.  Edges with radius >= cutoff are skipped.  The reverse
  *   expects edge_receivers non-decreasing (receiver-major edges, as the
  *   reference's prepared graph orders them) and harmonics_gradients
- *   present; it allocates its per-edge workspace stream-ordered
- *   (hipMallocAsync / hipFreeAsync) on the caller's stream.
+ *   present.  Its per-edge workspace (receiver offsets and source terms,
+ *   4*(N+1) + E*n_H*C*4 bytes) belongs to the configured model and only
+ *   grows: a launch on a larger graph than any before reallocates it (after
+ *   the previous launch that used it has finished), so callers that must
+ *   not allocate inside a launch size it first with smx_r1_plugin_reserve.
+ *   Launches of one model on different streams are ordered through an event
+ *   on that workspace.
+ * Each configure call binds its descriptor's launchers to that model: a
+ * loader that keeps an earlier descriptor keeps launching the earlier model
+ * (at most 8 models per process).
  */
 #ifndef SYMMETRIX_R1_PLUGIN_H
 #define SYMMETRIX_R1_PLUGIN_H
@@ -190,6 +198,14 @@ typedef struct SmxR1PluginIdentity {
  * kernels of its shape (channels, l_max, L_max) and fill the descriptor.
  * Uses the current HIP device.  Returns SMX_OK or SMX_ERR_*. */
 SMX_API int32_t smx_r1_plugin_configure(const char* model_path, const SmxR1PluginIdentity* identity);
+
+/* No counterpart in the reference (its generated launchers keep no
+ * workspace): size the reverse workspace of `plugin`'s model for graphs of
+ * up to num_nodes receivers and num_edges edges, so that later reverse
+ * launches of that size allocate nothing (e.g. before a caller captures them
+ * into a HIP graph).  A reverse launch on a larger graph grows the workspace
+ * itself.  Returns SMX_OK or SMX_ERR_*. */
+SMX_API int32_t smx_r1_plugin_reserve(const SymmetrixJitHipPluginV1* plugin, int64_t num_nodes, int64_t num_edges);
 
 /* No counterpart in the reference: the configured model's R1 spline table in
  * the plugin layout [1][intervals][4][functions] (FP32; one edge type, the

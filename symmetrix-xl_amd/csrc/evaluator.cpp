@@ -258,6 +258,7 @@ struct Evaluator {
     DevBuf d_pair_R0, d_pair_R1, d_pair_D0, d_pair_D1, d_type_to_active, d_edge_pair;
     int* h_invalid = nullptr;
     hipEvent_t geometry_done = nullptr;
+    hipEvent_t caller_ready = nullptr;  // LAMMPS V2: the caller's stream, waited on
     bool geometry_flag_pending = false;
     int stress_blocks = 256;
 
@@ -281,6 +282,7 @@ struct Evaluator {
         SMX_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
         SMX_HIP(hipHostMalloc(reinterpret_cast<void**>(&h_invalid), sizeof(int), hipHostMallocDefault));
         SMX_HIP(hipEventCreateWithFlags(&geometry_done, hipEventDisableTiming));
+        SMX_HIP(hipEventCreateWithFlags(&caller_ready, hipEventDisableTiming));
         upload_model();
         define_groups();
         SMX_HIP(hipStreamSynchronize(stream));
@@ -293,6 +295,7 @@ struct Evaluator {
             (void)hipStreamDestroy(stream);
         }
         if (geometry_done) (void)hipEventDestroy(geometry_done);
+        if (caller_ready) (void)hipEventDestroy(caller_ready);
         if (h_invalid) (void)hipHostFree(h_invalid);
     }
 
@@ -849,6 +852,8 @@ struct Evaluator {
             ks->layer1_forward(dm, g, t, ws, true, stream, tm);
         }
         post_geometry_flag();
+        // LAMMPS rows receive tile forces from the next sweep on: raise first
+        if (lmp) raise_if_invalid_geometry("LAMMPS positions");
         for (const auto& t : tiles) {
             tile_geometry(t, positions);
             ks->layer2(dm, g, t, ws, stream, tm);
@@ -880,6 +885,20 @@ struct Evaluator {
         launch_virial_accumulate(t.ne, ws.node_forces, tile_xyz(t), d_stress_partial.as<double>(), stress_blocks,
                                  d_virial.as<double>(), stream);
         if (tm) tm->end("tile_reductions", stream);
+    }
+
+    // wait for the invalid-edge count queued after the first geometry pass
+    // (the model kernels behind it keep running) and raise if it is not zero
+    void raise_if_invalid_geometry(const char* what) {
+        if (!geometry_flag_pending) return;
+        geometry_flag_pending = false;
+        SMX_HIP(hipEventSynchronize(geometry_done));
+        const int invalid = *h_invalid;
+        if (invalid > 0) {
+            evaluated = false;
+            throw std::invalid_argument(std::string(what) + " produced an invalid edge geometry (" +
+                                        std::to_string(invalid) + " zero-length or non-finite edges)");
+        }
     }
 
     // drain the stream; launch timings recorded so far become readable
@@ -950,6 +969,13 @@ struct Evaluator {
     void update_cell(std::uint64_t token, const double* cell_, const double* inv_) {
         check_generation(token);
         if (!has_fractional) throw std::logic_error("the prepared graph has no periodic geometry reference");
+        for (int k = 0; k < 9; ++k)
+            if (!std::isfinite(cell_[k]) || !std::isfinite(inv_[k]))
+                throw std::invalid_argument("cell matrices contain a non-finite value");
+        const double det = cell_[0] * (cell_[4] * cell_[8] - cell_[5] * cell_[7]) -
+                           cell_[1] * (cell_[3] * cell_[8] - cell_[5] * cell_[6]) +
+                           cell_[2] * (cell_[3] * cell_[7] - cell_[4] * cell_[6]);
+        if (!std::isfinite(det) || det == 0.0) throw std::invalid_argument("the cell matrix must be invertible");
         std::memcpy(cell, cell_, sizeof(cell));
         std::memcpy(inv_cell, inv_, sizeof(inv_cell));
     }
@@ -1097,6 +1123,14 @@ struct Evaluator {
         if (a.stride_atom < 0 || a.stride_neighbor < 0) throw std::invalid_argument("neighbour strides must be >= 0");
         const LammpsList L{a.ilist, a.numneigh, a.neighbors, a.stride_atom, a.stride_neighbor, a.type,
                            a.type_to_model, a.ntypes, a.owner};
+        // order after the caller's device work on x and f
+        if (a.struct_size >= sizeof(SmxLammpsArgsV2)) {
+            const auto* v2 = reinterpret_cast<const SmxLammpsArgsV2*>(&a);
+            SMX_HIP(hipEventRecord(caller_ready, static_cast<hipStream_t>(v2->stream)));
+            SMX_HIP(hipStreamWaitEvent(stream, caller_ready, 0));
+        } else {
+            SMX_HIP(hipDeviceSynchronize());
+        }
         if (a.rebuild || l_generation == 0 || l_generation != generation || a.inum != l_inum || a.nall != l_nall)
             lammps_topology(a, L);
         // edge vectors are made per tile from a.x (tile_geometry); forces of
@@ -1111,6 +1145,8 @@ struct Evaluator {
         lmp = &a;
         evaluate(nullptr);
         lmp = nullptr;
+        // an invalid geometry raises before anything is added to f or eatom
+        raise_if_invalid_geometry("LAMMPS positions");
         if (!tiled) {
             lammps_forces(a.nall, l_joff.as<int>(), l_jedges.as<int>(), l_node_of_atom.as<int>(), d_offsets.as<int>(),
                           ws.node_forces, a.f, stream);
@@ -1124,18 +1160,6 @@ struct Evaluator {
         SMX_HIP(hipMemcpyAsync(&total, d_total.as<double>(), sizeof(double), hipMemcpyDeviceToHost, stream));
         SMX_HIP(hipMemcpyAsync(w, d_virial.as<double>(), sizeof(w), hipMemcpyDeviceToHost, stream));
         sync();
-        // the count copied after the first geometry pass (the tiled plan
-        // makes each tile's edge vectors again in its later sweeps)
-        int invalid = 0;
-        if (geometry_flag_pending) {
-            geometry_flag_pending = false;
-            invalid = *h_invalid;
-        }
-        if (invalid > 0) {
-            evaluated = false;
-            throw std::invalid_argument("LAMMPS positions produced an invalid edge geometry (" +
-                                        std::to_string(invalid) + " zero-length or non-finite edges)");
-        }
         // w[a*3+b] = sum_e f_a xyz_b; LAMMPS order xx, yy, zz, xy, xz, yz
         if (energy) *energy = total;
         if (virial6) {

@@ -7,11 +7,19 @@
 //               num_neigh), output assigned;
 //   reverse  -> receiver offsets from edge_receivers (binary search),
 //               k_r1_reverse (directed forces subtracted, per-edge source
-//               terms W into a stream-ordered workspace), then
-//               k_source_gather adding the FP64 source sums to
-//               source_adjoint over the caller's source transpose.
+//               terms W into the state's workspace), then k_source_gather
+//               adding the FP64 source sums to source_adjoint over the
+//               caller's source transpose.
+//
+// Each configured model owns one launcher slot: the descriptor of a
+// configure call holds function pointers instantiated for that slot, so a
+// loader that keeps an earlier descriptor keeps launching that model.  The
+// reverse workspace belongs to the state and only grows (at a launch that
+// needs more, or at smx_r1_plugin_reserve); an event orders its reuse
+// across streams.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <climits>
 #include <cmath>
 #include <cstring>
@@ -59,16 +67,64 @@ struct PluginState {
     int intervals = 0;
     double h = 0.0, x0 = 0.0;
     bool configured = false;
+    // reverse workspace: receiver offsets and per-edge source terms W
+    std::mutex ws_mutex;
+    void* ws = nullptr;
+    std::size_t ws_bytes = 0;
+    hipEvent_t ws_done = nullptr;  // recorded after the last launch that used ws
+    hipStream_t ws_stream = nullptr;
+    bool ws_used = false;
     ~PluginState() {
+        if (ws_done) (void)hipEventSynchronize(ws_done);
+        if (ws) (void)hipFree(ws);
+        if (ws_done) (void)hipEventDestroy(ws_done);
         if (cg) (void)hipFree(cg);
     }
 };
 
+// Bytes of the reverse workspace for a graph: receiver offsets [N+1] padded
+// to 256 B, then W [E][NH][C] floats.
+std::size_t reverse_offsets_bytes(std::int64_t N) {
+    return ((static_cast<std::size_t>(N) + 1) * sizeof(int) + 255) / 256 * 256;
+}
+std::size_t reverse_workspace_bytes(const PluginState& st, std::int64_t N, std::int64_t E) {
+    return reverse_offsets_bytes(N) + static_cast<std::size_t>(E) * st.NH * st.C * sizeof(float);
+}
+
+// Grow the state's workspace to at least `bytes` (caller holds ws_mutex):
+// the previous buffer is freed once its last launch has finished.
+hipError_t grow_workspace(PluginState& st, std::size_t bytes) {
+    if (bytes <= st.ws_bytes) return hipSuccess;
+    if (!st.ws_done) {
+        const hipError_t e = hipEventCreateWithFlags(&st.ws_done, hipEventDisableTiming);
+        if (e != hipSuccess) return e;
+    }
+    if (st.ws) {
+        if (st.ws_used) {
+            const hipError_t e = hipEventSynchronize(st.ws_done);
+            if (e != hipSuccess) return e;
+        }
+        (void)hipFree(st.ws);
+        st.ws = nullptr;
+        st.ws_bytes = 0;
+    }
+    const hipError_t e = hipMalloc(&st.ws, bytes);
+    if (e != hipSuccess) {
+        st.ws = nullptr;
+        return e;
+    }
+    st.ws_bytes = bytes;
+    st.ws_used = false;
+    return hipSuccess;
+}
+
 std::mutex g_mutex;
-// configured states; earlier ones stay alive because a loader may still
-// hold their descriptor
+// configured states, each bound to one launcher slot; they stay alive because
+// a loader may still hold their descriptor
+constexpr int kSlots = 8;
 std::vector<std::unique_ptr<PluginState>> g_states;
-PluginState* g_active = nullptr;  // read by the launchers and the query
+std::atomic<PluginState*> g_slot[kSlots];
+PluginState* g_active = nullptr;  // the query's answer (guarded by g_mutex)
 
 template <int NY>
 PluginEdges<NY> plugin_edges(const PluginState& st, const SymmetrixJitHipRadialSplineV1& radial,
@@ -102,9 +158,9 @@ bool radial_ok(const PluginState& st, const SymmetrixJitHipRadialSplineV1& r, un
            std::isfinite(r.h) && r.h > 0.0 && std::isfinite(r.x0);
 }
 
-template <int C, int LMAX, int LMAXH>
+template <int C, int LMAX, int LMAXH, int SLOT>
 int32_t forward_launch(const SymmetrixJitHipR1ForwardArgsV1* a, void* stream, int32_t persistent_blocks) {
-    PluginState* st = g_active;
+    PluginState* st = g_slot[SLOT].load(std::memory_order_acquire);
     if (!st || !a || a->struct_size < sizeof(SymmetrixJitHipR1ForwardArgsV1) || a->num_nodes < 0 ||
         a->num_nodes > INT32_MAX || a->num_edges < 0 || a->num_edges > INT32_MAX || !std::isfinite(a->cutoff) ||
         a->cutoff <= 0.0 || a->active_type_count == 0 || persistent_blocks <= 0 ||
@@ -128,50 +184,87 @@ int32_t forward_launch(const SymmetrixJitHipR1ForwardArgsV1* a, void* stream, in
     return static_cast<int32_t>(hipPeekAtLastError());
 }
 
-template <int C, int LMAX, int LMAXH>
-int32_t reverse_launch(const SymmetrixJitHipR1SourceArgsV1* s, const SymmetrixJitHipR1EdgeArgsV1* e, void* stream,
-                       int32_t persistent_blocks) {
-    PluginState* st = g_active;
+// Checks of the reverse packets (jit_codegen.py:3346-3410); hipSuccess when
+// the launch may proceed.
+hipError_t check_reverse(const PluginState* st, const SymmetrixJitHipR1SourceArgsV1* s,
+                         const SymmetrixJitHipR1EdgeArgsV1* e, int32_t persistent_blocks) {
     if (!st || !s || !e || s->struct_size < sizeof(SymmetrixJitHipR1SourceArgsV1) ||
         e->struct_size < sizeof(SymmetrixJitHipR1EdgeArgsV1) || s->num_nodes < 0 || s->num_nodes > INT32_MAX ||
         s->num_edges < 0 || s->num_edges > INT32_MAX || s->num_edges != e->num_edges ||
         s->num_nodes != e->num_nodes || s->active_type_count != e->active_type_count || s->cutoff != e->cutoff ||
         !std::isfinite(s->cutoff) || s->cutoff <= 0.0 || s->active_type_count == 0 || persistent_blocks <= 0 ||
         !radial_ok(*st, s->radial, s->active_type_count) || !radial_ok(*st, e->radial, e->active_type_count))
-        return static_cast<int32_t>(hipErrorInvalidValue);
-    if (s->num_nodes == 0 || s->num_edges == 0) return static_cast<int32_t>(hipSuccess);
+        return hipErrorInvalidValue;
+    if (s->num_nodes == 0 || s->num_edges == 0) return hipSuccess;
     const bool unit = e->coordinates_are_unit != 0;
     if (!e->node_types || !e->neigh_indices || !e->neigh_types || !e->edge_receivers || !e->type_to_active ||
         !e->xyz || !e->radius || !e->harmonics_values || !e->harmonics_gradients || !e->neighbor_features ||
         !e->output_adjoint || !e->directed_forces || !s->source_offsets || !s->source_edges ||
         !s->source_adjoint || e->coordinate_scalar_size != (unit ? sizeof(float) : sizeof(double)))
-        return static_cast<int32_t>(hipErrorInvalidValue);
+        return hipErrorInvalidValue;
+    return hipSuccess;
+}
+
+// The reverse kernels over a workspace of reverse_workspace_bytes(N, E):
+// receiver offsets, then W.
+template <int C, int LMAX, int LMAXH>
+hipError_t reverse_kernels(const PluginState& st, const SymmetrixJitHipR1SourceArgsV1* s,
+                           const SymmetrixJitHipR1EdgeArgsV1* e, hipStream_t hs, void* ws) {
     using S = Shape<LMAX, LMAXH>;
     const int N = static_cast<int>(s->num_nodes);
     const std::int64_t E = s->num_edges;
-    const auto hs = static_cast<hipStream_t>(stream);
-    // stream-ordered workspace: receiver offsets [N+1] (padded) and W [E][NH][C]
-    const std::size_t off_bytes = ((static_cast<std::size_t>(N) + 1) * sizeof(int) + 255) / 256 * 256;
-    const std::size_t w_bytes = static_cast<std::size_t>(E) * S::NH * C * sizeof(float);
-    void* ws = nullptr;
-    hipError_t err = hipMallocAsync(&ws, off_bytes + w_bytes, hs);
-    if (err != hipSuccess) return static_cast<int32_t>(err);
+    const bool unit = e->coordinates_are_unit != 0;
     int* offsets = static_cast<int*>(ws);
-    float* W = reinterpret_cast<float*>(static_cast<char*>(ws) + off_bytes);
+    float* W = reinterpret_cast<float*>(static_cast<char*>(ws) + reverse_offsets_bytes(N));
     k_offsets_from_receivers<<<blocks_for(static_cast<std::int64_t>(N) + 1, 256), 256, 0, hs>>>(
         N, static_cast<int>(E), e->edge_receivers, offsets);
-    const auto edges = plugin_edges<S::NY>(*st, e->radial, e->radius, e->harmonics_values, e->harmonics_gradients,
+    const auto edges = plugin_edges<S::NY>(st, e->radial, e->radius, e->harmonics_values, e->harmonics_gradients,
                                            e->xyz, unit, e->node_types, e->neigh_types, e->type_to_active,
                                            e->active_type_count, e->cutoff);
     constexpr unsigned kAll = SourceGroups<LMAX, LMAXH>::masks[0];
     k_r1_reverse<C, LMAX, LMAXH, kAll, true, PluginEdges<S::NY>><<<static_cast<unsigned>(N), C, 0, hs>>>(
-        0, 0, offsets, e->neigh_indices, edges, static_cast<const float*>(e->neighbor_features), st->cg,
+        0, 0, offsets, e->neigh_indices, edges, static_cast<const float*>(e->neighbor_features), st.cg,
         static_cast<const float*>(e->output_adjoint), W, e->directed_forces);
     k_source_gather<C, S::NH, true><<<static_cast<unsigned>(N), C, 0, hs>>>(
         s->source_offsets, s->source_edges, W, e->radius, e->cutoff, static_cast<float*>(s->source_adjoint));
-    err = hipPeekAtLastError();
-    const hipError_t ferr = hipFreeAsync(ws, hs);
-    return static_cast<int32_t>(err != hipSuccess ? err : ferr);
+    return hipPeekAtLastError();
+}
+
+template <int C, int LMAX, int LMAXH, int SLOT>
+int32_t reverse_launch(const SymmetrixJitHipR1SourceArgsV1* s, const SymmetrixJitHipR1EdgeArgsV1* e, void* stream,
+                       int32_t persistent_blocks) {
+    PluginState* st = g_slot[SLOT].load(std::memory_order_acquire);
+    hipError_t err = check_reverse(st, s, e, persistent_blocks);
+    if (err != hipSuccess || s->num_nodes == 0 || s->num_edges == 0) return static_cast<int32_t>(err);
+    const auto hs = static_cast<hipStream_t>(stream);
+    std::lock_guard<std::mutex> lock(st->ws_mutex);
+    err = grow_workspace(*st, reverse_workspace_bytes(*st, s->num_nodes, s->num_edges));
+    if (err != hipSuccess) return static_cast<int32_t>(err);
+    // a launch on another stream than the workspace's last one waits for it
+    if (st->ws_used && st->ws_stream != hs) {
+        err = hipStreamWaitEvent(hs, st->ws_done, 0);
+        if (err != hipSuccess) return static_cast<int32_t>(err);
+    }
+    err = reverse_kernels<C, LMAX, LMAXH>(*st, s, e, hs, st->ws);
+    const hipError_t rec = hipEventRecord(st->ws_done, hs);
+    st->ws_stream = hs;
+    st->ws_used = true;
+    return static_cast<int32_t>(err != hipSuccess ? err : rec);
+}
+
+// Launcher pointers of one shape for slot `slot`.
+template <int C, int LMAX, int LMAXH, int SLOT = 0>
+bool slot_launchers(int slot, SymmetrixJitHipR1ForwardLaunchV1& fwd, SymmetrixJitHipR1CoordinateReverseLaunchV1& rev) {
+    if constexpr (SLOT < kSlots) {
+        if (slot == SLOT) {
+            fwd = &forward_launch<C, LMAX, LMAXH, SLOT>;
+            rev = &reverse_launch<C, LMAX, LMAXH, SLOT>;
+            return true;
+        }
+        return slot_launchers<C, LMAX, LMAXH, SLOT + 1>(slot, fwd, rev);
+    } else {
+        return false;
+    }
 }
 
 }  // namespace
@@ -192,6 +285,7 @@ int32_t smx_r1_plugin_configure(const char* model_path, const SmxR1PluginIdentit
             throw std::invalid_argument("artifact id and contract fingerprint are required");
         if (id->embedding <= 0 || id->persistent_blocks_per_compute_unit <= 0)
             throw std::invalid_argument("embedding and persistent blocks per compute unit must be positive");
+        std::lock_guard<std::mutex> lock(smx::g_mutex);
         smx::HostModel hm;
         hm.load(model_path, "");
         auto st = std::make_unique<smx::PluginState>();
@@ -209,12 +303,14 @@ int32_t smx_r1_plugin_configure(const char* model_path, const SmxR1PluginIdentit
         if (!smx::kernel_paths(hm.l_max, hm.L_max, le, ls, lo) || le != hm.path_le ||
             ls != hm.path_ls || lo != hm.path_lo)
             throw std::domain_error("the model's R1 paths have no compiled kernels");
+        const int slot = static_cast<int>(smx::g_states.size());
+        if (slot >= smx::kSlots)
+            throw std::logic_error("at most " + std::to_string(smx::kSlots) +
+                                   " R1 plugin models can be configured in one process");
         if (hm.C == 32 && hm.l_max == 2 && hm.L_max == 1) {
-            fwd = &smx::forward_launch<32, 2, 1>;
-            rev = &smx::reverse_launch<32, 2, 1>;
+            smx::slot_launchers<32, 2, 1>(slot, fwd, rev);
         } else if (hm.C == 128 && hm.l_max == 3 && hm.L_max == 1) {
-            fwd = &smx::forward_launch<128, 3, 1>;
-            rev = &smx::reverse_launch<128, 3, 1>;
+            smx::slot_launchers<128, 3, 1>(slot, fwd, rev);
         } else {
             throw std::domain_error("no R1 kernels are compiled for " + std::to_string(hm.C) + " channels, l_max " +
                                     std::to_string(hm.l_max) + ", L_max " + std::to_string(hm.L_max));
@@ -265,9 +361,9 @@ int32_t smx_r1_plugin_configure(const char* model_path, const SmxR1PluginIdentit
         d.r1_forward_launch = fwd;
         d.r1_coordinate_reverse_launch = rev;
         st->configured = true;
-        std::lock_guard<std::mutex> lock(smx::g_mutex);
         smx::g_states.push_back(std::move(st));
         smx::g_active = smx::g_states.back().get();
+        smx::g_slot[slot].store(smx::g_active, std::memory_order_release);
         return SMX_OK;
     } catch (const std::bad_alloc&) {
         smx::set_last_error("out of memory (device or host allocation failed)");
@@ -278,6 +374,9 @@ int32_t smx_r1_plugin_configure(const char* model_path, const SmxR1PluginIdentit
     } catch (const std::invalid_argument& e) {
         smx::set_last_error(e.what());
         return SMX_ERR_INVALID_ARGUMENT;
+    } catch (const std::logic_error& e) {
+        smx::set_last_error(e.what());
+        return SMX_ERR_LOGIC;
     } catch (const std::exception& e) {
         smx::set_last_error(e.what());
         return SMX_ERR_RUNTIME;
@@ -285,6 +384,30 @@ int32_t smx_r1_plugin_configure(const char* model_path, const SmxR1PluginIdentit
         smx::set_last_error("unknown error");
         return SMX_ERR_RUNTIME;
     }
+}
+
+int32_t smx_r1_plugin_reserve(const SymmetrixJitHipPluginV1* plugin, int64_t num_nodes, int64_t num_edges) {
+    smx::PluginState* st = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(smx::g_mutex);
+        for (const auto& p : smx::g_states)
+            if (&p->descriptor == plugin) st = p.get();
+    }
+    if (!st) {
+        smx::set_last_error("the descriptor was not returned by this library's R1 plugin query");
+        return SMX_ERR_INVALID_ARGUMENT;
+    }
+    if (num_nodes < 0 || num_nodes > INT32_MAX || num_edges < 0 || num_edges > INT32_MAX) {
+        smx::set_last_error("node and edge counts must lie in [0, 2^31)");
+        return SMX_ERR_INVALID_ARGUMENT;
+    }
+    std::lock_guard<std::mutex> lock(st->ws_mutex);
+    const hipError_t e = smx::grow_workspace(*st, smx::reverse_workspace_bytes(*st, num_nodes, num_edges));
+    if (e != hipSuccess) {
+        smx::set_last_error(std::string("R1 plugin workspace: ") + hipGetErrorString(e));
+        return e == hipErrorOutOfMemory ? SMX_ERR_OUT_OF_MEMORY : SMX_ERR_RUNTIME;
+    }
+    return SMX_OK;
 }
 
 int32_t smx_r1_plugin_spline_table(float* out, int64_t capacity, int32_t* intervals, int32_t* functions, double* h,

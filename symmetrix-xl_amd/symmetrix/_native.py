@@ -62,6 +62,12 @@ class SmxLammpsArgsV1(ctypes.Structure):
                 ("reserved", ctypes.c_int32), ("f", ctypes.c_void_p), ("eatom", ctypes.c_void_p)]
 
 
+class SmxLammpsArgsV2(ctypes.Structure):
+    """SmxLammpsArgsV1 followed by the caller's hipStream_t: the call waits
+    for the work the caller queued there instead of synchronising the device."""
+    _fields_ = SmxLammpsArgsV1._fields_ + [("stream", ctypes.c_void_p)]
+
+
 # (name, restype, argtypes) of every exported entry point
 _i32 = ctypes.c_int32
 _i64 = ctypes.c_int64
@@ -112,6 +118,7 @@ SIGNATURES = [
     ("smx_neighbor_list", _i32, [_i32, _vp, _vp, _vp, _dbl, _p_i64, _vp, _vp, _vp, _vp, _vp]),
     ("smx_r1_plugin_configure", _i32, [_cp, ctypes.POINTER(SmxR1PluginIdentity)]),
     ("smx_r1_plugin_spline_table", _i32, [_vp, _i64, _p_i32, _p_i32, _p_dbl, _p_dbl]),
+    ("smx_r1_plugin_reserve", _i32, [_vp, _i64, _i64]),
     ("smx_model_array_f32", _i32, [_cp, _cp, _vp, _i64, _p_i64, _p_i32, _p_dbl, _p_dbl]),
     ("smx_model_array_i32", _i32, [_cp, _cp, _vp, _i64, _p_i64, _p_i32]),
 ]

@@ -229,14 +229,17 @@ class MACEKokkosFloat:
 
     def _lammps_compute(self, args):
         """smx_lammps_compute (the pair style's single-rank path) with an
-        SmxLammpsArgsV1 of device pointers; returns (energy, virial[6])."""
-        from ._native import SmxLammpsArgsV1
-        if not isinstance(args, SmxLammpsArgsV1):
-            raise TypeError("args must be an SmxLammpsArgsV1")
-        args.struct_size = ctypes.sizeof(SmxLammpsArgsV1)
+        SmxLammpsArgsV1 (device synchronised on entry) or SmxLammpsArgsV2
+        (ordered after args.stream) of device pointers; returns (energy,
+        virial[6])."""
+        from ._native import SmxLammpsArgsV1, SmxLammpsArgsV2
+        if not isinstance(args, (SmxLammpsArgsV1, SmxLammpsArgsV2)):
+            raise TypeError("args must be an SmxLammpsArgsV1 or SmxLammpsArgsV2")
+        args.struct_size = ctypes.sizeof(type(args))
         energy = ctypes.c_double()
         virial = (ctypes.c_double * 6)()
-        check(lib.smx_lammps_compute(self._h, ctypes.byref(args), ctypes.byref(energy), virial))
+        check(lib.smx_lammps_compute(self._h, ctypes.cast(ctypes.byref(args), ctypes.POINTER(SmxLammpsArgsV1)),
+                                     ctypes.byref(energy), virial))
         return energy.value, np.array(virial[:])
 
     def set_kernel_timing(self, enabled=True):

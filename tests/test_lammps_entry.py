@@ -72,8 +72,10 @@ def _lammps_arrays(positions, cell, numbers, cutoff, lmp_type_of_z):
     return allpos, owner, alltypes, rows
 
 
-def _run(ev, hip, allpos, owner, alltypes, rows, ilist, type_to_model, rebuild):
-    from symmetrix._native import SmxLammpsArgsV1
+def _args(hip, allpos, owner, alltypes, rows, ilist, type_to_model, rebuild, f0=None, eatom0=None, stream=None):
+    """LAMMPS-shaped arguments on the device (SmxLammpsArgsV2 when a stream
+    is given), with f and eatom starting from f0 / eatom0 (zero)."""
+    from symmetrix._native import SmxLammpsArgsV1, SmxLammpsArgsV2
     n, nall = len(rows), len(allpos)
     maxn = max(len(r) for r in rows)
     # column-major [maxn][n] with special-bond bits on every 7th entry
@@ -83,9 +85,9 @@ def _run(ev, hip, allpos, owner, alltypes, rows, ilist, type_to_model, rebuild):
         marked[::7] |= (1 << 30)
         nb[:len(r), i] = marked
     numneigh = np.array([len(r) for r in rows], np.int32)
-    f = np.zeros((nall, 3))
-    eatom = np.zeros(nall)
-    a = SmxLammpsArgsV1()
+    f = np.zeros((nall, 3)) if f0 is None else np.array(f0, dtype=np.float64)
+    eatom = np.zeros(nall) if eatom0 is None else np.array(eatom0, dtype=np.float64)
+    a = SmxLammpsArgsV1() if stream is None else SmxLammpsArgsV2()
     a.inum, a.nall, a.ntypes = n, nall, len(type_to_model)
     a.ilist = hip.put(ilist)
     a.numneigh = hip.put(numneigh)
@@ -98,6 +100,13 @@ def _run(ev, hip, allpos, owner, alltypes, rows, ilist, type_to_model, rebuild):
     a.rebuild = 1 if rebuild else 0
     a.f = hip.put(f)
     a.eatom = hip.put(eatom)
+    if stream is not None:
+        a.stream = stream
+    return a, f, eatom
+
+
+def _run(ev, hip, allpos, owner, alltypes, rows, ilist, type_to_model, rebuild):
+    a, f, eatom = _args(hip, allpos, owner, alltypes, rows, ilist, type_to_model, rebuild)
     energy, virial = ev._lammps_compute(a)
     return energy, virial, hip.get(a.f, f), hip.get(a.eatom, eatom)
 
@@ -206,13 +215,74 @@ def test_lammps_entry_zero_length_edge_raises_and_next_call_recovers(tiny_model_
     hip = _Hip()
     try:
         e0, v0, f0, _ = _run(ev, hip, allpos, owner, alltypes, rows, ilist, type_to_model, True)
+        # the failed call leaves the caller's force and energy rows as they were
+        rng = np.random.default_rng(1)
+        fill_f, fill_e = rng.normal(size=(len(bad), 3)), rng.normal(size=len(bad))
+        a, _, _ = _args(hip, bad, owner, alltypes, rows, ilist, type_to_model, False, fill_f, fill_e)
         with pytest.raises(ValueError, match=r"invalid edge geometry \(1 zero-length"):
-            _run(ev, hip, bad, owner, alltypes, rows, ilist, type_to_model, False)
+            ev._lammps_compute(a)
+        np.testing.assert_array_equal(hip.get(a.f, fill_f), fill_f)
+        np.testing.assert_array_equal(hip.get(a.eatom, fill_e), fill_e)
         e1, v1, f1, _ = _run(ev, hip, allpos, owner, alltypes, rows, ilist, type_to_model, False)
         assert e1 == e0
         np.testing.assert_array_equal(f1, f0)
         np.testing.assert_array_equal(v1, v0)
     finally:
+        hip.free()
+
+
+@pytest.mark.parametrize("version", ["v1", "v2"])
+def test_lammps_entry_orders_after_caller_stream(tiny_model_path, version):
+    """The caller updates x and clears f with asynchronous copies on its own
+    stream (behind a long fill, as Kokkos queues fix nve and force_clear)
+    right before the call; V2 passes that stream, V1 relies on the device
+    synchronisation on entry.  The results are those of the new positions
+    (the oracle's) with f cleared first."""
+    from oracle import oracle
+    from symmetrix import systems
+    from symmetrix.mace_kokkos import MACEKokkosFloat
+    h = ctypes.CDLL("libamdhip64.so")
+    h.hipStreamCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+    h.hipStreamDestroy.argtypes = [ctypes.c_void_p]
+    h.hipMemcpyAsync.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_void_p]
+    h.hipMemsetAsync.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t, ctypes.c_void_p]
+    h.hipStreamSynchronize.argtypes = [ctypes.c_void_p]
+    s = systems.srtio3_supercell(3, sigma=0.05, seed=0)
+    ev = MACEKokkosFloat(tiny_model_path)
+    om = oracle.OracleModel(tiny_model_path)
+    model_of_z = {int(z): k for k, z in enumerate(ev.atomic_numbers)}
+    type_to_model = [model_of_z[8], model_of_z[22], model_of_z[38]]
+    cell = np.asarray(s["cell"], float)
+    allpos, owner, alltypes, rows = _lammps_arrays(s["positions"], cell, s["numbers"], ev.r_cut + 0.5,
+                                                   {8: 1, 22: 2, 38: 3})
+    n = len(rows)
+    moved = s["positions"] + np.random.default_rng(7).normal(scale=0.02, size=s["positions"].shape)
+    shifts = allpos[n:] - np.tile(s["positions"], (26, 1))
+    moved_all = np.concatenate([moved, np.tile(moved, (26, 1)) + shifts])
+    ref = oracle.evaluate_system(om, s, positions=moved)
+    ilist = np.arange(n, dtype=np.int32)
+    hip = _Hip()
+    stream = ctypes.c_void_p()
+    assert h.hipStreamCreate(ctypes.byref(stream)) == 0
+    try:
+        # first call builds the list on the old positions
+        _run(ev, hip, allpos, owner, alltypes, rows, ilist, type_to_model, True)
+        a, _, _ = _args(hip, allpos, owner, alltypes, rows, ilist, type_to_model, False,
+                        f0=np.full((len(allpos), 3), 1e3), stream=stream.value if version == "v2" else None)
+        staged = hip.put(moved_all)
+        big = hip.put(np.zeros(1 << 27, np.uint8))   # 128 MiB fill ahead of the updates
+        assert h.hipMemsetAsync(big, 0, 1 << 27, stream) == 0
+        assert h.hipMemcpyAsync(a.x, staged, moved_all.nbytes, 3, stream) == 0
+        assert h.hipMemsetAsync(a.f, 0, len(allpos) * 24, stream) == 0
+        energy, virial = ev._lammps_compute(a)
+        assert h.hipStreamSynchronize(stream) == 0
+        f = hip.get(a.f, np.zeros((len(allpos), 3)))
+        folded = np.zeros((n, 3))
+        np.add.at(folded, owner, f)
+        assert abs(energy - ref["energy"]) / n < E_TOL
+        assert np.max(np.abs(folded - ref["forces"])) < F_TOL
+    finally:
+        h.hipStreamDestroy(stream)
         hip.free()
 
 

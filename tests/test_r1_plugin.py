@@ -45,87 +45,113 @@ def test_query_is_null_until_configured_and_bad_model_is_rejected(tmp_path):
     assert r1_plugin.descriptor() is None
 
 
+class _PluginCase:
+    """Device arrays of the tiny system in the reference's per-edge layout,
+    with the oracle's R1 stages as inputs and references."""
+
+    def __init__(self, model_path):
+        from _hip import DeviceArray
+        from oracle import oracle
+        from symmetrix import systems
+
+        s = systems.srtio3_supercell(3, sigma=0.05, seed=0)
+        om = oracle.OracleModel(model_path)
+        ref = oracle.evaluate_system(om, s, skin=0.5)
+        self.om, self.ref = om, ref
+        g = ref["graph"]
+        self.N = N = len(s["numbers"])
+        self.E = E = len(g["sources"])
+        self.C = om.num_channels
+        types = om.types_of(s["numbers"]).astype(np.int32)
+        self.ntypes = ntypes = int(types.max()) + 1
+        self.offsets = offsets = g["offsets"].astype(np.int32)
+        self.sources = sources = g["sources"].astype(np.int32)
+        self.receivers = receivers = np.repeat(np.arange(N, dtype=np.int32), np.diff(offsets))
+        self.d_types = DeviceArray(types)
+        self.d_num = DeviceArray(np.diff(offsets).astype(np.int32))
+        self.d_first = DeviceArray(offsets[:-1].copy())
+        self.d_src = DeviceArray(sources)
+        self.d_ntypes = DeviceArray(types[sources])
+        self.d_map = DeviceArray(np.arange(ntypes, dtype=np.int32))
+        self.d_r = DeviceArray(ref["r"].astype(np.float64))
+        self.d_xyz = DeviceArray(ref["xyz"].astype(np.float64))
+        self.d_Y = DeviceArray(om.stage("Y").astype(np.float32))
+        self.d_G = DeviceArray(om.stage("Ygrad").astype(np.float32))
+        self.d_H1 = DeviceArray(om.stage("H1").astype(np.float32))
+        self.d_dphi = DeviceArray(om.stage("dPhi1").astype(np.float32))
+        order = np.argsort(sources, kind="stable")
+        soff = np.zeros(N + 1, np.int32)
+        np.cumsum(np.bincount(sources, minlength=N), out=soff[1:])
+        self.d_soff = DeviceArray(soff)
+        self.d_sedges = DeviceArray(order.astype(np.int32))
+        self.d_recv = DeviceArray(receivers)
+        self.cutoff = om.r_cut
+
+    def radial(self):
+        from _hip import DeviceArray
+        table, h, x0 = r1_plugin.spline_table()
+        pairs = self.ntypes * (self.ntypes + 1) // 2
+        self._coef = DeviceArray(np.repeat(table, pairs, axis=0))   # same tabulation for every pair type
+        return r1_plugin.RadialSpline(ctypes.sizeof(r1_plugin.RadialSpline), pairs, table.shape[1],
+                                      table.shape[3], h, x0, self._coef.value)
+
+    def forward(self, d, radial):
+        from _hip import DeviceArray, hip
+        out = DeviceArray(np.full(self.om.stage("Phi1").shape, np.nan, np.float32))
+        fa = r1_plugin.ForwardArgs(ctypes.sizeof(r1_plugin.ForwardArgs), self.ntypes, self.N, self.E,
+                                   self.d_types.value, self.d_num.value, self.d_first.value, self.d_src.value,
+                                   self.d_ntypes.value, self.d_map.value, self.d_r.value, radial, self.d_Y.value,
+                                   self.d_H1.value, out.value, self.cutoff)
+        assert d.r1_forward_launch(ctypes.byref(fa), None, 1) == 0
+        assert hip().hipDeviceSynchronize() == 0
+        return out.get(), fa
+
+    def reverse(self, d, radial, launch=None):
+        """(source adjoint added to 0.25, forces subtracted from -0.5) of one
+        reverse launch through d (or through `launch`, same arguments)."""
+        from _hip import DeviceArray, hip
+        base_adj = np.full(self.om.stage("H1_adj").shape, 0.25, np.float32)
+        d_adj = DeviceArray(base_adj)
+        base_f = np.full((self.E, 3), -0.5, np.float64)
+        d_f = DeviceArray(base_f)
+        sa = r1_plugin.SourceArgs(ctypes.sizeof(r1_plugin.SourceArgs), self.ntypes, self.N, self.E,
+                                  self.d_types.value, self.d_ntypes.value, self.d_soff.value, self.d_sedges.value,
+                                  self.d_recv.value, self.d_map.value, self.d_r.value, radial, self.d_Y.value,
+                                  self.d_dphi.value, d_adj.value, self.cutoff)
+        ea = r1_plugin.EdgeArgs(ctypes.sizeof(r1_plugin.EdgeArgs), self.ntypes, 8, 0, self.N, self.E,
+                                self.d_types.value, self.d_src.value, self.d_ntypes.value, self.d_recv.value,
+                                self.d_map.value, self.d_xyz.value, self.d_r.value, radial, self.d_Y.value,
+                                self.d_G.value, self.d_H1.value, self.d_dphi.value, d_f.value, self.cutoff)
+        rc = (launch or d.r1_coordinate_reverse_launch)(ctypes.byref(sa), ctypes.byref(ea), None, 1)
+        assert rc == 0, rc
+        assert hip().hipDeviceSynchronize() == 0
+        return d_adj.get().astype(np.float64) - 0.25, d_f.get() - base_f
+
+
 @pytest.mark.gpu
 def test_plugin_launchers_match_oracle_r1_stages(tiny_model_path):
-    from _hip import DeviceArray, hip
-    from oracle import oracle
-    from symmetrix import systems
-
-    s = systems.srtio3_supercell(3, sigma=0.05, seed=0)
-    om = oracle.OracleModel(tiny_model_path)
-    ref = oracle.evaluate_system(om, s, skin=0.5)
-    g = ref["graph"]
+    case = _PluginCase(tiny_model_path)
+    om = case.om
     d = r1_plugin.configure(tiny_model_path, artifact_id="tiny-test", contract_fingerprint="fp-tiny",
                             embedding=8)
     assert d.capabilities & (r1_plugin.FORWARD | r1_plugin.COORDINATE_REVERSE) == 3
     assert d.abi_tag == r1_plugin.ABI_TAG and d.channels == om.num_channels
     assert d.contract_fingerprint == b"fp-tiny" and d.target_architecture == b"gfx950"
+    radial = case.radial()
 
-    N = len(s["numbers"])
-    E = len(g["sources"])
-    C = om.num_channels
-    types = om.types_of(s["numbers"]).astype(np.int32)
-    ntypes = int(types.max()) + 1
-    table, h, x0 = r1_plugin.spline_table()
-    pairs = ntypes * (ntypes + 1) // 2
-    coef = DeviceArray(np.repeat(table, pairs, axis=0))   # same tabulation for every pair type
-    radial = r1_plugin.RadialSpline(ctypes.sizeof(r1_plugin.RadialSpline), pairs, table.shape[1], table.shape[3],
-                                    h, x0, coef.value)
-    offsets = g["offsets"].astype(np.int32)
-    sources = g["sources"].astype(np.int32)
-    receivers = np.repeat(np.arange(N, dtype=np.int32), np.diff(offsets))
-    d_types = DeviceArray(types)
-    d_num = DeviceArray(np.diff(offsets).astype(np.int32))
-    d_first = DeviceArray(offsets[:-1].copy())
-    d_src = DeviceArray(sources)
-    d_ntypes = DeviceArray(types[sources])
-    d_map = DeviceArray(np.arange(ntypes, dtype=np.int32))
-    d_r = DeviceArray(ref["r"].astype(np.float64))
-    d_xyz = DeviceArray(ref["xyz"].astype(np.float64))
-    d_Y = DeviceArray(om.stage("Y").astype(np.float32))
-    d_G = DeviceArray(om.stage("Ygrad").astype(np.float32))
-    d_H1 = DeviceArray(om.stage("H1").astype(np.float32))
     phi_ref = om.stage("Phi1")
-    d_out = DeviceArray(np.full(phi_ref.shape, np.nan, np.float32))
-    cutoff = om.r_cut
-
-    fa = r1_plugin.ForwardArgs(ctypes.sizeof(r1_plugin.ForwardArgs), ntypes, N, E, d_types.value, d_num.value,
-                               d_first.value, d_src.value, d_ntypes.value, d_map.value, d_r.value, radial,
-                               d_Y.value, d_H1.value, d_out.value, cutoff)
-    assert d.r1_forward_launch(ctypes.byref(fa), None, 1) == 0
-    assert hip().hipDeviceSynchronize() == 0
-    phi = d_out.get().astype(np.float64)
-    err = np.max(np.abs(phi - phi_ref)) / np.max(np.abs(phi_ref))
+    phi, fa = case.forward(d, radial)
+    err = np.max(np.abs(phi.astype(np.float64) - phi_ref)) / np.max(np.abs(phi_ref))
     print("plugin forward Phi1 relative max err %.3e" % err)
     assert err < 1e-5
 
     # coordinate reverse with the oracle's dPhi1 as the output adjoint
-    order = np.argsort(sources, kind="stable")
-    soff = np.zeros(N + 1, np.int32)
-    np.cumsum(np.bincount(sources, minlength=N), out=soff[1:])
-    d_soff = DeviceArray(soff)
-    d_sedges = DeviceArray(order.astype(np.int32))
-    d_recv = DeviceArray(receivers)
-    d_dphi = DeviceArray(om.stage("dPhi1").astype(np.float32))
+    adj, f = case.reverse(d, radial)
     h1adj_ref = om.stage("H1_adj")
-    base_adj = np.full(h1adj_ref.shape, 0.25, np.float32)   # the launcher adds to what is there
-    d_adj = DeviceArray(base_adj)
-    base_f = np.full((E, 3), -0.5, np.float64)                # and subtracts its forces
-    d_f = DeviceArray(base_f)
-    sa = r1_plugin.SourceArgs(ctypes.sizeof(r1_plugin.SourceArgs), ntypes, N, E, d_types.value, d_ntypes.value,
-                              d_soff.value, d_sedges.value, d_recv.value, d_map.value, d_r.value, radial,
-                              d_Y.value, d_dphi.value, d_adj.value, cutoff)
-    ea = r1_plugin.EdgeArgs(ctypes.sizeof(r1_plugin.EdgeArgs), ntypes, 8, 0, N, E, d_types.value, d_src.value,
-                            d_ntypes.value, d_recv.value, d_map.value, d_xyz.value, d_r.value, radial, d_Y.value,
-                            d_G.value, d_H1.value, d_dphi.value, d_f.value, cutoff)
-    assert d.r1_coordinate_reverse_launch(ctypes.byref(sa), ctypes.byref(ea), None, 1) == 0
-    assert hip().hipDeviceSynchronize() == 0
-    adj = d_adj.get().astype(np.float64) - 0.25
     err = np.max(np.abs(adj - h1adj_ref)) / np.max(np.abs(h1adj_ref))
     print("plugin source adjoint relative max err %.3e" % err)
     assert err < 1e-5
-    f = d_f.get() - base_f
-    f_ref = om.stage("node_forces_r1").reshape(E, 3)
+    f_ref = om.stage("node_forces_r1").reshape(case.E, 3)
     ferr = np.max(np.abs(f - f_ref))
     print("plugin R1 directed forces max abs err %.3e (scale %.3e)" % (ferr, np.max(np.abs(f_ref))))
     assert ferr < 1e-5
@@ -135,3 +161,34 @@ def test_plugin_launchers_match_oracle_r1_stages(tiny_model_path):
     bad.struct_size = 8
     assert d.r1_forward_launch(ctypes.byref(bad), None, 1) != 0
     assert d.r1_forward_launch(ctypes.byref(fa), None, 0) != 0
+
+
+@pytest.mark.gpu
+def test_descriptor_keeps_its_model_after_another_configure(tiny_model_path, tmp_path):
+    """A loader that holds the descriptor of model A keeps launching A after
+    model B (same shape, coupling coefficients doubled) is configured; B's
+    descriptor launches B.  The reverse workspace sized by
+    smx_r1_plugin_reserve gives the same results as one grown by a launch."""
+    import json
+    case = _PluginCase(tiny_model_path)
+    dA = r1_plugin.configure(tiny_model_path, artifact_id="model-a", contract_fingerprint="fp-a", embedding=8)
+    pA = r1_plugin._query()
+    radial = case.radial()
+    phiA, _ = case.forward(dA, radial)
+    adjA, fA = case.reverse(dA, radial)
+    with open(tiny_model_path) as fh:
+        j = json.load(fh)
+    j["Phi1_clebsch_gordan"] = [2.0 * c for c in j["Phi1_clebsch_gordan"]]
+    path_b = tmp_path / "tiny_double_cg.json"
+    path_b.write_text(json.dumps(j))
+    dB = r1_plugin.configure(str(path_b), artifact_id="model-b", contract_fingerprint="fp-b", embedding=8)
+    assert r1_plugin.descriptor().artifact_id == b"model-b"
+    phiA2, _ = case.forward(dA, radial)
+    np.testing.assert_array_equal(phiA2, phiA)
+    phiB, _ = case.forward(dB, radial)
+    np.testing.assert_allclose(phiB, 2.0 * phiA, rtol=1e-6, atol=1e-7 * np.max(np.abs(phiA)))
+    assert _native.lib.smx_r1_plugin_reserve(pA, case.N, case.E) == 0
+    adjA2, fA2 = case.reverse(dA, radial)
+    np.testing.assert_array_equal(adjA2, adjA)
+    np.testing.assert_array_equal(fA2, fA)
+    assert _native.lib.smx_r1_plugin_reserve(None, case.N, case.E) == _native.SMX_ERR_INVALID_ARGUMENT
