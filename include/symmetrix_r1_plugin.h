@@ -207,6 +207,25 @@ SMX_API int32_t smx_r1_plugin_configure(const char* model_path, const SmxR1Plugi
  * itself.  Returns SMX_OK or SMX_ERR_*. */
 SMX_API int32_t smx_r1_plugin_reserve(const SymmetrixJitHipPluginV1* plugin, int64_t num_nodes, int64_t num_edges);
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): the coordinate reverse of `plugin`'s model, with the
+ * same arguments, kernels and results as its r1_coordinate_reverse_launch,
+ * but with the workspace (receiver offsets and per-edge source terms,
+ * 4*(N+1) rounded up to 256 B, plus E*n_H*C*4 bytes) in a fixed 256 MiB
+ * device array of the library instead of allocated memory: up to about
+ * 512k edges at 32 channels and L_max 1, 131k edges at 128 channels.  Larger
+ * graphs are refused with hipErrorInvalidValue and a message in
+ * smx_last_error().  It calls no allocating routine.  The array is the
+ * current device's (each GPU holds its own copy for the life of the
+ * process); every call on a GPU shares it, so calls that overlap on one GPU
+ * (several streams, or host threads) race and must be serialised by the
+ * caller.  Returns the numeric hipError_t. */
+SMX_API int32_t smx_r1_plugin_reverse_launch_noalloc(const SymmetrixJitHipPluginV1* plugin,
+                                                     const SymmetrixJitHipR1SourceArgsV1* source_args,
+                                                     const SymmetrixJitHipR1EdgeArgsV1* edge_args, void* stream,
+                                                     int32_t persistent_blocks);
+
 /* No counterpart in the reference: the configured model's R1 spline table in
  * the plugin layout [1][intervals][4][functions] (FP32; one edge type, the
  * radial networks' tabulation being the same for every type pair), with its

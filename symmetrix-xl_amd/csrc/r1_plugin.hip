@@ -267,10 +267,89 @@ bool slot_launchers(int slot, SymmetrixJitHipR1ForwardLaunchV1& fwd, SymmetrixJi
     }
 }
 
+// ---------------------------------------------------------------------------
+// Allocation-free reverse launch: the workspace (receiver offsets and W) lives
+// in a fixed device array, one per GPU, held until the process ends.  Host
+// code uses the address hipGetSymbolAddress reports for the current device,
+// never the array's name.
+// ---------------------------------------------------------------------------
+constexpr std::size_t kScratchBytes = std::size_t(256) << 20;  // 256 MiB
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The scratch address on the current device (looked up once per device).
+hipError_t scratch_address(void** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        if (!p) return hipErrorInvalidSymbol;
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return hipSuccess;
+}
+
+PluginState* state_of(const SymmetrixJitHipPluginV1* plugin) {
+    std::lock_guard<std::mutex> lock(g_mutex);
+    for (const auto& p : g_states)
+        if (&p->descriptor == plugin) return p.get();
+    return nullptr;
+}
+
 }  // namespace
 }  // namespace smx
 
 extern "C" {
+
+int32_t smx_r1_plugin_reverse_launch_noalloc(const SymmetrixJitHipPluginV1* plugin,
+                                             const SymmetrixJitHipR1SourceArgsV1* s,
+                                             const SymmetrixJitHipR1EdgeArgsV1* e, void* stream,
+                                             int32_t persistent_blocks) {
+    smx::PluginState* st = smx::state_of(plugin);
+    if (!st) {
+        smx::set_last_error("the descriptor was not returned by this library's R1 plugin query");
+        return static_cast<int32_t>(hipErrorInvalidValue);
+    }
+    hipError_t err = smx::check_reverse(st, s, e, persistent_blocks);
+    if (err != hipSuccess) {
+        smx::set_last_error("malformed R1 reverse packets");
+        return static_cast<int32_t>(err);
+    }
+    if (s->num_nodes == 0 || s->num_edges == 0) return static_cast<int32_t>(hipSuccess);
+    const std::size_t need = smx::reverse_workspace_bytes(*st, s->num_nodes, s->num_edges);
+    if (need > smx::kScratchBytes) {
+        smx::set_last_error("the allocation-free R1 reverse launch needs " + std::to_string(need) +
+                            " bytes of workspace for " + std::to_string(s->num_nodes) + " nodes and " +
+                            std::to_string(s->num_edges) + " edges; its fixed scratch holds " +
+                            std::to_string(smx::kScratchBytes) + " bytes (" +
+                            std::to_string(st->NH * st->C * sizeof(float)) + " bytes per edge at this shape)");
+        return static_cast<int32_t>(hipErrorInvalidValue);
+    }
+    void* ws = nullptr;
+    err = smx::scratch_address(&ws);
+    if (err != hipSuccess) {
+        smx::set_last_error(std::string("scratch address: ") + hipGetErrorString(err));
+        return static_cast<int32_t>(err);
+    }
+    const auto hs = static_cast<hipStream_t>(stream);
+    if (st->C == 32 && st->l_max == 2 && st->L_max == 1)
+        err = smx::reverse_kernels<32, 2, 1>(*st, s, e, hs, ws);
+    else if (st->C == 128 && st->l_max == 3 && st->L_max == 1)
+        err = smx::reverse_kernels<128, 3, 1>(*st, s, e, hs, ws);
+    else
+        err = hipErrorInvalidValue;
+    return static_cast<int32_t>(err);
+}
+
 
 const SymmetrixJitHipPluginV1* symmetrix_jit_hip_plugin_query_v1(void) {
     std::lock_guard<std::mutex> lock(smx::g_mutex);
@@ -387,12 +466,7 @@ int32_t smx_r1_plugin_configure(const char* model_path, const SmxR1PluginIdentit
 }
 
 int32_t smx_r1_plugin_reserve(const SymmetrixJitHipPluginV1* plugin, int64_t num_nodes, int64_t num_edges) {
-    smx::PluginState* st = nullptr;
-    {
-        std::lock_guard<std::mutex> lock(smx::g_mutex);
-        for (const auto& p : smx::g_states)
-            if (&p->descriptor == plugin) st = p.get();
-    }
+    smx::PluginState* st = smx::state_of(plugin);
     if (!st) {
         smx::set_last_error("the descriptor was not returned by this library's R1 plugin query");
         return SMX_ERR_INVALID_ARGUMENT;

@@ -119,6 +119,7 @@ SIGNATURES = [
     ("smx_r1_plugin_configure", _i32, [_cp, ctypes.POINTER(SmxR1PluginIdentity)]),
     ("smx_r1_plugin_spline_table", _i32, [_vp, _i64, _p_i32, _p_i32, _p_dbl, _p_dbl]),
     ("smx_r1_plugin_reserve", _i32, [_vp, _i64, _i64]),
+    ("smx_r1_plugin_reverse_launch_noalloc", _i32, [_vp, _vp, _vp, _vp, _i32]),
     ("smx_model_array_f32", _i32, [_cp, _cp, _vp, _i64, _p_i64, _p_i32, _p_dbl, _p_dbl]),
     ("smx_model_array_i32", _i32, [_cp, _cp, _vp, _i64, _p_i64, _p_i32]),
 ]

@@ -49,12 +49,12 @@ class _PluginCase:
     """Device arrays of the tiny system in the reference's per-edge layout,
     with the oracle's R1 stages as inputs and references."""
 
-    def __init__(self, model_path):
+    def __init__(self, model_path, cells=3):
         from _hip import DeviceArray
         from oracle import oracle
         from symmetrix import systems
 
-        s = systems.srtio3_supercell(3, sigma=0.05, seed=0)
+        s = systems.srtio3_supercell(cells, sigma=0.05, seed=0)
         om = oracle.OracleModel(model_path)
         ref = oracle.evaluate_system(om, s, skin=0.5)
         self.om, self.ref = om, ref
