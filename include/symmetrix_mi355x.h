@@ -111,28 +111,102 @@ SMX_API int32_t smx_prepare_factorized_graph_device(SmxEvaluator* ev, int32_t nu
                                                     const int32_t* neigh_types_device, uint64_t* generation);
 /* prepare_periodic_factorized_graph (mace_kokkos.hpp:393-398; pybind
  * _prepare_periodic_factorized_graph, mace_kokkos.cpp:1580): device
- * neighbour list at neighbor_cutoff, positions kept as the geometry
- * reference.  cell rows are lattice vectors; inverse_cell = inv(cell). */
+ * neighbour list at neighbor_cutoff; the builder's wrapped fractional
+ * positions and edge images are kept as the (fractional) geometry
+ * reference, so the cell may change with smx_update_factorized_cell.
+ * cell rows are lattice vectors; inverse_cell = inv(cell). */
 SMX_API int32_t smx_prepare_periodic_factorized_graph(SmxEvaluator* ev, int32_t num_nodes, const int32_t* node_types,
                                                       const double* positions, const double* cell,
                                                       const double* inverse_cell, double neighbor_cutoff,
                                                       uint64_t* generation, int64_t* num_edges);
-/* Execution plan request (set_execution_plan_request, mace_kokkos.hpp:95-96;
- * calculator execution_profile / allow_fixed_workspace): "speed" keeps every
- * edge's workspace (one receiver tile), "capacity" runs the three-sweep
- * tiled plan with at most tile_receivers receivers per tile (the reference's
- * dual-layer tiled plan, mace_kokkos_evaluate.cpp:755-1148), "auto" picks
- * the tiled plan when the untiled workspace would exceed 70% of the free
- * device memory.  tile_receivers 0 keeps the current limit (default 32768,
- * mace_kokkos.hpp:542).  Applies to graphs prepared afterwards. */
+/* Plan shorthand with the tile size (no single counterpart; the receiver
+ * tile limit is mace_kokkos.hpp:542's 32768): "speed" = the speed profile,
+ * "capacity" = the three-sweep tiled plan pinned (the reference's dual-layer
+ * tiled plan, mace_kokkos_evaluate.cpp:755-1148) with at most tile_receivers
+ * receivers per tile, "auto" = the capacity profile with fixed workspaces
+ * allowed.  tile_receivers 0 keeps the current limit.  Applies to graphs
+ * prepared afterwards. */
 SMX_API int32_t smx_set_execution_plan(SmxEvaluator* ev, const char* profile, int32_t tile_receivers);
-/* execution_plan report of the prepared graph (execution_plan.hpp:38-50) */
+/* execution_plan description of the prepared graph (plan, polynomial kernels,
+ * tiles) as one line of text */
 SMX_API int32_t smx_execution_plan(SmxEvaluator* ev, char* out, int64_t capacity);
+/* _set_execution_plan_request(algorithm, profile, debug_plan) (pybind
+ * mace_kokkos.cpp:266-270; mace_kokkos.hpp:95-96): algorithm "direct"
+ * ("factorized" and "direct_streamed" are its aliases), profile "capacity"
+ * (the reference's default) or "speed", debug_plan "" (planner) or one of
+ * "mh0-direct-speed", "mh0-direct-capacity-retained",
+ * "mh0-dual-layer-tiled-v1" to pin a plan.  Under "capacity" the planner
+ * selects the tiled plan only when fixed workspaces are allowed and the
+ * retained workspace would exceed 70% of the available device memory.
+ * Applies to graphs prepared afterwards. */
+SMX_API int32_t smx_set_execution_plan_request(SmxEvaluator* ev, const char* algorithm, const char* profile,
+                                               const char* debug_plan);
+/* _set_allow_fixed_workspace (pybind mace_kokkos.cpp:444-445; the
+ * calculator's allow_fixed_workspace): permit the planner to select the
+ * tiled plan. */
+SMX_API int32_t smx_set_allow_fixed_workspace(SmxEvaluator* ev, int32_t allow);
+/* execution_plan_report (pybind mace_kokkos.cpp:271-297) as a JSON object:
+ * requested_algorithm, requested_profile, selection_source, state,
+ * selected_id, selection_reason, available_bytes, reserve_bytes,
+ * candidates [{id, qualified, estimated_bytes, reason}].  *size receives the
+ * bytes needed (with the terminating NUL); out may be NULL. */
+SMX_API int32_t smx_execution_plan_report(SmxEvaluator* ev, char* out, int64_t capacity, int64_t* size);
+/* Diagnostics counters (factorized_last_graph_prepare_ms and
+ * factorized_last_evaluation_ms, pybind mace_kokkos.cpp:1045-1053): host
+ * wall time of the last graph preparation and of the last evaluation call
+ * (a device-positions call returns before its model kernels finish). */
+typedef struct SmxEvaluatorCounters {
+    uint32_t struct_size;
+    uint32_t reserved;
+    double last_graph_prepare_ms;
+    double last_evaluation_ms;
+    int64_t graph_prepare_count;
+    int64_t evaluation_count;
+    int64_t geometry_prepare_count;
+} SmxEvaluatorCounters;
+SMX_API int32_t smx_evaluator_counters(const SmxEvaluator* ev, SmxEvaluatorCounters* out);
+/* prepare_active_types (pybind mace_kokkos.cpp:2076; lifecycle.cpp:3949):
+ * tabulate the per-type-pair radial tables of these model types now (models
+ * with a distance transform) and keep them for later graphs whose types they
+ * cover. */
+SMX_API int32_t smx_prepare_active_types(SmxEvaluator* ev, const int32_t* types, int32_t count);
 /* update_factorized_cell (mace_kokkos.hpp:436; pybind _update_factorized_cell):
  * finite entries and a non-zero determinant are required, as in
  * mace_kokkos_factorized_lifecycle.cpp:2735-2766. */
 SMX_API int32_t smx_update_factorized_cell(SmxEvaluator* ev, uint64_t generation, const double* cell,
                                            const double* inverse_cell);
+
+/* Geometry of a prepared graph for positions calls (the reference's three
+ * forms, mace_kokkos.hpp:415-435; pybind _prepare_factorized_geometry,
+ * _prepare_factorized_shift_geometry, _prepare_factorized_fractional_geometry,
+ * mace_kokkos.cpp:1608-1672; lifecycle.cpp:2455-2733).  Each positions call
+ * then forms, per atom, delta = position - reference position (the latter
+ * times the cell when fractional), wrapped to the minimum image along the
+ * axes with pbc[k] != 0, and per edge xyz = reference edge vector +
+ * delta[src] - delta[rcv], with r >= r_cut clamped.  Counts are numbers of
+ * values: positions_count = 3 N, xyz/shifts_count = 3 E of the graph.
+ *   - Cartesian: reference positions and reference xyz per edge, any pbc;
+ *   - fractional: fractional positions and fractional xyz per edge (edge
+ *     vector = frac . cell), fully periodic and invertible cell; the cell may
+ *     then change with smx_update_factorized_cell (affine strain);
+ *   - shift: reference positions and integer cell shifts per edge (edge
+ *     vector = pos[src] - pos[rcv] + shift . cell); only under the tiled
+ *     plan, as the reference requires.
+ * Non-finite values or mismatched extents: SMX_ERR_INVALID_ARGUMENT. */
+SMX_API int32_t smx_prepare_factorized_geometry(SmxEvaluator* ev, uint64_t generation,
+                                                const double* reference_positions, int64_t positions_count,
+                                                const double* reference_xyz, int64_t xyz_count, const double* cell,
+                                                const double* inverse_cell, const int32_t* pbc);
+SMX_API int32_t smx_prepare_factorized_shift_geometry(SmxEvaluator* ev, uint64_t generation,
+                                                      const double* reference_positions, int64_t positions_count,
+                                                      const int32_t* shifts, int64_t shifts_count,
+                                                      const double* cell, const double* inverse_cell,
+                                                      const int32_t* pbc);
+SMX_API int32_t smx_prepare_factorized_fractional_geometry(SmxEvaluator* ev, uint64_t generation,
+                                                           const double* fractional_positions,
+                                                           int64_t positions_count, const double* fractional_xyz,
+                                                           int64_t xyz_count, const double* cell,
+                                                           const double* inverse_cell, const int32_t* pbc);
 
 /* compute_prepared_factorized(token, xyz, r) (mace_kokkos.hpp:440-443):
  * energies and directed forces from host edge vectors xyz[E][3], r[E]. */

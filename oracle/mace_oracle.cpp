@@ -1660,21 +1660,54 @@ int oracle_neighbor_fill(const double* pos, int n, const double* cell, const dou
     });
 }
 
-// Prepared edge geometry (lifecycle.cpp:2915-3079, fractional reference):
-// xyz_e = frac_e . cell + disp[src] - disp[rcv]; r = |xyz|, clamped to cutoff
-// with xyz scaled to it.  Returns the number of invalid edges.
-int oracle_prepared_geometry(int n, long long E, const int* receivers, const int* sources,
-                             const double* fractional_xyz, const double* cell, const double* inv,
-                             const double* reference_positions, const double* positions, double cutoff,
-                             double* xyz, double* r) {
+// Wrapped fractional positions of the neighbour list (the reference's
+// periodic graph keeps them as its geometry reference,
+// neighbor_graph_kokkos.cpp wrap step; lifecycle.cpp:2231-2244):
+// f = pos . inv, f - floor(f).
+int oracle_wrapped_fractional(const double* pos, int n, const double* inv, double* wfrac) {
+    for (int a = 0; a < n; ++a)
+        for (int ax = 0; ax < 3; ++ax) {
+            double v = 0.0;
+            for (int c = 0; c < 3; ++c) v += pos[3 * a + c] * inv[3 * c + ax];
+            wfrac[3 * a + ax] = v - static_cast<int>(std::floor(v));
+        }
+    return 0;
+}
+
+// Prepared edge geometry of a positions call (lifecycle.cpp:2915-3079 and the
+// shift form of the tiled geometry, :1860-1880).  kind 0: Cartesian
+// reference positions and reference xyz per edge; 1: fractional positions and
+// fractional xyz per edge; 2: Cartesian positions and integer shifts per edge.
+// Per atom: reference = ref (or ref . cell), delta = pos - reference; with no
+// periodic axis disp = delta, else delta in lattice coordinates, periodic
+// components minus floor(f + 0.5), back to Cartesian.  Per edge: vector =
+// reference edge vector + disp[src] - disp[rcv]; r = |vector| clamped to the
+// cutoff with the vector scaled to it.  Returns the number of invalid edges.
+int oracle_prepared_geometry(int kind, int n, long long E, const int* receivers, const int* sources,
+                             const double* ref_positions, const double* ref_edges, const int* shifts,
+                             const double* cell, const double* inv, const int* pbc, const double* positions,
+                             double cutoff, double* xyz, double* r) {
+    const bool fractional = kind == 1;
+    const bool any_pbc = pbc[0] || pbc[1] || pbc[2];
     std::vector<double> disp(3 * static_cast<std::size_t>(n));
     for (int a = 0; a < n; ++a) {
         double delta[3], f[3];
-        for (int c = 0; c < 3; ++c) delta[c] = positions[3 * a + c] - reference_positions[3 * a + c];
+        for (int c = 0; c < 3; ++c) {
+            double reference = ref_positions[3 * a + c];
+            if (fractional) {
+                reference = 0.0;
+                for (int lat = 0; lat < 3; ++lat) reference += ref_positions[3 * a + lat] * cell[3 * lat + c];
+            }
+            delta[c] = positions[3 * a + c] - reference;
+        }
+        if (!any_pbc) {
+            for (int c = 0; c < 3; ++c) disp[3 * a + c] = delta[c];
+            continue;
+        }
         for (int lat = 0; lat < 3; ++lat) {
             f[lat] = 0.0;
             for (int c = 0; c < 3; ++c) f[lat] += delta[c] * inv[3 * c + lat];
-            f[lat] -= std::floor(f[lat] + 0.5);
+            if (pbc[lat]) f[lat] -= std::floor(f[lat] + 0.5);
         }
         for (int c = 0; c < 3; ++c) {
             double v = 0.0;
@@ -1687,8 +1720,16 @@ int oracle_prepared_geometry(int n, long long E, const int* receivers, const int
         const int rc = receivers[e], sc = sources[e];
         double vec[3], d2 = 0.0;
         for (int c = 0; c < 3; ++c) {
-            double ref = 0.0;
-            for (int lat = 0; lat < 3; ++lat) ref += fractional_xyz[3 * e + lat] * cell[3 * lat + c];
+            double ref;
+            if (kind == 2) {
+                ref = ref_positions[3 * sc + c] - ref_positions[3 * rc + c];
+                for (int lat = 0; lat < 3; ++lat) ref += static_cast<double>(shifts[3 * e + lat]) * cell[3 * lat + c];
+            } else if (fractional) {
+                ref = 0.0;
+                for (int lat = 0; lat < 3; ++lat) ref += ref_edges[3 * e + lat] * cell[3 * lat + c];
+            } else {
+                ref = ref_edges[3 * e + c];
+            }
             vec[c] = ref + disp[3 * sc + c] - disp[3 * rc + c];
             d2 += vec[c] * vec[c];
         }

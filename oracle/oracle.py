@@ -59,8 +59,10 @@ def lib():
         L.oracle_neighbor_count.argtypes = [_f64p, ctypes.c_int, _f64p, _f64p, ctypes.c_double]
         L.oracle_neighbor_fill.argtypes = [_f64p, ctypes.c_int, _f64p, _f64p, ctypes.c_double,
                                            _i32p, _i32p, _i32p, _i32p, _f64p]
-        L.oracle_prepared_geometry.argtypes = [ctypes.c_int, ctypes.c_longlong, _i32p, _i32p, _f64p,
-                                               _f64p, _f64p, _f64p, _f64p, ctypes.c_double, _f64p, _f64p]
+        L.oracle_prepared_geometry.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_longlong, _i32p, _i32p, _f64p,
+                                               ctypes.c_void_p, ctypes.c_void_p, _f64p, _f64p, _i32p, _f64p,
+                                               ctypes.c_double, _f64p, _f64p]
+        L.oracle_wrapped_fractional.argtypes = [_f64p, ctypes.c_int, _f64p, _f64p]
         L.oracle_reduce_forces.argtypes = [ctypes.c_int, ctypes.c_longlong, _i32p, _i32p, _f64p, _f64p]
         L.oracle_reduce_stress.argtypes = [ctypes.c_longlong, _f64p, _f64p, ctypes.c_double, _f64p]
         L.oracle_zbl.argtypes = [ctypes.c_double, ctypes.c_double, _f64p, _f64p, ctypes.c_int, ctypes.c_int,
@@ -178,18 +180,47 @@ def neighbor_graph(positions, cell, cutoff):
     return out
 
 
-def prepared_geometry(graph, cell, reference_positions, positions, cutoff):
-    E = len(graph["sources"])
-    n = len(graph["num_neigh"])
+GEOMETRY_KINDS = {"cartesian": 0, "fractional": 1, "shifts": 2}
+
+
+def prepared_geometry_kind(kind, receivers, sources, ref_positions, ref_edges, cell, positions, cutoff,
+                           pbc=(1, 1, 1)):
+    """Edge vectors and lengths of a positions call on a prepared geometry
+    (lifecycle.cpp:2915-3079): kind "cartesian" (ref xyz per edge),
+    "fractional" (fractional positions and xyz) or "shifts" (integer cell
+    shifts per edge).  Raises ValueError on an invalid edge."""
+    receivers, sources = _c(receivers, np.int32), _c(sources, np.int32)
+    E = len(sources)
+    n = len(np.asarray(positions)) if np.ndim(positions) == 2 else len(np.asarray(positions)) // 3
+    cell = _c(cell, np.float64).reshape(3, 3)
+    inv = _c(np.linalg.inv(cell) if abs(np.linalg.det(cell)) > 0 else np.zeros((3, 3)), np.float64)
     xyz = np.zeros(3 * E)
     r = np.zeros(E)
+    edges = _c(ref_edges, np.int32 if kind == "shifts" else np.float64).ravel()
     bad = lib().oracle_prepared_geometry(
-        n, E, graph["receivers"], graph["sources"], _c(graph["fractional_xyz"], np.float64).ravel(),
-        _c(cell, np.float64).ravel(), _c(np.linalg.inv(cell), np.float64).ravel(),
-        _c(reference_positions, np.float64).ravel(), _c(positions, np.float64).ravel(), cutoff, xyz, r)
+        GEOMETRY_KINDS[kind], n, E, receivers, sources, _c(ref_positions, np.float64).ravel(),
+        edges.ctypes.data if E else None, edges.ctypes.data if (E and kind == "shifts") else None,
+        cell.ravel(), inv.ravel(), _c(pbc, np.int32), _c(positions, np.float64).ravel(), cutoff, xyz, r)
     if bad:
         raise ValueError("invalid edge geometry")
     return xyz.reshape(E, 3), r
+
+
+def wrapped_fractional(positions, cell):
+    pos = _c(positions, np.float64).ravel()
+    out = np.zeros_like(pos)
+    lib().oracle_wrapped_fractional(pos, len(pos) // 3, _c(np.linalg.inv(cell), np.float64).ravel(), out)
+    return out.reshape(-1, 3)
+
+
+def prepared_geometry(graph, cell, reference_positions, positions, cutoff):
+    """Edge geometry of the periodic graph the device builder prepares: its
+    fractional reference (wrapped fractional positions of reference_positions
+    and the list's fractional edge vectors)."""
+    cell = np.asarray(cell, dtype=np.float64)
+    return prepared_geometry_kind("fractional", graph["receivers"], graph["sources"],
+                                  wrapped_fractional(reference_positions, cell), graph["fractional_xyz"], cell,
+                                  positions, cutoff)
 
 
 def reduce_forces(n, receivers, sources, node_forces):

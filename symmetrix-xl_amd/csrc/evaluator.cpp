@@ -13,6 +13,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <climits>
 #include <cmath>
 #include <cstring>
@@ -213,10 +214,24 @@ struct Evaluator {
     int max_n_a0 = 0, max_n_h1 = 0, max_n_a1f = 0, max_n_a1r = 0;
     int sub_a0 = 1, sub_h1 = 1, sub_a1f = 1, sub_a1r = 1;
 
-    // execution plan request
-    std::string profile = "auto";   // auto | speed | capacity
+    // execution plan request (set_execution_plan_request, set_allow_fixed_workspace,
+    // mace_kokkos.hpp:95-96; the calculator's execution_profile and
+    // allow_fixed_workspace): profile "capacity" (default) or "speed"; a
+    // debug plan id pins a plan; the tiled plan is chosen by the planner only
+    // when fixed workspaces are allowed
+    std::string request_profile = "capacity";
+    std::string debug_plan;
+    bool allow_fixed = false;
     int tile_limit = 32768;         // receivers per tile in the tiled plan
     bool tiled = false;
+    // report of the last planning (execution_plan_report)
+    std::string plan_source = "none", plan_reason = "no graph prepared";
+    std::size_t plan_available = 0, plan_untiled = 0, plan_tiled = 0;
+    // pinned active types (prepare_active_types): pair tables kept for them
+    std::vector<int> pinned_active;
+    // counters (factorized_last_graph_prepare_ms, factorized_last_evaluation_ms)
+    double last_prepare_ms = 0.0, last_evaluation_ms = 0.0;
+    std::int64_t prepare_count = 0, evaluation_count = 0, geometry_prepare_count = 0;
 
     // graph
     std::uint64_t generation = 0, next_generation = 1;
@@ -236,10 +251,15 @@ struct Evaluator {
     std::vector<std::size_t> touched_begin;
     int max_tile_nr = 0;
     std::int64_t max_tile_ne = 0;
-    // periodic geometry reference (wrapped fractional positions + edge images)
-    bool has_fractional = false;
+    // geometry reference of the prepared graph (the reference's prepared
+    // geometry kinds, lifecycle.cpp:2455-2735): the device neighbour list's
+    // wrapped fractional positions + packed edge images, or host-given
+    // Cartesian / fractional reference vectors, or integer cell shifts
+    enum class Geometry { none, device_fractional, cartesian, fractional, shifts };
+    Geometry geom = Geometry::none;
+    int pbc[3] = {1, 1, 1};
     double cell[9] = {0}, inv_cell[9] = {0};
-    DevBuf d_wfrac, d_images, d_ref_positions, d_disp, d_positions;
+    DevBuf d_wfrac, d_images, d_ref_positions, d_ref_edges, d_disp, d_positions;
     // per call
     DevBuf d_xyz, d_r, d_invalid;
     DevBuf w_erec, w_Phi0, w_A0, w_M0, w_Phi1, w_A1, w_A1_adj, w_M1, w_dPhi1, w_Wsrc, w_M0_adj, w_A0_adj, w_Phi0_adj,
@@ -434,18 +454,96 @@ struct Evaluator {
         return node * n + edge * e;
     }
 
+    static constexpr const char* kPlanSpeed = "mh0-direct-speed";
+    static constexpr const char* kPlanRetained = "mh0-direct-capacity-retained";
+    static constexpr const char* kPlanTiled = "mh0-dual-layer-tiled-v1";
+
+    // Bytes of the tiled plan: graph-wide node state plus one tile's workspace.
+    std::size_t tiled_bytes(std::int64_t n, std::int64_t e) const {
+        const std::size_t C = hm.C, NY = hm.num_lm, NH = hm.num_LM, NLME = hm.num_lme;
+        const std::size_t nt = std::min<std::int64_t>(n, tile_limit);
+        const std::size_t et = n > 0 ? static_cast<std::size_t>(static_cast<double>(e) * nt / n) + 1 : 0;
+        const std::size_t graph = (2 * NH + 2) * C * 4 * n + 56 * n + 20 * e;
+        const std::size_t tile = (6 * NY + 4 * NH + 2 * NLME + 3) * C * 4 * nt +
+                                 ((ks->record_floats() + NH * C) * 4 + 24 + 32 + 24) * et;
+        return graph + tile;
+    }
+
     void choose_plan() {
-        if (profile == "capacity") {
+        std::size_t free_b = 0, total_b = 0;
+        SMX_HIP(hipMemGetInfo(&free_b, &total_b));
+        plan_available = free_b + workspace_bytes();
+        plan_untiled = untiled_bytes(N, E);
+        plan_tiled = tiled_bytes(N, E);
+        if (debug_plan == kPlanTiled) {
             tiled = true;
-        } else if (profile == "speed") {
+            plan_source = "debug_plan";
+            plan_reason = "pinned by the debug plan request";
+        } else if (debug_plan == kPlanSpeed || debug_plan == kPlanRetained) {
             tiled = false;
+            plan_source = "debug_plan";
+            plan_reason = "pinned by the debug plan request";
+        } else if (request_profile == "speed") {
+            tiled = false;
+            plan_source = "profile";
+            plan_reason = "the speed profile retains every edge's workspace";
+        } else if (!allow_fixed) {
+            tiled = false;
+            plan_source = "planner";
+            plan_reason = "fixed workspaces are not allowed; the retained direct plan is the capacity plan";
         } else {
-            std::size_t free_b = 0, total_b = 0;
-            SMX_HIP(hipMemGetInfo(&free_b, &total_b));
-            const std::size_t have = free_b + workspace_bytes();
-            tiled = untiled_bytes(N, E) > have / 10 * 7;
+            tiled = plan_untiled > plan_available / 10 * 7;
+            plan_source = "planner";
+            plan_reason = tiled ? "the retained workspace exceeds 70% of the available device memory"
+                                : "the retained workspace fits 70% of the available device memory";
         }
-        if (N <= tile_limit && profile != "capacity") tiled = false;
+        if (N <= tile_limit && debug_plan != kPlanTiled && tiled) {
+            tiled = false;
+            plan_reason = "the graph fits one receiver tile";
+        }
+    }
+
+    const char* selected_plan() const {
+        if (tiled) return kPlanTiled;
+        return request_profile == "speed" || debug_plan == kPlanSpeed ? kPlanSpeed : kPlanRetained;
+    }
+
+    static std::string json_string(const std::string& v) {
+        std::string o = "\"";
+        for (char c : v) {
+            if (c == '"' || c == '\\') o += '\\';
+            o += c;
+        }
+        return o + "\"";
+    }
+
+    // execution_plan_report (pybind mace_kokkos.cpp:271-297) as JSON
+    std::string plan_report() const {
+        const bool resolved = generation != 0;
+        std::string o = "{";
+        o += "\"requested_algorithm\":\"direct\",";
+        o += "\"requested_profile\":" + json_string(request_profile) + ",";
+        o += "\"allow_fixed_workspace\":" + std::string(allow_fixed ? "true" : "false") + ",";
+        o += "\"debug_plan\":" + json_string(debug_plan) + ",";
+        o += "\"selection_source\":" + json_string(plan_source) + ",";
+        o += "\"state\":" + json_string(resolved ? "resolved" : "pending") + ",";
+        o += "\"selected_id\":" + json_string(resolved ? selected_plan() : "") + ",";
+        o += "\"selection_reason\":" + json_string(plan_reason) + ",";
+        o += "\"available_bytes\":" + std::to_string(plan_available) + ",";
+        o += "\"reserve_bytes\":" + std::to_string(plan_available - plan_available / 10 * 7) + ",";
+        o += "\"boundary_attempt\":false,";
+        o += "\"tiles\":" + std::to_string(tiles.size()) + ",";
+        o += "\"max_tile_receivers\":" + std::to_string(max_tile_nr) + ",";
+        o += "\"candidates\":[";
+        o += "{\"id\":\"" + std::string(request_profile == "speed" ? kPlanSpeed : kPlanRetained) +
+             "\",\"qualified\":true,\"estimated_bytes\":" + std::to_string(plan_untiled) +
+             ",\"reason\":\"every edge's workspace retained\"},";
+        o += "{\"id\":\"" + std::string(kPlanTiled) + "\",\"qualified\":" +
+             std::string(allow_fixed || debug_plan == kPlanTiled ? "true" : "false") +
+             ",\"estimated_bytes\":" + std::to_string(plan_tiled) +
+             ",\"reason\":\"three sweeps over receiver tiles of at most " + std::to_string(tile_limit) +
+             " receivers\"}]}";
+        return o;
     }
 
     std::size_t workspace_bytes() const {
@@ -655,6 +753,36 @@ struct Evaluator {
         std::sort(act.begin(), act.end());
         act.erase(std::unique(act.begin(), act.end()), act.end());
         if (act.empty()) act.push_back(0);
+        // the pinned active types serve every graph whose types they cover
+        if (!pinned_active.empty() && std::includes(pinned_active.begin(), pinned_active.end(), act.begin(), act.end()))
+            act = pinned_active;
+        tabulate_pairs(act);
+        const int na = static_cast<int>(act.size());
+        int* ep = static_cast<int*>(d_edge_pair.ensure(std::max<std::int64_t>(E, 1) * sizeof(int)));
+        int* bad = static_cast<int*>(d_counts.ensure(std::max(N, 1) * sizeof(int)));
+        launch_fill_zero(reinterpret_cast<float*>(bad), 1, stream);
+        launch_edge_pairs(E, d_receivers.as<int>(), d_node_types.as<int>(), d_neigh_types.as<int>(),
+                          d_type_to_active.as<int>(), na, ep, bad, stream);
+        int nbad = 0;
+        SMX_HIP(hipMemcpyAsync(&nbad, bad, sizeof(int), hipMemcpyDeviceToHost, stream));
+        SMX_HIP(hipStreamSynchronize(stream));
+        if (nbad > 0) throw std::invalid_argument("a neighbour type is not among the graph's node types");
+    }
+
+    // prepare_active_types (lifecycle.cpp:3949; pybind mace_kokkos.cpp:2076):
+    // tabulate the per-pair radial tables of these model types now, and keep
+    // them for every later graph whose types they cover.
+    void prepare_active_types(std::vector<int> types) {
+        for (int t : types)
+            if (t < 0 || t >= hm.num_elements) throw std::invalid_argument("active type index is out of range");
+        std::sort(types.begin(), types.end());
+        types.erase(std::unique(types.begin(), types.end()), types.end());
+        pinned_active = types;
+        if (hm.agnesi && !types.empty()) tabulate_pairs(types);
+    }
+
+    // per-pair tables of the active types act (a <= b pairs), when they change
+    void tabulate_pairs(const std::vector<int>& act) {
         const int na = static_cast<int>(act.size());
         if (act != pair_active) {
             std::vector<float> R0, R1, t0, t1;
@@ -676,15 +804,6 @@ struct Evaluator {
             upload(d_type_to_active, t2a, stream);
             pair_active = act;
         }
-        int* ep = static_cast<int*>(d_edge_pair.ensure(std::max<std::int64_t>(E, 1) * sizeof(int)));
-        int* bad = static_cast<int*>(d_counts.ensure(std::max(N, 1) * sizeof(int)));
-        launch_fill_zero(reinterpret_cast<float*>(bad), 1, stream);
-        launch_edge_pairs(E, d_receivers.as<int>(), d_node_types.as<int>(), d_neigh_types.as<int>(),
-                          d_type_to_active.as<int>(), na, ep, bad, stream);
-        int nbad = 0;
-        SMX_HIP(hipMemcpyAsync(&nbad, bad, sizeof(int), hipMemcpyDeviceToHost, stream));
-        SMX_HIP(hipStreamSynchronize(stream));
-        if (nbad > 0) throw std::invalid_argument("a neighbour type is not among the graph's node types");
     }
 
     std::uint64_t prepare_graph_host(int n, const int* node_types, const int* num_neigh, std::int64_t num_edges,
@@ -715,7 +834,7 @@ struct Evaluator {
         upload(d_offsets, off, stream);
         upload(d_neigh, std::vector<int>(neigh, neigh + E), stream);
         upload(d_neigh_types, std::vector<int>(neigh_types, neigh_types + E), stream);
-        has_fractional = false;
+        geom = Geometry::none;
         return finish_graph();
     }
 
@@ -740,7 +859,7 @@ struct Evaluator {
         if (n < 0) throw std::invalid_argument("num_nodes must be non-negative");
         validate_types(n, node_types);
         // release the previous graph's edge arrays first (capacity runs)
-        for (DevBuf* b : {&d_neigh, &d_neigh_types, &d_receivers, &d_sedges, &d_images}) b->release();
+        for (DevBuf* b : {&d_neigh, &d_neigh_types, &d_receivers, &d_sedges, &d_images, &d_ref_edges}) b->release();
         NeighborResult nr;
         struct Guard {
             NeighborResult& r;
@@ -767,12 +886,13 @@ struct Evaluator {
         nr.wfrac = nullptr;
         int* nt = static_cast<int*>(d_neigh_types.ensure(std::max<std::int64_t>(E, 1) * sizeof(int)));
         launch_gather_types(E, d_neigh.as<int>(), d_node_types.as<int>(), nt, stream);
-        double* rp = static_cast<double*>(d_ref_positions.ensure(std::max(N, 1) * 3 * sizeof(double)));
-        if (N > 0) SMX_HIP(hipMemcpyAsync(rp, positions, N * 3 * sizeof(double), hipMemcpyHostToDevice, stream));
         SMX_HIP(hipStreamSynchronize(stream));
         std::memcpy(cell, cell_, sizeof(cell));
         std::memcpy(inv_cell, inv_, sizeof(inv_cell));
-        has_fractional = true;
+        // fractional reference (prepare_periodic_factorized_graph keeps the
+        // builder's wrapped fractional positions, lifecycle.cpp:2231-2244)
+        geom = Geometry::device_fractional;
+        pbc[0] = pbc[1] = pbc[2] = 1;
         h_offsets.clear();
         const std::uint64_t token = finish_graph();
         return {token, E};
@@ -799,9 +919,9 @@ struct Evaluator {
             if (tm) tm->end("edge_geometry", stream);
         } else if (!xyz_host) {
             if (tm) tm->begin("edge_geometry", stream);
-            launch_edge_xyz(t.e0, t.ne, cell, d_receivers.as<int>(), d_neigh.as<int>(), d_wfrac.as<double>(),
-                            d_images.as<std::uint32_t>(), d_disp.as<double>(), hm.r_cut, d_xyz.as<double>(),
-                            d_r.as<double>(), d_invalid.as<int>(), stream);
+            launch_edge_xyz(t.e0, t.ne, edge_reference(), cell, d_receivers.as<int>(), d_neigh.as<int>(),
+                            d_disp.as<double>(), hm.r_cut, d_xyz.as<double>(), d_r.as<double>(), d_invalid.as<int>(),
+                            stream);
             if (tm) tm->end("edge_geometry", stream);
         }
         if (tm) tm->begin("edge_records", stream);
@@ -809,6 +929,78 @@ struct Evaluator {
                           ws.erec, stream);
         if (tm) tm->end("edge_records", stream);
         (void)positions;
+    }
+
+    EdgeReference edge_reference() const {
+        EdgeReference ref;
+        switch (geom) {
+            case Geometry::device_fractional:
+                ref.kind = kGeometryDeviceFractional;
+                ref.wfrac = d_wfrac.as<double>();
+                ref.images = d_images.as<std::uint32_t>();
+                break;
+            case Geometry::cartesian:
+                ref.kind = kGeometryCartesian;
+                ref.edges = d_ref_edges.as<double>();
+                break;
+            case Geometry::fractional:
+                ref.kind = kGeometryFractional;
+                ref.edges = d_ref_edges.as<double>();
+                break;
+            case Geometry::shifts:
+                ref.kind = kGeometryShifts;
+                ref.positions = d_ref_positions.as<double>();
+                ref.shifts = d_ref_edges.as<int>();
+                break;
+            case Geometry::none:
+                throw std::logic_error("the prepared graph has no geometry reference");
+        }
+        return ref;
+    }
+
+    // prepare_factorized_geometry / _fractional_geometry / _shift_geometry
+    // (lifecycle.cpp:2455-2733): the reference positions and per-edge
+    // reference vectors (Cartesian xyz, fractional xyz or integer shifts)
+    // that positions calls displace.
+    void prepare_geometry(std::uint64_t token, Geometry kind, const double* ref_positions,
+                          std::int64_t positions_count, const void* ref_edges, std::int64_t edges_count,
+                          const double* cell_, const double* inv_, const int* pbc_) {
+        check_generation(token);
+        if (kind == Geometry::shifts && !tiled)
+            throw std::invalid_argument("Shift geometry requires a fixed-workspace tiled plan.");
+        if (!cell_ || !inv_ || !pbc_ || (N > 0 && !ref_positions) || (E > 0 && !ref_edges))
+            throw std::invalid_argument("prepared geometry arrays are required");
+        if (positions_count != 3 * static_cast<std::int64_t>(N) || edges_count != 3 * E)
+            throw std::invalid_argument("prepared geometry extents are inconsistent with the graph");
+        if (kind == Geometry::fractional) {
+            if (!pbc_[0] || !pbc_[1] || !pbc_[2])
+                throw std::invalid_argument("Fractional geometry requires a fully periodic cell.");
+            const double det = cell_[0] * (cell_[4] * cell_[8] - cell_[5] * cell_[7]) -
+                               cell_[1] * (cell_[3] * cell_[8] - cell_[5] * cell_[6]) +
+                               cell_[2] * (cell_[3] * cell_[7] - cell_[4] * cell_[6]);
+            if (!std::isfinite(det) || det == 0.0)
+                throw std::invalid_argument("Fractional geometry cell matrix must be invertible.");
+        }
+        auto finite = [](const double* p, std::int64_t n) {
+            for (std::int64_t i = 0; i < n; ++i)
+                if (!std::isfinite(p[i])) return false;
+            return true;
+        };
+        if (!finite(ref_positions, positions_count) || !finite(cell_, 9) || !finite(inv_, 9) ||
+            (kind != Geometry::shifts && !finite(static_cast<const double*>(ref_edges), edges_count)))
+            throw std::invalid_argument("prepared geometry contains a non-finite value");
+        double* rp = static_cast<double*>(d_ref_positions.ensure(std::max(N, 1) * 3 * sizeof(double)));
+        if (N > 0)
+            SMX_HIP(hipMemcpyAsync(rp, ref_positions, N * 3 * sizeof(double), hipMemcpyHostToDevice, stream));
+        const std::size_t elem = kind == Geometry::shifts ? sizeof(int) : sizeof(double);
+        void* re = d_ref_edges.ensure(std::max<std::int64_t>(E, 1) * 3 * elem);
+        if (E > 0) SMX_HIP(hipMemcpyAsync(re, ref_edges, E * 3 * elem, hipMemcpyHostToDevice, stream));
+        SMX_HIP(hipStreamSynchronize(stream));
+        std::memcpy(cell, cell_, sizeof(cell));
+        std::memcpy(inv_cell, inv_, sizeof(inv_cell));
+        for (int k = 0; k < 3; ++k) pbc[k] = pbc_[k] != 0;
+        geom = kind;
+        ++geometry_prepare_count;
     }
 
     // queue the D2H copy of the invalid-edge count (positions and LAMMPS calls)
@@ -927,9 +1119,10 @@ struct Evaluator {
 
     void compute_positions(std::uint64_t token, const double* positions, bool on_device) {
         check_generation(token);
-        if (!has_fractional)
-            throw std::logic_error("the prepared graph has no periodic geometry reference; "
-                                   "use compute_prepared_factorized with xyz and r");
+        if (geom == Geometry::none)
+            throw std::invalid_argument("Execution R1 positions require current graph and geometry tokens: "
+                                        "prepare a geometry (prepare_factorized_geometry or its fractional or "
+                                        "shift form) or use compute_prepared_factorized with xyz and r");
         const double* pos = positions;
         if (!on_device) {
             for (int i = 0; i < 3 * N; ++i)
@@ -941,7 +1134,10 @@ struct Evaluator {
         xyz_host = false;
         launch_fill_zero(reinterpret_cast<float*>(d_invalid.as<int>()), 1, stream);
         if (timer) timer->begin("displacements", stream);
-        launch_displacements(N, cell, inv_cell, d_ref_positions.as<double>(), pos, d_disp.as<double>(), stream);
+        const bool frac_ref = geom == Geometry::device_fractional || geom == Geometry::fractional;
+        launch_displacements(N, cell, inv_cell, pbc, frac_ref,
+                             geom == Geometry::device_fractional ? d_wfrac.as<double>() : d_ref_positions.as<double>(),
+                             pos, d_disp.as<double>(), stream);
         if (timer) timer->end("displacements", stream);
         evaluate(pos);
         finish_call(!on_device);
@@ -968,7 +1164,9 @@ struct Evaluator {
 
     void update_cell(std::uint64_t token, const double* cell_, const double* inv_) {
         check_generation(token);
-        if (!has_fractional) throw std::logic_error("the prepared graph has no periodic geometry reference");
+        if (geom != Geometry::device_fractional && geom != Geometry::fractional && geom != Geometry::shifts)
+            throw std::invalid_argument("Prepared Execution R1 cell update requires current graph and fractional or "
+                                        "shift geometry tokens.");
         for (int k = 0; k < 9; ++k)
             if (!std::isfinite(cell_[k]) || !std::isfinite(inv_[k]))
                 throw std::invalid_argument("cell matrices contain a non-finite value");
@@ -1285,6 +1483,16 @@ void export_array(const std::vector<T>& v, T* out, int64_t capacity, int64_t* co
     if (capacity < static_cast<int64_t>(v.size())) throw std::invalid_argument("output capacity is too small");
     std::copy(v.begin(), v.end(), out);
 }
+// host wall time of a prepare or evaluation call, kept as the evaluator's
+// last_graph_prepare_ms / last_evaluation_ms counters
+template <class F>
+void timed(double& ms, std::int64_t& count, F&& f) {
+    const auto t0 = std::chrono::steady_clock::now();
+    f();
+    ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+    ++count;
+}
+
 const smx::Evaluator& E(const SmxEvaluator* ev) {
     if (!ev) throw std::invalid_argument("evaluator handle is NULL");
     return ev->impl;
@@ -1363,7 +1571,10 @@ int32_t smx_prepare_factorized_graph(SmxEvaluator* ev, int32_t num_nodes, const 
         if (!generation) throw std::invalid_argument("generation output is required");
         if (num_nodes > 0 && (!node_types || !num_neigh)) throw std::invalid_argument("node arrays are required");
         if (num_edges > 0 && (!neigh_indices || !neigh_types)) throw std::invalid_argument("edge arrays are required");
-        *generation = E(ev).prepare_graph_host(num_nodes, node_types, num_neigh, num_edges, neigh_indices, neigh_types);
+        auto& e = E(ev);
+        timed(e.last_prepare_ms, e.prepare_count, [&] {
+            *generation = e.prepare_graph_host(num_nodes, node_types, num_neigh, num_edges, neigh_indices, neigh_types);
+        });
     });
 }
 
@@ -1374,8 +1585,11 @@ int32_t smx_prepare_factorized_graph_device(SmxEvaluator* ev, int32_t num_nodes,
     return guarded([&] {
         if (!generation) throw std::invalid_argument("generation output is required");
         if (num_edges < 0 || num_edges > INT_MAX) throw std::invalid_argument("edge count exceeds the 32-bit graph limit");
-        *generation = E(ev).prepare_graph_device(num_nodes, node_types_device, num_neigh_device, num_edges,
+        auto& e = E(ev);
+        timed(e.last_prepare_ms, e.prepare_count, [&] {
+            *generation = e.prepare_graph_device(num_nodes, node_types_device, num_neigh_device, num_edges,
                                                  neigh_indices_device, neigh_types_device);
+        });
     });
 }
 
@@ -1385,9 +1599,12 @@ int32_t smx_prepare_periodic_factorized_graph(SmxEvaluator* ev, int32_t num_node
     return guarded([&] {
         if (!generation || !num_edges || !cell || !inverse_cell) throw std::invalid_argument("missing argument");
         if (num_nodes > 0 && (!node_types || !positions)) throw std::invalid_argument("node arrays are required");
-        const auto r = E(ev).prepare_periodic(num_nodes, node_types, positions, cell, inverse_cell, neighbor_cutoff);
-        *generation = r.first;
-        *num_edges = r.second;
+        auto& e = E(ev);
+        timed(e.last_prepare_ms, e.prepare_count, [&] {
+            const auto r = e.prepare_periodic(num_nodes, node_types, positions, cell, inverse_cell, neighbor_cutoff);
+            *generation = r.first;
+            *num_edges = r.second;
+        });
     });
 }
 
@@ -1398,8 +1615,45 @@ int32_t smx_set_execution_plan(SmxEvaluator* ev, const char* profile, int32_t ti
         if (p != "auto" && p != "speed" && p != "capacity")
             throw std::invalid_argument("execution profile must be 'auto', 'speed' or 'capacity'");
         if (tile_receivers < 0) throw std::invalid_argument("tile_receivers must be non-negative");
-        e.profile = p;
+        // auto: capacity profile with fixed workspaces allowed; capacity: the
+        // tiled plan pinned; speed: the speed profile
+        e.request_profile = p == "speed" ? "speed" : "capacity";
+        e.allow_fixed = p != "speed";
+        e.debug_plan = p == "capacity" ? smx::Evaluator::kPlanTiled : "";
         if (tile_receivers > 0) e.tile_limit = tile_receivers;
+    });
+}
+
+int32_t smx_set_execution_plan_request(SmxEvaluator* ev, const char* algorithm, const char* profile,
+                                       const char* debug_plan) {
+    return guarded([&] {
+        auto& e = E(ev);
+        const std::string a = algorithm ? algorithm : "direct", p = profile ? profile : "capacity";
+        const std::string d = debug_plan ? debug_plan : "";
+        if (a != "direct" && a != "factorized" && a != "direct_streamed")
+            throw std::invalid_argument("the MI355X evaluator implements the 'direct' execution algorithm");
+        if (p != "capacity" && p != "speed")
+            throw std::invalid_argument("execution profile must be 'capacity' or 'speed'");
+        if (!d.empty() && d != smx::Evaluator::kPlanSpeed && d != smx::Evaluator::kPlanRetained &&
+            d != smx::Evaluator::kPlanTiled)
+            throw std::invalid_argument("unknown debug execution plan '" + d + "'");
+        e.request_profile = p;
+        e.debug_plan = d;
+    });
+}
+
+int32_t smx_set_allow_fixed_workspace(SmxEvaluator* ev, int32_t allow) {
+    return guarded([&] { E(ev).allow_fixed = allow != 0; });
+}
+
+int32_t smx_execution_plan_report(SmxEvaluator* ev, char* out, int64_t capacity, int64_t* size) {
+    return guarded([&] {
+        const std::string r = E(ev).plan_report();
+        if (size) *size = static_cast<int64_t>(r.size()) + 1;
+        if (out) {
+            if (capacity < static_cast<int64_t>(r.size()) + 1) throw std::invalid_argument("buffer too small");
+            std::memcpy(out, r.c_str(), r.size() + 1);
+        }
     });
 }
 
@@ -1411,6 +1665,26 @@ int32_t smx_execution_plan(SmxEvaluator* ev, char* out, int64_t capacity) {
     });
 }
 
+int32_t smx_evaluator_counters(const SmxEvaluator* ev, SmxEvaluatorCounters* out) {
+    return guarded([&] {
+        if (!out || out->struct_size < sizeof(SmxEvaluatorCounters))
+            throw std::invalid_argument("SmxEvaluatorCounters.struct_size is too small");
+        const auto& e = E(ev);
+        out->last_graph_prepare_ms = e.last_prepare_ms;
+        out->last_evaluation_ms = e.last_evaluation_ms;
+        out->graph_prepare_count = e.prepare_count;
+        out->evaluation_count = e.evaluation_count;
+        out->geometry_prepare_count = e.geometry_prepare_count;
+    });
+}
+
+int32_t smx_prepare_active_types(SmxEvaluator* ev, const int32_t* types, int32_t count) {
+    return guarded([&] {
+        if (count < 0 || (count > 0 && !types)) throw std::invalid_argument("active types are required");
+        E(ev).prepare_active_types(std::vector<int>(types, types + count));
+    });
+}
+
 int32_t smx_update_factorized_cell(SmxEvaluator* ev, uint64_t generation, const double* cell,
                                    const double* inverse_cell) {
     return guarded([&] {
@@ -1419,11 +1693,41 @@ int32_t smx_update_factorized_cell(SmxEvaluator* ev, uint64_t generation, const 
     });
 }
 
+int32_t smx_prepare_factorized_geometry(SmxEvaluator* ev, uint64_t generation, const double* reference_positions,
+                                        int64_t positions_count, const double* reference_xyz, int64_t xyz_count,
+                                        const double* cell, const double* inverse_cell, const int32_t* pbc) {
+    return guarded([&] {
+        E(ev).prepare_geometry(generation, smx::Evaluator::Geometry::cartesian, reference_positions, positions_count,
+                               reference_xyz, xyz_count, cell, inverse_cell, pbc);
+    });
+}
+
+int32_t smx_prepare_factorized_shift_geometry(SmxEvaluator* ev, uint64_t generation,
+                                              const double* reference_positions, int64_t positions_count,
+                                              const int32_t* shifts, int64_t shifts_count, const double* cell,
+                                              const double* inverse_cell, const int32_t* pbc) {
+    return guarded([&] {
+        E(ev).prepare_geometry(generation, smx::Evaluator::Geometry::shifts, reference_positions, positions_count,
+                               shifts, shifts_count, cell, inverse_cell, pbc);
+    });
+}
+
+int32_t smx_prepare_factorized_fractional_geometry(SmxEvaluator* ev, uint64_t generation,
+                                                   const double* fractional_positions, int64_t positions_count,
+                                                   const double* fractional_xyz, int64_t xyz_count,
+                                                   const double* cell, const double* inverse_cell,
+                                                   const int32_t* pbc) {
+    return guarded([&] {
+        E(ev).prepare_geometry(generation, smx::Evaluator::Geometry::fractional, fractional_positions,
+                               positions_count, fractional_xyz, xyz_count, cell, inverse_cell, pbc);
+    });
+}
+
 int32_t smx_compute_prepared_factorized(SmxEvaluator* ev, uint64_t generation, const double* xyz, const double* r) {
     return guarded([&] {
         auto& e = E(ev);
         if (e.E > 0 && (!xyz || !r)) throw std::invalid_argument("xyz and r are required");
-        e.compute_xyz(generation, xyz, r);
+        timed(e.last_evaluation_ms, e.evaluation_count, [&] { e.compute_xyz(generation, xyz, r); });
     });
 }
 
@@ -1431,7 +1735,7 @@ int32_t smx_compute_prepared_factorized_positions(SmxEvaluator* ev, uint64_t gen
     return guarded([&] {
         auto& e = E(ev);
         if (e.N > 0 && !positions) throw std::invalid_argument("positions are required");
-        e.compute_positions(generation, positions, false);
+        timed(e.last_evaluation_ms, e.evaluation_count, [&] { e.compute_positions(generation, positions, false); });
     });
 }
 
@@ -1440,7 +1744,8 @@ int32_t smx_compute_prepared_factorized_positions_device(SmxEvaluator* ev, uint6
     return guarded([&] {
         auto& e = E(ev);
         if (e.N > 0 && !positions_device) throw std::invalid_argument("positions are required");
-        e.compute_positions(generation, positions_device, true);
+        timed(e.last_evaluation_ms, e.evaluation_count,
+              [&] { e.compute_positions(generation, positions_device, true); });
     });
 }
 
@@ -1449,8 +1754,11 @@ int32_t smx_compute_node_energies_forces(SmxEvaluator* ev, int32_t num_nodes, co
                                          const int32_t* neigh_types, const double* xyz, const double* r) {
     return guarded([&] {
         auto& e = E(ev);
-        const auto token = e.prepare_graph_host(num_nodes, node_types, num_neigh, num_edges, neigh_indices, neigh_types);
-        e.compute_xyz(token, xyz, r);
+        std::uint64_t token = 0;
+        timed(e.last_prepare_ms, e.prepare_count, [&] {
+            token = e.prepare_graph_host(num_nodes, node_types, num_neigh, num_edges, neigh_indices, neigh_types);
+        });
+        timed(e.last_evaluation_ms, e.evaluation_count, [&] { e.compute_xyz(token, xyz, r); });
     });
 }
 

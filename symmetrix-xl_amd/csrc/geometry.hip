@@ -261,16 +261,34 @@ __global__ void k_copy_i64_i32_plus(const long long* __restrict__ in, int* __res
 // ---------------------------------------------------------------------------
 // Prepared geometry (lifecycle.cpp:2915-3079)
 // ---------------------------------------------------------------------------
-__global__ void k_displacements(int N, Mat3 cell, Mat3 inv, const double* __restrict__ ref,
-                                const double* __restrict__ pos, double* __restrict__ disp) {
+// Per-atom displacement from the geometry reference
+// (mace_kokkos_factorized_lifecycle.cpp:2975-3006): the reference position is
+// ref (Cartesian) or ref . cell (fractional reference); delta = pos - reference;
+// without periodicity the displacement is delta, otherwise delta in lattice
+// coordinates with the periodic components wrapped to [-1/2, 1/2), back in
+// Cartesian coordinates.
+__global__ void k_displacements(int N, Mat3 cell, Mat3 inv, int pbc_mask, int ref_fractional,
+                                const double* __restrict__ ref, const double* __restrict__ pos,
+                                double* __restrict__ disp) {
     const int a = blockIdx.x * blockDim.x + threadIdx.x;
     if (a >= N) return;
     double delta[3], f[3];
-    for (int c = 0; c < 3; ++c) delta[c] = pos[3 * a + c] - ref[3 * a + c];
+    for (int c = 0; c < 3; ++c) {
+        double reference = ref[3 * a + c];
+        if (ref_fractional) {
+            reference = 0.0;
+            for (int lat = 0; lat < 3; ++lat) reference += ref[3 * a + lat] * cell.v[3 * lat + c];
+        }
+        delta[c] = pos[3 * a + c] - reference;
+    }
+    if (pbc_mask == 0) {
+        for (int c = 0; c < 3; ++c) disp[3 * a + c] = delta[c];
+        return;
+    }
     for (int lat = 0; lat < 3; ++lat) {
         f[lat] = 0.0;
         for (int c = 0; c < 3; ++c) f[lat] += delta[c] * inv.v[3 * c + lat];
-        f[lat] -= floor(f[lat] + 0.5);
+        if (pbc_mask & (1 << lat)) f[lat] -= floor(f[lat] + 0.5);
     }
     for (int c = 0; c < 3; ++c) {
         double v = 0.0;
@@ -283,27 +301,51 @@ __device__ __forceinline__ int image_component(std::uint32_t packed, int ax) {
     return static_cast<int>(static_cast<std::int8_t>((packed >> (8 * ax)) & 0xffu));
 }
 
-// Edges [e0, e0+ne): the reference fractional edge vector is rebuilt exactly
-// as the neighbour list formed it (wfrac[src] - wfrac[rcv] + image), then
-// xyz = frac . cell + disp[src] - disp[rcv]; r clamped to the cutoff.
-__global__ void k_edge_xyz(long long e0, long long ne, Mat3 cell, const int* __restrict__ receivers,
+// Edges [e0, e0+ne): the edge's reference vector, then
+// xyz = reference + disp[src] - disp[rcv], r = |xyz| clamped to the cutoff
+// with xyz scaled to it (lifecycle.cpp:3009-3048, 1860-1880).  References:
+//   device_fractional: (wfrac[src] - wfrac[rcv] + image) . cell, the
+//                      fractional edge vector the neighbour list formed;
+//   cartesian:         ref_edges[e];
+//   fractional:        ref_edges[e] . cell;
+//   shifts:            ref_pos[src] - ref_pos[rcv] + shift_e . cell.
+__global__ void k_edge_xyz(long long e0, long long ne, int kind, Mat3 cell, const int* __restrict__ receivers,
                            const int* __restrict__ sources, const double* __restrict__ wfrac,
-                           const std::uint32_t* __restrict__ images, const double* __restrict__ disp,
-                           double cutoff, double* __restrict__ xyz, double* __restrict__ r,
-                           int* __restrict__ invalid) {
+                           const std::uint32_t* __restrict__ images, const double* __restrict__ ref_pos,
+                           const double* __restrict__ ref_edges, const int* __restrict__ shifts,
+                           const double* __restrict__ disp, double cutoff, double* __restrict__ xyz,
+                           double* __restrict__ r, int* __restrict__ invalid) {
     const long long le = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (le >= ne) return;
     const long long e = e0 + le;
     const int rc = receivers[e], sc = sources[e];
-    const std::uint32_t img = images[e];
-    double fr[3];
-    for (int ax = 0; ax < 3; ++ax) fr[ax] = wfrac[3 * sc + ax] - wfrac[3 * rc + ax] + image_component(img, ax);
     double vec[3], d2 = 0.0;
-    for (int c = 0; c < 3; ++c) {
-        double ref = 0.0;
-        for (int lat = 0; lat < 3; ++lat) ref += fr[lat] * cell.v[3 * lat + c];
-        vec[c] = ref + disp[3 * sc + c] - disp[3 * rc + c];
-        d2 += vec[c] * vec[c];
+    if (kind == kGeometryDeviceFractional) {
+        const std::uint32_t img = images[e];
+        double fr[3];
+        for (int ax = 0; ax < 3; ++ax) fr[ax] = wfrac[3 * sc + ax] - wfrac[3 * rc + ax] + image_component(img, ax);
+        for (int c = 0; c < 3; ++c) {
+            double ref = 0.0;
+            for (int lat = 0; lat < 3; ++lat) ref += fr[lat] * cell.v[3 * lat + c];
+            vec[c] = ref + disp[3 * sc + c] - disp[3 * rc + c];
+            d2 += vec[c] * vec[c];
+        }
+    } else {
+        for (int c = 0; c < 3; ++c) {
+            double ref;
+            if (kind == kGeometryShifts) {
+                ref = ref_pos[3 * sc + c] - ref_pos[3 * rc + c];
+                for (int lat = 0; lat < 3; ++lat)
+                    ref += static_cast<double>(shifts[3 * e + lat]) * cell.v[3 * lat + c];
+            } else if (kind == kGeometryFractional) {
+                ref = 0.0;
+                for (int lat = 0; lat < 3; ++lat) ref += ref_edges[3 * e + lat] * cell.v[3 * lat + c];
+            } else {
+                ref = ref_edges[3 * e + c];
+            }
+            vec[c] = ref + disp[3 * sc + c] - disp[3 * rc + c];
+            d2 += vec[c] * vec[c];
+        }
     }
     if (!isfinite(d2) || !(d2 > 0.0)) {
         atomicAdd(invalid, 1);
@@ -602,20 +644,22 @@ void launch_gather_types(std::int64_t E, const int* sources, const int* node_typ
     SMX_LAUNCH_CHECK("gather_types");
 }
 
-void launch_displacements(int N, const double* cell, const double* inv_cell, const double* reference_positions,
-                          const double* positions, double* disp, hipStream_t s) {
+void launch_displacements(int N, const double* cell, const double* inv_cell, const int pbc[3], bool ref_fractional,
+                          const double* reference_positions, const double* positions, double* disp, hipStream_t s) {
     if (N == 0) return;
-    k_displacements<<<blocks_for(N, 256), 256, 0, s>>>(N, mat3(cell), mat3(inv_cell), reference_positions, positions,
-                                                       disp);
+    const int mask = (pbc[0] ? 1 : 0) | (pbc[1] ? 2 : 0) | (pbc[2] ? 4 : 0);
+    k_displacements<<<blocks_for(N, 256), 256, 0, s>>>(N, mat3(cell), mat3(inv_cell), mask, ref_fractional ? 1 : 0,
+                                                       reference_positions, positions, disp);
     SMX_LAUNCH_CHECK("geometry_displacements");
 }
 
-void launch_edge_xyz(std::int64_t e0, std::int64_t ne, const double* cell, const int* receivers, const int* sources,
-                     const double* wfrac, const std::uint32_t* images, const double* disp, double cutoff,
-                     double* xyz, double* r, int* invalid, hipStream_t s) {
+void launch_edge_xyz(std::int64_t e0, std::int64_t ne, const EdgeReference& ref, const double* cell,
+                     const int* receivers, const int* sources, const double* disp, double cutoff, double* xyz,
+                     double* r, int* invalid, hipStream_t s) {
     if (ne == 0) return;
-    k_edge_xyz<<<blocks_for(ne, 256), 256, 0, s>>>(e0, ne, mat3(cell), receivers, sources, wfrac, images, disp,
-                                                   cutoff, xyz, r, invalid);
+    k_edge_xyz<<<blocks_for(ne, 256), 256, 0, s>>>(e0, ne, ref.kind, mat3(cell), receivers, sources, ref.wfrac,
+                                                   ref.images, ref.positions, ref.edges, ref.shifts, disp, cutoff,
+                                                   xyz, r, invalid);
     SMX_LAUNCH_CHECK("geometry_edges");
 }
 

@@ -263,14 +263,27 @@ void launch_fill_zero(float* p, std::size_t n, hipStream_t s);
 void launch_fill_zero(double* p, std::size_t n, hipStream_t s);
 void launch_energy_sum(int N, const double* node_energies, double* total, hipStream_t s);
 
-// Geometry (FP64, no contraction): per-atom minimum-image displacement from
-// the reference positions, then xyz/r of the edges [e0, e0+ne) from the
-// reference fractional edge vector wfrac[src] - wfrac[rcv] + image.
-void launch_displacements(int N, const double* cell, const double* inv_cell, const double* reference_positions,
-                          const double* positions, double* disp, hipStream_t s);
-void launch_edge_xyz(std::int64_t e0, std::int64_t ne, const double* cell, const int* receivers, const int* sources,
-                     const double* wfrac, const std::uint32_t* images, const double* disp, double cutoff,
-                     double* xyz, double* r, int* invalid, hipStream_t s);
+// Geometry (FP64, no contraction): per-atom displacement from the reference
+// positions (Cartesian, or fractional when ref_fractional; wrapped to the
+// minimum image along the periodic axes), then xyz/r of the edges
+// [e0, e0+ne) from each edge's reference vector.
+constexpr int kGeometryDeviceFractional = 0;  // neighbour list's wfrac + packed images
+constexpr int kGeometryCartesian = 1;         // reference xyz per edge
+constexpr int kGeometryFractional = 2;        // reference fractional xyz per edge
+constexpr int kGeometryShifts = 3;            // reference positions + integer cell shifts per edge
+struct EdgeReference {
+    int kind = kGeometryDeviceFractional;
+    const double* wfrac = nullptr;            // [N][3] (device_fractional)
+    const std::uint32_t* images = nullptr;    // [E] (device_fractional)
+    const double* positions = nullptr;        // [N][3] Cartesian (shifts)
+    const double* edges = nullptr;            // [E][3] (cartesian, fractional)
+    const int* shifts = nullptr;              // [E][3] (shifts)
+};
+void launch_displacements(int N, const double* cell, const double* inv_cell, const int pbc[3], bool ref_fractional,
+                          const double* reference_positions, const double* positions, double* disp, hipStream_t s);
+void launch_edge_xyz(std::int64_t e0, std::int64_t ne, const EdgeReference& ref, const double* cell,
+                     const int* receivers, const int* sources, const double* disp, double cutoff, double* xyz,
+                     double* r, int* invalid, hipStream_t s);
 
 // Neighbour list (bit-exact with the reference's device builder).
 struct NeighborResult {

@@ -62,6 +62,13 @@ class SmxLammpsArgsV1(ctypes.Structure):
                 ("reserved", ctypes.c_int32), ("f", ctypes.c_void_p), ("eatom", ctypes.c_void_p)]
 
 
+class SmxEvaluatorCounters(ctypes.Structure):
+    _fields_ = [("struct_size", ctypes.c_uint32), ("reserved", ctypes.c_uint32),
+                ("last_graph_prepare_ms", ctypes.c_double), ("last_evaluation_ms", ctypes.c_double),
+                ("graph_prepare_count", ctypes.c_int64), ("evaluation_count", ctypes.c_int64),
+                ("geometry_prepare_count", ctypes.c_int64)]
+
+
 class SmxLammpsArgsV2(ctypes.Structure):
     """SmxLammpsArgsV1 followed by the caller's hipStream_t: the call waits
     for the work the caller queued there instead of synchronising the device."""
@@ -116,6 +123,14 @@ SIGNATURES = [
     ("smx_kernel_timing_reset", _i32, [_vp]),
     ("smx_kernel_timing", _i32, [_vp, _i32, ctypes.POINTER(_cp), _p_dbl, _p_i64]),
     ("smx_neighbor_list", _i32, [_i32, _vp, _vp, _vp, _dbl, _p_i64, _vp, _vp, _vp, _vp, _vp]),
+    ("smx_set_execution_plan_request", _i32, [_vp, _cp, _cp, _cp]),
+    ("smx_set_allow_fixed_workspace", _i32, [_vp, _i32]),
+    ("smx_execution_plan_report", _i32, [_vp, _vp, _i64, _p_i64]),
+    ("smx_evaluator_counters", _i32, [_vp, ctypes.POINTER(SmxEvaluatorCounters)]),
+    ("smx_prepare_active_types", _i32, [_vp, _vp, _i32]),
+    ("smx_prepare_factorized_geometry", _i32, [_vp, _u64, _vp, _i64, _vp, _i64, _vp, _vp, _vp]),
+    ("smx_prepare_factorized_shift_geometry", _i32, [_vp, _u64, _vp, _i64, _vp, _i64, _vp, _vp, _vp]),
+    ("smx_prepare_factorized_fractional_geometry", _i32, [_vp, _u64, _vp, _i64, _vp, _i64, _vp, _vp, _vp]),
     ("smx_r1_plugin_configure", _i32, [_cp, ctypes.POINTER(SmxR1PluginIdentity)]),
     ("smx_r1_plugin_spline_table", _i32, [_vp, _i64, _p_i32, _p_i32, _p_dbl, _p_dbl]),
     ("smx_r1_plugin_reserve", _i32, [_vp, _i64, _i64]),

@@ -1,28 +1,52 @@
 """ASE-style ``Symmetrix`` calculator on the MI355X evaluator.
 
 Caller contract of the reference calculator (symmetrix/source/symmetrix/
-calculator.py): ``calculate`` (:3934-4021) reuses the prepared neighbour graph
-while no atom has moved more than half the Verlet skin since it was built and
-the cell, numbers and periodicity are unchanged (:2838-3093, threshold
-:2894-2899); otherwise it rebuilds the graph on the device at cutoff + skin
-(:2931-2971).  Skin edges are clamped to the cutoff by the evaluator.  Results
-(:3821-3894): ``energy``/``free_energy`` are the FP64 sum of the node energies,
-``energies`` the node energies, ``forces`` the FP64 atom forces and ``stress``
-the Voigt 6-vector of sigma = -(1/V) sum_e f_e xyz_e^T.
+calculator.py), kept here:
+
+* ``calculate`` (:3934-4021) runs one prepared-graph evaluation per call and
+  returns ``energy``/``free_energy`` (FP64 sum of the node energies),
+  ``energies``, ``forces`` (FP64 atom forces) and ``stress`` (Voigt
+  6-vector of sigma = -(1/V) sum_e f_e xyz_e^T) (:3821-3894).
+* Graph cache (``_cached_neighbor_geometry``, :2838-3093): the graph is built
+  at cutoff + skin and reused while it stays valid.  Fully periodic cells
+  keep a fractional topology: the positions split into an affine part (the
+  topology's fractional positions times the current cell) and a non-affine
+  rest, and the topology stays valid while
+  ``||cell^-1 topology_cell||_2 (cutoff + 2 max|non-affine|) <= cutoff +
+  skin`` (:2858-2887); a changed cell then only updates the evaluator's cell
+  (``_update_factorized_cell``).  Other cells reuse the graph while no atom
+  has moved more than skin/2 (minimum image along the periodic axes) and
+  the cell is unchanged (:2888-2899).
+* Neighbour backend (:83-84, 165-173, 2931-2979): the device builder
+  (``_prepare_periodic_factorized_graph``) for fully periodic systems of at
+  least 512 atoms, else a host list (``symmetrix.neighbors``, the ``"ijS"``
+  list the reference takes from matscipy/ASE).  ``SYMMETRIX_NEIGHBOR_BACKEND``
+  = ``automatic`` | ``host`` | ``kokkos`` pins it as in the reference.
+* Host graphs go through ``_prepare_factorized_graph`` and one of the
+  evaluator's geometry forms (:3224-3300): integer shifts under the tiled
+  (fixed-workspace) plan, fractional positions and edge vectors for fully
+  periodic cells, Cartesian reference positions and edge vectors otherwise;
+  then ``_compute_prepared_factorized_positions``.
+* ``execution_profile`` ("capacity" default, or "speed") and
+  ``allow_fixed_workspace`` are passed to the evaluator's plan request
+  (:1165-1190); their checks follow :827-888.
 
 ASE is optional: with it installed the class is an ``ase.calculators.
 calculator.Calculator``; without it ``calculate`` takes any object with
 ``get_atomic_numbers``, ``get_positions``, ``get_cell`` and ``pbc`` (or a dict
-with ``numbers``, ``positions``, ``cell``).
+with ``numbers``, ``positions``, ``cell`` and optionally ``pbc``).
 """
 
 from __future__ import annotations
 
 import logging
+import os
+from dataclasses import dataclass
 
 import numpy as np
 
 from .mace_kokkos import MACEKokkosFloat
+from .neighbors import neighbor_list_ijS
 
 log = logging.getLogger(__name__)
 
@@ -46,6 +70,12 @@ except ImportError:  # pragma: no cover
                 self.atoms = atoms
 
 
+AUTOMATIC_DEVICE_NEIGHBOR_MIN_ATOMS = 512
+NEIGHBOR_BACKENDS = ("automatic", "host", "kokkos")
+EXECUTION_PROFILES = ("capacity", "speed")
+TILED_PLAN = "mh0-dual-layer-tiled-v1"
+
+
 def full_3x3_to_voigt_6_stress(s):
     """ASE's Voigt order: xx, yy, zz, yz, xz, xy."""
     s = np.asarray(s)
@@ -57,24 +87,56 @@ def _system_arrays(atoms):
     if isinstance(atoms, dict):
         numbers = np.asarray(atoms["numbers"])
         positions = np.asarray(atoms["positions"], dtype=float)
-        cell = np.asarray(atoms["cell"], dtype=float).reshape(3, 3)
-        pbc = np.asarray(atoms.get("pbc", [True, True, True]), dtype=bool)
+        cell = np.asarray(atoms.get("cell", np.zeros((3, 3))), dtype=float).reshape(3, 3)
+        pbc = np.asarray(atoms.get("pbc", [True, True, True]), dtype=bool).reshape(3)
     else:
         numbers = np.asarray(atoms.get_atomic_numbers())
         positions = np.asarray(atoms.get_positions(), dtype=float)
         cell = np.asarray(atoms.get_cell(), dtype=float).reshape(3, 3)
-        pbc = np.asarray(atoms.pbc, dtype=bool)
+        pbc = np.asarray(atoms.pbc, dtype=bool).reshape(3)
     return numbers, positions, cell, pbc
 
 
+def neighbor_backend_request():
+    request = os.environ.get("SYMMETRIX_NEIGHBOR_BACKEND", "automatic").strip().lower()
+    if request not in NEIGHBOR_BACKENDS:
+        raise ValueError("SYMMETRIX_NEIGHBOR_BACKEND must be one of %s; got %r"
+                         % (", ".join(sorted(NEIGHBOR_BACKENDS)), request))
+    return request
+
+
+def use_device_neighbor_graph(request, eligible, num_atoms):
+    """calculator.py:165-173 on a GPU evaluator."""
+    if not eligible or request == "host":
+        return False
+    if request == "kokkos":
+        return True
+    return num_atoms >= AUTOMATIC_DEVICE_NEIGHBOR_MIN_ATOMS
+
+
+def minimum_image(displacements, cell, pbc):
+    """Displacements wrapped to the minimum image along the periodic axes."""
+    if not np.any(pbc):
+        return displacements
+    f = np.linalg.solve(cell.T, displacements.T).T
+    f[:, pbc] -= np.rint(f[:, pbc])
+    return f @ cell
+
+
+@dataclass
 class _NeighborCache:
-    def __init__(self, generation, numbers, positions, cell, pbc, num_edges):
-        self.generation = generation
-        self.numbers = numbers.copy()
-        self.reference_positions = positions.copy()
-        self.cell = cell.copy()
-        self.pbc = pbc.copy()
-        self.num_edges = num_edges
+    numbers: np.ndarray
+    pbc: np.ndarray
+    topology_cell: np.ndarray
+    topology_positions: np.ndarray
+    topology_fractional: np.ndarray  # [N,3] when fully periodic, else empty
+    cell: np.ndarray
+    generation: int                  # evaluator graph token
+    device: bool
+    num_edges: int
+    receivers: np.ndarray
+    sources: np.ndarray
+    shifts: np.ndarray
 
 
 class Symmetrix(_Base):
@@ -83,22 +145,49 @@ class Symmetrix(_Base):
 
     implemented_properties = ["energy", "free_energy", "energies", "forces", "stress"]
 
-    def __init__(self, model_file, dtype="float32", streamed_edges="direct", neighbor_skin=0.5,
-                 head=None, **kwargs):
+    def __init__(self, model_file, dtype="float32", use_kokkos=True, streamed_edges="direct",
+                 execution_profile="capacity", allow_fixed_workspace=False, neighbor_skin=0.5, head=None,
+                 **kwargs):
         super().__init__(**kwargs)
         if dtype not in ("float32", np.float32):
             raise ValueError("the MI355X evaluator implements dtype='float32'")
-        if streamed_edges != "direct":
+        if not use_kokkos:
+            raise ValueError("the MI355X evaluator is the device (use_kokkos=True) path")
+        if streamed_edges not in ("direct", "factorized", "direct_streamed"):
             raise ValueError("the MI355X evaluator implements streamed_edges='direct'")
+        if execution_profile not in EXECUTION_PROFILES:
+            raise ValueError("execution_profile must be 'capacity' or 'speed'")
+        if streamed_edges in ("factorized", "direct_streamed") and execution_profile == "capacity":
+            execution_profile = "speed"  # the aliases keep the throughput behaviour (python_api.md:40-45)
+        if not isinstance(allow_fixed_workspace, bool):
+            raise ValueError("allow_fixed_workspace must be a bool.")
+        if allow_fixed_workspace and execution_profile != "capacity":
+            raise ValueError("allow_fixed_workspace=True requires execution_profile='capacity'.")
         if not (neighbor_skin >= 0.0):
             raise ValueError("neighbor_skin must be non-negative")
         self.evaluator = MACEKokkosFloat(model_file, head or "")
+        self.streamed_edges = "direct"
+        self.execution_profile = execution_profile
+        self.allow_fixed_workspace = allow_fixed_workspace
+        self.evaluator._set_allow_fixed_workspace(allow_fixed_workspace)
+        self.evaluator._set_execution_plan_request("direct", execution_profile, "")
         self.cutoff = float(self.evaluator.r_cut)
         self.neighbor_skin = float(neighbor_skin)
         self._types = {z: i for i, z in enumerate(self.evaluator.atomic_numbers)}
         self._neighbor_cache = None
-        self.neighbor_graph_rebuilds = 0
+        self.neighbor_cache_build_count = 0
+        self.neighbor_cache_reuse_count = 0
+        self.neighbor_cache_cell_update_count = 0
+        self.neighbor_graph_backend = None
         self.results = {}
+
+    @property
+    def neighbor_graph_rebuilds(self):
+        return self.neighbor_cache_build_count
+
+    @property
+    def execution_plan(self):
+        return self.evaluator.execution_plan_report
 
     # -------------------------------------------------------------- graph
     def _node_types(self, numbers):
@@ -107,34 +196,91 @@ class Symmetrix(_Base):
         except KeyError as exc:
             raise ValueError("atomic number %s is not in the model" % exc.args[0]) from None
 
-    def _cache_valid(self, numbers, positions, cell, pbc):
+    def _reuse(self, numbers, positions, cell, pbc):
+        """'reuse', 'cell' (topology valid under a new cell) or None."""
         c = self._neighbor_cache
         if c is None or len(numbers) != len(c.numbers) or not np.array_equal(numbers, c.numbers):
-            return False
-        if not np.array_equal(cell, c.cell) or not np.array_equal(pbc, c.pbc):
-            return False
-        disp = positions - c.reference_positions
-        # minimum image of the displacement (positions may have been wrapped)
-        inv = np.linalg.inv(cell)
-        f = disp @ inv
-        f -= np.floor(f + 0.5)
-        disp = f @ cell
-        return float(np.max(np.linalg.norm(disp, axis=1), initial=0.0)) <= 0.5 * self.neighbor_skin
+            return None
+        if not np.array_equal(pbc, c.pbc):
+            return None
+        cell_changed = not np.array_equal(cell, c.cell)
+        if np.all(pbc):
+            try:
+                non_affine = positions - c.topology_fractional @ cell
+                non_affine = minimum_image(non_affine, cell, pbc)
+                deformation = np.linalg.solve(cell, c.topology_cell)
+            except np.linalg.LinAlgError:
+                return None
+            max_non_affine = float(np.max(np.linalg.norm(non_affine, axis=1), initial=0.0))
+            contraction = float(np.linalg.norm(deformation, ord=2))
+            if contraction * (self.cutoff + 2.0 * max_non_affine) > self.cutoff + self.neighbor_skin:
+                return None
+            return "cell" if cell_changed else "reuse"
+        if cell_changed:
+            return None
+        disp = minimum_image(positions - c.topology_positions, cell, pbc)
+        if float(np.max(np.linalg.norm(disp, axis=1), initial=0.0)) > 0.5 * self.neighbor_skin:
+            return None
+        return "reuse"
+
+    def _fixed_workspace_plan_selected(self):
+        return self.evaluator.execution_plan_report.get("selected_id") == TILED_PLAN
 
     def _prepare(self, numbers, positions, cell, pbc):
-        if not np.all(pbc):
-            raise NotImplementedError("the MI355X device neighbour list requires a fully periodic cell")
-        if abs(np.linalg.det(cell)) <= 0.0:
-            raise ValueError("cell must be invertible")
         if not np.isfinite(positions).all():
             raise ValueError("positions must be finite")
         types = self._node_types(numbers)
-        inv = np.linalg.inv(cell)
-        g = self.evaluator._prepare_periodic_factorized_graph(
-            types, positions.reshape(-1), cell.reshape(-1), inv.reshape(-1), self.cutoff + self.neighbor_skin)
-        self._neighbor_cache = _NeighborCache(g["generation"], numbers, positions, cell, pbc, g["num_edges"])
-        self.neighbor_graph_rebuilds += 1
+        n = len(types)
+        periodic = bool(np.all(pbc))
+        if np.any(pbc) and not abs(np.linalg.det(cell)) > 0.0:
+            raise ValueError("a periodic cell must be invertible")
+        inv = np.linalg.inv(cell) if np.any(pbc) else np.zeros((3, 3))
+        frac = positions @ inv if periodic else np.zeros((0, 3))
+        request = neighbor_backend_request()
+        device = use_device_neighbor_graph(request, periodic, n)
+        if request == "kokkos" and not periodic:
+            raise RuntimeError("SYMMETRIX_NEIGHBOR_BACKEND=kokkos requires a fully periodic cell")
+        ev = self.evaluator
+        reach = self.cutoff + self.neighbor_skin
+        if device:
+            g = ev._prepare_periodic_factorized_graph(types, positions.reshape(-1), cell.reshape(-1),
+                                                      inv.reshape(-1), reach)
+            gen, num_edges = g["generation"], g["num_edges"]
+            receivers = sources = np.zeros(0, np.int32)
+            shifts = np.zeros((0, 3), np.int32)
+            self.neighbor_graph_backend = "device"
+        else:
+            receivers, sources, shifts = neighbor_list_ijS(positions, cell, pbc, reach)
+            num_neigh = np.bincount(receivers, minlength=n).astype(np.int32)
+            gen = ev._prepare_factorized_graph(n, types, num_neigh, sources, types[sources])
+            num_edges = len(sources)
+            pbc_i = pbc.astype(np.int32)
+            if self._fixed_workspace_plan_selected():
+                ev._prepare_factorized_shift_geometry(gen, positions, shifts, cell, inv, pbc_i)
+            elif periodic:
+                frac_xyz = frac[sources] - frac[receivers] + shifts
+                ev._prepare_factorized_fractional_geometry(gen, frac, frac_xyz, cell, inv, pbc_i)
+            else:
+                ref_xyz = positions[sources] - positions[receivers] + shifts @ cell
+                ev._prepare_factorized_geometry(gen, positions, ref_xyz, cell, inv, pbc_i)
+            self.neighbor_graph_backend = "host"
+        self._neighbor_cache = _NeighborCache(numbers.copy(), pbc.copy(), cell.copy(), positions.copy(),
+                                              frac.copy(), cell.copy(), gen, device, num_edges, receivers,
+                                              sources, shifts)
+        self.neighbor_cache_build_count += 1
         return self._neighbor_cache
+
+    def _graph(self, numbers, positions, cell, pbc):
+        state = self._reuse(numbers, positions, cell, pbc)
+        if state is None:
+            return self._prepare(numbers, positions, cell, pbc)
+        c = self._neighbor_cache
+        if state == "cell":
+            self.evaluator._update_factorized_cell(c.generation, cell.reshape(-1), np.linalg.inv(cell).reshape(-1))
+            c.cell = cell.copy()
+            self.neighbor_cache_cell_update_count += 1
+        self.neighbor_cache_reuse_count += 1
+        return c
 
     # ---------------------------------------------------------- calculate
     def calculate(self, atoms=None, properties=None, system_changes=_all_changes):
@@ -148,10 +294,7 @@ class Symmetrix(_Base):
         else:
             atoms = self.atoms
         numbers, positions, cell, pbc = _system_arrays(atoms)
-        if self._cache_valid(numbers, positions, cell, pbc):
-            cache = self._neighbor_cache
-        else:
-            cache = self._prepare(numbers, positions, cell, pbc)
+        cache = self._graph(numbers, positions, cell, pbc)
         ev = self.evaluator
         ev._compute_prepared_factorized_positions(cache.generation, positions.reshape(-1))
         node_energies = np.array(ev.node_energies, dtype=np.float64, copy=True)
@@ -160,6 +303,8 @@ class Symmetrix(_Base):
         self.results["forces"] = np.asarray(ev._reduce_atom_forces(len(numbers), None, None, cache.generation))
         if "stress" in properties:
             volume = abs(float(np.linalg.det(cell)))
+            if not volume > 0.0:
+                raise ValueError("stress needs a cell of non-zero volume")
             sigma = ev._reduce_stress(volume, None, cache.generation)
             self.results["stress"] = full_3x3_to_voigt_6_stress(sigma)
         return self.results

@@ -4,17 +4,25 @@ MI355X library.
 Method names, argument meanings and error behaviour follow the reference's
 pybind class (symmetrix/source/cpp/mace_kokkos.cpp): ``_prepare_factorized_graph``
 (:1561), ``_prepare_periodic_factorized_graph`` (:1580, returns
-``{"generation", "num_edges"}``), ``_update_factorized_cell``,
-``_compute_prepared_factorized`` (:1817), ``_compute_prepared_factorized_positions``
-(:1828), ``compute_node_energies_forces`` (:2169), ``_reduce_atom_forces``
-(:2103), ``_reduce_stress`` (:2134) and the ``node_energies``/``node_forces``/
-``r_cut``/``atomic_numbers`` attributes.  Bad inputs and stale generations
-raise ValueError, device failures RuntimeError.
+``{"generation", "num_edges"}``), ``_prepare_factorized_geometry``,
+``_prepare_factorized_shift_geometry`` and
+``_prepare_factorized_fractional_geometry`` (:1608-1672),
+``_update_factorized_cell``, ``_compute_prepared_factorized`` (:1817),
+``_compute_prepared_factorized_positions`` (:1828),
+``compute_node_energies_forces`` (:2169), ``_reduce_atom_forces`` (:2103),
+``_reduce_stress`` (:2134), ``prepare_active_types`` (:2076), the plan
+request ``_set_execution_plan_request`` / ``_set_allow_fixed_workspace`` /
+``execution_plan_report`` (:266-297, 444-447), the counters
+``factorized_last_graph_prepare_ms`` / ``factorized_last_evaluation_ms``
+(:1045-1053) and the ``node_energies``/``node_forces``/``r_cut``/
+``atomic_numbers`` attributes.  Bad inputs and stale generations raise
+ValueError, device failures RuntimeError.
 """
 
 from __future__ import annotations
 
 import ctypes
+import json
 
 import numpy as np
 
@@ -79,10 +87,65 @@ class MACEKokkosFloat:
         check(lib.smx_set_streamed_edges(self._h, str(mode).encode()))
 
     def set_execution_plan_request(self, profile="auto", tile_receivers=0):
-        """``"speed"`` (untiled), ``"capacity"`` (three-sweep tiled plan with at
-        most ``tile_receivers`` receivers per tile) or ``"auto"``; applies to
-        graphs prepared afterwards."""
+        """Shorthand with the tile size: ``"speed"`` (the speed profile),
+        ``"capacity"`` (the three-sweep tiled plan pinned, at most
+        ``tile_receivers`` receivers per tile) or ``"auto"`` (the capacity
+        profile with fixed workspaces allowed); applies to graphs prepared
+        afterwards."""
         check(lib.smx_set_execution_plan(self._h, str(profile).encode(), int(tile_receivers)))
+
+    def _set_execution_plan_request(self, algorithm, profile, debug_plan=""):
+        """The reference's plan request (mace_kokkos.cpp:266-270): algorithm
+        "direct", profile "capacity" or "speed", debug_plan "" or a plan id."""
+        check(lib.smx_set_execution_plan_request(self._h, str(algorithm).encode(), str(profile).encode(),
+                                                 str(debug_plan or "").encode()))
+
+    def _resolve_execution_plan(self):
+        """The plan is resolved when a graph is prepared; returns the report."""
+        return self.execution_plan_report
+
+    def _set_allow_fixed_workspace(self, allow):
+        check(lib.smx_set_allow_fixed_workspace(self._h, 1 if allow else 0))
+        self._allow_fixed = bool(allow)
+
+    @property
+    def allow_fixed_workspace(self):
+        return self.execution_plan_report["allow_fixed_workspace"]
+
+    @property
+    def execution_plan_report(self):
+        n = ctypes.c_int64()
+        check(lib.smx_execution_plan_report(self._h, None, 0, ctypes.byref(n)))
+        buf = ctypes.create_string_buffer(int(n.value))
+        check(lib.smx_execution_plan_report(self._h, ctypes.addressof(buf), n.value, None))
+        return json.loads(buf.value.decode())
+
+    def _counters(self):
+        c = _native.SmxEvaluatorCounters()
+        c.struct_size = ctypes.sizeof(c)
+        check(lib.smx_evaluator_counters(self._h, ctypes.byref(c)))
+        return c
+
+    @property
+    def factorized_last_graph_prepare_ms(self):
+        return self._counters().last_graph_prepare_ms
+
+    @property
+    def factorized_last_evaluation_ms(self):
+        return self._counters().last_evaluation_ms
+
+    def prepare_active_types(self, node_types, neigh_types=None):
+        """Tabulate the radial tables of these model types ahead of the graph
+        (mace_kokkos.cpp:223-254: node types, then unseen neighbour types)."""
+        types = [int(t) for t in np.asarray(node_types).ravel()]
+        if neigh_types is not None:
+            types += [int(t) for t in np.asarray(neigh_types).ravel()]
+        seen = []
+        for t in types:
+            if t not in seen:
+                seen.append(t)
+        arr = i32(seen)
+        check(lib.smx_prepare_active_types(self._h, ptr(arr) if arr.size else None, arr.size))
 
     @property
     def execution_plan(self):
@@ -138,6 +201,34 @@ class MACEKokkosFloat:
         self._num_nodes = node_types.size
         self._num_edges = int(ne.value)
         return {"generation": int(gen.value), "num_edges": int(ne.value)}
+
+    def _geometry_arrays(self, positions, edges, cell, inverse_cell, pbc, edge_dtype):
+        positions, cell, inverse_cell = f64(positions), f64(cell), f64(inverse_cell)
+        edges = np.ascontiguousarray(np.asarray(edges, dtype=edge_dtype).reshape(-1))
+        pbc = i32(np.asarray(pbc).astype(np.int32))
+        if cell.size != 9 or inverse_cell.size != 9 or pbc.size != 3:
+            raise ValueError("Execution R1 prepared geometry extents are inconsistent.")
+        return positions, edges, cell, inverse_cell, pbc
+
+    def _prepare_factorized_geometry(self, execution_graph_generation, reference_positions, reference_xyz, cell,
+                                     inverse_cell, pbc):
+        p, e, c, ic, b = self._geometry_arrays(reference_positions, reference_xyz, cell, inverse_cell, pbc,
+                                               np.float64)
+        check(lib.smx_prepare_factorized_geometry(self._h, int(execution_graph_generation), ptr(p), p.size, ptr(e),
+                                                  e.size, ptr(c), ptr(ic), ptr(b)))
+
+    def _prepare_factorized_shift_geometry(self, execution_graph_generation, reference_positions, shifts, cell,
+                                           inverse_cell, pbc):
+        p, e, c, ic, b = self._geometry_arrays(reference_positions, shifts, cell, inverse_cell, pbc, np.int32)
+        check(lib.smx_prepare_factorized_shift_geometry(self._h, int(execution_graph_generation), ptr(p), p.size,
+                                                        ptr(e), e.size, ptr(c), ptr(ic), ptr(b)))
+
+    def _prepare_factorized_fractional_geometry(self, execution_graph_generation, fractional_positions,
+                                                fractional_xyz, cell, inverse_cell, pbc):
+        p, e, c, ic, b = self._geometry_arrays(fractional_positions, fractional_xyz, cell, inverse_cell, pbc,
+                                               np.float64)
+        check(lib.smx_prepare_factorized_fractional_geometry(self._h, int(execution_graph_generation), ptr(p),
+                                                             p.size, ptr(e), e.size, ptr(c), ptr(ic), ptr(b)))
 
     def _update_factorized_cell(self, execution_graph_generation, cell, inverse_cell):
         cell, inverse_cell = f64(cell), f64(inverse_cell)

@@ -142,17 +142,50 @@ class FakeEvaluator:
     r_cut = 5.0
     atomic_numbers = [8, 22, 38]
 
-    def __init__(self):
+    def __init__(self, tiled=False):
         self.prepared = 0
+        self.device_prepared = 0
+        self.geometry = []
+        self.cell_updates = 0
         self.computed = []
         self._gen = 0
+        self.tiled = tiled
 
     def _prepare_periodic_factorized_graph(self, types, positions, cell, inv, cutoff):
         self.prepared += 1
+        self.device_prepared += 1
         self._gen += 1
         self.n = len(types)
         self.cutoff = cutoff
         return {"generation": self._gen, "num_edges": 10}
+
+    def _prepare_factorized_graph(self, n, types, num_neigh, sources, neigh_types):
+        assert int(np.sum(num_neigh)) == len(sources) and len(types) == n
+        self.prepared += 1
+        self._gen += 1
+        self.n = n
+        self.edges = len(sources)
+        return self._gen
+
+    def _prepare_factorized_geometry(self, gen, ref_positions, ref_xyz, cell, inv, pbc):
+        assert gen == self._gen and np.asarray(ref_xyz).size == 3 * self.edges
+        self.geometry.append("cartesian")
+
+    def _prepare_factorized_fractional_geometry(self, gen, frac, frac_xyz, cell, inv, pbc):
+        assert gen == self._gen and np.asarray(frac_xyz).size == 3 * self.edges
+        self.geometry.append("fractional")
+
+    def _prepare_factorized_shift_geometry(self, gen, ref_positions, shifts, cell, inv, pbc):
+        assert gen == self._gen and np.asarray(shifts).size == 3 * self.edges
+        self.geometry.append("shifts")
+
+    def _update_factorized_cell(self, gen, cell, inv):
+        assert gen == self._gen
+        self.cell_updates += 1
+
+    @property
+    def execution_plan_report(self):
+        return {"selected_id": "mh0-dual-layer-tiled-v1" if self.tiled else "mh0-direct-capacity-retained"}
 
     def _compute_prepared_factorized_positions(self, gen, positions):
         assert gen == self._gen
@@ -169,15 +202,18 @@ class FakeEvaluator:
         return np.eye(3) * 0.01
 
 
-def _calc(skin=0.5):
+def _calc(skin=0.5, tiled=False):
     c = Symmetrix.__new__(Symmetrix)
     Symmetrix.__bases__[0].__init__(c)
-    c.evaluator = FakeEvaluator()
+    c.evaluator = FakeEvaluator(tiled)
     c.cutoff = 5.0
     c.neighbor_skin = skin
     c._types = {8: 0, 22: 1, 38: 2}
     c._neighbor_cache = None
-    c.neighbor_graph_rebuilds = 0
+    c.neighbor_cache_build_count = 0
+    c.neighbor_cache_reuse_count = 0
+    c.neighbor_cache_cell_update_count = 0
+    c.neighbor_graph_backend = None
     c.results = {}
     return c
 
@@ -186,8 +222,8 @@ def test_calculator_reuses_graph_within_half_skin():
     c = _calc(skin=0.5)
     s = systems.srtio3_supercell(2, sigma=0.0)
     r = c.calculate(s, ["energy", "forces", "stress"])
-    assert c.evaluator.prepared == 1
-    assert c.evaluator.cutoff == pytest.approx(5.5)
+    assert c.evaluator.prepared == 1 and c.neighbor_graph_backend == "host"   # 40 atoms < 512
+    assert c.evaluator.geometry == ["fractional"]
     assert r["energy"] == pytest.approx(-1.5 * len(s["numbers"]))
     np.testing.assert_allclose(r["stress"], [0.01, 0.01, 0.01, 0, 0, 0])
     moved = dict(s)
@@ -199,18 +235,29 @@ def test_calculator_reuses_graph_within_half_skin():
     assert c.evaluator.prepared == 2  # one atom moved more than skin/2
 
 
-def test_calculator_rebuilds_on_cell_or_numbers_change():
-    c = _calc()
-    s = systems.srtio3_supercell(2, sigma=0.0)
-    c.calculate(s)
-    strained = dict(s)
-    strained["cell"] = s["cell"] * 1.001
-    c.calculate(strained)
-    assert c.evaluator.prepared == 2
-    swapped = dict(strained)
-    swapped["numbers"] = s["numbers"][::-1].copy()
-    c.calculate(swapped)
-    assert c.evaluator.prepared == 3
+def test_calculator_keeps_topology_under_affine_strain(monkeypatch):
+    """calculator.py:2858-2887: a strained cell with the atoms carried along
+    updates the evaluator's cell; a large strain or new numbers rebuild."""
+    for backend, device in (("host", 0), ("kokkos", 1)):
+        monkeypatch.setenv("SYMMETRIX_NEIGHBOR_BACKEND", backend)
+        c = _calc()
+        s = systems.srtio3_supercell(2, sigma=0.0)
+        c.calculate(s)
+        assert c.evaluator.device_prepared == device
+        strained = dict(s)
+        strained["cell"] = s["cell"] * 1.001
+        strained["positions"] = s["positions"] * 1.001
+        c.calculate(strained)
+        assert c.evaluator.prepared == 1 and c.evaluator.cell_updates == 1
+        far = dict(s)
+        far["cell"] = s["cell"] * 0.85
+        far["positions"] = s["positions"] * 0.85
+        c.calculate(far)
+        assert c.evaluator.prepared == 2   # compression: cutoff / 0.85 exceeds cutoff + skin
+        swapped = dict(far)
+        swapped["numbers"] = s["numbers"][::-1].copy()
+        c.calculate(swapped)
+        assert c.evaluator.prepared == 3
 
 
 def test_calculator_wrapped_positions_do_not_force_rebuild():
@@ -223,7 +270,37 @@ def test_calculator_wrapped_positions_do_not_force_rebuild():
     assert c.evaluator.prepared == 1
 
 
-def test_calculator_rejects_unknown_species_and_open_cells():
+def test_calculator_geometry_forms_by_boundary_and_plan(monkeypatch):
+    """Host graphs take the Cartesian form for open or mixed boundaries, the
+    fractional form for periodic cells and the shift form under the tiled
+    plan (calculator.py:3224-3300); large periodic systems use the device
+    builder (calculator.py:83-84, 165-173)."""
+    monkeypatch.delenv("SYMMETRIX_NEIGHBOR_BACKEND", raising=False)
+    s = systems.srtio3_supercell(2, sigma=0.0)
+    slab = dict(s, pbc=np.array([True, True, False]))
+    c = _calc()
+    c.calculate(slab, ["energy", "forces"])
+    assert c.evaluator.geometry == ["cartesian"]
+    molecule = dict(s, pbc=np.array([False, False, False]))
+    c = _calc()
+    c.calculate(molecule, ["energy", "forces"])
+    assert c.evaluator.geometry == ["cartesian"]
+    with pytest.raises(ValueError, match="volume"):
+        c.calculate(dict(molecule, cell=np.zeros((3, 3))), ["stress"])
+    c = _calc(tiled=True)
+    c.calculate(s)
+    assert c.evaluator.geometry == ["shifts"]
+    big = systems.srtio3_supercell(5, sigma=0.0)   # 625 atoms
+    c = _calc()
+    c.calculate(big)
+    assert c.evaluator.device_prepared == 1 and c.neighbor_graph_backend == "device"
+    monkeypatch.setenv("SYMMETRIX_NEIGHBOR_BACKEND", "host")
+    c = _calc()
+    c.calculate(big)
+    assert c.evaluator.device_prepared == 0 and c.evaluator.geometry == ["fractional"]
+
+
+def test_calculator_rejects_unknown_species():
     c = _calc()
     s = systems.srtio3_supercell(2, sigma=0.0)
     bad = dict(s)
@@ -231,7 +308,52 @@ def test_calculator_rejects_unknown_species_and_open_cells():
     bad["numbers"][0] = 1
     with pytest.raises(ValueError):
         c.calculate(bad)
-    open_ = dict(s)
-    open_["pbc"] = np.array([True, True, False])
-    with pytest.raises(NotImplementedError):
-        c.calculate(open_)
+
+
+def _brute_force_ijS(positions, cell, pbc, cutoff, reach=3):
+    out = set()
+    rng = [range(-reach, reach + 1) if p else range(0, 1) for p in pbc]
+    for i in range(len(positions)):
+        for j in range(len(positions)):
+            for a in rng[0]:
+                for b in rng[1]:
+                    for c in rng[2]:
+                        if i == j and a == b == c == 0:
+                            continue
+                        d = positions[j] - positions[i] + np.array([a, b, c]) @ cell
+                        if np.linalg.norm(d) < cutoff:
+                            out.add((i, j, a, b, c))
+    return out
+
+
+@pytest.mark.parametrize("pbc", [(True, True, True), (True, False, True), (False, False, False)])
+def test_host_neighbor_list_matches_brute_force(pbc):
+    """The host "ijS" list (the reference's matscipy/ASE list) on a
+    triclinic cell with atoms outside it: every pair closer than the cutoff,
+    receiver-major."""
+    from symmetrix.neighbors import neighbor_list_ijS
+    rng = np.random.default_rng(5)
+    cell = np.array([[6.0, 0.0, 0.0], [1.5, 5.5, 0.0], [-1.0, 0.5, 6.5]])
+    pos = rng.uniform(-0.3, 1.3, size=(30, 3)) @ cell
+    i, j, S = neighbor_list_ijS(pos, cell, pbc, 4.2)
+    assert np.all(np.diff(i) >= 0)
+    got = {(int(a), int(b), *map(int, s)) for a, b, s in zip(i, j, S)}
+    assert len(got) == len(i)
+    assert got == _brute_force_ijS(pos, cell, pbc, 4.2)
+
+
+def test_reference_caller_members_resolve():
+    """Every evaluator member the reference calculator reaches by getattr on
+    its prepared-execution route (calculator.py:1165-1190, 2838-3093,
+    3224-3300, 3418-3440) exists on MACEKokkosFloat."""
+    from symmetrix.mace_kokkos import MACEKokkosFloat
+    names = ["_set_allow_fixed_workspace", "_set_execution_plan_request", "_resolve_execution_plan",
+             "execution_plan_report", "streamed_edges_mode", "atomic_numbers",
+             "_prepare_periodic_factorized_graph", "_prepare_factorized_graph", "_compute_prepared_factorized",
+             "_prepare_factorized_geometry", "_prepare_factorized_fractional_geometry",
+             "_prepare_factorized_shift_geometry", "_update_factorized_cell",
+             "_compute_prepared_factorized_positions", "_reduce_atom_forces", "_reduce_stress", "node_energies",
+             "node_forces", "compute_node_energies_forces", "prepare_active_types",
+             "factorized_last_evaluation_ms", "factorized_last_graph_prepare_ms", "allow_fixed_workspace"]
+    missing = [n for n in names if not hasattr(MACEKokkosFloat, n)]
+    assert not missing, missing
