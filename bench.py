@@ -14,9 +14,18 @@ HBM: edge geometry, both interaction layers forward and reverse, FP64 atom
 forces, stress and the total energy on the device.  W untimed warm-up steps,
 then exactly K timed steps between device synchronisations.
 
-Also reported: per-kernel HIP-event timing of the dominant kernel on the
-evaluator stream (roofline), the PCIe-inclusive host-positions call, the cold
-call (graph rebuild) and the CPU oracle on a bounded sample (cpu_baseline).
+Also reported (extra keys, each measured in the same run):
+* roofline of the dominant kernel from HIP events on the evaluator stream,
+  with the algorithmic fraction (FP32 peak) and the executed-flop fraction
+  (the non-packed FP32 VALU ceiling);
+* the reference protocol (3 warm-ups, median of 10) with device-resident
+  positions, through the host-positions call, and through the Symmetrix
+  calculator (the reference's ASE-call boundary), plus the cold call;
+* the wide (30,000-atom water) and irregular (20,000 atoms, 10 species)
+  configs: median us/atom and the dominant kernel's fraction;
+* a short tiled capacity run at 11.5M atoms (3 NVE steps);
+* the CPU oracle on the box's host cores (3 warm-ups, median of 10, OMP
+  threads bound to cores), on all allowed cores and on 8 of them.
 """
 
 from __future__ import annotations
@@ -36,8 +45,15 @@ sys.path.insert(0, os.path.join(ROOT, "symmetrix-xl_amd"))
 sys.path.insert(0, ROOT)
 
 PEAK_FP32_TFLOPS = 157.3  # MI355X dense FP32 (matrix and packed vector)
+VALU_FP32_TFLOPS = 78.6   # FP32 VALU without packed FP32 (256 CUs x 4 SIMD x 16 lanes x 2 x 2.4 GHz)
 PEAK_HBM_GBS = 8000.0
 DOMINANT = "r1_reverse"
+# FP32 operations the R1 reverse executes per active edge and channel: the
+# coupled adjoints are contracted once per receiver, leaving per edge
+# T = Y G, s = G h, W = sum_p R T, A = sum_p dR h T, SB = sum_p R s and
+# f = u A + dY SB -- about 380 FMAs (760 flops) per edge-channel at the
+# medium shape (VALU instruction counts of the kernel agree within 5%).
+R1_REVERSE_EXECUTED_FLOPS_PER_EDGE_CHANNEL = {(10, 86, 88): 760}
 
 
 def r1_reverse_flops_per_edge_channel(num_paths, num_terms, num_rows):
@@ -86,48 +102,63 @@ def load_traffic():
         return None
 
 
-def cpu_baseline(model_path, system, cutoff, skin, max_seconds=25.0):
+CPU_WORKER = r"""
+import json, statistics, sys, time
+import numpy as np
+sys.path[:0] = [sys.argv[1], sys.argv[1] + "/symmetrix-xl_amd"]
+from oracle import oracle as ora
+from symmetrix import systems
+om = ora.OracleModel(sys.argv[2])
+system = systems.srtio3_supercell(10, sigma=0.05, seed=0)
+skin = float(sys.argv[3])
+graph = ora.neighbor_graph(system["positions"], system["cell"], om.r_cut + skin)
+cell = np.asarray(system["cell"], float)
+vol = abs(np.linalg.det(cell))
+types = om.types_of(system["numbers"])
+nt = types[graph["sources"]]
+def call():
+    xyz, r = ora.prepared_geometry(graph, cell, system["positions"], system["positions"], om.r_cut)
+    e, f = om.evaluate(types, graph["num_neigh"], graph["sources"], nt, xyz, r)
+    ora.reduce_forces(len(types), graph["receivers"], graph["sources"], f)
+    ora.reduce_stress(f, xyz, vol)
+for _ in range(3):
+    call()
+times = []
+for _ in range(10):
+    t0 = time.perf_counter()
+    call()
+    times.append(time.perf_counter() - t0)
+print(json.dumps({"us_per_atom": statistics.median(times) * 1e6 / len(types),
+                  "threads": int(ora.lib().oracle_num_threads())}))
+"""
+
+
+def cpu_baseline(model_path, skin):
     """The CPU oracle (FP32 C++/OpenMP restatement of the reference CPU path)
-    on the same workload: warm calls with the graph retained."""
-    from oracle import oracle as ora
-    om = ora.OracleModel(model_path)
-    graph = ora.neighbor_graph(system["positions"], system["cell"], cutoff + skin)
-    cell = np.asarray(system["cell"], float)
-    vol = abs(np.linalg.det(cell))
-    types = om.types_of(system["numbers"])
-    nt = types[graph["sources"]]
-
-    def call():
-        xyz, r = ora.prepared_geometry(graph, cell, system["positions"], system["positions"], om.r_cut)
-        e, f = om.evaluate(types, graph["num_neigh"], graph["sources"], nt, xyz, r)
-        ora.reduce_forces(len(types), graph["receivers"], graph["sources"], f)
-        ora.reduce_stress(f, xyz, vol)
-        return float(np.sum(e))
-
-    def median_us_per_atom(seconds, most):
-        times = []
-        t_start = time.perf_counter()
-        while True:
-            t0 = time.perf_counter()
-            call()
-            times.append(time.perf_counter() - t0)
-            if time.perf_counter() - t_start > seconds or len(times) >= most:
-                break
-        return round(statistics.median(times) * 1e6 / len(types), 3), len(times)
-
-    call()  # warm-up (radial tabulation for the active types)
-    cores = int(ora.lib().oracle_num_threads())
-    value, calls = median_us_per_atom(max_seconds, 5)
-    out = {"value": value, "unit": "us/atom", "cores": cores, "kind": "port",
-           "sample": "medium workload (5000 atoms, 496k edges), %d warm call(s) after 1 warm-up, median" % calls,
-           "cpu": cpu_model()}
-    # the reference quotes its CPU path on 8 cores: the same sample on 8 threads
-    if cores > 8:
-        ora.lib().oracle_set_num_threads(8)
-        v8, calls8 = median_us_per_atom(max_seconds / 2, 3)
-        ora.lib().oracle_set_num_threads(cores)
-        out["cores_8"] = {"value": v8, "unit": "us/atom", "cores": 8, "calls": calls8}
-    return out
+    on the headline workload in child processes (no GPU use), with the
+    reference protocol (3 warm-ups, median of 10 calls, graph retained) and
+    threads bound to cores as in benchmarks/openmp_full_property_qualification.py:319-322:
+    run A on every core this process may use (capped at 16, the box's CPU
+    share), run B on 8 of them (the reference's published 8-core figures)."""
+    import subprocess
+    allowed = sorted(os.sched_getaffinity(0))
+    runs = {}
+    for label, cores in (("all", allowed[:16]), ("8_cores", allowed[:8])):
+        env = dict(os.environ, OMP_NUM_THREADS=str(len(cores)), OMP_PROC_BIND="close", OMP_PLACES="cores")
+        cmd = ["taskset", "-c", ",".join(map(str, cores)), sys.executable, "-c", CPU_WORKER, ROOT, model_path,
+               str(skin)]
+        out = subprocess.run(cmd, env=env, capture_output=True, text=True, timeout=300)
+        if out.returncode != 0:
+            raise RuntimeError("CPU baseline worker failed: " + out.stderr[-2000:])
+        runs[label] = json.loads(out.stdout.strip().splitlines()[-1])
+        runs[label]["cpus"] = cores
+    a = runs["all"]
+    return {"value": round(a["us_per_atom"], 3), "unit": "us/atom", "cores": a["threads"], "kind": "port",
+            "sample": "medium workload (5000 atoms, 496k edges, graph retained): 3 warm-up calls, median of 10, "
+                      "OMP_PROC_BIND=close OMP_PLACES=cores, taskset to the listed CPUs",
+            "cpu": cpu_model(), "cpus": a["cpus"],
+            "cores_8": {"value": round(runs["8_cores"]["us_per_atom"], 3), "unit": "us/atom",
+                        "cores": runs["8_cores"]["threads"], "cpus": runs["8_cores"]["cpus"]}}
 
 
 def cpu_model():
@@ -143,7 +174,8 @@ def cpu_model():
 
 def capacity(n, md_steps, tile_receivers):
     """the medium model in the tiled plan on an n^3
-    SrTiO3 supercell; a velocity-Verlet NVE run of md_steps at 1 fs."""
+    SrTiO3 supercell; a velocity-Verlet NVE run of md_steps at 1 fs.
+    Returns the result record."""
     from symmetrix import md, random_model, systems
     from symmetrix.mace_kokkos import MACEKokkosFloat
 
@@ -177,7 +209,8 @@ def capacity(n, md_steps, tile_receivers):
         "energy_drift_eV_per_atom": (trace[-1] - trace[0]) / n_atoms,
         "reference": {"atoms": 11240455, "hardware": "A100 80 GB", "mode": "tiled streaming"},
     }
-    print(json.dumps(out), flush=True)
+    ev.close()
+    return out
 
 
 def copy_calibration(nbytes, repeats=5):
@@ -202,6 +235,10 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-calculator", action="store_true", help="skip the calculator-boundary timing")
+    ap.add_argument("--no-configs", action="store_true", help="skip the wide and irregular configs")
+    ap.add_argument("--capacity-steps", type=int, default=3,
+                    help="NVE steps of the tiled 11.5M-atom capacity extra key (0 skips it)")
     ap.add_argument("--capacity", type=int, default=0, metavar="N",
                     help="run the tiled capacity config on an N^3 SrTiO3 supercell instead")
     ap.add_argument("--md-steps", type=int, default=20)
@@ -217,15 +254,87 @@ def main():
         copy_calibration(args.copy_calibration)
         return
     if args.capacity:
-        capacity(args.capacity, args.md_steps, args.tile_receivers)
+        print(json.dumps(capacity(args.capacity, args.md_steps, args.tile_receivers)), flush=True)
         return
 
     from symmetrix import random_model, systems
-    from symmetrix.mace_kokkos import MACEKokkosFloat
+
+    def note(msg):
+        print("[bench] %s" % msg, file=sys.stderr, flush=True)
 
     model_path = random_model.cached_model("medium")
     system = systems.srtio3_supercell(10, sigma=0.05, seed=0)
     skin = 0.5
+    hip = hip_lib()
+    head = run_config(hip, model_path, system, skin, args.warmup, args.steps, timed_steps=True)
+    n_atoms = head["atoms"]
+    note("medium: %.4f us/atom (mean of %d), median %.4f" % (head["us_per_atom"], args.steps,
+                                                           head["median_us_per_atom"]))
+    out = {
+        "metric": "us/atom per E+F+stress call (FP32, 1 MI355X) at 5k atoms",
+        "value": round(head["us_per_atom"], 4),
+        "unit": "us/atom",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms_per_step"], 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic (random-init medium MACE, perturbed SrTiO3 supercell, seed 0)",
+        "config": {"workload": "medium: SrTiO3 10x10x10 (5000 atoms), MACE 128x0e+128x1o l_max 3 corr 3, "
+                               "r_cut 6.0 A + 0.5 A skin, graph retained",
+                   "atoms": n_atoms, "edges": head["edges"], "active_edges": head["active_edges"],
+                   "positions": "device-resident"},
+        "roofline": dict(head["roofline"], traffic=load_traffic(),
+                         traffic_source="profiles/hbm_traffic_medium_5k.md (FETCH_SIZE+WRITE_SIZE, copy-scaled)"),
+        "median_us_per_atom": round(head["median_us_per_atom"], 4),
+        "protocol": head["protocol"],
+        "host_positions_us_per_atom": round(head["host_us_per_atom"], 4),
+        "cold_call_ms": round(head["cold_ms"], 2),
+        "energy_eV": head["energy"],
+        "baseline_reference": {"value": 1.922, "hardware": "RTX 5090", "note": "published, trained OMAT-0 medium"},
+    }
+    if not args.no_calculator:
+        out["calculator_us_per_atom"] = calculator_protocol(model_path, system, skin)
+        note("calculator: %s" % out["calculator_us_per_atom"])
+    if not args.no_configs:
+        out["configs"] = {}
+        wide = systems.water_box(10000, seed=0)
+        out["configs"]["wide"] = summary(run_config(hip, random_model.cached_model("wide"), wide, skin, 3, 10),
+                                         "wide: 10,000 rigid waters (30,000 atoms), MACE 256x(0e+1o+2e) l_max 3 "
+                                         "corr 3, r_cut 5.0 A + 0.5 A skin")
+        note("wide: %s" % out["configs"]["wide"])
+        irregular = systems.irregular_box(20000, density=0.08, min_distance=1.8, seed=0)
+        out["configs"]["irregular"] = summary(run_config(hip, model_path, irregular, skin, 3, 10),
+                                              "irregular: 20,000 atoms uniform at 0.08/A^3, 1.8 A minimum "
+                                              "separation, 10 species, medium model")
+        note("irregular: %s" % out["configs"]["irregular"])
+    if args.capacity_steps > 0:
+        try:
+            out["capacity"] = capacity(132, args.capacity_steps, args.tile_receivers)
+        except Exception as exc:  # reported, never hidden
+            out["capacity"] = {"error": "%s: %s" % (type(exc).__name__, exc)}
+        note("capacity: %s" % out["capacity"])
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(model_path, skin)
+    print(json.dumps(out), flush=True)
+
+
+def summary(r, workload):
+    return {"workload": workload, "atoms": r["atoms"], "edges": r["edges"], "active_edges": r["active_edges"],
+            "median_us_per_atom": round(r["median_us_per_atom"], 4), "protocol": "3 warm-ups, median of 10",
+            "roofline": {k: r["roofline"][k] for k in ("kernel", "avg_launch_ms", "achieved", "frac",
+                                                         "executed_frac", "unit")}}
+
+
+def run_config(hip, model_path, system, skin, warmup, steps, timed_steps=False):
+    """One configuration on the device-resident positions path: cold call,
+    warm-ups, then `steps` calls with the dominant kernel timed by HIP
+    events on the evaluator stream."""
+    from symmetrix._native import check, lib
+    from symmetrix.mace_kokkos import MACEKokkosFloat
     ev = MACEKokkosFloat(model_path)
     lut = {z: i for i, z in enumerate(ev.atomic_numbers)}
     types = np.array([lut[int(z)] for z in system["numbers"]], np.int32)
@@ -233,17 +342,12 @@ def main():
     inv = np.linalg.inv(cell)
     vol = abs(float(np.linalg.det(cell)))
     n_atoms = len(types)
-
     t0 = time.perf_counter()
     g = ev._prepare_periodic_factorized_graph(types, system["positions"], cell, inv, ev.r_cut + skin)
     ev._compute_prepared_factorized_positions(g["generation"], system["positions"])
     cold_ms = (time.perf_counter() - t0) * 1e3
     gen = g["generation"]
-
-    hip = hip_lib()
     d_pos = device_copy_of(hip, np.ascontiguousarray(system["positions"], dtype=np.float64))
-
-    from symmetrix._native import check, lib
 
     def step():
         ev._compute_prepared_factorized_positions_device(gen, d_pos.value)
@@ -252,16 +356,15 @@ def main():
         check(lib.smx_total_energy_device(ev._h, None))
         ev.synchronize()
 
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         step()
-    # HIP events around the dominant kernel on the evaluator's own stream
     ev.set_kernel_timing(True)
     ev.set_kernel_timing_filter(DOMINANT)
     ev.reset_kernel_timing()
     per_call = []
     ev.synchronize()
     t_all = time.perf_counter()
-    for _ in range(args.steps):
+    for _ in range(steps):
         t0 = time.perf_counter()
         step()
         per_call.append(time.perf_counter() - t0)
@@ -269,66 +372,77 @@ def main():
     elapsed = time.perf_counter() - t_all
     timing = ev.kernel_timing()
     ev.set_kernel_timing(False)
-
-    ms_per_step = elapsed * 1e3 / args.steps
-    us_per_atom = elapsed * 1e6 / (args.steps * n_atoms)
-    median_us_per_atom = statistics.median(per_call) * 1e6 / n_atoms
-
-    # PCIe-inclusive call: positions from host memory, results copied back
-    t0 = time.perf_counter()
-    host_calls = 3
-    for _ in range(host_calls):
-        ev._compute_prepared_factorized_positions(gen, system["positions"])
-        e = ev.node_energies
-        ev._reduce_atom_forces(n_atoms, None, None, gen)
-        ev._reduce_stress(vol, None, gen)
-    host_us_per_atom = (time.perf_counter() - t0) * 1e6 / (host_calls * n_atoms)
-    energy = float(np.sum(e))
-
-    # roofline of the dominant kernel
+    out = {"atoms": n_atoms, "edges": int(g["num_edges"]), "cold_ms": cold_ms,
+           "ms_per_step": elapsed * 1e3 / steps, "us_per_atom": elapsed * 1e6 / (steps * n_atoms),
+           "median_us_per_atom": statistics.median(per_call) * 1e6 / n_atoms}
+    if timed_steps:
+        # the reference protocol on the same path: 3 warm-ups, median of 10
+        for _ in range(3):
+            step()
+        med = []
+        for _ in range(10):
+            t0 = time.perf_counter()
+            step()
+            med.append(time.perf_counter() - t0)
+        out["protocol"] = {"warmup": 3, "calls": 10, "median_us_per_atom": round(
+            statistics.median(med) * 1e6 / n_atoms, 4), "positions": "device-resident"}
+        # PCIe-inclusive call: positions from host memory, results copied back
+        for _ in range(3):
+            ev._compute_prepared_factorized_positions(gen, system["positions"])
+        host = []
+        for _ in range(10):
+            t0 = time.perf_counter()
+            ev._compute_prepared_factorized_positions(gen, system["positions"])
+            e = ev.node_energies
+            ev._reduce_atom_forces(n_atoms, None, None, gen)
+            ev._reduce_stress(vol, None, gen)
+            host.append(time.perf_counter() - t0)
+        out["host_us_per_atom"] = statistics.median(host) * 1e6 / n_atoms
+        out["energy"] = float(np.sum(e))
+    # roofline of the dominant kernel: algorithmic flops of the active edges
     P, T, rows, C = model_counts(model_path)
     rec = ev._stage("edge_records")
     E_active = int(np.count_nonzero(rec.reshape(g["num_edges"], -1)[:, 2].view(np.int32)))
     ms_r1, launches = timing.get(DOMINANT, (float("nan"), 0))
     avg_ms = ms_r1 / max(launches, 1)
-    flops = E_active * C * r1_reverse_flops_per_edge_channel(P, T, rows)
+    per_call = max(launches // max(steps, 1), 1)   # the wide shape runs one launch per source-component group
+    flops = E_active * C * r1_reverse_flops_per_edge_channel(P, T, rows) / per_call
     achieved = flops / (avg_ms * 1e-3) / 1e12
-    traffic = load_traffic()
-
-    out = {
-        "metric": "us/atom per E+F+stress call (FP32, 1 MI355X) at 5k atoms",
-        "value": round(us_per_atom, 4),
-        "unit": "us/atom",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 4),
-        "higher_is_better": False,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "fp32",
-        "data": "synthetic (random-init medium MACE, perturbed SrTiO3 supercell, seed 0)",
-        "config": {"workload": "medium: SrTiO3 10x10x10 (5000 atoms), MACE 128x0e+128x1o l_max 3 corr 3, "
-                               "r_cut 6.0 A + 0.5 A skin, graph retained",
-                   "atoms": n_atoms, "edges": int(g["num_edges"]), "active_edges": E_active,
-                   "positions": "device-resident"},
-        "roofline": {"bound": "mfma", "kernel": DOMINANT, "achieved": round(achieved, 3),
-                     "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_TFLOPS, 4),
-                     "traffic": traffic, "avg_launch_ms": round(avg_ms, 4),
-                     "flops_per_launch": flops,
-                     "compute": "FP32 VALU (edge-wise channel products; packed FP32 disabled, so 78.6 "
-                                "TFLOP/s is the attainable issue rate)",
-                     "traffic_source": "profiles/hbm_traffic_medium_5k.md (FETCH_SIZE+WRITE_SIZE, copy-scaled)"},
-        "median_us_per_atom": round(median_us_per_atom, 4),
-        "host_positions_us_per_atom": round(host_us_per_atom, 4),
-        "cold_call_ms": round(cold_ms, 2),
-        "energy_eV": energy,
-        "baseline_reference": {"value": 1.922, "hardware": "RTX 5090", "note": "published, trained OMAT-0 medium"},
-    }
-    if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(model_path, system, ev.r_cut, skin)
+    executed = R1_REVERSE_EXECUTED_FLOPS_PER_EDGE_CHANNEL.get((P, T, rows))
+    roof = {"bound": "valu", "kernel": DOMINANT, "achieved": round(achieved, 3), "peak": PEAK_FP32_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_TFLOPS, 4), "avg_launch_ms": round(avg_ms, 4),
+            "launches_per_call": per_call, "flops_per_launch": int(flops),
+            "compute": "FP32 VALU: edge-wise channel products, no MFMA; packed FP32 disabled, so 78.6 TFLOP/s "
+                       "is the attainable issue rate",
+            "executed_flops_per_launch": None, "executed_frac": None}
+    if executed:
+        ex = E_active * C * executed
+        roof["executed_flops_per_launch"] = ex
+        roof["executed_frac"] = round(ex / (avg_ms * 1e-3) / 1e12 / VALU_FP32_TFLOPS, 4)
+    out["roofline"] = roof
+    out["active_edges"] = E_active
     hip.hipFree(d_pos)
-    print(json.dumps(out), flush=True)
+    ev.close()
+    return out
+
+
+def calculator_protocol(model_path, system, skin):
+    """The reference's timing boundary: Symmetrix.calculate with host
+    positions in and energy, forces and stress out, graph retained (3
+    warm-ups, median of 10; benchmarks/mace_torch_comparison_protocol.md:65-90)."""
+    from symmetrix.calculator import Symmetrix
+    calc = Symmetrix(model_path, neighbor_skin=skin)
+    atoms = {"numbers": system["numbers"], "positions": system["positions"], "cell": system["cell"],
+             "pbc": [True, True, True]}
+    for _ in range(3):
+        calc.calculate(atoms, ["energy", "forces", "stress"])
+    times = []
+    for _ in range(10):
+        t0 = time.perf_counter()
+        calc.calculate(atoms, ["energy", "forces", "stress"])
+        times.append(time.perf_counter() - t0)
+    calc.evaluator.close()
+    return round(statistics.median(times) * 1e6 / len(system["numbers"]), 4)
 
 
 if __name__ == "__main__":
