@@ -97,6 +97,44 @@ __device__ __forceinline__ void stage_commit(const stage4 (&held)[stage_per(C, R
     }
 }
 
+// Two-part records: the forward part (RF floats per edge at srcF) and the
+// reverse part (RB floats per edge at srcB) of chunk c, laid out in LDS as
+// records of RF + RB floats.
+template <int C, int RF, int RB>
+__device__ __forceinline__ void stage_fetch2(stage4 (&held)[stage_per(C, RF + RB)], const stage4* __restrict__ srcF,
+                                             const stage4* __restrict__ srcB, int c, int edges) {
+    using RS = RecordStage<C, RF + RB>;
+    constexpr int F4 = RF / 4, B4 = RB / 4;
+    const int limit = min(kRecordChunk, edges - c * kRecordChunk) * RS::R4;
+#pragma unroll
+    for (int p = 0; p < RS::PER; ++p) {
+        const int idx = min(static_cast<int>(threadIdx.x) + p * C, limit - 1);
+        const int j = c * kRecordChunk + idx / RS::R4, q = idx % RS::R4;
+        held[p] = q < F4 ? srcF[static_cast<std::size_t>(j) * F4 + q] : srcB[static_cast<std::size_t>(j) * B4 + q - F4];
+    }
+}
+
+template <int C, int RF, int RB, class BODY>
+__device__ __forceinline__ void staged_records2(stage4* buf, const stage4* __restrict__ srcF,
+                                                const stage4* __restrict__ srcB, int edges, BODY&& body) {
+    constexpr int REC = RF + RB;
+    using RS = RecordStage<C, REC>;
+    const int chunks = (edges + kRecordChunk - 1) / kRecordChunk;
+    stage4 held[RS::PER];
+    if (chunks > 0) {
+        stage_fetch2<C, RF, RB>(held, srcF, srcB, 0, edges);
+        stage_commit<C, REC>(held, buf, 0, edges);
+    }
+    __syncthreads();
+    for (int c = 0; c < chunks; ++c) {
+        if (c + 1 < chunks) stage_fetch2<C, RF, RB>(held, srcF, srcB, c + 1, edges);
+        body(reinterpret_cast<const float*>(buf + (c & 1) * RS::SLOTS), c * kRecordChunk,
+             min(kRecordChunk, edges - c * kRecordChunk));
+        if (c + 1 < chunks) stage_commit<C, REC>(held, buf, c + 1, edges);
+        __syncthreads();
+    }
+}
+
 // Runs body(chunk_records, first_edge_offset, count) over the chunks of
 // `edges` records at src (records contiguous), staged through two LDS
 // buffers of SLOTS float4 each at buf.
@@ -122,19 +160,23 @@ __device__ __forceinline__ void staged_records(stage4* buf, const stage4* __rest
 // ---------------------------------------------------------------------------
 // Edge-input policies
 // ---------------------------------------------------------------------------
-// Packed record [x, interval, active, 0, Y[NY], dY/dX[NY], dY/dY[NY],
-// dY/dZ[NY], u[3], pad] per edge (tile-local index e - e0) and the Hermite
-// table [interval][function] as float4 (c0..c3).  With STAGED a receiver's
-// records are staged through LDS in chunks (staged_records; the fields then
-// sit in VGPRs), else the wave reads them with scalar loads (SGPRs).
-template <int C, int NY, int REC, bool STAGED>
+// Packed records in two parts per edge (tile-local index e - e0): forward
+// [x, interval, active, 0, Y[NY]] (RF floats) and reverse [dY/dX[NY],
+// dY/dY[NY], dY/dZ[NY], u[3], pad] (RB floats); the Hermite table
+// [interval][function] as float4 (c0..c3).  With STAGED a receiver's records
+// (both parts) are staged through LDS in chunks (staged_records2; the
+// fields then sit in VGPRs), else the wave reads the forward part with
+// scalar loads (SGPRs) -- the forward kernels need nothing else.
+template <int C, int NY, int RF, int RB, bool STAGED>
 struct RecordEdges {
-    const float* __restrict__ erec;
+    const float* __restrict__ erec;    // forward parts [ne][RF]
+    const float* __restrict__ erec_b;  // reverse parts [ne][RB]
     long long e0;
     const float4* __restrict__ coef;
     int functions;
 
-    static constexpr int kStageSlots = STAGED ? RecordStage<C, REC>::SLOTS : 1;
+    static constexpr int REC = STAGED ? RF + RB : RF;  // record stride where the kernel reads it
+    static constexpr int kStageSlots = STAGED ? RecordStage<C, RF + RB>::SLOTS : 1;
     // The unstaged records can be read one edge ahead (hold): the fields a
     // forward pass needs, wave-uniform, so they sit in SGPRs.
     static constexpr bool kHold = !STAGED;
@@ -144,7 +186,7 @@ struct RecordEdges {
         float y[NY];
     };
     __device__ __forceinline__ void hold(int e, Held& h) const {
-        const float* r = erec + static_cast<std::size_t>(e - e0) * REC;
+        const float* r = erec + static_cast<std::size_t>(e - e0) * RF;
         h.x = r[0];
         h.iv = __float_as_int(r[1]);
         h.active = __float_as_int(r[2]);
@@ -160,15 +202,19 @@ struct RecordEdges {
     template <class BODY>
     __device__ __forceinline__ void chunks(int ea, int eb, stage4* lds, BODY&& body) const {
         if constexpr (STAGED) {
-            const stage4* src = reinterpret_cast<const stage4*>(erec) + static_cast<std::size_t>(ea - e0) * (REC / 4);
-            staged_records<C, REC>(lds, src, eb - ea, [&](const float* chunk, int first, int n)
-                                                          __attribute__((always_inline)) { body(ea + first, n, chunk); });
+            const std::size_t first = static_cast<std::size_t>(ea - e0);
+            const stage4* srcF = reinterpret_cast<const stage4*>(erec) + first * (RF / 4);
+            const stage4* srcB = reinterpret_cast<const stage4*>(erec_b) + first * (RB / 4);
+            staged_records2<C, RF, RB>(lds, srcF, srcB, eb - ea, [&](const float* chunk, int f, int n)
+                                                                     __attribute__((always_inline)) {
+                body(ea + f, n, chunk);
+            });
         } else {
             for (int c0 = ea; c0 < eb; c0 += kRecordChunk) body(c0, min(kRecordChunk, eb - c0), nullptr);
         }
     }
     __device__ __forceinline__ bool open_at(int e, int /*receiver*/, const float* chunk, int j, Point& p) const {
-        p.rec = STAGED ? chunk + j * REC : erec + static_cast<std::size_t>(e - e0) * REC;
+        p.rec = STAGED ? chunk + j * REC : erec + static_cast<std::size_t>(e - e0) * RF;
         if (!edge_active(p.rec)) return false;
         p.x = p.rec[0];
         p.xx = p.x * p.x;
@@ -179,8 +225,15 @@ struct RecordEdges {
         return true;
     }
     __device__ __forceinline__ float Y(const Point& p, int lm) const { return p.rec[4 + lm]; }
-    __device__ __forceinline__ float dY(const Point& p, int c, int lm) const { return p.rec[4 + NY + c * NY + lm]; }
-    __device__ __forceinline__ float u(const Point& p, int c) const { return p.rec[4 + 4 * NY + c]; }
+    // reverse fields: staged records only
+    __device__ __forceinline__ float dY(const Point& p, int c, int lm) const {
+        static_assert(STAGED, "the reverse fields are read from staged records");
+        return p.rec[RF + c * NY + lm];
+    }
+    __device__ __forceinline__ float u(const Point& p, int c) const {
+        static_assert(STAGED, "the reverse fields are read from staged records");
+        return p.rec[RF + 3 * NY + c];
+    }
     __device__ __forceinline__ float value(const Point& p, int f) const {
         return spline_value(p.cf[f], p.x, p.xx, p.xxx);
     }

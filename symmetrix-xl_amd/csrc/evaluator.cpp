@@ -677,6 +677,7 @@ struct Evaluator {
         const std::size_t te = std::max<std::int64_t>(max_tile_ne, 1);
         auto f = [&](DevBuf& b, std::size_t count) { return static_cast<float*>(b.ensure(count * sizeof(float))); };
         ws.erec = f(w_erec, te * ks->record_floats());
+        ws.erec_b = ws.erec + te * ks->record_forward_floats();  // reverse parts after the forward parts
         ws.Phi0 = f(w_Phi0, tn * NY * C);
         ws.A0 = f(w_A0, tn * NY * C);
         ws.M0 = f(w_M0, tn * NH * C);
@@ -926,7 +927,7 @@ struct Evaluator {
         }
         if (tm) tm->begin("edge_records", stream);
         ks->edge_geometry(dm, t.ne, tile_xyz(t), tile_r(t), hm.agnesi ? d_edge_pair.as<int>() + t.e0 : nullptr,
-                          ws.erec, stream);
+                          ws.erec, ws.erec_b, stream);
         if (tm) tm->end("edge_records", stream);
         (void)positions;
     }
@@ -1400,7 +1401,8 @@ struct Evaluator {
         else if (name == "M0_adj") src = ws.M0_adj, count = n * NH * C;
         else if (name == "A0_adj") src = ws.A0_adj, count = n * NY * C;
         else if (name == "direct") src = ws.direct, count = static_cast<std::int64_t>(N) * C;
-        else if (name == "edge_records") src = ws.erec, count = (tiled ? max_tile_ne : E) * ks->record_floats();
+        else if (name == "edge_records")  // the forward parts [edge][x, interval, active, 0, Y...]
+            src = ws.erec, count = (tiled ? max_tile_ne : E) * ks->record_forward_floats();
         else throw std::invalid_argument("unknown stage '" + name + "'");
         if (out && capacity >= count && count > 0) {
             SMX_HIP(hipMemcpyAsync(out, src, count * sizeof(float), hipMemcpyDeviceToHost, stream));

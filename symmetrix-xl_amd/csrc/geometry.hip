@@ -401,9 +401,10 @@ __global__ __launch_bounds__(kRecordThreads) void k_edge_records(long long E, co
                                                                  const double* __restrict__ r, double r_cut,
                                                                  float x0, float h, int intervals,
                                                                  const int* __restrict__ edge_pair,
-                                                                 float* __restrict__ erec) {
+                                                                 float* __restrict__ erec,
+                                                                 float* __restrict__ erec_b) {
     using S = Shape<LMAX, 0>;
-    static_assert(S::REC % 4 == 0, "records are whole float4s");
+    static_assert(S::REC_F % 4 == 0 && S::REC_B % 4 == 0, "record parts are whole float4s");
     __shared__ float4 stage[kRecordThreads * S::REC / 4];
     const long long base = static_cast<long long>(blockIdx.x) * kRecordThreads;
     const long long e = base + threadIdx.x;
@@ -439,9 +440,13 @@ __global__ __launch_bounds__(kRecordThreads) void k_edge_records(long long E, co
         }
     }
     __syncthreads();
+    // the two parts to their arrays, coalesced float4 rows
+    constexpr int R4 = S::REC / 4, F4 = S::REC_F / 4, B4 = S::REC_B / 4;
     const long long count = E - base < kRecordThreads ? E - base : kRecordThreads;
-    float4* dst = reinterpret_cast<float4*>(erec + base * S::REC);
-    for (int q = threadIdx.x; q < count * (S::REC / 4); q += kRecordThreads) dst[q] = stage[q];
+    float4* dst = reinterpret_cast<float4*>(erec + base * S::REC_F);
+    for (int q = threadIdx.x; q < count * F4; q += kRecordThreads) dst[q] = stage[(q / F4) * R4 + q % F4];
+    float4* dstb = reinterpret_cast<float4*>(erec_b + base * S::REC_B);
+    for (int q = threadIdx.x; q < count * B4; q += kRecordThreads) dstb[q] = stage[(q / B4) * R4 + F4 + q % B4];
 }
 
 // Symmetric pair index over the active types (a <= b: a(2n-a-1)/2 + b,
@@ -689,14 +694,14 @@ int build_touched_sources(int N, std::int64_t e0, std::int64_t ne, const int* so
 }
 
 void geometry_records(int l_max, std::int64_t E, const double* xyz, const double* r, double r_cut, float x0, float h,
-                      int intervals, const int* edge_pair, float* erec, hipStream_t s) {
+                      int intervals, const int* edge_pair, float* erec, float* erec_b, hipStream_t s) {
     if (E == 0) return;
     if (l_max == 3)
         k_edge_records<3><<<blocks_for(E, kRecordThreads), kRecordThreads, 0, s>>>(E, xyz, r, r_cut, x0, h, intervals,
-                                                                                edge_pair, erec);
+                                                                                edge_pair, erec, erec_b);
     else if (l_max == 2)
         k_edge_records<2><<<blocks_for(E, kRecordThreads), kRecordThreads, 0, s>>>(E, xyz, r, r_cut, x0, h, intervals,
-                                                                                edge_pair, erec);
+                                                                                edge_pair, erec, erec_b);
     else
         throw std::invalid_argument("edge records are compiled for l_max 2 and 3");
     SMX_LAUNCH_CHECK("edge_records");

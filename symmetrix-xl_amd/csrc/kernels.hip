@@ -52,6 +52,7 @@ __device__ __forceinline__ double block_sum(double v, double* sbuf) {
 
 // ---------------------------------------------------------------------------
 // Layer 1: Phi0[i,lm,k] = sum_j R0_{l,k}(r_ij) Y_lm(ij) H0[type_j,k]
+// The forward parts of the receiver's records are staged through LDS.
 // ---------------------------------------------------------------------------
 template <int C, int LMAX>
 __global__ __launch_bounds__(C) void k_r0_forward(int r0, long long e0, const int* __restrict__ offsets,
@@ -67,12 +68,12 @@ __global__ __launch_bounds__(C) void k_r0_forward(int r0, long long e0, const in
 #pragma unroll
     for (int v = 0; v < NY; ++v) acc[v] = 0.0f;
     const int ea = offsets[i], eb = offsets[i + 1];
-    __shared__ stage4 stage_buf[2 * RecordStage<C, S::REC>::SLOTS];
-    const stage4* src = reinterpret_cast<const stage4*>(erec) + static_cast<std::size_t>(ea - e0) * (S::REC / 4);
-    staged_records<C, S::REC>(stage_buf, src, eb - ea, [&](const float* chunk, int first, int n)
-                                                           __attribute__((always_inline)) {
+    __shared__ stage4 stage_buf[2 * RecordStage<C, S::REC_F>::SLOTS];
+    const stage4* src = reinterpret_cast<const stage4*>(erec) + static_cast<std::size_t>(ea - e0) * (S::REC_F / 4);
+    staged_records<C, S::REC_F>(stage_buf, src, eb - ea, [&](const float* chunk, int first, int n)
+                                                             __attribute__((always_inline)) {
         for (int j = 0; j < n; ++j) {
-            const float* rec = chunk + j * S::REC;
+            const float* rec = chunk + j * S::REC_F;
             if (!edge_active(rec)) continue;
             const int e = ea + first + j;
             const float x = rec[0];
@@ -98,6 +99,7 @@ __global__ __launch_bounds__(C) void k_r0_forward(int r0, long long e0, const in
 template <int C, int LMAX, bool ACCUMULATE>
 __global__ __launch_bounds__(C) void k_r0_reverse(int r0, long long e0, const int* __restrict__ offsets,
                                                   const int* __restrict__ neigh_types, const float* __restrict__ erec,
+                                                  const float* __restrict__ erec_b,
                                                   const float4* __restrict__ R0c, const float* __restrict__ H0,
                                                   const float* __restrict__ Phi0_adj, double* __restrict__ node_forces) {
     using S = Shape<LMAX, 0>;
@@ -112,9 +114,10 @@ __global__ __launch_bounds__(C) void k_r0_reverse(int r0, long long e0, const in
 #pragma unroll
     for (int v = 0; v < NY; ++v) padj[v] = Phi0_adj[(static_cast<std::size_t>(li) * NY + v) * C + k];
     const int ea = offsets[i], eb = offsets[i + 1];
-    const stage4* src = reinterpret_cast<const stage4*>(erec) + static_cast<std::size_t>(ea - e0) * (S::REC / 4);
-    staged_records<C, S::REC>(stage_buf, src, eb - ea, [&](const float* chunk, int first, int n)
-                                                           __attribute__((always_inline)) {
+    const stage4* srcF = reinterpret_cast<const stage4*>(erec) + static_cast<std::size_t>(ea - e0) * (S::REC_F / 4);
+    const stage4* srcB = reinterpret_cast<const stage4*>(erec_b) + static_cast<std::size_t>(ea - e0) * (S::REC_B / 4);
+    staged_records2<C, S::REC_F, S::REC_B>(stage_buf, srcF, srcB, eb - ea, [&](const float* chunk, int first, int n)
+                                                                               __attribute__((always_inline)) {
         for (int j = 0; j < n; ++j) {
             const float* rec = chunk + j * S::REC;
             if (!edge_active(rec)) {
@@ -845,20 +848,21 @@ struct KernelSetImpl final : KernelSet {
     static constexpr bool kM0Unrolled = !std::is_same_v<M0TAB, void>;
     // R1 forward reads records with scalar loads (its VGPRs hold the 88+
     // coupling rows); the R1 reverse stages them through LDS
-    using Records = RecordEdges<C, S::NY, S::REC, false>;
-    using StagedRecords = RecordEdges<C, S::NY, S::REC, true>;
+    using Records = RecordEdges<C, S::NY, S::REC_F, S::REC_B, false>;
+    using StagedRecords = RecordEdges<C, S::NY, S::REC_F, S::REC_B, true>;
     using Groups = SourceGroups<LMAX, LMAXH>;
     static constexpr int kGroups = static_cast<int>(Groups::masks.size());
     int record_floats() const override { return S::REC; }
+    int record_forward_floats() const override { return S::REC_F; }
     template <class R = Records>
     static R records(const DeviceModel& m, const TileView& t, const Workspace& w) {
-        return R{w.erec, t.e0, m.R1c, S::P * C};
+        return R{w.erec, w.erec_b, t.e0, m.R1c, S::P * C};
     }
     const char* polynomial_mode() const override { return kM0Unrolled ? "unrolled" : "table"; }
 
     void edge_geometry(const DeviceModel& m, std::int64_t E, const double* xyz, const double* r,
-                       const int* edge_pair, float* erec, hipStream_t s) const override {
-        geometry_records(LMAX, E, xyz, r, m.r_cut, m.x0, m.h, m.intervals, edge_pair, erec, s);
+                       const int* edge_pair, float* erec, float* erec_b, hipStream_t s) const override {
+        geometry_records(LMAX, E, xyz, r, m.r_cut, m.x0, m.h, m.intervals, edge_pair, erec, erec_b, s);
     }
 
     void layer1_forward(const DeviceModel& m, const DeviceGraph& g, const TileView& t, const Workspace& w,
@@ -1000,11 +1004,11 @@ struct KernelSetImpl final : KernelSet {
         {
             TimerScope ts(tm, "r0_reverse", s);
             if (accumulate_forces)
-                k_r0_reverse<C, LMAX, true><<<t.nr, C, 0, s>>>(t.r0, t.e0, g.offsets, g.neigh_types, w.erec, m.R0c,
-                                                               m.H0, w.Phi0_adj, w.node_forces);
+                k_r0_reverse<C, LMAX, true><<<t.nr, C, 0, s>>>(t.r0, t.e0, g.offsets, g.neigh_types, w.erec,
+                                                               w.erec_b, m.R0c, m.H0, w.Phi0_adj, w.node_forces);
             else
-                k_r0_reverse<C, LMAX, false><<<t.nr, C, 0, s>>>(t.r0, t.e0, g.offsets, g.neigh_types, w.erec, m.R0c,
-                                                                m.H0, w.Phi0_adj, w.node_forces);
+                k_r0_reverse<C, LMAX, false><<<t.nr, C, 0, s>>>(t.r0, t.e0, g.offsets, g.neigh_types, w.erec,
+                                                                w.erec_b, m.R0c, m.H0, w.Phi0_adj, w.node_forces);
             SMX_LAUNCH_CHECK("r0_reverse");
         }
         if (m.A0_scaled) {

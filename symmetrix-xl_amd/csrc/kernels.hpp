@@ -133,7 +133,8 @@ struct TileView {
 // graph-wide arrays by the global index.
 struct Workspace {
     // tile-local
-    float* erec = nullptr;      // [ne][REC] per-edge records
+    float* erec = nullptr;      // [ne][REC_F] forward parts of the per-edge records
+    float* erec_b = nullptr;    // [ne][REC_B] reverse parts
     float* Phi0 = nullptr;      // [nr][NY][C]
     float* A0 = nullptr;        // [nr][NY][C]
     float* M0 = nullptr;        // [nr][NH][C]
@@ -173,13 +174,14 @@ struct LaunchTimer {
 // exchanged (H1 after layer 1, H1 adjoint after the layer-2 reverse).
 struct KernelSet {
     virtual ~KernelSet() = default;
-    virtual int record_floats() const = 0;
+    virtual int record_floats() const = 0;          // both parts of a record
+    virtual int record_forward_floats() const = 0;  // its forward part
     // "unrolled" when the product-basis kernels use compiled term tables
     virtual const char* polynomial_mode() const = 0;
     // per-edge records of a tile from its FP64 xyz and r
     // (edge_pair, indexed like xyz, selects each edge's table; null: one table)
     virtual void edge_geometry(const DeviceModel& m, std::int64_t ne, const double* xyz, const double* r,
-                               const int* edge_pair, float* erec, hipStream_t s) const = 0;
+                               const int* edge_pair, float* erec, float* erec_b, hipStream_t s) const = 0;
     // R0 forward + A0 linear; with through_h1 also M0, the scalar capture and
     // H1 rows r0.. of the graph-wide H1
     virtual void layer1_forward(const DeviceModel& m, const DeviceGraph& g, const TileView& t, const Workspace& w,
@@ -219,7 +221,7 @@ bool kernel_paths(int l_max, int L_max, std::vector<int>& le, std::vector<int>& 
 // Per-edge records (spline point, Y, dY, direction) from FP64 xyz and r.
 // (record field 1 is the table row: pair * intervals + interval)
 void geometry_records(int l_max, std::int64_t E, const double* xyz, const double* r, double r_cut, float x0, float h,
-                      int intervals, const int* edge_pair, float* erec, hipStream_t s);
+                      int intervals, const int* edge_pair, float* erec, float* erec_b, hipStream_t s);
 // edge_pair[e] = symmetric pair of the active types of receiver and source
 void launch_edge_pairs(std::int64_t E, const int* receivers, const int* node_types, const int* neigh_types,
                        const int* type_to_active, int active_types, int* edge_pair, int* bad, hipStream_t s);

@@ -111,12 +111,18 @@ struct Shape {
         return lme_base[paths[p].lo] + mo * num_e[paths[p].lo] + e_index[p];
     }
 
-    // per-edge record: [x, interval, active, pad, Y[NY], dY/dx[NY], dY/dy[NY],
-    // dY/dz[NY], u[3]] padded to a multiple of four floats
+    // per-edge records in two arrays, each padded to whole float4s: the
+    // forward part [x, interval, active, pad, Y[NY]] that the forward edge
+    // kernels read, and the reverse part [dY/dx[NY], dY/dy[NY], dY/dz[NY],
+    // u[3]] that only the reverse kernels add.  A reverse kernel stages a
+    // record in LDS as the two parts back to back (REC floats), so the
+    // offsets below index that concatenation.
+    static constexpr int REC_F = (4 + NY + 3) / 4 * 4;
+    static constexpr int REC_B = (3 * NY + 3 + 3) / 4 * 4;
+    static constexpr int REC = REC_F + REC_B;
     static constexpr int REC_Y = 4;
-    static constexpr int REC_DY = 4 + NY;
-    static constexpr int REC_U = 4 + 4 * NY;
-    static constexpr int REC = ((4 + 4 * NY + 3) + 3) / 4 * 4;
+    static constexpr int REC_DY = REC_F;
+    static constexpr int REC_U = REC_F + 3 * NY;
 };
 
 }  // namespace smx
