@@ -154,11 +154,36 @@ __global__ void k_bin_fill(int N, const int* __restrict__ abin, int* __restrict_
     batoms[slot] = a;
 }
 
-// ascending atom index within each bin (insertion sort, neighbor_graph_kokkos.cpp:233-249)
-__global__ void k_sort_segments(int nseg, const long long* __restrict__ off, int* __restrict__ items) {
-    const int b = blockIdx.x * blockDim.x + threadIdx.x;
-    if (b >= nseg) return;
-    const long long lo = off[b], hi = off[b + 1];
+// Ascending order within each segment (the bins' atom lists,
+// neighbor_graph_kokkos.cpp:233-249, and each source's edge list).  One
+// wave per segment: the segment is copied to LDS, each item's place is the
+// number of smaller items (the items of a segment are distinct), and the
+// items are written back in place.  Segments longer than the LDS copy fall
+// back to one lane's insertion sort.
+constexpr int kSortLds = 2048;
+
+__global__ __launch_bounds__(kWave) void k_sort_segments(int nseg, const long long* __restrict__ off,
+                                                         int* __restrict__ items) {
+    __shared__ int buf[kSortLds];
+    const int seg = blockIdx.x;
+    if (seg >= nseg) return;
+    const long long lo = off[seg], hi = off[seg + 1];
+    const long long n = hi - lo;
+    if (n <= 1) return;
+    const int lane = threadIdx.x;
+    if (n <= kSortLds) {
+        const int m = static_cast<int>(n);
+        for (int t = lane; t < m; t += kWave) buf[t] = items[lo + t];
+        __syncthreads();
+        for (int t = lane; t < m; t += kWave) {
+            const int v = buf[t];
+            int rank = 0;
+            for (int u = 0; u < m; ++u) rank += buf[u] < v ? 1 : 0;
+            items[lo + rank] = v;
+        }
+        return;
+    }
+    if (lane != 0) return;
     for (long long p = lo + 1; p < hi; ++p) {
         const int v = items[p];
         long long q = p - 1;
@@ -170,57 +195,95 @@ __global__ void k_sort_segments(int nseg, const long long* __restrict__ off, int
     }
 }
 
+// inclusive prefix sum over the wave's lanes
+__device__ __forceinline__ int wave_inclusive_sum(int x) {
+    const int lane = threadIdx.x % kWave;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+        const int t = __shfl_up(x, d, kWave);
+        if (lane >= d) x += t;
+    }
+    return x;
+}
+
+// One wave per receiver, lanes over the stencil bins in the reference's
+// dz -> dy -> dx order (neighbor_graph_kokkos.cpp:258-332): each lane scans
+// its bin's ascending atom list (d^2 <= rc^2 accepted, the receiver itself at
+// zero image excluded); a prefix sum of the lanes' counts gives each lane's
+// first output slot, so the edges come out in exactly the sequential order.
+// FILL = false counts, FILL = true writes.
+constexpr int kVisitWaves = 4;
+
 template <bool FILL>
-__global__ void k_neighbor_visit(int N, Mat3 cell, BinGrid g, double cut2, const double* __restrict__ wfrac,
-                                 const double* __restrict__ wpos, const int* __restrict__ wrap,
-                                 const int* __restrict__ abin, const long long* __restrict__ boff,
-                                 const int* __restrict__ batoms, int* __restrict__ counts,
-                                 const long long* __restrict__ eoff, int* __restrict__ sources,
-                                 std::uint32_t* __restrict__ images, int* __restrict__ shifts,
-                                 double* __restrict__ fxyz) {
-    const int rcv = blockIdx.x * blockDim.x + threadIdx.x;
-    if (rcv >= N) return;
+__global__ __launch_bounds__(kVisitWaves* kWave) void k_neighbor_visit(
+    int N, Mat3 cell, BinGrid g, double cut2, const double* __restrict__ wfrac, const double* __restrict__ wpos,
+    const int* __restrict__ wrap, const int* __restrict__ abin, const long long* __restrict__ boff,
+    const int* __restrict__ batoms, int* __restrict__ counts, const long long* __restrict__ eoff,
+    int* __restrict__ sources, std::uint32_t* __restrict__ images, int* __restrict__ shifts,
+    double* __restrict__ fxyz) {
+    const int rcv = blockIdx.x * kVisitWaves + static_cast<int>(threadIdx.x) / kWave;
+    const int lane = threadIdx.x % kWave;
+    if (rcv >= N) return;  // the whole wave
     const int rb = abin[rcv];
     const int rx = rb % g.bins[0], ry = (rb / g.bins[0]) % g.bins[1], rz = rb / (g.bins[0] * g.bins[1]);
-    long long e = FILL ? eoff[rcv] : 0;
-    int local = 0;
-    for (int dz = -g.reach[2]; dz <= g.reach[2]; ++dz) {
-        const int raw_z = rz + dz, sz = floor_div(raw_z, g.bins[2]), bz = raw_z - sz * g.bins[2];
-        for (int dy = -g.reach[1]; dy <= g.reach[1]; ++dy) {
-            const int raw_y = ry + dy, sy = floor_div(raw_y, g.bins[1]), by = raw_y - sy * g.bins[1];
-            for (int dx = -g.reach[0]; dx <= g.reach[0]; ++dx) {
-                const int raw_x = rx + dx, sx = floor_div(raw_x, g.bins[0]), bx = raw_x - sx * g.bins[0];
-                const int sb = (bz * g.bins[1] + by) * g.bins[0] + bx;
-                const int image[3] = {sx, sy, sz};
-                for (long long idx = boff[sb]; idx < boff[sb + 1]; ++idx) {
-                    const int src = batoms[idx];
-                    if (src == rcv && sx == 0 && sy == 0 && sz == 0) continue;
-                    double d2 = 0.0;
-                    for (int c = 0; c < 3; ++c) {
-                        double d = wpos[3 * src + c] - wpos[3 * rcv + c];
-                        for (int ax = 0; ax < 3; ++ax) d += image[ax] * cell.v[3 * ax + c];
-                        d2 += d * d;
+    const int nx = 2 * g.reach[0] + 1, ny = 2 * g.reach[1] + 1, nz = 2 * g.reach[2] + 1;
+    const int nst = nx * ny * nz;
+    const double p0 = wpos[3 * rcv], p1 = wpos[3 * rcv + 1], p2 = wpos[3 * rcv + 2];
+    long long done = FILL ? eoff[rcv] : 0;
+    for (int s0 = 0; s0 < nst; s0 += kWave) {
+        const int st = s0 + lane;
+        int image[3] = {0, 0, 0};
+        long long b0 = 0, b1 = 0;
+        if (st < nst) {
+            const int ix = st % nx, iy = (st / nx) % ny, iz = st / (nx * ny);
+            const int raw_z = rz + iz - g.reach[2], sz = floor_div(raw_z, g.bins[2]), bz = raw_z - sz * g.bins[2];
+            const int raw_y = ry + iy - g.reach[1], sy = floor_div(raw_y, g.bins[1]), by = raw_y - sy * g.bins[1];
+            const int raw_x = rx + ix - g.reach[0], sx = floor_div(raw_x, g.bins[0]), bx = raw_x - sx * g.bins[0];
+            const int sb = (bz * g.bins[1] + by) * g.bins[0] + bx;
+            image[0] = sx;
+            image[1] = sy;
+            image[2] = sz;
+            b0 = boff[sb];
+            b1 = boff[sb + 1];
+        }
+        const bool zero_image = image[0] == 0 && image[1] == 0 && image[2] == 0;
+        // image displacement of the bin (the same sums the sequential scan forms per pair)
+        auto accept = [&](int src) __attribute__((always_inline)) {
+            if (src == rcv && zero_image) return false;
+            double d2 = 0.0;
+            const double rp[3] = {p0, p1, p2};
+            for (int c = 0; c < 3; ++c) {
+                double d = wpos[3 * src + c] - rp[c];
+                for (int ax = 0; ax < 3; ++ax) d += image[ax] * cell.v[3 * ax + c];
+                d2 += d * d;
+            }
+            return !(d2 > cut2);
+        };
+        int cnt = 0;
+        for (long long idx = b0; idx < b1; ++idx) cnt += accept(batoms[idx]) ? 1 : 0;
+        const int incl = wave_inclusive_sum(cnt);
+        const int wave_total = __shfl(incl, kWave - 1, kWave);
+        if (FILL && cnt > 0) {
+            long long e = done + (incl - cnt);
+            for (long long idx = b0; idx < b1; ++idx) {
+                const int src = batoms[idx];
+                if (!accept(src)) continue;
+                sources[e] = src;
+                images[e] = (static_cast<std::uint32_t>(image[0]) & 0xffu) |
+                            ((static_cast<std::uint32_t>(image[1]) & 0xffu) << 8) |
+                            ((static_cast<std::uint32_t>(image[2]) & 0xffu) << 16);
+                if (shifts) {
+                    for (int ax = 0; ax < 3; ++ax) {
+                        shifts[3 * e + ax] = image[ax] - wrap[3 * src + ax] + wrap[3 * rcv + ax];
+                        fxyz[3 * e + ax] = wfrac[3 * src + ax] - wfrac[3 * rcv + ax] + image[ax];
                     }
-                    if (d2 > cut2) continue;
-                    if (FILL) {
-                        sources[e] = src;
-                        images[e] = (static_cast<std::uint32_t>(image[0]) & 0xffu) |
-                                    ((static_cast<std::uint32_t>(image[1]) & 0xffu) << 8) |
-                                    ((static_cast<std::uint32_t>(image[2]) & 0xffu) << 16);
-                        if (shifts) {
-                            for (int ax = 0; ax < 3; ++ax) {
-                                shifts[3 * e + ax] = image[ax] - wrap[3 * src + ax] + wrap[3 * rcv + ax];
-                                fxyz[3 * e + ax] = wfrac[3 * src + ax] - wfrac[3 * rcv + ax] + image[ax];
-                            }
-                        }
-                        ++e;
-                    }
-                    ++local;
                 }
+                ++e;
             }
         }
+        done += wave_total;
     }
-    if (!FILL) counts[rcv] = local;
+    if (!FILL && lane == 0) counts[rcv] = static_cast<int>(done);
 }
 
 // ---------------------------------------------------------------------------
@@ -562,11 +625,13 @@ void build_neighbor_list(int N, const double* positions_host, const double* cell
             k_bin_fill<<<ab, 256, 0, s>>>(N, abin, cursor, batoms);
             SMX_LAUNCH_CHECK("neighbor_bin_fill");
         }
-        k_sort_segments<<<blocks_for(nb, 256), 256, 0, s>>>(nb, boff, batoms);
+        k_sort_segments<<<nb, kWave, 0, s>>>(nb, boff, batoms);
         SMX_LAUNCH_CHECK("neighbor_sort_bins");
+        const unsigned vb = blocks_for(std::max(N, 1), kVisitWaves);
         if (N > 0) {
-            k_neighbor_visit<false><<<blocks_for(N, 128), 128, 0, s>>>(N, cell, g, cut2, wfrac, wpos, wrap, abin, boff, batoms, counts,
-                                                       nullptr, nullptr, nullptr, nullptr, nullptr);
+            k_neighbor_visit<false><<<vb, kVisitWaves * kWave, 0, s>>>(N, cell, g, cut2, wfrac, wpos, wrap, abin, boff,
+                                                                       batoms, counts, nullptr, nullptr, nullptr,
+                                                                       nullptr, nullptr);
             SMX_LAUNCH_CHECK("neighbor_count");
         }
         const long long E = device_exclusive_scan(counts, eoff, N, s);
@@ -584,9 +649,9 @@ void build_neighbor_list(int N, const double* positions_host, const double* cell
         k_copy_i64_i32_plus<<<blocks_for(N + 1, 256), 256, 0, s>>>(eoff, out.offsets, N);
         SMX_LAUNCH_CHECK("neighbor_offsets");
         if (N > 0 && E > 0) {
-            k_neighbor_visit<true><<<blocks_for(N, 128), 128, 0, s>>>(N, cell, g, cut2, wfrac, wpos, wrap, abin, boff, batoms, nullptr,
-                                                      eoff, out.sources, out.images, out.shifts,
-                                                      out.fractional_xyz);
+            k_neighbor_visit<true><<<vb, kVisitWaves * kWave, 0, s>>>(N, cell, g, cut2, wfrac, wpos, wrap, abin, boff,
+                                                                      batoms, nullptr, eoff, out.sources, out.images,
+                                                                      out.shifts, out.fractional_xyz);
             SMX_LAUNCH_CHECK("neighbor_fill");
         }
         SMX_HIP(hipStreamSynchronize(s));
@@ -616,7 +681,7 @@ void launch_transpose(int K, std::int64_t E, const int* keys, int* koff, int* ke
             k_fill_sources<<<blocks_for(E, 256), 256, 0, s>>>(E, keys, scratch_counts, kedges);
             SMX_LAUNCH_CHECK("transpose_fill");
         }
-        k_sort_segments<<<blocks_for(K, 256), 256, 0, s>>>(K, off64, kedges);
+        k_sort_segments<<<K, kWave, 0, s>>>(K, off64, kedges);
         SMX_LAUNCH_CHECK("transpose_sort");
         SMX_HIP(hipStreamSynchronize(s));
     } catch (...) {
