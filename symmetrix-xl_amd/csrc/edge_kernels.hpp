@@ -435,6 +435,10 @@ struct RowGroup {
 template <int LMAX, int LMAXH>
 struct SourceGroups;
 template <int LMAX>
+struct SourceGroups<LMAX, 0> {
+    static constexpr std::array<unsigned, 1> masks{0x1u};
+};
+template <int LMAX>
 struct SourceGroups<LMAX, 1> {
     static constexpr std::array<unsigned, 1> masks{0xfu};
 };

@@ -1081,6 +1081,15 @@ std::unique_ptr<KernelSet> make_kernel_set(int C, int l_max, int L_max, const st
     if (C == 128 && l_max == 3 && L_max == 1)
         return corr == 3 ? pick_polynomials<128, 3, 1, 3>(m0_terms, m0_offsets, m1_terms)
                          : std::make_unique<KernelSetImpl<128, 3, 1, void, void>>();
+    // the shapes of the MACE-OMAT-0 small (128x0e, l_max 3) and MP-0b2 large
+    // (128x0e+128x1o+128x2e) checkpoints
+    // (symmetrix/test/data/execution_contracts/jit_r1_mace_{omat0_small,mp0b2_large}_contract.json)
+    if (C == 128 && l_max == 3 && L_max == 0)
+        return corr == 3 ? pick_polynomials<128, 3, 0, 3>(m0_terms, m0_offsets, m1_terms)
+                         : std::make_unique<KernelSetImpl<128, 3, 0, void, void>>();
+    if (C == 128 && l_max == 3 && L_max == 2)
+        return corr == 3 ? pick_polynomials<128, 3, 2, 3>(m0_terms, m0_offsets, m1_terms)
+                         : std::make_unique<KernelSetImpl<128, 3, 2, void, void>>();
     return nullptr;
 }
 
@@ -1091,6 +1100,10 @@ bool kernel_paths(int l_max, int L_max, std::vector<int>& le, std::vector<int>& 
     }
     if (l_max == 3 && L_max == 1) {
         paths_of<3, 1>(le, ls, lo);
+        return true;
+    }
+    if (l_max == 3 && L_max == 0) {
+        paths_of<3, 0>(le, ls, lo);
         return true;
     }
     if (l_max == 3 && L_max == 2) {

@@ -16,6 +16,10 @@ SPECIES = {
     "compact_medium_m0": {38: 22, 22: 22, 8: 8},
     "compact_medium_linear": {38: 38, 22: 22, 8: 8},
     "compact_c4": {38: 1, 22: 8, 8: 8},
+    "compact_omat0_small": {38: 38, 22: 22, 8: 8},
+    "compact_mp0b2_large": {38: 38, 22: 22, 8: 8},
+    "compact_off23_small": {38: 38, 22: 22, 8: 8},
+    "compact_off23_large": {38: 38, 22: 22, 8: 8},
 }
 
 

@@ -17,7 +17,12 @@ Fixtures (tests/golden/compact_*.json.gz):
   writer then gives each M0 output one linear monomial), atomic numbers O, Ti
   and Sr, so the SrTiO3 systems run on it;
 * compact_c4: the reference's four-channel fixture contract
-  (jit_r1_fixture_c4_e3_l0_contract.json: l_max 0, L_max 0).
+  (jit_r1_fixture_c4_e3_l0_contract.json: l_max 0, L_max 0);
+* compact_omat0_small, compact_mp0b2_large, compact_off23_small,
+  compact_off23_large: the R1 contracts of the MACE-OMAT-0 small (128x0e
+  hidden, 4 paths), MP-0b2 large (128x0e+128x1o+128x2e, 17 paths),
+  MACE-OFF23 small (96x0e) and large (224x0e+224x1o+224x2e) checkpoints,
+  atomic numbers O, Ti and Sr.
 """
 
 import gzip
@@ -34,6 +39,10 @@ FIXTURES = {
     "compact_medium_m0": ("jit_r1_mace_mpa0_medium_contract.json", "standard_m0_contract.json", (8, 22)),
     "compact_medium_linear": ("jit_r1_mace_mpa0_medium_contract.json", None, (8, 22, 38)),
     "compact_c4": ("jit_r1_fixture_c4_e3_l0_contract.json", None, (1, 8)),
+    "compact_omat0_small": ("jit_r1_mace_omat0_small_contract.json", None, (8, 22, 38)),
+    "compact_mp0b2_large": ("jit_r1_mace_mp0b2_large_contract.json", None, (8, 22, 38)),
+    "compact_off23_small": ("jit_r1_mace_off23_small_contract.json", None, (8, 22, 38)),
+    "compact_off23_large": ("jit_r1_mace_off23_large_contract.json", None, (8, 22, 38)),
 }
 
 

@@ -1,6 +1,8 @@
 """HIP path against the oracle on models written by the reference's own
 writer (symmetrix/test/compact_r1_model.py, fixtures tests/golden/compact_*),
-whose layouts tests/test_model_layout.py pins stage by stage.
+whose layouts tests/test_model_layout.py pins stage by stage: the medium
+shape and the shapes of the MACE-OMAT-0 small (L_max 0) and MP-0b2 large
+(L_max 2) checkpoints at 128 channels.
 
 Bars: FP32 energy within 1e-5 eV/atom, forces 1e-4 eV/Angstrom, stress
 1e-6 eV/Angstrom^3; stages within 1e-4 of their largest magnitude.
@@ -37,7 +39,8 @@ def _run(name, cells, skin=0.5):
 
 
 @pytest.mark.parametrize("name,cells", [("compact_medium_m0", 3), ("compact_medium_linear", 3),
-                                        ("compact_medium_linear", 10)])
+                                        ("compact_medium_linear", 10), ("compact_omat0_small", 3),
+                                        ("compact_mp0b2_large", 3)])
 def test_reference_written_model_efs(name, cells):
     print("case", name, cells, flush=True)
     om, ref, ev, e, f, s = _run(name, cells)
@@ -50,7 +53,8 @@ def test_reference_written_model_efs(name, cells):
     np.testing.assert_allclose(e, ref["energies"], rtol=0, atol=1e-5 * max(1.0, np.max(np.abs(ref["energies"]))))
 
 
-@pytest.mark.parametrize("name", ["compact_medium_m0", "compact_medium_linear"])
+@pytest.mark.parametrize("name", ["compact_medium_m0", "compact_medium_linear", "compact_omat0_small",
+                                  "compact_mp0b2_large"])
 def test_reference_written_model_stages(name):
     print("case", name, flush=True)
     om, ref, ev, e, f, s = _run(name, 3)

@@ -119,7 +119,9 @@ class Run:
         return layout
 
 
-@pytest.fixture(scope="module", params=["compact_medium_m0", "compact_medium_linear", "compact_c4"])
+@pytest.fixture(scope="module", params=["compact_medium_m0", "compact_medium_linear", "compact_c4",
+                                        "compact_omat0_small", "compact_mp0b2_large", "compact_off23_small",
+                                        "compact_off23_large"])
 def run(request):
     return Run(request.param)
 
