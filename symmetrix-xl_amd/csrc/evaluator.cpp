@@ -286,6 +286,10 @@ struct Evaluator {
 
     Evaluator(const std::string& path, const std::string& head) {
         hm.load(path, head);
+        // channel counts that are neither a whole number of 64-lane waves nor
+        // at most one 32-lane half are run on the next multiple of 64 with
+        // zero extra channels (every cross-lane sum then spans whole waves)
+        if (hm.C > 32 && hm.C % 64 != 0 && hm.C % 16 == 0) hm.pad_channels((hm.C + 63) / 64 * 64);
         std::vector<int> le, ls, lo;
         if (!kernel_paths(hm.l_max, hm.L_max, le, ls, lo) || le != hm.path_le || ls != hm.path_ls ||
             lo != hm.path_lo)
@@ -1524,7 +1528,7 @@ int32_t smx_evaluator_info(const SmxEvaluator* ev, SmxModelInfo* info) {
         if (!info || info->struct_size < sizeof(SmxModelInfo))
             throw std::invalid_argument("SmxModelInfo.struct_size is too small");
         info->num_elements = m.num_elements;
-        info->num_channels = m.C;
+        info->num_channels = m.C_file;
         info->l_max = m.l_max;
         info->L_max = m.L_max;
         info->num_interactions = m.num_interactions;

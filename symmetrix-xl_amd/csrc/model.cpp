@@ -331,6 +331,20 @@ std::vector<double> HostModel::features(int ti, int tj) const {
     return feat;
 }
 
+// [rows][F * c_old][4] Hermite tables -> [rows][F * c_new][4], function
+// f = b * c + k (b: l or path), extra channels zero
+static std::vector<float> pad_function_table(const std::vector<float>& t, std::size_t rows, int blocks,
+                                             int c_old, int c_new) {
+    if (c_old == c_new) return t;
+    std::vector<float> out(rows * blocks * c_new * 4, 0.0f);
+    for (std::size_t i = 0; i < rows; ++i)
+        for (int b = 0; b < blocks; ++b)
+            for (int k = 0; k < c_old; ++k)
+                for (int q = 0; q < 4; ++q)
+                    out[((i * blocks + b) * c_new + k) * 4 + q] = t[((i * blocks + b) * c_old + k) * 4 + q];
+    return out;
+}
+
 void HostModel::pair_tables(int ti, int tj, std::vector<float>& R0, std::vector<float>& R1, std::vector<double>& D0,
                             std::vector<double>& D1) const {
     const auto feat = features(ti, tj);
@@ -338,10 +352,75 @@ void HostModel::pair_tables(int ti, int tj, std::vector<float>& R0, std::vector<
     std::vector<double> v, d;
     tabulate(R0_net, feat, nb, spline_points, h, v, d, R0);
     tabulate(R1_net, feat, nb, spline_points, h, v, d, R1);
+    R0 = pad_function_table(R0, spline_points - 1, l_max + 1, C_file, C);
+    R1 = pad_function_table(R1, spline_points - 1, num_paths, C_file, C);
     D0.clear();
     D1.clear();
     if (A0_scaled) D0 = density_table(A0_net, feat, nb, spline_points, h);
     if (A1_scaled) D1 = density_table(A1_net, feat, nb, spline_points, h);
+}
+
+void HostModel::pad_channels(int Cp) {
+    const int C0 = C;
+    if (Cp == C0) return;
+    if (Cp < C0) throw std::logic_error("channels can only be padded upwards");
+    // [outer][C0] -> [outer][Cp]
+    auto pad_rows = [&](std::vector<float>& v, std::size_t outer) {
+        std::vector<float> o(outer * Cp, 0.0f);
+        for (std::size_t r = 0; r < outer; ++r) std::copy_n(v.data() + r * C0, C0, o.data() + r * Cp);
+        v.swap(o);
+    };
+    // [blocks][C0][C0] -> [blocks][Cp][Cp]
+    auto pad_square = [&](std::vector<float>& v, std::size_t blocks) {
+        std::vector<float> o(blocks * Cp * Cp, 0.0f);
+        for (std::size_t b = 0; b < blocks; ++b)
+            for (int r = 0; r < C0; ++r)
+                std::copy_n(v.data() + (b * C0 + r) * C0, C0, o.data() + (b * Cp + r) * Cp);
+        v.swap(o);
+    };
+    pad_rows(H0, num_elements);
+    pad_square(A0_w, static_cast<std::size_t>(num_elements) * (l_max + 1));
+    transpose_blocks(A0_w, A0_wt, static_cast<std::size_t>(num_elements) * (l_max + 1), Cp, Cp);
+    pad_rows(m0_coef, static_cast<std::size_t>(num_elements) * m0_terms.size());
+    pad_square(H1_w, L_max + 1);
+    transpose_blocks(H1_w, H1_wt, L_max + 1, Cp, Cp);
+    {
+        // A1 per l: rows (e, k_in), columns k_out
+        std::vector<std::int64_t> off(l_max + 2, 0);
+        for (int l = 0; l <= l_max; ++l) off[l + 1] = off[l] + static_cast<std::int64_t>(num_e[l]) * Cp * Cp;
+        std::vector<float> w(off[l_max + 1], 0.0f), wt(off[l_max + 1], 0.0f);
+        for (int l = 0; l <= l_max; ++l) {
+            const int K = num_e[l] * Cp;
+            for (int e = 0; e < num_e[l]; ++e)
+                for (int ki = 0; ki < C0; ++ki)
+                    for (int ko = 0; ko < C0; ++ko) {
+                        const float v = A1_w[A1_offset[l] + (static_cast<std::size_t>(e) * C0 + ki) * C0 + ko];
+                        w[off[l] + (static_cast<std::size_t>(e) * Cp + ki) * Cp + ko] = v;
+                        wt[off[l] + static_cast<std::size_t>(ko) * K + e * Cp + ki] = v;
+                    }
+        }
+        A1_w.swap(w);
+        A1_wt.swap(wt);
+        A1_offset = off;
+    }
+    pad_rows(m1_coef, static_cast<std::size_t>(num_elements) * m1_terms.size());
+    pad_square(H2_T, num_elements);
+    transpose_blocks(H2_T, H2_Tt, num_elements, Cp, Cp);
+    pad_square(H2_M1, 1);
+    transpose_blocks(H2_M1, H2_M1t, 1, Cp, Cp);
+    readout_q.resize(Cp, 0.0);
+    {
+        std::vector<double> w1(static_cast<std::size_t>(readout_hidden) * Cp, 0.0);
+        for (int hdn = 0; hdn < readout_hidden; ++hdn)
+            std::copy_n(readout_W1.data() + static_cast<std::size_t>(hdn) * C0, C0,
+                        w1.data() + static_cast<std::size_t>(hdn) * Cp);
+        readout_W1.swap(w1);
+    }
+    R0_coef = pad_function_table(R0_coef, spline_points - 1, l_max + 1, C0, Cp);
+    R1_coef = pad_function_table(R1_coef, spline_points - 1, num_paths, C0, Cp);
+    R0_functions = (l_max + 1) * Cp;
+    R1_functions = num_paths * Cp;
+    C = Cp;
 }
 
 void HostModel::load(const std::string& path, const std::string& head) {
@@ -364,6 +443,7 @@ void HostModel::load(const std::string& path, const std::string& head) {
     if (num_interactions != 2) throw std::invalid_argument("only two-interaction MACE models are supported");
     num_elements = j.at("num_elements").as_int();
     C = j.at("num_channels").as_int();
+    C_file = C;
     r_cut = j.at("r_cut").as_number();
     l_max = j.at("l_max").as_int();
     L_max = j.at("L_max").as_int();

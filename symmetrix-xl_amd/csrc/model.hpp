@@ -33,9 +33,11 @@ struct RadialNetwork {
 };
 
 struct HostModel {
-    // shape
+    // shape (C: the channel count the tables are laid out for -- the file's
+    // own, or the kernels' padded count after pad_channels; C_file: the file's)
     int num_elements = 0;
     int C = 0;
+    int C_file = 0;
     int l_max = 0, L_max = 0;
     int num_lm = 0, num_LM = 0;
     int num_interactions = 2;
@@ -73,6 +75,10 @@ struct HostModel {
     // [interval][4] (the tables above are the pair (0, 0))
     void pair_tables(int ti, int tj, std::vector<float>& R0, std::vector<float>& R1, std::vector<double>& D0,
                      std::vector<double>& D1) const;
+    // Lay every per-channel table out for Cp >= C_file channels, the extra
+    // channels zero in every weight, coefficient and radial function, so they
+    // stay zero through the model and add nothing to energies or forces.
+    void pad_channels(int Cp);
     std::vector<double> features(int ti, int tj) const;
     // ZBL pair repulsion: per (type, type) {1/a, 14.3996 Z_u Z_v, r_max}
     bool has_zbl = false;

@@ -114,11 +114,9 @@ def test_reference_written_fixture_loads_or_is_unsupported():
                                              None, None)
         assert rc == 0, _native.lib.smx_last_error()
         assert list(dims)[:3] == [15, 4, 4 * 128]
-    # 4, 96 and 224 channels (not multiples of the 64-lane wave beyond 16) have no kernel set
-    for name in ("compact_c4", "compact_off23_small", "compact_off23_large"):
-        path, _ = compact_model(name)
-        rc, _ = _create(path)
-        assert rc == _native.SMX_ERR_UNSUPPORTED, name
+    path, _ = compact_model("compact_c4")
+    rc, _ = _create(path)
+    assert rc == _native.SMX_ERR_UNSUPPORTED
 
 
 def test_inconsistent_model_arrays_are_invalid(tmp_path):

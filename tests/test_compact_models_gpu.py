@@ -2,7 +2,9 @@
 writer (symmetrix/test/compact_r1_model.py, fixtures tests/golden/compact_*),
 whose layouts tests/test_model_layout.py pins stage by stage: the medium
 shape and the shapes of the MACE-OMAT-0 small (L_max 0) and MP-0b2 large
-(L_max 2) checkpoints at 128 channels.
+(L_max 2) checkpoints at 128 channels, and of the MACE-OFF23 small (96
+channels, L_max 0) and large (224 channels, L_max 2) checkpoints, which run
+on 128 and 256 lanes with zero extra channels.
 
 Bars: FP32 energy within 1e-5 eV/atom, forces 1e-4 eV/Angstrom, stress
 1e-6 eV/Angstrom^3; stages within 1e-4 of their largest magnitude.
@@ -40,7 +42,8 @@ def _run(name, cells, skin=0.5):
 
 @pytest.mark.parametrize("name,cells", [("compact_medium_m0", 3), ("compact_medium_linear", 3),
                                         ("compact_medium_linear", 10), ("compact_omat0_small", 3),
-                                        ("compact_mp0b2_large", 3)])
+                                        ("compact_mp0b2_large", 3), ("compact_off23_small", 3),
+                                        ("compact_off23_large", 3)])
 def test_reference_written_model_efs(name, cells):
     print("case", name, cells, flush=True)
     om, ref, ev, e, f, s = _run(name, cells)
