@@ -237,6 +237,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-calculator", action="store_true", help="skip the calculator-boundary timing")
     ap.add_argument("--no-configs", action="store_true", help="skip the wide and irregular configs")
+    ap.add_argument("--no-lammps", action="store_true", help="skip the LAMMPS pair-style step timing")
     ap.add_argument("--capacity-steps", type=int, default=3,
                     help="NVE steps of the tiled 11.5M-atom capacity extra key (0 skips it)")
     ap.add_argument("--capacity", type=int, default=0, metavar="N",
@@ -299,6 +300,11 @@ def main():
     if not args.no_calculator:
         out["calculator_us_per_atom"] = calculator_protocol(model_path, system, skin)
         note("calculator: %s" % out["calculator_us_per_atom"])
+    out["model_load_s"] = model_load_seconds(model_path)
+    note("model load: %s" % out["model_load_s"])
+    if not args.no_lammps:
+        out["lammps_step"] = lammps_step_protocol(hip, model_path, system, skin)
+        note("lammps step: %s" % out["lammps_step"])
     if not args.no_configs:
         out["configs"] = {}
         wide = systems.water_box(10000, seed=0)
@@ -423,6 +429,113 @@ def run_config(hip, model_path, system, skin, warmup, steps, timed_steps=False):
     out["active_edges"] = E_active
     hip.hipFree(d_pos)
     ev.close()
+    return out
+
+
+def lammps_arrays(system, cutoff):
+    """The arrays pair_style symmetrix/mace/kk holds on one rank
+    (pair_symmetrix_mace_kokkos.cpp:1010-1282): local atoms, the ghost images
+    within `cutoff` of the (orthorhombic) box, atom->map(tag) as owner, and a
+    full neighbour list (cutoff = r_cut + skin, LAMMPS's list cutoff) in a
+    column-major array, as Kokkos lays it out on the device."""
+    from scipy.spatial import cKDTree
+    pos = np.asarray(system["positions"], float)
+    cell = np.asarray(system["cell"], float)
+    if np.count_nonzero(cell - np.diag(np.diag(cell))):
+        raise ValueError("lammps_arrays expects an orthorhombic box")
+    n = len(pos)
+    L = np.diag(cell)
+    frac = pos / L
+    frac -= np.floor(frac)
+    local = frac * L
+    allpos, owner = [local], [np.arange(n)]
+    for a in (-1, 0, 1):
+        for b in (-1, 0, 1):
+            for c in (-1, 0, 1):
+                if (a, b, c) == (0, 0, 0):
+                    continue
+                img = local + np.array([a, b, c]) * L
+                keep = np.all((img > -cutoff) & (img < L + cutoff), axis=1)
+                allpos.append(img[keep])
+                owner.append(np.nonzero(keep)[0])
+    allpos = np.concatenate(allpos)
+    owner = np.concatenate(owner).astype(np.int32)
+    rows = cKDTree(allpos).query_ball_point(local, cutoff)
+    rows = [np.array(sorted(j for j in r if j != i), np.int32) for i, r in enumerate(rows)]
+    maxn = max(len(r) for r in rows)
+    nb = np.zeros((maxn, n), np.int32)
+    for i, r in enumerate(rows):
+        nb[:len(r), i] = r
+    numneigh = np.array([len(r) for r in rows], np.int32)
+    return allpos, owner, nb, numneigh
+
+
+def lammps_step_protocol(hip, model_path, system, skin):
+    """smx_lammps_compute, the pair style's compute(), on device-resident
+    LAMMPS arrays of the medium system: 3 warm-ups, median of 10 calls, once
+    on a retained neighbour list (rebuild = 0, the steps between LAMMPS
+    rebuilds) and once rebuilding the graph on every call (rebuild = 1).
+    The reference's 2.559 us/atom/step (RTX 5090, README.md:101-110) is a
+    whole LAMMPS step (integrator, communication and its own neighbour list
+    included); this is the pair-style part of one."""
+    from symmetrix._native import SmxLammpsArgsV2
+    from symmetrix.mace_kokkos import MACEKokkosFloat
+    ev = MACEKokkosFloat(model_path)
+    lut = {int(z): i for i, z in enumerate(ev.atomic_numbers)}
+    species = sorted(set(int(z) for z in system["numbers"]))
+    type_of_z = {z: t + 1 for t, z in enumerate(species)}
+    allpos, owner, nb, numneigh = lammps_arrays(system, ev.r_cut + skin)
+    n, nall = len(numneigh), len(allpos)
+    types = np.array([type_of_z[int(z)] for z in system["numbers"]], np.int32)[owner]
+    a = SmxLammpsArgsV2()
+    a.inum, a.nall, a.ntypes = n, nall, len(species)
+    a.ilist = device_copy_of(hip, np.arange(n, dtype=np.int32))
+    a.numneigh = device_copy_of(hip, numneigh)
+    a.neighbors = device_copy_of(hip, nb)
+    a.stride_atom, a.stride_neighbor = 1, n
+    a.x = device_copy_of(hip, np.ascontiguousarray(allpos))
+    a.type = device_copy_of(hip, types)
+    a.type_to_model = device_copy_of(hip, np.array([lut[z] for z in species], np.int32))
+    a.owner = device_copy_of(hip, owner)
+    a.f = device_copy_of(hip, np.zeros((nall, 3)))
+    a.eatom = None
+    a.stream = None
+    out = {"atoms": n, "ghosts": nall - n, "neighbors": int(numneigh.sum())}
+    for key, rebuild in (("retained_list_us_per_atom", 0), ("rebuild_every_call_us_per_atom", 1)):
+        a.rebuild = 1
+        ev._lammps_compute(a)
+        a.rebuild = rebuild
+        for _ in range(3):
+            ev._lammps_compute(a)
+        times = []
+        for _ in range(10):
+            t0 = time.perf_counter()
+            ev._lammps_compute(a)
+            times.append(time.perf_counter() - t0)
+        out[key] = round(statistics.median(times) * 1e6 / n, 4)
+    out["reference"] = {"value": 2.559, "hardware": "RTX 5090", "note": "whole LAMMPS step, trained model"}
+    for p in (a.ilist, a.numneigh, a.neighbors, a.x, a.type, a.type_to_model, a.owner, a.f):
+        hip.hipFree(ctypes.c_void_p(p))
+    ev.close()
+    return out
+
+
+def model_load_seconds(model_path):
+    """Evaluator construction (model file read, tables built, device upload)
+    from the JSON file and from its SMXB binary form."""
+    import tempfile
+    from symmetrix import model_format
+    from symmetrix.mace_kokkos import MACEKokkosFloat
+    out = {}
+    with tempfile.TemporaryDirectory() as d:
+        binary = os.path.join(d, "model.smxb")
+        model_format.convert(model_path, binary)
+        for key, path in (("json", model_path), ("binary", binary)):
+            t0 = time.perf_counter()
+            MACEKokkosFloat(path).close()
+            out[key] = round(time.perf_counter() - t0, 3)
+        out["json_bytes"] = os.path.getsize(model_path)
+        out["binary_bytes"] = os.path.getsize(binary)
     return out
 
 

@@ -332,6 +332,15 @@ SMX_API int32_t smx_kernel_timing_reset(SmxEvaluator* ev);
 SMX_API int32_t smx_kernel_timing(SmxEvaluator* ev, int32_t index, const char** name, double* total_ms,
                                   int64_t* launches);
 
+/* Model-file conversion (no reference counterpart: the reference reads JSON
+ * only, mace_kokkos_model.cpp via nlohmann::json).  Rewrites `source` (JSON v4
+ * text or the SMXB binary form, told apart by the magic) as `format`
+ * ("binary" or "json") at `destination`; the document is unchanged, so either
+ * file loads through smx_evaluator_create to the same model.  SMXB stores
+ * every number array as raw doubles (layout in csrc/model_binary.hpp): a
+ * medium model loads without number parsing. */
+SMX_API int32_t smx_model_convert(const char* source, const char* destination, const char* format);
+
 /* Standalone periodic neighbour list (neighbor_graph_kokkos.cpp:38-405),
  * bit-exact with the reference's device builder.  Two calls: with
  * sources == NULL it returns the edge count in *num_edges; then with

@@ -1522,6 +1522,14 @@ int32_t smx_evaluator_create(const char* model_path, const char* head, SmxEvalua
 
 void smx_evaluator_destroy(SmxEvaluator* ev) { delete ev; }
 
+int32_t smx_model_convert(const char* source, const char* destination, const char* format) {
+    return guarded([&] {
+        if (!source || !destination || !format)
+            throw std::invalid_argument("source, destination and format are required");
+        smx::convert_model_file(source, destination, format);
+    });
+}
+
 int32_t smx_evaluator_info(const SmxEvaluator* ev, SmxModelInfo* info) {
     return guarded([&] {
         const auto& m = E(ev).hm;

@@ -26,6 +26,7 @@
 #include <stdexcept>
 
 #include "json_lite.hpp"
+#include "model_binary.hpp"
 
 namespace smx {
 namespace {
@@ -424,7 +425,7 @@ void HostModel::pad_channels(int Cp) {
 }
 
 void HostModel::load(const std::string& path, const std::string& head) {
-    Value j = json_lite::parse_file(path);
+    Value j = json_lite::parse_model_file(path);
     if (j.get_int("symmetrix_format_version", 1) != 4)
         throw std::invalid_argument("only Symmetrix MACE model format version 4 is supported");
     select_prediction_head(j, head, selected_head, available_heads);
@@ -725,6 +726,19 @@ void HostModel::load(const std::string& path, const std::string& head) {
             readout_W2.size() != static_cast<std::size_t>(readout_hidden))
             throw std::invalid_argument("readout weights do not match the model shape");
     }
+}
+
+void convert_model_file(const std::string& source, const std::string& destination, const std::string& format) {
+    if (format != "binary" && format != "json")
+        throw std::invalid_argument("model file format must be 'binary' or 'json'");
+    if (source == destination) throw std::invalid_argument("source and destination must differ");
+    const Value doc = json_lite::parse_model_file(source);
+    if (!doc.is_object() || doc.get_int("symmetrix_format_version", 1) != 4)
+        throw std::invalid_argument("'" + source + "' is not a Symmetrix model file of format version 4");
+    if (format == "binary")
+        json_lite::write_binary_file(doc, destination);
+    else
+        json_lite::write_json_file(doc, destination);
 }
 
 }  // namespace smx

@@ -127,4 +127,8 @@ struct HostModel {
     void load(const std::string& path, const std::string& head);
 };
 
+// Rewrites a model file (JSON v4 text or its SMXB binary form) as `format`
+// ("binary" or "json"), the document unchanged.
+void convert_model_file(const std::string& source, const std::string& destination, const std::string& format);
+
 }  // namespace smx

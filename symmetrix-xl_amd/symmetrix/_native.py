@@ -123,6 +123,7 @@ SIGNATURES = [
     ("smx_kernel_timing_reset", _i32, [_vp]),
     ("smx_kernel_timing", _i32, [_vp, _i32, ctypes.POINTER(_cp), _p_dbl, _p_i64]),
     ("smx_neighbor_list", _i32, [_i32, _vp, _vp, _vp, _dbl, _p_i64, _vp, _vp, _vp, _vp, _vp]),
+    ("smx_model_convert", _i32, [_cp, _cp, _cp]),
     ("smx_set_execution_plan_request", _i32, [_vp, _cp, _cp, _cp]),
     ("smx_set_allow_fixed_workspace", _i32, [_vp, _i32]),
     ("smx_execution_plan_report", _i32, [_vp, _vp, _i64, _p_i64]),

@@ -41,6 +41,22 @@ def test_library_exports_every_declared_entry_point():
     assert set(names) <= bound
 
 
+def test_lammps_pair_style_uses_only_declared_entry_points():
+    # the pair-style class (built inside LAMMPS, not here) calls only what the
+    # header declares and fills only fields SmxLammpsArgsV2 has
+    src = os.path.join(ROOT, "symmetrix-xl_amd", "lammps", "pair_symmetrix_mace_mi355x.cpp")
+    with open(src) as f:
+        text = f.read()
+    declared = set(_declared_symbols())
+    used = set(re.findall(r"\b(smx_\w+)\s*\(", text))
+    assert used and used <= declared, used - declared
+    fields = {name for name, _ in _native.SmxLammpsArgsV2._fields_}
+    assigned = set(re.findall(r"\ba\.(\w+)\s*=", text))
+    assert assigned <= fields, assigned - fields
+    # every input field is set (reserved stays zero from the initialiser)
+    assert fields - {"reserved"} <= assigned, fields - {"reserved"} - assigned
+
+
 def test_abi_version_and_error_string():
     assert _native.lib.smx_abi_version() == 1
     assert isinstance(_native.lib.smx_last_error(), bytes)

@@ -20,14 +20,14 @@ pytestmark = pytest.mark.gpu
 E_TOL, F_TOL, S_TOL = 1e-5, 1e-4, 1e-6
 
 
-def _run(name, cells, skin=0.5):
+def _run(name, cells, skin=0.5, model_file=None):
     from oracle import oracle
     from symmetrix.mace_kokkos import MACEKokkosFloat
     path, _ = compact_model(name)
     system = fixture_system(name, cells=cells)
     om = oracle.OracleModel(path)
     ref = oracle.evaluate_system(om, system, skin=skin)
-    ev = MACEKokkosFloat(path)
+    ev = MACEKokkosFloat(model_file or path)
     types = om.types_of(system["numbers"])
     cell = np.asarray(system["cell"], float)
     g = ev._prepare_periodic_factorized_graph(types, system["positions"], cell, np.linalg.inv(cell),
@@ -69,3 +69,16 @@ def test_reference_written_model_stages(name):
         assert err < 1e-4, stage
     nf = ev.node_forces.reshape(-1, 3)
     assert np.max(np.abs(nf - ref["node_forces"])) < 1e-5
+
+
+def test_binary_model_file_evaluates_like_its_json(tmp_path):
+    # the SMXB form of a model loads to the same arrays: identical results
+    from symmetrix import model_format
+    print("case compact_medium_linear binary", flush=True)
+    path, _ = compact_model("compact_medium_linear")
+    binary = tmp_path / "model.smxb"
+    model_format.convert(path, binary)
+    _, ref, _, e0, f0, s0 = _run("compact_medium_linear", 3)
+    _, _, _, e1, f1, s1 = _run("compact_medium_linear", 3, model_file=binary)
+    assert np.array_equal(e0, e1) and np.array_equal(f0, f1) and np.array_equal(s0, s1)
+    assert np.max(np.abs(f1 - ref["forces"])) < F_TOL
