@@ -238,6 +238,8 @@ def main():
     ap.add_argument("--no-calculator", action="store_true", help="skip the calculator-boundary timing")
     ap.add_argument("--no-configs", action="store_true", help="skip the wide and irregular configs")
     ap.add_argument("--no-lammps", action="store_true", help="skip the LAMMPS pair-style step timing")
+    ap.add_argument("--only-config", choices=("wide", "irregular"),
+                    help="run only that config (3 warm-ups, median of 10) and print its summary")
     ap.add_argument("--capacity-steps", type=int, default=3,
                     help="NVE steps of the tiled 11.5M-atom capacity extra key (0 skips it)")
     ap.add_argument("--capacity", type=int, default=0, metavar="N",
@@ -259,6 +261,10 @@ def main():
         return
 
     from symmetrix import random_model, systems
+    if args.only_config:
+        model_path, system, workload = config_case(args.only_config)
+        print(json.dumps(summary(run_config(hip_lib(), model_path, system, 0.5, 3, 10), workload)), flush=True)
+        return
 
     def note(msg):
         print("[bench] %s" % msg, file=sys.stderr, flush=True)
@@ -307,16 +313,10 @@ def main():
         note("lammps step: %s" % out["lammps_step"])
     if not args.no_configs:
         out["configs"] = {}
-        wide = systems.water_box(10000, seed=0)
-        out["configs"]["wide"] = summary(run_config(hip, random_model.cached_model("wide"), wide, skin, 3, 10),
-                                         "wide: 10,000 rigid waters (30,000 atoms), MACE 256x(0e+1o+2e) l_max 3 "
-                                         "corr 3, r_cut 5.0 A + 0.5 A skin")
-        note("wide: %s" % out["configs"]["wide"])
-        irregular = systems.irregular_box(20000, density=0.08, min_distance=1.8, seed=0)
-        out["configs"]["irregular"] = summary(run_config(hip, model_path, irregular, skin, 3, 10),
-                                              "irregular: 20,000 atoms uniform at 0.08/A^3, 1.8 A minimum "
-                                              "separation, 10 species, medium model")
-        note("irregular: %s" % out["configs"]["irregular"])
+        for name in ("wide", "irregular"):
+            cfg_model, cfg_system, workload = config_case(name)
+            out["configs"][name] = summary(run_config(hip, cfg_model, cfg_system, skin, 3, 10), workload)
+            note("%s: %s" % (name, out["configs"][name]))
     if args.capacity_steps > 0:
         try:
             out["capacity"] = capacity(132, args.capacity_steps, args.tile_receivers)
@@ -326,6 +326,18 @@ def main():
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(model_path, skin)
     print(json.dumps(out), flush=True)
+
+
+def config_case(name):
+    """(model path, system, workload text) of the wide and irregular configs."""
+    from symmetrix import random_model, systems
+    if name == "wide":
+        return (random_model.cached_model("wide"), systems.water_box(10000, seed=0),
+                "wide: 10,000 rigid waters (30,000 atoms), MACE 256x(0e+1o+2e) l_max 3 corr 3, "
+                "r_cut 5.0 A + 0.5 A skin")
+    return (random_model.cached_model("medium"),
+            systems.irregular_box(20000, density=0.08, min_distance=1.8, seed=0),
+            "irregular: 20,000 atoms uniform at 0.08/A^3, 1.8 A minimum separation, 10 species, medium model")
 
 
 def summary(r, workload):
