@@ -193,7 +193,9 @@ struct PlanSet {
     std::vector<GemmTile> tiles;
     std::vector<std::size_t> tile_begin;  // per receiver tile: first GemmTile
     std::vector<int> rows;                // packed (local node << 4 | m)
-    DevBuf d_tiles, d_rows;
+    std::vector<GemmTileSet> sets;        // per receiver tile, tiles relative to its first
+    std::vector<std::size_t> set_begin;
+    DevBuf d_tiles, d_rows, d_sets;
 };
 
 }  // namespace
@@ -441,7 +443,7 @@ struct Evaluator {
         max_n_a1r = mx(groups_a1r);
         sub_a0 = sub(groups_a0);
         sub_h1 = sub(groups_h1);
-        sub_a1f = std::min(sub(groups_a1f), 4);  // the A1 forward (K up to 3C) measured faster at 64 columns
+        sub_a1f = sub(groups_a1f);  // (the A1 forward plan prefers 64 columns: K runs to 3C)
         sub_a1r = sub(groups_a1r);
         upload(d_groups_a0, groups_a0, stream);
         upload(d_groups_h1, groups_h1, stream);
@@ -585,6 +587,8 @@ struct Evaluator {
             p->tiles.clear();
             p->tile_begin.clear();
             p->rows.clear();
+            p->sets.clear();
+            p->set_begin.clear();
         }
         for (const auto& t : tiles) {
             const std::size_t base = h_node_list.size();
@@ -596,15 +600,23 @@ struct Evaluator {
                 return h_node_types[t.r0 + a] < h_node_types[t.r0 + b];
             });
             h_node_list.insert(h_node_list.end(), order.begin(), order.end());
-            for (PlanSet* p : {&ps_a0, &ps_h1, &ps_a1f, &ps_a1r}) p->tile_begin.push_back(p->tiles.size());
-            // rows (node order[a..b), m in [0, 2l+1)) of one group, cut into wave tiles
+            for (PlanSet* p : {&ps_a0, &ps_h1, &ps_a1f, &ps_a1r}) {
+                p->tile_begin.push_back(p->tiles.size());
+                p->set_begin.push_back(p->sets.size());
+            }
+            // rows (node order[a..b), m in [0, 2l+1)) of one group, cut into
+            // wave tiles, and the tiles into sets of up to kGemmShareWaves
             auto add = [&](PlanSet& P, int group, int l, int a, int b) {
                 const int start = static_cast<int>(P.rows.size());
                 for (int m = 0; m < 2 * l + 1; ++m)
                     for (int q = a; q < b; ++q) P.rows.push_back(order[q] << 4 | m);
                 const int end = static_cast<int>(P.rows.size());
+                const int t0 = static_cast<int>(P.tiles.size() - P.tile_begin.back());
                 for (int s0 = start; s0 < end; s0 += kGemmRows)
                     P.tiles.push_back(GemmTile{s0, std::min(kGemmRows, end - s0), group});
+                const int t1 = static_cast<int>(P.tiles.size() - P.tile_begin.back());
+                for (int t = t0; t < t1; t += kGemmShareWaves)
+                    P.sets.push_back(GemmTileSet{t, std::min(kGemmShareWaves, t1 - t)});
             };
             for (int p = 0; p < t.nr;) {
                 int q = p;
@@ -625,8 +637,10 @@ struct Evaluator {
         batch_begin.push_back(h_batches.size());
         for (PlanSet* p : {&ps_a0, &ps_h1, &ps_a1f, &ps_a1r}) {
             p->tile_begin.push_back(p->tiles.size());
+            p->set_begin.push_back(p->sets.size());
             upload(p->d_tiles, p->tiles, stream);
             upload(p->d_rows, p->rows, stream);
+            upload(p->d_sets, p->sets, stream);
         }
         upload(d_node_list, h_node_list, stream);
         upload(d_batches, h_batches, stream);
@@ -638,12 +652,15 @@ struct Evaluator {
             g.groups = groups.as<GemmGroup>();
             g.rows = P.d_rows.as<int>();
             g.max_n = max_n;
+            g.sets = P.d_sets.as<GemmTileSet>() + P.set_begin[ti];
+            g.num_sets = static_cast<int>(P.set_begin[ti + 1] - P.set_begin[ti]);
             return g;
         };
         for (std::size_t ti = 0; ti < tiles.size(); ++ti) {
             tiles[ti].a0 = view(ps_a0, ti, d_groups_a0, max_n_a0, sub_a0);
             tiles[ti].h1 = view(ps_h1, ti, d_groups_h1, max_n_h1, sub_h1);
             tiles[ti].a1f = view(ps_a1f, ti, d_groups_a1f, max_n_a1f, sub_a1f);
+            tiles[ti].a1f.narrow = true;
             tiles[ti].a1r = view(ps_a1r, ti, d_groups_a1r, max_n_a1r, sub_a1r);
             tiles[ti].node_list = d_node_list.as<int>() + node_list_begin[ti];
             tiles[ti].batches = d_batches.as<NodeBatch>() + batch_begin[ti];

@@ -95,6 +95,12 @@ constexpr int kGemmRows = 16;
 struct GemmTile {
     int row_start, count, group;  // rows [row_start, row_start+count), count <= kGemmRows
 };
+// Up to kGemmShareWaves consecutive tiles of one group: the workgroup of the
+// shared-operand GEMM kernel (tile indices relative to GemmPlan::tiles).
+constexpr int kGemmShareWaves = 8;
+struct GemmTileSet {
+    int first, count;
+};
 struct GemmPlan {
     const GemmTile* tiles = nullptr;
     const GemmGroup* groups = nullptr;
@@ -102,6 +108,9 @@ struct GemmPlan {
     int num_tiles = 0;
     int max_n = 0;
     int n_sub = 1;  // 16-column tiles per wave (8, 4, 2 or 1): divides every group's N/16
+    const GemmTileSet* sets = nullptr;  // tiles grouped for the shared-operand kernel
+    int num_sets = 0;
+    bool narrow = false;  // prefer 64-column waves to 128-column ones (long K)
 };
 
 // Readout batches: up to kReadoutBatch receivers of one type, as a range of
