@@ -88,24 +88,70 @@ void PairSymmetrixMACEMI355X<DeviceType>::allocate()
     for (int j = i; j <= n; j++) setflag[i][j] = 0;
 }
 
+// The reference's keywords (pair_symmetrix_mace_kokkos.cpp:180-370) where
+// this build has them: the mode token (only no_domain_decomposition),
+// profile capacity|speed and its low_memory yes|no alias, allow_fixed_workspace
+// yes|no, head NAME, streamed_edges auto|direct, _debug_execution_plan ID.
+// The JIT artefact keywords name files this build does not load (warned and
+// skipped); electric_field (MACEField) and the message-passing modes are
+// refused.
 template <class DeviceType>
 void PairSymmetrixMACEMI355X<DeviceType>::settings(int narg, char **arg)
 {
-  if (narg < 1 || strcmp(arg[0], "no_domain_decomposition") != 0)
-    error->all(FLERR, "pair_style symmetrix/mace/mi355x/kk runs the no_domain_decomposition mode");
   if (comm->nprocs != 1)
-    error->all(FLERR, "pair_style symmetrix/mace/mi355x/kk no_domain_decomposition needs one MPI rank");
-  for (int i = 1; i < narg; i += 2) {
-    if (i + 1 >= narg) error->all(FLERR, "pair_style symmetrix/mace/mi355x/kk: {} needs a value", arg[i]);
-    const std::string key = arg[i], value = arg[i + 1];
-    if (key == "head")
-      head = value;
-    else if (key == "execution_profile" && (value == "capacity" || value == "speed"))
-      execution_profile = value;
-    else if (key == "allow_fixed_workspace")
-      allow_fixed_workspace = utils::logical(FLERR, value, false, lmp) == 1;
-    else
-      error->all(FLERR, "pair_style symmetrix/mace/mi355x/kk: unknown option {} {}", key, value);
+    error->all(FLERR, "pair_style symmetrix/mace/mi355x/kk runs on one MPI rank (no_domain_decomposition)");
+  execution_profile = "capacity";
+  allow_fixed_workspace = false;
+  head.clear();
+  debug_plan.clear();
+  bool profile_set = false, alias_set = false;
+  std::string alias_profile;
+  auto value_of = [&](int &i, const char *what) -> std::string {
+    if (i + 1 >= narg) error->all(FLERR, "pair_style symmetrix/mace/mi355x/kk {} requires a value", what);
+    return arg[++i];
+  };
+  auto yes_no = [&](const std::string &key, const std::string &v) {
+    if (v != "yes" && v != "no")
+      error->all(FLERR, "pair_style symmetrix/mace/mi355x/kk {} requires yes or no", key);
+    return v == "yes";
+  };
+  for (int i = 0; i < narg; ++i) {
+    const std::string key = arg[i];
+    if (key == "no_domain_decomposition") {
+      continue;
+    } else if (key == "mpi_message_passing" || key == "no_mpi_message_passing") {
+      error->all(FLERR, "pair_style symmetrix/mace/mi355x/kk has no {} mode", key);
+    } else if (key == "profile") {
+      execution_profile = value_of(i, "profile");
+      if (execution_profile != "capacity" && execution_profile != "speed")
+        error->all(FLERR, "pair_style symmetrix/mace/mi355x/kk profile requires capacity or speed");
+      profile_set = true;
+    } else if (key == "low_memory") {
+      alias_profile = yes_no(key, value_of(i, "low_memory")) ? "capacity" : "speed";
+      alias_set = true;
+    } else if (key == "allow_fixed_workspace") {
+      allow_fixed_workspace = yes_no(key, value_of(i, "allow_fixed_workspace"));
+    } else if (key == "head") {
+      head = value_of(i, "head");
+    } else if (key == "streamed_edges") {
+      const std::string v = value_of(i, "streamed_edges");
+      if (v != "auto" && v != "direct")
+        error->all(FLERR, "pair_style symmetrix/mace/mi355x/kk streamed_edges runs auto or direct only");
+    } else if (key == "_debug_execution_plan") {
+      debug_plan = value_of(i, "_debug_execution_plan");
+    } else if (key.rfind("jit_", 0) == 0) {
+      const std::string v = value_of(i, key.c_str());
+      if (comm->me == 0) error->warning(FLERR, "pair_style symmetrix/mace/mi355x/kk ignores {} {}", key, v);
+    } else if (key == "electric_field") {
+      error->all(FLERR, "pair_style symmetrix/mace/mi355x/kk does not run field-coupled (MACEField) models");
+    } else {
+      error->all(FLERR, "The command 'pair_style symmetrix/mace/mi355x/kk {}' is invalid", key);
+    }
+  }
+  if (alias_set) {
+    if (profile_set && execution_profile != alias_profile)
+      error->all(FLERR, "pair_style symmetrix/mace/mi355x/kk low_memory contradicts profile");
+    execution_profile = alias_profile;
   }
 }
 
@@ -120,7 +166,8 @@ void PairSymmetrixMACEMI355X<DeviceType>::coeff(int narg, char **arg)
   utils::logmesg(lmp, "Loading MACE model from '{}' on the MI355X evaluator\n", arg[2]);
   check(smx_evaluator_create(arg[2], head.c_str(), &evaluator), "loading the model");
   check(smx_set_allow_fixed_workspace(evaluator, allow_fixed_workspace ? 1 : 0), "plan request");
-  check(smx_set_execution_plan_request(evaluator, "direct", execution_profile.c_str(), ""), "plan request");
+  check(smx_set_execution_plan_request(evaluator, "direct", execution_profile.c_str(), debug_plan.c_str()),
+        "plan request");
   SmxModelInfo info{};
   info.struct_size = sizeof(info);
   check(smx_evaluator_info(evaluator, &info), "model info");

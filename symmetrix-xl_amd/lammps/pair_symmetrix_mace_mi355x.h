@@ -12,8 +12,9 @@
    LAMMPS's reverse communication).
 
    Usage (the reference's keywords where they apply):
-     pair_style symmetrix/mace/mi355x/kk no_domain_decomposition [head NAME]
-                [execution_profile capacity|speed] [allow_fixed_workspace yes|no]
+     pair_style symmetrix/mace/mi355x/kk [no_domain_decomposition] [head NAME]
+                [profile capacity|speed] [low_memory yes|no]
+                [allow_fixed_workspace yes|no] [streamed_edges auto|direct]
      pair_coeff * * model.json O Ti Sr      (one element symbol per LAMMPS type)
    Requires newton pair on and an atom map.
 
@@ -59,6 +60,7 @@ class PairSymmetrixMACEMI355X : public Pair, public KokkosBase {
  protected:
   SmxEvaluator *evaluator = nullptr;
   std::string head;
+  std::string debug_plan;
   std::string execution_profile = "capacity";
   bool allow_fixed_workspace = false;
   double r_cut = 0.0;
