@@ -280,6 +280,8 @@ struct Evaluator {
     DevBuf d_pair_R0, d_pair_R1, d_pair_D0, d_pair_D1, d_type_to_active, d_edge_pair;
     int* h_invalid = nullptr;
     hipEvent_t geometry_done = nullptr;
+    hipEvent_t geometry_ready = nullptr;   // edge geometry done on the main stream
+    hipStream_t flag_stream = nullptr;     // carries the invalid-edge count to the host
     hipEvent_t caller_ready = nullptr;  // LAMMPS V2: the caller's stream, waited on
     bool geometry_flag_pending = false;
     int stress_blocks = 256;
@@ -308,6 +310,8 @@ struct Evaluator {
         SMX_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
         SMX_HIP(hipHostMalloc(reinterpret_cast<void**>(&h_invalid), sizeof(int), hipHostMallocDefault));
         SMX_HIP(hipEventCreateWithFlags(&geometry_done, hipEventDisableTiming));
+        SMX_HIP(hipEventCreateWithFlags(&geometry_ready, hipEventDisableTiming));
+        SMX_HIP(hipStreamCreateWithFlags(&flag_stream, hipStreamNonBlocking));
         SMX_HIP(hipEventCreateWithFlags(&caller_ready, hipEventDisableTiming));
         upload_model();
         define_groups();
@@ -320,7 +324,12 @@ struct Evaluator {
             timer.reset();
             (void)hipStreamDestroy(stream);
         }
+        if (flag_stream) {
+            (void)hipStreamSynchronize(flag_stream);
+            (void)hipStreamDestroy(flag_stream);
+        }
         if (geometry_done) (void)hipEventDestroy(geometry_done);
+        if (geometry_ready) (void)hipEventDestroy(geometry_ready);
         if (caller_ready) (void)hipEventDestroy(caller_ready);
         if (h_invalid) (void)hipHostFree(h_invalid);
     }
@@ -1025,11 +1034,21 @@ struct Evaluator {
         ++geometry_prepare_count;
     }
 
-    // queue the D2H copy of the invalid-edge count (positions and LAMMPS calls)
+    // queue the D2H copy of the invalid-edge count (positions and LAMMPS
+    // calls).  The direct plan copies on a side stream, so the model kernels
+    // follow the edge geometry on the main stream without the copy between
+    // them; the tiled plan's later sweeps count again into the same flag, so
+    // it copies in order on the main stream.
     void post_geometry_flag() {
         if (xyz_host) return;
-        SMX_HIP(hipMemcpyAsync(h_invalid, d_invalid.as<int>(), sizeof(int), hipMemcpyDeviceToHost, stream));
-        SMX_HIP(hipEventRecord(geometry_done, stream));
+        hipStream_t s = stream;
+        if (!tiled) {
+            SMX_HIP(hipEventRecord(geometry_ready, stream));
+            SMX_HIP(hipStreamWaitEvent(flag_stream, geometry_ready, 0));
+            s = flag_stream;
+        }
+        SMX_HIP(hipMemcpyAsync(h_invalid, d_invalid.as<int>(), sizeof(int), hipMemcpyDeviceToHost, s));
+        SMX_HIP(hipEventRecord(geometry_done, s));
         geometry_flag_pending = true;
     }
 
@@ -1154,12 +1173,12 @@ struct Evaluator {
             pos = dp;
         }
         xyz_host = false;
-        launch_fill_zero(reinterpret_cast<float*>(d_invalid.as<int>()), 1, stream);
         if (timer) timer->begin("displacements", stream);
         const bool frac_ref = geom == Geometry::device_fractional || geom == Geometry::fractional;
+        // (also clears the invalid-edge count)
         launch_displacements(N, cell, inv_cell, pbc, frac_ref,
                              geom == Geometry::device_fractional ? d_wfrac.as<double>() : d_ref_positions.as<double>(),
-                             pos, d_disp.as<double>(), stream);
+                             pos, d_disp.as<double>(), d_invalid.as<int>(), stream);
         if (timer) timer->end("displacements", stream);
         evaluate(pos);
         finish_call(!on_device);

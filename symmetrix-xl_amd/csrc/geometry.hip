@@ -332,8 +332,9 @@ __global__ void k_copy_i64_i32_plus(const long long* __restrict__ in, int* __res
 // Cartesian coordinates.
 __global__ void k_displacements(int N, Mat3 cell, Mat3 inv, int pbc_mask, int ref_fractional,
                                 const double* __restrict__ ref, const double* __restrict__ pos,
-                                double* __restrict__ disp) {
+                                double* __restrict__ disp, int* __restrict__ invalid) {
     const int a = blockIdx.x * blockDim.x + threadIdx.x;
+    if (a == 0) *invalid = 0;  // the edge pass that follows counts into it
     if (a >= N) return;
     double delta[3], f[3];
     for (int c = 0; c < 3; ++c) {
@@ -715,11 +716,11 @@ void launch_gather_types(std::int64_t E, const int* sources, const int* node_typ
 }
 
 void launch_displacements(int N, const double* cell, const double* inv_cell, const int pbc[3], bool ref_fractional,
-                          const double* reference_positions, const double* positions, double* disp, hipStream_t s) {
-    if (N == 0) return;
+                          const double* reference_positions, const double* positions, double* disp, int* invalid,
+                          hipStream_t s) {
     const int mask = (pbc[0] ? 1 : 0) | (pbc[1] ? 2 : 0) | (pbc[2] ? 4 : 0);
-    k_displacements<<<blocks_for(N, 256), 256, 0, s>>>(N, mat3(cell), mat3(inv_cell), mask, ref_fractional ? 1 : 0,
-                                                       reference_positions, positions, disp);
+    k_displacements<<<blocks_for(std::max(N, 1), 256), 256, 0, s>>>(
+        N, mat3(cell), mat3(inv_cell), mask, ref_fractional ? 1 : 0, reference_positions, positions, disp, invalid);
     SMX_LAUNCH_CHECK("geometry_displacements");
 }
 

@@ -290,8 +290,10 @@ struct EdgeReference {
     const double* edges = nullptr;            // [E][3] (cartesian, fractional)
     const int* shifts = nullptr;              // [E][3] (shifts)
 };
+// (also sets *invalid, the edge pass's invalid-edge count, to zero)
 void launch_displacements(int N, const double* cell, const double* inv_cell, const int pbc[3], bool ref_fractional,
-                          const double* reference_positions, const double* positions, double* disp, hipStream_t s);
+                          const double* reference_positions, const double* positions, double* disp, int* invalid,
+                          hipStream_t s);
 void launch_edge_xyz(std::int64_t e0, std::int64_t ne, const EdgeReference& ref, const double* cell,
                      const int* receivers, const int* sources, const double* disp, double cutoff, double* xyz,
                      double* r, int* invalid, hipStream_t s);
