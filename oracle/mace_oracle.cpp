@@ -486,6 +486,16 @@ struct Mace {
     std::vector<MonomialSet> M0_monos;      // [LM]
     std::vector<std::vector<P>> M0_coef;    // [type*num_LM + LM][k*T + t]
     std::vector<P> H1_w;                    // [l][C][C]
+    // h1_affine_mode "pre_linear_up" (mace.cpp:1759-1810): the scalar input
+    // of readout_1 and the H2 skip is x = M0[:,0,:] P0 (+ residual), and its
+    // direct adjoint d enters M0_adj as P0 d
+    bool pre_linear_up = false;
+    std::vector<P> P0;                      // [C][C] [in][out], H1_product_weights l = 0
+    // first_interaction_residual (mace.cpp:1843-1875, 2796-2826): H1 +=
+    // fused[type] (the residual through linear_up), x += residual[type][lm 0]
+    bool residual = false;
+    std::vector<P> res_fused;               // [type][LM][C]
+    std::vector<P> res_x;                   // [type][C]
     std::vector<int> Phi1_l, Phi1_l1, Phi1_l2, Phi1_lme, Phi1_row;
     std::vector<P> Phi1_cg;
     int num_rows = 0, num_lme = 0;
@@ -560,12 +570,16 @@ struct Mace {
         };
         if (j.get_int("symmetrix_format_version", 1) != 4)
             throw std::invalid_argument("only Symmetrix MACE format version 4 is supported");
-        if (j.get_string("h1_affine_mode", "") != "m0_composite")
-            throw std::invalid_argument("only h1_affine_mode 'm0_composite' is supported");
+        const std::string h1_mode = j.get_string("h1_affine_mode", "");
+        if (h1_mode != "m0_composite" && h1_mode != "pre_linear_up")
+            throw std::invalid_argument("h1_affine_mode must be 'm0_composite' or 'pre_linear_up'");
+        pre_linear_up = h1_mode == "pre_linear_up";
+        residual = j.get_bool("first_interaction_residual", false);
+        if (residual && !pre_linear_up)
+            throw std::invalid_argument("a first-interaction residual needs h1_affine_mode 'pre_linear_up'");
         if (j.get_string("radial_representation", "") != "compact")
             throw std::invalid_argument("only the compact radial representation is supported");
-        if (j.get_bool("has_field_coupling", false) ||
-            j.get_bool("first_interaction_residual", false) || j.get_bool("single_layer_readout", false))
+        if (j.get_bool("has_field_coupling", false) || j.get_bool("single_layer_readout", false))
             throw std::invalid_argument("model features outside the supported MACE path");
         num_elements = j.at("num_elements").as_int();
         C = j.at("num_channels").as_int();
@@ -616,6 +630,35 @@ struct Mace {
             }
         }
         H1_w = castv(j.at("H1_weights").as_doubles());
+        if (pre_linear_up) {
+            const auto pw = castv(j.at("H1_product_weights").as_doubles());
+            if (pw.size() != H1_w.size()) throw std::invalid_argument("H1_product_weights has the wrong size");
+            P0.assign(pw.begin(), pw.begin() + static_cast<std::size_t>(C) * C);
+        }
+        if (residual) {
+            // fused[a][lm][out] = sum_in residual[a][lm][in] U_l[in][out] in
+            // Precision, in the reference's loop order (mace.cpp:2809-2822)
+            const auto U = castv(j.at("H1_linear_up_weights").as_doubles());
+            const auto b = castv(j.at("H1_first_residual_weights").as_doubles());
+            const int LM = (L_max + 1) * (L_max + 1);
+            if (U.size() != H1_w.size() || b.size() != static_cast<std::size_t>(num_elements) * LM * C)
+                throw std::invalid_argument("residual weights have the wrong size");
+            res_fused.assign(b.size(), P(0));
+            res_x.assign(static_cast<std::size_t>(num_elements) * C, P(0));
+            for (int a = 0; a < num_elements; ++a) {
+                for (int l = 0; l <= L_max; ++l)
+                    for (int m = 0; m < 2 * l + 1; ++m)
+                        for (int out = 0; out < C; ++out)
+                            for (int in = 0; in < C; ++in) {
+                                const int lm = l * l + m;
+                                res_fused[(static_cast<std::size_t>(a) * LM + lm) * C + out] +=
+                                    b[(static_cast<std::size_t>(a) * LM + lm) * C + in] *
+                                    U[(static_cast<std::size_t>(l) * C + in) * C + out];
+                            }
+                for (int k = 0; k < C; ++k) res_x[static_cast<std::size_t>(a) * C + k] =
+                    b[static_cast<std::size_t>(a) * LM * C + k];
+            }
+        }
         Phi1_l = j.at("Phi1_l").as_ints();
         Phi1_l1 = j.at("Phi1_l1").as_ints();
         Phi1_l2 = j.at("Phi1_l2").as_ints();
@@ -649,7 +692,7 @@ struct Mace {
         }
         // H2 and readouts: the OpenMP backend keeps H2 weights in Precision and
         // accumulates H2 in FP64 (mace_kokkos.hpp:1805-1816).
-        const Value& t2 = j.at("H2_weights_for_M0");
+        const Value& t2 = j.at(pre_linear_up ? "H2_weights_for_H1_pre_linear_up" : "H2_weights_for_M0");
         for (int t = 0; t < num_elements; ++t) {
             const auto w = t2.at(t).as_doubles();
             std::vector<double> r(w.size());
@@ -661,7 +704,7 @@ struct Mace {
             H2_M1.resize(w.size());
             for (std::size_t i = 0; i < w.size(); ++i) H2_M1[i] = static_cast<double>(cast(w[i]));
         }
-        q = field("readout_1_weights_for_M0").as_doubles();
+        q = field(pre_linear_up ? "readout_1_weights_for_H1_pre_linear_up" : "readout_1_weights_for_M0").as_doubles();
         hidden = j.get_int("readout_2_hidden_size", 16);
         W1 = field("readout_2_weights_1").as_doubles();
         W2 = field("readout_2_weights_2").as_doubles();
@@ -879,7 +922,17 @@ struct Mace {
         xaff.assign(static_cast<std::size_t>(n) * Cs, P(0));
 #pragma omp parallel for schedule(static)
         for (int i = 0; i < n; ++i) {
-            for (int k = 0; k < C; ++k) xaff[i * Cs + k] = M0[static_cast<std::size_t>(i) * num_LM * Cs + k];
+            const P* m00 = &M0[static_cast<std::size_t>(i) * num_LM * Cs];
+            if (pre_linear_up) {
+                // x = M0[i,0,:] P0 (gemv in Precision, input order)
+                for (int k = 0; k < C; ++k) {
+                    P s = 0;
+                    for (int in = 0; in < C; ++in) s += m00[in] * P0[static_cast<std::size_t>(in) * C + k];
+                    xaff[i * Cs + k] = s;
+                }
+            } else {
+                for (int k = 0; k < C; ++k) xaff[i * Cs + k] = m00[k];
+            }
             for (int l = 0; l <= L_max; ++l)
                 for (int m = 0; m < 2 * l + 1; ++m) {
                     const P* src = &M0[(static_cast<std::size_t>(i) * num_LM + l * l + m) * Cs];
@@ -890,6 +943,14 @@ struct Mace {
                         for (int k = 0; k < C; ++k) dst[k] += a * W[kp * Cs + k];
                     }
                 }
+            if (residual) {
+                const int t = types[i];
+                for (int lm = 0; lm < num_LM; ++lm)
+                    for (int k = 0; k < C; ++k)
+                        H1[(static_cast<std::size_t>(i) * num_LM + lm) * Cs + k] +=
+                            res_fused[(static_cast<std::size_t>(t) * num_LM + lm) * C + k];
+                for (int k = 0; k < C; ++k) xaff[i * Cs + k] += res_x[static_cast<std::size_t>(t) * C + k];
+            }
         }
 
         // ---- Phi1 streamed (mace.cpp:2023-2084)
@@ -1183,8 +1244,18 @@ struct Mace {
                         dst[k] = s;
                     }
                 }
-            for (int k = 0; k < C; ++k)
-                M0_adj[static_cast<std::size_t>(i) * num_LM * Cs + k] += static_cast<P>(direct[i * Cs + k]);
+            if (pre_linear_up) {
+                // M0_adj[i,0,:] += P0 d (the scalar input was M0 P0 + residual)
+                for (int in = 0; in < C; ++in) {
+                    double s = 0.0;
+                    for (int o = 0; o < C; ++o)
+                        s += static_cast<double>(P0[static_cast<std::size_t>(in) * C + o]) * direct[i * Cs + o];
+                    M0_adj[static_cast<std::size_t>(i) * num_LM * Cs + in] += static_cast<P>(s);
+                }
+            } else {
+                for (int k = 0; k < C; ++k)
+                    M0_adj[static_cast<std::size_t>(i) * num_LM * Cs + k] += static_cast<P>(direct[i * Cs + k]);
+            }
         }
 
         // ---- reverse M0 (mace.cpp:1665-1689)

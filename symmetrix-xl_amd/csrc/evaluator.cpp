@@ -211,10 +211,10 @@ struct Evaluator {
 
     // model tables and node-linear groups (defined for every type and l)
     std::vector<std::unique_ptr<DevBuf>> model_bufs;
-    std::vector<GemmGroup> groups_a0, groups_h1, groups_a1f, groups_a1r;
-    DevBuf d_groups_a0, d_groups_h1, d_groups_a1f, d_groups_a1r;
+    std::vector<GemmGroup> groups_a0, groups_h1, groups_a1f, groups_a1r, groups_cap, groups_cap_r;
+    DevBuf d_groups_a0, d_groups_h1, d_groups_a1f, d_groups_a1r, d_groups_cap, d_groups_cap_r;
     int max_n_a0 = 0, max_n_h1 = 0, max_n_a1f = 0, max_n_a1r = 0;
-    int sub_a0 = 1, sub_h1 = 1, sub_a1f = 1, sub_a1r = 1;
+    int sub_a0 = 1, sub_h1 = 1, sub_a1f = 1, sub_a1r = 1, sub_cap = 1;
 
     // execution plan request (set_execution_plan_request, set_allow_fixed_workspace,
     // mace_kokkos.hpp:95-96; the calculator's execution_profile and
@@ -244,7 +244,7 @@ struct Evaluator {
     DevBuf d_node_types, d_offsets, d_neigh, d_neigh_types, d_receivers, d_soff, d_sedges, d_counts;
     // receiver tiles
     std::vector<TileView> tiles;
-    PlanSet ps_a0, ps_h1, ps_a1f, ps_a1r;
+    PlanSet ps_a0, ps_h1, ps_a1f, ps_a1r, ps_cap;
     std::vector<int> h_node_list;
     std::vector<std::size_t> node_list_begin;
     std::vector<NodeBatch> h_batches;
@@ -266,7 +266,7 @@ struct Evaluator {
     DevBuf d_xyz, d_r, d_invalid;
     DevBuf w_erec, w_Phi0, w_A0, w_M0, w_Phi1, w_A1, w_A1_adj, w_M1, w_dPhi1, w_Wsrc, w_M0_adj, w_A0_adj, w_Phi0_adj,
         w_node_forces, w_density;
-    DevBuf g_H1, g_H1_adj, g_xaff, g_direct, d_node_energies, d_atom_forces, d_virial, d_stress, d_stress_partial,
+    DevBuf g_H1, g_H1_adj, g_xaff, g_direct, g_direct_m0, d_node_energies, d_atom_forces, d_virial, d_stress, d_stress_partial,
         d_total;
     Workspace ws;
     bool evaluated = false;
@@ -379,6 +379,16 @@ struct Evaluator {
         dm.m0_coef = put(hm.m0_coef);
         dm.H1_w = put(swizzled(hm.H1_w, hm.L_max + 1, hm.C, hm.C));
         dm.H1_wt = put(swizzled(hm.H1_wt, hm.L_max + 1, hm.C, hm.C));
+        dm.pre_linear_up = hm.pre_linear_up;
+        dm.residual = hm.residual;
+        if (hm.pre_linear_up) {
+            dm.P0_w = put(swizzled(hm.P0, 1, hm.C, hm.C));
+            dm.P0_wt = put(swizzled(hm.P0t, 1, hm.C, hm.C));
+        }
+        if (hm.residual) {
+            dm.res_H1 = put(hm.res_H1);
+            dm.res_x = put(hm.res_x);
+        }
         dm.cg = put(hm.cg_dense);
         {
             std::vector<float> w(hm.A1_w.size()), wt(hm.A1_wt.size());
@@ -458,6 +468,15 @@ struct Evaluator {
         upload(d_groups_h1, groups_h1, stream);
         upload(d_groups_a1f, groups_a1f, stream);
         upload(d_groups_a1r, groups_a1r, stream);
+        if (hm.pre_linear_up) {
+            // x = M0[:,0,:] P0: rows (node, 0) of M0 into x [N][C]; and
+            // P0 d: rows of d [N][C] into direct_m0 [N][C]
+            groups_cap.push_back(GemmGroup{0, C, C, NH * C, 0, C, C, 0, 0});
+            groups_cap_r.push_back(GemmGroup{0, C, C, C, 0, 0, C, 0, 0});
+            sub_cap = sub(groups_cap);
+            upload(d_groups_cap, groups_cap, stream);
+            upload(d_groups_cap_r, groups_cap_r, stream);
+        }
     }
 
     // ------------------------------------------------------------- planning
@@ -592,7 +611,7 @@ struct Evaluator {
         node_list_begin.clear();
         h_batches.clear();
         batch_begin.clear();
-        for (PlanSet* p : {&ps_a0, &ps_h1, &ps_a1f, &ps_a1r}) {
+        for (PlanSet* p : {&ps_a0, &ps_h1, &ps_a1f, &ps_a1r, &ps_cap}) {
             p->tiles.clear();
             p->tile_begin.clear();
             p->rows.clear();
@@ -609,7 +628,7 @@ struct Evaluator {
                 return h_node_types[t.r0 + a] < h_node_types[t.r0 + b];
             });
             h_node_list.insert(h_node_list.end(), order.begin(), order.end());
-            for (PlanSet* p : {&ps_a0, &ps_h1, &ps_a1f, &ps_a1r}) {
+            for (PlanSet* p : {&ps_a0, &ps_h1, &ps_a1f, &ps_a1r, &ps_cap}) {
                 p->tile_begin.push_back(p->tiles.size());
                 p->set_begin.push_back(p->sets.size());
             }
@@ -637,6 +656,7 @@ struct Evaluator {
                 p = q;
             }
             for (int l = 0; l <= hm.L_max; ++l) add(ps_h1, l, l, 0, t.nr);
+            if (hm.pre_linear_up) add(ps_cap, 0, 0, 0, t.nr);
             for (int l = 0; l <= hm.l_max; ++l) {
                 if (hm.num_e[l] == 0) continue;
                 add(ps_a1f, l, l, 0, t.nr);
@@ -644,7 +664,7 @@ struct Evaluator {
             }
         }
         batch_begin.push_back(h_batches.size());
-        for (PlanSet* p : {&ps_a0, &ps_h1, &ps_a1f, &ps_a1r}) {
+        for (PlanSet* p : {&ps_a0, &ps_h1, &ps_a1f, &ps_a1r, &ps_cap}) {
             p->tile_begin.push_back(p->tiles.size());
             p->set_begin.push_back(p->sets.size());
             upload(p->d_tiles, p->tiles, stream);
@@ -671,6 +691,10 @@ struct Evaluator {
             tiles[ti].a1f = view(ps_a1f, ti, d_groups_a1f, max_n_a1f, sub_a1f);
             tiles[ti].a1f.narrow = true;
             tiles[ti].a1r = view(ps_a1r, ti, d_groups_a1r, max_n_a1r, sub_a1r);
+            if (hm.pre_linear_up) {
+                tiles[ti].cap = view(ps_cap, ti, d_groups_cap, hm.C, sub_cap);
+                tiles[ti].cap_r = view(ps_cap, ti, d_groups_cap_r, hm.C, sub_cap);
+            }
             tiles[ti].node_list = d_node_list.as<int>() + node_list_begin[ti];
             tiles[ti].batches = d_batches.as<NodeBatch>() + batch_begin[ti];
             tiles[ti].num_batches = static_cast<int>(batch_begin[ti + 1] - batch_begin[ti]);
@@ -732,6 +756,7 @@ struct Evaluator {
         ws.H1_adj = f(g_H1_adj, n * NH * C);
         ws.xaff = f(g_xaff, n * C);
         ws.direct = f(g_direct, n * C);
+        if (hm.pre_linear_up) ws.direct_m0 = f(g_direct_m0, n * C);
         ws.node_energies = static_cast<double*>(d_node_energies.ensure(n * sizeof(double)));
         d_atom_forces.ensure(n * 3 * sizeof(double));
         d_virial.ensure(9 * sizeof(double));

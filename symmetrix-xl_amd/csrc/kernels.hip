@@ -609,6 +609,15 @@ __global__ __launch_bounds__(256) void k_tile_forces_receivers(int r0, int nr, l
     }
 }
 
+// rows[li][c] += bias[types[r0 + li]][c]
+__global__ __launch_bounds__(256) void k_type_bias(int r0, int nr, const int* __restrict__ types, int row_len,
+                                                   const float* __restrict__ bias, float* __restrict__ rows) {
+    const long long idx = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= static_cast<long long>(nr) * row_len) return;
+    const int li = static_cast<int>(idx / row_len), c = static_cast<int>(idx % row_len);
+    rows[idx] += bias[static_cast<std::size_t>(types[r0 + li]) * row_len + c];
+}
+
 __global__ void k_fill_f32(std::size_t n, float* __restrict__ p) {
     for (std::size_t j = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x; j < n;
          j += static_cast<std::size_t>(gridDim.x) * blockDim.x)
@@ -971,6 +980,19 @@ struct KernelSetImpl final : KernelSet {
             TimerScope ts(tm, "h1_linear", s);
             launch_node_gemm(t.h1, m.H1_w, w.M0, w.H1 + static_cast<std::size_t>(t.r0) * S::NH * C, s);
         }
+        if (m.pre_linear_up) {
+            // the readout_1 / skip input in the pre_linear_up basis:
+            // x = M0[:,0,:] P0 (+ the residual's lm-0 row), and H1 += the
+            // residual through linear_up (mace.cpp:1759-1783, 1843-1875)
+            TimerScope ts(tm, "h1_affine_scalar", s);
+            float* x = w.xaff + static_cast<std::size_t>(t.r0) * C;
+            launch_node_gemm(t.cap, m.P0_w, w.M0, x, s);
+            if (m.residual) {
+                launch_type_bias(t.r0, t.nr, g.node_types, C, m.res_x, x, s);
+                launch_type_bias(t.r0, t.nr, g.node_types, S::NH * C, m.res_H1,
+                                 w.H1 + static_cast<std::size_t>(t.r0) * S::NH * C, s);
+            }
+        }
     }
 
     void layer2(const DeviceModel& m, const DeviceGraph& g, const TileView& t, const Workspace& w, hipStream_t s,
@@ -1056,13 +1078,22 @@ struct KernelSetImpl final : KernelSet {
             TimerScope ts(tm, "h1_linear_reverse", s);
             launch_node_gemm(t.h1, m.H1_wt, w.H1_adj + static_cast<std::size_t>(t.r0) * S::NH * C, w.M0_adj, s);
         }
+        // the direct adjoint of the readout_1 / skip input enters M0_adj[:,0,:]
+        // as is (m0_composite) or as P0 d (pre_linear_up, mace.cpp:1785-1814)
+        const float* direct = w.direct;
+        if (m.pre_linear_up) {
+            TimerScope ts(tm, "h1_affine_scalar_reverse", s);
+            launch_node_gemm(t.cap_r, m.P0_wt, w.direct + static_cast<std::size_t>(t.r0) * C,
+                             w.direct_m0 + static_cast<std::size_t>(t.r0) * C, s);
+            direct = w.direct_m0;
+        }
         {
             TimerScope ts(tm, "m0_reverse", s);
             if constexpr (kM0Unrolled)
                 k_m0_reverse_ct<C, S::NY, S::NH, M0TAB><<<t.nr, C, 0, s>>>(t.r0, g.node_types, w.A0, w.M0_adj,
-                                                                          w.direct, m.m0_coef, w.A0_adj);
+                                                                          direct, m.m0_coef, w.A0_adj);
             else
-                k_m0_reverse<C, S::NY, S::NH><<<t.nr, C, 0, s>>>(t.r0, g.node_types, w.A0, w.M0_adj, w.direct,
+                k_m0_reverse<C, S::NY, S::NH><<<t.nr, C, 0, s>>>(t.r0, g.node_types, w.A0, w.M0_adj, direct,
                                                                 m.m0_terms, m.m0_toff, m.T0, m.m0_coef, w.A0_adj);
             SMX_LAUNCH_CHECK("m0_reverse");
         }
@@ -1277,6 +1308,13 @@ void launch_tile_forces(const TileView& t, const int* touched, int touched_count
                                                                               receiver_row, node_forces, F);
         SMX_LAUNCH_CHECK("tile_forces_receivers");
     }
+}
+
+void launch_type_bias(int r0, int nr, const int* types, int row_len, const float* bias, float* rows, hipStream_t s) {
+    const long long n = static_cast<long long>(nr) * row_len;
+    if (n == 0) return;
+    k_type_bias<<<static_cast<unsigned>((n + 255) / 256), 256, 0, s>>>(r0, nr, types, row_len, bias, rows);
+    SMX_LAUNCH_CHECK("type_bias");
 }
 
 void launch_fill_zero(float* p, std::size_t n, hipStream_t s) {

@@ -30,6 +30,13 @@ struct DeviceModel {
     const float* m0_coef = nullptr;
     const float* H1_w = nullptr;
     const float* H1_wt = nullptr;
+    // pre_linear_up basis: x = M0[:,0,:] P0 and M0_adj[:,0,:] += P0 d (GEMM
+    // weights P0 and P0^T, swizzled); residual: per-type H1 and x offsets
+    bool pre_linear_up = false, residual = false;
+    const float* P0_w = nullptr;
+    const float* P0_wt = nullptr;
+    const float* res_H1 = nullptr;  // [type][NH][C]
+    const float* res_x = nullptr;   // [type][C]
     const float* cg = nullptr;
     const float* A1_w = nullptr;
     const float* A1_wt = nullptr;
@@ -127,6 +134,7 @@ struct TileView {
     int r0 = 0, nr = 0;
     std::int64_t e0 = 0, ne = 0;
     GemmPlan a0, h1, a1f, a1r;
+    GemmPlan cap, cap_r;  // pre_linear_up: x = M0[:,0,:] P0 and its reverse P0 d (rows (node, 0))
     const int* node_list = nullptr;    // tile-local receivers sorted by type
     const NodeBatch* batches = nullptr;
     int num_batches = 0;
@@ -168,6 +176,7 @@ struct Workspace {
     float* H1_adj = nullptr;    // [N][NH][C]
     float* xaff = nullptr;      // [N][C] scalar capture M0[i,0,:]
     float* direct = nullptr;    // [N][C] direct adjoint of the scalar capture
+    float* direct_m0 = nullptr; // [N][C] pre_linear_up: that adjoint carried to M0[:,0,:] (P0 d)
     double* node_energies = nullptr;  // [N]
 };
 
@@ -236,6 +245,8 @@ void launch_edge_pairs(std::int64_t E, const int* receivers, const int* node_typ
                        const int* type_to_active, int active_types, int* edge_pair, int* bad, hipStream_t s);
 
 void launch_node_gemm(const GemmPlan& plan, const float* W, const float* in, float* out, hipStream_t s);
+// rows[li][0..row_len) += bias[types[r0 + li]][0..row_len) for li < nr
+void launch_type_bias(int r0, int nr, const int* types, int row_len, const float* bias, float* rows, hipStream_t s);
 
 // Density scaling (density.hip).  Factors s0/s1 (either may be null) of the
 // tile's receivers from t.r; rows [nr][row_len] scaled (divide: A /= s in

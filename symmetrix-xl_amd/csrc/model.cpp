@@ -385,6 +385,14 @@ void HostModel::pad_channels(int Cp) {
     pad_rows(m0_coef, static_cast<std::size_t>(num_elements) * m0_terms.size());
     pad_square(H1_w, L_max + 1);
     transpose_blocks(H1_w, H1_wt, L_max + 1, Cp, Cp);
+    if (pre_linear_up) {
+        pad_square(P0, 1);
+        transpose_blocks(P0, P0t, 1, Cp, Cp);
+    }
+    if (residual) {
+        pad_rows(res_H1, static_cast<std::size_t>(num_elements) * num_LM);
+        pad_rows(res_x, static_cast<std::size_t>(num_elements));
+    }
     {
         // A1 per l: rows (e, k_in), columns k_out
         std::vector<std::int64_t> off(l_max + 2, 0);
@@ -429,14 +437,28 @@ void HostModel::load(const std::string& path, const std::string& head) {
     if (j.get_int("symmetrix_format_version", 1) != 4)
         throw std::invalid_argument("only Symmetrix MACE model format version 4 is supported");
     select_prediction_head(j, head, selected_head, available_heads);
-    if (j.get_string("h1_affine_mode", "") != "m0_composite")
-        throw std::invalid_argument("only h1_affine_mode 'm0_composite' is supported");
+    // h1_affine_schema.hpp:196-259: the two v4 bases, each with its own
+    // readout_1 / skip keys; a first-interaction residual needs pre_linear_up
+    const std::string h1_mode = j.get_string("h1_affine_mode", "");
+    if (h1_mode != "m0_composite" && h1_mode != "pre_linear_up")
+        throw std::invalid_argument("Symmetrix MACE format version 4 requires h1_affine_mode 'm0_composite' or "
+                                    "'pre_linear_up'");
+    pre_linear_up = h1_mode == "pre_linear_up";
+    const char* readout_key = pre_linear_up ? "readout_1_weights_for_H1_pre_linear_up" : "readout_1_weights_for_M0";
+    const char* skip_key = pre_linear_up ? "H2_weights_for_H1_pre_linear_up" : "H2_weights_for_M0";
+    if (j.contains(pre_linear_up ? "readout_1_weights_for_M0" : "readout_1_weights_for_H1_pre_linear_up") ||
+        j.contains(pre_linear_up ? "H2_weights_for_M0" : "H2_weights_for_H1_pre_linear_up"))
+        throw std::invalid_argument(std::string("a '") + h1_mode + "' MACE JSON must not hold the other basis's "
+                                    "readout_1 or H2 skip weights");
+    residual = j.get_bool("first_interaction_residual", false);
+    if (residual && !pre_linear_up)
+        throw std::invalid_argument("The m0_composite basis cannot represent first-interaction residual features; "
+                                    "such models use h1_affine_mode 'pre_linear_up'.");
     if (j.get_string("radial_representation", "") != "compact")
         throw std::invalid_argument("only the compact radial representation is supported");
-    if (j.get_bool("has_field_coupling", false) || j.get_bool("first_interaction_residual", false) ||
-        j.get_bool("single_layer_readout", false))
+    if (j.get_bool("has_field_coupling", false) || j.get_bool("single_layer_readout", false))
         throw std::invalid_argument("the model uses features outside the supported MACE path "
-                                    "(field coupling, first-interaction residual or single-layer readout)");
+                                    "(field coupling or single-layer readout)");
     // mace_kokkos_model.cpp:200 (required key), :1109 (optional key)
     A0_scaled = j.at("A0_scaled").as_bool();
     A1_scaled = j.get_bool("A1_scaled", false);
@@ -612,6 +634,45 @@ void HostModel::load(const std::string& path, const std::string& head) {
     if (H1_w.size() != static_cast<std::size_t>(L_max + 1) * Cs * Cs)
         throw std::invalid_argument("H1 weights have the wrong size");
     transpose_blocks(H1_w, H1_wt, L_max + 1, C, C);
+    if (pre_linear_up) {
+        const Value* pw = j.find("H1_product_weights");
+        if (!pw) throw std::invalid_argument("The pre_linear_up basis requires H1_product_weights.");
+        const auto P = pw->as_doubles();
+        if (P.size() != H1_w.size())
+            throw std::invalid_argument("The pre_linear_up basis requires H1_product_weights of the H1_weights extent.");
+        P0 = to_f32(std::vector<double>(P.begin(), P.begin() + Cs * Cs));
+        transpose_blocks(P0, P0t, 1, C, C);
+    }
+    if (residual) {
+        // fused[a][lm][out] = sum_in residual[a][lm][in] U_l[in][out]
+        // (mace.cpp:2809-2822; summed in FP64, rounded once)
+        const Value* uw = j.find("H1_linear_up_weights");
+        const Value* rw = j.find("H1_first_residual_weights");
+        if (!uw || !rw) throw std::invalid_argument("Residual-first MACE JSON requires split H1 weights.");
+        const auto U = uw->as_doubles();
+        const auto b = rw->as_doubles();
+        if (U.size() != H1_w.size()) throw std::invalid_argument("Residual-first MACE JSON requires split H1 weights.");
+        if (b.size() != static_cast<std::size_t>(num_elements) * num_LM * Cs)
+            throw std::invalid_argument("Residual-first MACE JSON has an invalid H1 residual extent.");
+        res_H1.assign(b.size(), 0.0f);
+        res_x.assign(static_cast<std::size_t>(num_elements) * Cs, 0.0f);
+        for (int a = 0; a < num_elements; ++a) {
+            for (int l = 0; l <= L_max; ++l)
+                for (int m = 0; m < 2 * l + 1; ++m) {
+                    const std::size_t row = static_cast<std::size_t>(a) * num_LM + l * l + m;
+                    for (int out = 0; out < C; ++out) {
+                        double s = 0.0;
+                        for (int in = 0; in < C; ++in)
+                            s += b[row * Cs + in] * U[(static_cast<std::size_t>(l) * Cs + in) * Cs + out];
+                        res_H1[row * Cs + out] = to_f32(s);
+                    }
+                }
+            for (int k = 0; k < C; ++k)
+                res_x[static_cast<std::size_t>(a) * Cs + k] = to_f32(b[static_cast<std::size_t>(a) * num_LM * Cs + k]);
+        }
+    } else if (j.contains("H1_first_residual_weights")) {
+        throw std::invalid_argument("Non-residual MACE JSON must not contain H1 residual weights.");
+    }
 
     // ---- R1 coupling (extract_mace_data.py:1326-1400 semantics)
     path_lo = j.at("Phi1_l").as_ints();
@@ -705,7 +766,7 @@ void HostModel::load(const std::string& path, const std::string& head) {
 
     // ---- H2 and readouts (mace.cpp:2516-2657, v4 m0_composite basis)
     {
-        const Value& t2 = j.at("H2_weights_for_M0");
+        const Value& t2 = j.at(skip_key);
         H2_T.assign(num_elements * Cs * Cs, 0.0f);
         for (int t = 0; t < num_elements; ++t) {
             const auto w = t2.at(t).as_doubles();
@@ -716,7 +777,7 @@ void HostModel::load(const std::string& path, const std::string& head) {
         H2_M1 = to_f32(j.at("H2_weights_for_M1").as_doubles());
         if (H2_M1.size() != Cs * Cs) throw std::invalid_argument("H2 M1 weights have the wrong size");
         transpose_blocks(H2_M1, H2_M1t, 1, C, C);
-        readout_q = j.at("readout_1_weights_for_M0").as_doubles();
+        readout_q = j.at(readout_key).as_doubles();
         readout_hidden = j.get_int("readout_2_hidden_size", 16);
         readout_W1 = j.at("readout_2_weights_1").as_doubles();
         readout_W2 = j.at("readout_2_weights_2").as_doubles();

@@ -96,6 +96,16 @@ struct HostModel {
     std::vector<float> m0_coef;                // [type][term][C]
 
     std::vector<float> H1_w, H1_wt;         // [l][C][C], l <= L_max
+    // h1_affine_mode "pre_linear_up" (h1_affine_schema.hpp:196-259,
+    // mace.cpp:1759-1810): the readout_1 / skip input is x = M0[:,0,:] P0,
+    // whose direct adjoint d enters M0_adj[:,0,:] as P0 d
+    bool pre_linear_up = false;
+    std::vector<float> P0, P0t;             // [C][C] H1_product_weights l = 0, [in][out] and [out][in]
+    // first_interaction_residual (mace.cpp:1843-1875, 2796-2826): per type,
+    // H1 += residual U (fused at load) and x += residual[lm 0]
+    bool residual = false;
+    std::vector<float> res_H1;              // [type][NH][C]
+    std::vector<float> res_x;               // [type][C]
 
     // R1 coupling
     std::vector<int> path_lo, path_le, path_ls;  // Phi1_l, Phi1_l1, Phi1_l2

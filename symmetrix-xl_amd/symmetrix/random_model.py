@@ -61,6 +61,13 @@ class ModelConfig:
     zbl: bool = False
     prediction_heads: bool = False
     agnesi: bool = False
+    # h1_affine_mode: "m0_composite", or "pre_linear_up" with split H1 weights
+    # (H1_product_weights P, H1_linear_up_weights U, H1_weights = P U) and the
+    # readout_1 / skip maps on the pre-linear_up scalar x = M0[:,0,:] P0
+    h1_mode: str = "m0_composite"
+    # first_interaction_residual (pre_linear_up only): per-type residual
+    # H1_first_residual_weights [type][LM][C]
+    residual: bool = False
     seed: int = 0
 
 
@@ -82,6 +89,12 @@ MODEL_CONFIGS = {
     # tiny with ZBL pair repulsion (zbl_kokkos.cpp)
     "tiny_zbl": ModelConfig("tiny_zbl", 32, 2, 1, 2, [8, 22, 38], radial_mlp=[32, 32],
                             r_cut=5.0, avg_num_neighbors=40.0, zbl=True),
+    # tiny in the pre_linear_up basis, without and with a first-interaction
+    # residual (h1_affine_schema.hpp:196-259; mace.cpp:1759-1875)
+    "tiny_plu": ModelConfig("tiny_plu", 32, 2, 1, 2, [8, 22, 38], radial_mlp=[32, 32],
+                            r_cut=5.0, avg_num_neighbors=40.0, h1_mode="pre_linear_up"),
+    "tiny_residual": ModelConfig("tiny_residual", 32, 2, 1, 2, [8, 22, 38], radial_mlp=[32, 32],
+                                 r_cut=5.0, avg_num_neighbors=40.0, h1_mode="pre_linear_up", residual=True),
     # 128x0e+128x1o, lmax 3, corr 3, 89 elements,
     # MLP [64,64,64], 6.0 A
     "medium": ModelConfig("medium", 128, 3, 1, 3, list(range(1, 90)),
@@ -158,7 +171,14 @@ def generate_model(config, seed=None):
 
     put("symmetrix_format_version", 4)
     put("model_type", "MACE")
-    put("h1_affine_mode", "m0_composite")
+    if cfg.h1_mode not in ("m0_composite", "pre_linear_up"):
+        raise ValueError("h1_mode must be m0_composite or pre_linear_up")
+    if cfg.residual and cfg.h1_mode != "pre_linear_up":
+        raise ValueError("a first-interaction residual needs the pre_linear_up basis")
+    if cfg.h1_mode == "pre_linear_up" and cfg.prediction_heads:
+        raise ValueError("prediction heads are generated for the m0_composite basis only")
+    pre = cfg.h1_mode == "pre_linear_up"
+    put("h1_affine_mode", cfg.h1_mode)
     put("h1_affine_version", 1)
     put("generator", {"name": "symmetrix-mi355x random_model", "config": cfg.name,
                       "seed": seed})
@@ -252,7 +272,20 @@ def generate_model(config, seed=None):
     del m0_weights
 
     # ---- H1 = product linear x interaction[1].linear_up, per l
-    frag["H1_weights"] = _fmt(rng.normal(size=(L_max + 1, C, C)) / math.sqrt(C))
+    h1 = rng.normal(size=(L_max + 1, C, C)) / math.sqrt(C)
+    if pre:
+        # split weights from their own generator (the other draws stay those
+        # of the m0_composite model of the same config)
+        prng = np.random.default_rng([seed, 3])
+        P = _f32(prng.normal(size=(L_max + 1, C, C)) / math.sqrt(C))
+        U = _f32(prng.normal(size=(L_max + 1, C, C)) / math.sqrt(C))
+        h1 = np.stack([P[l].astype(np.float64) @ U[l].astype(np.float64) for l in range(L_max + 1)])
+        frag["H1_product_weights"] = _fmt(P)
+        frag["H1_linear_up_weights"] = _fmt(U)
+        put("first_interaction_residual", bool(cfg.residual))
+        if cfg.residual:
+            frag["H1_first_residual_weights"] = _fmt(0.3 * prng.normal(size=(n_el, num_LM, C)))
+    frag["H1_weights"] = _fmt(h1)
 
     # ---- R1 coupling
     cpl = e3.r1_coupling(l_max, L_max)
@@ -278,14 +311,16 @@ def generate_model(config, seed=None):
             '"%d":%s' % (k, _fmt(coef1[0][t, k])) for k in range(C)) + "}"
         for t in range(n_el)) + "}"
 
-    # ---- H2 skip (T_z, [input][output]) and M1 linear
-    frag["H2_weights_for_M0"] = "[" + ",".join(
+    # ---- H2 skip (T_z, [input][output]) and M1 linear; in the pre_linear_up
+    # basis the skip and readout_1 act on x = M0[:,0,:] P0
+    skip_key = "H2_weights_for_H1_pre_linear_up" if pre else "H2_weights_for_M0"
+    frag[skip_key] = "[" + ",".join(
         _fmt(rng.normal(size=(C, C)) / math.sqrt(C)) for _ in range(n_el)) + "]"
     frag["H2_weights_for_M1"] = _fmt(rng.normal(size=(C, C)) / math.sqrt(C))
 
     # ---- readouts
     hid = cfg.readout_hidden
-    frag["readout_1_weights_for_M0"] = _fmt(
+    frag["readout_1_weights_for_H1_pre_linear_up" if pre else "readout_1_weights_for_M0"] = _fmt(
         rng.normal(size=C) / math.sqrt(C) * cfg.energy_scale)
     put("readout_2_hidden_size", hid)
     frag["readout_2_weights_1"] = _fmt(rng.normal(size=(hid, C)) / math.sqrt(C))

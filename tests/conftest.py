@@ -60,6 +60,18 @@ def tiny_heads_model_path():
 
 
 @pytest.fixture(scope="session")
+def tiny_plu_model_path():
+    from symmetrix import random_model
+    return random_model.cached_model("tiny_plu", directory=MODEL_DIR)
+
+
+@pytest.fixture(scope="session")
+def tiny_residual_model_path():
+    from symmetrix import random_model
+    return random_model.cached_model("tiny_residual", directory=MODEL_DIR)
+
+
+@pytest.fixture(scope="session")
 def tiny_agnesi_model_path():
     from symmetrix import random_model
     return random_model.cached_model("tiny_agnesi", directory=MODEL_DIR)

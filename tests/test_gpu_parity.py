@@ -175,6 +175,34 @@ def test_zbl_efs_and_tiled_plan(tiny_zbl_model_path):
     np.testing.assert_allclose(s1, st, rtol=0, atol=1e-9)
 
 
+@pytest.mark.parametrize("model", ["tiny_plu", "tiny_residual"])
+def test_pre_linear_up_basis_and_residual(request, model):
+    """The pre_linear_up H1 basis (x = M0[:,0,:] P0 for readout_1 and the H2
+    skip, its adjoint entering M0 as P0 d) and the first-interaction residual
+    (H1 += residual U, x += residual[lm 0]; mace.cpp:1759-1875) against the
+    oracle: H1, the adjoints, directed forces and E/F/S; the tiled plan
+    equals the direct one."""
+    from symmetrix.mace_kokkos import MACEKokkosFloat
+    path = request.getfixturevalue(model + "_model_path")
+    s = _system("tiny")
+    om, ref, ev, g, e, f, st = _evaluate_both(path, s)
+    for name in ("H1", "A1", "dPhi1", "H1_adj", "A0_adj"):
+        err = _stage_err(ev._stage(name).astype(np.float64), om.stage(name))
+        print(name, "relative max err %.3e" % err)
+        assert err < 1e-4, name
+    np.testing.assert_allclose(e, ref["energies"], rtol=0, atol=1e-4)
+    nf = ev.node_forces.reshape(-1, 3)
+    assert np.max(np.abs(nf - ref["node_forces"])) < 1e-5
+    _assert_efs(ref, e, f, st, len(e))
+    b = MACEKokkosFloat(path)
+    b.set_execution_plan_request("capacity", 64)
+    e1, f1, s1 = _run(b, s, om.types_of(s["numbers"]))
+    assert b.execution_plan.startswith("direct-tiled")
+    np.testing.assert_array_equal(e1, e)
+    np.testing.assert_allclose(f1, f, rtol=0, atol=1e-7)
+    np.testing.assert_allclose(s1, st, rtol=0, atol=1e-9)
+
+
 def test_prediction_heads(tiny_heads_model_path, tiny_model_path, tmp_path):
     """MACEKokkos(filename, head) (mace_kokkos.hpp:91; prediction_heads.hpp):
     the head's energies and readouts are used, selected_head and

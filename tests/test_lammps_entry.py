@@ -114,10 +114,10 @@ def _run(ev, hip, allpos, owner, alltypes, rows, ilist, type_to_model, rebuild):
 _ROWS = {}  # (model, plan, step) -> LAMMPS force rows, for the cross-plan check
 
 
-@pytest.mark.parametrize("model", ["tiny", "tiny_scaled", "tiny_zbl", "tiny_agnesi"])
+@pytest.mark.parametrize("model", ["tiny", "tiny_scaled", "tiny_zbl", "tiny_agnesi", "tiny_residual"])
 @pytest.mark.parametrize("tile", [None, 32], ids=["direct", "tiled32"])
 def test_lammps_entry_matches_oracle(request, model, tile):
-    # plain, density-scaled, ZBL and Agnesi (per-pair tables) models
+    # plain, density-scaled, ZBL, Agnesi (per-pair tables) and residual-first models
     tiny_model_path = request.getfixturevalue(model + "_model_path")
     from oracle import oracle
     from symmetrix import systems
