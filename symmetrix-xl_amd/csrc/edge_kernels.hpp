@@ -26,6 +26,7 @@
 #include <cstdint>
 
 #include "device_common.hpp"
+#include "coupling_rows.hpp"
 #include "shapes.hpp"
 
 namespace smx {
@@ -401,31 +402,54 @@ struct EdgeForceSink {
 // are disjoint, so each source-adjoint component W[lm2] comes from exactly one
 // pass; Phi1 and the forces are sums over the passes.
 // ---------------------------------------------------------------------------
+// Only live rows are kept: rows whose real-basis 3j coefficients vanish for
+// every output m (coupling_rows.hpp; the loader refuses a model with a term
+// in such a row) contribute nothing to Phi1, G or W, and are neither held in
+// registers nor accumulated.
 template <int LMAX, int LMAXH, unsigned MASK>
 struct RowGroup {
     using S = Shape<LMAX, LMAXH>;
     static constexpr bool in(int p, int m2) {
         return ((MASK >> (S::paths[p].ls * S::paths[p].ls + m2)) & 1u) != 0;
     }
-    static constexpr int m2_count(int p) {
+    // row (p, m1, m2) is in the group and carries coupling coefficients
+    static constexpr bool live(int p, int m1, int m2) {
+        return in(p, m2) && coupling_live(S::paths[p].le, S::paths[p].ls, S::paths[p].lo, m1, m2);
+    }
+    static constexpr int live_count(int p) {
         int n = 0;
-        for (int m2 = 0; m2 < 2 * S::paths[p].ls + 1; ++m2) n += in(p, m2) ? 1 : 0;
+        for (int m1 = 0; m1 < 2 * S::paths[p].le + 1; ++m1)
+            for (int m2 = 0; m2 < 2 * S::paths[p].ls + 1; ++m2) n += live(p, m1, m2) ? 1 : 0;
         return n;
     }
-    static constexpr int m2_rank(int p, int m2) {
-        int n = 0;
-        for (int q = 0; q < m2; ++q) n += in(p, q) ? 1 : 0;
-        return n;
+    static constexpr bool used(int p) { return live_count(p) > 0; }
+    static constexpr bool m1_live(int p, int m1) {
+        for (int m2 = 0; m2 < 2 * S::paths[p].ls + 1; ++m2)
+            if (live(p, m1, m2)) return true;
+        return false;
     }
-    static constexpr bool used(int p) { return m2_count(p) > 0; }
+    static constexpr bool m2_live(int p, int m2) {
+        for (int m1 = 0; m1 < 2 * S::paths[p].le + 1; ++m1)
+            if (live(p, m1, m2)) return true;
+        return false;
+    }
     static constexpr std::array<int, S::P + 1> make_base() {
         std::array<int, S::P + 1> b{};
-        for (int p = 0; p < S::P; ++p) b[p + 1] = b[p] + (2 * S::paths[p].le + 1) * m2_count(p);
+        for (int p = 0; p < S::P; ++p) b[p + 1] = b[p] + live_count(p);
         return b;
     }
     static constexpr std::array<int, S::P + 1> base = make_base();
     static constexpr int NR = base[S::P] > 0 ? base[S::P] : 1;
-    static constexpr int row(int p, int m1, int m2) { return base[p] + m1 * m2_count(p) + m2_rank(p, m2); }
+    // register index of a live row: its rank among path p's live rows
+    static constexpr int row(int p, int m1, int m2) {
+        int n = 0;
+        for (int a = 0; a < 2 * S::paths[p].le + 1; ++a)
+            for (int b = 0; b < 2 * S::paths[p].ls + 1; ++b) {
+                if (a == m1 && b == m2) return base[p] + n;
+                n += live(p, a, b) ? 1 : 0;
+            }
+        return -1;
+    }
     static constexpr bool component(int lm2) { return ((MASK >> lm2) & 1u) != 0; }
 };
 
@@ -487,20 +511,24 @@ __global__ __launch_bounds__(C) void k_r1_forward(int r0, const int* __restrict_
                     const float rh = rad * h[0];
                     static_for<0, 2 * le + 1>([&](auto m1c) {
                         constexpr int m1 = m1c;
-                        constexpr int r = RG::row(p, m1, 0);
-                        rows[r] += rh * Y(le * le + m1);
+                        if constexpr (RG::live(p, m1, 0)) {
+                            constexpr int r = RG::row(p, m1, 0);
+                            rows[r] += rh * Y(le * le + m1);
+                        }
                     });
                 } else {
                     static_for<0, 2 * le + 1>([&](auto m1c) {
                         constexpr int m1 = m1c;
-                        const float ry = rad * Y(le * le + m1);
-                        static_for<0, 2 * ls + 1>([&](auto m2c) {
-                            constexpr int m2 = m2c;
-                            if constexpr (RG::in(p, m2)) {
-                                constexpr int r = RG::row(p, m1, m2);
-                                rows[r] += ry * h[ls * ls + m2];
-                            }
-                        });
+                        if constexpr (RG::m1_live(p, m1)) {
+                            const float ry = rad * Y(le * le + m1);
+                            static_for<0, 2 * ls + 1>([&](auto m2c) {
+                                constexpr int m2 = m2c;
+                                if constexpr (RG::live(p, m1, m2)) {
+                                    constexpr int r = RG::row(p, m1, m2);
+                                    rows[r] += ry * h[ls * ls + m2];
+                                }
+                            });
+                        }
                     });
                 }
             }
@@ -554,7 +582,7 @@ __global__ __launch_bounds__(C) void k_r1_forward(int r0, const int* __restrict_
                     constexpr int m1 = m1c;
                     static_for<0, 2 * ls + 1>([&](auto m2c) {
                         constexpr int m2 = m2c;
-                        if constexpr (RG::in(p, m2)) {
+                        if constexpr (RG::live(p, m1, m2)) {
                             constexpr int r = RG::row(p, m1, m2);
                             o += cg[co + (m1 * (2 * ls + 1) + m2) * (2 * lo + 1) + mo] * rows[r];
                         }
@@ -609,7 +637,7 @@ __global__ __launch_bounds__(C) void k_r1_reverse(int r0, long long e0, const in
                         constexpr int m1 = m1c;
                         static_for<0, 2 * ls + 1>([&](auto m2c) {
                             constexpr int m2 = m2c;
-                            if constexpr (RG::in(p, m2)) {
+                            if constexpr (RG::live(p, m1, m2)) {
                                 constexpr int r = RG::row(p, m1, m2);
                                 G[r] += cg[co + (m1 * (2 * ls + 1) + m2) * (2 * lo + 1) + mo] * dq;
                             }
@@ -658,32 +686,36 @@ __global__ __launch_bounds__(C) void k_r1_reverse(int r0, long long e0, const in
                         const float rh = R * h[0];
                         static_for<0, 2 * le + 1>([&](auto m1c) {
                             constexpr int m1 = m1c;
-                            constexpr int r = RG::row(p, m1, 0);
-                            const float g = G[r];
-                            T[0] += edges.Y(pt, le * le + m1) * g;
-                            SB[le * le + m1] += rh * g;
+                            if constexpr (RG::live(p, m1, 0)) {
+                                constexpr int r = RG::row(p, m1, 0);
+                                const float g = G[r];
+                                T[0] += edges.Y(pt, le * le + m1) * g;
+                                SB[le * le + m1] += rh * g;
+                            }
                         });
                     } else {
                         static_for<0, 2 * le + 1>([&](auto m1c) {
                             constexpr int m1 = m1c;
-                            const float y = edges.Y(pt, le * le + m1);
-                            float sr = 0.0f;
-                            static_for<0, 2 * ls + 1>([&](auto m2c) {
-                                constexpr int m2 = m2c;
-                                if constexpr (RG::in(p, m2)) {
-                                    constexpr int r = RG::row(p, m1, m2);
-                                    const float g = G[r];
-                                    T[m2] += y * g;
-                                    sr += g * h[ls * ls + m2];
-                                }
-                            });
-                            SB[le * le + m1] += R * sr;
+                            if constexpr (RG::m1_live(p, m1)) {
+                                const float y = edges.Y(pt, le * le + m1);
+                                float sr = 0.0f;
+                                static_for<0, 2 * ls + 1>([&](auto m2c) {
+                                    constexpr int m2 = m2c;
+                                    if constexpr (RG::live(p, m1, m2)) {
+                                        constexpr int r = RG::row(p, m1, m2);
+                                        const float g = G[r];
+                                        T[m2] += y * g;
+                                        sr += g * h[ls * ls + m2];
+                                    }
+                                });
+                                SB[le * le + m1] += R * sr;
+                            }
                         });
                     }
                     float hT = 0.0f;
                     static_for<0, 2 * ls + 1>([&](auto m2c) {
                         constexpr int m2 = m2c;
-                        if constexpr (RG::in(p, m2)) {
+                        if constexpr (RG::m2_live(p, m2)) {
                             W[ls * ls + m2] += R * T[m2];
                             hT += h[ls * ls + m2] * T[m2];
                         }

@@ -25,6 +25,7 @@
 #include <map>
 #include <stdexcept>
 
+#include "coupling_rows.hpp"
 #include "json_lite.hpp"
 #include "model_binary.hpp"
 
@@ -722,6 +723,12 @@ void HostModel::load(const std::string& path, const std::string& head) {
             if (rel < 0 || rel >= (2 * lo + 1) * num_e[lo] || rel % num_e[lo] != e_of[q])
                 throw std::invalid_argument("R1 coupling output index does not match its path");
             const int mo = rel / num_e[lo];
+            // the R1 kernels hold only rows with real-basis 3j coefficients
+            // (coupling_rows.hpp); a term anywhere else has no kernel
+            if (cg[t] != 0.0 && (path_le[q] > kCouplingLMax || ls > kCouplingLMax || lo > kCouplingLMax ||
+                                 !coupling_live(path_le[q], ls, lo, m1, m2)))
+                throw std::domain_error("the model's R1 coupling has a term in a row whose real-basis 3j "
+                                        "coefficients are zero; no compiled kernel holds that row");
             float& dst = cg_dense[cg_offset[q] + ((m1 * (2 * ls + 1) + m2) * (2 * lo + 1) + mo)];
             // repeated (row, lme) terms accumulate like the reference's term loop
             dst = to_f32(static_cast<double>(dst) + cg[t]);
