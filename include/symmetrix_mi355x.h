@@ -121,8 +121,9 @@ SMX_API int32_t smx_prepare_periodic_factorized_graph(SmxEvaluator* ev, int32_t 
                                                       uint64_t* generation, int64_t* num_edges);
 /* Plan shorthand with the tile size (no single counterpart; the receiver
  * tile limit is mace_kokkos.hpp:542's 32768): "speed" = the speed profile,
- * "capacity" = the three-sweep tiled plan pinned (the reference's dual-layer
- * tiled plan, mace_kokkos_evaluate.cpp:755-1148) with at most tile_receivers
+ * "capacity" = the model's tiled plan pinned (the reference's dual-layer
+ * tiled plan, mace_kokkos_evaluate.cpp:755-1148, three sweeps; for a
+ * one-interaction model its single-layer tiled plan, :614-752, one sweep) with at most tile_receivers
  * receivers per tile, "auto" = the capacity profile with fixed workspaces
  * allowed.  tile_receivers 0 keeps the current limit.  Applies to graphs
  * prepared afterwards. */
@@ -135,7 +136,10 @@ SMX_API int32_t smx_execution_plan(SmxEvaluator* ev, char* out, int64_t capacity
  * ("factorized" and "direct_streamed" are its aliases), profile "capacity"
  * (the reference's default) or "speed", debug_plan "" (planner) or one of
  * "mh0-direct-speed", "mh0-direct-capacity-retained",
- * "mh0-dual-layer-tiled-v1" to pin a plan.  Under "capacity" the planner
+ * "mh0-dual-layer-tiled-v1" (two-interaction models) or
+ * "mh0-single-layer-tiled-v1" (one-interaction models; a tiled plan pinned
+ * for the other model kind is refused when the graph is prepared,
+ * mace_kokkos_runtime.cpp:2996-3030) to pin a plan.  Under "capacity" the planner
  * selects the tiled plan only when fixed workspaces are allowed and the
  * retained workspace would exceed 70% of the available device memory.
  * Applies to graphs prepared afterwards. */

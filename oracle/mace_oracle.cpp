@@ -17,7 +17,8 @@
 //     :1356-2657 (A0 :1356-1403, reverse A0 :1486-1560, M0 :1639-1689,
 //     H1 :1691-1757, v4 affine capture :1759-1814, Phi1 :2023-2084,
 //     reverse Phi1 :2199-2303, A1 :2305-2379, M1 :2461-2514, H2 :2516-2620,
-//     readouts :2622-2657), with the Kokkos evaluator's precision policy
+//     readouts :2622-2657; one-interaction models :255-281 with M1 over
+//     the H1 components :2461-2514), with the Kokkos evaluator's precision policy
 //     (FP64 H2, readouts, node energies, directed forces, and the FP64
 //     accumulation of the FP32 source adjoint: mace_kokkos.hpp:501,907-909,
 //     1805-1828)
@@ -494,6 +495,10 @@ struct Mace {
     // first_interaction_residual (mace.cpp:1843-1875, 2796-2826): H1 +=
     // fused[type] (the residual through linear_up), x += residual[type][lm 0]
     bool residual = false;
+    // single_layer_readout (mace.cpp:255-281, 2461-2514, 2676-2679): one
+    // interaction; M1 is taken of H1 (its num_LM components) instead of A1,
+    // so there is no R1, Phi1 or A1, and the M1 adjoint is H1's adjoint
+    bool single_layer = false;
     std::vector<P> res_fused;               // [type][LM][C]
     std::vector<P> res_x;                   // [type][C]
     std::vector<int> Phi1_l, Phi1_l1, Phi1_l2, Phi1_lme, Phi1_row;
@@ -575,11 +580,17 @@ struct Mace {
             throw std::invalid_argument("h1_affine_mode must be 'm0_composite' or 'pre_linear_up'");
         pre_linear_up = h1_mode == "pre_linear_up";
         residual = j.get_bool("first_interaction_residual", false);
-        if (residual && !pre_linear_up)
+        single_layer = j.get_bool("single_layer_readout", false);
+        // h1_affine_schema.hpp:227-237, mace.cpp:2676-2679
+        if (j.get_int("num_interactions", 2) != (single_layer ? 1 : 2))
+            throw std::invalid_argument("interaction count and single-layer readout metadata disagree");
+        if (residual && !pre_linear_up && !single_layer)
             throw std::invalid_argument("a first-interaction residual needs h1_affine_mode 'pre_linear_up'");
+        if (pre_linear_up && single_layer)
+            throw std::invalid_argument("the pre_linear_up basis applies to two-interaction models only");
         if (j.get_string("radial_representation", "") != "compact")
             throw std::invalid_argument("only the compact radial representation is supported");
-        if (j.get_bool("has_field_coupling", false) || j.get_bool("single_layer_readout", false))
+        if (j.get_bool("has_field_coupling", false))
             throw std::invalid_argument("model features outside the supported MACE path");
         num_elements = j.at("num_elements").as_int();
         C = j.at("num_channels").as_int();
@@ -602,6 +613,9 @@ struct Mace {
         A1_scaled = j.get_bool("A1_scaled", false);
         if (A0_scaled != radial.has_A0) throw std::invalid_argument("compact radial A0 network does not match A0_scaled");
         if (A1_scaled != radial.has_A1) throw std::invalid_argument("compact radial A1 network does not match A1_scaled");
+        if (radial.has_R1 == single_layer)
+            throw std::invalid_argument("compact radial R1 network does not match the interaction count");
+        if (single_layer && A1_scaled) throw std::invalid_argument("a one-interaction model has no A1 to scale");
         H0 = castv(j.at("H0_weights").as_doubles());
         const Value& a0 = j.at("A0_weights");
         A0_w.resize(num_elements);
@@ -659,12 +673,14 @@ struct Mace {
                     b[static_cast<std::size_t>(a) * LM * C + k];
             }
         }
-        Phi1_l = j.at("Phi1_l").as_ints();
-        Phi1_l1 = j.at("Phi1_l1").as_ints();
-        Phi1_l2 = j.at("Phi1_l2").as_ints();
-        Phi1_lme = j.at("Phi1_lme").as_ints();
-        Phi1_row = j.at("Phi1_lelm1lm2").as_ints();
-        Phi1_cg = castv(j.at("Phi1_clebsch_gordan").as_doubles());
+        if (!single_layer) {
+            Phi1_l = j.at("Phi1_l").as_ints();
+            Phi1_l1 = j.at("Phi1_l1").as_ints();
+            Phi1_l2 = j.at("Phi1_l2").as_ints();
+            Phi1_lme = j.at("Phi1_lme").as_ints();
+            Phi1_row = j.at("Phi1_lelm1lm2").as_ints();
+            Phi1_cg = castv(j.at("Phi1_clebsch_gordan").as_doubles());
+        }
         num_lme = 0;
         for (int l : Phi1_l) num_lme += 2 * l + 1;
         num_rows = 0;
@@ -673,12 +689,19 @@ struct Mace {
         for (int l : Phi1_l) num_e[l] += 1;
         lme_base.assign(l_max + 2, 0);
         for (int l = 0; l <= l_max; ++l) lme_base[l + 1] = lme_base[l] + (2 * l + 1) * num_e[l];
-        const Value& a1 = j.at("A1_weights");
-        for (int l = 0; l <= l_max; ++l) A1_w.push_back(castv(a1.at(l).as_doubles()));
-        // M1
+        if (!single_layer) {
+            const Value& a1 = j.at("A1_weights");
+            for (int l = 0; l <= l_max; ++l) A1_w.push_back(castv(a1.at(l).as_doubles()));
+        }
+        // M1: variables are A1's num_lm components, or H1's num_LM ones
         const Value& m1m = j.at("M1_monomials");
         std::vector<std::vector<int>> monos1;
-        for (std::size_t i = 0; i < m1m.size(); ++i) monos1.push_back(m1m.at(i).as_ints());
+        const int m1_vars = single_layer ? num_LM : num_lm;
+        for (std::size_t i = 0; i < m1m.size(); ++i) {
+            monos1.push_back(m1m.at(i).as_ints());
+            for (int v : monos1.back())
+                if (v < 0 || v >= m1_vars) throw std::invalid_argument("M1 monomial variable out of range");
+        }
         M1_monos = dedupe_monomials(monos1);
         const int T1 = static_cast<int>(M1_monos.monos.size());
         const Value& m1w = j.at("M1_weights");
@@ -742,9 +765,11 @@ struct Mace {
                     const int ti = req[a], tj = req[b];
                     std::vector<std::vector<double>> v0, d0, v1, d1;
                     radial.tabulate(radial.R0, v0, d0, ti, tj);
-                    radial.tabulate(radial.R1, v1, d1, ti, tj);
                     spl0.push_back(std::make_shared<SplineSet<P>>(hp, tof(v0), tof(d0), x0));
-                    spl1.push_back(std::make_shared<SplineSet<P>>(hp, tof(v1), tof(d1), x0));
+                    if (radial.has_R1) {
+                        radial.tabulate(radial.R1, v1, d1, ti, tj);
+                        spl1.push_back(std::make_shared<SplineSet<P>>(hp, tof(v1), tof(d1), x0));
+                    }
                     // RadialFunctionSetKokkos<double>(h, values, derivs, x0): FP64
                     // coefficients and evaluation (mace_kokkos_factorized_lifecycle.cpp:4084-4091)
                     if (A0_scaled) {
@@ -759,7 +784,7 @@ struct Mace {
                     }
                 } else {
                     spl0.push_back(spl0.front());
-                    spl1.push_back(spl1.front());
+                    if (radial.has_R1) spl1.push_back(spl1.front());
                     if (A0_scaled) dens0.push_back(dens0.front());
                     if (A1_scaled) dens1.push_back(dens1.front());
                 }
@@ -949,7 +974,10 @@ struct Mace {
                     for (int k = 0; k < C; ++k)
                         H1[(static_cast<std::size_t>(i) * num_LM + lm) * Cs + k] +=
                             res_fused[(static_cast<std::size_t>(t) * num_LM + lm) * C + k];
-                for (int k = 0; k < C; ++k) xaff[i * Cs + k] += res_x[static_cast<std::size_t>(t) * C + k];
+                // the scalar input takes the residual in the pre_linear_up
+                // basis only (mace.cpp:1863-1872)
+                if (pre_linear_up)
+                    for (int k = 0; k < C; ++k) xaff[i * Cs + k] += res_x[static_cast<std::size_t>(t) * C + k];
             }
         }
 
@@ -958,6 +986,7 @@ struct Mace {
         std::vector<int> row_base(np);
         for (int p = 0; p < np; ++p) row_base[p] = row_base_of_path(p);
         Phi1.assign(static_cast<std::size_t>(n) * num_lme * Cs, P(0));
+        if (!single_layer) {
 #pragma omp parallel for schedule(dynamic, 16)
         for (int i = 0; i < n; ++i) {
             std::vector<P> rows(static_cast<std::size_t>(num_rows) * Cs, P(0)), rad(Cs);
@@ -994,9 +1023,11 @@ struct Mace {
                 for (int k = 0; k < C; ++k) dst[k] += c * src[k];
             }
         }
+        }
 
         // ---- A1 (mace.cpp:2305-2341)
-        A1.assign(static_cast<std::size_t>(n) * nY * Cs, P(0));
+        A1.assign(single_layer ? 0 : static_cast<std::size_t>(n) * nY * Cs, P(0));
+        if (!single_layer) {
 #pragma omp parallel for schedule(static)
         for (int i = 0; i < n; ++i) {
             for (int l = 0; l <= l_max; ++l) {
@@ -1024,24 +1055,31 @@ struct Mace {
                 for (std::size_t v = 0; v < nY * Cs; ++v) a[v] *= inv;
             }
         }
+        }
 
-        // ---- M1, H2, readouts, reverse H2 / M1 (mace.cpp:2461-2657)
+        // ---- M1, H2, readouts, reverse H2 / M1 (mace.cpp:2461-2657).  M1's
+        // variables are A1's num_lm components or, with one interaction, H1's
+        // num_LM ones; their adjoint is A1_adj or H1_adj.
         const int T1 = static_cast<int>(M1_monos.monos.size());
+        const int nV = single_layer ? num_LM : nY;
+        const std::vector<P>& m1_in = single_layer ? H1 : A1;
+        std::vector<P>& m1_in_adj = single_layer ? H1_adj : A1_adj;
         M1.assign(static_cast<std::size_t>(n) * Cs, P(0));
-        M1_grad.assign(static_cast<std::size_t>(n) * nY * Cs, P(0));
+        M1_grad.assign(static_cast<std::size_t>(n) * nV * Cs, P(0));
         H2.assign(static_cast<std::size_t>(n) * Cs, 0.0);
         H2_adj.assign(static_cast<std::size_t>(n) * Cs, 0.0);
         direct.assign(static_cast<std::size_t>(n) * Cs, 0.0);
         node_energies.assign(n, 0.0);
-        A1_adj.assign(static_cast<std::size_t>(n) * nY * Cs, P(0));
+        A1_adj.assign(single_layer ? 0 : static_cast<std::size_t>(n) * nY * Cs, P(0));
+        if (single_layer) H1_adj.assign(static_cast<std::size_t>(n) * num_LM * Cs, P(0));
 #pragma omp parallel for schedule(static)
         for (int i = 0; i < n; ++i) {
             P x[16], g[16];
             const int t = types[i];
             for (int k = 0; k < C; ++k) {
-                for (int v = 0; v < nY; ++v) x[v] = A1[(static_cast<std::size_t>(i) * nY + v) * Cs + k];
-                M1[i * Cs + k] = poly_eval_grad<P>(M1_monos, M1_coef[t].data() + static_cast<std::size_t>(k) * T1, x, g, nY);
-                for (int v = 0; v < nY; ++v) M1_grad[(static_cast<std::size_t>(i) * nY + v) * Cs + k] = g[v];
+                for (int v = 0; v < nV; ++v) x[v] = m1_in[(static_cast<std::size_t>(i) * nV + v) * Cs + k];
+                M1[i * Cs + k] = poly_eval_grad<P>(M1_monos, M1_coef[t].data() + static_cast<std::size_t>(k) * T1, x, g, nV);
+                for (int v = 0; v < nV; ++v) M1_grad[(static_cast<std::size_t>(i) * nV + v) * Cs + k] = g[v];
             }
             double* h2 = &H2[i * Cs];
             for (int o = 0; o < C; ++o) {
@@ -1080,9 +1118,9 @@ struct Mace {
                 }
                 direct[i * Cs + in] = s;
                 const P m1adj = static_cast<P>(s1);
-                for (int v = 0; v < nY; ++v)
-                    A1_adj[(static_cast<std::size_t>(i) * nY + v) * Cs + in] =
-                        M1_grad[(static_cast<std::size_t>(i) * nY + v) * Cs + in] * m1adj;
+                for (int v = 0; v < nV; ++v)
+                    m1_in_adj[(static_cast<std::size_t>(i) * nV + v) * Cs + in] =
+                        M1_grad[(static_cast<std::size_t>(i) * nV + v) * Cs + in] * m1adj;
             }
         }
 
@@ -1113,6 +1151,9 @@ struct Mace {
 
         // ---- reverse A1 (mace.cpp:2343-2379)
         dPhi1.assign(static_cast<std::size_t>(n) * num_lme * Cs, P(0));
+        node_forces.assign(static_cast<std::size_t>(E) * 3, 0.0);
+        node_forces_r1 = node_forces;
+        if (!single_layer) {
 #pragma omp parallel for schedule(static)
         for (int i = 0; i < n; ++i) {
             for (int l = 0; l <= l_max; ++l) {
@@ -1135,7 +1176,6 @@ struct Mace {
 
         // ---- reverse Phi1 (mace.cpp:2199-2303): receiver-owned edge forces,
         // source adjoint via the source transpose (FP64 accumulation).
-        node_forces.assign(static_cast<std::size_t>(E) * 3, 0.0);
         std::vector<P> dPhi1r(static_cast<std::size_t>(n) * num_rows * Cs, P(0));
 #pragma omp parallel for schedule(static)
         for (int i = 0; i < n; ++i) {
@@ -1227,6 +1267,7 @@ struct Mace {
             }
             for (int v = 0; v < num_LM * C; ++v)
                 H1_adj[static_cast<std::size_t>(s) * num_LM * Cs + v] = static_cast<P>(acc[v]);
+        }
         }
 
         // ---- reverse H1 + direct adjoint (mace.cpp:1727-1757, 1785-1814)

@@ -295,8 +295,10 @@ struct Evaluator {
         // zero extra channels (every cross-lane sum then spans whole waves)
         if (hm.C > 32 && hm.C % 64 != 0 && hm.C % 16 == 0) hm.pad_channels((hm.C + 63) / 64 * 64);
         std::vector<int> le, ls, lo;
-        if (!kernel_paths(hm.l_max, hm.L_max, le, ls, lo) || le != hm.path_le || ls != hm.path_ls ||
-            lo != hm.path_lo)
+        // a one-interaction model has no R1 paths; the kernel set of its
+        // (l_max, L_max) serves its layer 1 and readout
+        if (!kernel_paths(hm.l_max, hm.L_max, le, ls, lo) ||
+            (!hm.single_layer && (le != hm.path_le || ls != hm.path_ls || lo != hm.path_lo)))
             throw std::domain_error("the model's R1 paths have no compiled kernel set (l_max " +
                                     std::to_string(hm.l_max) + ", L_max " + std::to_string(hm.L_max) + ")");
         if (hm.readout_hidden > kMaxReadoutHidden)
@@ -381,6 +383,7 @@ struct Evaluator {
         dm.H1_wt = put(swizzled(hm.H1_wt, hm.L_max + 1, hm.C, hm.C));
         dm.pre_linear_up = hm.pre_linear_up;
         dm.residual = hm.residual;
+        dm.single_layer = hm.single_layer;
         if (hm.pre_linear_up) {
             dm.P0_w = put(swizzled(hm.P0, 1, hm.C, hm.C));
             dm.P0_wt = put(swizzled(hm.P0t, 1, hm.C, hm.C));
@@ -483,14 +486,20 @@ struct Evaluator {
     // Bytes of the untiled plan for a graph (workspace high-water).
     std::size_t untiled_bytes(std::int64_t n, std::int64_t e) const {
         const std::size_t C = hm.C, NY = hm.num_lm, NH = hm.num_LM, NLME = hm.num_lme;
-        const std::size_t node = (6 * NY + 4 * NH + 2 * NLME + 3) * C * 4 + 200;
-        const std::size_t edge = (ks->record_floats() + NH * C) * 4 + 24 + 32 + 24;
+        const std::size_t node = ((two_layer() ? 6 : 4) * NY + 4 * NH + 2 * NLME + 3) * C * 4 + 200;
+        const std::size_t edge = (ks->record_floats() + (two_layer() ? NH * C : 0)) * 4 + 24 + 32 + 24;
         return node * n + edge * e;
     }
+
+    bool two_layer() const { return !hm.single_layer; }
 
     static constexpr const char* kPlanSpeed = "mh0-direct-speed";
     static constexpr const char* kPlanRetained = "mh0-direct-capacity-retained";
     static constexpr const char* kPlanTiled = "mh0-dual-layer-tiled-v1";
+    static constexpr const char* kPlanSingleTiled = "mh0-single-layer-tiled-v1";
+    // the tiled plan of this model: three sweeps (two interactions) or one
+    // (one interaction, mace_kokkos_evaluate.cpp:614-752)
+    const char* tiled_plan() const { return two_layer() ? kPlanTiled : kPlanSingleTiled; }
 
     // Bytes of the tiled plan: graph-wide node state plus one tile's workspace.
     std::size_t tiled_bytes(std::int64_t n, std::int64_t e) const {
@@ -498,8 +507,8 @@ struct Evaluator {
         const std::size_t nt = std::min<std::int64_t>(n, tile_limit);
         const std::size_t et = n > 0 ? static_cast<std::size_t>(static_cast<double>(e) * nt / n) + 1 : 0;
         const std::size_t graph = (2 * NH + 2) * C * 4 * n + 56 * n + 20 * e;
-        const std::size_t tile = (6 * NY + 4 * NH + 2 * NLME + 3) * C * 4 * nt +
-                                 ((ks->record_floats() + NH * C) * 4 + 24 + 32 + 24) * et;
+        const std::size_t tile = ((two_layer() ? 6 : 4) * NY + 4 * NH + 2 * NLME + 3) * C * 4 * nt +
+                                 ((ks->record_floats() + (two_layer() ? NH * C : 0)) * 4 + 24 + 32 + 24) * et;
         return graph + tile;
     }
 
@@ -509,7 +518,12 @@ struct Evaluator {
         plan_available = free_b + workspace_bytes();
         plan_untiled = untiled_bytes(N, E);
         plan_tiled = tiled_bytes(N, E);
-        if (debug_plan == kPlanTiled) {
+        // mace_kokkos_runtime.cpp:2996-3030: each tiled plan admits its own model kind
+        if (debug_plan == kPlanTiled && !two_layer())
+            throw std::invalid_argument("mh0-dual-layer-tiled-v1 requires an ordinary two-layer MACE model");
+        if (debug_plan == kPlanSingleTiled && two_layer())
+            throw std::invalid_argument("mh0-single-layer-tiled-v1 requires single_layer_readout=true");
+        if (debug_plan == kPlanTiled || debug_plan == kPlanSingleTiled) {
             tiled = true;
             plan_source = "debug_plan";
             plan_reason = "pinned by the debug plan request";
@@ -531,14 +545,14 @@ struct Evaluator {
             plan_reason = tiled ? "the retained workspace exceeds 70% of the available device memory"
                                 : "the retained workspace fits 70% of the available device memory";
         }
-        if (N <= tile_limit && debug_plan != kPlanTiled && tiled) {
+        if (N <= tile_limit && debug_plan != tiled_plan() && tiled) {
             tiled = false;
             plan_reason = "the graph fits one receiver tile";
         }
     }
 
     const char* selected_plan() const {
-        if (tiled) return kPlanTiled;
+        if (tiled) return tiled_plan();
         return request_profile == "speed" || debug_plan == kPlanSpeed ? kPlanSpeed : kPlanRetained;
     }
 
@@ -572,11 +586,11 @@ struct Evaluator {
         o += "{\"id\":\"" + std::string(request_profile == "speed" ? kPlanSpeed : kPlanRetained) +
              "\",\"qualified\":true,\"estimated_bytes\":" + std::to_string(plan_untiled) +
              ",\"reason\":\"every edge's workspace retained\"},";
-        o += "{\"id\":\"" + std::string(kPlanTiled) + "\",\"qualified\":" +
-             std::string(allow_fixed || debug_plan == kPlanTiled ? "true" : "false") +
-             ",\"estimated_bytes\":" + std::to_string(plan_tiled) +
-             ",\"reason\":\"three sweeps over receiver tiles of at most " + std::to_string(tile_limit) +
-             " receivers\"}]}";
+        o += "{\"id\":\"" + std::string(tiled_plan()) + "\",\"qualified\":" +
+             std::string(allow_fixed || debug_plan == tiled_plan() ? "true" : "false") +
+             ",\"estimated_bytes\":" + std::to_string(plan_tiled) + ",\"reason\":\"" +
+             std::string(two_layer() ? "three sweeps" : "one sweep") + " over receiver tiles of at most " +
+             std::to_string(tile_limit) + " receivers\"}]}";
         return o;
     }
 
@@ -735,12 +749,14 @@ struct Evaluator {
         ws.Phi0 = f(w_Phi0, tn * NY * C);
         ws.A0 = f(w_A0, tn * NY * C);
         ws.M0 = f(w_M0, tn * NH * C);
-        ws.Phi1 = f(w_Phi1, tn * NLME * C);
-        ws.A1 = f(w_A1, tn * NY * C);
-        ws.A1_adj = f(w_A1_adj, tn * NY * C);
+        // (no Phi1, A1 or per-edge source terms with one interaction)
+        const std::size_t two = two_layer() ? 1 : 0;
+        ws.Phi1 = f(w_Phi1, two * tn * NLME * C);
+        ws.A1 = f(w_A1, two * tn * NY * C);
+        ws.A1_adj = f(w_A1_adj, two * tn * NY * C);
         ws.M1 = f(w_M1, tn * C);
-        ws.dPhi1 = f(w_dPhi1, tn * NLME * C);
-        ws.Wsrc = f(w_Wsrc, te * NH * C);
+        ws.dPhi1 = f(w_dPhi1, two * tn * NLME * C);
+        ws.Wsrc = f(w_Wsrc, two * te * NH * C);
         ws.M0_adj = f(w_M0_adj, tn * NH * C);
         ws.A0_adj = f(w_A0_adj, tn * NY * C);
         ws.Phi0_adj = f(w_Phi0_adj, tn * NY * C);
@@ -965,8 +981,8 @@ struct Evaluator {
     }
     const double* tile_r(const TileView& t) const { return xyz_host ? d_r.as<double>() + t.e0 : d_r.as<double>(); }
 
-    // xyz, r and per-edge records of one tile
-    void tile_geometry(const TileView& t, const double* positions) {
+    // xyz, r and (with records) per-edge records of one tile
+    void tile_geometry(const TileView& t, const double* positions, bool records = true) {
         LaunchTimer* tm = timer.get();
         if (lmp) {
             if (tm) tm->begin("edge_geometry", stream);
@@ -980,6 +996,7 @@ struct Evaluator {
                             stream);
             if (tm) tm->end("edge_geometry", stream);
         }
+        if (!records) return;
         if (tm) tm->begin("edge_records", stream);
         ks->edge_geometry(dm, t.ne, tile_xyz(t), tile_r(t), hm.agnesi ? d_edge_pair.as<int>() + t.e0 : nullptr,
                           ws.erec, ws.erec_b, stream);
@@ -1078,7 +1095,7 @@ struct Evaluator {
     }
 
     void zero_a1_if_needed() {
-        if (std::find(hm.num_e.begin(), hm.num_e.end(), 0) != hm.num_e.end())
+        if (two_layer() && std::find(hm.num_e.begin(), hm.num_e.end(), 0) != hm.num_e.end())
             launch_fill_zero(ws.A1, static_cast<std::size_t>(std::max(max_tile_nr, 1)) * hm.num_lm * hm.C, stream);
     }
 
@@ -1095,9 +1112,33 @@ struct Evaluator {
             tile_geometry(t, positions);
             post_geometry_flag();
             ks->layer1_forward(dm, g, t, ws, true, stream, tm);
-            ks->layer2(dm, g, t, ws, stream, tm);
-            ks->source_adjoint_all(g, ws, tile_r(t), hm.r_cut, stream, tm);
+            if (two_layer()) {
+                ks->layer2(dm, g, t, ws, stream, tm);
+                ks->source_adjoint_all(g, ws, tile_r(t), hm.r_cut, stream, tm);
+            } else {
+                ks->single_readout(dm, g, t, ws, stream, tm);
+            }
             ks->layer1_reverse(dm, g, t, ws, true, stream, tm);
+            evaluated = true;
+            return;
+        }
+        if (!two_layer()) {
+            // one sweep: each tile's receivers need only their own H1 rows
+            // (mace_kokkos_evaluate.cpp:614-752)
+            launch_fill_zero(d_atom_forces.as<double>(), static_cast<std::size_t>(N) * 3, stream);
+            launch_fill_zero(d_virial.as<double>(), 9, stream);
+            // the invalid-edge count of every tile's edges first
+            for (const auto& t : tiles) tile_geometry(t, positions, false);
+            post_geometry_flag();
+            // LAMMPS rows receive tile forces from the first tile on: raise first
+            if (lmp) raise_if_invalid_geometry("LAMMPS positions");
+            for (const auto& t : tiles) {
+                tile_geometry(t, positions);
+                ks->layer1_forward(dm, g, t, ws, true, stream, tm);
+                ks->single_readout(dm, g, t, ws, stream, tm);
+                ks->layer1_reverse(dm, g, t, ws, true, stream, tm);
+                accumulate_tile_outputs(t);
+            }
             evaluated = true;
             return;
         }
@@ -1469,6 +1510,7 @@ struct Evaluator {
         else if (name == "edge_records")  // the forward parts [edge][x, interval, active, 0, Y...]
             src = ws.erec, count = (tiled ? max_tile_ne : E) * ks->record_forward_floats();
         else throw std::invalid_argument("unknown stage '" + name + "'");
+        if (count > 0 && !src) throw std::invalid_argument("stage '" + name + "' is not held for this model");
         if (out && capacity >= count && count > 0) {
             SMX_HIP(hipMemcpyAsync(out, src, count * sizeof(float), hipMemcpyDeviceToHost, stream));
             SMX_HIP(hipStreamSynchronize(stream));
@@ -1694,7 +1736,7 @@ int32_t smx_set_execution_plan(SmxEvaluator* ev, const char* profile, int32_t ti
         // tiled plan pinned; speed: the speed profile
         e.request_profile = p == "speed" ? "speed" : "capacity";
         e.allow_fixed = p != "speed";
-        e.debug_plan = p == "capacity" ? smx::Evaluator::kPlanTiled : "";
+        e.debug_plan = p == "capacity" ? e.tiled_plan() : "";
         if (tile_receivers > 0) e.tile_limit = tile_receivers;
     });
 }
@@ -1710,7 +1752,7 @@ int32_t smx_set_execution_plan_request(SmxEvaluator* ev, const char* algorithm, 
         if (p != "capacity" && p != "speed")
             throw std::invalid_argument("execution profile must be 'capacity' or 'speed'");
         if (!d.empty() && d != smx::Evaluator::kPlanSpeed && d != smx::Evaluator::kPlanRetained &&
-            d != smx::Evaluator::kPlanTiled)
+            d != smx::Evaluator::kPlanTiled && d != smx::Evaluator::kPlanSingleTiled)
             throw std::invalid_argument("unknown debug execution plan '" + d + "'");
         e.request_profile = p;
         e.debug_plan = d;

@@ -982,16 +982,18 @@ struct KernelSetImpl final : KernelSet {
         }
         if (m.pre_linear_up) {
             // the readout_1 / skip input in the pre_linear_up basis:
-            // x = M0[:,0,:] P0 (+ the residual's lm-0 row), and H1 += the
-            // residual through linear_up (mace.cpp:1759-1783, 1843-1875)
+            // x = M0[:,0,:] P0 (+ the residual's lm-0 row)
+            // (mace.cpp:1759-1783, 1863-1872)
             TimerScope ts(tm, "h1_affine_scalar", s);
             float* x = w.xaff + static_cast<std::size_t>(t.r0) * C;
             launch_node_gemm(t.cap, m.P0_w, w.M0, x, s);
-            if (m.residual) {
-                launch_type_bias(t.r0, t.nr, g.node_types, C, m.res_x, x, s);
-                launch_type_bias(t.r0, t.nr, g.node_types, S::NH * C, m.res_H1,
-                                 w.H1 + static_cast<std::size_t>(t.r0) * S::NH * C, s);
-            }
+            if (m.residual) launch_type_bias(t.r0, t.nr, g.node_types, C, m.res_x, x, s);
+        }
+        if (m.residual) {
+            // H1 += the residual through linear_up (mace.cpp:1843-1862)
+            TimerScope ts(tm, "h1_residual", s);
+            launch_type_bias(t.r0, t.nr, g.node_types, S::NH * C, m.res_H1,
+                             w.H1 + static_cast<std::size_t>(t.r0) * S::NH * C, s);
         }
     }
 
@@ -1048,6 +1050,32 @@ struct KernelSetImpl final : KernelSet {
             TimerScope ts(tm, "a1_density_forces", s);
             launch_density_forces(m, g, t, nullptr, nullptr, w.dens_s1, w.dens_dot1, w.node_forces, s);
         }
+        if (m.has_zbl) {
+            TimerScope ts(tm, "zbl", s);
+            launch_zbl(m, g, t, w.node_energies, w.node_forces, s);
+        }
+    }
+
+    void single_readout(const DeviceModel& m, const DeviceGraph& g, const TileView& t, const Workspace& w,
+                        hipStream_t s, LaunchTimer* tm) const override {
+        if (t.nr == 0) return;
+        // mace.cpp:265-281: M1 of H1 (its NH components, table-driven
+        // polynomial), H2, readouts, reverse H2 and M1 into H1_adj
+        const float* h1 = w.H1 + static_cast<std::size_t>(t.r0) * S::NH * C;
+        float* h1_adj = w.H1_adj + static_cast<std::size_t>(t.r0) * S::NH * C;
+        {
+            TimerScope ts(tm, "readout", s);
+            k_m1<C, S::NH, void><<<t.nr, C, 0, s>>>(t.r0, g.node_types, h1, m.m1_terms, m.T1, m.m1_coef, w.M1,
+                                                   h1_adj);
+            SMX_LAUNCH_CHECK("m1");
+            k_readout<C, S::NH><<<t.num_batches, 64 * kReadoutWaves, 0, s>>>(
+                t.r0, t.batches, t.node_list, g.node_types, w.M1, w.xaff, m.H2_T, m.H2_Tt, m.H2_M1, m.H2_M1t, m.q,
+                m.W1r, m.W2r, m.hidden, m.readout_scale, m.E0, w.node_energies, w.direct, h1_adj);
+            SMX_LAUNCH_CHECK("readout");
+        }
+        // the directed forces of the tile's edges start at zero: ZBL and the
+        // layer-1 reverse add to them
+        launch_fill_zero(w.node_forces, static_cast<std::size_t>(t.ne) * 3, s);
         if (m.has_zbl) {
             TimerScope ts(tm, "zbl", s);
             launch_zbl(m, g, t, w.node_energies, w.node_forces, s);

@@ -33,6 +33,8 @@ struct DeviceModel {
     // pre_linear_up basis: x = M0[:,0,:] P0 and M0_adj[:,0,:] += P0 d (GEMM
     // weights P0 and P0^T, swizzled); residual: per-type H1 and x offsets
     bool pre_linear_up = false, residual = false;
+    // one interaction: M1 of H1, no R1 / A1 (single_layer_readout)
+    bool single_layer = false;
     const float* P0_w = nullptr;
     const float* P0_wt = nullptr;
     const float* res_H1 = nullptr;  // [type][NH][C]
@@ -208,6 +210,11 @@ struct KernelSet {
     // direct adjoint, per-edge source terms, directed forces (assigned)
     virtual void layer2(const DeviceModel& m, const DeviceGraph& g, const TileView& t, const Workspace& w,
                         hipStream_t s, LaunchTimer* tm) const = 0;
+    // One-interaction models: M1 of the tile's H1 rows, readouts and their
+    // reverse: energies, the direct adjoint and the tile's H1_adj rows
+    // (assigned); the tile's directed forces are zeroed (then ZBL)
+    virtual void single_readout(const DeviceModel& m, const DeviceGraph& g, const TileView& t, const Workspace& w,
+                                hipStream_t s, LaunchTimer* tm) const = 0;
     // H1_adj = source sums of W over the whole graph (one tile); r: edge
     // lengths indexed like W (edges with r >= r_cut have no W row)
     virtual void source_adjoint_all(const DeviceGraph& g, const Workspace& w, const double* r, double r_cut,

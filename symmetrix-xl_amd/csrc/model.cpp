@@ -353,7 +353,8 @@ void HostModel::pair_tables(int ti, int tj, std::vector<float>& R0, std::vector<
     const int nb = static_cast<int>(bessel.size());
     std::vector<double> v, d;
     tabulate(R0_net, feat, nb, spline_points, h, v, d, R0);
-    tabulate(R1_net, feat, nb, spline_points, h, v, d, R1);
+    R1.clear();
+    if (!single_layer) tabulate(R1_net, feat, nb, spline_points, h, v, d, R1);
     R0 = pad_function_table(R0, spline_points - 1, l_max + 1, C_file, C);
     R1 = pad_function_table(R1, spline_points - 1, num_paths, C_file, C);
     D0.clear();
@@ -452,19 +453,25 @@ void HostModel::load(const std::string& path, const std::string& head) {
         throw std::invalid_argument(std::string("a '") + h1_mode + "' MACE JSON must not hold the other basis's "
                                     "readout_1 or H2 skip weights");
     residual = j.get_bool("first_interaction_residual", false);
-    if (residual && !pre_linear_up)
+    // a one-interaction model keeps the m0_composite basis, residual or not
+    // (h1_affine_schema.hpp:227-237)
+    single_layer = j.get_bool("single_layer_readout", false);
+    if (residual && !pre_linear_up && !single_layer)
         throw std::invalid_argument("The m0_composite basis cannot represent first-interaction residual features; "
                                     "such models use h1_affine_mode 'pre_linear_up'.");
+    if (pre_linear_up && single_layer)
+        throw std::invalid_argument("The pre_linear_up basis applies to two-interaction models only.");
     if (j.get_string("radial_representation", "") != "compact")
         throw std::invalid_argument("only the compact radial representation is supported");
-    if (j.get_bool("has_field_coupling", false) || j.get_bool("single_layer_readout", false))
-        throw std::invalid_argument("the model uses features outside the supported MACE path "
-                                    "(field coupling or single-layer readout)");
+    if (j.get_bool("has_field_coupling", false))
+        throw std::invalid_argument("the model uses features outside the supported MACE path (field coupling)");
     // mace_kokkos_model.cpp:200 (required key), :1109 (optional key)
     A0_scaled = j.at("A0_scaled").as_bool();
     A1_scaled = j.get_bool("A1_scaled", false);
     num_interactions = j.get_int("num_interactions", 2);
-    if (num_interactions != 2) throw std::invalid_argument("only two-interaction MACE models are supported");
+    if (num_interactions != (single_layer ? 1 : 2))
+        throw std::invalid_argument("MACE interaction count and single-layer readout metadata disagree.");
+    if (single_layer && A1_scaled) throw std::invalid_argument("a one-interaction model has no A1 to scale");
     num_elements = j.at("num_elements").as_int();
     C = j.at("num_channels").as_int();
     C_file = C;
@@ -551,9 +558,12 @@ void HostModel::load(const std::string& path, const std::string& head) {
     }
     const Value& nets = cr.at("networks");
     const Mlp R0net = read_mlp(nets.at("R0"));
-    const Mlp R1net = read_mlp(nets.at("R1"));
+    // mace.cpp:2769-2772: the R1 network is there iff there is a second interaction
+    if (nets.contains("R1") == single_layer)
+        throw std::invalid_argument("Compact radial R1 network does not match the MACE interaction count.");
+    const Mlp R1net = single_layer ? Mlp{} : read_mlp(nets.at("R1"));
     const int nb = static_cast<int>(bessel.size());
-    if (R0net.shape[0] != nb || R1net.shape[0] != nb)
+    if (R0net.shape[0] != nb || (!single_layer && R1net.shape[0] != nb))
         throw std::invalid_argument("radial networks do not take the Bessel features");
     if (R0net.tanh_square || R1net.tanh_square)
         throw std::invalid_argument("compact radial R0/R1 networks cannot use postprocessing");
@@ -580,11 +590,11 @@ void HostModel::load(const std::string& path, const std::string& head) {
     A0_net = A0net;
     A1_net = A1net;
     R0_functions = R0net.shape.back();
-    R1_functions = R1net.shape.back();
+    R1_functions = single_layer ? 0 : R1net.shape.back();
     if (R0_functions != (l_max + 1) * C) throw std::invalid_argument("R0 network width must be (l_max+1)*C");
     const auto feat = features(0, 0);
     tabulate(R0net, feat, nb, spline_points, h, R0_values, R0_derivs, R0_coef);
-    tabulate(R1net, feat, nb, spline_points, h, R1_values, R1_derivs, R1_coef);
+    if (!single_layer) tabulate(R1net, feat, nb, spline_points, h, R1_values, R1_derivs, R1_coef);
     if (A0_scaled) A0_density = density_table(A0net, feat, nb, spline_points, h);
     if (A1_scaled) A1_density = density_table(A1net, feat, nb, spline_points, h);
 
@@ -675,12 +685,16 @@ void HostModel::load(const std::string& path, const std::string& head) {
         throw std::invalid_argument("Non-residual MACE JSON must not contain H1 residual weights.");
     }
 
-    // ---- R1 coupling (extract_mace_data.py:1326-1400 semantics)
-    path_lo = j.at("Phi1_l").as_ints();
-    path_le = j.at("Phi1_l1").as_ints();
-    path_ls = j.at("Phi1_l2").as_ints();
+    // ---- R1 coupling (extract_mace_data.py:1326-1400 semantics); a
+    // one-interaction model has none (its Phi1 lists are empty or absent,
+    // extract_mace_data.py:1242-1248)
+    if (!single_layer) {
+        path_lo = j.at("Phi1_l").as_ints();
+        path_le = j.at("Phi1_l1").as_ints();
+        path_ls = j.at("Phi1_l2").as_ints();
+    }
     num_paths = static_cast<int>(path_lo.size());
-    if (num_paths == 0 || path_le.size() != path_lo.size() || path_ls.size() != path_lo.size())
+    if ((num_paths == 0 && !single_layer) || path_le.size() != path_lo.size() || path_ls.size() != path_lo.size())
         throw std::invalid_argument("R1 path lists are inconsistent");
     if (R1_functions != num_paths * C) throw std::invalid_argument("R1 network width must be num_paths*C");
     num_e.assign(l_max + 1, 0);
@@ -701,7 +715,7 @@ void HostModel::load(const std::string& path, const std::string& head) {
     }
     num_rows = row_base[num_paths];
     cg_dense.assign(cg_offset[num_paths], 0.0f);
-    {
+    if (!single_layer) {
         const auto lme = j.at("Phi1_lme").as_ints();
         const auto row = j.at("Phi1_lelm1lm2").as_ints();
         const auto cg = j.at("Phi1_clebsch_gordan").as_doubles();
@@ -735,14 +749,13 @@ void HostModel::load(const std::string& path, const std::string& head) {
         }
     }
 
-    // ---- A1
-    const Value& a1 = j.at("A1_weights");
+    // ---- A1 (none with one interaction: num_e is all zero)
     A1_offset.assign(l_max + 2, 0);
     for (int l = 0; l <= l_max; ++l) A1_offset[l + 1] = A1_offset[l] + static_cast<std::int64_t>(num_e[l]) * Cs * Cs;
     A1_w.assign(A1_offset[l_max + 1], 0.0f);
     A1_wt.assign(A1_offset[l_max + 1], 0.0f);
-    for (int l = 0; l <= l_max; ++l) {
-        const auto w = a1.at(l).as_doubles();
+    for (int l = 0; l <= l_max && !single_layer; ++l) {
+        const auto w = j.at("A1_weights").at(l).as_doubles();
         if (w.size() != static_cast<std::size_t>(num_e[l]) * Cs * Cs)
             throw std::invalid_argument("A1 weights have the wrong size");
         const int K = num_e[l] * C;
@@ -756,8 +769,9 @@ void HostModel::load(const std::string& path, const std::string& head) {
 
     // ---- M1
     {
+        // variables: A1's num_lm components, or H1's num_LM with one interaction
         const auto monos = read_monomials(j.at("M1_monomials"));
-        const Poly P = canonical_poly(monos, num_lm);
+        const Poly P = canonical_poly(monos, single_layer ? num_LM : num_lm);
         for (const auto& m : P.monos) m1_terms.push_back(pack_monomial(m));
         const std::size_t T1 = m1_terms.size();
         m1_coef.assign(num_elements * T1 * Cs, 0.0f);

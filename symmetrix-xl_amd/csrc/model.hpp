@@ -106,6 +106,10 @@ struct HostModel {
     bool residual = false;
     std::vector<float> res_H1;              // [type][NH][C]
     std::vector<float> res_x;               // [type][C]
+    // single_layer_readout (mace.cpp:255-281, 2461-2514): one interaction;
+    // M1 is an invariant of H1's num_LM components, and there is no R1,
+    // Phi1 or A1 (num_paths 0)
+    bool single_layer = false;
 
     // R1 coupling
     std::vector<int> path_lo, path_le, path_ls;  // Phi1_l, Phi1_l1, Phi1_l2

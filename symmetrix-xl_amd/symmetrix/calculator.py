@@ -73,7 +73,9 @@ except ImportError:  # pragma: no cover
 AUTOMATIC_DEVICE_NEIGHBOR_MIN_ATOMS = 512
 NEIGHBOR_BACKENDS = ("automatic", "host", "kokkos")
 EXECUTION_PROFILES = ("capacity", "speed")
-TILED_PLAN = "mh0-dual-layer-tiled-v1"
+# the fixed-workspace (tiled) plans of two- and one-interaction models
+TILED_PLANS = ("mh0-dual-layer-tiled-v1", "mh0-single-layer-tiled-v1")
+DEBUG_EXECUTION_PLANS = frozenset(("mh0-direct-speed", "mh0-direct-capacity-retained") + TILED_PLANS)
 
 
 def full_3x3_to_voigt_6_stress(s):
@@ -147,7 +149,7 @@ class Symmetrix(_Base):
 
     def __init__(self, model_file, dtype="float32", use_kokkos=True, streamed_edges="direct",
                  execution_profile="capacity", allow_fixed_workspace=False, neighbor_skin=0.5, head=None,
-                 **kwargs):
+                 _debug_execution_plan=None, **kwargs):
         super().__init__(**kwargs)
         if dtype not in ("float32", np.float32):
             raise ValueError("the MI355X evaluator implements dtype='float32'")
@@ -165,12 +167,21 @@ class Symmetrix(_Base):
             raise ValueError("allow_fixed_workspace=True requires execution_profile='capacity'.")
         if not (neighbor_skin >= 0.0):
             raise ValueError("neighbor_skin must be non-negative")
+        # the private plan pin (calculator.py:831-851): a known id, with the
+        # profile it belongs to
+        if _debug_execution_plan is not None:
+            if _debug_execution_plan not in DEBUG_EXECUTION_PLANS:
+                raise ValueError("_debug_execution_plan must be one of %s or None."
+                                 % sorted(DEBUG_EXECUTION_PLANS))
+            required = "speed" if _debug_execution_plan == "mh0-direct-speed" else "capacity"
+            if execution_profile != required:
+                raise ValueError("%s requires execution_profile=%r." % (_debug_execution_plan, required))
         self.evaluator = MACEKokkosFloat(model_file, head or "")
         self.streamed_edges = "direct"
         self.execution_profile = execution_profile
         self.allow_fixed_workspace = allow_fixed_workspace
         self.evaluator._set_allow_fixed_workspace(allow_fixed_workspace)
-        self.evaluator._set_execution_plan_request("direct", execution_profile, "")
+        self.evaluator._set_execution_plan_request("direct", execution_profile, _debug_execution_plan or "")
         self.cutoff = float(self.evaluator.r_cut)
         self.neighbor_skin = float(neighbor_skin)
         self._types = {z: i for i, z in enumerate(self.evaluator.atomic_numbers)}
@@ -224,7 +235,7 @@ class Symmetrix(_Base):
         return "reuse"
 
     def _fixed_workspace_plan_selected(self):
-        return self.evaluator.execution_plan_report.get("selected_id") == TILED_PLAN
+        return self.evaluator.execution_plan_report.get("selected_id") in TILED_PLANS
 
     def _prepare(self, numbers, positions, cell, pbc):
         if not np.isfinite(positions).all():

@@ -88,7 +88,7 @@ class MACEKokkosFloat:
 
     def set_execution_plan_request(self, profile="auto", tile_receivers=0):
         """Shorthand with the tile size: ``"speed"`` (the speed profile),
-        ``"capacity"`` (the three-sweep tiled plan pinned, at most
+        ``"capacity"`` (the model's tiled plan pinned, at most
         ``tile_receivers`` receivers per tile) or ``"auto"`` (the capacity
         profile with fixed workspaces allowed); applies to graphs prepared
         afterwards."""

@@ -65,9 +65,18 @@ class ModelConfig:
     # (H1_product_weights P, H1_linear_up_weights U, H1_weights = P U) and the
     # readout_1 / skip maps on the pre-linear_up scalar x = M0[:,0,:] P0
     h1_mode: str = "m0_composite"
-    # first_interaction_residual (pre_linear_up only): per-type residual
-    # H1_first_residual_weights [type][LM][C]
+    # first_interaction_residual (pre_linear_up, or a one-interaction model
+    # in either basis): per-type residual H1_first_residual_weights [type][LM][C]
+    # with split H1 weights
     residual: bool = False
+    # one interaction (single_layer_readout, extract_mace_data.py:1221-1262):
+    # no R1 network, Phi1 or A1; M1 is a correlation-`readout_correlation`
+    # invariant of H1's (L_max+1)^2 components.  The reference's extractor
+    # writes zero readout_1 and skip maps for such a model; these are random
+    # unless `zero_affine_maps`, so that the formulas that use them are tested.
+    single_layer: bool = False
+    readout_correlation: int = 2
+    zero_affine_maps: bool = False
     seed: int = 0
 
 
@@ -95,6 +104,11 @@ MODEL_CONFIGS = {
                             r_cut=5.0, avg_num_neighbors=40.0, h1_mode="pre_linear_up"),
     "tiny_residual": ModelConfig("tiny_residual", 32, 2, 1, 2, [8, 22, 38], radial_mlp=[32, 32],
                                  r_cut=5.0, avg_num_neighbors=40.0, h1_mode="pre_linear_up", residual=True),
+    # one-interaction models (mace.cpp:255-281), plain and with a residual
+    "tiny_single": ModelConfig("tiny_single", 32, 2, 1, 2, [8, 22, 38], radial_mlp=[32, 32],
+                               r_cut=5.0, avg_num_neighbors=40.0, single_layer=True),
+    "tiny_single_residual": ModelConfig("tiny_single_residual", 32, 2, 1, 2, [8, 22, 38], radial_mlp=[32, 32],
+                                        r_cut=5.0, avg_num_neighbors=40.0, single_layer=True, residual=True),
     # 128x0e+128x1o, lmax 3, corr 3, 89 elements,
     # MLP [64,64,64], 6.0 A
     "medium": ModelConfig("medium", 128, 3, 1, 3, list(range(1, 90)),
@@ -173,10 +187,12 @@ def generate_model(config, seed=None):
     put("model_type", "MACE")
     if cfg.h1_mode not in ("m0_composite", "pre_linear_up"):
         raise ValueError("h1_mode must be m0_composite or pre_linear_up")
-    if cfg.residual and cfg.h1_mode != "pre_linear_up":
+    if cfg.residual and cfg.h1_mode != "pre_linear_up" and not cfg.single_layer:
         raise ValueError("a first-interaction residual needs the pre_linear_up basis")
-    if cfg.h1_mode == "pre_linear_up" and cfg.prediction_heads:
-        raise ValueError("prediction heads are generated for the m0_composite basis only")
+    if cfg.h1_mode == "pre_linear_up" and (cfg.prediction_heads or cfg.single_layer):
+        raise ValueError("the pre_linear_up basis is generated for two-interaction models without heads")
+    if cfg.single_layer and cfg.density_scaled:
+        raise ValueError("a one-interaction model has no A1 density scale")
     pre = cfg.h1_mode == "pre_linear_up"
     put("h1_affine_mode", cfg.h1_mode)
     put("h1_affine_version", 1)
@@ -184,7 +200,10 @@ def generate_model(config, seed=None):
                       "seed": seed})
     put("num_elements", n_el)
     put("num_channels", C)
-    put("num_interactions", 2)
+    put("num_interactions", 1 if cfg.single_layer else 2)
+    if cfg.single_layer:
+        put("single_layer_readout", True)
+        put("readout_correlation", cfg.readout_correlation)
     put("r_cut", cfg.r_cut)
     put("l_max", l_max)
     put("L_max", L_max)
@@ -227,8 +246,10 @@ def generate_model(config, seed=None):
             {"type": "agnesi", "a": 1.0805, "q": 0.9183, "p": 4.5791,
              "covalent_radii": [_COVALENT_RADII.get(z, 1.5) for z in cfg.atomic_numbers]}
             if cfg.agnesi else {"type": "none"}),
-        "networks": {"R0": mlp((l_max + 1) * C), "R1": mlp(num_paths_r1 * C)},
+        "networks": {"R0": mlp((l_max + 1) * C)},
     }
+    if not cfg.single_layer:
+        compact["networks"]["R1"] = mlp(num_paths_r1 * C)
     if cfg.density_scaled:
         drng = np.random.default_rng([seed, 1])
         for name in ("A0", "A1"):
@@ -273,7 +294,7 @@ def generate_model(config, seed=None):
 
     # ---- H1 = product linear x interaction[1].linear_up, per l
     h1 = rng.normal(size=(L_max + 1, C, C)) / math.sqrt(C)
-    if pre:
+    if pre or cfg.residual:
         # split weights from their own generator (the other draws stay those
         # of the m0_composite model of the same config)
         prng = np.random.default_rng([seed, 3])
@@ -287,24 +308,36 @@ def generate_model(config, seed=None):
             frag["H1_first_residual_weights"] = _fmt(0.3 * prng.normal(size=(n_el, num_LM, C)))
     frag["H1_weights"] = _fmt(h1)
 
-    # ---- R1 coupling
-    cpl = e3.r1_coupling(l_max, L_max)
-    for key in ("Phi1_l", "Phi1_l1", "Phi1_l2", "Phi1_lme", "Phi1_lelm1lm2"):
-        put(key, cpl[key])
-    put("Phi1_clebsch_gordan", cpl["Phi1_clebsch_gordan"])
-    put("A1_scaled", bool(cfg.density_scaled))
+    if cfg.single_layer:
+        # no second interaction (extract_mace_data.py:1236-1248)
+        for key in ("Phi1_l", "Phi1_l1", "Phi1_l2", "Phi1_lme", "Phi1_clebsch_gordan", "Phi1_lelm1lm2"):
+            put(key, [])
+        put("A1_weights", [[] for _ in range(l_max + 1)])
+        put("A1_scaled", False)
+    else:
+        # ---- R1 coupling
+        cpl = e3.r1_coupling(l_max, L_max)
+        for key in ("Phi1_l", "Phi1_l1", "Phi1_l2", "Phi1_lme", "Phi1_lelm1lm2"):
+            put(key, cpl[key])
+        put("Phi1_clebsch_gordan", cpl["Phi1_clebsch_gordan"])
+        put("A1_scaled", bool(cfg.density_scaled))
 
-    # ---- A1: per l, [num_e(l)][C][C]
-    num_e = [sum(1 for l in cpl["Phi1_l"] if l == ll) for ll in range(l_max + 1)]
-    frag["A1_weights"] = "[" + ",".join(
-        _fmt(rng.normal(size=(num_e[l], C, C))
-             / (math.sqrt(num_e[l] * C) * cfg.avg_num_neighbors))
-        for l in range(l_max + 1)) + "]"
+        # ---- A1: per l, [num_e(l)][C][C]
+        num_e = [sum(1 for l in cpl["Phi1_l"] if l == ll) for ll in range(l_max + 1)]
+        frag["A1_weights"] = "[" + ",".join(
+            _fmt(rng.normal(size=(num_e[l], C, C))
+                 / (math.sqrt(num_e[l] * C) * cfg.avg_num_neighbors))
+            for l in range(l_max + 1)) + "]"
 
     # ---- M1: invariant contraction of A1 ((l_max+1)^2 harmonic components),
-    # with the same correlation order as the first product basis
-    monos1, coef1 = _product_weights(
-        rng, l_max, 0, cfg.correlation, n_el, C, scale=[1.0, 0.5, 0.25][:cfg.correlation])
+    # with the same correlation order as the first product basis; with one
+    # interaction, of H1 ((L_max+1)^2 components) at the readout correlation
+    if cfg.single_layer:
+        monos1, coef1 = _product_weights(
+            rng, L_max, 0, cfg.readout_correlation, n_el, C, scale=[1.0, 0.5, 0.25][:cfg.readout_correlation])
+    else:
+        monos1, coef1 = _product_weights(
+            rng, l_max, 0, cfg.correlation, n_el, C, scale=[1.0, 0.5, 0.25][:cfg.correlation])
     put("M1_monomials", monos1[0])
     frag["M1_weights"] = "{" + ",".join(
         '"%d":{' % t + ",".join(
@@ -314,14 +347,15 @@ def generate_model(config, seed=None):
     # ---- H2 skip (T_z, [input][output]) and M1 linear; in the pre_linear_up
     # basis the skip and readout_1 act on x = M0[:,0,:] P0
     skip_key = "H2_weights_for_H1_pre_linear_up" if pre else "H2_weights_for_M0"
+    affine = 0.0 if cfg.zero_affine_maps else 1.0
     frag[skip_key] = "[" + ",".join(
-        _fmt(rng.normal(size=(C, C)) / math.sqrt(C)) for _ in range(n_el)) + "]"
+        _fmt(affine * rng.normal(size=(C, C)) / math.sqrt(C)) for _ in range(n_el)) + "]"
     frag["H2_weights_for_M1"] = _fmt(rng.normal(size=(C, C)) / math.sqrt(C))
 
     # ---- readouts
     hid = cfg.readout_hidden
     frag["readout_1_weights_for_H1_pre_linear_up" if pre else "readout_1_weights_for_M0"] = _fmt(
-        rng.normal(size=C) / math.sqrt(C) * cfg.energy_scale)
+        affine * rng.normal(size=C) / math.sqrt(C) * cfg.energy_scale)
     put("readout_2_hidden_size", hid)
     frag["readout_2_weights_1"] = _fmt(rng.normal(size=(hid, C)) / math.sqrt(C))
     frag["readout_2_weights_2"] = _fmt(

@@ -114,10 +114,12 @@ def _run(ev, hip, allpos, owner, alltypes, rows, ilist, type_to_model, rebuild):
 _ROWS = {}  # (model, plan, step) -> LAMMPS force rows, for the cross-plan check
 
 
-@pytest.mark.parametrize("model", ["tiny", "tiny_scaled", "tiny_zbl", "tiny_agnesi", "tiny_residual"])
+@pytest.mark.parametrize("model", ["tiny", "tiny_scaled", "tiny_zbl", "tiny_agnesi", "tiny_residual",
+                                   "tiny_single_residual"])
 @pytest.mark.parametrize("tile", [None, 32], ids=["direct", "tiled32"])
 def test_lammps_entry_matches_oracle(request, model, tile):
-    # plain, density-scaled, ZBL, Agnesi (per-pair tables) and residual-first models
+    # plain, density-scaled, ZBL, Agnesi (per-pair tables), residual-first and
+    # one-interaction models
     tiny_model_path = request.getfixturevalue(model + "_model_path")
     from oracle import oracle
     from symmetrix import systems
@@ -191,15 +193,17 @@ def test_lammps_entry_rejects_unmapped_types(tiny_model_path):
         hip.free()
 
 
+@pytest.mark.parametrize("model", ["tiny", "tiny_single"])
 @pytest.mark.parametrize("tile", [None, 32], ids=["direct", "tiled32"])
-def test_lammps_entry_zero_length_edge_raises_and_next_call_recovers(tiny_model_path, tile):
-    # a ghost placed on the local atom that lists it: exactly one zero-length
-    # edge, counted once in either plan; the next call on good positions
-    # (same list, no rebuild) gives the first call's results again
+def test_lammps_entry_zero_length_edge_raises_and_next_call_recovers(request, model, tile):
+    # a ghost placed on the local atom that lists it (the last receiver, in
+    # the last tile): exactly one zero-length edge, counted once in either
+    # plan; the next call on good positions (same list, no rebuild) gives
+    # the first call's results again
     from symmetrix import systems
     from symmetrix.mace_kokkos import MACEKokkosFloat
     s = systems.srtio3_supercell(3, sigma=0.05, seed=0)
-    ev = MACEKokkosFloat(tiny_model_path)
+    ev = MACEKokkosFloat(request.getfixturevalue(model + "_model_path"))
     if tile is not None:
         ev.set_execution_plan_request("capacity", tile)
     model_of_z = {int(z): k for k, z in enumerate(ev.atomic_numbers)}
@@ -208,9 +212,9 @@ def test_lammps_entry_zero_length_edge_raises_and_next_call_recovers(tiny_model_
     allpos, owner, alltypes, rows = _lammps_arrays(s["positions"], cell, s["numbers"], ev.r_cut + 0.5,
                                                    {8: 1, 22: 2, 38: 3})
     n = len(rows)
-    ghost = int(next(j for j in rows[0] if j >= n))
+    ghost = int(next(j for j in rows[n - 1] if j >= n))
     bad = allpos.copy()
-    bad[ghost] = allpos[0]
+    bad[ghost] = allpos[n - 1]
     ilist = np.arange(n, dtype=np.int32)
     hip = _Hip()
     try:
