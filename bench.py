@@ -236,9 +236,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-calculator", action="store_true", help="skip the calculator-boundary timing")
-    ap.add_argument("--no-configs", action="store_true", help="skip the wide and irregular configs")
+    ap.add_argument("--no-configs", action="store_true", help="skip the wide, irregular and one-interaction configs")
     ap.add_argument("--no-lammps", action="store_true", help="skip the LAMMPS pair-style step timing")
-    ap.add_argument("--only-config", choices=("wide", "irregular"),
+    ap.add_argument("--only-config", choices=("wide", "irregular", "single"),
                     help="run only that config (3 warm-ups, median of 10) and print its summary")
     ap.add_argument("--capacity-steps", type=int, default=3,
                     help="NVE steps of the tiled 11.5M-atom capacity extra key (0 skips it)")
@@ -313,7 +313,7 @@ def main():
         note("lammps step: %s" % out["lammps_step"])
     if not args.no_configs:
         out["configs"] = {}
-        for name in ("wide", "irregular"):
+        for name in ("wide", "irregular", "single"):
             cfg_model, cfg_system, workload = config_case(name)
             out["configs"][name] = summary(run_config(hip, cfg_model, cfg_system, skin, 3, 10), workload)
             note("%s: %s" % (name, out["configs"][name]))
@@ -329,8 +329,13 @@ def main():
 
 
 def config_case(name):
-    """(model path, system, workload text) of the wide and irregular configs."""
+    """(model path, system, workload text) of the wide, irregular and
+    one-interaction configs."""
     from symmetrix import random_model, systems
+    if name == "single":
+        return (random_model.cached_model("medium_single"), systems.srtio3_supercell(10, sigma=0.05, seed=0),
+                "single: one-interaction MACE 128x0e+128x1o l_max 3 corr 3, readout corr 2, A0-scaled "
+                "(single_layer_readout), SrTiO3 10x10x10 (5000 atoms), r_cut 6.0 A + 0.5 A skin")
     if name == "wide":
         return (random_model.cached_model("wide"), systems.water_box(10000, seed=0),
                 "wide: 10,000 rigid waters (30,000 atoms), MACE 256x(0e+1o+2e) l_max 3 corr 3, "
@@ -343,8 +348,9 @@ def config_case(name):
 def summary(r, workload):
     return {"workload": workload, "atoms": r["atoms"], "edges": r["edges"], "active_edges": r["active_edges"],
             "median_us_per_atom": round(r["median_us_per_atom"], 4), "protocol": "3 warm-ups, median of 10",
-            "roofline": {k: r["roofline"][k] for k in ("kernel", "avg_launch_ms", "achieved", "frac",
-                                                         "executed_frac", "unit")}}
+            "roofline": None if r["roofline"] is None else {
+                k: r["roofline"][k] for k in ("kernel", "avg_launch_ms", "achieved", "frac", "executed_frac",
+                                              "unit")}}
 
 
 def run_config(hip, model_path, system, skin, warmup, steps, timed_steps=False):
@@ -421,6 +427,13 @@ def run_config(hip, model_path, system, skin, warmup, steps, timed_steps=False):
     P, T, rows, C = model_counts(model_path)
     rec = ev._stage("edge_records")
     E_active = int(np.count_nonzero(rec.reshape(g["num_edges"], -1)[:, 2].view(np.int32)))
+    out["active_edges"] = E_active
+    out["roofline"] = None
+    if P == 0:
+        # a one-interaction model has no R1 reverse
+        hip.hipFree(d_pos)
+        ev.close()
+        return out
     ms_r1, launches = timing.get(DOMINANT, (float("nan"), 0))
     avg_ms = ms_r1 / max(launches, 1)
     per_call = max(launches // max(steps, 1), 1)   # the wide shape runs one launch per source-component group
@@ -438,7 +451,6 @@ def run_config(hip, model_path, system, skin, warmup, steps, timed_steps=False):
         roof["executed_flops_per_launch"] = ex
         roof["executed_frac"] = round(ex / (avg_ms * 1e-3) / 1e12 / VALU_FP32_TFLOPS, 4)
     out["roofline"] = roof
-    out["active_edges"] = E_active
     hip.hipFree(d_pos)
     ev.close()
     return out

@@ -1185,10 +1185,17 @@ std::unique_ptr<KernelSet> pick_polynomials(const std::vector<std::int32_t>& m0_
     using T0 = ProductTable<LMAX, LMAXH, CORR>;
     using T1 = ProductTable<LMAX, 0, CORR>;
     const std::vector<std::int32_t> m1_offsets{0, static_cast<std::int32_t>(m1_terms.size())};
-    if constexpr (T0::available && T1::available) {
-        if (table_matches<T0>(m0_terms, m0_offsets) && table_matches<T1>(m1_terms, m1_offsets))
-            return std::make_unique<KernelSetImpl<C, LMAX, LMAXH, T0, T1>>();
-    }
+    // each product basis unrolled when its list is a compiled table (a
+    // one-interaction model's M1, over H1's components, never is)
+    bool m0 = false, m1 = false;
+    if constexpr (T0::available) m0 = table_matches<T0>(m0_terms, m0_offsets);
+    if constexpr (T1::available) m1 = table_matches<T1>(m1_terms, m1_offsets);
+    if constexpr (T0::available && T1::available)
+        if (m0 && m1) return std::make_unique<KernelSetImpl<C, LMAX, LMAXH, T0, T1>>();
+    if constexpr (T0::available)
+        if (m0) return std::make_unique<KernelSetImpl<C, LMAX, LMAXH, T0, void>>();
+    if constexpr (T1::available)
+        if (m1) return std::make_unique<KernelSetImpl<C, LMAX, LMAXH, void, T1>>();
     return std::make_unique<KernelSetImpl<C, LMAX, LMAXH, void, void>>();
 }
 

@@ -109,6 +109,11 @@ MODEL_CONFIGS = {
                                r_cut=5.0, avg_num_neighbors=40.0, single_layer=True),
     "tiny_single_residual": ModelConfig("tiny_single_residual", 32, 2, 1, 2, [8, 22, 38], radial_mlp=[32, 32],
                                         r_cut=5.0, avg_num_neighbors=40.0, single_layer=True, residual=True),
+    # the trained one-interaction shape (128x0e+128x1o, l_max 3, correlation
+    # 3, readout correlation 2, A0 density scaling: test_single_layer_mace.py:
+    # 71-81) on the benchmark's elements
+    "medium_single": ModelConfig("medium_single", 128, 3, 1, 3, [8, 22, 38], radial_mlp=[64, 64, 64],
+                                 r_cut=6.0, avg_num_neighbors=70.0, single_layer=True, density_scaled=True),
     # 128x0e+128x1o, lmax 3, corr 3, 89 elements,
     # MLP [64,64,64], 6.0 A
     "medium": ModelConfig("medium", 128, 3, 1, 3, list(range(1, 90)),
@@ -191,8 +196,6 @@ def generate_model(config, seed=None):
         raise ValueError("a first-interaction residual needs the pre_linear_up basis")
     if cfg.h1_mode == "pre_linear_up" and (cfg.prediction_heads or cfg.single_layer):
         raise ValueError("the pre_linear_up basis is generated for two-interaction models without heads")
-    if cfg.single_layer and cfg.density_scaled:
-        raise ValueError("a one-interaction model has no A1 density scale")
     pre = cfg.h1_mode == "pre_linear_up"
     put("h1_affine_mode", cfg.h1_mode)
     put("h1_affine_version", 1)
@@ -252,7 +255,8 @@ def generate_model(config, seed=None):
         compact["networks"]["R1"] = mlp(num_paths_r1 * C)
     if cfg.density_scaled:
         drng = np.random.default_rng([seed, 1])
-        for name in ("A0", "A1"):
+        # a one-interaction model scales A0 only (it has no A1)
+        for name in ("A0",) if cfg.single_layer else ("A0", "A1"):
             net = mlp(1, drng)
             # a larger last layer so that tanh(v^2) spans (0, 1) over the grid
             net["weights"][-1] = _f32(4.0 * np.asarray(net["weights"][-1])).tolist()

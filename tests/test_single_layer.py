@@ -96,7 +96,7 @@ def test_energy_is_the_readout_of_an_h1_invariant(tiny_single_model_path):
     assert np.max(np.abs(om.stage("node_forces_r1"))) == 0.0
 
 
-@pytest.mark.parametrize("model", ["tiny_single", "tiny_single_residual"])
+@pytest.mark.parametrize("model", ["tiny_single", "tiny_single_residual", "medium_single"])
 def test_forces_and_stress_are_energy_derivatives(request, model):
     path = request.getfixturevalue(model + "_model_path")
     m = oracle.OracleModel(path, fp64=True)

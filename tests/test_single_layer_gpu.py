@@ -42,6 +42,24 @@ def test_single_layer_model_matches_oracle(request, model):
         np.testing.assert_allclose(s1, st, rtol=0, atol=1e-9)
 
 
+def test_trained_one_interaction_shape(medium_single_model_path):
+    """128x0e+128x1o, l_max 3, correlation 3, readout correlation 2, A0
+    density scaling (the extracted single-layer checkpoint's shape,
+    test_single_layer_mace.py:71-81) on SrTiO3, both plans."""
+    from symmetrix.mace_kokkos import MACEKokkosFloat
+    s = _system("tiny")
+    om, ref, ev, g, e, f, st = _evaluate_both(medium_single_model_path, s)
+    _assert_efs(ref, e, f, st, len(e))
+    np.testing.assert_allclose(e, ref["energies"], rtol=0, atol=1e-4)
+    b = MACEKokkosFloat(medium_single_model_path)
+    b.set_execution_plan_request("capacity", 50)
+    e1, f1, s1 = _run(b, s, om.types_of(s["numbers"]))
+    assert b.execution_plan_report["selected_id"] == "mh0-single-layer-tiled-v1"
+    np.testing.assert_array_equal(e1, e)
+    np.testing.assert_allclose(f1, f, rtol=0, atol=1e-6)
+    np.testing.assert_allclose(s1, st, rtol=0, atol=1e-9)
+
+
 def test_tiled_plans_admit_only_their_model_kind(tiny_single_model_path, tiny_model_path):
     from symmetrix.mace_kokkos import MACEKokkosFloat
     s = _system("tiny")
