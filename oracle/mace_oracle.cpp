@@ -18,7 +18,9 @@
 //     H1 :1691-1757, v4 affine capture :1759-1814, Phi1 :2023-2084,
 //     reverse Phi1 :2199-2303, A1 :2305-2379, M1 :2461-2514, H2 :2516-2620,
 //     readouts :2622-2657; one-interaction models :255-281 with M1 over
-//     the H1 components :2461-2514), with the Kokkos evaluator's precision policy
+//     the H1 components :2461-2514; MACEField field coupling :322-395,
+//     1147-1240 with the path compilation of field_coupling.hpp:60-238 and
+//     the Kokkos forms mace_kokkos_h1_phi1.cpp:846-1150), with the Kokkos evaluator's precision policy
 //     (FP64 H2, readouts, node energies, directed forces, and the FP64
 //     accumulation of the FP32 source adjoint: mace_kokkos.hpp:501,907-909,
 //     1805-1828)
@@ -499,6 +501,24 @@ struct Mace {
     // interaction; M1 is taken of H1 (its num_LM components) instead of A1,
     // so there is no R1, Phi1 or A1, and the M1 adjoint is H1's adjoint
     bool single_layer = false;
+    // MACEField (field_coupling.hpp:60-238; mace.cpp:322-395, 1147-1240):
+    // with the split H1 weights, H1p = M0 P (+ residual b), then
+    // H1f[lm_out] = H1p[lm_out] + sum over angular entries of
+    // (coef E_c) H1p[lm_in] W_path, x = H1f[:,0,:], H1 = H1f U; the reverse
+    // carries H1_adj U^T (+ x's adjoint on lm 0) back through the field
+    // terms and accumulates dE/dE_c in FP64
+    bool has_field = false;
+    struct FieldEntry {
+        int lm_in, comp, lm_out, path;
+        P coef;
+    };
+    std::vector<FieldEntry> field_entries;
+    std::vector<P> field_W;                  // [path][C][C] [in][out]
+    std::vector<P> P_all, U_all;             // [l][C][C] H1_product / H1_linear_up weights
+    std::vector<P> res_b;                    // [type][LM][C] the residual before linear_up
+    std::vector<double> field_in;            // the evaluation's field: 3 (graph) or 3n (per node)
+    std::vector<double> field_adj;           // dE/dE, shaped like field_in
+    std::vector<P> H1_pre, H1_field;         // pre-field H1p and H1f (stages)
     std::vector<P> res_fused;               // [type][LM][C]
     std::vector<P> res_x;                   // [type][C]
     std::vector<int> Phi1_l, Phi1_l1, Phi1_l2, Phi1_lme, Phi1_row;
@@ -581,6 +601,14 @@ struct Mace {
         pre_linear_up = h1_mode == "pre_linear_up";
         residual = j.get_bool("first_interaction_residual", false);
         single_layer = j.get_bool("single_layer_readout", false);
+        has_field = j.get_bool("has_field_coupling", false);
+        {
+            const std::string mt = j.get_string("model_type", "MACE");
+            if (mt != "MACE" && mt != "MACEField") throw std::invalid_argument("unsupported model_type");
+        }
+        // h1_affine_schema.hpp:230-236: field coupling needs the pre_linear_up basis
+        if (has_field && !pre_linear_up)
+            throw std::invalid_argument("a field-coupled model needs h1_affine_mode 'pre_linear_up'");
         // h1_affine_schema.hpp:227-237, mace.cpp:2676-2679
         if (j.get_int("num_interactions", 2) != (single_layer ? 1 : 2))
             throw std::invalid_argument("interaction count and single-layer readout metadata disagree");
@@ -590,8 +618,6 @@ struct Mace {
             throw std::invalid_argument("the pre_linear_up basis applies to two-interaction models only");
         if (j.get_string("radial_representation", "") != "compact")
             throw std::invalid_argument("only the compact radial representation is supported");
-        if (j.get_bool("has_field_coupling", false))
-            throw std::invalid_argument("model features outside the supported MACE path");
         num_elements = j.at("num_elements").as_int();
         C = j.at("num_channels").as_int();
         r_cut = j.at("r_cut").as_number();
@@ -649,11 +675,13 @@ struct Mace {
             if (pw.size() != H1_w.size()) throw std::invalid_argument("H1_product_weights has the wrong size");
             P0.assign(pw.begin(), pw.begin() + static_cast<std::size_t>(C) * C);
         }
+        if (has_field) load_field(j);
         if (residual) {
             // fused[a][lm][out] = sum_in residual[a][lm][in] U_l[in][out] in
             // Precision, in the reference's loop order (mace.cpp:2809-2822)
             const auto U = castv(j.at("H1_linear_up_weights").as_doubles());
             const auto b = castv(j.at("H1_first_residual_weights").as_doubles());
+            res_b = b;
             const int LM = (L_max + 1) * (L_max + 1);
             if (U.size() != H1_w.size() || b.size() != static_cast<std::size_t>(num_elements) * LM * C)
                 throw std::invalid_argument("residual weights have the wrong size");
@@ -735,6 +763,235 @@ struct Mace {
         if (W1.size() != static_cast<std::size_t>(hidden) * C || W2.size() != static_cast<std::size_t>(hidden))
             throw std::invalid_argument("readout weights do not match the hidden size");
         type_to_active.assign(num_elements, -1);
+    }
+
+    P field_value(int i, int c) const {
+        return static_cast<P>(field_in[field_in.size() == 3 ? c : 3 * static_cast<std::size_t>(i) + c]);
+    }
+
+    // H1p = M0 P (+ b), H1f = H1p + field terms, x = H1f[:,0,:], H1 = H1f U
+    // (mace.cpp:1759-1783, 1845-1895; the field terms in the Kokkos order,
+    // mace_kokkos_h1_phi1.cpp:895-919: per output, the entry's coef E_c
+    // times each input's product in turn)
+    void field_forward(int n, const int* types) {
+        const std::size_t Cs = static_cast<std::size_t>(C), LMC = static_cast<std::size_t>(num_LM) * Cs;
+        if (field_in.size() != 3 && field_in.size() != 3 * static_cast<std::size_t>(n))
+            throw std::invalid_argument("MACEField electric_field must have shape (3,) or (num_nodes, 3)");
+        H1_pre.assign(n * LMC, P(0));
+        H1_field.assign(n * LMC, P(0));
+        H1.assign(n * LMC, P(0));
+#pragma omp parallel for schedule(static)
+        for (int i = 0; i < n; ++i) {
+            P* hp = &H1_pre[i * LMC];
+            P* hf = &H1_field[i * LMC];
+            for (int l = 0; l <= L_max; ++l)
+                for (int m = 0; m < 2 * l + 1; ++m) {
+                    const P* src = &M0[i * LMC + (l * l + m) * Cs];
+                    P* dst = hp + (l * l + m) * Cs;
+                    const P* W = &P_all[static_cast<std::size_t>(l) * Cs * Cs];
+                    for (int kp = 0; kp < C; ++kp)
+                        for (int k = 0; k < C; ++k) dst[k] += src[kp] * W[kp * Cs + k];
+                }
+            if (residual)
+                for (std::size_t v = 0; v < LMC; ++v) hp[v] += res_b[static_cast<std::size_t>(types[i]) * LMC + v];
+            for (int lo = 0; lo < num_LM; ++lo)
+                for (int out = 0; out < C; ++out) {
+                    P value = hp[lo * Cs + out];
+                    for (const auto& e : field_entries) {
+                        if (e.lm_out != lo) continue;
+                        const P af = e.coef * field_value(i, e.comp);
+                        const P* W = &field_W[static_cast<std::size_t>(e.path) * Cs * Cs];
+                        for (int in = 0; in < C; ++in) value += af * hp[e.lm_in * Cs + in] * W[in * Cs + out];
+                    }
+                    hf[lo * Cs + out] = value;
+                }
+            for (int k = 0; k < C; ++k) xaff[i * Cs + k] = hf[k];
+            for (int l = 0; l <= L_max; ++l)
+                for (int m = 0; m < 2 * l + 1; ++m) {
+                    const P* src = hf + (l * l + m) * Cs;
+                    P* dst = &H1[i * LMC + (l * l + m) * Cs];
+                    const P* W = &U_all[static_cast<std::size_t>(l) * Cs * Cs];
+                    for (int kp = 0; kp < C; ++kp)
+                        for (int k = 0; k < C; ++k) dst[k] += src[kp] * W[kp * Cs + k];
+                }
+        }
+    }
+
+    // H1p_adj = H1_adj U^T (+ x's adjoint on lm 0), then back through the
+    // field terms (mace_kokkos_h1_phi1.cpp:928-1150: per input, each entry's
+    // coef times W applied to the output adjoint; dE/dE_c summed in FP64),
+    // then M0_adj = H1p_adj P^T
+    void field_reverse(int n) {
+        const std::size_t Cs = static_cast<std::size_t>(C), LMC = static_cast<std::size_t>(num_LM) * Cs;
+        const bool global = field_in.size() == 3;
+        field_adj.assign(field_in.size(), 0.0);
+        std::vector<double> part(static_cast<std::size_t>(n) * 3, 0.0);
+#pragma omp parallel for schedule(static)
+        for (int i = 0; i < n; ++i) {
+            std::vector<P> a(LMC, P(0)), a2(LMC);
+            for (int l = 0; l <= L_max; ++l)
+                for (int m = 0; m < 2 * l + 1; ++m) {
+                    const P* src = &H1_adj[i * LMC + (l * l + m) * Cs];
+                    P* dst = &a[(l * l + m) * Cs];
+                    const P* W = &U_all[static_cast<std::size_t>(l) * Cs * Cs];
+                    for (int k = 0; k < C; ++k) {
+                        P acc = 0;
+                        for (int kp = 0; kp < C; ++kp) acc += src[kp] * W[k * Cs + kp];
+                        dst[k] = acc;
+                    }
+                }
+            for (int k = 0; k < C; ++k) a[k] += static_cast<P>(direct[i * Cs + k]);
+            const P* hp = &H1_pre[i * LMC];
+            for (int li = 0; li < num_LM; ++li)
+                for (int in = 0; in < C; ++in) {
+                    P value = a[li * Cs + in];
+                    for (const auto& e : field_entries) {
+                        if (e.lm_in != li) continue;
+                        const P* W = &field_W[static_cast<std::size_t>(e.path) * Cs * Cs + in * Cs];
+                        if (global) {
+                            P tr = 0;
+                            for (int out = 0; out < C; ++out) tr += W[out] * a[e.lm_out * Cs + out];
+                            const P contribution = e.coef * tr;
+                            value += field_value(i, e.comp) * contribution;
+                            part[3 * static_cast<std::size_t>(i) + e.comp] +=
+                                static_cast<double>(hp[li * Cs + in] * contribution);
+                        } else {
+                            const P af = e.coef * field_value(i, e.comp);
+                            for (int out = 0; out < C; ++out) value += af * W[out] * a[e.lm_out * Cs + out];
+                            for (int out = 0; out < C; ++out)
+                                part[3 * static_cast<std::size_t>(i) + e.comp] +=
+                                    static_cast<double>(e.coef * W[out] * hp[li * Cs + in] * a[e.lm_out * Cs + out]);
+                        }
+                    }
+                    a2[li * Cs + in] = value;
+                }
+            for (int l = 0; l <= L_max; ++l)
+                for (int m = 0; m < 2 * l + 1; ++m) {
+                    const P* src = &a2[(l * l + m) * Cs];
+                    P* dst = &M0_adj[i * LMC + (l * l + m) * Cs];
+                    const P* W = &P_all[static_cast<std::size_t>(l) * Cs * Cs];
+                    for (int k = 0; k < C; ++k) {
+                        P acc = 0;
+                        for (int kp = 0; kp < C; ++kp) acc += src[kp] * W[k * Cs + kp];
+                        dst[k] = acc;
+                    }
+                }
+        }
+        for (int i = 0; i < n; ++i)
+            for (int c = 0; c < 3; ++c) field_adj[global ? c : 3 * static_cast<std::size_t>(i) + c] += part[3 * i + c];
+    }
+
+    // field_coupling.hpp:60-238 (compile_field_coupling) and mace.cpp:2832-2860
+    void load_field(const Value& j) {
+        if (L_max < 1 || L_max > 2) throw std::invalid_argument("MACEField supports 1 <= L_max <= 2");
+        const Value& list = j.at("field_couplings");
+        if (list.size() != 1) throw std::invalid_argument("MACEField JSON must contain exactly one field coupling");
+        const Value& cp = list.at(0);
+        const bool legacy = !cp.contains("schema_version");
+        if (!legacy && cp.at("schema_version").as_int() != 1)
+            throw std::invalid_argument("unsupported MACEField field-coupling schema version");
+        if (legacy && L_max != 1) throw std::invalid_argument("unversioned MACEField coupling needs L_max == 1");
+        std::string hidden;
+        for (int l = 0; l <= L_max; ++l)
+            hidden += (l ? "+" : "") + std::to_string(C) + "x" + std::to_string(l) + (l % 2 ? "o" : "e");
+        if (cp.at("field_feats_irreps_in1").as_string() != hidden || cp.at("field_feats_irreps_in2").as_string() != "1x1o" ||
+            cp.at("field_feats_irreps_out").as_string() != hidden ||
+            cp.at("field_linear_irreps_in").as_string() != hidden ||
+            cp.at("field_linear_irreps_out").as_string() != hidden)
+            throw std::invalid_argument("MACEField coupling must use the canonical equal-channel hidden irreps");
+        const std::size_t hs = static_cast<std::size_t>(num_LM) * C;
+        for (const char* key : {"field_feats_output_mask", "field_linear_output_mask"}) {
+            const auto m = cp.at(key).as_doubles();
+            if (m.size() != hs) throw std::invalid_argument(std::string("MACEField ") + key + " has an invalid size");
+            for (double v : m)
+                if (v != 1.0) throw std::invalid_argument(std::string("MACEField ") + key + " must contain only ones");
+        }
+        if (cp.at("field_linear_bias").size() != 0) throw std::invalid_argument("MACEField field_linear bias must be empty");
+        const auto wf = j_doubles(cp.at("field_feats_weight"));
+        const auto wl = j_doubles(cp.at("field_linear_weight"));
+        const Value& fi_list = cp.at("field_feats_instructions");
+        const Value& li_list = cp.at("field_linear_instructions");
+        const std::size_t cc = static_cast<std::size_t>(C) * C;
+        if (fi_list.size() * cc != wf.size()) throw std::invalid_argument("MACEField field_feats weight size mismatch");
+        if (li_list.size() * cc != wl.size()) throw std::invalid_argument("MACEField field_linear weight size mismatch");
+        const auto U = j.at("H1_linear_up_weights").as_doubles();
+        const auto Pw = j.at("H1_product_weights").as_doubles();
+        if (U.size() != static_cast<std::size_t>(L_max + 1) * cc || Pw.size() != U.size())
+            throw std::invalid_argument("MACEField JSON must contain split H1 product and linear_up weights");
+        P_all = castv(Pw);
+        U_all = castv(U);
+        for (std::size_t li = 0; li < li_list.size(); ++li) {
+            const Value& ins = li_list.at(li);
+            if (ins.at("path_shape").as_ints() != std::vector<int>{C, C})
+                throw std::invalid_argument("MACEField field_linear instructions must be shaped (C, C)");
+            const int a = ins.at("i_in").as_int(), b = ins.at("i_out").as_int();
+            if (a < 0 || a > L_max || b != a)
+                throw std::invalid_argument("MACEField field_linear instructions must keep each angular block");
+        }
+        field_entries.clear();
+        field_W.clear();
+        int path = 0;
+        for (std::size_t fi = 0; fi < fi_list.size(); ++fi) {
+            const Value& ins = fi_list.at(fi);
+            if (ins.at("connection_mode").as_string() != "uvw" ||
+                ins.at("path_shape").as_ints() != std::vector<int>{C, 1, C})
+                throw std::invalid_argument("MACEField field_feats instructions must be uvw paths (C, 1, C)");
+            const int lin = ins.at("i_in1").as_int(), blk = ins.at("i_in2").as_int(), lmid = ins.at("i_out").as_int();
+            if (blk != 0 || lin < 0 || lin > L_max || lmid < 0 || lmid > L_max || std::abs(lin - lmid) != 1)
+                throw std::invalid_argument("MACEField field_feats instruction is not an adjacent-rank 1o coupling");
+            const int din = 2 * lin + 1, dmid = 2 * lmid + 1;
+            std::vector<double> w3(static_cast<std::size_t>(din) * 3 * dmid, 0.0);
+            if (legacy) {
+                // the unversioned files' fixed pattern (field_coupling.hpp:145-156)
+                for (int c = 0; c < 3; ++c) w3[lin == 0 ? c * 3 + c : c * 4] = 1.0 / std::sqrt(3.0);
+            } else {
+                if (ins.at("wigner_3j_shape").as_ints() != std::vector<int>{din, 3, dmid})
+                    throw std::invalid_argument("MACEField Wigner tensor shape does not match its path");
+                w3 = ins.at("wigner_3j").as_doubles();
+                if (w3.size() != static_cast<std::size_t>(din) * 3 * dmid)
+                    throw std::invalid_argument("MACEField Wigner tensor has an invalid size");
+            }
+            bool found = false;
+            for (std::size_t li = 0; li < li_list.size(); ++li) {
+                const Value& lins = li_list.at(li);
+                if (lins.at("i_in").as_int() != lmid) continue;
+                found = true;
+                const int lout = lins.at("i_out").as_int();
+                const int dout = 2 * lout + 1;
+                for (int mi = 0; mi < din; ++mi)
+                    for (int c = 0; c < 3; ++c)
+                        for (int mo = 0; mo < dout; ++mo) {
+                            const double w = w3[(static_cast<std::size_t>(mi) * 3 + c) * dout + mo];
+                            if (std::abs(w) > 1e-14)
+                                field_entries.push_back({lin * lin + mi, c, lout * lout + mo, path, cast(w)});
+                        }
+                const double scale = ins.at("path_weight").as_number() * lins.at("path_weight").as_number();
+                for (int in = 0; in < C; ++in)
+                    for (int out = 0; out < C; ++out) {
+                        double v = 0.0;
+                        for (int mid = 0; mid < C; ++mid)
+                            v += wf[fi * cc + static_cast<std::size_t>(in) * C + mid] *
+                                 wl[li * cc + static_cast<std::size_t>(mid) * C + out];
+                        field_W.push_back(cast(scale * v));
+                    }
+                ++path;
+            }
+            if (!found) throw std::invalid_argument("MACEField field_feats output has no field_linear instruction");
+        }
+        if (path == 0) throw std::invalid_argument("MACEField field coupling contains no executable paths");
+    }
+
+    // nested numeric arrays flattened in order
+    static std::vector<double> j_doubles(const Value& v) {
+        std::vector<double> out;
+        if (v.is_array() && !v.numeric_array && v.size() > 0 && v.at(0).is_array()) {
+            for (std::size_t i = 0; i < v.size(); ++i) {
+                const auto r = j_doubles(v.at(i));
+                out.insert(out.end(), r.begin(), r.end());
+            }
+            return out;
+        }
+        return v.as_doubles();
     }
 
     // mace.cpp:119-214
@@ -980,6 +1237,7 @@ struct Mace {
                     for (int k = 0; k < C; ++k) xaff[i * Cs + k] += res_x[static_cast<std::size_t>(t) * C + k];
             }
         }
+        if (has_field) field_forward(n, types);
 
         // ---- Phi1 streamed (mace.cpp:2023-2084)
         const int np = static_cast<int>(Phi1_l.size());
@@ -1272,6 +1530,8 @@ struct Mace {
 
         // ---- reverse H1 + direct adjoint (mace.cpp:1727-1757, 1785-1814)
         M0_adj.assign(static_cast<std::size_t>(n) * num_LM * Cs, P(0));
+        if (has_field) field_reverse(n);
+        if (!has_field) {
 #pragma omp parallel for schedule(static)
         for (int i = 0; i < n; ++i) {
             for (int l = 0; l <= L_max; ++l)
@@ -1297,6 +1557,7 @@ struct Mace {
                 for (int k = 0; k < C; ++k)
                     M0_adj[static_cast<std::size_t>(i) * num_LM * Cs + k] += static_cast<P>(direct[i * Cs + k]);
             }
+        }
         }
 
         // ---- reverse M0 (mace.cpp:1665-1689)
@@ -1586,6 +1847,17 @@ int oracle_atomic_numbers(void* hv, int* out) {
     return 0;
 }
 
+// the electric field of the next evaluations of a MACEField model: 3 values
+// (one field for the graph) or 3 per node; count 0 clears it
+int oracle_set_field(void* hv, const double* field, int count) {
+    return guarded([&]() -> int {
+        auto* h = static_cast<OracleHandle*>(hv);
+        std::vector<double> f(field, field + (count > 0 ? count : 0));
+        if (h->fp64) h->d->field_in = f; else h->f->field_in = f;
+        return 0;
+    });
+}
+
 int oracle_evaluate(void* hv, int n, const int* types, const int* num_neigh, const int* neigh,
                     const int* neigh_types, const double* xyz, const double* r, double* energies,
                     double* forces) {
@@ -1623,6 +1895,9 @@ long long oracle_stage(void* hv, const char* name, double* out, long long capaci
         if (s == "M0") return emit(m.M0);
         if (s == "M0_grad") return emit(m.M0_grad);
         if (s == "H1") return emit(m.H1);
+        if (s == "H1_pre") return emit(m.H1_pre);
+        if (s == "H1_field") return emit(m.H1_field);
+        if (s == "field_adj") return emit(m.field_adj);
         if (s == "Phi1") return emit(m.Phi1);
         if (s == "A1") return emit(m.A1);
         if (s == "M1") return emit(m.M1);

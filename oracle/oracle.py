@@ -44,6 +44,7 @@ def lib():
         L.oracle_evaluate.argtypes = [ctypes.c_void_p, ctypes.c_int, _i32p, _i32p, _i32p, _i32p,
                                       _f64p, _f64p, _f64p, _f64p]
         L.oracle_set_num_threads.argtypes = [ctypes.c_int]
+        L.oracle_set_field.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int]
         L.oracle_stage.restype = ctypes.c_longlong
         L.oracle_stage.argtypes = [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_void_p, ctypes.c_longlong]
         L.oracle_radial_tables.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
@@ -114,7 +115,12 @@ class OracleModel:
         lut = {int(z): i for i, z in enumerate(self.atomic_numbers)}
         return np.array([lut[int(z)] for z in numbers], dtype=np.int32)
 
-    def evaluate(self, node_types, num_neigh, neigh_indices, neigh_types, xyz, r):
+    def evaluate(self, node_types, num_neigh, neigh_indices, neigh_types, xyz, r, field=None):
+        """Node energies and directed forces; a MACEField model needs the
+        electric field (3 values, or 3 per node); dE/dE is then
+        stage("field_adj")."""
+        f64 = None if field is None else _c(field, np.float64).ravel()
+        lib().oracle_set_field(self._h, None if f64 is None else f64.ctypes.data, 0 if f64 is None else f64.size)
         node_types = _c(node_types, np.int32)
         n = len(node_types)
         E = len(neigh_indices)
@@ -237,7 +243,7 @@ def reduce_stress(node_forces, xyz, volume):
     return out.reshape(3, 3)
 
 
-def evaluate_system(model, system, skin=0.5, positions=None, graph=None):
+def evaluate_system(model, system, skin=0.5, positions=None, graph=None, field=None):
     """Energy, atom forces and 3x3 stress of a system with the oracle (the
     caller contract of calculator.py:3821-3894 on a fresh graph)."""
     pos0 = np.asarray(system["positions"], dtype=np.float64)
@@ -247,8 +253,11 @@ def evaluate_system(model, system, skin=0.5, positions=None, graph=None):
     pos = pos0 if positions is None else positions
     xyz, r = prepared_geometry(graph, cell, pos0, pos, model.r_cut)
     types = model.types_of(system["numbers"])
-    e, f = model.evaluate(types, graph["num_neigh"], graph["sources"], types[graph["sources"]], xyz, r)
+    e, f = model.evaluate(types, graph["num_neigh"], graph["sources"], types[graph["sources"]], xyz, r, field)
     forces = reduce_forces(len(types), graph["receivers"], graph["sources"], f)
     stress = reduce_stress(f, xyz, abs(np.linalg.det(cell)))
-    return {"energy": float(np.sum(e)), "energies": e, "forces": forces, "stress": stress,
-            "node_forces": f, "graph": graph, "xyz": xyz, "r": r}
+    out = {"energy": float(np.sum(e)), "energies": e, "forces": forces, "stress": stress,
+           "node_forces": f, "graph": graph, "xyz": xyz, "r": r}
+    if field is not None:
+        out["field_adj"] = model.stage("field_adj")
+    return out

@@ -77,6 +77,11 @@ class ModelConfig:
     single_layer: bool = False
     readout_correlation: int = 2
     zero_affine_maps: bool = False
+    # MACEField (pre_linear_up only): one field coupling, the electric field
+    # (1x1o) times the canonical H1 irreps into the adjacent ranks, then a
+    # per-l channel linear (extract_mace_data.py:562-598,769-819); weights
+    # from default_rng([seed, 4])
+    field: bool = False
     seed: int = 0
 
 
@@ -104,6 +109,12 @@ MODEL_CONFIGS = {
                             r_cut=5.0, avg_num_neighbors=40.0, h1_mode="pre_linear_up"),
     "tiny_residual": ModelConfig("tiny_residual", 32, 2, 1, 2, [8, 22, 38], radial_mlp=[32, 32],
                                  r_cut=5.0, avg_num_neighbors=40.0, h1_mode="pre_linear_up", residual=True),
+    # MACEField models (field_coupling.hpp; mace.cpp:322-395), L_max 1 and 2
+    "tiny_field": ModelConfig("tiny_field", 32, 2, 1, 2, [8, 22, 38], radial_mlp=[32, 32],
+                              r_cut=5.0, avg_num_neighbors=40.0, h1_mode="pre_linear_up", field=True),
+    "tiny_field_l2": ModelConfig("tiny_field_l2", 32, 2, 2, 2, [8, 22, 38], radial_mlp=[32, 32],
+                                 r_cut=5.0, avg_num_neighbors=40.0, h1_mode="pre_linear_up", field=True,
+                                 residual=True),
     # one-interaction models (mace.cpp:255-281), plain and with a residual
     "tiny_single": ModelConfig("tiny_single", 32, 2, 1, 2, [8, 22, 38], radial_mlp=[32, 32],
                                r_cut=5.0, avg_num_neighbors=40.0, single_layer=True),
@@ -173,6 +184,40 @@ def _product_weights(rng, l_in_max, L_out, correlation, num_types, C, scale):
     return monos_all, coef_all
 
 
+def _field_coupling(C, L_max, rng):
+    """One MACEField coupling in the extractor's schema-1 layout
+    (extract_mace_data.py:562-598): field_feats instructions (l_in x 1o ->
+    l_out, adjacent ranks, uvw, path shape (C, 1, C)) with e3nn's real 3j
+    tensor of (l_in, 1, l_out), and field_linear instructions (l -> l,
+    (C, C)); weights flat, [in][out] per instruction, float32 values."""
+    irreps = "+".join("%dx%d%s" % (C, l, "o" if l % 2 else "e") for l in range(L_max + 1))
+    feats, fw = [], []
+    for l_in in range(L_max + 1):
+        for l_out in (l_in - 1, l_in + 1):
+            if not 0 <= l_out <= L_max:
+                continue
+            w3 = e3.wigner_3j(l_in, 1, l_out)
+            feats.append({"i_in1": l_in, "i_in2": 0, "i_out": l_out, "connection_mode": "uvw", "has_weight": True,
+                          "path_weight": float(_f32(1.0 / math.sqrt(C))), "path_shape": [C, 1, C],
+                          "wigner_3j_shape": list(w3.shape), "wigner_3j": [float(v) for v in w3.ravel()]})
+            fw.append(_f32(rng.normal(size=(C, C))))
+    lins, lw = [], []
+    for l in range(L_max + 1):
+        lins.append({"i_in": l, "i_out": l, "path_weight": float(_f32(1.0 / math.sqrt(C))), "path_shape": [C, C]})
+        lw.append(_f32(rng.normal(size=(C, C))))
+    hidden = (L_max + 1) ** 2 * C
+    return {"schema_version": 1,
+            "field_feats_irreps_in1": irreps, "field_feats_irreps_in2": "1x1o", "field_feats_irreps_out": irreps,
+            "field_feats_instructions": feats,
+            "field_feats_weight": np.concatenate([w.ravel() for w in fw]).tolist(),
+            "field_feats_output_mask": [1.0] * hidden,
+            "field_linear_irreps_in": irreps, "field_linear_irreps_out": irreps,
+            "field_linear_instructions": lins,
+            "field_linear_weight": np.concatenate([w.ravel() for w in lw]).tolist(),
+            "field_linear_bias": [],
+            "field_linear_output_mask": [1.0] * hidden}
+
+
 def generate_model(config, seed=None):
     """Return the model as a dict of JSON *text fragments* keyed by JSON key
     (large arrays pre-formatted), plus a small dict of plain metadata."""
@@ -189,13 +234,15 @@ def generate_model(config, seed=None):
         frag[key] = json.dumps(value)
 
     put("symmetrix_format_version", 4)
-    put("model_type", "MACE")
+    put("model_type", "MACEField" if cfg.field else "MACE")
     if cfg.h1_mode not in ("m0_composite", "pre_linear_up"):
         raise ValueError("h1_mode must be m0_composite or pre_linear_up")
     if cfg.residual and cfg.h1_mode != "pre_linear_up" and not cfg.single_layer:
         raise ValueError("a first-interaction residual needs the pre_linear_up basis")
     if cfg.h1_mode == "pre_linear_up" and (cfg.prediction_heads or cfg.single_layer):
         raise ValueError("the pre_linear_up basis is generated for two-interaction models without heads")
+    if cfg.field and (cfg.h1_mode != "pre_linear_up" or not 1 <= cfg.L_max <= 2):
+        raise ValueError("a MACEField model needs the pre_linear_up basis and 1 <= L_max <= 2")
     pre = cfg.h1_mode == "pre_linear_up"
     put("h1_affine_mode", cfg.h1_mode)
     put("h1_affine_version", 1)
@@ -310,6 +357,9 @@ def generate_model(config, seed=None):
         put("first_interaction_residual", bool(cfg.residual))
         if cfg.residual:
             frag["H1_first_residual_weights"] = _fmt(0.3 * prng.normal(size=(n_el, num_LM, C)))
+    if cfg.field:
+        put("has_field_coupling", True)
+        frag["field_couplings"] = json.dumps([_field_coupling(C, L_max, np.random.default_rng([seed, 4]))])
     frag["H1_weights"] = _fmt(h1)
 
     if cfg.single_layer:

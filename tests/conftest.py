@@ -84,6 +84,18 @@ def tiny_single_residual_model_path():
 
 
 @pytest.fixture(scope="session")
+def tiny_field_model_path():
+    from symmetrix import random_model
+    return random_model.cached_model("tiny_field", directory=MODEL_DIR)
+
+
+@pytest.fixture(scope="session")
+def tiny_field_l2_model_path():
+    from symmetrix import random_model
+    return random_model.cached_model("tiny_field_l2", directory=MODEL_DIR)
+
+
+@pytest.fixture(scope="session")
 def medium_single_model_path():
     from symmetrix import random_model
     return random_model.cached_model("medium_single", directory=MODEL_DIR)
