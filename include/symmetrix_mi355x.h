@@ -227,6 +227,30 @@ SMX_API int32_t smx_compute_prepared_factorized_positions(SmxEvaluator* ev, uint
  * are ready for work ordered on that stream or after smx_synchronize. */
 SMX_API int32_t smx_compute_prepared_factorized_positions_device(SmxEvaluator* ev, uint64_t generation,
                                                                  const double* positions_device);
+/* MACEField models (field_coupling.hpp; mace.cpp:322-395, 1147-1240).
+ * _compute_prepared_factorized_positions_field(token, positions,
+ * electric_field) and _compute_prepared_factorized_field(token, xyz, r,
+ * electric_field) (pybind mace_kokkos.cpp:1837-1864): the positions and xyz
+ * evaluations of a field-coupled model in an electric field of 3 values (one
+ * field for the graph) or 3 per node (field_count 3 or 3*num_nodes).  The
+ * field stays set for later evaluations (the plain entry points and the
+ * LAMMPS entry).  A model without field coupling refuses a field; a
+ * field-coupled model refuses an evaluation without one, and the tiled plans
+ * (mace_kokkos_runtime.cpp:3005, 3042). */
+SMX_API int32_t smx_compute_prepared_factorized_positions_field(SmxEvaluator* ev, uint64_t generation,
+                                                                const double* positions, const double* field,
+                                                                int64_t field_count);
+SMX_API int32_t smx_compute_prepared_factorized_field(SmxEvaluator* ev, uint64_t generation, const double* xyz,
+                                                      const double* r, const double* field, int64_t field_count);
+/* the field of later evaluations (the pair style's electric_field Ex Ey Ez
+ * keyword, pair_symmetrix_mace_kokkos.cpp:207-224); field_count 0 clears it */
+SMX_API int32_t smx_set_electric_field(SmxEvaluator* ev, const double* field, int64_t field_count);
+/* electric_field_adj (pybind mace_kokkos.cpp:2156): dE/dE of the last field
+ * evaluation, shaped like its field (3, or 3 per node); FP64 sums.  *count
+ * gets the length; copies when out != NULL and capacity is large enough. */
+SMX_API int32_t smx_electric_field_adj(SmxEvaluator* ev, double* out, int64_t capacity, int64_t* count);
+/* has_field_coupling (the model file's flag, mace.cpp:2832) */
+SMX_API int32_t smx_has_field_coupling(const SmxEvaluator* ev, int32_t* out);
 /* compute_node_energies_forces with execution_graph_generation == 0
  * (mace_kokkos.hpp:654-662; pybind mace_kokkos.cpp:2169): prepares the
  * graph from the host CSR, then evaluates. */

@@ -215,6 +215,15 @@ struct Evaluator {
     DevBuf d_groups_a0, d_groups_h1, d_groups_a1f, d_groups_a1r, d_groups_cap, d_groups_cap_r;
     int max_n_a0 = 0, max_n_h1 = 0, max_n_a1f = 0, max_n_a1r = 0;
     int sub_a0 = 1, sub_h1 = 1, sub_a1f = 1, sub_a1r = 1, sub_cap = 1;
+    // MACEField path products: Z rows per path (l_in m's), Y rows (l_out m's)
+    std::vector<GemmGroup> groups_fz, groups_fy;
+    DevBuf d_groups_fz, d_groups_fy;
+    int sub_f = 1;
+    // the electric field of the next evaluations (FP64 on the device): 3
+    // values, or 3 per node; dE/dE of the last one
+    std::vector<double> h_efield;
+    DevBuf d_efield, d_field_part, d_field_adj;
+    bool field_evaluated = false;
 
     // execution plan request (set_execution_plan_request, set_allow_fixed_workspace,
     // mace_kokkos.hpp:95-96; the calculator's execution_profile and
@@ -244,7 +253,7 @@ struct Evaluator {
     DevBuf d_node_types, d_offsets, d_neigh, d_neigh_types, d_receivers, d_soff, d_sedges, d_counts;
     // receiver tiles
     std::vector<TileView> tiles;
-    PlanSet ps_a0, ps_h1, ps_a1f, ps_a1r, ps_cap;
+    PlanSet ps_a0, ps_h1, ps_a1f, ps_a1r, ps_cap, ps_fz, ps_fy;
     std::vector<int> h_node_list;
     std::vector<std::size_t> node_list_begin;
     std::vector<NodeBatch> h_batches;
@@ -266,6 +275,7 @@ struct Evaluator {
     DevBuf d_xyz, d_r, d_invalid;
     DevBuf w_erec, w_Phi0, w_A0, w_M0, w_Phi1, w_A1, w_A1_adj, w_M1, w_dPhi1, w_Wsrc, w_M0_adj, w_A0_adj, w_Phi0_adj,
         w_node_forces, w_density;
+    DevBuf g_H1p, g_H1f, g_H1p_adj, g_fzy;
     DevBuf g_H1, g_H1_adj, g_xaff, g_direct, g_direct_m0, d_node_energies, d_atom_forces, d_virial, d_stress, d_stress_partial,
         d_total;
     Workspace ws;
@@ -392,6 +402,33 @@ struct Evaluator {
             dm.res_H1 = put(hm.res_H1);
             dm.res_x = put(hm.res_x);
         }
+        dm.field = hm.field;
+        if (hm.field) {
+            const int nl = hm.L_max + 1, np = static_cast<int>(hm.field_paths.size());
+            dm.P_w = put(swizzled(hm.P_all, nl, hm.C, hm.C));
+            dm.P_wt = put(swizzled(hm.P_allt, nl, hm.C, hm.C));
+            dm.U_w = put(swizzled(hm.U_all, nl, hm.C, hm.C));
+            dm.U_wt = put(swizzled(hm.U_allt, nl, hm.C, hm.C));
+            dm.field_W = put(swizzled(hm.field_W, np, hm.C, hm.C));
+            dm.field_Wt = put(swizzled(hm.field_Wt, np, hm.C, hm.C));
+            if (hm.residual) dm.res_pre = put(hm.res_pre);
+            // Z rows: each path's l_in m's in turn; Y rows: its l_out m's
+            std::vector<int> zoff(np + 1, 0), yoff(np + 1, 0);
+            for (int p = 0; p < np; ++p) {
+                zoff[p + 1] = zoff[p] + 2 * hm.field_paths[p].l_in + 1;
+                yoff[p + 1] = yoff[p] + 2 * hm.field_paths[p].l_out + 1;
+            }
+            std::vector<FieldEntryDev> ent;
+            for (const auto& e : hm.field_entries) {
+                const auto& fp = hm.field_paths[e.path];
+                ent.push_back(FieldEntryDev{e.lm_in, e.comp, e.lm_out, zoff[e.path] + e.lm_in - fp.l_in * fp.l_in,
+                                            yoff[e.path] + e.lm_out - fp.l_out * fp.l_out, e.coef});
+            }
+            dm.field_entries = put(ent);
+            dm.num_field_entries = static_cast<int>(ent.size());
+            dm.field_zr = zoff[np];
+            dm.field_yr = yoff[np];
+        }
         dm.cg = put(hm.cg_dense);
         {
             std::vector<float> w(hm.A1_w.size()), wt(hm.A1_wt.size());
@@ -480,6 +517,22 @@ struct Evaluator {
             upload(d_groups_cap, groups_cap, stream);
             upload(d_groups_cap_r, groups_cap_r, stream);
         }
+        if (hm.field) {
+            // per path: Z = H1p[l_in rows] W into its Z rows, Y = H1p_adj[l_out
+            // rows] W^T into its Y rows
+            int zo = 0, yo = 0;
+            for (std::size_t p = 0; p < hm.field_paths.size(); ++p) {
+                const auto& fp = hm.field_paths[p];
+                const std::int64_t w = static_cast<std::int64_t>(p) * C * C;
+                groups_fz.push_back(GemmGroup{w, C, C, NH * C, fp.l_in * fp.l_in * C, C, dm.field_zr * C, zo * C, C});
+                groups_fy.push_back(GemmGroup{w, C, C, NH * C, fp.l_out * fp.l_out * C, C, dm.field_yr * C, yo * C, C});
+                zo += 2 * fp.l_in + 1;
+                yo += 2 * fp.l_out + 1;
+            }
+            sub_f = sub(groups_fz);
+            upload(d_groups_fz, groups_fz, stream);
+            upload(d_groups_fy, groups_fy, stream);
+        }
     }
 
     // ------------------------------------------------------------- planning
@@ -518,7 +571,10 @@ struct Evaluator {
         plan_available = free_b + workspace_bytes();
         plan_untiled = untiled_bytes(N, E);
         plan_tiled = tiled_bytes(N, E);
-        // mace_kokkos_runtime.cpp:2996-3030: each tiled plan admits its own model kind
+        // mace_kokkos_runtime.cpp:2996-3030: each tiled plan admits its own
+        // model kind, and neither admits field coupling
+        if (hm.field && (debug_plan == kPlanTiled || debug_plan == kPlanSingleTiled))
+            throw std::invalid_argument(debug_plan + " does not support field coupling");
         if (debug_plan == kPlanTiled && !two_layer())
             throw std::invalid_argument("mh0-dual-layer-tiled-v1 requires an ordinary two-layer MACE model");
         if (debug_plan == kPlanSingleTiled && two_layer())
@@ -544,6 +600,10 @@ struct Evaluator {
             plan_source = "planner";
             plan_reason = tiled ? "the retained workspace exceeds 70% of the available device memory"
                                 : "the retained workspace fits 70% of the available device memory";
+        }
+        if (hm.field && tiled) {
+            tiled = false;
+            plan_reason = "field coupling runs in the retained direct plan";
         }
         if (N <= tile_limit && debug_plan != tiled_plan() && tiled) {
             tiled = false;
@@ -625,7 +685,7 @@ struct Evaluator {
         node_list_begin.clear();
         h_batches.clear();
         batch_begin.clear();
-        for (PlanSet* p : {&ps_a0, &ps_h1, &ps_a1f, &ps_a1r, &ps_cap}) {
+        for (PlanSet* p : {&ps_a0, &ps_h1, &ps_a1f, &ps_a1r, &ps_cap, &ps_fz, &ps_fy}) {
             p->tiles.clear();
             p->tile_begin.clear();
             p->rows.clear();
@@ -642,7 +702,7 @@ struct Evaluator {
                 return h_node_types[t.r0 + a] < h_node_types[t.r0 + b];
             });
             h_node_list.insert(h_node_list.end(), order.begin(), order.end());
-            for (PlanSet* p : {&ps_a0, &ps_h1, &ps_a1f, &ps_a1r, &ps_cap}) {
+            for (PlanSet* p : {&ps_a0, &ps_h1, &ps_a1f, &ps_a1r, &ps_cap, &ps_fz, &ps_fy}) {
                 p->tile_begin.push_back(p->tiles.size());
                 p->set_begin.push_back(p->sets.size());
             }
@@ -671,6 +731,10 @@ struct Evaluator {
             }
             for (int l = 0; l <= hm.L_max; ++l) add(ps_h1, l, l, 0, t.nr);
             if (hm.pre_linear_up) add(ps_cap, 0, 0, 0, t.nr);
+            for (std::size_t p = 0; p < hm.field_paths.size(); ++p) {
+                add(ps_fz, static_cast<int>(p), hm.field_paths[p].l_in, 0, t.nr);
+                add(ps_fy, static_cast<int>(p), hm.field_paths[p].l_out, 0, t.nr);
+            }
             for (int l = 0; l <= hm.l_max; ++l) {
                 if (hm.num_e[l] == 0) continue;
                 add(ps_a1f, l, l, 0, t.nr);
@@ -678,7 +742,7 @@ struct Evaluator {
             }
         }
         batch_begin.push_back(h_batches.size());
-        for (PlanSet* p : {&ps_a0, &ps_h1, &ps_a1f, &ps_a1r, &ps_cap}) {
+        for (PlanSet* p : {&ps_a0, &ps_h1, &ps_a1f, &ps_a1r, &ps_cap, &ps_fz, &ps_fy}) {
             p->tile_begin.push_back(p->tiles.size());
             p->set_begin.push_back(p->sets.size());
             upload(p->d_tiles, p->tiles, stream);
@@ -708,6 +772,10 @@ struct Evaluator {
             if (hm.pre_linear_up) {
                 tiles[ti].cap = view(ps_cap, ti, d_groups_cap, hm.C, sub_cap);
                 tiles[ti].cap_r = view(ps_cap, ti, d_groups_cap_r, hm.C, sub_cap);
+            }
+            if (hm.field) {
+                tiles[ti].fz = view(ps_fz, ti, d_groups_fz, hm.C, sub_f);
+                tiles[ti].fy = view(ps_fy, ti, d_groups_fy, hm.C, sub_f);
             }
             tiles[ti].node_list = d_node_list.as<int>() + node_list_begin[ti];
             tiles[ti].batches = d_batches.as<NodeBatch>() + batch_begin[ti];
@@ -773,6 +841,14 @@ struct Evaluator {
         ws.xaff = f(g_xaff, n * C);
         ws.direct = f(g_direct, n * C);
         if (hm.pre_linear_up) ws.direct_m0 = f(g_direct_m0, n * C);
+        if (hm.field) {
+            ws.H1p = f(g_H1p, n * NH * C);
+            ws.H1f = f(g_H1f, n * NH * C);
+            ws.H1p_adj = f(g_H1p_adj, n * NH * C);
+            ws.fzy = f(g_fzy, n * static_cast<std::size_t>(std::max(dm.field_zr, dm.field_yr)) * C);
+            ws.field_part = static_cast<double*>(d_field_part.ensure(n * 3 * sizeof(double)));
+            d_field_adj.ensure(3 * sizeof(double));
+        }
         ws.node_energies = static_cast<double*>(d_node_energies.ensure(n * sizeof(double)));
         d_atom_forces.ensure(n * 3 * sizeof(double));
         d_virial.ensure(9 * sizeof(double));
@@ -1099,8 +1175,39 @@ struct Evaluator {
             launch_fill_zero(ws.A1, static_cast<std::size_t>(std::max(max_tile_nr, 1)) * hm.num_lm * hm.C, stream);
     }
 
+    // the electric field of the next evaluations (mace.cpp:1147-1160): 3
+    // values (one field for the graph) or 3 per node; an empty field clears it
+    void set_field(const double* field, std::int64_t count) {
+        if (count < 0 || (count > 0 && !field)) throw std::invalid_argument("electric_field is required");
+        if (count > 0 && !hm.field)
+            throw std::invalid_argument("the model has no field coupling; it takes no electric_field");
+        for (std::int64_t i = 0; i < count; ++i)
+            if (!std::isfinite(field[i])) throw std::invalid_argument("electric_field must be finite");
+        if (count > 0 && count != 3 && count % 3 != 0)
+            throw std::invalid_argument("MACEField electric_field must have shape (3,) or (num_nodes, 3).");
+        h_efield.assign(field, field + count);
+        if (count > 0) upload(d_efield, h_efield, stream);
+    }
+
+    // the field's device pointers for this evaluation (mace.cpp:1151-1154)
+    void bind_field() {
+        field_evaluated = false;
+        if (!hm.field) return;
+        if (h_efield.size() != 3 && h_efield.size() != 3 * static_cast<std::size_t>(N))
+            throw std::invalid_argument(h_efield.empty()
+                                            ? "a MACEField model is evaluated with an electric field (shape (3,) or "
+                                              "(num_nodes, 3))"
+                                            : "MACEField electric_field must have shape (3,) or (num_nodes, 3).");
+        ws.efield = d_efield.as<double>();
+        ws.efield_per_node = h_efield.size() != 3;
+        ws.field_adj = ws.efield_per_node ? ws.field_part : d_field_adj.as<double>();
+        if (N == 0) launch_fill_zero(ws.field_adj, 3, stream);
+        field_evaluated = true;
+    }
+
     void evaluate(const double* positions) {
         const DeviceGraph g = view();
+        bind_field();
         for (auto& t : tiles) {
             t.r = tile_r(t);
             t.xyz = tile_xyz(t);
@@ -1863,6 +1970,53 @@ int32_t smx_compute_prepared_factorized_positions_device(SmxEvaluator* ev, uint6
         if (e.N > 0 && !positions_device) throw std::invalid_argument("positions are required");
         timed(e.last_evaluation_ms, e.evaluation_count,
               [&] { e.compute_positions(generation, positions_device, true); });
+    });
+}
+
+int32_t smx_set_electric_field(SmxEvaluator* ev, const double* field, int64_t count) {
+    return guarded([&] { E(ev).set_field(field, count); });
+}
+
+int32_t smx_has_field_coupling(const SmxEvaluator* ev, int32_t* out) {
+    return guarded([&] {
+        if (!out) throw std::invalid_argument("out is NULL");
+        *out = E(ev).hm.field ? 1 : 0;
+    });
+}
+
+int32_t smx_compute_prepared_factorized_positions_field(SmxEvaluator* ev, uint64_t generation,
+                                                        const double* positions, const double* field,
+                                                        int64_t field_count) {
+    return guarded([&] {
+        auto& e = E(ev);
+        if (e.N > 0 && !positions) throw std::invalid_argument("positions are required");
+        if (!e.hm.field) throw std::invalid_argument("the model has no field coupling; it takes no electric_field");
+        e.set_field(field, field_count);
+        timed(e.last_evaluation_ms, e.evaluation_count, [&] { e.compute_positions(generation, positions, false); });
+    });
+}
+
+int32_t smx_compute_prepared_factorized_field(SmxEvaluator* ev, uint64_t generation, const double* xyz,
+                                              const double* r, const double* field, int64_t field_count) {
+    return guarded([&] {
+        auto& e = E(ev);
+        if (e.E > 0 && (!xyz || !r)) throw std::invalid_argument("xyz and r are required");
+        if (!e.hm.field) throw std::invalid_argument("the model has no field coupling; it takes no electric_field");
+        e.set_field(field, field_count);
+        timed(e.last_evaluation_ms, e.evaluation_count, [&] { e.compute_xyz(generation, xyz, r); });
+    });
+}
+
+int32_t smx_electric_field_adj(SmxEvaluator* ev, double* out, int64_t capacity, int64_t* count) {
+    return guarded([&] {
+        auto& e = E(ev);
+        if (!e.field_evaluated || !e.evaluated) throw std::logic_error("no field evaluation has run");
+        const std::int64_t n = static_cast<std::int64_t>(e.h_efield.size());
+        if (count) *count = n;
+        if (!out) return;
+        if (capacity < n) throw std::invalid_argument("buffer too small");
+        SMX_HIP(hipMemcpyAsync(out, e.ws.field_adj, n * sizeof(double), hipMemcpyDeviceToHost, e.stream));
+        SMX_HIP(hipStreamSynchronize(e.stream));
     });
 }
 

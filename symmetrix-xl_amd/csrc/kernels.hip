@@ -234,7 +234,9 @@ __global__ __launch_bounds__(C) void k_m0_reverse_ct(int r0, const int* __restri
     static_range<0, NH>([&](auto LMc) {
         constexpr int LM = LMc;
         float adj = M0_adj[(static_cast<std::size_t>(li) * NH + LM) * C + k];
-        if constexpr (LM == 0) adj += direct[static_cast<std::size_t>(i) * C + k];
+        if constexpr (LM == 0) {
+            if (direct) adj += direct[static_cast<std::size_t>(i) * C + k];
+        }
         float g[NY];
 #pragma unroll
         for (int v = 0; v < NY; ++v) g[v] = 0.0f;
@@ -289,7 +291,7 @@ __global__ __launch_bounds__(C) void k_m0_reverse(int r0, const int* __restrict_
     for (int LM = 0; LM < NH; ++LM) {
         const int begin = toff[LM], end = toff[LM + 1];
         float adj = M0_adj[(static_cast<std::size_t>(li) * NH + LM) * C + k];
-        if (LM == 0) adj += direct[static_cast<std::size_t>(i) * C + k];
+        if (LM == 0 && direct) adj += direct[static_cast<std::size_t>(i) * C + k];
 #pragma unroll
         for (int v = 0; v < NY; ++v) gs[v * C + k] = 0.0f;
         for (int t = begin; t < end; ++t) monomial_grad(xs, gs, C, k, terms[t], cf[static_cast<std::size_t>(t) * C]);
@@ -616,6 +618,94 @@ __global__ __launch_bounds__(256) void k_type_bias(int r0, int nr, const int* __
     if (idx >= static_cast<long long>(nr) * row_len) return;
     const int li = static_cast<int>(idx / row_len), c = static_cast<int>(idx % row_len);
     rows[idx] += bias[static_cast<std::size_t>(types[r0 + li]) * row_len + c];
+}
+
+// ---------------------------------------------------------------------------
+// MACEField field terms (mace_kokkos_h1_phi1.cpp:846-1150).  One workgroup per
+// node, lanes over channels; the path products Z = H1p[l_in rows] W and
+// Y = H1p_adj[l_out rows] W^T come from the node GEMM, so these kernels only
+// mix the m components with the entries' coef E_comp.
+// ---------------------------------------------------------------------------
+// H1f[i,lm] = H1p[i,lm] + sum over the entries into lm of coef E_comp Z[i,zrow];
+// x = H1f[i,0,:] (the scalar input of readout_1 and the skip)
+__global__ void k_field_combine(int r0, int NH, int C, int zr, const FieldEntryDev* __restrict__ entries, int ne,
+                                const double* __restrict__ field, int per_node, const float* __restrict__ H1p,
+                                const float* __restrict__ Z, float* __restrict__ H1f, float* __restrict__ xaff) {
+    const int i = r0 + static_cast<int>(blockIdx.x);
+    const int k = threadIdx.x;
+    const double* E = field + (per_node ? 3 * static_cast<std::size_t>(i) : 0);
+    const std::size_t base = static_cast<std::size_t>(i) * NH * C;
+    const float* z = Z + static_cast<std::size_t>(i) * zr * C;
+    for (int lm = 0; lm < NH; ++lm) {
+        float v = H1p[base + static_cast<std::size_t>(lm) * C + k];
+        for (int e = 0; e < ne; ++e) {
+            const FieldEntryDev en = entries[e];
+            if (en.lm_out != lm) continue;
+            v += (en.coef * static_cast<float>(E[en.comp])) * z[static_cast<std::size_t>(en.zrow) * C + k];
+        }
+        H1f[base + static_cast<std::size_t>(lm) * C + k] = v;
+        if (lm == 0) xaff[static_cast<std::size_t>(i) * C + k] = v;
+    }
+}
+
+// H1p_adj[i,0,:] += direct[i,:] (x = H1f[:,0,:], mace.cpp:1798-1804)
+__global__ void k_field_direct_add(int r0, int NH, int C, const float* __restrict__ direct,
+                                   float* __restrict__ H1p_adj) {
+    const int i = r0 + static_cast<int>(blockIdx.x);
+    const int k = threadIdx.x;
+    H1p_adj[static_cast<std::size_t>(i) * NH * C + k] += direct[static_cast<std::size_t>(i) * C + k];
+}
+
+// H1p_adj[i,lm] += sum over the entries from lm of E_comp (coef Y[i,yrow]) and
+// the node's dE/dE_c = sum of H1p[i,lm_in,k] coef Y[i,yrow,k] (FP32 products,
+// FP64 sums) into part[i][c]
+template <int C>
+__global__ __launch_bounds__(C) void k_field_reverse_combine(int r0, int NH, int yr,
+                                                            const FieldEntryDev* __restrict__ entries, int ne,
+                                                            const double* __restrict__ field, int per_node,
+                                                            const float* __restrict__ H1p, const float* __restrict__ Y,
+                                                            float* __restrict__ H1p_adj, double* __restrict__ part) {
+    __shared__ double sbuf[Lanes<C>::NW];
+    const int i = r0 + static_cast<int>(blockIdx.x);
+    const int k = threadIdx.x;
+    const double* E = field + (per_node ? 3 * static_cast<std::size_t>(i) : 0);
+    const std::size_t base = static_cast<std::size_t>(i) * NH * C;
+    const float* y = Y + static_cast<std::size_t>(i) * yr * C;
+    double acc[3] = {0.0, 0.0, 0.0};
+    for (int lm = 0; lm < NH; ++lm) {
+        float v = H1p_adj[base + static_cast<std::size_t>(lm) * C + k];
+        const float hp = H1p[base + static_cast<std::size_t>(lm) * C + k];
+        for (int e = 0; e < ne; ++e) {
+            const FieldEntryDev en = entries[e];
+            if (en.lm_in != lm) continue;
+            const float contribution = en.coef * y[static_cast<std::size_t>(en.yrow) * C + k];
+            v += static_cast<float>(E[en.comp]) * contribution;
+            acc[en.comp] += static_cast<double>(hp * contribution);
+        }
+        H1p_adj[base + static_cast<std::size_t>(lm) * C + k] = v;
+    }
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+        const double t = block_sum<C>(acc[c], sbuf);
+        if (k == 0) part[3 * static_cast<std::size_t>(i) + c] = t;
+    }
+}
+
+// dE/dE of a graph field: out[c] = sum_i part[i][c] in a fixed order
+__global__ __launch_bounds__(256) void k_field_adj_sum(int N, const double* __restrict__ part, double* __restrict__ out) {
+    __shared__ double sbuf[256];
+    for (int c = 0; c < 3; ++c) {
+        double t = 0.0;
+        for (int i = threadIdx.x; i < N; i += 256) t += part[3 * static_cast<std::size_t>(i) + c];
+        sbuf[threadIdx.x] = t;
+        __syncthreads();
+        for (int w = 128; w > 0; w >>= 1) {
+            if (static_cast<int>(threadIdx.x) < w) sbuf[threadIdx.x] += sbuf[threadIdx.x + w];
+            __syncthreads();
+        }
+        if (threadIdx.x == 0) out[c] = sbuf[0];
+        __syncthreads();
+    }
 }
 
 __global__ void k_fill_f32(std::size_t n, float* __restrict__ p) {
@@ -976,6 +1066,10 @@ struct KernelSetImpl final : KernelSet {
                                                                 m.T0, m.m0_coef, w.M0, w.xaff);
             SMX_LAUNCH_CHECK("m0_forward");
         }
+        if (m.field) {
+            field_forward(m, g, t, w, s, tm);
+            return;
+        }
         {
             TimerScope ts(tm, "h1_linear", s);
             launch_node_gemm(t.h1, m.H1_w, w.M0, w.H1 + static_cast<std::size_t>(t.r0) * S::NH * C, s);
@@ -995,6 +1089,45 @@ struct KernelSetImpl final : KernelSet {
             launch_type_bias(t.r0, t.nr, g.node_types, S::NH * C, m.res_H1,
                              w.H1 + static_cast<std::size_t>(t.r0) * S::NH * C, s);
         }
+    }
+
+    // MACEField H1 (mace.cpp:1845-1895, 1147-1186): H1p = M0 P (+ b),
+    // Z = H1p[l_in rows] W per path, H1f = H1p + coef E Z (and x = H1f[:,0,:]),
+    // H1 = H1f U
+    void field_forward(const DeviceModel& m, const DeviceGraph& g, const TileView& t, const Workspace& w,
+                       hipStream_t s, LaunchTimer* tm) const {
+        TimerScope ts(tm, "h1_field", s);
+        const std::size_t row0 = static_cast<std::size_t>(t.r0) * S::NH * C;
+        launch_node_gemm(t.h1, m.P_w, w.M0, w.H1p + row0, s);
+        if (m.residual) launch_type_bias(t.r0, t.nr, g.node_types, S::NH * C, m.res_pre, w.H1p + row0, s);
+        launch_node_gemm(t.fz, m.field_W, w.H1p + row0, w.fzy + static_cast<std::size_t>(t.r0) * m.field_zr * C, s);
+        k_field_combine<<<t.nr, C, 0, s>>>(t.r0, S::NH, C, m.field_zr, m.field_entries, m.num_field_entries, w.efield,
+                                           w.efield_per_node, w.H1p, w.fzy, w.H1f, w.xaff);
+        SMX_LAUNCH_CHECK("field_combine");
+        launch_node_gemm(t.h1, m.U_w, w.H1f + row0, w.H1 + row0, s);
+    }
+
+    // its reverse (mace.cpp:1897-1940, 1189-1240): H1p_adj = H1_adj U^T + x's
+    // adjoint on lm 0, Y = H1p_adj[l_out rows] W^T, H1p_adj += coef E Y with
+    // dE/dE, M0_adj = H1p_adj P^T
+    void field_reverse(const DeviceModel& m, const TileView& t, const Workspace& w, int N, hipStream_t s,
+                       LaunchTimer* tm) const {
+        TimerScope ts(tm, "h1_field_reverse", s);
+        const std::size_t row0 = static_cast<std::size_t>(t.r0) * S::NH * C;
+        launch_node_gemm(t.h1, m.U_wt, w.H1_adj + row0, w.H1p_adj + row0, s);
+        k_field_direct_add<<<t.nr, C, 0, s>>>(t.r0, S::NH, C, w.direct, w.H1p_adj);
+        SMX_LAUNCH_CHECK("field_direct_add");
+        launch_node_gemm(t.fy, m.field_Wt, w.H1p_adj + row0, w.fzy + static_cast<std::size_t>(t.r0) * m.field_yr * C,
+                         s);
+        k_field_reverse_combine<C><<<t.nr, C, 0, s>>>(t.r0, S::NH, m.field_yr, m.field_entries, m.num_field_entries,
+                                                      w.efield, w.efield_per_node, w.H1p, w.fzy, w.H1p_adj,
+                                                      w.field_part);
+        SMX_LAUNCH_CHECK("field_reverse_combine");
+        if (!w.efield_per_node) {
+            k_field_adj_sum<<<1, 256, 0, s>>>(N, w.field_part, w.field_adj);
+            SMX_LAUNCH_CHECK("field_adj_sum");
+        }
+        launch_node_gemm(t.h1, m.P_wt, w.H1p_adj + row0, w.M0_adj, s);
     }
 
     void layer2(const DeviceModel& m, const DeviceGraph& g, const TileView& t, const Workspace& w, hipStream_t s,
@@ -1102,14 +1235,18 @@ struct KernelSetImpl final : KernelSet {
     void layer1_reverse(const DeviceModel& m, const DeviceGraph& g, const TileView& t, const Workspace& w,
                         bool accumulate_forces, hipStream_t s, LaunchTimer* tm) const override {
         if (t.nr == 0) return;
-        {
+        // the direct adjoint of the readout_1 / skip input enters M0_adj[:,0,:]
+        // as is (m0_composite) or as P0 d (pre_linear_up, mace.cpp:1785-1814);
+        // with field coupling it entered H1p_adj[:,0,:] already
+        const float* direct = w.direct;
+        if (m.field) {
+            field_reverse(m, t, w, g.N, s, tm);
+            direct = nullptr;
+        } else {
             TimerScope ts(tm, "h1_linear_reverse", s);
             launch_node_gemm(t.h1, m.H1_wt, w.H1_adj + static_cast<std::size_t>(t.r0) * S::NH * C, w.M0_adj, s);
         }
-        // the direct adjoint of the readout_1 / skip input enters M0_adj[:,0,:]
-        // as is (m0_composite) or as P0 d (pre_linear_up, mace.cpp:1785-1814)
-        const float* direct = w.direct;
-        if (m.pre_linear_up) {
+        if (m.pre_linear_up && !m.field) {
             TimerScope ts(tm, "h1_affine_scalar_reverse", s);
             launch_node_gemm(t.cap_r, m.P0_wt, w.direct + static_cast<std::size_t>(t.r0) * C,
                              w.direct_m0 + static_cast<std::size_t>(t.r0) * C, s);

@@ -11,6 +11,14 @@
 
 namespace smx {
 
+// One angular entry of a MACEField path: H1f[lm_out] += coef E_comp Z[zrow]
+// (Z = H1p[lm_in] W_path) forward; H1p_adj[lm_in] += coef E_comp Y[yrow]
+// (Y = H1p_adj[lm_out] W_path^T) in reverse.
+struct FieldEntryDev {
+    int lm_in, comp, lm_out, zrow, yrow;
+    float coef;
+};
+
 // Model tables resident in HBM (owned by the evaluator).
 struct DeviceModel {
     int C = 0, l_max = 0, L_max = 0, num_lm = 0, num_LM = 0, num_elements = 0;
@@ -35,6 +43,19 @@ struct DeviceModel {
     bool pre_linear_up = false, residual = false;
     // one interaction: M1 of H1, no R1 / A1 (single_layer_readout)
     bool single_layer = false;
+    // MACEField: H1p = M0 P (+ b), H1f = H1p + field terms, x = H1f[:,0,:],
+    // H1 = H1f U (GEMM weights swizzled: P, U per l; W per path)
+    bool field = false;
+    const float* P_w = nullptr;
+    const float* P_wt = nullptr;
+    const float* U_w = nullptr;
+    const float* U_wt = nullptr;
+    const float* field_W = nullptr;
+    const float* field_Wt = nullptr;
+    const float* res_pre = nullptr;  // [type][NH][C]
+    const FieldEntryDev* field_entries = nullptr;
+    int num_field_entries = 0;
+    int field_zr = 0, field_yr = 0;  // rows of Z and Y per node
     const float* P0_w = nullptr;
     const float* P0_wt = nullptr;
     const float* res_H1 = nullptr;  // [type][NH][C]
@@ -137,6 +158,7 @@ struct TileView {
     std::int64_t e0 = 0, ne = 0;
     GemmPlan a0, h1, a1f, a1r;
     GemmPlan cap, cap_r;  // pre_linear_up: x = M0[:,0,:] P0 and its reverse P0 d (rows (node, 0))
+    GemmPlan fz, fy;      // MACEField: Z = H1p[l_in rows] W_path, Y = H1p_adj[l_out rows] W_path^T
     const int* node_list = nullptr;    // tile-local receivers sorted by type
     const NodeBatch* batches = nullptr;
     int num_batches = 0;
@@ -180,6 +202,17 @@ struct Workspace {
     float* direct = nullptr;    // [N][C] direct adjoint of the scalar capture
     float* direct_m0 = nullptr; // [N][C] pre_linear_up: that adjoint carried to M0[:,0,:] (P0 d)
     double* node_energies = nullptr;  // [N]
+    // MACEField (direct plan, graph-wide): the field of this evaluation
+    // (FP64, 3 values or 3 per node), H1p, H1f, H1p's adjoint, the Z / Y
+    // rows of the field paths, per-node dE/dE partials and dE/dE
+    const double* efield = nullptr;
+    int efield_per_node = 0;
+    float* H1p = nullptr;       // [N][NH][C]
+    float* H1f = nullptr;       // [N][NH][C]
+    float* H1p_adj = nullptr;   // [N][NH][C]
+    float* fzy = nullptr;       // [N][max(zr, yr)][C]
+    double* field_part = nullptr;  // [N][3]
+    double* field_adj = nullptr;   // [3] or [N][3]
 };
 
 // Timing hook: the evaluator brackets launches with events when enabled.

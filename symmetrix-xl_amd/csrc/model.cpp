@@ -395,6 +395,15 @@ void HostModel::pad_channels(int Cp) {
         pad_rows(res_H1, static_cast<std::size_t>(num_elements) * num_LM);
         pad_rows(res_x, static_cast<std::size_t>(num_elements));
     }
+    if (field) {
+        pad_square(P_all, L_max + 1);
+        transpose_blocks(P_all, P_allt, L_max + 1, Cp, Cp);
+        pad_square(U_all, L_max + 1);
+        transpose_blocks(U_all, U_allt, L_max + 1, Cp, Cp);
+        pad_square(field_W, field_paths.size());
+        transpose_blocks(field_W, field_Wt, field_paths.size(), Cp, Cp);
+        if (residual) pad_rows(res_pre, static_cast<std::size_t>(num_elements) * num_LM);
+    }
     {
         // A1 per l: rows (e, k_in), columns k_out
         std::vector<std::int64_t> off(l_max + 2, 0);
@@ -434,6 +443,137 @@ void HostModel::pad_channels(int Cp) {
     C = Cp;
 }
 
+// Flattened numbers of a (possibly nested) numeric array.
+static std::vector<double> flat_doubles(const Value& v) {
+    if (v.is_array() && !v.numeric_array && v.size() > 0 && v.at(0).is_array()) {
+        std::vector<double> out;
+        for (std::size_t i = 0; i < v.size(); ++i) {
+            const auto r = flat_doubles(v.at(i));
+            out.insert(out.end(), r.begin(), r.end());
+        }
+        return out;
+    }
+    return v.as_doubles();
+}
+
+// field_coupling.hpp:60-238 (the schema checks and path compilation) and
+// mace.cpp:2832-2860: one coupling; each field_feats instruction (l_in x 1o
+// -> an adjacent l) pairs with the field_linear instruction of that l; the
+// path's channel matrix is path_weight_f * path_weight_l * Wf Wl (FP64 sums,
+// rounded once) and its angular entries are the 3j tensor's nonzeros.
+void HostModel::load_field_coupling(const Value& j) {
+    if (L_max < 1 || L_max > 2)
+        throw std::invalid_argument("MACEField field coupling currently supports only 1 <= L_max <= 2.");
+    const Value& list = j.at("field_couplings");
+    if (list.size() != 1) throw std::invalid_argument("MACEField JSON must contain exactly one field coupling.");
+    const Value& cp = list.at(0);
+    const bool legacy = !cp.contains("schema_version");
+    if (!legacy && cp.at("schema_version").as_int() != 1)
+        throw std::invalid_argument("Unsupported MACEField field-coupling schema version.");
+    if (legacy && L_max != 1)
+        throw std::invalid_argument("Unversioned MACEField field coupling is supported only for legacy L_max == 1 data.");
+    std::string hidden;
+    for (int l = 0; l <= L_max; ++l)
+        hidden += (l ? "+" : "") + std::to_string(C) + "x" + std::to_string(l) + (l % 2 ? "o" : "e");
+    if (cp.at("field_feats_irreps_in1").as_string() != hidden || cp.at("field_feats_irreps_in2").as_string() != "1x1o" ||
+        cp.at("field_feats_irreps_out").as_string() != hidden || cp.at("field_linear_irreps_in").as_string() != hidden ||
+        cp.at("field_linear_irreps_out").as_string() != hidden)
+        throw std::invalid_argument("MACEField field coupling must use the canonical equal-channel hidden irreps.");
+    const std::size_t Cs = static_cast<std::size_t>(C), cc = Cs * Cs;
+    for (const char* key : {"field_feats_output_mask", "field_linear_output_mask"}) {
+        const auto m = cp.at(key).as_doubles();
+        if (m.size() != static_cast<std::size_t>(num_LM) * Cs)
+            throw std::invalid_argument(std::string("MACEField ") + key + " has an invalid size.");
+        for (double v : m)
+            if (v != 1.0) throw std::invalid_argument(std::string("MACEField ") + key + " must contain only ones.");
+    }
+    if (cp.at("field_linear_bias").size() != 0) throw std::invalid_argument("MACEField field_linear bias must be empty.");
+    const auto wf = flat_doubles(cp.at("field_feats_weight"));
+    const auto wl = flat_doubles(cp.at("field_linear_weight"));
+    const Value& fis = cp.at("field_feats_instructions");
+    const Value& lis = cp.at("field_linear_instructions");
+    const Value* uw = j.find("H1_linear_up_weights");
+    const Value* pw = j.find("H1_product_weights");
+    if (!uw || !pw) throw std::invalid_argument("MACEField JSON must contain split H1 product and linear_up weights.");
+    const auto U = uw->as_doubles();
+    const auto P = pw->as_doubles();
+    if (U.size() != static_cast<std::size_t>(L_max + 1) * cc || P.size() != U.size())
+        throw std::invalid_argument("MACEField split H1 linear_up weights have an invalid size.");
+    for (std::size_t fi = 0; fi < fis.size(); ++fi) {
+        const Value& ins = fis.at(fi);
+        if (ins.at("connection_mode").as_string() != "uvw" || ins.at("path_shape").as_ints() != std::vector<int>{C, 1, C})
+            throw std::invalid_argument("MACEField field_feats instructions must use uvw paths shaped (channels, 1, channels).");
+    }
+    if (fis.size() * cc != wf.size())
+        throw std::invalid_argument("MACEField field_feats weight size does not match its instructions.");
+    for (std::size_t li = 0; li < lis.size(); ++li) {
+        const Value& ins = lis.at(li);
+        if (ins.at("path_shape").as_ints() != std::vector<int>{C, C})
+            throw std::invalid_argument("MACEField field_linear instructions must be shaped (channels, channels).");
+        const int a = ins.at("i_in").as_int(), b = ins.at("i_out").as_int();
+        if (a < 0 || a > L_max || b != a)
+            throw std::invalid_argument("MACEField field_linear instructions must preserve each canonical angular block.");
+    }
+    if (lis.size() * cc != wl.size())
+        throw std::invalid_argument("MACEField field_linear weight size does not match its instructions.");
+    P_all = to_f32(P);
+    U_all = to_f32(U);
+    transpose_blocks(P_all, P_allt, L_max + 1, C, C);
+    transpose_blocks(U_all, U_allt, L_max + 1, C, C);
+    field_paths.clear();
+    field_entries.clear();
+    field_W.clear();
+    for (std::size_t fi = 0; fi < fis.size(); ++fi) {
+        const Value& ins = fis.at(fi);
+        const int lin = ins.at("i_in1").as_int(), blk = ins.at("i_in2").as_int(), lmid = ins.at("i_out").as_int();
+        if (blk != 0 || lin < 0 || lin > L_max || lmid < 0 || lmid > L_max || std::abs(lin - lmid) != 1)
+            throw std::invalid_argument("MACEField field_feats instruction is not an adjacent-rank 1o coupling.");
+        const int din = 2 * lin + 1, dmid = 2 * lmid + 1;
+        std::vector<double> w3(static_cast<std::size_t>(din) * 3 * dmid, 0.0);
+        if (legacy) {
+            for (int c = 0; c < 3; ++c) w3[lin == 0 ? c * 3 + c : c * 4] = 1.0 / std::sqrt(3.0);
+        } else {
+            if (ins.at("wigner_3j_shape").as_ints() != std::vector<int>{din, 3, dmid})
+                throw std::invalid_argument("MACEField Wigner tensor shape does not match its angular path.");
+            w3 = ins.at("wigner_3j").as_doubles();
+            if (w3.size() != static_cast<std::size_t>(din) * 3 * dmid)
+                throw std::invalid_argument("MACEField Wigner tensor data has an invalid size.");
+        }
+        bool found = false;
+        for (std::size_t li = 0; li < lis.size(); ++li) {
+            const Value& lins = lis.at(li);
+            if (lins.at("i_in").as_int() != lmid) continue;
+            found = true;
+            const int lout = lins.at("i_out").as_int(), dout = 2 * lout + 1;
+            const int path = static_cast<int>(field_paths.size());
+            field_paths.push_back({lin, lout});
+            for (int mi = 0; mi < din; ++mi)
+                for (int c = 0; c < 3; ++c)
+                    for (int mo = 0; mo < dout; ++mo) {
+                        const double w = w3[(static_cast<std::size_t>(mi) * 3 + c) * dout + mo];
+                        if (std::abs(w) > 1e-14)
+                            field_entries.push_back({lin * lin + mi, c, lout * lout + mo, path, to_f32(w)});
+                    }
+            const double scale = ins.at("path_weight").as_number() * lins.at("path_weight").as_number();
+            for (int in = 0; in < C; ++in)
+                for (int out = 0; out < C; ++out) {
+                    double v = 0.0;
+                    for (int mid = 0; mid < C; ++mid)
+                        v += wf[fi * cc + static_cast<std::size_t>(in) * Cs + mid] *
+                             wl[li * cc + static_cast<std::size_t>(mid) * Cs + out];
+                    field_W.push_back(to_f32(scale * v));
+                }
+        }
+        if (!found) throw std::invalid_argument("MACEField field_feats output has no compatible field_linear instruction.");
+    }
+    if (field_paths.empty()) throw std::invalid_argument("MACEField field coupling contains no executable paths.");
+    transpose_blocks(field_W, field_Wt, field_paths.size(), C, C);
+    if (residual) {
+        const auto b = j.at("H1_first_residual_weights").as_doubles();
+        res_pre = to_f32(b);
+    }
+}
+
 void HostModel::load(const std::string& path, const std::string& head) {
     Value j = json_lite::parse_model_file(path);
     if (j.get_int("symmetrix_format_version", 1) != 4)
@@ -461,10 +601,17 @@ void HostModel::load(const std::string& path, const std::string& head) {
                                     "such models use h1_affine_mode 'pre_linear_up'.");
     if (pre_linear_up && single_layer)
         throw std::invalid_argument("The pre_linear_up basis applies to two-interaction models only.");
+    field = j.get_bool("has_field_coupling", false);
+    {
+        const std::string mt = j.get_string("model_type", "MACE");
+        if (mt != "MACE" && mt != "MACEField")
+            throw std::invalid_argument("Format version 4 is the standard MACE / MACEField format.");
+    }
+    if (field && !pre_linear_up)
+        throw std::invalid_argument("The m0_composite basis cannot represent field-coupled features; such models "
+                                    "use h1_affine_mode 'pre_linear_up'.");
     if (j.get_string("radial_representation", "") != "compact")
         throw std::invalid_argument("only the compact radial representation is supported");
-    if (j.get_bool("has_field_coupling", false))
-        throw std::invalid_argument("the model uses features outside the supported MACE path (field coupling)");
     // mace_kokkos_model.cpp:200 (required key), :1109 (optional key)
     A0_scaled = j.at("A0_scaled").as_bool();
     A1_scaled = j.get_bool("A1_scaled", false);
@@ -684,6 +831,7 @@ void HostModel::load(const std::string& path, const std::string& head) {
     } else if (j.contains("H1_first_residual_weights")) {
         throw std::invalid_argument("Non-residual MACE JSON must not contain H1 residual weights.");
     }
+    if (field) load_field_coupling(j);
 
     // ---- R1 coupling (extract_mace_data.py:1326-1400 semantics); a
     // one-interaction model has none (its Phi1 lists are empty or absent,

@@ -14,6 +14,10 @@
 #include <string>
 #include <vector>
 
+namespace json_lite {
+struct Value;
+}
+
 namespace smx {
 
 // One packed monomial: variables v0,v1,v2 (byte each) and degree (top byte).
@@ -110,6 +114,24 @@ struct HostModel {
     // M1 is an invariant of H1's num_LM components, and there is no R1,
     // Phi1 or A1 (num_paths 0)
     bool single_layer = false;
+    // MACEField (field_coupling.hpp:60-238; mace.cpp:322-395, 1147-1240):
+    // H1p = M0 P (+ residual b), H1f[lm_out] = H1p[lm_out] + sum over the
+    // angular entries of (coef E_c) H1p[lm_in] W_path, x = H1f[:,0,:],
+    // H1 = H1f U.  Paths are (field_feats, field_linear) instruction pairs.
+    bool field = false;
+    struct FieldPath {
+        int l_in, l_out;
+    };
+    struct FieldEntry {
+        int lm_in, comp, lm_out, path;
+        float coef;
+    };
+    std::vector<FieldPath> field_paths;
+    std::vector<FieldEntry> field_entries;
+    std::vector<float> field_W, field_Wt;   // [path][C][C] [in][out] and [out][in]
+    std::vector<float> P_all, P_allt;        // [l][C][C] H1_product_weights and transposes
+    std::vector<float> U_all, U_allt;        // [l][C][C] H1_linear_up_weights and transposes
+    std::vector<float> res_pre;              // [type][NH][C] the residual before linear_up
 
     // R1 coupling
     std::vector<int> path_lo, path_le, path_ls;  // Phi1_l, Phi1_l1, Phi1_l2
@@ -139,6 +161,7 @@ struct HostModel {
     double readout_scale = 1.0;
 
     void load(const std::string& path, const std::string& head);
+    void load_field_coupling(const ::json_lite::Value& j);
 };
 
 // Rewrites a model file (JSON v4 text or its SMXB binary form) as `format`

@@ -22,6 +22,7 @@
 #include "neighbor.h"
 #include "utils.h"
 
+#include <cstdlib>
 #include <cstring>
 
 using namespace LAMMPS_NS;
@@ -91,10 +92,10 @@ void PairSymmetrixMACEMI355X<DeviceType>::allocate()
 // The reference's keywords (pair_symmetrix_mace_kokkos.cpp:180-370) where
 // this build has them: the mode token (only no_domain_decomposition),
 // profile capacity|speed and its low_memory yes|no alias, allow_fixed_workspace
-// yes|no, head NAME, streamed_edges auto|direct, _debug_execution_plan ID.
-// The JIT artefact keywords name files this build does not load (warned and
-// skipped); electric_field (MACEField) and the message-passing modes are
-// refused.
+// yes|no, head NAME, streamed_edges auto|direct, _debug_execution_plan ID,
+// electric_field Ex Ey Ez (MACEField, :207-224).  The JIT artefact keywords
+// name files this build does not load (warned and skipped); the
+// message-passing modes are refused.
 template <class DeviceType>
 void PairSymmetrixMACEMI355X<DeviceType>::settings(int narg, char **arg)
 {
@@ -104,6 +105,7 @@ void PairSymmetrixMACEMI355X<DeviceType>::settings(int narg, char **arg)
   allow_fixed_workspace = false;
   head.clear();
   debug_plan.clear();
+  electric_field_set = false;
   bool profile_set = false, alias_set = false;
   std::string alias_profile;
   auto value_of = [&](int &i, const char *what) -> std::string {
@@ -143,7 +145,15 @@ void PairSymmetrixMACEMI355X<DeviceType>::settings(int narg, char **arg)
       const std::string v = value_of(i, key.c_str());
       if (comm->me == 0) error->warning(FLERR, "pair_style symmetrix/mace/mi355x/kk ignores {} {}", key, v);
     } else if (key == "electric_field") {
-      error->all(FLERR, "pair_style symmetrix/mace/mi355x/kk does not run field-coupled (MACEField) models");
+      if (i + 3 >= narg) error->all(FLERR, "pair_style symmetrix/mace/mi355x/kk electric_field requires three components");
+      for (int c = 0; c < 3; ++c) {
+        char *end = nullptr;
+        electric_field[c] = std::strtod(arg[i + 1 + c], &end);
+        if (end == arg[i + 1 + c] || *end != '\0')
+          error->all(FLERR, "pair_style symmetrix/mace/mi355x/kk electric_field components must be numeric");
+      }
+      i += 3;
+      electric_field_set = true;
     } else {
       error->all(FLERR, "The command 'pair_style symmetrix/mace/mi355x/kk {}' is invalid", key);
     }
@@ -168,6 +178,13 @@ void PairSymmetrixMACEMI355X<DeviceType>::coeff(int narg, char **arg)
   check(smx_set_allow_fixed_workspace(evaluator, allow_fixed_workspace ? 1 : 0), "plan request");
   check(smx_set_execution_plan_request(evaluator, "direct", execution_profile.c_str(), debug_plan.c_str()),
         "plan request");
+  // a MACEField model runs in the electric_field of the pair style
+  // (pair_symmetrix_mace_kokkos.cpp:598-599); a plain model takes none
+  int32_t field_model = 0;
+  check(smx_has_field_coupling(evaluator, &field_model), "model info");
+  if (field_model && !electric_field_set)
+    error->all(FLERR, "MACEField models require pair_style symmetrix/mace/mi355x/kk electric_field Ex Ey Ez");
+  if (electric_field_set) check(smx_set_electric_field(evaluator, electric_field, 3), "electric_field");
   SmxModelInfo info{};
   info.struct_size = sizeof(info);
   check(smx_evaluator_info(evaluator, &info), "model info");

@@ -15,6 +15,7 @@
      pair_style symmetrix/mace/mi355x/kk [no_domain_decomposition] [head NAME]
                 [profile capacity|speed] [low_memory yes|no]
                 [allow_fixed_workspace yes|no] [streamed_edges auto|direct]
+                [electric_field Ex Ey Ez]   (required by MACEField models)
      pair_coeff * * model.json O Ti Sr      (one element symbol per LAMMPS type)
    Requires newton pair on and an atom map.
 
@@ -63,6 +64,8 @@ class PairSymmetrixMACEMI355X : public Pair, public KokkosBase {
   std::string debug_plan;
   std::string execution_profile = "capacity";
   bool allow_fixed_workspace = false;
+  double electric_field[3] = {0.0, 0.0, 0.0};  // electric_field Ex Ey Ez (MACEField models)
+  bool electric_field_set = false;
   double r_cut = 0.0;
 
   Kokkos::View<int *, DeviceType> d_type_to_model;  // [ntypes] model type of LAMMPS type t+1

@@ -149,7 +149,7 @@ class Symmetrix(_Base):
 
     def __init__(self, model_file, dtype="float32", use_kokkos=True, streamed_edges="direct",
                  execution_profile="capacity", allow_fixed_workspace=False, neighbor_skin=0.5, head=None,
-                 _debug_execution_plan=None, **kwargs):
+                 _debug_execution_plan=None, electric_field=None, **kwargs):
         super().__init__(**kwargs)
         if dtype not in ("float32", np.float32):
             raise ValueError("the MI355X evaluator implements dtype='float32'")
@@ -191,6 +191,40 @@ class Symmetrix(_Base):
         self.neighbor_cache_cell_update_count = 0
         self.neighbor_graph_backend = None
         self.results = {}
+        # MACEField models (calculator.py:971-976, 1247-1249): the graph's
+        # electric field, and the polarization -dE/dE / V among the results
+        self._electric_field = electric_field
+        if getattr(self.evaluator, "has_field_coupling", False):
+            self.implemented_properties = list(self.implemented_properties) + ["polarization"]
+
+    @property
+    def electric_field(self):
+        return self._electric_field
+
+    @electric_field.setter
+    def electric_field(self, value):
+        self._electric_field = value
+
+    def _resolve_electric_field(self, atoms):
+        """calculator.py:2782-2805: the calculator's field, else the atoms'
+        info["electric_field"] / info["REF_electric_field"], else zero; one
+        field for the graph, shape (3,) or (1, 3)."""
+        info = atoms.get("info", {}) if isinstance(atoms, dict) else getattr(atoms, "info", {})
+        if self._electric_field is not None:
+            field = self._electric_field
+        elif "electric_field" in info:
+            field = info["electric_field"]
+        elif "REF_electric_field" in info:
+            field = info["REF_electric_field"]
+        else:
+            field = np.zeros(3)
+        field = np.asarray(field, dtype=float)
+        if field.shape in ((3,), (1, 3)):
+            return field.reshape(3)
+        if field.ndim == 2 and field.shape[1] == 3:
+            raise ValueError("MACEField ASE electric_field must be a graph-level electric_field with shape (3,) or "
+                             "(1, 3); per-atom fields are not supported.")
+        raise ValueError("electric_field must have shape (3,) or (1, 3).")
 
     @property
     def neighbor_graph_rebuilds(self):
@@ -305,9 +339,13 @@ class Symmetrix(_Base):
         else:
             atoms = self.atoms
         numbers, positions, cell, pbc = _system_arrays(atoms)
+        field = self._resolve_electric_field(atoms) if getattr(self.evaluator, "has_field_coupling", False) else None
         cache = self._graph(numbers, positions, cell, pbc)
         ev = self.evaluator
-        ev._compute_prepared_factorized_positions(cache.generation, positions.reshape(-1))
+        if field is None:
+            ev._compute_prepared_factorized_positions(cache.generation, positions.reshape(-1))
+        else:
+            ev._compute_prepared_factorized_positions_field(cache.generation, positions.reshape(-1), field)
         node_energies = np.array(ev.node_energies, dtype=np.float64, copy=True)
         energy = float(np.sum(node_energies, dtype=np.float64))
         self.results = {"energy": energy, "free_energy": energy, "energies": node_energies}
@@ -318,6 +356,12 @@ class Symmetrix(_Base):
                 raise ValueError("stress needs a cell of non-zero volume")
             sigma = ev._reduce_stress(volume, None, cache.generation)
             self.results["stress"] = full_3x3_to_voigt_6_stress(sigma)
+        if field is not None:
+            # calculator.py:3672-3678: P = -dE/dE / V
+            volume = abs(float(np.linalg.det(cell)))
+            if not volume > 0.0:
+                raise ValueError("polarization needs a cell of non-zero volume")
+            self.results["polarization"] = -np.asarray(ev.electric_field_adj, dtype=float) / volume
         return self.results
 
     def get_property(self, name, atoms=None, allow_calculation=True):

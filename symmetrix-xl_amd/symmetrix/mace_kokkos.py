@@ -249,6 +249,45 @@ class MACEKokkosFloat:
         check(lib.smx_compute_prepared_factorized_positions(self._h, int(execution_graph_generation),
                                                             ptr(positions)))
 
+    # -------------------------------------------------------- MACEField
+    @property
+    def has_field_coupling(self):
+        out = ctypes.c_int32()
+        check(lib.smx_has_field_coupling(self._h, ctypes.byref(out)))
+        return bool(out.value)
+
+    def _field(self, electric_field):
+        field = f64(electric_field)
+        if field.size not in (3, 3 * self._num_nodes):
+            raise ValueError("MACEField electric_field must have shape (3,) or (num_nodes, 3).")
+        return field
+
+    def _compute_prepared_factorized_positions_field(self, execution_graph_generation, positions, electric_field):
+        positions, field = f64(positions), self._field(electric_field)
+        if positions.size != 3 * self._num_nodes:
+            raise ValueError("positions do not match the prepared graph")
+        check(lib.smx_compute_prepared_factorized_positions_field(
+            self._h, int(execution_graph_generation), ptr(positions), ptr(field), field.size))
+
+    def _compute_prepared_factorized_field(self, execution_graph_generation, xyz, r, electric_field):
+        xyz, r, field = f64(xyz), f64(r), self._field(electric_field)
+        if xyz.size != 3 * self._num_edges or r.size != self._num_edges:
+            raise ValueError("xyz and r do not match the prepared graph")
+        check(lib.smx_compute_prepared_factorized_field(self._h, int(execution_graph_generation), ptr(xyz), ptr(r),
+                                                        ptr(field), field.size))
+
+    def _set_electric_field(self, electric_field=None):
+        field = np.zeros(0) if electric_field is None else f64(electric_field)
+        check(lib.smx_set_electric_field(self._h, ptr(field), field.size))
+
+    @property
+    def electric_field_adj(self):
+        n = ctypes.c_int64()
+        check(lib.smx_electric_field_adj(self._h, None, 0, ctypes.byref(n)))
+        out = np.zeros(n.value)
+        check(lib.smx_electric_field_adj(self._h, ptr(out), out.size, None))
+        return out
+
     def _compute_prepared_factorized_positions_device(self, execution_graph_generation, positions_device_ptr):
         check(lib.smx_compute_prepared_factorized_positions_device(self._h, int(execution_graph_generation),
                                                                    ctypes.c_void_p(positions_device_ptr)))

@@ -177,6 +177,40 @@ def test_lammps_entry_matches_oracle(request, model, tile):
         hip.free()
 
 
+def test_lammps_entry_in_an_electric_field(tiny_field_model_path):
+    # pair_style symmetrix/mace/kk electric_field Ex Ey Ez
+    # (pair_symmetrix_mace_kokkos.cpp:207-224, 598-599): the field set once
+    # applies to every compute; without it a MACEField model is refused
+    from oracle import oracle
+    from symmetrix import systems
+    from symmetrix.mace_kokkos import MACEKokkosFloat
+    s = systems.srtio3_supercell(3, sigma=0.05, seed=0)
+    field = np.array([0.1, -0.05, 0.2])
+    om = oracle.OracleModel(tiny_field_model_path)
+    ref = oracle.evaluate_system(om, s, skin=0.5, field=field)
+    ev = MACEKokkosFloat(tiny_field_model_path)
+    model_of_z = {int(z): k for k, z in enumerate(ev.atomic_numbers)}
+    type_to_model = [model_of_z[8], model_of_z[22], model_of_z[38]]
+    cell = np.asarray(s["cell"], float)
+    n = len(s["numbers"])
+    allpos, owner, alltypes, rows = _lammps_arrays(s["positions"], cell, s["numbers"], ev.r_cut + 0.5,
+                                                   {8: 1, 22: 2, 38: 3})
+    ilist = np.arange(n, dtype=np.int32)
+    hip = _Hip()
+    try:
+        with pytest.raises(ValueError, match="electric field"):
+            _run(ev, hip, allpos, owner, alltypes, rows, ilist, type_to_model, True)
+        ev._set_electric_field(field)
+        energy, virial, f, eatom = _run(ev, hip, allpos, owner, alltypes, rows, ilist, type_to_model, True)
+        folded = np.zeros((n, 3))
+        np.add.at(folded, owner, f)
+        assert abs(energy - ref["energy"]) / n < E_TOL
+        assert np.max(np.abs(folded - ref["forces"])) < F_TOL
+        np.testing.assert_allclose(eatom[:n], ref["energies"], rtol=0, atol=1e-4)
+    finally:
+        hip.free()
+
+
 def test_lammps_entry_rejects_unmapped_types(tiny_model_path):
     from symmetrix import systems
     from symmetrix.mace_kokkos import MACEKokkosFloat

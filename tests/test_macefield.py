@@ -43,7 +43,7 @@ def _small():
 FIELD = np.array([0.12, -0.21, 0.27])
 
 
-@pytest.mark.parametrize("model", ["tiny_field", "tiny_field_l2"])
+@pytest.mark.parametrize("model", ["tiny_field", "field_l2"])
 def test_zero_field_equals_the_field_free_twin(request, tmp_path, model):
     doc = _doc(request.getfixturevalue(model + "_model_path"))
     C, L = doc["num_channels"], doc["L_max"]
@@ -67,7 +67,7 @@ def test_zero_field_equals_the_field_free_twin(request, tmp_path, model):
     assert abs(f["energy"] - a["energy"]) > 1e-6 * scale
 
 
-@pytest.mark.parametrize("model", ["tiny_field", "tiny_field_l2"])
+@pytest.mark.parametrize("model", ["tiny_field", "field_l2"])
 def test_field_adjoint_is_the_field_derivative(request, model):
     om = oracle.OracleModel(request.getfixturevalue(model + "_model_path"), fp64=True)
     s = _small()
@@ -98,7 +98,7 @@ def test_field_adjoint_is_the_field_derivative(request, model):
     assert same["energy"] == pytest.approx(r["energy"], abs=1e-10)
 
 
-@pytest.mark.parametrize("model", ["tiny_field", "tiny_field_l2"])
+@pytest.mark.parametrize("model", ["tiny_field", "field_l2"])
 def test_rotating_atoms_and_field_together_is_invariant(request, tmp_path, model):
     path = request.getfixturevalue(model + "_model_path")
     doc = _doc(path)
@@ -131,8 +131,8 @@ def test_rotating_atoms_and_field_together_is_invariant(request, tmp_path, model
     assert abs(ea - eb) > 1e-6 * abs(ea)
 
 
-def test_forces_and_stress_are_energy_derivatives_in_a_field(tiny_field_l2_model_path):
-    m = oracle.OracleModel(tiny_field_l2_model_path, fp64=True)
+def test_forces_and_stress_are_energy_derivatives_in_a_field(field_l2_model_path):
+    m = oracle.OracleModel(field_l2_model_path, fp64=True)
     s = _small()
     base = oracle.evaluate_system(m, s, skin=0.5, field=FIELD)
     h = 1e-4
