@@ -680,7 +680,22 @@ struct Evaluator {
             max_tile_nr = std::max(max_tile_nr, t.nr);
             max_tile_ne = std::max(max_tile_ne, t.ne);
         }
-        // node lists (local rows sorted by type), readout batches and node-linear tiles
+        // node lists (local rows sorted by type), readout batches and
+        // node-linear tiles depend only on the tiles' receiver ranges and the
+        // node types: a graph rebuilt over the same atoms (a LAMMPS neighbour
+        // list rebuild) keeps them
+        std::vector<int> key{N, tiled ? 1 : 0, tiled ? tile_limit : 0};
+        key.insert(key.end(), h_node_types.begin(), h_node_types.end());
+        if (key != plan_key) {
+            plan_key.swap(key);
+            build_node_plans();
+        }
+        assign_tile_plans();
+    }
+
+    std::vector<int> plan_key;  // (N, tiling, node types) of the node plans on the device
+
+    void build_node_plans() {
         h_node_list.clear();
         node_list_begin.clear();
         h_batches.clear();
@@ -751,6 +766,11 @@ struct Evaluator {
         }
         upload(d_node_list, h_node_list, stream);
         upload(d_batches, h_batches, stream);
+    }
+
+    // the tiles' views of the node plans, and the touched sources of each
+    // tile (these depend on the edges)
+    void assign_tile_plans() {
         auto view = [&](const PlanSet& P, std::size_t ti, const DevBuf& groups, int max_n, int n_sub) {
             GemmPlan g;
             g.n_sub = n_sub;
@@ -999,6 +1019,30 @@ struct Evaluator {
             SMX_HIP(hipMemcpy(nt.data(), neigh_types, sizeof(int) * num_edges, hipMemcpyDeviceToHost));
         }
         return prepare_graph_host(n, t.data(), nn.data(), num_edges, nb.data(), nt.data());
+    }
+
+    // A receiver CSR that this library's own kernels built and checked on the
+    // device (the LAMMPS topology): offsets come from the host, the edge
+    // arrays are copied device to device, only the node types come back.
+    std::uint64_t prepare_graph_checked(int n, const int* node_types, const std::vector<int>& offsets,
+                                        std::int64_t num_edges, const int* neigh, const int* neigh_types) {
+        N = n;
+        E = num_edges;
+        h_node_types.resize(n);
+        if (n > 0) SMX_HIP(hipMemcpy(h_node_types.data(), node_types, sizeof(int) * n, hipMemcpyDeviceToHost));
+        validate_types(n, h_node_types.data());
+        h_offsets = offsets;
+        upload(d_offsets, offsets, stream);
+        int* nt = static_cast<int*>(d_node_types.ensure(std::max(n, 1) * sizeof(int)));
+        int* nb = static_cast<int*>(d_neigh.ensure(std::max<std::int64_t>(E, 1) * sizeof(int)));
+        int* nbt = static_cast<int*>(d_neigh_types.ensure(std::max<std::int64_t>(E, 1) * sizeof(int)));
+        if (n > 0) SMX_HIP(hipMemcpyAsync(nt, node_types, sizeof(int) * n, hipMemcpyDeviceToDevice, stream));
+        if (E > 0) {
+            SMX_HIP(hipMemcpyAsync(nb, neigh, sizeof(int) * E, hipMemcpyDeviceToDevice, stream));
+            SMX_HIP(hipMemcpyAsync(nbt, neigh_types, sizeof(int) * E, hipMemcpyDeviceToDevice, stream));
+        }
+        geom = Geometry::none;
+        return finish_graph();
     }
 
     std::pair<std::uint64_t, std::int64_t> prepare_periodic(int n, const int* node_types, const double* positions,
@@ -1451,7 +1495,7 @@ struct Evaluator {
     // ---------------------------------------------------------- LAMMPS entry
     // pair_symmetrix_mace_kokkos.cpp:1010-1282: topology on a rebuild,
     // edge vectors every call, reductions into LAMMPS's per-atom arrays
-    DevBuf l_node_types, l_num_neigh, l_node_of_atom, l_neigh, l_neigh_types, l_lmp_j, l_joff, l_jedges, l_counts,
+    DevBuf l_node_types, l_num_neigh, l_node_of_atom, l_neigh, l_neigh_types, l_lmp_j, l_joff, l_jedges, l_counts, l_offsets,
         l_flag, l_touched;
     std::vector<std::size_t> l_touched_begin;  // tiled plan: LAMMPS atoms each tile's edges leave
     const SmxLammpsArgsV1* lmp = nullptr;      // set while a LAMMPS call evaluates
@@ -1485,18 +1529,18 @@ struct Evaluator {
             if (total > kMaxEdges) throw std::invalid_argument("edge count exceeds the 32-bit graph limit");
             off[ii + 1] = static_cast<int>(total);
         }
-        DevBuf d_off;
-        upload(d_off, off, stream);
+        int* d_off = upload(l_offsets, off, stream);
         const std::size_t e = static_cast<std::size_t>(std::max<std::int64_t>(total, 1));
         int* nb = static_cast<int*>(l_neigh.ensure(e * sizeof(int)));
         int* nbt = static_cast<int*>(l_neigh_types.ensure(e * sizeof(int)));
         int* lj = static_cast<int*>(l_lmp_j.ensure(e * sizeof(int)));
         launch_fill_zero(reinterpret_cast<float*>(flag), 1, stream);
-        lammps_edges(inum, nall, L, d_off.as<int>(), noa, nb, nbt, lj, flag, stream);
+        lammps_edges(inum, nall, L, d_off, noa, nb, nbt, lj, flag, stream);
         if (read_flag(l_flag) != 0)
             throw std::invalid_argument("LAMMPS neighbour outside [0, nall), with an owner that is not a local "
                                         "ilist atom, or with an unmapped type");
-        prepare_graph_device(inum, nt, nn, total, nb, nbt);
+        // the kernels above checked every index and type of the CSR
+        prepare_graph_checked(inum, nt, off, total, nb, nbt);
         int* joff = static_cast<int*>(l_joff.ensure((static_cast<std::size_t>(nall) + 1) * sizeof(int)));
         int* jed = static_cast<int*>(l_jedges.ensure(e * sizeof(int)));
         int* cnt = static_cast<int*>(l_counts.ensure(std::max(nall, 1) * sizeof(int)));

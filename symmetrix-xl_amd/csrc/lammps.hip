@@ -44,14 +44,22 @@ __global__ void k_lmp_nodes(int inum, int nall, LammpsList L, int* __restrict__ 
     num_neigh[ii] = n;
 }
 
-__global__ void k_lmp_edges(int inum, int nall, LammpsList L, const int* __restrict__ offsets,
-                            const int* __restrict__ node_of_atom, int* __restrict__ neigh,
-                            int* __restrict__ neigh_types, int* __restrict__ lmp_j, int* __restrict__ bad) {
-    const int ii = blockIdx.x * blockDim.x + threadIdx.x;
+// Each workgroup takes 64 consecutive ilist entries (one per lane, so the
+// lanes of a wave read one neighbour slot of 64 atoms: coalesced for the
+// column-major Kokkos list) and kEdgePhases waves, wave w taking the slots
+// jj = w, w + kEdgePhases, ...
+constexpr int kEdgePhases = 16;
+__global__ __launch_bounds__(64 * kEdgePhases) void k_lmp_edges(int inum, int nall, LammpsList L,
+                                                                const int* __restrict__ offsets,
+                                                                const int* __restrict__ node_of_atom,
+                                                                int* __restrict__ neigh, int* __restrict__ neigh_types,
+                                                                int* __restrict__ lmp_j, int* __restrict__ bad) {
+    const int ii = blockIdx.x * 64 + static_cast<int>(threadIdx.x % 64);
+    const int phase = static_cast<int>(threadIdx.x / 64);
     if (ii >= inum) return;
     const int i = L.ilist[ii];
     const int e0 = offsets[ii], n = offsets[ii + 1] - e0;
-    for (int jj = 0; jj < n; ++jj) {
+    for (int jj = phase; jj < n; jj += kEdgePhases) {
         const int j = L.neighbors[static_cast<long long>(i) * L.stride_atom + static_cast<long long>(jj) * L.stride_neighbor] &
                       kNeighMask;
         int node = -1, t = -1;
@@ -155,8 +163,8 @@ void lammps_nodes(int inum, int nall, const LammpsList& L, int* node_types, int*
 void lammps_edges(int inum, int nall, const LammpsList& L, const int* offsets, const int* node_of_atom, int* neigh,
                   int* neigh_types, int* lmp_j, int* bad, hipStream_t s) {
     if (inum == 0) return;
-    k_lmp_edges<<<blocks_for(inum, 256), 256, 0, s>>>(inum, nall, L, offsets, node_of_atom, neigh, neigh_types, lmp_j,
-                                                      bad);
+    k_lmp_edges<<<blocks_for(inum, 64), 64 * kEdgePhases, 0, s>>>(inum, nall, L, offsets, node_of_atom, neigh,
+                                                                   neigh_types, lmp_j, bad);
     SMX_LAUNCH_CHECK("lammps_edges");
 }
 
