@@ -227,6 +227,75 @@ SMX_API int32_t smx_compute_prepared_factorized_positions(SmxEvaluator* ev, uint
  * are ready for work ordered on that stream or after smx_synchronize. */
 SMX_API int32_t smx_compute_prepared_factorized_positions_device(SmxEvaluator* ev, uint64_t generation,
                                                                  const double* positions_device);
+/* Graphs with ghost feature nodes: one GPU's share of a domain-decomposed
+ * system (the LAMMPS multi-rank path, pair_symmetrix_mace_kokkos.cpp:
+ * 1285-1704).  prepare_factorized_graph with feature nodes
+ * (mace_kokkos.hpp:378-386, 399-413; mace_kokkos_factorized_lifecycle.cpp:
+ * 949-1104, 2346-2380): num_receivers receivers, each the feature node
+ * receiver_feature_indices[ii] (unique, same type), num_feature_nodes >=
+ * num_receivers feature nodes of types feature_types, and edges that leave
+ * any feature node (neigh_indices are feature indices; each neighbour type
+ * must equal its feature node's).  Such a graph takes explicit edge vectors
+ * (no prepared positions geometry), runs the retained direct plan, and is
+ * evaluated by the split-phase calls below (a one-interaction model also by
+ * the plain xyz call).  The node forces reduced by
+ * smx_reduce_prepared_node_forces are the feature nodes' (3 *
+ * num_feature_nodes doubles, caller order; ghosts' forces are the caller's
+ * to return to their owners).  Field-coupled models are refused. */
+SMX_API int32_t smx_prepare_factorized_feature_graph(SmxEvaluator* ev, int32_t num_receivers,
+                                                     int32_t num_feature_nodes,
+                                                     const int32_t* receiver_feature_indices,
+                                                     const int32_t* node_types, const int32_t* feature_types,
+                                                     const int32_t* num_neigh, int64_t num_edges,
+                                                     const int32_t* neigh_indices, const int32_t* neigh_types,
+                                                     uint64_t* generation);
+/* same arrays in device memory (checked on host copies) */
+SMX_API int32_t smx_prepare_factorized_feature_graph_device(SmxEvaluator* ev, int32_t num_receivers,
+                                                            int32_t num_feature_nodes,
+                                                            const int32_t* receiver_feature_indices,
+                                                            const int32_t* node_types, const int32_t* feature_types,
+                                                            const int32_t* num_neigh, int64_t num_edges,
+                                                            const int32_t* neigh_indices,
+                                                            const int32_t* neigh_types, uint64_t* generation);
+/* compute_factorized_single_layer_distributed_evaluation (mace_kokkos.hpp:
+ * 683-688; mace_kokkos_evaluate.cpp:1495-1552): a one-interaction model over
+ * a feature graph in one call (no features are exchanged); xyz[E][3] and
+ * r[E] on the host or (on_device != 0) in device memory. */
+SMX_API int32_t smx_compute_factorized_single_layer_distributed_evaluation(SmxEvaluator* ev, uint64_t generation,
+                                                                           int32_t num_receivers,
+                                                                           int32_t num_feature_nodes,
+                                                                           const double* xyz, const double* r,
+                                                                           int32_t on_device);
+/* The split-phase evaluation of a two-interaction model
+ * (mace_kokkos.hpp:672-697; mace_kokkos_evaluate.cpp:1658-1990):
+ *  1. begin: layer 1 up to H1 of the receivers (smx_distributed_exchange
+ *     which=0: num_receivers rows, receiver order);
+ *  2. the caller fills H1 of every feature node (its receivers' rows placed
+ *     at their feature indices, the ghosts' from their owners) and calls
+ *     continue with those num_feature_nodes rows (caller feature order): layer
+ *     2, energies, and the H1 adjoint of every feature node
+ *     (smx_distributed_exchange which=1: num_feature_nodes rows, caller
+ *     feature order, in device memory the caller may add into);
+ *  3. the caller adds each ghost row's adjoint into its owner's row and calls
+ *     finish, with those rows or (h1_adjoint NULL) the exchange buffer as
+ *     changed in place: the layer-1 reverse and the edge forces.
+ * A row is row_floats FP32 values (num_LM x the evaluator's channel count);
+ * callers copy rows whole.  Each phase returns with its outputs complete.
+ * Every other call on the evaluator is refused while a phase is pending;
+ * an error resets the phases. */
+SMX_API int32_t smx_begin_factorized_distributed_evaluation(SmxEvaluator* ev, uint64_t generation,
+                                                            int32_t num_receivers, int32_t num_feature_nodes,
+                                                            const double* xyz, const double* r, int32_t on_device);
+SMX_API int32_t smx_continue_factorized_distributed_evaluation(SmxEvaluator* ev, const float* communicated_h1,
+                                                               int64_t rows, int32_t on_device);
+SMX_API int32_t smx_finish_factorized_distributed_evaluation(SmxEvaluator* ev, const float* h1_adjoint,
+                                                             int64_t rows, int32_t on_device);
+/* the rows a phase leaves for the exchange (which 0: receivers' H1 after
+ * begin; 1: feature nodes' H1 adjoint after continue): device pointer, row
+ * count and FP32 values per row; the pair style's H1 / H1_adj views
+ * (pair_symmetrix_mace_kokkos.cpp:1582-1600, 1690-1704) */
+SMX_API int32_t smx_distributed_exchange(SmxEvaluator* ev, int32_t which, float** device_rows, int64_t* rows,
+                                         int64_t* row_floats);
 /* MACEField models (field_coupling.hpp; mace.cpp:322-395, 1147-1240).
  * _compute_prepared_factorized_positions_field(token, positions,
  * electric_field) and _compute_prepared_factorized_field(token, xyz, r,

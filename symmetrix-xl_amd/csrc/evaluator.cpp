@@ -248,6 +248,23 @@ struct Evaluator {
     std::uint64_t generation = 0, next_generation = 1;
     int N = 0;
     std::int64_t E = 0;
+    // Feature graphs (prepare_factorized_graph with feature nodes,
+    // lifecycle.cpp:949-1104; the domain-decomposed LAMMPS path,
+    // pair_symmetrix_mace_kokkos.cpp:1285-1704): F >= N feature nodes, the
+    // receivers' own and ghost atoms, any of which an edge may leave. The
+    // evaluator numbers them receivers first (receiver ii is node ii), then
+    // the other feature nodes in the caller's order; h_feature_of[k] is node
+    // k's caller feature index (empty when the caller's order is this one).
+    int F = 0;
+    std::vector<int> h_feature_types, h_feature_of;
+    DevBuf d_feature_of, d_h1_exchange;
+    // split-phase (distributed) evaluation: layer 1 -> H1 of the receivers;
+    // H1 of every feature node in -> layer 2 and the H1 adjoint of every
+    // feature node out; the receivers' summed H1 adjoint in -> layer-1 reverse
+    // (mace_kokkos_evaluate.cpp:1658-1990)
+    enum class Phase { idle, prefix_complete, middle_complete };
+    Phase phase = Phase::idle;
+    bool feature_graph() const { return F != N || !h_feature_of.empty(); }
     std::vector<int> h_node_types;
     std::vector<int> h_offsets;
     DevBuf d_node_types, d_offsets, d_neigh, d_neigh_types, d_receivers, d_soff, d_sedges, d_counts;
@@ -579,6 +596,8 @@ struct Evaluator {
             throw std::invalid_argument("mh0-dual-layer-tiled-v1 requires an ordinary two-layer MACE model");
         if (debug_plan == kPlanSingleTiled && two_layer())
             throw std::invalid_argument("mh0-single-layer-tiled-v1 requires single_layer_readout=true");
+        if (feature_graph() && (debug_plan == kPlanTiled || debug_plan == kPlanSingleTiled))
+            throw std::invalid_argument(debug_plan + " does not take graphs with ghost feature nodes");
         if (debug_plan == kPlanTiled || debug_plan == kPlanSingleTiled) {
             tiled = true;
             plan_source = "debug_plan";
@@ -604,6 +623,10 @@ struct Evaluator {
         if (hm.field && tiled) {
             tiled = false;
             plan_reason = "field coupling runs in the retained direct plan";
+        }
+        if (feature_graph() && tiled) {
+            tiled = false;
+            plan_reason = "graphs with ghost feature nodes run in the retained direct plan";
         }
         if (N <= tile_limit && debug_plan != tiled_plan() && tiled) {
             tiled = false;
@@ -856,8 +879,9 @@ struct Evaluator {
             ws.dens_dot0 = d + 2 * tn;
             ws.dens_dot1 = d + 3 * tn;
         }
-        ws.H1 = f(g_H1, n * NH * C);
-        ws.H1_adj = f(g_H1_adj, n * NH * C);
+        const std::size_t nf = std::max(F, 1);
+        ws.H1 = f(g_H1, nf * NH * C);
+        ws.H1_adj = f(g_H1_adj, nf * NH * C);
         ws.xaff = f(g_xaff, n * C);
         ws.direct = f(g_direct, n * C);
         if (hm.pre_linear_up) ws.direct_m0 = f(g_direct_m0, n * C);
@@ -870,7 +894,8 @@ struct Evaluator {
             d_field_adj.ensure(3 * sizeof(double));
         }
         ws.node_energies = static_cast<double*>(d_node_energies.ensure(n * sizeof(double)));
-        d_atom_forces.ensure(n * 3 * sizeof(double));
+        d_atom_forces.ensure(nf * 3 * sizeof(double));
+        if (feature_graph()) d_h1_exchange.ensure(nf * NH * C * sizeof(float));
         d_virial.ensure(9 * sizeof(double));
         d_stress.ensure(9 * sizeof(double));
         d_stress_partial.ensure(static_cast<std::size_t>(stress_blocks) * 9 * sizeof(double));
@@ -893,10 +918,10 @@ struct Evaluator {
     // receiver CSR on the device -> schedule, tiles, plans, workspace, token
     std::uint64_t finish_graph() {
         d_receivers.ensure(std::max<std::int64_t>(E, 1) * sizeof(int));
-        d_soff.ensure((N + 1) * sizeof(int));
+        d_soff.ensure((F + 1) * sizeof(int));
         d_sedges.ensure(std::max<std::int64_t>(E, 1) * sizeof(int));
-        d_counts.ensure(std::max(N, 1) * sizeof(int));
-        launch_graph_schedule(N, E, d_offsets.as<int>(), d_neigh.as<int>(), d_receivers.as<int>(), d_soff.as<int>(),
+        d_counts.ensure(std::max(F, 1) * sizeof(int));
+        launch_graph_schedule(N, F, E, d_offsets.as<int>(), d_neigh.as<int>(), d_receivers.as<int>(), d_soff.as<int>(),
                               d_sedges.as<int>(), d_counts.as<int>(), stream);
         if (static_cast<int>(h_offsets.size()) != N + 1) {
             h_offsets.resize(N + 1);
@@ -918,6 +943,7 @@ struct Evaluator {
     void prepare_pair_tables() {
         if (!hm.agnesi) return;
         std::vector<int> act(h_node_types.begin(), h_node_types.end());
+        act.insert(act.end(), h_feature_types.begin(), h_feature_types.end());
         std::sort(act.begin(), act.end());
         act.erase(std::unique(act.begin(), act.end()), act.end());
         if (act.empty()) act.push_back(0);
@@ -974,8 +1000,21 @@ struct Evaluator {
         }
     }
 
+    void require_idle() const {
+        if (phase != Phase::idle)
+            throw std::logic_error("A prepared factorized graph cannot change during a distributed evaluation.");
+    }
+
+    // num_features > n: a feature graph whose node order (receivers first)
+    // and h_feature_of / h_feature_types the caller has set
     std::uint64_t prepare_graph_host(int n, const int* node_types, const int* num_neigh, std::int64_t num_edges,
-                                     const int* neigh, const int* neigh_types) {
+                                     const int* neigh, const int* neigh_types, int num_features = -1) {
+        require_idle();
+        if (num_features < 0) {
+            num_features = n;
+            h_feature_of.clear();
+            h_feature_types.clear();
+        }
         if (n < 0) throw std::invalid_argument("num_nodes must be non-negative");
         if (num_edges < 0 || num_edges > kMaxEdges)
             throw std::invalid_argument("edge count exceeds the 32-bit graph limit");
@@ -990,14 +1029,17 @@ struct Evaluator {
         }
         if (total != num_edges) throw std::invalid_argument("num_neigh does not sum to the number of edges");
         for (std::int64_t e = 0; e < num_edges; ++e) {
-            if (neigh[e] < 0 || neigh[e] >= n) throw std::invalid_argument("neighbour index is out of range");
+            if (neigh[e] < 0 || neigh[e] >= num_features)
+                throw std::invalid_argument("neighbour index is out of range");
             if (neigh_types[e] < 0 || neigh_types[e] >= hm.num_elements)
                 throw std::invalid_argument("neighbour type index is out of range");
         }
         N = n;
+        F = num_features;
         E = num_edges;
         h_node_types.assign(node_types, node_types + n);
         h_offsets = off;
+        if (!h_feature_of.empty()) upload(d_feature_of, h_feature_of, stream);
         upload(d_node_types, h_node_types, stream);
         upload(d_offsets, off, stream);
         upload(d_neigh, std::vector<int>(neigh, neigh + E), stream);
@@ -1021,12 +1063,197 @@ struct Evaluator {
         return prepare_graph_host(n, t.data(), nn.data(), num_edges, nb.data(), nt.data());
     }
 
+    // prepare_factorized_graph with feature nodes (lifecycle.cpp:949-1104): the
+    // caller's checks, then the feature nodes renumbered receivers first
+    std::uint64_t prepare_feature_graph_host(int nr, int nf, const int* receiver_features, const int* node_types,
+                                             const int* feature_types, const int* num_neigh, std::int64_t num_edges,
+                                             const int* neigh, const int* neigh_types) {
+        require_idle();
+        if (nr < 0 || nf < nr) throw std::invalid_argument("Prepared Execution R1 graph extents are inconsistent.");
+        if (num_edges < 0 || num_edges > kMaxEdges)
+            throw std::invalid_argument("edge count exceeds the 32-bit graph limit");
+        validate_types(nr, node_types);
+        validate_types(nf, feature_types);
+        std::vector<int> node_of(nf, -1);
+        for (int ii = 0; ii < nr; ++ii) {
+            const int f = receiver_features[ii];
+            if (f < 0 || f >= nf) throw std::out_of_range("Prepared Execution R1 receiver feature index is out of range.");
+            if (node_types[ii] != feature_types[f])
+                throw std::invalid_argument("Prepared Execution R1 receiver and feature types disagree.");
+            if (node_of[f] >= 0)
+                throw std::invalid_argument("Prepared Execution R1 receiver feature indices must be unique.");
+            node_of[f] = ii;
+        }
+        std::vector<int> feature_of(nf);
+        for (int ii = 0; ii < nr; ++ii) feature_of[ii] = receiver_features[ii];
+        int k = nr;
+        for (int f = 0; f < nf; ++f)
+            if (node_of[f] < 0) {
+                node_of[f] = k;
+                feature_of[k++] = f;
+            }
+        std::vector<int> src(num_edges);
+        for (std::int64_t e = 0; e < num_edges; ++e) {
+            const int f = neigh[e];
+            if (f < 0 || f >= nf) throw std::out_of_range("Prepared Execution R1 source index is out of range.");
+            if (neigh_types[e] != feature_types[f])
+                throw std::invalid_argument("a neighbour type differs from its feature node's type");
+            src[e] = node_of[f];
+        }
+        bool identity = true;
+        for (int q = 0; q < nf && identity; ++q) identity = feature_of[q] == q;
+        if (hm.field && (nf != nr || !identity))
+            throw std::invalid_argument("field-coupled (MACEField) models take graphs without ghost feature nodes");
+        h_feature_types.resize(nf);
+        for (int q = 0; q < nf; ++q) h_feature_types[q] = feature_types[feature_of[q]];
+        if (identity)
+            h_feature_of.clear();
+        else
+            h_feature_of.swap(feature_of);
+        if (nf == nr && identity) h_feature_types.clear();
+        return prepare_graph_host(nr, node_types, num_neigh, num_edges, src.data(), neigh_types, nf);
+    }
+
+    // ------------------------------------------------- split-phase evaluation
+    // edge vectors of the whole graph from the caller (host: checked here;
+    // device: counted by a kernel and read back)
+    void take_xyz(const double* xyz, const double* r, bool on_device) {
+        if (E > 0 && (!xyz || !r)) throw std::invalid_argument("xyz and r are required");
+        d_xyz.ensure(std::max<std::int64_t>(E, 1) * 3 * sizeof(double));
+        d_r.ensure(std::max<std::int64_t>(E, 1) * sizeof(double));
+        xyz_host = true;
+        if (!on_device) {
+            for (std::int64_t e = 0; e < E; ++e)
+                if (!std::isfinite(r[e]) || !(r[e] > 0.0) || !std::isfinite(xyz[3 * e]) ||
+                    !std::isfinite(xyz[3 * e + 1]) || !std::isfinite(xyz[3 * e + 2]))
+                    throw std::invalid_argument("MACE graph has an invalid distance or displacement vector");
+            if (E > 0) {
+                SMX_HIP(hipMemcpyAsync(d_xyz.as<double>(), xyz, E * 3 * sizeof(double), hipMemcpyHostToDevice, stream));
+                SMX_HIP(hipMemcpyAsync(d_r.as<double>(), r, E * sizeof(double), hipMemcpyHostToDevice, stream));
+            }
+            return;
+        }
+        if (E > 0) {
+            SMX_HIP(hipMemcpyAsync(d_xyz.as<double>(), xyz, E * 3 * sizeof(double), hipMemcpyDeviceToDevice, stream));
+            SMX_HIP(hipMemcpyAsync(d_r.as<double>(), r, E * sizeof(double), hipMemcpyDeviceToDevice, stream));
+        }
+        launch_fill_zero(reinterpret_cast<float*>(d_invalid.as<int>()), 1, stream);
+        launch_count_invalid_edges(E, d_xyz.as<double>(), d_r.as<double>(), d_invalid.as<int>(), stream);
+        if (read_flag(d_invalid) > 0)
+            throw std::invalid_argument("MACE graph has an invalid distance or displacement vector");
+    }
+
+    void check_phase_graph(std::uint64_t token, int nr, int nf) const {
+        if (phase != Phase::idle) throw std::logic_error("A factorized distributed evaluation is already active.");
+        check_generation(token);
+        if (nr != N || nf != F)
+            throw std::invalid_argument("Distributed factorized graph or geometry extents are inconsistent.");
+        if (hm.field)
+            throw std::invalid_argument("the split-phase evaluation does not take field-coupled (MACEField) models");
+    }
+
+    // a one-interaction model needs no exchanged features: one call over the
+    // feature graph (mace_kokkos_evaluate.cpp:1495-1552)
+    void single_layer_distributed(std::uint64_t token, int nr, int nf, const double* xyz, const double* r,
+                                  bool on_device) {
+        check_phase_graph(token, nr, nf);
+        if (two_layer())
+            throw std::invalid_argument("Complete distributed evaluation requires a standard single-layer model.");
+        take_xyz(xyz, r, on_device);
+        evaluate(nullptr);
+        finish_call(true);
+    }
+
+    // begin_factorized_distributed_evaluation: layer 1 up to H1 of the receivers
+    void begin_distributed(std::uint64_t token, int nr, int nf, const double* xyz, const double* r, bool on_device) {
+        check_phase_graph(token, nr, nf);
+        if (!two_layer())
+            throw std::invalid_argument(
+                "a one-interaction model is evaluated in one call (compute_factorized_single_layer_distributed_evaluation)");
+        evaluated = false;
+        take_xyz(xyz, r, on_device);
+        TileView& t = tiles[0];
+        t.r = tile_r(t);
+        t.xyz = tile_xyz(t);
+        zero_a1_if_needed();
+        tile_geometry(t, nullptr);
+        ks->layer1_forward(dm, view(), t, ws, true, stream, timer.get());
+        sync();
+        phase = Phase::prefix_complete;
+    }
+
+    // the H1 rows of every feature node in (caller order), layer 2, and the
+    // H1 adjoint of every feature node out (caller order, in d_h1_exchange or,
+    // for the caller's own order, the workspace)
+    void continue_distributed(const float* h1, std::int64_t rows, bool on_device) {
+        if (phase != Phase::prefix_complete)
+            throw std::logic_error("Distributed factorized middle phase requires a completed prefix.");
+        if (!h1 || rows < F) throw std::invalid_argument("Communicated H1 does not match the distributed graph.");
+        const std::size_t row = static_cast<std::size_t>(hm.num_LM) * hm.C;
+        const bool permuted = !h_feature_of.empty();
+        float* dst = permuted ? d_h1_exchange.as<float>() : ws.H1;
+        try {
+            if (F > 0)
+                SMX_HIP(hipMemcpyAsync(dst, h1, F * row * sizeof(float),
+                                       on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, stream));
+            if (permuted)
+                launch_gather_rows(F, static_cast<int>(row), d_feature_of.as<int>(), dst, ws.H1, stream);
+            const DeviceGraph g = view();
+            const TileView& t = tiles[0];
+            ks->layer2(dm, g, t, ws, stream, timer.get());
+            ks->source_adjoint_all(g, ws, tile_r(t), hm.r_cut, stream, timer.get());
+            if (permuted)
+                launch_scatter_rows(F, static_cast<int>(row), d_feature_of.as<int>(), ws.H1_adj,
+                                    d_h1_exchange.as<float>(), stream);
+            sync();
+        } catch (...) {
+            phase = Phase::idle;
+            throw;
+        }
+        phase = Phase::middle_complete;
+    }
+
+    // the H1 adjoint the caller exchanges (caller order, F rows)
+    float* h1_adjoint_exchange() {
+        return h_feature_of.empty() ? ws.H1_adj : d_h1_exchange.as<float>();
+    }
+
+    // finish_factorized_distributed_evaluation: the receivers' H1 adjoint (the
+    // exchange buffer, summed over the owners' ghost images by the caller, or
+    // rows given here) -> layer-1 reverse, energies and edge forces
+    void finish_distributed(const float* h1_adj, std::int64_t rows, bool on_device) {
+        if (phase != Phase::middle_complete)
+            throw std::logic_error("Distributed factorized suffix requires a completed middle phase.");
+        const std::size_t row = static_cast<std::size_t>(hm.num_LM) * hm.C;
+        try {
+            if (h1_adj) {
+                if (rows < F) throw std::invalid_argument("the H1 adjoint does not match the distributed graph");
+                if (F > 0)
+                    SMX_HIP(hipMemcpyAsync(h1_adjoint_exchange(), h1_adj, F * row * sizeof(float),
+                                           on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, stream));
+            }
+            if (!h_feature_of.empty())
+                launch_gather_rows(N, static_cast<int>(row), d_feature_of.as<int>(), d_h1_exchange.as<float>(),
+                                   ws.H1_adj, stream);
+            ks->layer1_reverse(dm, view(), tiles[0], ws, true, stream, timer.get());
+            sync();
+        } catch (...) {
+            phase = Phase::idle;
+            throw;
+        }
+        phase = Phase::idle;
+        evaluated = true;
+    }
+
     // A receiver CSR that this library's own kernels built and checked on the
     // device (the LAMMPS topology): offsets come from the host, the edge
     // arrays are copied device to device, only the node types come back.
     std::uint64_t prepare_graph_checked(int n, const int* node_types, const std::vector<int>& offsets,
                                         std::int64_t num_edges, const int* neigh, const int* neigh_types) {
-        N = n;
+        require_idle();
+        N = F = n;
+        h_feature_of.clear();
+        h_feature_types.clear();
         E = num_edges;
         h_node_types.resize(n);
         if (n > 0) SMX_HIP(hipMemcpy(h_node_types.data(), node_types, sizeof(int) * n, hipMemcpyDeviceToHost));
@@ -1048,6 +1275,7 @@ struct Evaluator {
     std::pair<std::uint64_t, std::int64_t> prepare_periodic(int n, const int* node_types, const double* positions,
                                                             const double* cell_, const double* inv_,
                                                             double cutoff) {
+        require_idle();
         if (n < 0) throw std::invalid_argument("num_nodes must be non-negative");
         validate_types(n, node_types);
         // release the previous graph's edge arrays first (capacity runs)
@@ -1064,7 +1292,9 @@ struct Evaluator {
             }
         } guard{nr};
         build_neighbor_list(n, positions, cell_, inv_, cutoff, false, nr, stream);
-        N = n;
+        N = F = n;
+        h_feature_of.clear();
+        h_feature_types.clear();
         E = nr.num_edges;
         h_node_types.assign(node_types, node_types + n);
         upload(d_node_types, h_node_types, stream);
@@ -1159,6 +1389,9 @@ struct Evaluator {
                           std::int64_t positions_count, const void* ref_edges, std::int64_t edges_count,
                           const double* cell_, const double* inv_, const int* pbc_) {
         check_generation(token);
+        require_idle();
+        if (feature_graph())
+            throw std::invalid_argument("a graph with ghost feature nodes takes explicit edge vectors (xyz and r)");
         if (kind == Geometry::shifts && !tiled)
             throw std::invalid_argument("Shift geometry requires a fixed-workspace tiled plan.");
         if (!cell_ || !inv_ || !pbc_ || (N > 0 && !ref_positions) || (E > 0 && !ref_edges))
@@ -1375,8 +1608,20 @@ struct Evaluator {
         }
     }
 
+    // a plain call over a graph with ghost feature nodes: one interaction only
+    // (two need the ghosts' H1 from their owners, the split-phase calls)
+    void require_plain_call() const {
+        if (phase != Phase::idle)
+            throw std::logic_error("a factorized distributed evaluation is active: finish it first");
+        if (two_layer() && feature_graph())
+            throw std::invalid_argument(
+                "a two-interaction model on a graph with ghost feature nodes is evaluated in the split phases "
+                "(begin, continue and finish_factorized_distributed_evaluation)");
+    }
+
     void compute_positions(std::uint64_t token, const double* positions, bool on_device) {
         check_generation(token);
+        require_plain_call();
         if (geom == Geometry::none)
             throw std::invalid_argument("Execution R1 positions require current graph and geometry tokens: "
                                         "prepare a geometry (prepare_factorized_geometry or its fractional or "
@@ -1403,6 +1648,7 @@ struct Evaluator {
 
     void compute_xyz(std::uint64_t token, const double* xyz, const double* r) {
         check_generation(token);
+        require_plain_call();
         for (std::int64_t e = 0; e < E; ++e) {
             if (!std::isfinite(r[e]) || !(r[e] > 0.0) || !std::isfinite(xyz[3 * e]) || !std::isfinite(xyz[3 * e + 1]) ||
                 !std::isfinite(xyz[3 * e + 2]))
@@ -1439,6 +1685,7 @@ struct Evaluator {
     DeviceGraph view() const {
         DeviceGraph g;
         g.N = N;
+        g.F = F;
         g.E = E;
         g.node_types = d_node_types.as<int>();
         g.offsets = d_offsets.as<int>();
@@ -1459,11 +1706,12 @@ struct Evaluator {
     void reduce_forces(std::uint64_t token, double* out) {
         require_evaluated(token);
         if (!tiled)
-            launch_atom_forces(N, d_offsets.as<int>(), d_soff.as<int>(), d_sedges.as<int>(), ws.node_forces,
+            launch_atom_forces(N, F, d_offsets.as<int>(), d_soff.as<int>(), d_sedges.as<int>(),
+                               h_feature_of.empty() ? nullptr : d_feature_of.as<int>(), ws.node_forces,
                                d_atom_forces.as<double>(), stream);
         if (out) {
-            if (N > 0)
-                SMX_HIP(hipMemcpyAsync(out, d_atom_forces.as<double>(), N * 3 * sizeof(double), hipMemcpyDeviceToHost,
+            if (F > 0)
+                SMX_HIP(hipMemcpyAsync(out, d_atom_forces.as<double>(), F * 3 * sizeof(double), hipMemcpyDeviceToHost,
                                        stream));
             SMX_HIP(hipStreamSynchronize(stream));
         }
@@ -1568,6 +1816,7 @@ struct Evaluator {
     }
 
     void lammps_compute(const SmxLammpsArgsV1& a, double* energy, double* virial6) {
+        require_idle();
         if (a.struct_size < sizeof(SmxLammpsArgsV1)) throw std::invalid_argument("SmxLammpsArgsV1.struct_size is too small");
         if (a.inum < 0 || a.nall < a.inum || a.ntypes < 1)
             throw std::invalid_argument("LAMMPS counts are invalid (0 <= inum <= nall, ntypes >= 1)");
@@ -1991,6 +2240,105 @@ int32_t smx_prepare_factorized_fractional_geometry(SmxEvaluator* ev, uint64_t ge
     });
 }
 
+int32_t smx_prepare_factorized_feature_graph(SmxEvaluator* ev, int32_t num_receivers, int32_t num_feature_nodes,
+                                             const int32_t* receiver_feature_indices, const int32_t* node_types,
+                                             const int32_t* feature_types, const int32_t* num_neigh, int64_t num_edges,
+                                             const int32_t* neigh_indices, const int32_t* neigh_types,
+                                             uint64_t* generation) {
+    return guarded([&] {
+        if (!generation) throw std::invalid_argument("generation output is required");
+        if (num_receivers < 0 || num_feature_nodes < num_receivers)
+            throw std::invalid_argument("Prepared Execution R1 graph extents are inconsistent.");
+        if ((num_receivers > 0 && (!receiver_feature_indices || !node_types || !num_neigh)) ||
+            (num_feature_nodes > 0 && !feature_types) || (num_edges > 0 && (!neigh_indices || !neigh_types)))
+            throw std::invalid_argument("graph arrays are required");
+        auto& e = E(ev);
+        timed(e.last_prepare_ms, e.prepare_count, [&] {
+            *generation = e.prepare_feature_graph_host(num_receivers, num_feature_nodes, receiver_feature_indices,
+                                                       node_types, feature_types, num_neigh, num_edges, neigh_indices,
+                                                       neigh_types);
+        });
+    });
+}
+int32_t smx_prepare_factorized_feature_graph_device(SmxEvaluator* ev, int32_t num_receivers, int32_t num_feature_nodes,
+                                                    const int32_t* receiver_feature_indices, const int32_t* node_types,
+                                                    const int32_t* feature_types, const int32_t* num_neigh,
+                                                    int64_t num_edges, const int32_t* neigh_indices,
+                                                    const int32_t* neigh_types, uint64_t* generation) {
+    return guarded([&] {
+        if (num_receivers < 0 || num_feature_nodes < num_receivers || num_edges < 0 || num_edges > INT_MAX)
+            throw std::invalid_argument("Prepared Execution R1 graph extents are inconsistent.");
+        // checked on host copies, like the reference's device entry (lifecycle.cpp:2346-2380)
+        auto copy = [](const int32_t* p, std::int64_t n) {
+            std::vector<int> v(static_cast<std::size_t>(n));
+            if (n > 0) {
+                if (!p) throw std::invalid_argument("graph arrays are required");
+                SMX_HIP(hipMemcpy(v.data(), p, sizeof(int) * n, hipMemcpyDeviceToHost));
+            }
+            return v;
+        };
+        const auto rf = copy(receiver_feature_indices, num_receivers), nt = copy(node_types, num_receivers);
+        const auto ft = copy(feature_types, num_feature_nodes), nn = copy(num_neigh, num_receivers);
+        const auto nb = copy(neigh_indices, num_edges), nbt = copy(neigh_types, num_edges);
+        if (!generation) throw std::invalid_argument("generation output is required");
+        auto& e = E(ev);
+        timed(e.last_prepare_ms, e.prepare_count, [&] {
+            *generation = e.prepare_feature_graph_host(num_receivers, num_feature_nodes, rf.data(), nt.data(),
+                                                       ft.data(), nn.data(), num_edges, nb.data(), nbt.data());
+        });
+    });
+}
+int32_t smx_compute_factorized_single_layer_distributed_evaluation(SmxEvaluator* ev, uint64_t generation,
+                                                                   int32_t num_receivers, int32_t num_feature_nodes,
+                                                                   const double* xyz, const double* r,
+                                                                   int32_t on_device) {
+    return guarded([&] {
+        auto& e = E(ev);
+        timed(e.last_evaluation_ms, e.evaluation_count, [&] {
+            e.single_layer_distributed(generation, num_receivers, num_feature_nodes, xyz, r, on_device != 0);
+        });
+    });
+}
+int32_t smx_begin_factorized_distributed_evaluation(SmxEvaluator* ev, uint64_t generation, int32_t num_receivers,
+                                                    int32_t num_feature_nodes, const double* xyz, const double* r,
+                                                    int32_t on_device) {
+    return guarded([&] {
+        auto& e = E(ev);
+        e.begin_distributed(generation, num_receivers, num_feature_nodes, xyz, r, on_device != 0);
+    });
+}
+int32_t smx_continue_factorized_distributed_evaluation(SmxEvaluator* ev, const float* communicated_h1, int64_t rows,
+                                                       int32_t on_device) {
+    return guarded([&] { E(ev).continue_distributed(communicated_h1, rows, on_device != 0); });
+}
+int32_t smx_finish_factorized_distributed_evaluation(SmxEvaluator* ev, const float* h1_adjoint, int64_t rows,
+                                                     int32_t on_device) {
+    return guarded([&] {
+        auto& e = E(ev);
+        timed(e.last_evaluation_ms, e.evaluation_count,
+              [&] { e.finish_distributed(h1_adjoint, rows, on_device != 0); });
+    });
+}
+int32_t smx_distributed_exchange(SmxEvaluator* ev, int32_t which, float** device_rows, int64_t* rows,
+                                 int64_t* row_floats) {
+    return guarded([&] {
+        auto& e = E(ev);
+        if (which == 0) {
+            if (e.phase != smx::Evaluator::Phase::prefix_complete)
+                throw std::logic_error("the receivers' H1 is available after the prefix phase");
+            if (device_rows) *device_rows = e.ws.H1;
+            if (rows) *rows = e.N;
+        } else if (which == 1) {
+            if (e.phase != smx::Evaluator::Phase::middle_complete)
+                throw std::logic_error("the H1 adjoint is available after the middle phase");
+            if (device_rows) *device_rows = e.h1_adjoint_exchange();
+            if (rows) *rows = e.F;
+        } else {
+            throw std::invalid_argument("which must be 0 (receivers' H1) or 1 (feature nodes' H1 adjoint)");
+        }
+        if (row_floats) *row_floats = static_cast<int64_t>(e.hm.num_LM) * e.hm.C;
+    });
+}
 int32_t smx_compute_prepared_factorized(SmxEvaluator* ev, uint64_t generation, const double* xyz, const double* r) {
     return guarded([&] {
         auto& e = E(ev);
@@ -2088,7 +2436,7 @@ int32_t smx_reduce_prepared_stress(SmxEvaluator* ev, uint64_t generation, double
 int32_t smx_node_energies(SmxEvaluator* ev, double* out, int64_t capacity) {
     return guarded([&] {
         auto& e = E(ev);
-        if (!out || capacity < e.N) throw std::invalid_argument("buffer too small");
+        if ((!out && e.N > 0) || capacity < e.N) throw std::invalid_argument("buffer too small");
         if (!e.evaluated) throw std::logic_error("no evaluation has run");
         if (e.N > 0)
             SMX_HIP(hipMemcpyAsync(out, e.ws.node_energies, e.N * sizeof(double), hipMemcpyDeviceToHost, e.stream));
@@ -2099,7 +2447,7 @@ int32_t smx_node_energies(SmxEvaluator* ev, double* out, int64_t capacity) {
 int32_t smx_node_forces(SmxEvaluator* ev, double* out, int64_t capacity) {
     return guarded([&] {
         auto& e = E(ev);
-        if (!out || capacity < 3 * e.E) throw std::invalid_argument("buffer too small");
+        if ((!out && e.E > 0) || capacity < 3 * e.E) throw std::invalid_argument("buffer too small");
         if (!e.evaluated) throw std::logic_error("no evaluation has run");
         const double* nf = e.node_forces_device();
         if (e.E > 0) SMX_HIP(hipMemcpyAsync(out, nf, 3 * e.E * sizeof(double), hipMemcpyDeviceToHost, e.stream));

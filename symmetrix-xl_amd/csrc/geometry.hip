@@ -692,12 +692,28 @@ void launch_transpose(int K, std::int64_t E, const int* keys, int* koff, int* ke
     SMX_HIP(hipFree(off64));
 }
 
-void launch_graph_schedule(int N, std::int64_t E, const int* offsets, const int* sources, int* receivers, int* soff,
-                           int* sedges, int* scratch_counts, hipStream_t s) {
-    if (N == 0) return;
-    k_receivers<<<blocks_for(N, 256), 256, 0, s>>>(N, offsets, receivers);
-    SMX_LAUNCH_CHECK("graph_receivers");
-    launch_transpose(N, E, sources, soff, sedges, scratch_counts, s);
+void launch_graph_schedule(int N, int F, std::int64_t E, const int* offsets, const int* sources, int* receivers,
+                           int* soff, int* sedges, int* scratch_counts, hipStream_t s) {
+    if (N > 0) {
+        k_receivers<<<blocks_for(N, 256), 256, 0, s>>>(N, offsets, receivers);
+        SMX_LAUNCH_CHECK("graph_receivers");
+    }
+    launch_transpose(F, E, sources, soff, sedges, scratch_counts, s);
+}
+
+__global__ void k_count_invalid_edges(std::int64_t E, const double* __restrict__ xyz, const double* __restrict__ r,
+                                      int* __restrict__ invalid) {
+    const std::int64_t e = static_cast<std::int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (e >= E) return;
+    const double d = r[e];
+    if (!isfinite(d) || !(d > 0.0) || !isfinite(xyz[3 * e]) || !isfinite(xyz[3 * e + 1]) || !isfinite(xyz[3 * e + 2]))
+        atomicAdd(invalid, 1);
+}
+
+void launch_count_invalid_edges(std::int64_t E, const double* xyz, const double* r, int* invalid, hipStream_t s) {
+    if (E == 0) return;
+    k_count_invalid_edges<<<blocks_for(E, 256), 256, 0, s>>>(E, xyz, r, invalid);
+    SMX_LAUNCH_CHECK("count_invalid_edges");
 }
 
 void launch_edge_pairs(std::int64_t E, const int* receivers, const int* node_types, const int* neigh_types,

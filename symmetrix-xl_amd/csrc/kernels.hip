@@ -907,12 +907,13 @@ __global__ __launch_bounds__(64 * kGemmShareWaves) void k_node_gemm_shared(
 // ---------------------------------------------------------------------------
 // One wave per atom: F[a] = sum over edges leaving a of f_e - sum over edges
 // arriving at a of f_e (FP64; fixed lane partition, deterministic).
-__global__ __launch_bounds__(256) void k_atom_forces(int N, const int* __restrict__ offsets,
+__global__ __launch_bounds__(256) void k_atom_forces(int N, int num_features, const int* __restrict__ offsets,
                                                      const int* __restrict__ soff, const int* __restrict__ sedges,
+                                                     const int* __restrict__ feature_of,
                                                      const double* __restrict__ nf, double* __restrict__ F) {
     const int a = blockIdx.x * (256 / kWave) + threadIdx.x / kWave;
     const int lane = threadIdx.x % kWave;
-    if (a >= N) return;
+    if (a >= num_features) return;
     double f0 = 0.0, f1 = 0.0, f2 = 0.0;
     for (int t = soff[a] + lane; t < soff[a + 1]; t += kWave) {
         const std::size_t e = static_cast<std::size_t>(sedges[t]);
@@ -920,18 +921,20 @@ __global__ __launch_bounds__(256) void k_atom_forces(int N, const int* __restric
         f1 += nf[3 * e + 1];
         f2 += nf[3 * e + 2];
     }
-    for (int e = offsets[a] + lane; e < offsets[a + 1]; e += kWave) {
-        f0 -= nf[3 * static_cast<std::size_t>(e)];
-        f1 -= nf[3 * static_cast<std::size_t>(e) + 1];
-        f2 -= nf[3 * static_cast<std::size_t>(e) + 2];
-    }
+    if (a < N)
+        for (int e = offsets[a] + lane; e < offsets[a + 1]; e += kWave) {
+            f0 -= nf[3 * static_cast<std::size_t>(e)];
+            f1 -= nf[3 * static_cast<std::size_t>(e) + 1];
+            f2 -= nf[3 * static_cast<std::size_t>(e) + 2];
+        }
     f0 = wave_sum<kWave>(f0);
     f1 = wave_sum<kWave>(f1);
     f2 = wave_sum<kWave>(f2);
     if (lane == 0) {
-        F[3 * static_cast<std::size_t>(a)] = f0;
-        F[3 * static_cast<std::size_t>(a) + 1] = f1;
-        F[3 * static_cast<std::size_t>(a) + 2] = f2;
+        const std::size_t o = 3 * static_cast<std::size_t>(feature_of ? feature_of[a] : a);
+        F[o] = f0;
+        F[o + 1] = f1;
+        F[o + 2] = f2;
     }
 }
 
@@ -1217,9 +1220,9 @@ struct KernelSetImpl final : KernelSet {
 
     void source_adjoint_all(const DeviceGraph& g, const Workspace& w, const double* r, double r_cut, hipStream_t s,
                             LaunchTimer* tm) const override {
-        if (g.N == 0) return;
+        if (g.F == 0) return;
         TimerScope ts(tm, "source_gather", s);
-        k_source_gather<C, S::NH, false><<<g.N, C, 0, s>>>(g.soff, g.sedges, w.Wsrc, r, r_cut, w.H1_adj);
+        k_source_gather<C, S::NH, false><<<g.F, C, 0, s>>>(g.soff, g.sedges, w.Wsrc, r, r_cut, w.H1_adj);
         SMX_LAUNCH_CHECK("source_gather");
     }
 
@@ -1438,11 +1441,33 @@ void swizzle_gemm_weights(const float* w, int K, int N, float* out) {
                             w[static_cast<std::size_t>(16 * kc + 4 * kg + s) * N + 16 * nb + c];
 }
 
-void launch_atom_forces(int N, const int* offsets, const int* soff, const int* sedges, const double* node_forces,
-                        double* atom_forces, hipStream_t s) {
-    if (N == 0) return;
-    k_atom_forces<<<blocks_for(N, 256 / kWave), 256, 0, s>>>(N, offsets, soff, sedges, node_forces, atom_forces);
+void launch_atom_forces(int N, int F, const int* offsets, const int* soff, const int* sedges, const int* feature_of,
+                        const double* node_forces, double* atom_forces, hipStream_t s) {
+    if (F == 0) return;
+    k_atom_forces<<<blocks_for(F, 256 / kWave), 256, 0, s>>>(N, F, offsets, soff, sedges, feature_of, node_forces,
+                                                             atom_forces);
     SMX_LAUNCH_CHECK("atom_forces");
+}
+
+template <bool kScatter>
+__global__ __launch_bounds__(256) void k_move_rows(int row_floats, const int* __restrict__ index,
+                                                   const float* __restrict__ src, float* __restrict__ dst) {
+    const std::size_t k = blockIdx.x;
+    const std::size_t from = kScatter ? k : static_cast<std::size_t>(index[k]);
+    const std::size_t to = kScatter ? static_cast<std::size_t>(index[k]) : k;
+    for (int q = threadIdx.x; q < row_floats; q += 256) dst[to * row_floats + q] = src[from * row_floats + q];
+}
+
+void launch_gather_rows(int count, int row_floats, const int* index, const float* src, float* dst, hipStream_t s) {
+    if (count == 0) return;
+    k_move_rows<false><<<count, 256, 0, s>>>(row_floats, index, src, dst);
+    SMX_LAUNCH_CHECK("gather_rows");
+}
+
+void launch_scatter_rows(int count, int row_floats, const int* index, const float* src, float* dst, hipStream_t s) {
+    if (count == 0) return;
+    k_move_rows<true><<<count, 256, 0, s>>>(row_floats, index, src, dst);
+    SMX_LAUNCH_CHECK("scatter_rows");
 }
 
 void launch_stress(std::int64_t E, const double* node_forces, const double* xyz, double volume, double* partial,

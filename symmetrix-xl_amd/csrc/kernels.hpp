@@ -93,14 +93,15 @@ struct DeviceModel {
 
 // One prepared graph on the device (receiver-major CSR + source transpose).
 struct DeviceGraph {
-    int N = 0;
+    int N = 0;                        // receivers
+    int F = 0;                        // feature nodes (sources may be any of them; F >= N)
     std::int64_t E = 0;
     const int* node_types = nullptr;
     const int* offsets = nullptr;     // [N+1]
     const int* neigh = nullptr;       // sources [E]
     const int* neigh_types = nullptr;
     const int* receivers = nullptr;   // [E]
-    const int* soff = nullptr;        // [N+1]
+    const int* soff = nullptr;        // [F+1]
     const int* sedges = nullptr;      // [E] edges ordered by source, ascending edge id
     // [E] radial-table pair of each edge (symmetric index over the active
     // types) when tables differ per pair (Agnesi transform), else null
@@ -306,8 +307,16 @@ void launch_zbl(const DeviceModel& m, const DeviceGraph& g, const TileView& t, d
                 double* node_forces, hipStream_t s);
 
 // Reductions (FP64, deterministic order)
-void launch_atom_forces(int N, const int* offsets, const int* soff, const int* sedges, const double* node_forces,
-                        double* atom_forces, hipStream_t s);
+// forces of the F feature nodes: edges leaving a node minus (receivers,
+// a < N) its own edges; row a goes to atom_forces[feature_of[a]] (or a)
+void launch_atom_forces(int N, int F, const int* offsets, const int* soff, const int* sedges, const int* feature_of,
+                        const double* node_forces, double* atom_forces, hipStream_t s);
+// rows of row_floats floats: dst[k] = src[index[k]] (gather) or
+// dst[index[k]] = src[k] (scatter), k < count
+void launch_gather_rows(int count, int row_floats, const int* index, const float* src, float* dst, hipStream_t s);
+void launch_scatter_rows(int count, int row_floats, const int* index, const float* src, float* dst, hipStream_t s);
+// edges with a non-finite or non-positive length or a non-finite vector
+void launch_count_invalid_edges(std::int64_t E, const double* xyz, const double* r, int* invalid, hipStream_t s);
 void launch_stress(std::int64_t E, const double* node_forces, const double* xyz, double volume, double* partial,
                    int partial_blocks, double* stress, hipStream_t s);
 // virial[9] += sum_e f_e xyz_e^T over E edges
@@ -367,7 +376,7 @@ void build_neighbor_list(int N, const double* positions_host, const double* cell
                          double cutoff, bool with_shifts, NeighborResult& out, hipStream_t s);
 
 // Edge receivers and source transpose from a receiver CSR (all on device).
-void launch_graph_schedule(int N, std::int64_t E, const int* offsets, const int* sources, int* receivers,
+void launch_graph_schedule(int N, int F, std::int64_t E, const int* offsets, const int* sources, int* receivers,
                            int* soff, int* sedges, int* scratch_counts, hipStream_t s);
 // LAMMPS pair-style entry (lammps.hip): a full neighbour list as the Kokkos
 // pair style holds it, on the device.

@@ -99,6 +99,15 @@ SIGNATURES = [
     ("smx_evaluator_stream", _vp, [_vp]),
     ("smx_prepare_factorized_graph", _i32, [_vp, _i32, _vp, _vp, _i64, _vp, _vp, _p_u64]),
     ("smx_prepare_factorized_graph_device", _i32, [_vp, _i32, _vp, _vp, _i64, _vp, _vp, _p_u64]),
+    ("smx_prepare_factorized_feature_graph", _i32,
+     [_vp, _i32, _i32, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _p_u64]),
+    ("smx_prepare_factorized_feature_graph_device", _i32,
+     [_vp, _i32, _i32, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _p_u64]),
+    ("smx_compute_factorized_single_layer_distributed_evaluation", _i32, [_vp, _u64, _i32, _i32, _vp, _vp, _i32]),
+    ("smx_begin_factorized_distributed_evaluation", _i32, [_vp, _u64, _i32, _i32, _vp, _vp, _i32]),
+    ("smx_continue_factorized_distributed_evaluation", _i32, [_vp, _vp, _i64, _i32]),
+    ("smx_finish_factorized_distributed_evaluation", _i32, [_vp, _vp, _i64, _i32]),
+    ("smx_distributed_exchange", _i32, [_vp, _i32, ctypes.POINTER(_vp), _p_i64, _p_i64]),
     ("smx_prepare_periodic_factorized_graph", _i32,
      [_vp, _i32, _vp, _vp, _vp, _vp, _dbl, _p_u64, _p_i64]),
     ("smx_set_execution_plan", _i32, [_vp, _cp, _i32]),

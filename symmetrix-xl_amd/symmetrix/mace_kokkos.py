@@ -29,6 +29,17 @@ import numpy as np
 from . import _native
 from ._native import check, f64, i32, lib, ptr
 
+_HIP = None
+
+
+def _hip():
+    """the HIP runtime, for host copies of device rows the library hands out"""
+    global _HIP
+    if _HIP is None:
+        _HIP = ctypes.CDLL("libamdhip64.so")
+        _HIP.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    return _HIP
+
 
 class MACEKokkosFloat:
     """FP32 MACE evaluator on one MI355X (``streamed_edges="direct"``)."""
@@ -59,6 +70,7 @@ class MACEKokkosFloat:
                 break
             self.available_heads.append(name)
         self._num_nodes = 0
+        self._num_feature_nodes = 0
         self._num_edges = 0
 
     def _head(self, index):
@@ -181,9 +193,87 @@ class MACEKokkosFloat:
         check(lib.smx_prepare_factorized_graph(self._h, int(num_nodes), ptr(node_types), ptr(num_neigh),
                                                len(neigh_indices), ptr(neigh_indices), ptr(neigh_types),
                                                ctypes.byref(gen)))
-        self._num_nodes = int(num_nodes)
+        self._num_nodes = self._num_feature_nodes = int(num_nodes)
         self._num_edges = len(neigh_indices)
         return int(gen.value)
+
+    # ------------------------------------ feature graphs and split phases
+    def _prepare_factorized_feature_graph(self, num_receivers, num_feature_nodes, receiver_feature_indices,
+                                          node_types, feature_types, num_neigh, neigh_indices, neigh_types):
+        """prepare_factorized_graph with feature nodes (mace_kokkos.hpp:378-386):
+        one domain's receivers, its receivers' and ghost atoms as feature
+        nodes, and edges leaving any feature node (feature indices)."""
+        rf, node_types, feature_types = i32(receiver_feature_indices), i32(node_types), i32(feature_types)
+        num_neigh, neigh_indices, neigh_types = i32(num_neigh), i32(neigh_indices), i32(neigh_types)
+        if rf.size != num_receivers or node_types.size != num_receivers or num_neigh.size != num_receivers:
+            raise ValueError("receiver arrays do not match num_receivers")
+        if feature_types.size != num_feature_nodes:
+            raise ValueError("feature_types does not match num_feature_nodes")
+        if neigh_types.size != neigh_indices.size:
+            raise ValueError("neighbour arrays have different lengths")
+        gen = ctypes.c_uint64()
+        check(lib.smx_prepare_factorized_feature_graph(self._h, int(num_receivers), int(num_feature_nodes), ptr(rf),
+                                                       ptr(node_types), ptr(feature_types), ptr(num_neigh),
+                                                       neigh_indices.size, ptr(neigh_indices), ptr(neigh_types),
+                                                       ctypes.byref(gen)))
+        self._num_nodes = int(num_receivers)
+        self._num_feature_nodes = int(num_feature_nodes)
+        self._num_edges = neigh_indices.size
+        return int(gen.value)
+
+    def _edge_vectors(self, xyz, r):
+        xyz, r = f64(xyz), f64(r)
+        if xyz.size != 3 * self._num_edges or r.size != self._num_edges:
+            raise ValueError("xyz and r do not match the prepared graph")
+        return xyz, r
+
+    def _compute_factorized_single_layer_distributed_evaluation(self, execution_graph_generation, xyz, r):
+        xyz, r = self._edge_vectors(xyz, r)
+        check(lib.smx_compute_factorized_single_layer_distributed_evaluation(
+            self._h, int(execution_graph_generation), self._num_nodes, self._num_feature_nodes, ptr(xyz), ptr(r), 0))
+
+    def _begin_factorized_distributed_evaluation(self, execution_graph_generation, xyz, r):
+        xyz, r = self._edge_vectors(xyz, r)
+        check(lib.smx_begin_factorized_distributed_evaluation(
+            self._h, int(execution_graph_generation), self._num_nodes, self._num_feature_nodes, ptr(xyz), ptr(r), 0))
+
+    def _distributed_rows(self, which):
+        """host copy of the rows a phase leaves for the exchange: 0, the
+        receivers' H1; 1, the feature nodes' H1 adjoint"""
+        dev, rows, width = ctypes.c_void_p(), ctypes.c_int64(), ctypes.c_int64()
+        check(lib.smx_distributed_exchange(self._h, int(which), ctypes.byref(dev), ctypes.byref(rows),
+                                           ctypes.byref(width)))
+        out = np.zeros((rows.value, width.value), np.float32)
+        if out.size and _hip().hipMemcpy(out.ctypes.data_as(ctypes.c_void_p), dev, ctypes.c_size_t(out.nbytes), 2):
+            raise RuntimeError("hipMemcpy of the exchange rows failed")
+        return out
+
+    def _distributed_h1(self):
+        return self._distributed_rows(0)
+
+    def _distributed_h1_adjoint(self):
+        return self._distributed_rows(1)
+
+    def _exchange_rows(self, which, rows, name):
+        """rows as a float32 [num_feature_nodes, row_floats] array, the
+        phase's row width checked (the library reads whole rows)"""
+        width = ctypes.c_int64()
+        check(lib.smx_distributed_exchange(self._h, int(which), None, None, ctypes.byref(width)))
+        h = np.ascontiguousarray(rows, dtype=np.float32)
+        if h.shape != (self._num_feature_nodes, width.value):
+            raise ValueError("%s must have shape (%d, %d)" % (name, self._num_feature_nodes, width.value))
+        return h
+
+    def _continue_factorized_distributed_evaluation(self, communicated_h1):
+        h = self._exchange_rows(0, communicated_h1, "communicated H1")
+        check(lib.smx_continue_factorized_distributed_evaluation(self._h, ptr(h), h.shape[0], 0))
+
+    def _finish_factorized_distributed_evaluation(self, h1_adjoint=None):
+        if h1_adjoint is None:
+            check(lib.smx_finish_factorized_distributed_evaluation(self._h, None, 0, 0))
+            return
+        h = self._exchange_rows(1, h1_adjoint, "the H1 adjoint")
+        check(lib.smx_finish_factorized_distributed_evaluation(self._h, ptr(h), h.shape[0], 0))
 
     def _prepare_periodic_factorized_graph(self, node_types, positions, cell, inverse_cell, neighbor_cutoff):
         node_types = i32(node_types)
@@ -198,7 +288,7 @@ class MACEKokkosFloat:
         check(lib.smx_prepare_periodic_factorized_graph(self._h, node_types.size, ptr(node_types), ptr(positions),
                                                         ptr(cell), ptr(inverse_cell), float(neighbor_cutoff),
                                                         ctypes.byref(gen), ctypes.byref(ne)))
-        self._num_nodes = node_types.size
+        self._num_nodes = self._num_feature_nodes = node_types.size
         self._num_edges = int(ne.value)
         return {"generation": int(gen.value), "num_edges": int(ne.value)}
 
@@ -305,7 +395,7 @@ class MACEKokkosFloat:
         check(lib.smx_compute_node_energies_forces(self._h, int(num_nodes), ptr(node_types), ptr(num_neigh),
                                                    neigh_indices.size, ptr(neigh_indices), ptr(neigh_types),
                                                    ptr(xyz), ptr(r)))
-        self._num_nodes = int(num_nodes)
+        self._num_nodes = self._num_feature_nodes = int(num_nodes)
         self._num_edges = neigh_indices.size
 
     # ------------------------------------------------------------ reductions
@@ -322,7 +412,7 @@ class MACEKokkosFloat:
                 out[:, c] = (np.bincount(src, weights=f[:, c], minlength=num_nodes)
                              - np.bincount(rcv, weights=f[:, c], minlength=num_nodes))
             return out
-        out = np.zeros((self._num_nodes, 3))
+        out = np.zeros((self._num_feature_nodes, 3))
         check(lib.smx_reduce_prepared_node_forces(self._h, int(execution_graph_generation), ptr(out)))
         return out
 

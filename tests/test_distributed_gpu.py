@@ -1,0 +1,180 @@
+"""One GPU's share of a domain-decomposed evaluation (the LAMMPS multi-rank
+path, pair_symmetrix_mace_kokkos.cpp:1285-1704; the evaluator's split phases,
+mace_kokkos_evaluate.cpp:1495-1990; feature graphs, mace_kokkos_factorized_
+lifecycle.cpp:949-1104).
+
+A periodic system is cut into slabs.  Each slab gets its own evaluator over a
+graph of its receivers and the ghost atoms their edges leave, with the
+feature nodes in a shuffled order (receivers among them).  Between the phases
+the H1 rows and their adjoints are exchanged on the host, as LAMMPS's forward
+and reverse communication would move them between ranks.  The sums over the
+slabs must give the whole system's energies, forces and stress: the oracle's,
+and this library's own whole-system evaluation to FP32 summation order.
+"""
+
+import numpy as np
+import pytest
+
+from test_gpu_parity import _assert_efs, _system
+
+pytestmark = pytest.mark.gpu
+
+
+def _slabs(s, ref, parts, seed):
+    """per slab: receivers (global ids, shuffled), feature nodes (global ids,
+    shuffled), the receivers' feature indices and the slab's CSR"""
+    g = ref["graph"]
+    cell = np.asarray(s["cell"], float)
+    frac = (np.asarray(s["positions"], float) @ np.linalg.inv(cell))[:, 0] % 1.0
+    owner = np.minimum((frac * parts).astype(int), parts - 1)
+    rng = np.random.default_rng(seed)
+    off, src = g["offsets"], g["sources"]
+    out = []
+    for d in range(parts):
+        recv = rng.permutation(np.flatnonzero(owner == d))
+        edges = np.concatenate([np.arange(off[i], off[i + 1]) for i in recv]) if recv.size else np.zeros(0, int)
+        ghosts = np.setdiff1d(np.unique(src[edges]), recv)
+        feats = rng.permutation(np.concatenate([recv, ghosts]))
+        index = {int(a): k for k, a in enumerate(feats)}
+        out.append(dict(recv=recv, feats=feats, edges=edges,
+                        rfi=np.array([index[int(a)] for a in recv], np.int32),
+                        neigh=np.array([index[int(a)] for a in src[edges]], np.int32),
+                        num_neigh=(off[recv + 1] - off[recv]).astype(np.int32)))
+    return out
+
+
+def _run(path, s, ref, types, parts, seed=0):
+    """the slabs' split-phase evaluations with the host exchange; energies,
+    forces and stress summed over the slabs"""
+    from symmetrix.mace_kokkos import MACEKokkosFloat
+    n = len(types)
+    slabs = _slabs(s, ref, parts, seed)
+    evs = []
+    for sl in slabs:
+        ev = MACEKokkosFloat(path)
+        sl["gen"] = ev._prepare_factorized_feature_graph(
+            len(sl["recv"]), len(sl["feats"]), sl["rfi"], types[sl["recv"]], types[sl["feats"]], sl["num_neigh"],
+            sl["neigh"], types[ref["graph"]["sources"][sl["edges"]]])
+        sl["xyz"] = ref["xyz"].reshape(-1, 3)[sl["edges"]]
+        sl["r"] = ref["r"][sl["edges"]]
+        evs.append(ev)
+    if evs[0].num_interactions == 1:
+        for ev, sl in zip(evs, slabs):
+            ev._compute_factorized_single_layer_distributed_evaluation(sl["gen"], sl["xyz"], sl["r"])
+    else:
+        for ev, sl in zip(evs, slabs):
+            ev._begin_factorized_distributed_evaluation(sl["gen"], sl["xyz"], sl["r"])
+        # forward communication: each atom's H1 row from its owner
+        rows = [ev._distributed_h1() for ev in evs]
+        H1 = np.zeros((n, rows[0].shape[1]), np.float32)
+        for sl, h in zip(slabs, rows):
+            H1[sl["recv"]] = h
+        for ev, sl in zip(evs, slabs):
+            ev._continue_factorized_distributed_evaluation(H1[sl["feats"]])
+        # reverse communication: every image's adjoint summed onto the owner
+        adj = np.zeros_like(H1, dtype=np.float64)
+        for ev, sl in zip(evs, slabs):
+            np.add.at(adj, sl["feats"], ev._distributed_h1_adjoint().astype(np.float64))
+        for ev, sl in zip(evs, slabs):
+            ev._finish_factorized_distributed_evaluation(adj[sl["feats"]].astype(np.float32))
+    e = np.zeros(n)
+    f = np.zeros((n, 3))
+    st = np.zeros((3, 3))
+    V = abs(np.linalg.det(np.asarray(s["cell"], float)))
+    for ev, sl in zip(evs, slabs):
+        e[sl["recv"]] = ev.node_energies
+        np.add.at(f, sl["feats"], ev._reduce_atom_forces(len(sl["feats"]), None, None, sl["gen"]))
+        st += ev._reduce_stress(V, None, sl["gen"])
+    return e, f, st
+
+
+@pytest.mark.parametrize("model", ["tiny", "tiny_residual", "tiny_agnesi", "tiny_scaled", "tiny_zbl",
+                                   "tiny_single"])
+@pytest.mark.parametrize("parts", [2, 3])
+def test_slabs_sum_to_the_whole_system(request, model, parts):
+    from oracle import oracle
+    from symmetrix.mace_kokkos import MACEKokkosFloat
+    path = request.getfixturevalue(model + "_model_path")
+    s = _system("tiny")
+    om = oracle.OracleModel(path)
+    ref = oracle.evaluate_system(om, s, skin=0.5)
+    types = om.types_of(s["numbers"])
+    n = len(types)
+    e, f, st = _run(path, s, ref, types, parts)
+    _assert_efs(ref, e, f, st, n)
+    np.testing.assert_allclose(e, ref["energies"], rtol=0, atol=1e-4)
+    # the whole system on one evaluator, same graph and edge vectors
+    whole = MACEKokkosFloat(path)
+    g = ref["graph"]
+    gen = whole._prepare_factorized_graph(n, types, g["num_neigh"], g["sources"], types[g["sources"]])
+    whole._compute_prepared_factorized(gen, ref["xyz"], ref["r"])
+    fw = whole._reduce_atom_forces(n, None, None, gen)
+    print("slabs vs whole: energy %.3e force %.3e" % (np.max(np.abs(e - whole.node_energies)),
+                                                     np.max(np.abs(f - fw))))
+    np.testing.assert_allclose(e, whole.node_energies, rtol=0, atol=2e-5)
+    np.testing.assert_allclose(f, fw, rtol=0, atol=2e-5)
+
+
+def test_a_slab_without_receivers(tiny_model_path):
+    """a rank whose domain holds no atoms still passes through the phases
+    (its H1 adjoint rows are zero)"""
+    from symmetrix.mace_kokkos import MACEKokkosFloat
+    ev = MACEKokkosFloat(tiny_model_path)
+    gen = ev._prepare_factorized_feature_graph(0, 4, [], [], [0, 1, 2, 0], [], [], [])
+    ev._begin_factorized_distributed_evaluation(gen, np.zeros((0, 3)), np.zeros(0))
+    assert ev._distributed_h1().shape[0] == 0
+    w = ev._distributed_rows(0).shape[1]
+    ev._continue_factorized_distributed_evaluation(np.ones((4, w), np.float32))
+    adj = ev._distributed_h1_adjoint()
+    assert adj.shape == (4, w) and not adj.any()
+    ev._finish_factorized_distributed_evaluation()
+    assert ev.node_energies.size == 0
+    assert not ev._reduce_atom_forces(4, None, None, gen).any()
+
+
+def test_phase_order_and_refusals(tiny_model_path, tiny_single_model_path, tiny_field_model_path):
+    from oracle import oracle
+    from symmetrix.mace_kokkos import MACEKokkosFloat
+    s = _system("tiny")
+    om = oracle.OracleModel(tiny_model_path)
+    ref = oracle.evaluate_system(om, s, skin=0.5)
+    types = om.types_of(s["numbers"])
+    sl = _slabs(s, ref, 2, 1)[0]
+    args = (len(sl["recv"]), len(sl["feats"]), sl["rfi"], types[sl["recv"]], types[sl["feats"]], sl["num_neigh"],
+            sl["neigh"], types[ref["graph"]["sources"][sl["edges"]]])
+    xyz, r = ref["xyz"].reshape(-1, 3)[sl["edges"]], ref["r"][sl["edges"]]
+    ev = MACEKokkosFloat(tiny_model_path)
+    gen = ev._prepare_factorized_feature_graph(*args)
+    # a two-interaction model needs the exchange: no plain call over ghosts
+    with pytest.raises(ValueError, match="split phases"):
+        ev._compute_prepared_factorized(gen, xyz, r)
+    with pytest.raises(RuntimeError, match="prefix"):
+        ev._continue_factorized_distributed_evaluation(np.zeros((1, 1), np.float32))
+    ev._begin_factorized_distributed_evaluation(gen, xyz, r)
+    with pytest.raises(RuntimeError, match="already active"):
+        ev._begin_factorized_distributed_evaluation(gen, xyz, r)
+    with pytest.raises(RuntimeError, match="distributed evaluation"):
+        ev._prepare_factorized_feature_graph(*args)
+    w = ev._distributed_h1().shape[1]
+    with pytest.raises(ValueError, match="shape"):
+        ev._continue_factorized_distributed_evaluation(np.zeros((len(sl["feats"]) - 1, w), np.float32))
+    with pytest.raises(RuntimeError, match="middle phase"):
+        ev._finish_factorized_distributed_evaluation()
+    # a refused phase leaves the evaluator idle: the one-call form still runs
+    ev2 = MACEKokkosFloat(tiny_single_model_path)
+    gen2 = ev2._prepare_factorized_feature_graph(*args)
+    with pytest.raises(ValueError, match="one call"):
+        ev2._begin_factorized_distributed_evaluation(gen2, xyz, r)
+    ev2._compute_factorized_single_layer_distributed_evaluation(gen2, xyz, r)
+    assert np.all(np.isfinite(ev2.node_energies))
+    # graph checks
+    bad = list(args)
+    bad[2] = np.zeros_like(sl["rfi"])
+    with pytest.raises(ValueError, match="unique|disagree"):
+        MACEKokkosFloat(tiny_model_path)._prepare_factorized_feature_graph(*bad)
+    bad = list(args)
+    bad[6] = np.where(np.arange(len(sl["neigh"])) == 0, len(sl["feats"]), sl["neigh"]).astype(np.int32)
+    with pytest.raises(ValueError, match="out of range"):
+        MACEKokkosFloat(tiny_model_path)._prepare_factorized_feature_graph(*bad)
+    with pytest.raises(ValueError, match="MACEField"):
+        MACEKokkosFloat(tiny_field_model_path)._prepare_factorized_feature_graph(*args)
