@@ -2323,6 +2323,8 @@ int32_t smx_distributed_exchange(SmxEvaluator* ev, int32_t which, float** device
                                  int64_t* row_floats) {
     return guarded([&] {
         auto& e = E(ev);
+        if (row_floats) *row_floats = static_cast<int64_t>(e.hm.num_LM) * e.hm.C;
+        if (!device_rows && !rows) return;  // the row width alone, at any time
         if (which == 0) {
             if (e.phase != smx::Evaluator::Phase::prefix_complete)
                 throw std::logic_error("the receivers' H1 is available after the prefix phase");
@@ -2336,7 +2338,6 @@ int32_t smx_distributed_exchange(SmxEvaluator* ev, int32_t which, float** device
         } else {
             throw std::invalid_argument("which must be 0 (receivers' H1) or 1 (feature nodes' H1 adjoint)");
         }
-        if (row_floats) *row_floats = static_cast<int64_t>(e.hm.num_LM) * e.hm.C;
     });
 }
 int32_t smx_compute_prepared_factorized(SmxEvaluator* ev, uint64_t generation, const double* xyz, const double* r) {

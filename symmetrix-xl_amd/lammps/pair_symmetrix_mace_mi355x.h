@@ -2,17 +2,24 @@
    pair_style symmetrix/mace/mi355x/kk: MACE energies, forces and virial on
    one MI355X through libsymmetrix_mi355x.so (include/symmetrix_mi355x.h).
 
-   The single-rank path of the reference's pair_style symmetrix/mace/kk
-   without domain decomposition (pair_symmetrix_mace_kokkos.cpp:1010-1282):
-   one full Kokkos neighbour list with ghosts, every local atom a graph
-   node, every neighbour (local or ghost) an edge to the local atom it is an
-   image of.  The library builds the graph on neighbour-list rebuilds, forms
-   the edge vectors from x each step, evaluates the model and adds the edge
-   forces to the local and ghost rows of f (the ghost rows then go through
-   LAMMPS's reverse communication).
+   Two of the reference's pair_style symmetrix/mace/kk modes:
+   * no_domain_decomposition (one MPI rank; pair_symmetrix_mace_kokkos.cpp:
+     1010-1282): one full Kokkos neighbour list with ghosts, every local atom
+     a graph node, every neighbour (local or ghost) an edge to the local atom
+     it is an image of.  The library builds the graph on neighbour-list
+     rebuilds, forms the edge vectors from x each step, evaluates the model
+     and adds the edge forces to the local and ghost rows of f (the ghost rows
+     then go through LAMMPS's reverse communication).
+   * mpi_message_passing (one rank per GPU; :1285-1704): each rank's local
+     atoms are the receivers and every local or ghost atom a feature node of
+     the library's split-phase evaluation; between its phases the H1 rows of
+     the ghosts come from their owners (forward communication) and the H1
+     adjoint rows of the ghosts go back to them (reverse communication).
+   The default is no_domain_decomposition on one rank and
+   mpi_message_passing on several.
 
    Usage (the reference's keywords where they apply):
-     pair_style symmetrix/mace/mi355x/kk [no_domain_decomposition] [head NAME]
+     pair_style symmetrix/mace/mi355x/kk [no_domain_decomposition|mpi_message_passing] [head NAME]
                 [profile capacity|speed] [low_memory yes|no]
                 [allow_fixed_workspace yes|no] [streamed_edges auto|direct]
                 [electric_field Ex Ey Ez]   (required by MACEField models)
@@ -58,6 +65,16 @@ class PairSymmetrixMACEMI355X : public Pair, public KokkosBase {
   double init_one(int, int) override;
   void init_style() override;
 
+  // H1 rows forward, H1 adjoint rows in reverse (mpi_message_passing)
+  int pack_forward_comm_kokkos(int, DAT::tdual_int_1d, DAT::tdual_double_1d &, int, int *) override;
+  void unpack_forward_comm_kokkos(int, int, DAT::tdual_double_1d &) override;
+  int pack_reverse_comm_kokkos(int, int, DAT::tdual_double_1d &) override;
+  void unpack_reverse_comm_kokkos(int, DAT::tdual_int_1d, DAT::tdual_double_1d &) override;
+  int pack_forward_comm(int, int *, double *, int, int *) override;
+  void unpack_forward_comm(int, int, double *) override;
+  int pack_reverse_comm(int, int, double *) override;
+  void unpack_reverse_comm(int, int *, double *) override;
+
  protected:
   SmxEvaluator *evaluator = nullptr;
   std::string head;
@@ -68,6 +85,20 @@ class PairSymmetrixMACEMI355X : public Pair, public KokkosBase {
   bool electric_field_set = false;
   double r_cut = 0.0;
 
+  std::string mode;                 // no_domain_decomposition or mpi_message_passing
+  bool single_layer = false;        // one-interaction model: no features are exchanged
+  int row_floats = 0;               // FP32 values of one atom's H1 row
+  uint64_t generation = 0;          // the rank's feature graph (mpi_message_passing)
+  int graph_nall = -1;
+  int64_t num_edges = 0;
+  Kokkos::View<int *, DeviceType> d_feature_types, d_receiver_features, d_node_types, d_num_neigh, d_first,
+      d_neigh, d_neigh_types;
+  Kokkos::View<double *, DeviceType> d_xyz, d_r;
+  Kokkos::View<float *, DeviceType> d_h1;          // [nall][row_floats] H1 rows by LAMMPS index
+  float *exchange_rows = nullptr;                   // the evaluator's H1 adjoint rows while they are exchanged
+  Kokkos::View<double *, DeviceType> d_stage;       // host-staged communication
+  Kokkos::View<int *, DeviceType> d_stage_list;
+
   Kokkos::View<int *, DeviceType> d_type_to_model;  // [ntypes] model type of LAMMPS type t+1
   Kokkos::View<int *, DeviceType> d_owner;          // [nall] local atom each atom is an image of
   typename Kokkos::View<int *, DeviceType>::HostMirror h_owner;
@@ -75,6 +106,9 @@ class PairSymmetrixMACEMI355X : public Pair, public KokkosBase {
 
   void allocate();
   void check(int32_t status, const char *what);
+  void compute_no_domain_decomposition();
+  void compute_mpi_message_passing();
+  void stage(size_t values);
 };
 
 }    // namespace LAMMPS_NS

@@ -148,8 +148,9 @@ def test_phase_order_and_refusals(tiny_model_path, tiny_single_model_path, tiny_
     # a two-interaction model needs the exchange: no plain call over ghosts
     with pytest.raises(ValueError, match="split phases"):
         ev._compute_prepared_factorized(gen, xyz, r)
+    from symmetrix._native import check, lib
     with pytest.raises(RuntimeError, match="prefix"):
-        ev._continue_factorized_distributed_evaluation(np.zeros((1, 1), np.float32))
+        check(lib.smx_continue_factorized_distributed_evaluation(ev._h, None, 0, 0))
     ev._begin_factorized_distributed_evaluation(gen, xyz, r)
     with pytest.raises(RuntimeError, match="already active"):
         ev._begin_factorized_distributed_evaluation(gen, xyz, r)
@@ -178,3 +179,89 @@ def test_phase_order_and_refusals(tiny_model_path, tiny_single_model_path, tiny_
         MACEKokkosFloat(tiny_model_path)._prepare_factorized_feature_graph(*bad)
     with pytest.raises(ValueError, match="MACEField"):
         MACEKokkosFloat(tiny_field_model_path)._prepare_factorized_feature_graph(*args)
+
+
+def test_device_forms_as_the_pair_style_calls_them(tiny_model_path):
+    """The C entry points with device arrays, in the order the pair style's
+    mpi_message_passing compute makes them: the feature graph from device
+    arrays, device edge vectors, the exchange rows read and (reverse
+    communication) written in place in device memory, finish without rows."""
+    import ctypes
+    from oracle import oracle
+    from symmetrix._native import check, lib
+    from symmetrix.mace_kokkos import MACEKokkosFloat
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    hip.hipFree.argtypes = [ctypes.c_void_p]
+    held = []
+
+    def dev(a):
+        a = np.ascontiguousarray(a)
+        p = ctypes.c_void_p()
+        assert hip.hipMalloc(ctypes.byref(p), ctypes.c_size_t(max(a.nbytes, 8))) == 0
+        assert hip.hipMemcpy(p, a.ctypes.data_as(ctypes.c_void_p), ctypes.c_size_t(a.nbytes), 1) == 0
+        held.append(p)
+        return p
+
+    def to_host(p, shape):
+        out = np.zeros(shape, np.float32)
+        assert hip.hipMemcpy(out.ctypes.data_as(ctypes.c_void_p), p, ctypes.c_size_t(out.nbytes), 2) == 0
+        return out
+
+    s = _system("tiny")
+    om = oracle.OracleModel(tiny_model_path)
+    ref = oracle.evaluate_system(om, s, skin=0.5)
+    types = om.types_of(s["numbers"]).astype(np.int32)
+    n = len(types)
+    slabs = _slabs(s, ref, 2, 3)
+    evs = []
+    try:
+        for sl in slabs:
+            ev = MACEKokkosFloat(tiny_model_path)
+            gen = ctypes.c_uint64()
+            src = ref["graph"]["sources"][sl["edges"]]
+            check(lib.smx_prepare_factorized_feature_graph_device(
+                ev._h, len(sl["recv"]), len(sl["feats"]), dev(sl["rfi"]), dev(types[sl["recv"]]),
+                dev(types[sl["feats"]]), dev(sl["num_neigh"]), len(sl["edges"]), dev(sl["neigh"]),
+                dev(types[src]), ctypes.byref(gen)))
+            sl["gen"] = gen.value
+            check(lib.smx_begin_factorized_distributed_evaluation(
+                ev._h, gen.value, len(sl["recv"]), len(sl["feats"]), dev(ref["xyz"].reshape(-1, 3)[sl["edges"]]),
+                dev(ref["r"][sl["edges"]]), 1))
+            ev._num_nodes, ev._num_feature_nodes, ev._num_edges = len(sl["recv"]), len(sl["feats"]), len(sl["edges"])
+            evs.append(ev)
+
+        def rows(ev, which):
+            p, cnt, w = ctypes.c_void_p(), ctypes.c_int64(), ctypes.c_int64()
+            check(lib.smx_distributed_exchange(ev._h, which, ctypes.byref(p), ctypes.byref(cnt), ctypes.byref(w)))
+            return p, cnt.value, w.value
+
+        H1 = None
+        for ev, sl in zip(evs, slabs):
+            p, cnt, w = rows(ev, 0)
+            H1 = np.zeros((n, w), np.float32) if H1 is None else H1
+            H1[sl["recv"]] = to_host(p, (cnt, w))
+        for ev, sl in zip(evs, slabs):
+            check(lib.smx_continue_factorized_distributed_evaluation(ev._h, dev(H1[sl["feats"]]), len(sl["feats"]),
+                                                                     1))
+        adj = np.zeros(H1.shape)
+        ptrs = []
+        for ev, sl in zip(evs, slabs):
+            p, cnt, w = rows(ev, 1)
+            np.add.at(adj, sl["feats"], to_host(p, (cnt, w)).astype(np.float64))
+            ptrs.append(p)
+        for ev, sl, p in zip(evs, slabs, ptrs):
+            mine = np.ascontiguousarray(adj[sl["feats"]], dtype=np.float32)
+            assert hip.hipMemcpy(p, mine.ctypes.data_as(ctypes.c_void_p), ctypes.c_size_t(mine.nbytes), 1) == 0
+            check(lib.smx_finish_factorized_distributed_evaluation(ev._h, None, 0, 1))
+        e = np.zeros(n)
+        f = np.zeros((n, 3))
+        for ev, sl in zip(evs, slabs):
+            e[sl["recv"]] = ev.node_energies
+            np.add.at(f, sl["feats"], ev._reduce_atom_forces(len(sl["feats"]), None, None, sl["gen"]))
+        np.testing.assert_allclose(e, ref["energies"], rtol=0, atol=1e-4)
+        assert np.max(np.abs(f - ref["forces"])) < 1e-4
+    finally:
+        for p in held:
+            hip.hipFree(p)
