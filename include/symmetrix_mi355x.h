@@ -241,7 +241,12 @@ SMX_API int32_t smx_compute_prepared_factorized_positions_device(SmxEvaluator* e
  * the plain xyz call).  The node forces reduced by
  * smx_reduce_prepared_node_forces are the feature nodes' (3 *
  * num_feature_nodes doubles, caller order; ghosts' forces are the caller's
- * to return to their owners).  Field-coupled models are refused. */
+ * to return to their owners).  A field-coupled model exchanges H1 before
+ * its field (H1p = M0 P + b) and the adjoint of that; the field paths and
+ * linear_up run over every feature node, a per-node field
+ * (smx_set_electric_field) has 3 values per feature node in the caller's
+ * order, and smx_electric_field_adj returns this rank's part of dE/dE (the
+ * ranks' parts sum to the whole). */
 SMX_API int32_t smx_prepare_factorized_feature_graph(SmxEvaluator* ev, int32_t num_receivers,
                                                      int32_t num_feature_nodes,
                                                      const int32_t* receiver_feature_indices,
@@ -279,7 +284,8 @@ SMX_API int32_t smx_compute_factorized_single_layer_distributed_evaluation(SmxEv
  *  3. the caller adds each ghost row's adjoint into its owner's row and calls
  *     finish, with those rows or (h1_adjoint NULL) the exchange buffer as
  *     changed in place: the layer-1 reverse and the edge forces.
- * A row is row_floats FP32 values (num_LM x the evaluator's channel count);
+ * A row is row_floats FP32 values (num_LM x the evaluator's channel count;
+ * H1p rows for a field-coupled model);
  * callers copy rows whole.  Each phase returns with its outputs complete.
  * Every other call on the evaluator is refused while a phase is pending;
  * an error resets the phases. */

@@ -264,6 +264,10 @@ struct Evaluator {
     // (mace_kokkos_evaluate.cpp:1658-1990)
     enum class Phase { idle, prefix_complete, middle_complete };
     Phase phase = Phase::idle;
+    // MACEField over a feature graph: the field paths and linear_up run over
+    // every feature node (one tile of F rows, plans over all of them)
+    PlanSet ps_feat_h1, ps_feat_fz, ps_feat_fy;
+    TileView feature_tile;
     bool feature_graph() const { return F != N || !h_feature_of.empty(); }
     std::vector<int> h_node_types;
     std::vector<int> h_offsets;
@@ -718,6 +722,59 @@ struct Evaluator {
 
     std::vector<int> plan_key;  // (N, tiling, node types) of the node plans on the device
 
+    // one tile over all F feature nodes: the h1 (U, U^T), fz and fy plans
+    void build_feature_tile() {
+        for (PlanSet* p : {&ps_feat_h1, &ps_feat_fz, &ps_feat_fy}) {
+            p->tiles.clear();
+            p->rows.clear();
+            p->sets.clear();
+            p->tile_begin.assign(1, 0);
+            p->set_begin.assign(1, 0);
+        }
+        auto add = [&](PlanSet& P, int group, int l) {
+            const int start = static_cast<int>(P.rows.size());
+            for (int m = 0; m < 2 * l + 1; ++m)
+                for (int q = 0; q < F; ++q) P.rows.push_back(q << 4 | m);
+            const int end = static_cast<int>(P.rows.size());
+            const int t0 = static_cast<int>(P.tiles.size());
+            for (int s0 = start; s0 < end; s0 += kGemmRows)
+                P.tiles.push_back(GemmTile{s0, std::min(kGemmRows, end - s0), group});
+            const int t1 = static_cast<int>(P.tiles.size());
+            for (int t = t0; t < t1; t += kGemmShareWaves)
+                P.sets.push_back(GemmTileSet{t, std::min(kGemmShareWaves, t1 - t)});
+        };
+        for (int l = 0; l <= hm.L_max; ++l) add(ps_feat_h1, l, l);
+        for (std::size_t p = 0; p < hm.field_paths.size(); ++p) {
+            add(ps_feat_fz, static_cast<int>(p), hm.field_paths[p].l_in);
+            add(ps_feat_fy, static_cast<int>(p), hm.field_paths[p].l_out);
+        }
+        auto view = [&](PlanSet& P, const DevBuf& groups, int max_n, int n_sub) {
+            P.tile_begin.push_back(P.tiles.size());
+            P.set_begin.push_back(P.sets.size());
+            upload(P.d_tiles, P.tiles, stream);
+            upload(P.d_rows, P.rows, stream);
+            upload(P.d_sets, P.sets, stream);
+            GemmPlan g;
+            g.n_sub = n_sub;
+            g.tiles = P.d_tiles.as<GemmTile>();
+            g.num_tiles = static_cast<int>(P.tiles.size());
+            g.groups = groups.as<GemmGroup>();
+            g.rows = P.d_rows.as<int>();
+            g.max_n = max_n;
+            g.sets = P.d_sets.as<GemmTileSet>();
+            g.num_sets = static_cast<int>(P.sets.size());
+            return g;
+        };
+        feature_tile = TileView{};
+        feature_tile.r0 = 0;
+        feature_tile.nr = F;
+        feature_tile.e0 = 0;
+        feature_tile.ne = E;
+        feature_tile.h1 = view(ps_feat_h1, d_groups_h1, max_n_h1, sub_h1);
+        feature_tile.fz = view(ps_feat_fz, d_groups_fz, hm.C, sub_f);
+        feature_tile.fy = view(ps_feat_fy, d_groups_fy, hm.C, sub_f);
+    }
+
     void build_node_plans() {
         h_node_list.clear();
         node_list_begin.clear();
@@ -882,15 +939,15 @@ struct Evaluator {
         const std::size_t nf = std::max(F, 1);
         ws.H1 = f(g_H1, nf * NH * C);
         ws.H1_adj = f(g_H1_adj, nf * NH * C);
-        ws.xaff = f(g_xaff, n * C);
+        ws.xaff = f(g_xaff, (hm.field ? nf : n) * C);
         ws.direct = f(g_direct, n * C);
         if (hm.pre_linear_up) ws.direct_m0 = f(g_direct_m0, n * C);
         if (hm.field) {
-            ws.H1p = f(g_H1p, n * NH * C);
-            ws.H1f = f(g_H1f, n * NH * C);
-            ws.H1p_adj = f(g_H1p_adj, n * NH * C);
-            ws.fzy = f(g_fzy, n * static_cast<std::size_t>(std::max(dm.field_zr, dm.field_yr)) * C);
-            ws.field_part = static_cast<double*>(d_field_part.ensure(n * 3 * sizeof(double)));
+            ws.H1p = f(g_H1p, nf * NH * C);
+            ws.H1f = f(g_H1f, nf * NH * C);
+            ws.H1p_adj = f(g_H1p_adj, nf * NH * C);
+            ws.fzy = f(g_fzy, nf * static_cast<std::size_t>(std::max(dm.field_zr, dm.field_yr)) * C);
+            ws.field_part = static_cast<double*>(d_field_part.ensure(nf * 3 * sizeof(double)));
             d_field_adj.ensure(3 * sizeof(double));
         }
         ws.node_energies = static_cast<double*>(d_node_energies.ensure(n * sizeof(double)));
@@ -930,6 +987,7 @@ struct Evaluator {
         prepare_pair_tables();
         choose_plan();
         build_tiles();
+        if (hm.field && feature_graph()) build_feature_tile();
         ensure_workspace();
         SMX_HIP(hipStreamSynchronize(stream));
         evaluated = false;
@@ -1102,8 +1160,6 @@ struct Evaluator {
         }
         bool identity = true;
         for (int q = 0; q < nf && identity; ++q) identity = feature_of[q] == q;
-        if (hm.field && (nf != nr || !identity))
-            throw std::invalid_argument("field-coupled (MACEField) models take graphs without ghost feature nodes");
         h_feature_types.resize(nf);
         for (int q = 0; q < nf; ++q) h_feature_types[q] = feature_types[feature_of[q]];
         if (identity)
@@ -1148,8 +1204,6 @@ struct Evaluator {
         check_generation(token);
         if (nr != N || nf != F)
             throw std::invalid_argument("Distributed factorized graph or geometry extents are inconsistent.");
-        if (hm.field)
-            throw std::invalid_argument("the split-phase evaluation does not take field-coupled (MACEField) models");
     }
 
     // a one-interaction model needs no exchanged features: one call over the
@@ -1172,12 +1226,17 @@ struct Evaluator {
                 "a one-interaction model is evaluated in one call (compute_factorized_single_layer_distributed_evaluation)");
         evaluated = false;
         take_xyz(xyz, r, on_device);
+        bind_field();
         TileView& t = tiles[0];
         t.r = tile_r(t);
         t.xyz = tile_xyz(t);
         zero_a1_if_needed();
         tile_geometry(t, nullptr);
+        // a field-coupled model exchanges H1 before the field (H1p = M0 P + b):
+        // the field and linear_up then run over every feature node
+        ws.field_product_only = hm.field;
         ks->layer1_forward(dm, view(), t, ws, true, stream, timer.get());
+        ws.field_product_only = false;
         sync();
         phase = Phase::prefix_complete;
     }
@@ -1191,19 +1250,24 @@ struct Evaluator {
         if (!h1 || rows < F) throw std::invalid_argument("Communicated H1 does not match the distributed graph.");
         const std::size_t row = static_cast<std::size_t>(hm.num_LM) * hm.C;
         const bool permuted = !h_feature_of.empty();
-        float* dst = permuted ? d_h1_exchange.as<float>() : ws.H1;
+        float* rows_in = hm.field ? ws.H1p : ws.H1;  // the exchanged H1 rows
+        float* dst = permuted ? d_h1_exchange.as<float>() : rows_in;
         try {
             if (F > 0)
                 SMX_HIP(hipMemcpyAsync(dst, h1, F * row * sizeof(float),
                                        on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, stream));
             if (permuted)
-                launch_gather_rows(F, static_cast<int>(row), d_feature_of.as<int>(), dst, ws.H1, stream);
+                launch_gather_rows(F, static_cast<int>(row), d_feature_of.as<int>(), dst, rows_in, stream);
             const DeviceGraph g = view();
             const TileView& t = tiles[0];
+            if (hm.field) ks->field_features(dm, feature_tile, ws, stream, timer.get());
             ks->layer2(dm, g, t, ws, stream, timer.get());
             ks->source_adjoint_all(g, ws, tile_r(t), hm.r_cut, stream, timer.get());
+            // a field-coupled model's exchanged adjoint is H1p's (the
+            // readout's direct adjoint enters the receivers' rows here)
+            if (hm.field) ks->field_features_reverse(dm, feature_tile, ws, N, stream, timer.get());
             if (permuted)
-                launch_scatter_rows(F, static_cast<int>(row), d_feature_of.as<int>(), ws.H1_adj,
+                launch_scatter_rows(F, static_cast<int>(row), d_feature_of.as<int>(), hm.field ? ws.H1p_adj : ws.H1_adj,
                                     d_h1_exchange.as<float>(), stream);
             sync();
         } catch (...) {
@@ -1215,7 +1279,8 @@ struct Evaluator {
 
     // the H1 adjoint the caller exchanges (caller order, F rows)
     float* h1_adjoint_exchange() {
-        return h_feature_of.empty() ? ws.H1_adj : d_h1_exchange.as<float>();
+        if (!h_feature_of.empty()) return d_h1_exchange.as<float>();
+        return hm.field ? ws.H1p_adj : ws.H1_adj;
     }
 
     // finish_factorized_distributed_evaluation: the receivers' H1 adjoint (the
@@ -1234,8 +1299,10 @@ struct Evaluator {
             }
             if (!h_feature_of.empty())
                 launch_gather_rows(N, static_cast<int>(row), d_feature_of.as<int>(), d_h1_exchange.as<float>(),
-                                   ws.H1_adj, stream);
+                                   hm.field ? ws.H1p_adj : ws.H1_adj, stream);
+            ws.field_reverse_done = hm.field;
             ks->layer1_reverse(dm, view(), tiles[0], ws, true, stream, timer.get());
+            ws.field_reverse_done = false;
             sync();
         } catch (...) {
             phase = Phase::idle;
@@ -1463,27 +1530,40 @@ struct Evaluator {
         if (count > 0 && count != 3 && count % 3 != 0)
             throw std::invalid_argument("MACEField electric_field must have shape (3,) or (num_nodes, 3).");
         h_efield.assign(field, field + count);
-        if (count > 0) upload(d_efield, h_efield, stream);
     }
 
     // the field's device pointers for this evaluation (mace.cpp:1151-1154)
     void bind_field() {
         field_evaluated = false;
         if (!hm.field) return;
-        if (h_efield.size() != 3 && h_efield.size() != 3 * static_cast<std::size_t>(N))
+        // one field per graph, or one per feature node (every node of a
+        // graph without ghosts), in the caller's node order
+        if (h_efield.size() != 3 && h_efield.size() != 3 * static_cast<std::size_t>(F))
             throw std::invalid_argument(h_efield.empty()
                                             ? "a MACEField model is evaluated with an electric field (shape (3,) or "
                                               "(num_nodes, 3))"
                                             : "MACEField electric_field must have shape (3,) or (num_nodes, 3).");
-        ws.efield = d_efield.as<double>();
         ws.efield_per_node = h_efield.size() != 3;
+        if (ws.efield_per_node && !h_feature_of.empty()) {
+            // per-node values in the evaluator's node order
+            std::vector<double> mine(h_efield.size());
+            for (int k = 0; k < F; ++k)
+                for (int c = 0; c < 3; ++c) mine[3 * k + c] = h_efield[3 * static_cast<std::size_t>(h_feature_of[k]) + c];
+            upload(d_efield, mine, stream);
+        } else if (!h_efield.empty()) {
+            upload(d_efield, h_efield, stream);
+        }
+        ws.efield = d_efield.as<double>();
         ws.field_adj = ws.efield_per_node ? ws.field_part : d_field_adj.as<double>();
         if (N == 0) launch_fill_zero(ws.field_adj, 3, stream);
+        // ghosts' rows of a one-call evaluation take no field term
+        if (ws.efield_per_node && F > N) launch_fill_zero(ws.field_part, static_cast<std::size_t>(F) * 3, stream);
         field_evaluated = true;
     }
 
     void evaluate(const double* positions) {
         const DeviceGraph g = view();
+        ws.field_product_only = ws.field_reverse_done = false;
         bind_field();
         for (auto& t : tiles) {
             t.r = tile_r(t);
@@ -2328,7 +2408,7 @@ int32_t smx_distributed_exchange(SmxEvaluator* ev, int32_t which, float** device
         if (which == 0) {
             if (e.phase != smx::Evaluator::Phase::prefix_complete)
                 throw std::logic_error("the receivers' H1 is available after the prefix phase");
-            if (device_rows) *device_rows = e.ws.H1;
+            if (device_rows) *device_rows = e.hm.field ? e.ws.H1p : e.ws.H1;
             if (rows) *rows = e.N;
         } else if (which == 1) {
             if (e.phase != smx::Evaluator::Phase::middle_complete)
@@ -2410,6 +2490,12 @@ int32_t smx_electric_field_adj(SmxEvaluator* ev, double* out, int64_t capacity, 
         if (capacity < n) throw std::invalid_argument("buffer too small");
         SMX_HIP(hipMemcpyAsync(out, e.ws.field_adj, n * sizeof(double), hipMemcpyDeviceToHost, e.stream));
         SMX_HIP(hipStreamSynchronize(e.stream));
+        if (n != 3 && !e.h_feature_of.empty()) {
+            // per-node rows back in the caller's feature order
+            const std::vector<double> mine(out, out + n);
+            for (int k = 0; k < e.F; ++k)
+                for (int c = 0; c < 3; ++c) out[3 * static_cast<std::size_t>(e.h_feature_of[k]) + c] = mine[3 * k + c];
+        }
     });
 }
 

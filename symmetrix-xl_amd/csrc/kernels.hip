@@ -1070,7 +1070,10 @@ struct KernelSetImpl final : KernelSet {
             SMX_LAUNCH_CHECK("m0_forward");
         }
         if (m.field) {
-            field_forward(m, g, t, w, s, tm);
+            if (w.field_product_only)
+                field_product(m, g, t, w, s, tm);
+            else
+                field_forward(m, g, t, w, s, tm);
             return;
         }
         {
@@ -1097,12 +1100,25 @@ struct KernelSetImpl final : KernelSet {
     // MACEField H1 (mace.cpp:1845-1895, 1147-1186): H1p = M0 P (+ b),
     // Z = H1p[l_in rows] W per path, H1f = H1p + coef E Z (and x = H1f[:,0,:]),
     // H1 = H1f U
-    void field_forward(const DeviceModel& m, const DeviceGraph& g, const TileView& t, const Workspace& w,
+    void field_product(const DeviceModel& m, const DeviceGraph& g, const TileView& t, const Workspace& w,
                        hipStream_t s, LaunchTimer* tm) const {
-        TimerScope ts(tm, "h1_field", s);
+        TimerScope ts(tm, "h1_product", s);
         const std::size_t row0 = static_cast<std::size_t>(t.r0) * S::NH * C;
         launch_node_gemm(t.h1, m.P_w, w.M0, w.H1p + row0, s);
         if (m.residual) launch_type_bias(t.r0, t.nr, g.node_types, S::NH * C, m.res_pre, w.H1p + row0, s);
+    }
+
+    void field_forward(const DeviceModel& m, const DeviceGraph& g, const TileView& t, const Workspace& w,
+                       hipStream_t s, LaunchTimer* tm) const {
+        field_product(m, g, t, w, s, tm);
+        field_features(m, t, w, s, tm);
+    }
+
+    void field_features(const DeviceModel& m, const TileView& t, const Workspace& w, hipStream_t s,
+                        LaunchTimer* tm) const override {
+        if (t.nr == 0) return;
+        TimerScope ts(tm, "h1_field", s);
+        const std::size_t row0 = static_cast<std::size_t>(t.r0) * S::NH * C;
         launch_node_gemm(t.fz, m.field_W, w.H1p + row0, w.fzy + static_cast<std::size_t>(t.r0) * m.field_zr * C, s);
         k_field_combine<<<t.nr, C, 0, s>>>(t.r0, S::NH, C, m.field_zr, m.field_entries, m.num_field_entries, w.efield,
                                            w.efield_per_node, w.H1p, w.fzy, w.H1f, w.xaff);
@@ -1113,13 +1129,23 @@ struct KernelSetImpl final : KernelSet {
     // its reverse (mace.cpp:1897-1940, 1189-1240): H1p_adj = H1_adj U^T + x's
     // adjoint on lm 0, Y = H1p_adj[l_out rows] W^T, H1p_adj += coef E Y with
     // dE/dE, M0_adj = H1p_adj P^T
-    void field_reverse(const DeviceModel& m, const TileView& t, const Workspace& w, int N, hipStream_t s,
+    void field_reverse(const DeviceModel& m, const TileView& t, const Workspace& w, hipStream_t s,
                        LaunchTimer* tm) const {
+        field_features_reverse(m, t, w, t.nr, s, tm);
+        TimerScope ts(tm, "h1_product_reverse", s);
+        launch_node_gemm(t.h1, m.P_wt, w.H1p_adj + static_cast<std::size_t>(t.r0) * S::NH * C, w.M0_adj, s);
+    }
+
+    void field_features_reverse(const DeviceModel& m, const TileView& t, const Workspace& w, int direct_rows,
+                                hipStream_t s, LaunchTimer* tm) const override {
+        if (t.nr == 0) return;
         TimerScope ts(tm, "h1_field_reverse", s);
         const std::size_t row0 = static_cast<std::size_t>(t.r0) * S::NH * C;
         launch_node_gemm(t.h1, m.U_wt, w.H1_adj + row0, w.H1p_adj + row0, s);
-        k_field_direct_add<<<t.nr, C, 0, s>>>(t.r0, S::NH, C, w.direct, w.H1p_adj);
-        SMX_LAUNCH_CHECK("field_direct_add");
+        if (direct_rows > 0) {
+            k_field_direct_add<<<direct_rows, C, 0, s>>>(t.r0, S::NH, C, w.direct, w.H1p_adj);
+            SMX_LAUNCH_CHECK("field_direct_add");
+        }
         launch_node_gemm(t.fy, m.field_Wt, w.H1p_adj + row0, w.fzy + static_cast<std::size_t>(t.r0) * m.field_yr * C,
                          s);
         k_field_reverse_combine<C><<<t.nr, C, 0, s>>>(t.r0, S::NH, m.field_yr, m.field_entries, m.num_field_entries,
@@ -1127,10 +1153,9 @@ struct KernelSetImpl final : KernelSet {
                                                       w.field_part);
         SMX_LAUNCH_CHECK("field_reverse_combine");
         if (!w.efield_per_node) {
-            k_field_adj_sum<<<1, 256, 0, s>>>(N, w.field_part, w.field_adj);
+            k_field_adj_sum<<<1, 256, 0, s>>>(t.r0 + t.nr, w.field_part, w.field_adj);
             SMX_LAUNCH_CHECK("field_adj_sum");
         }
-        launch_node_gemm(t.h1, m.P_wt, w.H1p_adj + row0, w.M0_adj, s);
     }
 
     void layer2(const DeviceModel& m, const DeviceGraph& g, const TileView& t, const Workspace& w, hipStream_t s,
@@ -1242,8 +1267,12 @@ struct KernelSetImpl final : KernelSet {
         // as is (m0_composite) or as P0 d (pre_linear_up, mace.cpp:1785-1814);
         // with field coupling it entered H1p_adj[:,0,:] already
         const float* direct = w.direct;
-        if (m.field) {
-            field_reverse(m, t, w, g.N, s, tm);
+        if (m.field && w.field_reverse_done) {
+            TimerScope ts(tm, "h1_product_reverse", s);
+            launch_node_gemm(t.h1, m.P_wt, w.H1p_adj + static_cast<std::size_t>(t.r0) * S::NH * C, w.M0_adj, s);
+            direct = nullptr;
+        } else if (m.field) {
+            field_reverse(m, t, w, s, tm);
             direct = nullptr;
         } else {
             TimerScope ts(tm, "h1_linear_reverse", s);

@@ -214,6 +214,10 @@ struct Workspace {
     float* fzy = nullptr;       // [N][max(zr, yr)][C]
     double* field_part = nullptr;  // [N][3]
     double* field_adj = nullptr;   // [3] or [N][3]
+    // split-phase evaluation (feature graphs): layer 1 stops at H1p; the
+    // layer-1 reverse starts from H1p's adjoint (field paths already run)
+    bool field_product_only = false;
+    bool field_reverse_done = false;
 };
 
 // Timing hook: the evaluator brackets launches with events when enabled.
@@ -260,6 +264,13 @@ struct KernelSet {
     // to, or assigned to, the tile's buffer)
     virtual void layer1_reverse(const DeviceModel& m, const DeviceGraph& g, const TileView& t, const Workspace& w,
                                 bool accumulate_forces, hipStream_t s, LaunchTimer* tm) const = 0;
+    // MACEField, rows t.r0.. of t: H1 from H1p through the field paths and
+    // linear_up; and its reverse to H1p_adj, the direct adjoint entering the
+    // first direct_rows rows, dE/dE summed over the t.nr rows for one field
+    virtual void field_features(const DeviceModel& m, const TileView& t, const Workspace& w, hipStream_t s,
+                                LaunchTimer* tm) const = 0;
+    virtual void field_features_reverse(const DeviceModel& m, const TileView& t, const Workspace& w, int direct_rows,
+                                        hipStream_t s, LaunchTimer* tm) const = 0;
 };
 
 // Message returned by smx_last_error() on the calling thread.

@@ -72,6 +72,7 @@ class MACEKokkosFloat:
         self._num_nodes = 0
         self._num_feature_nodes = 0
         self._num_edges = 0
+        self._generation = 0
 
     def _head(self, index):
         name = ctypes.c_char_p()
@@ -138,6 +139,40 @@ class MACEKokkosFloat:
         check(lib.smx_evaluator_counters(self._h, ctypes.byref(c)))
         return c
 
+    # the prepared graph and the plan request (pybind mace_kokkos.cpp:448-449,
+    # 529-562, 897-949)
+    @property
+    def low_memory(self):
+        """the capacity profile is requested (set_low_memory(True) selects it)"""
+        return self.execution_plan_report["requested_profile"] == "capacity"
+
+    def _set_low_memory(self, enabled):
+        self._set_execution_plan_request("direct", "capacity" if enabled else "speed")
+
+    @property
+    def execution_active_receiver_count(self):
+        return self._num_nodes
+
+    @property
+    def execution_active_feature_node_count(self):
+        return self._num_feature_nodes
+
+    @property
+    def execution_active_edge_count(self):
+        return self._num_edges
+
+    @property
+    def factorized_graph_generation(self):
+        return self._generation
+
+    @property
+    def factorized_prepared_graph_count(self):
+        return int(self._counters().graph_prepare_count)
+
+    @property
+    def factorized_prepared_evaluation_count(self):
+        return int(self._counters().evaluation_count)
+
     @property
     def factorized_last_graph_prepare_ms(self):
         return self._counters().last_graph_prepare_ms
@@ -195,7 +230,8 @@ class MACEKokkosFloat:
                                                ctypes.byref(gen)))
         self._num_nodes = self._num_feature_nodes = int(num_nodes)
         self._num_edges = len(neigh_indices)
-        return int(gen.value)
+        self._generation = int(gen.value)
+        return self._generation
 
     # ------------------------------------ feature graphs and split phases
     def _prepare_factorized_feature_graph(self, num_receivers, num_feature_nodes, receiver_feature_indices,
@@ -219,7 +255,8 @@ class MACEKokkosFloat:
         self._num_nodes = int(num_receivers)
         self._num_feature_nodes = int(num_feature_nodes)
         self._num_edges = neigh_indices.size
-        return int(gen.value)
+        self._generation = int(gen.value)
+        return self._generation
 
     def _edge_vectors(self, xyz, r):
         xyz, r = f64(xyz), f64(r)
@@ -290,7 +327,8 @@ class MACEKokkosFloat:
                                                         ctypes.byref(gen), ctypes.byref(ne)))
         self._num_nodes = self._num_feature_nodes = node_types.size
         self._num_edges = int(ne.value)
-        return {"generation": int(gen.value), "num_edges": int(ne.value)}
+        self._generation = int(gen.value)
+        return {"generation": self._generation, "num_edges": int(ne.value)}
 
     def _geometry_arrays(self, positions, edges, cell, inverse_cell, pbc, edge_dtype):
         positions, cell, inverse_cell = f64(positions), f64(cell), f64(inverse_cell)

@@ -43,15 +43,18 @@ def _slabs(s, ref, parts, seed):
     return out
 
 
-def _run(path, s, ref, types, parts, seed=0):
+def _run(path, s, ref, types, parts, seed=0, field=None):
     """the slabs' split-phase evaluations with the host exchange; energies,
-    forces and stress summed over the slabs"""
+    forces and stress summed over the slabs (and dE/dE in a field: one field,
+    or one per atom given to each slab for its feature nodes)"""
     from symmetrix.mace_kokkos import MACEKokkosFloat
     n = len(types)
     slabs = _slabs(s, ref, parts, seed)
     evs = []
     for sl in slabs:
         ev = MACEKokkosFloat(path)
+        if field is not None:
+            ev._set_electric_field(field if np.size(field) == 3 else np.asarray(field)[sl["feats"]])
         sl["gen"] = ev._prepare_factorized_feature_graph(
             len(sl["recv"]), len(sl["feats"]), sl["rfi"], types[sl["recv"]], types[sl["feats"]], sl["num_neigh"],
             sl["neigh"], types[ref["graph"]["sources"][sl["edges"]]])
@@ -80,11 +83,18 @@ def _run(path, s, ref, types, parts, seed=0):
     e = np.zeros(n)
     f = np.zeros((n, 3))
     st = np.zeros((3, 3))
+    adj = None if field is None else np.zeros(np.shape(field))
     V = abs(np.linalg.det(np.asarray(s["cell"], float)))
     for ev, sl in zip(evs, slabs):
         e[sl["recv"]] = ev.node_energies
         np.add.at(f, sl["feats"], ev._reduce_atom_forces(len(sl["feats"]), None, None, sl["gen"]))
         st += ev._reduce_stress(V, None, sl["gen"])
+        if field is not None and np.size(field) == 3:
+            adj += ev.electric_field_adj
+        elif field is not None:
+            np.add.at(adj, sl["feats"], ev.electric_field_adj.reshape(-1, 3))
+    if field is not None:
+        return e, f, st, adj
     return e, f, st
 
 
@@ -113,6 +123,30 @@ def test_slabs_sum_to_the_whole_system(request, model, parts):
                                                      np.max(np.abs(f - fw))))
     np.testing.assert_allclose(e, whole.node_energies, rtol=0, atol=2e-5)
     np.testing.assert_allclose(f, fw, rtol=0, atol=2e-5)
+
+
+@pytest.mark.parametrize("model", ["tiny_field", "field_l2"])
+def test_slabs_in_an_electric_field(request, model):
+    """MACEField: H1 is exchanged before the field (H1p) and the field paths
+    run over every feature node; each slab's dE/dE is its part of the whole
+    (one field), or its feature nodes' parts (one field per atom)"""
+    from oracle import oracle
+    path = request.getfixturevalue(model + "_model_path")
+    s = _system("tiny")
+    om = oracle.OracleModel(path)
+    types = om.types_of(s["numbers"])
+    n = len(types)
+    field = np.array([0.12, -0.21, 0.27])
+    per = np.tile(field, (n, 1)) + 0.05 * np.random.default_rng(4).normal(size=(n, 3))
+    for fld in (field, per):
+        ref = oracle.evaluate_system(om, s, skin=0.5, field=fld)
+        e, f, st, adj = _run(path, s, ref, types, 3, seed=2, field=fld)
+        _assert_efs(ref, e, f, st, n)
+        np.testing.assert_allclose(e, ref["energies"], rtol=0, atol=1e-4)
+        scale = max(np.max(np.abs(ref["field_adj"])), 1e-30)
+        err = np.max(np.abs(adj.ravel() - ref["field_adj"])) / scale
+        print("dE/dE relative max err %.3e" % err)
+        assert err < 2e-5
 
 
 def test_a_slab_without_receivers(tiny_model_path):
@@ -144,7 +178,13 @@ def test_phase_order_and_refusals(tiny_model_path, tiny_single_model_path, tiny_
             sl["neigh"], types[ref["graph"]["sources"][sl["edges"]]])
     xyz, r = ref["xyz"].reshape(-1, 3)[sl["edges"]], ref["r"][sl["edges"]]
     ev = MACEKokkosFloat(tiny_model_path)
+    assert ev.low_memory
+    ev._set_low_memory(False)
+    assert not ev.low_memory
     gen = ev._prepare_factorized_feature_graph(*args)
+    assert ev.factorized_graph_generation == gen and ev.factorized_prepared_graph_count == 1
+    assert (ev.execution_active_receiver_count, ev.execution_active_feature_node_count,
+            ev.execution_active_edge_count) == (len(sl["recv"]), len(sl["feats"]), len(sl["edges"]))
     # a two-interaction model needs the exchange: no plain call over ghosts
     with pytest.raises(ValueError, match="split phases"):
         ev._compute_prepared_factorized(gen, xyz, r)
@@ -177,8 +217,11 @@ def test_phase_order_and_refusals(tiny_model_path, tiny_single_model_path, tiny_
     bad[6] = np.where(np.arange(len(sl["neigh"])) == 0, len(sl["feats"]), sl["neigh"]).astype(np.int32)
     with pytest.raises(ValueError, match="out of range"):
         MACEKokkosFloat(tiny_model_path)._prepare_factorized_feature_graph(*bad)
-    with pytest.raises(ValueError, match="MACEField"):
-        MACEKokkosFloat(tiny_field_model_path)._prepare_factorized_feature_graph(*args)
+    # a field-coupled model needs its field before the phases
+    fev = MACEKokkosFloat(tiny_field_model_path)
+    fgen = fev._prepare_factorized_feature_graph(*args)
+    with pytest.raises(ValueError, match="electric field"):
+        fev._begin_factorized_distributed_evaluation(fgen, xyz, r)
 
 
 def test_device_forms_as_the_pair_style_calls_them(tiny_model_path):
