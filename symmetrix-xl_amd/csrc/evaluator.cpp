@@ -257,7 +257,7 @@ struct Evaluator {
     // k's caller feature index (empty when the caller's order is this one).
     int F = 0;
     std::vector<int> h_feature_types, h_feature_of;
-    DevBuf d_feature_of, d_h1_exchange;
+    DevBuf d_feature_of, d_h1_exchange, d_forces_caller;
     // split-phase (distributed) evaluation: layer 1 -> H1 of the receivers;
     // H1 of every feature node in -> layer 2 and the H1 adjoint of every
     // feature node out; the receivers' summed H1 adjoint in -> layer-1 reverse
@@ -600,8 +600,6 @@ struct Evaluator {
             throw std::invalid_argument("mh0-dual-layer-tiled-v1 requires an ordinary two-layer MACE model");
         if (debug_plan == kPlanSingleTiled && two_layer())
             throw std::invalid_argument("mh0-single-layer-tiled-v1 requires single_layer_readout=true");
-        if (feature_graph() && (debug_plan == kPlanTiled || debug_plan == kPlanSingleTiled))
-            throw std::invalid_argument(debug_plan + " does not take graphs with ghost feature nodes");
         if (debug_plan == kPlanTiled || debug_plan == kPlanSingleTiled) {
             tiled = true;
             plan_source = "debug_plan";
@@ -628,10 +626,7 @@ struct Evaluator {
             tiled = false;
             plan_reason = "field coupling runs in the retained direct plan";
         }
-        if (feature_graph() && tiled) {
-            tiled = false;
-            plan_reason = "graphs with ghost feature nodes run in the retained direct plan";
-        }
+
         if (N <= tile_limit && debug_plan != tiled_plan() && tiled) {
             tiled = false;
             plan_reason = "the graph fits one receiver tile";
@@ -885,14 +880,14 @@ struct Evaluator {
         touched_begin.assign(1, 0);
         if (tiled && N > 0) {
             DevBuf bitmap, counts, one;
-            const int words = N / 32 + 1;
+            const int words = F / 32 + 1;
             bitmap.ensure(sizeof(std::uint32_t) * words);
             counts.ensure(sizeof(int) * words);
-            one.ensure(sizeof(int) * N);
+            one.ensure(sizeof(int) * F);
             std::vector<int> all;
-            std::vector<int> host(N);
+            std::vector<int> host(F);
             for (auto& t : tiles) {
-                const int cnt = build_touched_sources(N, t.e0, t.ne, d_neigh.as<int>(), bitmap.as<std::uint32_t>(),
+                const int cnt = build_touched_sources(F, t.e0, t.ne, d_neigh.as<int>(), bitmap.as<std::uint32_t>(),
                                                       counts.as<int>(), one.as<int>(), stream);
                 if (cnt > 0)
                     SMX_HIP(hipMemcpy(host.data(), one.as<int>(), sizeof(int) * cnt, hipMemcpyDeviceToHost));
@@ -1227,10 +1222,18 @@ struct Evaluator {
         evaluated = false;
         take_xyz(xyz, r, on_device);
         bind_field();
-        TileView& t = tiles[0];
-        t.r = tile_r(t);
-        t.xyz = tile_xyz(t);
+        for (auto& t : tiles) {
+            t.r = tile_r(t);
+            t.xyz = tile_xyz(t);
+        }
         zero_a1_if_needed();
+        if (tiled) {
+            tiled_sweep_h1(nullptr);
+            sync();
+            phase = Phase::prefix_complete;
+            return;
+        }
+        TileView& t = tiles[0];
         tile_geometry(t, nullptr);
         // a field-coupled model exchanges H1 before the field (H1p = M0 P + b):
         // the field and linear_up then run over every feature node
@@ -1261,8 +1264,12 @@ struct Evaluator {
             const DeviceGraph g = view();
             const TileView& t = tiles[0];
             if (hm.field) ks->field_features(dm, feature_tile, ws, stream, timer.get());
-            ks->layer2(dm, g, t, ws, stream, timer.get());
-            ks->source_adjoint_all(g, ws, tile_r(t), hm.r_cut, stream, timer.get());
+            if (tiled) {
+                tiled_sweep_layer2(nullptr);
+            } else {
+                ks->layer2(dm, g, t, ws, stream, timer.get());
+                ks->source_adjoint_all(g, ws, tile_r(t), hm.r_cut, stream, timer.get());
+            }
             // a field-coupled model's exchanged adjoint is H1p's (the
             // readout's direct adjoint enters the receivers' rows here)
             if (hm.field) ks->field_features_reverse(dm, feature_tile, ws, N, stream, timer.get());
@@ -1300,9 +1307,13 @@ struct Evaluator {
             if (!h_feature_of.empty())
                 launch_gather_rows(N, static_cast<int>(row), d_feature_of.as<int>(), d_h1_exchange.as<float>(),
                                    hm.field ? ws.H1p_adj : ws.H1_adj, stream);
-            ws.field_reverse_done = hm.field;
-            ks->layer1_reverse(dm, view(), tiles[0], ws, true, stream, timer.get());
-            ws.field_reverse_done = false;
+            if (tiled) {
+                tiled_sweep_reverse(nullptr);
+            } else {
+                ws.field_reverse_done = hm.field;
+                ks->layer1_reverse(dm, view(), tiles[0], ws, true, stream, timer.get());
+                ws.field_reverse_done = false;
+            }
             sync();
         } catch (...) {
             phase = Phase::idle;
@@ -1589,7 +1600,7 @@ struct Evaluator {
         if (!two_layer()) {
             // one sweep: each tile's receivers need only their own H1 rows
             // (mace_kokkos_evaluate.cpp:614-752)
-            launch_fill_zero(d_atom_forces.as<double>(), static_cast<std::size_t>(N) * 3, stream);
+            launch_fill_zero(d_atom_forces.as<double>(), static_cast<std::size_t>(F) * 3, stream);
             launch_fill_zero(d_virial.as<double>(), 9, stream);
             // the invalid-edge count of every tile's edges first
             for (const auto& t : tiles) tile_geometry(t, positions, false);
@@ -1603,33 +1614,63 @@ struct Evaluator {
                 ks->layer1_reverse(dm, g, t, ws, true, stream, tm);
                 accumulate_tile_outputs(t);
             }
+            forces_to_caller_order();
             evaluated = true;
             return;
         }
         // three sweeps over receiver tiles (graph-wide H1, H1 adjoint between them)
-        launch_fill_zero(ws.H1_adj, static_cast<std::size_t>(N) * hm.num_LM * hm.C, stream);
-        launch_fill_zero(d_atom_forces.as<double>(), static_cast<std::size_t>(N) * 3, stream);
-        launch_fill_zero(d_virial.as<double>(), 9, stream);
-        for (const auto& t : tiles) {
-            tile_geometry(t, positions);
-            ks->layer1_forward(dm, g, t, ws, true, stream, tm);
-        }
+        tiled_sweep_h1(positions);
         post_geometry_flag();
         // LAMMPS rows receive tile forces from the next sweep on: raise first
         if (lmp) raise_if_invalid_geometry("LAMMPS positions");
-        for (const auto& t : tiles) {
-            tile_geometry(t, positions);
-            ks->layer2(dm, g, t, ws, stream, tm);
-            ks->source_adjoint_tile(g, t, ws, tile_r(t), hm.r_cut, stream, tm);
-            accumulate_tile_outputs(t);
-        }
-        for (const auto& t : tiles) {
-            tile_geometry(t, positions);
-            ks->layer1_forward(dm, g, t, ws, false, stream, tm);
-            ks->layer1_reverse(dm, g, t, ws, false, stream, tm);
-            accumulate_tile_outputs(t);
-        }
+        tiled_sweep_layer2(positions);
+        tiled_sweep_reverse(positions);
         evaluated = true;
+    }
+
+    // the tiled plan's sweeps: layer 1 to H1; layer 2 with the source
+    // adjoint accumulated over the tiles; the layer-1 reverse (forces and
+    // virial accumulated as each tile finishes)
+    void tiled_sweep_h1(const double* positions) {
+        const DeviceGraph g = view();
+        for (const auto& t : tiles) {
+            tile_geometry(t, positions);
+            ks->layer1_forward(dm, g, t, ws, true, stream, timer.get());
+        }
+    }
+
+    void tiled_sweep_layer2(const double* positions) {
+        const DeviceGraph g = view();
+        launch_fill_zero(ws.H1_adj, static_cast<std::size_t>(F) * hm.num_LM * hm.C, stream);
+        launch_fill_zero(d_atom_forces.as<double>(), static_cast<std::size_t>(F) * 3, stream);
+        launch_fill_zero(d_virial.as<double>(), 9, stream);
+        for (const auto& t : tiles) {
+            tile_geometry(t, positions);
+            ks->layer2(dm, g, t, ws, stream, timer.get());
+            ks->source_adjoint_tile(g, t, ws, tile_r(t), hm.r_cut, stream, timer.get());
+            accumulate_tile_outputs(t);
+        }
+    }
+
+    void tiled_sweep_reverse(const double* positions) {
+        const DeviceGraph g = view();
+        for (const auto& t : tiles) {
+            tile_geometry(t, positions);
+            ks->layer1_forward(dm, g, t, ws, false, stream, timer.get());
+            ks->layer1_reverse(dm, g, t, ws, false, stream, timer.get());
+            accumulate_tile_outputs(t);
+        }
+        forces_to_caller_order();
+    }
+
+    // tiles accumulate the feature nodes' forces in the evaluator's order;
+    // a feature graph's caller reads them in its own
+    void forces_to_caller_order() {
+        if (h_feature_of.empty() || F == 0) return;
+        double* tmp = static_cast<double*>(d_forces_caller.ensure(static_cast<std::size_t>(F) * 3 * sizeof(double)));
+        launch_scatter_rows(F, 3, d_feature_of.as<int>(), d_atom_forces.as<double>(), tmp, stream);
+        SMX_HIP(hipMemcpyAsync(d_atom_forces.as<double>(), tmp, static_cast<std::size_t>(F) * 3 * sizeof(double),
+                               hipMemcpyDeviceToDevice, stream));
     }
 
     void accumulate_tile_outputs(const TileView& t) {

@@ -1478,9 +1478,9 @@ void launch_atom_forces(int N, int F, const int* offsets, const int* soff, const
     SMX_LAUNCH_CHECK("atom_forces");
 }
 
-template <bool kScatter>
+template <class T, bool kScatter>
 __global__ __launch_bounds__(256) void k_move_rows(int row_floats, const int* __restrict__ index,
-                                                   const float* __restrict__ src, float* __restrict__ dst) {
+                                                   const T* __restrict__ src, T* __restrict__ dst) {
     const std::size_t k = blockIdx.x;
     const std::size_t from = kScatter ? k : static_cast<std::size_t>(index[k]);
     const std::size_t to = kScatter ? static_cast<std::size_t>(index[k]) : k;
@@ -1489,14 +1489,21 @@ __global__ __launch_bounds__(256) void k_move_rows(int row_floats, const int* __
 
 void launch_gather_rows(int count, int row_floats, const int* index, const float* src, float* dst, hipStream_t s) {
     if (count == 0) return;
-    k_move_rows<false><<<count, 256, 0, s>>>(row_floats, index, src, dst);
+    k_move_rows<float, false><<<count, 256, 0, s>>>(row_floats, index, src, dst);
     SMX_LAUNCH_CHECK("gather_rows");
 }
 
 void launch_scatter_rows(int count, int row_floats, const int* index, const float* src, float* dst, hipStream_t s) {
     if (count == 0) return;
-    k_move_rows<true><<<count, 256, 0, s>>>(row_floats, index, src, dst);
+    k_move_rows<float, true><<<count, 256, 0, s>>>(row_floats, index, src, dst);
     SMX_LAUNCH_CHECK("scatter_rows");
+}
+
+void launch_scatter_rows(int count, int row_values, const int* index, const double* src, double* dst,
+                         hipStream_t s) {
+    if (count == 0) return;
+    k_move_rows<double, true><<<count, 256, 0, s>>>(row_values, index, src, dst);
+    SMX_LAUNCH_CHECK("scatter_rows_f64");
 }
 
 void launch_stress(std::int64_t E, const double* node_forces, const double* xyz, double volume, double* partial,

@@ -326,6 +326,8 @@ void launch_atom_forces(int N, int F, const int* offsets, const int* soff, const
 // dst[index[k]] = src[k] (scatter), k < count
 void launch_gather_rows(int count, int row_floats, const int* index, const float* src, float* dst, hipStream_t s);
 void launch_scatter_rows(int count, int row_floats, const int* index, const float* src, float* dst, hipStream_t s);
+void launch_scatter_rows(int count, int row_values, const int* index, const double* src, double* dst,
+                         hipStream_t s);
 // edges with a non-finite or non-positive length or a non-finite vector
 void launch_count_invalid_edges(std::int64_t E, const double* xyz, const double* r, int* invalid, hipStream_t s);
 void launch_stress(std::int64_t E, const double* node_forces, const double* xyz, double volume, double* partial,

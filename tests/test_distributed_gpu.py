@@ -43,7 +43,7 @@ def _slabs(s, ref, parts, seed):
     return out
 
 
-def _run(path, s, ref, types, parts, seed=0, field=None):
+def _run(path, s, ref, types, parts, seed=0, field=None, tile=0):
     """the slabs' split-phase evaluations with the host exchange; energies,
     forces and stress summed over the slabs (and dE/dE in a field: one field,
     or one per atom given to each slab for its feature nodes)"""
@@ -53,11 +53,15 @@ def _run(path, s, ref, types, parts, seed=0, field=None):
     evs = []
     for sl in slabs:
         ev = MACEKokkosFloat(path)
+        if tile:
+            ev.set_execution_plan_request("capacity", tile)
         if field is not None:
             ev._set_electric_field(field if np.size(field) == 3 else np.asarray(field)[sl["feats"]])
         sl["gen"] = ev._prepare_factorized_feature_graph(
             len(sl["recv"]), len(sl["feats"]), sl["rfi"], types[sl["recv"]], types[sl["feats"]], sl["num_neigh"],
             sl["neigh"], types[ref["graph"]["sources"][sl["edges"]]])
+        if tile:
+            assert ev.execution_plan_report["selected_id"].endswith("tiled-v1")
         sl["xyz"] = ref["xyz"].reshape(-1, 3)[sl["edges"]]
         sl["r"] = ref["r"][sl["edges"]]
         evs.append(ev)
@@ -100,8 +104,10 @@ def _run(path, s, ref, types, parts, seed=0, field=None):
 
 @pytest.mark.parametrize("model", ["tiny", "tiny_residual", "tiny_agnesi", "tiny_scaled", "tiny_zbl",
                                    "tiny_single"])
-@pytest.mark.parametrize("parts", [2, 3])
-def test_slabs_sum_to_the_whole_system(request, model, parts):
+@pytest.mark.parametrize("parts,tile", [(2, 0), (3, 0), (2, 16)])
+def test_slabs_sum_to_the_whole_system(request, model, parts, tile):
+    """tile > 0: each slab under its tiled plan, tiles of at most that many
+    receivers (the sweeps split at the same exchanges)"""
     from oracle import oracle
     from symmetrix.mace_kokkos import MACEKokkosFloat
     path = request.getfixturevalue(model + "_model_path")
@@ -110,7 +116,7 @@ def test_slabs_sum_to_the_whole_system(request, model, parts):
     ref = oracle.evaluate_system(om, s, skin=0.5)
     types = om.types_of(s["numbers"])
     n = len(types)
-    e, f, st = _run(path, s, ref, types, parts)
+    e, f, st = _run(path, s, ref, types, parts, tile=tile)
     _assert_efs(ref, e, f, st, n)
     np.testing.assert_allclose(e, ref["energies"], rtol=0, atol=1e-4)
     # the whole system on one evaluator, same graph and edge vectors
