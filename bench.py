@@ -311,6 +311,8 @@ def main():
     if not args.no_lammps:
         out["lammps_step"] = lammps_step_protocol(hip, model_path, system, skin)
         note("lammps step: %s" % out["lammps_step"])
+        out["split_phases"] = split_phase_protocol(hip, model_path, system, skin)
+        note("split phases: %s" % out["split_phases"])
     if not args.no_configs:
         out["configs"] = {}
         for name in ("wide", "irregular", "single"):
@@ -541,6 +543,88 @@ def lammps_step_protocol(hip, model_path, system, skin):
     for p in (a.ilist, a.numneigh, a.neighbors, a.x, a.type, a.type_to_model, a.owner, a.f):
         hip.hipFree(ctypes.c_void_p(p))
     ev.close()
+    return out
+
+
+def split_phase_protocol(hip, model_path, system, skin, parts=2):
+    """One rank's share of the medium system cut into `parts` slabs along x
+    (the split-phase evaluation a domain-decomposed LAMMPS run makes per
+    step): each slab's begin, continue and finish with device edge vectors
+    and device exchange rows (3 warm-ups, median of 10).  The inter-rank
+    copies themselves are the caller's (MPI/RCCL) and not timed; the rows
+    handed to continue are the slab's from a first full exchange."""
+    from symmetrix._native import check, lib
+    from symmetrix.mace_kokkos import MACEKokkosFloat, neighbor_list
+    probe = MACEKokkosFloat(model_path)
+    lut = {int(z): i for i, z in enumerate(probe.atomic_numbers)}
+    r_cut = probe.r_cut
+    probe.close()
+    pos = np.asarray(system["positions"], float)
+    cell = np.asarray(system["cell"], float)
+    g = neighbor_list(pos, cell, r_cut + skin)
+    types = np.array([lut[int(z)] for z in system["numbers"]], np.int32)
+    xyz_all = g["fractional_xyz"] @ cell
+    d = np.linalg.norm(xyz_all, axis=1)
+    scale = np.where(d >= r_cut, r_cut / d, 1.0)
+    xyz_all, r_all = xyz_all * scale[:, None], d * scale
+    frac = (pos @ np.linalg.inv(cell))[:, 0] % 1.0
+    owner = np.minimum((frac * parts).astype(int), parts - 1)
+    off, src = g["offsets"], g["sources"]
+    n = len(types)
+    slabs, held = [], []
+
+    def dev(a):
+        p = device_copy_of(hip, np.ascontiguousarray(a))
+        held.append(p)
+        return p
+    for dd in range(parts):
+        recv = np.flatnonzero(owner == dd)
+        edges = np.concatenate([np.arange(off[i], off[i + 1]) for i in recv])
+        feats = np.concatenate([recv, np.setdiff1d(np.unique(src[edges]), recv)])
+        index = np.full(n, -1, np.int64)
+        index[feats] = np.arange(len(feats))
+        ev = MACEKokkosFloat(model_path)
+        gen = ev._prepare_factorized_feature_graph(len(recv), len(feats), index[recv], types[recv], types[feats],
+                                                   (off[recv + 1] - off[recv]).astype(np.int32),
+                                                   index[src[edges]].astype(np.int32), types[src[edges]])
+        slabs.append(dict(ev=ev, gen=gen, recv=recv, feats=feats, E=len(edges),
+                          xyz=dev(xyz_all[edges]), r=dev(r_all[edges])))
+    # one full exchange on the host gives every slab its feature rows
+    for sl in slabs:
+        check(lib.smx_begin_factorized_distributed_evaluation(sl["ev"]._h, sl["gen"], len(sl["recv"]),
+                                                              len(sl["feats"]), sl["xyz"], sl["r"], 1))
+    H1 = None
+    for sl in slabs:
+        h = sl["ev"]._distributed_h1()
+        H1 = np.zeros((n, h.shape[1]), np.float32) if H1 is None else H1
+        H1[sl["recv"]] = h
+    for sl in slabs:
+        sl["rows"] = dev(H1[sl["feats"]])
+        check(lib.smx_continue_factorized_distributed_evaluation(sl["ev"]._h, sl["rows"], len(sl["feats"]), 1))
+        check(lib.smx_finish_factorized_distributed_evaluation(sl["ev"]._h, None, 0, 1))
+    sl = slabs[0]
+    h = sl["ev"]._h
+
+    def step():
+        check(lib.smx_begin_factorized_distributed_evaluation(h, sl["gen"], len(sl["recv"]), len(sl["feats"]),
+                                                              sl["xyz"], sl["r"], 1))
+        check(lib.smx_continue_factorized_distributed_evaluation(h, sl["rows"], len(sl["feats"]), 1))
+        check(lib.smx_finish_factorized_distributed_evaluation(h, None, 0, 1))
+    for _ in range(3):
+        step()
+    times = []
+    for _ in range(10):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    out = {"slabs": parts, "receivers": int(len(sl["recv"])), "feature_nodes": int(len(sl["feats"])),
+           "edges": int(sl["E"]), "ms_per_step": round(statistics.median(times) * 1e3, 4),
+           "us_per_receiver": round(statistics.median(times) * 1e6 / len(sl["recv"]), 4),
+           "note": "begin + continue + finish of one slab; the inter-rank row copies are not timed"}
+    for s_ in slabs:
+        s_["ev"].close()
+    for p in held:
+        hip.hipFree(p)
     return out
 
 
