@@ -420,6 +420,16 @@ class MACEKokkosFloat:
         check(lib.smx_compute_prepared_factorized_positions_device(self._h, int(execution_graph_generation),
                                                                    ctypes.c_void_p(positions_device_ptr)))
 
+    def compute_node_energies_forces_field(self, num_nodes, node_types, num_neigh, neigh_indices, neigh_types, xyz,
+                                           r, electric_field):
+        """compute_node_energies_forces of a MACEField model in an electric
+        field (3 values, or 3 per node; pybind mace_kokkos.cpp:2205-2225);
+        the field stays set for later calls, dE/dE is electric_field_adj."""
+        if not self.has_field_coupling:
+            raise ValueError("the model has no field coupling; it takes no electric_field")
+        self._set_electric_field(electric_field)
+        self.compute_node_energies_forces(num_nodes, node_types, num_neigh, neigh_indices, neigh_types, xyz, r)
+
     def compute_node_energies_forces(self, num_nodes, node_types, num_neigh, neigh_indices, neigh_types, xyz, r,
                                      execution_graph_generation=0):
         if execution_graph_generation:

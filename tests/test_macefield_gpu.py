@@ -113,3 +113,26 @@ def test_calculator_polarization_in_a_field(tiny_field_model_path):
     assert abs(zero["energy"] - z_ref["energy"]) / n < 1e-5
     with pytest.raises(ValueError, match="per-atom"):
         Symmetrix(tiny_field_model_path, electric_field=np.zeros((n, 3))).calculate(dict(s))
+
+
+def test_unprepared_call_in_a_field(tiny_field_model_path, tiny_model_path):
+    """compute_node_energies_forces_field (pybind mace_kokkos.cpp:2205-2225):
+    the host-graph call of a MACEField model, against the oracle."""
+    from oracle import oracle
+    from symmetrix.mace_kokkos import MACEKokkosFloat
+    s = _system("tiny")
+    om = oracle.OracleModel(tiny_field_model_path)
+    ref = oracle.evaluate_system(om, s, skin=0.5, field=FIELD)
+    types = om.types_of(s["numbers"])
+    g = ref["graph"]
+    n = len(types)
+    ev = MACEKokkosFloat(tiny_field_model_path)
+    ev.compute_node_energies_forces_field(n, types, g["num_neigh"], g["sources"], types[g["sources"]], ref["xyz"],
+                                          ref["r"], FIELD)
+    np.testing.assert_allclose(ev.node_energies, ref["energies"], rtol=0, atol=1e-4)
+    scale = np.max(np.abs(ref["field_adj"]))
+    np.testing.assert_allclose(ev.electric_field_adj, ref["field_adj"], rtol=0, atol=2e-5 * scale)
+    plain = MACEKokkosFloat(tiny_model_path)
+    with pytest.raises(ValueError, match="no field coupling"):
+        plain.compute_node_energies_forces_field(n, types, g["num_neigh"], g["sources"], types[g["sources"]],
+                                                 ref["xyz"], ref["r"], FIELD)
