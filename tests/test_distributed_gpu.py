@@ -314,3 +314,62 @@ def test_device_forms_as_the_pair_style_calls_them(tiny_model_path):
     finally:
         for p in held:
             hip.hipFree(p)
+
+
+@pytest.mark.parametrize("model", ["tiny", "tiny_field"])
+def test_one_rank_with_ghost_images_as_the_pair_style_runs_it(request, model):
+    """The pair style's mpi_message_passing compute on one rank: local atoms
+    (in a shuffled ilist order) are the receivers, the local atoms and their
+    26 ghost images are the feature nodes by LAMMPS index, the forward
+    communication copies each ghost's H1 row from its owner, the reverse
+    communication adds each ghost's adjoint row onto its owner, and the ghost
+    rows of the forces are folded onto their owners (LAMMPS's reverse
+    communication of f)."""
+    from oracle import oracle
+    from symmetrix.mace_kokkos import MACEKokkosFloat
+    from test_lammps_entry import _lammps_arrays
+    path = request.getfixturevalue(model + "_model_path")
+    s = _system("tiny")
+    om = oracle.OracleModel(path)
+    field = np.array([0.12, -0.21, 0.27]) if model == "tiny_field" else None
+    ref = oracle.evaluate_system(om, s, skin=0.5, field=field)
+    ev = MACEKokkosFloat(path)
+    lut = {int(z): i for i, z in enumerate(ev.atomic_numbers)}
+    species = sorted(set(int(z) for z in s["numbers"]))
+    allpos, owner, alltypes, rows = _lammps_arrays(np.asarray(s["positions"], float), np.asarray(s["cell"], float),
+                                                   s["numbers"], ev.r_cut + 0.5,
+                                                   {z: t + 1 for t, z in enumerate(species)})
+    n, nall = len(rows), len(allpos)
+    model_type = np.array([lut[species[t - 1]] for t in alltypes], np.int32)
+    ilist = np.random.default_rng(5).permutation(n).astype(np.int32)
+    neigh = np.concatenate([rows[i] for i in ilist]).astype(np.int32)
+    recv = np.repeat(ilist, [len(rows[i]) for i in ilist])
+    xyz = allpos[neigh] - allpos[recv]
+    d = np.linalg.norm(xyz, axis=1)
+    sc = np.where(d >= ev.r_cut, ev.r_cut / d, 1.0)
+    xyz, r = xyz * sc[:, None], d * sc
+    if field is not None:
+        ev._set_electric_field(field)
+    gen = ev._prepare_factorized_feature_graph(n, nall, ilist, model_type[ilist], model_type,
+                                               np.array([len(rows[i]) for i in ilist], np.int32), neigh,
+                                               model_type[neigh])
+    ev._begin_factorized_distributed_evaluation(gen, xyz, r)
+    h = ev._distributed_h1()
+    H1 = np.zeros((nall, h.shape[1]), np.float32)
+    H1[ilist] = h
+    H1[n:] = H1[owner[n:]]                      # forward communication
+    ev._continue_factorized_distributed_evaluation(H1)
+    adj = ev._distributed_h1_adjoint().astype(np.float64)
+    np.add.at(adj, owner[n:], adj[n:])          # reverse communication
+    ev._finish_factorized_distributed_evaluation(adj.astype(np.float32))
+    e = np.zeros(n)
+    e[ilist] = ev.node_energies
+    f_all = ev._reduce_atom_forces(nall, None, None, gen)
+    f = np.zeros((n, 3))
+    np.add.at(f, owner, f_all)                  # ghost forces onto owners
+    st = ev._reduce_stress(abs(np.linalg.det(np.asarray(s["cell"], float))), None, gen)
+    _assert_efs(ref, e, f, st, n)
+    np.testing.assert_allclose(e, ref["energies"], rtol=0, atol=1e-4)
+    if field is not None:
+        scale = np.max(np.abs(ref["field_adj"]))
+        np.testing.assert_allclose(ev.electric_field_adj, ref["field_adj"], rtol=0, atol=2e-5 * scale)
