@@ -300,7 +300,9 @@ SMX_API int32_t smx_finish_factorized_distributed_evaluation(SmxEvaluator* ev, c
  * begin; 1: feature nodes' H1 adjoint after continue): device pointer, row
  * count and FP32 values per row; the pair style's H1 / H1_adj views
  * (pair_symmetrix_mace_kokkos.cpp:1582-1600, 1690-1704).  With device_rows
- * and rows both NULL it reports row_floats alone, in any phase. */
+ * and rows both NULL it reports row_floats alone, in any phase.  The
+ * pointer is into the evaluator's workspace: valid until the next phase
+ * call, graph or evaluation on this evaluator. */
 SMX_API int32_t smx_distributed_exchange(SmxEvaluator* ev, int32_t which, float** device_rows, int64_t* rows,
                                          int64_t* row_floats);
 /* MACEField models (field_coupling.hpp; mace.cpp:322-395, 1147-1240).

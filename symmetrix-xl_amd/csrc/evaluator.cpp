@@ -1020,6 +1020,7 @@ struct Evaluator {
     // tabulate the per-pair radial tables of these model types now, and keep
     // them for every later graph whose types they cover.
     void prepare_active_types(std::vector<int> types) {
+        require_idle();  // the radial tables of a pending phase stay as they are
         for (int t : types)
             if (t < 0 || t >= hm.num_elements) throw std::invalid_argument("active type index is out of range");
         std::sort(types.begin(), types.end());
