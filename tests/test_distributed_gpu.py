@@ -373,3 +373,33 @@ def test_one_rank_with_ghost_images_as_the_pair_style_runs_it(request, model):
     if field is not None:
         scale = np.max(np.abs(ref["field_adj"]))
         np.testing.assert_allclose(ev.electric_field_adj, ref["field_adj"], rtol=0, atol=2e-5 * scale)
+
+
+def test_medium_slabs_sum_to_the_whole_system(medium_model_path):
+    """The benchmark workload (5,000 atoms, 496k edges) cut into two slabs:
+    the slabs' energies, forces and stress equal the one-evaluator call on
+    the same graph and edge vectors (size-independent check of the split
+    phases at full size)."""
+    from symmetrix.mace_kokkos import MACEKokkosFloat, neighbor_list
+    s = _system("medium")
+    whole = MACEKokkosFloat(medium_model_path)
+    lut = {int(z): i for i, z in enumerate(whole.atomic_numbers)}
+    types = np.array([lut[int(z)] for z in s["numbers"]], np.int32)
+    cell = np.asarray(s["cell"], float)
+    g = neighbor_list(np.asarray(s["positions"], float), cell, whole.r_cut + 0.5)
+    xyz = g["fractional_xyz"] @ cell
+    d = np.linalg.norm(xyz, axis=1)
+    sc = np.where(d >= whole.r_cut, whole.r_cut / d, 1.0)
+    ref = {"graph": g, "xyz": (xyz * sc[:, None]).ravel(), "r": d * sc}
+    n = len(types)
+    gen = whole._prepare_factorized_graph(n, types, g["num_neigh"], g["sources"], types[g["sources"]])
+    whole._compute_prepared_factorized(gen, ref["xyz"], ref["r"])
+    V = abs(np.linalg.det(cell))
+    ew, fw, sw = whole.node_energies, whole._reduce_atom_forces(n, None, None, gen), whole._reduce_stress(V, None, gen)
+    whole.close()
+    e, f, st = _run(medium_model_path, s, ref, types, 2)
+    print("medium slabs vs whole: energy %.3e force %.3e stress %.3e" % (
+        np.max(np.abs(e - ew)), np.max(np.abs(f - fw)), np.max(np.abs(st - sw))))
+    np.testing.assert_allclose(e, ew, rtol=0, atol=2e-5)
+    np.testing.assert_allclose(f, fw, rtol=0, atol=2e-5)
+    np.testing.assert_allclose(st, sw, rtol=0, atol=1e-8)
