@@ -471,6 +471,25 @@ struct SourceGroups<LMAX, 2> {
     static constexpr std::array<unsigned, 3> masks{0x00fu, 0x070u, 0x180u};
 };
 
+// Channel slices of the R1 forward over unstaged records: with C >= 128 each
+// 64-lane wave is a workgroup of its own holding one slice of a receiver's
+// channels, and the slices go to alternate XCDs (slice = XCD mod slices), so
+// an XCD reads only its slice of the spline table and of the H1 rows and its
+// 4 MB L2 holds that working set; the receivers are cut into contiguous
+// ranges, one per group of XCDs (ranges of nearby atoms share sources).
+template <int C, class EDGES>
+constexpr int r1_forward_slices() {
+    return (EDGES::kHold && C >= 128 && kXcds % (C / 64) == 0) ? C / 64 : 1;
+}
+// grid of the forward over nr receivers (padded to whole rounds of XCDs)
+template <int C, class EDGES>
+inline unsigned r1_forward_blocks(int nr) {
+    constexpr int SL = r1_forward_slices<C, EDGES>();
+    if constexpr (SL == 1) return static_cast<unsigned>(nr);
+    const int per_xcd = (nr * SL + kXcds - 1) / kXcds;  // receivers per range
+    return static_cast<unsigned>(per_xcd * kXcds);
+}
+
 // ---------------------------------------------------------------------------
 // R1 forward: rows[i,(p,m1,m2),k] = sum_j R1_{p,k}(r) Y_{lm1} H1[j,lm2,k];
 // Phi1[i,lme,k] = sum CG rows (dense per-path coupling blocks).  Each output
@@ -481,16 +500,27 @@ struct SourceGroups<LMAX, 2> {
 // rows are indexed by li.
 // ---------------------------------------------------------------------------
 template <int C, int LMAX, int LMAXH, unsigned MASK, bool ACCUMULATE, class EDGES>
-__global__ __launch_bounds__(C) void k_r1_forward(int r0, const int* __restrict__ first,
+__global__ __launch_bounds__(C) void k_r1_forward(int r0, int nr, const int* __restrict__ first,
                                                   const int* __restrict__ count, const int* __restrict__ neigh,
                                                   EDGES edges, const float* __restrict__ H1,
                                                   const float* __restrict__ cg, float* __restrict__ Phi1) {
     using S = Shape<LMAX, LMAXH>;
     using RG = RowGroup<LMAX, LMAXH, MASK>;
     constexpr int NH = S::NH;
-    const int li = xcd_remap(blockIdx.x, gridDim.x);
+    constexpr int SL = r1_forward_slices<C, EDGES>();
+    int li, k = threadIdx.x;
+    if constexpr (SL == 1) {
+        li = xcd_remap(blockIdx.x, gridDim.x);
+    } else {
+        // block b runs on XCD b mod 8: slice (b mod 8) mod SL of receiver
+        // (b mod 8) / SL * per_xcd + b / 8 (no barrier below: the padding
+        // blocks leave at once)
+        const int x = static_cast<int>(blockIdx.x) % kXcds, j = static_cast<int>(blockIdx.x) / kXcds;
+        li = (x / SL) * static_cast<int>(gridDim.x / kXcds) + j;
+        if (li >= nr) return;
+        k += (x % SL) * (C / SL);
+    }
     const int i = r0 + li;
-    const int k = threadIdx.x;
     float rows[RG::NR];
 #pragma unroll
     for (int r = 0; r < RG::NR; ++r) rows[r] = 0.0f;

@@ -1165,8 +1165,10 @@ struct KernelSetImpl final : KernelSet {
             TimerScope ts(tm, "r1_forward", s);
             static_for<0, kGroups>([&](auto gc) {
                 constexpr int gi = gc;
-                k_r1_forward<C, LMAX, LMAXH, Groups::masks[gi], (gi > 0), Records><<<t.nr, C, 0, s>>>(
-                    t.r0, g.offsets, nullptr, g.neigh, records(m, t, w), w.H1, m.cg, w.Phi1);
+                constexpr int SL = r1_forward_slices<C, Records>();
+                k_r1_forward<C, LMAX, LMAXH, Groups::masks[gi], (gi > 0), Records>
+                    <<<r1_forward_blocks<C, Records>(t.nr), C / SL, 0, s>>>(t.r0, t.nr, g.offsets, nullptr, g.neigh,
+                                                                           records(m, t, w), w.H1, m.cg, w.Phi1);
                 SMX_LAUNCH_CHECK("r1_forward");
             });
         }

@@ -179,7 +179,8 @@ int32_t forward_launch(const SymmetrixJitHipR1ForwardArgsV1* a, void* stream, in
     constexpr unsigned kAll = SourceGroups<LMAX, LMAXH>::masks[0];
     k_r1_forward<C, LMAX, LMAXH, kAll, false, PluginEdges<S::NY>><<<static_cast<unsigned>(a->num_nodes), C, 0,
                                                       static_cast<hipStream_t>(stream)>>>(
-        0, a->first_neigh, a->num_neigh, a->neigh_indices, edges, static_cast<const float*>(a->neighbor_features),
+        0, a->num_nodes, a->first_neigh, a->num_neigh, a->neigh_indices, edges,
+        static_cast<const float*>(a->neighbor_features),
         st->cg, static_cast<float*>(a->output));
     return static_cast<int32_t>(hipPeekAtLastError());
 }
