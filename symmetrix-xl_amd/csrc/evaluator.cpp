@@ -224,6 +224,7 @@ struct Evaluator {
     std::vector<double> h_efield;
     DevBuf d_efield, d_field_part, d_field_adj;
     bool field_evaluated = false;
+    std::int64_t field_adj_count = 0;  // values of the last evaluation's dE/dE
 
     // execution plan request (set_execution_plan_request, set_allow_fixed_workspace,
     // mace_kokkos.hpp:95-96; the calculator's execution_profile and
@@ -1570,6 +1571,7 @@ struct Evaluator {
         if (N == 0) launch_fill_zero(ws.field_adj, 3, stream);
         // ghosts' rows of a one-call evaluation take no field term
         if (ws.efield_per_node && F > N) launch_fill_zero(ws.field_part, static_cast<std::size_t>(F) * 3, stream);
+        field_adj_count = static_cast<std::int64_t>(h_efield.size());
         field_evaluated = true;
     }
 
@@ -2526,7 +2528,9 @@ int32_t smx_electric_field_adj(SmxEvaluator* ev, double* out, int64_t capacity, 
     return guarded([&] {
         auto& e = E(ev);
         if (!e.field_evaluated || !e.evaluated) throw std::logic_error("no field evaluation has run");
-        const std::int64_t n = static_cast<std::int64_t>(e.h_efield.size());
+        // the shape of the field that evaluation ran in (a field set since
+        // applies to the next one)
+        const std::int64_t n = e.field_adj_count;
         if (count) *count = n;
         if (!out) return;
         if (capacity < n) throw std::invalid_argument("buffer too small");

@@ -136,3 +136,23 @@ def test_unprepared_call_in_a_field(tiny_field_model_path, tiny_model_path):
     with pytest.raises(ValueError, match="no field coupling"):
         plain.compute_node_energies_forces_field(n, types, g["num_neigh"], g["sources"], types[g["sources"]],
                                                  ref["xyz"], ref["r"], FIELD)
+
+
+def test_field_adjoint_keeps_the_evaluated_shape(tiny_field_model_path):
+    """dE/dE is that of the last evaluation: a field of another shape set
+    afterwards applies to the next evaluation only."""
+    from symmetrix.mace_kokkos import MACEKokkosFloat
+    s = _system("tiny")
+    ev = MACEKokkosFloat(tiny_field_model_path)
+    lut = {int(z): i for i, z in enumerate(ev.atomic_numbers)}
+    types = np.array([lut[int(z)] for z in s["numbers"]], np.int32)
+    g = _prepare(ev, s, types)
+    ev._compute_prepared_factorized_positions_field(g["generation"], s["positions"], FIELD)
+    adj = ev.electric_field_adj
+    assert adj.shape == (3,)
+    n = len(types)
+    ev._set_electric_field(np.tile(FIELD, (n, 1)))
+    np.testing.assert_array_equal(ev.electric_field_adj, adj)
+    ev._compute_prepared_factorized_positions(g["generation"], s["positions"])
+    per = ev.electric_field_adj.reshape(n, 3)
+    np.testing.assert_allclose(per.sum(axis=0), adj, rtol=0, atol=1e-6 * np.max(np.abs(adj)))
