@@ -271,6 +271,21 @@ SMX_API int32_t smx_compute_factorized_single_layer_distributed_evaluation(SmxEv
                                                                            int32_t num_feature_nodes,
                                                                            const double* xyz, const double* r,
                                                                            int32_t on_device);
+/* The positions forms (mace_kokkos.hpp:678-682, 689-693;
+ * mace_kokkos_evaluate.cpp:1554-1656): instead of edge vectors, the
+ * positions of the feature nodes (3 per node, caller feature order, host or
+ * device); each edge vector is x[source] - x[receiver], scaled to r_cut when
+ * longer, as the pair style forms them, in whichever plan the graph runs.
+ * Only for graphs prepared with feature nodes (the ghosts are explicit
+ * atoms there, so no cell shift is needed). */
+SMX_API int32_t smx_begin_factorized_distributed_positions_evaluation(SmxEvaluator* ev, uint64_t generation,
+                                                                      int32_t num_receivers,
+                                                                      int32_t num_feature_nodes,
+                                                                      const double* feature_positions,
+                                                                      int32_t on_device);
+SMX_API int32_t smx_compute_factorized_single_layer_distributed_positions_evaluation(
+    SmxEvaluator* ev, uint64_t generation, int32_t num_receivers, int32_t num_feature_nodes,
+    const double* feature_positions, int32_t on_device);
 /* The split-phase evaluation of a two-interaction model
  * (mace_kokkos.hpp:672-697; mace_kokkos_evaluate.cpp:1658-1990):
  *  1. begin: layer 1 up to H1 of the receivers (smx_distributed_exchange

@@ -259,6 +259,12 @@ struct Evaluator {
     int F = 0;
     std::vector<int> h_feature_types, h_feature_of;
     DevBuf d_feature_of, d_h1_exchange, d_forces_caller;
+    // the positions form of a feature graph: each edge's source and each
+    // receiver as caller feature indices, and the feature nodes' positions
+    // (edge vectors x[source] - x[receiver], as the pair style forms them)
+    DevBuf d_edge_src_feature, d_recv_feature, d_fpos;
+    bool fpos_mode = false;
+    bool feature_prepared = false;  // the graph came through the feature-node prepare
     // split-phase (distributed) evaluation: layer 1 -> H1 of the receivers;
     // H1 of every feature node in -> layer 2 and the H1 adjoint of every
     // feature node out; the receivers' summed H1 adjoint in -> layer-1 reverse
@@ -1069,6 +1075,7 @@ struct Evaluator {
             num_features = n;
             h_feature_of.clear();
             h_feature_types.clear();
+            feature_prepared = false;
         }
         if (n < 0) throw std::invalid_argument("num_nodes must be non-negative");
         if (num_edges < 0 || num_edges > kMaxEdges)
@@ -1163,6 +1170,9 @@ struct Evaluator {
             h_feature_of.clear();
         else
             h_feature_of.swap(feature_of);
+        upload(d_edge_src_feature, std::vector<int>(neigh, neigh + num_edges), stream);
+        upload(d_recv_feature, std::vector<int>(receiver_features, receiver_features + nr), stream);
+        feature_prepared = true;
         if (nf == nr && identity) h_feature_types.clear();
         return prepare_graph_host(nr, node_types, num_neigh, num_edges, src.data(), neigh_types, nf);
     }
@@ -1171,6 +1181,7 @@ struct Evaluator {
     // edge vectors of the whole graph from the caller (host: checked here;
     // device: counted by a kernel and read back)
     void take_xyz(const double* xyz, const double* r, bool on_device) {
+        fpos_mode = false;
         if (E > 0 && (!xyz || !r)) throw std::invalid_argument("xyz and r are required");
         d_xyz.ensure(std::max<std::int64_t>(E, 1) * 3 * sizeof(double));
         d_r.ensure(std::max<std::int64_t>(E, 1) * sizeof(double));
@@ -1196,6 +1207,36 @@ struct Evaluator {
             throw std::invalid_argument("MACE graph has an invalid distance or displacement vector");
     }
 
+    // the positions form (begin_factorized_distributed_positions_evaluation,
+    // mace_kokkos_evaluate.cpp:1615-1656): 3 per feature node, host or device
+    void take_feature_positions(const double* pos, bool on_device) {
+        if (!feature_prepared)
+            throw std::invalid_argument("the positions form takes a graph prepared with feature nodes");
+        if (F > 0 && !pos) throw std::invalid_argument("feature positions are required");
+        if (!on_device)
+            for (std::int64_t q = 0; q < 3 * static_cast<std::int64_t>(F); ++q)
+                if (!std::isfinite(pos[q])) throw std::invalid_argument("positions must be finite");
+        double* dst = static_cast<double*>(d_fpos.ensure(std::max(F, 1) * 3 * sizeof(double)));
+        if (F > 0)
+            SMX_HIP(hipMemcpyAsync(dst, pos, static_cast<std::size_t>(F) * 3 * sizeof(double),
+                                   on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, stream));
+        // edge vectors of the whole graph (direct plan) or of one tile at a
+        // time (tiled plan), formed where the plan forms them
+        d_xyz.ensure(std::max<std::int64_t>(tiled ? max_tile_ne : E, 1) * 3 * sizeof(double));
+        d_r.ensure(std::max<std::int64_t>(tiled ? max_tile_ne : E, 1) * sizeof(double));
+        xyz_host = false;
+        fpos_mode = true;
+        launch_fill_zero(reinterpret_cast<float*>(d_invalid.as<int>()), 1, stream);
+    }
+
+    void raise_if_invalid_feature_geometry() {
+        if (read_flag(d_invalid) > 0) {
+            evaluated = false;
+            throw std::invalid_argument("feature positions produced an invalid edge geometry (zero-length or "
+                                        "non-finite edges)");
+        }
+    }
+
     void check_phase_graph(std::uint64_t token, int nr, int nf) const {
         if (phase != Phase::idle) throw std::logic_error("A factorized distributed evaluation is already active.");
         check_generation(token);
@@ -1206,23 +1247,30 @@ struct Evaluator {
     // a one-interaction model needs no exchanged features: one call over the
     // feature graph (mace_kokkos_evaluate.cpp:1495-1552)
     void single_layer_distributed(std::uint64_t token, int nr, int nf, const double* xyz, const double* r,
-                                  bool on_device) {
+                                  const double* feature_positions, bool on_device) {
         check_phase_graph(token, nr, nf);
         if (two_layer())
             throw std::invalid_argument("Complete distributed evaluation requires a standard single-layer model.");
-        take_xyz(xyz, r, on_device);
+        if (feature_positions)
+            take_feature_positions(feature_positions, on_device);
+        else
+            take_xyz(xyz, r, on_device);
         evaluate(nullptr);
         finish_call(true);
     }
 
     // begin_factorized_distributed_evaluation: layer 1 up to H1 of the receivers
-    void begin_distributed(std::uint64_t token, int nr, int nf, const double* xyz, const double* r, bool on_device) {
+    void begin_distributed(std::uint64_t token, int nr, int nf, const double* xyz, const double* r,
+                           const double* feature_positions, bool on_device) {
         check_phase_graph(token, nr, nf);
         if (!two_layer())
             throw std::invalid_argument(
                 "a one-interaction model is evaluated in one call (compute_factorized_single_layer_distributed_evaluation)");
         evaluated = false;
-        take_xyz(xyz, r, on_device);
+        if (feature_positions)
+            take_feature_positions(feature_positions, on_device);
+        else
+            take_xyz(xyz, r, on_device);
         bind_field();
         for (auto& t : tiles) {
             t.r = tile_r(t);
@@ -1232,6 +1280,7 @@ struct Evaluator {
         if (tiled) {
             tiled_sweep_h1(nullptr);
             sync();
+            if (fpos_mode) raise_if_invalid_feature_geometry();
             phase = Phase::prefix_complete;
             return;
         }
@@ -1243,6 +1292,7 @@ struct Evaluator {
         ks->layer1_forward(dm, view(), t, ws, true, stream, timer.get());
         ws.field_product_only = false;
         sync();
+        if (fpos_mode) raise_if_invalid_feature_geometry();
         phase = Phase::prefix_complete;
     }
 
@@ -1334,6 +1384,7 @@ struct Evaluator {
         N = F = n;
         h_feature_of.clear();
         h_feature_types.clear();
+        feature_prepared = false;
         E = num_edges;
         h_node_types.resize(n);
         if (n > 0) SMX_HIP(hipMemcpy(h_node_types.data(), node_types, sizeof(int) * n, hipMemcpyDeviceToHost));
@@ -1375,6 +1426,7 @@ struct Evaluator {
         N = F = n;
         h_feature_of.clear();
         h_feature_types.clear();
+        feature_prepared = false;
         E = nr.num_edges;
         h_node_types.assign(node_types, node_types + n);
         upload(d_node_types, h_node_types, stream);
@@ -1418,6 +1470,12 @@ struct Evaluator {
             if (tm) tm->begin("edge_geometry", stream);
             lammps_geometry(t.e0, t.ne, d_receivers.as<int>(), lmp->ilist, l_lmp_j.as<int>(), lmp->x, hm.r_cut,
                             d_xyz.as<double>(), d_r.as<double>(), d_invalid.as<int>(), stream);
+            if (tm) tm->end("edge_geometry", stream);
+        } else if (fpos_mode) {
+            if (tm) tm->begin("edge_geometry", stream);
+            lammps_geometry(t.e0, t.ne, d_receivers.as<int>(), d_recv_feature.as<int>(), d_edge_src_feature.as<int>(),
+                            d_fpos.as<double>(), hm.r_cut, d_xyz.as<double>(), d_r.as<double>(), d_invalid.as<int>(),
+                            stream);
             if (tm) tm->end("edge_geometry", stream);
         } else if (!xyz_host) {
             if (tm) tm->begin("edge_geometry", stream);
@@ -1746,6 +1804,7 @@ struct Evaluator {
     void compute_positions(std::uint64_t token, const double* positions, bool on_device) {
         check_generation(token);
         require_plain_call();
+        fpos_mode = false;
         if (geom == Geometry::none)
             throw std::invalid_argument("Execution R1 positions require current graph and geometry tokens: "
                                         "prepare a geometry (prepare_factorized_geometry or its fractional or "
@@ -1773,6 +1832,7 @@ struct Evaluator {
     void compute_xyz(std::uint64_t token, const double* xyz, const double* r) {
         check_generation(token);
         require_plain_call();
+        fpos_mode = false;
         for (std::int64_t e = 0; e < E; ++e) {
             if (!std::isfinite(r[e]) || !(r[e] > 0.0) || !std::isfinite(xyz[3 * e]) || !std::isfinite(xyz[3 * e + 1]) ||
                 !std::isfinite(xyz[3 * e + 2]))
@@ -1941,6 +2001,7 @@ struct Evaluator {
 
     void lammps_compute(const SmxLammpsArgsV1& a, double* energy, double* virial6) {
         require_idle();
+        fpos_mode = false;
         if (a.struct_size < sizeof(SmxLammpsArgsV1)) throw std::invalid_argument("SmxLammpsArgsV1.struct_size is too small");
         if (a.inum < 0 || a.nall < a.inum || a.ntypes < 1)
             throw std::invalid_argument("LAMMPS counts are invalid (0 <= inum <= nall, ntypes >= 1)");
@@ -2419,7 +2480,7 @@ int32_t smx_compute_factorized_single_layer_distributed_evaluation(SmxEvaluator*
     return guarded([&] {
         auto& e = E(ev);
         timed(e.last_evaluation_ms, e.evaluation_count, [&] {
-            e.single_layer_distributed(generation, num_receivers, num_feature_nodes, xyz, r, on_device != 0);
+            e.single_layer_distributed(generation, num_receivers, num_feature_nodes, xyz, r, nullptr, on_device != 0);
         });
     });
 }
@@ -2428,7 +2489,28 @@ int32_t smx_begin_factorized_distributed_evaluation(SmxEvaluator* ev, uint64_t g
                                                     int32_t on_device) {
     return guarded([&] {
         auto& e = E(ev);
-        e.begin_distributed(generation, num_receivers, num_feature_nodes, xyz, r, on_device != 0);
+        e.begin_distributed(generation, num_receivers, num_feature_nodes, xyz, r, nullptr, on_device != 0);
+    });
+}
+int32_t smx_begin_factorized_distributed_positions_evaluation(SmxEvaluator* ev, uint64_t generation,
+                                                              int32_t num_receivers, int32_t num_feature_nodes,
+                                                              const double* feature_positions, int32_t on_device) {
+    return guarded([&] {
+        E(ev).begin_distributed(generation, num_receivers, num_feature_nodes, nullptr, nullptr, feature_positions,
+                                on_device != 0);
+    });
+}
+int32_t smx_compute_factorized_single_layer_distributed_positions_evaluation(SmxEvaluator* ev, uint64_t generation,
+                                                                             int32_t num_receivers,
+                                                                             int32_t num_feature_nodes,
+                                                                             const double* feature_positions,
+                                                                             int32_t on_device) {
+    return guarded([&] {
+        auto& e = E(ev);
+        timed(e.last_evaluation_ms, e.evaluation_count, [&] {
+            e.single_layer_distributed(generation, num_receivers, num_feature_nodes, nullptr, nullptr,
+                                       feature_positions, on_device != 0);
+        });
     });
 }
 int32_t smx_continue_factorized_distributed_evaluation(SmxEvaluator* ev, const float* communicated_h1, int64_t rows,

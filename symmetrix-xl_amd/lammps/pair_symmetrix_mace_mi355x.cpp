@@ -386,40 +386,17 @@ void PairSymmetrixMACEMI355X<DeviceType>::compute_mpi_message_passing()
     graph_nall = nall;
   }
 
-  // edge vectors, scaled to the cutoff when longer: prepared execution keeps
-  // every listed neighbour (:1520-1560)
-  Kokkos::realloc(d_xyz, 3 * (num_edges > 0 ? num_edges : 1));
-  Kokkos::realloc(d_r, num_edges > 0 ? num_edges : 1);
-  {
-    auto xyz = d_xyz;
-    auto r = d_r;
-    auto first = d_first;
-    const double rc = r_cut;
-    Kokkos::parallel_for(
-        Kokkos::RangePolicy<DeviceType>(0, inum), KOKKOS_LAMBDA(const int ii) {
-          const int i = d_ilist(ii);
-          for (int jj = 0; jj < d_numneigh(i); ++jj) {
-            const int j = d_neighbors(i, jj) & NEIGHMASK;
-            const double dx = x(j, 0) - x(i, 0), dy = x(j, 1) - x(i, 1), dz = x(j, 2) - x(i, 2);
-            const double d = sqrt(dx * dx + dy * dy + dz * dz);
-            const double scale = d >= rc ? rc / d : 1.0;
-            const int e = first(ii) + jj;
-            xyz(3 * e) = scale * dx;
-            xyz(3 * e + 1) = scale * dy;
-            xyz(3 * e + 2) = scale * dz;
-            r(e) = scale * d;
-          }
-        });
-  }
+  // the feature nodes' positions are x itself (local and ghost rows, by
+  // LAMMPS index): the library forms each edge vector x[j] - x[i], scaled
+  // to the cutoff when longer (prepared execution keeps every listed
+  // neighbour, :1520-1560)
   Kokkos::fence();
-
   if (single_layer) {
-    check(smx_compute_factorized_single_layer_distributed_evaluation(evaluator, generation, inum, nall,
-                                                                     d_xyz.data(), d_r.data(), 1),
+    check(smx_compute_factorized_single_layer_distributed_positions_evaluation(evaluator, generation, inum, nall,
+                                                                               x.data(), 1),
           "evaluation");
   } else {
-    check(smx_begin_factorized_distributed_evaluation(evaluator, generation, inum, nall, d_xyz.data(),
-                                                      d_r.data(), 1),
+    check(smx_begin_factorized_distributed_positions_evaluation(evaluator, generation, inum, nall, x.data(), 1),
           "evaluation (prefix)");
     // the receivers' H1 rows at their LAMMPS indices, then the ghosts' from
     // their owners (:1582-1689)

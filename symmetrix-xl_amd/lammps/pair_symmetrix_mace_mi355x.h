@@ -93,7 +93,6 @@ class PairSymmetrixMACEMI355X : public Pair, public KokkosBase {
   int64_t num_edges = 0;
   Kokkos::View<int *, DeviceType> d_feature_types, d_receiver_features, d_node_types, d_num_neigh, d_first,
       d_neigh, d_neigh_types;
-  Kokkos::View<double *, DeviceType> d_xyz, d_r;
   Kokkos::View<float *, DeviceType> d_h1;          // [nall][row_floats] H1 rows by LAMMPS index
   float *exchange_rows = nullptr;                   // the evaluator's H1 adjoint rows while they are exchanged
   Kokkos::View<double *, DeviceType> d_stage;       // host-staged communication

@@ -105,6 +105,9 @@ SIGNATURES = [
      [_vp, _i32, _i32, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _p_u64]),
     ("smx_compute_factorized_single_layer_distributed_evaluation", _i32, [_vp, _u64, _i32, _i32, _vp, _vp, _i32]),
     ("smx_begin_factorized_distributed_evaluation", _i32, [_vp, _u64, _i32, _i32, _vp, _vp, _i32]),
+    ("smx_begin_factorized_distributed_positions_evaluation", _i32, [_vp, _u64, _i32, _i32, _vp, _i32]),
+    ("smx_compute_factorized_single_layer_distributed_positions_evaluation", _i32,
+     [_vp, _u64, _i32, _i32, _vp, _i32]),
     ("smx_continue_factorized_distributed_evaluation", _i32, [_vp, _vp, _i64, _i32]),
     ("smx_finish_factorized_distributed_evaluation", _i32, [_vp, _vp, _i64, _i32]),
     ("smx_distributed_exchange", _i32, [_vp, _i32, ctypes.POINTER(_vp), _p_i64, _p_i64]),

@@ -274,6 +274,23 @@ class MACEKokkosFloat:
         check(lib.smx_begin_factorized_distributed_evaluation(
             self._h, int(execution_graph_generation), self._num_nodes, self._num_feature_nodes, ptr(xyz), ptr(r), 0))
 
+    def _feature_positions(self, positions):
+        positions = f64(positions)
+        if positions.size != 3 * self._num_feature_nodes:
+            raise ValueError("positions must hold three coordinates per feature node")
+        return positions
+
+    def _begin_factorized_distributed_positions_evaluation(self, execution_graph_generation, positions):
+        p = self._feature_positions(positions)
+        check(lib.smx_begin_factorized_distributed_positions_evaluation(
+            self._h, int(execution_graph_generation), self._num_nodes, self._num_feature_nodes, ptr(p), 0))
+
+    def _compute_factorized_single_layer_distributed_positions_evaluation(self, execution_graph_generation,
+                                                                          positions):
+        p = self._feature_positions(positions)
+        check(lib.smx_compute_factorized_single_layer_distributed_positions_evaluation(
+            self._h, int(execution_graph_generation), self._num_nodes, self._num_feature_nodes, ptr(p), 0))
+
     def _distributed_rows(self, which):
         """host copy of the rows a phase leaves for the exchange: 0, the
         receivers' H1; 1, the feature nodes' H1 adjoint"""

@@ -223,6 +223,12 @@ def test_phase_order_and_refusals(tiny_model_path, tiny_single_model_path, tiny_
     bad[6] = np.where(np.arange(len(sl["neigh"])) == 0, len(sl["feats"]), sl["neigh"]).astype(np.int32)
     with pytest.raises(ValueError, match="out of range"):
         MACEKokkosFloat(tiny_model_path)._prepare_factorized_feature_graph(*bad)
+    # the positions form needs explicit feature nodes
+    pl = MACEKokkosFloat(tiny_model_path)
+    g = ref["graph"]
+    pg = pl._prepare_factorized_graph(len(types), types, g["num_neigh"], g["sources"], types[g["sources"]])
+    with pytest.raises(ValueError, match="feature nodes"):
+        pl._begin_factorized_distributed_positions_evaluation(pg, s["positions"])
     # a field-coupled model needs its field before the phases
     fev = MACEKokkosFloat(tiny_field_model_path)
     fgen = fev._prepare_factorized_feature_graph(*args)
@@ -316,8 +322,10 @@ def test_device_forms_as_the_pair_style_calls_them(tiny_model_path):
             hip.hipFree(p)
 
 
-@pytest.mark.parametrize("model", ["tiny", "tiny_field"])
-def test_one_rank_with_ghost_images_as_the_pair_style_runs_it(request, model):
+@pytest.mark.parametrize("model,form,tile", [("tiny", "xyz", 0), ("tiny_field", "xyz", 0),
+                                             ("tiny", "positions", 0), ("tiny", "positions", 16),
+                                             ("tiny_single", "positions", 16)])
+def test_one_rank_with_ghost_images_as_the_pair_style_runs_it(request, model, form, tile):
     """The pair style's mpi_message_passing compute on one rank: local atoms
     (in a shuffled ilist order) are the receivers, the local atoms and their
     26 ghost images are the feature nodes by LAMMPS index, the forward
@@ -350,18 +358,26 @@ def test_one_rank_with_ghost_images_as_the_pair_style_runs_it(request, model):
     xyz, r = xyz * sc[:, None], d * sc
     if field is not None:
         ev._set_electric_field(field)
+    if tile:
+        ev.set_execution_plan_request("capacity", tile)
     gen = ev._prepare_factorized_feature_graph(n, nall, ilist, model_type[ilist], model_type,
                                                np.array([len(rows[i]) for i in ilist], np.int32), neigh,
                                                model_type[neigh])
-    ev._begin_factorized_distributed_evaluation(gen, xyz, r)
-    h = ev._distributed_h1()
-    H1 = np.zeros((nall, h.shape[1]), np.float32)
-    H1[ilist] = h
-    H1[n:] = H1[owner[n:]]                      # forward communication
-    ev._continue_factorized_distributed_evaluation(H1)
-    adj = ev._distributed_h1_adjoint().astype(np.float64)
-    np.add.at(adj, owner[n:], adj[n:])          # reverse communication
-    ev._finish_factorized_distributed_evaluation(adj.astype(np.float32))
+    if ev.num_interactions == 1:
+        ev._compute_factorized_single_layer_distributed_positions_evaluation(gen, allpos)
+    else:
+        if form == "positions":
+            ev._begin_factorized_distributed_positions_evaluation(gen, allpos)
+        else:
+            ev._begin_factorized_distributed_evaluation(gen, xyz, r)
+        h = ev._distributed_h1()
+        H1 = np.zeros((nall, h.shape[1]), np.float32)
+        H1[ilist] = h
+        H1[n:] = H1[owner[n:]]                      # forward communication
+        ev._continue_factorized_distributed_evaluation(H1)
+        adj = ev._distributed_h1_adjoint().astype(np.float64)
+        np.add.at(adj, owner[n:], adj[n:])          # reverse communication
+        ev._finish_factorized_distributed_evaluation(adj.astype(np.float32))
     e = np.zeros(n)
     e[ilist] = ev.node_energies
     f_all = ev._reduce_atom_forces(nall, None, None, gen)
