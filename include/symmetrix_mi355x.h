@@ -86,6 +86,14 @@ SMX_API void smx_evaluator_destroy(SmxEvaluator* ev);
 SMX_API int32_t smx_evaluator_info(const SmxEvaluator* ev, SmxModelInfo* info);
 /* atomic_numbers property (pybind mace_kokkos.cpp:1896) */
 SMX_API int32_t smx_evaluator_atomic_numbers(const SmxEvaluator* ev, int32_t* out, int32_t capacity);
+/* atomic_energies property (pybind mace_kokkos.cpp:1900-1903): E0 per
+ * element, model order */
+SMX_API int32_t smx_evaluator_atomic_energies(const SmxEvaluator* ev, double* out, int32_t capacity);
+/* active_atomic_numbers property (pybind mace_kokkos.cpp:1906-1909;
+ * lifecycle.cpp:4096-4101, mace.cpp:2738): the elements whose per-pair
+ * radial tables are on the device (models with a distance transform; in
+ * model type order), else every element of the model.  out NULL: count only. */
+SMX_API int32_t smx_active_atomic_numbers(const SmxEvaluator* ev, int32_t* out, int32_t capacity, int32_t* count);
 /* selected_head / available_heads (mace_kokkos.cpp:1904-1905): index -1 gives
  * the head in use ("" when the file names none), index 0.. the heads the
  * file stores (NULL past the end).  The strings live as long as ev. */

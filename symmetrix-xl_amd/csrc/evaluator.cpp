@@ -2242,6 +2242,31 @@ int32_t smx_evaluator_atomic_numbers(const SmxEvaluator* ev, int32_t* out, int32
     });
 }
 
+int32_t smx_evaluator_atomic_energies(const SmxEvaluator* ev, double* out, int32_t capacity) {
+    return guarded([&] {
+        const auto& e0 = E(ev).hm.atomic_energies;
+        if (!out || capacity < static_cast<int32_t>(e0.size())) throw std::invalid_argument("buffer too small");
+        std::copy(e0.begin(), e0.end(), out);
+    });
+}
+
+int32_t smx_active_atomic_numbers(const SmxEvaluator* ev, int32_t* out, int32_t capacity, int32_t* count) {
+    return guarded([&] {
+        const auto& e = E(ev);
+        // models with per-pair radial tables keep tables for the active
+        // types only; the others serve every type
+        std::vector<int32_t> z;
+        if (e.hm.agnesi)
+            for (int t : e.pair_active) z.push_back(e.hm.atomic_numbers[t]);
+        else
+            z.assign(e.hm.atomic_numbers.begin(), e.hm.atomic_numbers.end());
+        if (count) *count = static_cast<int32_t>(z.size());
+        if (!out) return;
+        if (capacity < static_cast<int32_t>(z.size())) throw std::invalid_argument("buffer too small");
+        std::copy(z.begin(), z.end(), out);
+    });
+}
+
 int32_t smx_prediction_head(const SmxEvaluator* ev, int32_t index, const char** name) {
     return guarded([&] {
         if (!name) throw std::invalid_argument("name output is required");

@@ -94,6 +94,8 @@ SIGNATURES = [
     ("smx_evaluator_destroy", None, [_vp]),
     ("smx_evaluator_info", _i32, [_vp, ctypes.POINTER(SmxModelInfo)]),
     ("smx_evaluator_atomic_numbers", _i32, [_vp, _vp, _i32]),
+    ("smx_evaluator_atomic_energies", _i32, [_vp, _vp, _i32]),
+    ("smx_active_atomic_numbers", _i32, [_vp, _vp, _i32, _p_i32]),
     ("smx_prediction_head", _i32, [_vp, _i32, ctypes.POINTER(ctypes.c_char_p)]),
     ("smx_set_streamed_edges", _i32, [_vp, _cp]),
     ("smx_evaluator_stream", _vp, [_vp]),

@@ -93,6 +93,20 @@ class MACEKokkosFloat:
         return [int(v) for v in self._atomic_numbers]
 
     @property
+    def atomic_energies(self):
+        out = np.zeros(self.num_elements)
+        check(lib.smx_evaluator_atomic_energies(self._h, ptr(out), out.size))
+        return [float(v) for v in out]
+
+    @property
+    def active_atomic_numbers(self):
+        n = ctypes.c_int32()
+        check(lib.smx_active_atomic_numbers(self._h, None, 0, ctypes.byref(n)))
+        out = np.zeros(n.value, dtype=np.int32)
+        check(lib.smx_active_atomic_numbers(self._h, ptr(out), out.size, None))
+        return [int(v) for v in out]
+
+    @property
     def streamed_edges_mode(self):
         return "direct"
 

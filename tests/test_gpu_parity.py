@@ -494,3 +494,19 @@ def test_invalid_positions_raise_and_next_call_recovers(tiny_model_path):
         free()
     ev._compute_prepared_factorized_positions(gen, s["positions"])
     assert ev.node_energies.tobytes() == e0.tobytes()
+
+
+def test_atomic_energies_and_active_elements(tiny_model_path, tiny_agnesi_model_path):
+    """atomic_energies and active_atomic_numbers (pybind mace_kokkos.cpp:
+    1900-1909): E0 as the file holds it; every element for a model without
+    per-pair tables, the tabulated ones for a model with them."""
+    import json
+    from symmetrix.mace_kokkos import MACEKokkosFloat
+    with open(tiny_model_path) as f:
+        e0 = np.asarray(json.load(f)["atomic_energies"], float).ravel()
+    ev = MACEKokkosFloat(tiny_model_path)
+    np.testing.assert_array_equal(ev.atomic_energies, e0[: ev.num_elements])
+    assert ev.active_atomic_numbers == ev.atomic_numbers
+    ag = MACEKokkosFloat(tiny_agnesi_model_path)
+    ag.prepare_active_types([1])
+    assert ag.active_atomic_numbers == [ag.atomic_numbers[1]]
