@@ -23,7 +23,7 @@ Also reported (extra keys, each measured in the same run):
   calculator (the reference's ASE-call boundary), plus the cold call;
 * the wide (30,000-atom water) and irregular (20,000 atoms, 10 species)
   configs: median us/atom and the dominant kernel's fraction;
-* a short tiled capacity run at 11.5M atoms (3 NVE steps);
+* the tiled capacity config at 11.5M atoms (20 NVE steps at 1 fs);
 * the CPU oracle on the box's host cores (3 warm-ups, median of 10, OMP
   threads bound to cores), on all allowed cores and on 8 of them.
 """
@@ -240,7 +240,7 @@ def main():
     ap.add_argument("--no-lammps", action="store_true", help="skip the LAMMPS pair-style step timing")
     ap.add_argument("--only-config", choices=("wide", "irregular", "single"),
                     help="run only that config (3 warm-ups, median of 10) and print its summary")
-    ap.add_argument("--capacity-steps", type=int, default=3,
+    ap.add_argument("--capacity-steps", type=int, default=20,
                     help="NVE steps of the tiled 11.5M-atom capacity extra key (0 skips it)")
     ap.add_argument("--capacity", type=int, default=0, metavar="N",
                     help="run the tiled capacity config on an N^3 SrTiO3 supercell instead")
@@ -442,15 +442,23 @@ def run_config(hip, model_path, system, skin, warmup, steps, timed_steps=False):
     flops = E_active * C * r1_reverse_flops_per_edge_channel(P, T, rows) / per_call
     achieved = flops / (avg_ms * 1e-3) / 1e12
     executed = R1_REVERSE_EXECUTED_FLOPS_PER_EDGE_CHANNEL.get((P, T, rows))
+    # achieved/peak/frac: the algorithmic-equivalent rate (the survey's flop
+    # count of the R1 reverse over the published FP32 peak); the kernel
+    # executes fewer flops than that count (the coupling is contracted once
+    # per receiver), so its hardware efficiency is executed_frac, executed
+    # flops over the 78.6 TFLOP/s this VALU code can issue
     roof = {"bound": "valu", "kernel": DOMINANT, "achieved": round(achieved, 3), "peak": PEAK_FP32_TFLOPS,
-            "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_TFLOPS, 4), "avg_launch_ms": round(avg_ms, 4),
-            "launches_per_call": per_call, "flops_per_launch": int(flops),
+            "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_TFLOPS, 4),
+            "achieved_kind": "algorithmic-equivalent (not executed flops; see executed_frac)",
+            "avg_launch_ms": round(avg_ms, 4), "launches_per_call": per_call, "flops_per_launch": int(flops),
             "compute": "FP32 VALU: edge-wise channel products, no MFMA; packed FP32 disabled, so 78.6 TFLOP/s "
                        "is the attainable issue rate",
-            "executed_flops_per_launch": None, "executed_frac": None}
+            "executed_flops_per_launch": None, "executed_achieved": None, "executed_peak": VALU_FP32_TFLOPS,
+            "executed_frac": None}
     if executed:
         ex = E_active * C * executed
         roof["executed_flops_per_launch"] = ex
+        roof["executed_achieved"] = round(ex / (avg_ms * 1e-3) / 1e12, 3)
         roof["executed_frac"] = round(ex / (avg_ms * 1e-3) / 1e12 / VALU_FP32_TFLOPS, 4)
     out["roofline"] = roof
     hip.hipFree(d_pos)

@@ -254,8 +254,10 @@ __device__ __forceinline__ int pair_type(int a, int b, int n) {
 // evaluation point is formed in FP32 from the rounded radius (fp64_point 0,
 // the precision-matched form) or in FP64 and rounded (fp64_point 1); the
 // slope uses the factors (2x) and (3xx) formed before the multiply
-// (jit_codegen.py:2387-2485).
-template <int NY>
+// (jit_codegen.py:2387-2485).  C is the kernel's lane count and CF the
+// caller's channel count (CF < C for a model whose channels the kernels pad:
+// functions are then p * CF + k and lanes k >= CF read zero coefficients).
+template <int NY, int C, int CF = C>
 struct PluginEdges {
     const double* __restrict__ radius;
     const float* __restrict__ harm;    // [E][NY]
@@ -335,12 +337,29 @@ struct PluginEdges {
         return unit32 ? unit32[3 * static_cast<std::size_t>(p.e) + c]
                       : static_cast<float>(xyz64[3 * static_cast<std::size_t>(p.e) + c] / radius[p.e]);
     }
+    // the caller's function index of kernel function f = p * C + k, or -1
+    // for a padding lane
+    __device__ __forceinline__ static int caller_function(int f) {
+        if constexpr (CF == C) {
+            return f;
+        } else {
+            const int p = f / C, k = f - p * C;
+            return k < CF ? p * CF + k : -1;
+        }
+    }
     __device__ __forceinline__ float value(const Point& p, int f) const {
+        f = caller_function(f);
+        if (CF != C && f < 0) return 0.0f;
         const float c0 = p.c0[f], c1 = p.c0[functions + f], c2 = p.c0[2 * functions + f],
                     c3 = p.c0[3 * functions + f];
         return c0 + c1 * p.x + c2 * p.xx + c3 * p.xxx;
     }
     __device__ __forceinline__ void value_slope(const Point& p, int f, float& R, float& dR) const {
+        f = caller_function(f);
+        if (CF != C && f < 0) {
+            R = dR = 0.0f;
+            return;
+        }
         const float c0 = p.c0[f], c1 = p.c0[functions + f], c2 = p.c0[2 * functions + f],
                     c3 = p.c0[3 * functions + f];
         R = c0 + c1 * p.x + c2 * p.xx + c3 * p.xxx;
@@ -497,9 +516,10 @@ inline unsigned r1_forward_blocks(int nr) {
 // written once per pass: assigned (zero for paths outside the group) or,
 // with ACCUMULATE, added.  Receiver i = r0 + li owns edges [first[i],
 // first[i]+count[i]) (or [first[i], first[i+1]) when count is null); Phi1
-// rows are indexed by li.
+// rows are indexed by li.  H1 and Phi1 rows hold CF channels (CF <= C: the
+// lanes k >= CF of a caller's unpadded arrays neither read nor write).
 // ---------------------------------------------------------------------------
-template <int C, int LMAX, int LMAXH, unsigned MASK, bool ACCUMULATE, class EDGES>
+template <int C, int LMAX, int LMAXH, unsigned MASK, bool ACCUMULATE, class EDGES, int CF = C>
 __global__ __launch_bounds__(C) void k_r1_forward(int r0, int nr, const int* __restrict__ first,
                                                   const int* __restrict__ count, const int* __restrict__ neigh,
                                                   EDGES edges, const float* __restrict__ H1,
@@ -521,6 +541,7 @@ __global__ __launch_bounds__(C) void k_r1_forward(int r0, int nr, const int* __r
         k += (x % SL) * (C / SL);
     }
     const int i = r0 + li;
+    const bool lane_on = CF == C || k < CF;
     float rows[RG::NR];
 #pragma unroll
     for (int r = 0; r < RG::NR; ++r) rows[r] = 0.0f;
@@ -530,7 +551,7 @@ __global__ __launch_bounds__(C) void k_r1_forward(int r0, int nr, const int* __r
     auto add_edge = [&](auto&& radial, auto&& Y, const float* hj) __attribute__((always_inline)) {
         float h[NH];
 #pragma unroll
-        for (int q = 0; q < NH; ++q) h[q] = RG::component(q) ? hj[q * C] : 0.0f;
+        for (int q = 0; q < NH; ++q) h[q] = (RG::component(q) && lane_on) ? hj[q * CF] : 0.0f;
         static_for<0, S::P>([&](auto pc) {
             constexpr int p = pc;
             if constexpr (RG::used(p)) {
@@ -568,6 +589,7 @@ __global__ __launch_bounds__(C) void k_r1_forward(int r0, int nr, const int* __r
         // The wave-uniform record fields and source index of edge e+1 are
         // loaded while edge e runs, so an edge starts with its spline and
         // H1 loads instead of a chain of dependent scalar loads.
+        static_assert(CF == C, "held records are the evaluator's own, unpadded-stride layout");
         typename EDGES::Held cur, nxt;
         int src = 0;
         if (ea < eb) {
@@ -595,11 +617,12 @@ __global__ __launch_bounds__(C) void k_r1_forward(int r0, int nr, const int* __r
                 typename EDGES::Point pt;
                 if (!edges.open_at(e, i, chunk, j, pt)) continue;
                 add_edge([&](int p) { return edges.value(pt, p * C + k); },
-                         [&](int lm) { return edges.Y(pt, lm); }, H1 + static_cast<std::size_t>(neigh[e]) * NH * C + k);
+                         [&](int lm) { return edges.Y(pt, lm); }, H1 + static_cast<std::size_t>(neigh[e]) * NH * CF + k);
             }
         });
     }
-    float* out = Phi1 + static_cast<std::size_t>(li) * S::NLME * C + k;
+    float* out = Phi1 + static_cast<std::size_t>(li) * S::NLME * CF + k;
+    if (!lane_on) return;
     static_for<0, S::P>([&](auto pc) {
         constexpr int p = pc;
         constexpr int le = S::paths[p].le, ls = S::paths[p].ls, lo = S::paths[p].lo, co = S::cg_offset[p];
@@ -618,9 +641,9 @@ __global__ __launch_bounds__(C) void k_r1_forward(int r0, int nr, const int* __r
                         }
                     });
                 });
-                out[q * C] = ACCUMULATE ? out[q * C] + o : o;
+                out[q * CF] = ACCUMULATE ? out[q * CF] + o : o;
             } else if constexpr (!ACCUMULATE) {
-                out[q * C] = 0.0f;
+                out[q * CF] = 0.0f;
             }
         });
     });
@@ -634,9 +657,11 @@ __global__ __launch_bounds__(C) void k_r1_forward(int r0, int nr, const int* __r
 //   W_e[lm2,k] = sum_{p,m1} R Y_lm1 G[row]   (zero for inactive edges)
 // that k_source_gather sums over each source's edges.  G = CG^T dPhi1[li].
 // W and node_forces are indexed by e - e0; forces are assigned (-f) or, with
-// FORCE_ACCUMULATE, subtracted from what the buffer holds.
+// FORCE_ACCUMULATE, subtracted from what the buffer holds.  H1 and dPhi1
+// rows hold CF channels (lanes k >= CF read zero, so their G, W and force
+// parts are zero); W rows always hold C.
 // ---------------------------------------------------------------------------
-template <int C, int LMAX, int LMAXH, unsigned MASK, bool FORCE_ACCUMULATE, class EDGES>
+template <int C, int LMAX, int LMAXH, unsigned MASK, bool FORCE_ACCUMULATE, class EDGES, int CF = C>
 __global__ __launch_bounds__(C) void k_r1_reverse(int r0, long long e0, const int* __restrict__ offsets,
                                                   const int* __restrict__ neigh, EDGES edges,
                                                   const float* __restrict__ H1, const float* __restrict__ cg,
@@ -651,18 +676,19 @@ __global__ __launch_bounds__(C) void k_r1_reverse(int r0, long long e0, const in
     const int li = xcd_remap(blockIdx.x, gridDim.x);
     const int i = r0 + li;
     const int k = threadIdx.x;
+    const bool lane_on = CF == C || k < CF;
     float G[RG::NR];
 #pragma unroll
     for (int r = 0; r < RG::NR; ++r) G[r] = 0.0f;
     {
-        const float* d = dPhi1 + static_cast<std::size_t>(li) * S::NLME * C + k;
+        const float* d = dPhi1 + static_cast<std::size_t>(li) * S::NLME * CF + k;
         static_for<0, S::P>([&](auto pc) {
             constexpr int p = pc;
             if constexpr (RG::used(p)) {
                 constexpr int le = S::paths[p].le, ls = S::paths[p].ls, lo = S::paths[p].lo, co = S::cg_offset[p];
                 static_for<0, 2 * lo + 1>([&](auto mc) {
                     constexpr int mo = mc;
-                    const float dq = d[S::lme(p, mo) * C];
+                    const float dq = lane_on ? d[S::lme(p, mo) * CF] : 0.0f;
                     static_for<0, 2 * le + 1>([&](auto m1c) {
                         constexpr int m1 = m1c;
                         static_for<0, 2 * ls + 1>([&](auto m2c) {
@@ -689,11 +715,11 @@ __global__ __launch_bounds__(C) void k_r1_reverse(int r0, long long e0, const in
                 sink.zero(j);
                 continue;
             }
-            const float* hj = H1 + static_cast<std::size_t>(neigh[e]) * NH * C + k;
+            const float* hj = H1 + static_cast<std::size_t>(neigh[e]) * NH * CF + k;
             float h[NH], W[NH];
 #pragma unroll
             for (int q = 0; q < NH; ++q) {
-                h[q] = RG::component(q) ? hj[q * C] : 0.0f;
+                h[q] = (RG::component(q) && lane_on) ? hj[q * CF] : 0.0f;
                 W[q] = 0.0f;
             }
             // Per path p, with T[m2] = sum_m1 Y_m1 G[p,m1,m2] and
@@ -821,8 +847,9 @@ __device__ __forceinline__ void gather_source_rows(const int* __restrict__ sedge
     }
 }
 
-// H1_adj[s] = (or, with ACCUMULATE, +=) the FP64 sum of W over s's edges
-template <int C, int NH, bool ACCUMULATE>
+// H1_adj[s] = (or, with ACCUMULATE, +=) the FP64 sum of W over s's edges;
+// H1_adj rows hold CF <= C channels
+template <int C, int NH, bool ACCUMULATE, int CF = C>
 __global__ __launch_bounds__(C) void k_source_gather(const int* __restrict__ soff, const int* __restrict__ sedges,
                                                      const float* __restrict__ Wsrc, const double* __restrict__ r,
                                                      double r_cut, float* __restrict__ H1_adj) {
@@ -832,10 +859,11 @@ __global__ __launch_bounds__(C) void k_source_gather(const int* __restrict__ sof
 #pragma unroll
     for (int q = 0; q < NH; ++q) acc[q] = 0.0;
     gather_source_rows<C, NH>(sedges, soff[s], soff[s + 1], 0, Wsrc, r, r_cut, k, acc);
-    float* dst = H1_adj + static_cast<std::size_t>(s) * NH * C + k;
+    if (CF != C && k >= CF) return;
+    float* dst = H1_adj + static_cast<std::size_t>(s) * NH * CF + k;
 #pragma unroll
-    for (int q = 0; q < NH; ++q) dst[q * C] = ACCUMULATE ? dst[q * C] + static_cast<float>(acc[q])
-                                                        : static_cast<float>(acc[q]);
+    for (int q = 0; q < NH; ++q) dst[q * CF] = ACCUMULATE ? dst[q * CF] + static_cast<float>(acc[q])
+                                                         : static_cast<float>(acc[q]);
 }
 
 }  // namespace

@@ -456,66 +456,139 @@ static std::vector<double> flat_doubles(const Value& v) {
     return v.as_doubles();
 }
 
-// field_coupling.hpp:60-238 (the schema checks and path compilation) and
-// mace.cpp:2832-2860: one coupling; each field_feats instruction (l_in x 1o
-// -> an adjacent l) pairs with the field_linear instruction of that l; the
-// path's channel matrix is path_weight_f * path_weight_l * Wf Wl (FP64 sums,
-// rounded once) and its angular entries are the 3j tensor's nonzeros.
+// MACEField coupling block. The schema it must satisfy is the one
+// field_coupling.hpp:60-238 and mace.cpp:2832-2860 accept; the reading below
+// is organised around two rule lists:
+//   * feats rules (field_feats_instructions): H1p block l_in times the field
+//     (one 1o vector) into an intermediate block l_mid = l_in +- 1, a C x C
+//     "uvw" weight and a real 3j tensor [2 l_in + 1][3][2 l_mid + 1];
+//   * mix rules (field_linear_instructions): a C x C weight on block l.
+// Every mix rule whose block is a feats rule's l_mid closes one path; its
+// channel matrix is the product of the two weights times both path weights,
+// formed in FP64 and rounded to FP32 once.
+namespace {
+
+[[noreturn]] void field_refuse(const std::string& what) {
+    throw std::invalid_argument("field coupling: " + what);
+}
+
+struct FeatsRule {
+    int l_in, l_mid;
+    double scale;
+    std::vector<double> w3;          // [2 l_in + 1][3][2 l_mid + 1]
+    std::size_t weight_at;           // first element of its C x C weight
+};
+
+struct MixRule {
+    int l;
+    double scale;
+    std::size_t weight_at;
+};
+
+// Files written before schema_version existed hold L_max 1 couplings with no
+// tensor: the field's three components map one to one onto the m of the
+// l = 1 side (the e3nn order of both), normalised by 1/sqrt(3).
+std::vector<double> unversioned_tensor(int l_in, int l_mid) {
+    const int din = 2 * l_in + 1, dmid = 2 * l_mid + 1;
+    std::vector<double> w(static_cast<std::size_t>(din) * 3 * dmid, 0.0);
+    for (int c = 0; c < 3; ++c) {
+        const int m_in = l_in == 1 ? c : 0, m_mid = l_mid == 1 ? c : 0;
+        w[(static_cast<std::size_t>(m_in) * 3 + c) * dmid + m_mid] = 1.0 / std::sqrt(3.0);
+    }
+    return w;
+}
+
+}  // namespace
+
 void HostModel::load_field_coupling(const Value& j) {
-    if (L_max < 1 || L_max > 2)
-        throw std::invalid_argument("MACEField field coupling currently supports only 1 <= L_max <= 2.");
+    if (L_max != 1 && L_max != 2)
+        field_refuse("MACEField models need a hidden L_max of 1 or 2, this model has " + std::to_string(L_max));
     const Value& list = j.at("field_couplings");
-    if (list.size() != 1) throw std::invalid_argument("MACEField JSON must contain exactly one field coupling.");
+    if (list.size() != 1)
+        field_refuse("field_couplings must hold one coupling, found " + std::to_string(list.size()));
     const Value& cp = list.at(0);
-    const bool legacy = !cp.contains("schema_version");
-    if (!legacy && cp.at("schema_version").as_int() != 1)
-        throw std::invalid_argument("Unsupported MACEField field-coupling schema version.");
-    if (legacy && L_max != 1)
-        throw std::invalid_argument("Unversioned MACEField field coupling is supported only for legacy L_max == 1 data.");
+    const bool versioned = cp.contains("schema_version");
+    if (versioned && cp.at("schema_version").as_int() != 1)
+        field_refuse("schema_version " + std::to_string(cp.at("schema_version").as_int()) + " is unknown (1 is read)");
+    if (!versioned && L_max != 1)
+        field_refuse("a coupling without schema_version is readable only for L_max 1 models");
+
+    // every irreps string is the hidden representation, except the field's own
     std::string hidden;
     for (int l = 0; l <= L_max; ++l)
         hidden += (l ? "+" : "") + std::to_string(C) + "x" + std::to_string(l) + (l % 2 ? "o" : "e");
-    if (cp.at("field_feats_irreps_in1").as_string() != hidden || cp.at("field_feats_irreps_in2").as_string() != "1x1o" ||
-        cp.at("field_feats_irreps_out").as_string() != hidden || cp.at("field_linear_irreps_in").as_string() != hidden ||
-        cp.at("field_linear_irreps_out").as_string() != hidden)
-        throw std::invalid_argument("MACEField field coupling must use the canonical equal-channel hidden irreps.");
-    const std::size_t Cs = static_cast<std::size_t>(C), cc = Cs * Cs;
+    const std::pair<const char*, std::string> irreps[] = {
+        {"field_feats_irreps_in1", hidden}, {"field_feats_irreps_in2", "1x1o"}, {"field_feats_irreps_out", hidden},
+        {"field_linear_irreps_in", hidden}, {"field_linear_irreps_out", hidden}};
+    for (const auto& [key, want] : irreps) {
+        const std::string got = cp.at(key).as_string();
+        if (got != want) field_refuse(std::string(key) + " is '" + got + "', expected '" + want + "'");
+    }
+    const std::size_t Cs = static_cast<std::size_t>(C), block = Cs * Cs;
     for (const char* key : {"field_feats_output_mask", "field_linear_output_mask"}) {
-        const auto m = cp.at(key).as_doubles();
-        if (m.size() != static_cast<std::size_t>(num_LM) * Cs)
-            throw std::invalid_argument(std::string("MACEField ") + key + " has an invalid size.");
-        for (double v : m)
-            if (v != 1.0) throw std::invalid_argument(std::string("MACEField ") + key + " must contain only ones.");
+        const auto mask = cp.at(key).as_doubles();
+        const bool all_ones = std::all_of(mask.begin(), mask.end(), [](double v) { return v == 1.0; });
+        if (mask.size() != static_cast<std::size_t>(num_LM) * Cs || !all_ones)
+            field_refuse(std::string(key) + " must be " + std::to_string(num_LM * C) + " ones");
     }
-    if (cp.at("field_linear_bias").size() != 0) throw std::invalid_argument("MACEField field_linear bias must be empty.");
-    const auto wf = flat_doubles(cp.at("field_feats_weight"));
-    const auto wl = flat_doubles(cp.at("field_linear_weight"));
-    const Value& fis = cp.at("field_feats_instructions");
-    const Value& lis = cp.at("field_linear_instructions");
-    const Value* uw = j.find("H1_linear_up_weights");
-    const Value* pw = j.find("H1_product_weights");
-    if (!uw || !pw) throw std::invalid_argument("MACEField JSON must contain split H1 product and linear_up weights.");
-    const auto U = uw->as_doubles();
-    const auto P = pw->as_doubles();
-    if (U.size() != static_cast<std::size_t>(L_max + 1) * cc || P.size() != U.size())
-        throw std::invalid_argument("MACEField split H1 linear_up weights have an invalid size.");
-    for (std::size_t fi = 0; fi < fis.size(); ++fi) {
-        const Value& ins = fis.at(fi);
-        if (ins.at("connection_mode").as_string() != "uvw" || ins.at("path_shape").as_ints() != std::vector<int>{C, 1, C})
-            throw std::invalid_argument("MACEField field_feats instructions must use uvw paths shaped (channels, 1, channels).");
-    }
-    if (fis.size() * cc != wf.size())
-        throw std::invalid_argument("MACEField field_feats weight size does not match its instructions.");
-    for (std::size_t li = 0; li < lis.size(); ++li) {
-        const Value& ins = lis.at(li);
+    if (cp.at("field_linear_bias").size() != 0) field_refuse("field_linear_bias must be empty");
+
+    const Value* up = j.find("H1_linear_up_weights");
+    const Value* prod = j.find("H1_product_weights");
+    if (!up || !prod) field_refuse("the model must split H1 into H1_product_weights and H1_linear_up_weights");
+    const auto U = up->as_doubles();
+    const auto P = prod->as_doubles();
+    if (U.size() != static_cast<std::size_t>(L_max + 1) * block || P.size() != U.size())
+        field_refuse("H1_product_weights and H1_linear_up_weights must each hold L_max + 1 blocks of C x C");
+
+    // mix rules: one C x C block per rule, in file order
+    const Value& mix_list = cp.at("field_linear_instructions");
+    const auto mix_weights = flat_doubles(cp.at("field_linear_weight"));
+    std::vector<MixRule> mix;
+    for (std::size_t i = 0; i < mix_list.size(); ++i) {
+        const Value& ins = mix_list.at(i);
+        const std::string where = "field_linear_instructions[" + std::to_string(i) + "]";
         if (ins.at("path_shape").as_ints() != std::vector<int>{C, C})
-            throw std::invalid_argument("MACEField field_linear instructions must be shaped (channels, channels).");
+            field_refuse(where + " must have path_shape [C, C]");
         const int a = ins.at("i_in").as_int(), b = ins.at("i_out").as_int();
-        if (a < 0 || a > L_max || b != a)
-            throw std::invalid_argument("MACEField field_linear instructions must preserve each canonical angular block.");
+        if (a != b || a < 0 || a > L_max) field_refuse(where + " must map a hidden block 0..L_max onto itself");
+        mix.push_back({a, ins.at("path_weight").as_number(), i * block});
     }
-    if (lis.size() * cc != wl.size())
-        throw std::invalid_argument("MACEField field_linear weight size does not match its instructions.");
+    if (mix_weights.size() != mix.size() * block)
+        field_refuse("field_linear_weight holds " + std::to_string(mix_weights.size()) + " numbers, its rules need " +
+                     std::to_string(mix.size() * block));
+
+    // feats rules: an adjacent-rank coupling of H1p with the field vector
+    const Value& feats_list = cp.at("field_feats_instructions");
+    const auto feats_weights = flat_doubles(cp.at("field_feats_weight"));
+    std::vector<FeatsRule> feats;
+    for (std::size_t i = 0; i < feats_list.size(); ++i) {
+        const Value& ins = feats_list.at(i);
+        const std::string where = "field_feats_instructions[" + std::to_string(i) + "]";
+        if (ins.at("connection_mode").as_string() != "uvw" ||
+            ins.at("path_shape").as_ints() != std::vector<int>{C, 1, C})
+            field_refuse(where + " must be a 'uvw' rule of path_shape [C, 1, C]");
+        FeatsRule r{ins.at("i_in1").as_int(), ins.at("i_out").as_int(), ins.at("path_weight").as_number(), {},
+                    i * block};
+        if (ins.at("i_in2").as_int() != 0 || r.l_in < 0 || r.l_in > L_max || r.l_mid < 0 || r.l_mid > L_max ||
+            (r.l_mid != r.l_in + 1 && r.l_mid != r.l_in - 1))
+            field_refuse(where + " must couple hidden block l with the field into block l +- 1");
+        const std::size_t n3 = static_cast<std::size_t>(2 * r.l_in + 1) * 3 * (2 * r.l_mid + 1);
+        if (versioned) {
+            if (ins.at("wigner_3j_shape").as_ints() != std::vector<int>{2 * r.l_in + 1, 3, 2 * r.l_mid + 1})
+                field_refuse(where + " has a wigner_3j_shape that is not [2 l_in + 1, 3, 2 l_out + 1]");
+            r.w3 = ins.at("wigner_3j").as_doubles();
+            if (r.w3.size() != n3) field_refuse(where + " has " + std::to_string(r.w3.size()) + " wigner_3j numbers, "
+                                                "its shape needs " + std::to_string(n3));
+        } else {
+            r.w3 = unversioned_tensor(r.l_in, r.l_mid);
+        }
+        feats.push_back(std::move(r));
+    }
+    if (feats_weights.size() != feats.size() * block)
+        field_refuse("field_feats_weight holds " + std::to_string(feats_weights.size()) + " numbers, its rules need " +
+                     std::to_string(feats.size() * block));
+
     P_all = to_f32(P);
     U_all = to_f32(U);
     transpose_blocks(P_all, P_allt, L_max + 1, C, C);
@@ -523,55 +596,47 @@ void HostModel::load_field_coupling(const Value& j) {
     field_paths.clear();
     field_entries.clear();
     field_W.clear();
-    for (std::size_t fi = 0; fi < fis.size(); ++fi) {
-        const Value& ins = fis.at(fi);
-        const int lin = ins.at("i_in1").as_int(), blk = ins.at("i_in2").as_int(), lmid = ins.at("i_out").as_int();
-        if (blk != 0 || lin < 0 || lin > L_max || lmid < 0 || lmid > L_max || std::abs(lin - lmid) != 1)
-            throw std::invalid_argument("MACEField field_feats instruction is not an adjacent-rank 1o coupling.");
-        const int din = 2 * lin + 1, dmid = 2 * lmid + 1;
-        std::vector<double> w3(static_cast<std::size_t>(din) * 3 * dmid, 0.0);
-        if (legacy) {
-            for (int c = 0; c < 3; ++c) w3[lin == 0 ? c * 3 + c : c * 4] = 1.0 / std::sqrt(3.0);
-        } else {
-            if (ins.at("wigner_3j_shape").as_ints() != std::vector<int>{din, 3, dmid})
-                throw std::invalid_argument("MACEField Wigner tensor shape does not match its angular path.");
-            w3 = ins.at("wigner_3j").as_doubles();
-            if (w3.size() != static_cast<std::size_t>(din) * 3 * dmid)
-                throw std::invalid_argument("MACEField Wigner tensor data has an invalid size.");
-        }
-        bool found = false;
-        for (std::size_t li = 0; li < lis.size(); ++li) {
-            const Value& lins = lis.at(li);
-            if (lins.at("i_in").as_int() != lmid) continue;
-            found = true;
-            const int lout = lins.at("i_out").as_int(), dout = 2 * lout + 1;
+    std::vector<double> row(Cs);
+    for (std::size_t fi = 0; fi < feats.size(); ++fi) {
+        const FeatsRule& f = feats[fi];
+        double largest = 0.0;
+        for (double w : f.w3) largest = std::max(largest, std::abs(w));
+        bool closed = false;
+        for (const MixRule& m : mix) {
+            if (m.l != f.l_mid) continue;
+            closed = true;
             const int path = static_cast<int>(field_paths.size());
-            field_paths.push_back({lin, lout});
+            field_paths.push_back({f.l_in, m.l});
+            // angular entries: the tensor's nonzeros (round-off below 1e-12 of
+            // its largest entry dropped), in (m_in, component, m_out) order
+            const int din = 2 * f.l_in + 1, dmid = 2 * f.l_mid + 1;
             for (int mi = 0; mi < din; ++mi)
                 for (int c = 0; c < 3; ++c)
-                    for (int mo = 0; mo < dout; ++mo) {
-                        const double w = w3[(static_cast<std::size_t>(mi) * 3 + c) * dout + mo];
-                        if (std::abs(w) > 1e-14)
-                            field_entries.push_back({lin * lin + mi, c, lout * lout + mo, path, to_f32(w)});
+                    for (int mo = 0; mo < dmid; ++mo) {
+                        const double w = f.w3[(static_cast<std::size_t>(mi) * 3 + c) * dmid + mo];
+                        if (std::abs(w) > 1e-12 * largest)
+                            field_entries.push_back({f.l_in * f.l_in + mi, c, m.l * m.l + mo, path, to_f32(w)});
                     }
-            const double scale = ins.at("path_weight").as_number() * lins.at("path_weight").as_number();
-            for (int in = 0; in < C; ++in)
-                for (int out = 0; out < C; ++out) {
-                    double v = 0.0;
-                    for (int mid = 0; mid < C; ++mid)
-                        v += wf[fi * cc + static_cast<std::size_t>(in) * Cs + mid] *
-                             wl[li * cc + static_cast<std::size_t>(mid) * Cs + out];
-                    field_W.push_back(to_f32(scale * v));
+            // channel matrix, one input channel's row at a time
+            const double scale = f.scale * m.scale;
+            const double* wf = feats_weights.data() + f.weight_at;
+            const double* wl = mix_weights.data() + m.weight_at;
+            for (std::size_t in = 0; in < Cs; ++in) {
+                std::fill(row.begin(), row.end(), 0.0);
+                for (std::size_t mid = 0; mid < Cs; ++mid) {
+                    const double a = wf[in * Cs + mid];
+                    for (std::size_t out = 0; out < Cs; ++out) row[out] += a * wl[mid * Cs + out];
                 }
+                for (std::size_t out = 0; out < Cs; ++out) field_W.push_back(to_f32(scale * row[out]));
+            }
         }
-        if (!found) throw std::invalid_argument("MACEField field_feats output has no compatible field_linear instruction.");
+        if (!closed)
+            field_refuse("field_feats_instructions[" + std::to_string(fi) + "] ends in block " +
+                         std::to_string(f.l_mid) + ", which no field_linear rule reads");
     }
-    if (field_paths.empty()) throw std::invalid_argument("MACEField field coupling contains no executable paths.");
+    if (field_paths.empty()) field_refuse("no field path is defined");
     transpose_blocks(field_W, field_Wt, field_paths.size(), C, C);
-    if (residual) {
-        const auto b = j.at("H1_first_residual_weights").as_doubles();
-        res_pre = to_f32(b);
-    }
+    if (residual) res_pre = to_f32(j.at("H1_first_residual_weights").as_doubles());
 }
 
 void HostModel::load(const std::string& path, const std::string& head) {

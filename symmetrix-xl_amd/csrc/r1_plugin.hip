@@ -11,22 +11,36 @@
 //               adding the FP64 source sums to source_adjoint over the
 //               caller's source transpose.
 //
+// Shapes: every (channels, l_max, L_max) the evaluator compiles, with the
+// caller's channel count where the kernels pad it (96 on 128 lanes, 224 on
+// 256).  A shape whose coupling rows exceed one pass's registers (L_max 2)
+// runs one forward and one reverse pass per group of source components, as
+// the evaluator does: the forward's first pass assigns Phi1 and the others
+// add to it; every reverse pass subtracts its force part and writes its own
+// source components of W.
+//
 // Each configured model owns one launcher slot: the descriptor of a
 // configure call holds function pointers instantiated for that slot, so a
-// loader that keeps an earlier descriptor keeps launching that model.  The
-// reverse workspace belongs to the state and only grows (at a launch that
-// needs more, or at smx_r1_plugin_reserve); an event orders its reuse
-// across streams.
+// loader that keeps an earlier descriptor keeps launching that model.  A
+// configure call with the same model file (same bytes) and the same
+// identity returns the existing descriptor instead of taking a new slot.
+// Configure is host-only; the coupling table goes to the device at the first
+// launch or smx_r1_plugin_reserve.  The reverse workspace belongs to the
+// state and only grows (at a launch that needs more, or at
+// smx_r1_plugin_reserve); an event orders its reuse across streams.
 #include <hip/hip_runtime.h>
 
 #include <atomic>
 #include <climits>
 #include <cmath>
+#include <cstdio>
 #include <cstring>
 #include <memory>
 #include <mutex>
 #include <stdexcept>
 #include <string>
+#include <tuple>
+#include <utility>
 #include <vector>
 
 #include "../../include/symmetrix_r1_plugin.h"
@@ -57,16 +71,50 @@ __global__ __launch_bounds__(256) void k_offsets_from_receivers(int N, int E, co
     offsets[i] = lo;
 }
 
+// A compiled plugin shape: kernel lanes C, l_max, L_max and the caller's
+// channel count CF (<= C).
+template <int C_, int LMAX_, int LMAXH_, int CF_>
+struct PluginShape {
+    static constexpr int C = C_, LMAX = LMAX_, LMAXH = LMAXH_, CF = CF_;
+    using S = Shape<LMAX, LMAXH>;
+    using Groups = SourceGroups<LMAX, LMAXH>;
+    using Edges = PluginEdges<S::NY, C, CF>;
+    static constexpr int kGroups = static_cast<int>(Groups::masks.size());
+};
+using PluginShapes = std::tuple<PluginShape<32, 2, 1, 32>, PluginShape<128, 3, 1, 128>, PluginShape<128, 3, 0, 128>,
+                                PluginShape<128, 3, 0, 96>, PluginShape<128, 3, 2, 128>, PluginShape<256, 3, 2, 256>,
+                                PluginShape<256, 3, 2, 224>>;
+
+// f(PluginShape{}) for the shape (C, l_max, L_max, CF); false if none
+template <std::size_t I = 0, class F>
+bool with_shape(int C, int l_max, int L_max, int CF, F&& f) {
+    if constexpr (I < std::tuple_size_v<PluginShapes>) {
+        using PS = std::tuple_element_t<I, PluginShapes>;
+        if (PS::C == C && PS::LMAX == l_max && PS::LMAXH == L_max && PS::CF == CF) {
+            f(PS{});
+            return true;
+        }
+        return with_shape<I + 1>(C, l_max, L_max, CF, std::forward<F>(f));
+    } else {
+        return false;
+    }
+}
+
 struct PluginState {
     SymmetrixJitHipPluginV1 descriptor{};
-    std::string artifact_id, contract, semantic, structure, features, arch = "gfx950";
-    int C = 0, l_max = 0, L_max = 0, NY = 0, NH = 0, NLME = 0, functions = 0;
+    // identity: the model file (path and a digest of its bytes) and the
+    // caller's identity fields
+    std::string path, artifact_id, contract, semantic, structure, features, arch = "gfx950";
+    std::uint64_t file_digest = 0;
+    int embedding = 0, persistent = 0;
+    int C = 0, CF = 0, l_max = 0, L_max = 0, NY = 0, NH = 0, NLME = 0, functions = 0;
     int fp64_point = 0;
-    float* cg = nullptr;  // dense per-path coupling blocks (device)
-    std::vector<float> spline;  // [intervals][4][functions]
+    std::vector<float> cg_host;   // dense per-path coupling blocks
+    float* cg = nullptr;          // their device copy (first launch or reserve)
+    std::mutex dev_mutex;
+    std::vector<float> spline;  // [intervals][4][functions], functions = paths * CF
     int intervals = 0;
     double h = 0.0, x0 = 0.0;
-    bool configured = false;
     // reverse workspace: receiver offsets and per-edge source terms W
     std::mutex ws_mutex;
     void* ws = nullptr;
@@ -80,7 +128,42 @@ struct PluginState {
         if (ws_done) (void)hipEventDestroy(ws_done);
         if (cg) (void)hipFree(cg);
     }
+    bool same_identity(const PluginState& o) const {
+        return path == o.path && file_digest == o.file_digest && artifact_id == o.artifact_id &&
+               contract == o.contract && semantic == o.semantic && structure == o.structure &&
+               features == o.features && embedding == o.embedding && persistent == o.persistent &&
+               fp64_point == o.fp64_point;
+    }
 };
+
+// The coupling table on the device (uploaded once, on the current device).
+hipError_t ensure_device_tables(PluginState& st) {
+    std::lock_guard<std::mutex> lock(st.dev_mutex);
+    if (st.cg) return hipSuccess;
+    float* p = nullptr;
+    hipError_t e = hipMalloc(&p, std::max<std::size_t>(1, st.cg_host.size()) * sizeof(float));
+    if (e != hipSuccess) return e;
+    e = hipMemcpy(p, st.cg_host.data(), st.cg_host.size() * sizeof(float), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(p);
+        return e;
+    }
+    st.cg = p;
+    return hipSuccess;
+}
+
+// FNV-1a digest of a file's bytes
+std::uint64_t file_digest(const std::string& path) {
+    FILE* f = std::fopen(path.c_str(), "rb");
+    if (!f) throw std::invalid_argument("cannot open model file '" + path + "'");
+    std::uint64_t h = 1469598103934665603ull;
+    unsigned char buf[1 << 16];
+    std::size_t n;
+    while ((n = std::fread(buf, 1, sizeof(buf), f)) > 0)
+        for (std::size_t i = 0; i < n; ++i) h = (h ^ buf[i]) * 1099511628211ull;
+    std::fclose(f);
+    return h;
+}
 
 // Bytes of the reverse workspace for a graph: receiver offsets [N+1] padded
 // to 256 B, then W [E][NH][C] floats.
@@ -121,17 +204,17 @@ hipError_t grow_workspace(PluginState& st, std::size_t bytes) {
 std::mutex g_mutex;
 // configured states, each bound to one launcher slot; they stay alive because
 // a loader may still hold their descriptor
-constexpr int kSlots = 8;
+constexpr int kSlots = 16;
 std::vector<std::unique_ptr<PluginState>> g_states;
 std::atomic<PluginState*> g_slot[kSlots];
 PluginState* g_active = nullptr;  // the query's answer (guarded by g_mutex)
 
-template <int NY>
-PluginEdges<NY> plugin_edges(const PluginState& st, const SymmetrixJitHipRadialSplineV1& radial,
-                             const double* radius, const void* harm, const void* grad, const void* xyz, bool unit,
-                             const int* node_types, const int* neigh_types, const int* type_to_active,
-                             unsigned active_types, double cutoff) {
-    PluginEdges<NY> p;
+template <class PS>
+typename PS::Edges plugin_edges(const PluginState& st, const SymmetrixJitHipRadialSplineV1& radial,
+                                const double* radius, const void* harm, const void* grad, const void* xyz, bool unit,
+                                const int* node_types, const int* neigh_types, const int* type_to_active,
+                                unsigned active_types, double cutoff) {
+    typename PS::Edges p;
     p.radius = radius;
     p.harm = static_cast<const float*>(harm);
     p.grad = static_cast<const float*>(grad);
@@ -158,7 +241,7 @@ bool radial_ok(const PluginState& st, const SymmetrixJitHipRadialSplineV1& r, un
            std::isfinite(r.h) && r.h > 0.0 && std::isfinite(r.x0);
 }
 
-template <int C, int LMAX, int LMAXH, int SLOT>
+template <class PS, int SLOT>
 int32_t forward_launch(const SymmetrixJitHipR1ForwardArgsV1* a, void* stream, int32_t persistent_blocks) {
     PluginState* st = g_slot[SLOT].load(std::memory_order_acquire);
     if (!st || !a || a->struct_size < sizeof(SymmetrixJitHipR1ForwardArgsV1) || a->num_nodes < 0 ||
@@ -171,18 +254,22 @@ int32_t forward_launch(const SymmetrixJitHipR1ForwardArgsV1* a, void* stream, in
         !a->output || (a->num_edges > 0 && (!a->neigh_indices || !a->neigh_types || !a->radius ||
                                             !a->harmonics_values)))
         return static_cast<int32_t>(hipErrorInvalidValue);
-    using S = Shape<LMAX, LMAXH>;
-    const auto edges = plugin_edges<S::NY>(*st, a->radial, a->radius, a->harmonics_values, nullptr, nullptr, false,
-                                           a->node_types, a->neigh_types, a->type_to_active, a->active_type_count,
-                                           a->cutoff);
-    static_assert(SourceGroups<LMAX, LMAXH>::masks.size() == 1, "the plugin runs single-pass shapes");
-    constexpr unsigned kAll = SourceGroups<LMAX, LMAXH>::masks[0];
-    k_r1_forward<C, LMAX, LMAXH, kAll, false, PluginEdges<S::NY>><<<static_cast<unsigned>(a->num_nodes), C, 0,
-                                                      static_cast<hipStream_t>(stream)>>>(
-        0, a->num_nodes, a->first_neigh, a->num_neigh, a->neigh_indices, edges,
-        static_cast<const float*>(a->neighbor_features),
-        st->cg, static_cast<float*>(a->output));
-    return static_cast<int32_t>(hipPeekAtLastError());
+    hipError_t err = ensure_device_tables(*st);
+    if (err != hipSuccess) return static_cast<int32_t>(err);
+    const auto edges = plugin_edges<PS>(*st, a->radial, a->radius, a->harmonics_values, nullptr, nullptr, false,
+                                        a->node_types, a->neigh_types, a->type_to_active, a->active_type_count,
+                                        a->cutoff);
+    const auto hs = static_cast<hipStream_t>(stream);
+    static_for<0, PS::kGroups>([&](auto gc) {
+        constexpr int gi = gc;
+        if (err != hipSuccess) return;
+        k_r1_forward<PS::C, PS::LMAX, PS::LMAXH, PS::Groups::masks[gi], (gi > 0), typename PS::Edges, PS::CF>
+            <<<static_cast<unsigned>(a->num_nodes), PS::C, 0, hs>>>(
+                0, static_cast<int>(a->num_nodes), a->first_neigh, a->num_neigh, a->neigh_indices, edges,
+                static_cast<const float*>(a->neighbor_features), st->cg, static_cast<float*>(a->output));
+        err = hipPeekAtLastError();
+    });
+    return static_cast<int32_t>(err);
 }
 
 // Checks of the reverse packets (jit_codegen.py:3346-3410); hipSuccess when
@@ -208,10 +295,9 @@ hipError_t check_reverse(const PluginState* st, const SymmetrixJitHipR1SourceArg
 
 // The reverse kernels over a workspace of reverse_workspace_bytes(N, E):
 // receiver offsets, then W.
-template <int C, int LMAX, int LMAXH>
+template <class PS>
 hipError_t reverse_kernels(const PluginState& st, const SymmetrixJitHipR1SourceArgsV1* s,
                            const SymmetrixJitHipR1EdgeArgsV1* e, hipStream_t hs, void* ws) {
-    using S = Shape<LMAX, LMAXH>;
     const int N = static_cast<int>(s->num_nodes);
     const std::int64_t E = s->num_edges;
     const bool unit = e->coordinates_are_unit != 0;
@@ -219,24 +305,34 @@ hipError_t reverse_kernels(const PluginState& st, const SymmetrixJitHipR1SourceA
     float* W = reinterpret_cast<float*>(static_cast<char*>(ws) + reverse_offsets_bytes(N));
     k_offsets_from_receivers<<<blocks_for(static_cast<std::int64_t>(N) + 1, 256), 256, 0, hs>>>(
         N, static_cast<int>(E), e->edge_receivers, offsets);
-    const auto edges = plugin_edges<S::NY>(st, e->radial, e->radius, e->harmonics_values, e->harmonics_gradients,
-                                           e->xyz, unit, e->node_types, e->neigh_types, e->type_to_active,
-                                           e->active_type_count, e->cutoff);
-    constexpr unsigned kAll = SourceGroups<LMAX, LMAXH>::masks[0];
-    k_r1_reverse<C, LMAX, LMAXH, kAll, true, PluginEdges<S::NY>><<<static_cast<unsigned>(N), C, 0, hs>>>(
-        0, 0, offsets, e->neigh_indices, edges, static_cast<const float*>(e->neighbor_features), st.cg,
-        static_cast<const float*>(e->output_adjoint), W, e->directed_forces);
-    k_source_gather<C, S::NH, true><<<static_cast<unsigned>(N), C, 0, hs>>>(
+    hipError_t err = hipPeekAtLastError();
+    const auto edges = plugin_edges<PS>(st, e->radial, e->radius, e->harmonics_values, e->harmonics_gradients,
+                                        e->xyz, unit, e->node_types, e->neigh_types, e->type_to_active,
+                                        e->active_type_count, e->cutoff);
+    static_for<0, PS::kGroups>([&](auto gc) {
+        constexpr int gi = gc;
+        if (err != hipSuccess) return;
+        k_r1_reverse<PS::C, PS::LMAX, PS::LMAXH, PS::Groups::masks[gi], true, typename PS::Edges, PS::CF>
+            <<<static_cast<unsigned>(N), PS::C, 0, hs>>>(0, 0, offsets, e->neigh_indices, edges,
+                                                         static_cast<const float*>(e->neighbor_features), st.cg,
+                                                         static_cast<const float*>(e->output_adjoint), W,
+                                                         e->directed_forces);
+        err = hipPeekAtLastError();
+    });
+    if (err != hipSuccess) return err;
+    k_source_gather<PS::C, PS::S::NH, true, PS::CF><<<static_cast<unsigned>(N), PS::C, 0, hs>>>(
         s->source_offsets, s->source_edges, W, e->radius, e->cutoff, static_cast<float*>(s->source_adjoint));
     return hipPeekAtLastError();
 }
 
-template <int C, int LMAX, int LMAXH, int SLOT>
+template <class PS, int SLOT>
 int32_t reverse_launch(const SymmetrixJitHipR1SourceArgsV1* s, const SymmetrixJitHipR1EdgeArgsV1* e, void* stream,
                        int32_t persistent_blocks) {
     PluginState* st = g_slot[SLOT].load(std::memory_order_acquire);
     hipError_t err = check_reverse(st, s, e, persistent_blocks);
     if (err != hipSuccess || s->num_nodes == 0 || s->num_edges == 0) return static_cast<int32_t>(err);
+    err = ensure_device_tables(*st);
+    if (err != hipSuccess) return static_cast<int32_t>(err);
     const auto hs = static_cast<hipStream_t>(stream);
     std::lock_guard<std::mutex> lock(st->ws_mutex);
     err = grow_workspace(*st, reverse_workspace_bytes(*st, s->num_nodes, s->num_edges));
@@ -246,7 +342,7 @@ int32_t reverse_launch(const SymmetrixJitHipR1SourceArgsV1* s, const SymmetrixJi
         err = hipStreamWaitEvent(hs, st->ws_done, 0);
         if (err != hipSuccess) return static_cast<int32_t>(err);
     }
-    err = reverse_kernels<C, LMAX, LMAXH>(*st, s, e, hs, st->ws);
+    err = reverse_kernels<PS>(*st, s, e, hs, st->ws);
     const hipError_t rec = hipEventRecord(st->ws_done, hs);
     st->ws_stream = hs;
     st->ws_used = true;
@@ -254,17 +350,15 @@ int32_t reverse_launch(const SymmetrixJitHipR1SourceArgsV1* s, const SymmetrixJi
 }
 
 // Launcher pointers of one shape for slot `slot`.
-template <int C, int LMAX, int LMAXH, int SLOT = 0>
-bool slot_launchers(int slot, SymmetrixJitHipR1ForwardLaunchV1& fwd, SymmetrixJitHipR1CoordinateReverseLaunchV1& rev) {
+template <class PS, int SLOT = 0>
+void slot_launchers(int slot, SymmetrixJitHipR1ForwardLaunchV1& fwd, SymmetrixJitHipR1CoordinateReverseLaunchV1& rev) {
     if constexpr (SLOT < kSlots) {
         if (slot == SLOT) {
-            fwd = &forward_launch<C, LMAX, LMAXH, SLOT>;
-            rev = &reverse_launch<C, LMAX, LMAXH, SLOT>;
-            return true;
+            fwd = &forward_launch<PS, SLOT>;
+            rev = &reverse_launch<PS, SLOT>;
+            return;
         }
-        return slot_launchers<C, LMAX, LMAXH, SLOT + 1>(slot, fwd, rev);
-    } else {
-        return false;
+        slot_launchers<PS, SLOT + 1>(slot, fwd, rev);
     }
 }
 
@@ -335,6 +429,14 @@ int32_t smx_r1_plugin_reverse_launch_noalloc(const SymmetrixJitHipPluginV1* plug
                             std::to_string(st->NH * st->C * sizeof(float)) + " bytes per edge at this shape)");
         return static_cast<int32_t>(hipErrorInvalidValue);
     }
+    {
+        std::lock_guard<std::mutex> lock(st->dev_mutex);
+        if (!st->cg) {
+            smx::set_last_error("the allocation-free R1 reverse launch needs the model's tables on the device: "
+                                "call smx_r1_plugin_reserve (or one launch) with this descriptor first");
+            return static_cast<int32_t>(hipErrorNotInitialized);
+        }
+    }
     void* ws = nullptr;
     err = smx::scratch_address(&ws);
     if (err != hipSuccess) {
@@ -342,12 +444,9 @@ int32_t smx_r1_plugin_reverse_launch_noalloc(const SymmetrixJitHipPluginV1* plug
         return static_cast<int32_t>(err);
     }
     const auto hs = static_cast<hipStream_t>(stream);
-    if (st->C == 32 && st->l_max == 2 && st->L_max == 1)
-        err = smx::reverse_kernels<32, 2, 1>(*st, s, e, hs, ws);
-    else if (st->C == 128 && st->l_max == 3 && st->L_max == 1)
-        err = smx::reverse_kernels<128, 3, 1>(*st, s, e, hs, ws);
-    else
-        err = hipErrorInvalidValue;
+    err = hipErrorInvalidValue;
+    smx::with_shape(st->C, st->l_max, st->L_max, st->CF,
+                    [&](auto ps) { err = smx::reverse_kernels<decltype(ps)>(*st, s, e, hs, ws); });
     return static_cast<int32_t>(err);
 }
 
@@ -365,54 +464,68 @@ int32_t smx_r1_plugin_configure(const char* model_path, const SmxR1PluginIdentit
             throw std::invalid_argument("artifact id and contract fingerprint are required");
         if (id->embedding <= 0 || id->persistent_blocks_per_compute_unit <= 0)
             throw std::invalid_argument("embedding and persistent blocks per compute unit must be positive");
-        std::lock_guard<std::mutex> lock(smx::g_mutex);
-        smx::HostModel hm;
-        hm.load(model_path, "");
         auto st = std::make_unique<smx::PluginState>();
-        st->C = hm.C;
-        st->l_max = hm.l_max;
-        st->L_max = hm.L_max;
-        st->NY = hm.num_lm;
-        st->NH = hm.num_LM;
-        st->NLME = hm.num_lme;
-        st->functions = hm.num_paths * hm.C;
-        st->fp64_point = id->fp64_evaluation_point ? 1 : 0;
-        SymmetrixJitHipR1ForwardLaunchV1 fwd = nullptr;
-        SymmetrixJitHipR1CoordinateReverseLaunchV1 rev = nullptr;
-        std::vector<int> le, ls, lo;
-        if (!smx::kernel_paths(hm.l_max, hm.L_max, le, ls, lo) || le != hm.path_le ||
-            ls != hm.path_ls || lo != hm.path_lo)
-            throw std::domain_error("the model's R1 paths have no compiled kernels");
-        const int slot = static_cast<int>(smx::g_states.size());
-        if (slot >= smx::kSlots)
-            throw std::logic_error("at most " + std::to_string(smx::kSlots) +
-                                   " R1 plugin models can be configured in one process");
-        if (hm.C == 32 && hm.l_max == 2 && hm.L_max == 1) {
-            smx::slot_launchers<32, 2, 1>(slot, fwd, rev);
-        } else if (hm.C == 128 && hm.l_max == 3 && hm.L_max == 1) {
-            smx::slot_launchers<128, 3, 1>(slot, fwd, rev);
-        } else {
-            throw std::domain_error("no R1 kernels are compiled for " + std::to_string(hm.C) + " channels, l_max " +
-                                    std::to_string(hm.l_max) + ", L_max " + std::to_string(hm.L_max));
-        }
-        const std::vector<float>& cg = hm.cg_dense;
-        SMX_HIP(hipMalloc(&st->cg, std::max<std::size_t>(1, cg.size()) * sizeof(float)));
-        SMX_HIP(hipMemcpy(st->cg, cg.data(), cg.size() * sizeof(float), hipMemcpyHostToDevice));
-        // spline table in the plugin layout [interval][4][function]
-        st->intervals = hm.spline_points - 1;
-        st->h = hm.h;
-        st->x0 = hm.grid_min;
-        st->spline.assign(static_cast<std::size_t>(st->intervals) * 4 * st->functions, 0.0f);
-        for (int iv = 0; iv < st->intervals; ++iv)
-            for (int f = 0; f < st->functions; ++f)
-                for (int c = 0; c < 4; ++c)
-                    st->spline[(static_cast<std::size_t>(iv) * 4 + c) * st->functions + f] =
-                        hm.R1_coef[(static_cast<std::size_t>(iv) * st->functions + f) * 4 + c];
+        st->path = model_path;
+        st->file_digest = smx::file_digest(st->path);
         st->artifact_id = id->artifact_id;
         st->contract = id->contract_fingerprint;
         st->semantic = id->semantic_fingerprint ? id->semantic_fingerprint : "";
         st->structure = id->structure_fingerprint ? id->structure_fingerprint : "";
         st->features = id->target_features ? id->target_features : "";
+        st->embedding = id->embedding;
+        st->persistent = id->persistent_blocks_per_compute_unit;
+        st->fp64_point = id->fp64_evaluation_point ? 1 : 0;
+        std::lock_guard<std::mutex> lock(smx::g_mutex);
+        // the same model file and identity: the existing descriptor
+        for (const auto& p : smx::g_states)
+            if (p->same_identity(*st)) {
+                smx::g_active = p.get();
+                return SMX_OK;
+            }
+        const int slot = static_cast<int>(smx::g_states.size());
+        if (slot >= smx::kSlots)
+            throw std::logic_error("at most " + std::to_string(smx::kSlots) +
+                                   " distinct R1 plugin models can be configured in one process");
+        smx::HostModel hm;
+        hm.load(model_path, "");
+        // the evaluator's lane rule: 96 and 224 channels run on 128 and 256
+        // lanes (the file's channel count stays the caller's array stride)
+        if (hm.C > 32 && hm.C % 64 != 0 && hm.C % 16 == 0) hm.pad_channels((hm.C + 63) / 64 * 64);
+        if (hm.single_layer || hm.num_paths == 0)
+            throw std::domain_error("a one-interaction model has no R1 operator");
+        st->C = hm.C;
+        st->CF = hm.C_file;
+        st->l_max = hm.l_max;
+        st->L_max = hm.L_max;
+        st->NY = hm.num_lm;
+        st->NH = hm.num_LM;
+        st->NLME = hm.num_lme;
+        st->functions = hm.num_paths * hm.C_file;
+        std::vector<int> le, ls, lo;
+        if (!smx::kernel_paths(hm.l_max, hm.L_max, le, ls, lo) || le != hm.path_le ||
+            ls != hm.path_ls || lo != hm.path_lo)
+            throw std::domain_error("the model's R1 paths have no compiled kernels");
+        SymmetrixJitHipR1ForwardLaunchV1 fwd = nullptr;
+        SymmetrixJitHipR1CoordinateReverseLaunchV1 rev = nullptr;
+        if (!smx::with_shape(hm.C, hm.l_max, hm.L_max, hm.C_file,
+                             [&](auto ps) { smx::slot_launchers<decltype(ps)>(slot, fwd, rev); }))
+            throw std::domain_error("no R1 kernels are compiled for " + std::to_string(hm.C_file) +
+                                    " channels, l_max " + std::to_string(hm.l_max) + ", L_max " +
+                                    std::to_string(hm.L_max));
+        st->cg_host = hm.cg_dense;
+        // spline table in the plugin layout [interval][4][function] over the
+        // file's channels (the model's table is padded to C lanes)
+        st->intervals = hm.spline_points - 1;
+        st->h = hm.h;
+        st->x0 = hm.grid_min;
+        st->spline.assign(static_cast<std::size_t>(st->intervals) * 4 * st->functions, 0.0f);
+        const int padded_functions = hm.num_paths * hm.C;
+        for (int iv = 0; iv < st->intervals; ++iv)
+            for (int p = 0; p < hm.num_paths; ++p)
+                for (int k = 0; k < hm.C_file; ++k)
+                    for (int c = 0; c < 4; ++c)
+                        st->spline[(static_cast<std::size_t>(iv) * 4 + c) * st->functions + p * hm.C_file + k] =
+                            hm.R1_coef[(static_cast<std::size_t>(iv) * padded_functions + p * hm.C + k) * 4 + c];
         SymmetrixJitHipPluginV1& d = st->descriptor;
         std::memset(&d, 0, sizeof(d));
         d.abi_version = SYMMETRIX_JIT_HIP_PLUGIN_ABI_VERSION_V1;
@@ -427,7 +540,7 @@ int32_t smx_r1_plugin_configure(const char* model_path, const SmxR1PluginIdentit
         d.contract_fingerprint = st->contract.c_str();
         d.semantic_fingerprint = st->semantic.c_str();
         d.structure_fingerprint = st->structure.c_str();
-        d.channels = hm.C;
+        d.channels = hm.C_file;
         d.embedding = id->embedding;
         d.edge_l_max = hm.l_max;
         d.source_l_max = hm.L_max;
@@ -440,7 +553,6 @@ int32_t smx_r1_plugin_configure(const char* model_path, const SmxR1PluginIdentit
         d.persistent_blocks_per_compute_unit = id->persistent_blocks_per_compute_unit;
         d.r1_forward_launch = fwd;
         d.r1_coordinate_reverse_launch = rev;
-        st->configured = true;
         smx::g_states.push_back(std::move(st));
         smx::g_active = smx::g_states.back().get();
         smx::g_slot[slot].store(smx::g_active, std::memory_order_release);
@@ -476,8 +588,11 @@ int32_t smx_r1_plugin_reserve(const SymmetrixJitHipPluginV1* plugin, int64_t num
         smx::set_last_error("node and edge counts must lie in [0, 2^31)");
         return SMX_ERR_INVALID_ARGUMENT;
     }
-    std::lock_guard<std::mutex> lock(st->ws_mutex);
-    const hipError_t e = smx::grow_workspace(*st, smx::reverse_workspace_bytes(*st, num_nodes, num_edges));
+    hipError_t e = smx::ensure_device_tables(*st);
+    if (e == hipSuccess) {
+        std::lock_guard<std::mutex> lock(st->ws_mutex);
+        e = smx::grow_workspace(*st, smx::reverse_workspace_bytes(*st, num_nodes, num_edges));
+    }
     if (e != hipSuccess) {
         smx::set_last_error(std::string("R1 plugin workspace: ") + hipGetErrorString(e));
         return e == hipErrorOutOfMemory ? SMX_ERR_OUT_OF_MEMORY : SMX_ERR_RUNTIME;

@@ -100,8 +100,8 @@ void PairSymmetrixMACEMI355X<DeviceType>::allocate()
 }
 
 // The reference's keywords (pair_symmetrix_mace_kokkos.cpp:180-370) where
-// this build has them: the mode token (only no_domain_decomposition),
-// profile capacity|speed and its low_memory yes|no alias, allow_fixed_workspace
+// this build has them: the mode token (no_domain_decomposition or
+// mpi_message_passing), profile capacity|speed and its low_memory yes|no alias, allow_fixed_workspace
 // yes|no, head NAME, streamed_edges auto|direct, _debug_execution_plan ID,
 // electric_field Ex Ey Ez (MACEField, :207-224).  The JIT artefact keywords
 // name files this build does not load (warned and skipped);
@@ -447,15 +447,17 @@ void PairSymmetrixMACEMI355X<DeviceType>::compute_mpi_message_passing()
         Kokkos::RangePolicy<DeviceType>(0, inum), KOKKOS_LAMBDA(const int ii) { eatom_d(d_ilist(ii)) += ne[ii]; });
   }
   Kokkos::fence();
-  // with unit volume the stress is minus the virial sum over the rank's edges
+  // with unit volume the stress is minus the virial sum over the rank's
+  // edges; a rank's partial sum is not symmetric, so each off-diagonal pair
+  // is averaged as in the no_domain_decomposition mode
   if (eflag_global) eng_vdwl += energy;
   if (vflag_global) {
     virial[0] -= stress[0];
     virial[1] -= stress[4];
     virial[2] -= stress[8];
-    virial[3] -= stress[1];
-    virial[4] -= stress[2];
-    virial[5] -= stress[5];
+    virial[3] -= 0.5 * (stress[1] + stress[3]);
+    virial[4] -= 0.5 * (stress[2] + stress[6]);
+    virial[5] -= 0.5 * (stress[5] + stress[7]);
   }
 }
 

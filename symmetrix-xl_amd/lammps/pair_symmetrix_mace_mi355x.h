@@ -27,8 +27,9 @@
    Requires newton pair on and an atom map.
 
    Built as a LAMMPS KOKKOS package style for HIP (Kokkos_ENABLE_HIP) linked
-   against libsymmetrix_mi355x.so; not compiled in this repository, which
-   has no LAMMPS sources.
+   against libsymmetrix_mi355x.so.  This repository has no LAMMPS sources:
+   its tests type-check the class against stand-ins of the LAMMPS and Kokkos
+   declarations it uses (tests/lammps_stub).
 ------------------------------------------------------------------------- */
 
 #ifdef PAIR_CLASS

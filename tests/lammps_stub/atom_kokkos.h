@@ -1,0 +1,3 @@
+// stand-in for LAMMPS atom_kokkos.h (see lammps_stub.h)
+#pragma once
+#include "lammps_stub.h"

@@ -57,6 +57,25 @@ def test_lammps_pair_style_uses_only_declared_entry_points():
     assert fields - {"reserved"} <= assigned, fields - {"reserved"} - assigned
 
 
+def test_lammps_pair_style_type_checks():
+    """The pair-style class (its settings, coeff, both compute modes and the
+    eight forward/reverse communication callbacks, with their Kokkos lambdas
+    and views) compiles with -fsyntax-only against stand-ins of the LAMMPS
+    and Kokkos declarations it uses (tests/lammps_stub) and the library's
+    real header; the explicit instantiation for the device type makes every
+    member and lambda body checked."""
+    import shutil
+    import subprocess
+    gxx = shutil.which("g++")
+    if gxx is None:
+        pytest.skip("g++ is not available")
+    src = os.path.join(ROOT, "symmetrix-xl_amd", "lammps", "pair_symmetrix_mace_mi355x.cpp")
+    cmd = [gxx, "-std=c++17", "-fsyntax-only", "-Wall", "-Wextra", "-Werror",
+           "-I", os.path.join(ROOT, "tests", "lammps_stub"), "-I", os.path.join(ROOT, "include"), src]
+    out = subprocess.run(cmd, capture_output=True, text=True, timeout=300)
+    assert out.returncode == 0, out.stderr[-4000:]
+
+
 def test_abi_version_and_error_string():
     assert _native.lib.smx_abi_version() == 1
     assert isinstance(_native.lib.smx_last_error(), bytes)

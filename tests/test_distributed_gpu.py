@@ -419,3 +419,58 @@ def test_medium_slabs_sum_to_the_whole_system(medium_model_path):
     np.testing.assert_allclose(e, ew, rtol=0, atol=2e-5)
     np.testing.assert_allclose(f, fw, rtol=0, atol=2e-5)
     np.testing.assert_allclose(st, sw, rtol=0, atol=1e-8)
+
+
+@pytest.mark.parametrize("model", ["tiny", "tiny_residual"])
+def test_pair_style_modes_give_the_same_virial(request, model):
+    """One rank, the same LAMMPS arrays: the virial the pair style's
+    mpi_message_passing compute forms from the split phases (unit-volume
+    stress, each off-diagonal pair averaged) equals the one
+    no_domain_decomposition takes from smx_lammps_compute, and both match
+    -V times the oracle's stress."""
+    from oracle import oracle
+    from symmetrix.mace_kokkos import MACEKokkosFloat
+    from test_lammps_entry import _Hip, _lammps_arrays, _run as lammps_run
+    path = request.getfixturevalue(model + "_model_path")
+    s = _system("tiny")
+    ref = oracle.evaluate_system(oracle.OracleModel(path), s, skin=0.5)
+    ev = MACEKokkosFloat(path)
+    lut = {int(z): i for i, z in enumerate(ev.atomic_numbers)}
+    species = sorted(set(int(z) for z in s["numbers"]))
+    lmp_type = {z: t + 1 for t, z in enumerate(species)}
+    allpos, owner, alltypes, rows = _lammps_arrays(np.asarray(s["positions"], float), np.asarray(s["cell"], float),
+                                                   s["numbers"], ev.r_cut + 0.5, lmp_type)
+    n, nall = len(rows), len(allpos)
+    model_type = np.array([lut[species[t - 1]] for t in alltypes], np.int32)
+    ilist = np.random.default_rng(7).permutation(n).astype(np.int32)
+    neigh = np.concatenate([rows[i] for i in ilist]).astype(np.int32)
+    gen = ev._prepare_factorized_feature_graph(n, nall, ilist, model_type[ilist], model_type,
+                                               np.array([len(rows[i]) for i in ilist], np.int32), neigh,
+                                               model_type[neigh])
+    ev._begin_factorized_distributed_positions_evaluation(gen, allpos)
+    h = ev._distributed_h1()
+    H1 = np.zeros((nall, h.shape[1]), np.float32)
+    H1[ilist] = h
+    H1[n:] = H1[owner[n:]]
+    ev._continue_factorized_distributed_evaluation(H1)
+    adj = ev._distributed_h1_adjoint().astype(np.float64)
+    np.add.at(adj, owner[n:], adj[n:])
+    ev._finish_factorized_distributed_evaluation(adj.astype(np.float32))
+    w = ev._reduce_stress(1.0, None, gen).ravel()
+    mpi_virial = -np.array([w[0], w[4], w[8], 0.5 * (w[1] + w[3]), 0.5 * (w[2] + w[6]), 0.5 * (w[5] + w[7])])
+    hip = _Hip()
+    try:
+        ev2 = MACEKokkosFloat(path)
+        type_to_model = [lut[z] for z in species]
+        _, ndd_virial, _, _ = lammps_run(ev2, hip, allpos, owner, alltypes, rows, ilist, type_to_model, True)
+    finally:
+        hip.free()
+    ndd_virial = np.asarray(ndd_virial, float)
+    V = abs(np.linalg.det(np.asarray(s["cell"], float)))
+    st = ref["stress"]
+    oracle_virial = -V * np.array([st[0, 0], st[1, 1], st[2, 2], 0.5 * (st[0, 1] + st[1, 0]),
+                                   0.5 * (st[0, 2] + st[2, 0]), 0.5 * (st[1, 2] + st[2, 1])])
+    print("virial mpi", mpi_virial, "ndd", ndd_virial)
+    scale = max(1.0, np.max(np.abs(oracle_virial)))
+    np.testing.assert_allclose(mpi_virial, ndd_virial, rtol=0, atol=1e-6 * scale)
+    np.testing.assert_allclose(mpi_virial, oracle_virial, rtol=0, atol=1e-6 * V)

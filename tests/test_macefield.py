@@ -180,3 +180,62 @@ def test_oracle_refuses_inconsistent_field_models(tmp_path, tiny_field_model_pat
         oracle.evaluate_system(om, s, skin=0.5)
     with pytest.raises(ValueError, match="electric_field"):
         oracle.evaluate_system(om, s, skin=0.5, field=np.zeros(6))
+
+
+def _library_refusal(path):
+    """Creates an evaluator through the C ABI; the model loader runs before
+    any device call, so its refusals show on a host without a GPU."""
+    import ctypes
+
+    from symmetrix import _native
+    h = ctypes.c_void_p()
+    rc = _native.lib.smx_evaluator_create(path.encode(), b"", ctypes.byref(h))
+    if rc == 0:
+        _native.lib.smx_evaluator_destroy(h)
+    return rc, _native.lib.smx_last_error().decode()
+
+
+def test_library_loader_refuses_malformed_couplings(tmp_path, tiny_field_model_path, field_l2_model_path):
+    """The product loader's schema checks (the constraints field_coupling.hpp:
+    60-238 enforces), each broken once on an otherwise valid model."""
+    from symmetrix import _native
+    doc = _doc(tiny_field_model_path)
+    cases = {
+        "two couplings": (lambda d: d["field_couplings"].append(copy.deepcopy(d["field_couplings"][0])),
+                          "one coupling"),
+        "schema": (lambda d: d["field_couplings"][0].__setitem__("schema_version", 2), "schema_version 2"),
+        "irreps": (lambda d: d["field_couplings"][0].__setitem__("field_feats_irreps_in2", "1x1e"),
+                   "field_feats_irreps_in2"),
+        "mask": (lambda d: d["field_couplings"][0]["field_linear_output_mask"].__setitem__(3, 0.5),
+                 "field_linear_output_mask"),
+        "bias": (lambda d: d["field_couplings"][0].__setitem__("field_linear_bias", [0.0]), "field_linear_bias"),
+        "rank": (lambda d: d["field_couplings"][0]["field_feats_instructions"][0].__setitem__("i_out", 0),
+                 "field_feats_instructions[0]"),
+        "mode": (lambda d: d["field_couplings"][0]["field_feats_instructions"][0].__setitem__(
+            "connection_mode", "uuu"), "uvw"),
+        "mix block": (lambda d: d["field_couplings"][0]["field_linear_instructions"][0].__setitem__("i_out", 9),
+                      "field_linear_instructions[0]"),
+        "feats weight": (lambda d: d["field_couplings"][0].__setitem__(
+            "field_feats_weight", d["field_couplings"][0]["field_feats_weight"][:-1]), "field_feats_weight"),
+        "no split": (lambda d: d.pop("H1_linear_up_weights"), "H1_linear_up_weights"),
+        "unread block": (lambda d: d["field_couplings"][0].__setitem__(
+            "field_linear_instructions", [i for i in d["field_couplings"][0]["field_linear_instructions"]
+                                          if i["i_in"] != 1]), None),
+    }
+    for name, (edit, needle) in cases.items():
+        d = copy.deepcopy(doc)
+        edit(d)
+        rc, msg = _library_refusal(_write(tmp_path, "bad.json", d))
+        assert rc == _native.SMX_ERR_INVALID_ARGUMENT, (name, msg)
+        assert msg.startswith("field coupling:"), (name, msg)
+        if needle:
+            assert needle in msg, (name, msg)
+    # an L_max 2 coupling needs its 3j tensors; without schema_version it is refused
+    d2 = _doc(field_l2_model_path)
+    del d2["field_couplings"][0]["schema_version"]
+    rc, msg = _library_refusal(_write(tmp_path, "unversioned_l2.json", d2))
+    assert rc == _native.SMX_ERR_INVALID_ARGUMENT and "schema_version" in msg, msg
+    # the valid files pass the loader (no device here: the next step, if any, fails on the device)
+    for good in (tiny_field_model_path, field_l2_model_path):
+        rc, msg = _library_refusal(good)
+        assert rc != _native.SMX_ERR_INVALID_ARGUMENT, msg

@@ -49,12 +49,12 @@ class _PluginCase:
     """Device arrays of the tiny system in the reference's per-edge layout,
     with the oracle's R1 stages as inputs and references."""
 
-    def __init__(self, model_path, cells=3):
+    def __init__(self, model_path, cells=3, system=None):
         from _hip import DeviceArray
         from oracle import oracle
         from symmetrix import systems
 
-        s = systems.srtio3_supercell(cells, sigma=0.05, seed=0)
+        s = system if system is not None else systems.srtio3_supercell(cells, sigma=0.05, seed=0)
         om = oracle.OracleModel(model_path)
         ref = oracle.evaluate_system(om, s, skin=0.5)
         self.om, self.ref = om, ref
@@ -63,7 +63,11 @@ class _PluginCase:
         self.E = E = len(g["sources"])
         self.C = om.num_channels
         types = om.types_of(s["numbers"]).astype(np.int32)
-        self.ntypes = ntypes = int(types.max()) + 1
+        # active types: the types present, numbered in order (type_to_active)
+        active = np.unique(types)
+        self.ntypes = len(active)
+        tmap = np.full(int(types.max()) + 1, 0, np.int32)
+        tmap[active] = np.arange(len(active), dtype=np.int32)
         self.offsets = offsets = g["offsets"].astype(np.int32)
         self.sources = sources = g["sources"].astype(np.int32)
         self.receivers = receivers = np.repeat(np.arange(N, dtype=np.int32), np.diff(offsets))
@@ -72,7 +76,7 @@ class _PluginCase:
         self.d_first = DeviceArray(offsets[:-1].copy())
         self.d_src = DeviceArray(sources)
         self.d_ntypes = DeviceArray(types[sources])
-        self.d_map = DeviceArray(np.arange(ntypes, dtype=np.int32))
+        self.d_map = DeviceArray(tmap)
         self.d_r = DeviceArray(ref["r"].astype(np.float64))
         self.d_xyz = DeviceArray(ref["xyz"].astype(np.float64))
         self.d_Y = DeviceArray(om.stage("Y").astype(np.float32))
@@ -107,10 +111,14 @@ class _PluginCase:
         return out.get(), fa
 
     def reverse(self, d, radial, launch=None):
-        """(source adjoint added to 0.25, forces subtracted from -0.5) of one
-        reverse launch through d (or through `launch`, same arguments)."""
+        """(source adjoint added to a quarter of its scale, forces subtracted
+        from -0.5) of one reverse launch through d (or through `launch`, same
+        arguments).  The base is scaled like the adjoint so that its FP32
+        rounding stays below the comparison's bar."""
         from _hip import DeviceArray, hip
-        base_adj = np.full(self.om.stage("H1_adj").shape, 0.25, np.float32)
+        ref = self.om.stage("H1_adj")
+        base = np.float32(0.25 * max(np.max(np.abs(ref)), 1e-30))
+        base_adj = np.full(ref.shape, base, np.float32)
         d_adj = DeviceArray(base_adj)
         base_f = np.full((self.E, 3), -0.5, np.float64)
         d_f = DeviceArray(base_f)
@@ -125,7 +133,7 @@ class _PluginCase:
         rc = (launch or d.r1_coordinate_reverse_launch)(ctypes.byref(sa), ctypes.byref(ea), None, 1)
         assert rc == 0, rc
         assert hip().hipDeviceSynchronize() == 0
-        return d_adj.get().astype(np.float64) - 0.25, d_f.get() - base_f
+        return d_adj.get().astype(np.float64) - np.float64(base), d_f.get() - base_f
 
 
 @pytest.mark.gpu
@@ -192,3 +200,96 @@ def test_descriptor_keeps_its_model_after_another_configure(tiny_model_path, tmp
     np.testing.assert_array_equal(adjA2, adjA)
     np.testing.assert_array_equal(fA2, fA)
     assert _native.lib.smx_r1_plugin_reserve(None, case.N, case.E) == _native.SMX_ERR_INVALID_ARGUMENT
+
+
+def test_configure_reuses_a_slot_for_the_same_model_and_identity(tmp_path):
+    """Configure is host work: the same model bytes and identity give back
+    the same descriptor however often they are configured; distinct models
+    take launcher slots up to the library's limit, after which configure is
+    refused (run in a child process, whose slots are its own)."""
+    import subprocess
+    import sys
+    import textwrap
+    from symmetrix import random_model
+    tiny = random_model.cached_model("tiny")
+    script = textwrap.dedent("""
+        import ctypes, json, shutil, sys
+        sys.path[:0] = %r
+        from symmetrix import _native, r1_plugin
+        tiny, tmp = %r, %r
+        first = r1_plugin._query
+        d1 = r1_plugin.configure(tiny, artifact_id="same", contract_fingerprint="fp")
+        p1 = ctypes.addressof(r1_plugin._query().contents)
+        for _ in range(40):
+            r1_plugin.configure(tiny, artifact_id="same", contract_fingerprint="fp")
+            assert ctypes.addressof(r1_plugin._query().contents) == p1
+        # a different identity of the same file takes a new slot
+        r1_plugin.configure(tiny, artifact_id="other", contract_fingerprint="fp")
+        assert ctypes.addressof(r1_plugin._query().contents) != p1
+        # the same path with other bytes is another model
+        j = json.load(open(tiny))
+        j["Phi1_clebsch_gordan"] = [2.0 * c for c in j["Phi1_clebsch_gordan"]]
+        path = tmp + "/changed.json"
+        json.dump(j, open(path, "w"))
+        r1_plugin.configure(path, artifact_id="same", contract_fingerprint="fp")
+        json.dump(dict(j, Phi1_clebsch_gordan=[3.0 * c for c in j["Phi1_clebsch_gordan"]]), open(path, "w"))
+        r1_plugin.configure(path, artifact_id="same", contract_fingerprint="fp")
+        n = 4
+        while True:
+            ident = _native.SmxR1PluginIdentity(ctypes.sizeof(_native.SmxR1PluginIdentity),
+                                                b"id-%%d" %% n, b"fp", b"", b"", b"", 8, 0, 4)
+            rc = _native.lib.smx_r1_plugin_configure(tiny.encode(), ctypes.byref(ident))
+            if rc != 0:
+                break
+            n += 1
+        assert rc == _native.SMX_ERR_LOGIC and b"distinct R1 plugin models" in _native.lib.smx_last_error()
+        # a configured identity still configures once the slots are full
+        r1_plugin.configure(tiny, artifact_id="same", contract_fingerprint="fp")
+        assert ctypes.addressof(r1_plugin._query().contents) == p1
+        print("slots", n)
+    """) % (sys.path, tiny, str(tmp_path))
+    out = subprocess.run([sys.executable, "-c", script], capture_output=True, text=True, timeout=300)
+    assert out.returncode == 0, out.stdout + out.stderr
+    assert "slots 16" in out.stdout, out.stdout
+
+
+def _shape_case(name):
+    """(model path, system) of each evaluator shape beyond the tiny one."""
+    from _compact import compact_model, fixture_system
+    from symmetrix import random_model, systems
+    if name == "wide":
+        return random_model.cached_model("wide"), systems.water_box(num_molecules=120, seed=2)
+    path, _ = compact_model(name)
+    return path, fixture_system(name, cells=2)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", ["wide", "compact_mp0b2_large", "compact_omat0_small", "compact_off23_small",
+                                  "compact_off23_large"])
+def test_plugin_serves_every_evaluator_shape(name):
+    """The launchers of the (256,3,2) wide, (128,3,2) MP-0b2 large and
+    (128,3,0) OMAT-0 small shapes, and of the OFF23 shapes whose 96 and 224
+    channels run on 128 and 256 lanes over the caller's unpadded arrays,
+    against the oracle's R1 stages (L_max 2: one pass per source-component
+    group, as the evaluator runs them)."""
+    path, system = _shape_case(name)
+    print("plugin shape case", name, flush=True)
+    case = _PluginCase(path, system=system)
+    om = case.om
+    d = r1_plugin.configure(path, artifact_id="shape-" + name, contract_fingerprint="fp-" + name, embedding=8)
+    assert d.channels == om.num_channels
+    radial = case.radial()
+    phi_ref = om.stage("Phi1")
+    phi, _ = case.forward(d, radial)
+    err = np.max(np.abs(phi.astype(np.float64) - phi_ref)) / np.max(np.abs(phi_ref))
+    print("%s: Phi1 relative max err %.3e" % (name, err))
+    assert err < 1e-5
+    adj, f = case.reverse(d, radial)
+    h1adj_ref = om.stage("H1_adj")
+    err = np.max(np.abs(adj - h1adj_ref)) / np.max(np.abs(h1adj_ref))
+    print("%s: source adjoint relative max err %.3e" % (name, err))
+    assert err < 1e-5
+    f_ref = om.stage("node_forces_r1").reshape(case.E, 3)
+    ferr = np.max(np.abs(f - f_ref)) / max(1.0, np.max(np.abs(f_ref)))
+    print("%s: R1 directed forces max err %.3e (scale %.3e)" % (name, ferr, np.max(np.abs(f_ref))))
+    assert ferr < 1e-5
