@@ -161,13 +161,18 @@ __device__ __forceinline__ void staged_records(stage4* buf, const stage4* __rest
 // ---------------------------------------------------------------------------
 // Edge-input policies
 // ---------------------------------------------------------------------------
-// Packed records in two parts per edge (tile-local index e - e0): forward
-// [x, interval, active, 0, Y[NY]] (RF floats) and reverse [dY/dX[NY],
-// dY/dY[NY], dY/dZ[NY], u[3], pad] (RB floats); the Hermite table
-// [interval][function] as float4 (c0..c3).  With STAGED a receiver's records
-// (both parts) are staged through LDS in chunks (staged_records2; the
-// fields then sit in VGPRs), else the wave reads the forward part with
-// scalar loads (SGPRs) -- the forward kernels need nothing else.
+// Packed records in two parts per execution slot (tile-local slot e - e0):
+// forward [x, table row, source type + 1 (0: inactive), source node, Y[NY]]
+// (RF floats) and reverse [dY/dX[NY], dY/dY[NY], dY/dZ[NY], u[3], edge row]
+// (RB floats); the Hermite table [row][function] as float4 (c0..c3).  The
+// slots of a receiver hold its edges in execution order (by table row), so
+// consecutive edges often share a row and the kernels keep its coefficients
+// in registers (kReuse); per-edge outputs (directed forces, source terms W)
+// go to the edge's own row in the caller's order (the reverse part's last
+// field, tile-local).  With STAGED a receiver's records (both parts) are
+// staged through LDS in chunks (staged_records2; the fields then sit in
+// VGPRs), else the wave reads the forward part with scalar loads (SGPRs) --
+// the forward kernels need nothing else.
 template <int C, int NY, int RF, int RB, bool STAGED>
 struct RecordEdges {
     const float* __restrict__ erec;    // forward parts [ne][RF]
@@ -178,12 +183,14 @@ struct RecordEdges {
 
     static constexpr int REC = STAGED ? RF + RB : RF;  // record stride where the kernel reads it
     static constexpr int kStageSlots = STAGED ? RecordStage<C, RF + RB>::SLOTS : 1;
+    static constexpr int kEdgeRow = RF + RB - 1;       // caller row field (staged records)
+    static constexpr bool kReuse = true;               // table rows shared by consecutive slots
     // The unstaged records can be read one edge ahead (hold): the fields a
     // forward pass needs, wave-uniform, so they sit in SGPRs.
     static constexpr bool kHold = !STAGED;
     struct Held {
         float x;
-        int iv, active;
+        int iv, active, src;
         float y[NY];
     };
     __device__ __forceinline__ void hold(int e, Held& h) const {
@@ -191,6 +198,7 @@ struct RecordEdges {
         h.x = r[0];
         h.iv = __float_as_int(r[1]);
         h.active = __float_as_int(r[2]);
+        h.src = __float_as_int(r[3]);
 #pragma unroll
         for (int lm = 0; lm < NY; ++lm) h.y[lm] = r[4 + lm];
     }
@@ -199,6 +207,16 @@ struct RecordEdges {
         const float4* cf;
         float x, xx, xxx, x2, xx3;
     };
+    __device__ __forceinline__ int row(const Point& p) const { return __float_as_int(p.rec[1]); }
+    __device__ __forceinline__ float4 coef_at(const Point& p, int f) const { return p.cf[f]; }
+    __device__ __forceinline__ int source(const Point& p, int /*e*/, const int* /*neigh*/) const {
+        return __float_as_int(p.rec[3]);
+    }
+    // tile-local row of the per-edge outputs of slot j of a staged chunk
+    __device__ __forceinline__ long long out_row(const float* chunk, int j, long long /*slot*/) const {
+        static_assert(STAGED, "the caller row is read from staged records");
+        return __float_as_int(chunk[j * REC + kEdgeRow]);
+    }
     // body(first edge, count, staged records of the chunk) over [ea, eb)
     template <class BODY>
     __device__ __forceinline__ void chunks(int ea, int eb, stage4* lds, BODY&& body) const {
@@ -273,11 +291,17 @@ struct PluginEdges {
 
     static constexpr int kStageSlots = 1;
     static constexpr bool kHold = false;
+    static constexpr bool kReuse = false;
     struct Point {
         int e;
         const float* c0;  // coefficient c0 of function 0 of this edge's interval
         float x, xx, xxx, x2, xx3;
     };
+    __device__ __forceinline__ int row(const Point&) const { return 0; }
+    __device__ __forceinline__ float4 coef_at(const Point&, int) const { return float4{}; }
+    __device__ __forceinline__ int source(const Point&, int e, const int* neigh) const { return neigh[e]; }
+    // the caller's arrays are in edge order: slot e writes row e
+    __device__ __forceinline__ long long out_row(const float*, int, long long slot) const { return slot; }
     template <class BODY>
     __device__ __forceinline__ void chunks(int ea, int eb, stage4*, BODY&& body) const {
         for (int c0 = ea; c0 < eb; c0 += kRecordChunk) body(c0, min(kRecordChunk, eb - c0), nullptr);
@@ -394,16 +418,17 @@ struct EdgeForceSink {
             part[r][slot][0] = part[r][slot][1] = part[r][slot][2] = 0.0f;
         }
     }
-    // node_forces[e] = -f (assign) or node_forces[e] -= f (accumulate)
-    template <bool ACCUMULATE>
-    __device__ __forceinline__ void flush(long long c0, int count, double* __restrict__ node_forces) {
+    // node_forces[row(el)] = -f (assign) or node_forces[row(el)] -= f
+    // (accumulate) for the chunk's slots el < count
+    template <bool ACCUMULATE, class ROW>
+    __device__ __forceinline__ void flush(int count, double* __restrict__ node_forces, ROW&& row) {
         __syncthreads();
         for (int t = threadIdx.x; t < count * 3; t += C) {
             const int el = t / 3, comp = t % 3;
             float s = 0.0f;
 #pragma unroll
             for (int r = 0; r < ROWS; ++r) s += part[r][el][comp];
-            double* dst = node_forces + static_cast<std::size_t>(c0 + el) * 3 + comp;
+            double* dst = node_forces + static_cast<std::size_t>(row(el)) * 3 + comp;
             if (ACCUMULATE)
                 *dst = *dst - static_cast<double>(s);
             else
@@ -586,28 +611,32 @@ __global__ __launch_bounds__(C) void k_r1_forward(int r0, int nr, const int* __r
         });
     };
     if constexpr (EDGES::kHold) {
-        // The wave-uniform record fields and source index of edge e+1 are
-        // loaded while edge e runs, so an edge starts with its spline and
-        // H1 loads instead of a chain of dependent scalar loads.
+        // The wave-uniform record fields (source node included) of slot e+1
+        // are loaded while slot e runs, so a slot starts with its spline and
+        // H1 loads instead of a chain of dependent scalar loads.  The table
+        // row's coefficients of the group's paths stay in registers while
+        // consecutive slots share the row.
         static_assert(CF == C, "held records are the evaluator's own, unpadded-stride layout");
         typename EDGES::Held cur, nxt;
-        int src = 0;
-        if (ea < eb) {
-            edges.hold(ea, cur);
-            src = neigh[ea];
-        }
+        float4 cc[S::P];
+        int cached = -1;
+        if (ea < eb) edges.hold(ea, cur);
         for (int e = ea; e < eb; ++e) {
             const int en = min(e + 1, eb - 1);
             edges.hold(en, nxt);
-            const int src_n = neigh[en];
             if (cur.active) {
                 const float x = cur.x, xx = x * x, xxx = xx * x;
-                const float4* cf = edges.coef + static_cast<std::size_t>(cur.iv) * edges.functions;
-                add_edge([&](int p) { return spline_value(cf[p * C + k], x, xx, xxx); },
-                         [&](int lm) { return cur.y[lm]; }, H1 + static_cast<std::size_t>(src) * NH * C + k);
+                if (cur.iv != cached) {
+                    cached = cur.iv;
+                    const float4* cf = edges.coef + static_cast<std::size_t>(cur.iv) * edges.functions;
+                    static_for<0, S::P>([&](auto pc) {
+                        if constexpr (RG::used(pc)) cc[pc] = cf[pc * C + k];
+                    });
+                }
+                add_edge([&](int p) { return spline_value(cc[p], x, xx, xxx); }, [&](int lm) { return cur.y[lm]; },
+                         H1 + static_cast<std::size_t>(cur.src) * NH * C + k);
             }
             cur = nxt;
-            src = src_n;
         }
     } else {
         __shared__ stage4 stage_buf[2 * EDGES::kStageSlots];
@@ -616,8 +645,8 @@ __global__ __launch_bounds__(C) void k_r1_forward(int r0, int nr, const int* __r
                 const int e = e_first + j;
                 typename EDGES::Point pt;
                 if (!edges.open_at(e, i, chunk, j, pt)) continue;
-                add_edge([&](int p) { return edges.value(pt, p * C + k); },
-                         [&](int lm) { return edges.Y(pt, lm); }, H1 + static_cast<std::size_t>(neigh[e]) * NH * CF + k);
+                add_edge([&](int p) { return edges.value(pt, p * C + k); }, [&](int lm) { return edges.Y(pt, lm); },
+                         H1 + static_cast<std::size_t>(edges.source(pt, e, neigh)) * NH * CF + k);
             }
         });
     }
@@ -704,10 +733,11 @@ __global__ __launch_bounds__(C) void k_r1_reverse(int r0, long long e0, const in
         });
     }
     const int ea = offsets[i], eb = offsets[i + 1];
+    [[maybe_unused]] float4 cc[S::P];
+    [[maybe_unused]] int cached = -1;
     edges.chunks(ea, eb, stage_buf, [&](int c0, int n, const float* chunk) __attribute__((always_inline)) {
         for (int j = 0; j < n; ++j) {
             const int e = c0 + j;
-            float* wdst = Wsrc + static_cast<std::size_t>(e - e0) * NH * C + k;
             typename EDGES::Point pt;
             if (!edges.open_at(e, i, chunk, j, pt)) {
                 // inactive edges (r >= cutoff) contribute nothing: their W is
@@ -715,7 +745,19 @@ __global__ __launch_bounds__(C) void k_r1_reverse(int r0, long long e0, const in
                 sink.zero(j);
                 continue;
             }
-            const float* hj = H1 + static_cast<std::size_t>(neigh[e]) * NH * CF + k;
+            float* wdst = Wsrc + static_cast<std::size_t>(edges.out_row(chunk, j, e - e0)) * NH * C + k;
+            if constexpr (EDGES::kReuse) {
+                // the row's coefficients stay in registers while consecutive
+                // slots share it (the row is wave-uniform)
+                const int row = edges.row(pt);
+                if (row != cached) {
+                    cached = row;
+                    static_for<0, S::P>([&](auto pc) {
+                        if constexpr (RG::used(pc)) cc[pc] = edges.coef_at(pt, pc * C + k);
+                    });
+                }
+            }
+            const float* hj = H1 + static_cast<std::size_t>(edges.source(pt, e, neigh)) * NH * CF + k;
             float h[NH], W[NH];
 #pragma unroll
             for (int q = 0; q < NH; ++q) {
@@ -734,7 +776,12 @@ __global__ __launch_bounds__(C) void k_r1_reverse(int r0, long long e0, const in
                 if constexpr (RG::used(p)) {
                     constexpr int le = S::paths[p].le, ls = S::paths[p].ls;
                     float R, dR;
-                    edges.value_slope(pt, p * C + k, R, dR);
+                    if constexpr (EDGES::kReuse) {
+                        R = spline_value(cc[p], pt.x, pt.xx, pt.xxx);
+                        dR = spline_slope(cc[p], pt.x2, pt.xx3);
+                    } else {
+                        edges.value_slope(pt, p * C + k, R, dR);
+                    }
                     float T[2 * ls + 1];
                     static_for<0, 2 * ls + 1>([&](auto m2c) { T[m2c] = 0.0f; });
                     if constexpr (ls == 0) {
@@ -793,7 +840,8 @@ __global__ __launch_bounds__(C) void k_r1_reverse(int r0, long long e0, const in
                 if (RG::component(q)) __builtin_nontemporal_store(W[q], wdst + q * C);
             sink.put(j, edges.u(pt, 0) * A + b0, edges.u(pt, 1) * A + b1, edges.u(pt, 2) * A + b2);
         }
-        sink.template flush<FORCE_ACCUMULATE>(static_cast<long long>(c0) - e0, n, node_forces);
+        sink.template flush<FORCE_ACCUMULATE>(n, node_forces,
+                                              [&](int el) { return edges.out_row(chunk, el, c0 + el - e0); });
     });
 }
 

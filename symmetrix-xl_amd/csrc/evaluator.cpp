@@ -302,7 +302,7 @@ struct Evaluator {
     // per call
     DevBuf d_xyz, d_r, d_invalid;
     DevBuf w_erec, w_Phi0, w_A0, w_M0, w_Phi1, w_A1, w_A1_adj, w_M1, w_dPhi1, w_Wsrc, w_M0_adj, w_A0_adj, w_Phi0_adj,
-        w_node_forces, w_density;
+        w_node_forces, w_density, w_exec;
     DevBuf g_H1p, g_H1f, g_H1p_adj, g_fzy;
     DevBuf g_H1, g_H1_adj, g_xaff, g_direct, g_direct_m0, d_node_energies, d_atom_forces, d_virial, d_stress, d_stress_partial,
         d_total;
@@ -686,7 +686,7 @@ struct Evaluator {
     std::size_t workspace_bytes() const {
         std::size_t b = 0;
         for (const DevBuf* x : {&w_erec, &w_Phi0, &w_A0, &w_M0, &w_Phi1, &w_A1, &w_A1_adj, &w_M1, &w_dPhi1, &w_Wsrc,
-                                &w_M0_adj, &w_A0_adj, &w_Phi0_adj, &w_node_forces, &d_xyz, &d_r})
+                                &w_M0_adj, &w_A0_adj, &w_Phi0_adj, &w_node_forces, &w_exec, &d_xyz, &d_r})
             b += x->capacity();
         return b;
     }
@@ -1486,7 +1486,8 @@ struct Evaluator {
         }
         if (!records) return;
         if (tm) tm->begin("edge_records", stream);
-        ks->edge_geometry(dm, t.ne, tile_xyz(t), tile_r(t), hm.agnesi ? d_edge_pair.as<int>() + t.e0 : nullptr,
+        ks->edge_geometry(dm, view(), t, tile_xyz(t), tile_r(t), hm.agnesi ? d_edge_pair.as<int>() + t.e0 : nullptr,
+                          static_cast<int*>(w_exec.ensure(std::max<std::int64_t>(max_tile_ne, 1) * sizeof(int))),
                           ws.erec, ws.erec_b, stream);
         if (tm) tm->end("edge_records", stream);
         (void)positions;

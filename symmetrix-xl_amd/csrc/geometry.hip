@@ -460,20 +460,78 @@ __global__ void k_compact_bits(int words, const std::uint32_t* __restrict__ bitm
 // lane written directly strides 288 B between lanes).
 constexpr int kRecordThreads = 128;
 
+// Spline evaluation point of an edge of length rf (cubic_spline_set.cpp:
+// 33-46): the interval, clamped to the table, and the offset in it.
+__device__ __forceinline__ int spline_point(float rf, float x0, float h, int intervals, float& xloc) {
+    int interval = static_cast<int>(floorf((rf - x0) / h));
+    xloc = rf - x0 - h * static_cast<float>(interval);
+    if (interval < 0) {
+        interval = 0;
+        xloc = 0.0f;
+    } else if (interval >= intervals) {
+        interval = intervals - 1;
+        xloc = h;
+    }
+    return interval;
+}
+
+// table row of edge e (the pair's block of intervals, one block without
+// per-pair tables), or INT_MAX for an inactive edge
+__device__ __forceinline__ int edge_row(const double* __restrict__ r, const int* __restrict__ edge_pair,
+                                        long long e, double r_cut, float x0, float h, int intervals) {
+    const double re = r[e];
+    if (!(re < r_cut)) return INT_MAX;
+    float xloc;
+    const int interval = spline_point(static_cast<float>(re), x0, h, intervals, xloc);
+    return (edge_pair ? edge_pair[e] * intervals : 0) + interval;
+}
+
+// One wave per receiver: each lane ranks its edges (lane, lane + 64, ...)
+// against all of the receiver's edges, whose rows the wave reads in turn.
+// Order: (row, position); a rank is a slot of the receiver's segment.
+constexpr int kOrderWaves = 4;
+__global__ __launch_bounds__(64 * kOrderWaves) void k_execution_order(int r0, int nr, long long e0,
+                                                                      const int* __restrict__ offsets,
+                                                                      const double* __restrict__ r, double r_cut,
+                                                                      float x0, float h, int intervals,
+                                                                      const int* __restrict__ edge_pair,
+                                                                      int* __restrict__ exec) {
+    const int li = blockIdx.x * kOrderWaves + static_cast<int>(threadIdx.x) / 64;
+    const int lane = threadIdx.x % 64;
+    if (li >= nr) return;
+    const long long ea = offsets[r0 + li] - e0;
+    const int n = offsets[r0 + li + 1] - offsets[r0 + li];
+    for (int j0 = 0; j0 < n; j0 += 64) {
+        const int j = j0 + lane;
+        const int kj = j < n ? edge_row(r, edge_pair, ea + j, r_cut, x0, h, intervals) : INT_MAX;
+        int rank = 0;
+        for (int m = 0; m < n; ++m) {
+            const int km = edge_row(r, edge_pair, ea + m, r_cut, x0, h, intervals);
+            rank += (km < kj || (km == kj && m < j)) ? 1 : 0;
+        }
+        if (j < n) exec[ea + rank] = static_cast<int>(ea + j);
+    }
+}
+
 template <int LMAX>
 __global__ __launch_bounds__(kRecordThreads) void k_edge_records(long long E, const double* __restrict__ xyz,
                                                                  const double* __restrict__ r, double r_cut,
                                                                  float x0, float h, int intervals,
                                                                  const int* __restrict__ edge_pair,
+                                                                 const int* __restrict__ exec,
+                                                                 const int* __restrict__ neigh,
+                                                                 const int* __restrict__ neigh_types,
                                                                  float* __restrict__ erec,
                                                                  float* __restrict__ erec_b) {
     using S = Shape<LMAX, 0>;
     static_assert(S::REC_F % 4 == 0 && S::REC_B % 4 == 0, "record parts are whole float4s");
+    static_assert(S::REC_U + 3 < S::REC, "the reverse part has a free field for the edge's row");
     __shared__ float4 stage[kRecordThreads * S::REC / 4];
     const long long base = static_cast<long long>(blockIdx.x) * kRecordThreads;
-    const long long e = base + threadIdx.x;
+    const long long slot = base + threadIdx.x;
     float* rec = reinterpret_cast<float*>(stage) + threadIdx.x * S::REC;
-    if (e < E) {
+    if (slot < E) {
+        const long long e = exec ? exec[slot] : slot;
         const double re = r[e];
         if (!(re < r_cut)) {
             for (int q = 0; q < S::REC; ++q) rec[q] = 0.0f;
@@ -481,27 +539,19 @@ __global__ __launch_bounds__(kRecordThreads) void k_edge_records(long long E, co
             float d[3];
             for (int c = 0; c < 3; ++c) d[c] = static_cast<float>(xyz[3 * e + c] / re);
             const float rf = static_cast<float>(re);
-            // spline evaluation point (cubic_spline_set.cpp:33-46)
-            int interval = static_cast<int>(floorf((rf - x0) / h));
-            float xloc = rf - x0 - h * static_cast<float>(interval);
-            if (interval < 0) {
-                interval = 0;
-                xloc = 0.0f;
-            } else if (interval >= intervals) {
-                interval = intervals - 1;
-                xloc = h;
-            }
+            float xloc;
+            const int interval = spline_point(rf, x0, h, intervals, xloc);
             rec[0] = xloc;
-            // table row: the pair's block of intervals (one block without per-pair tables)
             rec[1] = __int_as_float((edge_pair ? edge_pair[e] * intervals : 0) + interval);
-            rec[2] = __int_as_float(1);
-            rec[3] = 0.0f;
+            rec[2] = __int_as_float(neigh_types[e] + 1);
+            rec[3] = __int_as_float(neigh[e]);
             edge_harmonics<LMAX>(d, rf, rec + S::REC_Y, rec + S::REC_DY);
             rec[S::REC_U] = d[0];
             rec[S::REC_U + 1] = d[1];
             rec[S::REC_U + 2] = d[2];
             for (int q = S::REC_U + 3; q < S::REC; ++q) rec[q] = 0.0f;
         }
+        rec[S::REC - 1] = __int_as_float(static_cast<int>(e));
     }
     __syncthreads();
     // the two parts to their arrays, coalesced float4 rows
@@ -775,15 +825,24 @@ int build_touched_sources(int N, std::int64_t e0, std::int64_t ne, const int* so
     return static_cast<int>(total);
 }
 
+void launch_execution_order(int r0, int nr, std::int64_t e0, const int* offsets, const double* r, double r_cut,
+                            float x0, float h, int intervals, const int* edge_pair, int* exec, hipStream_t s) {
+    if (nr == 0) return;
+    k_execution_order<<<blocks_for(nr, kOrderWaves), 64 * kOrderWaves, 0, s>>>(r0, nr, e0, offsets, r, r_cut, x0, h,
+                                                                             intervals, edge_pair, exec);
+    SMX_LAUNCH_CHECK("execution_order");
+}
+
 void geometry_records(int l_max, std::int64_t E, const double* xyz, const double* r, double r_cut, float x0, float h,
-                      int intervals, const int* edge_pair, float* erec, float* erec_b, hipStream_t s) {
+                      int intervals, const int* edge_pair, const int* exec, const int* neigh, const int* neigh_types,
+                      float* erec, float* erec_b, hipStream_t s) {
     if (E == 0) return;
     if (l_max == 3)
-        k_edge_records<3><<<blocks_for(E, kRecordThreads), kRecordThreads, 0, s>>>(E, xyz, r, r_cut, x0, h, intervals,
-                                                                                edge_pair, erec, erec_b);
+        k_edge_records<3><<<blocks_for(E, kRecordThreads), kRecordThreads, 0, s>>>(
+            E, xyz, r, r_cut, x0, h, intervals, edge_pair, exec, neigh, neigh_types, erec, erec_b);
     else if (l_max == 2)
-        k_edge_records<2><<<blocks_for(E, kRecordThreads), kRecordThreads, 0, s>>>(E, xyz, r, r_cut, x0, h, intervals,
-                                                                                edge_pair, erec, erec_b);
+        k_edge_records<2><<<blocks_for(E, kRecordThreads), kRecordThreads, 0, s>>>(
+            E, xyz, r, r_cut, x0, h, intervals, edge_pair, exec, neigh, neigh_types, erec, erec_b);
     else
         throw std::invalid_argument("edge records are compiled for l_max 2 and 3");
     SMX_LAUNCH_CHECK("edge_records");

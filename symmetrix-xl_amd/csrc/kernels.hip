@@ -52,13 +52,14 @@ __device__ __forceinline__ double block_sum(double v, double* sbuf) {
 
 // ---------------------------------------------------------------------------
 // Layer 1: Phi0[i,lm,k] = sum_j R0_{l,k}(r_ij) Y_lm(ij) H0[type_j,k]
-// The forward parts of the receiver's records are staged through LDS.
+// The forward parts of the receiver's records (in execution order, the
+// source type in the activity field) are staged through LDS; the table
+// row's coefficients stay in registers while consecutive slots share it.
 // ---------------------------------------------------------------------------
 template <int C, int LMAX>
 __global__ __launch_bounds__(C) void k_r0_forward(int r0, long long e0, const int* __restrict__ offsets,
-                                                  const int* __restrict__ neigh_types, const float* __restrict__ erec,
-                                                  const float4* __restrict__ R0c, const float* __restrict__ H0,
-                                                  float* __restrict__ Phi0) {
+                                                  const float* __restrict__ erec, const float4* __restrict__ R0c,
+                                                  const float* __restrict__ H0, float* __restrict__ Phi0) {
     using S = Shape<LMAX, 0>;
     constexpr int NY = S::NY, NF = (LMAX + 1) * C;
     const int li = xcd_remap(blockIdx.x, gridDim.x);
@@ -70,20 +71,25 @@ __global__ __launch_bounds__(C) void k_r0_forward(int r0, long long e0, const in
     const int ea = offsets[i], eb = offsets[i + 1];
     __shared__ stage4 stage_buf[2 * RecordStage<C, S::REC_F>::SLOTS];
     const stage4* src = reinterpret_cast<const stage4*>(erec) + static_cast<std::size_t>(ea - e0) * (S::REC_F / 4);
-    staged_records<C, S::REC_F>(stage_buf, src, eb - ea, [&](const float* chunk, int first, int n)
+    float4 cc[LMAX + 1];
+    int cached = -1;
+    staged_records<C, S::REC_F>(stage_buf, src, eb - ea, [&](const float* chunk, int /*first*/, int n)
                                                              __attribute__((always_inline)) {
         for (int j = 0; j < n; ++j) {
             const float* rec = chunk + j * S::REC_F;
             if (!edge_active(rec)) continue;
-            const int e = ea + first + j;
             const float x = rec[0];
             const int iv = __float_as_int(rec[1]);
             const float xx = x * x, xxx = xx * x;
-            const float h0 = H0[neigh_types[e] * C + k];
-            const float4* cf = R0c + static_cast<std::size_t>(iv) * NF + k;
+            const float h0 = H0[(__float_as_int(rec[2]) - 1) * C + k];
+            if (iv != cached) {
+                cached = iv;
+                const float4* cf = R0c + static_cast<std::size_t>(iv) * NF + k;
+                static_for<0, LMAX + 1>([&](auto lc) { cc[lc] = cf[lc * C]; });
+            }
             static_for<0, LMAX + 1>([&](auto lc) {
                 constexpr int l = lc;
-                const float rh = spline_value(cf[l * C], x, xx, xxx) * h0;
+                const float rh = spline_value(cc[l], x, xx, xxx) * h0;
                 static_for<0, 2 * l + 1>([&](auto mc) {
                     constexpr int lm = l * l + mc;
                     acc[lm] += rh * rec[S::REC_Y + lm];
@@ -96,10 +102,10 @@ __global__ __launch_bounds__(C) void k_r0_forward(int r0, long long e0, const in
 }
 
 // Layer-1 reverse: node_forces[e] -= sum_k sum_lm Phi0_adj[i,lm,k] H0 (u dR Y + R dY)
+// (records in execution order; each slot's force goes to its edge's row)
 template <int C, int LMAX, bool ACCUMULATE>
 __global__ __launch_bounds__(C) void k_r0_reverse(int r0, long long e0, const int* __restrict__ offsets,
-                                                  const int* __restrict__ neigh_types, const float* __restrict__ erec,
-                                                  const float* __restrict__ erec_b,
+                                                  const float* __restrict__ erec, const float* __restrict__ erec_b,
                                                   const float4* __restrict__ R0c, const float* __restrict__ H0,
                                                   const float* __restrict__ Phi0_adj, double* __restrict__ node_forces) {
     using S = Shape<LMAX, 0>;
@@ -116,26 +122,31 @@ __global__ __launch_bounds__(C) void k_r0_reverse(int r0, long long e0, const in
     const int ea = offsets[i], eb = offsets[i + 1];
     const stage4* srcF = reinterpret_cast<const stage4*>(erec) + static_cast<std::size_t>(ea - e0) * (S::REC_F / 4);
     const stage4* srcB = reinterpret_cast<const stage4*>(erec_b) + static_cast<std::size_t>(ea - e0) * (S::REC_B / 4);
-    staged_records2<C, S::REC_F, S::REC_B>(stage_buf, srcF, srcB, eb - ea, [&](const float* chunk, int first, int n)
-                                                                               __attribute__((always_inline)) {
+    float4 cc[LMAX + 1];
+    int cached = -1;
+    staged_records2<C, S::REC_F, S::REC_B>(stage_buf, srcF, srcB, eb - ea, [&](const float* chunk, int /*first*/,
+                                                                               int n) __attribute__((always_inline)) {
         for (int j = 0; j < n; ++j) {
             const float* rec = chunk + j * S::REC;
             if (!edge_active(rec)) {
                 sink.zero(j);
                 continue;
             }
-            const int e = ea + first + j;
             const float x = rec[0];
             const int iv = __float_as_int(rec[1]);
             const float xx = x * x, xxx = xx * x, x2 = 2.0f * x, xx3 = 3.0f * xx;
-            const float h0 = H0[neigh_types[e] * C + k];
-            const float4* cf = R0c + static_cast<std::size_t>(iv) * NF + k;
+            const float h0 = H0[(__float_as_int(rec[2]) - 1) * C + k];
+            if (iv != cached) {
+                cached = iv;
+                const float4* cf = R0c + static_cast<std::size_t>(iv) * NF + k;
+                static_for<0, LMAX + 1>([&](auto lc) { cc[lc] = cf[lc * C]; });
+            }
             // per l: dR_l sum_m adj Y_lm (radial slope) and R_l sum_m adj dY_lm,
             // the common factor H0[type_j] applied once
             float a = 0.0f, b0 = 0.0f, b1 = 0.0f, b2 = 0.0f;
             static_for<0, LMAX + 1>([&](auto lc) {
                 constexpr int l = lc;
-                const float4 c4 = cf[l * C];
+                const float4 c4 = cc[l];
                 const float R = spline_value(c4, x, xx, xxx);
                 const float dR = spline_slope(c4, x2, xx3);
                 float sa = 0.0f, s0 = 0.0f, s1 = 0.0f, s2 = 0.0f;
@@ -154,7 +165,8 @@ __global__ __launch_bounds__(C) void k_r0_reverse(int r0, long long e0, const in
             const float u0 = rec[S::REC_U], u1 = rec[S::REC_U + 1], u2 = rec[S::REC_U + 2];
             sink.put(j, h0 * (u0 * a + b0), h0 * (u1 * a + b1), h0 * (u2 * a + b2));
         }
-        sink.template flush<ACCUMULATE>(static_cast<long long>(ea + first) - e0, n, node_forces);
+        sink.template flush<ACCUMULATE>(
+            n, node_forces, [&](int el) { return __float_as_int(chunk[el * S::REC + S::REC - 1]); });
     });
 }
 
@@ -1035,9 +1047,12 @@ struct KernelSetImpl final : KernelSet {
     }
     const char* polynomial_mode() const override { return kM0Unrolled ? "unrolled" : "table"; }
 
-    void edge_geometry(const DeviceModel& m, std::int64_t E, const double* xyz, const double* r,
-                       const int* edge_pair, float* erec, float* erec_b, hipStream_t s) const override {
-        geometry_records(LMAX, E, xyz, r, m.r_cut, m.x0, m.h, m.intervals, edge_pair, erec, erec_b, s);
+    void edge_geometry(const DeviceModel& m, const DeviceGraph& g, const TileView& t, const double* xyz,
+                       const double* r, const int* edge_pair, int* exec, float* erec, float* erec_b,
+                       hipStream_t s) const override {
+        launch_execution_order(t.r0, t.nr, t.e0, g.offsets, r, m.r_cut, m.x0, m.h, m.intervals, edge_pair, exec, s);
+        geometry_records(LMAX, t.ne, xyz, r, m.r_cut, m.x0, m.h, m.intervals, edge_pair, exec, g.neigh + t.e0,
+                         g.neigh_types + t.e0, erec, erec_b, s);
     }
 
     void layer1_forward(const DeviceModel& m, const DeviceGraph& g, const TileView& t, const Workspace& w,
@@ -1045,8 +1060,7 @@ struct KernelSetImpl final : KernelSet {
         if (t.nr == 0) return;
         {
             TimerScope ts(tm, "r0_forward", s);
-            k_r0_forward<C, LMAX><<<t.nr, C, 0, s>>>(t.r0, t.e0, g.offsets, g.neigh_types, w.erec, m.R0c, m.H0,
-                                                     w.Phi0);
+            k_r0_forward<C, LMAX><<<t.nr, C, 0, s>>>(t.r0, t.e0, g.offsets, w.erec, m.R0c, m.H0, w.Phi0);
             SMX_LAUNCH_CHECK("r0_forward");
         }
         {
@@ -1307,11 +1321,11 @@ struct KernelSetImpl final : KernelSet {
         {
             TimerScope ts(tm, "r0_reverse", s);
             if (accumulate_forces)
-                k_r0_reverse<C, LMAX, true><<<t.nr, C, 0, s>>>(t.r0, t.e0, g.offsets, g.neigh_types, w.erec,
-                                                               w.erec_b, m.R0c, m.H0, w.Phi0_adj, w.node_forces);
+                k_r0_reverse<C, LMAX, true><<<t.nr, C, 0, s>>>(t.r0, t.e0, g.offsets, w.erec, w.erec_b, m.R0c, m.H0,
+                                                               w.Phi0_adj, w.node_forces);
             else
-                k_r0_reverse<C, LMAX, false><<<t.nr, C, 0, s>>>(t.r0, t.e0, g.offsets, g.neigh_types, w.erec,
-                                                                w.erec_b, m.R0c, m.H0, w.Phi0_adj, w.node_forces);
+                k_r0_reverse<C, LMAX, false><<<t.nr, C, 0, s>>>(t.r0, t.e0, g.offsets, w.erec, w.erec_b, m.R0c, m.H0,
+                                                                w.Phi0_adj, w.node_forces);
             SMX_LAUNCH_CHECK("r0_reverse");
         }
         if (m.A0_scaled) {

@@ -236,10 +236,14 @@ struct KernelSet {
     virtual int record_forward_floats() const = 0;  // its forward part
     // "unrolled" when the product-basis kernels use compiled term tables
     virtual const char* polynomial_mode() const = 0;
-    // per-edge records of a tile from its FP64 xyz and r
-    // (edge_pair, indexed like xyz, selects each edge's table; null: one table)
-    virtual void edge_geometry(const DeviceModel& m, std::int64_t ne, const double* xyz, const double* r,
-                               const int* edge_pair, float* erec, float* erec_b, hipStream_t s) const = 0;
+    // per-edge records of tile t from its FP64 xyz and r (tile-local, in the
+    // caller's edge order), written in execution order: each receiver's
+    // edges by spline-table row (exec: the tile's [ne] slot -> edge map,
+    // filled here).  edge_pair, indexed like xyz, selects each edge's table
+    // (null: one table).
+    virtual void edge_geometry(const DeviceModel& m, const DeviceGraph& g, const TileView& t, const double* xyz,
+                               const double* r, const int* edge_pair, int* exec, float* erec, float* erec_b,
+                               hipStream_t s) const = 0;
     // R0 forward + A0 linear; with through_h1 also M0, the scalar capture and
     // H1 rows r0.. of the graph-wide H1
     virtual void layer1_forward(const DeviceModel& m, const DeviceGraph& g, const TileView& t, const Workspace& w,
@@ -288,10 +292,20 @@ void swizzle_gemm_weights(const float* w, int K, int N, float* out);
 // paths of the compiled kernel set for (l_max, L_max), false if none
 bool kernel_paths(int l_max, int L_max, std::vector<int>& le, std::vector<int>& ls, std::vector<int>& lo);
 
-// Per-edge records (spline point, Y, dY, direction) from FP64 xyz and r.
-// (record field 1 is the table row: pair * intervals + interval)
+// Execution order of the edges of receivers [r0, r0+nr) (edges [e0, ...)
+// of the receiver-major CSR offsets; r, edge_pair and exec tile-local):
+// within each receiver the active edges by spline-table row, ties by their
+// position, then the inactive ones (r >= r_cut); exec[slot] = edge.
+void launch_execution_order(int r0, int nr, std::int64_t e0, const int* offsets, const double* r, double r_cut,
+                            float x0, float h, int intervals, const int* edge_pair, int* exec, hipStream_t s);
+// Per-edge records (spline point, Y, dY, direction) from FP64 xyz and r,
+// slot s built from edge exec[s] (all tile-local; exec null: the identity).
+// Forward part: [x, table row (pair * intervals + interval), source type + 1
+// (0 for an inactive edge), source node, Y]; reverse part: [dY, unit
+// direction, ..., the edge's row].
 void geometry_records(int l_max, std::int64_t E, const double* xyz, const double* r, double r_cut, float x0, float h,
-                      int intervals, const int* edge_pair, float* erec, float* erec_b, hipStream_t s);
+                      int intervals, const int* edge_pair, const int* exec, const int* neigh, const int* neigh_types,
+                      float* erec, float* erec_b, hipStream_t s);
 // edge_pair[e] = symmetric pair of the active types of receiver and source
 void launch_edge_pairs(std::int64_t E, const int* receivers, const int* node_types, const int* neigh_types,
                        const int* type_to_active, int active_types, int* edge_pair, int* bad, hipStream_t s);
