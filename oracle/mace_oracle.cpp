@@ -473,6 +473,35 @@ static P poly_eval_grad(const MonomialSet& ms, const P* coef, const P* x, P* g, 
     return f;
 }
 
+// The directional derivative along dx of the polynomial and of its gradient:
+// returns sum_v g_v dx_v, with g the gradient and gd its derivative along dx
+// (each factor of a term differentiated in turn, as poly_eval_grad does).
+template <class P>
+static P poly_tangent(const MonomialSet& ms, const P* coef, const P* x, const P* dx, P* g, P* gd, int nvar) {
+    P fd = 0;
+    for (int v = 0; v < nvar; ++v) g[v] = gd[v] = 0;
+    for (std::size_t t = 0; t < ms.monos.size(); ++t) {
+        const auto& m = ms.monos[t];
+        for (std::size_t q = 0; q < m.size(); ++q) {
+            P d = coef[t];
+            for (std::size_t q2 = 0; q2 < m.size(); ++q2)
+                if (q2 != q) d *= x[m[q2]];
+            g[m[q]] += d;
+            fd += d * dx[m[q]];
+            P dd = 0;
+            for (std::size_t q3 = 0; q3 < m.size(); ++q3) {
+                if (q3 == q) continue;
+                P e = coef[t];
+                for (std::size_t q2 = 0; q2 < m.size(); ++q2)
+                    if (q2 != q && q2 != q3) e *= x[m[q2]];
+                dd += e * dx[m[q3]];
+            }
+            gd[m[q]] += dd;
+        }
+    }
+    return fd;
+}
+
 // ---------------------------------------------------------------------------
 // Model and evaluator
 // ---------------------------------------------------------------------------
@@ -879,6 +908,437 @@ struct Mace {
         }
         for (int i = 0; i < n; ++i)
             for (int c = 0; c < 3; ++c) field_adj[global ? c : 3 * static_cast<std::size_t>(i) + c] += part[3 * i + c];
+    }
+
+    // ---- MACEField response (mace_kokkos_response.tpp:136-2343 with the
+    // reducer of mace_kokkos_response.cpp:49-140): for each field component s,
+    // the tangent d/dE_s of the last evaluation, forward and reverse.  The
+    // field enters H1f linearly, so H1f_dot = sum over the entries of
+    // component s of coef H1p[lm_in] W; the tangent then runs through R1, A1
+    // (and its density scale), M1 (the polynomial's gradient and its
+    // derivative), H2 and the readout MLP (FP64, with act''), their reverses,
+    // the R1 reverse (bilinear in H1 and dPhi1: both tangents), and the field
+    // terms' reverse, where the Hessian column s is collected:
+    //   field_hessian[c*3 + s] = sum_i sum_entries(c) coef H1p[lm_in] W . H1f_adj_dot[lm_out]
+    // With forces, the layer-1 reverse carries H1p_adj_dot to the directed
+    // forces' tangent field_force_derivative[s][e][3] (M0, A0 and the R0
+    // path depend on the field only through the adjoint).  Needs the state
+    // of evaluate() on the same inputs and one field for the graph.
+    std::vector<double> field_hessian, field_force_derivative;
+    // terms of the tangent left out, for the tests that show each is needed:
+    // 1 the M1 gradient's tangent, 2 act'', 4 the (dPhi1, H1_dot) half of the
+    // R1 reverse, 8 its (dPhi1_dot, H1) half, 16 the seed's own field term in
+    // the field reverse, 32 the density scales' tangents
+    int response_drop = 0;
+
+    void field_response(int n, const int* types, const int* num_neigh, const int* neigh, const int* neigh_types,
+                        const double* xyz, const double* r, bool with_forces) {
+        if (!has_field) throw std::invalid_argument("the MACEField response needs a field-coupled model");
+        if (single_layer) throw std::invalid_argument("the MACEField response runs two-interaction models");
+        if (field_in.size() != 3)
+            throw std::invalid_argument("the MACEField response needs one electric field for the graph (3 values)");
+        std::vector<long long> off(n + 1, 0);
+        for (int i = 0; i < n; ++i) off[i + 1] = off[i] + num_neigh[i];
+        const long long E = off[n];
+        const int nY = num_lm;
+        const std::size_t Cs = static_cast<std::size_t>(C), LMC = static_cast<std::size_t>(num_LM) * Cs;
+        const std::size_t YC = static_cast<std::size_t>(nY) * Cs, LMEC = static_cast<std::size_t>(num_lme) * Cs;
+        const int np = static_cast<int>(Phi1_l.size());
+        std::vector<int> row_base(np);
+        for (int p = 0; p < np; ++p) row_base[p] = row_base_of_path(p);
+        std::vector<int> recv(E);
+        for (int i = 0; i < n; ++i)
+            for (long long e = off[i]; e < off[i + 1]; ++e) recv[e] = i;
+        std::vector<char> active(E);
+        std::vector<P> dirs(3 * static_cast<std::size_t>(E), P(0));
+        for (long long e = 0; e < E; ++e) {
+            active[e] = r[e] < r_cut;
+            if (active[e])
+                for (int c = 0; c < 3; ++c) dirs[3 * e + c] = static_cast<P>(xyz[3 * e + c] / r[e]);
+        }
+        std::vector<long long> soff(n + 1, 0);
+        for (long long e = 0; e < E; ++e) soff[neigh[e] + 1] += 1;
+        for (int s = 0; s < n; ++s) soff[s + 1] += soff[s];
+        std::vector<long long> sedges(E), cursor(soff.begin(), soff.end() - 1);
+        for (long long e = 0; e < E; ++e) sedges[cursor[neigh[e]]++] = e;
+        auto lin_fwd = [&](const P* src, const P* W, P* dst) {  // dst[k] = sum_kp src[kp] W[kp][k]
+            for (int k = 0; k < C; ++k) dst[k] = 0;
+            for (int kp = 0; kp < C; ++kp)
+                for (int k = 0; k < C; ++k) dst[k] += src[kp] * W[kp * Cs + k];
+        };
+        auto lin_rev = [&](const P* src, const P* W, P* dst) {  // dst[k] = sum_kp src[kp] W[k][kp]
+            for (int k = 0; k < C; ++k) {
+                P acc = 0;
+                for (int kp = 0; kp < C; ++kp) acc += src[kp] * W[k * Cs + kp];
+                dst[k] = acc;
+            }
+        };
+        auto radial1 = [&](long long e, P* rad, P* drad) {
+            const auto& sp = *spl1[pair_index(types[recv[e]], neigh_types[e])];
+            const auto pt = sp.point(static_cast<P>(r[e]));
+            const P* cf = sp.coefficients(pt);
+            const int ns = sp.num_splines;
+            for (int f = 0; f < ns; ++f) {
+                rad[f] = cf[f] + cf[ns + f] * pt.x + cf[2 * ns + f] * pt.xx + cf[3 * ns + f] * pt.xxx;
+                drad[f] = cf[ns + f] + P(2.0) * cf[2 * ns + f] * pt.x + P(3.0) * cf[3 * ns + f] * pt.xx;
+            }
+        };
+        // seed-independent: the primal rows of dPhi1 (CG) and H1f_adj = H1_adj U^T (+ direct on lm 0)
+        std::vector<P> rows(static_cast<std::size_t>(n) * num_rows * Cs, P(0)), H1f_adj(n * LMC, P(0));
+        std::vector<double> M1_adj(n * Cs, 0.0);
+#pragma omp parallel for schedule(static)
+        for (int i = 0; i < n; ++i) {
+            P* rw = &rows[static_cast<std::size_t>(i) * num_rows * Cs];
+            for (std::size_t t = 0; t < Phi1_cg.size(); ++t)
+                for (int k = 0; k < C; ++k) rw[Phi1_row[t] * Cs + k] += Phi1_cg[t] * dPhi1[i * LMEC + Phi1_lme[t] * Cs + k];
+            for (int l = 0; l <= L_max; ++l)
+                for (int m = 0; m < 2 * l + 1; ++m)
+                    lin_rev(&H1_adj[i * LMC + (l * l + m) * Cs], &U_all[static_cast<std::size_t>(l) * Cs * Cs],
+                            &H1f_adj[i * LMC + (l * l + m) * Cs]);
+            for (int k = 0; k < C; ++k) H1f_adj[i * LMC + k] += static_cast<P>(direct[i * Cs + k]);
+            for (int in = 0; in < C; ++in) {
+                double s1 = 0.0;
+                for (int o = 0; o < C; ++o) s1 += H2_M1[in * Cs + o] * H2_adj[i * Cs + o];
+                M1_adj[i * Cs + in] = s1;
+            }
+        }
+        field_hessian.assign(9, 0.0);
+        field_force_derivative.assign(with_forces ? 9 * static_cast<std::size_t>(E) : 0, 0.0);
+        const int T1 = static_cast<int>(M1_monos.monos.size());
+        for (int seed = 0; seed < 3; ++seed) {
+            // 1. H1f_dot, x_dot = H1f_dot[:,0,:], H1_dot = H1f_dot U
+            std::vector<P> H1f_dot(n * LMC, P(0)), H1_dot(n * LMC, P(0));
+#pragma omp parallel for schedule(static)
+            for (int i = 0; i < n; ++i) {
+                const P* hp = &H1_pre[i * LMC];
+                P* hd = &H1f_dot[i * LMC];
+                for (const auto& en : field_entries) {
+                    if (en.comp != seed) continue;
+                    const P* W = &field_W[static_cast<std::size_t>(en.path) * Cs * Cs];
+                    for (int out = 0; out < C; ++out) {
+                        P z = 0;
+                        for (int in = 0; in < C; ++in) z += hp[en.lm_in * Cs + in] * W[in * Cs + out];
+                        hd[en.lm_out * Cs + out] += en.coef * z;
+                    }
+                }
+                for (int l = 0; l <= L_max; ++l)
+                    for (int m = 0; m < 2 * l + 1; ++m)
+                        lin_fwd(hd + (l * l + m) * Cs, &U_all[static_cast<std::size_t>(l) * Cs * Cs],
+                                &H1_dot[i * LMC + (l * l + m) * Cs]);
+            }
+            // 2-3. Phi1_dot (the R1 forward of H1_dot), A1_dot (scaled like A1)
+            std::vector<P> A1_dot(n * YC, P(0));
+#pragma omp parallel for schedule(dynamic, 16)
+            for (int i = 0; i < n; ++i) {
+                std::vector<P> rw(static_cast<std::size_t>(num_rows) * Cs, P(0)), rad(np * Cs), drad(np * Cs);
+                std::vector<P> phi(LMEC, P(0));
+                for (long long e = off[i]; e < off[i + 1]; ++e) {
+                    if (!active[e]) continue;
+                    radial1(e, rad.data(), drad.data());
+                    const P* Hj = &H1_dot[static_cast<std::size_t>(neigh[e]) * LMC];
+                    for (int p = 0; p < np; ++p) {
+                        const int l1 = Phi1_l1[p], l2 = Phi1_l2[p];
+                        int row = row_base[p];
+                        for (int lm1 = l1 * l1; lm1 <= l1 * (l1 + 2); ++lm1)
+                            for (int lm2 = l2 * l2; lm2 <= l2 * (l2 + 2); ++lm2) {
+                                const P y = Y[e * nY + lm1];
+                                for (int k = 0; k < C; ++k) rw[row * Cs + k] += rad[p * Cs + k] * y * Hj[lm2 * Cs + k];
+                                ++row;
+                            }
+                    }
+                }
+                for (std::size_t t = 0; t < Phi1_cg.size(); ++t)
+                    for (int k = 0; k < C; ++k) phi[Phi1_lme[t] * Cs + k] += Phi1_cg[t] * rw[Phi1_row[t] * Cs + k];
+                P* ad = &A1_dot[i * YC];
+                for (int l = 0; l <= l_max; ++l) {
+                    const int ne = num_e[l];
+                    const P* W = A1_w[l].data();
+                    for (int m = 0; m < 2 * l + 1; ++m)
+                        for (int e2 = 0; e2 < ne; ++e2) {
+                            const P* src = &phi[(lme_base[l] + m * ne + e2) * Cs];
+                            for (int kp = 0; kp < C; ++kp)
+                                for (int k = 0; k < C; ++k)
+                                    ad[(l * l + m) * Cs + k] += src[kp] * W[(static_cast<std::size_t>(e2) * Cs + kp) * Cs + k];
+                        }
+                }
+                if (A1_scaled) {
+                    const P inv = static_cast<P>(1.0 / A1_scale[i]);
+                    for (std::size_t v = 0; v < YC; ++v) ad[v] *= inv;
+                }
+            }
+            // 4-7. M1 tangent, readout tangents (FP64), A1 adjoint tangent
+            // (and its density scale), dPhi1_dot
+            std::vector<P> dPhi1_dot(n * LMEC, P(0));
+            std::vector<double> direct_dot(n * Cs, 0.0);
+            std::vector<double> fdot(with_forces ? 3 * static_cast<std::size_t>(E) : 0, 0.0);
+            std::vector<double> dens_dot1(n, 0.0);
+#pragma omp parallel for schedule(static)
+            for (int i = 0; i < n; ++i) {
+                const int t = types[i];
+                std::vector<P> g(YC), gd(YC), M1_dot(Cs);
+                P x[16], dx[16], gv[16], gdv[16];
+                for (int k = 0; k < C; ++k) {
+                    for (int v = 0; v < nY; ++v) {
+                        x[v] = A1[i * YC + v * Cs + k];
+                        dx[v] = A1_dot[i * YC + v * Cs + k];
+                    }
+                    M1_dot[k] = poly_tangent<P>(M1_monos, M1_coef[t].data() + static_cast<std::size_t>(k) * T1, x, dx, gv,
+                                                gdv, nY);
+                    for (int v = 0; v < nY; ++v) {
+                        g[v * Cs + k] = gv[v];
+                        gd[v * Cs + k] = gdv[v];
+                    }
+                }
+                const double* h2 = &H2[i * Cs];
+                std::vector<double> h2d(Cs), zd(hidden), h2ad(Cs);
+                for (int o = 0; o < C; ++o) {
+                    double s = 0.0;
+                    for (int in = 0; in < C; ++in)
+                        s += H2_T[t][in * Cs + o] * static_cast<double>(H1f_dot[i * LMC + in]);
+                    for (int in = 0; in < C; ++in) s += H2_M1[in * Cs + o] * static_cast<double>(M1_dot[in]);
+                    h2d[o] = s;
+                }
+                std::vector<double> dd(hidden);
+                for (int hdn = 0; hdn < hidden; ++hdn) {
+                    double z = 0.0, zt = 0.0;
+                    for (int k = 0; k < C; ++k) {
+                        z += W1[hdn * Cs + k] * h2[k];
+                        zt += W1[hdn * Cs + k] * h2d[k];
+                    }
+                    const double sg = 1.0 / (1.0 + std::exp(-z));
+                    // d/dz of scale (sg + z sg (1 - sg))
+                    const double act2 = readout_scale * sg * (1.0 - sg) * (2.0 + z * (1.0 - 2.0 * sg));
+                    dd[hdn] = (response_drop & 2) ? 0.0 : W2[hdn] * act2 * zt;
+                }
+                for (int k = 0; k < C; ++k) {
+                    double s = 0.0;
+                    for (int hdn = 0; hdn < hidden; ++hdn) s += dd[hdn] * W1[hdn * Cs + k];
+                    h2ad[k] = s;
+                }
+                std::vector<P> a1s_adj_dot(YC), a1s_adj(YC);
+                for (int in = 0; in < C; ++in) {
+                    double sd = 0.0, s1 = 0.0;
+                    for (int o = 0; o < C; ++o) {
+                        sd += H2_T[t][in * Cs + o] * h2ad[o];
+                        s1 += H2_M1[in * Cs + o] * h2ad[o];
+                    }
+                    direct_dot[i * Cs + in] = sd;
+                    const P m1adj_dot = static_cast<P>(s1), m1adj = static_cast<P>(M1_adj[i * Cs + in]);
+                    for (int v = 0; v < nY; ++v) {
+                        a1s_adj_dot[v * Cs + in] =
+                            g[v * Cs + in] * m1adj_dot + ((response_drop & 1) ? P(0) : gd[v * Cs + in] * m1adj);
+                        a1s_adj[v * Cs + in] = g[v * Cs + in] * m1adj;
+                    }
+                }
+                if (A1_scaled && !(response_drop & 32)) {
+                    // dot = sum A1_adj A1 in the scaled basis: its tangent
+                    const P* a = &A1[i * YC];
+                    const P* ad = &A1_dot[i * YC];
+                    double dot = 0.0;
+                    for (std::size_t v = 0; v < YC; ++v)
+                        dot += static_cast<double>(a1s_adj_dot[v] * a[v]) + static_cast<double>(a1s_adj[v] * ad[v]);
+                    dens_dot1[i] = dot;
+                }
+                if (A1_scaled) {
+                    const P inv = static_cast<P>(1.0 / A1_scale[i]);
+                    for (std::size_t v = 0; v < YC; ++v) a1s_adj_dot[v] *= inv;
+                }
+                for (int l = 0; l <= l_max; ++l) {
+                    const int ne = num_e[l];
+                    const P* W = A1_w[l].data();
+                    for (int m = 0; m < 2 * l + 1; ++m)
+                        for (int e2 = 0; e2 < ne; ++e2) {
+                            P* dst = &dPhi1_dot[i * LMEC + (lme_base[l] + m * ne + e2) * Cs];
+                            for (int k = 0; k < C; ++k) {
+                                const P* wr = W + (static_cast<std::size_t>(e2) * Cs + k) * Cs;
+                                P s = 0;
+                                for (int kp = 0; kp < C; ++kp) s += a1s_adj_dot[(l * l + m) * Cs + kp] * wr[kp];
+                                dst[k] = s;
+                            }
+                        }
+                }
+            }
+            if (with_forces && A1_scaled)
+                for (int i = 0; i < n; ++i)
+                    for (long long e = off[i]; e < off[i + 1]; ++e) {
+                        double f, d;
+                        density_eval(*dens1[pair_index(types[i], neigh_types[e])], r[e], f, d);
+                        const double scale = dens_dot1[i] / A1_scale[i] * d;
+                        for (int c = 0; c < 3; ++c) fdot[3 * e + c] += scale * (xyz[3 * e + c] / r[e]);
+                    }
+            // 8. the R1 reverse's tangents: edge forces from (dPhi1_dot, H1)
+            // and (dPhi1, H1_dot); H1_adj_dot from dPhi1_dot over the transpose
+            std::vector<P> rows_dot(static_cast<std::size_t>(n) * num_rows * Cs, P(0));
+#pragma omp parallel for schedule(static)
+            for (int i = 0; i < n; ++i) {
+                P* rw = &rows_dot[static_cast<std::size_t>(i) * num_rows * Cs];
+                for (std::size_t t = 0; t < Phi1_cg.size(); ++t)
+                    for (int k = 0; k < C; ++k)
+                        rw[Phi1_row[t] * Cs + k] += Phi1_cg[t] * dPhi1_dot[i * LMEC + Phi1_lme[t] * Cs + k];
+            }
+            if (with_forces) {
+#pragma omp parallel
+                {
+                std::vector<P> rad(np * Cs), drad(np * Cs);
+#pragma omp for schedule(dynamic, 64)
+                for (long long e = 0; e < E; ++e) {
+                    if (!active[e]) continue;
+                    const int i = recv[e];
+                    radial1(e, rad.data(), drad.data());
+                    const P* ra = &rows[static_cast<std::size_t>(i) * num_rows * Cs];
+                    const P* rd = &rows_dot[static_cast<std::size_t>(i) * num_rows * Cs];
+                    const P* Hj = &H1[static_cast<std::size_t>(neigh[e]) * LMC];
+                    const P* Hd = &H1_dot[static_cast<std::size_t>(neigh[e]) * LMC];
+                    const P* y = &Y[e * nY];
+                    const P* gy = &Ygrad[e * 3 * nY];
+                    double f[3] = {0, 0, 0};
+                    for (int p = 0; p < np; ++p) {
+                        const int l1 = Phi1_l1[p], l2 = Phi1_l2[p];
+                        int row = row_base[p];
+                        for (int lm1 = l1 * l1; lm1 <= l1 * (l1 + 2); ++lm1)
+                            for (int lm2 = l2 * l2; lm2 <= l2 * (l2 + 2); ++lm2) {
+                                P radial_sum = 0, angular_sum = 0;
+                                for (int k = 0; k < C; ++k) {
+                                    const P b = ((response_drop & 8) ? P(0) : rd[row * Cs + k] * Hj[lm2 * Cs + k]) +
+                                                ((response_drop & 4) ? P(0) : ra[row * Cs + k] * Hd[lm2 * Cs + k]);
+                                    radial_sum += b * drad[p * Cs + k];
+                                    angular_sum += b * rad[p * Cs + k];
+                                }
+                                for (int c = 0; c < 3; ++c)
+                                    f[c] -= static_cast<double>(dirs[3 * e + c] * radial_sum * y[lm1] +
+                                                                angular_sum * gy[c * nY + lm1]);
+                                ++row;
+                            }
+                    }
+                    for (int c = 0; c < 3; ++c) fdot[3 * e + c] += f[c];
+                }
+                }
+            }
+            std::vector<P> H1_adj_dot(n * LMC, P(0));
+#pragma omp parallel for schedule(dynamic, 16)
+            for (int s = 0; s < n; ++s) {
+                std::vector<double> acc(LMC, 0.0);
+                std::vector<P> rad(np * Cs), drad(np * Cs);
+                for (long long q2 = soff[s]; q2 < soff[s + 1]; ++q2) {
+                    const long long e = sedges[q2];
+                    if (!active[e]) continue;
+                    radial1(e, rad.data(), drad.data());
+                    const P* rd = &rows_dot[static_cast<std::size_t>(recv[e]) * num_rows * Cs];
+                    const P* y = &Y[e * nY];
+                    for (int p = 0; p < np; ++p) {
+                        const int l1 = Phi1_l1[p], l2 = Phi1_l2[p];
+                        int row = row_base[p];
+                        for (int lm1 = l1 * l1; lm1 <= l1 * (l1 + 2); ++lm1)
+                            for (int lm2 = l2 * l2; lm2 <= l2 * (l2 + 2); ++lm2) {
+                                for (int k = 0; k < C; ++k)
+                                    acc[lm2 * Cs + k] += static_cast<double>(rad[p * Cs + k] * y[lm1] * rd[row * Cs + k]);
+                                ++row;
+                            }
+                    }
+                }
+                for (std::size_t v = 0; v < LMC; ++v) H1_adj_dot[s * LMC + v] = static_cast<P>(acc[v]);
+            }
+            // 9. the field terms' reverse tangent and the Hessian column
+            std::vector<double> part(static_cast<std::size_t>(n) * 3, 0.0);
+            std::vector<P> H1p_adj_dot(n * LMC, P(0));
+#pragma omp parallel for schedule(static)
+            for (int i = 0; i < n; ++i) {
+                std::vector<P> ad(LMC);
+                for (int l = 0; l <= L_max; ++l)
+                    for (int m = 0; m < 2 * l + 1; ++m)
+                        lin_rev(&H1_adj_dot[i * LMC + (l * l + m) * Cs], &U_all[static_cast<std::size_t>(l) * Cs * Cs],
+                                &ad[(l * l + m) * Cs]);
+                for (int k = 0; k < C; ++k) ad[k] += static_cast<P>(direct_dot[i * Cs + k]);
+                const P* hp = &H1_pre[i * LMC];
+                const P* fa = &H1f_adj[i * LMC];
+                for (int li = 0; li < num_LM; ++li)
+                    for (int in = 0; in < C; ++in) {
+                        P value = ad[li * Cs + in];
+                        for (const auto& en : field_entries) {
+                            if (en.lm_in != li) continue;
+                            const P* W = &field_W[static_cast<std::size_t>(en.path) * Cs * Cs + in * Cs];
+                            P tr_dot = 0, tr = 0;
+                            for (int out = 0; out < C; ++out) {
+                                tr_dot += W[out] * ad[en.lm_out * Cs + out];
+                                tr += W[out] * fa[en.lm_out * Cs + out];
+                            }
+                            value += field_value(i, en.comp) * (en.coef * tr_dot);
+                            if (en.comp == seed && !(response_drop & 16)) value += en.coef * tr;
+                            part[3 * static_cast<std::size_t>(i) + en.comp] +=
+                                static_cast<double>(hp[li * Cs + in] * (en.coef * tr_dot));
+                        }
+                        H1p_adj_dot[i * LMC + li * Cs + in] = value;
+                    }
+            }
+            for (int i = 0; i < n; ++i)
+                for (int c = 0; c < 3; ++c) field_hessian[c * 3 + seed] += part[3 * static_cast<std::size_t>(i) + c];
+            if (!with_forces) continue;
+            // 10. the layer-1 reverse of H1p_adj_dot: M0, A0 (density scale),
+            // the R0 reverse
+            std::vector<double> dens_dot0(n, 0.0);
+#pragma omp parallel for schedule(dynamic, 16)
+            for (int i = 0; i < n; ++i) {
+                std::vector<P> m0a(LMC), a0a(YC, P(0)), padj(YC), rad(Cs), drad(Cs);
+                for (int l = 0; l <= L_max; ++l)
+                    for (int m = 0; m < 2 * l + 1; ++m)
+                        lin_rev(&H1p_adj_dot[i * LMC + (l * l + m) * Cs], &P_all[static_cast<std::size_t>(l) * Cs * Cs],
+                                &m0a[(l * l + m) * Cs]);
+                for (int v = 0; v < nY; ++v)
+                    for (int LM = 0; LM < num_LM; ++LM) {
+                        const P* g = &M0_grad[((static_cast<std::size_t>(i) * num_LM + LM) * nY + v) * Cs];
+                        for (int k = 0; k < C; ++k) a0a[v * Cs + k] += g[k] * m0a[LM * Cs + k];
+                    }
+                if (A0_scaled) {
+                    const P* a = &A0[i * YC];
+                    double dot = 0.0;
+                    for (std::size_t v = 0; v < YC; ++v) dot += static_cast<double>(a0a[v] * a[v]);
+                    dens_dot0[i] = (response_drop & 32) ? 0.0 : dot;
+                    for (std::size_t v = 0; v < YC; ++v)
+                        a0a[v] = static_cast<P>(static_cast<double>(a0a[v]) / A0_scale[i]);
+                }
+                for (int l = 0; l <= l_max; ++l)
+                    for (int m = 0; m < 2 * l + 1; ++m)
+                        lin_rev(&a0a[(l * l + m) * Cs], A0_w[types[i]][l].data(), &padj[(l * l + m) * Cs]);
+                for (long long e = off[i]; e < off[i + 1]; ++e) {
+                    if (!active[e]) continue;
+                    const auto& sp = *spl0[pair_index(types[i], neigh_types[e])];
+                    const auto pt = sp.point(static_cast<P>(r[e]));
+                    const P* cf = sp.coefficients(pt);
+                    const int ns = sp.num_splines;
+                    const P* h0 = &H0[static_cast<std::size_t>(neigh_types[e]) * Cs];
+                    const P* y = &Y[e * nY];
+                    const P* gy = &Ygrad[e * 3 * nY];
+                    double f[3] = {0, 0, 0};
+                    for (int l = 0; l <= l_max; ++l) {
+                        for (int k = 0; k < C; ++k) {
+                            const int fi = l * C + k;
+                            rad[k] = cf[fi] + cf[ns + fi] * pt.x + cf[2 * ns + fi] * pt.xx + cf[3 * ns + fi] * pt.xxx;
+                            drad[k] = cf[ns + fi] + P(2.0) * cf[2 * ns + fi] * pt.x + P(3.0) * cf[3 * ns + fi] * pt.xx;
+                        }
+                        for (int m = -l; m <= l; ++m) {
+                            const int lm = l * l + l + m;
+                            P radial_sum = 0, angular_sum = 0;
+                            for (int k = 0; k < C; ++k) {
+                                radial_sum += padj[lm * Cs + k] * drad[k] * h0[k];
+                                angular_sum += padj[lm * Cs + k] * rad[k] * h0[k];
+                            }
+                            for (int c = 0; c < 3; ++c)
+                                f[c] -= static_cast<double>(dirs[3 * e + c] * radial_sum * y[lm] + angular_sum * gy[c * nY + lm]);
+                        }
+                    }
+                    for (int c = 0; c < 3; ++c) fdot[3 * e + c] += f[c];
+                }
+            }
+            if (A0_scaled)
+                for (int i = 0; i < n; ++i)
+                    for (long long e = off[i]; e < off[i + 1]; ++e) {
+                        double f, d;
+                        density_eval(*dens0[pair_index(types[i], neigh_types[e])], r[e], f, d);
+                        for (int c = 0; c < 3; ++c)
+                            fdot[3 * e + c] += dens_dot0[i] / A0_scale[i] * d * xyz[3 * e + c] / r[e];
+                    }
+            std::copy(fdot.begin(), fdot.end(), field_force_derivative.begin() + 3 * static_cast<std::size_t>(E) * seed);
+        }
     }
 
     // field_coupling.hpp:60-238 (compile_field_coupling) and mace.cpp:2832-2860
@@ -1872,6 +2332,34 @@ int oracle_evaluate(void* hv, int n, const int* types, const int* num_neigh, con
         };
         if (h->fp64) run(*h->d); else run(*h->f);
         (void)E;
+        return 0;
+    });
+}
+
+// MACEField response of a field-coupled model in the field set by
+// oracle_set_field (3 values): evaluates, then the tangents in each field
+// component.  hessian[c*3 + s] = d(dE/dE_c)/dE_s; with force_derivative
+// non-null, force_derivative[s][e][3] = d(directed force of e)/dE_s.
+// leave out terms of the response's tangent (bit mask, see Mace::response_drop)
+int oracle_set_response_drop(void* hv, int mask) {
+    auto* h = static_cast<OracleHandle*>(hv);
+    if (h->fp64) h->d->response_drop = mask; else h->f->response_drop = mask;
+    return 0;
+}
+
+int oracle_field_response(void* hv, int n, const int* types, const int* num_neigh, const int* neigh,
+                          const int* neigh_types, const double* xyz, const double* r, double* hessian,
+                          double* force_derivative) {
+    return guarded([&]() -> int {
+        auto* h = static_cast<OracleHandle*>(hv);
+        auto run = [&](auto& m) {
+            m.evaluate(n, types, num_neigh, neigh, neigh_types, xyz, r);
+            m.field_response(n, types, num_neigh, neigh, neigh_types, xyz, r, force_derivative != nullptr);
+            std::copy(m.field_hessian.begin(), m.field_hessian.end(), hessian);
+            if (force_derivative)
+                std::copy(m.field_force_derivative.begin(), m.field_force_derivative.end(), force_derivative);
+        };
+        if (h->fp64) run(*h->d); else run(*h->f);
         return 0;
     });
 }

@@ -45,6 +45,9 @@ def lib():
                                       _f64p, _f64p, _f64p, _f64p]
         L.oracle_set_num_threads.argtypes = [ctypes.c_int]
         L.oracle_set_field.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int]
+        L.oracle_set_response_drop.argtypes = [ctypes.c_void_p, ctypes.c_int]
+        L.oracle_field_response.argtypes = [ctypes.c_void_p, ctypes.c_int, _i32p, _i32p, _i32p, _i32p,
+                                            _f64p, _f64p, _f64p, ctypes.c_void_p]
         L.oracle_stage.restype = ctypes.c_longlong
         L.oracle_stage.argtypes = [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_void_p, ctypes.c_longlong]
         L.oracle_radial_tables.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
@@ -132,6 +135,28 @@ class OracleModel:
         if rc != 0:
             raise ValueError(_err())
         return e, f.reshape(E, 3)
+
+    def field_response(self, node_types, num_neigh, neigh_indices, neigh_types, xyz, r, field, forces=True):
+        """MACEField response in a graph field (3 values): the Hessian
+        d2E/dE_c dE_s as [c][s], and with forces the directed forces'
+        tangent [s][edge][3] (else None).  Evaluates first."""
+        f64 = _c(field, np.float64).ravel()
+        lib().oracle_set_field(self._h, f64.ctypes.data, f64.size)
+        node_types = _c(node_types, np.int32)
+        E = len(neigh_indices)
+        hess = np.zeros(9)
+        fd = np.zeros(9 * E) if forces else None
+        rc = lib().oracle_field_response(self._h, len(node_types), node_types, _c(num_neigh, np.int32),
+                                         _c(neigh_indices, np.int32), _c(neigh_types, np.int32),
+                                         _c(xyz, np.float64).ravel(), _c(r, np.float64), hess,
+                                         fd.ctypes.data if forces else None)
+        if rc != 0:
+            raise ValueError(_err())
+        return hess.reshape(3, 3), (fd.reshape(3, E, 3) if forces else None)
+
+    def set_response_drop(self, mask):
+        """Leave terms out of the response's tangent (tests of the pins only)."""
+        lib().oracle_set_response_drop(self._h, int(mask))
 
     def stage(self, name):
         size = lib().oracle_stage(self._h, name.encode(), None, 0)
@@ -260,4 +285,27 @@ def evaluate_system(model, system, skin=0.5, positions=None, graph=None, field=N
            "node_forces": f, "graph": graph, "xyz": xyz, "r": r}
     if field is not None:
         out["field_adj"] = model.stage("field_adj")
+    return out
+
+
+def field_response_system(model, system, field, skin=0.5, positions=None, graph=None, forces=True):
+    """The MACEField response of a system (the calculator's contract,
+    calculator.py:3783-3817): Hessian [c][s], the directed forces' tangent
+    [s][edge][3], Born charges bec[i][s][xyz] = dF_i/dE_s (sources plus,
+    receivers minus) and the graph."""
+    pos0 = np.asarray(system["positions"], dtype=np.float64)
+    cell = np.asarray(system["cell"], dtype=np.float64)
+    if graph is None:
+        graph = neighbor_graph(pos0, cell, model.r_cut + skin)
+    pos = pos0 if positions is None else positions
+    xyz, r = prepared_geometry(graph, cell, pos0, pos, model.r_cut)
+    types = model.types_of(system["numbers"])
+    hess, fd = model.field_response(types, graph["num_neigh"], graph["sources"], types[graph["sources"]], xyz, r,
+                                    field, forces)
+    out = {"hessian": hess, "graph": graph, "xyz": xyz, "r": r}
+    if forces:
+        n = len(types)
+        out["force_derivative"] = fd
+        out["bec"] = np.stack([reduce_forces(n, graph["receivers"], graph["sources"], fd[s]) for s in range(3)],
+                              axis=1)
     return out

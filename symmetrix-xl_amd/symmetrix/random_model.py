@@ -112,6 +112,10 @@ MODEL_CONFIGS = {
     # MACEField models (field_coupling.hpp; mace.cpp:322-395), L_max 1 and 2
     "tiny_field": ModelConfig("tiny_field", 32, 2, 1, 2, [8, 22, 38], radial_mlp=[32, 32],
                               r_cut=5.0, avg_num_neighbors=40.0, h1_mode="pre_linear_up", field=True),
+    # with A0/A1 density scaling and ZBL (the response's density tangents)
+    "tiny_field_scaled": ModelConfig("tiny_field_scaled", 32, 2, 1, 2, [8, 22, 38], radial_mlp=[32, 32],
+                                     r_cut=5.0, avg_num_neighbors=40.0, h1_mode="pre_linear_up", field=True,
+                                     density_scaled=True, zbl=True),
     # (L_max 2 at a compiled kernel shape: 128 channels, l_max 3)
     "field_l2": ModelConfig("field_l2", 128, 3, 2, 3, [8, 22, 38], radial_mlp=[32, 32],
                             r_cut=5.0, avg_num_neighbors=40.0, h1_mode="pre_linear_up", field=True,

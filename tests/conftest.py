@@ -90,6 +90,12 @@ def tiny_field_model_path():
 
 
 @pytest.fixture(scope="session")
+def tiny_field_scaled_model_path():
+    from symmetrix import random_model
+    return random_model.cached_model("tiny_field_scaled", directory=MODEL_DIR)
+
+
+@pytest.fixture(scope="session")
 def field_l2_model_path():
     from symmetrix import random_model
     return random_model.cached_model("field_l2", directory=MODEL_DIR)
