@@ -352,6 +352,36 @@ SMX_API int32_t smx_set_electric_field(SmxEvaluator* ev, const double* field, in
 SMX_API int32_t smx_electric_field_adj(SmxEvaluator* ev, double* out, int64_t capacity, int64_t* count);
 /* has_field_coupling (the model file's flag, mace.cpp:2832) */
 SMX_API int32_t smx_has_field_coupling(const SmxEvaluator* ev, int32_t* out);
+/* MACEField response: _compute_prepared_factorized_field_response(token,
+ * electric_field, include_force_derivative, scatter_bec_bins) (pybind
+ * mace_kokkos.cpp:1865-1879; mace_kokkos_response.tpp:2504-2543, the tangents
+ * :136-2343).  Runs after a completed field evaluation of the current graph
+ * token, in the same graph-level field (field_count 3; a field that differs
+ * from that evaluation's is refused, as is a per-node field, a feature
+ * graph with ghosts, a one-interaction model and a stale token): the field
+ * Hessian d2E/dE_c dE_s (smx_electric_field_hessian) and, with
+ * include_force_derivative, the directed forces' field derivative per edge
+ * (smx_electric_field_force_derivative) or, with scatter_bec_bins too, its
+ * reduction to the atoms (smx_electric_field_bec_bins, the Born effective
+ * charges dF_i/dE_s).  Leaves the evaluation's results as they were. */
+SMX_API int32_t smx_compute_prepared_factorized_field_response(SmxEvaluator* ev, uint64_t generation,
+                                                               const double* field, int64_t field_count,
+                                                               int32_t include_force_derivative,
+                                                               int32_t scatter_bec_bins);
+/* electric_field_hessian (pybind mace_kokkos.cpp:2160-2163): 9 values,
+ * [c*3 + s] = d(dE/dE_c)/dE_s, of the last response (FP64 sums). */
+SMX_API int32_t smx_electric_field_hessian(SmxEvaluator* ev, double* out, int64_t capacity, int64_t* count);
+/* electric_field_force_derivative (pybind mace_kokkos.cpp:2164-2167):
+ * [3][num_edges][3], the field component's derivative of each edge's
+ * directed force in the caller's edge order (9 * num_edges values), or none
+ * when the last response took no force derivative or scattered it into
+ * bins.  *count gets the length; copies when out != NULL. */
+SMX_API int32_t smx_electric_field_force_derivative(SmxEvaluator* ev, double* out, int64_t capacity,
+                                                    int64_t* count);
+/* electric_field_bec_bins (pybind mace_kokkos.cpp:2335-2349): [num_nodes][3][3],
+ * bins[i][s][x] = dF_ix/dE_s (edges leaving i plus, arriving minus), or none
+ * when the last response scattered no bins. */
+SMX_API int32_t smx_electric_field_bec_bins(SmxEvaluator* ev, double* out, int64_t capacity, int64_t* count);
 /* compute_node_energies_forces with execution_graph_generation == 0
  * (mace_kokkos.hpp:654-662; pybind mace_kokkos.cpp:2169): prepares the
  * graph from the host CSR, then evaluates. */

@@ -225,6 +225,17 @@ struct Evaluator {
     DevBuf d_efield, d_field_part, d_field_adj;
     bool field_evaluated = false;
     std::int64_t field_adj_count = 0;  // values of the last evaluation's dE/dE
+    std::vector<double> evaluated_field;  // the field the last evaluation ran in
+    // MACEField response (compute_prepared_factorized_field_response,
+    // mace_kokkos_response.tpp:2504-2543): tangent buffers, the Hessian
+    // [c*3 + s] on the host, the force derivative [3][E][3] or the Born
+    // charge bins [3][N][3] on the device
+    ResponseWorkspace rws;
+    DevBuf r_f32, r_f64;
+    double response_hessian[9] = {0};
+    bool response_done = false, response_has_forces = false, response_has_bins = false;
+    int response_N = 0;
+    std::int64_t response_E = 0;
 
     // execution plan request (set_execution_plan_request, set_allow_fixed_workspace,
     // mace_kokkos.hpp:95-96; the calculator's execution_profile and
@@ -1631,7 +1642,101 @@ struct Evaluator {
         // ghosts' rows of a one-call evaluation take no field term
         if (ws.efield_per_node && F > N) launch_fill_zero(ws.field_part, static_cast<std::size_t>(F) * 3, stream);
         field_adj_count = static_cast<std::int64_t>(h_efield.size());
+        evaluated_field = h_efield;
         field_evaluated = true;
+    }
+
+    void ensure_response() {
+        const std::size_t C = hm.C, NY = hm.num_lm, NH = hm.num_LM, NLME = hm.num_lme;
+        const std::size_t n = std::max(N, 1), e = std::max<std::int64_t>(E, 1);
+        const std::size_t zr = std::max(dm.field_zr, 1), yr = std::max(dm.field_yr, 1);
+        // each array starts on a 256-byte boundary
+        auto round = [](std::size_t v) { return (v + 63) / 64 * 64; };
+        const std::size_t sizes[] = {n * zr * C,   n * NH * C, n * yr * C,   n * NH * C,   n * C,      n * NH * C,
+                                     n * NLME * C, n * NY * C, n * C,        n * NY * C,   n * NY * C, n * NY * C,
+                                     n * NY * C,   n * C,      n * NLME * C, n * NH * C,   n * NH * C, n * yr * C,
+                                     n * NH * C,   n * NY * C, n * NY * C};
+        float** slots[] = {&rws.Z,          &rws.H1f_adj,    &rws.Y,         &rws.H1f_dot,   &rws.x_dot,
+                           &rws.H1_dot,     &rws.Phi1_dot,   &rws.A1_dot,    &rws.M1_dot,    &rws.g,
+                           &rws.gd,         &rws.A1_adj_dot, &rws.A1s_adj,   &rws.direct_dot, &rws.dPhi1_dot,
+                           &rws.H1_adj_dot, &rws.H1p_adj_dot, &rws.Y_dot,     &rws.M0_adj_dot, &rws.A0_adj_dot,
+                           &rws.Phi0_adj_dot};
+        static_assert(sizeof(sizes) / sizeof(sizes[0]) == sizeof(slots) / sizeof(slots[0]), "one size per array");
+        std::size_t total = 0;
+        for (std::size_t v : sizes) total += round(v);
+        float* base = static_cast<float*>(r_f32.ensure(total * sizeof(float)));
+        for (std::size_t a = 0; a < sizeof(sizes) / sizeof(sizes[0]); ++a) {
+            *slots[a] = base;
+            base += round(sizes[a]);
+        }
+        const std::size_t dsizes[] = {n, n, 3 * n, 3 * n, 9, 9, 9 * e, 9 * n};
+        std::size_t dtotal = 0;
+        for (std::size_t v : dsizes) dtotal += (v + 31) / 32 * 32;
+        double* d = static_cast<double*>(r_f64.ensure(dtotal * sizeof(double)));
+        double* at[8];
+        for (int a = 0; a < 8; ++a) {
+            at[a] = d;
+            d += (dsizes[a] + 31) / 32 * 32;
+        }
+        rws.dot_a = at[0];
+        rws.dot_b = at[1];
+        rws.part = at[2];
+        rws.part_scratch = at[3];
+        rws.unit = at[4];
+        rws.hessian_t = at[5];
+        rws.forces = at[6];
+        response_bins_dev = at[7];
+        const double unit[9] = {1, 0, 0, 0, 1, 0, 0, 0, 1};
+        SMX_HIP(hipMemcpyAsync(at[4], unit, sizeof(unit), hipMemcpyHostToDevice, stream));
+    }
+    double* response_bins_dev = nullptr;
+
+    // the tangents of the last evaluation in each field component
+    // (mace_kokkos_response.tpp:136-2343): the field Hessian, and with
+    // forces the directed forces' field derivative (per edge, or reduced to
+    // the atoms as Born charge bins)
+    void field_response(std::uint64_t token, const double* field, std::int64_t count, bool forces, bool bins) {
+        check_generation(token);
+        if (!hm.field) throw std::invalid_argument("the MACEField response requires field coupling");
+        if (count != 3 || !field)
+            throw std::invalid_argument("the MACEField response requires a graph-level electric field (3 values)");
+        if (!two_layer()) throw std::invalid_argument("the MACEField response runs two-interaction models");
+        if (phase != Phase::idle || feature_graph())
+            throw std::invalid_argument("the MACEField response runs on a graph without ghost feature nodes");
+        if (!evaluated || !field_evaluated || tiled)
+            throw std::logic_error(
+                "the MACEField response requires a completed field evaluation of the current graph token");
+        if (evaluated_field.size() != 3)
+            throw std::invalid_argument("the MACEField response requires an evaluation in a graph-level field");
+        for (int c = 0; c < 3; ++c)
+            if (field[c] != evaluated_field[c])
+                throw std::invalid_argument(
+                    "the response's electric field differs from the field of the completed evaluation");
+        ensure_response();
+        const DeviceGraph g = view();
+        const TileView& t = tiles[0];
+        LaunchTimer* tm = timer.get();
+        launch_fill_zero(rws.hessian_t, 9, stream);
+        // A1 rows of an l without paths are not written by its GEMM
+        if (std::find(hm.num_e.begin(), hm.num_e.end(), 0) != hm.num_e.end())
+            launch_fill_zero(rws.A1_dot, static_cast<std::size_t>(N) * hm.num_lm * hm.C, stream);
+        ks->field_response_prepare(dm, t, ws, rws, stream, tm);
+        for (int seed = 0; seed < 3; ++seed) ks->field_response_seed(dm, g, t, ws, rws, seed, forces, stream, tm);
+        if (forces && bins)
+            for (int seed = 0; seed < 3; ++seed)
+                launch_atom_forces(N, F, d_offsets.as<int>(), d_soff.as<int>(), d_sedges.as<int>(), nullptr,
+                                   rws.forces + static_cast<std::size_t>(seed) * 3 * E,
+                                   response_bins_dev + static_cast<std::size_t>(seed) * 3 * N, stream);
+        double ht[9];
+        SMX_HIP(hipMemcpyAsync(ht, rws.hessian_t, sizeof(ht), hipMemcpyDeviceToHost, stream));
+        sync();
+        for (int c = 0; c < 3; ++c)
+            for (int s = 0; s < 3; ++s) response_hessian[c * 3 + s] = ht[s * 3 + c];
+        response_done = true;
+        response_has_forces = forces && !bins;
+        response_has_bins = forces && bins;
+        response_N = N;
+        response_E = E;
     }
 
     void evaluate(const double* positions) {
@@ -2650,6 +2755,59 @@ int32_t smx_electric_field_adj(SmxEvaluator* ev, double* out, int64_t capacity, 
             for (int k = 0; k < e.F; ++k)
                 for (int c = 0; c < 3; ++c) out[3 * static_cast<std::size_t>(e.h_feature_of[k]) + c] = mine[3 * k + c];
         }
+    });
+}
+
+int32_t smx_compute_prepared_factorized_field_response(SmxEvaluator* ev, uint64_t generation, const double* field,
+                                                       int64_t field_count, int32_t include_force_derivative,
+                                                       int32_t scatter_bec_bins) {
+    return guarded([&] {
+        E(ev).field_response(generation, field, field_count, include_force_derivative != 0,
+                             include_force_derivative != 0 && scatter_bec_bins != 0);
+    });
+}
+
+int32_t smx_electric_field_hessian(SmxEvaluator* ev, double* out, int64_t capacity, int64_t* count) {
+    return guarded([&] {
+        auto& e = E(ev);
+        if (!e.response_done) throw std::logic_error("no MACEField response has run");
+        if (count) *count = 9;
+        if (!out) return;
+        if (capacity < 9) throw std::invalid_argument("buffer too small");
+        std::copy(e.response_hessian, e.response_hessian + 9, out);
+    });
+}
+
+int32_t smx_electric_field_force_derivative(SmxEvaluator* ev, double* out, int64_t capacity, int64_t* count) {
+    return guarded([&] {
+        auto& e = E(ev);
+        if (!e.response_done) throw std::logic_error("no MACEField response has run");
+        const std::int64_t n = e.response_has_forces ? 9 * e.response_E : 0;
+        if (count) *count = n;
+        if (!out || n == 0) return;
+        if (capacity < n) throw std::invalid_argument("buffer too small");
+        SMX_HIP(hipMemcpyAsync(out, e.rws.forces, n * sizeof(double), hipMemcpyDeviceToHost, e.stream));
+        SMX_HIP(hipStreamSynchronize(e.stream));
+    });
+}
+
+int32_t smx_electric_field_bec_bins(SmxEvaluator* ev, double* out, int64_t capacity, int64_t* count) {
+    return guarded([&] {
+        auto& e = E(ev);
+        if (!e.response_done) throw std::logic_error("no MACEField response has run");
+        const std::int64_t n = e.response_has_bins ? 9 * static_cast<std::int64_t>(e.response_N) : 0;
+        if (count) *count = n;
+        if (!out || n == 0) return;
+        if (capacity < n) throw std::invalid_argument("buffer too small");
+        // device [s][i][x] -> [i][s][x]
+        std::vector<double> t(n);
+        SMX_HIP(hipMemcpyAsync(t.data(), e.response_bins_dev, n * sizeof(double), hipMemcpyDeviceToHost, e.stream));
+        SMX_HIP(hipStreamSynchronize(e.stream));
+        const int N = e.response_N;
+        for (int s = 0; s < 3; ++s)
+            for (int i = 0; i < N; ++i)
+                for (int x = 0; x < 3; ++x)
+                    out[(static_cast<std::size_t>(i) * 3 + s) * 3 + x] = t[(static_cast<std::size_t>(s) * N + i) * 3 + x];
     });
 }
 

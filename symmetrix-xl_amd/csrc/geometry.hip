@@ -486,21 +486,43 @@ __device__ __forceinline__ int edge_row(const double* __restrict__ r, const int*
     return (edge_pair ? edge_pair[e] * intervals : 0) + interval;
 }
 
-// One wave per receiver: each lane ranks its edges (lane, lane + 64, ...)
-// against all of the receiver's edges, whose rows the wave reads in turn.
-// Order: (row, position); a rank is a slot of the receiver's segment.
-constexpr int kOrderWaves = 4;
-__global__ __launch_bounds__(64 * kOrderWaves) void k_execution_order(int r0, int nr, long long e0,
-                                                                      const int* __restrict__ offsets,
-                                                                      const double* __restrict__ r, double r_cut,
-                                                                      float x0, float h, int intervals,
-                                                                      const int* __restrict__ edge_pair,
-                                                                      int* __restrict__ exec) {
-    const int li = blockIdx.x * kOrderWaves + static_cast<int>(threadIdx.x) / 64;
-    const int lane = threadIdx.x % 64;
-    if (li >= nr) return;
+// One wave (workgroup) per receiver: each lane ranks its edges (lane, lane
+// + 64, ...) against all of the receiver's edges.  Order: (row, position); a
+// rank is a slot of the receiver's segment.  The rows of up to kOrderStage
+// edges are staged in LDS (padded to whole int4s with inactive rows, which
+// rank after every edge) and read back four at a time; a longer segment
+// reads them from the edge lengths.
+constexpr int kOrderStage = 512;
+__global__ __launch_bounds__(64) void k_execution_order(int r0, long long e0, const int* __restrict__ offsets,
+                                                        const double* __restrict__ r, double r_cut, float x0,
+                                                        float h, int intervals, const int* __restrict__ edge_pair,
+                                                        int* __restrict__ exec) {
+    __shared__ int4 rows4[kOrderStage / 4];
+    int* rows = reinterpret_cast<int*>(rows4);
+    const int li = blockIdx.x;
+    const int lane = threadIdx.x;
     const long long ea = offsets[r0 + li] - e0;
     const int n = offsets[r0 + li + 1] - offsets[r0 + li];
+    if (n <= kOrderStage) {
+        const int n4 = (n + 3) & ~3;
+        for (int j = lane; j < n4; j += 64)
+            rows[j] = j < n ? edge_row(r, edge_pair, ea + j, r_cut, x0, h, intervals) : INT_MAX;
+        __syncthreads();
+        for (int j0 = 0; j0 < n; j0 += 64) {
+            const int j = j0 + lane;
+            const int kj = j < n ? rows[j] : INT_MAX;
+            int rank = 0;
+            for (int m = 0; m < n4; m += 4) {
+                const int4 q = rows4[m >> 2];
+                rank += (q.x < kj || (q.x == kj && m < j)) ? 1 : 0;
+                rank += (q.y < kj || (q.y == kj && m + 1 < j)) ? 1 : 0;
+                rank += (q.z < kj || (q.z == kj && m + 2 < j)) ? 1 : 0;
+                rank += (q.w < kj || (q.w == kj && m + 3 < j)) ? 1 : 0;
+            }
+            if (j < n) exec[ea + rank] = static_cast<int>(ea + j);
+        }
+        return;
+    }
     for (int j0 = 0; j0 < n; j0 += 64) {
         const int j = j0 + lane;
         const int kj = j < n ? edge_row(r, edge_pair, ea + j, r_cut, x0, h, intervals) : INT_MAX;
@@ -828,8 +850,7 @@ int build_touched_sources(int N, std::int64_t e0, std::int64_t ne, const int* so
 void launch_execution_order(int r0, int nr, std::int64_t e0, const int* offsets, const double* r, double r_cut,
                             float x0, float h, int intervals, const int* edge_pair, int* exec, hipStream_t s) {
     if (nr == 0) return;
-    k_execution_order<<<blocks_for(nr, kOrderWaves), 64 * kOrderWaves, 0, s>>>(r0, nr, e0, offsets, r, r_cut, x0, h,
-                                                                             intervals, edge_pair, exec);
+    k_execution_order<<<nr, 64, 0, s>>>(r0, e0, offsets, r, r_cut, x0, h, intervals, edge_pair, exec);
     SMX_LAUNCH_CHECK("execution_order");
 }
 

@@ -720,6 +720,174 @@ __global__ __launch_bounds__(256) void k_field_adj_sum(int N, const double* __re
     }
 }
 
+// ---------------------------------------------------------------------------
+// MACEField response (mace_kokkos_response.tpp:136-2343): the tangent d/dE_s
+// of a completed evaluation for one field component s.  H1f is linear in the
+// field, so its tangent is the entries of component s applied to Z; the
+// other tangents run through the evaluation's own kernels (R1 forward and
+// reverse, node GEMMs, M0 reverse, R0 reverse) on tangent buffers, plus the
+// kernels below for the two nonlinear stages the reverse differentiates
+// again: the M1 polynomial and the readout MLP.
+// ---------------------------------------------------------------------------
+// H1f_dot[i,lm] = sum over the entries of component seed into lm of coef Z[i,zrow];
+// x_dot = H1f_dot[i,0,:]
+__global__ void k_field_tangent(int NH, int C, int zr, const FieldEntryDev* __restrict__ entries, int ne, int seed,
+                                const float* __restrict__ Z, float* __restrict__ H1f_dot, float* __restrict__ x_dot) {
+    const int i = static_cast<int>(blockIdx.x);
+    const int k = threadIdx.x;
+    const float* z = Z + static_cast<std::size_t>(i) * zr * C;
+    for (int lm = 0; lm < NH; ++lm) {
+        float v = 0.0f;
+        for (int e = 0; e < ne; ++e) {
+            const FieldEntryDev en = entries[e];
+            if (en.lm_out == lm && en.comp == seed) v += en.coef * z[static_cast<std::size_t>(en.zrow) * C + k];
+        }
+        H1f_dot[(static_cast<std::size_t>(i) * NH + lm) * C + k] = v;
+        if (lm == 0) x_dot[static_cast<std::size_t>(i) * C + k] = v;
+    }
+}
+
+// M1's tangent along A1_dot: M1_dot = sum_v g_v A1_dot_v, the gradient g and
+// its derivative gd along A1_dot (each factor of a term differentiated in
+// turn), from the monomial list in HBM.  Lanes are channels; a workgroup
+// holds kTangentLanes of them (blockIdx.y picks the channel block).
+constexpr int kTangentLanes = 128;
+template <int C, int NY>
+__global__ __launch_bounds__(C < kTangentLanes ? C : kTangentLanes) void k_m1_tangent(
+    const int* __restrict__ types, const float* __restrict__ A1, const float* __restrict__ A1_dot,
+    const std::int32_t* __restrict__ terms, int T1, const float* __restrict__ m1_coef, float* __restrict__ M1_dot,
+    float* __restrict__ g, float* __restrict__ gd) {
+    constexpr int L = C < kTangentLanes ? C : kTangentLanes;
+    static_assert(C % L == 0, "whole channel blocks");
+    __shared__ float xs[NY * L], dxs[NY * L], gs[NY * L], gds[NY * L];
+    const int i = static_cast<int>(blockIdx.x);
+    const int j = threadIdx.x;
+    const int k = static_cast<int>(blockIdx.y) * L + j;
+    const std::size_t row = static_cast<std::size_t>(i) * NY * C + k;
+#pragma unroll
+    for (int v = 0; v < NY; ++v) {
+        xs[v * L + j] = A1[row + v * C];
+        dxs[v * L + j] = A1_dot[row + v * C];
+        gs[v * L + j] = 0.0f;
+        gds[v * L + j] = 0.0f;
+    }
+    const float* cf = m1_coef + static_cast<std::size_t>(types[i]) * T1 * C + k;
+    float fd = 0.0f;
+    for (int t = 0; t < T1; ++t) {
+        const int pk = terms[t];
+        const float c = cf[static_cast<std::size_t>(t) * C];
+        const int deg = pk >> 24;
+        const int v0 = pk & 0xff, v1 = (pk >> 8) & 0xff, v2 = (pk >> 16) & 0xff;
+        const float x0 = xs[v0 * L + j], d0 = dxs[v0 * L + j];
+        if (deg == 1) {
+            gs[v0 * L + j] += c;
+            fd += c * d0;
+        } else if (deg == 2) {
+            const float x1 = xs[v1 * L + j], d1 = dxs[v1 * L + j];
+            gs[v0 * L + j] += c * x1;
+            gs[v1 * L + j] += c * x0;
+            gds[v0 * L + j] += c * d1;
+            gds[v1 * L + j] += c * d0;
+            fd += c * (x1 * d0 + x0 * d1);
+        } else {
+            const float x1 = xs[v1 * L + j], d1 = dxs[v1 * L + j];
+            const float x2 = xs[v2 * L + j], d2 = dxs[v2 * L + j];
+            gs[v0 * L + j] += c * x1 * x2;
+            gs[v1 * L + j] += c * x0 * x2;
+            gs[v2 * L + j] += c * x0 * x1;
+            gds[v0 * L + j] += c * (d1 * x2 + x1 * d2);
+            gds[v1 * L + j] += c * (d0 * x2 + x0 * d2);
+            gds[v2 * L + j] += c * (d0 * x1 + x0 * d1);
+            fd += c * (x1 * x2 * d0 + x0 * x2 * d1 + x0 * x1 * d2);
+        }
+    }
+    M1_dot[static_cast<std::size_t>(i) * C + k] = fd;
+#pragma unroll
+    for (int v = 0; v < NY; ++v) {
+        g[row + v * C] = gs[v * L + j];
+        gd[row + v * C] = gds[v * L + j];
+    }
+}
+
+// The readout's tangent for one node (FP64, one workgroup of C lanes): H2 and
+// H2_dot = T^T x_dot + W^T M1_dot, the MLP's pre-activations and their
+// tangents, H2_adj = sum_h W2 act'(z) W1 and H2_adj_dot = sum_h W2 act''(z)
+// z_dot W1, then direct_dot = T H2_adj_dot and the M1 adjoint and its tangent
+// W H2_adj(_dot), which scale the M1 gradient and its tangent into
+//   A1_adj_dot = g float(M1_adj_dot) + gd float(M1_adj)
+// and (a1s_adj non-null) the A1 adjoint itself, g float(M1_adj).
+template <int C>
+__global__ __launch_bounds__(C) void k_readout_tangent(
+    const int* __restrict__ types, int NY, const float* __restrict__ M1, const float* __restrict__ M1_dot,
+    const float* __restrict__ xaff, const float* __restrict__ x_dot, const float* __restrict__ H2_T,
+    const float* __restrict__ H2_Tt, const float* __restrict__ H2_M1, const float* __restrict__ H2_M1t,
+    const double* __restrict__ W1r, const double* __restrict__ W2r, int hidden, double scale,
+    const float* __restrict__ g, const float* __restrict__ gd, float* __restrict__ direct_dot,
+    float* __restrict__ A1_adj_dot, float* __restrict__ a1s_adj) {
+    __shared__ double sx[C], sxd[C], sm[C], smd[C], sh[C], shd[C];
+    __shared__ double sa[kMaxReadoutHidden], sad[kMaxReadoutHidden];
+    const int i = static_cast<int>(blockIdx.x);
+    const int k = threadIdx.x;
+    const int t = types[i];
+    sx[k] = xaff[static_cast<std::size_t>(i) * C + k];
+    sxd[k] = x_dot[static_cast<std::size_t>(i) * C + k];
+    sm[k] = M1[static_cast<std::size_t>(i) * C + k];
+    smd[k] = M1_dot[static_cast<std::size_t>(i) * C + k];
+    __syncthreads();
+    {
+        const float* T = H2_T + static_cast<std::size_t>(t) * C * C;
+        double h = 0.0, hd = 0.0;
+        for (int in = 0; in < C; ++in) {
+            const double a = T[in * C + k], b = H2_M1[in * C + k];
+            h += a * sx[in] + b * sm[in];
+            hd += a * sxd[in] + b * smd[in];
+        }
+        sh[k] = h;
+        shd[k] = hd;
+    }
+    __syncthreads();
+    for (int hdn = k; hdn < hidden; hdn += C) {
+        const double* w1 = W1r + static_cast<std::size_t>(hdn) * C;
+        double z = 0.0, zd = 0.0;
+        for (int c = 0; c < C; ++c) {
+            z += w1[c] * sh[c];
+            zd += w1[c] * shd[c];
+        }
+        const double sg = 1.0 / (1.0 + exp(-z));
+        // act(z) = scale z sigmoid(z): act' and act''
+        const double act1 = scale * sg + scale * z * sg * (1.0 - sg);
+        const double act2 = scale * sg * (1.0 - sg) * (2.0 + z * (1.0 - 2.0 * sg));
+        sa[hdn] = W2r[hdn] * act1;
+        sad[hdn] = W2r[hdn] * act2 * zd;
+    }
+    __syncthreads();
+    double ha = 0.0, had = 0.0;
+    for (int hdn = 0; hdn < hidden; ++hdn) {
+        const double w = W1r[static_cast<std::size_t>(hdn) * C + k];
+        ha += sa[hdn] * w;
+        had += sad[hdn] * w;
+    }
+    __syncthreads();
+    sh[k] = ha;
+    shd[k] = had;
+    __syncthreads();
+    const float* Tt = H2_Tt + static_cast<std::size_t>(t) * C * C;
+    double dd = 0.0, m1a = 0.0, m1ad = 0.0;
+    for (int o = 0; o < C; ++o) {
+        const double wt = H2_M1t[o * C + k];
+        dd += static_cast<double>(Tt[o * C + k]) * shd[o];
+        m1a += wt * sh[o];
+        m1ad += wt * shd[o];
+    }
+    direct_dot[static_cast<std::size_t>(i) * C + k] = static_cast<float>(dd);
+    const float fa = static_cast<float>(m1a), fad = static_cast<float>(m1ad);
+    for (int v = 0; v < NY; ++v) {
+        const std::size_t q = (static_cast<std::size_t>(i) * NY + v) * C + k;
+        A1_adj_dot[q] = g[q] * fad + gd[q] * fa;
+        if (a1s_adj) a1s_adj[q] = g[q] * fa;
+    }
+}
+
 __global__ void k_fill_f32(std::size_t n, float* __restrict__ p) {
     for (std::size_t j = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x; j < n;
          j += static_cast<std::size_t>(gridDim.x) * blockDim.x)
@@ -1331,6 +1499,129 @@ struct KernelSetImpl final : KernelSet {
         if (m.A0_scaled) {
             TimerScope ts(tm, "a0_density_forces", s);
             launch_density_forces(m, g, t, w.dens_s0, w.dens_dot0, nullptr, nullptr, w.node_forces, s);
+        }
+    }
+
+    void field_response_prepare(const DeviceModel& m, const TileView& t, const Workspace& w,
+                                const ResponseWorkspace& rw, hipStream_t s, LaunchTimer* tm) const override {
+        if constexpr (LMAXH == 0) {
+            throw std::invalid_argument("MACEField models have a hidden L_max of 1 or 2");
+        } else {
+            if (t.nr == 0) return;
+            TimerScope ts(tm, "field_response_prepare", s);
+            launch_node_gemm(t.fz, m.field_W, w.H1p, rw.Z, s);
+            launch_node_gemm(t.h1, m.U_wt, w.H1_adj, rw.H1f_adj, s);
+            k_field_direct_add<<<t.nr, C, 0, s>>>(0, S::NH, C, w.direct, rw.H1f_adj);
+            SMX_LAUNCH_CHECK("field_direct_add");
+            launch_node_gemm(t.fy, m.field_Wt, rw.H1f_adj, rw.Y, s);
+        }
+    }
+
+    // One field component's tangent (mace_kokkos_response.tpp:396-2343) over
+    // the direct plan's single tile (receivers and feature nodes are the
+    // same N nodes, r0 = e0 = 0)
+    void field_response_seed(const DeviceModel& m, const DeviceGraph& g, const TileView& t, const Workspace& w,
+                             const ResponseWorkspace& rw, int seed, bool forces, hipStream_t s,
+                             LaunchTimer* tm) const override {
+        if constexpr (LMAXH == 0) {
+            throw std::invalid_argument("MACEField models have a hidden L_max of 1 or 2");
+        } else {
+            const int N = t.nr;
+            if (N == 0) return;
+            double* f = rw.forces + static_cast<std::size_t>(seed) * 3 * t.ne;
+            TimerScope ts(tm, "field_response", s);
+            // H1f_dot (and x_dot), H1_dot = H1f_dot U
+            k_field_tangent<<<N, C, 0, s>>>(S::NH, C, m.field_zr, m.field_entries, m.num_field_entries, seed, rw.Z,
+                                            rw.H1f_dot, rw.x_dot);
+            SMX_LAUNCH_CHECK("field_tangent");
+            launch_node_gemm(t.h1, m.U_w, rw.H1f_dot, rw.H1_dot, s);
+            // Phi1_dot: the R1 forward of H1_dot; A1_dot (density-scaled like A1)
+            static_for<0, kGroups>([&](auto gc) {
+                constexpr int gi = gc;
+                constexpr int SL = r1_forward_slices<C, Records>();
+                k_r1_forward<C, LMAX, LMAXH, Groups::masks[gi], (gi > 0), Records>
+                    <<<r1_forward_blocks<C, Records>(N), C / SL, 0, s>>>(0, N, g.offsets, nullptr, g.neigh,
+                                                                         records(m, t, w), rw.H1_dot, m.cg,
+                                                                         rw.Phi1_dot);
+                SMX_LAUNCH_CHECK("r1_forward");
+            });
+            launch_node_gemm(t.a1f, m.A1_w, rw.Phi1_dot, rw.A1_dot, s);
+            if (m.A1_scaled) launch_density_scale(N, S::NY * C, w.dens_s1, false, rw.A1_dot, s);
+            // M1_dot, the M1 gradient and its tangent; the readout's tangent
+            constexpr int TL = C < kTangentLanes ? C : kTangentLanes;
+            k_m1_tangent<C, S::NY><<<dim3(N, C / TL), TL, 0, s>>>(g.node_types, w.A1, rw.A1_dot, m.m1_terms, m.T1,
+                                                                  m.m1_coef, rw.M1_dot, rw.g, rw.gd);
+            SMX_LAUNCH_CHECK("m1_tangent");
+            k_readout_tangent<C><<<N, C, 0, s>>>(g.node_types, S::NY, w.M1, rw.M1_dot, w.xaff, rw.x_dot, m.H2_T,
+                                                 m.H2_Tt, m.H2_M1, m.H2_M1t, m.W1r, m.W2r, m.hidden,
+                                                 m.readout_scale, rw.g, rw.gd, rw.direct_dot, rw.A1_adj_dot,
+                                                 m.A1_scaled ? rw.A1s_adj : nullptr);
+            SMX_LAUNCH_CHECK("readout_tangent");
+            if (m.A1_scaled) {
+                // the scale's adjoint dot product sum A1_adj A1 and its tangent
+                // (both factors), then the adjoint's tangent scaled by 1/s
+                launch_density_adjoint(N, S::NY * C, w.A1, w.dens_s1, false, rw.A1_adj_dot, rw.dot_a, s);
+                launch_density_adjoint(N, S::NY * C, rw.A1_dot, w.dens_s1, false, rw.A1s_adj, rw.dot_b, s);
+            }
+            launch_node_gemm(t.a1r, m.A1_wt, rw.A1_adj_dot, rw.dPhi1_dot, s);
+            // the R1 reverse, bilinear in (H1, dPhi1): (H1, dPhi1_dot) gives
+            // the source terms of H1_adj_dot and part of the forces,
+            // (H1_dot, dPhi1) the rest of the forces (its source terms unused)
+            static_for<0, kGroups>([&](auto gc) {
+                constexpr int gi = gc;
+                k_r1_reverse<C, LMAX, LMAXH, Groups::masks[gi], (gi > 0), StagedRecords><<<N, C, 0, s>>>(
+                    0, 0, g.offsets, g.neigh, records<StagedRecords>(m, t, w), w.H1, m.cg, rw.dPhi1_dot, w.Wsrc, f);
+                SMX_LAUNCH_CHECK("r1_reverse");
+            });
+            k_source_gather<C, S::NH, false><<<g.F, C, 0, s>>>(g.soff, g.sedges, w.Wsrc, t.r, m.r_cut,
+                                                               rw.H1_adj_dot);
+            SMX_LAUNCH_CHECK("source_gather");
+            if (forces) {
+                static_for<0, kGroups>([&](auto gc) {
+                    constexpr int gi = gc;
+                    k_r1_reverse<C, LMAX, LMAXH, Groups::masks[gi], true, StagedRecords><<<N, C, 0, s>>>(
+                        0, 0, g.offsets, g.neigh, records<StagedRecords>(m, t, w), rw.H1_dot, m.cg, w.dPhi1, w.Wsrc,
+                        f);
+                    SMX_LAUNCH_CHECK("r1_reverse");
+                });
+                if (m.A1_scaled) {
+                    launch_density_forces(m, g, t, nullptr, nullptr, w.dens_s1, rw.dot_a, f, s);
+                    launch_density_forces(m, g, t, nullptr, nullptr, w.dens_s1, rw.dot_b, f, s);
+                }
+            }
+            // the field terms' reverse: H1f_adj_dot = H1_adj_dot U^T (+
+            // direct_dot), its path products Y_dot, then H1p_adj_dot += coef
+            // (E Y_dot + [c = seed] Y) with the Hessian column from Y_dot
+            launch_node_gemm(t.h1, m.U_wt, rw.H1_adj_dot, rw.H1p_adj_dot, s);
+            k_field_direct_add<<<N, C, 0, s>>>(0, S::NH, C, rw.direct_dot, rw.H1p_adj_dot);
+            SMX_LAUNCH_CHECK("field_direct_add");
+            launch_node_gemm(t.fy, m.field_Wt, rw.H1p_adj_dot, rw.Y_dot, s);
+            k_field_reverse_combine<C><<<N, C, 0, s>>>(0, S::NH, m.field_yr, m.field_entries, m.num_field_entries,
+                                                       w.efield, 0, w.H1p, rw.Y_dot, rw.H1p_adj_dot, rw.part);
+            SMX_LAUNCH_CHECK("field_reverse_combine");
+            k_field_adj_sum<<<1, 256, 0, s>>>(N, rw.part, rw.hessian_t + 3 * seed);
+            SMX_LAUNCH_CHECK("field_adj_sum");
+            k_field_reverse_combine<C><<<N, C, 0, s>>>(0, S::NH, m.field_yr, m.field_entries, m.num_field_entries,
+                                                       rw.unit + 3 * seed, 0, w.H1p, rw.Y, rw.H1p_adj_dot,
+                                                       rw.part_scratch);
+            SMX_LAUNCH_CHECK("field_reverse_combine");
+            if (!forces) return;
+            // the layer-1 reverse of H1p_adj_dot (M0 and A0 do not depend on
+            // the field): M0_adj_dot, A0_adj_dot (density scale), the R0 reverse
+            launch_node_gemm(t.h1, m.P_wt, rw.H1p_adj_dot, rw.M0_adj_dot, s);
+            if constexpr (kM0Unrolled)
+                k_m0_reverse_ct<C, S::NY, S::NH, M0TAB><<<N, C, 0, s>>>(0, g.node_types, w.A0, rw.M0_adj_dot, nullptr,
+                                                                       m.m0_coef, rw.A0_adj_dot);
+            else
+                k_m0_reverse<C, S::NY, S::NH><<<N, C, 0, s>>>(0, g.node_types, w.A0, rw.M0_adj_dot, nullptr,
+                                                             m.m0_terms, m.m0_toff, m.T0, m.m0_coef, rw.A0_adj_dot);
+            SMX_LAUNCH_CHECK("m0_reverse");
+            if (m.A0_scaled) launch_density_adjoint(N, S::NY * C, w.A0, w.dens_s0, true, rw.A0_adj_dot, rw.dot_a, s);
+            launch_node_gemm(t.a0, m.A0_wt, rw.A0_adj_dot, rw.Phi0_adj_dot, s);
+            k_r0_reverse<C, LMAX, true><<<N, C, 0, s>>>(0, 0, g.offsets, w.erec, w.erec_b, m.R0c, m.H0,
+                                                        rw.Phi0_adj_dot, f);
+            SMX_LAUNCH_CHECK("r0_reverse");
+            if (m.A0_scaled) launch_density_forces(m, g, t, w.dens_s0, rw.dot_a, nullptr, nullptr, f, s);
         }
     }
 };

@@ -220,6 +220,40 @@ struct Workspace {
     bool field_reverse_done = false;
 };
 
+// MACEField response buffers (direct plan, graph-wide, N nodes and E edges):
+// the tangents of one field component's pass, reused for each component.
+struct ResponseWorkspace {
+    // seed-independent: Z = H1p W, H1f_adj = H1_adj U^T (+ direct), Y = H1f_adj W^T
+    float* Z = nullptr;          // [N][zr][C]
+    float* H1f_adj = nullptr;    // [N][NH][C]
+    float* Y = nullptr;          // [N][yr][C]
+    float* H1f_dot = nullptr;    // [N][NH][C]
+    float* x_dot = nullptr;      // [N][C]
+    float* H1_dot = nullptr;     // [N][NH][C]
+    float* Phi1_dot = nullptr;   // [N][NLME][C]
+    float* A1_dot = nullptr;     // [N][NY][C]
+    float* M1_dot = nullptr;     // [N][C]
+    float* g = nullptr;          // [N][NY][C] dM1/dA1
+    float* gd = nullptr;         // [N][NY][C] its tangent
+    float* A1_adj_dot = nullptr; // [N][NY][C]
+    float* A1s_adj = nullptr;    // [N][NY][C] (A1 density scaling)
+    float* direct_dot = nullptr; // [N][C]
+    float* dPhi1_dot = nullptr;  // [N][NLME][C]
+    float* H1_adj_dot = nullptr; // [N][NH][C]
+    float* H1p_adj_dot = nullptr;  // [N][NH][C]
+    float* Y_dot = nullptr;      // [N][yr][C]
+    float* M0_adj_dot = nullptr; // [N][NH][C]
+    float* A0_adj_dot = nullptr; // [N][NY][C]
+    float* Phi0_adj_dot = nullptr;  // [N][NY][C]
+    double* dot_a = nullptr;     // [N] density adjoint dot products
+    double* dot_b = nullptr;     // [N]
+    double* part = nullptr;      // [N][3]
+    double* part_scratch = nullptr;  // [N][3]
+    const double* unit = nullptr;    // [3][3] the unit field of each component
+    double* hessian_t = nullptr;     // [3][3]: [s][c] = d(dE/dE_c)/dE_s
+    double* forces = nullptr;        // [3][E][3] directed forces' tangent per component
+};
+
 // Timing hook: the evaluator brackets launches with events when enabled.
 struct LaunchTimer {
     virtual ~LaunchTimer() = default;
@@ -275,6 +309,16 @@ struct KernelSet {
                                 LaunchTimer* tm) const = 0;
     virtual void field_features_reverse(const DeviceModel& m, const TileView& t, const Workspace& w, int direct_rows,
                                         hipStream_t s, LaunchTimer* tm) const = 0;
+    // MACEField response of the last direct-plan evaluation (t: its one
+    // tile, every receiver; w: its retained state, w.Wsrc taken as scratch):
+    // the seed-independent products, then one field component's tangent
+    // pass: the Hessian column rw.hessian_t[seed] and, with forces, the
+    // directed forces' tangent rw.forces[seed]
+    virtual void field_response_prepare(const DeviceModel& m, const TileView& t, const Workspace& w,
+                                        const ResponseWorkspace& rw, hipStream_t s, LaunchTimer* tm) const = 0;
+    virtual void field_response_seed(const DeviceModel& m, const DeviceGraph& g, const TileView& t,
+                                     const Workspace& w, const ResponseWorkspace& rw, int seed, bool forces,
+                                     hipStream_t s, LaunchTimer* tm) const = 0;
 };
 
 // Message returned by smx_last_error() on the calling thread.

@@ -125,6 +125,10 @@ SIGNATURES = [
     ("smx_set_electric_field", _i32, [_vp, _vp, _i64]),
     ("smx_electric_field_adj", _i32, [_vp, _vp, _i64, _p_i64]),
     ("smx_has_field_coupling", _i32, [_vp, _p_i32]),
+    ("smx_compute_prepared_factorized_field_response", _i32, [_vp, _u64, _vp, _i64, _i32, _i32]),
+    ("smx_electric_field_hessian", _i32, [_vp, _vp, _i64, _p_i64]),
+    ("smx_electric_field_force_derivative", _i32, [_vp, _vp, _i64, _p_i64]),
+    ("smx_electric_field_bec_bins", _i32, [_vp, _vp, _i64, _p_i64]),
     ("smx_compute_prepared_factorized_positions_device", _i32, [_vp, _u64, _vp]),
     ("smx_compute_node_energies_forces", _i32, [_vp, _i32, _vp, _vp, _i64, _vp, _vp, _vp, _vp]),
     ("smx_reduce_prepared_node_forces", _i32, [_vp, _u64, _vp]),

@@ -146,6 +146,8 @@ class Symmetrix(_Base):
     streamed edges)."""
 
     implemented_properties = ["energy", "free_energy", "energies", "forces", "stress"]
+    # vacuum permittivity in e / (V A) (calculator.py:729)
+    _macefield_eps0 = 8.8541878128e-12 / 1.602176634e-19 / 1e10
 
     def __init__(self, model_file, dtype="float32", use_kokkos=True, streamed_edges="direct",
                  execution_profile="capacity", allow_fixed_workspace=False, neighbor_skin=0.5, head=None,
@@ -195,7 +197,8 @@ class Symmetrix(_Base):
         # electric field, and the polarization -dE/dE / V among the results
         self._electric_field = electric_field
         if getattr(self.evaluator, "has_field_coupling", False):
-            self.implemented_properties = list(self.implemented_properties) + ["polarization"]
+            self.implemented_properties = list(self.implemented_properties) + ["polarization", "becs",
+                                                                               "polarizability"]
 
     @property
     def electric_field(self):
@@ -330,7 +333,8 @@ class Symmetrix(_Base):
     # ---------------------------------------------------------- calculate
     def calculate(self, atoms=None, properties=None, system_changes=_all_changes):
         if properties is None:
-            properties = self.implemented_properties
+            # the response properties run only when asked for
+            properties = [p for p in self.implemented_properties if p not in ("becs", "polarizability")]
         if HAVE_ASE:
             super().calculate(atoms, properties, system_changes)
             atoms = self.atoms
@@ -362,6 +366,17 @@ class Symmetrix(_Base):
             if not volume > 0.0:
                 raise ValueError("polarization needs a cell of non-zero volume")
             self.results["polarization"] = -np.asarray(ev.electric_field_adj, dtype=float) / volume
+            # calculator.py:3783-3817: polarizability -d2E/dE2 / (V eps0), Born
+            # charges dF_i/dE from the device bins (one response for both)
+            want_becs = "becs" in properties
+            if want_becs or "polarizability" in properties:
+                ev._compute_prepared_factorized_field_response(cache.generation, field, want_becs,
+                                                               scatter_bec_bins=want_becs)
+                if "polarizability" in properties:
+                    pol = -np.asarray(ev.electric_field_hessian, dtype=float).reshape(3, 3)
+                    self.results["polarizability"] = np.array((pol / volume / self._macefield_eps0).reshape(9))
+                if want_becs:
+                    self.results["becs"] = np.array(ev.electric_field_bec_bins, dtype=float).reshape(len(numbers), 9)
         return self.results
 
     def get_property(self, name, atoms=None, allow_calculation=True):

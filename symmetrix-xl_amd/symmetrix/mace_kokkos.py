@@ -447,6 +447,92 @@ class MACEKokkosFloat:
         check(lib.smx_electric_field_adj(self._h, ptr(out), out.size, None))
         return out
 
+    # MACEField response (pybind mace_kokkos.cpp:1865-1879, 2160-2167,
+    # 2226-2349; mace_kokkos_response.tpp)
+    _CURRENT_RESPONSE_ERROR = ("MACEField current response requires a completed prepared Execution evaluation for "
+                               "the current graph token.")
+
+    def _compute_prepared_factorized_field_response(self, execution_graph_generation, electric_field,
+                                                    include_force_derivative, scatter_bec_bins=False):
+        """The field Hessian and (include_force_derivative) the directed
+        forces' field derivative, or with scatter_bec_bins the Born charge
+        bins, of the completed field evaluation of this graph token."""
+        field = f64(electric_field)
+        if field.size != 3:
+            raise ValueError("MACEKokkos::compute_electric_field_hessian requires a graph-level electric field.")
+        check(lib.smx_compute_prepared_factorized_field_response(
+            self._h, int(execution_graph_generation), ptr(field), field.size, int(bool(include_force_derivative)),
+            int(bool(scatter_bec_bins))))
+
+    def _response_values(self, fn):
+        n = ctypes.c_int64()
+        check(fn(self._h, None, 0, ctypes.byref(n)))
+        out = np.zeros(n.value)
+        if n.value:
+            check(fn(self._h, ptr(out), out.size, None))
+        return out
+
+    @property
+    def electric_field_hessian(self):
+        """[c*3 + s] = d(dE/dE_c)/dE_s of the last response (9 values)."""
+        return self._response_values(lib.smx_electric_field_hessian).tolist()
+
+    @property
+    def electric_field_force_derivative(self):
+        """[s][edge][3] flattened: each edge's directed-force derivative in
+        field component s (empty when the last response took none)."""
+        return self._response_values(lib.smx_electric_field_force_derivative).tolist()
+
+    @property
+    def electric_field_bec_bins(self):
+        """Born charge bins [num_nodes][s][3] = dF/dE_s of the last response
+        that scattered them (shape (0, 3, 3) otherwise)."""
+        return self._response_values(lib.smx_electric_field_bec_bins).reshape(-1, 3, 3)
+
+    def _host_graph_response(self, num_nodes, node_types, num_neigh, neigh_indices, neigh_types, xyz, r,
+                             electric_field, forces):
+        token = self._prepare_factorized_graph(num_nodes, node_types, num_neigh, neigh_indices, neigh_types)
+        self._compute_prepared_factorized_field(token, xyz, r, electric_field)
+        self._compute_prepared_factorized_field_response(token, electric_field, forces)
+
+    def compute_electric_field_hessian(self, num_nodes, node_types, num_neigh, neigh_indices, neigh_types, xyz, r,
+                                       electric_field):
+        """Evaluate the host graph in the field, then its field Hessian
+        (mace_kokkos_response.tpp:2394-2408)."""
+        if not self.has_field_coupling:
+            raise ValueError("MACEKokkos::compute_electric_field_hessian requires field coupling.")
+        self._host_graph_response(num_nodes, node_types, num_neigh, neigh_indices, neigh_types, xyz, r,
+                                  electric_field, False)
+
+    def compute_electric_field_force_derivative(self, num_nodes, node_types, num_neigh, neigh_indices, neigh_types,
+                                                xyz, r, electric_field):
+        """Evaluate the host graph in the field, then the Hessian and the
+        per-edge force derivative (mace_kokkos_response.tpp:2436-2450)."""
+        if not self.has_field_coupling:
+            raise ValueError("MACEKokkos::compute_electric_field_hessian requires field coupling.")
+        self._host_graph_response(num_nodes, node_types, num_neigh, neigh_indices, neigh_types, xyz, r,
+                                  electric_field, True)
+
+    def _current_response(self, graph_generation, electric_field, forces, bins):
+        if not graph_generation:
+            raise RuntimeError(self._CURRENT_RESPONSE_ERROR)
+        self._compute_prepared_factorized_field_response(graph_generation, electric_field, forces, bins)
+
+    def _compute_current_electric_field_hessian(self, num_nodes, node_types, num_neigh, neigh_indices, neigh_types,
+                                                xyz, r, electric_field, graph_generation):
+        """The response of the completed evaluation of graph_generation (the
+        graph arrays are those of the prepared graph;
+        mace_kokkos_response.tpp:2410-2434)."""
+        self._current_response(graph_generation, electric_field, False, False)
+
+    def _compute_current_electric_field_force_derivative(self, num_nodes, node_types, num_neigh, neigh_indices,
+                                                         neigh_types, xyz, r, electric_field, graph_generation):
+        self._current_response(graph_generation, electric_field, True, False)
+
+    def _compute_current_electric_field_bec_bins(self, num_nodes, node_types, num_neigh, neigh_indices,
+                                                 neigh_types, xyz, r, electric_field, graph_generation):
+        self._current_response(graph_generation, electric_field, True, True)
+
     def _compute_prepared_factorized_positions_device(self, execution_graph_generation, positions_device_ptr):
         check(lib.smx_compute_prepared_factorized_positions_device(self._h, int(execution_graph_generation),
                                                                    ctypes.c_void_p(positions_device_ptr)))
