@@ -238,7 +238,7 @@ def main():
     ap.add_argument("--no-calculator", action="store_true", help="skip the calculator-boundary timing")
     ap.add_argument("--no-configs", action="store_true", help="skip the wide, irregular and one-interaction configs")
     ap.add_argument("--no-lammps", action="store_true", help="skip the LAMMPS pair-style step timing")
-    ap.add_argument("--only-config", choices=("wide", "irregular", "single"),
+    ap.add_argument("--only-config", choices=("wide", "irregular", "single", "field"),
                     help="run only that config (3 warm-ups, median of 10) and print its summary")
     ap.add_argument("--capacity-steps", type=int, default=20,
                     help="NVE steps of the tiled 11.5M-atom capacity extra key (0 skips it)")
@@ -261,6 +261,9 @@ def main():
         return
 
     from symmetrix import random_model, systems
+    if args.only_config == "field":
+        print(json.dumps(field_response_protocol(hip_lib(), 0.5)), flush=True)
+        return
     if args.only_config:
         model_path, system, workload = config_case(args.only_config)
         print(json.dumps(summary(run_config(hip_lib(), model_path, system, 0.5, 3, 10), workload)), flush=True)
@@ -319,6 +322,8 @@ def main():
             cfg_model, cfg_system, workload = config_case(name)
             out["configs"][name] = summary(run_config(hip, cfg_model, cfg_system, skin, 3, 10), workload)
             note("%s: %s" % (name, out["configs"][name]))
+        out["field_response"] = field_response_protocol(hip, skin)
+        note("field response: %s" % out["field_response"])
     if args.capacity_steps > 0:
         try:
             out["capacity"] = capacity(132, args.capacity_steps, args.tile_receivers)
@@ -328,6 +333,57 @@ def main():
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(model_path, skin)
     print(json.dumps(out), flush=True)
+
+
+def field_response_protocol(hip, skin):
+    """The MACEField path at the benchmark size: the field_l2 model (128
+    channels, 0e+1o+2e hidden, l_max 3, correlation 3, a first-interaction
+    residual) on the medium SrTiO3 system in a graph field; the evaluation
+    (E, F, S and dE/dE, device positions) and then its response (the field
+    Hessian and the Born charge bins: three tangent passes), 3 warm-ups and
+    the median of 10 of each."""
+    from symmetrix import random_model, systems
+    from symmetrix.mace_kokkos import MACEKokkosFloat
+    from symmetrix._native import check, lib
+    model_path = random_model.cached_model("field_l2")
+    system = systems.srtio3_supercell(10, sigma=0.05, seed=0)
+    field = np.array([0.12, -0.21, 0.27])
+    ev = MACEKokkosFloat(model_path)
+    lut = {z: i for i, z in enumerate(ev.atomic_numbers)}
+    types = np.array([lut[int(z)] for z in system["numbers"]], np.int32)
+    cell = np.asarray(system["cell"], float)
+    vol = abs(float(np.linalg.det(cell)))
+    n = len(types)
+    g = ev._prepare_periodic_factorized_graph(types, system["positions"], cell, np.linalg.inv(cell), ev.r_cut + skin)
+    gen = g["generation"]
+    ev._set_electric_field(field)
+    d_pos = device_copy_of(hip, np.ascontiguousarray(system["positions"], dtype=np.float64))
+
+    def evaluation():
+        ev._compute_prepared_factorized_positions_device(gen, d_pos.value)
+        check(lib.smx_reduce_prepared_node_forces(ev._h, gen, None))
+        check(lib.smx_reduce_prepared_stress(ev._h, gen, vol, None))
+        ev.synchronize()
+
+    def response():
+        ev._compute_prepared_factorized_field_response(gen, field, True, scatter_bec_bins=True)
+
+    out = {"workload": "field_l2 MACEField model (128x(0e+1o+2e), l_max 3, corr 3, residual) on SrTiO3 10x10x10 "
+                       "(5000 atoms), graph field, r_cut 5.0 A + 0.5 A skin",
+           "atoms": n, "edges": int(g["num_edges"])}
+    for key, fn in (("evaluation_ms", evaluation), ("response_ms", response)):
+        for _ in range(3):
+            fn()
+        times = []
+        for _ in range(10):
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+        out[key] = round(statistics.median(times) * 1e3, 3)
+    out["response_per_component_us_per_atom"] = round(out["response_ms"] * 1e3 / 3 / n, 4)
+    hip.hipFree(d_pos)
+    ev.close()
+    return out
 
 
 def config_case(name):
