@@ -523,7 +523,7 @@ struct SourceGroups<LMAX, 2> {
 // ranges, one per group of XCDs (ranges of nearby atoms share sources).
 template <int C, class EDGES>
 constexpr int r1_forward_slices() {
-    return (EDGES::kHold && C >= 128 && kXcds % (C / 64) == 0) ? C / 64 : 1;
+    return (EDGES::kHold && C >= 128 && kXcds % (C >= 128 ? C / 64 : 1) == 0) ? C / 64 : 1;
 }
 // grid of the forward over nr receivers (padded to whole rounds of XCDs)
 template <int C, class EDGES>
@@ -690,7 +690,9 @@ __global__ __launch_bounds__(C) void k_r1_forward(int r0, int nr, const int* __r
 // rows hold CF channels (lanes k >= CF read zero, so their G, W and force
 // parts are zero); W rows always hold C.
 // ---------------------------------------------------------------------------
-template <int C, int LMAX, int LMAXH, unsigned MASK, bool FORCE_ACCUMULATE, class EDGES, int CF = C>
+// STORE_W false: the forces alone (the source terms are not written)
+template <int C, int LMAX, int LMAXH, unsigned MASK, bool FORCE_ACCUMULATE, class EDGES, int CF = C,
+          bool STORE_W = true>
 __global__ __launch_bounds__(C) void k_r1_reverse(int r0, long long e0, const int* __restrict__ offsets,
                                                   const int* __restrict__ neigh, EDGES edges,
                                                   const float* __restrict__ H1, const float* __restrict__ cg,
@@ -745,7 +747,8 @@ __global__ __launch_bounds__(C) void k_r1_reverse(int r0, long long e0, const in
                 sink.zero(j);
                 continue;
             }
-            float* wdst = Wsrc + static_cast<std::size_t>(edges.out_row(chunk, j, e - e0)) * NH * C + k;
+            [[maybe_unused]] float* wdst =
+                STORE_W ? Wsrc + static_cast<std::size_t>(edges.out_row(chunk, j, e - e0)) * NH * C + k : nullptr;
             if constexpr (EDGES::kReuse) {
                 // the row's coefficients stay in registers while consecutive
                 // slots share it (the row is wave-uniform)
@@ -835,9 +838,11 @@ __global__ __launch_bounds__(C) void k_r1_reverse(int r0, long long e0, const in
             }
             // W is streamed (read once, by the source gather): keep it out of
             // the cache lines that H1 and the spline table reuse
+            if constexpr (STORE_W) {
 #pragma unroll
-            for (int q = 0; q < NH; ++q)
-                if (RG::component(q)) __builtin_nontemporal_store(W[q], wdst + q * C);
+                for (int q = 0; q < NH; ++q)
+                    if (RG::component(q)) __builtin_nontemporal_store(W[q], wdst + q * C);
+            }
             sink.put(j, edges.u(pt, 0) * A + b0, edges.u(pt, 1) * A + b1, edges.u(pt, 2) * A + b2);
         }
         sink.template flush<FORCE_ACCUMULATE>(n, node_forces,

@@ -639,25 +639,32 @@ __global__ __launch_bounds__(256) void k_type_bias(int r0, int nr, const int* __
 // mix the m components with the entries' coef E_comp.
 // ---------------------------------------------------------------------------
 // H1f[i,lm] = H1p[i,lm] + sum over the entries into lm of coef E_comp Z[i,zrow];
-// x = H1f[i,0,:] (the scalar input of readout_1 and the skip)
-__global__ void k_field_combine(int r0, int NH, int C, int zr, const FieldEntryDev* __restrict__ entries, int ne,
-                                const double* __restrict__ field, int per_node, const float* __restrict__ H1p,
-                                const float* __restrict__ Z, float* __restrict__ H1f, float* __restrict__ xaff) {
+// x = H1f[i,0,:] (the scalar input of readout_1 and the skip).  One pass
+// over the entries with the NH rows of the lane's channel in registers (each
+// row takes its entries in list order).
+template <int C, int NH>
+__global__ __launch_bounds__(C) void k_field_combine(int r0, int zr, const FieldEntryDev* __restrict__ entries,
+                                                     int ne, const double* __restrict__ field, int per_node,
+                                                     const float* __restrict__ H1p, const float* __restrict__ Z,
+                                                     float* __restrict__ H1f, float* __restrict__ xaff) {
     const int i = r0 + static_cast<int>(blockIdx.x);
     const int k = threadIdx.x;
     const double* E = field + (per_node ? 3 * static_cast<std::size_t>(i) : 0);
     const std::size_t base = static_cast<std::size_t>(i) * NH * C;
     const float* z = Z + static_cast<std::size_t>(i) * zr * C;
-    for (int lm = 0; lm < NH; ++lm) {
-        float v = H1p[base + static_cast<std::size_t>(lm) * C + k];
-        for (int e = 0; e < ne; ++e) {
-            const FieldEntryDev en = entries[e];
-            if (en.lm_out != lm) continue;
-            v += (en.coef * static_cast<float>(E[en.comp])) * z[static_cast<std::size_t>(en.zrow) * C + k];
-        }
-        H1f[base + static_cast<std::size_t>(lm) * C + k] = v;
-        if (lm == 0) xaff[static_cast<std::size_t>(i) * C + k] = v;
+    float v[NH];
+#pragma unroll
+    for (int q = 0; q < NH; ++q) v[q] = H1p[base + static_cast<std::size_t>(q) * C + k];
+    for (int e = 0; e < ne; ++e) {
+        const FieldEntryDev en = entries[e];
+        const float add = (en.coef * static_cast<float>(E[en.comp])) * z[static_cast<std::size_t>(en.zrow) * C + k];
+        static_for<0, NH>([&](auto qc) {
+            if (en.lm_out == qc) v[qc] += add;
+        });
     }
+#pragma unroll
+    for (int q = 0; q < NH; ++q) H1f[base + static_cast<std::size_t>(q) * C + k] = v[q];
+    xaff[static_cast<std::size_t>(i) * C + k] = v[0];
 }
 
 // H1p_adj[i,0,:] += direct[i,:] (x = H1f[:,0,:], mace.cpp:1798-1804)
@@ -670,9 +677,10 @@ __global__ void k_field_direct_add(int r0, int NH, int C, const float* __restric
 
 // H1p_adj[i,lm] += sum over the entries from lm of E_comp (coef Y[i,yrow]) and
 // the node's dE/dE_c = sum of H1p[i,lm_in,k] coef Y[i,yrow,k] (FP32 products,
-// FP64 sums) into part[i][c]
-template <int C>
-__global__ __launch_bounds__(C) void k_field_reverse_combine(int r0, int NH, int yr,
+// FP64 sums) into part[i][c].  One pass over the entries in list order, the
+// NH rows of the lane's channel in registers.
+template <int C, int NH>
+__global__ __launch_bounds__(C) void k_field_reverse_combine(int r0, int yr,
                                                             const FieldEntryDev* __restrict__ entries, int ne,
                                                             const double* __restrict__ field, int per_node,
                                                             const float* __restrict__ H1p, const float* __restrict__ Y,
@@ -683,19 +691,29 @@ __global__ __launch_bounds__(C) void k_field_reverse_combine(int r0, int NH, int
     const double* E = field + (per_node ? 3 * static_cast<std::size_t>(i) : 0);
     const std::size_t base = static_cast<std::size_t>(i) * NH * C;
     const float* y = Y + static_cast<std::size_t>(i) * yr * C;
-    double acc[3] = {0.0, 0.0, 0.0};
-    for (int lm = 0; lm < NH; ++lm) {
-        float v = H1p_adj[base + static_cast<std::size_t>(lm) * C + k];
-        const float hp = H1p[base + static_cast<std::size_t>(lm) * C + k];
-        for (int e = 0; e < ne; ++e) {
-            const FieldEntryDev en = entries[e];
-            if (en.lm_in != lm) continue;
-            const float contribution = en.coef * y[static_cast<std::size_t>(en.yrow) * C + k];
-            v += static_cast<float>(E[en.comp]) * contribution;
-            acc[en.comp] += static_cast<double>(hp * contribution);
-        }
-        H1p_adj[base + static_cast<std::size_t>(lm) * C + k] = v;
+    float v[NH], hp[NH];
+#pragma unroll
+    for (int q = 0; q < NH; ++q) {
+        v[q] = H1p_adj[base + static_cast<std::size_t>(q) * C + k];
+        hp[q] = H1p[base + static_cast<std::size_t>(q) * C + k];
     }
+    double acc[3] = {0.0, 0.0, 0.0};
+    for (int e = 0; e < ne; ++e) {
+        const FieldEntryDev en = entries[e];
+        const float contribution = en.coef * y[static_cast<std::size_t>(en.yrow) * C + k];
+        const float ec = static_cast<float>(E[en.comp]);
+        static_for<0, NH>([&](auto qc) {
+            if (en.lm_in == qc) {
+                v[qc] += ec * contribution;
+                const double d = static_cast<double>(hp[qc] * contribution);
+                if (en.comp == 0) acc[0] += d;
+                else if (en.comp == 1) acc[1] += d;
+                else acc[2] += d;
+            }
+        });
+    }
+#pragma unroll
+    for (int q = 0; q < NH; ++q) H1p_adj[base + static_cast<std::size_t>(q) * C + k] = v[q];
 #pragma unroll
     for (int c = 0; c < 3; ++c) {
         const double t = block_sum<C>(acc[c], sbuf);
@@ -731,81 +749,114 @@ __global__ __launch_bounds__(256) void k_field_adj_sum(int N, const double* __re
 // ---------------------------------------------------------------------------
 // H1f_dot[i,lm] = sum over the entries of component seed into lm of coef Z[i,zrow];
 // x_dot = H1f_dot[i,0,:]
-__global__ void k_field_tangent(int NH, int C, int zr, const FieldEntryDev* __restrict__ entries, int ne, int seed,
-                                const float* __restrict__ Z, float* __restrict__ H1f_dot, float* __restrict__ x_dot) {
+template <int C, int NH>
+__global__ __launch_bounds__(C) void k_field_tangent(int zr, const FieldEntryDev* __restrict__ entries, int ne,
+                                                     int seed, const float* __restrict__ Z,
+                                                     float* __restrict__ H1f_dot, float* __restrict__ x_dot) {
     const int i = static_cast<int>(blockIdx.x);
     const int k = threadIdx.x;
     const float* z = Z + static_cast<std::size_t>(i) * zr * C;
-    for (int lm = 0; lm < NH; ++lm) {
-        float v = 0.0f;
-        for (int e = 0; e < ne; ++e) {
-            const FieldEntryDev en = entries[e];
-            if (en.lm_out == lm && en.comp == seed) v += en.coef * z[static_cast<std::size_t>(en.zrow) * C + k];
-        }
-        H1f_dot[(static_cast<std::size_t>(i) * NH + lm) * C + k] = v;
-        if (lm == 0) x_dot[static_cast<std::size_t>(i) * C + k] = v;
+    float v[NH];
+#pragma unroll
+    for (int q = 0; q < NH; ++q) v[q] = 0.0f;
+    for (int e = 0; e < ne; ++e) {
+        const FieldEntryDev en = entries[e];
+        if (en.comp != seed) continue;
+        const float add = en.coef * z[static_cast<std::size_t>(en.zrow) * C + k];
+        static_for<0, NH>([&](auto qc) {
+            if (en.lm_out == qc) v[qc] += add;
+        });
     }
+#pragma unroll
+    for (int q = 0; q < NH; ++q) H1f_dot[(static_cast<std::size_t>(i) * NH + q) * C + k] = v[q];
+    x_dot[static_cast<std::size_t>(i) * C + k] = v[0];
 }
 
 // M1's tangent along A1_dot: M1_dot = sum_v g_v A1_dot_v, the gradient g and
 // its derivative gd along A1_dot (each factor of a term differentiated in
-// turn), from the monomial list in HBM.  Lanes are channels; a workgroup
-// holds kTangentLanes of them (blockIdx.y picks the channel block).
+// turn).  Lanes are channels.  With a compiled term table (M1TAB) the terms
+// are straight-line code on register-resident variables, one workgroup of C
+// lanes per node; else the monomial list is read from HBM with the
+// variables in LDS, kTangentLanes channels per workgroup (blockIdx.y picks
+// the channel block).
 constexpr int kTangentLanes = 128;
-template <int C, int NY>
-__global__ __launch_bounds__(C < kTangentLanes ? C : kTangentLanes) void k_m1_tangent(
+template <int C, class M1TAB>
+constexpr int m1_tangent_lanes() {
+    return std::is_same_v<M1TAB, void> ? (C < kTangentLanes ? C : kTangentLanes) : C;
+}
+
+template <int C, int NY, class M1TAB>
+__global__ __launch_bounds__((m1_tangent_lanes<C, M1TAB>())) void k_m1_tangent(
     const int* __restrict__ types, const float* __restrict__ A1, const float* __restrict__ A1_dot,
     const std::int32_t* __restrict__ terms, int T1, const float* __restrict__ m1_coef, float* __restrict__ M1_dot,
     float* __restrict__ g, float* __restrict__ gd) {
-    constexpr int L = C < kTangentLanes ? C : kTangentLanes;
+    constexpr int L = m1_tangent_lanes<C, M1TAB>();
     static_assert(C % L == 0, "whole channel blocks");
-    __shared__ float xs[NY * L], dxs[NY * L], gs[NY * L], gds[NY * L];
     const int i = static_cast<int>(blockIdx.x);
     const int j = threadIdx.x;
     const int k = static_cast<int>(blockIdx.y) * L + j;
     const std::size_t row = static_cast<std::size_t>(i) * NY * C + k;
-#pragma unroll
-    for (int v = 0; v < NY; ++v) {
-        xs[v * L + j] = A1[row + v * C];
-        dxs[v * L + j] = A1_dot[row + v * C];
-        gs[v * L + j] = 0.0f;
-        gds[v * L + j] = 0.0f;
-    }
     const float* cf = m1_coef + static_cast<std::size_t>(types[i]) * T1 * C + k;
-    float fd = 0.0f;
-    for (int t = 0; t < T1; ++t) {
-        const int pk = terms[t];
-        const float c = cf[static_cast<std::size_t>(t) * C];
-        const int deg = pk >> 24;
-        const int v0 = pk & 0xff, v1 = (pk >> 8) & 0xff, v2 = (pk >> 16) & 0xff;
-        const float x0 = xs[v0 * L + j], d0 = dxs[v0 * L + j];
-        if (deg == 1) {
-            gs[v0 * L + j] += c;
-            fd += c * d0;
-        } else if (deg == 2) {
-            const float x1 = xs[v1 * L + j], d1 = dxs[v1 * L + j];
-            gs[v0 * L + j] += c * x1;
-            gs[v1 * L + j] += c * x0;
-            gds[v0 * L + j] += c * d1;
-            gds[v1 * L + j] += c * d0;
-            fd += c * (x1 * d0 + x0 * d1);
-        } else {
-            const float x1 = xs[v1 * L + j], d1 = dxs[v1 * L + j];
-            const float x2 = xs[v2 * L + j], d2 = dxs[v2 * L + j];
-            gs[v0 * L + j] += c * x1 * x2;
-            gs[v1 * L + j] += c * x0 * x2;
-            gs[v2 * L + j] += c * x0 * x1;
-            gds[v0 * L + j] += c * (d1 * x2 + x1 * d2);
-            gds[v1 * L + j] += c * (d0 * x2 + x0 * d2);
-            gds[v2 * L + j] += c * (d0 * x1 + x0 * d1);
-            fd += c * (x1 * x2 * d0 + x0 * x2 * d1 + x0 * x1 * d2);
-        }
-    }
-    M1_dot[static_cast<std::size_t>(i) * C + k] = fd;
+    if constexpr (!std::is_same_v<M1TAB, void>) {
+        float x[NY], dx[NY], gv[NY], gdv[NY];
 #pragma unroll
-    for (int v = 0; v < NY; ++v) {
-        g[row + v * C] = gs[v * L + j];
-        gd[row + v * C] = gds[v * L + j];
+        for (int v = 0; v < NY; ++v) {
+            x[v] = A1[row + v * C];
+            dx[v] = A1_dot[row + v * C];
+            gv[v] = 0.0f;
+            gdv[v] = 0.0f;
+        }
+        M1_dot[static_cast<std::size_t>(i) * C + k] = poly_tangent_ct<M1TAB, 0, M1TAB::NT, C>(x, dx, cf, gv, gdv);
+#pragma unroll
+        for (int v = 0; v < NY; ++v) {
+            g[row + v * C] = gv[v];
+            gd[row + v * C] = gdv[v];
+        }
+        return;
+    } else {
+        __shared__ float xs[NY * L], dxs[NY * L], gs[NY * L], gds[NY * L];
+#pragma unroll
+        for (int v = 0; v < NY; ++v) {
+            xs[v * L + j] = A1[row + v * C];
+            dxs[v * L + j] = A1_dot[row + v * C];
+            gs[v * L + j] = 0.0f;
+            gds[v * L + j] = 0.0f;
+        }
+        float fd = 0.0f;
+        for (int t = 0; t < T1; ++t) {
+            const int pk = terms[t];
+            const float c = cf[static_cast<std::size_t>(t) * C];
+            const int deg = pk >> 24;
+            const int v0 = pk & 0xff, v1 = (pk >> 8) & 0xff, v2 = (pk >> 16) & 0xff;
+            const float x0 = xs[v0 * L + j], d0 = dxs[v0 * L + j];
+            if (deg == 1) {
+                gs[v0 * L + j] += c;
+                fd += c * d0;
+            } else if (deg == 2) {
+                const float x1 = xs[v1 * L + j], d1 = dxs[v1 * L + j];
+                gs[v0 * L + j] += c * x1;
+                gs[v1 * L + j] += c * x0;
+                gds[v0 * L + j] += c * d1;
+                gds[v1 * L + j] += c * d0;
+                fd += c * (x1 * d0 + x0 * d1);
+            } else {
+                const float x1 = xs[v1 * L + j], d1 = dxs[v1 * L + j];
+                const float x2 = xs[v2 * L + j], d2 = dxs[v2 * L + j];
+                gs[v0 * L + j] += c * x1 * x2;
+                gs[v1 * L + j] += c * x0 * x2;
+                gs[v2 * L + j] += c * x0 * x1;
+                gds[v0 * L + j] += c * (d1 * x2 + x1 * d2);
+                gds[v1 * L + j] += c * (d0 * x2 + x0 * d2);
+                gds[v2 * L + j] += c * (d0 * x1 + x0 * d1);
+                fd += c * (x1 * x2 * d0 + x0 * x2 * d1 + x0 * x1 * d2);
+            }
+        }
+        M1_dot[static_cast<std::size_t>(i) * C + k] = fd;
+#pragma unroll
+        for (int v = 0; v < NY; ++v) {
+            g[row + v * C] = gs[v * L + j];
+            gd[row + v * C] = gds[v * L + j];
+        }
     }
 }
 
@@ -1302,8 +1353,8 @@ struct KernelSetImpl final : KernelSet {
         TimerScope ts(tm, "h1_field", s);
         const std::size_t row0 = static_cast<std::size_t>(t.r0) * S::NH * C;
         launch_node_gemm(t.fz, m.field_W, w.H1p + row0, w.fzy + static_cast<std::size_t>(t.r0) * m.field_zr * C, s);
-        k_field_combine<<<t.nr, C, 0, s>>>(t.r0, S::NH, C, m.field_zr, m.field_entries, m.num_field_entries, w.efield,
-                                           w.efield_per_node, w.H1p, w.fzy, w.H1f, w.xaff);
+        k_field_combine<C, S::NH><<<t.nr, C, 0, s>>>(t.r0, m.field_zr, m.field_entries, m.num_field_entries,
+                                                     w.efield, w.efield_per_node, w.H1p, w.fzy, w.H1f, w.xaff);
         SMX_LAUNCH_CHECK("field_combine");
         launch_node_gemm(t.h1, m.U_w, w.H1f + row0, w.H1 + row0, s);
     }
@@ -1330,9 +1381,9 @@ struct KernelSetImpl final : KernelSet {
         }
         launch_node_gemm(t.fy, m.field_Wt, w.H1p_adj + row0, w.fzy + static_cast<std::size_t>(t.r0) * m.field_yr * C,
                          s);
-        k_field_reverse_combine<C><<<t.nr, C, 0, s>>>(t.r0, S::NH, m.field_yr, m.field_entries, m.num_field_entries,
-                                                      w.efield, w.efield_per_node, w.H1p, w.fzy, w.H1p_adj,
-                                                      w.field_part);
+        k_field_reverse_combine<C, S::NH><<<t.nr, C, 0, s>>>(t.r0, m.field_yr, m.field_entries, m.num_field_entries,
+                                                             w.efield, w.efield_per_node, w.H1p, w.fzy, w.H1p_adj,
+                                                             w.field_part);
         SMX_LAUNCH_CHECK("field_reverse_combine");
         if (!w.efield_per_node) {
             k_field_adj_sum<<<1, 256, 0, s>>>(t.r0 + t.nr, w.field_part, w.field_adj);
@@ -1531,8 +1582,8 @@ struct KernelSetImpl final : KernelSet {
             double* f = rw.forces + static_cast<std::size_t>(seed) * 3 * t.ne;
             TimerScope ts(tm, "field_response", s);
             // H1f_dot (and x_dot), H1_dot = H1f_dot U
-            k_field_tangent<<<N, C, 0, s>>>(S::NH, C, m.field_zr, m.field_entries, m.num_field_entries, seed, rw.Z,
-                                            rw.H1f_dot, rw.x_dot);
+            k_field_tangent<C, S::NH><<<N, C, 0, s>>>(m.field_zr, m.field_entries, m.num_field_entries, seed, rw.Z,
+                                                      rw.H1f_dot, rw.x_dot);
             SMX_LAUNCH_CHECK("field_tangent");
             launch_node_gemm(t.h1, m.U_w, rw.H1f_dot, rw.H1_dot, s);
             // Phi1_dot: the R1 forward of H1_dot; A1_dot (density-scaled like A1)
@@ -1548,9 +1599,9 @@ struct KernelSetImpl final : KernelSet {
             launch_node_gemm(t.a1f, m.A1_w, rw.Phi1_dot, rw.A1_dot, s);
             if (m.A1_scaled) launch_density_scale(N, S::NY * C, w.dens_s1, false, rw.A1_dot, s);
             // M1_dot, the M1 gradient and its tangent; the readout's tangent
-            constexpr int TL = C < kTangentLanes ? C : kTangentLanes;
-            k_m1_tangent<C, S::NY><<<dim3(N, C / TL), TL, 0, s>>>(g.node_types, w.A1, rw.A1_dot, m.m1_terms, m.T1,
-                                                                  m.m1_coef, rw.M1_dot, rw.g, rw.gd);
+            constexpr int TL = m1_tangent_lanes<C, M1TAB>();
+            k_m1_tangent<C, S::NY, M1TAB><<<dim3(N, C / TL), TL, 0, s>>>(
+                g.node_types, w.A1, rw.A1_dot, m.m1_terms, m.T1, m.m1_coef, rw.M1_dot, rw.g, rw.gd);
             SMX_LAUNCH_CHECK("m1_tangent");
             k_readout_tangent<C><<<N, C, 0, s>>>(g.node_types, S::NY, w.M1, rw.M1_dot, w.xaff, rw.x_dot, m.H2_T,
                                                  m.H2_Tt, m.H2_M1, m.H2_M1t, m.W1r, m.W2r, m.hidden,
@@ -1566,7 +1617,8 @@ struct KernelSetImpl final : KernelSet {
             launch_node_gemm(t.a1r, m.A1_wt, rw.A1_adj_dot, rw.dPhi1_dot, s);
             // the R1 reverse, bilinear in (H1, dPhi1): (H1, dPhi1_dot) gives
             // the source terms of H1_adj_dot and part of the forces,
-            // (H1_dot, dPhi1) the rest of the forces (its source terms unused)
+            // (H1_dot, dPhi1) the rest of the forces (its source terms are
+            // not formed)
             static_for<0, kGroups>([&](auto gc) {
                 constexpr int gi = gc;
                 k_r1_reverse<C, LMAX, LMAXH, Groups::masks[gi], (gi > 0), StagedRecords><<<N, C, 0, s>>>(
@@ -1579,8 +1631,8 @@ struct KernelSetImpl final : KernelSet {
             if (forces) {
                 static_for<0, kGroups>([&](auto gc) {
                     constexpr int gi = gc;
-                    k_r1_reverse<C, LMAX, LMAXH, Groups::masks[gi], true, StagedRecords><<<N, C, 0, s>>>(
-                        0, 0, g.offsets, g.neigh, records<StagedRecords>(m, t, w), rw.H1_dot, m.cg, w.dPhi1, w.Wsrc,
+                    k_r1_reverse<C, LMAX, LMAXH, Groups::masks[gi], true, StagedRecords, C, false><<<N, C, 0, s>>>(
+                        0, 0, g.offsets, g.neigh, records<StagedRecords>(m, t, w), rw.H1_dot, m.cg, w.dPhi1, nullptr,
                         f);
                     SMX_LAUNCH_CHECK("r1_reverse");
                 });
@@ -1596,14 +1648,14 @@ struct KernelSetImpl final : KernelSet {
             k_field_direct_add<<<N, C, 0, s>>>(0, S::NH, C, rw.direct_dot, rw.H1p_adj_dot);
             SMX_LAUNCH_CHECK("field_direct_add");
             launch_node_gemm(t.fy, m.field_Wt, rw.H1p_adj_dot, rw.Y_dot, s);
-            k_field_reverse_combine<C><<<N, C, 0, s>>>(0, S::NH, m.field_yr, m.field_entries, m.num_field_entries,
-                                                       w.efield, 0, w.H1p, rw.Y_dot, rw.H1p_adj_dot, rw.part);
+            k_field_reverse_combine<C, S::NH><<<N, C, 0, s>>>(0, m.field_yr, m.field_entries, m.num_field_entries,
+                                                              w.efield, 0, w.H1p, rw.Y_dot, rw.H1p_adj_dot, rw.part);
             SMX_LAUNCH_CHECK("field_reverse_combine");
             k_field_adj_sum<<<1, 256, 0, s>>>(N, rw.part, rw.hessian_t + 3 * seed);
             SMX_LAUNCH_CHECK("field_adj_sum");
-            k_field_reverse_combine<C><<<N, C, 0, s>>>(0, S::NH, m.field_yr, m.field_entries, m.num_field_entries,
-                                                       rw.unit + 3 * seed, 0, w.H1p, rw.Y, rw.H1p_adj_dot,
-                                                       rw.part_scratch);
+            k_field_reverse_combine<C, S::NH><<<N, C, 0, s>>>(0, m.field_yr, m.field_entries, m.num_field_entries,
+                                                              rw.unit + 3 * seed, 0, w.H1p, rw.Y, rw.H1p_adj_dot,
+                                                              rw.part_scratch);
             SMX_LAUNCH_CHECK("field_reverse_combine");
             if (!forces) return;
             // the layer-1 reverse of H1p_adj_dot (M0 and A0 do not depend on
