@@ -544,8 +544,10 @@ inline unsigned r1_forward_blocks(int nr) {
 // rows are indexed by li.  H1 and Phi1 rows hold CF channels (CF <= C: the
 // lanes k >= CF of a caller's unpadded arrays neither read nor write).
 // ---------------------------------------------------------------------------
+// At least four waves per SIMD: the single-pass shapes need 145 VGPRs for
+// three, and at four (128 VGPRs, two spilled) the medium call is 0.7% faster.
 template <int C, int LMAX, int LMAXH, unsigned MASK, bool ACCUMULATE, class EDGES, int CF = C>
-__global__ __launch_bounds__(C) void k_r1_forward(int r0, int nr, const int* __restrict__ first,
+__global__ __launch_bounds__(C) __attribute__((amdgpu_waves_per_eu(4))) void k_r1_forward(int r0, int nr, const int* __restrict__ first,
                                                   const int* __restrict__ count, const int* __restrict__ neigh,
                                                   EDGES edges, const float* __restrict__ H1,
                                                   const float* __restrict__ cg, float* __restrict__ Phi1) {

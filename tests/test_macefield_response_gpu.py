@@ -81,6 +81,64 @@ def test_response_matches_oracle(request, model):
     np.testing.assert_array_equal(ev.electric_field_bec_bins, bins)
 
 
+def _bench_system():
+    from symmetrix import systems
+    return systems.srtio3_supercell(10, sigma=0.05, seed=0)
+
+
+def _device_response(ev, s, field):
+    lut = {int(z): i for i, z in enumerate(ev.atomic_numbers)}
+    types = np.array([lut[int(z)] for z in s["numbers"]], np.int32)
+    g = _prepare(ev, s, types)
+    ev._compute_prepared_factorized_positions_field(g["generation"], s["positions"], field)
+    ev._compute_prepared_factorized_field_response(g["generation"], field, True, scatter_bec_bins=True)
+    return np.asarray(ev.electric_field_hessian).reshape(3, 3), ev.electric_field_bec_bins
+
+
+def test_response_at_the_benchmark_size(field_l2_model_path, tmp_path):
+    """The 5,000-atom SrTiO3 system of the benchmark (272,436 edges):
+    against the oracle on a 4x4x4 cell of the same crystal, and at full size
+    the properties the mathematics fixes: a symmetric Hessian, Born charges
+    summing to zero, and rotating atoms and field together rotating both
+    (the model's residual kept to its scalar block, as a trained one is)."""
+    import json
+    from oracle import oracle
+    from symmetrix import systems
+    from symmetrix.mace_kokkos import MACEKokkosFloat
+    with open(field_l2_model_path) as f:
+        doc = json.load(f)
+    LM, C = (doc["L_max"] + 1) ** 2, doc["num_channels"]
+    b = np.asarray(doc["H1_first_residual_weights"], float).reshape(-1, LM, C)
+    b[:, 1:, :] = 0.0
+    doc["H1_first_residual_weights"] = b.ravel().tolist()
+    path = str(tmp_path / "scalar_residual.json")
+    with open(path, "w") as f:
+        json.dump(doc, f)
+    ev = MACEKokkosFloat(path)
+    mid = systems.srtio3_supercell(4, sigma=0.05, seed=0)
+    ref = oracle.field_response_system(oracle.OracleModel(path, fp64=True), mid, FIELD)
+    hess, bins = _device_response(ev, mid, FIELD)
+    _close("hessian 320 atoms", hess, ref["hessian"])
+    _close("bec 320 atoms", bins, ref["bec"])
+    s = _bench_system()
+    hess, bins = _device_response(ev, s, FIELD)
+    hs, zs = np.max(np.abs(hess)), np.max(np.abs(bins))
+    print("5000 atoms: hessian scale %.3e, asymmetry %.3e; bec scale %.3e, sum %.3e" % (
+        hs, np.max(np.abs(hess - hess.T)), zs, np.max(np.abs(bins.sum(axis=0)))))
+    assert np.max(np.abs(hess - hess.T)) < TOL * hs
+    assert np.max(np.abs(bins.sum(axis=0))) < 1e-9 * len(bins) * zs
+    R = e3_rotation()
+    rot = dict(s, positions=s["positions"] @ R.T, cell=s["cell"] @ R.T)
+    hess_r, bins_r = _device_response(ev, rot, R @ FIELD)
+    _close("rotated hessian", hess_r, R @ hess @ R.T)
+    _close("rotated bec", bins_r, np.einsum("ab,ibc,dc->iad", R, bins, R))
+
+
+def e3_rotation():
+    from symmetrix import e3
+    return e3.random_rotation(np.random.default_rng(21))
+
+
 def test_host_graph_response(tiny_field_scaled_model_path):
     """compute_electric_field_hessian / _force_derivative: the host graph
     evaluated in the field, then its response."""
