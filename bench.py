@@ -468,16 +468,14 @@ def run_config(hip, model_path, system, skin, warmup, steps, timed_steps=False):
             med.append(time.perf_counter() - t0)
         out["protocol"] = {"warmup": 3, "calls": 10, "median_us_per_atom": round(
             statistics.median(med) * 1e6 / n_atoms, 4), "positions": "device-resident"}
-        # PCIe-inclusive call: positions from host memory, results copied back
+        # PCIe-inclusive call: positions from host memory, node energies,
+        # atom forces and stress copied back (the one-call form)
         for _ in range(3):
-            ev._compute_prepared_factorized_positions(gen, system["positions"])
+            ev._compute_prepared_factorized_positions_results(gen, system["positions"], vol)
         host = []
         for _ in range(10):
             t0 = time.perf_counter()
-            ev._compute_prepared_factorized_positions(gen, system["positions"])
-            e = ev.node_energies
-            ev._reduce_atom_forces(n_atoms, None, None, gen)
-            ev._reduce_stress(vol, None, gen)
+            e, _, _ = ev._compute_prepared_factorized_positions_results(gen, system["positions"], vol)
             host.append(time.perf_counter() - t0)
         out["host_us_per_atom"] = statistics.median(host) * 1e6 / n_atoms
         out["energy"] = float(np.sum(e))

@@ -235,6 +235,18 @@ SMX_API int32_t smx_compute_prepared_factorized_positions(SmxEvaluator* ev, uint
  * are ready for work ordered on that stream or after smx_synchronize. */
 SMX_API int32_t smx_compute_prepared_factorized_positions_device(SmxEvaluator* ev, uint64_t generation,
                                                                  const double* positions_device);
+/* The calculator's call in one.  No counterpart in the reference, whose
+ * calculator makes these calls in turn (calculator.py:3821-3894:
+ * _compute_prepared_factorized_positions, node_energies,
+ * _reduce_atom_forces, _reduce_stress): host positions (3 * num_nodes) in,
+ * node energies (num_nodes), atom forces (3 * num_feature_nodes) and, with
+ * stress != NULL, the 3x3 stress of a cell of that volume out, through
+ * pinned staging and one wait for the device.  The refusals are those of
+ * smx_compute_prepared_factorized_positions and smx_reduce_prepared_stress. */
+SMX_API int32_t smx_compute_prepared_factorized_positions_results(SmxEvaluator* ev, uint64_t generation,
+                                                                  const double* positions, double volume,
+                                                                  double* node_energies, double* forces,
+                                                                  double* stress);
 /* Graphs with ghost feature nodes: one GPU's share of a domain-decomposed
  * system (the LAMMPS multi-rank path, pair_symmetrix_mace_kokkos.cpp:
  * 1285-1704).  prepare_factorized_graph with feature nodes

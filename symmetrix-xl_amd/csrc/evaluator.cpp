@@ -383,6 +383,22 @@ struct Evaluator {
         if (geometry_ready) (void)hipEventDestroy(geometry_ready);
         if (caller_ready) (void)hipEventDestroy(caller_ready);
         if (h_invalid) (void)hipHostFree(h_invalid);
+        if (h_stage) (void)hipHostFree(h_stage);
+    }
+
+    // pinned host staging of the one-call results path: positions in,
+    // energies, forces and stress out (grown on demand, freed at the end)
+    double* h_stage = nullptr;
+    std::size_t h_stage_count = 0;
+    double* host_stage(std::size_t count) {
+        if (count > h_stage_count) {
+            if (h_stage) SMX_HIP(hipHostFree(h_stage));
+            h_stage = nullptr;
+            h_stage_count = 0;
+            SMX_HIP(hipHostMalloc(reinterpret_cast<void**>(&h_stage), count * sizeof(double), hipHostMallocDefault));
+            h_stage_count = count;
+        }
+        return h_stage;
     }
 
     template <class T>
@@ -1935,6 +1951,62 @@ struct Evaluator {
         finish_call(!on_device);
     }
 
+    // The calculator's call in one (calculator.py:3821-3894 makes these in
+    // turn): host positions through pinned memory, the evaluation, the atom
+    // forces and (stress non-null) the stress, and every result copied back
+    // through pinned memory behind one wait for the device
+    void compute_results(std::uint64_t token, const double* positions, double volume, double* energies,
+                         double* forces, double* stress) {
+        check_generation(token);
+        require_plain_call();
+        if (geom == Geometry::none)
+            throw std::invalid_argument("Execution R1 positions require current graph and geometry tokens: "
+                                        "prepare a geometry (prepare_factorized_geometry or its fractional or "
+                                        "shift form) or use compute_prepared_factorized with xyz and r");
+        if (N > 0 && (!positions || !energies || !forces)) throw std::invalid_argument("a result buffer is NULL");
+        if (stress && (!(volume > 0.0) || !std::isfinite(volume))) throw std::invalid_argument("volume must be positive");
+        for (int i = 0; i < 3 * N; ++i)
+            if (!std::isfinite(positions[i])) throw std::invalid_argument("positions must be finite");
+        const std::size_t n = N, f = F;
+        double* st = host_stage(3 * n + n + 3 * f + 9);
+        double* d_pos = d_positions.as<double>();
+        if (N > 0) {
+            std::memcpy(st, positions, 3 * n * sizeof(double));
+            SMX_HIP(hipMemcpyAsync(d_pos, st, 3 * n * sizeof(double), hipMemcpyHostToDevice, stream));
+        }
+        fpos_mode = false;
+        xyz_host = false;
+        if (timer) timer->begin("displacements", stream);
+        const bool frac_ref = geom == Geometry::device_fractional || geom == Geometry::fractional;
+        launch_displacements(N, cell, inv_cell, pbc, frac_ref,
+                             geom == Geometry::device_fractional ? d_wfrac.as<double>() : d_ref_positions.as<double>(),
+                             d_pos, d_disp.as<double>(), d_invalid.as<int>(), stream);
+        if (timer) timer->end("displacements", stream);
+        evaluate(d_pos);
+        if (!tiled)
+            launch_atom_forces(N, F, d_offsets.as<int>(), d_soff.as<int>(), d_sedges.as<int>(),
+                               h_feature_of.empty() ? nullptr : d_feature_of.as<int>(), ws.node_forces,
+                               d_atom_forces.as<double>(), stream);
+        if (stress) {
+            if (!tiled)
+                launch_stress(E, ws.node_forces, d_xyz.as<double>(), volume, d_stress_partial.as<double>(),
+                              stress_blocks, d_stress.as<double>(), stream);
+            else
+                launch_scale9(d_virial.as<double>(), -1.0 / volume, d_stress.as<double>(), stream);
+        }
+        double* se = st + 3 * n;
+        double* sf = se + n;
+        double* ss = sf + 3 * f;
+        if (N > 0) SMX_HIP(hipMemcpyAsync(se, ws.node_energies, n * sizeof(double), hipMemcpyDeviceToHost, stream));
+        if (F > 0)
+            SMX_HIP(hipMemcpyAsync(sf, d_atom_forces.as<double>(), 3 * f * sizeof(double), hipMemcpyDeviceToHost, stream));
+        if (stress) SMX_HIP(hipMemcpyAsync(ss, d_stress.as<double>(), 9 * sizeof(double), hipMemcpyDeviceToHost, stream));
+        finish_call(true);
+        std::memcpy(energies, se, n * sizeof(double));
+        std::memcpy(forces, sf, 3 * f * sizeof(double));
+        if (stress) std::memcpy(stress, ss, 9 * sizeof(double));
+    }
+
     void compute_xyz(std::uint64_t token, const double* xyz, const double* r) {
         check_generation(token);
         require_plain_call();
@@ -2690,6 +2762,16 @@ int32_t smx_compute_prepared_factorized_positions(SmxEvaluator* ev, uint64_t gen
         auto& e = E(ev);
         if (e.N > 0 && !positions) throw std::invalid_argument("positions are required");
         timed(e.last_evaluation_ms, e.evaluation_count, [&] { e.compute_positions(generation, positions, false); });
+    });
+}
+
+int32_t smx_compute_prepared_factorized_positions_results(SmxEvaluator* ev, uint64_t generation,
+                                                          const double* positions, double volume,
+                                                          double* node_energies, double* forces, double* stress) {
+    return guarded([&] {
+        auto& e = E(ev);
+        timed(e.last_evaluation_ms, e.evaluation_count,
+              [&] { e.compute_results(generation, positions, volume, node_energies, forces, stress); });
     });
 }
 

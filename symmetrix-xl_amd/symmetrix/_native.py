@@ -121,6 +121,7 @@ SIGNATURES = [
     ("smx_compute_prepared_factorized", _i32, [_vp, _u64, _vp, _vp]),
     ("smx_compute_prepared_factorized_positions", _i32, [_vp, _u64, _vp]),
     ("smx_compute_prepared_factorized_positions_field", _i32, [_vp, _u64, _vp, _vp, _i64]),
+    ("smx_compute_prepared_factorized_positions_results", _i32, [_vp, _u64, _vp, _dbl, _vp, _vp, _vp]),
     ("smx_compute_prepared_factorized_field", _i32, [_vp, _u64, _vp, _vp, _vp, _i64]),
     ("smx_set_electric_field", _i32, [_vp, _vp, _i64]),
     ("smx_electric_field_adj", _i32, [_vp, _vp, _i64, _p_i64]),

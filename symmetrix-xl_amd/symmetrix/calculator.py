@@ -116,13 +116,26 @@ def use_device_neighbor_graph(request, eligible, num_atoms):
     return num_atoms >= AUTOMATIC_DEVICE_NEIGHBOR_MIN_ATOMS
 
 
-def minimum_image(displacements, cell, pbc):
+def minimum_image(displacements, cell, pbc, inverse_cell=None):
     """Displacements wrapped to the minimum image along the periodic axes."""
     if not np.any(pbc):
         return displacements
-    f = np.linalg.solve(cell.T, displacements.T).T
-    f[:, pbc] -= np.rint(f[:, pbc])
+    if inverse_cell is None:
+        f = np.linalg.solve(cell.T, displacements.T).T
+    else:
+        f = displacements @ inverse_cell
+    if np.all(pbc):
+        f -= np.rint(f)
+    else:
+        f[:, pbc] -= np.rint(f[:, pbc])
     return f @ cell
+
+
+def _max_norm(vectors):
+    """Largest row norm of an (N, 3) array (0 for none)."""
+    if len(vectors) == 0:
+        return 0.0
+    return float(np.sqrt(np.max(np.einsum("ij,ij->i", vectors, vectors))))
 
 
 @dataclass
@@ -254,20 +267,22 @@ class Symmetrix(_Base):
         cell_changed = not np.array_equal(cell, c.cell)
         if np.all(pbc):
             try:
+                inverse = np.linalg.inv(cell)
                 non_affine = positions - c.topology_fractional @ cell
-                non_affine = minimum_image(non_affine, cell, pbc)
-                deformation = np.linalg.solve(cell, c.topology_cell)
+                non_affine = minimum_image(non_affine, cell, pbc, inverse)
+                # the topology's own cell: no deformation
+                contraction = 1.0 if np.array_equal(cell, c.topology_cell) else float(
+                    np.linalg.norm(np.linalg.solve(cell, c.topology_cell), ord=2))
             except np.linalg.LinAlgError:
                 return None
-            max_non_affine = float(np.max(np.linalg.norm(non_affine, axis=1), initial=0.0))
-            contraction = float(np.linalg.norm(deformation, ord=2))
+            max_non_affine = _max_norm(non_affine)
             if contraction * (self.cutoff + 2.0 * max_non_affine) > self.cutoff + self.neighbor_skin:
                 return None
             return "cell" if cell_changed else "reuse"
         if cell_changed:
             return None
         disp = minimum_image(positions - c.topology_positions, cell, pbc)
-        if float(np.max(np.linalg.norm(disp, axis=1), initial=0.0)) > 0.5 * self.neighbor_skin:
+        if _max_norm(disp) > 0.5 * self.neighbor_skin:
             return None
         return "reuse"
 
@@ -346,19 +361,21 @@ class Symmetrix(_Base):
         field = self._resolve_electric_field(atoms) if getattr(self.evaluator, "has_field_coupling", False) else None
         cache = self._graph(numbers, positions, cell, pbc)
         ev = self.evaluator
-        if field is None:
-            ev._compute_prepared_factorized_positions(cache.generation, positions.reshape(-1))
-        else:
-            ev._compute_prepared_factorized_positions_field(cache.generation, positions.reshape(-1), field)
-        node_energies = np.array(ev.node_energies, dtype=np.float64, copy=True)
-        energy = float(np.sum(node_energies, dtype=np.float64))
-        self.results = {"energy": energy, "free_energy": energy, "energies": node_energies}
-        self.results["forces"] = np.asarray(ev._reduce_atom_forces(len(numbers), None, None, cache.generation))
+        volume = None
         if "stress" in properties:
             volume = abs(float(np.linalg.det(cell)))
             if not volume > 0.0:
                 raise ValueError("stress needs a cell of non-zero volume")
-            sigma = ev._reduce_stress(volume, None, cache.generation)
+        if field is not None:
+            ev._set_electric_field(field)
+        # the reference's sequence (positions call, node energies, atom
+        # forces, stress; calculator.py:3821-3894) in one device round trip
+        node_energies, forces, sigma = ev._compute_prepared_factorized_positions_results(
+            cache.generation, positions.reshape(-1), volume)
+        energy = float(np.sum(node_energies, dtype=np.float64))
+        self.results = {"energy": energy, "free_energy": energy, "energies": node_energies}
+        self.results["forces"] = forces
+        if sigma is not None:
             self.results["stress"] = full_3x3_to_voigt_6_stress(sigma)
         if field is not None:
             # calculator.py:3672-3678: P = -dE/dE / V

@@ -408,6 +408,22 @@ class MACEKokkosFloat:
         check(lib.smx_compute_prepared_factorized_positions(self._h, int(execution_graph_generation),
                                                             ptr(positions)))
 
+    def _compute_prepared_factorized_positions_results(self, execution_graph_generation, positions, volume=None):
+        """The calculator's call in one: host positions in; node energies,
+        atom forces and (volume given) the 3x3 stress out, behind one wait
+        for the device (the reference's calculator makes these calls in
+        turn, calculator.py:3821-3894)."""
+        positions = f64(positions)
+        if positions.size != 3 * self._num_nodes:
+            raise ValueError("positions do not match the prepared graph")
+        energies = np.zeros(self._num_nodes)
+        forces = np.zeros((self._num_feature_nodes, 3))
+        stress = None if volume is None else np.zeros((3, 3))
+        check(lib.smx_compute_prepared_factorized_positions_results(
+            self._h, int(execution_graph_generation), ptr(positions), 0.0 if volume is None else float(volume),
+            ptr(energies), ptr(forces), None if stress is None else ptr(stress)))
+        return energies, forces, stress
+
     # -------------------------------------------------------- MACEField
     @property
     def has_field_coupling(self):

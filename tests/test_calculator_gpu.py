@@ -271,3 +271,45 @@ def test_geometry_errors_and_counters(tiny_model_path):
     with pytest.raises(ValueError):
         ev._set_execution_plan_request("materialized", "speed", "")
     ev.prepare_active_types([0, 1, 2])
+
+
+@pytest.mark.parametrize("plan", ["direct", "tiled"])
+def test_results_call_equals_the_calls_in_turn(tiny_model_path, plan):
+    """smx_compute_prepared_factorized_positions_results, the calculator's
+    one-call path: bit-identical to the positions call followed by
+    node_energies, _reduce_atom_forces and _reduce_stress, under the direct
+    and the tiled plan; without a volume no stress; non-finite positions and
+    a non-positive volume raise."""
+    from symmetrix.mace_kokkos import MACEKokkosFloat
+    s = _system()
+    ev = MACEKokkosFloat(tiny_model_path)
+    if plan == "tiled":
+        ev.set_execution_plan_request("capacity", 16)
+    lut = {int(z): i for i, z in enumerate(ev.atomic_numbers)}
+    types = np.array([lut[int(z)] for z in s["numbers"]], np.int32)
+    cell = np.asarray(s["cell"], float)
+    g = ev._prepare_periodic_factorized_graph(types, s["positions"], cell, np.linalg.inv(cell), ev.r_cut + 0.5)
+    gen = g["generation"]
+    V = abs(np.linalg.det(cell))
+    pos = s["positions"] + 0.01 * np.random.default_rng(5).normal(size=s["positions"].shape)
+    ev._compute_prepared_factorized_positions(gen, pos)
+    e_ref = np.array(ev.node_energies)
+    f_ref = ev._reduce_atom_forces(len(types), None, None, gen)
+    s_ref = ev._reduce_stress(V, None, gen)
+    e, f, st = ev._compute_prepared_factorized_positions_results(gen, pos, V)
+    np.testing.assert_array_equal(e, e_ref)
+    np.testing.assert_array_equal(f, f_ref)
+    np.testing.assert_array_equal(st, s_ref)
+    e2, f2, st2 = ev._compute_prepared_factorized_positions_results(gen, pos)
+    assert st2 is None
+    np.testing.assert_array_equal(e2, e_ref)
+    np.testing.assert_array_equal(f2, f_ref)
+    bad = pos.copy()
+    bad[1, 0] = np.nan
+    with pytest.raises(ValueError, match="finite"):
+        ev._compute_prepared_factorized_positions_results(gen, bad, V)
+    with pytest.raises(ValueError, match="volume"):
+        ev._compute_prepared_factorized_positions_results(gen, pos, -1.0)
+    # the evaluator still evaluates afterwards
+    e3, f3, _ = ev._compute_prepared_factorized_positions_results(gen, pos, V)
+    np.testing.assert_array_equal(f3, f_ref)
