@@ -14,6 +14,10 @@ constexpr int kWave = 64;
 // mace_kokkos_runtime.cpp:199); the margin keeps strided int loops over edge
 // ranges (stride <= 4096) from overflowing.
 constexpr long long kMaxEdges = 2147483647LL - 4096;
+// The tiled plan indexes the graph's edges with 64 bits (each tile's kernels
+// see 32-bit offsets relative to the tile's first edge); its bound keeps a
+// one-thread-per-edge launch under the 2^32 work-items of a dispatch.
+constexpr long long kMaxWideEdges = (1LL << 32) - (1LL << 20);
 constexpr int kXcds = 8;
 
 inline void hip_check(hipError_t e, const char* what) {

@@ -861,16 +861,18 @@ __global__ __launch_bounds__(C) void k_r1_reverse(int r0, long long e0, const in
 // 64 transpose slots, takes the ballot of the active ones and walks its set
 // bits in order, eight rows in flight at a time; the sum keeps the
 // source-transpose order (a padded slot adds +0.0, which leaves the FP64
-// accumulator unchanged: it starts at +0.0 and so is never -0.0).
+// accumulator unchanged: it starts at +0.0 and so is never -0.0).  T is the
+// transpose's position and edge-id type (int, or long long in the tiled
+// plan); e_base is the first edge of the rows of Wsrc and r.
 // ---------------------------------------------------------------------------
-template <int C, int NH>
-__device__ __forceinline__ void gather_source_rows(const int* __restrict__ sedges, int t0, int t1, long long e_base,
+template <int C, int NH, class T = int>
+__device__ __forceinline__ void gather_source_rows(const T* __restrict__ sedges, T t0, T t1, long long e_base,
                                                    const float* __restrict__ Wsrc, const double* __restrict__ r,
                                                    double r_cut, int k, double* acc) {
     constexpr int L = C < kWave ? C : kWave;
     constexpr int G = 8;
     const int lane = threadIdx.x % kWave;
-    for (int base = t0; base < t1; base += L) {
+    for (T base = t0; base < t1; base += L) {
         int e = 0;
         bool on = false;
         if (base + lane < t1) {

@@ -288,8 +288,15 @@ struct Evaluator {
     TileView feature_tile;
     bool feature_graph() const { return F != N || !h_feature_of.empty(); }
     std::vector<int> h_node_types;
-    std::vector<int> h_offsets;
+    std::vector<std::int64_t> h_offsets;
     DevBuf d_node_types, d_offsets, d_neigh, d_neigh_types, d_receivers, d_soff, d_sedges, d_counts;
+    // The tiled plan indexes edges with 64 bits: its source transpose
+    // (d_soff64/d_sedges64 in place of d_soff/d_sedges) and the device
+    // neighbour list's offsets (d_offsets64, until the schedule is built;
+    // d_offsets is then absent beyond kMaxEdges edges).  Each tile's kernels
+    // read 32-bit offsets relative to its first edge: d_tile_off holds them,
+    // tile after tile (tile ti's nr+1 values start at r0 + ti).
+    DevBuf d_offsets64, d_soff64, d_sedges64, d_tile_off;
     // receiver tiles
     std::vector<TileView> tiles;
     PlanSet ps_a0, ps_h1, ps_a1f, ps_a1r, ps_cap, ps_fz, ps_fy;
@@ -614,7 +621,7 @@ struct Evaluator {
         const std::size_t C = hm.C, NY = hm.num_lm, NH = hm.num_LM, NLME = hm.num_lme;
         const std::size_t nt = std::min<std::int64_t>(n, tile_limit);
         const std::size_t et = n > 0 ? static_cast<std::size_t>(static_cast<double>(e) * nt / n) + 1 : 0;
-        const std::size_t graph = (2 * NH + 2) * C * 4 * n + 56 * n + 20 * e;
+        const std::size_t graph = (2 * NH + 2) * C * 4 * n + 64 * n + 24 * e;
         const std::size_t tile = ((two_layer() ? 6 : 4) * NY + 4 * NH + 2 * NLME + 3) * C * 4 * nt +
                                  ((ks->record_floats() + (two_layer() ? NH * C : 0)) * 4 + 24 + 32 + 24) * et;
         return graph + tile;
@@ -664,6 +671,17 @@ struct Evaluator {
         if (N <= tile_limit && debug_plan != tiled_plan() && tiled) {
             tiled = false;
             plan_reason = "the graph fits one receiver tile";
+        }
+        // the direct plan's edge ids are 32-bit; the tiled plan's are 64-bit
+        if (E > kMaxEdges && !tiled) {
+            if (hm.field)
+                throw std::invalid_argument("a MACEField model runs in the retained direct plan, whose edge count is "
+                                            "limited to 2^31 - 4096");
+            if (debug_plan == kPlanSpeed || debug_plan == kPlanRetained)
+                throw std::invalid_argument(debug_plan + " limits the edge count to 2^31 - 4096; this graph needs " +
+                                            tiled_plan());
+            tiled = true;
+            plan_reason = "the edge count exceeds the direct plan's 32-bit edge ids";
         }
     }
 
@@ -726,9 +744,19 @@ struct Evaluator {
             t.r0 = r0;
             t.nr = std::min(limit, N - r0);
             t.e0 = h_offsets[r0];
-            t.ne = static_cast<std::int64_t>(h_offsets[r0 + t.nr]) - t.e0;
+            t.ne = h_offsets[r0 + t.nr] - t.e0;
+            if (t.ne > kMaxEdges) throw std::length_error("a receiver tile holds more than 2^31 - 4096 edges");
             tiles.push_back(t);
             if (N == 0) break;
+        }
+        if (tiled) {
+            std::vector<int> rel;
+            rel.reserve(static_cast<std::size_t>(N) + tiles.size());
+            for (const auto& t : tiles)
+                for (int i = 0; i <= t.nr; ++i) rel.push_back(static_cast<int>(h_offsets[t.r0 + i] - t.e0));
+            upload(d_tile_off, rel, stream);
+        } else {
+            d_tile_off.release();
         }
         max_tile_nr = 0;
         max_tile_ne = 0;
@@ -1003,18 +1031,42 @@ struct Evaluator {
 
     // receiver CSR on the device -> schedule, tiles, plans, workspace, token
     std::uint64_t finish_graph() {
-        d_receivers.ensure(std::max<std::int64_t>(E, 1) * sizeof(int));
-        d_soff.ensure((F + 1) * sizeof(int));
-        d_sedges.ensure(std::max<std::int64_t>(E, 1) * sizeof(int));
-        d_counts.ensure(std::max(F, 1) * sizeof(int));
-        launch_graph_schedule(N, F, E, d_offsets.as<int>(), d_neigh.as<int>(), d_receivers.as<int>(), d_soff.as<int>(),
-                              d_sedges.as<int>(), d_counts.as<int>(), stream);
-        if (static_cast<int>(h_offsets.size()) != N + 1) {
-            h_offsets.resize(N + 1);
-            SMX_HIP(hipMemcpy(h_offsets.data(), d_offsets.as<int>(), sizeof(int) * (N + 1), hipMemcpyDeviceToHost));
-        }
-        prepare_pair_tables();
+        // the plan first: it sets the width of the source transpose
         choose_plan();
+        const bool wide_offsets = d_offsets64.capacity() > 0;
+        d_receivers.ensure(std::max<std::int64_t>(E, 1) * sizeof(int));
+        d_counts.ensure(std::max(F, 1) * sizeof(int));
+        if (wide_offsets)
+            launch_receivers(N, d_offsets64.as<long long>(), d_receivers.as<int>(), stream);
+        else
+            launch_receivers(N, d_offsets.as<int>(), d_receivers.as<int>(), stream);
+        if (tiled) {
+            for (DevBuf* b : {&d_soff, &d_sedges}) b->release();
+            d_soff64.ensure((static_cast<std::size_t>(F) + 1) * sizeof(long long));
+            d_sedges64.ensure(std::max<std::int64_t>(E, 1) * sizeof(long long));
+            launch_transpose(F, E, d_neigh.as<int>(), d_soff64.as<long long>(), d_sedges64.as<long long>(),
+                             d_counts.as<int>(), stream);
+        } else {
+            for (DevBuf* b : {&d_soff64, &d_sedges64}) b->release();
+            d_soff.ensure((static_cast<std::size_t>(F) + 1) * sizeof(int));
+            d_sedges.ensure(std::max<std::int64_t>(E, 1) * sizeof(int));
+            launch_transpose(F, E, d_neigh.as<int>(), d_soff.as<int>(), d_sedges.as<int>(), d_counts.as<int>(),
+                             stream);
+        }
+        if (static_cast<std::int64_t>(h_offsets.size()) != static_cast<std::int64_t>(N) + 1) {
+            h_offsets.resize(static_cast<std::size_t>(N) + 1);
+            if (wide_offsets) {
+                SMX_HIP(hipMemcpy(h_offsets.data(), d_offsets64.as<long long>(), sizeof(long long) * (N + 1),
+                                  hipMemcpyDeviceToHost));
+            } else {
+                std::vector<int> off(static_cast<std::size_t>(N) + 1);
+                SMX_HIP(hipMemcpy(off.data(), d_offsets.as<int>(), sizeof(int) * (N + 1), hipMemcpyDeviceToHost));
+                h_offsets.assign(off.begin(), off.end());
+            }
+        }
+        // the 64-bit offsets serve the schedule and the host copy only
+        d_offsets64.release();
+        prepare_pair_tables();
         build_tiles();
         if (hm.field && feature_graph()) build_feature_tile();
         ensure_workspace();
@@ -1127,7 +1179,7 @@ struct Evaluator {
         F = num_features;
         E = num_edges;
         h_node_types.assign(node_types, node_types + n);
-        h_offsets = off;
+        h_offsets.assign(off.begin(), off.end());
         if (!h_feature_of.empty()) upload(d_feature_of, h_feature_of, stream);
         upload(d_node_types, h_node_types, stream);
         upload(d_offsets, off, stream);
@@ -1416,7 +1468,7 @@ struct Evaluator {
         h_node_types.resize(n);
         if (n > 0) SMX_HIP(hipMemcpy(h_node_types.data(), node_types, sizeof(int) * n, hipMemcpyDeviceToHost));
         validate_types(n, h_node_types.data());
-        h_offsets = offsets;
+        h_offsets.assign(offsets.begin(), offsets.end());
         upload(d_offsets, offsets, stream);
         int* nt = static_cast<int*>(d_node_types.ensure(std::max(n, 1) * sizeof(int)));
         int* nb = static_cast<int*>(d_neigh.ensure(std::max<std::int64_t>(E, 1) * sizeof(int)));
@@ -1437,7 +1489,9 @@ struct Evaluator {
         if (n < 0) throw std::invalid_argument("num_nodes must be non-negative");
         validate_types(n, node_types);
         // release the previous graph's edge arrays first (capacity runs)
-        for (DevBuf* b : {&d_neigh, &d_neigh_types, &d_receivers, &d_sedges, &d_images, &d_ref_edges}) b->release();
+        for (DevBuf* b : {&d_neigh, &d_neigh_types, &d_receivers, &d_sedges, &d_sedges64, &d_images, &d_ref_edges,
+                          &d_edge_pair})
+            b->release();
         NeighborResult nr;
         struct Guard {
             NeighborResult& r;
@@ -1445,11 +1499,12 @@ struct Evaluator {
                 for (void* p : {static_cast<void*>(r.num_neigh), static_cast<void*>(r.offsets),
                                 static_cast<void*>(r.sources), static_cast<void*>(r.images),
                                 static_cast<void*>(r.wfrac), static_cast<void*>(r.shifts),
-                                static_cast<void*>(r.fractional_xyz)})
+                                static_cast<void*>(r.fractional_xyz), static_cast<void*>(r.offsets64)})
                     if (p) (void)hipFree(p);
             }
         } guard{nr};
-        build_neighbor_list(n, positions, cell_, inv_, cutoff, false, nr, stream);
+        // 64-bit offsets: graphs beyond kMaxEdges edges run in the tiled plan
+        build_neighbor_list(n, positions, cell_, inv_, cutoff, false, nr, stream, true);
         N = F = n;
         h_feature_of.clear();
         h_feature_types.clear();
@@ -1457,8 +1512,10 @@ struct Evaluator {
         E = nr.num_edges;
         h_node_types.assign(node_types, node_types + n);
         upload(d_node_types, h_node_types, stream);
-        d_offsets.adopt(nr.offsets, (N + 1) * sizeof(int));
+        d_offsets.adopt(nr.offsets, (N + 1) * sizeof(int));  // null beyond kMaxEdges edges
         nr.offsets = nullptr;
+        d_offsets64.adopt(nr.offsets64, (N + 1) * sizeof(long long));
+        nr.offsets64 = nullptr;
         d_neigh.adopt(nr.sources, std::max<std::int64_t>(E, 1) * sizeof(int));
         nr.sources = nullptr;
         d_images.adopt(nr.images, std::max<std::int64_t>(E, 1) * sizeof(std::uint32_t));
@@ -1513,7 +1570,8 @@ struct Evaluator {
         }
         if (!records) return;
         if (tm) tm->begin("edge_records", stream);
-        ks->edge_geometry(dm, view(), t, tile_xyz(t), tile_r(t), hm.agnesi ? d_edge_pair.as<int>() + t.e0 : nullptr,
+        const auto [g, lt] = tile_view(t);
+        ks->edge_geometry(dm, g, lt, tile_xyz(t), tile_r(t), g.edge_pair ? g.edge_pair + lt.e0 : nullptr,
                           static_cast<int*>(w_exec.ensure(std::max<std::int64_t>(max_tile_ne, 1) * sizeof(int))),
                           ws.erec, ws.erec_b, stream);
         if (tm) tm->end("edge_records", stream);
@@ -1792,9 +1850,10 @@ struct Evaluator {
             if (lmp) raise_if_invalid_geometry("LAMMPS positions");
             for (const auto& t : tiles) {
                 tile_geometry(t, positions);
-                ks->layer1_forward(dm, g, t, ws, true, stream, tm);
-                ks->single_readout(dm, g, t, ws, stream, tm);
-                ks->layer1_reverse(dm, g, t, ws, true, stream, tm);
+                const auto [gt, lt] = tile_view(t);
+                ks->layer1_forward(dm, gt, lt, ws, true, stream, tm);
+                ks->single_readout(dm, gt, lt, ws, stream, tm);
+                ks->layer1_reverse(dm, gt, lt, ws, true, stream, tm);
                 accumulate_tile_outputs(t);
             }
             forces_to_caller_order();
@@ -1815,32 +1874,32 @@ struct Evaluator {
     // adjoint accumulated over the tiles; the layer-1 reverse (forces and
     // virial accumulated as each tile finishes)
     void tiled_sweep_h1(const double* positions) {
-        const DeviceGraph g = view();
         for (const auto& t : tiles) {
             tile_geometry(t, positions);
-            ks->layer1_forward(dm, g, t, ws, true, stream, timer.get());
+            const auto [g, lt] = tile_view(t);
+            ks->layer1_forward(dm, g, lt, ws, true, stream, timer.get());
         }
     }
 
     void tiled_sweep_layer2(const double* positions) {
-        const DeviceGraph g = view();
         launch_fill_zero(ws.H1_adj, static_cast<std::size_t>(F) * hm.num_LM * hm.C, stream);
         launch_fill_zero(d_atom_forces.as<double>(), static_cast<std::size_t>(F) * 3, stream);
         launch_fill_zero(d_virial.as<double>(), 9, stream);
         for (const auto& t : tiles) {
             tile_geometry(t, positions);
-            ks->layer2(dm, g, t, ws, stream, timer.get());
-            ks->source_adjoint_tile(g, t, ws, tile_r(t), hm.r_cut, stream, timer.get());
+            const auto [g, lt] = tile_view(t);
+            ks->layer2(dm, g, lt, ws, stream, timer.get());
+            ks->source_adjoint_tile(g, lt, ws, tile_r(t), hm.r_cut, stream, timer.get());
             accumulate_tile_outputs(t);
         }
     }
 
     void tiled_sweep_reverse(const double* positions) {
-        const DeviceGraph g = view();
         for (const auto& t : tiles) {
             tile_geometry(t, positions);
-            ks->layer1_forward(dm, g, t, ws, false, stream, timer.get());
-            ks->layer1_reverse(dm, g, t, ws, false, stream, timer.get());
+            const auto [g, lt] = tile_view(t);
+            ks->layer1_forward(dm, g, lt, ws, false, stream, timer.get());
+            ks->layer1_reverse(dm, g, lt, ws, false, stream, timer.get());
             accumulate_tile_outputs(t);
         }
         forces_to_caller_order();
@@ -1864,10 +1923,12 @@ struct Evaluator {
             const std::size_t ti = static_cast<std::size_t>(&t - tiles.data());
             launch_tile_forces(t, l_touched.as<int>() + l_touched_begin[ti],
                                static_cast<int>(l_touched_begin[ti + 1] - l_touched_begin[ti]), d_offsets.as<int>(),
-                               l_joff.as<int>(), l_jedges.as<int>(), lmp->ilist, ws.node_forces, lmp->f, stream);
+                               t.e0, l_joff.as<int>(), l_jedges.as<int>(), lmp->ilist, ws.node_forces, lmp->f, stream);
         } else {
-            launch_tile_forces(t, t.touched, t.touched_count, d_offsets.as<int>(), d_soff.as<int>(),
-                               d_sedges.as<int>(), nullptr, ws.node_forces, d_atom_forces.as<double>(), stream);
+            const auto [g, lt] = tile_view(t);
+            launch_tile_forces(t, t.touched, t.touched_count, g.offsets, lt.e0, d_soff64.as<long long>(),
+                               d_sedges64.as<long long>(), nullptr, ws.node_forces, d_atom_forces.as<double>(),
+                               stream);
         }
         launch_virial_accumulate(t.ne, ws.node_forces, tile_xyz(t), d_stress_partial.as<double>(), stress_blocks,
                                  d_virial.as<double>(), stream);
@@ -2056,8 +2117,30 @@ struct Evaluator {
         g.receivers = d_receivers.as<int>();
         g.soff = d_soff.as<int>();
         g.sedges = d_sedges.as<int>();
+        g.soff64 = d_soff64.as<long long>();
+        g.sedges64 = d_sedges64.as<long long>();
         g.edge_pair = hm.agnesi ? d_edge_pair.as<int>() : nullptr;
         return g;
+    }
+
+    // The kernels' view of one tile.  Direct plan: the graph and the tile as
+    // they are.  Tiled plan: the per-edge arrays start at the tile's first
+    // edge, the offsets are the tile's relative ones and the tile's e0 is 0,
+    // so the kernels' edge indices stay 32-bit at any graph size.
+    std::pair<DeviceGraph, TileView> tile_view(const TileView& t) const {
+        DeviceGraph g = view();
+        TileView lt = t;
+        if (!tiled) return {g, lt};
+        const std::size_t ti = static_cast<std::size_t>(&t - tiles.data());
+        g.offsets = d_tile_off.as<int>() + ti;
+        g.neigh += t.e0;
+        g.neigh_types += t.e0;
+        g.receivers += t.e0;
+        if (g.edge_pair) g.edge_pair += t.e0;
+        g.E = t.ne;
+        g.edge_base = t.e0;
+        lt.e0 = 0;
+        return {g, lt};
     }
 
     void require_evaluated(std::uint64_t token) const {

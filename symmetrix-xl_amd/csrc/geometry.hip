@@ -162,9 +162,10 @@ __global__ void k_bin_fill(int N, const int* __restrict__ abin, int* __restrict_
 // back to one lane's insertion sort.
 constexpr int kSortLds = 2048;
 
+template <class T>
 __global__ __launch_bounds__(kWave) void k_sort_segments(int nseg, const long long* __restrict__ off,
-                                                         int* __restrict__ items) {
-    __shared__ int buf[kSortLds];
+                                                         T* __restrict__ items) {
+    __shared__ T buf[kSortLds];
     const int seg = blockIdx.x;
     if (seg >= nseg) return;
     const long long lo = off[seg], hi = off[seg + 1];
@@ -176,7 +177,7 @@ __global__ __launch_bounds__(kWave) void k_sort_segments(int nseg, const long lo
         for (int t = lane; t < m; t += kWave) buf[t] = items[lo + t];
         __syncthreads();
         for (int t = lane; t < m; t += kWave) {
-            const int v = buf[t];
+            const T v = buf[t];
             int rank = 0;
             for (int u = 0; u < m; ++u) rank += buf[u] < v ? 1 : 0;
             items[lo + rank] = v;
@@ -185,7 +186,7 @@ __global__ __launch_bounds__(kWave) void k_sort_segments(int nseg, const long lo
     }
     if (lane != 0) return;
     for (long long p = lo + 1; p < hi; ++p) {
-        const int v = items[p];
+        const T v = items[p];
         long long q = p - 1;
         while (q >= lo && items[q] > v) {
             items[q + 1] = items[q];
@@ -290,10 +291,11 @@ __global__ __launch_bounds__(kVisitWaves* kWave) void k_neighbor_visit(
 // Edge schedules: receiver of each edge, source transpose (edges ordered by
 // source, ascending edge id) -- lifecycle.cpp:3605-3823.
 // ---------------------------------------------------------------------------
-__global__ void k_receivers(int N, const int* __restrict__ off, int* __restrict__ receivers) {
+template <class Off>
+__global__ void k_receivers(int N, const Off* __restrict__ off, int* __restrict__ receivers) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= N) return;
-    for (int e = off[i]; e < off[i + 1]; ++e) receivers[e] = i;
+    for (long long e = off[i]; e < off[i + 1]; ++e) receivers[e] = i;
 }
 
 __global__ void k_count_sources(long long E, const int* __restrict__ sources, int* __restrict__ counts) {
@@ -308,6 +310,15 @@ __global__ void k_fill_sources(long long E, const int* __restrict__ sources, int
     if (e >= E) return;
     const int slot = atomicAdd(&cursor[sources[e]], 1);
     sedges[slot] = static_cast<int>(e);
+}
+
+// the same with 64-bit slots and edge ids (graphs beyond 2^31 edges)
+__global__ void k_fill_sources_wide(long long E, const int* __restrict__ sources,
+                                    unsigned long long* __restrict__ cursor, long long* __restrict__ sedges) {
+    const long long e = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (e >= E) return;
+    const unsigned long long slot = atomicAdd(&cursor[sources[e]], 1ull);
+    sedges[slot] = e;
 }
 
 __global__ void k_gather_int(long long n, const int* __restrict__ idx, const int* __restrict__ table,
@@ -633,7 +644,7 @@ std::int64_t device_exclusive_scan(const int* in, long long* out, int n, hipStre
 }
 
 void build_neighbor_list(int N, const double* positions_host, const double* cell_host, const double* inv_host,
-                         double cutoff, bool with_shifts, NeighborResult& out, hipStream_t s) {
+                         double cutoff, bool with_shifts, NeighborResult& out, hipStream_t s, bool wide) {
     if (!std::isfinite(cutoff) || !(cutoff > 0.0)) throw std::invalid_argument("neighbor cutoff must be positive");
     if (N < 0) throw std::invalid_argument("negative atom count");
     for (int i = 0; i < 3 * N; ++i)
@@ -682,6 +693,7 @@ void build_neighbor_list(int N, const double* positions_host, const double* cell
                         static_cast<void*>(boff), static_cast<void*>(cursor), static_cast<void*>(batoms),
                         static_cast<void*>(counts), static_cast<void*>(eoff)})
             (void)hipFree(p);
+        eoff = nullptr;
     };
     try {
         SMX_HIP(hipMemcpyAsync(d_pos, positions_host, 3 * sizeof(double) * N, hipMemcpyHostToDevice, s));
@@ -708,10 +720,11 @@ void build_neighbor_list(int N, const double* positions_host, const double* cell
             SMX_LAUNCH_CHECK("neighbor_count");
         }
         const long long E = device_exclusive_scan(counts, eoff, N, s);
-        if (E > kMaxEdges) throw std::length_error("neighbor edge count exceeds the 32-bit graph limit");
+        if (E > (wide ? kMaxWideEdges : kMaxEdges))
+            throw std::length_error(wide ? "neighbor edge count exceeds the tiled plan's edge limit"
+                                         : "neighbor edge count exceeds the 32-bit graph limit");
         out.num_edges = E;
         out.num_neigh = dev_alloc<int>(N);
-        out.offsets = dev_alloc<int>(N + 1);
         out.sources = dev_alloc<int>(E);
         out.images = dev_alloc<std::uint32_t>(E);
         if (with_shifts) {
@@ -719,8 +732,11 @@ void build_neighbor_list(int N, const double* positions_host, const double* cell
             out.fractional_xyz = dev_alloc<double>(3 * static_cast<std::size_t>(E));
         }
         SMX_HIP(hipMemcpyAsync(out.num_neigh, counts, sizeof(int) * N, hipMemcpyDeviceToDevice, s));
-        k_copy_i64_i32_plus<<<blocks_for(N + 1, 256), 256, 0, s>>>(eoff, out.offsets, N);
-        SMX_LAUNCH_CHECK("neighbor_offsets");
+        if (E <= kMaxEdges) {
+            out.offsets = dev_alloc<int>(N + 1);
+            k_copy_i64_i32_plus<<<blocks_for(N + 1, 256), 256, 0, s>>>(eoff, out.offsets, N);
+            SMX_LAUNCH_CHECK("neighbor_offsets");
+        }
         if (N > 0 && E > 0) {
             k_neighbor_visit<true><<<vb, kVisitWaves * kWave, 0, s>>>(N, cell, g, cut2, wfrac, wpos, wrap, abin, boff,
                                                                       batoms, nullptr, eoff, out.sources, out.images,
@@ -728,6 +744,10 @@ void build_neighbor_list(int N, const double* positions_host, const double* cell
             SMX_LAUNCH_CHECK("neighbor_fill");
         }
         SMX_HIP(hipStreamSynchronize(s));
+        if (wide) {
+            out.offsets64 = eoff;  // the caller's now
+            eoff = nullptr;
+        }
     } catch (...) {
         release();
         throw;
@@ -764,12 +784,49 @@ void launch_transpose(int K, std::int64_t E, const int* keys, int* koff, int* ke
     SMX_HIP(hipFree(off64));
 }
 
+void launch_transpose(int K, std::int64_t E, const int* keys, long long* koff, long long* kedges, int* scratch_counts,
+                      hipStream_t s) {
+    if (K == 0) return;
+    SMX_HIP(hipMemsetAsync(scratch_counts, 0, sizeof(int) * K, s));
+    if (E > 0) {
+        k_count_sources<<<blocks_for(E, 256), 256, 0, s>>>(E, keys, scratch_counts);
+        SMX_LAUNCH_CHECK("transpose_count");
+    }
+    device_exclusive_scan(scratch_counts, koff, K, s);
+    if (E > 0) {
+        // each key's write cursor starts at its segment
+        unsigned long long* cursor = dev_alloc<unsigned long long>(K);
+        try {
+            SMX_HIP(hipMemcpyAsync(cursor, koff, sizeof(long long) * K, hipMemcpyDeviceToDevice, s));
+            k_fill_sources_wide<<<blocks_for(E, 256), 256, 0, s>>>(E, keys, cursor, kedges);
+            SMX_LAUNCH_CHECK("transpose_fill");
+            SMX_HIP(hipStreamSynchronize(s));
+        } catch (...) {
+            (void)hipFree(cursor);
+            throw;
+        }
+        SMX_HIP(hipFree(cursor));
+    }
+    k_sort_segments<<<K, kWave, 0, s>>>(K, koff, kedges);
+    SMX_LAUNCH_CHECK("transpose_sort");
+    SMX_HIP(hipStreamSynchronize(s));
+}
+
+void launch_receivers(int N, const int* offsets, int* receivers, hipStream_t s) {
+    if (N == 0) return;
+    k_receivers<<<blocks_for(N, 256), 256, 0, s>>>(N, offsets, receivers);
+    SMX_LAUNCH_CHECK("graph_receivers");
+}
+
+void launch_receivers(int N, const long long* offsets, int* receivers, hipStream_t s) {
+    if (N == 0) return;
+    k_receivers<<<blocks_for(N, 256), 256, 0, s>>>(N, offsets, receivers);
+    SMX_LAUNCH_CHECK("graph_receivers");
+}
+
 void launch_graph_schedule(int N, int F, std::int64_t E, const int* offsets, const int* sources, int* receivers,
                            int* soff, int* sedges, int* scratch_counts, hipStream_t s) {
-    if (N > 0) {
-        k_receivers<<<blocks_for(N, 256), 256, 0, s>>>(N, offsets, receivers);
-        SMX_LAUNCH_CHECK("graph_receivers");
-    }
+    launch_receivers(N, offsets, receivers, s);
     launch_transpose(F, E, sources, soff, sedges, scratch_counts, s);
 }
 

@@ -529,12 +529,15 @@ __global__ __launch_bounds__(64 * kReadoutWaves) void k_readout(
 // Tiled execution: per-tile contributions of edges to their sources.  The
 // edges of source s inside the tile's edge range [e0, e1) are a contiguous
 // run of s's source-transpose segment (edge ids ascend within a segment and
-// edges are receiver-major), found by a binary search.
+// edges are receiver-major), found by a binary search.  T is the
+// transpose's position and edge-id type: long long for the tiled plan's own
+// graphs (beyond 2^31 edges), int for the LAMMPS neighbour transpose.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ int lower_edge(const int* __restrict__ sedges, int lo, int hi, long long key) {
+template <class T>
+__device__ __forceinline__ T lower_edge(const T* __restrict__ sedges, T lo, T hi, long long key) {
     while (lo < hi) {
         // lo + hi can exceed 2^31 when the graph has more than 2^30 edges
-        const int mid = lo + ((hi - lo) >> 1);
+        const T mid = lo + ((hi - lo) >> 1);
         if (sedges[mid] < key)
             lo = mid + 1;
         else
@@ -545,10 +548,9 @@ __device__ __forceinline__ int lower_edge(const int* __restrict__ sedges, int lo
 
 // H1_adj[s] += sum over the tile's edges leaving s of W_e (FP64 sum, one
 // read-modify-write per source and tile; tiles run in order).
-template <int C, int NH>
+template <int C, int NH, class T>
 __global__ __launch_bounds__(C) void k_tile_source_adjoint(const int* __restrict__ touched, long long e0, long long e1,
-                                                           const int* __restrict__ soff,
-                                                           const int* __restrict__ sedges,
+                                                           const T* __restrict__ soff, const T* __restrict__ sedges,
                                                            const float* __restrict__ Wsrc,
                                                            const double* __restrict__ r, double r_cut,
                                                            float* __restrict__ H1_adj) {
@@ -557,9 +559,9 @@ __global__ __launch_bounds__(C) void k_tile_source_adjoint(const int* __restrict
     double acc[NH];
 #pragma unroll
     for (int q = 0; q < NH; ++q) acc[q] = 0.0;
-    const int hi = soff[s + 1];
-    const int lo = lower_edge(sedges, soff[s], hi, e0);
-    const int end = lower_edge(sedges, lo, hi, e1);
+    const T hi = soff[s + 1];
+    const T lo = lower_edge(sedges, soff[s], hi, e0);
+    const T end = lower_edge(sedges, lo, hi, e1);
     gather_source_rows<C, NH>(sedges, lo, end, e0, Wsrc, r, r_cut, k, acc);
     float* dst = H1_adj + static_cast<std::size_t>(s) * NH * C + k;
 #pragma unroll
@@ -567,18 +569,19 @@ __global__ __launch_bounds__(C) void k_tile_source_adjoint(const int* __restrict
 }
 
 // F[s] += sum of the tile's directed forces on edges leaving s (one wave per source)
+template <class T>
 __global__ __launch_bounds__(256) void k_tile_forces_sources(const int* __restrict__ touched, int count, long long e0,
-                                                             long long e1, const int* __restrict__ soff,
-                                                             const int* __restrict__ sedges,
+                                                             long long e1, const T* __restrict__ soff,
+                                                             const T* __restrict__ sedges,
                                                              const double* __restrict__ nf, double* __restrict__ F) {
     const int b = blockIdx.x * (256 / kWave) + threadIdx.x / kWave;
     const int lane = threadIdx.x % kWave;
     if (b >= count) return;
     const int s = touched[b];
-    const int hi = soff[s + 1];
-    const int lo = lower_edge(sedges, soff[s], hi, e0);
+    const T hi = soff[s + 1];
+    const T lo = lower_edge(sedges, soff[s], hi, e0);
     double f0 = 0.0, f1 = 0.0, f2 = 0.0;
-    for (int t = lo + lane; t < hi; t += kWave) {
+    for (T t = lo + lane; t < hi; t += kWave) {
         const long long e = sedges[t];
         if (e >= e1) break;
         const std::size_t le = static_cast<std::size_t>(e - e0);
@@ -1490,8 +1493,13 @@ struct KernelSetImpl final : KernelSet {
                              double r_cut, hipStream_t s, LaunchTimer* tm) const override {
         if (t.touched_count == 0) return;
         TimerScope ts(tm, "source_gather", s);
-        k_tile_source_adjoint<C, S::NH><<<t.touched_count, C, 0, s>>>(t.touched, t.e0, t.e0 + t.ne, g.soff, g.sedges,
-                                                                     w.Wsrc, r, r_cut, w.H1_adj);
+        const long long e0 = g.edge_base + t.e0;
+        if (g.sedges64)
+            k_tile_source_adjoint<C, S::NH><<<t.touched_count, C, 0, s>>>(t.touched, e0, e0 + t.ne, g.soff64,
+                                                                         g.sedges64, w.Wsrc, r, r_cut, w.H1_adj);
+        else
+            k_tile_source_adjoint<C, S::NH><<<t.touched_count, C, 0, s>>>(t.touched, e0, e0 + t.ne, g.soff, g.sedges,
+                                                                         w.Wsrc, r, r_cut, w.H1_adj);
         SMX_LAUNCH_CHECK("tile_source_adjoint");
     }
 
@@ -1887,19 +1895,32 @@ void launch_scale9(const double* in, double scale, double* out, hipStream_t s) {
     SMX_LAUNCH_CHECK("scale9");
 }
 
-void launch_tile_forces(const TileView& t, const int* touched, int touched_count, const int* offsets,
-                        const int* soff, const int* sedges, const int* receiver_row, const double* node_forces,
-                        double* F, hipStream_t s) {
+template <class T>
+void tile_forces(const TileView& t, const int* touched, int touched_count, const int* offsets, long long offsets_e0,
+                 const T* soff, const T* sedges, const int* receiver_row, const double* node_forces, double* F,
+                 hipStream_t s) {
     if (touched_count > 0) {
         k_tile_forces_sources<<<blocks_for(touched_count, 256 / kWave), 256, 0, s>>>(
             touched, touched_count, t.e0, t.e0 + t.ne, soff, sedges, node_forces, F);
         SMX_LAUNCH_CHECK("tile_forces_sources");
     }
     if (t.nr > 0) {
-        k_tile_forces_receivers<<<blocks_for(t.nr, 256 / kWave), 256, 0, s>>>(t.r0, t.nr, t.e0, offsets,
+        k_tile_forces_receivers<<<blocks_for(t.nr, 256 / kWave), 256, 0, s>>>(t.r0, t.nr, offsets_e0, offsets,
                                                                               receiver_row, node_forces, F);
         SMX_LAUNCH_CHECK("tile_forces_receivers");
     }
+}
+
+void launch_tile_forces(const TileView& t, const int* touched, int touched_count, const int* offsets,
+                        long long offsets_e0, const int* soff, const int* sedges, const int* receiver_row,
+                        const double* node_forces, double* F, hipStream_t s) {
+    tile_forces(t, touched, touched_count, offsets, offsets_e0, soff, sedges, receiver_row, node_forces, F, s);
+}
+
+void launch_tile_forces(const TileView& t, const int* touched, int touched_count, const int* offsets,
+                        long long offsets_e0, const long long* soff, const long long* sedges,
+                        const int* receiver_row, const double* node_forces, double* F, hipStream_t s) {
+    tile_forces(t, touched, touched_count, offsets, offsets_e0, soff, sedges, receiver_row, node_forces, F, s);
 }
 
 void launch_type_bias(int r0, int nr, const int* types, int row_len, const float* bias, float* rows, hipStream_t s) {

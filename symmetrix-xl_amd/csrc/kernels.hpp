@@ -106,6 +106,13 @@ struct DeviceGraph {
     // [E] radial-table pair of each edge (symmetric index over the active
     // types) when tables differ per pair (Agnesi transform), else null
     const int* edge_pair = nullptr;
+    // The tiled plan's source transpose, with 64-bit positions and edge ids
+    // (soff/sedges are then null).  Its tiles see the graph through views
+    // whose per-edge arrays and 32-bit offsets start at the tile's first
+    // edge, graph edge edge_base (0 in a whole-graph view).
+    const long long* soff64 = nullptr;    // [F+1]
+    const long long* sedges64 = nullptr;  // [E]
+    long long edge_base = 0;
 };
 
 // Node linears: out[row, n] = sum_k in[row, k] W[k, n] over the rows of one
@@ -395,12 +402,17 @@ void launch_virial_accumulate(std::int64_t E, const double* node_forces, const d
                               int partial_blocks, double* virial, hipStream_t s);
 void launch_scale9(const double* in, double scale, double* out, hipStream_t s);
 // F[src] += f_e, F[rcv] -= f_e for one tile's edges (tile-local forces).
-// touched/touched_count: the sources the tile's edges leave, listed in the
-// index space of soff/sedges; receiver_row maps a graph node to its F row
-// (nullptr: the node index itself).
+// t.e0/t.ne: the tile's range in the edge ids of sedges; touched/
+// touched_count: the sources the tile's edges leave, listed in the index
+// space of soff/sedges; offsets[r0..r0+nr] the receivers' edge ranges, whose
+// first tile edge is offsets_e0 (the tile's own relative offsets: 0);
+// receiver_row maps a graph node to its F row (nullptr: the node index).
 void launch_tile_forces(const TileView& t, const int* touched, int touched_count, const int* offsets,
-                        const int* soff, const int* sedges, const int* receiver_row, const double* node_forces,
-                        double* F, hipStream_t s);
+                        long long offsets_e0, const int* soff, const int* sedges, const int* receiver_row,
+                        const double* node_forces, double* F, hipStream_t s);
+void launch_tile_forces(const TileView& t, const int* touched, int touched_count, const int* offsets,
+                        long long offsets_e0, const long long* soff, const long long* sedges,
+                        const int* receiver_row, const double* node_forces, double* F, hipStream_t s);
 void launch_fill_zero(float* p, std::size_t n, hipStream_t s);
 void launch_fill_zero(double* p, std::size_t n, hipStream_t s);
 void launch_energy_sum(int N, const double* node_energies, double* total, hipStream_t s);
@@ -439,16 +451,22 @@ struct NeighborResult {
     double* wfrac = nullptr;         // [N][3] wrapped fractional positions
     int* shifts = nullptr;           // [E][3] (only when requested)
     double* fractional_xyz = nullptr;  // [E][3] (only when requested)
+    long long* offsets64 = nullptr;    // [N+1] (only when wide)
 };
 // Builds into buffers allocated with hipMalloc (freed by the caller with
 // hipFree); positions/cell/inverse on the host.  with_shifts also fills
-// shifts and fractional_xyz.
+// shifts and fractional_xyz.  wide admits up to kMaxWideEdges edges and
+// hands out the 64-bit offsets too; the 32-bit offsets are then filled only
+// when the edge count is at most kMaxEdges.
 void build_neighbor_list(int N, const double* positions_host, const double* cell_host, const double* inv_host,
-                         double cutoff, bool with_shifts, NeighborResult& out, hipStream_t s);
+                         double cutoff, bool with_shifts, NeighborResult& out, hipStream_t s, bool wide = false);
 
 // Edge receivers and source transpose from a receiver CSR (all on device).
 void launch_graph_schedule(int N, int F, std::int64_t E, const int* offsets, const int* sources, int* receivers,
                            int* soff, int* sedges, int* scratch_counts, hipStream_t s);
+// receivers[e] = i for the edges of receiver i
+void launch_receivers(int N, const int* offsets, int* receivers, hipStream_t s);
+void launch_receivers(int N, const long long* offsets, int* receivers, hipStream_t s);
 // LAMMPS pair-style entry (lammps.hip): a full neighbour list as the Kokkos
 // pair style holds it, on the device.
 struct LammpsList {
@@ -479,6 +497,9 @@ void lammps_eatom(int inum, const int* ilist, const double* node_energies, doubl
 // Transpose of an edge -> key map (keys in [0, K)): koff[K+1] and kedges[E]
 // listing each key's edges in ascending edge order.  scratch_counts: K ints.
 void launch_transpose(int K, std::int64_t E, const int* keys, int* koff, int* kedges, int* scratch_counts,
+                      hipStream_t s);
+// the same with 64-bit positions and edge ids (the tiled plan's source transpose)
+void launch_transpose(int K, std::int64_t E, const int* keys, long long* koff, long long* kedges, int* scratch_counts,
                       hipStream_t s);
 // neigh_types[e] = node_types[sources[e]]
 void launch_gather_types(std::int64_t E, const int* sources, const int* node_types, int* neigh_types,

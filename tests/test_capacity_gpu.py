@@ -21,7 +21,10 @@ Full-system properties at the same size: the atom forces sum to zero
 (every directed edge force enters once with each sign), and on the
 unperturbed crystal, where every site is an inversion centre, every atom's
 energy equals its site's energy in the oracle's 3x3x3 cell, every force
-vanishes and the stress equals the oracle's.
+vanishes and the stress equals the oracle's.  The unperturbed check also
+runs at n = 164 (22M atoms, 2.18B edges), past the 2^31 - 4096 edges that
+32-bit edge ids hold: the tiled plan's 64-bit source transpose and
+tile-relative offsets carry every edge beyond that index.
 
 Bars: energy 1e-5 eV/atom, forces 1e-4 eV/A, stress 1e-6 eV/A^3.
 """
@@ -112,10 +115,12 @@ def test_tiled_plan_against_oracle_probes_at_size(medium_model_path, cells, rand
     assert worst_e < 1e-6 and worst_f < 1e-6
 
 
-def test_unperturbed_crystal_at_eleven_million_atoms(medium_model_path):
-    """n = 132 unperturbed (every site an inversion centre): each atom's
-    energy equals its species' site energy in the oracle's 3x3x3 cell, every
-    force vanishes, and the stress equals the oracle's."""
+@pytest.mark.parametrize("cells", [132, 164])
+def test_unperturbed_crystal_at_size(medium_model_path, cells):
+    """n = 132 (11.5M atoms) and n = 164 (22M atoms, beyond 2^31 edges)
+    unperturbed (every site an inversion centre): each atom's energy equals
+    its species' site energy in the oracle's 3x3x3 cell, every force
+    vanishes, and the stress equals the oracle's."""
     from oracle import oracle
     from symmetrix import systems
     om = oracle.OracleModel(medium_model_path)
@@ -127,10 +132,12 @@ def test_unperturbed_crystal_at_eleven_million_atoms(medium_model_path):
     for z, v in site.items():
         assert np.ptp(v) < 5e-6, (z, np.ptp(v))    # equivalent sites in the oracle too
     site = {z: float(np.mean(v)) for z, v in site.items()}
-    system = systems.srtio3_supercell(132, sigma=0.0)
+    system = systems.srtio3_supercell(cells, sigma=0.0)
     n = len(system["numbers"])
-    _say("capacity case: unperturbed SrTiO3 n=132, %d atoms" % n)
+    _say("capacity case: unperturbed SrTiO3 n=%d, %d atoms" % (cells, n))
     types, e, f, s, total, E = _tiled_call(medium_model_path, system)
+    if cells == 164:
+        assert E > 2**31, E   # edge ids beyond 32 bits
     expect = np.array([site[int(z)] for z in system["numbers"][:5]])
     de = np.max(np.abs(e.reshape(-1, 5) - expect[None, :]))
     df = float(np.max(np.abs(f)))
