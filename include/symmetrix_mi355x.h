@@ -122,7 +122,11 @@ SMX_API int32_t smx_prepare_factorized_graph_device(SmxEvaluator* ev, int32_t nu
  * neighbour list at neighbor_cutoff; the builder's wrapped fractional
  * positions and edge images are kept as the (fractional) geometry
  * reference, so the cell may change with smx_update_factorized_cell.
- * cell rows are lattice vectors; inverse_cell = inv(cell). */
+ * cell rows are lattice vectors; inverse_cell = inv(cell).  A graph of more
+ * than 2^31 - 4096 edges (the reference's limit) is accepted up to
+ * 2^32 - 2^20 edges and runs in the tiled plan, which indexes edges with
+ * 64 bits; a request pinning a direct plan, or a MACEField model, is then
+ * refused. */
 SMX_API int32_t smx_prepare_periodic_factorized_graph(SmxEvaluator* ev, int32_t num_nodes, const int32_t* node_types,
                                                       const double* positions, const double* cell,
                                                       const double* inverse_cell, double neighbor_cutoff,
