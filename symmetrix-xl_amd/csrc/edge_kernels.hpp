@@ -514,6 +514,16 @@ template <int LMAX>
 struct SourceGroups<LMAX, 2> {
     static constexpr std::array<unsigned, 3> masks{0x00fu, 0x070u, 0x180u};
 };
+// The R1 reverse stages its records through LDS and is not capped at 128
+// VGPRs, so with L_max 2 its second pass takes all five l = 2 components
+// (225 VGPRs, two waves per SIMD like the first pass): one pass fewer of
+// record, spline and harmonic work than the forward's grouping.
+template <int LMAX, int LMAXH>
+struct ReverseSourceGroups : SourceGroups<LMAX, LMAXH> {};
+template <int LMAX>
+struct ReverseSourceGroups<LMAX, 2> {
+    static constexpr std::array<unsigned, 2> masks{0x00fu, 0x1f0u};
+};
 
 // Channel slices of the R1 forward over unstaged records: with C >= 128 each
 // 64-lane wave is a workgroup of its own holding one slice of a receiver's
@@ -695,7 +705,7 @@ __global__ __launch_bounds__(C) __attribute__((amdgpu_waves_per_eu(4))) void k_r
 // STORE_W false: the forces alone (the source terms are not written)
 template <int C, int LMAX, int LMAXH, unsigned MASK, bool FORCE_ACCUMULATE, class EDGES, int CF = C,
           bool STORE_W = true>
-__global__ __launch_bounds__(C) void k_r1_reverse(int r0, long long e0, const int* __restrict__ offsets,
+__global__ __launch_bounds__(C) __attribute__((amdgpu_waves_per_eu(2))) void k_r1_reverse(int r0, long long e0, const int* __restrict__ offsets,
                                                   const int* __restrict__ neigh, EDGES edges,
                                                   const float* __restrict__ H1, const float* __restrict__ cg,
                                                   const float* __restrict__ dPhi1, float* __restrict__ Wsrc,
