@@ -510,18 +510,14 @@ template <int LMAX>
 struct SourceGroups<LMAX, 1> {
     static constexpr std::array<unsigned, 1> masks{0xfu};
 };
+// L_max 2: the l <= 1 components, then the five l = 2 ones.  A pass
+// re-reads the records and recomputes the spline and harmonic terms, so
+// fewer passes pay less of that work: the l = 2 pass runs at three waves per
+// SIMD in the forward (158 VGPRs) and two in the reverse (256 VGPRs, a few
+// spilled); against three passes (l <= 1, lm 4-6, lm 7-8) the wide config
+// measured 6% faster with the reverse alone in two passes.
 template <int LMAX>
 struct SourceGroups<LMAX, 2> {
-    static constexpr std::array<unsigned, 3> masks{0x00fu, 0x070u, 0x180u};
-};
-// The R1 reverse stages its records through LDS and is not capped at 128
-// VGPRs, so with L_max 2 its second pass takes all five l = 2 components
-// (225 VGPRs, two waves per SIMD like the first pass): one pass fewer of
-// record, spline and harmonic work than the forward's grouping.
-template <int LMAX, int LMAXH>
-struct ReverseSourceGroups : SourceGroups<LMAX, LMAXH> {};
-template <int LMAX>
-struct ReverseSourceGroups<LMAX, 2> {
     static constexpr std::array<unsigned, 2> masks{0x00fu, 0x1f0u};
 };
 
@@ -556,8 +552,11 @@ inline unsigned r1_forward_blocks(int nr) {
 // ---------------------------------------------------------------------------
 // At least four waves per SIMD: the single-pass shapes need 145 VGPRs for
 // three, and at four (128 VGPRs, two spilled) the medium call is 0.7% faster.
+// A pass over more than four source components (the l = 2 pass) keeps three
+// (158 VGPRs; capped at 128 it spills 48).
+constexpr int r1_forward_waves(unsigned mask) { return __builtin_popcount(mask) > 4 ? 3 : 4; }
 template <int C, int LMAX, int LMAXH, unsigned MASK, bool ACCUMULATE, class EDGES, int CF = C>
-__global__ __launch_bounds__(C) __attribute__((amdgpu_waves_per_eu(4))) void k_r1_forward(int r0, int nr, const int* __restrict__ first,
+__global__ __launch_bounds__(C) __attribute__((amdgpu_waves_per_eu(r1_forward_waves(MASK)))) void k_r1_forward(int r0, int nr, const int* __restrict__ first,
                                                   const int* __restrict__ count, const int* __restrict__ neigh,
                                                   EDGES edges, const float* __restrict__ H1,
                                                   const float* __restrict__ cg, float* __restrict__ Phi1) {
@@ -702,7 +701,9 @@ __global__ __launch_bounds__(C) __attribute__((amdgpu_waves_per_eu(4))) void k_r
 // rows hold CF channels (lanes k >= CF read zero, so their G, W and force
 // parts are zero); W rows always hold C.
 // ---------------------------------------------------------------------------
-// STORE_W false: the forces alone (the source terms are not written)
+// STORE_W false: the forces alone (the source terms are not written).  At
+// least two waves per SIMD: the l = 2 pass of L_max-2 models would otherwise
+// take 264 registers and run one wave per SIMD.
 template <int C, int LMAX, int LMAXH, unsigned MASK, bool FORCE_ACCUMULATE, class EDGES, int CF = C,
           bool STORE_W = true>
 __global__ __launch_bounds__(C) __attribute__((amdgpu_waves_per_eu(2))) void k_r1_reverse(int r0, long long e0, const int* __restrict__ offsets,

@@ -1261,8 +1261,6 @@ struct KernelSetImpl final : KernelSet {
     using StagedRecords = RecordEdges<C, S::NY, S::REC_F, S::REC_B, true>;
     using Groups = SourceGroups<LMAX, LMAXH>;
     static constexpr int kGroups = static_cast<int>(Groups::masks.size());
-    using RGroups = ReverseSourceGroups<LMAX, LMAXH>;
-    static constexpr int kRGroups = static_cast<int>(RGroups::masks.size());
     int record_floats() const override { return S::REC; }
     int record_forward_floats() const override { return S::REC_F; }
     template <class R = Records>
@@ -1439,9 +1437,9 @@ struct KernelSetImpl final : KernelSet {
         }
         {
             TimerScope ts(tm, "r1_reverse", s);
-            static_for<0, kRGroups>([&](auto gc) {
+            static_for<0, kGroups>([&](auto gc) {
                 constexpr int gi = gc;
-                k_r1_reverse<C, LMAX, LMAXH, RGroups::masks[gi], (gi > 0), StagedRecords><<<t.nr, C, 0, s>>>(
+                k_r1_reverse<C, LMAX, LMAXH, Groups::masks[gi], (gi > 0), StagedRecords><<<t.nr, C, 0, s>>>(
                     t.r0, t.e0, g.offsets, g.neigh, records<StagedRecords>(m, t, w), w.H1, m.cg, w.dPhi1, w.Wsrc,
                     w.node_forces);
                 SMX_LAUNCH_CHECK("r1_reverse");
@@ -1629,9 +1627,9 @@ struct KernelSetImpl final : KernelSet {
             // the source terms of H1_adj_dot and part of the forces,
             // (H1_dot, dPhi1) the rest of the forces (its source terms are
             // not formed)
-            static_for<0, kRGroups>([&](auto gc) {
+            static_for<0, kGroups>([&](auto gc) {
                 constexpr int gi = gc;
-                k_r1_reverse<C, LMAX, LMAXH, RGroups::masks[gi], (gi > 0), StagedRecords><<<N, C, 0, s>>>(
+                k_r1_reverse<C, LMAX, LMAXH, Groups::masks[gi], (gi > 0), StagedRecords><<<N, C, 0, s>>>(
                     0, 0, g.offsets, g.neigh, records<StagedRecords>(m, t, w), w.H1, m.cg, rw.dPhi1_dot, w.Wsrc, f);
                 SMX_LAUNCH_CHECK("r1_reverse");
             });
@@ -1639,9 +1637,9 @@ struct KernelSetImpl final : KernelSet {
                                                                rw.H1_adj_dot);
             SMX_LAUNCH_CHECK("source_gather");
             if (forces) {
-                static_for<0, kRGroups>([&](auto gc) {
+                static_for<0, kGroups>([&](auto gc) {
                     constexpr int gi = gc;
-                    k_r1_reverse<C, LMAX, LMAXH, RGroups::masks[gi], true, StagedRecords, C, false><<<N, C, 0, s>>>(
+                    k_r1_reverse<C, LMAX, LMAXH, Groups::masks[gi], true, StagedRecords, C, false><<<N, C, 0, s>>>(
                         0, 0, g.offsets, g.neigh, records<StagedRecords>(m, t, w), rw.H1_dot, m.cg, w.dPhi1, nullptr,
                         f);
                     SMX_LAUNCH_CHECK("r1_reverse");
