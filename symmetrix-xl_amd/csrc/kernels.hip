@@ -965,7 +965,8 @@ __global__ void k_fill_f64(std::size_t n, double* __restrict__ p) {
 // one chunk and 16-column block are one contiguous 1 KB float4 load per wave.
 // Per chunk a wave issues RI + NSUB loads and 4*RI*NSUB MFMAs.  Two operand
 // sets alternate: the loads of chunk kc+1 are in flight while chunk kc runs on
-// the MFMA unit.  NSUB is a template constant so that the chunk body is
+// the MFMA unit (a three-set ring measured the same at the medium shape: it
+// costs two waves per SIMD of occupancy).  NSUB is a template constant so that the chunk body is
 // straight-line code (no per-tile branches) and the only waits are for the
 // operands of the chunk about to run.
 // ---------------------------------------------------------------------------
@@ -1097,15 +1098,23 @@ __global__ __launch_bounds__(64 * kGemmShareWaves) void k_node_gemm_shared(
 #pragma unroll
     for (int j = 0; j < NSUB; ++j) acc[j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
     const int chunks = g.K / 16;
+    // operands two chunks ahead: chunk kc runs from a0 and LDS buffer kc&1
+    // while the global loads of chunks kc+1 (a1, b1) and kc+2 (a2, b2) are
+    // in flight; b1 enters LDS at the end of chunk kc
+    const std::size_t bstep = static_cast<std::size_t>(nblk) * 64;
     float4 a0 = *reinterpret_cast<const float4*>(arow);
+    float4 a1 = a0, b1 = B[0];
+    if (chunks > 1) {
+        a1 = *reinterpret_cast<const float4*>(arow + 16);
+        b1 = B[bstep];
+    }
     sb[0][threadIdx.x] = B[0];
     __syncthreads();
     for (int kc = 0; kc < chunks; ++kc) {
-        const bool more = kc + 1 < chunks;
-        float4 bn, a1;
-        if (more) {
-            bn = B[static_cast<std::size_t>(kc + 1) * nblk * 64];
-            a1 = *reinterpret_cast<const float4*>(arow + 16 * (kc + 1));
+        float4 a2 = a1, b2 = b1;
+        if (kc + 2 < chunks) {
+            a2 = *reinterpret_cast<const float4*>(arow + 16 * (kc + 2));
+            b2 = B[static_cast<std::size_t>(kc + 2) * bstep];
         }
         float4 b[NSUB];
 #pragma unroll
@@ -1119,9 +1128,11 @@ __global__ __launch_bounds__(64 * kGemmShareWaves) void k_node_gemm_shared(
                 acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[j], 0, 0, 0);
             }
         }
-        if (more) sb[(kc + 1) & 1][threadIdx.x] = bn;
+        if (kc + 1 < chunks) sb[(kc + 1) & 1][threadIdx.x] = b1;
         __syncthreads();
-        if (more) a0 = a1;
+        a0 = a1;
+        a1 = a2;
+        b1 = b2;
     }
     if (wave >= set.count) return;
 #pragma unroll
