@@ -420,10 +420,16 @@ __global__ __launch_bounds__(64 * kReadoutWaves) void k_readout(
     static_assert(C % 16 == 0, "16-column MFMA blocks");
     constexpr int R = kReadoutBatch, NT = C / 16, WAVES = kReadoutWaves, THREADS = 64 * WAVES;
     constexpr int HMAX = kMaxReadoutHidden;
-    __shared__ float sA[R][2 * C + 1];      // [x | M1] rows (FP32 values)
-    __shared__ double sH[R][C + 1];         // H2, then its adjoint
-    __shared__ double sZ[R][HMAX + 1];      // pre-activations, then W2 act'(z)
-    __shared__ double sP[R][HMAX + 1];      // W2 act(z) terms of the energy
+    // The energy terms sP are written after the last read of sA, so they
+    // share its storage where it is large enough (C >= 64): at 256 channels
+    // the workgroup then needs 74 KB of LDS and two fit a CU.
+    constexpr bool kShareA = sizeof(float) * (2 * C + 1) >= sizeof(double) * (HMAX + 1);
+    __shared__ __align__(16) float sA[R][2 * C + 1];  // [x | M1] rows (FP32 values)
+    __shared__ double sH[R][C + 1];                   // H2, then its adjoint
+    __shared__ double sZ[R][HMAX + 1];                // pre-activations, then W2 act'(z)
+    __shared__ double sPown[kShareA ? 1 : R][HMAX + 1];
+    // W2 act(z) terms of the energy
+    double (*sP)[HMAX + 1] = kShareA ? reinterpret_cast<double (*)[HMAX + 1]>(&sA[0][0]) : sPown;
     const NodeBatch b = batches[blockIdx.x];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int r = lane & 15, kk = lane >> 4;
@@ -437,6 +443,10 @@ __global__ __launch_bounds__(64 * kReadoutWaves) void k_readout(
     }
     for (int p = tid; p < R * (HMAX + 1); p += THREADS) sZ[p / (HMAX + 1)][p % (HMAX + 1)] = 0.0;
     __syncthreads();
+    // q . x of each receiver, read now (sA is overwritten below)
+    double qx = 0.0;
+    if (tid < b.count)
+        for (int k = 0; k < C; ++k) qx += q[k] * static_cast<double>(sA[tid][k]);
     // H2[n][c] = sum_in T[in][c] x[n][in] + sum_in W[in][c] M1[n][in]
     {
         const float* T = H2_T + static_cast<std::size_t>(t) * C * C;
@@ -467,7 +477,8 @@ __global__ __launch_bounds__(64 * kReadoutWaves) void k_readout(
         for (int v = 0; v < 4; ++v) sZ[kk + 4 * v][hd] = acc[v];
     }
     __syncthreads();
-    // activation: energy terms and g = W2 act'(z)
+    // activation: energy terms and g = W2 act'(z) (sA is no longer read:
+    // the z phase's barrier follows the H2 phase's last read of it)
     for (int p = tid; p < R * hidden; p += THREADS) {
         const int n = p / hidden, hd = p % hidden;
         const double z = sZ[n][hd];
@@ -478,8 +489,6 @@ __global__ __launch_bounds__(64 * kReadoutWaves) void k_readout(
     __syncthreads();
     if (tid < b.count) {
         const int n = tid;
-        double qx = 0.0;
-        for (int k = 0; k < C; ++k) qx += q[k] * static_cast<double>(sA[n][k]);
         double out = 0.0;
         for (int hd = 0; hd < hidden; ++hd) out += sP[n][hd];
         node_energies[r0 + node_list[b.start + n]] = E0[t] + qx + out;
