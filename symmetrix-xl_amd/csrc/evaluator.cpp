@@ -2131,7 +2131,9 @@ struct Evaluator {
         DeviceGraph g = view();
         TileView lt = t;
         if (!tiled) return {g, lt};
-        const std::size_t ti = static_cast<std::size_t>(&t - tiles.data());
+        const std::ptrdiff_t ti = &t - tiles.data();
+        if (ti < 0 || ti >= static_cast<std::ptrdiff_t>(tiles.size()))
+            throw std::logic_error("tile_view takes one of the graph's own tiles");
         g.offsets = d_tile_off.as<int>() + ti;
         g.neigh += t.e0;
         g.neigh_types += t.e0;
