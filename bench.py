@@ -48,12 +48,14 @@ PEAK_FP32_TFLOPS = 157.3  # MI355X dense FP32 (matrix and packed vector)
 VALU_FP32_TFLOPS = 78.6   # FP32 VALU without packed FP32 (256 CUs x 4 SIMD x 16 lanes x 2 x 2.4 GHz)
 PEAK_HBM_GBS = 8000.0
 DOMINANT = "r1_reverse"
-# FP32 operations the R1 reverse executes per active edge and channel: the
-# coupled adjoints are contracted once per receiver, leaving per edge
-# T = Y G, s = G h, W = sum_p R T, A = sum_p dR h T, SB = sum_p R s and
-# f = u A + dY SB -- about 380 FMAs (760 flops) per edge-channel at the
-# medium shape (VALU instruction counts of the kernel agree within 5%).
-R1_REVERSE_EXECUTED_FLOPS_PER_EDGE_CHANNEL = {(10, 86, 88): 760}
+# FP32 operations the R1 reverse executes per active edge and channel, all
+# source-group passes of one call: the coupled adjoints are contracted once
+# per receiver, leaving per edge T = Y G, s = G h, W = sum_p R T,
+# A = sum_p dR h T, SB = sum_p R s and f = u A + dY SB.  Measured with the
+# VALU counters (64 x (ADD_F32 + MUL_F32 + 2 FMA_F32) per dispatch over
+# E_active x C; profiles/executed_flops_r1.md), keyed by the model's
+# (paths, coupling terms, rows): medium and wide shapes.
+R1_REVERSE_EXECUTED_FLOPS_PER_EDGE_CHANNEL = {(10, 86, 88): 692.5, (17, 215, 243): 1565.8}
 
 
 def r1_reverse_flops_per_edge_channel(num_paths, num_terms, num_rows):
@@ -510,8 +512,8 @@ def run_config(hip, model_path, system, skin, warmup, steps, timed_steps=False):
             "executed_flops_per_launch": None, "executed_achieved": None, "executed_peak": VALU_FP32_TFLOPS,
             "executed_frac": None}
     if executed:
-        ex = E_active * C * executed
-        roof["executed_flops_per_launch"] = ex
+        ex = E_active * C * executed / per_call
+        roof["executed_flops_per_launch"] = int(ex)
         roof["executed_achieved"] = round(ex / (avg_ms * 1e-3) / 1e12, 3)
         roof["executed_frac"] = round(ex / (avg_ms * 1e-3) / 1e12 / VALU_FP32_TFLOPS, 4)
     out["roofline"] = roof
