@@ -23,6 +23,7 @@
 #include <type_traits>
 
 #include "device_common.hpp"
+#include "harmonic_gradients.hpp"
 #include "edge_kernels.hpp"
 #include "kernels.hpp"
 #include "polynomial.hpp"
@@ -101,8 +102,22 @@ __global__ __launch_bounds__(C) void k_r0_forward(int r0, long long e0, const in
     for (int v = 0; v < NY; ++v) Phi0[(static_cast<std::size_t>(li) * NY + v) * C + k] = acc[v];
 }
 
+// degree l of harmonic index q = l^2 + m
+constexpr int harmonic_degree(int q) {
+    int l = 0;
+    while ((l + 1) * (l + 1) <= q) ++l;
+    return l;
+}
+
 // Layer-1 reverse: node_forces[e] -= sum_k sum_lm Phi0_adj[i,lm,k] H0 (u dR Y + R dY)
-// (records in execution order; each slot's force goes to its edge's row)
+// (records in execution order; each slot's force goes to its edge's row).
+// The gradient term goes through the identity of the records' gradients
+// (harmonic_gradients.hpp): dY^c_q = (sum_q' G[q][c][q'] Y_q' - l u_c Y_q) / r
+// with q' of degree l - 1, so with Q[c][q'] = sum_q Phi0_adj[q] G[q][c][q']
+// formed once per receiver and s_l = sum_m Phi0_adj[lm] Y_lm,
+//   sum_lm Phi0_adj[lm] R_l dY^c_lm = (sum_l R_l sum_q' Y_q' Q[c][q'] - u_c sum_l l R_l s_l) / r,
+// 43 products per edge and channel at l_max 3 instead of 64.  1/r is the
+// trace of the l = 1 gradient block (a tangent projector: trace 2) over 2 sqrt(3).
 template <int C, int LMAX, bool ACCUMULATE>
 __global__ __launch_bounds__(C) void k_r0_reverse(int r0, long long e0, const int* __restrict__ offsets,
                                                   const float* __restrict__ erec, const float* __restrict__ erec_b,
@@ -119,6 +134,22 @@ __global__ __launch_bounds__(C) void k_r0_reverse(int r0, long long e0, const in
     float padj[NY];
 #pragma unroll
     for (int v = 0; v < NY; ++v) padj[v] = Phi0_adj[(static_cast<std::size_t>(li) * NY + v) * C + k];
+    // Q[c][q'] over the harmonics q' of degree < l_max
+    constexpr int NQ = LMAX * LMAX;
+    float qg[3][NQ > 0 ? NQ : 1];
+    static_for<0, 3>([&](auto cc_) {
+        constexpr int c = cc_;
+        static_for<0, NQ>([&](auto qc) {
+            constexpr int qp = qc, d = harmonic_degree(qp);
+            float acc = 0.0f;
+            static_for<0, 2 * d + 3>([&](auto mc) {
+                constexpr int q = (d + 1) * (d + 1) + mc;
+                constexpr double gv = kHarmonicGrad[q][c][qp - d * d];
+                if constexpr (gv != 0.0) acc += padj[q] * static_cast<float>(gv);
+            });
+            qg[c][qp] = acc;
+        });
+    });
     const int ea = offsets[i], eb = offsets[i + 1];
     const stage4* srcF = reinterpret_cast<const stage4*>(erec) + static_cast<std::size_t>(ea - e0) * (S::REC_F / 4);
     const stage4* srcB = reinterpret_cast<const stage4*>(erec_b) + static_cast<std::size_t>(ea - e0) * (S::REC_B / 4);
@@ -141,29 +172,43 @@ __global__ __launch_bounds__(C) void k_r0_reverse(int r0, long long e0, const in
                 const float4* cf = R0c + static_cast<std::size_t>(iv) * NF + k;
                 static_for<0, LMAX + 1>([&](auto lc) { cc[lc] = cf[lc * C]; });
             }
-            // per l: dR_l sum_m adj Y_lm (radial slope) and R_l sum_m adj dY_lm,
-            // the common factor H0[type_j] applied once
+            // per l: s_l = sum_m adj Y_lm and the gradient sums q_c; the
+            // radial factor (dR_l - l R_l / r) of s_l and R_l of q_c, the
+            // common factor H0[type_j] applied once
+            [[maybe_unused]] float rinv = 0.0f;
+            if constexpr (LMAX >= 1)
+                rinv = (rec[S::REC_DY + 1] + rec[S::REC_DY + NY + 2] + rec[S::REC_DY + 2 * NY + 3]) *
+                       static_cast<float>(0.28867513459481287);  // 1 / (2 sqrt 3)
             float a = 0.0f, b0 = 0.0f, b1 = 0.0f, b2 = 0.0f;
             static_for<0, LMAX + 1>([&](auto lc) {
                 constexpr int l = lc;
                 const float4 c4 = cc[l];
                 const float R = spline_value(c4, x, xx, xxx);
                 const float dR = spline_slope(c4, x2, xx3);
-                float sa = 0.0f, s0 = 0.0f, s1 = 0.0f, s2 = 0.0f;
+                float sa = 0.0f;
                 static_for<0, 2 * l + 1>([&](auto mc) {
                     constexpr int lm = l * l + mc;
                     sa += padj[lm] * rec[S::REC_Y + lm];
-                    s0 += padj[lm] * rec[S::REC_DY + lm];
-                    s1 += padj[lm] * rec[S::REC_DY + NY + lm];
-                    s2 += padj[lm] * rec[S::REC_DY + 2 * NY + lm];
                 });
-                a += dR * sa;
-                b0 += R * s0;
-                b1 += R * s1;
-                b2 += R * s2;
+                if constexpr (l == 0) {
+                    a += dR * sa;
+                } else {
+                    a += (dR - static_cast<float>(l) * R * rinv) * sa;
+                    float q0 = 0.0f, q1 = 0.0f, q2 = 0.0f;
+                    static_for<0, 2 * l - 1>([&](auto jc) {
+                        constexpr int qp = (l - 1) * (l - 1) + jc;
+                        const float y = rec[S::REC_Y + qp];
+                        q0 += y * qg[0][qp];
+                        q1 += y * qg[1][qp];
+                        q2 += y * qg[2][qp];
+                    });
+                    b0 += R * q0;
+                    b1 += R * q1;
+                    b2 += R * q2;
+                }
             });
             const float u0 = rec[S::REC_U], u1 = rec[S::REC_U + 1], u2 = rec[S::REC_U + 2];
-            sink.put(j, h0 * (u0 * a + b0), h0 * (u1 * a + b1), h0 * (u2 * a + b2));
+            sink.put(j, h0 * (u0 * a + rinv * b0), h0 * (u1 * a + rinv * b1), h0 * (u2 * a + rinv * b2));
         }
         sink.template flush<ACCUMULATE>(
             n, node_forces, [&](int el) { return __float_as_int(chunk[el * S::REC + S::REC - 1]); });
