@@ -145,3 +145,36 @@ def test_unperturbed_crystal_at_size(medium_model_path, cells):
     _say("max |E_i - site energy| %.2e eV, max |F| %.2e eV/A, max |dS| %.2e eV/A^3" % (de, df, ds))
     assert de < E_TOL and df < F_TOL and ds < S_TOL
     assert abs(total / n - ref["energy"] / len(small["numbers"])) < E_TOL
+
+
+def test_graphs_beyond_32_bit_edge_ids_are_planned_tiled(medium_model_path):
+    """n = 164 unperturbed (2.27B edges): the speed profile, which keeps the
+    direct plan for a graph of 32-bit edge ids, gets the tiled plan with the
+    reason stated; a request pinning a direct plan is refused with the
+    reference's edge limit named."""
+    from symmetrix import systems
+    from symmetrix.mace_kokkos import MACEKokkosFloat
+    system = systems.srtio3_supercell(164, sigma=0.0)
+    pos = np.ascontiguousarray(system["positions"], np.float64).reshape(-1)
+    cell = np.asarray(system["cell"], np.float64)
+    args = (cell.reshape(-1), np.linalg.inv(cell).reshape(-1))
+
+    def prepare(ev):
+        lut = {int(z): i for i, z in enumerate(ev.atomic_numbers)}
+        types = np.array([lut[int(z)] for z in system["numbers"]], np.int32)
+        return ev._prepare_periodic_factorized_graph(types, pos, *args, ev.r_cut + SKIN)
+
+    ev = MACEKokkosFloat(medium_model_path)
+    ev.set_execution_plan_request("speed")
+    g = prepare(ev)
+    report = ev.execution_plan_report
+    _say("speed profile at %d edges: %s (%s)" % (g["num_edges"], report["selected_id"], report["selection_reason"]))
+    assert g["num_edges"] > 2**31
+    assert report["selected_id"] == "mh0-dual-layer-tiled-v1"
+    assert "32-bit edge ids" in report["selection_reason"]
+    ev.close()
+    ev = MACEKokkosFloat(medium_model_path)
+    ev._set_execution_plan_request("direct", "speed", "mh0-direct-speed")
+    with pytest.raises(ValueError, match="2\\^31 - 4096"):
+        prepare(ev)
+    ev.close()
