@@ -274,7 +274,7 @@ def test_energy_forces_stress_irregular(medium_model_path):
 
 def test_energy_forces_stress_wide(wide_model_path):
     """BASELINE configs[4] shape: 256 channels, 0e+1o+2e hidden (L_max 2, 243
-    coupling rows run as three source-component passes), l_max 3,
+    coupling rows run as two source-component passes), l_max 3,
     correlation 3, r_cut 5 A, on a rigid-water box (1,000 molecules, 3,000
     atoms; the config's 30,000-atom box has the same per-atom work)."""
     from symmetrix import systems
