@@ -1030,10 +1030,18 @@ struct Evaluator {
     }
 
     // receiver CSR on the device -> schedule, tiles, plans, workspace, token
-    std::uint64_t finish_graph() {
+    // wide_offsets: the CSR's offsets are the 64-bit d_offsets64 (the device
+    // neighbour list's; d_offsets is absent beyond kMaxEdges edges), else the
+    // 32-bit d_offsets.  d_offsets64 serves the schedule and the host copy
+    // only and is released on the way out, also when a step throws.
+    std::uint64_t finish_graph(bool wide_offsets = false) {
+        struct Release {
+            DevBuf& b;
+            ~Release() { b.release(); }
+        } release_offsets64{d_offsets64};
+        if (!wide_offsets) d_offsets64.release();
         // the plan first: it sets the width of the source transpose
         choose_plan();
-        const bool wide_offsets = d_offsets64.capacity() > 0;
         d_receivers.ensure(std::max<std::int64_t>(E, 1) * sizeof(int));
         d_counts.ensure(std::max(F, 1) * sizeof(int));
         if (wide_offsets)
@@ -1064,8 +1072,6 @@ struct Evaluator {
                 h_offsets.assign(off.begin(), off.end());
             }
         }
-        // the 64-bit offsets serve the schedule and the host copy only
-        d_offsets64.release();
         prepare_pair_tables();
         build_tiles();
         if (hm.field && feature_graph()) build_feature_tile();
@@ -1150,12 +1156,8 @@ struct Evaluator {
     std::uint64_t prepare_graph_host(int n, const int* node_types, const int* num_neigh, std::int64_t num_edges,
                                      const int* neigh, const int* neigh_types, int num_features = -1) {
         require_idle();
-        if (num_features < 0) {
-            num_features = n;
-            h_feature_of.clear();
-            h_feature_types.clear();
-            feature_prepared = false;
-        }
+        const bool plain = num_features < 0;
+        if (plain) num_features = n;
         if (n < 0) throw std::invalid_argument("num_nodes must be non-negative");
         if (num_edges < 0 || num_edges > kMaxEdges)
             throw std::invalid_argument("edge count exceeds the 32-bit graph limit");
@@ -1174,6 +1176,12 @@ struct Evaluator {
                 throw std::invalid_argument("neighbour index is out of range");
             if (neigh_types[e] < 0 || neigh_types[e] >= hm.num_elements)
                 throw std::invalid_argument("neighbour type index is out of range");
+        }
+        invalidate_graph();
+        if (plain) {
+            h_feature_of.clear();
+            h_feature_types.clear();
+            feature_prepared = false;
         }
         N = n;
         F = num_features;
@@ -1241,6 +1249,7 @@ struct Evaluator {
                 throw std::invalid_argument("a neighbour type differs from its feature node's type");
             src[e] = node_of[f];
         }
+        invalidate_graph();
         bool identity = true;
         for (int q = 0; q < nf && identity; ++q) identity = feature_of[q] == q;
         h_feature_types.resize(nf);
@@ -1460,6 +1469,7 @@ struct Evaluator {
     std::uint64_t prepare_graph_checked(int n, const int* node_types, const std::vector<int>& offsets,
                                         std::int64_t num_edges, const int* neigh, const int* neigh_types) {
         require_idle();
+        invalidate_graph();
         N = F = n;
         h_feature_of.clear();
         h_feature_types.clear();
@@ -1488,6 +1498,7 @@ struct Evaluator {
         require_idle();
         if (n < 0) throw std::invalid_argument("num_nodes must be non-negative");
         validate_types(n, node_types);
+        invalidate_graph();
         // release the previous graph's edge arrays first (capacity runs)
         for (DevBuf* b : {&d_neigh, &d_neigh_types, &d_receivers, &d_sedges, &d_sedges64, &d_images, &d_ref_edges,
                           &d_edge_pair})
@@ -1532,8 +1543,15 @@ struct Evaluator {
         geom = Geometry::device_fractional;
         pbc[0] = pbc[1] = pbc[2] = 1;
         h_offsets.clear();
-        const std::uint64_t token = finish_graph();
+        const std::uint64_t token = finish_graph(true);
         return {token, E};
+    }
+
+    // A prepare that has started to replace the graph voids the previous
+    // token first: if it then fails, no call runs on a half-built graph.
+    void invalidate_graph() {
+        generation = 0;
+        evaluated = false;
     }
 
     void check_generation(std::uint64_t token) const {
@@ -2206,6 +2224,9 @@ struct Evaluator {
     }
 
     void lammps_topology(const SmxLammpsArgsV1& a, const LammpsList& L) {
+        // the LAMMPS arrays below are rewritten first: a failure on the way
+        // leaves no topology that a later call could take as current
+        l_generation = 0;
         const int inum = a.inum, nall = a.nall;
         int* nt = static_cast<int*>(l_node_types.ensure(std::max(inum, 1) * sizeof(int)));
         int* nn = static_cast<int*>(l_num_neigh.ensure(std::max(inum, 1) * sizeof(int)));

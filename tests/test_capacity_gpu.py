@@ -178,3 +178,4 @@ def test_graphs_beyond_32_bit_edge_ids_are_planned_tiled(medium_model_path):
     with pytest.raises(ValueError, match="2\\^31 - 4096"):
         prepare(ev)
     ev.close()
+

@@ -510,3 +510,36 @@ def test_atomic_energies_and_active_elements(tiny_model_path, tiny_agnesi_model_
     ag = MACEKokkosFloat(tiny_agnesi_model_path)
     ag.prepare_active_types([1])
     assert ag.active_atomic_numbers == [ag.atomic_numbers[1]]
+
+
+def test_a_failed_prepare_voids_the_previous_token(tiny_field_model_path):
+    """A prepare that fails after it has started to replace the graph (here
+    the plan step: a MACEField model with the tiled plan pinned) leaves no
+    token that runs on the half-replaced graph: the previous token is stale,
+    and a new prepare works."""
+    from symmetrix.mace_kokkos import MACEKokkosFloat
+    s = _system("tiny")
+    ev = MACEKokkosFloat(tiny_field_model_path)
+    lut = {int(z): i for i, z in enumerate(ev.atomic_numbers)}
+    types = np.array([lut[int(z)] for z in s["numbers"]], np.int32)
+    pos = np.ascontiguousarray(s["positions"], np.float64).reshape(-1)
+    cell = np.asarray(s["cell"], np.float64)
+
+    def prepare():
+        return ev._prepare_periodic_factorized_graph(types, pos, cell.reshape(-1), np.linalg.inv(cell).reshape(-1),
+                                                     ev.r_cut + 0.5)["generation"]
+
+    field = np.array([0.1, 0.0, -0.05])
+    g1 = prepare()
+    ev._compute_prepared_factorized_positions_field(g1, pos, field)
+    e1 = np.array(ev.node_energies)
+    ev._set_execution_plan_request("direct", "capacity", "mh0-dual-layer-tiled-v1")
+    with pytest.raises(ValueError, match="field coupling"):
+        prepare()
+    with pytest.raises(ValueError, match="stale"):
+        ev._compute_prepared_factorized_positions_field(g1, pos, field)
+    ev._set_execution_plan_request("direct", "capacity", "")
+    g2 = prepare()
+    ev._compute_prepared_factorized_positions_field(g2, pos, field)
+    np.testing.assert_array_equal(np.array(ev.node_energies), e1)
+    ev.close()
