@@ -162,7 +162,7 @@ class TensorProduct:
             x2 = X2[:, o2:o2 + m2 * d2].reshape(B, m2, d2)
             w = self._w(Wt, B, mode, m1, m2, has_w, off)
             if mode == "uvu":
-                y = np.einsum("buv,ijk,bui,bvj->buk", w, w3j, x1, x2)
+                y = np.einsum("buv,ijk,bui,bvj->buk", w, w3j, x1, x2, optimize=True)
             else:
                 y = np.einsum("bu,ijk,bui,buj->buk", w, w3j, x1, x2)
             Y[:, o3:o3 + m1 * d3] += pw * y.reshape(B, m1 * d3)
@@ -180,13 +180,13 @@ class TensorProduct:
             g = pw * Gm[:, o3:o3 + m1 * d3].reshape(B, m1, d3)
             w = self._w(Wt, B, mode, m1, m2, has_w, off)
             if mode == "uvu":
-                A1[:, o1:o1 + m1 * d1] += np.einsum("buv,ijk,bvj,buk->bui", w, w3j, x2, g).reshape(B, -1)
-                A2[:, o2:o2 + m2 * d2] += np.einsum("buv,ijk,bui,buk->bvj", w, w3j, x1, g).reshape(B, -1)
+                A1[:, o1:o1 + m1 * d1] += np.einsum("buv,ijk,bvj,buk->bui", w, w3j, x2, g, optimize=True).reshape(B, m1 * d1)
+                A2[:, o2:o2 + m2 * d2] += np.einsum("buv,ijk,bui,buk->bvj", w, w3j, x1, g, optimize=True).reshape(B, m2 * d2)
                 if has_w:
-                    AW[:, off:off + m1 * m2] += np.einsum("ijk,bui,bvj,buk->buv", w3j, x1, x2, g).reshape(B, -1)
+                    AW[:, off:off + m1 * m2] += np.einsum("ijk,bui,bvj,buk->buv", w3j, x1, x2, g, optimize=True).reshape(B, m1 * m2)
             else:
-                A1[:, o1:o1 + m1 * d1] += np.einsum("bu,ijk,buj,buk->bui", w, w3j, x2, g).reshape(B, -1)
-                A2[:, o2:o2 + m2 * d2] += np.einsum("bu,ijk,bui,buk->buj", w, w3j, x1, g).reshape(B, -1)
+                A1[:, o1:o1 + m1 * d1] += np.einsum("bu,ijk,buj,buk->bui", w, w3j, x2, g).reshape(B, m1 * d1)
+                A2[:, o2:o2 + m2 * d2] += np.einsum("bu,ijk,bui,buk->buj", w, w3j, x1, g).reshape(B, m2 * d2)
                 if has_w:
                     AW[:, off:off + m1] += np.einsum("ijk,bui,buj,buk->bu", w3j, x1, x2, g)
         return A1, A2, AW
@@ -281,7 +281,7 @@ class Gate:
             Y[:, off:off + x.shape[1]] = self.sc[k] * x * _sigmoid(x)
         for k, mul, d, go, vo, oo in self._segments():
             g = self.gc[k] * _sigmoid(X[:, go:go + mul])
-            Y[:, oo:oo + mul * d] = (g[:, :, None] * X[:, vo:vo + mul * d].reshape(N, mul, d)).reshape(N, -1)
+            Y[:, oo:oo + mul * d] = (g[:, :, None] * X[:, vo:vo + mul * d].reshape(N, mul, d)).reshape(N, mul * d)
         return Y
 
     def reverse(self, X, G):
@@ -296,7 +296,7 @@ class Gate:
             p = _sigmoid(X[:, go:go + mul])
             v = X[:, vo:vo + mul * d].reshape(N, mul, d)
             g = G[:, oo:oo + mul * d].reshape(N, mul, d)
-            A[:, vo:vo + mul * d] = (self.gc[k] * p[:, :, None] * g).reshape(N, -1)
+            A[:, vo:vo + mul * d] = (self.gc[k] * p[:, :, None] * g).reshape(N, mul * d)
             A[:, go:go + mul] = self.gc[k] * p * (1.0 - p) * np.sum(v * g, axis=2)
         return A
 
@@ -338,22 +338,21 @@ class Product:
             a += d
         return F
 
+    _FWD = {1: "mic,nci->ncm", 2: "mijc,nci,ncj->ncm", 3: "mijkc,nci,ncj,nck->ncm"}
+
     def _contract(self, F, elems):
         N = F.shape[0]
         out = np.zeros((N, self.out.dim))
         for (mul, l, _, off), (L, terms) in zip(self.out.blocks, self.contractions):
             acc = np.zeros((N, self.C, 2 * L + 1))
             for nu, coef in enumerate(terms, start=1):
-                c = coef[elems]  # [N, M, i.., C]
-                if nu == 1:
-                    acc += np.einsum("nmic,nci->ncm", c, F)
-                elif nu == 2:
-                    acc += np.einsum("nmijc,nci,ncj->ncm", c, F, F)
-                elif nu == 3:
-                    acc += np.einsum("nmijkc,nci,ncj,nck->ncm", c, F, F, F)
-                else:
+                if nu > 3:
                     raise ValueError("correlation above 3")
-            out[:, off:off + mul * (2 * L + 1)] = acc.reshape(N, -1)
+                for e in np.unique(elems):
+                    sel = elems == e
+                    f = F[sel]
+                    acc[sel] += np.einsum(self._FWD[nu], coef[e], *([f] * nu), optimize=True)
+            out[:, off:off + mul * (2 * L + 1)] = acc.reshape(N, mul * (2 * L + 1))
         return out
 
     def forward(self, X, skip, elems):
@@ -369,20 +368,24 @@ class Product:
         for (mul, l, _, off), (L, terms) in zip(self.out.blocks, self.contractions):
             g = gc[:, off:off + mul * (2 * L + 1)].reshape(N, self.C, 2 * L + 1)
             for nu, coef in enumerate(terms, start=1):
-                c = coef[elems]
-                if nu == 1:
-                    AF += np.einsum("nmic,ncm->nci", c, g)
-                elif nu == 2:
-                    AF += np.einsum("nmijc,ncj,ncm->nci", c, F, g) + np.einsum("nmjic,ncj,ncm->nci", c, F, g)
-                else:
-                    AF += (np.einsum("nmijkc,ncj,nck,ncm->nci", c, F, F, g)
-                           + np.einsum("nmjikc,ncj,nck,ncm->nci", c, F, F, g)
-                           + np.einsum("nmjkic,ncj,nck,ncm->nci", c, F, F, g))
+                for e in np.unique(elems):
+                    sel = elems == e
+                    c, f, gs = coef[e], F[sel], g[sel]
+                    if nu == 1:
+                        a = np.einsum("mic,ncm->nci", c, gs, optimize=True)
+                    elif nu == 2:
+                        a = (np.einsum("mijc,ncj,ncm->nci", c, f, gs, optimize=True)
+                             + np.einsum("mjic,ncj,ncm->nci", c, f, gs, optimize=True))
+                    else:
+                        a = (np.einsum("mijkc,ncj,nck,ncm->nci", c, f, f, gs, optimize=True)
+                             + np.einsum("mjikc,ncj,nck,ncm->nci", c, f, f, gs, optimize=True)
+                             + np.einsum("mjkic,ncj,nck,ncm->nci", c, f, f, gs, optimize=True))
+                    AF[sel] += a
         AX = np.zeros((N, self.inp.dim))
         a = 0
         for mul, l, _, off in self.inp.blocks:
             d = 2 * l + 1
-            AX[:, off:off + mul * d] = AF[:, :, a:a + d].reshape(N, -1)
+            AX[:, off:off + mul * d] = AF[:, :, a:a + d].reshape(N, mul * d)
             a += d
         return AX, (G if self.use_sc else np.zeros_like(G))
 

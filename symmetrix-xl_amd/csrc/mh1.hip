@@ -1,0 +1,1618 @@
+// MH-1 (MACE_Nonlinear) evaluator on MI355X: HIP kernels, the evaluation
+// schedule and the C ABI of include/symmetrix_mh1.h.
+//
+// Reference: libsymmetrix/source/mace_nonlinear.cpp:471-1010 (one
+// compute_node_energies_forces call: harmonics, radial features, per layer
+// the up/residual/skip linears, the conditioned edge MLPs, the "uvu"
+// convolution summed into receivers, the density normalisation, gate,
+// linear_2, product basis; readouts and energies; then the reverse pass to
+// per-edge forces) and its Kokkos form mace_nonlinear_kokkos_impl.tpp.
+//
+// MI355X layout (FP32 arithmetic, FP64 energies and forces):
+// * node rows [N][dim] in the irreps layout of each linear; one thread per
+//   (node, output element) for the linears, which walk the instruction
+//   table of their output block (adjacent threads read adjacent weights and
+//   the same input row);
+// * edge MLPs over tiles of edges in LDS (radial features formed in the
+//   tile, the first layer's embedding columns read as per-type rows); the
+//   reverse re-runs the tile forward and keeps each layer's input in LDS;
+// * the convolution: one thread per (receiver, channel), the receiver's
+//   edges streamed in CSR order, each thread's output components accumulated
+//   in its own LDS column (no atomics: the sum over a receiver's edges is a
+//   sequential loop, so results are run-to-run identical); the reverse
+//   writes per-edge weight adjoints and first-input adjoints, reduces the
+//   harmonic adjoints over the channel lanes with butterflies, and a gather
+//   over the source transpose sums the first-input adjoints per source;
+// * the product basis: one thread per (node, channel) walking the compiled
+//   monomial terms, the channel's angular components in LDS.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <numeric>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../include/symmetrix_mh1.h"
+#include "device_common.hpp"
+#include "harmonics.hpp"
+#include "mh1_model.hpp"
+
+namespace smx {
+void set_last_error(const std::string& message);  // evaluator.cpp
+
+namespace mh1 {
+namespace {
+
+constexpr int kTpThreads = 128;
+constexpr int kMlpThreads = 256;
+constexpr std::size_t kMaxLds = 60 * 1024;
+
+// ------------------------------------------------------------- device views
+
+struct DLinear {
+    int in_dim, out_dim;
+    const int* instr;
+    const int* block_first;
+    const int* elem;
+    const float* W;
+    const float* bias;
+    const float* out_mask;
+    const float* in_mask;
+};
+
+struct DMlp {
+    int num_layers, radial, first_width, num_types, width;
+    const int* layers;
+    const float* eps;
+    const float* params;
+    const float* type_rows;
+};
+
+struct DRadial {
+    int nb, p, apply_cutoff, agnesi, num_types;
+    double prefactor, r_cut, a, q, pp;
+    double bessel[32];
+    const double* r0;  // [type][type] Agnesi length
+};
+
+struct DTp {
+    int channels, in1_dim, out_dim, numel, slots, nin1, num_paths;
+    const int* paths;
+    const int* in1_slot;
+    const int* out_slot;
+    const int* entries;
+    const float* values;
+};
+
+struct DGate {
+    int in_dim, out_dim;
+    const int* out_src;
+    const int* out_gate;
+    const float* out_const;
+    const int* in_kind;
+    const int* in_out;
+    const int* in_aux;
+    const int* in_count;
+    const float* in_const;
+};
+
+struct DProduct {
+    int channels, angular, in_dim, out_dim, out_slots, num_terms;
+    const int* ang_src;
+    const int* out_slot;
+    const int* terms;
+    const float* coef;
+};
+
+struct DZbl {
+    int num_types;
+    const double* pair;  // [type][type][3]: 1/a, bare prefactor, r_max
+    double c[4];
+    int p;
+};
+
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
+
+// ---------------------------------------------------------------- radial
+
+// Bessel features of the (Agnesi-transformed) distance, the polynomial
+// envelope applied when apply_cutoff; value and d/dr (mace_nonlinear.cpp:
+// 383-449), FP64.
+__device__ __forceinline__ void envelope(const DRadial& rd, double r, double& env, double& denv) {
+    const double x = r / rd.r_cut;
+    const double p = rd.p;
+    if (r < rd.r_cut) {
+        const double xp = pow(x, p);
+        env = 1.0 - 0.5 * (p + 1.0) * (p + 2.0) * xp + p * (p + 2.0) * xp * x - 0.5 * p * (p + 1.0) * xp * x * x;
+        const double xm1 = pow(x, p - 1.0);
+        denv = (-0.5 * p * (p + 1.0) * (p + 2.0) * xm1 + p * (p + 1.0) * (p + 2.0) * xp -
+                0.5 * p * (p + 1.0) * (p + 2.0) * xp * x) / rd.r_cut;
+    } else {
+        env = 0.0;
+        denv = 0.0;
+    }
+}
+
+__device__ void radial_eval(const DRadial& rd, double r, int ts, int tt, double* f, double* df, double& env,
+                            double& denv) {
+    envelope(rd, r, env, denv);
+    double t = r, dt = 1.0;
+    if (rd.agnesi) {
+        const double r0 = rd.r0[ts * rd.num_types + tt];
+        const double u = r / r0;
+        const double us = pow(u, rd.q - rd.pp);
+        const double den = 1.0 + us;
+        const double g = rd.a * pow(u, rd.q) / den;
+        const double dg = rd.a * (rd.q * pow(u, rd.q - 1.0) * den - (rd.q - rd.pp) * pow(u, 2.0 * rd.q - rd.pp - 1.0)) /
+                          (den * den);
+        t = 1.0 / (1.0 + g);
+        dt = -dg / (r0 * (1.0 + g) * (1.0 + g));
+    }
+    for (int k = 0; k < rd.nb; ++k) {
+        const double w = rd.bessel[k];
+        double s, c;
+        sincos(w * t, &s, &c);
+        const double base = rd.prefactor * s / t;
+        if (f) f[k] = rd.apply_cutoff ? base * env : base;
+        if (df) {
+            const double db = rd.prefactor * (w * c * t - s) / (t * t) * dt;
+            df[k] = rd.apply_cutoff ? db * env + base * denv : db;
+        }
+    }
+}
+
+// ---------------------------------------------------------------- kernels
+
+template <int LMAX>
+__global__ __launch_bounds__(256) void k_geometry(long long E, const double* __restrict__ xyz,
+                                                  const double* __restrict__ r, const DRadial rd,
+                                                  float* __restrict__ Y, float* __restrict__ cut) {
+    constexpr int NY = (LMAX + 1) * (LMAX + 1);
+    const long long e = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
+    if (e >= E) return;
+    const float d[3] = {static_cast<float>(xyz[3 * e]), static_cast<float>(xyz[3 * e + 1]),
+                        static_cast<float>(xyz[3 * e + 2])};
+    float y[NY], g[3 * NY];
+    edge_harmonics<LMAX>(d, static_cast<float>(r[e]), y, g);
+    for (int q = 0; q < NY; ++q) Y[e * NY + q] = y[q];
+    double env = 0.0, denv = 0.0;
+    envelope(rd, r[e], env, denv);
+    cut[e] = static_cast<float>(env);
+}
+
+// node features of the embedding: one row per type
+__global__ __launch_bounds__(256) void k_embed(int N, int dim, const int* __restrict__ types,
+                                               const float* __restrict__ table, float* __restrict__ out) {
+    const long long t = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
+    if (t >= static_cast<long long>(N) * dim) return;
+    const int n = static_cast<int>(t / dim), j = static_cast<int>(t % dim);
+    out[t] = table[static_cast<std::size_t>(types[n]) * dim + j];
+}
+
+// y = (op(x) + bias) * mask (+ addend) (accumulate: y += ...); one thread per
+// (node, output element).  The instructions of the element's output block are
+// walked in file order (e3nn.cpp:146-166).
+__global__ __launch_bounds__(256) void k_linear(const DLinear op, int N, const float* __restrict__ x,
+                                                float* __restrict__ y, const float* __restrict__ addend,
+                                                int accumulate) {
+    const long long t = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
+    if (t >= static_cast<long long>(N) * op.out_dim) return;
+    const int n = static_cast<int>(t / op.out_dim), j = static_cast<int>(t % op.out_dim);
+    const int b = op.elem[3 * j], w = op.elem[3 * j + 1], m = op.elem[3 * j + 2];
+    const float* xr = x + static_cast<std::size_t>(n) * op.in_dim;
+    float acc = 0.0f;
+    for (int q = op.block_first[b]; q < op.block_first[b + 1]; ++q) {
+        const int* I = op.instr + 6 * q;
+        const int in_off = I[0] + m, mul_in = I[1], d = I[2], mul_out = I[5];
+        const float* Wp = op.W + I[3] + w;
+        if (op.in_mask) {
+            for (int u = 0; u < mul_in; ++u) acc += Wp[u * mul_out] * xr[in_off + u * d] * op.in_mask[in_off + u * d];
+        } else {
+            for (int u = 0; u < mul_in; ++u) acc += Wp[u * mul_out] * xr[in_off + u * d];
+        }
+    }
+    if (op.bias) acc += op.bias[j];
+    if (op.out_mask) acc *= op.out_mask[j];
+    if (addend) acc += addend[t];
+    if (accumulate)
+        y[t] += acc;
+    else
+        y[t] = acc;
+}
+
+__device__ __forceinline__ void mlp_first_inputs(const DRadial& rd, double r, int ts, int tt, float* row) {
+    double f[32], env, denv;
+    radial_eval(rd, r, ts, tt, f, nullptr, env, denv);
+    for (int k = 0; k < rd.nb; ++k) row[k] = static_cast<float>(f[k]);
+}
+
+// One linear layer of an edge tile in LDS: dst[e][j] = b[j] + W[j] . src[e]
+// (layer 0: the per-type rows stand in for the bias and embedding columns).
+__device__ __forceinline__ void mlp_linear_tile(const DMlp& m, int L, int ne, const int* __restrict__ ts,
+                                                const int* __restrict__ tt, const float* src, float* dst,
+                                                float* __restrict__ gout, long long e0) {
+    const int in = m.layers[4 * L + 1], out = m.layers[4 * L + 2], off = m.layers[4 * L + 3];
+    const float* Wt = m.params + off;
+    const float* bias = Wt + static_cast<std::size_t>(out) * in;
+    for (int idx = threadIdx.x; idx < ne * out; idx += blockDim.x) {
+        const int e = idx / out, j = idx % out;
+        float acc;
+        if (L == 0)
+            acc = m.type_rows[static_cast<std::size_t>(ts[e]) * m.first_width + j] +
+                  m.type_rows[static_cast<std::size_t>(m.num_types + tt[e]) * m.first_width + j];
+        else
+            acc = bias[j];
+        const float* s = src + e * m.width;
+        const float* wr = Wt + static_cast<std::size_t>(j) * in;
+        for (int k = 0; k < in; ++k) acc += wr[k] * s[k];
+        if (gout)
+            gout[(e0 + e) * out + j] = acc;
+        else
+            dst[e * m.width + j] = acc;
+    }
+}
+
+__device__ __forceinline__ void mlp_norm_tile(const DMlp& m, int L, int ne, const float* src, float* dst,
+                                              float* stats) {
+    const int w = m.layers[4 * L + 1], off = m.layers[4 * L + 3];
+    const float* g = m.params + off;
+    const float* b = g + w;
+    for (int e = threadIdx.x; e < ne; e += blockDim.x) {
+        const float* s = src + e * m.width;
+        float mean = 0.0f;
+        for (int k = 0; k < w; ++k) mean += s[k];
+        mean /= w;
+        float var = 0.0f;
+        for (int k = 0; k < w; ++k) var += (s[k] - mean) * (s[k] - mean);
+        var /= w;
+        stats[2 * e] = mean;
+        stats[2 * e + 1] = 1.0f / sqrtf(var + m.eps[L]);
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < ne * w; idx += blockDim.x) {
+        const int e = idx / w, j = idx % w;
+        dst[e * m.width + j] = (src[e * m.width + j] - stats[2 * e]) * stats[2 * e + 1] * g[j] + b[j];
+    }
+}
+
+// Forward of an affine MLP over a tile of TE edges per workgroup; out
+// [E][out_dim].  LDS: two activation buffers [TE][width] and [TE][2] stats.
+__global__ __launch_bounds__(kMlpThreads) void k_mlp_forward(const DMlp m, const DRadial rd, long long E, int TE,
+                                                              const double* __restrict__ r,
+                                                              const int* __restrict__ ets,
+                                                              const int* __restrict__ ett, float* __restrict__ out) {
+    extern __shared__ float lds[];
+    float* a = lds;
+    float* b = lds + TE * m.width;
+    float* stats = lds + 2 * TE * m.width;
+    const long long e0 = static_cast<long long>(blockIdx.x) * TE;
+    const int ne = static_cast<int>(min(static_cast<long long>(TE), E - e0));
+    const int* ts = ets + e0;
+    const int* tt = ett + e0;
+    for (int e = threadIdx.x; e < ne; e += blockDim.x) mlp_first_inputs(rd, r[e0 + e], ts[e], tt[e], a + e * m.width);
+    __syncthreads();
+    for (int L = 0; L < m.num_layers; ++L) {
+        const int type = m.layers[4 * L];
+        const bool last = L == m.num_layers - 1;
+        if (type == 0) {
+            mlp_linear_tile(m, L, ne, ts, tt, a, b, last ? out : nullptr, e0);
+            float* t = a;
+            a = b;
+            b = t;
+        } else if (type == 1) {
+            mlp_norm_tile(m, L, ne, a, b, stats);
+            float* t = a;
+            a = b;
+            b = t;
+        } else {
+            const int w = m.layers[4 * L + 1];
+            for (int idx = threadIdx.x; idx < ne * w; idx += blockDim.x) {
+                float* v = a + (idx / w) * m.width + idx % w;
+                *v = *v * sigmoidf_(*v);
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// Reverse of an affine MLP: re-runs the tile forward keeping each layer's
+// input ([num_layers][TE][width] in LDS), then pulls gout [E][out_dim] back
+// to the radial features: rad_adj [E][nb] += d/d(radial).
+__global__ __launch_bounds__(kMlpThreads) void k_mlp_reverse(const DMlp m, const DRadial rd, long long E, int TE,
+                                                              const double* __restrict__ r,
+                                                              const int* __restrict__ ets,
+                                                              const int* __restrict__ ett,
+                                                              const float* __restrict__ gout,
+                                                              float* __restrict__ rad_adj) {
+    extern __shared__ float lds[];
+    const int slab = TE * m.width;
+    float* acts = lds;                                   // [num_layers][TE][width]: input of each layer
+    float* g = lds + m.num_layers * slab;                // adjoint
+    float* h = g + slab;                                 // next adjoint
+    float* stats = h + slab;
+    const long long e0 = static_cast<long long>(blockIdx.x) * TE;
+    const int ne = static_cast<int>(min(static_cast<long long>(TE), E - e0));
+    const int* ts = ets + e0;
+    const int* tt = ett + e0;
+    for (int e = threadIdx.x; e < ne; e += blockDim.x) mlp_first_inputs(rd, r[e0 + e], ts[e], tt[e], acts + e * m.width);
+    __syncthreads();
+    for (int L = 0; L + 1 < m.num_layers; ++L) {
+        const int type = m.layers[4 * L];
+        float* src = acts + L * slab;
+        float* dst = acts + (L + 1) * slab;
+        if (type == 0) {
+            mlp_linear_tile(m, L, ne, ts, tt, src, dst, nullptr, e0);
+        } else if (type == 1) {
+            mlp_norm_tile(m, L, ne, src, dst, stats);
+        } else {
+            const int w = m.layers[4 * L + 1];
+            for (int idx = threadIdx.x; idx < ne * w; idx += blockDim.x) {
+                const float v = src[(idx / w) * m.width + idx % w];
+                dst[(idx / w) * m.width + idx % w] = v * sigmoidf_(v);
+            }
+        }
+        __syncthreads();
+    }
+    // last layer (linear): g[e][k] = sum_o W[o][k] gout[e][o]
+    {
+        const int L = m.num_layers - 1;
+        const int in = m.layers[4 * L + 1], out = m.layers[4 * L + 2], off = m.layers[4 * L + 3];
+        const float* Wt = m.params + off;
+        const int lin = L == 0 ? rd.nb : in;
+        for (int idx = threadIdx.x; idx < ne * lin; idx += blockDim.x) {
+            const int e = idx / lin, k = idx % lin;
+            const float* go = gout + (e0 + e) * out;
+            float acc = 0.0f;
+            for (int o = 0; o < out; ++o) acc += Wt[static_cast<std::size_t>(o) * in + k] * go[o];
+            if (L == 0)
+                rad_adj[(e0 + e) * rd.nb + k] += acc;
+            else
+                g[e * m.width + k] = acc;
+        }
+        __syncthreads();
+    }
+    for (int L = m.num_layers - 2; L >= 0; --L) {
+        const int type = m.layers[4 * L];
+        const float* x = acts + L * slab;
+        if (type == 0) {
+            const int in = m.layers[4 * L + 1], out = m.layers[4 * L + 2], off = m.layers[4 * L + 3];
+            const float* Wt = m.params + off;
+            for (int idx = threadIdx.x; idx < ne * in; idx += blockDim.x) {
+                const int e = idx / in, k = idx % in;
+                float acc = 0.0f;
+                for (int o = 0; o < out; ++o) acc += Wt[static_cast<std::size_t>(o) * in + k] * g[e * m.width + o];
+                if (L == 0)
+                    rad_adj[(e0 + e) * rd.nb + k] += acc;
+                else
+                    h[e * m.width + k] = acc;
+            }
+        } else if (type == 1) {
+            const int w = m.layers[4 * L + 1], off = m.layers[4 * L + 3];
+            const float* gam = m.params + off;
+            for (int e = threadIdx.x; e < ne; e += blockDim.x) {
+                const float* xs = x + e * m.width;
+                float mean = 0.0f;
+                for (int k = 0; k < w; ++k) mean += xs[k];
+                mean /= w;
+                float var = 0.0f;
+                for (int k = 0; k < w; ++k) var += (xs[k] - mean) * (xs[k] - mean);
+                var /= w;
+                const float rs = 1.0f / sqrtf(var + m.eps[L]);
+                float mg = 0.0f, mgx = 0.0f;
+                for (int k = 0; k < w; ++k) {
+                    const float gh = g[e * m.width + k] * gam[k];
+                    mg += gh;
+                    mgx += gh * (xs[k] - mean) * rs;
+                }
+                stats[2 * e] = mg / w;
+                stats[2 * e + 1] = mgx / w;
+            }
+            __syncthreads();
+            for (int idx = threadIdx.x; idx < ne * w; idx += blockDim.x) {
+                const int e = idx / w, k = idx % w;
+                const float* xs = x + e * m.width;
+                float mean = 0.0f;
+                for (int q = 0; q < w; ++q) mean += xs[q];
+                mean /= w;
+                float var = 0.0f;
+                for (int q = 0; q < w; ++q) var += (xs[q] - mean) * (xs[q] - mean);
+                var /= w;
+                const float rs = 1.0f / sqrtf(var + m.eps[L]);
+                const float xh = (xs[k] - mean) * rs;
+                h[e * m.width + k] = rs * (g[e * m.width + k] * gam[k] - stats[2 * e] - xh * stats[2 * e + 1]);
+            }
+        } else {
+            const int w = m.layers[4 * L + 1];
+            for (int idx = threadIdx.x; idx < ne * w; idx += blockDim.x) {
+                const int e = idx / w, k = idx % w;
+                const float v = x[e * m.width + k];
+                const float s = sigmoidf_(v);
+                h[e * m.width + k] = g[e * m.width + k] * (s + v * s * (1.0f - s));
+            }
+        }
+        __syncthreads();
+        float* t = g;
+        g = h;
+        h = t;
+    }
+}
+
+// Convolution into receivers: msg[i][(block, u, k)] = sum over the receiver's
+// edges of pw * w[e][path][u] * sum_ab W3j[a][b][k] up[src][(block1, u, a)]
+// Y[e][l2^2 + b] (e3nn.cpp:343-357), plus the density sum (tanh of the
+// squared density output, mace_nonlinear.cpp:702-708).  Thread per (receiver,
+// channel); the channel's output and first-input components in LDS columns.
+__global__ __launch_bounds__(kTpThreads) void k_tp_forward(const DTp t, int N, const int* __restrict__ offsets,
+                                                            const int* __restrict__ src,
+                                                            const float* __restrict__ up,
+                                                            const float* __restrict__ Y, int NY,
+                                                            const float* __restrict__ wraw,
+                                                            const float* __restrict__ cut,
+                                                            const float* __restrict__ draw,
+                                                            float* __restrict__ msg, float* __restrict__ density) {
+    extern __shared__ float lds[];
+    float* acc = lds;                          // [slots][kTpThreads]
+    float* x1 = lds + t.slots * kTpThreads;    // [nin1][kTpThreads]
+    const int tid = threadIdx.x;
+    const long long gt = blockIdx.x * static_cast<long long>(kTpThreads) + tid;
+    const int i = static_cast<int>(gt / t.channels), u = static_cast<int>(gt % t.channels);
+    if (i >= N) return;
+    for (int s = 0; s < t.slots; ++s) acc[s * kTpThreads + tid] = 0.0f;
+    float dens = 0.0f;
+    for (int e = offsets[i]; e < offsets[i + 1]; ++e) {
+        const float* urow = up + static_cast<std::size_t>(src[e]) * t.in1_dim;
+        for (int q = 0; q < t.nin1; ++q)
+            x1[q * kTpThreads + tid] = urow[t.in1_slot[3 * q] + u * t.in1_slot[3 * q + 1] + t.in1_slot[3 * q + 2]];
+        const float cf = cut ? cut[e] : 1.0f;
+        const float* ye = Y + static_cast<std::size_t>(e) * NY;
+        const float* we = wraw + static_cast<std::size_t>(e) * t.numel;
+        for (int p = 0; p < t.num_paths; ++p) {
+            const int* P = t.paths + 8 * p;
+            const float w = we[P[5] + u] * cf;
+            for (int q = P[6]; q < P[6] + P[7]; ++q) {
+                const int ent = t.entries[q];
+                const int a = ent & 255, b = (ent >> 8) & 255, k = ent >> 16;
+                acc[(P[3] + k) * kTpThreads + tid] += w * t.values[q] * x1[(P[0] + a) * kTpThreads + tid] * ye[P[2] + b];
+            }
+        }
+        const float dr = draw[e];
+        dens += tanhf(dr * dr) * cf;
+    }
+    float* mrow = msg + static_cast<std::size_t>(i) * t.out_dim;
+    for (int s = 0; s < t.slots; ++s)
+        mrow[t.out_slot[3 * s] + u * t.out_slot[3 * s + 1] + t.out_slot[3 * s + 2]] = acc[s * kTpThreads + tid];
+    if (u == 0) density[i] = dens;
+}
+
+// Reverse of the convolution for the receiver's edges (e3nn.cpp:361-407 and
+// mace_nonlinear.cpp:851-900): per edge the weight adjoints (times the cutoff
+// when the cutoff is on the weights), the first-input adjoint rows (gathered
+// per source afterwards), the harmonic adjoints and the cutoff and density
+// adjoints (summed over the channel lanes).
+__global__ __launch_bounds__(kTpThreads) void k_tp_reverse(
+    const DTp t, int N, const int* __restrict__ offsets, const int* __restrict__ src, const float* __restrict__ up,
+    const float* __restrict__ Y, int NY, const float* __restrict__ wraw, const float* __restrict__ cut,
+    const float* __restrict__ draw, const float* __restrict__ amsg, const float* __restrict__ adens,
+    float* __restrict__ wadj, float* __restrict__ a1, float* __restrict__ Yadj, float* __restrict__ cut_adj,
+    float* __restrict__ adraw) {
+    extern __shared__ float lds[];
+    float* g = lds;                               // [slots]
+    float* x1 = g + t.slots * kTpThreads;         // [nin1]
+    float* xa = x1 + t.nin1 * kTpThreads;         // [nin1]
+    float* ya = xa + t.nin1 * kTpThreads;         // [NY]
+    const int tid = threadIdx.x;
+    const long long gt = blockIdx.x * static_cast<long long>(kTpThreads) + tid;
+    const int i = static_cast<int>(gt / t.channels), u = static_cast<int>(gt % t.channels);
+    if (i >= N) return;
+    const float* grow = amsg + static_cast<std::size_t>(i) * t.out_dim;
+    for (int s = 0; s < t.slots; ++s)
+        g[s * kTpThreads + tid] = grow[t.out_slot[3 * s] + u * t.out_slot[3 * s + 1] + t.out_slot[3 * s + 2]];
+    const float ad = adens[i];
+    for (int e = offsets[i]; e < offsets[i + 1]; ++e) {
+        const float* urow = up + static_cast<std::size_t>(src[e]) * t.in1_dim;
+        for (int q = 0; q < t.nin1; ++q) {
+            x1[q * kTpThreads + tid] = urow[t.in1_slot[3 * q] + u * t.in1_slot[3 * q + 1] + t.in1_slot[3 * q + 2]];
+            xa[q * kTpThreads + tid] = 0.0f;
+        }
+        for (int b = 0; b < NY; ++b) ya[b * kTpThreads + tid] = 0.0f;
+        const float cf = cut ? cut[e] : 1.0f;
+        const float* ye = Y + static_cast<std::size_t>(e) * NY;
+        const float* we = wraw + static_cast<std::size_t>(e) * t.numel;
+        float* wa = wadj + static_cast<std::size_t>(e) * t.numel;
+        float cpart = 0.0f;
+        for (int p = 0; p < t.num_paths; ++p) {
+            const int* P = t.paths + 8 * p;
+            const float wr = we[P[5] + u];
+            const float w = wr * cf;
+            float gw = 0.0f;
+            for (int q = P[6]; q < P[6] + P[7]; ++q) {
+                const int ent = t.entries[q];
+                const int a = ent & 255, b = (ent >> 8) & 255, k = ent >> 16;
+                const float vg = t.values[q] * g[(P[3] + k) * kTpThreads + tid];
+                const float xv = x1[(P[0] + a) * kTpThreads + tid];
+                const float yv = ye[P[2] + b];
+                gw += vg * xv * yv;
+                xa[(P[0] + a) * kTpThreads + tid] += vg * w * yv;
+                ya[(P[2] + b) * kTpThreads + tid] += vg * w * xv;
+            }
+            wa[P[5] + u] = gw * cf;
+            cpart += gw * wr;
+        }
+        float* arow = a1 + static_cast<std::size_t>(e) * t.in1_dim;
+        for (int q = 0; q < t.nin1; ++q)
+            arow[t.in1_slot[3 * q] + u * t.in1_slot[3 * q + 1] + t.in1_slot[3 * q + 2]] = xa[q * kTpThreads + tid];
+        // sums over the receiver's channel lanes (aligned groups of t.channels lanes)
+        for (int b = 0; b < NY; ++b) {
+            float v = ya[b * kTpThreads + tid];
+            for (int off = t.channels / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+            if (u == 0) Yadj[static_cast<std::size_t>(e) * NY + b] += v;
+        }
+        for (int off = t.channels / 2; off > 0; off >>= 1) cpart += __shfl_xor(cpart, off, kWave);
+        if (u == 0) {
+            const float dr = draw[e];
+            const float base = tanhf(dr * dr);
+            adraw[e] = ad * (1.0f - base * base) * 2.0f * dr * cf;
+            if (cut_adj) cut_adj[e] += cpart + ad * base;
+        }
+    }
+}
+
+// adjoint rows of the first input, summed per source over the source
+// transpose (deterministic order): aup[s] += sum_e a1[e]
+__global__ __launch_bounds__(256) void k_gather_sources(int N, int dim, const int* __restrict__ t_off,
+                                                        const int* __restrict__ t_edges,
+                                                        const float* __restrict__ a1, float* __restrict__ aup) {
+    const long long t = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
+    if (t >= static_cast<long long>(N) * dim) return;
+    const int s = static_cast<int>(t / dim), c = static_cast<int>(t % dim);
+    float acc = 0.0f;
+    for (int q = t_off[s]; q < t_off[s + 1]; ++q) acc += a1[static_cast<std::size_t>(t_edges[q]) * dim + c];
+    aup[t] += acc;
+}
+
+// pre_gate = lin1 / (alpha + beta * density) + residual (mace_nonlinear.cpp:751-760)
+__global__ __launch_bounds__(256) void k_pregate(int N, int dim, const float* __restrict__ lin1,
+                                                 const float* __restrict__ res, const float* __restrict__ density,
+                                                 float alpha, float beta, float* __restrict__ pre) {
+    const long long t = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
+    if (t >= static_cast<long long>(N) * dim) return;
+    const int n = static_cast<int>(t / dim);
+    pre[t] = lin1[t] / (alpha + beta * density[n]) + res[t];
+}
+
+__global__ __launch_bounds__(256) void k_gate_forward(const DGate gt, int N, const float* __restrict__ x,
+                                                      float* __restrict__ y) {
+    const long long t = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
+    if (t >= static_cast<long long>(N) * gt.out_dim) return;
+    const int n = static_cast<int>(t / gt.out_dim), j = static_cast<int>(t % gt.out_dim);
+    const float* xr = x + static_cast<std::size_t>(n) * gt.in_dim;
+    const float v = xr[gt.out_src[j]];
+    const int gi = gt.out_gate[j];
+    y[t] = gi < 0 ? gt.out_const[j] * v * sigmoidf_(v) : gt.out_const[j] * sigmoidf_(xr[gi]) * v;
+}
+
+// gate adjoint per input element (mace_nonlinear.cpp:103-142)
+__global__ __launch_bounds__(256) void k_gate_reverse(const DGate gt, int N, const float* __restrict__ x,
+                                                      const float* __restrict__ G, float* __restrict__ A) {
+    const long long t = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
+    if (t >= static_cast<long long>(N) * gt.in_dim) return;
+    const int n = static_cast<int>(t / gt.in_dim), i = static_cast<int>(t % gt.in_dim);
+    const float* xr = x + static_cast<std::size_t>(n) * gt.in_dim;
+    const float* gr = G + static_cast<std::size_t>(n) * gt.out_dim;
+    const int kind = gt.in_kind[i], o = gt.in_out[i];
+    const float c = gt.in_const[i];
+    float a;
+    if (kind == 0) {
+        const float v = xr[i], s = sigmoidf_(v);
+        a = gr[o] * c * (s + v * s * (1.0f - s));
+    } else if (kind == 1) {
+        a = gr[o] * c * sigmoidf_(xr[gt.in_aux[i]]);
+    } else {
+        const float s = sigmoidf_(xr[i]);
+        float dot = 0.0f;
+        for (int k = 0; k < gt.in_count[i]; ++k) dot += xr[gt.in_aux[i] + k] * gr[o + k];
+        a = c * s * (1.0f - s) * dot;
+    }
+    A[t] = a;
+}
+
+// a_lin = a_pre / norm, a_dens = -beta / norm^2 sum_j a_pre[j] lin1[j]
+// (mace_nonlinear.cpp:825-834); one wave per node
+__global__ __launch_bounds__(256) void k_norm_reverse(int N, int dim, const float* __restrict__ apre,
+                                                      const float* __restrict__ lin1,
+                                                      const float* __restrict__ density, float alpha, float beta,
+                                                      float* __restrict__ alin, float* __restrict__ adens) {
+    const int lane = threadIdx.x % kWave;
+    const long long n = (blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x) / kWave;
+    if (n >= N) return;
+    const float norm = alpha + beta * density[n];
+    const float* ap = apre + n * dim;
+    const float* l1 = lin1 + n * dim;
+    float dot = 0.0f;
+    for (int j = lane; j < dim; j += kWave) {
+        dot += ap[j] * l1[j];
+        alin[n * dim + j] = ap[j] / norm;
+    }
+    dot = wave_sum<kWave>(dot);
+    if (lane == 0) adens[n] = -dot * beta / (norm * norm);
+}
+
+// Product basis: one thread per (node, channel); the channel's angular
+// components in LDS (the last slot holds 1 for monomials of lower degree).
+__global__ __launch_bounds__(256) void k_product_forward(const DProduct P, int N, const int* __restrict__ elems,
+                                                         const float* __restrict__ X, float* __restrict__ out) {
+    __shared__ float x[17 * 256];
+    __shared__ float o[16 * 256];
+    const int tid = threadIdx.x;
+    const long long t = blockIdx.x * static_cast<long long>(blockDim.x) + tid;
+    if (t >= static_cast<long long>(N) * P.channels) return;
+    const int n = static_cast<int>(t / P.channels), f = static_cast<int>(t % P.channels);
+    const float* xr = X + static_cast<std::size_t>(n) * P.in_dim;
+    for (int a = 0; a < P.angular; ++a)
+        x[a * 256 + tid] = xr[P.ang_src[3 * a] + f * P.ang_src[3 * a + 1] + P.ang_src[3 * a + 2]];
+    x[P.angular * 256 + tid] = 1.0f;
+    for (int s = 0; s < P.out_slots; ++s) o[s * 256 + tid] = 0.0f;
+    const float* cf = P.coef + (static_cast<std::size_t>(elems ? elems[n] : 0) * P.num_terms) * P.channels + f;
+    for (int q = 0; q < P.num_terms; ++q) {
+        const int* T = P.terms + 4 * q;
+        o[T[3] * 256 + tid] += cf[static_cast<std::size_t>(q) * P.channels] * x[T[0] * 256 + tid] *
+                               x[T[1] * 256 + tid] * x[T[2] * 256 + tid];
+    }
+    float* orow = out + static_cast<std::size_t>(n) * P.out_dim;
+    for (int s = 0; s < P.out_slots; ++s)
+        orow[P.out_slot[3 * s] + f * P.out_slot[3 * s + 1] + P.out_slot[3 * s + 2]] = o[s * 256 + tid];
+}
+
+__global__ __launch_bounds__(256) void k_product_reverse(const DProduct P, int N, const int* __restrict__ elems,
+                                                         const float* __restrict__ X, const float* __restrict__ G,
+                                                         float* __restrict__ A) {
+    __shared__ float x[17 * 256];
+    __shared__ float ax[17 * 256];
+    __shared__ float g[16 * 256];
+    const int tid = threadIdx.x;
+    const long long t = blockIdx.x * static_cast<long long>(blockDim.x) + tid;
+    if (t >= static_cast<long long>(N) * P.channels) return;
+    const int n = static_cast<int>(t / P.channels), f = static_cast<int>(t % P.channels);
+    const float* xr = X + static_cast<std::size_t>(n) * P.in_dim;
+    for (int a = 0; a < P.angular; ++a) {
+        x[a * 256 + tid] = xr[P.ang_src[3 * a] + f * P.ang_src[3 * a + 1] + P.ang_src[3 * a + 2]];
+        ax[a * 256 + tid] = 0.0f;
+    }
+    x[P.angular * 256 + tid] = 1.0f;
+    ax[P.angular * 256 + tid] = 0.0f;
+    const float* gr = G + static_cast<std::size_t>(n) * P.out_dim;
+    for (int s = 0; s < P.out_slots; ++s)
+        g[s * 256 + tid] = gr[P.out_slot[3 * s] + f * P.out_slot[3 * s + 1] + P.out_slot[3 * s + 2]];
+    const float* cf = P.coef + (static_cast<std::size_t>(elems ? elems[n] : 0) * P.num_terms) * P.channels + f;
+    for (int q = 0; q < P.num_terms; ++q) {
+        const int* T = P.terms + 4 * q;
+        const float cg = cf[static_cast<std::size_t>(q) * P.channels] * g[T[3] * 256 + tid];
+        const float x0 = x[T[0] * 256 + tid], x1 = x[T[1] * 256 + tid], x2 = x[T[2] * 256 + tid];
+        ax[T[0] * 256 + tid] += cg * x1 * x2;
+        ax[T[1] * 256 + tid] += cg * x0 * x2;
+        ax[T[2] * 256 + tid] += cg * x0 * x1;
+    }
+    float* arow = A + static_cast<std::size_t>(n) * P.in_dim;
+    for (int a = 0; a < P.angular; ++a)
+        arow[P.ang_src[3 * a] + f * P.ang_src[3 * a + 1] + P.ang_src[3 * a + 2]] = ax[a * 256 + tid];
+}
+
+// readout activation: y = c * silu(x); reverse: a = g * c * silu'(x)
+__global__ __launch_bounds__(256) void k_silu_scaled(long long n, float c, const float* __restrict__ x,
+                                                     const float* __restrict__ g, float* __restrict__ y) {
+    const long long t = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
+    if (t >= n) return;
+    const float v = x[t], s = sigmoidf_(v);
+    y[t] = g ? g[t] * c * (s + v * s * (1.0f - s)) : c * v * s;
+}
+
+__global__ __launch_bounds__(256) void k_fill(long long n, float v, float* __restrict__ y) {
+    const long long t = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
+    if (t < n) y[t] = v;
+}
+
+__device__ __forceinline__ void zbl_pair(const DZbl& z, int tu, int tv, double r, double& value, double& grad) {
+    const double* pc = z.pair + 3 * (static_cast<std::size_t>(tu) * z.num_types + tv);
+    const double ia = pc[0], bare_pref = pc[1], rmax = pc[2];
+    if (r >= rmax) {
+        value = grad = 0.0;
+        return;
+    }
+    const double ra = r * ia;
+    const double e0 = z.c[0] * exp(-3.2 * ra), e1 = z.c[1] * exp(-0.9423 * ra), e2 = z.c[2] * exp(-0.4028 * ra),
+                 e3 = z.c[3] * exp(-0.2016 * ra);
+    const double phi = e0 + e1 + e2 + e3;
+    const double dphi = ia * (-3.2 * e0 - 0.9423 * e1 - 0.4028 * e2 - 0.2016 * e3);
+    const double bare = bare_pref / r * phi;
+    const double bare_g = bare_pref / (r * r) * (r * dphi - phi);
+    const double p = z.p, x = r / rmax;
+    const double xm1 = pow(x, p - 1.0), xp = xm1 * x;
+    const double env = 1.0 - (p + 1.0) * (p + 2.0) / 2.0 * xp + p * (p + 2.0) * xp * x - p * (p + 1.0) / 2.0 * xp * x * x;
+    const double denv =
+        (-(p + 1.0) * (p + 2.0) / 2.0 * p * xm1 + p * (p + 2.0) * (p + 1.0) * xp - p * (p + 1.0) / 2.0 * (p + 2.0) * xp * x) /
+        rmax;
+    value = 0.5 * bare * env;
+    grad = 0.5 * (bare * denv + bare_g * env);
+}
+
+// node energies: E_i = e0[type] + scale * sum_layers readout_l(i) + shift (+ scale * ZBL)
+// (mace_nonlinear.cpp:770-781, 1000-1009)
+__global__ __launch_bounds__(256) void k_energies(int N, int num_readouts, const int* __restrict__ types,
+                                                  const double* __restrict__ e0, double scale, double shift,
+                                                  const float* __restrict__ ro, const int* __restrict__ offsets,
+                                                  const int* __restrict__ ets, const double* __restrict__ r,
+                                                  const DZbl z, int has_zbl, double* __restrict__ out) {
+    const int n = blockIdx.x * blockDim.x + threadIdx.x;
+    if (n >= N) return;
+    double s = 0.0;
+    for (int k = 0; k < num_readouts; ++k) s += ro[static_cast<std::size_t>(k) * N + n];
+    double e = e0[types[n]] + scale * s + shift;
+    if (has_zbl) {
+        double zs = 0.0;
+        for (int q = offsets[n]; q < offsets[n + 1]; ++q) {
+            double v, g;
+            zbl_pair(z, types[n], ets[q], r[q], v, g);
+            zs += v;
+        }
+        e += scale * zs;
+    }
+    out[n] = e;
+}
+
+// per-edge forces: -(dE/dr xyz/r + sum_lm dE/dY_lm dY_lm/dxyz) (mace_nonlinear.cpp:983-996)
+template <int LMAX>
+__global__ __launch_bounds__(256) void k_edge_forces(long long E, const double* __restrict__ xyz,
+                                                     const double* __restrict__ r, const DRadial rd,
+                                                     const int* __restrict__ ets, const int* __restrict__ ett,
+                                                     const float* __restrict__ rad_adj,
+                                                     const float* __restrict__ cut_adj,
+                                                     const float* __restrict__ Yadj, const DZbl z, int has_zbl,
+                                                     double scale, double* __restrict__ nf) {
+    constexpr int NY = (LMAX + 1) * (LMAX + 1);
+    const long long e = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
+    if (e >= E) return;
+    const double re = r[e];
+    double df[32], env, denv;
+    radial_eval(rd, re, ets[e], ett[e], nullptr, df, env, denv);
+    double dr = 0.0;
+    for (int k = 0; k < rd.nb; ++k) dr += static_cast<double>(rad_adj[e * rd.nb + k]) * df[k];
+    if (cut_adj) dr += static_cast<double>(cut_adj[e]) * denv;
+    const float d[3] = {static_cast<float>(xyz[3 * e]), static_cast<float>(xyz[3 * e + 1]),
+                        static_cast<float>(xyz[3 * e + 2])};
+    float y[NY], g[3 * NY];
+    edge_harmonics<LMAX>(d, static_cast<float>(re), y, g);
+    double zg = 0.0;
+    if (has_zbl) {
+        double v;
+        zbl_pair(z, ett[e], ets[e], re, v, zg);
+    }
+    for (int c = 0; c < 3; ++c) {
+        double v = (dr + scale * zg) * xyz[3 * e + c] / re;
+        for (int q = 0; q < NY; ++q) v += static_cast<double>(Yadj[e * NY + q]) * g[c * NY + q];
+        nf[3 * e + c] = -v;
+    }
+}
+
+// ----------------------------------------------------------------- host side
+
+inline unsigned blocks_for(long long n, int threads) { return static_cast<unsigned>((n + threads - 1) / threads); }
+
+class Arena {
+public:
+    ~Arena() {
+        if (ptr_) (void)hipFree(ptr_);
+    }
+    void reserve(std::size_t bytes) {
+        if (bytes <= cap_) return;
+        if (ptr_) SMX_HIP(hipFree(ptr_));
+        ptr_ = nullptr;
+        cap_ = 0;
+        if (hipMalloc(&ptr_, bytes) != hipSuccess) {
+            ptr_ = nullptr;
+            throw std::bad_alloc();
+        }
+        cap_ = bytes;
+    }
+    char* base() const { return static_cast<char*>(ptr_); }
+
+private:
+    void* ptr_ = nullptr;
+    std::size_t cap_ = 0;
+};
+
+// carves aligned sub-buffers out of one block (sizes first, then addresses)
+class Layout {
+public:
+    template <class T>
+    std::size_t add(std::size_t count) {
+        off_ = (off_ + 255) & ~static_cast<std::size_t>(255);
+        const std::size_t at = off_;
+        off_ += std::max<std::size_t>(1, count) * sizeof(T);
+        return at;
+    }
+    std::size_t size() const { return off_ + 256; }
+
+private:
+    std::size_t off_ = 0;
+};
+
+struct Timer {
+    bool enabled = false;
+    struct Pending {
+        std::string name;
+        hipEvent_t a, b;
+    };
+    std::vector<Pending> pending;
+    std::vector<std::string> order;
+    std::map<std::string, std::pair<double, long long>> totals;
+    void begin(const char* name, hipStream_t s, hipEvent_t& a) {
+        if (!enabled) return;
+        SMX_HIP(hipEventCreate(&a));
+        SMX_HIP(hipEventRecord(a, s));
+        (void)name;
+    }
+    void end(const char* name, hipStream_t s, hipEvent_t a) {
+        if (!enabled) return;
+        hipEvent_t b;
+        SMX_HIP(hipEventCreate(&b));
+        SMX_HIP(hipEventRecord(b, s));
+        pending.push_back({name, a, b});
+    }
+    void collect() {
+        for (auto& p : pending) {
+            float ms = 0.0f;
+            SMX_HIP(hipEventElapsedTime(&ms, p.a, p.b));
+            auto it = totals.find(p.name);
+            if (it == totals.end()) {
+                order.push_back(p.name);
+                totals[p.name] = {ms, 1};
+            } else {
+                it->second.first += ms;
+                it->second.second += 1;
+            }
+            (void)hipEventDestroy(p.a);
+            (void)hipEventDestroy(p.b);
+        }
+        pending.clear();
+    }
+};
+
+class Evaluator {
+public:
+    Evaluator(const std::string& path, const std::string& head) : model_(Model::load(path, head)) {
+        SMX_HIP(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
+        upload_model();
+    }
+    ~Evaluator() {
+        if (params_) (void)hipFree(params_);
+        if (stream_) (void)hipStreamDestroy(stream_);
+    }
+    const Model& model() const { return model_; }
+    void compute(int N, const int* types, const int* num_neigh, const int* neigh, const int* neigh_types,
+                 const double* xyz, const double* r, long long E);
+    const std::vector<double>& node_energies() const { return energies_; }
+    const std::vector<double>& node_forces() const { return forces_; }
+    std::vector<float> stage(const std::string& name);
+    Timer timer;
+
+private:
+    struct LinearDev {
+        DLinear fwd, rev;
+    };
+    struct InteractionDev {
+        LinearDev up, skip, res, lin1, lin2;
+        DTp tp;
+        DMlp wmlp, dmlp;
+        DGate gate;
+        float alpha, beta;
+    };
+    struct ProductDev {
+        DProduct P;
+        LinearDev lin;
+    };
+    struct ReadoutDev {
+        bool nonlinear;
+        LinearDev l1, l2;
+        float c;
+    };
+
+    void upload_model();
+    void launch_linear(const DLinear& op, int N, const float* x, float* y, const float* addend, bool accumulate,
+                       const char* name);
+    template <class K, class... A>
+    void launch(const char* name, K kernel, unsigned grid, unsigned block, std::size_t lds, A... args) {
+        if (grid == 0) return;
+        hipEvent_t a = nullptr;
+        timer.begin(name, stream_, a);
+        hipLaunchKernelGGL(kernel, dim3(grid), dim3(block), lds, stream_, args...);
+        SMX_LAUNCH_CHECK(name);
+        timer.end(name, stream_, a);
+    }
+
+    Model model_;
+    hipStream_t stream_ = nullptr;
+    void* params_ = nullptr;
+    std::vector<InteractionDev> inter_;
+    std::vector<ProductDev> prod_;
+    std::vector<ReadoutDev> ro_;
+    DRadial rad_{};
+    DZbl zbl_{};
+    const float* embed_table_ = nullptr;
+    const double* atomic_e_ = nullptr;
+    int embed_dim_ = 0;
+    Arena work_;
+    std::vector<double> energies_, forces_;
+    // last call's stage buffers (device) for the debug hook
+    std::map<std::string, std::pair<const float*, std::size_t>> stages_;
+};
+
+// ---- model upload: every table into one device block
+
+struct Packer {
+    std::vector<char> bytes;
+    template <class T>
+    std::size_t put(const std::vector<T>& v) {
+        std::size_t at = (bytes.size() + 255) & ~static_cast<std::size_t>(255);
+        bytes.resize(at + std::max<std::size_t>(1, v.size()) * sizeof(T), 0);
+        if (!v.empty()) std::memcpy(bytes.data() + at, v.data(), v.size() * sizeof(T));
+        return at;
+    }
+};
+
+void Evaluator::upload_model() {
+    Packer pk;
+    struct LinOff {
+        std::size_t instr, bf, elem, W, bias, om, im;
+        bool has_bias, has_om, has_im;
+        int in_dim, out_dim;
+    };
+    auto put_lin = [&](const LinearTables& T) {
+        return LinOff{pk.put(T.instr), pk.put(T.block_first), pk.put(T.elem), pk.put(T.weights), pk.put(T.bias),
+                      pk.put(T.out_mask), pk.put(T.in_mask), !T.bias.empty(), !T.out_mask.empty(),
+                      !T.in_mask.empty(), T.in_dim, T.out_dim};
+    };
+    struct MlpOff {
+        std::size_t layers, eps, params, rows;
+    };
+    auto put_mlp = [&](const MlpTables& T) {
+        return MlpOff{pk.put(T.layers), pk.put(T.eps), pk.put(T.params), pk.put(T.type_rows)};
+    };
+    const Model& M = model_;
+    const int nt = static_cast<int>(M.atomic_numbers.size());
+    // embedding rows per type (FP64 on the host)
+    std::vector<float> table;
+    embed_dim_ = M.embedding.out.dim;
+    for (int t = 0; t < nt; ++t) {
+        const LinearTables& T = M.embedding.fwd;
+        for (int j = 0; j < T.out_dim; ++j) {
+            const int b = T.elem[3 * j], ch = T.elem[3 * j + 1];
+            double acc = 0.0;
+            for (int q = T.block_first[b]; q < T.block_first[b + 1]; ++q) {
+                const int* I = &T.instr[6 * q];
+                for (int u = 0; u < I[1]; ++u)
+                    if (I[0] + u * I[2] == M.model_indices[t]) acc += T.weights[I[3] + u * I[5] + ch];
+            }
+            if (!T.bias.empty()) acc += T.bias[j];
+            if (!T.out_mask.empty()) acc *= T.out_mask[j];
+            table.push_back(static_cast<float>(acc));
+        }
+    }
+    const std::size_t o_table = pk.put(table);
+    const std::size_t o_ae = pk.put(M.atomic_energies);
+    std::vector<double> r0(static_cast<std::size_t>(nt) * nt, 1.0);
+    if (M.agnesi)
+        for (int a = 0; a < nt; ++a)
+            for (int b = 0; b < nt; ++b)
+                r0[a * nt + b] = 0.5 * (M.covalent_radii[M.model_atomic_numbers[M.model_indices[a]]] +
+                                        M.covalent_radii[M.model_atomic_numbers[M.model_indices[b]]]);
+    const std::size_t o_r0 = pk.put(r0);
+    std::vector<double> zpair(static_cast<std::size_t>(nt) * nt * 3, 0.0);
+    if (M.has_zbl)
+        for (int a = 0; a < nt; ++a)
+            for (int b = 0; b < nt; ++b) {
+                const int za = M.atomic_numbers[a], zb = M.atomic_numbers[b];
+                double* pc = &zpair[3 * (static_cast<std::size_t>(a) * nt + b)];
+                pc[0] = (std::pow(static_cast<double>(za), M.zbl_a_exp) + std::pow(static_cast<double>(zb), M.zbl_a_exp)) /
+                        (M.zbl_a_prefactor * 0.529);
+                pc[1] = 14.3996 * static_cast<double>(za * zb);
+                pc[2] = M.zbl_radii[za] + M.zbl_radii[zb];
+            }
+    const std::size_t o_zbl = pk.put(zpair);
+
+    struct InterOff {
+        LinOff up[2], skip[2], res[2], lin1[2], lin2[2];
+        std::size_t tp_paths, tp_in1, tp_out, tp_ent, tp_val;
+        MlpOff w, d;
+        std::size_t g[9];
+    };
+    std::vector<InterOff> io;
+    for (const Interaction& I : M.interactions) {
+        InterOff o{};
+        const Linear* lins[5] = {&I.up, &I.skip, &I.res, &I.lin1, &I.lin2};
+        LinOff* outs[5] = {o.up, o.skip, o.res, o.lin1, o.lin2};
+        for (int k = 0; k < 5; ++k) {
+            outs[k][0] = put_lin(lins[k]->fwd);
+            outs[k][1] = put_lin(lins[k]->rev);
+        }
+        o.tp_paths = pk.put(I.tp.paths);
+        o.tp_in1 = pk.put(I.tp.in1_slot);
+        o.tp_out = pk.put(I.tp.out_slot);
+        o.tp_ent = pk.put(I.tp.entries);
+        o.tp_val = pk.put(I.tp.values);
+        o.w = put_mlp(I.weights_mlp);
+        o.d = put_mlp(I.density_mlp);
+        const GateTables& G = I.gate;
+        o.g[0] = pk.put(G.out_src);
+        o.g[1] = pk.put(G.out_gate);
+        o.g[2] = pk.put(G.out_const);
+        o.g[3] = pk.put(G.in_kind);
+        o.g[4] = pk.put(G.in_out);
+        o.g[5] = pk.put(G.in_aux);
+        o.g[6] = pk.put(G.in_count);
+        o.g[7] = pk.put(G.in_const);
+        io.push_back(o);
+    }
+    struct ProdOff {
+        std::size_t ang, slot, terms, coef;
+        LinOff lin[2];
+    };
+    std::vector<ProdOff> po;
+    for (const ProductTables& P : M.products)
+        po.push_back(ProdOff{pk.put(P.ang_src), pk.put(P.out_slot), pk.put(P.terms), pk.put(P.coef),
+                             {put_lin(P.linear.fwd), put_lin(P.linear.rev)}});
+    std::vector<std::array<LinOff, 4>> roo;
+    for (const Readout& R : M.readouts) {
+        std::array<LinOff, 4> a{};
+        a[0] = put_lin(R.lin1.fwd);
+        a[1] = put_lin(R.lin1.rev);
+        if (R.nonlinear) {
+            a[2] = put_lin(R.lin2.fwd);
+            a[3] = put_lin(R.lin2.rev);
+        }
+        roo.push_back(a);
+    }
+    SMX_HIP(hipMalloc(&params_, pk.bytes.size()));
+    SMX_HIP(hipMemcpy(params_, pk.bytes.data(), pk.bytes.size(), hipMemcpyHostToDevice));
+    char* base = static_cast<char*>(params_);
+    auto F = [&](std::size_t o) { return reinterpret_cast<const float*>(base + o); };
+    auto I_ = [&](std::size_t o) { return reinterpret_cast<const int*>(base + o); };
+    auto lin = [&](const LinOff& o) {
+        return DLinear{o.in_dim, o.out_dim, I_(o.instr), I_(o.bf), I_(o.elem), F(o.W),
+                       o.has_bias ? F(o.bias) : nullptr, o.has_om ? F(o.om) : nullptr, o.has_im ? F(o.im) : nullptr};
+    };
+    auto mlp = [&](const MlpTables& T, const MlpOff& o) {
+        return DMlp{T.num_layers, T.radial, T.first_width, nt, T.max_hidden, I_(o.layers), F(o.eps), F(o.params),
+                    F(o.rows)};
+    };
+    embed_table_ = F(o_table);
+    atomic_e_ = reinterpret_cast<const double*>(base + o_ae);
+    rad_.nb = static_cast<int>(M.bessel.size());
+    rad_.p = M.cutoff_p;
+    rad_.apply_cutoff = M.apply_cutoff ? 1 : 0;
+    rad_.agnesi = M.agnesi ? 1 : 0;
+    rad_.num_types = nt;
+    rad_.prefactor = M.prefactor;
+    rad_.r_cut = M.r_cut;
+    rad_.a = M.agnesi_a;
+    rad_.q = M.agnesi_q;
+    rad_.pp = M.agnesi_p;
+    for (int k = 0; k < rad_.nb; ++k) rad_.bessel[k] = M.bessel[k];
+    rad_.r0 = reinterpret_cast<const double*>(base + o_r0);
+    zbl_.num_types = nt;
+    zbl_.pair = reinterpret_cast<const double*>(base + o_zbl);
+    for (int k = 0; k < 4; ++k) zbl_.c[k] = M.zbl_c[k];
+    zbl_.p = M.zbl_p;
+    for (std::size_t k = 0; k < M.interactions.size(); ++k) {
+        const Interaction& I = M.interactions[k];
+        const InterOff& o = io[k];
+        InteractionDev d{};
+        d.up = {lin(o.up[0]), lin(o.up[1])};
+        d.skip = {lin(o.skip[0]), lin(o.skip[1])};
+        d.res = {lin(o.res[0]), lin(o.res[1])};
+        d.lin1 = {lin(o.lin1[0]), lin(o.lin1[1])};
+        d.lin2 = {lin(o.lin2[0]), lin(o.lin2[1])};
+        d.tp = DTp{I.tp.channels, I.tp.in1_dim, I.tp.out_dim, I.tp.numel, I.tp.slots, I.tp.in1_per_channel,
+                   I.tp.num_paths, I_(o.tp_paths), I_(o.tp_in1), I_(o.tp_out), I_(o.tp_ent), F(o.tp_val)};
+        d.wmlp = mlp(I.weights_mlp, o.w);
+        d.dmlp = mlp(I.density_mlp, o.d);
+        d.gate = DGate{I.gate.in_dim, I.gate.out_dim, I_(o.g[0]), I_(o.g[1]), F(o.g[2]), I_(o.g[3]),
+                       I_(o.g[4]), I_(o.g[5]), I_(o.g[6]), F(o.g[7])};
+        d.alpha = static_cast<float>(I.alpha);
+        d.beta = static_cast<float>(I.beta);
+        inter_.push_back(d);
+    }
+    for (std::size_t k = 0; k < M.products.size(); ++k) {
+        const ProductTables& P = M.products[k];
+        const ProdOff& o = po[k];
+        prod_.push_back(ProductDev{DProduct{P.channels, P.angular, P.in_dim, P.out_dim, P.out_slots, P.num_terms,
+                                            I_(o.ang), I_(o.slot), I_(o.terms), F(o.coef)},
+                                   {lin(o.lin[0]), lin(o.lin[1])}});
+    }
+    for (std::size_t k = 0; k < M.readouts.size(); ++k) {
+        const Readout& R = M.readouts[k];
+        ReadoutDev d{};
+        d.nonlinear = R.nonlinear;
+        d.l1 = {lin(roo[k][0]), lin(roo[k][1])};
+        if (R.nonlinear) d.l2 = {lin(roo[k][2]), lin(roo[k][3])};
+        d.c = static_cast<float>(R.activation_constant);
+        ro_.push_back(d);
+    }
+}
+
+void Evaluator::launch_linear(const DLinear& op, int N, const float* x, float* y, const float* addend,
+                              bool accumulate, const char* name) {
+    launch(name, k_linear, blocks_for(static_cast<long long>(N) * op.out_dim, 256), 256, 0, op, N, x, y, addend,
+           accumulate ? 1 : 0);
+}
+
+int mlp_tile(const DMlp& m, bool reverse) {
+    const std::size_t per_edge = static_cast<std::size_t>(reverse ? m.num_layers + 2 : 2) * m.width * 4 + 8;
+    return static_cast<int>(std::max<std::size_t>(1, std::min<std::size_t>(32, kMaxLds / per_edge)));
+}
+
+std::size_t mlp_lds(const DMlp& m, int TE, bool reverse) {
+    return static_cast<std::size_t>(reverse ? m.num_layers + 2 : 2) * TE * m.width * 4 + 8 * TE;
+}
+
+void Evaluator::compute(int N, const int* types, const int* num_neigh, const int* neigh, const int* neigh_types,
+                        const double* xyz, const double* r, long long E) {
+    const Model& M = model_;
+    const int nt = static_cast<int>(M.atomic_numbers.size());
+    // ---- input checks (mace_nonlinear.cpp:475-521)
+    if (N < 0 || E < 0) throw std::invalid_argument("MH-1: negative node or edge count");
+    if ((N > 0 && (!types || !num_neigh)) || (E > 0 && (!neigh || !neigh_types || !xyz || !r)))
+        throw std::invalid_argument("MH-1: a graph array is NULL");
+    if (E > kMaxEdges) throw std::invalid_argument("MH-1: more than 2^31 edges in one call");
+    long long total = 0;
+    for (int i = 0; i < N; ++i) {
+        if (types[i] < 0 || types[i] >= nt) throw std::invalid_argument("MH-1: node type out of range");
+        if (num_neigh[i] < 0) throw std::invalid_argument("MH-1: negative neighbour count");
+        total += num_neigh[i];
+    }
+    if (total != E) throw std::invalid_argument("MH-1: neighbour counts do not sum to the edge count");
+    for (long long e = 0; e < E; ++e) {
+        if (neigh[e] < 0 || neigh[e] >= N || neigh_types[e] != types[neigh[e]])
+            throw std::invalid_argument("MH-1: edge source out of range or of the wrong type");
+        if (!(r[e] > 0.0) || !std::isfinite(r[e]) || !std::isfinite(xyz[3 * e]) || !std::isfinite(xyz[3 * e + 1]) ||
+            !std::isfinite(xyz[3 * e + 2]))
+            throw std::invalid_argument("MH-1: edge length or vector is not finite and positive");
+    }
+    // ---- host-side graph arrays
+    std::vector<int> offsets(N + 1, 0), tt(E), t_off(N + 1, 0), t_edges(E);
+    for (int i = 0; i < N; ++i) offsets[i + 1] = offsets[i] + num_neigh[i];
+    for (int i = 0; i < N; ++i)
+        for (int e = offsets[i]; e < offsets[i + 1]; ++e) tt[e] = types[i];
+    for (long long e = 0; e < E; ++e) ++t_off[neigh[e] + 1];
+    for (int i = 0; i < N; ++i) t_off[i + 1] += t_off[i];
+    {
+        std::vector<int> fill(t_off.begin(), t_off.end() - 1);
+        for (long long e = 0; e < E; ++e) t_edges[fill[neigh[e]]++] = static_cast<int>(e);
+    }
+    const int NY = M.num_lm, R = static_cast<int>(M.bessel.size());
+    const int L = static_cast<int>(M.interactions.size());
+    // ---- workspace layout
+    Layout lay;
+    const std::size_t o_types = lay.add<int>(N), o_off = lay.add<int>(N + 1), o_src = lay.add<int>(E),
+                      o_ts = lay.add<int>(E), o_tt = lay.add<int>(E), o_toff = lay.add<int>(N + 1),
+                      o_tedge = lay.add<int>(E), o_xyz = lay.add<double>(3 * E), o_r = lay.add<double>(E),
+                      o_Y = lay.add<float>(static_cast<std::size_t>(E) * NY), o_cut = lay.add<float>(E),
+                      o_feat0 = lay.add<float>(static_cast<std::size_t>(N) * embed_dim_);
+    struct LayerOff {
+        std::size_t up, res, skip, msg, dens, lin1, pre, gated, iout, feat, wraw, draw;
+        std::size_t a_feat, contr, a_iout, a_gated, a_pre, a_lin, a_msg, a_up, a_dens, wadj, a1, adraw;
+    };
+    std::vector<LayerOff> lo(L);
+    for (int k = 0; k < L; ++k) {
+        const Interaction& I = M.interactions[k];
+        const std::size_t n = N;
+        LayerOff& o = lo[k];
+        o.up = lay.add<float>(n * I.up.out.dim);
+        o.res = lay.add<float>(n * I.res.out.dim);
+        o.skip = lay.add<float>(n * I.skip.out.dim);
+        o.msg = lay.add<float>(n * I.tp.out_dim);
+        o.dens = lay.add<float>(n);
+        o.lin1 = lay.add<float>(n * I.lin1.out.dim);
+        o.pre = lay.add<float>(n * I.gate.in_dim);
+        o.gated = lay.add<float>(n * I.gate.out_dim);
+        o.iout = lay.add<float>(n * I.lin2.out.dim);
+        o.feat = lay.add<float>(n * M.products[k].out_dim);
+        o.wraw = lay.add<float>(static_cast<std::size_t>(E) * I.tp.numel);
+        o.draw = lay.add<float>(E);
+        o.a_feat = lay.add<float>(n * M.products[k].out_dim);
+        o.contr = lay.add<float>(n * M.products[k].out_dim);
+        o.a_iout = lay.add<float>(n * I.lin2.out.dim);
+        o.a_gated = lay.add<float>(n * I.gate.out_dim);
+        o.a_pre = lay.add<float>(n * I.gate.in_dim);
+        o.a_lin = lay.add<float>(n * I.gate.in_dim);
+        o.a_msg = lay.add<float>(n * I.tp.out_dim);
+        o.a_up = lay.add<float>(n * I.up.out.dim);
+        o.a_dens = lay.add<float>(n);
+        o.wadj = lay.add<float>(static_cast<std::size_t>(E) * I.tp.numel);
+        o.a1 = lay.add<float>(static_cast<std::size_t>(E) * I.tp.in1_dim);
+        o.adraw = lay.add<float>(E);
+    }
+    int ro_width = 1;
+    for (const Readout& ro : M.readouts) ro_width = std::max(ro_width, ro.nonlinear ? ro.lin1.out.dim : 1);
+    const std::size_t o_elems = lay.add<int>(N);
+    const std::size_t o_ro = lay.add<float>(static_cast<std::size_t>(L) * N),
+                      o_h = lay.add<float>(static_cast<std::size_t>(N) * ro_width),
+                      o_act = lay.add<float>(static_cast<std::size_t>(N) * ro_width),
+                      o_ones = lay.add<float>(N), o_radadj = lay.add<float>(static_cast<std::size_t>(E) * R),
+                      o_Yadj = lay.add<float>(static_cast<std::size_t>(E) * NY), o_cadj = lay.add<float>(E),
+                      o_en = lay.add<double>(N), o_nf = lay.add<double>(3 * E);
+    work_.reserve(lay.size());
+    char* W = work_.base();
+    auto f = [&](std::size_t o) { return reinterpret_cast<float*>(W + o); };
+    auto ip = [&](std::size_t o) { return reinterpret_cast<int*>(W + o); };
+    auto dp = [&](std::size_t o) { return reinterpret_cast<double*>(W + o); };
+    auto put = [&](std::size_t o, const void* src, std::size_t bytes) {
+        if (bytes) SMX_HIP(hipMemcpyAsync(W + o, src, bytes, hipMemcpyHostToDevice, stream_));
+    };
+    put(o_types, types, sizeof(int) * N);
+    put(o_off, offsets.data(), sizeof(int) * (N + 1));
+    put(o_src, neigh, sizeof(int) * E);
+    put(o_ts, neigh_types, sizeof(int) * E);
+    put(o_tt, tt.data(), sizeof(int) * E);
+    put(o_toff, t_off.data(), sizeof(int) * (N + 1));
+    put(o_tedge, t_edges.data(), sizeof(int) * E);
+    put(o_xyz, xyz, sizeof(double) * 3 * E);
+    put(o_r, r, sizeof(double) * E);
+    std::vector<int> midx(N);
+    for (int i = 0; i < N; ++i) midx[i] = M.model_indices[types[i]];
+    put(o_elems, midx.data(), sizeof(int) * N);
+    const int* d_types = ip(o_types);
+    const int* d_off = ip(o_off);
+    const int* d_src = ip(o_src);
+    const int* d_ts = ip(o_ts);
+    const int* d_tt = ip(o_tt);
+    const double* d_xyz = dp(o_xyz);
+    const double* d_r = dp(o_r);
+    float* Y = f(o_Y);
+    float* cut = f(o_cut);
+    const unsigned eg = blocks_for(E, 256);
+    switch (M.l_max) {
+        case 0: launch("mh1_geometry", k_geometry<0>, eg, 256, 0, E, d_xyz, d_r, rad_, Y, cut); break;
+        case 1: launch("mh1_geometry", k_geometry<1>, eg, 256, 0, E, d_xyz, d_r, rad_, Y, cut); break;
+        case 2: launch("mh1_geometry", k_geometry<2>, eg, 256, 0, E, d_xyz, d_r, rad_, Y, cut); break;
+        default: launch("mh1_geometry", k_geometry<3>, eg, 256, 0, E, d_xyz, d_r, rad_, Y, cut); break;
+    }
+    const float* cut_w = M.apply_cutoff ? nullptr : cut;
+    float* feats = f(o_feat0);
+    launch("mh1_embed", k_embed, blocks_for(static_cast<long long>(N) * embed_dim_, 256), 256, 0, N, embed_dim_,
+           d_types, embed_table_, feats);
+    stages_.clear();
+    // ---- forward (mace_nonlinear.cpp:583-768)
+    for (int k = 0; k < L; ++k) {
+        const InteractionDev& I = inter_[k];
+        const LayerOff& o = lo[k];
+        const std::string s = std::to_string(k);
+        launch_linear(I.up.fwd, N, feats, f(o.up), nullptr, false, "mh1_linear_up");
+        launch_linear(I.res.fwd, N, f(o.up), f(o.res), nullptr, false, "mh1_linear_res");
+        launch_linear(I.skip.fwd, N, feats, f(o.skip), nullptr, false, "mh1_linear_skip");
+        const int TE = mlp_tile(I.wmlp, false), TD = mlp_tile(I.dmlp, false);
+        launch("mh1_mlp_forward", k_mlp_forward, blocks_for(E, TE), kMlpThreads, mlp_lds(I.wmlp, TE, false), I.wmlp,
+               rad_, E, TE, d_r, d_ts, d_tt, f(o.wraw));
+        launch("mh1_mlp_forward", k_mlp_forward, blocks_for(E, TD), kMlpThreads, mlp_lds(I.dmlp, TD, false), I.dmlp,
+               rad_, E, TD, d_r, d_ts, d_tt, f(o.draw));
+        const std::size_t tp_lds = static_cast<std::size_t>(I.tp.slots + I.tp.nin1) * kTpThreads * 4;
+        launch("mh1_tp_forward", k_tp_forward, blocks_for(static_cast<long long>(N) * I.tp.channels, kTpThreads),
+               kTpThreads, tp_lds, I.tp, N, d_off, d_src, f(o.up), Y, NY, f(o.wraw), cut_w, f(o.draw), f(o.msg),
+               f(o.dens));
+        launch_linear(I.lin1.fwd, N, f(o.msg), f(o.lin1), nullptr, false, "mh1_linear_1");
+        launch("mh1_pregate", k_pregate, blocks_for(static_cast<long long>(N) * I.gate.in_dim, 256), 256, 0, N,
+               I.gate.in_dim, f(o.lin1), f(o.res), f(o.dens), I.alpha, I.beta, f(o.pre));
+        launch("mh1_gate", k_gate_forward, blocks_for(static_cast<long long>(N) * I.gate.out_dim, 256), 256, 0,
+               I.gate, N, f(o.pre), f(o.gated));
+        launch_linear(I.lin2.fwd, N, f(o.gated), f(o.iout), nullptr, false, "mh1_linear_2");
+        const ProductDev& P = prod_[k];
+        const int* elems = M.products[k].agnostic ? nullptr : ip(o_elems);
+        launch("mh1_product_forward", k_product_forward, blocks_for(static_cast<long long>(N) * P.P.channels, 256), 256,
+               0, P.P, N, elems, f(o.iout), f(o.contr));
+        launch_linear(P.lin.fwd, N, f(o.contr), f(o.feat), M.products[k].use_sc ? f(o.skip) : nullptr, false,
+                      "mh1_product_linear");
+        feats = f(o.feat);
+        stages_["up" + s] = {f(o.up), static_cast<std::size_t>(N) * M.interactions[k].up.out.dim};
+        stages_["msg" + s] = {f(o.msg), static_cast<std::size_t>(N) * M.interactions[k].tp.out_dim};
+        stages_["density" + s] = {f(o.dens), static_cast<std::size_t>(N)};
+        stages_["w" + s] = {f(o.wraw), static_cast<std::size_t>(E) * M.interactions[k].tp.numel};
+        stages_["pre_gate" + s] = {f(o.pre), static_cast<std::size_t>(N) * M.interactions[k].gate.in_dim};
+        stages_["interaction_out" + s] = {f(o.iout), static_cast<std::size_t>(N) * M.interactions[k].lin2.out.dim};
+        stages_["features" + s] = {f(o.feat), static_cast<std::size_t>(N) * M.products[k].out_dim};
+    }
+    // ---- readouts and energies
+    float* ro = f(o_ro);
+    for (int k = 0; k < L; ++k) {
+        const ReadoutDev& R_ = ro_[k];
+        const float* x = f(lo[k].feat);
+        if (!R_.nonlinear) {
+            launch_linear(R_.l1.fwd, N, x, ro + static_cast<std::size_t>(k) * N, nullptr, false, "mh1_readout");
+        } else {
+            const long long nh = static_cast<long long>(N) * R_.l1.fwd.out_dim;
+            launch_linear(R_.l1.fwd, N, x, f(o_h), nullptr, false, "mh1_readout");
+            launch("mh1_readout_act", k_silu_scaled, blocks_for(nh, 256), 256, 0, nh, R_.c, f(o_h),
+                   static_cast<const float*>(nullptr), f(o_act));
+            launch_linear(R_.l2.fwd, N, f(o_act), ro + static_cast<std::size_t>(k) * N, nullptr, false, "mh1_readout");
+        }
+    }
+    launch("mh1_energies", k_energies, blocks_for(N, 256), 256, 0, N, L, d_types, atomic_e_, M.scale, M.shift, ro,
+           d_off, d_ts, d_r, zbl_, M.has_zbl ? 1 : 0, dp(o_en));
+    // ---- reverse (mace_nonlinear.cpp:782-1000)
+    const float scale_f = static_cast<float>(M.scale);
+    launch("mh1_fill", k_fill, blocks_for(N, 256), 256, 0, static_cast<long long>(N), scale_f, f(o_ones));
+    for (int k = 0; k < L; ++k) {
+        const ReadoutDev& R_ = ro_[k];
+        float* af = f(lo[k].a_feat);
+        if (!R_.nonlinear) {
+            launch_linear(R_.l1.rev, N, f(o_ones), af, nullptr, false, "mh1_readout_reverse");
+        } else {
+            const long long nh = static_cast<long long>(N) * R_.l1.fwd.out_dim;
+            launch_linear(R_.l1.fwd, N, f(lo[k].feat), f(o_h), nullptr, false, "mh1_readout_reverse");
+            launch_linear(R_.l2.rev, N, f(o_ones), f(o_act), nullptr, false, "mh1_readout_reverse");
+            launch("mh1_readout_act", k_silu_scaled, blocks_for(nh, 256), 256, 0, nh, R_.c, f(o_h), f(o_act), f(o_act));
+            launch_linear(R_.l1.rev, N, f(o_act), af, nullptr, false, "mh1_readout_reverse");
+        }
+    }
+    float* radadj = f(o_radadj);
+    float* Yadj = f(o_Yadj);
+    float* cadj = f(o_cadj);
+    launch("mh1_fill", k_fill, blocks_for(static_cast<long long>(E) * R, 256), 256, 0, static_cast<long long>(E) * R,
+           0.0f, radadj);
+    launch("mh1_fill", k_fill, blocks_for(static_cast<long long>(E) * NY, 256), 256, 0,
+           static_cast<long long>(E) * NY, 0.0f, Yadj);
+    launch("mh1_fill", k_fill, eg, 256, 0, static_cast<long long>(E), 0.0f, cadj);
+    for (int k = L - 1; k >= 0; --k) {
+        const InteractionDev& I = inter_[k];
+        const ProductDev& P = prod_[k];
+        const LayerOff& o = lo[k];
+        const int* elems = M.products[k].agnostic ? nullptr : ip(o_elems);
+        const float* in_feats = k == 0 ? f(o_feat0) : f(lo[k - 1].feat);
+        // product: a_contracted = linear^T(a_feat), then through the contraction
+        float* a_contr = f(o.contr);
+        launch_linear(P.lin.rev, N, f(o.a_feat), a_contr, nullptr, false, "mh1_product_linear_reverse");
+        launch("mh1_product_reverse", k_product_reverse, blocks_for(static_cast<long long>(N) * P.P.channels, 256),
+               256, 0, P.P, N, elems, f(o.iout), a_contr, f(o.a_iout));
+        launch_linear(I.lin2.rev, N, f(o.a_iout), f(o.a_gated), nullptr, false, "mh1_linear_2_reverse");
+        launch("mh1_gate_reverse", k_gate_reverse, blocks_for(static_cast<long long>(N) * I.gate.in_dim, 256), 256, 0,
+               I.gate, N, f(o.pre), f(o.a_gated), f(o.a_pre));
+        launch("mh1_norm_reverse", k_norm_reverse, blocks_for(static_cast<long long>(N) * kWave, 256), 256, 0, N,
+               I.gate.in_dim, f(o.a_pre), f(o.lin1), f(o.dens), I.alpha, I.beta, f(o.a_lin), f(o.a_dens));
+        launch_linear(I.lin1.rev, N, f(o.a_lin), f(o.a_msg), nullptr, false, "mh1_linear_1_reverse");
+        launch_linear(I.res.rev, N, f(o.a_pre), f(o.a_up), nullptr, false, "mh1_linear_res_reverse");
+        const std::size_t tp_lds = static_cast<std::size_t>(I.tp.slots + 2 * I.tp.nin1 + NY) * kTpThreads * 4;
+        launch("mh1_tp_reverse", k_tp_reverse, blocks_for(static_cast<long long>(N) * I.tp.channels, kTpThreads),
+               kTpThreads, tp_lds, I.tp, N, d_off, d_src, f(o.up), Y, NY, f(o.wraw), cut_w, f(o.draw), f(o.a_msg),
+               f(o.a_dens), f(o.wadj), f(o.a1), Yadj, M.apply_cutoff ? nullptr : cadj, f(o.adraw));
+        launch("mh1_gather_sources", k_gather_sources,
+               blocks_for(static_cast<long long>(N) * I.tp.in1_dim, 256), 256, 0, N, I.tp.in1_dim, ip(o_toff),
+               ip(o_tedge), f(o.a1), f(o.a_up));
+        const int TE = mlp_tile(I.wmlp, true), TD = mlp_tile(I.dmlp, true);
+        launch("mh1_mlp_reverse", k_mlp_reverse, blocks_for(E, TE), kMlpThreads, mlp_lds(I.wmlp, TE, true), I.wmlp,
+               rad_, E, TE, d_r, d_ts, d_tt, f(o.wadj), radadj);
+        launch("mh1_mlp_reverse", k_mlp_reverse, blocks_for(E, TD), kMlpThreads, mlp_lds(I.dmlp, TD, true), I.dmlp,
+               rad_, E, TD, d_r, d_ts, d_tt, f(o.adraw), radadj);
+        if (k > 0) {
+            // a_feat[k-1] += up^T(a_up) + skip^T(a_skip), a_skip = a_feat[k] when the product has a skip
+            float* prev = f(lo[k - 1].a_feat);
+            launch_linear(I.up.rev, N, f(o.a_up), prev, nullptr, true, "mh1_linear_up_reverse");
+            if (M.products[k].use_sc)
+                launch_linear(I.skip.rev, N, f(o.a_feat), prev, nullptr, true, "mh1_linear_skip_reverse");
+        }
+        (void)in_feats;
+    }
+    switch (M.l_max) {
+        case 0: launch("mh1_edge_forces", k_edge_forces<0>, eg, 256, 0, E, d_xyz, d_r, rad_, d_ts, d_tt, radadj,
+                       M.apply_cutoff ? static_cast<const float*>(nullptr) : cadj, Yadj, zbl_, M.has_zbl ? 1 : 0,
+                       M.scale, dp(o_nf)); break;
+        case 1: launch("mh1_edge_forces", k_edge_forces<1>, eg, 256, 0, E, d_xyz, d_r, rad_, d_ts, d_tt, radadj,
+                       M.apply_cutoff ? static_cast<const float*>(nullptr) : cadj, Yadj, zbl_, M.has_zbl ? 1 : 0,
+                       M.scale, dp(o_nf)); break;
+        case 2: launch("mh1_edge_forces", k_edge_forces<2>, eg, 256, 0, E, d_xyz, d_r, rad_, d_ts, d_tt, radadj,
+                       M.apply_cutoff ? static_cast<const float*>(nullptr) : cadj, Yadj, zbl_, M.has_zbl ? 1 : 0,
+                       M.scale, dp(o_nf)); break;
+        default: launch("mh1_edge_forces", k_edge_forces<3>, eg, 256, 0, E, d_xyz, d_r, rad_, d_ts, d_tt, radadj,
+                        M.apply_cutoff ? static_cast<const float*>(nullptr) : cadj, Yadj, zbl_, M.has_zbl ? 1 : 0,
+                        M.scale, dp(o_nf)); break;
+    }
+    stages_["Yadj"] = {Yadj, static_cast<std::size_t>(E) * NY};
+    stages_["rad_adj"] = {radadj, static_cast<std::size_t>(E) * R};
+    energies_.resize(N);
+    forces_.resize(3 * E);
+    if (N) SMX_HIP(hipMemcpyAsync(energies_.data(), dp(o_en), sizeof(double) * N, hipMemcpyDeviceToHost, stream_));
+    if (E) SMX_HIP(hipMemcpyAsync(forces_.data(), dp(o_nf), sizeof(double) * 3 * E, hipMemcpyDeviceToHost, stream_));
+    SMX_HIP(hipStreamSynchronize(stream_));
+    timer.collect();
+}
+
+std::vector<float> Evaluator::stage(const std::string& name) {
+    auto it = stages_.find(name);
+    if (it == stages_.end()) throw std::invalid_argument("MH-1: no stage named '" + name + "' in the last call");
+    std::vector<float> out(it->second.second);
+    if (!out.empty())
+        SMX_HIP(hipMemcpyAsync(out.data(), it->second.first, out.size() * sizeof(float), hipMemcpyDeviceToHost,
+                               stream_));
+    SMX_HIP(hipStreamSynchronize(stream_));
+    return out;
+}
+
+template <class F>
+int32_t guarded(F&& fn) {
+    try {
+        fn();
+        return SMX_OK;
+    } catch (const std::bad_alloc&) {
+        set_last_error("out of memory (device or host allocation failed)");
+        return SMX_ERR_OUT_OF_MEMORY;
+    } catch (const std::domain_error& e) {
+        set_last_error(e.what());
+        return SMX_ERR_UNSUPPORTED;
+    } catch (const std::invalid_argument& e) {
+        set_last_error(e.what());
+        return SMX_ERR_INVALID_ARGUMENT;
+    } catch (const std::out_of_range& e) {
+        set_last_error(e.what());
+        return SMX_ERR_INVALID_ARGUMENT;
+    } catch (const std::logic_error& e) {
+        set_last_error(e.what());
+        return SMX_ERR_LOGIC;
+    } catch (const std::exception& e) {
+        set_last_error(e.what());
+        return SMX_ERR_RUNTIME;
+    } catch (...) {
+        set_last_error("unknown error");
+        return SMX_ERR_RUNTIME;
+    }
+}
+
+}  // namespace
+}  // namespace mh1
+}  // namespace smx
+
+struct SmxMh1Evaluator {
+    std::unique_ptr<smx::mh1::Evaluator> impl;
+};
+
+namespace {
+smx::mh1::Evaluator& ev_of(SmxMh1Evaluator* ev) {
+    if (!ev || !ev->impl) throw std::invalid_argument("MH-1 evaluator handle is NULL");
+    return *ev->impl;
+}
+const smx::mh1::Evaluator& ev_of(const SmxMh1Evaluator* ev) {
+    if (!ev || !ev->impl) throw std::invalid_argument("MH-1 evaluator handle is NULL");
+    return *ev->impl;
+}
+}  // namespace
+
+extern "C" {
+
+int32_t smx_mh1_create(const char* model_path, const char* head, SmxMh1Evaluator** out) {
+    return smx::mh1::guarded([&] {
+        if (!model_path || !out) throw std::invalid_argument("model path and output handle are required");
+        *out = nullptr;
+        auto h = std::make_unique<SmxMh1Evaluator>();
+        h->impl = std::make_unique<smx::mh1::Evaluator>(model_path, head ? head : "");
+        *out = h.release();
+    });
+}
+
+void smx_mh1_destroy(SmxMh1Evaluator* ev) { delete ev; }
+
+int32_t smx_mh1_info(const SmxMh1Evaluator* ev, SmxMh1Info* info) {
+    return smx::mh1::guarded([&] {
+        if (!info) throw std::invalid_argument("info is NULL");
+        const smx::mh1::Model& M = ev_of(ev).model();
+        SmxMh1Info v{};
+        v.struct_size = sizeof(SmxMh1Info);
+        v.num_elements = static_cast<int32_t>(M.atomic_numbers.size());
+        v.l_max = M.l_max;
+        v.num_interactions = static_cast<int32_t>(M.interactions.size());
+        v.is_mh1_family = M.family ? 1 : 0;
+        v.node_channels = M.family_node_channels;
+        v.edge_channels = M.family_edge_channels;
+        v.radial_size = M.family_radial;
+        v.has_zbl = M.has_zbl ? 1 : 0;
+        v.r_cut = M.r_cut;
+        *info = v;
+    });
+}
+
+int32_t smx_mh1_family_rejection(const SmxMh1Evaluator* ev, const char** reason) {
+    return smx::mh1::guarded([&] {
+        if (!reason) throw std::invalid_argument("reason is NULL");
+        *reason = ev_of(ev).model().family_rejection.c_str();
+    });
+}
+
+int32_t smx_mh1_atomic_numbers(const SmxMh1Evaluator* ev, int32_t* out, int32_t capacity) {
+    int32_t n = 0;
+    const int32_t rc = smx::mh1::guarded([&] {
+        const auto& z = ev_of(ev).model().atomic_numbers;
+        n = static_cast<int32_t>(z.size());
+        for (int32_t i = 0; out && i < std::min(n, capacity); ++i) out[i] = z[i];
+    });
+    return rc ? rc : n;
+}
+
+int32_t smx_mh1_atomic_energies(const SmxMh1Evaluator* ev, double* out, int32_t capacity) {
+    int32_t n = 0;
+    const int32_t rc = smx::mh1::guarded([&] {
+        const auto& e = ev_of(ev).model().atomic_energies;
+        n = static_cast<int32_t>(e.size());
+        for (int32_t i = 0; out && i < std::min(n, capacity); ++i) out[i] = e[i];
+    });
+    return rc ? rc : n;
+}
+
+int32_t smx_mh1_selected_head(const SmxMh1Evaluator* ev, const char** name) {
+    return smx::mh1::guarded([&] {
+        if (!name) throw std::invalid_argument("name is NULL");
+        *name = ev_of(ev).model().selected_head.c_str();
+    });
+}
+
+int32_t smx_mh1_compute_node_energies_forces(SmxMh1Evaluator* ev, int32_t num_nodes, const int32_t* node_types,
+                                             const int32_t* num_neigh, const int32_t* neigh_indices,
+                                             const int32_t* neigh_types, const double* xyz, const double* r,
+                                             int64_t num_edges) {
+    return smx::mh1::guarded([&] {
+        ev_of(ev).compute(num_nodes, node_types, num_neigh, neigh_indices, neigh_types, xyz, r, num_edges);
+    });
+}
+
+int32_t smx_mh1_node_energies(SmxMh1Evaluator* ev, double* out, int64_t capacity) {
+    return smx::mh1::guarded([&] {
+        const auto& v = ev_of(ev).node_energies();
+        if (v.empty()) return;
+        if (!out || capacity < static_cast<int64_t>(v.size())) throw std::invalid_argument("output buffer too small");
+        std::copy(v.begin(), v.end(), out);
+    });
+}
+
+int32_t smx_mh1_node_forces(SmxMh1Evaluator* ev, double* out, int64_t capacity) {
+    return smx::mh1::guarded([&] {
+        const auto& v = ev_of(ev).node_forces();
+        if (v.empty()) return;
+        if (!out || capacity < static_cast<int64_t>(v.size())) throw std::invalid_argument("output buffer too small");
+        std::copy(v.begin(), v.end(), out);
+    });
+}
+
+int32_t smx_mh1_debug_stage(SmxMh1Evaluator* ev, const char* name, float* out, int64_t capacity, int64_t* count) {
+    return smx::mh1::guarded([&] {
+        if (!name) throw std::invalid_argument("stage name is NULL");
+        const std::vector<float> v = ev_of(ev).stage(name);
+        if (count) *count = static_cast<int64_t>(v.size());
+        if (out) std::copy(v.begin(), v.begin() + std::min<int64_t>(capacity, static_cast<int64_t>(v.size())), out);
+    });
+}
+
+int32_t smx_mh1_set_kernel_timing(SmxMh1Evaluator* ev, int32_t enabled) {
+    return smx::mh1::guarded([&] {
+        auto& t = ev_of(ev).timer;
+        t.enabled = enabled != 0;
+        t.totals.clear();
+        t.order.clear();
+    });
+}
+
+int32_t smx_mh1_kernel_timing(SmxMh1Evaluator* ev, int32_t index, const char** name, double* total_ms,
+                              int64_t* launches) {
+    int32_t n = 0;
+    const int32_t rc = smx::mh1::guarded([&] {
+        auto& t = ev_of(ev).timer;
+        n = static_cast<int32_t>(t.order.size());
+        if (index >= 0 && index < n) {
+            const std::string& k = t.order[index];
+            if (name) *name = k.c_str();
+            if (total_ms) *total_ms = t.totals[k].first;
+            if (launches) *launches = t.totals[k].second;
+        }
+    });
+    return rc ? rc : n;
+}
+
+}  // extern "C"

@@ -69,6 +69,13 @@ class SmxEvaluatorCounters(ctypes.Structure):
                 ("geometry_prepare_count", ctypes.c_int64)]
 
 
+class SmxMh1Info(ctypes.Structure):
+    _fields_ = [("struct_size", ctypes.c_uint32), ("num_elements", ctypes.c_int32), ("l_max", ctypes.c_int32),
+                ("num_interactions", ctypes.c_int32), ("is_mh1_family", ctypes.c_int32),
+                ("node_channels", ctypes.c_int32), ("edge_channels", ctypes.c_int32),
+                ("radial_size", ctypes.c_int32), ("has_zbl", ctypes.c_int32), ("r_cut", ctypes.c_double)]
+
+
 class SmxLammpsArgsV2(ctypes.Structure):
     """SmxLammpsArgsV1 followed by the caller's hipStream_t: the call waits
     for the work the caller queued there instead of synchronising the device."""
@@ -162,6 +169,20 @@ SIGNATURES = [
     ("smx_r1_plugin_reverse_launch_noalloc", _i32, [_vp, _vp, _vp, _vp, _i32]),
     ("smx_model_array_f32", _i32, [_cp, _cp, _vp, _i64, _p_i64, _p_i32, _p_dbl, _p_dbl]),
     ("smx_model_array_i32", _i32, [_cp, _cp, _vp, _i64, _p_i64, _p_i32]),
+    # MH-1 (MACE_Nonlinear), include/symmetrix_mh1.h
+    ("smx_mh1_create", _i32, [_cp, _cp, ctypes.POINTER(_vp)]),
+    ("smx_mh1_destroy", None, [_vp]),
+    ("smx_mh1_info", _i32, [_vp, ctypes.POINTER(SmxMh1Info)]),
+    ("smx_mh1_family_rejection", _i32, [_vp, ctypes.POINTER(_cp)]),
+    ("smx_mh1_atomic_numbers", _i32, [_vp, _vp, _i32]),
+    ("smx_mh1_atomic_energies", _i32, [_vp, _vp, _i32]),
+    ("smx_mh1_selected_head", _i32, [_vp, ctypes.POINTER(_cp)]),
+    ("smx_mh1_compute_node_energies_forces", _i32, [_vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _i64]),
+    ("smx_mh1_node_energies", _i32, [_vp, _vp, _i64]),
+    ("smx_mh1_node_forces", _i32, [_vp, _vp, _i64]),
+    ("smx_mh1_debug_stage", _i32, [_vp, _cp, _vp, _i64, _p_i64]),
+    ("smx_mh1_set_kernel_timing", _i32, [_vp, _i32]),
+    ("smx_mh1_kernel_timing", _i32, [_vp, _i32, ctypes.POINTER(_cp), _p_dbl, _p_i64]),
 ]
 
 

@@ -225,7 +225,7 @@ def product(rng, l_max, C, out_blocks, correlation):
             T = _u_tensor(l_max, L, nu)
             us.append(_tensor(T, list(T.shape)))
             K = T.shape[-1]
-            ws[nu] = _tensor(rng.normal(size=(1, K, C)) / math.sqrt(max(K, 1)) * (0.6 ** (nu - 1)), [1, K, C])
+            ws[nu] = _tensor(rng.normal(size=(1, K, C)) / math.sqrt(max(K, 1)) * (0.35 ** (nu - 1)), [1, K, C])
         contractions.append({"correlation": correlation,
                              "weights": [ws[nu] for nu in range(correlation - 1, 0, -1)],
                              "weights_max": ws[correlation], "u_tensors": us})
@@ -266,7 +266,8 @@ def interaction(rng, cfg, layer, num_elements):
             "linear_up": linear(rng, node, edge, bias=cfg.linear_bias),
             "skip_tp": linear(rng, node, hidden),
             "linear_res": linear(rng, edge, gate_in),
-            "linear_1": linear(rng, msg_blocks, gate_in, scale=0.5),
+            # messages sum over ~20-70 neighbours: keep the pre-gate values O(1)
+            "linear_1": linear(rng, msg_blocks, gate_in, scale=0.15),
             "linear_2": linear(rng, full, full),
             "conv_tp": tp,
             "conv_tp_weights": affine_mlp(rng, [cond] + list(cfg.radial_hidden) + [numel]),
@@ -336,7 +337,7 @@ def cached_mh1(config, seed=None, directory=None):
     seed = cfg.seed if seed is None else seed
     directory = directory or os.environ.get("SYMMETRIX_MODEL_CACHE", "/tmp/symmetrix_models")
     os.makedirs(directory, exist_ok=True)
-    path = os.path.join(directory, "%s_seed%d_v1.json" % (cfg.name, seed))
+    path = os.path.join(directory, "%s_seed%d_v2.json" % (cfg.name, seed))
     if not os.path.exists(path):
         write_mh1(cfg, path, seed)
     return path

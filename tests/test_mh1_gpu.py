@@ -1,0 +1,175 @@
+"""MH-1 (MACE_Nonlinear) on the GPU against the float64 oracle
+(oracle/mh1_oracle.py, pinned in tests/test_mh1_oracle.py).
+
+The HIP path runs in FP32; the bars are the north star's: energy 1e-5
+eV/atom, forces 1e-4 eV/A, stress 1e-6 eV/A^3, with the reference's own
+MH-1 float32 comparisons (test_mh1.py:429-463, 1e-3 absolute on generated
+float32 paths) far looser.  Models: cutoff on the features (l_max 2 and 3),
+cutoff on the weights with Agnesi distances, a linear bias and ZBL, and the
+64/32-channel l_max-3 member.  Stage checks (up-projection, messages,
+density, layer features, edge weights) localise a failure.
+"""
+
+import numpy as np
+import pytest
+
+from oracle import mh1_oracle as mo
+from oracle import oracle
+from symmetrix import random_mh1, systems
+
+pytestmark = pytest.mark.gpu
+
+TINY = ["mh1_tiny", "mh1_tiny_l3", "mh1_tiny_raw"]
+
+
+@pytest.fixture(scope="module")
+def paths(tmp_path_factory):
+    d = str(tmp_path_factory.mktemp("mh1gpu"))
+    return {n: random_mh1.cached_mh1(n, directory=d) for n in TINY + ["mh1_medium"]}
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def _random_system(model, n, L, seed, min_dist=1.2):
+    rng = np.random.default_rng(seed)
+    pos = np.zeros((n, 3))
+    for i in range(n):
+        while True:
+            p = rng.random(3) * L
+            d = pos[:i] - p
+            d -= L * np.rint(d / L)
+            if i == 0 or np.min(np.linalg.norm(d, axis=1)) > min_dist:
+                pos[i] = p
+                break
+    nums = rng.choice(model.atomic_numbers, n)
+    return pos, np.eye(3) * L, model.types_of(nums)
+
+
+def _graph(model, pos, cell):
+    g = oracle.neighbor_graph(pos, cell, model.r_cut)
+    xyz, r = oracle.prepared_geometry(g, cell, pos, pos, 1e3)
+    return g, xyz, r
+
+
+def _gpu(path, types, g, xyz, r):
+    from symmetrix.mace_nonlinear import MACENonlinearKokkosFloat
+    ev = MACENonlinearKokkosFloat(path)
+    src = g["sources"]
+    ev.compute_node_energies_forces(len(types), types, g["num_neigh"], src, types[src], xyz, r)
+    return ev, ev.node_energies, ev.node_forces.reshape(-1, 3)
+
+
+def _compare(model, path, pos, cell, types, stages=False):
+    g, xyz, r = _graph(model, pos, cell)
+    n = len(types)
+    _say("mh1 case: %s, %d atoms, %d edges" % (path.split("/")[-1], n, len(r)))
+    e_ref, f_ref = model.evaluate(types, g["receivers"], g["sources"], xyz)
+    ev, e, f = _gpu(path, types, g, xyz, r)
+    vol = abs(np.linalg.det(cell))
+    F = mo.reduce_forces(n, g["receivers"], g["sources"], f)
+    F_ref = mo.reduce_forces(n, g["receivers"], g["sources"], f_ref)
+    S = mo.reduce_stress(f, xyz, vol)
+    S_ref = mo.reduce_stress(f_ref, xyz, vol)
+    de = abs(e.sum() - e_ref.sum()) / n
+    dn = np.abs(e - e_ref).max()
+    dF = np.abs(F - F_ref).max()
+    dS = np.abs(S - S_ref).max()
+    _say("  |dE|/atom %.2e  max|dE_i| %.2e  max|dF| %.2e (|F| %.2f)  max|dS| %.2e" %
+         (de, dn, dF, np.abs(F_ref).max(), dS))
+    if stages:
+        st = model.stages["states"]
+        for k in range(len(st)):
+            for name, ref in (("up", st[k]["up"]), ("msg", st[k]["msg"]), ("density", st[k]["density"]),
+                              ("w", st[k]["wraw"]), ("features", model.stages["layer_features"][k])):
+                got = ev._stage("%s%d" % (name, k)).reshape(np.shape(ref))
+                err = np.abs(got - ref).max() / max(1.0, np.abs(ref).max())
+                _say("  stage %s%d: scaled max err %.2e" % (name, k, err))
+                assert err < 2e-5, (name, k, err)
+    assert de < 1e-5
+    assert dn < 1e-4
+    assert dF < 1e-4
+    assert dS < 1e-6
+    return ev
+
+
+@pytest.mark.parametrize("name", TINY)
+def test_mh1_matches_oracle(paths, name):
+    model = mo.MH1Oracle(paths[name])
+    pos, cell, types = _random_system(model, 40, 8.0, seed=3)
+    _compare(model, paths[name], pos, cell, types, stages=True)
+
+
+def test_mh1_medium_member_matches_oracle(paths):
+    model = mo.MH1Oracle(paths["mh1_medium"])
+    s = systems.irregular_box(120, seed=2)
+    pos, cell = np.asarray(s["positions"]), np.asarray(s["cell"])
+    _compare(model, paths["mh1_medium"], pos, cell, model.types_of(s["numbers"]))
+
+
+def test_mh1_repeat_calls_and_graph_changes(paths):
+    """Two calls on one evaluator (workspace reuse, a smaller second graph),
+    then the first graph again: identical results."""
+    path = paths["mh1_tiny"]
+    model = mo.MH1Oracle(path)
+    pos, cell, types = _random_system(model, 40, 8.0, seed=5)
+    g, xyz, r = _graph(model, pos, cell)
+    from symmetrix.mace_nonlinear import MACENonlinearKokkosFloat
+    ev = MACENonlinearKokkosFloat(path)
+    src = g["sources"]
+    ev.compute_node_energies_forces(len(types), types, g["num_neigh"], src, types[src], xyz, r)
+    e1, f1 = ev.node_energies.copy(), ev.node_forces.copy()
+    pos2, cell2, types2 = _random_system(model, 12, 6.0, seed=6)
+    g2, xyz2, r2 = _graph(model, pos2, cell2)
+    ev.compute_node_energies_forces(len(types2), types2, g2["num_neigh"], g2["sources"], types2[g2["sources"]],
+                                    xyz2, r2)
+    e_ref, _ = model.evaluate(types2, g2["receivers"], g2["sources"], xyz2)
+    assert np.abs(ev.node_energies - e_ref).max() < 1e-4
+    ev.compute_node_energies_forces(len(types), types, g["num_neigh"], src, types[src], xyz, r)
+    assert np.array_equal(ev.node_energies, e1) and np.array_equal(ev.node_forces, f1)
+
+
+def test_mh1_isolated_atoms_and_empty_graph(paths):
+    """Atoms without neighbours get their atomic energy plus the readouts of
+    the embedding alone; an empty graph is valid."""
+    path = paths["mh1_tiny"]
+    model = mo.MH1Oracle(path)
+    types = np.array([0, 1, 2], dtype=np.int32)
+    empty = np.zeros((0, 3))
+    from symmetrix.mace_nonlinear import MACENonlinearKokkosFloat
+    ev = MACENonlinearKokkosFloat(path)
+    ev.compute_node_energies_forces(3, types, np.zeros(3, np.int32), np.zeros(0, np.int32),
+                                    np.zeros(0, np.int32), empty, np.zeros(0))
+    e_ref, _ = model.evaluate(types, np.zeros(0, np.int64), np.zeros(0, np.int64), empty)
+    assert np.abs(ev.node_energies - e_ref).max() < 1e-5
+    assert ev.node_forces.size == 0
+
+
+def test_mh1_rejects_bad_graphs(paths):
+    from symmetrix.mace_nonlinear import MACENonlinearKokkosFloat
+    ev = MACENonlinearKokkosFloat(paths["mh1_tiny"])
+    t = np.array([0, 1], dtype=np.int32)
+    xyz = np.array([[1.0, 0.0, 0.0], [-1.0, 0.0, 0.0]])
+    r = np.ones(2)
+    ok = dict(num_nodes=2, node_types=t, num_neigh=[1, 1], neigh_indices=[1, 0], neigh_types=[1, 0], xyz=xyz, r=r)
+    ev.compute_node_energies_forces(**ok)
+    for bad in (dict(neigh_types=[0, 0]), dict(neigh_indices=[2, 0]), dict(num_neigh=[2, 1]),
+                dict(r=np.array([1.0, np.nan])), dict(node_types=np.array([0, 9], np.int32))):
+        args = dict(ok)
+        args.update(bad)
+        with pytest.raises(ValueError):
+            ev.compute_node_energies_forces(**args)
+    # the evaluator still works after the refusals
+    ev.compute_node_energies_forces(**ok)
+    assert np.all(np.isfinite(ev.node_energies))
+
+
+def test_mh1_family_facts(paths):
+    from symmetrix.mace_nonlinear import MACENonlinearKokkosFloat
+    ev = MACENonlinearKokkosFloat(paths["mh1_medium"])
+    assert ev.is_mh1_family and ev.mh1_family_rejection_reason == ""
+    assert (ev.mh1_node_channels, ev.mh1_edge_channels, ev.mh1_radial_size, ev.mh1_l_max) == (64, 32, 8, 3)
+    assert ev.atomic_numbers == [1, 6, 7, 8, 13, 14, 22, 26, 29, 38]
+    model = mo.MH1Oracle(paths["mh1_medium"])
+    assert np.allclose(ev.atomic_energies, model.atomic_energies)
