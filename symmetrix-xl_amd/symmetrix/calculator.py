@@ -46,6 +46,7 @@ from dataclasses import dataclass
 import numpy as np
 
 from .mace_kokkos import MACEKokkosFloat
+from .mace_nonlinear import MACENonlinearKokkosFloat, is_nonlinear_model
 from .neighbors import neighbor_list_ijS
 
 log = logging.getLogger(__name__)
@@ -191,12 +192,21 @@ class Symmetrix(_Base):
             required = "speed" if _debug_execution_plan == "mh0-direct-speed" else "capacity"
             if execution_profile != required:
                 raise ValueError("%s requires execution_profile=%r." % (_debug_execution_plan, required))
-        self.evaluator = MACEKokkosFloat(model_file, head or "")
-        self.streamed_edges = "direct"
+        # MH-1 files dispatch on model_type (calculator.py:1093-1126; test_mh1.py:2678)
+        self._nonlinear = is_nonlinear_model(model_file)
+        if self._nonlinear:
+            if allow_fixed_workspace or _debug_execution_plan is not None:
+                raise ValueError("MACE_Nonlinear models have no fixed-workspace or debug execution plans.")
+            self.evaluator = MACENonlinearKokkosFloat(model_file, head or "")
+            self.streamed_edges = "generic"
+        else:
+            self.evaluator = MACEKokkosFloat(model_file, head or "")
+            self.streamed_edges = "direct"
         self.execution_profile = execution_profile
         self.allow_fixed_workspace = allow_fixed_workspace
-        self.evaluator._set_allow_fixed_workspace(allow_fixed_workspace)
-        self.evaluator._set_execution_plan_request("direct", execution_profile, _debug_execution_plan or "")
+        if not self._nonlinear:
+            self.evaluator._set_allow_fixed_workspace(allow_fixed_workspace)
+            self.evaluator._set_execution_plan_request("direct", execution_profile, _debug_execution_plan or "")
         self.cutoff = float(self.evaluator.r_cut)
         self.neighbor_skin = float(neighbor_skin)
         self._types = {z: i for i, z in enumerate(self.evaluator.atomic_numbers)}
@@ -248,6 +258,8 @@ class Symmetrix(_Base):
 
     @property
     def execution_plan(self):
+        if self._nonlinear:
+            return {"selected_id": "mh1-generic", "streamed_edges": "generic"}
         return self.evaluator.execution_plan_report
 
     # -------------------------------------------------------------- graph
@@ -287,7 +299,7 @@ class Symmetrix(_Base):
         return "reuse"
 
     def _fixed_workspace_plan_selected(self):
-        return self.evaluator.execution_plan_report.get("selected_id") in TILED_PLANS
+        return (not self._nonlinear) and self.evaluator.execution_plan_report.get("selected_id") in TILED_PLANS
 
     def _prepare(self, numbers, positions, cell, pbc):
         if not np.isfinite(positions).all():
@@ -300,7 +312,8 @@ class Symmetrix(_Base):
         inv = np.linalg.inv(cell) if np.any(pbc) else np.zeros((3, 3))
         frac = positions @ inv if periodic else np.zeros((0, 3))
         request = neighbor_backend_request()
-        device = use_device_neighbor_graph(request, periodic, n)
+        # MH-1 takes its graph in host memory (mace_nonlinear.hpp:44-51)
+        device = use_device_neighbor_graph(request, periodic, n) and not self._nonlinear
         if request == "kokkos" and not periodic:
             raise RuntimeError("SYMMETRIX_NEIGHBOR_BACKEND=kokkos requires a fully periodic cell")
         ev = self.evaluator
@@ -312,6 +325,10 @@ class Symmetrix(_Base):
             receivers = sources = np.zeros(0, np.int32)
             shifts = np.zeros((0, 3), np.int32)
             self.neighbor_graph_backend = "device"
+        elif self._nonlinear:
+            receivers, sources, shifts = neighbor_list_ijS(positions, cell, pbc, reach)
+            gen, num_edges = 0, len(sources)
+            self.neighbor_graph_backend = "host"
         else:
             receivers, sources, shifts = neighbor_list_ijS(positions, cell, pbc, reach)
             num_neigh = np.bincount(receivers, minlength=n).astype(np.int32)
@@ -339,7 +356,9 @@ class Symmetrix(_Base):
             return self._prepare(numbers, positions, cell, pbc)
         c = self._neighbor_cache
         if state == "cell":
-            self.evaluator._update_factorized_cell(c.generation, cell.reshape(-1), np.linalg.inv(cell).reshape(-1))
+            if not self._nonlinear:
+                self.evaluator._update_factorized_cell(c.generation, cell.reshape(-1),
+                                                       np.linalg.inv(cell).reshape(-1))
             c.cell = cell.copy()
             self.neighbor_cache_cell_update_count += 1
         self.neighbor_cache_reuse_count += 1
@@ -366,6 +385,8 @@ class Symmetrix(_Base):
             volume = abs(float(np.linalg.det(cell)))
             if not volume > 0.0:
                 raise ValueError("stress needs a cell of non-zero volume")
+        if self._nonlinear:
+            return self._calculate_nonlinear(numbers, positions, cell, cache, volume)
         if field is not None:
             ev._set_electric_field(field)
         # the reference's sequence (positions call, node energies, atom
@@ -394,6 +415,32 @@ class Symmetrix(_Base):
                     self.results["polarizability"] = np.array((pol / volume / self._macefield_eps0).reshape(9))
                 if want_becs:
                     self.results["becs"] = np.array(ev.electric_field_bec_bins, dtype=float).reshape(len(numbers), 9)
+        return self.results
+
+    def _calculate_nonlinear(self, numbers, positions, cell, cache, volume):
+        """MH-1: the cached skin graph's edges inside the cutoff
+        (calculator.py:3087-3093), one compute_node_energies_forces call,
+        forces and stress reduced in FP64 (calculator.py:3821-3894)."""
+        recv, src = cache.receivers, cache.sources
+        xyz = positions[src] - positions[recv] + cache.shifts @ cell
+        r = np.sqrt(np.einsum("ij,ij->i", xyz, xyz))
+        active = r < self.cutoff
+        recv, src, xyz, r = recv[active], src[active], np.ascontiguousarray(xyz[active]), r[active]
+        n = len(numbers)
+        types = self._node_types(numbers)
+        num_neigh = np.bincount(recv, minlength=n).astype(np.int32)
+        ev = self.evaluator
+        ev.compute_node_energies_forces(n, types, num_neigh, src, types[src], xyz.reshape(-1), r)
+        node_energies = ev.node_energies
+        nf = ev.node_forces.reshape(-1, 3)
+        forces = np.zeros((n, 3))
+        np.add.at(forces, src, nf)
+        np.add.at(forces, recv, -nf)
+        energy = float(np.sum(node_energies, dtype=np.float64))
+        self.results = {"energy": energy, "free_energy": energy, "energies": node_energies, "forces": forces}
+        if volume is not None:
+            sigma = -np.einsum("ea,eb->ab", nf, xyz) / volume
+            self.results["stress"] = full_3x3_to_voigt_6_stress(sigma)
         return self.results
 
     def get_property(self, name, atoms=None, allow_calculation=True):

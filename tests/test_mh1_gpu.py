@@ -173,3 +173,66 @@ def test_mh1_family_facts(paths):
     assert ev.atomic_numbers == [1, 6, 7, 8, 13, 14, 22, 26, 29, 38]
     model = mo.MH1Oracle(paths["mh1_medium"])
     assert np.allclose(ev.atomic_energies, model.atomic_energies)
+
+
+def _oracle_system(model, pos, cell, pbc, types):
+    """Oracle E, F, S (3x3) on the graph r < r_cut (brute force over the
+    images that can reach the cutoff)."""
+    n = len(pos)
+    recv, src, vec = [], [], []
+    rng = [range(-2, 3) if p else range(0, 1) for p in pbc]
+    for i in range(n):
+        for j in range(n):
+            for a in rng[0]:
+                for b in rng[1]:
+                    for c in rng[2]:
+                        d = pos[j] - pos[i] + np.array([a, b, c]) @ cell
+                        r = np.linalg.norm(d)
+                        if 0.0 < r < model.r_cut:
+                            recv.append(i)
+                            src.append(j)
+                            vec.append(d)
+    recv, src, vec = np.array(recv), np.array(src), np.array(vec).reshape(-1, 3)
+    order = np.argsort(recv, kind="stable")
+    recv, src, vec = recv[order], src[order], vec[order]
+    e, f = model.evaluate(types, recv, src, vec)
+    F = mo.reduce_forces(n, recv, src, f)
+    vol = abs(np.linalg.det(cell)) if all(pbc) else None
+    S = mo.reduce_stress(f, vec, vol) if vol else None
+    return e.sum(), F, S
+
+
+def test_mh1_calculator_matches_oracle_and_reuses_its_graph(paths):
+    from symmetrix.calculator import Symmetrix, full_3x3_to_voigt_6_stress
+    path = paths["mh1_tiny_raw"]
+    model = mo.MH1Oracle(path)
+    pos, cell, types = _random_system(model, 24, 7.5, seed=11)
+    numbers = np.array(model.atomic_numbers)[types]
+    calc = Symmetrix(path, neighbor_skin=0.5)
+    for step in range(3):
+        # moves well inside half the skin: the graph is reused
+        p = pos + 0.02 * step * np.random.default_rng(step).normal(size=pos.shape)
+        res = calc.calculate({"numbers": numbers, "positions": p, "cell": cell, "pbc": [True] * 3},
+                             ["energy", "forces", "stress"])
+        e, F, S = _oracle_system(model, p, cell, [True] * 3, types)
+        _say("mh1 calculator step %d: |dE| %.2e max|dF| %.2e max|dS| %.2e" %
+             (step, abs(res["energy"] - e), np.abs(res["forces"] - F).max(),
+              np.abs(res["stress"] - full_3x3_to_voigt_6_stress(S)).max()))
+        assert abs(res["energy"] - e) / len(p) < 1e-5
+        assert np.abs(res["forces"] - F).max() < 1e-4
+        assert np.abs(res["stress"] - full_3x3_to_voigt_6_stress(S)).max() < 1e-6
+    assert calc.neighbor_cache_build_count == 1 and calc.neighbor_cache_reuse_count == 2
+
+
+def test_mh1_calculator_open_cluster(paths):
+    from symmetrix.calculator import Symmetrix
+    path = paths["mh1_tiny_l3"]
+    model = mo.MH1Oracle(path)
+    pos, _, types = _random_system(model, 16, 6.0, seed=12)
+    numbers = np.array(model.atomic_numbers)[types]
+    calc = Symmetrix(path)
+    res = calc.calculate({"numbers": numbers, "positions": pos, "cell": np.zeros((3, 3)), "pbc": [False] * 3},
+                         ["energy", "forces"])
+    e, F, _ = _oracle_system(model, pos, np.eye(3), [False] * 3, types)
+    assert abs(res["energy"] - e) / len(pos) < 1e-5
+    assert np.abs(res["forces"] - F).max() < 1e-4
