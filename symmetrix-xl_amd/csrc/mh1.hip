@@ -49,7 +49,6 @@ namespace mh1 {
 namespace {
 
 constexpr int kTpThreads = 128;
-constexpr int kMlpThreads = 256;
 constexpr std::size_t kMaxLds = 60 * 1024;
 
 // ------------------------------------------------------------- device views
@@ -66,11 +65,13 @@ struct DLinear {
 };
 
 struct DMlp {
-    int num_layers, radial, first_width, num_types, width;
+    int num_layers, radial, first_width, num_types, width, tape_width;
     const int* layers;
     const float* eps;
     const float* params;
     const float* type_rows;
+    const int* wt_offset;    // per layer: transposed weights [in][out] (linear layers)
+    const int* tape_offset;  // per layer: output offset in the edge's tape row (-1: last layer)
 };
 
 struct DRadial {
@@ -231,39 +232,52 @@ __device__ __forceinline__ void mlp_first_inputs(const DRadial& rd, double r, in
     for (int k = 0; k < rd.nb; ++k) row[k] = static_cast<float>(f[k]);
 }
 
-// One linear layer of an edge tile in LDS: dst[e][j] = b[j] + W[j] . src[e]
-// (layer 0: the per-type rows stand in for the bias and embedding columns).
-__device__ __forceinline__ void mlp_linear_tile(const DMlp& m, int L, int ne, const int* __restrict__ ts,
-                                                const int* __restrict__ tt, const float* src, float* dst,
-                                                float* __restrict__ gout, long long e0) {
-    const int in = m.layers[4 * L + 1], out = m.layers[4 * L + 2], off = m.layers[4 * L + 3];
-    const float* Wt = m.params + off;
-    const float* bias = Wt + static_cast<std::size_t>(out) * in;
-    for (int idx = threadIdx.x; idx < ne * out; idx += blockDim.x) {
-        const int e = idx / out, j = idx % out;
-        float acc;
-        if (L == 0)
-            acc = m.type_rows[static_cast<std::size_t>(ts[e]) * m.first_width + j] +
-                  m.type_rows[static_cast<std::size_t>(m.num_types + tt[e]) * m.first_width + j];
-        else
-            acc = bias[j];
-        const float* s = src + e * m.width;
-        const float* wr = Wt + static_cast<std::size_t>(j) * in;
-        for (int k = 0; k < in; ++k) acc += wr[k] * s[k];
-        if (gout)
-            gout[(e0 + e) * out + j] = acc;
-        else
-            dst[e * m.width + j] = acc;
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// Edge-tile GEMM on MFMA (v_mfma_f32_16x16x4_f32): wave w of the workgroup
+// owns rows 16w..16w+15 of the tile; D[row][c] = sum_k A[row][k] B(k, c) with
+// A in LDS (row stride lda) or global memory, B(k, c) = B[k * ldb + c] in
+// global memory (weights, L1/L2 resident).  Lane l supplies A[l%16][k0+l/16]
+// and B(k0+l/16, c0+l%16) and holds D[4(l/16)+v][l%16].  K and the columns are
+// padded to the fragment size with zeros, rows from a_rows on read zeros;
+// `epi(row, col, value)` stores.
+template <class Epi>
+__device__ __forceinline__ void tile_gemm(const float* A, int lda, int a_rows, int K, const float* __restrict__ B,
+                                          int ldb, int N, Epi epi) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int r = lane & 15, kg = lane >> 4;
+    const bool row_ok = 16 * wave + r < a_rows;
+    const float* arow = A + static_cast<std::size_t>(row_ok ? 16 * wave + r : 0) * lda;
+    for (int c0 = 0; c0 < N; c0 += 64) {
+        v4f acc[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int k0 = 0; k0 < K; k0 += 4) {
+            const int k = k0 + kg;
+            const float a = (row_ok && k < K) ? arow[k] : 0.0f;
+            const float* brow = B + static_cast<std::size_t>(k) * ldb;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int c = c0 + 16 * j + r;
+                const float b = (k < K && c < N) ? brow[c] : 0.0f;
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc[j], 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int c = c0 + 16 * j + r;
+            if (c < N) {
+#pragma unroll
+                for (int v = 0; v < 4; ++v) epi(16 * wave + 4 * kg + v, c, acc[j][v]);
+            }
+        }
     }
 }
 
-__device__ __forceinline__ void mlp_norm_tile(const DMlp& m, int L, int ne, const float* src, float* dst,
-                                              float* stats) {
-    const int w = m.layers[4 * L + 1], off = m.layers[4 * L + 3];
-    const float* g = m.params + off;
-    const float* b = g + w;
+// Row statistics of a LayerNorm over the tile's rows (one thread per row).
+__device__ __forceinline__ void ln_stats(const float* x, int ldx, int w, int ne, float eps, float* stats) {
     for (int e = threadIdx.x; e < ne; e += blockDim.x) {
-        const float* s = src + e * m.width;
+        const float* s = x + static_cast<std::size_t>(e) * ldx;
         float mean = 0.0f;
         for (int k = 0; k < w; ++k) mean += s[k];
         mean /= w;
@@ -271,131 +285,119 @@ __device__ __forceinline__ void mlp_norm_tile(const DMlp& m, int L, int ne, cons
         for (int k = 0; k < w; ++k) var += (s[k] - mean) * (s[k] - mean);
         var /= w;
         stats[2 * e] = mean;
-        stats[2 * e + 1] = 1.0f / sqrtf(var + m.eps[L]);
-    }
-    __syncthreads();
-    for (int idx = threadIdx.x; idx < ne * w; idx += blockDim.x) {
-        const int e = idx / w, j = idx % w;
-        dst[e * m.width + j] = (src[e * m.width + j] - stats[2 * e]) * stats[2 * e + 1] * g[j] + b[j];
+        stats[2 * e + 1] = 1.0f / sqrtf(var + eps);
     }
 }
 
-// Forward of an affine MLP over a tile of TE edges per workgroup; out
-// [E][out_dim].  LDS: two activation buffers [TE][width] and [TE][2] stats.
-__global__ __launch_bounds__(kMlpThreads) void k_mlp_forward(const DMlp m, const DRadial rd, long long E, int TE,
-                                                              const double* __restrict__ r,
-                                                              const int* __restrict__ ets,
-                                                              const int* __restrict__ ett, float* __restrict__ out) {
+// Forward of an affine MLP over tiles of 16*waves edges: linear layers on
+// MFMA, LayerNorm and SiLU as passes over the tile in LDS (two buffers of row
+// stride ld).  Every layer but the last also writes its output to the edge's
+// tape row (the reverse reads the LayerNorm and SiLU inputs from there); the
+// last layer writes out [E][out_dim].
+__global__ __launch_bounds__(256) void k_mlp_forward(const DMlp m, const DRadial rd, long long E, int ld,
+                                                     const double* __restrict__ r, const int* __restrict__ ets,
+                                                     const int* __restrict__ ett, float* __restrict__ out,
+                                                     float* __restrict__ tape) {
     extern __shared__ float lds[];
+    const int rows = blockDim.x / 4;  // 16 per wave
     float* a = lds;
-    float* b = lds + TE * m.width;
-    float* stats = lds + 2 * TE * m.width;
-    const long long e0 = static_cast<long long>(blockIdx.x) * TE;
-    const int ne = static_cast<int>(min(static_cast<long long>(TE), E - e0));
+    float* b = lds + rows * ld;
+    float* stats = lds + 2 * rows * ld;
+    const long long e0 = static_cast<long long>(blockIdx.x) * rows;
+    const int ne = static_cast<int>(min(static_cast<long long>(rows), E - e0));
     const int* ts = ets + e0;
     const int* tt = ett + e0;
-    for (int e = threadIdx.x; e < ne; e += blockDim.x) mlp_first_inputs(rd, r[e0 + e], ts[e], tt[e], a + e * m.width);
+    for (int idx = threadIdx.x; idx < rows * ld; idx += blockDim.x) a[idx] = 0.0f;
+    __syncthreads();
+    for (int e = threadIdx.x; e < ne; e += blockDim.x) mlp_first_inputs(rd, r[e0 + e], ts[e], tt[e], a + e * ld);
     __syncthreads();
     for (int L = 0; L < m.num_layers; ++L) {
-        const int type = m.layers[4 * L];
+        const int type = m.layers[4 * L], in = m.layers[4 * L + 1], w = m.layers[4 * L + 2], off = m.layers[4 * L + 3];
         const bool last = L == m.num_layers - 1;
+        float* trow = tape + m.tape_offset[L];
         if (type == 0) {
-            mlp_linear_tile(m, L, ne, ts, tt, a, b, last ? out : nullptr, e0);
+            const float* WT = m.params + m.wt_offset[L];
+            const float* bias = m.params + off + static_cast<std::size_t>(w) * in;
+            tile_gemm(a, ld, rows, in, WT, w, w, [&](int row, int c, float v) {
+                if (row >= ne) {
+                    if (!last) b[row * ld + c] = 0.0f;
+                    return;
+                }
+                v += L == 0 ? m.type_rows[static_cast<std::size_t>(ts[row]) * m.first_width + c] +
+                                  m.type_rows[static_cast<std::size_t>(m.num_types + tt[row]) * m.first_width + c]
+                            : bias[c];
+                if (last) {
+                    out[(e0 + row) * w + c] = v;
+                } else {
+                    b[row * ld + c] = v;
+                    trow[(e0 + row) * m.tape_width + c] = v;
+                }
+            });
             float* t = a;
             a = b;
             b = t;
         } else if (type == 1) {
-            mlp_norm_tile(m, L, ne, a, b, stats);
+            const float* g = m.params + off;
+            const float* bb = g + w;
+            ln_stats(a, ld, w, ne, m.eps[L], stats);
+            __syncthreads();
+            for (int idx = threadIdx.x; idx < ne * w; idx += blockDim.x) {
+                const int e = idx / w, j = idx % w;
+                const float v = (a[e * ld + j] - stats[2 * e]) * stats[2 * e + 1] * g[j] + bb[j];
+                b[e * ld + j] = v;
+                trow[(e0 + e) * m.tape_width + j] = v;
+            }
             float* t = a;
             a = b;
             b = t;
         } else {
-            const int w = m.layers[4 * L + 1];
             for (int idx = threadIdx.x; idx < ne * w; idx += blockDim.x) {
-                float* v = a + (idx / w) * m.width + idx % w;
-                *v = *v * sigmoidf_(*v);
+                const int e = idx / w, j = idx % w;
+                float* p = a + e * ld + j;
+                *p = *p * sigmoidf_(*p);
+                trow[(e0 + e) * m.tape_width + j] = *p;
             }
         }
         __syncthreads();
     }
 }
 
-// Reverse of an affine MLP: re-runs the tile forward keeping each layer's
-// input ([num_layers][TE][width] in LDS), then pulls gout [E][out_dim] back
-// to the radial features: rad_adj [E][nb] += d/d(radial).
-__global__ __launch_bounds__(kMlpThreads) void k_mlp_reverse(const DMlp m, const DRadial rd, long long E, int TE,
-                                                              const double* __restrict__ r,
-                                                              const int* __restrict__ ets,
-                                                              const int* __restrict__ ett,
-                                                              const float* __restrict__ gout,
-                                                              float* __restrict__ rad_adj) {
+// Reverse of an affine MLP: gout [E][out_dim] pulled back through the layers
+// (linear layers on MFMA with the row-major weights as B, LayerNorm and SiLU
+// from the forward's tape) to the radial features: rad_adj [E][nb] +=.
+__global__ __launch_bounds__(256) void k_mlp_reverse(const DMlp m, const DRadial rd, long long E, int ld,
+                                                     const float* __restrict__ tape, const float* __restrict__ gout,
+                                                     float* __restrict__ rad_adj) {
     extern __shared__ float lds[];
-    const int slab = TE * m.width;
-    float* acts = lds;                                   // [num_layers][TE][width]: input of each layer
-    float* g = lds + m.num_layers * slab;                // adjoint
-    float* h = g + slab;                                 // next adjoint
-    float* stats = h + slab;
-    const long long e0 = static_cast<long long>(blockIdx.x) * TE;
-    const int ne = static_cast<int>(min(static_cast<long long>(TE), E - e0));
-    const int* ts = ets + e0;
-    const int* tt = ett + e0;
-    for (int e = threadIdx.x; e < ne; e += blockDim.x) mlp_first_inputs(rd, r[e0 + e], ts[e], tt[e], acts + e * m.width);
-    __syncthreads();
-    for (int L = 0; L + 1 < m.num_layers; ++L) {
-        const int type = m.layers[4 * L];
-        float* src = acts + L * slab;
-        float* dst = acts + (L + 1) * slab;
+    const int rows = blockDim.x / 4;
+    float* g = lds;
+    float* h = lds + rows * ld;
+    float* stats = lds + 2 * rows * ld;
+    const long long e0 = static_cast<long long>(blockIdx.x) * rows;
+    const int ne = static_cast<int>(min(static_cast<long long>(rows), E - e0));
+    int cur_w = m.layers[4 * (m.num_layers - 1) + 2];
+    bool from_gout = true;
+    for (int L = m.num_layers - 1; L >= 0; --L) {
+        const int type = m.layers[4 * L], in = m.layers[4 * L + 1], w = m.layers[4 * L + 2], off = m.layers[4 * L + 3];
         if (type == 0) {
-            mlp_linear_tile(m, L, ne, ts, tt, src, dst, nullptr, e0);
+            const float* W = m.params + off;  // [w][in]: B(k = output, c = input)
+            // the last layer reads its adjoint rows straight from gout (rows past the edges read zeros)
+            const float* A = from_gout ? gout + e0 * w : g;
+            tile_gemm(A, from_gout ? w : ld, from_gout ? ne : rows, w, W, in, in, [&](int row, int c, float v) {
+                if (L == 0) {
+                    if (row < ne) rad_adj[(e0 + row) * rd.nb + c] += v;
+                } else {
+                    h[row * ld + c] = row < ne ? v : 0.0f;
+                }
+            });
+            from_gout = false;
+            cur_w = in;
         } else if (type == 1) {
-            mlp_norm_tile(m, L, ne, src, dst, stats);
-        } else {
-            const int w = m.layers[4 * L + 1];
-            for (int idx = threadIdx.x; idx < ne * w; idx += blockDim.x) {
-                const float v = src[(idx / w) * m.width + idx % w];
-                dst[(idx / w) * m.width + idx % w] = v * sigmoidf_(v);
-            }
-        }
-        __syncthreads();
-    }
-    // last layer (linear): g[e][k] = sum_o W[o][k] gout[e][o]
-    {
-        const int L = m.num_layers - 1;
-        const int in = m.layers[4 * L + 1], out = m.layers[4 * L + 2], off = m.layers[4 * L + 3];
-        const float* Wt = m.params + off;
-        const int lin = L == 0 ? rd.nb : in;
-        for (int idx = threadIdx.x; idx < ne * lin; idx += blockDim.x) {
-            const int e = idx / lin, k = idx % lin;
-            const float* go = gout + (e0 + e) * out;
-            float acc = 0.0f;
-            for (int o = 0; o < out; ++o) acc += Wt[static_cast<std::size_t>(o) * in + k] * go[o];
-            if (L == 0)
-                rad_adj[(e0 + e) * rd.nb + k] += acc;
-            else
-                g[e * m.width + k] = acc;
-        }
-        __syncthreads();
-    }
-    for (int L = m.num_layers - 2; L >= 0; --L) {
-        const int type = m.layers[4 * L];
-        const float* x = acts + L * slab;
-        if (type == 0) {
-            const int in = m.layers[4 * L + 1], out = m.layers[4 * L + 2], off = m.layers[4 * L + 3];
-            const float* Wt = m.params + off;
-            for (int idx = threadIdx.x; idx < ne * in; idx += blockDim.x) {
-                const int e = idx / in, k = idx % in;
-                float acc = 0.0f;
-                for (int o = 0; o < out; ++o) acc += Wt[static_cast<std::size_t>(o) * in + k] * g[e * m.width + o];
-                if (L == 0)
-                    rad_adj[(e0 + e) * rd.nb + k] += acc;
-                else
-                    h[e * m.width + k] = acc;
-            }
-        } else if (type == 1) {
-            const int w = m.layers[4 * L + 1], off = m.layers[4 * L + 3];
+            // input of this layer = output of layer L-1 (tape)
+            const float* x = tape + m.tape_offset[L - 1];
             const float* gam = m.params + off;
             for (int e = threadIdx.x; e < ne; e += blockDim.x) {
-                const float* xs = x + e * m.width;
+                const float* xs = x + (e0 + e) * m.tape_width;
                 float mean = 0.0f;
                 for (int k = 0; k < w; ++k) mean += xs[k];
                 mean /= w;
@@ -405,34 +407,29 @@ __global__ __launch_bounds__(kMlpThreads) void k_mlp_reverse(const DMlp m, const
                 const float rs = 1.0f / sqrtf(var + m.eps[L]);
                 float mg = 0.0f, mgx = 0.0f;
                 for (int k = 0; k < w; ++k) {
-                    const float gh = g[e * m.width + k] * gam[k];
+                    const float gh = g[e * ld + k] * gam[k];
                     mg += gh;
                     mgx += gh * (xs[k] - mean) * rs;
                 }
-                stats[2 * e] = mg / w;
-                stats[2 * e + 1] = mgx / w;
+                mg /= w;
+                mgx /= w;
+                for (int k = 0; k < w; ++k)
+                    h[e * ld + k] = rs * (g[e * ld + k] * gam[k] - mg - (xs[k] - mean) * rs * mgx);
             }
-            __syncthreads();
-            for (int idx = threadIdx.x; idx < ne * w; idx += blockDim.x) {
-                const int e = idx / w, k = idx % w;
-                const float* xs = x + e * m.width;
-                float mean = 0.0f;
-                for (int q = 0; q < w; ++q) mean += xs[q];
-                mean /= w;
-                float var = 0.0f;
-                for (int q = 0; q < w; ++q) var += (xs[q] - mean) * (xs[q] - mean);
-                var /= w;
-                const float rs = 1.0f / sqrtf(var + m.eps[L]);
-                const float xh = (xs[k] - mean) * rs;
-                h[e * m.width + k] = rs * (g[e * m.width + k] * gam[k] - stats[2 * e] - xh * stats[2 * e + 1]);
-            }
+            for (int idx = threadIdx.x; idx < (rows - ne) * w; idx += blockDim.x)
+                h[(ne + idx / w) * ld + idx % w] = 0.0f;
+            (void)stats;
         } else {
-            const int w = m.layers[4 * L + 1];
-            for (int idx = threadIdx.x; idx < ne * w; idx += blockDim.x) {
+            const float* x = tape + m.tape_offset[L - 1];
+            for (int idx = threadIdx.x; idx < rows * w; idx += blockDim.x) {
                 const int e = idx / w, k = idx % w;
-                const float v = x[e * m.width + k];
-                const float s = sigmoidf_(v);
-                h[e * m.width + k] = g[e * m.width + k] * (s + v * s * (1.0f - s));
+                float v = 0.0f;
+                if (e < ne) {
+                    const float xv = x[(e0 + e) * m.tape_width + k];
+                    const float sg = sigmoidf_(xv);
+                    v = g[e * ld + k] * (sg + xv * sg * (1.0f - sg));
+                }
+                h[e * ld + k] = v;
             }
         }
         __syncthreads();
@@ -440,6 +437,7 @@ __global__ __launch_bounds__(kMlpThreads) void k_mlp_reverse(const DMlp m, const
         g = h;
         h = t;
     }
+    (void)cur_w;
 }
 
 // Convolution into receivers: msg[i][(block, u, k)] = sum over the receiver's
@@ -977,10 +975,11 @@ void Evaluator::upload_model() {
                       !T.in_mask.empty(), T.in_dim, T.out_dim};
     };
     struct MlpOff {
-        std::size_t layers, eps, params, rows;
+        std::size_t layers, eps, params, rows, wt, tape;
     };
     auto put_mlp = [&](const MlpTables& T) {
-        return MlpOff{pk.put(T.layers), pk.put(T.eps), pk.put(T.params), pk.put(T.type_rows)};
+        return MlpOff{pk.put(T.layers), pk.put(T.eps), pk.put(T.params), pk.put(T.type_rows), pk.put(T.wt_offset),
+                      pk.put(T.tape_offset)};
     };
     const Model& M = model_;
     const int nt = static_cast<int>(M.atomic_numbers.size());
@@ -1086,8 +1085,8 @@ void Evaluator::upload_model() {
                        o.has_bias ? F(o.bias) : nullptr, o.has_om ? F(o.om) : nullptr, o.has_im ? F(o.im) : nullptr};
     };
     auto mlp = [&](const MlpTables& T, const MlpOff& o) {
-        return DMlp{T.num_layers, T.radial, T.first_width, nt, T.max_hidden, I_(o.layers), F(o.eps), F(o.params),
-                    F(o.rows)};
+        return DMlp{T.num_layers, T.radial, T.first_width, nt, T.max_hidden, T.tape_width, I_(o.layers), F(o.eps),
+                    F(o.params), F(o.rows), I_(o.wt), I_(o.tape)};
     };
     embed_table_ = F(o_table);
     atomic_e_ = reinterpret_cast<const double*>(base + o_ae);
@@ -1150,13 +1149,21 @@ void Evaluator::launch_linear(const DLinear& op, int N, const float* x, float* y
            accumulate ? 1 : 0);
 }
 
-int mlp_tile(const DMlp& m, bool reverse) {
-    const std::size_t per_edge = static_cast<std::size_t>(reverse ? m.num_layers + 2 : 2) * m.width * 4 + 8;
-    return static_cast<int>(std::max<std::size_t>(1, std::min<std::size_t>(32, kMaxLds / per_edge)));
+// row stride of an MLP tile buffer: the widest layer plus 4 (two-way LDS
+// bank conflicts at most on the MFMA A reads)
+int mlp_ld(const DMlp& m) { return ((m.width + 3) / 4) * 4 + 4; }
+
+std::size_t mlp_lds(const DMlp& m, int waves) {
+    const int rows = 16 * waves;
+    return static_cast<std::size_t>(2 * rows * mlp_ld(m) + 2 * rows) * sizeof(float);
 }
 
-std::size_t mlp_lds(const DMlp& m, int TE, bool reverse) {
-    return static_cast<std::size_t>(reverse ? m.num_layers + 2 : 2) * TE * m.width * 4 + 8 * TE;
+// waves per tile workgroup: four unless the buffers exceed the LDS budget
+int mlp_waves(const DMlp& m) {
+    int w = 4;
+    while (w > 1 && mlp_lds(m, w) > kMaxLds) w /= 2;
+    if (mlp_lds(m, w) > kMaxLds) throw std::domain_error("MH-1 model: an edge MLP layer is too wide for the LDS tile");
+    return w;
 }
 
 void Evaluator::compute(int N, const int* types, const int* num_neigh, const int* neigh, const int* neigh_types,
@@ -1203,7 +1210,7 @@ void Evaluator::compute(int N, const int* types, const int* num_neigh, const int
                       o_Y = lay.add<float>(static_cast<std::size_t>(E) * NY), o_cut = lay.add<float>(E),
                       o_feat0 = lay.add<float>(static_cast<std::size_t>(N) * embed_dim_);
     struct LayerOff {
-        std::size_t up, res, skip, msg, dens, lin1, pre, gated, iout, feat, wraw, draw;
+        std::size_t up, res, skip, msg, dens, lin1, pre, gated, iout, feat, wraw, draw, wtape, dtape;
         std::size_t a_feat, contr, a_iout, a_gated, a_pre, a_lin, a_msg, a_up, a_dens, wadj, a1, adraw;
     };
     std::vector<LayerOff> lo(L);
@@ -1222,6 +1229,8 @@ void Evaluator::compute(int N, const int* types, const int* num_neigh, const int
         o.iout = lay.add<float>(n * I.lin2.out.dim);
         o.feat = lay.add<float>(n * M.products[k].out_dim);
         o.wraw = lay.add<float>(static_cast<std::size_t>(E) * I.tp.numel);
+        o.wtape = lay.add<float>(static_cast<std::size_t>(E) * I.weights_mlp.tape_width);
+        o.dtape = lay.add<float>(static_cast<std::size_t>(E) * I.density_mlp.tape_width);
         o.draw = lay.add<float>(E);
         o.a_feat = lay.add<float>(n * M.products[k].out_dim);
         o.contr = lay.add<float>(n * M.products[k].out_dim);
@@ -1294,11 +1303,11 @@ void Evaluator::compute(int N, const int* types, const int* num_neigh, const int
         launch_linear(I.up.fwd, N, feats, f(o.up), nullptr, false, "mh1_linear_up");
         launch_linear(I.res.fwd, N, f(o.up), f(o.res), nullptr, false, "mh1_linear_res");
         launch_linear(I.skip.fwd, N, feats, f(o.skip), nullptr, false, "mh1_linear_skip");
-        const int TE = mlp_tile(I.wmlp, false), TD = mlp_tile(I.dmlp, false);
-        launch("mh1_mlp_forward", k_mlp_forward, blocks_for(E, TE), kMlpThreads, mlp_lds(I.wmlp, TE, false), I.wmlp,
-               rad_, E, TE, d_r, d_ts, d_tt, f(o.wraw));
-        launch("mh1_mlp_forward", k_mlp_forward, blocks_for(E, TD), kMlpThreads, mlp_lds(I.dmlp, TD, false), I.dmlp,
-               rad_, E, TD, d_r, d_ts, d_tt, f(o.draw));
+        const int WW = mlp_waves(I.wmlp), WD = mlp_waves(I.dmlp);
+        launch("mh1_mlp_forward", k_mlp_forward, blocks_for(E, 16 * WW), 64 * WW, mlp_lds(I.wmlp, WW), I.wmlp, rad_,
+               E, mlp_ld(I.wmlp), d_r, d_ts, d_tt, f(o.wraw), f(o.wtape));
+        launch("mh1_mlp_forward", k_mlp_forward, blocks_for(E, 16 * WD), 64 * WD, mlp_lds(I.dmlp, WD), I.dmlp, rad_,
+               E, mlp_ld(I.dmlp), d_r, d_ts, d_tt, f(o.draw), f(o.dtape));
         const std::size_t tp_lds = static_cast<std::size_t>(I.tp.slots + I.tp.nin1) * kTpThreads * 4;
         launch("mh1_tp_forward", k_tp_forward, blocks_for(static_cast<long long>(N) * I.tp.channels, kTpThreads),
                kTpThreads, tp_lds, I.tp, N, d_off, d_src, f(o.up), Y, NY, f(o.wraw), cut_w, f(o.draw), f(o.msg),
@@ -1390,11 +1399,11 @@ void Evaluator::compute(int N, const int* types, const int* num_neigh, const int
         launch("mh1_gather_sources", k_gather_sources,
                blocks_for(static_cast<long long>(N) * I.tp.in1_dim, 256), 256, 0, N, I.tp.in1_dim, ip(o_toff),
                ip(o_tedge), f(o.a1), f(o.a_up));
-        const int TE = mlp_tile(I.wmlp, true), TD = mlp_tile(I.dmlp, true);
-        launch("mh1_mlp_reverse", k_mlp_reverse, blocks_for(E, TE), kMlpThreads, mlp_lds(I.wmlp, TE, true), I.wmlp,
-               rad_, E, TE, d_r, d_ts, d_tt, f(o.wadj), radadj);
-        launch("mh1_mlp_reverse", k_mlp_reverse, blocks_for(E, TD), kMlpThreads, mlp_lds(I.dmlp, TD, true), I.dmlp,
-               rad_, E, TD, d_r, d_ts, d_tt, f(o.adraw), radadj);
+        const int WW = mlp_waves(I.wmlp), WD = mlp_waves(I.dmlp);
+        launch("mh1_mlp_reverse", k_mlp_reverse, blocks_for(E, 16 * WW), 64 * WW, mlp_lds(I.wmlp, WW), I.wmlp, rad_,
+               E, mlp_ld(I.wmlp), f(o.wtape), f(o.wadj), radadj);
+        launch("mh1_mlp_reverse", k_mlp_reverse, blocks_for(E, 16 * WD), 64 * WD, mlp_lds(I.dmlp, WD), I.dmlp, rad_,
+               E, mlp_ld(I.dmlp), f(o.dtape), f(o.adraw), radadj);
         if (k > 0) {
             // a_feat[k-1] += up^T(a_up) + skip^T(a_skip), a_skip = a_feat[k] when the product has a skip
             float* prev = f(lo[k - 1].a_feat);

@@ -253,6 +253,21 @@ MlpTables build_mlp(const Value& v, int radial, const std::vector<std::vector<do
     T.out_dim = prev;
     for (int k = 0; k + 1 < T.num_layers; ++k) T.max_hidden = std::max(T.max_hidden, T.layers[4 * k + 2]);
     T.max_hidden = std::max(T.max_hidden, T.radial);
+    for (int k = 0; k < T.num_layers; ++k) {
+        const int* L = &T.layers[4 * k];
+        if (L[0] == 0) {
+            T.wt_offset.push_back(static_cast<int>(T.params.size()));
+            for (int i = 0; i < L[1]; ++i)
+                for (int o = 0; o < L[2]; ++o) {
+                    const float w = T.params[L[3] + static_cast<std::size_t>(o) * L[1] + i];
+                    T.params.push_back(w);
+                }
+        } else {
+            T.wt_offset.push_back(-1);
+        }
+        T.tape_offset.push_back(k + 1 < T.num_layers ? T.tape_width : -1);
+        if (k + 1 < T.num_layers) T.tape_width += L[2];
+    }
     return T;
 }
 

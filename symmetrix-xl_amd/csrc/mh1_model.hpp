@@ -73,6 +73,10 @@ struct MlpTables {
     std::vector<float> params;     // linear: W [out][in] then b [out]; LN: w, b
     int radial = 0, first_width = 0, out_dim = 0, max_hidden = 0, num_layers = 0;
     std::vector<float> type_rows;  // [2][num_types][first_width]: source rows (+ bias), target rows
+    // per layer: offset of a linear's transposed weights [in][out] in params (-1 otherwise), and of
+    // the layer's output in a per-edge tape row (-1 for the last layer); tape_width floats per edge
+    std::vector<int> wt_offset, tape_offset;
+    int tape_width = 0;
 };
 
 struct TensorTables {
