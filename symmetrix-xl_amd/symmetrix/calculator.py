@@ -433,9 +433,10 @@ class Symmetrix(_Base):
         ev.compute_node_energies_forces(n, types, num_neigh, src, types[src], xyz.reshape(-1), r)
         node_energies = ev.node_energies
         nf = ev.node_forces.reshape(-1, 3)
-        forces = np.zeros((n, 3))
-        np.add.at(forces, src, nf)
-        np.add.at(forces, recv, -nf)
+        forces = np.empty((n, 3))
+        for c in range(3):
+            forces[:, c] = (np.bincount(src, weights=nf[:, c], minlength=n)
+                            - np.bincount(recv, weights=nf[:, c], minlength=n))
         energy = float(np.sum(node_energies, dtype=np.float64))
         self.results = {"energy": energy, "free_energy": energy, "energies": node_energies, "forces": forces}
         if volume is not None:
