@@ -35,12 +35,14 @@
 #include <numeric>
 #include <stdexcept>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "../../include/symmetrix_mh1.h"
 #include "device_common.hpp"
 #include "harmonics.hpp"
 #include "mh1_model.hpp"
+#include "mh1_paths.hpp"
 
 namespace smx {
 void set_last_error(const std::string& message);  // evaluator.cpp
@@ -88,6 +90,8 @@ struct DTp {
     const int* out_slot;
     const int* entries;
     const float* values;
+    int compiled;        // family structure index (mh1_paths.hpp) or -1
+    const float* cval;   // its Wigner values x path weight, structure order
 };
 
 struct DGate {
@@ -552,6 +556,194 @@ __global__ __launch_bounds__(kTpThreads) void k_tp_reverse(
         }
         for (int off = t.channels / 2; off > 0; off >>= 1) cpart += __shfl_xor(cpart, off, kWave);
         if (u == 0) {
+            const float dr = draw[e];
+            const float base = tanhf(dr * dr);
+            adraw[e] = ad * (1.0f - base * base) * 2.0f * dr * cf;
+            if (cut_adj) cut_adj[e] += cpart + ad * base;
+        }
+    }
+}
+
+// ---- convolution kernels of the compiled family structures (mh1_paths.hpp):
+// the same sums as k_tp_forward / k_tp_reverse with every path, Wigner
+// position and slot a compile-time constant, so accumulators, the channel's
+// first-input components, the edge's harmonics and adjoints stay in registers
+// (the Wigner values are uniform loads from the model tables).
+
+template <class S, int P, int Q>
+__device__ __forceinline__ void tpc_fwd_entry(float (&acc)[S::kSlots], const float (&x1)[S::kIn1], const float* y,
+                                              float w, const float* __restrict__ cv) {
+    constexpr TpPathC p = S::paths[P];
+    constexpr TpEntryC en = S::entries[p.first + Q];
+    acc[p.out_base + en.k] += w * cv[p.first + Q] * x1[p.in_base + en.a] * y[p.l2 * p.l2 + en.b];
+}
+
+template <class S, int P, int... Q>
+__device__ __forceinline__ void tpc_fwd_path(float (&acc)[S::kSlots], const float (&x1)[S::kIn1], const float* y,
+                                             float w, const float* __restrict__ cv, std::integer_sequence<int, Q...>) {
+    (tpc_fwd_entry<S, P, Q>(acc, x1, y, w, cv), ...);
+}
+
+template <class S, int... P>
+__device__ __forceinline__ void tpc_fwd(float (&acc)[S::kSlots], const float (&x1)[S::kIn1], const float* y,
+                                        const float (&w)[S::kPaths], const float* __restrict__ cv,
+                                        std::integer_sequence<int, P...>) {
+    (tpc_fwd_path<S, P>(acc, x1, y, w[P], cv, std::make_integer_sequence<int, S::paths[P].count>{}), ...);
+}
+
+template <class S, int P, int Q>
+__device__ __forceinline__ void tpc_rev_entry(const float (&g)[S::kSlots], const float (&x1)[S::kIn1],
+                                              const float* y, float w, const float* __restrict__ cv, float& gw,
+                                              float (&xa)[S::kIn1], float* ya) {
+    constexpr TpPathC p = S::paths[P];
+    constexpr TpEntryC en = S::entries[p.first + Q];
+    const float vg = cv[p.first + Q] * g[p.out_base + en.k];
+    const float xv = x1[p.in_base + en.a], yv = y[p.l2 * p.l2 + en.b];
+    gw += vg * xv * yv;
+    xa[p.in_base + en.a] += vg * w * yv;
+    ya[p.l2 * p.l2 + en.b] += vg * w * xv;
+}
+
+template <class S, int P, int... Q>
+__device__ __forceinline__ void tpc_rev_path(const float (&g)[S::kSlots], const float (&x1)[S::kIn1], const float* y,
+                                             float w, const float* __restrict__ cv, float& gw, float (&xa)[S::kIn1],
+                                             float* ya, std::integer_sequence<int, Q...>) {
+    (tpc_rev_entry<S, P, Q>(g, x1, y, w, cv, gw, xa, ya), ...);
+}
+
+template <class S, int... P>
+__device__ __forceinline__ void tpc_rev(const float (&g)[S::kSlots], const float (&x1)[S::kIn1], const float* y,
+                                        const float (&w)[S::kPaths], const float* __restrict__ cv,
+                                        float (&gw)[S::kPaths], float (&xa)[S::kIn1], float* ya,
+                                        std::integer_sequence<int, P...>) {
+    (tpc_rev_path<S, P>(g, x1, y, w[P], cv, gw[P], xa, ya, std::make_integer_sequence<int, S::paths[P].count>{}),
+     ...);
+}
+
+// first-input components of channel u: the 0e value, then the 1o triple
+template <class S>
+__device__ __forceinline__ void tpc_load_x1(const float* urow, int E, int u, float (&x1)[S::kIn1]) {
+    x1[0] = urow[u];
+    if constexpr (S::kIn1 == 4) {
+#pragma unroll
+        for (int a = 0; a < 3; ++a) x1[1 + a] = urow[E + 3 * u + a];
+    }
+}
+
+template <int L1MAX, int LMAX>
+__global__ __launch_bounds__(kTpThreads) void k_tp_forward_c(const DTp t, int N, const int* __restrict__ offsets,
+                                                              const int* __restrict__ src,
+                                                              const float* __restrict__ up,
+                                                              const float* __restrict__ Y,
+                                                              const float* __restrict__ wraw,
+                                                              const float* __restrict__ cut,
+                                                              const float* __restrict__ draw,
+                                                              float* __restrict__ msg, float* __restrict__ density) {
+    using S = TpStructure<L1MAX, LMAX>;
+    constexpr int NY = (LMAX + 1) * (LMAX + 1);
+    const long long gt = blockIdx.x * static_cast<long long>(kTpThreads) + threadIdx.x;
+    const int E = t.channels;
+    const int i = static_cast<int>(gt / E), u = static_cast<int>(gt % E);
+    if (i >= N) return;
+    float acc[S::kSlots];
+#pragma unroll
+    for (int s = 0; s < S::kSlots; ++s) acc[s] = 0.0f;
+    float dens = 0.0f;
+    for (int e = offsets[i]; e < offsets[i + 1]; ++e) {
+        float x1[S::kIn1];
+        tpc_load_x1<S>(up + static_cast<std::size_t>(src[e]) * t.in1_dim, E, u, x1);
+        float y[NY];
+#pragma unroll
+        for (int b = 0; b < NY; ++b) y[b] = Y[static_cast<std::size_t>(e) * NY + b];
+        const float cf = cut ? cut[e] : 1.0f;
+        const float* we = wraw + static_cast<std::size_t>(e) * t.numel + u;
+        float w[S::kPaths];
+#pragma unroll
+        for (int p = 0; p < S::kPaths; ++p) w[p] = we[p * E] * cf;
+        tpc_fwd<S>(acc, x1, y, w, t.cval, std::make_integer_sequence<int, S::kPaths>{});
+        const float dr = draw[e];
+        dens += tanhf(dr * dr) * cf;
+    }
+    float* mrow = msg + static_cast<std::size_t>(i) * t.out_dim;
+#pragma unroll
+    for (int p = 0; p < S::kPaths; ++p) {
+        // output block of path p: per-channel slots out_base.., E * out_base floats before it
+        const int ob = S::paths[p].out_base, d3 = 2 * S::paths[p].l3 + 1;
+#pragma unroll
+        for (int k = 0; k < 7; ++k)
+            if (k < d3) mrow[E * ob + u * d3 + k] = acc[ob + k];
+    }
+    if (u == 0) density[i] = dens;
+}
+
+template <int L1MAX, int LMAX>
+__global__ __launch_bounds__(kTpThreads) void k_tp_reverse_c(
+    const DTp t, int N, const int* __restrict__ offsets, const int* __restrict__ src, const float* __restrict__ up,
+    const float* __restrict__ Y, const float* __restrict__ wraw, const float* __restrict__ cut,
+    const float* __restrict__ draw, const float* __restrict__ amsg, const float* __restrict__ adens,
+    float* __restrict__ wadj, float* __restrict__ a1, float* __restrict__ Yadj, float* __restrict__ cut_adj,
+    float* __restrict__ adraw) {
+    using S = TpStructure<L1MAX, LMAX>;
+    constexpr int NY = (LMAX + 1) * (LMAX + 1);
+    const long long gt = blockIdx.x * static_cast<long long>(kTpThreads) + threadIdx.x;
+    const int E = t.channels;
+    const int i = static_cast<int>(gt / E), u = static_cast<int>(gt % E);
+    if (i >= N) return;
+    float g[S::kSlots];
+    const float* grow = amsg + static_cast<std::size_t>(i) * t.out_dim;
+#pragma unroll
+    for (int p = 0; p < S::kPaths; ++p) {
+        const int ob = S::paths[p].out_base, d3 = 2 * S::paths[p].l3 + 1;
+#pragma unroll
+        for (int k = 0; k < 7; ++k)
+            if (k < d3) g[ob + k] = grow[E * ob + u * d3 + k];
+    }
+    const float ad = adens[i];
+    for (int e = offsets[i]; e < offsets[i + 1]; ++e) {
+        float x1[S::kIn1];
+        tpc_load_x1<S>(up + static_cast<std::size_t>(src[e]) * t.in1_dim, E, u, x1);
+        float y[NY];
+#pragma unroll
+        for (int b = 0; b < NY; ++b) y[b] = Y[static_cast<std::size_t>(e) * NY + b];
+        const float cf = cut ? cut[e] : 1.0f;
+        const float* we = wraw + static_cast<std::size_t>(e) * t.numel + u;
+        float wr[S::kPaths], w[S::kPaths], gw[S::kPaths], xa[S::kIn1], ya[NY];
+#pragma unroll
+        for (int p = 0; p < S::kPaths; ++p) {
+            wr[p] = we[p * E];
+            w[p] = wr[p] * cf;
+            gw[p] = 0.0f;
+        }
+#pragma unroll
+        for (int a = 0; a < S::kIn1; ++a) xa[a] = 0.0f;
+#pragma unroll
+        for (int b = 0; b < NY; ++b) ya[b] = 0.0f;
+        tpc_rev<S>(g, x1, y, w, t.cval, gw, xa, ya, std::make_integer_sequence<int, S::kPaths>{});
+        float* wa = wadj + static_cast<std::size_t>(e) * t.numel + u;
+        float cpart = 0.0f;
+#pragma unroll
+        for (int p = 0; p < S::kPaths; ++p) {
+            wa[p * E] = gw[p] * cf;
+            cpart += gw[p] * wr[p];
+        }
+        float* arow = a1 + static_cast<std::size_t>(e) * t.in1_dim;
+        arow[u] = xa[0];
+        if constexpr (S::kIn1 == 4) {
+#pragma unroll
+            for (int a = 0; a < 3; ++a) arow[E + 3 * u + a] = xa[1 + a];
+        }
+        // sums over the receiver's channel lanes (aligned groups of E lanes)
+#pragma unroll
+        for (int b = 0; b < NY; ++b) {
+            float v = ya[b];
+            for (int off = E / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+            ya[b] = v;
+        }
+        for (int off = E / 2; off > 0; off >>= 1) cpart += __shfl_xor(cpart, off, kWave);
+        if (u == 0) {
+            float* yo = Yadj + static_cast<std::size_t>(e) * NY;
+#pragma unroll
+            for (int b = 0; b < NY; ++b) yo[b] += ya[b];
             const float dr = draw[e];
             const float base = tanhf(dr * dr);
             adraw[e] = ad * (1.0f - base * base) * 2.0f * dr * cf;
@@ -1025,7 +1217,7 @@ void Evaluator::upload_model() {
 
     struct InterOff {
         LinOff up[2], skip[2], res[2], lin1[2], lin2[2];
-        std::size_t tp_paths, tp_in1, tp_out, tp_ent, tp_val;
+        std::size_t tp_paths, tp_in1, tp_out, tp_ent, tp_val, tp_cval;
         MlpOff w, d;
         std::size_t g[9];
     };
@@ -1043,6 +1235,7 @@ void Evaluator::upload_model() {
         o.tp_out = pk.put(I.tp.out_slot);
         o.tp_ent = pk.put(I.tp.entries);
         o.tp_val = pk.put(I.tp.values);
+        o.tp_cval = pk.put(I.tp.compiled_values);
         o.w = put_mlp(I.weights_mlp);
         o.d = put_mlp(I.density_mlp);
         const GateTables& G = I.gate;
@@ -1116,7 +1309,8 @@ void Evaluator::upload_model() {
         d.lin1 = {lin(o.lin1[0]), lin(o.lin1[1])};
         d.lin2 = {lin(o.lin2[0]), lin(o.lin2[1])};
         d.tp = DTp{I.tp.channels, I.tp.in1_dim, I.tp.out_dim, I.tp.numel, I.tp.slots, I.tp.in1_per_channel,
-                   I.tp.num_paths, I_(o.tp_paths), I_(o.tp_in1), I_(o.tp_out), I_(o.tp_ent), F(o.tp_val)};
+                   I.tp.num_paths, I_(o.tp_paths), I_(o.tp_in1), I_(o.tp_out), I_(o.tp_ent), F(o.tp_val),
+                   I.tp.compiled, F(o.tp_cval)};
         d.wmlp = mlp(I.weights_mlp, o.w);
         d.dmlp = mlp(I.density_mlp, o.d);
         d.gate = DGate{I.gate.in_dim, I.gate.out_dim, I_(o.g[0]), I_(o.g[1]), F(o.g[2]), I_(o.g[3]),
@@ -1308,10 +1502,18 @@ void Evaluator::compute(int N, const int* types, const int* num_neigh, const int
                E, mlp_ld(I.wmlp), d_r, d_ts, d_tt, f(o.wraw), f(o.wtape));
         launch("mh1_mlp_forward", k_mlp_forward, blocks_for(E, 16 * WD), 64 * WD, mlp_lds(I.dmlp, WD), I.dmlp, rad_,
                E, mlp_ld(I.dmlp), d_r, d_ts, d_tt, f(o.draw), f(o.dtape));
-        const std::size_t tp_lds = static_cast<std::size_t>(I.tp.slots + I.tp.nin1) * kTpThreads * 4;
-        launch("mh1_tp_forward", k_tp_forward, blocks_for(static_cast<long long>(N) * I.tp.channels, kTpThreads),
-               kTpThreads, tp_lds, I.tp, N, d_off, d_src, f(o.up), Y, NY, f(o.wraw), cut_w, f(o.draw), f(o.msg),
-               f(o.dens));
+        const unsigned tpg = blocks_for(static_cast<long long>(N) * I.tp.channels, kTpThreads);
+        if (I.tp.compiled >= 0) {
+            auto kf = I.tp.compiled == 0 ? k_tp_forward_c<0, 2> : I.tp.compiled == 1 ? k_tp_forward_c<0, 3>
+                    : I.tp.compiled == 2 ? k_tp_forward_c<1, 2> : k_tp_forward_c<1, 3>;
+            launch("mh1_tp_forward", kf, tpg, kTpThreads, 0, I.tp, N, d_off, d_src, static_cast<const float*>(f(o.up)),
+                   static_cast<const float*>(Y), static_cast<const float*>(f(o.wraw)), cut_w,
+                   static_cast<const float*>(f(o.draw)), f(o.msg), f(o.dens));
+        } else {
+            const std::size_t tp_lds = static_cast<std::size_t>(I.tp.slots + I.tp.nin1) * kTpThreads * 4;
+            launch("mh1_tp_forward_table", k_tp_forward, tpg, kTpThreads, tp_lds, I.tp, N, d_off, d_src, f(o.up), Y, NY,
+                   f(o.wraw), cut_w, f(o.draw), f(o.msg), f(o.dens));
+        }
         launch_linear(I.lin1.fwd, N, f(o.msg), f(o.lin1), nullptr, false, "mh1_linear_1");
         launch("mh1_pregate", k_pregate, blocks_for(static_cast<long long>(N) * I.gate.in_dim, 256), 256, 0, N,
                I.gate.in_dim, f(o.lin1), f(o.res), f(o.dens), I.alpha, I.beta, f(o.pre));
@@ -1392,10 +1594,21 @@ void Evaluator::compute(int N, const int* types, const int* num_neigh, const int
                I.gate.in_dim, f(o.a_pre), f(o.lin1), f(o.dens), I.alpha, I.beta, f(o.a_lin), f(o.a_dens));
         launch_linear(I.lin1.rev, N, f(o.a_lin), f(o.a_msg), nullptr, false, "mh1_linear_1_reverse");
         launch_linear(I.res.rev, N, f(o.a_pre), f(o.a_up), nullptr, false, "mh1_linear_res_reverse");
-        const std::size_t tp_lds = static_cast<std::size_t>(I.tp.slots + 2 * I.tp.nin1 + NY) * kTpThreads * 4;
-        launch("mh1_tp_reverse", k_tp_reverse, blocks_for(static_cast<long long>(N) * I.tp.channels, kTpThreads),
-               kTpThreads, tp_lds, I.tp, N, d_off, d_src, f(o.up), Y, NY, f(o.wraw), cut_w, f(o.draw), f(o.a_msg),
-               f(o.a_dens), f(o.wadj), f(o.a1), Yadj, M.apply_cutoff ? nullptr : cadj, f(o.adraw));
+        const unsigned tpg = blocks_for(static_cast<long long>(N) * I.tp.channels, kTpThreads);
+        if (I.tp.compiled >= 0) {
+            auto kr = I.tp.compiled == 0 ? k_tp_reverse_c<0, 2> : I.tp.compiled == 1 ? k_tp_reverse_c<0, 3>
+                    : I.tp.compiled == 2 ? k_tp_reverse_c<1, 2> : k_tp_reverse_c<1, 3>;
+            launch("mh1_tp_reverse", kr, tpg, kTpThreads, 0, I.tp, N, d_off, d_src,
+                   static_cast<const float*>(f(o.up)), static_cast<const float*>(Y),
+                   static_cast<const float*>(f(o.wraw)), cut_w, static_cast<const float*>(f(o.draw)),
+                   static_cast<const float*>(f(o.a_msg)), static_cast<const float*>(f(o.a_dens)), f(o.wadj), f(o.a1),
+                   Yadj, M.apply_cutoff ? static_cast<float*>(nullptr) : cadj, f(o.adraw));
+        } else {
+            const std::size_t tp_lds = static_cast<std::size_t>(I.tp.slots + 2 * I.tp.nin1 + NY) * kTpThreads * 4;
+            launch("mh1_tp_reverse_table", k_tp_reverse, tpg, kTpThreads, tp_lds, I.tp, N, d_off, d_src, f(o.up), Y, NY,
+                   f(o.wraw), cut_w, f(o.draw), f(o.a_msg), f(o.a_dens), f(o.wadj), f(o.a1), Yadj,
+                   M.apply_cutoff ? nullptr : cadj, f(o.adraw));
+        }
         launch("mh1_gather_sources", k_gather_sources,
                blocks_for(static_cast<long long>(N) * I.tp.in1_dim, 256), 256, 0, N, I.tp.in1_dim, ip(o_toff),
                ip(o_tedge), f(o.a1), f(o.a_up));

@@ -11,6 +11,8 @@
 // facts mace_nonlinear_schema.cpp:108-207.
 #include "mh1_model.hpp"
 
+#include "mh1_paths.hpp"
+
 #include <algorithm>
 #include <cmath>
 #include <map>
@@ -271,6 +273,33 @@ MlpTables build_mlp(const Value& v, int radial, const std::vector<std::vector<do
     return T;
 }
 
+// Match the table-driven paths against a compiled family structure: same
+// paths in the same order, Wigner entries inside the compiled positions.
+template <int L1MAX, int LMAX>
+bool match_structure(TensorTables& T) {
+    using S = TpStructure<L1MAX, LMAX>;
+    if (T.num_paths != S::kPaths || T.slots != S::kSlots || T.in1_per_channel != S::kIn1) return false;
+    std::vector<float> vals(S::kEntries, 0.0f);
+    for (int p = 0; p < S::kPaths; ++p) {
+        const int* P = &T.paths[8 * p];
+        const TpPathC& c = S::paths[p];
+        if (P[0] != c.in_base || P[1] != 2 * c.l1 + 1 || P[2] != c.l2 * c.l2 || P[3] != c.out_base ||
+            P[4] != 2 * c.l3 + 1 || P[5] != p * T.channels)
+            return false;
+        for (int q = P[6]; q < P[6] + P[7]; ++q) {
+            const int a = T.entries[q] & 255, b = (T.entries[q] >> 8) & 255, k = T.entries[q] >> 16;
+            int hit = -1;
+            for (int j = c.first; j < c.first + c.count; ++j)
+                if (S::entries[j].a == a && S::entries[j].b == b && S::entries[j].k == k) hit = j;
+            if (hit < 0) return false;
+            vals[hit] = T.values[q];
+        }
+    }
+    T.compiled = 2 * L1MAX + (LMAX - 2);
+    T.compiled_values = vals;
+    return true;
+}
+
 TensorTables build_tp(const Value& v, int l_max) {
     TensorTables T;
     const Irreps in1(v.at("irreps_in1").as_string()), in2(v.at("irreps_in2").as_string()),
@@ -339,6 +368,13 @@ TensorTables build_tp(const Value& v, int l_max) {
         for (int a = 0; a < 2 * b.l + 1; ++a) T.in1_slot.insert(T.in1_slot.end(), {b.offset, 2 * b.l + 1, a});
     for (const Block& b : out.blocks)
         for (int k = 0; k < 2 * b.l + 1; ++k) T.out_slot.insert(T.out_slot.end(), {b.offset, 2 * b.l + 1, k});
+    const bool scalar_in = in1.blocks.size() == 1 && in1.blocks[0].l == 0 && in1.blocks[0].parity == 1;
+    const bool vector_in = in1.blocks.size() == 2 && in1.blocks[0].l == 0 && in1.blocks[0].parity == 1 &&
+                           in1.blocks[1].l == 1 && in1.blocks[1].parity == -1;
+    if (l_max == 2 && scalar_in) match_structure<0, 2>(T);
+    if (l_max == 3 && scalar_in) match_structure<0, 3>(T);
+    if (l_max == 2 && vector_in) match_structure<1, 2>(T);
+    if (l_max == 3 && vector_in) match_structure<1, 3>(T);
     return T;
 }
 

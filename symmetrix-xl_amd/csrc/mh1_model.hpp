@@ -87,6 +87,10 @@ struct TensorTables {
     std::vector<int> in1_slot, out_slot;  // 3 per slot: block offset, width, component
     std::vector<int> entries;      // a | b << 8 | k << 16
     std::vector<float> values;     // Wigner value x path weight
+    // a compiled family structure (mh1_paths.hpp): 2 * L1MAX + (l_max - 2), or -1; its values in the
+    // structure's entry order (x path weight, 0 where the file has no entry)
+    int compiled = -1;
+    std::vector<float> compiled_values;
 };
 
 struct GateTables {

@@ -68,6 +68,9 @@ class MH1Config:
     agnesi: bool = False
     zbl: bool = False
     linear_bias: bool = False
+    # highest l of the first interaction's output (the MH-1 family has 1;
+    # 2 gives a convolution structure outside the family's compiled ones)
+    hidden_lmax: int = 1
     seed: int = 0
 
 
@@ -76,6 +79,7 @@ MH1_CONFIGS = {
     "mh1_tiny_l3": MH1Config("mh1_tiny_l3", l_max=3, node_channels=8, edge_channels=8, seed=1),
     "mh1_tiny_raw": MH1Config("mh1_tiny_raw", apply_cutoff=False, agnesi=True, zbl=True, linear_bias=True,
                               seed=2),
+    "mh1_tiny_l2e": MH1Config("mh1_tiny_l2e", node_channels=8, edge_channels=4, hidden_lmax=2, seed=4),
     # channel counts of the MH-1 family's small members
     "mh1_medium": MH1Config("mh1_medium", node_channels=64, edge_channels=32, l_max=3,
                             atomic_numbers=[1, 6, 7, 8, 13, 14, 22, 26, 29, 38], r_cut=6.0,
@@ -247,9 +251,10 @@ def gate(C, l_max):
 
 def interaction(rng, cfg, layer, num_elements):
     C, E, l = cfg.node_channels, cfg.edge_channels, cfg.l_max
-    node = [(C, 0, 1)] if layer == 0 else [(C, 0, 1), (C, 1, -1)]
-    edge = [(E, 0, 1)] if layer == 0 else [(E, 0, 1), (E, 1, -1)]
-    hidden = [(C, 0, 1), (C, 1, -1)] if layer == 0 else [(C, 0, 1)]
+    vec = [(C, l, (-1) ** l) for l in range(cfg.hidden_lmax + 1)]
+    node = [(C, 0, 1)] if layer == 0 else vec
+    edge = [(E, 0, 1)] if layer == 0 else [(E, l, (-1) ** l) for l in range(cfg.hidden_lmax + 1)]
+    hidden = vec if layer == 0 else [(C, 0, 1)]
     full = _full(C, l)
     gate_in = _full(C, l, l + 1)
     tp, msg_blocks, numel = conv_tp(edge, l)
@@ -280,7 +285,7 @@ def generate_mh1(cfg, seed=None):
     Z = list(cfg.atomic_numbers)
     n_el = len(Z)
     C, l = cfg.node_channels, cfg.l_max
-    hidden = [[(C, 0, 1), (C, 1, -1)], [(C, 0, 1)]]
+    hidden = [[(C, l, (-1) ** l) for l in range(cfg.hidden_lmax + 1)], [(C, 0, 1)]]
     model = {
         "symmetrix_format_version": 4, "model_type": "MACE_Nonlinear", "head": None,
         "atomic_numbers": Z, "model_atomic_numbers": Z, "model_indices": list(range(n_el)),

@@ -19,7 +19,10 @@ from symmetrix import random_mh1, systems
 
 pytestmark = pytest.mark.gpu
 
-TINY = ["mh1_tiny", "mh1_tiny_l3", "mh1_tiny_raw"]
+# mh1_tiny_l2e (2e node and edge features in the second interaction) is
+# outside the family's compiled convolution structures: its convolutions run
+# the table-driven kernels
+TINY = ["mh1_tiny", "mh1_tiny_l3", "mh1_tiny_raw", "mh1_tiny_l2e"]
 
 
 @pytest.fixture(scope="module")
@@ -236,3 +239,20 @@ def test_mh1_calculator_open_cluster(paths):
     e, F, _ = _oracle_system(model, pos, np.eye(3), [False] * 3, types)
     assert abs(res["energy"] - e) / len(pos) < 1e-5
     assert np.abs(res["forces"] - F).max() < 1e-4
+
+
+def test_mh1_convolution_kernel_choice(paths):
+    """Family convolutions run the compiled-structure kernels; a structure
+    outside them (2e edge features) runs the table-driven ones."""
+    from symmetrix.mace_nonlinear import MACENonlinearKokkosFloat
+    for name, table in (("mh1_tiny_l3", False), ("mh1_tiny_l2e", True)):
+        model = mo.MH1Oracle(paths[name])
+        pos, cell, types = _random_system(model, 12, 6.0, seed=13)
+        g, xyz, r = _graph(model, pos, cell)
+        ev = MACENonlinearKokkosFloat(paths[name])
+        ev._set_kernel_timing(True)
+        ev.compute_node_energies_forces(len(types), types, g["num_neigh"], g["sources"], types[g["sources"]], xyz, r)
+        names = set(ev._kernel_timing())
+        assert ("mh1_tp_forward_table" in names) == table
+        assert ("mh1_tp_reverse_table" in names) == table
+        assert "mh1_tp_forward" in names if not table else True

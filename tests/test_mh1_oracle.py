@@ -29,7 +29,7 @@ from oracle import mh1_oracle as mo
 from oracle import oracle
 from symmetrix import e3, random_mh1
 
-MODELS = ["mh1_tiny", "mh1_tiny_raw", "mh1_tiny_l3"]
+MODELS = ["mh1_tiny", "mh1_tiny_raw", "mh1_tiny_l3", "mh1_tiny_l2e"]
 
 
 @pytest.fixture(scope="module")
