@@ -278,26 +278,40 @@ __device__ __forceinline__ void tile_gemm(const float* A, int lda, int a_rows, i
     }
 }
 
-// Row statistics of a LayerNorm over the tile's rows (one thread per row).
-__device__ __forceinline__ void ln_stats(const float* x, int ldx, int w, int ne, float eps, float* stats) {
-    for (int e = threadIdx.x; e < ne; e += blockDim.x) {
-        const float* s = x + static_cast<std::size_t>(e) * ldx;
-        float mean = 0.0f;
-        for (int k = 0; k < w; ++k) mean += s[k];
-        mean /= w;
-        float var = 0.0f;
-        for (int k = 0; k < w; ++k) var += (s[k] - mean) * (s[k] - mean);
-        var /= w;
-        stats[2 * e] = mean;
-        stats[2 * e + 1] = 1.0f / sqrtf(var + eps);
+// Sum over the four lanes that share a tile row (rows = blockDim / 4).
+__device__ __forceinline__ float row4_sum(float v) {
+    v += __shfl_xor(v, 1, kWave);
+    v += __shfl_xor(v, 2, kWave);
+    return v;
+}
+
+// Mean and 1/std of each tile row of x (LDS, row stride ld), four lanes per
+// row: every lane of the row gets them in mean/rs, lane 0 also stores them.
+__device__ __forceinline__ void ln_stats(const float* x, int ld, int w, int ne, float eps, float* stats, float& mean_out,
+                                         float& rs_out) {
+    const int row = threadIdx.x >> 2, j = threadIdx.x & 3;
+    const float* xr = x + row * ld;
+    float s = 0.0f;
+    if (row < ne)
+        for (int k = j; k < w; k += 4) s += xr[k];
+    const float mean = row4_sum(s) / w;
+    float v = 0.0f;
+    if (row < ne)
+        for (int k = j; k < w; k += 4) v += (xr[k] - mean) * (xr[k] - mean);
+    v = row4_sum(v) / w;
+    mean_out = mean;
+    rs_out = 1.0f / sqrtf(v + eps);
+    if (j == 0) {
+        stats[2 * row] = mean;
+        stats[2 * row + 1] = rs_out;
     }
 }
 
 // Forward of an affine MLP over tiles of 16*waves edges: linear layers on
 // MFMA, LayerNorm and SiLU as passes over the tile in LDS (two buffers of row
-// stride ld).  Every layer but the last also writes its output to the edge's
-// tape row (the reverse reads the LayerNorm and SiLU inputs from there); the
-// last layer writes out [E][out_dim].
+// stride ld).  A layer's output that feeds a LayerNorm or SiLU also goes to
+// the tape ([E][width] blocks, layer-major) for the reverse; the last layer
+// writes out [E][out_dim].
 __global__ __launch_bounds__(256) void k_mlp_forward(const DMlp m, const DRadial rd, long long E, int ld,
                                                      const double* __restrict__ r, const int* __restrict__ ets,
                                                      const int* __restrict__ ett, float* __restrict__ out,
@@ -318,7 +332,7 @@ __global__ __launch_bounds__(256) void k_mlp_forward(const DMlp m, const DRadial
     for (int L = 0; L < m.num_layers; ++L) {
         const int type = m.layers[4 * L], in = m.layers[4 * L + 1], w = m.layers[4 * L + 2], off = m.layers[4 * L + 3];
         const bool last = L == m.num_layers - 1;
-        float* trow = tape + m.tape_offset[L];
+        float* tl = m.tape_offset[L] >= 0 ? tape + static_cast<std::size_t>(m.tape_offset[L]) * E + e0 * w : nullptr;
         if (type == 0) {
             const float* WT = m.params + m.wt_offset[L];
             const float* bias = m.params + off + static_cast<std::size_t>(w) * in;
@@ -334,7 +348,7 @@ __global__ __launch_bounds__(256) void k_mlp_forward(const DMlp m, const DRadial
                     out[(e0 + row) * w + c] = v;
                 } else {
                     b[row * ld + c] = v;
-                    trow[(e0 + row) * m.tape_width + c] = v;
+                    if (tl) tl[row * w + c] = v;
                 }
             });
             float* t = a;
@@ -343,23 +357,23 @@ __global__ __launch_bounds__(256) void k_mlp_forward(const DMlp m, const DRadial
         } else if (type == 1) {
             const float* g = m.params + off;
             const float* bb = g + w;
-            ln_stats(a, ld, w, ne, m.eps[L], stats);
+            float mean_r, rs_r;
+            ln_stats(a, ld, w, ne, m.eps[L], stats, mean_r, rs_r);
             __syncthreads();
             for (int idx = threadIdx.x; idx < ne * w; idx += blockDim.x) {
                 const int e = idx / w, j = idx % w;
                 const float v = (a[e * ld + j] - stats[2 * e]) * stats[2 * e + 1] * g[j] + bb[j];
                 b[e * ld + j] = v;
-                trow[(e0 + e) * m.tape_width + j] = v;
+                if (tl) tl[idx] = v;
             }
             float* t = a;
             a = b;
             b = t;
         } else {
             for (int idx = threadIdx.x; idx < ne * w; idx += blockDim.x) {
-                const int e = idx / w, j = idx % w;
-                float* p = a + e * ld + j;
+                float* p = a + (idx / w) * ld + idx % w;
                 *p = *p * sigmoidf_(*p);
-                trow[(e0 + e) * m.tape_width + j] = *p;
+                if (tl) tl[idx] = *p;
             }
         }
         __syncthreads();
@@ -367,8 +381,9 @@ __global__ __launch_bounds__(256) void k_mlp_forward(const DMlp m, const DRadial
 }
 
 // Reverse of an affine MLP: gout [E][out_dim] pulled back through the layers
-// (linear layers on MFMA with the row-major weights as B, LayerNorm and SiLU
-// from the forward's tape) to the radial features: rad_adj [E][nb] +=.
+// (linear layers on MFMA with the row-major weights as B; LayerNorm and SiLU
+// from their inputs on the tape, staged in LDS) to the radial features:
+// rad_adj [E][nb] +=.
 __global__ __launch_bounds__(256) void k_mlp_reverse(const DMlp m, const DRadial rd, long long E, int ld,
                                                      const float* __restrict__ tape, const float* __restrict__ gout,
                                                      float* __restrict__ rad_adj) {
@@ -376,10 +391,10 @@ __global__ __launch_bounds__(256) void k_mlp_reverse(const DMlp m, const DRadial
     const int rows = blockDim.x / 4;
     float* g = lds;
     float* h = lds + rows * ld;
-    float* stats = lds + 2 * rows * ld;
+    float* x = lds + 2 * rows * ld;
+    float* stats = lds + 3 * rows * ld;
     const long long e0 = static_cast<long long>(blockIdx.x) * rows;
     const int ne = static_cast<int>(min(static_cast<long long>(rows), E - e0));
-    int cur_w = m.layers[4 * (m.num_layers - 1) + 2];
     bool from_gout = true;
     for (int L = m.num_layers - 1; L >= 0; --L) {
         const int type = m.layers[4 * L], in = m.layers[4 * L + 1], w = m.layers[4 * L + 2], off = m.layers[4 * L + 3];
@@ -395,45 +410,54 @@ __global__ __launch_bounds__(256) void k_mlp_reverse(const DMlp m, const DRadial
                 }
             });
             from_gout = false;
-            cur_w = in;
-        } else if (type == 1) {
-            // input of this layer = output of layer L-1 (tape)
-            const float* x = tape + m.tape_offset[L - 1];
-            const float* gam = m.params + off;
-            for (int e = threadIdx.x; e < ne; e += blockDim.x) {
-                const float* xs = x + (e0 + e) * m.tape_width;
-                float mean = 0.0f;
-                for (int k = 0; k < w; ++k) mean += xs[k];
-                mean /= w;
-                float var = 0.0f;
-                for (int k = 0; k < w; ++k) var += (xs[k] - mean) * (xs[k] - mean);
-                var /= w;
-                const float rs = 1.0f / sqrtf(var + m.eps[L]);
-                float mg = 0.0f, mgx = 0.0f;
-                for (int k = 0; k < w; ++k) {
-                    const float gh = g[e * ld + k] * gam[k];
-                    mg += gh;
-                    mgx += gh * (xs[k] - mean) * rs;
-                }
-                mg /= w;
-                mgx /= w;
-                for (int k = 0; k < w; ++k)
-                    h[e * ld + k] = rs * (g[e * ld + k] * gam[k] - mg - (xs[k] - mean) * rs * mgx);
-            }
-            for (int idx = threadIdx.x; idx < (rows - ne) * w; idx += blockDim.x)
-                h[(ne + idx / w) * ld + idx % w] = 0.0f;
-            (void)stats;
         } else {
-            const float* x = tape + m.tape_offset[L - 1];
-            for (int idx = threadIdx.x; idx < rows * w; idx += blockDim.x) {
-                const int e = idx / w, k = idx % w;
-                float v = 0.0f;
-                if (e < ne) {
-                    const float xv = x[(e0 + e) * m.tape_width + k];
-                    const float sg = sigmoidf_(xv);
-                    v = g[e * ld + k] * (sg + xv * sg * (1.0f - sg));
+            // this layer's input is layer L-1's output, kept on the tape
+            const float* tin = tape + static_cast<std::size_t>(m.tape_offset[L - 1]) * E + e0 * w;
+            for (int idx = threadIdx.x; idx < ne * w; idx += blockDim.x) x[(idx / w) * ld + idx % w] = tin[idx];
+            __syncthreads();
+            if (type == 1) {
+                const float* gam = m.params + off;
+                float mean, rs;
+                ln_stats(x, ld, w, ne, m.eps[L], stats, mean, rs);
+                // row means of g*gamma and g*gamma*xhat (four lanes per row)
+                const int row = threadIdx.x >> 2, j = threadIdx.x & 3;
+                float mg = 0.0f, mgx = 0.0f;
+                if (row < ne) {
+                    for (int k = j; k < w; k += 4) {
+                        const float gh = g[row * ld + k] * gam[k];
+                        mg += gh;
+                        mgx += gh * (x[row * ld + k] - mean) * rs;
+                    }
                 }
-                h[e * ld + k] = v;
+                mg = row4_sum(mg) / w;
+                mgx = row4_sum(mgx) / w;
+                __syncthreads();
+                if (j == 0) {
+                    stats[4 * rows + 2 * row] = mg;
+                    stats[4 * rows + 2 * row + 1] = mgx;
+                }
+                __syncthreads();
+                for (int idx = threadIdx.x; idx < rows * w; idx += blockDim.x) {
+                    const int e = idx / w, k = idx % w;
+                    float v = 0.0f;
+                    if (e < ne) {
+                        const float rs = stats[2 * e + 1];
+                        const float xh = (x[e * ld + k] - stats[2 * e]) * rs;
+                        v = rs * (g[e * ld + k] * gam[k] - stats[4 * rows + 2 * e] - xh * stats[4 * rows + 2 * e + 1]);
+                    }
+                    h[e * ld + k] = v;
+                }
+            } else {
+                for (int idx = threadIdx.x; idx < rows * w; idx += blockDim.x) {
+                    const int e = idx / w, k = idx % w;
+                    float v = 0.0f;
+                    if (e < ne) {
+                        const float xv = x[e * ld + k];
+                        const float sg = sigmoidf_(xv);
+                        v = g[e * ld + k] * (sg + xv * sg * (1.0f - sg));
+                    }
+                    h[e * ld + k] = v;
+                }
             }
         }
         __syncthreads();
@@ -441,7 +465,6 @@ __global__ __launch_bounds__(256) void k_mlp_reverse(const DMlp m, const DRadial
         g = h;
         h = t;
     }
-    (void)cur_w;
 }
 
 // Convolution into receivers: msg[i][(block, u, k)] = sum over the receiver's
@@ -1347,16 +1370,19 @@ void Evaluator::launch_linear(const DLinear& op, int N, const float* x, float* y
 // bank conflicts at most on the MFMA A reads)
 int mlp_ld(const DMlp& m) { return ((m.width + 3) / 4) * 4 + 4; }
 
-std::size_t mlp_lds(const DMlp& m, int waves) {
+// forward: two tile buffers and row statistics; reverse: three buffers (the
+// adjoint, the next adjoint, the staged tape input) and four statistics per row
+std::size_t mlp_lds(const DMlp& m, int waves, bool reverse) {
     const int rows = 16 * waves;
-    return static_cast<std::size_t>(2 * rows * mlp_ld(m) + 2 * rows) * sizeof(float);
+    return static_cast<std::size_t>((reverse ? 3 : 2) * rows * mlp_ld(m) + 6 * rows) * sizeof(float);
 }
 
-// waves per tile workgroup: four unless the buffers exceed the LDS budget
+// waves per tile workgroup: four unless the reverse's buffers exceed the LDS budget
 int mlp_waves(const DMlp& m) {
     int w = 4;
-    while (w > 1 && mlp_lds(m, w) > kMaxLds) w /= 2;
-    if (mlp_lds(m, w) > kMaxLds) throw std::domain_error("MH-1 model: an edge MLP layer is too wide for the LDS tile");
+    while (w > 1 && mlp_lds(m, w, true) > kMaxLds) w /= 2;
+    if (mlp_lds(m, w, true) > kMaxLds)
+        throw std::domain_error("MH-1 model: an edge MLP layer is too wide for the LDS tile");
     return w;
 }
 
@@ -1498,10 +1524,10 @@ void Evaluator::compute(int N, const int* types, const int* num_neigh, const int
         launch_linear(I.res.fwd, N, f(o.up), f(o.res), nullptr, false, "mh1_linear_res");
         launch_linear(I.skip.fwd, N, feats, f(o.skip), nullptr, false, "mh1_linear_skip");
         const int WW = mlp_waves(I.wmlp), WD = mlp_waves(I.dmlp);
-        launch("mh1_mlp_forward", k_mlp_forward, blocks_for(E, 16 * WW), 64 * WW, mlp_lds(I.wmlp, WW), I.wmlp, rad_,
-               E, mlp_ld(I.wmlp), d_r, d_ts, d_tt, f(o.wraw), f(o.wtape));
-        launch("mh1_mlp_forward", k_mlp_forward, blocks_for(E, 16 * WD), 64 * WD, mlp_lds(I.dmlp, WD), I.dmlp, rad_,
-               E, mlp_ld(I.dmlp), d_r, d_ts, d_tt, f(o.draw), f(o.dtape));
+        launch("mh1_mlp_forward", k_mlp_forward, blocks_for(E, 16 * WW), 64 * WW, mlp_lds(I.wmlp, WW, false), I.wmlp,
+               rad_, E, mlp_ld(I.wmlp), d_r, d_ts, d_tt, f(o.wraw), f(o.wtape));
+        launch("mh1_mlp_forward", k_mlp_forward, blocks_for(E, 16 * WD), 64 * WD, mlp_lds(I.dmlp, WD, false), I.dmlp,
+               rad_, E, mlp_ld(I.dmlp), d_r, d_ts, d_tt, f(o.draw), f(o.dtape));
         const unsigned tpg = blocks_for(static_cast<long long>(N) * I.tp.channels, kTpThreads);
         if (I.tp.compiled >= 0) {
             auto kf = I.tp.compiled == 0 ? k_tp_forward_c<0, 2> : I.tp.compiled == 1 ? k_tp_forward_c<0, 3>
@@ -1613,10 +1639,10 @@ void Evaluator::compute(int N, const int* types, const int* num_neigh, const int
                blocks_for(static_cast<long long>(N) * I.tp.in1_dim, 256), 256, 0, N, I.tp.in1_dim, ip(o_toff),
                ip(o_tedge), f(o.a1), f(o.a_up));
         const int WW = mlp_waves(I.wmlp), WD = mlp_waves(I.dmlp);
-        launch("mh1_mlp_reverse", k_mlp_reverse, blocks_for(E, 16 * WW), 64 * WW, mlp_lds(I.wmlp, WW), I.wmlp, rad_,
-               E, mlp_ld(I.wmlp), f(o.wtape), f(o.wadj), radadj);
-        launch("mh1_mlp_reverse", k_mlp_reverse, blocks_for(E, 16 * WD), 64 * WD, mlp_lds(I.dmlp, WD), I.dmlp, rad_,
-               E, mlp_ld(I.dmlp), f(o.dtape), f(o.adraw), radadj);
+        launch("mh1_mlp_reverse", k_mlp_reverse, blocks_for(E, 16 * WW), 64 * WW, mlp_lds(I.wmlp, WW, true), I.wmlp,
+               rad_, E, mlp_ld(I.wmlp), f(o.wtape), f(o.wadj), radadj);
+        launch("mh1_mlp_reverse", k_mlp_reverse, blocks_for(E, 16 * WD), 64 * WD, mlp_lds(I.dmlp, WD, true), I.dmlp,
+               rad_, E, mlp_ld(I.dmlp), f(o.dtape), f(o.adraw), radadj);
         if (k > 0) {
             // a_feat[k-1] += up^T(a_up) + skip^T(a_skip), a_skip = a_feat[k] when the product has a skip
             float* prev = f(lo[k - 1].a_feat);

@@ -267,8 +267,10 @@ MlpTables build_mlp(const Value& v, int radial, const std::vector<std::vector<do
         } else {
             T.wt_offset.push_back(-1);
         }
-        T.tape_offset.push_back(k + 1 < T.num_layers ? T.tape_width : -1);
-        if (k + 1 < T.num_layers) T.tape_width += L[2];
+        // the reverse needs a layer's output only as the input of a LayerNorm or SiLU
+        const bool keep = k + 1 < T.num_layers && T.layers[4 * (k + 1)] != 0;
+        T.tape_offset.push_back(keep ? T.tape_width : -1);
+        if (keep) T.tape_width += L[2];
     }
     return T;
 }

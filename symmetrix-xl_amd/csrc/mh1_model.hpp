@@ -74,7 +74,9 @@ struct MlpTables {
     int radial = 0, first_width = 0, out_dim = 0, max_hidden = 0, num_layers = 0;
     std::vector<float> type_rows;  // [2][num_types][first_width]: source rows (+ bias), target rows
     // per layer: offset of a linear's transposed weights [in][out] in params (-1 otherwise), and of
-    // the layer's output in a per-edge tape row (-1 for the last layer); tape_width floats per edge
+    // the layer's output in the tape (kept only when a LayerNorm or SiLU follows; -1 otherwise): the
+    // tape is layer-major, the kept layer's [E][width] block at tape_offset * E; tape_width floats
+    // per edge in all
     std::vector<int> wt_offset, tape_offset;
     int tape_width = 0;
 };
