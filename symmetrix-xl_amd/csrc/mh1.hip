@@ -55,6 +55,8 @@ constexpr std::size_t kMaxLds = 60 * 1024;
 
 // ------------------------------------------------------------- device views
 
+constexpr int kLinearMaxBlocks = 32;
+
 struct DLinear {
     int in_dim, out_dim;
     const int* instr;
@@ -64,6 +66,10 @@ struct DLinear {
     const float* bias;
     const float* out_mask;
     const float* in_mask;
+    // output blocks (offset, multiplicity, width) for the MFMA form; nblk 0 when there are more than
+    // kLinearMaxBlocks (the per-element kernel runs)
+    int nblk;
+    int blk_off[kLinearMaxBlocks], blk_mul[kLinearMaxBlocks], blk_d[kLinearMaxBlocks];
 };
 
 struct DMlp {
@@ -120,6 +126,8 @@ struct DZbl {
     double c[4];
     int p;
 };
+
+typedef float v4f __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
 
@@ -230,13 +238,78 @@ __global__ __launch_bounds__(256) void k_linear(const DLinear op, int N, const f
         y[t] = acc;
 }
 
+// The same linear on MFMA (v_mfma_f32_16x16x4_f32): one wave per tile of 16
+// rows (node, component) x 64 output channels of one output block; K runs
+// over the input channels of every instruction into that block.  Tiles are
+// numbered block by block (rows, then column blocks).
+__global__ __launch_bounds__(64) void k_linear_mfma(const DLinear op, int N, const float* __restrict__ x,
+                                                    float* __restrict__ y, const float* __restrict__ addend,
+                                                    int accumulate) {
+    long long t = blockIdx.x;
+    int b = 0;
+    for (; b < op.nblk; ++b) {
+        const long long cnt = ((static_cast<long long>(N) * op.blk_d[b] + 15) / 16) * ((op.blk_mul[b] + 63) / 64);
+        if (t < cnt) break;
+        t -= cnt;
+    }
+    if (b == op.nblk) return;
+    const int d = op.blk_d[b], mul = op.blk_mul[b], boff = op.blk_off[b];
+    const int ctiles = (mul + 63) / 64;
+    const long long R = static_cast<long long>(N) * d;
+    const long long row0 = (t / ctiles) * 16;
+    const int col0 = static_cast<int>(t % ctiles) * 64;
+    const int lane = threadIdx.x, r = lane & 15, kg = lane >> 4;
+    const long long row = row0 + r;
+    const bool rok = row < R;
+    const int n = rok ? static_cast<int>(row / d) : 0, m = rok ? static_cast<int>(row % d) : 0;
+    v4f acc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int q = op.block_first[b]; q < op.block_first[b + 1]; ++q) {
+        const int* I = op.instr + 6 * q;
+        const int in_off = I[0] + m, mul_in = I[1], w_off = I[3];
+        const float* xr = x + static_cast<std::size_t>(n) * op.in_dim + in_off;
+        for (int k0 = 0; k0 < mul_in; k0 += 4) {
+            const int u = k0 + kg;
+            float a = 0.0f;
+            if (rok && u < mul_in) {
+                a = xr[u * d];
+                if (op.in_mask) a *= op.in_mask[in_off + u * d];
+            }
+            const float* wr = op.W + w_off + static_cast<std::size_t>(u) * mul;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int c = col0 + 16 * j + r;
+                const float bv = (u < mul_in && c < mul) ? wr[c] : 0.0f;
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, bv, acc[j], 0, 0, 0);
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int c = col0 + 16 * j + r;
+        if (c >= mul) continue;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const long long rr = row0 + 4 * kg + v;
+            if (rr >= R) continue;
+            const int nn = static_cast<int>(rr / d), mm = static_cast<int>(rr % d);
+            const int jo = boff + c * d + mm;
+            const std::size_t idx = static_cast<std::size_t>(nn) * op.out_dim + jo;
+            float val = acc[j][v];
+            if (op.bias) val += op.bias[jo];
+            if (op.out_mask) val *= op.out_mask[jo];
+            if (addend) val += addend[idx];
+            y[idx] = accumulate ? y[idx] + val : val;
+        }
+    }
+}
+
 __device__ __forceinline__ void mlp_first_inputs(const DRadial& rd, double r, int ts, int tt, float* row) {
     double f[32], env, denv;
     radial_eval(rd, r, ts, tt, f, nullptr, env, denv);
     for (int k = 0; k < rd.nb; ++k) row[k] = static_cast<float>(f[k]);
 }
-
-typedef float v4f __attribute__((ext_vector_type(4)));
 
 // Edge-tile GEMM on MFMA (v_mfma_f32_16x16x4_f32): wave w of the workgroup
 // owns rows 16w..16w+15 of the tile; D[row][c] = sum_k A[row][k] B(k, c) with
@@ -1183,11 +1256,12 @@ void Evaluator::upload_model() {
         std::size_t instr, bf, elem, W, bias, om, im;
         bool has_bias, has_om, has_im;
         int in_dim, out_dim;
+        std::vector<int> blocks;
     };
     auto put_lin = [&](const LinearTables& T) {
         return LinOff{pk.put(T.instr), pk.put(T.block_first), pk.put(T.elem), pk.put(T.weights), pk.put(T.bias),
                       pk.put(T.out_mask), pk.put(T.in_mask), !T.bias.empty(), !T.out_mask.empty(),
-                      !T.in_mask.empty(), T.in_dim, T.out_dim};
+                      !T.in_mask.empty(), T.in_dim, T.out_dim, T.out_blocks};
     };
     struct MlpOff {
         std::size_t layers, eps, params, rows, wt, tape;
@@ -1297,8 +1371,19 @@ void Evaluator::upload_model() {
     auto F = [&](std::size_t o) { return reinterpret_cast<const float*>(base + o); };
     auto I_ = [&](std::size_t o) { return reinterpret_cast<const int*>(base + o); };
     auto lin = [&](const LinOff& o) {
-        return DLinear{o.in_dim, o.out_dim, I_(o.instr), I_(o.bf), I_(o.elem), F(o.W),
-                       o.has_bias ? F(o.bias) : nullptr, o.has_om ? F(o.om) : nullptr, o.has_im ? F(o.im) : nullptr};
+        DLinear d{o.in_dim, o.out_dim, I_(o.instr), I_(o.bf), I_(o.elem), F(o.W),
+                  o.has_bias ? F(o.bias) : nullptr, o.has_om ? F(o.om) : nullptr, o.has_im ? F(o.im) : nullptr,
+                  0, {}, {}, {}};
+        const int nb = static_cast<int>(o.blocks.size() / 3);
+        if (nb <= kLinearMaxBlocks) {
+            d.nblk = nb;
+            for (int b = 0; b < nb; ++b) {
+                d.blk_off[b] = o.blocks[3 * b];
+                d.blk_mul[b] = o.blocks[3 * b + 1];
+                d.blk_d[b] = o.blocks[3 * b + 2];
+            }
+        }
+        return d;
     };
     auto mlp = [&](const MlpTables& T, const MlpOff& o) {
         return DMlp{T.num_layers, T.radial, T.first_width, nt, T.max_hidden, T.tape_width, I_(o.layers), F(o.eps),
@@ -1362,8 +1447,16 @@ void Evaluator::upload_model() {
 
 void Evaluator::launch_linear(const DLinear& op, int N, const float* x, float* y, const float* addend,
                               bool accumulate, const char* name) {
-    launch(name, k_linear, blocks_for(static_cast<long long>(N) * op.out_dim, 256), 256, 0, op, N, x, y, addend,
-           accumulate ? 1 : 0);
+    if (op.nblk == 0) {
+        launch(name, k_linear, blocks_for(static_cast<long long>(N) * op.out_dim, 256), 256, 0, op, N, x, y, addend,
+               accumulate ? 1 : 0);
+        return;
+    }
+    long long tiles = 0;
+    for (int b = 0; b < op.nblk; ++b)
+        tiles += ((static_cast<long long>(N) * op.blk_d[b] + 15) / 16) * ((op.blk_mul[b] + 63) / 64);
+    if (tiles > 0x7fffffffLL) throw std::invalid_argument("MH-1: linear too large for one launch");
+    launch(name, k_linear_mfma, static_cast<unsigned>(tiles), 64, 0, op, N, x, y, addend, accumulate ? 1 : 0);
 }
 
 // row stride of an MLP tile buffer: the widest layer plus 4 (two-way LDS

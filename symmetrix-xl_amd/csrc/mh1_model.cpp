@@ -99,6 +99,7 @@ void build_linear(Linear& L, const std::vector<std::array<int, 2>>& pairs, const
         T.block_first[T.num_out_blocks] = static_cast<int>(T.instr.size() / 6);
         for (int ob = 0; ob < T.num_out_blocks; ++ob) {
             const Block& c = O.blocks[ob];
+            T.out_blocks.insert(T.out_blocks.end(), {c.offset, c.mul, 2 * c.l + 1});
             for (int ch = 0; ch < c.mul; ++ch)
                 for (int m = 0; m < 2 * c.l + 1; ++m) T.elem.insert(T.elem.end(), {ob, ch, m});
         }

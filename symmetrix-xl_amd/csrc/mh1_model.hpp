@@ -53,6 +53,7 @@ struct LinearTables {
     std::vector<int> instr;        // 6 per instruction: in_off, mul_in, d, w_off, out_off, mul_out
     std::vector<int> block_first;  // [num_out_blocks + 1]
     std::vector<int> elem;         // 3 per output element: block, channel, component
+    std::vector<int> out_blocks;   // 3 per output block: offset, multiplicity, width 2l+1
     std::vector<float> weights;    // path weight folded in
     std::vector<float> bias;       // empty or [out_dim]
     std::vector<float> out_mask;   // empty (all ones) or [out_dim]
