@@ -181,10 +181,29 @@ __device__ void radial_eval(const DRadial& rd, double r, int ts, int tt, double*
 
 // ---------------------------------------------------------------- kernels
 
+// radial features of one edge straight into out[0..nb) (FP64 arithmetic)
+__device__ __forceinline__ void radial_features_to(const DRadial& rd, double r, int ts, int tt, float* out) {
+    double env, denv;
+    envelope(rd, r, env, denv);
+    double t = r;
+    if (rd.agnesi) {
+        const double r0 = rd.r0[ts * rd.num_types + tt];
+        const double u = r / r0;
+        t = 1.0 / (1.0 + rd.a * pow(u, rd.q) / (1.0 + pow(u, rd.q - rd.pp)));
+    }
+    for (int k = 0; k < rd.nb; ++k) {
+        const double base = rd.prefactor * sin(rd.bessel[k] * t) / t;
+        out[k] = static_cast<float>(rd.apply_cutoff ? base * env : base);
+    }
+}
+
+// Per edge: harmonics, cutoff and the radial features the edge MLPs share.
 template <int LMAX>
 __global__ __launch_bounds__(256) void k_geometry(long long E, const double* __restrict__ xyz,
                                                   const double* __restrict__ r, const DRadial rd,
-                                                  float* __restrict__ Y, float* __restrict__ cut) {
+                                                  const int* __restrict__ ets, const int* __restrict__ ett,
+                                                  float* __restrict__ Y, float* __restrict__ cut,
+                                                  float* __restrict__ rad) {
     constexpr int NY = (LMAX + 1) * (LMAX + 1);
     const long long e = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
     if (e >= E) return;
@@ -196,6 +215,7 @@ __global__ __launch_bounds__(256) void k_geometry(long long E, const double* __r
     double env = 0.0, denv = 0.0;
     envelope(rd, r[e], env, denv);
     cut[e] = static_cast<float>(env);
+    radial_features_to(rd, r[e], ets[e], ett[e], rad + e * rd.nb);
 }
 
 // node features of the embedding: one row per type
@@ -305,12 +325,6 @@ __global__ __launch_bounds__(64) void k_linear_mfma(const DLinear op, int N, con
     }
 }
 
-__device__ __forceinline__ void mlp_first_inputs(const DRadial& rd, double r, int ts, int tt, float* row) {
-    double f[32], env, denv;
-    radial_eval(rd, r, ts, tt, f, nullptr, env, denv);
-    for (int k = 0; k < rd.nb; ++k) row[k] = static_cast<float>(f[k]);
-}
-
 // Edge-tile GEMM on MFMA (v_mfma_f32_16x16x4_f32): wave w of the workgroup
 // owns rows 16w..16w+15 of the tile; D[row][c] = sum_k A[row][k] B(k, c) with
 // A in LDS (row stride lda) or global memory, B(k, c) = B[k * ldb + c] in
@@ -386,7 +400,7 @@ __device__ __forceinline__ void ln_stats(const float* x, int ld, int w, int ne, 
 // the tape ([E][width] blocks, layer-major) for the reverse; the last layer
 // writes out [E][out_dim].
 __global__ __launch_bounds__(256) void k_mlp_forward(const DMlp m, const DRadial rd, long long E, int ld,
-                                                     const double* __restrict__ r, const int* __restrict__ ets,
+                                                     const float* __restrict__ rad, const int* __restrict__ ets,
                                                      const int* __restrict__ ett, float* __restrict__ out,
                                                      float* __restrict__ tape) {
     extern __shared__ float lds[];
@@ -400,7 +414,8 @@ __global__ __launch_bounds__(256) void k_mlp_forward(const DMlp m, const DRadial
     const int* tt = ett + e0;
     for (int idx = threadIdx.x; idx < rows * ld; idx += blockDim.x) a[idx] = 0.0f;
     __syncthreads();
-    for (int e = threadIdx.x; e < ne; e += blockDim.x) mlp_first_inputs(rd, r[e0 + e], ts[e], tt[e], a + e * ld);
+    for (int idx = threadIdx.x; idx < ne * rd.nb; idx += blockDim.x)
+        a[(idx / rd.nb) * ld + idx % rd.nb] = rad[e0 * rd.nb + idx];
     __syncthreads();
     for (int L = 0; L < m.num_layers; ++L) {
         const int type = m.layers[4 * L], in = m.layers[4 * L + 1], w = m.layers[4 * L + 2], off = m.layers[4 * L + 3];
@@ -1521,6 +1536,7 @@ void Evaluator::compute(int N, const int* types, const int* num_neigh, const int
                       o_ts = lay.add<int>(E), o_tt = lay.add<int>(E), o_toff = lay.add<int>(N + 1),
                       o_tedge = lay.add<int>(E), o_xyz = lay.add<double>(3 * E), o_r = lay.add<double>(E),
                       o_Y = lay.add<float>(static_cast<std::size_t>(E) * NY), o_cut = lay.add<float>(E),
+                      o_rad = lay.add<float>(static_cast<std::size_t>(E) * M.bessel.size()),
                       o_feat0 = lay.add<float>(static_cast<std::size_t>(N) * embed_dim_);
     struct LayerOff {
         std::size_t up, res, skip, msg, dens, lin1, pre, gated, iout, feat, wraw, draw, wtape, dtape;
@@ -1598,10 +1614,10 @@ void Evaluator::compute(int N, const int* types, const int* num_neigh, const int
     float* cut = f(o_cut);
     const unsigned eg = blocks_for(E, 256);
     switch (M.l_max) {
-        case 0: launch("mh1_geometry", k_geometry<0>, eg, 256, 0, E, d_xyz, d_r, rad_, Y, cut); break;
-        case 1: launch("mh1_geometry", k_geometry<1>, eg, 256, 0, E, d_xyz, d_r, rad_, Y, cut); break;
-        case 2: launch("mh1_geometry", k_geometry<2>, eg, 256, 0, E, d_xyz, d_r, rad_, Y, cut); break;
-        default: launch("mh1_geometry", k_geometry<3>, eg, 256, 0, E, d_xyz, d_r, rad_, Y, cut); break;
+        case 0: launch("mh1_geometry", k_geometry<0>, eg, 256, 0, E, d_xyz, d_r, rad_, d_ts, d_tt, Y, cut, f(o_rad)); break;
+        case 1: launch("mh1_geometry", k_geometry<1>, eg, 256, 0, E, d_xyz, d_r, rad_, d_ts, d_tt, Y, cut, f(o_rad)); break;
+        case 2: launch("mh1_geometry", k_geometry<2>, eg, 256, 0, E, d_xyz, d_r, rad_, d_ts, d_tt, Y, cut, f(o_rad)); break;
+        default: launch("mh1_geometry", k_geometry<3>, eg, 256, 0, E, d_xyz, d_r, rad_, d_ts, d_tt, Y, cut, f(o_rad)); break;
     }
     const float* cut_w = M.apply_cutoff ? nullptr : cut;
     float* feats = f(o_feat0);
@@ -1618,9 +1634,11 @@ void Evaluator::compute(int N, const int* types, const int* num_neigh, const int
         launch_linear(I.skip.fwd, N, feats, f(o.skip), nullptr, false, "mh1_linear_skip");
         const int WW = mlp_waves(I.wmlp), WD = mlp_waves(I.dmlp);
         launch("mh1_mlp_forward", k_mlp_forward, blocks_for(E, 16 * WW), 64 * WW, mlp_lds(I.wmlp, WW, false), I.wmlp,
-               rad_, E, mlp_ld(I.wmlp), d_r, d_ts, d_tt, f(o.wraw), f(o.wtape));
+               rad_, E, mlp_ld(I.wmlp), static_cast<const float*>(f(o_rad)), d_ts, d_tt, f(o.wraw),
+               f(o.wtape));
         launch("mh1_mlp_forward", k_mlp_forward, blocks_for(E, 16 * WD), 64 * WD, mlp_lds(I.dmlp, WD, false), I.dmlp,
-               rad_, E, mlp_ld(I.dmlp), d_r, d_ts, d_tt, f(o.draw), f(o.dtape));
+               rad_, E, mlp_ld(I.dmlp), static_cast<const float*>(f(o_rad)), d_ts, d_tt, f(o.draw),
+               f(o.dtape));
         const unsigned tpg = blocks_for(static_cast<long long>(N) * I.tp.channels, kTpThreads);
         if (I.tp.compiled >= 0) {
             auto kf = I.tp.compiled == 0 ? k_tp_forward_c<0, 2> : I.tp.compiled == 1 ? k_tp_forward_c<0, 3>
