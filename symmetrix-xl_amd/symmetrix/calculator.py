@@ -153,6 +153,8 @@ class _NeighborCache:
     receivers: np.ndarray
     sources: np.ndarray
     shifts: np.ndarray
+    shift_cart: np.ndarray = None    # shifts @ shift_cell (MH-1 host geometry)
+    shift_cell: np.ndarray = None
 
 
 class Symmetrix(_Base):
@@ -160,6 +162,7 @@ class Symmetrix(_Base):
     streamed edges)."""
 
     implemented_properties = ["energy", "free_energy", "energies", "forces", "stress"]
+    _nonlinear = False  # an MH-1 (MACE_Nonlinear) evaluator
     # vacuum permittivity in e / (V A) (calculator.py:729)
     _macefield_eps0 = 8.8541878128e-12 / 1.602176634e-19 / 1e10
 
@@ -422,10 +425,18 @@ class Symmetrix(_Base):
         (calculator.py:3087-3093), one compute_node_energies_forces call,
         forces and stress reduced in FP64 (calculator.py:3821-3894)."""
         recv, src = cache.receivers, cache.sources
-        xyz = positions[src] - positions[recv] + cache.shifts @ cell
-        r = np.sqrt(np.einsum("ij,ij->i", xyz, xyz))
-        active = r < self.cutoff
-        recv, src, xyz, r = recv[active], src[active], np.ascontiguousarray(xyz[active]), r[active]
+        # Cartesian cell shifts of the skin graph, formed once per cell
+        if cache.shift_cell is None or not np.array_equal(cache.shift_cell, cell):
+            cache.shift_cart = cache.shifts.astype(np.float64) @ cell
+            cache.shift_cell = cell.copy()
+        xyz = np.take(positions, src, axis=0)
+        xyz -= np.take(positions, recv, axis=0)
+        xyz += cache.shift_cart
+        r2 = np.einsum("ij,ij->i", xyz, xyz)
+        active = np.flatnonzero(r2 < self.cutoff * self.cutoff)
+        recv, src = recv[active], src[active]
+        xyz = np.take(xyz, active, axis=0)
+        r = np.sqrt(r2[active])
         n = len(numbers)
         types = self._node_types(numbers)
         num_neigh = np.bincount(recv, minlength=n).astype(np.int32)
@@ -440,7 +451,7 @@ class Symmetrix(_Base):
         energy = float(np.sum(node_energies, dtype=np.float64))
         self.results = {"energy": energy, "free_energy": energy, "energies": node_energies, "forces": forces}
         if volume is not None:
-            sigma = -np.einsum("ea,eb->ab", nf, xyz) / volume
+            sigma = -(nf.T @ xyz) / volume
             self.results["stress"] = full_3x3_to_voigt_6_stress(sigma)
         return self.results
 

@@ -397,3 +397,67 @@ def test_reference_caller_members_resolve():
              "factorized_last_evaluation_ms", "factorized_last_graph_prepare_ms", "allow_fixed_workspace"]
     missing = [n for n in names if not hasattr(MACEKokkosFloat, n)]
     assert not missing, missing
+
+
+class FakeMH1:
+    """Stands in for MACENonlinearKokkosFloat: records the graph it gets and
+    returns node energy 1 per node and node_forces[e] = xyz[e] * r[e]."""
+
+    has_field_coupling = False
+
+    def __init__(self):
+        self.calls = []
+
+    def compute_node_energies_forces(self, n, types, num_neigh, src, neigh_types, xyz, r):
+        self.calls.append((n, np.array(num_neigh), np.array(src), np.array(xyz).reshape(-1, 3), np.array(r)))
+        self._n = n
+        self._nf = (np.array(xyz).reshape(-1, 3) * np.array(r)[:, None]).reshape(-1)
+
+    @property
+    def node_energies(self):
+        return np.ones(self._n)
+
+    @property
+    def node_forces(self):
+        return self._nf
+
+
+def test_calculator_mh1_passes_edges_inside_cutoff_and_reduces():
+    """The MH-1 route (calculator.py:3087-3093): the skin graph's edges with
+    r < r_cut, in receiver order; F_i = sum over edges with source i of f_e
+    minus those with receiver i; sigma = -sum f_e xyz_e^T / V."""
+    c = _calc(skin=0.5)
+    c._nonlinear = True
+    c.evaluator = FakeMH1()
+    s = systems.srtio3_supercell(2, sigma=0.1, seed=4)
+    res = c.calculate(s, ["energy", "forces", "stress"])
+    n, num_neigh, src, xyz, r = c.evaluator.calls[-1]
+    pos, cell = np.asarray(s["positions"]), np.asarray(s["cell"])
+    # brute force over images
+    want = []
+    for i in range(n):
+        for j in range(n):
+            for S in np.ndindex(5, 5, 5):
+                d = pos[j] - pos[i] + (np.array(S) - 2) @ cell
+                rr = np.linalg.norm(d)
+                if 0 < rr < c.cutoff:
+                    want.append((i, j, rr))
+    assert len(r) == len(want) and num_neigh.sum() == len(r)
+    assert np.all(r < c.cutoff)
+    recv = np.repeat(np.arange(n), num_neigh)
+    np.testing.assert_allclose(np.linalg.norm(xyz, axis=1), r)
+    np.testing.assert_allclose(sorted(r), sorted(w[2] for w in want), rtol=1e-12)
+    f = xyz * r[:, None]
+    F = np.zeros((n, 3))
+    np.add.at(F, src, f)
+    np.add.at(F, recv, -f)
+    np.testing.assert_allclose(res["forces"], F, atol=1e-12)
+    sig = -np.einsum("ea,eb->ab", f, xyz) / abs(np.linalg.det(cell))
+    np.testing.assert_allclose(res["stress"], [sig[0, 0], sig[1, 1], sig[2, 2], sig[1, 2], sig[0, 2], sig[0, 1]],
+                               atol=1e-12)
+    assert res["energy"] == n
+    # a second call inside half the skin reuses the graph
+    moved = dict(s)
+    moved["positions"] = pos + 0.1
+    c.calculate(moved)
+    assert c.neighbor_cache_build_count == 1 and c.neighbor_cache_reuse_count == 1
