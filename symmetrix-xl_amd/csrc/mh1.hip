@@ -337,12 +337,40 @@ __device__ __forceinline__ void tile_gemm(const float* A, int lda, int a_rows, i
                                           int ldb, int N, Epi epi) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int r = lane & 15, kg = lane >> 4;
+    if ((K & 3) == 0 && (N & 63) == 0 && a_rows >= static_cast<int>(blockDim.x / 4)) {
+        // every row valid, K and the columns whole fragments: no predicates, pointer steps only
+        const float* arow = A + static_cast<std::size_t>(16 * wave + r) * lda + kg;
+        for (int c0 = 0; c0 < N; c0 += 64) {
+            v4f acc[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            const float* ap = arow;
+            const float* bp = B + static_cast<std::size_t>(kg) * ldb + c0 + r;
+
+            for (int k0 = 0; k0 < K; k0 += 4) {
+                const float a = *ap;
+                const float b0 = bp[0], b1 = bp[16], b2 = bp[32], b3 = bp[48];
+                acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b0, acc[0], 0, 0, 0);
+                acc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b1, acc[1], 0, 0, 0);
+                acc[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b2, acc[2], 0, 0, 0);
+                acc[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b3, acc[3], 0, 0, 0);
+                ap += 4;
+                bp += 4 * static_cast<std::size_t>(ldb);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) epi(16 * wave + 4 * kg + v, c0 + 16 * j + r, acc[j][v]);
+        }
+        return;
+    }
     const bool row_ok = 16 * wave + r < a_rows;
     const float* arow = A + static_cast<std::size_t>(row_ok ? 16 * wave + r : 0) * lda;
     for (int c0 = 0; c0 < N; c0 += 64) {
         v4f acc[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+
         for (int k0 = 0; k0 < K; k0 += 4) {
             const int k = k0 + kg;
             const float a = (row_ok && k < K) ? arow[k] : 0.0f;
