@@ -872,17 +872,38 @@ __global__ __launch_bounds__(kTpThreads) void k_tp_reverse_c(
             for (int a = 0; a < 3; ++a) arow[E + 3 * u + a] = xa[1 + a];
         }
         // sums over the receiver's channel lanes (aligned groups of E lanes)
+        float* yo = Yadj + static_cast<std::size_t>(e) * NY;
+        if (E >= 16) {
+            // reduce-scatter of the (padded) 16 harmonic adjoints: four halving
+            // steps leave lane u with value u / (E/16), summed over 16 lanes;
+            // plain butterflies finish the rest (15 shuffles instead of 16 log2 E)
+            float v[16];
 #pragma unroll
-        for (int b = 0; b < NY; ++b) {
-            float v = ya[b];
-            for (int off = E / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
-            ya[b] = v;
+            for (int b = 0; b < 16; ++b) v[b] = b < NY ? ya[b] : 0.0f;
+#pragma unroll
+            for (int s = 0, half = 8; s < 4; ++s, half >>= 1) {
+                const int off = E >> (s + 1);
+                const bool up = (u & off) != 0;
+#pragma unroll
+                for (int q = 0; q < half; ++q) {
+                    const float send = up ? v[q] : v[half + q];
+                    const float keep = up ? v[half + q] : v[q];
+                    v[q] = keep + __shfl_xor(send, off, kWave);
+                }
+            }
+            for (int off = E >> 5; off > 0; off >>= 1) v[0] += __shfl_xor(v[0], off, kWave);
+            const int group = E >> 4;
+            if (u % group == 0 && u / group < NY) yo[u / group] += v[0];
+        } else {
+#pragma unroll
+            for (int b = 0; b < NY; ++b) {
+                float v = ya[b];
+                for (int off = E / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+                if (u == 0) yo[b] += v;
+            }
         }
         for (int off = E / 2; off > 0; off >>= 1) cpart += __shfl_xor(cpart, off, kWave);
         if (u == 0) {
-            float* yo = Yadj + static_cast<std::size_t>(e) * NY;
-#pragma unroll
-            for (int b = 0; b < NY; ++b) yo[b] += ya[b];
             const float dr = draw[e];
             const float base = tanhf(dr * dr);
             adraw[e] = ad * (1.0f - base * base) * 2.0f * dr * cf;
