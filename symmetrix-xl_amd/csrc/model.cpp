@@ -641,6 +641,11 @@ void HostModel::load_field_coupling(const Value& j) {
 
 void HostModel::load(const std::string& path, const std::string& head) {
     Value j = json_lite::parse_model_file(path);
+    // the nonlinear family has its own evaluator (the pair style refuses it,
+    // as pair_symmetrix_mace_kokkos.cpp:419-420 does)
+    if (j.is_object() && j.get_string("model_type", "MACE") == "MACE_Nonlinear")
+        throw std::invalid_argument("MACE_Nonlinear models are not supported by this evaluator; load them with "
+                                    "smx_mh1_create (MACENonlinearKokkosFloat)");
     if (j.get_int("symmetrix_format_version", 1) != 4)
         throw std::invalid_argument("only Symmetrix MACE model format version 4 is supported");
     select_prediction_head(j, head, selected_head, available_heads);

@@ -284,3 +284,15 @@ def test_planted_transposed_linear_read_fails_known_answer():
     wrong = np.arange(6.0).reshape(3, 2) @ x[0]
     assert np.allclose(right, [30.0, 41.0, 52.0])
     assert not np.allclose(right, wrong)
+
+
+def test_mace_evaluator_refuses_nonlinear_files(tmp_path):
+    """A MACE_Nonlinear file given to the MACE evaluator (and so to the pair
+    style, as the reference's pair styles refuse it) fails with a message
+    that names the MH-1 entry point, before any device work."""
+    import json as _json
+    from symmetrix import mace_kokkos
+    p = tmp_path / "nonlinear.json"
+    p.write_text(_json.dumps({"symmetrix_format_version": 3, "model_type": "MACE_Nonlinear"}))
+    with pytest.raises(ValueError, match="MACE_Nonlinear models are not supported"):
+        mace_kokkos.MACEKokkosFloat(str(p))
