@@ -256,3 +256,74 @@ def test_mh1_convolution_kernel_choice(paths):
         assert ("mh1_tp_forward_table" in names) == table
         assert ("mh1_tp_reverse_table" in names) == table
         assert "mh1_tp_forward" in names if not table else True
+
+
+def _neighbor_arrays(ev, pos, cell):
+    from symmetrix.neighbors import neighbor_list_ijS
+    recv, src, shifts = neighbor_list_ijS(pos, cell, np.array([True] * 3), ev.r_cut)
+    xyz = pos[src] - pos[recv] + shifts @ cell
+    r = np.sqrt(np.einsum("ij,ij->i", xyz, xyz))
+    keep = r < ev.r_cut
+    return recv[keep], src[keep], np.ascontiguousarray(xyz[keep]), r[keep]
+
+
+def _gpu_system(ev, numbers, pos, cell):
+    lut = {z: i for i, z in enumerate(ev.atomic_numbers)}
+    types = np.array([lut[int(z)] for z in numbers], np.int32)
+    recv, src, xyz, r = _neighbor_arrays(ev, pos, cell)
+    n = len(types)
+    ev.compute_node_energies_forces(n, types, np.bincount(recv, minlength=n).astype(np.int32), src, types[src],
+                                    xyz.reshape(-1), r)
+    nf = ev.node_forces.reshape(-1, 3)
+    F = mo.reduce_forces(n, recv, src, nf)
+    S = mo.reduce_stress(nf, xyz, abs(np.linalg.det(cell)))
+    return ev.node_energies.copy(), F, S, len(r)
+
+
+def test_mh1_benchmark_size_unperturbed_crystal(paths):
+    """The bench's 5,000-atom SrTiO3 cell without displacements: every site
+    is an inversion centre, so each atom's energy equals its site's energy in
+    the oracle's 3x3x3 cell, all forces vanish and the stress equals the
+    oracle's (r_cut 6.0 A: 369k edges through every MH-1 kernel)."""
+    from symmetrix.mace_nonlinear import MACENonlinearKokkosFloat
+    path = paths["mh1_medium"]
+    model = mo.MH1Oracle(path)
+    small = systems.srtio3_supercell(3, sigma=0.0)
+    ps, cs = np.asarray(small["positions"]), np.asarray(small["cell"])
+    ts = model.types_of(small["numbers"])
+    g, xyz, r = _graph(model, ps, cs)
+    e_ref, f_ref = model.evaluate(ts, g["receivers"], g["sources"], xyz)
+    S_ref = mo.reduce_stress(f_ref, xyz, abs(np.linalg.det(cs)))
+    site = {int(z): e_ref[np.asarray(small["numbers"]) == z].mean() for z in set(small["numbers"])}
+    big = systems.srtio3_supercell(10, sigma=0.0)
+    ev = MACENonlinearKokkosFloat(path)
+    e, F, S, E = _gpu_system(ev, big["numbers"], np.asarray(big["positions"]), np.asarray(big["cell"]))
+    want = np.array([site[int(z)] for z in big["numbers"]])
+    _say("mh1 unperturbed 10x10x10: %d edges, max|dE_i| %.2e, max|F| %.2e, max|dS| %.2e"
+         % (E, np.abs(e - want).max(), np.abs(F).max(), np.abs(S - S_ref).max()))
+    assert E > 300000
+    assert np.abs(e - want).max() < 1e-4
+    assert abs(e.sum() - want.sum()) / len(e) < 1e-5
+    assert np.abs(F).max() < 1e-4
+    assert np.abs(S - S_ref).max() < 1e-6
+
+
+def test_mh1_benchmark_size_rotation_and_translation(paths):
+    """The perturbed 5,000-atom cell rotated and shifted as a whole: node
+    energies unchanged and forces rotated, within the FP32 bars."""
+    from symmetrix import e3
+    from symmetrix.mace_nonlinear import MACENonlinearKokkosFloat
+    ev = MACENonlinearKokkosFloat(paths["mh1_medium"])
+    s = systems.srtio3_supercell(10, sigma=0.05, seed=0)
+    pos, cell = np.asarray(s["positions"]), np.asarray(s["cell"])
+    e0, F0, _, _ = _gpu_system(ev, s["numbers"], pos, cell)
+    R = e3.random_rotation(np.random.default_rng(21))
+    e1, F1, _, _ = _gpu_system(ev, s["numbers"], pos @ R.T + np.array([0.7, -1.3, 2.1]), cell @ R.T)
+    _say("mh1 rotated 10x10x10: max|dE_i| %.2e, |dE|/atom %.2e, max|dF| %.2e (|F| %.2f)"
+         % (np.abs(e1 - e0).max(), abs(e1.sum() - e0.sum()) / len(e0), np.abs(F1 - F0 @ R.T).max(),
+            np.abs(F0).max()))
+    # the bar is the energy per atom; single node energies carry the FP32
+    # rounding of their own sums (two different rounding patterns here)
+    assert abs(e1.sum() - e0.sum()) / len(e0) < 1e-5
+    assert np.abs(e1 - e0).max() < 5e-4
+    assert np.abs(F1 - F0 @ R.T).max() < 1e-4
