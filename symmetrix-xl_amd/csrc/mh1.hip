@@ -1234,9 +1234,22 @@ struct Timer {
 
 class Evaluator {
 public:
-    Evaluator(const std::string& path, const std::string& head) : model_(Model::load(path, head)) {
-        SMX_HIP(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
+    // The file is parsed and checked here; the device tables are made on the
+    // first compute call (after its inputs are checked), so a model's facts and
+    // its load errors need no GPU.
+    Evaluator(const std::string& path, const std::string& head) : model_(Model::load(path, head)) {}
+    void ensure_device() {
+        if (uploaded_) return;
+        if (!stream_) SMX_HIP(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
+        if (params_) {
+            SMX_HIP(hipFree(params_));
+            params_ = nullptr;
+        }
+        inter_.clear();
+        prod_.clear();
+        ro_.clear();
         upload_model();
+        uploaded_ = true;
     }
     ~Evaluator() {
         if (params_) (void)hipFree(params_);
@@ -1285,6 +1298,7 @@ private:
     }
 
     Model model_;
+    bool uploaded_ = false;
     hipStream_t stream_ = nullptr;
     void* params_ = nullptr;
     std::vector<InteractionDev> inter_;
@@ -1566,6 +1580,7 @@ void Evaluator::compute(int N, const int* types, const int* num_neigh, const int
             !std::isfinite(xyz[3 * e + 2]))
             throw std::invalid_argument("MH-1: edge length or vector is not finite and positive");
     }
+    ensure_device();
     // ---- host-side graph arrays
     std::vector<int> offsets(N + 1, 0), tt(E), t_off(N + 1, 0), t_edges(E);
     for (int i = 0; i < N; ++i) offsets[i + 1] = offsets[i] + num_neigh[i];
