@@ -816,7 +816,7 @@ __global__ __launch_bounds__(kTpThreads) void k_tp_forward_c(const DTp t, int N,
 }
 
 template <int L1MAX, int LMAX>
-__global__ __launch_bounds__(kTpThreads) void k_tp_reverse_c(
+__global__ __launch_bounds__(kTpThreads) __attribute__((amdgpu_waves_per_eu(3))) void k_tp_reverse_c(
     const DTp t, int N, const int* __restrict__ offsets, const int* __restrict__ src, const float* __restrict__ up,
     const float* __restrict__ Y, const float* __restrict__ wraw, const float* __restrict__ cut,
     const float* __restrict__ draw, const float* __restrict__ amsg, const float* __restrict__ adens,
