@@ -72,6 +72,15 @@ struct DLinear {
     int blk_off[kLinearMaxBlocks], blk_mul[kLinearMaxBlocks], blk_d[kLinearMaxBlocks];
 };
 
+constexpr int kRegStages = MlpTables::kRegStages;
+constexpr int kRegTiles = 1;  // 16-edge tiles per wave in the register-form edge MLPs
+
+// A stage of the register form: widths and parameter offsets (see MlpTables::reg_stage).
+struct DMlpStage {
+    int in, out, w, b, wt, ln;
+    float eps;
+};
+
 struct DMlp {
     int num_layers, radial, first_width, num_types, width, tape_width;
     const int* layers;
@@ -80,6 +89,8 @@ struct DMlp {
     const float* type_rows;
     const int* wt_offset;    // per layer: transposed weights [in][out] (linear layers)
     const int* tape_offset;  // per layer: output offset in the edge's tape row (-1: last layer)
+    int reg_hw, reg_stages;  // register form (reg_hw 0: the LDS-tile kernels run)
+    DMlpStage st[kRegStages + 1];  // hidden stages from 0, the final linear at kRegStages
 };
 
 struct DRadial {
@@ -580,6 +591,378 @@ __global__ __launch_bounds__(256) void k_mlp_reverse(const DMlp m, const DRadial
         float* t = g;
         g = h;
         h = t;
+    }
+}
+
+// ---- edge MLPs in registers
+//
+// The units of a layer are the rows and the edges the columns of
+// v_mfma_f32_16x16x4_f32: lane (r, kg) of a wave (r = lane % 16, kg =
+// lane / 16) holds, for edge e0 + 16t + r of its t-th tile of 16 edges,
+// units 16i + 4kg + v (v < 4) of a layer in x[t][i][v] (the D layout).  With
+// the k index of step (J, v) of lane group kg taken as 16J + 4kg + v, the same
+// registers are the B operand of the next layer, and the A operand (weight row
+// 16i + r) is one 16-byte load per J: a tile's activations never leave
+// registers and no LDS is used.  Every hidden stage has the width 16 MT, so
+// the MFMA chains are straight-line code.  Lanes r, r+16, r+32, r+48 hold one edge, so
+// a LayerNorm's row sums are the lane's 16 units plus two cross-group shuffles.
+// The reverse recomputes the hidden stages from the radial features instead
+// of reading a tape, as the reference's streamed reverse re-runs the
+// conditioned MLPs per edge block (mace_nonlinear.cpp:916-929).
+
+__device__ __forceinline__ v4f ld4(const float* p) { return *reinterpret_cast<const v4f*>(p); }
+
+// Ends an MFMA chain whose results VALU code reads next.  A read of an MFMA
+// result needs ten wait states after a v_mfma_f32_16x16x4_f32 (8 passes) on
+// every path; in these kernels the chains sit in runtime-conditional blocks
+// and the compiler padded only the fall-through path of a join (the assembly
+// showed a read of the last accumulator register right after its MFMA on the
+// taken branch).  Sixteen wait states inside the chain's own block, with the
+// scheduler fenced on both sides, cover every path.
+__device__ __forceinline__ void mfma_settle() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_nop 7\n\ts_nop 7");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// entries k..k+3 of a row of n floats, zeros from n on (one 16-byte load when n % 4 == 0)
+__device__ __forceinline__ v4f ld4_row(const float* row, int k, int n) {
+    if ((n & 3) == 0) {
+        v4f x{0.0f, 0.0f, 0.0f, 0.0f};
+        if (k < n) x = ld4(row + k);
+        return x;
+    }
+    v4f x;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) x[v] = k + v < n ? row[k + v] : 0.0f;
+    return x;
+}
+
+__device__ __forceinline__ void st4_row(float* row, int k, int n, v4f v) {
+    if ((n & 3) == 0) {
+        if (k < n) *reinterpret_cast<v4f*>(row + k) = v;
+        return;
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+        if (k + q < n) row[k + q] = v[q];
+}
+
+// sum over the four lane groups that hold one edge
+__device__ __forceinline__ float group4_sum(float v) {
+    v += __shfl_xor(v, 16, kWave);
+    v += __shfl_xor(v, 32, kWave);
+    return v;
+}
+
+// acc[t][i] = sum_k W[16i + r][k] x[t][k] (W row-major with row stride K; K = M = 16 MT)
+template <int MT, int NT>
+__device__ __forceinline__ void reg_linear(const float* __restrict__ W, int K, int M, const float (&x)[NT][MT][4],
+                                           v4f (&acc)[NT][MT]) {
+    const int lane = threadIdx.x & 63, r = lane & 15, kg = lane >> 4;
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int i = 0; i < MT; ++i) acc[t][i] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int J = 0; J < MT; ++J) {
+        v4f a[MT];
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+            a[i] = ld4(W + static_cast<std::size_t>(16 * i + r) * K + 16 * J + 4 * kg);
+        }
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+#pragma unroll
+            for (int i = 0; i < MT; ++i) {
+#pragma unroll
+                for (int t = 0; t < NT; ++t)
+                    acc[t][i] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][v], x[t][J][v], acc[t][i], 0, 0, 0);
+            }
+    }
+    mfma_settle();
+}
+
+// A stage's LayerNorm (when it has one) and SiLU of its linear output acc, into x.  With SAVE the
+// normalized values (the SiLU input, without a LayerNorm) and 1/std per edge are kept for the reverse.
+template <int MT, int NT, bool SAVE>
+__device__ __forceinline__ void reg_norm_silu(const float* __restrict__ params, const DMlpStage& S,
+                                              const v4f (&acc)[NT][MT], float (&x)[NT][MT][4],
+                                              float (&xs)[NT][MT][4], float (&rs)[NT]) {
+    const int kg = (threadIdx.x & 63) >> 4;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        float mean = 0.0f, rstd = 1.0f;
+        if (S.ln >= 0) {
+            float s = 0.0f;
+#pragma unroll
+            for (int i = 0; i < MT; ++i) {
+    #pragma unroll
+                for (int v = 0; v < 4; ++v) s += acc[t][i][v];
+            }
+            mean = group4_sum(s) / S.out;
+            float q = 0.0f;
+#pragma unroll
+            for (int i = 0; i < MT; ++i) {
+    #pragma unroll
+                for (int v = 0; v < 4; ++v) q += (acc[t][i][v] - mean) * (acc[t][i][v] - mean);
+            }
+            rstd = 1.0f / sqrtf(group4_sum(q) / S.out + S.eps);
+        }
+        if (SAVE) rs[t] = rstd;
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+            v4f g{1.0f, 1.0f, 1.0f, 1.0f}, b{0.0f, 0.0f, 0.0f, 0.0f};
+            if (S.ln >= 0) {
+                g = ld4(params + S.ln + 16 * i + 4 * kg);
+                b = ld4(params + S.ln + S.out + 16 * i + 4 * kg);
+            }
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const float h = (acc[t][i][v] - mean) * rstd;
+                if (SAVE) xs[t][i][v] = h;
+                const float z = h * g[v] + b[v];
+                x[t][i][v] = z * sigmoidf_(z);
+            }
+        }
+    }
+}
+
+// Reverse of reg_norm_silu: g (adjoint of the stage's output) to gx (adjoint of its linear output),
+// SiLU from z = xs * gamma + beta recomputed, then LayerNorm
+// dx = rstd (gamma g - mean(gamma g) - xhat mean(gamma g xhat)).
+template <int MT, int NT>
+__device__ __forceinline__ void reg_silu_norm_reverse(const float* __restrict__ params, const DMlpStage& S,
+                                                      const v4f (&g)[NT][MT], const float (&xs)[NT][MT][4],
+                                                      const float (&rs)[NT], float (&gx)[NT][MT][4]) {
+    const int kg = (threadIdx.x & 63) >> 4;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        float m1 = 0.0f, m2 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+            v4f ga{1.0f, 1.0f, 1.0f, 1.0f}, be{0.0f, 0.0f, 0.0f, 0.0f};
+            if (S.ln >= 0) {
+                ga = ld4(params + S.ln + 16 * i + 4 * kg);
+                be = ld4(params + S.ln + S.out + 16 * i + 4 * kg);
+            }
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const float h = xs[t][i][v];
+                const float z = h * ga[v] + be[v];
+                const float sg = sigmoidf_(z);
+                const float gh = g[t][i][v] * (sg + z * sg * (1.0f - sg)) * ga[v];
+                gx[t][i][v] = gh;
+                m1 += gh;
+                m2 += gh * h;
+            }
+        }
+        if (S.ln >= 0) {
+            m1 = group4_sum(m1) / S.out;
+            m2 = group4_sum(m2) / S.out;
+#pragma unroll
+            for (int i = 0; i < MT; ++i) {
+    #pragma unroll
+                for (int v = 0; v < 4; ++v) gx[t][i][v] = rs[t] * (gx[t][i][v] - m1 - xs[t][i][v] * m2);
+            }
+        }
+    }
+}
+
+// The hidden stages of a tile of NT x 16 edges from e0: the conditioned first linear over the radial
+// features plus the per-type rows, then each later stage's linear and bias; every stage ends in
+// reg_norm_silu.  x receives the last stage's output.
+template <int HW, int NT, bool SAVE>
+__device__ __forceinline__ void reg_hidden(const DMlp& m, long long E, long long e0, const float* __restrict__ rad,
+                                           const int* __restrict__ ets, const int* __restrict__ ett,
+                                           float (&x)[NT][HW / 16][4], float (&xs)[kRegStages][NT][HW / 16][4],
+                                           float (&rs)[kRegStages][NT]) {
+    constexpr int MT = HW / 16;
+    const int lane = threadIdx.x & 63, r = lane & 15, kg = lane >> 4;
+    const int nb = m.radial;
+    long long ec[NT];  // the tile's edges (past E: the last edge, whose columns are never stored)
+#pragma unroll
+    for (int t = 0; t < NT; ++t) ec[t] = min(e0 + 16 * t + r, E - 1);
+    v4f acc[NT][MT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int i = 0; i < MT; ++i) acc[t][i] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    const DMlpStage& S0 = m.st[0];
+    const float* W0 = m.params + S0.w;  // [S0.out][nb]
+    for (int k0 = 0; k0 < nb; k0 += 4) {
+        const int k = k0 + kg;
+        float b[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            b[t] = 0.0f;
+            if (k < nb) b[t] = rad[ec[t] * nb + k];
+        }
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+            float a = 0.0f;
+            if (k < nb) a = W0[(16 * i + r) * nb + k];
+#pragma unroll
+            for (int t = 0; t < NT; ++t) acc[t][i] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b[t], acc[t][i], 0, 0, 0);
+        }
+        mfma_settle();
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const float* ps = m.type_rows + static_cast<std::size_t>(ets[ec[t]]) * S0.out + 4 * kg;
+        const float* pt = m.type_rows + static_cast<std::size_t>(m.num_types + ett[ec[t]]) * S0.out + 4 * kg;
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+            acc[t][i] += ld4(ps + 16 * i) + ld4(pt + 16 * i);
+        }
+    }
+    reg_norm_silu<MT, NT, SAVE>(m.params, S0, acc, x, xs[0], rs[0]);
+#pragma unroll
+    for (int h = 1; h < kRegStages; ++h) {
+        if (h >= m.reg_stages) break;
+        const DMlpStage& S = m.st[h];
+        reg_linear<MT, NT>(m.params + S.w, S.in, S.out, x, acc);
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int i = 0; i < MT; ++i) {
+                    acc[t][i] += ld4(m.params + S.b + 16 * i + 4 * kg);
+            }
+        reg_norm_silu<MT, NT, SAVE>(m.params, S, acc, x, xs[h], rs[h]);
+    }
+}
+
+// Forward of an edge MLP in registers: one wave per NT x 16 edges, out [E][out_dim].
+template <int HW, int NT>
+__global__ __launch_bounds__(256) void k_mlp_forward_r(const DMlp m, long long E, const float* __restrict__ rad,
+                                                       const int* __restrict__ ets, const int* __restrict__ ett,
+                                                       float* __restrict__ out) {
+    constexpr int MT = HW / 16;
+    const int lane = threadIdx.x & 63, r = lane & 15, kg = lane >> 4;
+    const long long e0 = (static_cast<long long>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6)) * (16 * NT);
+    if (e0 >= E) return;
+    float x[NT][MT][4], xs[kRegStages][NT][MT][4], rs[kRegStages][NT];
+    reg_hidden<HW, NT, false>(m, E, e0, rad, ets, ett, x, xs, rs);
+    const DMlpStage& F = m.st[kRegStages];
+    const float* W = m.params + F.w;
+    const float* bias = m.params + F.b;
+    const int K = F.in, M = F.out;
+    // two 16-row tiles of the output per pass (independent MFMA chains); rows past M read row M-1
+    // and are not stored
+    for (int i0 = 0; i0 < M; i0 += 32) {
+        const int ra = min(i0 + r, M - 1), rb = min(i0 + 16 + r, M - 1);
+        v4f acc[NT][2];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[t][0] = acc[t][1] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int J = 0; J < MT; ++J) {
+                const v4f a0 = ld4(W + static_cast<std::size_t>(ra) * K + 16 * J + 4 * kg);
+            const v4f a1 = ld4(W + static_cast<std::size_t>(rb) * K + 16 * J + 4 * kg);
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    acc[t][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0[v], x[t][J][v], acc[t][0], 0, 0, 0);
+                    acc[t][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1[v], x[t][J][v], acc[t][1], 0, 0, 0);
+                }
+        }
+        mfma_settle();
+        const v4f b0 = ld4_row(bias, i0 + 4 * kg, M), b1 = ld4_row(bias, i0 + 16 + 4 * kg, M);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const long long e = e0 + 16 * t + r;
+            if (e >= E) continue;
+            float* orow = out + e * M;
+            st4_row(orow, i0 + 4 * kg, M, acc[t][0] + b0);
+            st4_row(orow, i0 + 16 + 4 * kg, M, acc[t][1] + b1);
+        }
+    }
+}
+
+// Reverse of an edge MLP in registers: the hidden stages recomputed (normalized values kept), gout
+// [E][out_dim] pulled back through the final linear and every stage to the radial features:
+// rad_adj [E][nb] +=.
+template <int HW, int NT>
+__global__ __launch_bounds__(256) void k_mlp_reverse_r(const DMlp m, long long E, const float* __restrict__ rad,
+                                                       const int* __restrict__ ets, const int* __restrict__ ett,
+                                                       const float* __restrict__ gout, float* __restrict__ rad_adj) {
+    constexpr int MT = HW / 16;
+    const int lane = threadIdx.x & 63, r = lane & 15, kg = lane >> 4;
+    const long long e0 = (static_cast<long long>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6)) * (16 * NT);
+    if (e0 >= E) return;
+    float x[NT][MT][4], xs[kRegStages][NT][MT][4], rs[kRegStages][NT];
+    reg_hidden<HW, NT, true>(m, E, e0, rad, ets, ett, x, xs, rs);
+    long long ec[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) ec[t] = min(e0 + 16 * t + r, E - 1);
+    // adjoint of the last stage's output: g[t][i] = sum_k W_F[k][16i + r] gout[e][k]
+    const DMlpStage& F = m.st[kRegStages];
+    const float* WT = m.params + F.wt;  // [F.in][F.out]
+    v4f g[NT][MT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int i = 0; i < MT; ++i) g[t][i] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int k0 = 0; k0 < F.out; k0 += 16) {
+        v4f gb[NT], a[MT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) gb[t] = ld4_row(gout + ec[t] * F.out, k0 + 4 * kg, F.out);
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+            a[i] = ld4_row(WT + static_cast<std::size_t>(16 * i + r) * F.out, k0 + 4 * kg, F.out);
+        }
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+#pragma unroll
+            for (int i = 0; i < MT; ++i) {
+#pragma unroll
+                for (int t = 0; t < NT; ++t)
+                    g[t][i] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][v], gb[t][v], g[t][i], 0, 0, 0);
+            }
+        mfma_settle();
+    }
+    float gx[NT][MT][4];
+#pragma unroll
+    for (int h = kRegStages - 1; h >= 0; --h) {
+        if (h >= m.reg_stages) continue;
+        const DMlpStage& S = m.st[h];
+        reg_silu_norm_reverse<MT, NT>(m.params, S, g, xs[h], rs[h], gx);
+        if (h > 0) {
+            // adjoint of the previous stage's output: W_h^T gx, W_h^T = [S.in][S.out] row-major
+            reg_linear<MT, NT>(m.params + S.wt, S.out, S.in, gx, g);
+            continue;
+        }
+        // radial adjoint: rad_adj[e][k] += sum_u W0[u][k] gx[e][u], W0^T = [nb][S.out]
+        const int nb = m.radial;
+        const float* WT0 = m.params + S.wt;
+        for (int k0 = 0; k0 < nb; k0 += 16) {
+            const int kr = min(k0 + r, nb - 1);
+            const bool kv = k0 + r < nb;
+            v4f acc[NT];
+#pragma unroll
+            for (int t = 0; t < NT; ++t) acc[t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int J = 0; J < MT; ++J) {
+                v4f a = ld4(WT0 + static_cast<std::size_t>(kr) * S.out + 16 * J + 4 * kg);
+                if (!kv) a = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+#pragma unroll
+                    for (int t = 0; t < NT; ++t)
+                        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[v], gx[t][J][v], acc[t], 0, 0, 0);
+            }
+            mfma_settle();
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const long long e = e0 + 16 * t + r;
+                if (e >= E) continue;
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int k = k0 + 4 * kg + v;
+                    if (k < nb) rad_adj[e * nb + k] += acc[t][v];
+                }
+            }
+        }
     }
 }
 
@@ -1464,8 +1847,14 @@ void Evaluator::upload_model() {
         return d;
     };
     auto mlp = [&](const MlpTables& T, const MlpOff& o) {
-        return DMlp{T.num_layers, T.radial, T.first_width, nt, T.max_hidden, T.tape_width, I_(o.layers), F(o.eps),
-                    F(o.params), F(o.rows), I_(o.wt), I_(o.tape)};
+        DMlp d{T.num_layers, T.radial, T.first_width, nt, T.max_hidden, T.tape_width, I_(o.layers), F(o.eps),
+               F(o.params), F(o.rows), I_(o.wt), I_(o.tape), T.reg_hw, T.reg_stages, {}};
+        // hidden stages from slot 0, the final linear in slot kRegStages
+        for (int k = 0; T.reg_hw && k <= T.reg_stages; ++k) {
+            const int* S = &T.reg_stage[6 * k];
+            d.st[k < T.reg_stages ? k : kRegStages] = DMlpStage{S[0], S[1], S[2], S[3], S[4], S[5], T.reg_eps[k]};
+        }
+        return d;
     };
     embed_table_ = F(o_table);
     atomic_e_ = reinterpret_cast<const double*>(base + o_ae);
@@ -1622,8 +2011,9 @@ void Evaluator::compute(int N, const int* types, const int* num_neigh, const int
         o.iout = lay.add<float>(n * I.lin2.out.dim);
         o.feat = lay.add<float>(n * M.products[k].out_dim);
         o.wraw = lay.add<float>(static_cast<std::size_t>(E) * I.tp.numel);
-        o.wtape = lay.add<float>(static_cast<std::size_t>(E) * I.weights_mlp.tape_width);
-        o.dtape = lay.add<float>(static_cast<std::size_t>(E) * I.density_mlp.tape_width);
+        // the register-form kernels recompute the hidden stages and keep no tape
+        o.wtape = lay.add<float>(static_cast<std::size_t>(E) * (I.weights_mlp.reg_hw ? 0 : I.weights_mlp.tape_width));
+        o.dtape = lay.add<float>(static_cast<std::size_t>(E) * (I.density_mlp.reg_hw ? 0 : I.density_mlp.tape_width));
         o.draw = lay.add<float>(E);
         o.a_feat = lay.add<float>(n * M.products[k].out_dim);
         o.contr = lay.add<float>(n * M.products[k].out_dim);
@@ -1688,6 +2078,30 @@ void Evaluator::compute(int N, const int* types, const int* num_neigh, const int
     launch("mh1_embed", k_embed, blocks_for(static_cast<long long>(N) * embed_dim_, 256), 256, 0, N, embed_dim_,
            d_types, embed_table_, feats);
     stages_.clear();
+    const float* radf = f(o_rad);
+    // edge MLPs: the register form when the MLP has it, else the LDS-tile kernels with a tape
+    auto mlp_forward = [&](const DMlp& m, float* out, float* tape) {
+        if (m.reg_hw) {
+            auto k = m.reg_hw == 16 ? k_mlp_forward_r<16, kRegTiles>
+                   : m.reg_hw == 32 ? k_mlp_forward_r<32, kRegTiles> : k_mlp_forward_r<64, kRegTiles>;
+            launch("mh1_mlp_forward", k, blocks_for(E, 64 * kRegTiles), 256, 0, m, E, radf, d_ts, d_tt, out);
+            return;
+        }
+        const int W = mlp_waves(m);
+        launch("mh1_mlp_forward", k_mlp_forward, blocks_for(E, 16 * W), 64 * W, mlp_lds(m, W, false), m, rad_, E,
+               mlp_ld(m), radf, d_ts, d_tt, out, tape);
+    };
+    auto mlp_reverse = [&](const DMlp& m, const float* tape, const float* gout, float* radadj) {
+        if (m.reg_hw) {
+            auto k = m.reg_hw == 16 ? k_mlp_reverse_r<16, kRegTiles>
+                   : m.reg_hw == 32 ? k_mlp_reverse_r<32, kRegTiles> : k_mlp_reverse_r<64, kRegTiles>;
+            launch("mh1_mlp_reverse", k, blocks_for(E, 64 * kRegTiles), 256, 0, m, E, radf, d_ts, d_tt, gout, radadj);
+            return;
+        }
+        const int W = mlp_waves(m);
+        launch("mh1_mlp_reverse", k_mlp_reverse, blocks_for(E, 16 * W), 64 * W, mlp_lds(m, W, true), m, rad_, E,
+               mlp_ld(m), tape, gout, radadj);
+    };
     // ---- forward (mace_nonlinear.cpp:583-768)
     for (int k = 0; k < L; ++k) {
         const InteractionDev& I = inter_[k];
@@ -1696,13 +2110,8 @@ void Evaluator::compute(int N, const int* types, const int* num_neigh, const int
         launch_linear(I.up.fwd, N, feats, f(o.up), nullptr, false, "mh1_linear_up");
         launch_linear(I.res.fwd, N, f(o.up), f(o.res), nullptr, false, "mh1_linear_res");
         launch_linear(I.skip.fwd, N, feats, f(o.skip), nullptr, false, "mh1_linear_skip");
-        const int WW = mlp_waves(I.wmlp), WD = mlp_waves(I.dmlp);
-        launch("mh1_mlp_forward", k_mlp_forward, blocks_for(E, 16 * WW), 64 * WW, mlp_lds(I.wmlp, WW, false), I.wmlp,
-               rad_, E, mlp_ld(I.wmlp), static_cast<const float*>(f(o_rad)), d_ts, d_tt, f(o.wraw),
-               f(o.wtape));
-        launch("mh1_mlp_forward", k_mlp_forward, blocks_for(E, 16 * WD), 64 * WD, mlp_lds(I.dmlp, WD, false), I.dmlp,
-               rad_, E, mlp_ld(I.dmlp), static_cast<const float*>(f(o_rad)), d_ts, d_tt, f(o.draw),
-               f(o.dtape));
+        mlp_forward(I.wmlp, f(o.wraw), f(o.wtape));
+        mlp_forward(I.dmlp, f(o.draw), f(o.dtape));
         const unsigned tpg = blocks_for(static_cast<long long>(N) * I.tp.channels, kTpThreads);
         if (I.tp.compiled >= 0) {
             auto kf = I.tp.compiled == 0 ? k_tp_forward_c<0, 2> : I.tp.compiled == 1 ? k_tp_forward_c<0, 3>
@@ -1813,11 +2222,10 @@ void Evaluator::compute(int N, const int* types, const int* num_neigh, const int
         launch("mh1_gather_sources", k_gather_sources,
                blocks_for(static_cast<long long>(N) * I.tp.in1_dim, 256), 256, 0, N, I.tp.in1_dim, ip(o_toff),
                ip(o_tedge), f(o.a1), f(o.a_up));
-        const int WW = mlp_waves(I.wmlp), WD = mlp_waves(I.dmlp);
-        launch("mh1_mlp_reverse", k_mlp_reverse, blocks_for(E, 16 * WW), 64 * WW, mlp_lds(I.wmlp, WW, true), I.wmlp,
-               rad_, E, mlp_ld(I.wmlp), f(o.wtape), f(o.wadj), radadj);
-        launch("mh1_mlp_reverse", k_mlp_reverse, blocks_for(E, 16 * WD), 64 * WD, mlp_lds(I.dmlp, WD, true), I.dmlp,
-               rad_, E, mlp_ld(I.dmlp), f(o.dtape), f(o.adraw), radadj);
+        mlp_reverse(I.wmlp, f(o.wtape), f(o.wadj), radadj);
+        mlp_reverse(I.dmlp, f(o.dtape), f(o.adraw), radadj);
+        stages_["w_adj" + std::to_string(k)] = {f(o.wadj), static_cast<std::size_t>(E) * M.interactions[k].tp.numel};
+        stages_["density_adj" + std::to_string(k)] = {f(o.adraw), static_cast<std::size_t>(E)};
         if (k > 0) {
             // a_feat[k-1] += up^T(a_up) + skip^T(a_skip), a_skip = a_feat[k] when the product has a skip
             float* prev = f(lo[k - 1].a_feat);

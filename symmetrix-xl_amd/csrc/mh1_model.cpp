@@ -185,6 +185,60 @@ std::vector<double> linear_apply(const Linear& L, const std::vector<double>& x) 
     return y;
 }
 
+void align4(std::vector<float>& v) {
+    while (v.size() % 4) v.push_back(0.0f);
+}
+
+// Stages of the register form (MlpTables::reg_stage), or reg_hw = 0 when the
+// layers are not [linear, LayerNorm?, SiLU]... linear with one hidden width of
+// 16, 32 or 64.
+void plan_register_form(MlpTables& T) {
+    T.reg_hw = 0;
+    T.reg_stages = 0;
+    T.reg_stage.clear();
+    T.reg_eps.clear();
+    const auto type = [&](int k) { return T.layers[4 * k]; };
+    int k = 0, widest = 0;
+    std::vector<int> st;
+    std::vector<float> eps;
+    while (true) {
+        if (k >= T.num_layers || type(k) != 0) return;
+        const int* L = &T.layers[4 * k];
+        const int in = L[1], out = L[2];
+        const int bias = k == 0 ? -1 : L[3] + out * in;
+        if (k + 1 == T.num_layers) {
+            st.insert(st.end(), {in, out, L[3], bias, T.wt_offset[k], -1});
+            eps.push_back(0.0f);
+            break;
+        }
+        int ln = -1;
+        float e = 0.0f;
+        int next = k + 1;
+        if (type(next) == 1) {
+            ln = T.layers[4 * next + 3];
+            e = T.eps[next];
+            ++next;
+        }
+        if (next >= T.num_layers || type(next) != 2) return;
+        if (out % 16 != 0 || out > 64) return;
+        if (k > 0 && (in % 16 != 0 || (bias % 4) != 0)) return;
+        if (ln >= 0 && ln % 4 != 0) return;
+        st.insert(st.end(), {in, out, L[3], bias, T.wt_offset[k], ln});
+        eps.push_back(e);
+        widest = std::max(widest, out);
+        k = next + 1;
+    }
+    const int stages = static_cast<int>(eps.size()) - 1;
+    if (stages < 1 || stages > MlpTables::kRegStages) return;
+    if (widest != 16 && widest != 32 && widest != 64) return;
+    for (int h = 0; h < stages; ++h)
+        if (st[6 * h + 1] != widest) return;
+    T.reg_hw = widest;
+    T.reg_stages = stages;
+    T.reg_stage = st;
+    T.reg_eps = eps;
+}
+
 MlpTables build_mlp(const Value& v, int radial, const std::vector<std::vector<double>>& src_emb,
                     const std::vector<std::vector<double>>& tgt_emb, const char* what) {
     MlpTables T;
@@ -204,6 +258,7 @@ MlpTables build_mlp(const Value& v, int radial, const std::vector<std::vector<do
             if (shape.size() != 2 || static_cast<int>(b.size()) != shape[0]) bad(std::string(what) + " linear shapes disagree");
             const int out = shape[0], in = shape[1];
             if (prev >= 0 && in != prev) bad(std::string(what) + " layer widths do not chain");
+            align4(T.params);
             const int off = static_cast<int>(T.params.size());
             if (k == 0) {
                 // conditioned first layer: [radial | source embedding | target embedding]
@@ -237,6 +292,7 @@ MlpTables build_mlp(const Value& v, int radial, const std::vector<std::vector<do
             if (ns.size() != 1 || ns[0] != prev || static_cast<int>(w.size()) != prev ||
                 static_cast<int>(b.size()) != prev || !(eps > 0.0))
                 bad(std::string(what) + " LayerNorm does not match its input width");
+            align4(T.params);
             const int off = static_cast<int>(T.params.size());
             for (double x : w) T.params.push_back(static_cast<float>(x));
             for (double x : b) T.params.push_back(static_cast<float>(x));
@@ -259,6 +315,7 @@ MlpTables build_mlp(const Value& v, int radial, const std::vector<std::vector<do
     for (int k = 0; k < T.num_layers; ++k) {
         const int* L = &T.layers[4 * k];
         if (L[0] == 0) {
+            align4(T.params);
             T.wt_offset.push_back(static_cast<int>(T.params.size()));
             for (int i = 0; i < L[1]; ++i)
                 for (int o = 0; o < L[2]; ++o) {
@@ -273,6 +330,7 @@ MlpTables build_mlp(const Value& v, int radial, const std::vector<std::vector<do
         T.tape_offset.push_back(keep ? T.tape_width : -1);
         if (keep) T.tape_width += L[2];
     }
+    plan_register_form(T);
     return T;
 }
 

@@ -80,6 +80,16 @@ struct MlpTables {
     // per edge in all
     std::vector<int> wt_offset, tape_offset;
     int tape_width = 0;
+    // register form: the conditioned first linear and each later hidden linear, with an optional
+    // LayerNorm, feed a SiLU (a hidden stage), and a final linear follows the last stage; at most
+    // kRegStages stages, all of one width, 16, 32 or 64.  reg_hw is that width (the kernel class),
+    // 0 when the MLP has another form.  Per stage, then for the
+    // final linear, 6 ints: in, out, W [out][in], bias (-1: the per-type rows), W^T [in][out],
+    // LayerNorm weight (bias follows; -1 without) as offsets into params, all 16-byte aligned
+    static constexpr int kRegStages = 4;
+    int reg_hw = 0, reg_stages = 0;
+    std::vector<int> reg_stage;
+    std::vector<float> reg_eps;
 };
 
 struct TensorTables {
