@@ -73,7 +73,8 @@ struct DLinear {
 };
 
 constexpr int kRegStages = MlpTables::kRegStages;
-constexpr int kRegTiles = 1;  // 16-edge tiles per wave in the register-form edge MLPs
+// 16-edge tiles per wave in the register-form edge MLPs (forward, reverse)
+constexpr int kRegTilesFwd = 2, kRegTilesRev = 1;
 
 // A stage of the register form: widths and parameter offsets (see MlpTables::reg_stage).
 struct DMlpStage {
@@ -648,6 +649,9 @@ __device__ __forceinline__ void st4_row(float* row, int k, int n, v4f v) {
         if (k + q < n) row[k + q] = v[q];
 }
 
+// logistic function with the hardware reciprocal (1 ulp) in place of an IEEE division
+__device__ __forceinline__ float sigmoid_rcp(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
+
 // sum over the four lane groups that hold one edge
 __device__ __forceinline__ float group4_sum(float v) {
     v += __shfl_xor(v, 16, kWave);
@@ -722,7 +726,7 @@ __device__ __forceinline__ void reg_norm_silu(const float* __restrict__ params, 
                 const float h = (acc[t][i][v] - mean) * rstd;
                 if (SAVE) xs[t][i][v] = h;
                 const float z = h * g[v] + b[v];
-                x[t][i][v] = z * sigmoidf_(z);
+                x[t][i][v] = z * sigmoid_rcp(z);
             }
         }
     }
@@ -750,7 +754,7 @@ __device__ __forceinline__ void reg_silu_norm_reverse(const float* __restrict__ 
             for (int v = 0; v < 4; ++v) {
                 const float h = xs[t][i][v];
                 const float z = h * ga[v] + be[v];
-                const float sg = sigmoidf_(z);
+                const float sg = sigmoid_rcp(z);
                 const float gh = g[t][i][v] * (sg + z * sg * (1.0f - sg)) * ga[v];
                 gx[t][i][v] = gh;
                 m1 += gh;
@@ -1558,6 +1562,34 @@ private:
     std::size_t cap_ = 0;
 };
 
+// grow-only pinned host block (hipHostMalloc): the staging area of a call's
+// host inputs and results, one DMA transfer each way
+class PinnedArena {
+public:
+    PinnedArena() = default;
+    PinnedArena(const PinnedArena&) = delete;
+    PinnedArena& operator=(const PinnedArena&) = delete;
+    ~PinnedArena() {
+        if (ptr_) (void)hipHostFree(ptr_);
+    }
+    void reserve(std::size_t bytes) {
+        if (bytes <= cap_) return;
+        if (ptr_) SMX_HIP(hipHostFree(ptr_));
+        ptr_ = nullptr;
+        cap_ = 0;
+        if (hipHostMalloc(&ptr_, bytes, hipHostMallocDefault) != hipSuccess) {
+            ptr_ = nullptr;
+            throw std::bad_alloc();
+        }
+        cap_ = bytes;
+    }
+    char* base() const { return static_cast<char*>(ptr_); }
+
+private:
+    void* ptr_ = nullptr;
+    std::size_t cap_ = 0;
+};
+
 // carves aligned sub-buffers out of one block (sizes first, then addresses)
 class Layout {
 public:
@@ -1641,8 +1673,13 @@ public:
     const Model& model() const { return model_; }
     void compute(int N, const int* types, const int* num_neigh, const int* neigh, const int* neigh_types,
                  const double* xyz, const double* r, long long E);
-    const std::vector<double>& node_energies() const { return energies_; }
-    const std::vector<double>& node_forces() const { return forces_; }
+    // the last call's results (pinned host memory, valid until the next call)
+    struct Span {
+        const double* data;
+        std::size_t size;
+    };
+    Span node_energies() const { return {num_energies_ ? energies_ : nullptr, num_energies_}; }
+    Span node_forces() const { return {num_forces_ ? forces_ : nullptr, num_forces_}; }
     std::vector<float> stage(const std::string& name);
     Timer timer;
 
@@ -1693,7 +1730,10 @@ private:
     const double* atomic_e_ = nullptr;
     int embed_dim_ = 0;
     Arena work_;
-    std::vector<double> energies_, forces_;
+    PinnedArena host_in_, host_out_;
+    const double* energies_ = nullptr;
+    const double* forces_ = nullptr;
+    std::size_t num_energies_ = 0, num_forces_ = 0;
     // last call's stage buffers (device) for the debug hook
     std::map<std::string, std::pair<const float*, std::size_t>> stages_;
 };
@@ -1969,6 +2009,8 @@ void Evaluator::compute(int N, const int* types, const int* num_neigh, const int
             !std::isfinite(xyz[3 * e + 2]))
             throw std::invalid_argument("MH-1: edge length or vector is not finite and positive");
     }
+    // past the checks a call replaces the results (a rejected graph leaves the last ones)
+    num_energies_ = num_forces_ = 0;
     ensure_device();
     // ---- host-side graph arrays
     std::vector<int> offsets(N + 1, 0), tt(E), t_off(N + 1, 0), t_edges(E);
@@ -2042,8 +2084,12 @@ void Evaluator::compute(int N, const int* types, const int* num_neigh, const int
     auto f = [&](std::size_t o) { return reinterpret_cast<float*>(W + o); };
     auto ip = [&](std::size_t o) { return reinterpret_cast<int*>(W + o); };
     auto dp = [&](std::size_t o) { return reinterpret_cast<double*>(W + o); };
+    // the host inputs lead the layout: staged at their device offsets in pinned memory, one transfer
+    const std::size_t in_end = o_r + sizeof(double) * static_cast<std::size_t>(E);
+    host_in_.reserve(in_end);
+    char* H = host_in_.base();
     auto put = [&](std::size_t o, const void* src, std::size_t bytes) {
-        if (bytes) SMX_HIP(hipMemcpyAsync(W + o, src, bytes, hipMemcpyHostToDevice, stream_));
+        if (bytes) std::memcpy(H + o, src, bytes);
     };
     put(o_types, types, sizeof(int) * N);
     put(o_off, offsets.data(), sizeof(int) * (N + 1));
@@ -2054,9 +2100,10 @@ void Evaluator::compute(int N, const int* types, const int* num_neigh, const int
     put(o_tedge, t_edges.data(), sizeof(int) * E);
     put(o_xyz, xyz, sizeof(double) * 3 * E);
     put(o_r, r, sizeof(double) * E);
+    SMX_HIP(hipMemcpyAsync(W, H, in_end, hipMemcpyHostToDevice, stream_));
     std::vector<int> midx(N);
     for (int i = 0; i < N; ++i) midx[i] = M.model_indices[types[i]];
-    put(o_elems, midx.data(), sizeof(int) * N);
+    if (N) SMX_HIP(hipMemcpyAsync(W + o_elems, midx.data(), sizeof(int) * N, hipMemcpyHostToDevice, stream_));
     const int* d_types = ip(o_types);
     const int* d_off = ip(o_off);
     const int* d_src = ip(o_src);
@@ -2082,9 +2129,9 @@ void Evaluator::compute(int N, const int* types, const int* num_neigh, const int
     // edge MLPs: the register form when the MLP has it, else the LDS-tile kernels with a tape
     auto mlp_forward = [&](const DMlp& m, float* out, float* tape) {
         if (m.reg_hw) {
-            auto k = m.reg_hw == 16 ? k_mlp_forward_r<16, kRegTiles>
-                   : m.reg_hw == 32 ? k_mlp_forward_r<32, kRegTiles> : k_mlp_forward_r<64, kRegTiles>;
-            launch("mh1_mlp_forward", k, blocks_for(E, 64 * kRegTiles), 256, 0, m, E, radf, d_ts, d_tt, out);
+            auto k = m.reg_hw == 16 ? k_mlp_forward_r<16, kRegTilesFwd>
+                   : m.reg_hw == 32 ? k_mlp_forward_r<32, kRegTilesFwd> : k_mlp_forward_r<64, kRegTilesFwd>;
+            launch("mh1_mlp_forward", k, blocks_for(E, 64 * kRegTilesFwd), 256, 0, m, E, radf, d_ts, d_tt, out);
             return;
         }
         const int W = mlp_waves(m);
@@ -2093,9 +2140,10 @@ void Evaluator::compute(int N, const int* types, const int* num_neigh, const int
     };
     auto mlp_reverse = [&](const DMlp& m, const float* tape, const float* gout, float* radadj) {
         if (m.reg_hw) {
-            auto k = m.reg_hw == 16 ? k_mlp_reverse_r<16, kRegTiles>
-                   : m.reg_hw == 32 ? k_mlp_reverse_r<32, kRegTiles> : k_mlp_reverse_r<64, kRegTiles>;
-            launch("mh1_mlp_reverse", k, blocks_for(E, 64 * kRegTiles), 256, 0, m, E, radf, d_ts, d_tt, gout, radadj);
+            auto k = m.reg_hw == 16 ? k_mlp_reverse_r<16, kRegTilesRev>
+                   : m.reg_hw == 32 ? k_mlp_reverse_r<32, kRegTilesRev> : k_mlp_reverse_r<64, kRegTilesRev>;
+            launch("mh1_mlp_reverse", k, blocks_for(E, 64 * kRegTilesRev), 256, 0, m, E, radf, d_ts, d_tt, gout,
+                   radadj);
             return;
         }
         const int W = mlp_waves(m);
@@ -2251,11 +2299,15 @@ void Evaluator::compute(int N, const int* types, const int* num_neigh, const int
     }
     stages_["Yadj"] = {Yadj, static_cast<std::size_t>(E) * NY};
     stages_["rad_adj"] = {radadj, static_cast<std::size_t>(E) * R};
-    energies_.resize(N);
-    forces_.resize(3 * E);
-    if (N) SMX_HIP(hipMemcpyAsync(energies_.data(), dp(o_en), sizeof(double) * N, hipMemcpyDeviceToHost, stream_));
-    if (E) SMX_HIP(hipMemcpyAsync(forces_.data(), dp(o_nf), sizeof(double) * 3 * E, hipMemcpyDeviceToHost, stream_));
+    // energies and per-edge forces end the layout: one transfer into pinned memory
+    const std::size_t out_end = o_nf + sizeof(double) * 3 * static_cast<std::size_t>(E);
+    host_out_.reserve(out_end - o_en);
+    SMX_HIP(hipMemcpyAsync(host_out_.base(), W + o_en, out_end - o_en, hipMemcpyDeviceToHost, stream_));
     SMX_HIP(hipStreamSynchronize(stream_));
+    energies_ = reinterpret_cast<const double*>(host_out_.base());
+    forces_ = reinterpret_cast<const double*>(host_out_.base() + (o_nf - o_en));
+    num_energies_ = static_cast<std::size_t>(N);
+    num_forces_ = 3 * static_cast<std::size_t>(E);
     timer.collect();
 }
 
@@ -2396,19 +2448,19 @@ int32_t smx_mh1_compute_node_energies_forces(SmxMh1Evaluator* ev, int32_t num_no
 
 int32_t smx_mh1_node_energies(SmxMh1Evaluator* ev, double* out, int64_t capacity) {
     return smx::mh1::guarded([&] {
-        const auto& v = ev_of(ev).node_energies();
-        if (v.empty()) return;
-        if (!out || capacity < static_cast<int64_t>(v.size())) throw std::invalid_argument("output buffer too small");
-        std::copy(v.begin(), v.end(), out);
+        const auto v = ev_of(ev).node_energies();
+        if (v.size == 0) return;
+        if (!out || capacity < static_cast<int64_t>(v.size)) throw std::invalid_argument("output buffer too small");
+        std::copy(v.data, v.data + v.size, out);
     });
 }
 
 int32_t smx_mh1_node_forces(SmxMh1Evaluator* ev, double* out, int64_t capacity) {
     return smx::mh1::guarded([&] {
-        const auto& v = ev_of(ev).node_forces();
-        if (v.empty()) return;
-        if (!out || capacity < static_cast<int64_t>(v.size())) throw std::invalid_argument("output buffer too small");
-        std::copy(v.begin(), v.end(), out);
+        const auto v = ev_of(ev).node_forces();
+        if (v.size == 0) return;
+        if (!out || capacity < static_cast<int64_t>(v.size)) throw std::invalid_argument("output buffer too small");
+        std::copy(v.data, v.data + v.size, out);
     });
 }
 
