@@ -73,8 +73,8 @@ struct DLinear {
 };
 
 constexpr int kRegStages = MlpTables::kRegStages;
-// 16-edge tiles per wave in the register-form edge MLPs (forward, reverse)
-constexpr int kRegTilesFwd = 2, kRegTilesRev = 1;
+// 16-edge tiles per wave in the register-form edge MLPs (forward, reverse, first half of a split reverse)
+constexpr int kRegTilesFwd = 2, kRegTilesRev = 1, kRegTilesOut = 2;
 
 // A stage of the register form: widths and parameter offsets (see MlpTables::reg_stage).
 struct DMlpStage {
@@ -93,6 +93,9 @@ struct DMlp {
     int reg_hw, reg_stages;  // register form (reg_hw 0: the LDS-tile kernels run)
     DMlpStage st[kRegStages + 1];  // hidden stages from 0, the final linear at kRegStages
 };
+
+// the reverse of a register-form MLP with a wide final linear runs in two kernels
+inline bool mlp_split(const DMlp& m) { return m.reg_hw && m.st[kRegStages].out >= 64; }
 
 struct DRadial {
     int nb, p, apply_cutoff, agnesi, num_types;
@@ -809,8 +812,8 @@ __device__ __forceinline__ void reg_hidden(const DMlp& m, long long E, long long
 #pragma unroll
             for (int t = 0; t < NT; ++t) acc[t][i] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b[t], acc[t][i], 0, 0, 0);
         }
-        mfma_settle();
     }
+    mfma_settle();
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
         const float* ps = m.type_rows + static_cast<std::size_t>(ets[ec[t]]) * S0.out + 4 * kg;
@@ -883,26 +886,14 @@ __global__ __launch_bounds__(256) void k_mlp_forward_r(const DMlp m, long long E
     }
 }
 
-// Reverse of an edge MLP in registers: the hidden stages recomputed (normalized values kept), gout
-// [E][out_dim] pulled back through the final linear and every stage to the radial features:
-// rad_adj [E][nb] +=.
-template <int HW, int NT>
-__global__ __launch_bounds__(256) void k_mlp_reverse_r(const DMlp m, long long E, const float* __restrict__ rad,
-                                                       const int* __restrict__ ets, const int* __restrict__ ett,
-                                                       const float* __restrict__ gout, float* __restrict__ rad_adj) {
-    constexpr int MT = HW / 16;
+// Adjoint of the last hidden stage's output from the final linear's output adjoint:
+// g[t][i] = sum_k W_F[k][16i + r] gout[e][k] (W_F^T rows as the A operand, gout rows as B).
+template <int MT, int NT>
+__device__ __forceinline__ void reg_out_reverse(const DMlp& m, const long long (&ec)[NT], const float* __restrict__ gout,
+                                                v4f (&g)[NT][MT]) {
     const int lane = threadIdx.x & 63, r = lane & 15, kg = lane >> 4;
-    const long long e0 = (static_cast<long long>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6)) * (16 * NT);
-    if (e0 >= E) return;
-    float x[NT][MT][4], xs[kRegStages][NT][MT][4], rs[kRegStages][NT];
-    reg_hidden<HW, NT, true>(m, E, e0, rad, ets, ett, x, xs, rs);
-    long long ec[NT];
-#pragma unroll
-    for (int t = 0; t < NT; ++t) ec[t] = min(e0 + 16 * t + r, E - 1);
-    // adjoint of the last stage's output: g[t][i] = sum_k W_F[k][16i + r] gout[e][k]
     const DMlpStage& F = m.st[kRegStages];
     const float* WT = m.params + F.wt;  // [F.in][F.out]
-    v4f g[NT][MT];
 #pragma unroll
     for (int t = 0; t < NT; ++t)
 #pragma unroll
@@ -912,19 +903,69 @@ __global__ __launch_bounds__(256) void k_mlp_reverse_r(const DMlp m, long long E
 #pragma unroll
         for (int t = 0; t < NT; ++t) gb[t] = ld4_row(gout + ec[t] * F.out, k0 + 4 * kg, F.out);
 #pragma unroll
-        for (int i = 0; i < MT; ++i) {
+        for (int i = 0; i < MT; ++i)
             a[i] = ld4_row(WT + static_cast<std::size_t>(16 * i + r) * F.out, k0 + 4 * kg, F.out);
-        }
 #pragma unroll
         for (int v = 0; v < 4; ++v)
 #pragma unroll
-            for (int i = 0; i < MT; ++i) {
+            for (int i = 0; i < MT; ++i)
 #pragma unroll
                 for (int t = 0; t < NT; ++t)
                     g[t][i] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][v], gb[t][v], g[t][i], 0, 0, 0);
-            }
-        mfma_settle();
     }
+    mfma_settle();
+}
+
+// First half of a split reverse (wide outputs): reg_out_reverse over tiles of NT x 16 edges, g
+// written [E][HW] (edge row, unit) for the second half.  Few registers, so enough waves stream
+// gout from HBM while others run MFMAs.
+template <int HW, int NT>
+__global__ __launch_bounds__(256) void k_mlp_out_reverse_r(const DMlp m, long long E, const float* __restrict__ gout,
+                                                           float* __restrict__ gbuf) {
+    constexpr int MT = HW / 16;
+    const int lane = threadIdx.x & 63, r = lane & 15, kg = lane >> 4;
+    const long long e0 = (static_cast<long long>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6)) * (16 * NT);
+    if (e0 >= E) return;
+    long long ec[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) ec[t] = min(e0 + 16 * t + r, E - 1);
+    v4f g[NT][MT];
+    reg_out_reverse<MT, NT>(m, ec, gout, g);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const long long e = e0 + 16 * t + r;
+        if (e >= E) continue;
+#pragma unroll
+        for (int i = 0; i < MT; ++i) *reinterpret_cast<v4f*>(gbuf + e * HW + 16 * i + 4 * kg) = g[t][i];
+    }
+}
+
+// Reverse of an edge MLP in registers: the hidden stages recomputed (normalized values kept), gout
+// [E][out_dim] pulled back through the final linear (or, with SPLIT, its result read from gbuf
+// [E][HW]) and every stage to the radial features: rad_adj [E][nb] +=.
+template <int HW, int NT, bool SPLIT>
+__global__ __launch_bounds__(256) void k_mlp_reverse_r(const DMlp m, long long E, const float* __restrict__ rad,
+                                                       const int* __restrict__ ets, const int* __restrict__ ett,
+                                                       const float* __restrict__ gout, const float* __restrict__ gbuf,
+                                                       float* __restrict__ rad_adj) {
+    constexpr int MT = HW / 16;
+    const int lane = threadIdx.x & 63, r = lane & 15, kg = lane >> 4;
+    const long long e0 = (static_cast<long long>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6)) * (16 * NT);
+    if (e0 >= E) return;
+    long long ec[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) ec[t] = min(e0 + 16 * t + r, E - 1);
+    v4f g[NT][MT];
+    if constexpr (SPLIT) {
+        // issued before the recompute, which hides their latency
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int i = 0; i < MT; ++i) g[t][i] = ld4(gbuf + ec[t] * HW + 16 * i + 4 * kg);
+    }
+    float x[NT][MT][4], xs[kRegStages][NT][MT][4], rs[kRegStages][NT];
+    reg_hidden<HW, NT, true>(m, E, e0, rad, ets, ett, x, xs, rs);
+    if constexpr (!SPLIT) reg_out_reverse<MT, NT>(m, ec, gout, g);
     float gx[NT][MT][4];
 #pragma unroll
     for (int h = kRegStages - 1; h >= 0; --h) {
@@ -2072,11 +2113,16 @@ void Evaluator::compute(int N, const int* types, const int* num_neigh, const int
     }
     int ro_width = 1;
     for (const Readout& ro : M.readouts) ro_width = std::max(ro_width, ro.nonlinear ? ro.lin1.out.dim : 1);
+    int mlpg_width = 0;  // the split reverse's [E][width] buffer
+    for (const InteractionDev& I : inter_)
+        for (const DMlp* m : {&I.wmlp, &I.dmlp})
+            if (mlp_split(*m)) mlpg_width = std::max(mlpg_width, m->reg_hw);
     const std::size_t o_elems = lay.add<int>(N);
     const std::size_t o_ro = lay.add<float>(static_cast<std::size_t>(L) * N),
                       o_h = lay.add<float>(static_cast<std::size_t>(N) * ro_width),
                       o_act = lay.add<float>(static_cast<std::size_t>(N) * ro_width),
                       o_ones = lay.add<float>(N), o_radadj = lay.add<float>(static_cast<std::size_t>(E) * R),
+                      o_mlpg = lay.add<float>(static_cast<std::size_t>(E) * mlpg_width),
                       o_Yadj = lay.add<float>(static_cast<std::size_t>(E) * NY), o_cadj = lay.add<float>(E),
                       o_en = lay.add<double>(N), o_nf = lay.add<double>(3 * E);
     work_.reserve(lay.size());
@@ -2126,6 +2172,7 @@ void Evaluator::compute(int N, const int* types, const int* num_neigh, const int
            d_types, embed_table_, feats);
     stages_.clear();
     const float* radf = f(o_rad);
+    float* mlpg = f(o_mlpg);
     // edge MLPs: the register form when the MLP has it, else the LDS-tile kernels with a tape
     auto mlp_forward = [&](const DMlp& m, float* out, float* tape) {
         if (m.reg_hw) {
@@ -2140,10 +2187,17 @@ void Evaluator::compute(int N, const int* types, const int* num_neigh, const int
     };
     auto mlp_reverse = [&](const DMlp& m, const float* tape, const float* gout, float* radadj) {
         if (m.reg_hw) {
-            auto k = m.reg_hw == 16 ? k_mlp_reverse_r<16, kRegTilesRev>
-                   : m.reg_hw == 32 ? k_mlp_reverse_r<32, kRegTilesRev> : k_mlp_reverse_r<64, kRegTilesRev>;
+            const bool split = mlp_split(m);
+            if (split) {
+                auto ka = m.reg_hw == 16 ? k_mlp_out_reverse_r<16, kRegTilesOut>
+                        : m.reg_hw == 32 ? k_mlp_out_reverse_r<32, kRegTilesOut> : k_mlp_out_reverse_r<64, kRegTilesOut>;
+                launch("mh1_mlp_out_reverse", ka, blocks_for(E, 64 * kRegTilesOut), 256, 0, m, E, gout, mlpg);
+            }
+            auto k = m.reg_hw == 16 ? (split ? k_mlp_reverse_r<16, kRegTilesRev, true> : k_mlp_reverse_r<16, kRegTilesRev, false>)
+                   : m.reg_hw == 32 ? (split ? k_mlp_reverse_r<32, kRegTilesRev, true> : k_mlp_reverse_r<32, kRegTilesRev, false>)
+                   : (split ? k_mlp_reverse_r<64, kRegTilesRev, true> : k_mlp_reverse_r<64, kRegTilesRev, false>);
             launch("mh1_mlp_reverse", k, blocks_for(E, 64 * kRegTilesRev), 256, 0, m, E, radf, d_ts, d_tt, gout,
-                   radadj);
+                   static_cast<const float*>(mlpg), radadj);
             return;
         }
         const int W = mlp_waves(m);
