@@ -146,6 +146,19 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
 
+// Ends an MFMA chain whose results VALU code reads next.  A read of an MFMA
+// result needs ten wait states after a v_mfma_f32_16x16x4_f32 (8 passes) on
+// every path; in these kernels the chains sit in runtime-conditional blocks
+// and the compiler padded only the fall-through path of a join (the assembly
+// showed a read of the last accumulator register right after its MFMA on the
+// taken branch).  Sixteen wait states inside the chain's own block, with the
+// scheduler fenced on both sides, cover every path.
+__device__ __forceinline__ void mfma_settle() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_nop 7\n\ts_nop 7");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
 // ---------------------------------------------------------------- radial
 
 // Bessel features of the (Agnesi-transformed) distance, the polynomial
@@ -273,13 +286,18 @@ __global__ __launch_bounds__(256) void k_linear(const DLinear op, int N, const f
         y[t] = acc;
 }
 
-// The same linear on MFMA (v_mfma_f32_16x16x4_f32): one wave per tile of 16
-// rows (node, component) x 64 output channels of one output block; K runs
-// over the input channels of every instruction into that block.  Tiles are
-// numbered block by block (rows, then column blocks).
-__global__ __launch_bounds__(64) void k_linear_mfma(const DLinear op, int N, const float* __restrict__ x,
-                                                    float* __restrict__ y, const float* __restrict__ addend,
-                                                    int accumulate) {
+// The same linear on MFMA (v_mfma_f32_16x16x4_f32): one workgroup of four
+// waves per tile of 16 rows (node, component) x 64 output channels of one
+// output block; K runs over the input channels of every instruction into that
+// block, every fourth 4-channel step to each wave (the node-count launches are
+// a few hundred tiles: split K gives four times the waves and a quarter of the
+// serial load-MFMA chain).  The partial tiles meet in LDS and wave w finishes
+// columns 16w..16w+15.  Tiles are numbered block by block (rows, then column
+// blocks).
+__global__ __launch_bounds__(256) void k_linear_mfma(const DLinear op, int N, const float* __restrict__ x,
+                                                     float* __restrict__ y, const float* __restrict__ addend,
+                                                     int accumulate) {
+    __shared__ v4f part[4][4][64];  // [wave][column chunk][lane]
     long long t = blockIdx.x;
     int b = 0;
     for (; b < op.nblk; ++b) {
@@ -293,7 +311,7 @@ __global__ __launch_bounds__(64) void k_linear_mfma(const DLinear op, int N, con
     const long long R = static_cast<long long>(N) * d;
     const long long row0 = (t / ctiles) * 16;
     const int col0 = static_cast<int>(t % ctiles) * 64;
-    const int lane = threadIdx.x, r = lane & 15, kg = lane >> 4;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane & 15, kg = lane >> 4;
     const long long row = row0 + r;
     const bool rok = row < R;
     const int n = rok ? static_cast<int>(row / d) : 0, m = rok ? static_cast<int>(row % d) : 0;
@@ -304,7 +322,7 @@ __global__ __launch_bounds__(64) void k_linear_mfma(const DLinear op, int N, con
         const int* I = op.instr + 6 * q;
         const int in_off = I[0] + m, mul_in = I[1], w_off = I[3];
         const float* xr = x + static_cast<std::size_t>(n) * op.in_dim + in_off;
-        for (int k0 = 0; k0 < mul_in; k0 += 4) {
+        for (int k0 = 4 * wave; k0 < mul_in; k0 += 16) {
             const int u = k0 + kg;
             float a = 0.0f;
             if (rok && u < mul_in) {
@@ -320,23 +338,26 @@ __global__ __launch_bounds__(64) void k_linear_mfma(const DLinear op, int N, con
             }
         }
     }
+    mfma_settle();
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int c = col0 + 16 * j + r;
-        if (c >= mul) continue;
+    for (int j = 0; j < 4; ++j) part[wave][j][lane] = acc[j];
+    __syncthreads();
+    const int j = wave;
+    const int c = col0 + 16 * j + r;
+    if (c >= mul) return;
+    const v4f sum = (part[0][j][lane] + part[1][j][lane]) + (part[2][j][lane] + part[3][j][lane]);
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const long long rr = row0 + 4 * kg + v;
-            if (rr >= R) continue;
-            const int nn = static_cast<int>(rr / d), mm = static_cast<int>(rr % d);
-            const int jo = boff + c * d + mm;
-            const std::size_t idx = static_cast<std::size_t>(nn) * op.out_dim + jo;
-            float val = acc[j][v];
-            if (op.bias) val += op.bias[jo];
-            if (op.out_mask) val *= op.out_mask[jo];
-            if (addend) val += addend[idx];
-            y[idx] = accumulate ? y[idx] + val : val;
-        }
+    for (int v = 0; v < 4; ++v) {
+        const long long rr = row0 + 4 * kg + v;
+        if (rr >= R) continue;
+        const int nn = static_cast<int>(rr / d), mm = static_cast<int>(rr % d);
+        const int jo = boff + c * d + mm;
+        const std::size_t idx = static_cast<std::size_t>(nn) * op.out_dim + jo;
+        float val = sum[v];
+        if (op.bias) val += op.bias[jo];
+        if (op.out_mask) val *= op.out_mask[jo];
+        if (addend) val += addend[idx];
+        y[idx] = accumulate ? y[idx] + val : val;
     }
 }
 
@@ -616,18 +637,6 @@ __global__ __launch_bounds__(256) void k_mlp_reverse(const DMlp m, const DRadial
 
 __device__ __forceinline__ v4f ld4(const float* p) { return *reinterpret_cast<const v4f*>(p); }
 
-// Ends an MFMA chain whose results VALU code reads next.  A read of an MFMA
-// result needs ten wait states after a v_mfma_f32_16x16x4_f32 (8 passes) on
-// every path; in these kernels the chains sit in runtime-conditional blocks
-// and the compiler padded only the fall-through path of a join (the assembly
-// showed a read of the last accumulator register right after its MFMA on the
-// taken branch).  Sixteen wait states inside the chain's own block, with the
-// scheduler fenced on both sides, cover every path.
-__device__ __forceinline__ void mfma_settle() {
-    __builtin_amdgcn_sched_barrier(0);
-    asm volatile("s_nop 7\n\ts_nop 7");
-    __builtin_amdgcn_sched_barrier(0);
-}
 
 // entries k..k+3 of a row of n floats, zeros from n on (one 16-byte load when n % 4 == 0)
 __device__ __forceinline__ v4f ld4_row(const float* row, int k, int n) {
@@ -1348,8 +1357,20 @@ __global__ __launch_bounds__(256) void k_gather_sources(int N, int dim, const in
     const long long t = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
     if (t >= static_cast<long long>(N) * dim) return;
     const int s = static_cast<int>(t / dim), c = static_cast<int>(t % dim);
+    // eight edges per step: their indices, then their rows, in flight together
     float acc = 0.0f;
-    for (int q = t_off[s]; q < t_off[s + 1]; ++q) acc += a1[static_cast<std::size_t>(t_edges[q]) * dim + c];
+    int q = t_off[s];
+    const int qe = t_off[s + 1];
+    for (; q + 8 <= qe; q += 8) {
+        int e[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) e[k] = t_edges[q + k];
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = a1[static_cast<std::size_t>(e[k]) * dim + c];
+        acc += ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+    }
+    for (; q < qe; ++q) acc += a1[static_cast<std::size_t>(t_edges[q]) * dim + c];
     aup[t] += acc;
 }
 
@@ -2004,7 +2025,7 @@ void Evaluator::launch_linear(const DLinear& op, int N, const float* x, float* y
     for (int b = 0; b < op.nblk; ++b)
         tiles += ((static_cast<long long>(N) * op.blk_d[b] + 15) / 16) * ((op.blk_mul[b] + 63) / 64);
     if (tiles > 0x7fffffffLL) throw std::invalid_argument("MH-1: linear too large for one launch");
-    launch(name, k_linear_mfma, static_cast<unsigned>(tiles), 64, 0, op, N, x, y, addend, accumulate ? 1 : 0);
+    launch(name, k_linear_mfma, static_cast<unsigned>(tiles), 256, 0, op, N, x, y, addend, accumulate ? 1 : 0);
 }
 
 // row stride of an MLP tile buffer: the widest layer plus 4 (two-way LDS
