@@ -953,7 +953,7 @@ __global__ __launch_bounds__(256) void k_mlp_out_reverse_r(const DMlp m, long lo
 // [E][out_dim] pulled back through the final linear (or, with SPLIT, its result read from gbuf
 // [E][HW]) and every stage to the radial features: rad_adj [E][nb] +=.
 template <int HW, int NT, bool SPLIT>
-__global__ __launch_bounds__(256) void k_mlp_reverse_r(const DMlp m, long long E, const float* __restrict__ rad,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k_mlp_reverse_r(const DMlp m, long long E, const float* __restrict__ rad,
                                                        const int* __restrict__ ets, const int* __restrict__ ett,
                                                        const float* __restrict__ gout, const float* __restrict__ gbuf,
                                                        float* __restrict__ rad_adj) {

@@ -86,7 +86,7 @@ struct MlpTables {
     // 0 when the MLP has another form.  Per stage, then for the
     // final linear, 6 ints: in, out, W [out][in], bias (-1: the per-type rows), W^T [in][out],
     // LayerNorm weight (bias follows; -1 without) as offsets into params, all 16-byte aligned
-    static constexpr int kRegStages = 4;
+    static constexpr int kRegStages = 3;
     int reg_hw = 0, reg_stages = 0;
     std::vector<int> reg_stage;
     std::vector<float> reg_eps;
