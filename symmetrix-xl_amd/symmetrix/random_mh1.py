@@ -80,6 +80,10 @@ MH1_CONFIGS = {
     "mh1_tiny_raw": MH1Config("mh1_tiny_raw", apply_cutoff=False, agnesi=True, zbl=True, linear_bias=True,
                               seed=2),
     "mh1_tiny_l2e": MH1Config("mh1_tiny_l2e", node_channels=8, edge_channels=4, hidden_lmax=2, seed=4),
+    # edge-MLP forms: one 32-wide LayerNorm stage (and a 16-wide density stage), and four stages (beyond
+    # the register-form kernels' three, so the LDS-tile kernels with LayerNorm) with a 32-wide density stage
+    "mh1_tiny_mlp32": MH1Config("mh1_tiny_mlp32", radial_hidden=[32], density_hidden=16, seed=5),
+    "mh1_tiny_mlp4": MH1Config("mh1_tiny_mlp4", radial_hidden=[16, 16, 16, 16], density_hidden=32, seed=6),
     # channel counts of the MH-1 family's small members
     "mh1_medium": MH1Config("mh1_medium", node_channels=64, edge_channels=32, l_max=3,
                             atomic_numbers=[1, 6, 7, 8, 13, 14, 22, 26, 29, 38], r_cut=6.0,

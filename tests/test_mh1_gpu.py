@@ -21,8 +21,9 @@ pytestmark = pytest.mark.gpu
 
 # mh1_tiny_l2e (2e node and edge features in the second interaction) is
 # outside the family's compiled convolution structures: its convolutions run
-# the table-driven kernels
-TINY = ["mh1_tiny", "mh1_tiny_l3", "mh1_tiny_raw", "mh1_tiny_l2e"]
+# the table-driven kernels; mh1_tiny_mlp32 (one 32-wide LayerNorm stage) and
+# mh1_tiny_mlp4 (four stages: the LDS-tile MLP kernels) cover the edge-MLP forms
+TINY = ["mh1_tiny", "mh1_tiny_l3", "mh1_tiny_raw", "mh1_tiny_l2e", "mh1_tiny_mlp32", "mh1_tiny_mlp4"]
 
 
 @pytest.fixture(scope="module")
