@@ -146,13 +146,14 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
 
-// Ends an MFMA chain whose results VALU code reads next.  A read of an MFMA
-// result needs ten wait states after a v_mfma_f32_16x16x4_f32 (8 passes) on
-// every path; in these kernels the chains sit in runtime-conditional blocks
-// and the compiler padded only the fall-through path of a join (the assembly
+// Ends an MFMA chain whose results VALU or memory instructions read next.  A
+// read of an MFMA result needs ten wait states after a v_mfma_f32_16x16x4_f32
+// (8 passes) on every path.  Where a chain sat in a runtime-conditional block,
+// the compiler padded only the fall-through path into the join: the assembly
 // showed a read of the last accumulator register right after its MFMA on the
-// taken branch).  Sixteen wait states inside the chain's own block, with the
-// scheduler fenced on both sides, cover every path.
+// taken branch (a stale value, no error).  Sixteen wait states after the
+// chain, with the scheduler fenced on both sides, cover every path;
+// check_mfma_waits.py verifies the generated assembly.
 __device__ __forceinline__ void mfma_settle() {
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("s_nop 7\n\ts_nop 7");
